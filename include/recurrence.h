@@ -1,0 +1,152 @@
+/*
+ * recurrence.h — C ABI of librecurrence_gfx950.so, the MI355X (gfx950) kernels
+ * behind the fused linear-recurrence scans ssd_scan / gla_scan / rglru_scan /
+ * rotlru_scan.
+ *
+ * Each entry point replaces one MLX `mx.fast.metal_kernel` launcher of the
+ * reference (D-CSIL/mlx-recurrence v0.3.0); the citation above each declaration
+ * names it.  In the reference those launchers are Python functions that build a
+ * Metal source string, JIT it and call it on MLX arrays; here they are plain C
+ * functions over device pointers, so any host language with an FFI (ctypes,
+ * cgo, JNI, N-API) can bind them.
+ *
+ * Conventions shared by every entry point
+ *   - All pointers are device pointers (HBM) except where noted; every tensor is
+ *     dense row-major (C-contiguous) in the layout given in its comment.
+ *   - `dtype` is the element type of the large inputs (and of the gradients
+ *     written for them): RR_F32, RR_BF16 or RR_F16.  Outputs y, checkpoints,
+ *     initial/final states and dA_neg are always fp32; state and accumulation
+ *     are fp32 (reference ssd.py:29-31, gla.py:23-26).
+ *   - `seg` is validated exactly like the reference (seg > 0, L % seg == 0,
+ *     lane_dim % 32 == 0; _chassis.py:92-115).  Checkpoints are written every
+ *     T = rr_chunk_len(L, seg) steps: the largest power of two <= 32 dividing
+ *     seg (so T divides L).  For the default seg=32, T = 32 = seg.
+ *   - The caller allocates every buffer (outputs, checkpoints, workspace); the
+ *     library never allocates, frees or keeps device memory.  All work is
+ *     enqueued on `stream` (a hipStream_t; NULL = the default stream) and the
+ *     call returns without synchronising.
+ *   - Nullable arguments: h0 (zero initial state), dfinal (no cotangent on the
+ *     final state), dh0 (initial-state gradient not wanted).
+ *   - Return value: RR_OK, or an error code with a message available from
+ *     rr_last_error() (thread-local).  Argument errors are detected before any
+ *     work is enqueued.
+ */
+#ifndef RR_RECURRENCE_H
+#define RR_RECURRENCE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RR_ABI_VERSION 1
+
+enum rr_dtype { RR_F32 = 0, RR_BF16 = 1, RR_F16 = 2 };
+
+enum rr_status {
+  RR_OK = 0,
+  RR_EINVAL = 1,      /* invalid argument (shape rule, null pointer, dtype)     */
+  RR_EUNSUPPORTED = 2,/* valid call outside what the kernels implement         */
+  RR_EHIP = 3,        /* HIP runtime error while enqueueing                   */
+  RR_EWORKSPACE = 4   /* workspace smaller than the matching *_workspace_bytes */
+};
+
+/* ABI revision of this header (RR_ABI_VERSION). No reference counterpart. */
+int rr_abi_version(void);
+
+/* Message for the last non-RR_OK return on the calling thread.
+ * Stands in for the reference's eager ValueError text (_chassis.py:104-115). */
+const char* rr_last_error(void);
+
+/* Checkpoint interval T used for (L, seg); 0 if seg/L are invalid.
+ * The reference checkpoints every `seg` steps (ssd.py:103-110). */
+int64_t rr_chunk_len(int64_t L, int64_t seg);
+
+/* ------------------------------------------------------------------ SSD --
+ * u [B,L,H,Dh], delta [B,L,H], Bm/Cm [B,L,H,N] (dtype); A_neg [H,N] fp32.
+ * y [B,L,H,Dh] fp32.  ckpt [B,H,nC,Dh,N] fp32, nC = L/T: the state after the
+ * last step of each chunk (ckpt[:,:,nC-1] is the final state [B,H,Dh,N]).
+ * h0 / dfinal / dh0: [B,H,Dh,N] fp32 (the Mamba-2 state layout of
+ * ssd_scan_with_state, ssd.py:365-375).
+ */
+
+/* Workspace bytes needed by rr_ssd_fwd (pass=0) or rr_ssd_bwd (pass=1). */
+size_t rr_ssd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N,
+                              int64_t seg, int pass);
+
+/* Replaces _ssd_forward_kernel (reference mlx_recurrence/ssd.py:54-135). */
+int rr_ssd_fwd(const void* u, const void* delta, const void* Bm, const void* Cm,
+               const float* A_neg, int dtype, int64_t B, int64_t L, int64_t H,
+               int64_t Dh, int64_t N, int64_t seg, const float* h0, float* y,
+               float* ckpt, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Replaces _ssd_backward_kernel and the host mx.sum epilogue
+ * (reference mlx_recurrence/ssd.py:142-307).  dy [B,L,H,Dh] fp32; gradients
+ * du/ddelta/dB/dC in `dtype` with the shapes of their inputs; dA_neg [H,N] fp32
+ * (summed over the batch, ssd.py:305). */
+int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, const void* delta,
+               const void* Bm, const void* Cm, const float* A_neg, int dtype,
+               int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N, int64_t seg,
+               const float* h0, const float* ckpt, void* du, void* ddelta, void* dB,
+               void* dC, float* dA_neg, float* dh0, void* workspace,
+               size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------ GLA --
+ * q/k/v [B,L,H,Dh], gates [B,L,H] (dtype).  y [B,L,H,Dh] fp32.
+ * ckpt [B,H,nC,Dh(j),Dh(i)] fp32: state S[i,j] stored with i fastest, so
+ * ckpt[:,:,nC-1].transpose(-1,-2) is the final state [B,H,Dh(i),Dh(j)].
+ * h0 / dfinal / dh0: [B,H,Dh(i),Dh(j)] fp32 (gla.py:321-329 layout).
+ */
+size_t rr_gla_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t seg,
+                              int pass);
+
+/* Replaces _gla_forward_kernel (reference mlx_recurrence/gla.py:49-123). */
+int rr_gla_fwd(const void* q, const void* k, const void* v, const void* gates, int dtype,
+               int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t seg,
+               const float* h0, float* y, float* ckpt, void* workspace,
+               size_t workspace_bytes, void* stream);
+
+/* Replaces _gla_backward_kernel and its mx.sum epilogue
+ * (reference mlx_recurrence/gla.py:130-270). */
+int rr_gla_bwd(const float* dy, const float* dfinal, const void* q, const void* k,
+               const void* v, const void* gates, int dtype, int64_t B, int64_t L,
+               int64_t H, int64_t Dh, int64_t seg, const float* h0, const float* ckpt,
+               void* dq, void* dk, void* dv, void* dgates, float* dh0, void* workspace,
+               size_t workspace_bytes, void* stream);
+
+/* --------------------------------------------------------------- RG-LRU --
+ * a, x [B,L,D] (dtype).  y [B,L,D] fp32.  ckpt [B,nC,D] fp32.
+ * h0 / dfinal / dh0: [B,D] fp32.  No workspace.
+ */
+/* Replaces _rglru_forward_kernel (reference mlx_recurrence/rglru.py:64-123). */
+int rr_rglru_fwd(const void* a, const void* x, int dtype, int64_t B, int64_t L, int64_t D,
+                 int64_t seg, const float* h0, float* y, float* ckpt, void* stream);
+
+/* Replaces _rglru_backward_kernel (reference mlx_recurrence/rglru.py:130-203). */
+int rr_rglru_bwd(const float* dy, const float* dfinal, const void* a, const void* x,
+                 int dtype, int64_t B, int64_t L, int64_t D, int64_t seg, const float* h0,
+                 const float* ckpt, void* da, void* dx, float* dh0, void* stream);
+
+/* --------------------------------------------------------------- rotLRU --
+ * a, cs, sn [B,L,Dp]; x [B,L,2*Dp] with (u,w) pairs interleaved (dtype).
+ * y [B,L,2*Dp] fp32 (interleaved).  ckpt [B,nC,2*Dp] fp32.
+ * h0 / dfinal / dh0: [B,2*Dp] fp32 (interleaved).  No workspace.
+ */
+/* Replaces _rotlru_forward_kernel (reference mlx_recurrence/rotlru.py:80-146). */
+int rr_rotlru_fwd(const void* a, const void* cs, const void* sn, const void* x, int dtype,
+                  int64_t B, int64_t L, int64_t Dp, int64_t seg, const float* h0, float* y,
+                  float* ckpt, void* stream);
+
+/* Replaces _rotlru_backward_kernel (reference mlx_recurrence/rotlru.py:153-266). */
+int rr_rotlru_bwd(const float* dy, const float* dfinal, const void* a, const void* cs,
+                  const void* sn, const void* x, int dtype, int64_t B, int64_t L,
+                  int64_t Dp, int64_t seg, const float* h0, const float* ckpt, void* da,
+                  void* dcs, void* dsn, void* dx, float* dh0, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RR_RECURRENCE_H */

@@ -1,0 +1,219 @@
+"""ctypes binding of librecurrence_gfx950.so (C ABI declared in include/recurrence.h).
+
+The library is built ahead of time for gfx950 by ``mlx-recurrence_amd/build.py``
+and loaded from this directory.  There is no fallback: if the library is
+missing or the tensors are not on a ROCm device the call raises.
+
+Every wrapper here takes torch tensors, checks device/dtype/contiguity, and
+passes raw device pointers plus the current stream of the tensors' device.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+
+import torch
+
+LIB_NAME = "librecurrence_gfx950.so"
+LIB_PATH = pathlib.Path(__file__).resolve().parent / LIB_NAME
+
+RR_OK = 0
+RR_EINVAL = 1
+RR_EUNSUPPORTED = 2
+RR_EHIP = 3
+RR_EWORKSPACE = 4
+
+DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+_c_i64 = ctypes.c_int64
+_c_int = ctypes.c_int
+_c_ptr = ctypes.c_void_p
+_c_size = ctypes.c_size_t
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "rr_abi_version": (_c_int, []),
+    "rr_last_error": (ctypes.c_char_p, []),
+    "rr_chunk_len": (_c_i64, [_c_i64, _c_i64]),
+    "rr_ssd_workspace_bytes": (_c_size, [_c_i64] * 6 + [_c_int]),
+    "rr_ssd_fwd": (_c_int, [_c_ptr] * 5 + [_c_int] + [_c_i64] * 6 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
+    "rr_ssd_bwd": (_c_int, [_c_ptr] * 7 + [_c_int] + [_c_i64] * 6 + [_c_ptr] * 9 + [_c_size, _c_ptr]),
+    "rr_gla_workspace_bytes": (_c_size, [_c_i64] * 5 + [_c_int]),
+    "rr_gla_fwd": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
+    "rr_gla_bwd": (_c_int, [_c_ptr] * 6 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 8 + [_c_size, _c_ptr]),
+    "rr_rglru_fwd": (_c_int, [_c_ptr] * 2 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 4),
+    "rr_rglru_bwd": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 6),
+    "rr_rotlru_fwd": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 4),
+    "rr_rotlru_bwd": (_c_int, [_c_ptr] * 6 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 8),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGS)
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raise if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_NAME} not found at {LIB_PATH}; build it with "
+            "`python mlx-recurrence_amd/build.py` (hipcc, gfx950)"
+        )
+    lib = ctypes.CDLL(os.fspath(LIB_PATH))
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def abi_version() -> int:
+    return load().rr_abi_version()
+
+
+def chunk_len(L: int, seg: int) -> int:
+    return int(load().rr_chunk_len(L, seg))
+
+
+def _check(rc: int, what: str) -> None:
+    if rc == RR_OK:
+        return
+    msg = load().rr_last_error().decode(errors="replace")
+    if rc in (RR_EINVAL, RR_EWORKSPACE):
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def require_device(*tensors: torch.Tensor) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "mlx_recurrence_amd kernels run on a ROCm GPU; got a tensor on "
+                f"{t.device} (use the *_scan_reference functions for CPU tensors)"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"all tensors must be on one device, got {dev} and {t.device}")
+    return dev
+
+
+def prep(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Contiguous, 16-byte aligned, of the requested dtype."""
+    if t.dtype != dtype:
+        t = t.to(dtype)
+    if not t.is_contiguous():
+        t = t.contiguous()
+    if t.data_ptr() % 16 != 0:
+        t = t.clone()
+    return t
+
+
+def common_dtype(*tensors: torch.Tensor) -> torch.dtype:
+    dt = tensors[0].dtype
+    for t in tensors[1:]:
+        dt = torch.promote_types(dt, t.dtype)
+    if dt not in DTYPE_CODE:
+        if dt.is_floating_point:
+            dt = torch.float32
+        else:
+            raise TypeError(f"unsupported input dtype {dt}; use float32, bfloat16 or float16")
+    return dt
+
+
+# ---------------------------------------------------------------- SSD
+def ssd_workspace(B, L, H, Dh, N, seg, pass_, device) -> torch.Tensor | None:
+    n = int(load().rr_ssd_workspace_bytes(B, L, H, Dh, N, seg, pass_))
+    return torch.empty(n, dtype=torch.uint8, device=device) if n else None
+
+
+def ssd_fwd(u, delta, Bm, Cm, A_neg, h0, seg, y, ckpt, ws):
+    B, L, H, Dh = u.shape
+    N = A_neg.shape[-1]
+    rc = load().rr_ssd_fwd(
+        ptr(u), ptr(delta), ptr(Bm), ptr(Cm), ptr(A_neg), DTYPE_CODE[u.dtype],
+        B, L, H, Dh, N, seg, ptr(h0), ptr(y), ptr(ckpt), ptr(ws),
+        0 if ws is None else ws.numel(), stream_of(u))
+    _check(rc, "rr_ssd_fwd")
+
+
+def ssd_bwd(dy, dfinal, u, delta, Bm, Cm, A_neg, h0, ckpt, seg, du, ddelta, dB, dC, dA, dh0, ws):
+    B, L, H, Dh = u.shape
+    N = A_neg.shape[-1]
+    rc = load().rr_ssd_bwd(
+        ptr(dy), ptr(dfinal), ptr(u), ptr(delta), ptr(Bm), ptr(Cm), ptr(A_neg),
+        DTYPE_CODE[u.dtype], B, L, H, Dh, N, seg, ptr(h0), ptr(ckpt), ptr(du),
+        ptr(ddelta), ptr(dB), ptr(dC), ptr(dA), ptr(dh0), ptr(ws),
+        0 if ws is None else ws.numel(), stream_of(u))
+    _check(rc, "rr_ssd_bwd")
+
+
+# ---------------------------------------------------------------- GLA
+def gla_workspace(B, L, H, Dh, seg, pass_, device) -> torch.Tensor | None:
+    n = int(load().rr_gla_workspace_bytes(B, L, H, Dh, seg, pass_))
+    return torch.empty(n, dtype=torch.uint8, device=device) if n else None
+
+
+def gla_fwd(q, k, v, g, h0, seg, y, ckpt, ws):
+    B, L, H, Dh = q.shape
+    rc = load().rr_gla_fwd(
+        ptr(q), ptr(k), ptr(v), ptr(g), DTYPE_CODE[q.dtype], B, L, H, Dh, seg,
+        ptr(h0), ptr(y), ptr(ckpt), ptr(ws), 0 if ws is None else ws.numel(), stream_of(q))
+    _check(rc, "rr_gla_fwd")
+
+
+def gla_bwd(dy, dfinal, q, k, v, g, h0, ckpt, seg, dq, dk, dv, dg, dh0, ws):
+    B, L, H, Dh = q.shape
+    rc = load().rr_gla_bwd(
+        ptr(dy), ptr(dfinal), ptr(q), ptr(k), ptr(v), ptr(g), DTYPE_CODE[q.dtype],
+        B, L, H, Dh, seg, ptr(h0), ptr(ckpt), ptr(dq), ptr(dk), ptr(dv), ptr(dg),
+        ptr(dh0), ptr(ws), 0 if ws is None else ws.numel(), stream_of(q))
+    _check(rc, "rr_gla_bwd")
+
+
+# ---------------------------------------------------------------- RG-LRU
+def rglru_fwd(a, x, h0, seg, y, ckpt):
+    B, L, D = a.shape
+    rc = load().rr_rglru_fwd(ptr(a), ptr(x), DTYPE_CODE[a.dtype], B, L, D, seg,
+                             ptr(h0), ptr(y), ptr(ckpt), stream_of(a))
+    _check(rc, "rr_rglru_fwd")
+
+
+def rglru_bwd(dy, dfinal, a, x, h0, ckpt, seg, da, dx, dh0):
+    B, L, D = a.shape
+    rc = load().rr_rglru_bwd(ptr(dy), ptr(dfinal), ptr(a), ptr(x), DTYPE_CODE[a.dtype],
+                             B, L, D, seg, ptr(h0), ptr(ckpt), ptr(da), ptr(dx), ptr(dh0),
+                             stream_of(a))
+    _check(rc, "rr_rglru_bwd")
+
+
+# ---------------------------------------------------------------- rotLRU
+def rotlru_fwd(a, cs, sn, x, h0, seg, y, ckpt):
+    B, L, Dp = a.shape
+    rc = load().rr_rotlru_fwd(ptr(a), ptr(cs), ptr(sn), ptr(x), DTYPE_CODE[a.dtype],
+                              B, L, Dp, seg, ptr(h0), ptr(y), ptr(ckpt), stream_of(a))
+    _check(rc, "rr_rotlru_fwd")
+
+
+def rotlru_bwd(dy, dfinal, a, cs, sn, x, h0, ckpt, seg, da, dcs, dsn, dx, dh0):
+    B, L, Dp = a.shape
+    rc = load().rr_rotlru_bwd(ptr(dy), ptr(dfinal), ptr(a), ptr(cs), ptr(sn), ptr(x),
+                              DTYPE_CODE[a.dtype], B, L, Dp, seg, ptr(h0), ptr(ckpt),
+                              ptr(da), ptr(dcs), ptr(dsn), ptr(dx), ptr(dh0), stream_of(a))
+    _check(rc, "rr_rotlru_bwd")

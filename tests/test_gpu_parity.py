@@ -1,0 +1,282 @@
+"""GPU parity of the four scans against the float64 oracle (MI355X only).
+
+Each case runs the public API (mlx_recurrence_amd.*_scan_with_state -> C ABI
+-> HIP kernels) forward and backward on seeded inputs and compares y, the final
+state and every gradient with oracle/recurrence_oracle.py on the same
+(dtype-rounded) inputs.  The loss is sum(y * W) + sum(final * Wf) so the
+final-state cotangent path is exercised; cases with ``dfinal=False`` use the
+reference's loss sum(y * W) alone (_chassis.py:171-175).
+
+Shapes: the reference's own test shapes (tests/test_v2_*.py), the BASELINE
+configurations (full size where the oracle finishes in seconds, reduced
+otherwise), and edge cases (Dh/D = 32, seg != 32, L = seg, negative gates,
+initial state).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import recurrence_oracle as orc
+from tests.gpu_util import TOL, check, rounded, to_dev
+
+import mlx_recurrence_amd as mr
+
+pytestmark = pytest.mark.gpu
+
+F32, BF16, F16 = torch.float32, torch.bfloat16, torch.float16
+
+
+def _sigmoid(z):
+    return 1.0 / (1.0 + np.exp(-z))
+
+
+def _w(rng, shape):
+    return rng.standard_normal(shape).astype(np.float32).astype(np.float64)
+
+
+def _announce(name, **kw):
+    print(f"[case] {name} " + " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+# ----------------------------------------------------------------- RG-LRU
+RGLRU_CASES = [
+    # (B, L, D, seg, dtype, gates, h0, dfinal, seed)
+    (2, 64, 64, 32, F32, "pos", False, False, 0),     # test_v2_rglru.py:155-159
+    (1, 128, 32, 32, F32, "pos", False, False, 1),
+    (2, 96, 32, 16, F32, "pos", False, False, 2),
+    (2, 64, 64, 32, F32, "neg", False, False, 7),     # test_v2_rglru.py:199-219
+    (2, 256, 96, 32, F32, "neg", True, True, 3),
+    (1, 32, 32, 32, F32, "pos", True, True, 4),       # L == seg, single chunk
+    (3, 200, 64, 8, F32, "pos", True, True, 5),       # T = 8, 25 chunks
+    (2, 1024, 320, 32, BF16, "pos", True, True, 6),
+    (2, 512, 128, 32, F16, "neg", False, True, 8),
+    (8, 4096, 2560, 32, BF16, "pos", False, False, 9),  # BASELINE config 3, full size
+]
+
+
+@pytest.mark.parametrize("B,L,D,seg,dtype,gates,h0,dfinal,seed", RGLRU_CASES)
+def test_rglru_parity(B, L, D, seg, dtype, gates, h0, dfinal, seed):
+    _announce("rglru", B=B, L=L, D=D, seg=seg, dtype=dtype, gates=gates, h0=h0, seed=seed)
+    rng = np.random.default_rng(seed)
+    a = _sigmoid(rng.standard_normal((B, L, D)) + 2.0) if gates == "pos" else rng.uniform(-0.99, 0.99, (B, L, D))
+    x = rng.standard_normal((B, L, D)) * 0.5
+    at, xt = to_dev(a, dtype, True), to_dev(x, dtype, True)
+    h0t = to_dev(rng.standard_normal((B, D)), F32, True) if h0 else None
+    y, fs = mr.rglru_scan_with_state(at, xt, seg=seg, initial_state=h0t)
+    W = _w(rng, (B, L, D))
+    Wf = _w(rng, (B, D)) if dfinal else None
+    loss = (y * torch.tensor(W, dtype=F32, device=y.device)).sum()
+    if dfinal:
+        loss = loss + (fs * torch.tensor(Wf, dtype=F32, device=y.device)).sum()
+    loss.backward()
+    ra, rx = rounded(at), rounded(xt)
+    rh0 = rounded(h0t) if h0 else None
+    y_o, fs_o = orc.rglru_forward(ra, rx, rh0)
+    da_o, dx_o, dh0_o = orc.rglru_backward(W, ra, rx, rh0, Wf)
+    tol, rep = TOL[dtype], {}
+    assert y.dtype == F32 and fs.shape == (B, D)
+    check("y", y, y_o, TOL[F32] if dtype == F32 else tol, rep)
+    check("final", fs, fs_o, TOL[F32] if dtype == F32 else tol, rep)
+    check("grad_a", at.grad, da_o, tol, rep)
+    check("grad_x", xt.grad, dx_o, tol, rep)
+    if h0:
+        check("grad_h0", h0t.grad, dh0_o, tol, rep)
+    print(rep, flush=True)
+
+
+def test_rglru_final_equals_last_step():
+    rng = np.random.default_rng(11)
+    a = to_dev(_sigmoid(rng.standard_normal((2, 64, 64)) + 2), F32)
+    x = to_dev(rng.standard_normal((2, 64, 64)), F32)
+    y, fs = mr.rglru_scan_with_state(a, x)
+    assert torch.equal(fs, y[:, -1])
+
+
+# ----------------------------------------------------------------- rotLRU
+ROTLRU_CASES = [
+    # (B, L, Dp, seg, dtype, a_range, h0, dfinal, seed)
+    (2, 64, 32, 32, F32, (0.0, 0.99), False, False, 264),  # test_v2_rotlru.py:262-279
+    (1, 96, 16, 32, F32, (0.0, 0.99), False, False, 196),
+    (2, 64, 32, 32, F32, (-0.99, 0.99), False, False, 7),  # :282-293
+    (2, 160, 48, 16, F32, (-0.99, 0.99), True, True, 3),
+    (2, 1024, 160, 32, BF16, (0.5, 0.99), True, True, 4),
+    (8, 4096, 1280, 32, BF16, "sigmoid", False, False, 9),  # BASELINE config 3, full size
+]
+
+
+@pytest.mark.parametrize("B,L,Dp,seg,dtype,arange,h0,dfinal,seed", ROTLRU_CASES)
+def test_rotlru_parity(B, L, Dp, seg, dtype, arange, h0, dfinal, seed):
+    _announce("rotlru", B=B, L=L, Dp=Dp, seg=seg, dtype=dtype, h0=h0, seed=seed)
+    rng = np.random.default_rng(seed)
+    if arange == "sigmoid":
+        a = _sigmoid(rng.standard_normal((B, L, Dp)) + 2.0)
+        th = rng.uniform(-np.pi, np.pi, (B, L, Dp)) * 0.1
+    else:
+        a = rng.uniform(arange[0], arange[1], (B, L, Dp))
+        th = rng.uniform(0.0, np.pi, (B, L, Dp))
+    cs, sn = np.cos(th), np.sin(th)
+    x = rng.standard_normal((B, L, 2 * Dp)) * 0.5
+    at, ct, st, xt = (to_dev(v, dtype, True) for v in (a, cs, sn, x))
+    h0t = to_dev(rng.standard_normal((B, 2 * Dp)), F32, True) if h0 else None
+    y, fs = mr.rotlru_scan_with_state(at, ct, st, xt, seg=seg, initial_state=h0t)
+    W = _w(rng, (B, L, 2 * Dp))
+    Wf = _w(rng, (B, 2 * Dp)) if dfinal else None
+    loss = (y * torch.tensor(W, dtype=F32, device=y.device)).sum()
+    if dfinal:
+        loss = loss + (fs * torch.tensor(Wf, dtype=F32, device=y.device)).sum()
+    loss.backward()
+    r = [rounded(t) for t in (at, ct, st, xt)]
+    rh0 = rounded(h0t) if h0 else None
+    y_o, fs_o = orc.rotlru_forward(*r, rh0)
+    grads_o = orc.rotlru_backward(W, *r, rh0, Wf)
+    tol, rep = TOL[dtype], {}
+    ftol = TOL[F32] if dtype == F32 else tol
+    check("y", y, y_o, ftol, rep)
+    check("final", fs, fs_o, ftol, rep)
+    for name, t, g in zip(("a", "cs", "sn", "x"), (at, ct, st, xt), grads_o):
+        check(f"grad_{name}", t.grad, g, tol, rep)
+    if h0:
+        check("grad_h0", h0t.grad, grads_o[4], tol, rep)
+    print(rep, flush=True)
+
+
+def test_rotlru_invariants():
+    """theta = 0 reduces to RG-LRU; pure rotation preserves the pair norm
+    (test_v2_rotlru.py:77-115); final == y[:, -1] (:118-123)."""
+    rng = np.random.default_rng(3)
+    B, L, Dp = 2, 64, 32
+    a = rng.uniform(-0.9, 0.9, (B, L, Dp))
+    x = rng.standard_normal((B, L, 2 * Dp))
+    y_rot = mr.rotlru_scan(to_dev(a, F32), to_dev(np.ones_like(a), F32), to_dev(np.zeros_like(a), F32), to_dev(x, F32))
+    y_rg = mr.rglru_scan(to_dev(np.repeat(a, 2, axis=-1), F32), to_dev(x, F32))
+    assert float((y_rot - y_rg).abs().max()) < 1e-6
+
+    th = rng.uniform(0.1, 3.0, (1, L, Dp))
+    x1 = np.zeros((1, L, 2 * Dp))
+    x1[:, 0] = rng.standard_normal(2 * Dp)
+    y = mr.rotlru_scan(to_dev(np.ones((1, L, Dp)), F32), to_dev(np.cos(th), F32), to_dev(np.sin(th), F32), to_dev(x1, F32))
+    yp = y.reshape(1, L, Dp, 2)
+    nrm = torch.sqrt(yp[..., 0] ** 2 + yp[..., 1] ** 2)
+    assert float((nrm[:, -1] - nrm[:, 0]).abs().max()) < 1e-5
+
+    y, fs = mr.rotlru_scan_with_state(to_dev(a, F32), to_dev(np.cos(th[0:1].repeat(2, 0)), F32),
+                                      to_dev(np.sin(th[0:1].repeat(2, 0)), F32), to_dev(x, F32))
+    assert fs.shape == (B, 2 * Dp) and torch.equal(fs, y[:, -1])
+
+
+# -------------------------------------------------------------------- SSD
+def _ssd_inputs(rng, B, L, H, Dh, N, dist):
+    if dist == "ref":   # test_v2_ssd.py:15-23
+        u = rng.standard_normal((B, L, H, Dh)) * 0.5
+        delta = np.abs(rng.standard_normal((B, L, H))) * 0.05 + 0.001
+        Bm = rng.standard_normal((B, L, H, N)) * 0.5
+        Cm = rng.standard_normal((B, L, H, N)) * 0.5
+        A = -np.abs(rng.standard_normal((H, N))) - 0.1
+    else:               # BASELINE configs 0/1/4: A per head, broadcast over n
+        u = rng.standard_normal((B, L, H, Dh))
+        delta = np.abs(rng.standard_normal((B, L, H))) * 0.1 + 0.01
+        Bm = rng.standard_normal((B, L, H, N))
+        Cm = rng.standard_normal((B, L, H, N))
+        A = np.repeat(-np.exp(rng.uniform(0, np.log(16), (H, 1))), N, axis=1)
+    return u, delta, Bm, Cm, A
+
+
+SSD_CASES = [
+    # (B, L, H, Dh, N, seg, dtype, dist, h0, dfinal, seed)
+    (2, 64, 2, 64, 8, 32, F32, "ref", False, False, 0),    # test_v2_ssd.py:26-30
+    (1, 128, 3, 32, 16, 32, F32, "ref", False, False, 1),
+    (2, 96, 2, 32, 8, 16, F32, "ref", False, False, 2),
+    (1, 128, 2, 32, 16, 32, F32, "cfg", False, False, 10),
+    (2, 64, 2, 64, 16, 32, F32, "cfg", True, True, 3),
+    (1, 64, 1, 96, 5, 8, F32, "ref", True, True, 4),        # odd N, Dh = 96
+    (1, 32, 2, 32, 24, 32, F32, "ref", True, True, 5),      # N = 24, single chunk
+    (3, 512, 12, 64, 16, 32, BF16, "cfg", False, False, 11),  # BASELINE config 1, full size
+    (1, 256, 4, 64, 128, 32, BF16, "cfg", True, True, 12),  # config 4's N = 128, reduced
+]
+
+
+@pytest.mark.parametrize("B,L,H,Dh,N,seg,dtype,dist,h0,dfinal,seed", SSD_CASES)
+def test_ssd_parity(B, L, H, Dh, N, seg, dtype, dist, h0, dfinal, seed):
+    _announce("ssd", B=B, L=L, H=H, Dh=Dh, N=N, seg=seg, dtype=dtype, dist=dist, h0=h0, seed=seed)
+    rng = np.random.default_rng(seed)
+    u, delta, Bm, Cm, A = _ssd_inputs(rng, B, L, H, Dh, N, dist)
+    ut, dt, Bt, Ct = (to_dev(v, dtype, True) for v in (u, delta, Bm, Cm))
+    At = to_dev(A, F32, True)
+    h0t = to_dev(rng.standard_normal((B, H, Dh, N)) * 0.5, F32, True) if h0 else None
+    y, fs = mr.ssd_scan_with_state(ut, dt, Bt, Ct, At, seg=seg, initial_state=h0t)
+    W = _w(rng, (B, L, H, Dh))
+    Wf = _w(rng, (B, H, Dh, N)) if dfinal else None
+    loss = (y * torch.tensor(W, dtype=F32, device=y.device)).sum()
+    if dfinal:
+        loss = loss + (fs * torch.tensor(Wf, dtype=F32, device=y.device)).sum()
+    loss.backward()
+    r = [rounded(t) for t in (ut, dt, Bt, Ct, At)]
+    rh0 = rounded(h0t) if h0 else None
+    y_o, fs_o = orc.ssd_forward(*r, rh0)
+    grads_o = orc.ssd_backward(W, *r, rh0, Wf)
+    tol, rep = TOL[dtype], {}
+    ftol = TOL[F32] if dtype == F32 else tol
+    assert fs.shape == (B, H, Dh, N)
+    check("y", y, y_o, ftol, rep)
+    check("final", fs, fs_o, ftol, rep)
+    for name, t, g in zip(("u", "delta", "B", "C", "A_neg"), (ut, dt, Bt, Ct, At), grads_o):
+        check(f"grad_{name}", t.grad, g, tol if name != "A_neg" else max(tol, 1e-5), rep)
+    if h0:
+        check("grad_h0", h0t.grad, grads_o[5], tol, rep)
+    print(rep, flush=True)
+
+
+# -------------------------------------------------------------------- GLA
+def _gla_inputs(rng, B, L, H, Dh, dist):
+    if dist == "ref":   # test_v2_gla.py:11-18
+        q = rng.standard_normal((B, L, H, Dh)) * Dh ** -0.5
+        k = rng.standard_normal((B, L, H, Dh)) * 0.5
+        v = rng.standard_normal((B, L, H, Dh)) * 0.5
+    else:
+        q, k, v = (rng.standard_normal((B, L, H, Dh)) / np.sqrt(Dh) for _ in range(3))
+    g = _sigmoid(rng.standard_normal((B, L, H)) + 2.0)
+    return q, k, v, g
+
+
+GLA_CASES = [
+    # (B, L, H, Dh, seg, dtype, dist, h0, dfinal, seed)
+    (2, 64, 2, 64, 32, F32, "ref", False, False, 0),    # test_v2_gla.py:21-25
+    (1, 128, 3, 32, 32, F32, "ref", False, False, 1),
+    (2, 96, 2, 32, 16, F32, "ref", False, False, 2),
+    (2, 64, 2, 64, 32, F32, "cfg", True, True, 3),
+    (1, 40, 1, 128, 8, F32, "ref", True, True, 4),      # Dh = 128, T = 8
+    (3, 512, 12, 64, 32, BF16, "cfg", False, False, 12),  # BASELINE config 2, full size
+    (2, 256, 4, 64, 32, F16, "cfg", True, True, 13),
+]
+
+
+@pytest.mark.parametrize("B,L,H,Dh,seg,dtype,dist,h0,dfinal,seed", GLA_CASES)
+def test_gla_parity(B, L, H, Dh, seg, dtype, dist, h0, dfinal, seed):
+    _announce("gla", B=B, L=L, H=H, Dh=Dh, seg=seg, dtype=dtype, dist=dist, h0=h0, seed=seed)
+    rng = np.random.default_rng(seed)
+    q, k, v, g = _gla_inputs(rng, B, L, H, Dh, dist)
+    qt, kt, vt, gt = (to_dev(t, dtype, True) for t in (q, k, v, g))
+    h0t = to_dev(rng.standard_normal((B, H, Dh, Dh)) * 0.1, F32, True) if h0 else None
+    y, fs = mr.gla_scan_with_state(qt, kt, vt, gt, seg=seg, initial_state=h0t)
+    W = _w(rng, (B, L, H, Dh))
+    Wf = _w(rng, (B, H, Dh, Dh)) if dfinal else None
+    loss = (y * torch.tensor(W, dtype=F32, device=y.device)).sum()
+    if dfinal:
+        loss = loss + (fs * torch.tensor(Wf, dtype=F32, device=y.device)).sum()
+    loss.backward()
+    r = [rounded(t) for t in (qt, kt, vt, gt)]
+    rh0 = rounded(h0t) if h0 else None
+    y_o, fs_o = orc.gla_forward(*r, rh0)
+    grads_o = orc.gla_backward(W, *r, rh0, Wf)
+    tol, rep = TOL[dtype], {}
+    ftol = TOL[F32] if dtype == F32 else tol
+    assert fs.shape == (B, H, Dh, Dh)
+    check("y", y, y_o, ftol, rep)
+    check("final", fs, fs_o, ftol, rep)
+    for name, t, gr in zip(("q", "k", "v", "gates"), (qt, kt, vt, gt), grads_o):
+        check(f"grad_{name}", t.grad, gr, tol, rep)
+    if h0:
+        check("grad_h0", h0t.grad, grads_o[4], tol, rep)
+    print(rep, flush=True)
