@@ -1,0 +1,712 @@
+// ssd_gla.hip — SSD and GLA scans on gfx950 (chunk-parallel VALU engine).
+//
+// Both recurrences are instances of one "diagonal decay, rank-1 input, linear
+// readout" scan over a state h[d, n] per (batch, head):
+//
+//     h_t[d, n] = dec_t[n] * h_{t-1}[d, n] + inB_t[n] * u_t[d]
+//     y_t[d]    = sum_n outC_t[n] * h_t[d, n]
+//
+//   SSD (reference ssd.py:85-111):  d = channel (Dh), n = state (N),
+//       dec = exp(delta_t A[n]), inB = delta_t B_t[n], outC = C_t[n], u = u_t.
+//   GLA (reference gla.py:78-100):  d = j (value index), n = i (key index),
+//       dec = g_t, inB = k_t[i], outC = q_t[i], u = v_t[j].
+//
+// Its adjoint (reference ssd.py:203-268, gla.py:184-236), with lam[d, n]:
+//     lam += gy_t[d] outC_t[n]
+//     gu_t[d]   = sum_n lam inB_t[n]           (SSD du, GLA dv)
+//     Gin_t[n]  = sum_d lam u_t[d]             (SSD dB / delta, GLA dk)
+//     Gout_t[n] = sum_d h_t gy_t[d]            (SSD dC, GLA dq)
+//     Hp_t[n]   = sum_d lam h_{t-1}            (SSD d(delta), dA; GLA dgates)
+//     lam *= dec_t[n]
+//
+// Work decomposition.  A workgroup owns a 16(d) x 16(n) tile of one head's
+// state for the whole sequence; lane = 4*dl + ng holds d = 16*dt + dl and the
+// four states n = 16*nt + 4*ng + k.  Its NW waves take NW consecutive chunks of
+// T steps at once (chunk-parallel scan): each wave stages its chunk's per-step
+// coefficients (dec, inB, outC; one exp per (t, n) instead of one per lane)
+// in LDS, folds the chunk into the affine map h -> P*h + E, the maps are
+// exchanged through LDS, and each wave replays its chunk from the composed
+// entering state.  The backward pass recomputes each chunk from the forward
+// checkpoint (history kept in registers) and runs the same scheme in reverse
+// time for the adjoint.  Sums over n of a tile and over d of a tile are done
+// with cross-lane shuffles; sums across tiles go through fp32 partial buffers
+// in the caller's workspace and a finalize kernel that also applies the
+// recurrence-specific epilogue (dB = delta*Gin, d(delta), dA, dgates).
+#include "rr_common.h"
+
+namespace {
+
+constexpr int kMaxT = 32;
+constexpr int kTile = 16;
+constexpr int kFwdWaves = 8;
+constexpr int kBwdWaves = 4;
+constexpr int kFinRows = 32;  // (b, t) rows per finalize workgroup
+
+__device__ __forceinline__ float qxor1(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float qxor2(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+// Sum over the 4 lanes of a quad (the 4 n-groups of one d).
+__device__ __forceinline__ float quad_sum(float v) {
+  v += qxor1(v);
+  v += qxor2(v);
+  return v;
+}
+// Sum over the 16 lanes sharing (lane & 3) (the 16 d of a tile).
+__device__ __forceinline__ float dsum16(float v) {
+  v += __shfl_xor(v, 4);
+  v += __shfl_xor(v, 8);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+template <typename InT>
+struct Args {
+  // SSD: lane_in=u, step=delta, in_coef=B, out_coef=C, A=A_neg.
+  // GLA: lane_in=v, step=gates, in_coef=k, out_coef=q, A=null.
+  const InT* lane_in;
+  const InT* step;
+  const InT* in_coef;
+  const InT* out_coef;
+  const float* A;
+  const float* h0;      // initial state (nullable)
+  const float* dy;      // bwd: upstream gradient of y
+  const float* dfinal;  // bwd: cotangent of the final state (nullable)
+  float* y;             // fwd output, or its per-n-tile partials
+  float* ckpt;          // [B,H,nC,DL,NS]
+  InT* gu;              // bwd: du / dv when NN == 1
+  float* gu_part;       // bwd: per-n-tile partials of gu when NN > 1
+  float* g3;            // bwd: [3][ND][B*L*H][NS] partial Gin, Gout, Hp
+  float* dh0;           // bwd: gradient of the initial state (nullable)
+  int L, H, DL, NS, T, nC, ND, NN;
+  int64_t rows;         // B*L*H
+};
+
+// State layout of h0 / dfinal / dh0 within one (b, head): SSD [Dh, N] (d-major),
+// GLA [i, j] = [n, d] (n-major).
+template <bool GLA>
+__device__ __forceinline__ int64_t state_idx(int d, int n, int DL, int NS) {
+  return GLA ? (int64_t)n * DL + d : (int64_t)d * NS + n;
+}
+
+template <typename InT, bool GLA>
+__device__ __forceinline__ void stage_chunk(const Args<InT>& p, float4 (*coef)[kMaxT][4],
+                                            int b, int h, int c, bool act, int nt, int lane) {
+  for (int i = lane; i < kMaxT * kTile; i += 64) {
+    const int t = i >> 4, nn = i & 15, n = nt * kTile + nn;
+    float dec = 1.f, inb = 0.f, outc = 0.f;
+    if (act && t < p.T && n < p.NS) {
+      const int64_t row = ((int64_t)b * p.L + (int64_t)c * p.T + t) * p.H + h;
+      const float sv = rr::ld(p.step, row);
+      if (GLA) {
+        dec = sv;
+        inb = rr::ld(p.in_coef, row * p.NS + n);
+      } else {
+        dec = expf(sv * p.A[(int64_t)h * p.NS + n]);
+        inb = sv * rr::ld(p.in_coef, row * p.NS + n);
+      }
+      outc = rr::ld(p.out_coef, row * p.NS + n);
+    }
+    reinterpret_cast<float*>(&coef[0][t][0])[nn] = dec;
+    reinterpret_cast<float*>(&coef[1][t][0])[nn] = inb;
+    reinterpret_cast<float*>(&coef[2][t][0])[nn] = outc;
+  }
+}
+
+__device__ __forceinline__ void unpack(float4 v, float (&a)[4]) {
+  a[0] = v.x;
+  a[1] = v.y;
+  a[2] = v.z;
+  a[3] = v.w;
+}
+
+template <typename InT, bool GLA, int NW>
+__global__ __launch_bounds__(64 * NW) void r1_fwd_kernel(Args<InT> p) {
+  __shared__ float4 sCoef[NW][3][kMaxT][4];
+  __shared__ float4 sE[NW][64];
+  __shared__ float4 sP[NW][4];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int ng = lane & 3, dl = lane >> 2;
+  const int dt = blockIdx.x / p.NN, nt = blockIdx.x % p.NN;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int d = dt * kTile + dl;
+  const bool dok = d < p.DL;
+  const int nb = nt * kTile + ng * 4;
+  const int64_t bh = (int64_t)b * p.H + h;
+
+  float carry[4] = {0.f, 0.f, 0.f, 0.f};
+  if (p.h0 != nullptr && dok) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (nb + k < p.NS) carry[k] = p.h0[bh * p.DL * p.NS + state_idx<GLA>(d, nb + k, p.DL, p.NS)];
+  }
+  float* yout = p.y + (p.NN > 1 ? (int64_t)nt * p.rows * p.DL : 0);
+
+  for (int c0 = 0; c0 < p.nC; c0 += NW) {
+    const int c = c0 + w;
+    const bool act = c < p.nC;
+    stage_chunk<InT, GLA>(p, sCoef[w], b, h, c, act, nt, lane);
+    float uv[kMaxT];
+#pragma unroll
+    for (int t = 0; t < kMaxT; ++t) {
+      uv[t] = 0.f;
+      if (t < p.T && act && dok)
+        uv[t] = rr::ld(p.lane_in, (((int64_t)b * p.L + (int64_t)c * p.T + t) * p.H + h) * p.DL + d);
+    }
+    __syncthreads();
+    float e[4] = {0.f, 0.f, 0.f, 0.f}, P[4] = {1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+    for (int t = 0; t < kMaxT; ++t) {
+      if (t < p.T) {
+        float dec[4], inb[4];
+        unpack(sCoef[w][0][t][ng], dec);
+        unpack(sCoef[w][1][t][ng], inb);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          e[k] = dec[k] * e[k] + inb[k] * uv[t];
+          P[k] *= dec[k];
+        }
+      }
+    }
+    sE[w][lane] = make_float4(e[0], e[1], e[2], e[3]);
+    if (dl == 0) sP[w][ng] = make_float4(P[0], P[1], P[2], P[3]);
+    __syncthreads();
+    float hin[4], nxt[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) hin[k] = nxt[k] = carry[k];
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+      float pj[4], ej[4];
+      unpack(sP[j][ng], pj);
+      unpack(sE[j][lane], ej);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (j < w) hin[k] = pj[k] * hin[k] + ej[k];
+        nxt[k] = pj[k] * nxt[k] + ej[k];
+      }
+    }
+    float hs[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) hs[k] = hin[k];
+#pragma unroll
+    for (int t = 0; t < kMaxT; ++t) {
+      if (t < p.T) {
+        float dec[4], inb[4], outc[4];
+        unpack(sCoef[w][0][t][ng], dec);
+        unpack(sCoef[w][1][t][ng], inb);
+        unpack(sCoef[w][2][t][ng], outc);
+        float yp = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          hs[k] = dec[k] * hs[k] + inb[k] * uv[t];
+          yp += outc[k] * hs[k];
+        }
+        yp = quad_sum(yp);
+        if (act && dok && ng == (t & 3))
+          yout[(((int64_t)b * p.L + (int64_t)c * p.T + t) * p.H + h) * p.DL + d] = yp;
+      }
+    }
+    if (act && dok) {
+      float* ck = p.ckpt + ((bh * p.nC + c) * p.DL + d) * p.NS;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (nb + k < p.NS) ck[nb + k] = hs[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) carry[k] = nxt[k];
+  }
+}
+
+template <typename InT, bool GLA, int NW>
+__global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
+  __shared__ float4 sCoef[NW][3][kMaxT][4];
+  __shared__ float sU[NW][kMaxT][kTile];   // u_t[d] of the wave's chunk
+  __shared__ float sG[NW][kMaxT][kTile];   // dy_t[d]
+  __shared__ float4 sE[NW][64];
+  __shared__ float4 sP[NW][4];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int ng = lane & 3, dl = lane >> 2;
+  const int dt = blockIdx.x / p.NN, nt = blockIdx.x % p.NN;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int d = dt * kTile + dl;
+  const bool dok = d < p.DL;
+  const int nb = nt * kTile + ng * 4;
+  const int64_t bh = (int64_t)b * p.H + h;
+  const int64_t sbase = bh * p.DL * p.NS;
+  float* gin_p = p.g3 + (int64_t)dt * p.rows * p.NS;
+  float* gout_p = gin_p + (int64_t)p.ND * p.rows * p.NS;
+  float* hp_p = gout_p + (int64_t)p.ND * p.rows * p.NS;
+
+  float carry[4] = {0.f, 0.f, 0.f, 0.f};
+  if (p.dfinal != nullptr && dok) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (nb + k < p.NS) carry[k] = p.dfinal[sbase + state_idx<GLA>(d, nb + k, p.DL, p.NS)];
+  }
+
+  for (int r0 = 0; r0 < p.nC; r0 += NW) {
+    const int c = p.nC - 1 - (r0 + w);
+    const bool act = c >= 0;
+    stage_chunk<InT, GLA>(p, sCoef[w], b, h, c, act, nt, lane);
+    for (int i = lane; i < kMaxT * kTile; i += 64) {
+      const int t = i >> 4, dd = dt * kTile + (i & 15);
+      float uvv = 0.f, gyv = 0.f;
+      if (act && t < p.T && dd < p.DL) {
+        const int64_t j = (((int64_t)b * p.L + (int64_t)c * p.T + t) * p.H + h) * p.DL + dd;
+        uvv = rr::ld(p.lane_in, j);
+        gyv = p.dy[j];
+      }
+      sU[w][t][i & 15] = uvv;
+      sG[w][t][i & 15] = gyv;
+    }
+    float hst[4] = {0.f, 0.f, 0.f, 0.f};
+    if (act && dok) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (nb + k < p.NS) {
+          if (c > 0) hst[k] = p.ckpt[((bh * p.nC + (c - 1)) * p.DL + d) * p.NS + nb + k];
+          else if (p.h0 != nullptr) hst[k] = p.h0[sbase + state_idx<GLA>(d, nb + k, p.DL, p.NS)];
+        }
+      }
+    }
+    __syncthreads();
+    // Recompute the chunk's states: hs[t][k] = h_t.
+    float hs[kMaxT][4];
+    {
+      float hc[4] = {hst[0], hst[1], hst[2], hst[3]};
+#pragma unroll
+      for (int t = 0; t < kMaxT; ++t) {
+        if (t < p.T) {
+          float dec[4], inb[4];
+          unpack(sCoef[w][0][t][ng], dec);
+          unpack(sCoef[w][1][t][ng], inb);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) hc[k] = dec[k] * hc[k] + inb[k] * sU[w][t][dl];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) hs[t][k] = hc[k];
+      }
+    }
+    // Chunk map of the adjoint from a zero carry.
+    float e[4] = {0.f, 0.f, 0.f, 0.f}, P[4] = {1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+    for (int t = kMaxT - 1; t >= 0; --t) {
+      if (t < p.T) {
+        float dec[4], outc[4];
+        unpack(sCoef[w][0][t][ng], dec);
+        unpack(sCoef[w][2][t][ng], outc);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          e[k] = (e[k] + sG[w][t][dl] * outc[k]) * dec[k];
+          P[k] *= dec[k];
+        }
+      }
+    }
+    sE[w][lane] = make_float4(e[0], e[1], e[2], e[3]);
+    if (dl == 0) sP[w][ng] = make_float4(P[0], P[1], P[2], P[3]);
+    __syncthreads();
+    float lam[4], nxt[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) lam[k] = nxt[k] = carry[k];
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+      float pj[4], ej[4];
+      unpack(sP[j][ng], pj);
+      unpack(sE[j][lane], ej);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (j < w) lam[k] = pj[k] * lam[k] + ej[k];
+        nxt[k] = pj[k] * nxt[k] + ej[k];
+      }
+    }
+#pragma unroll
+    for (int t = kMaxT - 1; t >= 0; --t) {
+      if (t < p.T) {
+        float dec[4], inb[4], outc[4];
+        unpack(sCoef[w][0][t][ng], dec);
+        unpack(sCoef[w][1][t][ng], inb);
+        unpack(sCoef[w][2][t][ng], outc);
+        const float uvt = sU[w][t][dl], gyt = sG[w][t][dl];
+        float gup = 0.f, gin[4], gout[4], hp[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          lam[k] += gyt * outc[k];
+          gup += lam[k] * inb[k];
+          gin[k] = dsum16(lam[k] * uvt);
+          gout[k] = dsum16(hs[t][k] * gyt);
+          const float hprev = (t > 0) ? hs[t - 1][k] : hst[k];
+          hp[k] = dsum16(lam[k] * hprev);
+          lam[k] *= dec[k];
+        }
+        gup = quad_sum(gup);
+        const int64_t row = ((int64_t)b * p.L + (int64_t)c * p.T + t) * p.H + h;
+        if (act && dl == 0) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            if (nb + k < p.NS) {
+              gin_p[row * p.NS + nb + k] = gin[k];
+              gout_p[row * p.NS + nb + k] = gout[k];
+              hp_p[row * p.NS + nb + k] = hp[k];
+            }
+          }
+        }
+        if (act && dok && ng == (t & 3)) {
+          if (p.NN > 1) p.gu_part[((int64_t)nt * p.rows + row) * p.DL + d] = gup;
+          else rr::st(p.gu, row * p.DL + d, gup);
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) carry[k] = nxt[k];
+  }
+  if (p.dh0 != nullptr && dok && w == 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (nb + k < p.NS) p.dh0[sbase + state_idx<GLA>(d, nb + k, p.DL, p.NS)] = carry[k];
+  }
+}
+
+// y = sum over n-tiles of the forward partials.
+__global__ void sum_tiles_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                 int64_t n, int tiles) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float s = 0.f;
+  for (int j = 0; j < tiles; ++j) s += part[(int64_t)j * n + i];
+  out[i] = s;
+}
+
+template <typename InT>
+struct FinArgs {
+  const float* g3;       // [3][ND][rows][NS]
+  const float* gu_part;  // [NN][rows][DL] (NN > 1)
+  const InT* step;       // delta / gates
+  const InT* in_coef;    // B (SSD)
+  const float* A;        // SSD
+  InT* g_in;             // SSD dB  / GLA dk
+  InT* g_out;            // SSD dC  / GLA dq
+  InT* g_step;           // SSD d(delta) / GLA dgates
+  InT* gu;               // du / dv (when NN > 1)
+  float* gA_part;        // SSD: [H][nblk][NS]
+  int64_t BL;            // B*L
+  int H, DL, NS, ND, NN;
+};
+
+// One workgroup = one head h and kFinRows consecutive (b, t) rows; wave w takes
+// rows w, w+4, ...; lanes stride over n (and over d for the gu sum).
+template <typename InT, bool GLA>
+__global__ __launch_bounds__(256) void r1_finalize_kernel(FinArgs<InT> p) {
+  __shared__ float sA[4][256];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int h = blockIdx.y;
+  const int64_t rows = p.BL * p.H;
+  const int64_t plane = (int64_t)p.ND * rows * p.NS;
+  float gacc[4] = {0.f, 0.f, 0.f, 0.f};  // SSD dA partial for n = lane + 64*q
+  for (int r = w; r < kFinRows; r += 4) {
+    const int64_t bt = (int64_t)blockIdx.x * kFinRows + r;
+    if (bt >= p.BL) break;
+    const int64_t row = bt * p.H + h;
+    const float sv = rr::ld(p.step, row);
+    float acc = 0.f;
+    for (int q = 0; q * 64 < p.NS; ++q) {
+      const int n = q * 64 + lane;
+      if (n < p.NS) {
+        float gin = 0.f, gout = 0.f, hp = 0.f;
+        for (int j = 0; j < p.ND; ++j) {
+          const int64_t i = ((int64_t)j * rows + row) * p.NS + n;
+          gin += p.g3[i];
+          gout += p.g3[plane + i];
+          hp += p.g3[2 * plane + i];
+        }
+        if (GLA) {
+          rr::st(p.g_in, row * p.NS + n, gin);
+          rr::st(p.g_out, row * p.NS + n, gout);
+          acc += hp;
+        } else {
+          const float a = p.A[(int64_t)h * p.NS + n];
+          const float dec = expf(sv * a);
+          rr::st(p.g_in, row * p.NS + n, sv * gin);
+          rr::st(p.g_out, row * p.NS + n, gout);
+          acc += a * dec * hp + rr::ld(p.in_coef, row * p.NS + n) * gin;
+          if (q < 4) gacc[q] += sv * dec * hp;
+        }
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
+    if (lane == 0) rr::st(p.g_step, row, acc);
+    if (p.NN > 1) {
+      for (int d = lane; d < p.DL; d += 64) {
+        float s = 0.f;
+        for (int j = 0; j < p.NN; ++j) s += p.gu_part[((int64_t)j * rows + row) * p.DL + d];
+        rr::st(p.gu, row * p.DL + d, s);
+      }
+    }
+  }
+  if (!GLA) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sA[w][q * 64 + lane] = gacc[q];
+    __syncthreads();
+    for (int n = threadIdx.x; n < p.NS; n += 256) {
+      const float s = sA[0][n] + sA[1][n] + sA[2][n] + sA[3][n];
+      p.gA_part[((int64_t)h * gridDim.x + blockIdx.x) * p.NS + n] = s;
+    }
+  }
+}
+
+// dA_neg[h, n] = sum over finalize blocks (fixed order: deterministic).
+__global__ void sum_gA_kernel(const float* __restrict__ part, float* __restrict__ dA, int H,
+                              int NS, int nblk) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= H * NS) return;
+  const int h = i / NS, n = i % NS;
+  float s = 0.f;
+  for (int j = 0; j < nblk; ++j) s += part[((int64_t)h * nblk + j) * NS + n];
+  dA[i] = s;
+}
+
+// ------------------------------------------------------------------ host
+struct Plan {
+  int64_t T, nC, ND, NN, rows, nblk;
+  size_t off_y, off_g3, off_gu, off_gA, fwd_bytes, bwd_bytes;
+};
+
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+Plan make_plan(int64_t B, int64_t L, int64_t H, int64_t DL, int64_t NS, int64_t seg) {
+  Plan q{};
+  q.T = rr::chunk_len(L, seg);
+  q.nC = q.T ? L / q.T : 0;
+  q.ND = (DL + kTile - 1) / kTile;
+  q.NN = (NS + kTile - 1) / kTile;
+  q.rows = B * L * H;
+  q.nblk = (B * L + kFinRows - 1) / kFinRows;
+  const size_t f = sizeof(float);
+  q.off_y = 0;
+  q.fwd_bytes = q.NN > 1 ? align256(q.NN * q.rows * DL * f) : 0;
+  q.off_g3 = 0;
+  size_t o = align256(3 * q.ND * q.rows * NS * f);
+  q.off_gu = o;
+  o += q.NN > 1 ? align256(q.NN * q.rows * DL * f) : 0;
+  q.off_gA = o;
+  o += align256(H * q.nblk * NS * f);
+  q.bwd_bytes = o;
+  return q;
+}
+
+int check_dims(const char* who, int64_t B, int64_t L, int64_t H, int64_t DL, int64_t NS,
+               int64_t seg, int dtype, const char* lane_name) {
+  if (B <= 0 || L <= 0 || H <= 0 || DL <= 0 || NS <= 0)
+    return rr::fail(RR_EINVAL, std::string(who) + ": all dimensions must be positive");
+  if (int rc = rr::check_segment_shape(L, seg, DL, lane_name)) return rc;
+  if (!rr::valid_dtype(dtype)) return rr::fail(RR_EINVAL, std::string(who) + ": unsupported dtype");
+  if (B > 65535 || H > 65535)
+    return rr::fail(RR_EUNSUPPORTED, std::string(who) + ": B and H must be <= 65535");
+  if (B * L > ((int64_t)1 << 31) / kFinRows * kFinRows)
+    return rr::fail(RR_EUNSUPPORTED, std::string(who) + ": B*L too large");
+  return RR_OK;
+}
+
+template <typename InT, bool GLA>
+int launch_fwd(Args<InT> a, const Plan& q, int64_t B, void* ws, hipStream_t s, float* y) {
+  const dim3 grid((unsigned)(q.ND * q.NN), (unsigned)a.H, (unsigned)B);
+  hipLaunchKernelGGL((r1_fwd_kernel<InT, GLA, kFwdWaves>), grid, dim3(64 * kFwdWaves), 0, s, a);
+  if (int rc = rr::check_launch("scan forward")) return rc;
+  if (q.NN > 1) {
+    const int64_t n = q.rows * a.DL;
+    hipLaunchKernelGGL(sum_tiles_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                       static_cast<const float*>(ws), y, n, (int)q.NN);
+    if (int rc = rr::check_launch("scan forward tile sum")) return rc;
+  }
+  return RR_OK;
+}
+
+template <typename InT, bool GLA>
+int launch_bwd(Args<InT> a, FinArgs<InT> f, const Plan& q, int64_t B, hipStream_t s,
+               float* dA) {
+  const dim3 grid((unsigned)(q.ND * q.NN), (unsigned)a.H, (unsigned)B);
+  hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kBwdWaves>), grid, dim3(64 * kBwdWaves), 0, s, a);
+  if (int rc = rr::check_launch("scan backward")) return rc;
+  const dim3 fgrid((unsigned)q.nblk, (unsigned)a.H);
+  hipLaunchKernelGGL((r1_finalize_kernel<InT, GLA>), fgrid, dim3(256), 0, s, f);
+  if (int rc = rr::check_launch("scan backward finalize")) return rc;
+  if (!GLA) {
+    const int n = (int)(a.H * a.NS);
+    hipLaunchKernelGGL(sum_gA_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                       f.gA_part, dA, a.H, a.NS, (int)q.nblk);
+    if (int rc = rr::check_launch("scan backward dA")) return rc;
+  }
+  return RR_OK;
+}
+
+}  // namespace
+
+// ====================================================================== SSD
+extern "C" size_t rr_ssd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N,
+                                         int64_t seg, int pass) {
+  if (B <= 0 || L <= 0 || H <= 0 || Dh <= 0 || N <= 0 || rr::chunk_len(L, seg) == 0) return 0;
+  const Plan q = make_plan(B, L, H, Dh, N, seg);
+  return pass == 0 ? q.fwd_bytes : q.bwd_bytes;
+}
+
+extern "C" int rr_ssd_fwd(const void* u, const void* delta, const void* Bm, const void* Cm,
+                          const float* A_neg, int dtype, int64_t B, int64_t L, int64_t H,
+                          int64_t Dh, int64_t N, int64_t seg, const float* h0, float* y,
+                          float* ckpt, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_dims("ssd_fwd", B, L, H, Dh, N, seg, dtype, "Dh")) return rc;
+  if (N > 256) return rr::fail(RR_EUNSUPPORTED, "ssd_fwd: N > 256 is not supported");
+  if (!u || !delta || !Bm || !Cm || !A_neg || !y || !ckpt)
+    return rr::fail(RR_EINVAL, "ssd_fwd: null pointer argument");
+  const Plan q = make_plan(B, L, H, Dh, N, seg);
+  if (workspace_bytes < q.fwd_bytes || (q.fwd_bytes && !workspace))
+    return rr::fail(RR_EWORKSPACE, "ssd_fwd: workspace too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  RR_DISPATCH_DTYPE(dtype, {
+    Args<InT> a{};
+    a.lane_in = static_cast<const InT*>(u);
+    a.step = static_cast<const InT*>(delta);
+    a.in_coef = static_cast<const InT*>(Bm);
+    a.out_coef = static_cast<const InT*>(Cm);
+    a.A = A_neg;
+    a.h0 = h0;
+    a.y = q.NN > 1 ? static_cast<float*>(workspace) : y;
+    a.ckpt = ckpt;
+    a.L = (int)L; a.H = (int)H; a.DL = (int)Dh; a.NS = (int)N; a.T = (int)q.T;
+    a.nC = (int)q.nC; a.ND = (int)q.ND; a.NN = (int)q.NN; a.rows = q.rows;
+    return launch_fwd<InT, false>(a, q, B, workspace, s, y);
+  });
+  return RR_OK;
+}
+
+extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, const void* delta,
+                          const void* Bm, const void* Cm, const float* A_neg, int dtype,
+                          int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N, int64_t seg,
+                          const float* h0, const float* ckpt, void* du, void* ddelta, void* dB,
+                          void* dC, float* dA_neg, float* dh0, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  if (int rc = check_dims("ssd_bwd", B, L, H, Dh, N, seg, dtype, "Dh")) return rc;
+  if (N > 256) return rr::fail(RR_EUNSUPPORTED, "ssd_bwd: N > 256 is not supported");
+  if (!dy || !u || !delta || !Bm || !Cm || !A_neg || !ckpt || !du || !ddelta || !dB || !dC ||
+      !dA_neg)
+    return rr::fail(RR_EINVAL, "ssd_bwd: null pointer argument");
+  const Plan q = make_plan(B, L, H, Dh, N, seg);
+  if (workspace_bytes < q.bwd_bytes || !workspace)
+    return rr::fail(RR_EWORKSPACE, "ssd_bwd: workspace too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  RR_DISPATCH_DTYPE(dtype, {
+    Args<InT> a{};
+    a.lane_in = static_cast<const InT*>(u);
+    a.step = static_cast<const InT*>(delta);
+    a.in_coef = static_cast<const InT*>(Bm);
+    a.out_coef = static_cast<const InT*>(Cm);
+    a.A = A_neg;
+    a.h0 = h0;
+    a.dy = dy;
+    a.dfinal = dfinal;
+    a.ckpt = const_cast<float*>(ckpt);
+    a.gu = static_cast<InT*>(du);
+    a.gu_part = reinterpret_cast<float*>(ws + q.off_gu);
+    a.g3 = reinterpret_cast<float*>(ws + q.off_g3);
+    a.dh0 = dh0;
+    a.L = (int)L; a.H = (int)H; a.DL = (int)Dh; a.NS = (int)N; a.T = (int)q.T;
+    a.nC = (int)q.nC; a.ND = (int)q.ND; a.NN = (int)q.NN; a.rows = q.rows;
+    FinArgs<InT> f{};
+    f.g3 = a.g3;
+    f.gu_part = a.gu_part;
+    f.step = a.step;
+    f.in_coef = a.in_coef;
+    f.A = A_neg;
+    f.g_in = static_cast<InT*>(dB);
+    f.g_out = static_cast<InT*>(dC);
+    f.g_step = static_cast<InT*>(ddelta);
+    f.gu = static_cast<InT*>(du);
+    f.gA_part = reinterpret_cast<float*>(ws + q.off_gA);
+    f.BL = B * L; f.H = (int)H; f.DL = (int)Dh; f.NS = (int)N; f.ND = (int)q.ND; f.NN = (int)q.NN;
+    return launch_bwd<InT, false>(a, f, q, B, s, dA_neg);
+  });
+  return RR_OK;
+}
+
+// ====================================================================== GLA
+extern "C" size_t rr_gla_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh,
+                                         int64_t seg, int pass) {
+  if (B <= 0 || L <= 0 || H <= 0 || Dh <= 0 || rr::chunk_len(L, seg) == 0) return 0;
+  const Plan q = make_plan(B, L, H, Dh, Dh, seg);
+  return pass == 0 ? q.fwd_bytes : q.bwd_bytes;
+}
+
+extern "C" int rr_gla_fwd(const void* qp, const void* kp, const void* vp, const void* gates,
+                          int dtype, int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t seg,
+                          const float* h0, float* y, float* ckpt, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  if (int rc = check_dims("gla_fwd", B, L, H, Dh, Dh, seg, dtype, "Dh")) return rc;
+  if (!qp || !kp || !vp || !gates || !y || !ckpt)
+    return rr::fail(RR_EINVAL, "gla_fwd: null pointer argument");
+  const Plan q = make_plan(B, L, H, Dh, Dh, seg);
+  if (workspace_bytes < q.fwd_bytes || (q.fwd_bytes && !workspace))
+    return rr::fail(RR_EWORKSPACE, "gla_fwd: workspace too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  RR_DISPATCH_DTYPE(dtype, {
+    Args<InT> a{};
+    a.lane_in = static_cast<const InT*>(vp);
+    a.step = static_cast<const InT*>(gates);
+    a.in_coef = static_cast<const InT*>(kp);
+    a.out_coef = static_cast<const InT*>(qp);
+    a.h0 = h0;
+    a.y = q.NN > 1 ? static_cast<float*>(workspace) : y;
+    a.ckpt = ckpt;
+    a.L = (int)L; a.H = (int)H; a.DL = (int)Dh; a.NS = (int)Dh; a.T = (int)q.T;
+    a.nC = (int)q.nC; a.ND = (int)q.ND; a.NN = (int)q.NN; a.rows = q.rows;
+    return launch_fwd<InT, true>(a, q, B, workspace, s, y);
+  });
+  return RR_OK;
+}
+
+extern "C" int rr_gla_bwd(const float* dy, const float* dfinal, const void* qp, const void* kp,
+                          const void* vp, const void* gates, int dtype, int64_t B, int64_t L,
+                          int64_t H, int64_t Dh, int64_t seg, const float* h0, const float* ckpt,
+                          void* dq, void* dk, void* dv, void* dgates, float* dh0, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  if (int rc = check_dims("gla_bwd", B, L, H, Dh, Dh, seg, dtype, "Dh")) return rc;
+  if (!dy || !qp || !kp || !vp || !gates || !ckpt || !dq || !dk || !dv || !dgates)
+    return rr::fail(RR_EINVAL, "gla_bwd: null pointer argument");
+  const Plan q = make_plan(B, L, H, Dh, Dh, seg);
+  if (workspace_bytes < q.bwd_bytes || !workspace)
+    return rr::fail(RR_EWORKSPACE, "gla_bwd: workspace too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  RR_DISPATCH_DTYPE(dtype, {
+    Args<InT> a{};
+    a.lane_in = static_cast<const InT*>(vp);
+    a.step = static_cast<const InT*>(gates);
+    a.in_coef = static_cast<const InT*>(kp);
+    a.out_coef = static_cast<const InT*>(qp);
+    a.h0 = h0;
+    a.dy = dy;
+    a.dfinal = dfinal;
+    a.ckpt = const_cast<float*>(ckpt);
+    a.gu = static_cast<InT*>(dv);
+    a.gu_part = reinterpret_cast<float*>(ws + q.off_gu);
+    a.g3 = reinterpret_cast<float*>(ws + q.off_g3);
+    a.dh0 = dh0;
+    a.L = (int)L; a.H = (int)H; a.DL = (int)Dh; a.NS = (int)Dh; a.T = (int)q.T;
+    a.nC = (int)q.nC; a.ND = (int)q.ND; a.NN = (int)q.NN; a.rows = q.rows;
+    FinArgs<InT> f{};
+    f.g3 = a.g3;
+    f.gu_part = a.gu_part;
+    f.step = a.step;
+    f.g_in = static_cast<InT*>(dk);
+    f.g_out = static_cast<InT*>(dq);
+    f.g_step = static_cast<InT*>(dgates);
+    f.gu = static_cast<InT*>(dv);
+    f.BL = B * L; f.H = (int)H; f.DL = (int)Dh; f.NS = (int)Dh; f.ND = (int)q.ND; f.NN = (int)q.NN;
+    return launch_bwd<InT, true>(a, f, q, B, s, nullptr);
+  });
+  return RR_OK;
+}
