@@ -133,10 +133,12 @@ def make_ssd(cfg, device, dtype):
     Bm = _gen((B, L, H, N), g)
     Cm = _gen((B, L, H, N), g)
     A = -torch.exp(_gen((H,), g, "uniform") * math.log(16.0))
-    A_neg = A[:, None].expand(H, N).contiguous()
     dy = _gen((B, L, H, Dh), g)
-    cpu = dict(u=u, delta=delta, Bm=Bm, Cm=Cm, A_neg=A_neg, dy=dy)
+    cpu = dict(u=u, delta=delta, Bm=Bm, Cm=Cm, A_neg=A[:, None].expand(H, N).contiguous(), dy=dy)
     d = {k: (v.to(dtype) if k not in ("A_neg", "dy") else v).to(device) for k, v in cpu.items()}
+    # A per head, broadcast over N (stride 0): the layout the kernels take as A_stride_n = 0
+    d["A"] = A.to(device)
+    d["A_neg"] = d["A"][:, None].expand(H, N)
     T = _lib.chunk_len(L, seg)
     nC = L // T
     f32 = torch.float32
@@ -158,17 +160,17 @@ def make_ssd(cfg, device, dtype):
     bwd_bytes = n_u * 4 + n_ck * 4 + inputs + (n_u + n_d + 2 * n_bc) * es + H * N * 4
 
     def fwd():
-        _lib.ssd_fwd(d["u"], d["delta"], d["Bm"], d["Cm"], d["A_neg"], None, seg, out["y"], out["ckpt"], out["wsf"])
+        _lib.ssd_fwd(d["u"], d["delta"], d["Bm"], d["Cm"], d["A"], 0, None, seg, out["y"], out["ckpt"], out["wsf"])
 
     def bwd():
-        _lib.ssd_bwd(d["dy"], None, d["u"], d["delta"], d["Bm"], d["Cm"], d["A_neg"], None, out["ckpt"], seg,
+        _lib.ssd_bwd(d["dy"], None, d["u"], d["delta"], d["Bm"], d["Cm"], d["A"], 0, None, out["ckpt"], seg,
                      out["du"], out["dd"], out["dB"], out["dC"], out["dA"], None, out["wsb"])
 
     def eager():
         import mlx_recurrence_amd as mr
         xs = [d[k].detach().requires_grad_(True) for k in ("u", "delta", "Bm", "Cm")]
-        A_ = d["A_neg"].detach().requires_grad_(True)
-        y = mr.ssd_scan(*xs, A_, seg=seg)
+        A_ = d["A"].detach().requires_grad_(True)
+        y = mr.ssd_scan(*xs, A_[:, None].expand(H, N), seg=seg)
         y.backward(d["dy"])
 
     def cpu_sample():

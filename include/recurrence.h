@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define RR_ABI_VERSION 1
+#define RR_ABI_VERSION 2
 
 enum rr_dtype { RR_F32 = 0, RR_BF16 = 1, RR_F16 = 2 };
 
@@ -65,7 +65,10 @@ const char* rr_last_error(void);
 int64_t rr_chunk_len(int64_t L, int64_t seg);
 
 /* ------------------------------------------------------------------ SSD --
- * u [B,L,H,Dh], delta [B,L,H], Bm/Cm [B,L,H,N] (dtype); A_neg [H,N] fp32.
+ * u [B,L,H,Dh], delta [B,L,H], Bm/Cm [B,L,H,N] (dtype); A_neg fp32, element
+ * (h, n) at A_neg[h * (A_stride_n ? N : 1) + n * A_stride_n]: A_stride_n = 1 for a
+ * dense [H,N] array, 0 for one rate per head broadcast over N (Mamba-2's A,
+ * the BASELINE configurations; these calls run on the chunked MFMA kernels).
  * y [B,L,H,Dh] fp32.  ckpt [B,H,nC,Dh,N] fp32, nC = L/T: the state after the
  * last step of each chunk (ckpt[:,:,nC-1] is the final state [B,H,Dh,N]).
  * h0 / dfinal / dh0: [B,H,Dh,N] fp32 (the Mamba-2 state layout of
@@ -78,16 +81,16 @@ size_t rr_ssd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64
 
 /* Replaces _ssd_forward_kernel (reference mlx_recurrence/ssd.py:54-135). */
 int rr_ssd_fwd(const void* u, const void* delta, const void* Bm, const void* Cm,
-               const float* A_neg, int dtype, int64_t B, int64_t L, int64_t H,
+               const float* A_neg, int64_t A_stride_n, int dtype, int64_t B, int64_t L, int64_t H,
                int64_t Dh, int64_t N, int64_t seg, const float* h0, float* y,
                float* ckpt, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Replaces _ssd_backward_kernel and the host mx.sum epilogue
  * (reference mlx_recurrence/ssd.py:142-307).  dy [B,L,H,Dh] fp32; gradients
  * du/ddelta/dB/dC in `dtype` with the shapes of their inputs; dA_neg [H,N] fp32
- * (summed over the batch, ssd.py:305). */
+ * (summed over the batch, ssd.py:305), dense even when A_stride_n == 0. */
 int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, const void* delta,
-               const void* Bm, const void* Cm, const float* A_neg, int dtype,
+               const void* Bm, const void* Cm, const float* A_neg, int64_t A_stride_n, int dtype,
                int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N, int64_t seg,
                const float* h0, const float* ckpt, void* du, void* ddelta, void* dB,
                void* dC, float* dA_neg, float* dh0, void* workspace,

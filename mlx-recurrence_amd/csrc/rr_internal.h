@@ -1,0 +1,45 @@
+// rr_internal.h — interfaces between the C-ABI entry points and the chunked
+// (MFMA) SSD kernels.  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rr {
+
+// Longest run of earlier chunks the entering-state sum of the chunked SSD
+// kernels handles (sizes an LDS table of per-chunk delta totals).
+constexpr int kMaxCarryChunks = 64;
+
+struct Ssd2Args {
+  const uint16_t* u;       // [B,L,H,Dh] bf16
+  const uint16_t* delta;   // [B,L,H]
+  const uint16_t* Bm;      // [B,L,H,N]
+  const uint16_t* Cm;      // [B,L,H,N]
+  const float* A;          // head-uniform decay rate: A[h * A_stride_h]
+  int64_t A_stride_h;
+  const float* h0;         // [B,H,Dh,N] or null
+  float* y;                // [B,L,H,Dh]
+  float* ckpt;             // [B,H,nC,Dh,N]
+  // backward
+  const float* dy;         // [B,L,H,Dh]
+  const float* dfinal;     // [B,H,Dh,N] or null
+  uint16_t* du;
+  uint16_t* ddelta;
+  uint16_t* dB;
+  uint16_t* dC;
+  float* dA;               // [H,N]
+  float* dh0;              // [B,H,Dh,N] or null
+  float* ws;               // backward workspace
+  int L, H, DH, NS, nC, R;
+};
+
+// True when the chunked kernels cover this call: bf16 inputs, a head-uniform A
+// (A_stride_n == 0), checkpoint interval 32, Dh in {32, 64, 128} and
+// N in {16, 32, 64, 128}.
+bool ssd2_supported(int dtype, int64_t L, int64_t seg, int64_t Dh, int64_t N, int64_t A_stride_n);
+// Chunks per workgroup.
+int ssd2_pick_run(int64_t B, int64_t H, int64_t nC, int64_t N);
+int ssd2_fwd(const Ssd2Args& p, int64_t B, hipStream_t s);
+
+}  // namespace rr

@@ -33,6 +33,7 @@
 // in the caller's workspace and a finalize kernel that also applies the
 // recurrence-specific epilogue (dB = delta*Gin, d(delta), dA, dgates).
 #include "rr_common.h"
+#include "rr_internal.h"
 
 namespace {
 
@@ -72,6 +73,7 @@ struct Args {
   const InT* in_coef;
   const InT* out_coef;
   const float* A;
+  int64_t a_sh, a_sn;   // A[h * a_sh + n * a_sn]
   const float* h0;      // initial state (nullable)
   const float* dy;      // bwd: upstream gradient of y
   const float* dfinal;  // bwd: cotangent of the final state (nullable)
@@ -105,7 +107,7 @@ __device__ __forceinline__ void stage_chunk(const Args<InT>& p, float4 (*coef)[k
         dec = sv;
         inb = rr::ld(p.in_coef, row * p.NS + n);
       } else {
-        dec = expf(sv * p.A[(int64_t)h * p.NS + n]);
+        dec = expf(sv * p.A[(int64_t)h * p.a_sh + (int64_t)n * p.a_sn]);
         inb = sv * rr::ld(p.in_coef, row * p.NS + n);
       }
       outc = rr::ld(p.out_coef, row * p.NS + n);
@@ -388,6 +390,7 @@ struct FinArgs {
   const InT* step;       // delta / gates
   const InT* in_coef;    // B (SSD)
   const float* A;        // SSD
+  int64_t a_sh, a_sn;
   InT* g_in;             // SSD dB  / GLA dk
   InT* g_out;            // SSD dC  / GLA dq
   InT* g_step;           // SSD d(delta) / GLA dgates
@@ -428,7 +431,7 @@ __global__ __launch_bounds__(256) void r1_finalize_kernel(FinArgs<InT> p) {
           rr::st(p.g_out, row * p.NS + n, gout);
           acc += hp;
         } else {
-          const float a = p.A[(int64_t)h * p.NS + n];
+          const float a = p.A[(int64_t)h * p.a_sh + (int64_t)n * p.a_sn];
           const float dec = expf(sv * a);
           rr::st(p.g_in, row * p.NS + n, sv * gin);
           rr::st(p.g_out, row * p.NS + n, gout);
@@ -555,17 +558,34 @@ extern "C" size_t rr_ssd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_
 }
 
 extern "C" int rr_ssd_fwd(const void* u, const void* delta, const void* Bm, const void* Cm,
-                          const float* A_neg, int dtype, int64_t B, int64_t L, int64_t H,
+                          const float* A_neg, int64_t A_stride_n, int dtype, int64_t B, int64_t L, int64_t H,
                           int64_t Dh, int64_t N, int64_t seg, const float* h0, float* y,
                           float* ckpt, void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_dims("ssd_fwd", B, L, H, Dh, N, seg, dtype, "Dh")) return rc;
   if (N > 256) return rr::fail(RR_EUNSUPPORTED, "ssd_fwd: N > 256 is not supported");
   if (!u || !delta || !Bm || !Cm || !A_neg || !y || !ckpt)
     return rr::fail(RR_EINVAL, "ssd_fwd: null pointer argument");
+  if (A_stride_n != 0 && A_stride_n != 1)
+    return rr::fail(RR_EINVAL, "ssd_fwd: A_stride_n must be 0 or 1");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (rr::ssd2_supported(dtype, L, seg, Dh, N, A_stride_n)) {
+    rr::Ssd2Args a{};
+    a.u = static_cast<const uint16_t*>(u);
+    a.delta = static_cast<const uint16_t*>(delta);
+    a.Bm = static_cast<const uint16_t*>(Bm);
+    a.Cm = static_cast<const uint16_t*>(Cm);
+    a.A = A_neg;
+    a.A_stride_h = 1;
+    a.h0 = h0;
+    a.y = y;
+    a.ckpt = ckpt;
+    a.L = (int)L; a.H = (int)H; a.DH = (int)Dh; a.NS = (int)N; a.nC = (int)(L / 32);
+    a.R = rr::ssd2_pick_run(B, H, a.nC, N);
+    return rr::ssd2_fwd(a, B, s);
+  }
   const Plan q = make_plan(B, L, H, Dh, N, seg);
   if (workspace_bytes < q.fwd_bytes || (q.fwd_bytes && !workspace))
     return rr::fail(RR_EWORKSPACE, "ssd_fwd: workspace too small");
-  hipStream_t s = static_cast<hipStream_t>(stream);
   RR_DISPATCH_DTYPE(dtype, {
     Args<InT> a{};
     a.lane_in = static_cast<const InT*>(u);
@@ -573,6 +593,8 @@ extern "C" int rr_ssd_fwd(const void* u, const void* delta, const void* Bm, cons
     a.in_coef = static_cast<const InT*>(Bm);
     a.out_coef = static_cast<const InT*>(Cm);
     a.A = A_neg;
+    a.a_sh = A_stride_n ? N : 1;
+    a.a_sn = A_stride_n;
     a.h0 = h0;
     a.y = q.NN > 1 ? static_cast<float*>(workspace) : y;
     a.ckpt = ckpt;
@@ -584,7 +606,8 @@ extern "C" int rr_ssd_fwd(const void* u, const void* delta, const void* Bm, cons
 }
 
 extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, const void* delta,
-                          const void* Bm, const void* Cm, const float* A_neg, int dtype,
+                          const void* Bm, const void* Cm, const float* A_neg, int64_t A_stride_n,
+                          int dtype,
                           int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N, int64_t seg,
                           const float* h0, const float* ckpt, void* du, void* ddelta, void* dB,
                           void* dC, float* dA_neg, float* dh0, void* workspace,
@@ -594,6 +617,8 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
   if (!dy || !u || !delta || !Bm || !Cm || !A_neg || !ckpt || !du || !ddelta || !dB || !dC ||
       !dA_neg)
     return rr::fail(RR_EINVAL, "ssd_bwd: null pointer argument");
+  if (A_stride_n != 0 && A_stride_n != 1)
+    return rr::fail(RR_EINVAL, "ssd_bwd: A_stride_n must be 0 or 1");
   const Plan q = make_plan(B, L, H, Dh, N, seg);
   if (workspace_bytes < q.bwd_bytes || !workspace)
     return rr::fail(RR_EWORKSPACE, "ssd_bwd: workspace too small");
@@ -606,6 +631,8 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
     a.in_coef = static_cast<const InT*>(Bm);
     a.out_coef = static_cast<const InT*>(Cm);
     a.A = A_neg;
+    a.a_sh = A_stride_n ? N : 1;
+    a.a_sn = A_stride_n;
     a.h0 = h0;
     a.dy = dy;
     a.dfinal = dfinal;
@@ -622,6 +649,8 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
     f.step = a.step;
     f.in_coef = a.in_coef;
     f.A = A_neg;
+    f.a_sh = A_stride_n ? N : 1;
+    f.a_sn = A_stride_n;
     f.g_in = static_cast<InT*>(dB);
     f.g_out = static_cast<InT*>(dC);
     f.g_step = static_cast<InT*>(ddelta);

@@ -37,8 +37,8 @@ _SIGS = {
     "rr_last_error": (ctypes.c_char_p, []),
     "rr_chunk_len": (_c_i64, [_c_i64, _c_i64]),
     "rr_ssd_workspace_bytes": (_c_size, [_c_i64] * 6 + [_c_int]),
-    "rr_ssd_fwd": (_c_int, [_c_ptr] * 5 + [_c_int] + [_c_i64] * 6 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
-    "rr_ssd_bwd": (_c_int, [_c_ptr] * 7 + [_c_int] + [_c_i64] * 6 + [_c_ptr] * 9 + [_c_size, _c_ptr]),
+    "rr_ssd_fwd": (_c_int, [_c_ptr] * 5 + [_c_i64, _c_int] + [_c_i64] * 6 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
+    "rr_ssd_bwd": (_c_int, [_c_ptr] * 7 + [_c_i64, _c_int] + [_c_i64] * 6 + [_c_ptr] * 9 + [_c_size, _c_ptr]),
     "rr_gla_workspace_bytes": (_c_size, [_c_i64] * 5 + [_c_int]),
     "rr_gla_fwd": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
     "rr_gla_bwd": (_c_int, [_c_ptr] * 6 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 8 + [_c_size, _c_ptr]),
@@ -143,21 +143,22 @@ def ssd_workspace(B, L, H, Dh, N, seg, pass_, device) -> torch.Tensor | None:
     return torch.empty(n, dtype=torch.uint8, device=device) if n else None
 
 
-def ssd_fwd(u, delta, Bm, Cm, A_neg, h0, seg, y, ckpt, ws):
+def ssd_fwd(u, delta, Bm, Cm, A, a_stride_n, h0, seg, y, ckpt, ws):
+    """A is [H, N] fp32 (a_stride_n=1) or one rate per head [H] (a_stride_n=0)."""
     B, L, H, Dh = u.shape
-    N = A_neg.shape[-1]
+    N = Bm.shape[-1]
     rc = load().rr_ssd_fwd(
-        ptr(u), ptr(delta), ptr(Bm), ptr(Cm), ptr(A_neg), DTYPE_CODE[u.dtype],
+        ptr(u), ptr(delta), ptr(Bm), ptr(Cm), ptr(A), a_stride_n, DTYPE_CODE[u.dtype],
         B, L, H, Dh, N, seg, ptr(h0), ptr(y), ptr(ckpt), ptr(ws),
         0 if ws is None else ws.numel(), stream_of(u))
     _check(rc, "rr_ssd_fwd")
 
 
-def ssd_bwd(dy, dfinal, u, delta, Bm, Cm, A_neg, h0, ckpt, seg, du, ddelta, dB, dC, dA, dh0, ws):
+def ssd_bwd(dy, dfinal, u, delta, Bm, Cm, A, a_stride_n, h0, ckpt, seg, du, ddelta, dB, dC, dA, dh0, ws):
     B, L, H, Dh = u.shape
-    N = A_neg.shape[-1]
+    N = Bm.shape[-1]
     rc = load().rr_ssd_bwd(
-        ptr(dy), ptr(dfinal), ptr(u), ptr(delta), ptr(Bm), ptr(Cm), ptr(A_neg),
+        ptr(dy), ptr(dfinal), ptr(u), ptr(delta), ptr(Bm), ptr(Cm), ptr(A), a_stride_n,
         DTYPE_CODE[u.dtype], B, L, H, Dh, N, seg, ptr(h0), ptr(ckpt), ptr(du),
         ptr(ddelta), ptr(dB), ptr(dC), ptr(dA), ptr(dh0), ptr(ws),
         0 if ws is None else ws.numel(), stream_of(u))

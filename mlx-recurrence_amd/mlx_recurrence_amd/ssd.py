@@ -41,24 +41,37 @@ def _validate(u, delta, B, C, A_neg):
     return Bsz, L, H, Dh, N
 
 
+def _decay_rates(A_neg):
+    """fp32 decay rates for the kernels and their layout flag.
+
+    An ``A_neg`` that is one rate per head broadcast over N (stride 0 along N,
+    e.g. ``A[:, None].expand(H, N)``) is passed as the [H] vector with flag 0,
+    which selects the chunked MFMA kernels; any other [H, N] array is passed
+    dense with flag 1.  Both give the same results; the gradient is [H, N]."""
+    if A_neg.shape[1] > 1 and A_neg.stride(1) == 0:
+        return _lib.prep(A_neg[:, 0], torch.float32), 0
+    return _lib.prep(A_neg, torch.float32), 1
+
+
 class _SSDScan(torch.autograd.Function):
     @staticmethod
     def forward(ctx, u, delta, Bm, Cm, A_neg, h0, seg):
         dev = _lib.require_device(u, delta, Bm, Cm, A_neg, h0)
         dt = _lib.common_dtype(u, delta, Bm, Cm)
         u_, d_, B_, C_ = (_lib.prep(t, dt) for t in (u, delta, Bm, Cm))
-        A_ = _lib.prep(A_neg, torch.float32)
+        A_, a_sn = _decay_rates(A_neg)
         Bsz, L, H, Dh = u_.shape
-        N = A_.shape[1]
+        N = B_.shape[-1]
         h0_ = None if h0 is None else _lib.prep(h0, torch.float32)
         nC = L // _lib.chunk_len(L, seg)
         y = torch.empty((Bsz, L, H, Dh), dtype=torch.float32, device=dev)
         ckpt = torch.empty((Bsz, H, nC, Dh, N), dtype=torch.float32, device=dev)
         with torch.cuda.device(dev):
             ws = _lib.ssd_workspace(Bsz, L, H, Dh, N, seg, 0, dev)
-            _lib.ssd_fwd(u_, d_, B_, C_, A_, h0_, seg, y, ckpt, ws)
+            _lib.ssd_fwd(u_, d_, B_, C_, A_, a_sn, h0_, seg, y, ckpt, ws)
         ctx.save_for_backward(u_, d_, B_, C_, A_, h0_, ckpt)
         ctx.seg = seg
+        ctx.a_sn = a_sn
         ctx.set_materialize_grads(False)
         return y, ckpt[:, :, -1]
 
@@ -66,7 +79,7 @@ class _SSDScan(torch.autograd.Function):
     def backward(ctx, dy, dfinal):
         u_, d_, B_, C_, A_, h0_, ckpt = ctx.saved_tensors
         Bsz, L, H, Dh = u_.shape
-        N = A_.shape[1]
+        N = B_.shape[-1]
         dev = u_.device
         dy = torch.zeros((Bsz, L, H, Dh), dtype=torch.float32, device=dev) if dy is None else _lib.prep(dy, torch.float32)
         dfinal = None if dfinal is None else _lib.prep(dfinal, torch.float32)
@@ -75,7 +88,7 @@ class _SSDScan(torch.autograd.Function):
         dh0 = torch.empty((Bsz, H, Dh, N), dtype=torch.float32, device=dev) if ctx.needs_input_grad[5] else None
         with torch.cuda.device(dev):
             ws = _lib.ssd_workspace(Bsz, L, H, Dh, N, ctx.seg, 1, dev)
-            _lib.ssd_bwd(dy, dfinal, u_, d_, B_, C_, A_, h0_, ckpt, ctx.seg, du, dd, dB, dC, dA, dh0, ws)
+            _lib.ssd_bwd(dy, dfinal, u_, d_, B_, C_, A_, ctx.a_sn, h0_, ckpt, ctx.seg, du, dd, dB, dC, dA, dh0, ws)
         return du, dd, dB, dC, dA, dh0, None
 
 

@@ -33,7 +33,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.rr_abi_version() == 1
+    assert lib.rr_abi_version() == 2
 
 
 @pytest.mark.parametrize("L,seg,T", [(512, 32, 32), (96, 16, 16), (128, 64, 32), (96, 48, 16),
@@ -61,13 +61,15 @@ def test_rejects_bad_shapes_before_launch(lib):
 
 def test_ssd_gla_validation(lib):
     p = ctypes.c_void_p(16)
-    rc = lib.rr_ssd_fwd(p, p, p, p, p, 0, 1, 30, 2, 32, 8, 32, None, p, p, None, 0, None)
+    rc = lib.rr_ssd_fwd(p, p, p, p, p, 1, 0, 1, 30, 2, 32, 8, 32, None, p, p, None, 0, None)
     assert rc == _lib.RR_EINVAL and b"L=30" in lib.rr_last_error()
     rc = lib.rr_gla_fwd(p, p, p, p, 0, 1, 32, 2, 16, 32, None, p, p, None, 0, None)
     assert rc == _lib.RR_EINVAL and b"Dh=16" in lib.rr_last_error()
+    rc = lib.rr_ssd_fwd(p, p, p, p, p, 3, 0, 1, 32, 2, 32, 8, 32, None, p, p, None, 0, None)
+    assert rc == _lib.RR_EINVAL and b"A_stride_n" in lib.rr_last_error()
     # too-small workspace is reported, not overrun
     need = lib.rr_ssd_workspace_bytes(2, 64, 2, 64, 8, 32, 1)
     if need:
-        rc = lib.rr_ssd_bwd(p, None, p, p, p, p, p, 0, 2, 64, 2, 64, 8, 32, None, p, p, p, p, p, p, None,
+        rc = lib.rr_ssd_bwd(p, None, p, p, p, p, p, 1, 0, 2, 64, 2, 64, 8, 32, None, p, p, p, p, p, p, None,
                             p, need - 1, None)
         assert rc == _lib.RR_EWORKSPACE

@@ -184,7 +184,8 @@ def _ssd_inputs(rng, B, L, H, Dh, N, dist):
 
 
 SSD_CASES = [
-    # (B, L, H, Dh, N, seg, dtype, dist, h0, dfinal, seed)
+    # (B, L, H, Dh, N, seg, dtype, dist, h0, dfinal, seed); dist "cfg" passes A as a
+    # per-head rate broadcast over N (stride 0), the chunked-kernel layout, "ref" dense
     (2, 64, 2, 64, 8, 32, F32, "ref", False, False, 0),    # test_v2_ssd.py:26-30
     (1, 128, 3, 32, 16, 32, F32, "ref", False, False, 1),
     (2, 96, 2, 32, 8, 16, F32, "ref", False, False, 2),
@@ -194,6 +195,10 @@ SSD_CASES = [
     (1, 32, 2, 32, 24, 32, F32, "ref", True, True, 5),      # N = 24, single chunk
     (3, 512, 12, 64, 16, 32, BF16, "cfg", False, False, 11),  # BASELINE config 1, full size
     (1, 256, 4, 64, 128, 32, BF16, "cfg", True, True, 12),  # config 4's N = 128, reduced
+    (2, 512, 3, 64, 16, 32, BF16, "cfg", True, True, 13),   # chunked kernels, entering-state sums
+    (1, 128, 2, 32, 32, 32, BF16, "cfg", True, False, 14),
+    (1, 96, 2, 128, 64, 32, BF16, "cfg", False, True, 15),
+    (2, 64, 2, 64, 16, 32, BF16, "ref", False, False, 16),  # dense A, bf16: VALU engine
 ]
 
 
@@ -203,7 +208,11 @@ def test_ssd_parity(B, L, H, Dh, N, seg, dtype, dist, h0, dfinal, seed):
     rng = np.random.default_rng(seed)
     u, delta, Bm, Cm, A = _ssd_inputs(rng, B, L, H, Dh, N, dist)
     ut, dt, Bt, Ct = (to_dev(v, dtype, True) for v in (u, delta, Bm, Cm))
-    At = to_dev(A, F32, True)
+    if dist == "cfg":   # one rate per head, broadcast over N
+        Ah = to_dev(A[:, 0], F32, True)
+        At = Ah[:, None].expand(H, N)
+    else:
+        Ah = At = to_dev(A, F32, True)
     h0t = to_dev(rng.standard_normal((B, H, Dh, N)) * 0.5, F32, True) if h0 else None
     y, fs = mr.ssd_scan_with_state(ut, dt, Bt, Ct, At, seg=seg, initial_state=h0t)
     W = _w(rng, (B, L, H, Dh))
@@ -215,13 +224,15 @@ def test_ssd_parity(B, L, H, Dh, N, seg, dtype, dist, h0, dfinal, seed):
     r = [rounded(t) for t in (ut, dt, Bt, Ct, At)]
     rh0 = rounded(h0t) if h0 else None
     y_o, fs_o = orc.ssd_forward(*r, rh0)
-    grads_o = orc.ssd_backward(W, *r, rh0, Wf)
+    grads_o = list(orc.ssd_backward(W, *r, rh0, Wf))
+    if dist == "cfg":
+        grads_o[4] = grads_o[4].sum(1)   # d/dA of the broadcast per-head rate
     tol, rep = TOL[dtype], {}
     ftol = TOL[F32] if dtype == F32 else tol
     assert fs.shape == (B, H, Dh, N)
     check("y", y, y_o, ftol, rep)
     check("final", fs, fs_o, ftol, rep)
-    for name, t, g in zip(("u", "delta", "B", "C", "A_neg"), (ut, dt, Bt, Ct, At), grads_o):
+    for name, t, g in zip(("u", "delta", "B", "C", "A_neg"), (ut, dt, Bt, Ct, Ah), grads_o):
         check(f"grad_{name}", t.grad, g, tol if name != "A_neg" else max(tol, 1e-5), rep)
     if h0:
         check("grad_h0", h0t.grad, grads_o[5], tol, rep)
