@@ -150,8 +150,8 @@ def make_ssd(cfg, device, dtype):
         dB=torch.empty((B, L, H, N), dtype=dtype, device=device),
         dC=torch.empty((B, L, H, N), dtype=dtype, device=device),
         dA=torch.empty((H, N), dtype=f32, device=device),
-        wsf=_lib.ssd_workspace(B, L, H, Dh, N, seg, 0, device),
-        wsb=_lib.ssd_workspace(B, L, H, Dh, N, seg, 1, device),
+        wsf=_lib.ssd_workspace(B, L, H, Dh, N, seg, 0, dtype, 0, device),
+        wsb=_lib.ssd_workspace(B, L, H, Dh, N, seg, 0, dtype, 1, device),
     )
     es = torch.tensor([], dtype=dtype).element_size()
     n_u, n_d, n_bc, n_ck = B * L * H * Dh, B * L * H, B * L * H * N, B * H * nC * Dh * N

@@ -75,9 +75,10 @@ int64_t rr_chunk_len(int64_t L, int64_t seg);
  * ssd_scan_with_state, ssd.py:365-375).
  */
 
-/* Workspace bytes needed by rr_ssd_fwd (pass=0) or rr_ssd_bwd (pass=1). */
+/* Workspace bytes needed by rr_ssd_fwd (pass=0) or rr_ssd_bwd (pass=1) for
+ * these arguments (the kernels chosen depend on A_stride_n and dtype). */
 size_t rr_ssd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N,
-                              int64_t seg, int pass);
+                              int64_t seg, int64_t A_stride_n, int dtype, int pass);
 
 /* Replaces _ssd_forward_kernel (reference mlx_recurrence/ssd.py:54-135). */
 int rr_ssd_fwd(const void* u, const void* delta, const void* Bm, const void* Cm,

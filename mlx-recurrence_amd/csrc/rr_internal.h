@@ -41,5 +41,10 @@ bool ssd2_supported(int dtype, int64_t L, int64_t seg, int64_t Dh, int64_t N, in
 // Chunks per workgroup.
 int ssd2_pick_run(int64_t B, int64_t H, int64_t nC, int64_t N);
 int ssd2_fwd(const Ssd2Args& p, int64_t B, hipStream_t s);
+// The chunked backward covers Dh in {32, 64} and N in {16, 32} (on top of
+// ssd2_supported); its workspace holds one dA partial per (batch, head, run).
+bool ssd2_bwd_supported(int64_t Dh, int64_t N);
+size_t ssd2_bwd_ws_bytes(int64_t B, int64_t H, int64_t nC, int R, int64_t N);
+int ssd2_bwd(const Ssd2Args& p, int64_t B, hipStream_t s);
 
 }  // namespace rr

@@ -46,6 +46,9 @@ __device__ __forceinline__ f32x16_t mfma32(const u16x8_t& a, const u16x8_t& b, f
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
+// Store an fp32 value as bf16 (round to nearest even).
+__device__ __forceinline__ void st_bf16(uint16_t* p, int64_t i, float v) { p[i] = bf_bits(v); }
+
 // 16-byte fragment read from LDS (address must be 16-byte aligned).
 __device__ __forceinline__ u16x8_t frag(const uint16_t* p) {
   return *reinterpret_cast<const u16x8_t*>(p);

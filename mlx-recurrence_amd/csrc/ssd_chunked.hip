@@ -379,3 +379,578 @@ int ssd2_fwd(const Ssd2Args& p, int64_t B, hipStream_t s) {
 }
 
 }  // namespace rr
+
+// ===================================================================== backward
+//
+// Per chunk (reference adjoint ssd.py:203-268 in matrix form), with lam the
+// adjoint flowing in from later chunks (dL/dh_end through the next step),
+// h_in the chunk's entering state (forward checkpoint), cd/gam/M as above and
+// m31_t = M[31, t]:
+//   CB = C B^T, G2 = dY U^T, P = M o CB, GH = dY h_in, UL = U lam
+//   du = diag(delta) (P^T dY + diag(m31) B lam^T)
+//   Z  = (M o G2)^T C + diag(m31) UL;   dB = diag(delta) Z
+//   dC = diag(gam) GH + (M o G2 o delta_s) B
+//   d(delta)_t = a T_t + (1 - a delta_t) sum_n B_t Z_t, where
+//     T_t = sum_{d,n} lam_t h_t = R_t + sum_{t'>=t} gam X + sum_{s<=t} m31 delta Y + m31_t gam_t tr,
+//     R_t = sum_{t'>=t} sum_{s<=t} (M o delta_s o G2 o CB)[t', s],
+//     X = rowsum(GH o C), Y = rowsum(UL o B), tr = sum(lam o h_in)
+//   dA[n] = sum_t' C (K B) + sum gam cd C GH + sum m31 delta (cd_31 - cd + delta) B UL
+//           + gam_31 cd_31 sum_d lam h_in - sum delta^2 B Z,  K = M o delta_s o G2 o span
+//   lam_prev = (gam o dY)^T C + gam_31 lam
+// (derived from the per-step adjoint; checked against the float64 oracle).
+// The adjoint entering a run from later chunks is the weighted sum
+//   lam = sum_{t >= end} exp(a sum_{r=end}^{t} delta_r) dy_t C_t^T + exp(a sum_{r>=end} delta_r) dfinal.
+
+namespace {
+
+template <int DH, int NS>
+struct BwdSmem {
+  static constexpr int PD = DH + 8, PN = NS + 8;
+  uint16_t U[Q][PD];
+  uint16_t Bn[Q][PN];
+  uint16_t Cn[Q][PN];
+  uint16_t BT[NS][PQ];
+  uint16_t CT[NS][PQ];
+  uint16_t CgT_hi[NS][PQ], CgT_lo[NS][PQ];
+  uint16_t GY_hi[Q][PD], GY_lo[Q][PD];
+  uint16_t GYT_hi[DH][PQ], GYT_lo[DH][PQ];
+  uint16_t LM_hi[DH][PN], LM_lo[DH][PN];
+  uint16_t LMT_hi[NS][PD], LMT_lo[NS][PD];
+  uint16_t HT_hi[NS][PD], HT_lo[NS][PD];
+  float CB[Q][Q + 1];
+  float G2[Q][Q + 1];
+  float F[Q][Q + 1];
+  float GH[Q][NS + 1];
+  float UL[Q][NS + 1];
+  float Z[Q][NS + 1];
+  float KB[Q][NS + 1];
+  uint16_t PT_hi[Q][PQ], PT_lo[Q][PQ];
+  uint16_t MGT_hi[Q][PQ], MGT_lo[Q][PQ];
+  uint16_t MGd_hi[Q][PQ], MGd_lo[Q][PQ];
+  uint16_t Km_hi[Q][PQ], Km_lo[Q][PQ];
+  float del[Q], cd[Q], gam[Q], m31[Q], R[Q];
+  float t4[4][NS];
+};
+
+template <int DH, int NS>
+struct BwdCarrySmem {
+  uint16_t GYw_hi[4][DH][PQ], GYw_lo[4][DH][PQ];
+  uint16_t CT[4][NS][PQ];
+  float tot[rr::kMaxCarryChunks];
+};
+
+template <int DH, int NS>
+union BwdShared {
+  BwdSmem<DH, NS> m;
+  BwdCarrySmem<DH, NS> c;
+  CarryRed<DH, NS> r;
+};
+
+// Adjoint entering chunk cend-1 from chunks cend .. nC-1 (and dfinal).
+template <int DH, int NS>
+__device__ void lam_carry(const rr::Ssd2Args& p, BwdShared<DH, NS>& sm, int b, int h, int cend,
+                          float a, f32x4_t (&lam)[Cfg<DH, NS>::NBW]) {
+  using K = Cfg<DH, NS>;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t rowH = p.H;
+  for (int k = cend + w; k < p.nC; k += 4) {
+    float dv = 0.f;
+    if (lane < Q) dv = bf_val(p.delta[((int64_t)b * p.L + (int64_t)k * Q + lane) * rowH + h]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) dv += __shfl_xor(dv, o);
+    if (lane == 0) sm.c.tot[k - cend] = dv;
+  }
+  __syncthreads();
+  float total = 0.f;
+  for (int k = cend; k < p.nC; ++k) total += sm.c.tot[k - cend];
+  f32x4_t acc[K::NB];
+#pragma unroll
+  for (int j = 0; j < K::NB; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int k = cend + w; k < p.nC; k += 4) {
+    float before = 0.f;  // delta over chunks cend .. k-1
+    for (int kk = cend; kk < k; ++kk) before += sm.c.tot[kk - cend];
+    const int64_t row0 = (int64_t)b * p.L + (int64_t)k * Q;
+    float dv = 0.f;
+    if (lane < Q) dv = bf_val(p.delta[(row0 + lane) * rowH + h]);
+    const float cdv = prefix32(dv, lane);
+    const float wgt = expf(a * (before + cdv));
+    // (w o dY)^T [d][t] split, C^T [n][t]
+    for (int i = lane; i < Q * DH / 4; i += 64) {
+      const int tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
+      const float4 g = *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0);
+      const float wt = __shfl(wgt, tl);
+      const float gv[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint16_t hi, lo;
+        bf_split(wt * gv[e], hi, lo);
+        sm.c.GYw_hi[w][d0 + e][tl] = hi;
+        sm.c.GYw_lo[w][d0 + e][tl] = lo;
+      }
+    }
+    for (int i = lane; i < Q * NS / 8; i += 64) {
+      const int tl = i / (NS / 8), n0 = 8 * (i % (NS / 8));
+      const u16x8_t v = *reinterpret_cast<const u16x8_t*>(p.Cm + ((row0 + tl) * rowH + h) * NS + n0);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm.c.CT[w][n0 + e][tl] = v[e];
+    }
+    rr::wave_lds_sync();
+#pragma unroll
+    for (int j = 0; j < K::NB; ++j) {
+      const int db = j / K::NBN, nb = j % K::NBN;
+      const u16x8_t fb = frag(&sm.c.CT[w][16 * nb + (lane & 15)][8 * (lane >> 4)]);
+      acc[j] = mfma16(frag(&sm.c.GYw_hi[w][16 * db + (lane & 15)][8 * (lane >> 4)]), fb, acc[j]);
+      acc[j] = mfma16(frag(&sm.c.GYw_lo[w][16 * db + (lane & 15)][8 * (lane >> 4)]), fb, acc[j]);
+    }
+    rr::wave_lds_sync();
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < K::NB; ++j) {
+    const int db = j / K::NBN, nb = j % K::NBN;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      sm.r.part[w][16 * db + 4 * (lane >> 4) + r][16 * nb + (lane & 15)] = acc[j][r];
+  }
+  __syncthreads();
+  const float gf = expf(a * total);
+#pragma unroll
+  for (int jj = 0; jj < K::NBW; ++jj) {
+    const int j = w + 4 * jj;
+    if (j < K::NB) {
+      const int db = j / K::NBN, nb = j % K::NBN;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
+        float s = sm.r.part[0][d][n] + sm.r.part[1][d][n] + sm.r.part[2][d][n] + sm.r.part[3][d][n];
+        if (p.dfinal != nullptr) s += gf * p.dfinal[(((int64_t)b * p.H + h) * DH + d) * NS + n];
+        lam[jj][r] = s;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ int r32row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+template <int DH, int NS>
+__global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
+  using K = Cfg<DH, NS>;
+  using S = BwdSmem<DH, NS>;
+  __shared__ BwdShared<DH, NS> sm;
+  S& m = sm.m;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int cbeg = blockIdx.x * p.R;
+  const int cend = min(cbeg + p.R, p.nC);
+  const float a = p.A[(int64_t)h * p.A_stride_h];
+  const int64_t rowH = p.H;
+  const int64_t sbase = ((int64_t)b * p.H + h) * DH * NS;
+  constexpr int NBN = K::NBN;
+
+  f32x4_t lam[K::NBW];
+#pragma unroll
+  for (int jj = 0; jj < K::NBW; ++jj) lam[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if (cend < p.nC) {
+    lam_carry<DH, NS>(p, sm, b, h, cend, a, lam);
+  } else if (p.dfinal != nullptr) {
+#pragma unroll
+    for (int jj = 0; jj < K::NBW; ++jj) {
+      const int j = w + 4 * jj;
+      if (j < K::NB) {
+        const int db = j / NBN, nb = j % NBN;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          lam[jj][r] = p.dfinal[sbase + (16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)];
+      }
+    }
+  }
+  float dA_acc = 0.f;  // thread tid < NS accumulates dA[h, tid] over the run
+
+  for (int c = cend - 1; c >= cbeg; --c) {
+    const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;
+    // ------------------------------------------------ A: stage
+    for (int i = tid; i < Q * DH / 8; i += 256) {
+      const int tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
+      *reinterpret_cast<u16x8_t*>(&m.U[tl][d0]) =
+          *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0);
+    }
+    for (int i = tid; i < Q * NS / 8; i += 256) {
+      const int tl = i / (NS / 8), n0 = 8 * (i % (NS / 8));
+      const int64_t g = ((row0 + tl) * rowH + h) * NS + n0;
+      const u16x8_t vb = *reinterpret_cast<const u16x8_t*>(p.Bm + g);
+      const u16x8_t vc = *reinterpret_cast<const u16x8_t*>(p.Cm + g);
+      *reinterpret_cast<u16x8_t*>(&m.Bn[tl][n0]) = vb;
+      *reinterpret_cast<u16x8_t*>(&m.Cn[tl][n0]) = vc;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        m.BT[n0 + e][tl] = vb[e];
+        m.CT[n0 + e][tl] = vc[e];
+      }
+    }
+    for (int i = tid; i < Q * DH / 4; i += 256) {
+      const int tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
+      const float4 g = *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0);
+      const float gv[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint16_t hi, lo;
+        bf_split(gv[e], hi, lo);
+        m.GY_hi[tl][d0 + e] = hi;
+        m.GY_lo[tl][d0 + e] = lo;
+        m.GYT_hi[d0 + e][tl] = hi;
+        m.GYT_lo[d0 + e][tl] = lo;
+      }
+    }
+    if (w == 0) {
+      const float dv = lane < Q ? bf_val(p.delta[(row0 + (lane & 31)) * rowH + h]) : 0.f;
+      const float cdv = prefix32(dv, lane);
+      const float c31 = __shfl(cdv, 31);
+      if (lane < Q) {
+        m.del[lane] = dv;
+        m.cd[lane] = cdv;
+        m.gam[lane] = expf(a * cdv);
+        m.m31[lane] = expf(a * (c31 - cdv));
+      }
+    }
+    // lam (registers) and h_in (checkpoint) in the block layout
+    f32x4_t hin[K::NBW];
+#pragma unroll
+    for (int jj = 0; jj < K::NBW; ++jj) {
+      const int j = w + 4 * jj;
+      hin[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if (j < K::NB) {
+        const int db = j / NBN, nb = j % NBN;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
+          if (c > 0) hin[jj][r] = p.ckpt[(((int64_t)b * p.H + h) * p.nC + (c - 1)) * DH * NS + d * NS + n];
+          else if (p.h0 != nullptr) hin[jj][r] = p.h0[sbase + d * NS + n];
+          uint16_t hi, lo;
+          bf_split(lam[jj][r], hi, lo);
+          m.LM_hi[d][n] = hi;
+          m.LM_lo[d][n] = lo;
+          m.LMT_hi[n][d] = hi;
+          m.LMT_lo[n][d] = lo;
+          bf_split(hin[jj][r], hi, lo);
+          m.HT_hi[n][d] = hi;
+          m.HT_lo[n][d] = lo;
+        }
+      }
+    }
+    __syncthreads();
+    // ------------------------------------------------ B1: CB, G2 (32x32), GH, UL (16x16), (gam o C)^T
+    if (w == 0) {
+      f32x16_t cb = {};
+#pragma unroll
+      for (int kb = 0; kb < NS / 16; ++kb)
+        cb = mfma32(frag(&m.Cn[lane & 31][16 * kb + 8 * (lane >> 5)]),
+                    frag(&m.Bn[lane & 31][16 * kb + 8 * (lane >> 5)]), cb);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) m.CB[r32row(r, lane)][lane & 31] = cb[r];
+    } else if (w == 1) {
+      f32x16_t g2 = {};
+#pragma unroll
+      for (int kb = 0; kb < DH / 16; ++kb) {
+        const u16x8_t fb = frag(&m.U[lane & 31][16 * kb + 8 * (lane >> 5)]);
+        g2 = mfma32(frag(&m.GY_hi[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, g2);
+        g2 = mfma32(frag(&m.GY_lo[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, g2);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) m.G2[r32row(r, lane)][lane & 31] = g2[r];
+    } else {
+      // tasks: GH blocks (tb, nb) and UL blocks (sb, nb); waves 2 and 3
+      for (int task = w - 2; task < 4 * NBN; task += 2) {
+        const bool isGH = task < 2 * NBN;
+        const int tt = isGH ? task : task - 2 * NBN;
+        const int tb = tt / NBN, nb = tt % NBN;
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+        const int row = 16 * tb + (lane & 15), col = 16 * nb + (lane & 15);
+#pragma unroll
+        for (int kb = 0; kb < DH / 32; ++kb) {
+          const int k0 = 32 * kb + 8 * (lane >> 4);
+          if (isGH) {
+            const u16x8_t ah = frag(&m.GY_hi[row][k0]), al = frag(&m.GY_lo[row][k0]);
+            const u16x8_t bh = frag(&m.HT_hi[col][k0]), bl = frag(&m.HT_lo[col][k0]);
+            acc = mfma16(ah, bh, acc);
+            acc = mfma16(ah, bl, acc);
+            acc = mfma16(al, bh, acc);
+          } else {
+            const u16x8_t fa = frag(&m.U[row][k0]);
+            acc = mfma16(fa, frag(&m.LMT_hi[col][k0]), acc);
+            acc = mfma16(fa, frag(&m.LMT_lo[col][k0]), acc);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * tb + 4 * (lane >> 4) + r;
+          if (isGH) m.GH[t][col] = acc[r];
+          else m.UL[t][col] = acc[r];
+        }
+      }
+      for (int i = tid - 128; i < NS * Q; i += 128) {
+        const int n = i / Q, t = i % Q;
+        uint16_t hi, lo;
+        bf_split(m.gam[t] * bf_val(m.Cn[t][n]), hi, lo);
+        m.CgT_hi[n][t] = hi;
+        m.CgT_lo[n][t] = lo;
+      }
+    }
+    __syncthreads();
+    // ------------------------------------------------ B2: masked products, rectangle sums
+    if (w == 0) {
+      // P = M o CB, stored transposed [t][t']
+      const int s = lane & 31;
+      const float cds = m.cd[s];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int tp = r32row(r, lane);
+        const float v = (s <= tp) ? expf(a * (m.cd[tp] - cds)) * m.CB[tp][s] : 0.f;
+        uint16_t hi, lo;
+        bf_split(v, hi, lo);
+        m.PT_hi[s][tp] = hi;
+        m.PT_lo[s][tp] = lo;
+      }
+    } else if (w == 1) {
+      const int s = lane & 31;
+      const float cds = m.cd[s], ds = m.del[s];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int tp = r32row(r, lane);
+        const float mg = (s <= tp) ? expf(a * (m.cd[tp] - cds)) * m.G2[tp][s] : 0.f;
+        uint16_t hi, lo;
+        bf_split(mg, hi, lo);
+        m.MGT_hi[s][tp] = hi;
+        m.MGT_lo[s][tp] = lo;
+        bf_split(mg * ds, hi, lo);
+        m.MGd_hi[tp][s] = hi;
+        m.MGd_lo[tp][s] = lo;
+        bf_split(mg * ds * (m.cd[tp] - cds + ds), hi, lo);
+        m.Km_hi[tp][s] = hi;
+        m.Km_lo[tp][s] = lo;
+      }
+    } else if (w == 2) {
+      // F[t'][t] = sum_{s <= t} E[t'][s]; lane t' < 32 walks its row
+      if (lane < Q) {
+        const int tp = lane;
+        const float cdt = m.cd[tp];
+        float run = 0.f;
+        for (int s = 0; s < Q; ++s) {
+          if (s <= tp) run += expf(a * (cdt - m.cd[s])) * m.del[s] * m.G2[tp][s] * m.CB[tp][s];
+          m.F[tp][s] = run;
+        }
+      }
+      rr::wave_lds_sync();
+      if (lane < Q) {
+        float rs = 0.f;
+        for (int tp = lane; tp < Q; ++tp) rs += m.F[tp][lane];
+        m.R[lane] = rs;
+      }
+    }
+    __syncthreads();
+    // ------------------------------------------------ C: du, Z/dB, dC, KB, lam_prev
+    const float gam31 = m.gam[Q - 1];
+    if (w < DH / 32) {
+      const int d0 = 32 * w;
+      f32x16_t a1 = {}, a2 = {};
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int k0 = 16 * kb + 8 * (lane >> 5);
+        const u16x8_t ph = frag(&m.PT_hi[lane & 31][k0]), pl = frag(&m.PT_lo[lane & 31][k0]);
+        const u16x8_t gh = frag(&m.GYT_hi[d0 + (lane & 31)][k0]), gl = frag(&m.GYT_lo[d0 + (lane & 31)][k0]);
+        a1 = mfma32(ph, gh, a1);
+        a1 = mfma32(ph, gl, a1);
+        a1 = mfma32(pl, gh, a1);
+      }
+#pragma unroll
+      for (int kb = 0; kb < NS / 16; ++kb) {
+        const int k0 = 16 * kb + 8 * (lane >> 5);
+        const u16x8_t fa = frag(&m.Bn[lane & 31][k0]);
+        a2 = mfma32(fa, frag(&m.LM_hi[d0 + (lane & 31)][k0]), a2);
+        a2 = mfma32(fa, frag(&m.LM_lo[d0 + (lane & 31)][k0]), a2);
+      }
+      const int d = d0 + (lane & 31);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = r32row(r, lane);
+        rr::st_bf16(p.du, ((row0 + t) * rowH + h) * DH + d, m.del[t] * (a1[r] + m.m31[t] * a2[r]));
+      }
+    } else {
+      // Z, dC, KB blocks over the waves >= DH/32
+      const int nw = 4 - DH / 32;
+      for (int task = w - DH / 32; task < 6 * NBN; task += nw) {
+        const int kind = task / (2 * NBN), tt = task % (2 * NBN);
+        const int tb = tt / NBN, nb = tt % NBN;
+        const int row = 16 * tb + (lane & 15), col = 16 * nb + (lane & 15);
+        const int k0 = 8 * (lane >> 4);
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+        if (kind == 0) {
+          const u16x8_t fb = frag(&m.CT[col][k0]);
+          acc = mfma16(frag(&m.MGT_hi[row][k0]), fb, acc);
+          acc = mfma16(frag(&m.MGT_lo[row][k0]), fb, acc);
+        } else if (kind == 1) {
+          const u16x8_t fb = frag(&m.BT[col][k0]);
+          acc = mfma16(frag(&m.MGd_hi[row][k0]), fb, acc);
+          acc = mfma16(frag(&m.MGd_lo[row][k0]), fb, acc);
+        } else {
+          const u16x8_t fb = frag(&m.BT[col][k0]);
+          acc = mfma16(frag(&m.Km_hi[row][k0]), fb, acc);
+          acc = mfma16(frag(&m.Km_lo[row][k0]), fb, acc);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * tb + 4 * (lane >> 4) + r;
+          const int64_t gi = ((row0 + t) * rowH + h) * NS + col;
+          if (kind == 0) {
+            const float z = acc[r] + m.m31[t] * m.UL[t][col];
+            m.Z[t][col] = z;
+            rr::st_bf16(p.dB, gi, m.del[t] * z);
+          } else if (kind == 1) {
+            rr::st_bf16(p.dC, gi, m.gam[t] * m.GH[t][col] + acc[r]);
+          } else {
+            m.KB[t][col] = acc[r];
+          }
+        }
+      }
+    }
+    // lam_prev = (gam o dY)^T C + gam31 lam; sum_d lam h_in per n (for tr and dA)
+    {
+      float t4p[NBN];
+#pragma unroll
+      for (int nb = 0; nb < NBN; ++nb) t4p[nb] = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < K::NBW; ++jj) {
+        const int j = w + 4 * jj;
+        if (j < K::NB) {
+          const int db = j / NBN, nb = j % NBN;
+          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+          const int k0 = 8 * (lane >> 4);
+          const u16x8_t ah = frag(&m.GYT_hi[16 * db + (lane & 15)][k0]);
+          const u16x8_t al = frag(&m.GYT_lo[16 * db + (lane & 15)][k0]);
+          const u16x8_t bh = frag(&m.CgT_hi[16 * nb + (lane & 15)][k0]);
+          const u16x8_t bl = frag(&m.CgT_lo[16 * nb + (lane & 15)][k0]);
+          acc = mfma16(ah, bh, acc);
+          acc = mfma16(ah, bl, acc);
+          acc = mfma16(al, bh, acc);
+          float part = 0.f;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            part += lam[jj][r] * hin[jj][r];
+            lam[jj][r] = acc[r] + gam31 * lam[jj][r];
+          }
+          part += __shfl_xor(part, 16);
+          part += __shfl_xor(part, 32);
+#pragma unroll
+          for (int q = 0; q < NBN; ++q)
+            if (q == nb) t4p[q] += part;
+        }
+      }
+      if (lane < 16) {
+#pragma unroll
+        for (int nb = 0; nb < NBN; ++nb) m.t4[w][16 * nb + lane] = t4p[nb];
+      }
+    }
+    __syncthreads();
+    // ------------------------------------------------ D: d(delta), dA
+    if (w == 0) {
+      const int t = lane & 31;
+      float X = 0.f, Y = 0.f, BZ = 0.f, tr = 0.f;
+      for (int n = 0; n < NS; ++n) {
+        const float bv = bf_val(m.Bn[t][n]);
+        X += m.GH[t][n] * bf_val(m.Cn[t][n]);
+        Y += m.UL[t][n] * bv;
+        BZ += bv * m.Z[t][n];
+        tr += m.t4[0][n] + m.t4[1][n] + m.t4[2][n] + m.t4[3][n];
+      }
+      const float dt = m.del[t], gt = m.gam[t], mt = m.m31[t];
+      // suffix over t' >= t of gam X; prefix over s <= t of m31 delta Y
+      float suf = gt * X, pre = mt * dt * Y;
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) {
+        const float xs = __shfl_down(suf, o, 32);
+        const float xp = __shfl_up(pre, o, 32);
+        if (t + o < 32) suf += xs;
+        if (t >= o) pre += xp;
+      }
+      const float T = m.R[t] + suf + pre + mt * gt * tr;
+      if (lane < Q) rr::st_bf16(p.ddelta, (row0 + t) * rowH + h, a * T + (1.f - a * dt) * BZ);
+    } else if (w == 1 && lane < NS) {
+      const int n = lane;
+      const float cd31 = m.cd[Q - 1];
+      float s = gam31 * cd31 * (m.t4[0][n] + m.t4[1][n] + m.t4[2][n] + m.t4[3][n]);
+      for (int t = 0; t < Q; ++t) {
+        const float bv = bf_val(m.Bn[t][n]), cv = bf_val(m.Cn[t][n]);
+        const float dt = m.del[t];
+        s += cv * m.KB[t][n] + m.gam[t] * m.cd[t] * cv * m.GH[t][n] +
+             m.m31[t] * dt * (cd31 - m.cd[t] + dt) * bv * m.UL[t][n] - dt * dt * bv * m.Z[t][n];
+      }
+      dA_acc += s;
+    }
+    __syncthreads();
+  }
+  // per-run dA partial and the initial-state gradient
+  if (w == 1 && lane < NS) {
+    const int nR = gridDim.x;
+    p.ws[(((int64_t)b * p.H + h) * nR + blockIdx.x) * NS + lane] = dA_acc;
+  }
+  if (cbeg == 0 && p.dh0 != nullptr) {
+#pragma unroll
+    for (int jj = 0; jj < K::NBW; ++jj) {
+      const int j = w + 4 * jj;
+      if (j < K::NB) {
+        const int db = j / NBN, nb = j % NBN;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          p.dh0[sbase + (16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)] = lam[jj][r];
+      }
+    }
+  }
+}
+
+// dA[h, n] = sum over batch rows and runs, in a fixed order.
+__global__ void ssd2_dA_kernel(const float* __restrict__ part, float* __restrict__ dA, int Bsz,
+                               int H, int nR, int NS) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= H * NS) return;
+  const int h = i / NS, n = i % NS;
+  float s = 0.f;
+  for (int b = 0; b < Bsz; ++b)
+    for (int r = 0; r < nR; ++r) s += part[(((int64_t)b * H + h) * nR + r) * NS + n];
+  dA[i] = s;
+}
+
+template <int DH, int NS>
+int launch_bwd(const rr::Ssd2Args& p, int64_t B, hipStream_t s) {
+  const int nR = (p.nC + p.R - 1) / p.R;
+  hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS>), dim3(nR, p.H, (unsigned)B), dim3(256), 0, s, p);
+  if (int rc = rr::check_launch("ssd chunked backward")) return rc;
+  const int n = p.H * p.NS;
+  hipLaunchKernelGGL(ssd2_dA_kernel, dim3((n + 127) / 128), dim3(128), 0, s, p.ws, p.dA, (int)B, p.H,
+                     nR, p.NS);
+  return rr::check_launch("ssd chunked backward dA");
+}
+
+}  // namespace
+
+namespace rr {
+
+bool ssd2_bwd_supported(int64_t Dh, int64_t N) {
+  return (Dh == 32 || Dh == 64) && (N == 16 || N == 32);
+}
+
+size_t ssd2_bwd_ws_bytes(int64_t B, int64_t H, int64_t nC, int R, int64_t N) {
+  const int64_t nR = (nC + R - 1) / R;
+  return (size_t)(B * H * nR * N) * sizeof(float);
+}
+
+int ssd2_bwd(const Ssd2Args& p, int64_t B, hipStream_t s) {
+  switch (p.DH * 1000 + p.NS) {
+    case 32016: return launch_bwd<32, 16>(p, B, s);
+    case 32032: return launch_bwd<32, 32>(p, B, s);
+    case 64016: return launch_bwd<64, 16>(p, B, s);
+    case 64032: return launch_bwd<64, 32>(p, B, s);
+    default: return fail(RR_EUNSUPPORTED, "ssd chunked backward: unsupported (Dh, N)");
+  }
+}
+
+}  // namespace rr

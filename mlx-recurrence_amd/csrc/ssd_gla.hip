@@ -551,8 +551,13 @@ int launch_bwd(Args<InT> a, FinArgs<InT> f, const Plan& q, int64_t B, hipStream_
 
 // ====================================================================== SSD
 extern "C" size_t rr_ssd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N,
-                                         int64_t seg, int pass) {
+                                         int64_t seg, int64_t A_stride_n, int dtype, int pass) {
   if (B <= 0 || L <= 0 || H <= 0 || Dh <= 0 || N <= 0 || rr::chunk_len(L, seg) == 0) return 0;
+  if (rr::ssd2_supported(dtype, L, seg, Dh, N, A_stride_n)) {
+    if (pass == 0) return 0;
+    if (rr::ssd2_bwd_supported(Dh, N))
+      return rr::ssd2_bwd_ws_bytes(B, H, L / 32, rr::ssd2_pick_run(B, H, L / 32, N), N);
+  }
   const Plan q = make_plan(B, L, H, Dh, N, seg);
   return pass == 0 ? q.fwd_bytes : q.bwd_bytes;
 }
@@ -619,6 +624,32 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
     return rr::fail(RR_EINVAL, "ssd_bwd: null pointer argument");
   if (A_stride_n != 0 && A_stride_n != 1)
     return rr::fail(RR_EINVAL, "ssd_bwd: A_stride_n must be 0 or 1");
+  if (rr::ssd2_supported(dtype, L, seg, Dh, N, A_stride_n) && rr::ssd2_bwd_supported(Dh, N)) {
+    const int nC = (int)(L / 32);
+    const int R = rr::ssd2_pick_run(B, H, nC, N);
+    if (!workspace || workspace_bytes < rr::ssd2_bwd_ws_bytes(B, H, nC, R, N))
+      return rr::fail(RR_EWORKSPACE, "ssd_bwd: workspace too small");
+    rr::Ssd2Args a{};
+    a.u = static_cast<const uint16_t*>(u);
+    a.delta = static_cast<const uint16_t*>(delta);
+    a.Bm = static_cast<const uint16_t*>(Bm);
+    a.Cm = static_cast<const uint16_t*>(Cm);
+    a.A = A_neg;
+    a.A_stride_h = 1;
+    a.h0 = h0;
+    a.ckpt = const_cast<float*>(ckpt);
+    a.dy = dy;
+    a.dfinal = dfinal;
+    a.du = static_cast<uint16_t*>(du);
+    a.ddelta = static_cast<uint16_t*>(ddelta);
+    a.dB = static_cast<uint16_t*>(dB);
+    a.dC = static_cast<uint16_t*>(dC);
+    a.dA = dA_neg;
+    a.dh0 = dh0;
+    a.ws = static_cast<float*>(workspace);
+    a.L = (int)L; a.H = (int)H; a.DH = (int)Dh; a.NS = (int)N; a.nC = nC; a.R = R;
+    return rr::ssd2_bwd(a, B, static_cast<hipStream_t>(stream));
+  }
   const Plan q = make_plan(B, L, H, Dh, N, seg);
   if (workspace_bytes < q.bwd_bytes || !workspace)
     return rr::fail(RR_EWORKSPACE, "ssd_bwd: workspace too small");

@@ -36,7 +36,7 @@ _SIGS = {
     "rr_abi_version": (_c_int, []),
     "rr_last_error": (ctypes.c_char_p, []),
     "rr_chunk_len": (_c_i64, [_c_i64, _c_i64]),
-    "rr_ssd_workspace_bytes": (_c_size, [_c_i64] * 6 + [_c_int]),
+    "rr_ssd_workspace_bytes": (_c_size, [_c_i64] * 7 + [_c_int, _c_int]),
     "rr_ssd_fwd": (_c_int, [_c_ptr] * 5 + [_c_i64, _c_int] + [_c_i64] * 6 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
     "rr_ssd_bwd": (_c_int, [_c_ptr] * 7 + [_c_i64, _c_int] + [_c_i64] * 6 + [_c_ptr] * 9 + [_c_size, _c_ptr]),
     "rr_gla_workspace_bytes": (_c_size, [_c_i64] * 5 + [_c_int]),
@@ -138,8 +138,8 @@ def common_dtype(*tensors: torch.Tensor) -> torch.dtype:
 
 
 # ---------------------------------------------------------------- SSD
-def ssd_workspace(B, L, H, Dh, N, seg, pass_, device) -> torch.Tensor | None:
-    n = int(load().rr_ssd_workspace_bytes(B, L, H, Dh, N, seg, pass_))
+def ssd_workspace(B, L, H, Dh, N, seg, a_stride_n, dtype, pass_, device) -> torch.Tensor | None:
+    n = int(load().rr_ssd_workspace_bytes(B, L, H, Dh, N, seg, a_stride_n, DTYPE_CODE[dtype], pass_))
     return torch.empty(n, dtype=torch.uint8, device=device) if n else None
 
 

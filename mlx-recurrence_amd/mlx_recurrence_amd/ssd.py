@@ -67,7 +67,7 @@ class _SSDScan(torch.autograd.Function):
         y = torch.empty((Bsz, L, H, Dh), dtype=torch.float32, device=dev)
         ckpt = torch.empty((Bsz, H, nC, Dh, N), dtype=torch.float32, device=dev)
         with torch.cuda.device(dev):
-            ws = _lib.ssd_workspace(Bsz, L, H, Dh, N, seg, 0, dev)
+            ws = _lib.ssd_workspace(Bsz, L, H, Dh, N, seg, a_sn, dt, 0, dev)
             _lib.ssd_fwd(u_, d_, B_, C_, A_, a_sn, h0_, seg, y, ckpt, ws)
         ctx.save_for_backward(u_, d_, B_, C_, A_, h0_, ckpt)
         ctx.seg = seg
@@ -87,7 +87,7 @@ class _SSDScan(torch.autograd.Function):
         dA = torch.empty((H, N), dtype=torch.float32, device=dev)
         dh0 = torch.empty((Bsz, H, Dh, N), dtype=torch.float32, device=dev) if ctx.needs_input_grad[5] else None
         with torch.cuda.device(dev):
-            ws = _lib.ssd_workspace(Bsz, L, H, Dh, N, ctx.seg, 1, dev)
+            ws = _lib.ssd_workspace(Bsz, L, H, Dh, N, ctx.seg, ctx.a_sn, u_.dtype, 1, dev)
             _lib.ssd_bwd(dy, dfinal, u_, d_, B_, C_, A_, ctx.a_sn, h0_, ckpt, ctx.seg, du, dd, dB, dC, dA, dh0, ws)
         return du, dd, dB, dC, dA, dh0, None
 

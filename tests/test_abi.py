@@ -68,7 +68,7 @@ def test_ssd_gla_validation(lib):
     rc = lib.rr_ssd_fwd(p, p, p, p, p, 3, 0, 1, 32, 2, 32, 8, 32, None, p, p, None, 0, None)
     assert rc == _lib.RR_EINVAL and b"A_stride_n" in lib.rr_last_error()
     # too-small workspace is reported, not overrun
-    need = lib.rr_ssd_workspace_bytes(2, 64, 2, 64, 8, 32, 1)
+    need = lib.rr_ssd_workspace_bytes(2, 64, 2, 64, 8, 32, 1, 0, 1)
     if need:
         rc = lib.rr_ssd_bwd(p, None, p, p, p, p, p, 1, 0, 2, 64, 2, 64, 8, 32, None, p, p, p, p, p, p, None,
                             p, need - 1, None)
