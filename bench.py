@@ -9,15 +9,19 @@ inputs, fp32 state/accumulation, seg=32 — plus config 2 (GLA) reported beside
 it.  A "step" is one forward + backward pass over one batch of synthetic
 inputs resident in HBM: the forward kernel(s) then the backward kernel(s),
 launched through the same C-ABI calls the autograd Function makes.  The step is
-captured once in a HIP graph and replayed; W warm-up steps, then K timed steps
-bracketed by synchronisation.  The eager torch.autograd path is timed too and
+captured in a HIP graph (G consecutive steps per graph, G the largest divisor
+of K up to 20, so the ~15 us host cost of a graph launch is amortised as it
+would be inside a model's graph) and replayed; W warm-up steps, then K timed
+steps bracketed by synchronisation.  The eager torch.autograd path is timed too and
 reported as "eager_ms_per_step".
 
-Roofline: the dominant kernel of the step is isolated by capturing each pass
-into a HIP graph, deleting every other node and replaying the single-node graph
-between HIP events on the stream it runs on; achieved = algorithmic bytes of
-the kernel's pass (inputs + outputs + checkpoints at their API dtypes, the
-per-unit figures of the workload) / that kernel's average duration.
+Roofline: the dominant kernel of the step is isolated by capturing 50 copies
+of its pass into a HIP graph, deleting every other node, re-chaining the 50
+copies of the kernel and timing one launch of that graph between HIP events on
+the stream it runs on; achieved = algorithmic bytes of the kernel's pass
+(inputs + outputs + checkpoints at their API dtypes, the per-unit figures of
+the workload) / that kernel's average duration (which therefore includes the
+dispatch gap between dependent launches).
 
 CPU baseline: the float64 oracle (oracle/recurrence_oracle.py, forward +
 explicit adjoint) on the same workload's shape, on the host cores, rank 0
@@ -61,6 +65,7 @@ class _Hip:
         L.hipGraphLaunch.argtypes = [vp, vp]
         L.hipGraphExecDestroy.argtypes = [vp]
         L.hipGraphDestroy.argtypes = [vp]
+        L.hipGraphAddDependencies.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), sz]
 
     def ok(self, rc, what):
         if rc != 0:
@@ -82,30 +87,18 @@ class _Hip:
         self.ok(self.lib.hipGraphGetNodes(graph, arr, ctypes.byref(n)), "hipGraphGetNodes")
         return list(arr)
 
-    def kernel_count(self, graph):
-        cnt = 0
+    def kernel_nodes(self, graph):
+        out = []
         for nd in self.nodes(graph):
             t = ctypes.c_int(-1)
             self.ok(self.lib.hipGraphNodeGetType(nd, ctypes.byref(t)), "hipGraphNodeGetType")
-            cnt += t.value == 0  # hipGraphNodeTypeKernel
-        return cnt
+            if t.value == 0:  # hipGraphNodeTypeKernel
+                out.append(nd)
+        return out
 
-    def single_kernel_exec(self, graph, k):
-        """Executable graph holding only the k-th kernel node of `graph`."""
-        clone = ctypes.c_void_p()
-        self.ok(self.lib.hipGraphClone(ctypes.byref(clone), graph), "hipGraphClone")
-        kidx = 0
-        for nd in self.nodes(clone):
-            t = ctypes.c_int(-1)
-            self.ok(self.lib.hipGraphNodeGetType(nd, ctypes.byref(t)), "hipGraphNodeGetType")
-            if t.value == 0 and kidx == k:
-                kidx += 1
-                continue
-            kidx += t.value == 0
-            self.ok(self.lib.hipGraphDestroyNode(nd), "hipGraphDestroyNode")
-        ex = ctypes.c_void_p()
-        self.ok(self.lib.hipGraphInstantiate(ctypes.byref(ex), clone, None, None, 0), "hipGraphInstantiate")
-        return ex, clone
+    def add_edge(self, graph, a, b):
+        fa, fb = (ctypes.c_void_p * 1)(a), (ctypes.c_void_p * 1)(b)
+        self.ok(self.lib.hipGraphAddDependencies(graph, fa, fb, 1), "hipGraphAddDependencies")
 
     def launch(self, ex, stream):
         self.ok(self.lib.hipGraphLaunch(ex, stream), "hipGraphLaunch")
@@ -367,51 +360,64 @@ def measure(name, steps, warmup, dtype, device, with_cpu):
         w["bwd"]()
     torch.cuda.synchronize()
 
-    # one HIP graph per step (forward then backward)
+    # G steps per HIP graph (a graph launch costs ~15 us of host time on this
+    # platform, so one step per graph would measure the launch, not the GPU)
+    G = max(g for g in range(1, 21) if steps % g == 0)
     with torch.cuda.stream(stream):
-        step_graph = hip.capture(sh, lambda: (w["fwd"](), w["bwd"]()))
+        step_graph = hip.capture(sh, lambda: [(w["fwd"](), w["bwd"]()) for _ in range(G)])
     ex = ctypes.c_void_p()
     hip.ok(hip.lib.hipGraphInstantiate(ctypes.byref(ex), step_graph, None, None, 0), "hipGraphInstantiate")
-    for _ in range(warmup):
+    for _ in range(max(1, warmup // G)):
         hip.launch(ex, sh)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
+    for _ in range(steps // G):
         hip.launch(ex, sh)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_step = (t1 - t0) * 1e3 / steps
 
-    # per-pass and per-kernel durations with HIP events on `stream`
-    def event_time(launch, reps):
-        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        for _ in range(3):
-            launch()
-        st.record(stream)
-        for _ in range(reps):
-            launch()
-        en.record(stream)
-        en.synchronize()
-        return st.elapsed_time(en) * 1e3 / reps  # us
+    # Per-pass and per-kernel durations: a graph of REPS back-to-back copies of
+    # the pass (or of one of its kernels, the other nodes deleted and the copies
+    # re-chained), timed with HIP events on `stream`; per launch = total / REPS.
+    # Includes the dispatch gap between dependent launches.
+    REPS = 50
 
-    reps = max(steps, 20)
+    def chain_time(fn, keep=None):
+        with torch.cuda.stream(stream):
+            g = hip.capture(sh, lambda: [fn() for _ in range(REPS)])
+        knodes = hip.kernel_nodes(g)
+        per = len(knodes) // REPS
+        if keep is not None:
+            kept = [knodes[i * per + keep] for i in range(REPS)]
+            keep_set = {n for n in kept}
+            for nd in hip.nodes(g):
+                if nd not in keep_set:
+                    hip.ok(hip.lib.hipGraphDestroyNode(nd), "hipGraphDestroyNode")
+            for i in range(REPS - 1):
+                hip.add_edge(g, kept[i], kept[i + 1])
+        gex = ctypes.c_void_p()
+        hip.ok(hip.lib.hipGraphInstantiate(ctypes.byref(gex), g, None, None, 0), "hipGraphInstantiate")
+        best = None
+        for _ in range(5):
+            st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            st.record(stream)
+            hip.launch(gex, sh)
+            en.record(stream)
+            en.synchronize()
+            us = st.elapsed_time(en) * 1e3 / REPS
+            best = us if best is None else min(best, us)
+        hip.lib.hipGraphExecDestroy(gex)
+        hip.lib.hipGraphDestroy(g)
+        return best, per
+
     kernels = []
     pass_us = {}
     for pname, fn, nbytes in (("fwd", w["fwd"], w["fwd_bytes"]), ("bwd", w["bwd"], w["bwd_bytes"])):
-        with torch.cuda.stream(stream):
-            g = hip.capture(sh, fn)
-        pex = ctypes.c_void_p()
-        hip.ok(hip.lib.hipGraphInstantiate(ctypes.byref(pex), g, None, None, 0), "hipGraphInstantiate")
-        pass_us[pname] = event_time(lambda: hip.launch(pex, sh), reps)
-        nk = hip.kernel_count(g)
+        pass_us[pname], nk = chain_time(fn)
         for k in range(nk):
-            kex, kg = hip.single_kernel_exec(g, k)
-            us = event_time(lambda: hip.launch(kex, sh), reps)
+            us = pass_us[pname] if nk == 1 else chain_time(fn, keep=k)[0]
             kernels.append(dict(pass_=pname, index=k, us=us, pass_bytes=nbytes, n_kernels=nk))
-            hip.lib.hipGraphExecDestroy(kex)
-            hip.lib.hipGraphDestroy(kg)
-        hip.lib.hipGraphExecDestroy(pex)
-        hip.lib.hipGraphDestroy(g)
     dom = max(kernels, key=lambda r: r["us"])
     achieved = dom["pass_bytes"] / (dom["us"] * 1e-6) / 1e9  # GB/s
 

@@ -67,6 +67,8 @@ struct CarrySmem {
   uint16_t BwT_hi[4][NS][PQ];
   uint16_t BwT_lo[4][NS][PQ];
   float tot[rr::kMaxCarryChunks];
+  float after[rr::kMaxCarryChunks];   // delta summed over the later chunks before the start
+  float total;
 };
 
 template <int DH, int NS>
@@ -97,67 +99,113 @@ __device__ __forceinline__ float prefix32(float v, int lane) {
   return v;
 }
 
-// Entering state of chunk `cstart` (>= 1): weighted sum over steps < start, with
-// the four waves taking every 4th earlier chunk; result in the caller's blocks.
+// Entering state of chunk `cstart` (>= 1): weighted sum over steps < start.
+// The four waves take every 4th earlier chunk; each wave issues the loads of
+// up to kBatch of its chunks at once (one memory latency per batch), then
+// stages and multiplies them one by one; the four partial sums are added in a
+// fixed order.
 template <int DH, int NS>
 __device__ void carry_in(const rr::Ssd2Args& p, FwdShared<DH, NS>& sm, int b, int h, int cstart,
                          float a, f32x4_t (&hst)[Cfg<DH, NS>::NBW]) {
   using K = Cfg<DH, NS>;
+  constexpr int kBatch = 4;
+  constexpr int UV = Q * DH / 8 / 64;               // u16x8 of U per lane per chunk
+  constexpr int BV = (Q * NS / 8 + 63) / 64;        // u16x8 of B per lane per chunk
+  constexpr int KPW = rr::kMaxCarryChunks / 4;      // chunks per wave, at most
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t rowH = p.H;
-  // 1. per-chunk delta totals
-  for (int k = w; k < cstart; k += 4) {
-    float dv = 0.f;
-    if (lane < Q) dv = bf_val(p.delta[((int64_t)b * p.L + (int64_t)k * Q + lane) * rowH + h]);
+  // 1. per-chunk delta totals (all loads first), suffix sums by one thread
+  {
+    float dv[KPW];
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) dv += __shfl_xor(dv, o);
-    if (lane == 0) sm.c.tot[k] = dv;
+    for (int j = 0; j < KPW; ++j) {
+      const int k = w + 4 * j;
+      dv[j] = (k < cstart && lane < Q) ? bf_val(p.delta[((int64_t)b * p.L + (int64_t)k * Q + lane) * rowH + h]) : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) dv[j] += __shfl_xor(dv[j], o);
+      const int k = w + 4 * j;
+      if (lane == 0 && k < cstart) sm.c.tot[k] = dv[j];
+    }
   }
   __syncthreads();
-  float total = 0.f;  // sum of delta over [0, start)
-  for (int k = 0; k < cstart; ++k) total += sm.c.tot[k];
+  if (tid == 0) {
+    float acc = 0.f;
+    for (int k = cstart - 1; k >= 0; --k) {
+      sm.c.after[k] = acc;
+      acc += sm.c.tot[k];
+    }
+    sm.c.total = acc;
+  }
+  __syncthreads();
 
   f32x4_t acc[K::NB];
 #pragma unroll
   for (int j = 0; j < K::NB; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int k = w; k < cstart; k += 4) {
-    float after = 0.f;  // sum of delta over chunks k+1 .. cstart-1
-    for (int kk = k + 1; kk < cstart; ++kk) after += sm.c.tot[kk];
-    // stage U^T of chunk k
-    for (int i = lane; i < Q * DH / 8; i += 64) {
-      const int tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
-      const u16x8_t v = *reinterpret_cast<const u16x8_t*>(
-          p.u + (((int64_t)b * p.L + (int64_t)k * Q + tl) * rowH + h) * DH + d0);
+  for (int k0 = w; k0 < cstart; k0 += 4 * kBatch) {
+    u16x8_t uv[kBatch][UV], bv[kBatch][BV];
+    float dl[kBatch];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sm.c.Ut[w][d0 + e][tl] = v[e];
-    }
-    // weights w_s = exp(a (sum_{r=s+1}^{31} delta_r + after)) delta_s, lanes 0..31
-    float dv = 0.f;
-    if (lane < Q) dv = bf_val(p.delta[((int64_t)b * p.L + (int64_t)k * Q + lane) * rowH + h]);
-    const float cdv = prefix32(dv, lane);
-    const float c31 = __shfl(cdv, 31);
-    const float wgt = expf(a * (c31 - cdv + after)) * dv;
-    // (w o B)^T [n][s], split
-    for (int i = lane; i < Q * NS; i += 64) {
-      const int s = i / NS, n = i % NS;
-      const float ws = __shfl(wgt, s);
-      const float v = ws * bf_val(p.Bm[((int64_t)b * p.L + (int64_t)k * Q + s) * rowH * NS + (int64_t)h * NS + n]);
-      uint16_t hi, lo;
-      bf_split(v, hi, lo);
-      sm.c.BwT_hi[w][n][s] = hi;
-      sm.c.BwT_lo[w][n][s] = lo;
-    }
-    rr::wave_lds_sync();
+    for (int q = 0; q < kBatch; ++q) {
+      const int k = k0 + 4 * q;
+      const bool ok = k < cstart;
+      const int64_t row0 = (int64_t)b * p.L + (int64_t)k * Q;
 #pragma unroll
-    for (int j = 0; j < K::NB; ++j) {
-      const int db = j / K::NBN, nb = j % K::NBN;
-      const u16x8_t fa = frag(&sm.c.Ut[w][16 * db + (lane & 15)][8 * (lane >> 4)]);
-      acc[j] = mfma16(fa, frag(&sm.c.BwT_hi[w][16 * nb + (lane & 15)][8 * (lane >> 4)]), acc[j]);
-      acc[j] = mfma16(fa, frag(&sm.c.BwT_lo[w][16 * nb + (lane & 15)][8 * (lane >> 4)]), acc[j]);
+      for (int v = 0; v < UV; ++v) {
+        const int i = lane + 64 * v, tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
+        uv[q][v] = ok ? *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0) : u16x8_t{};
+      }
+#pragma unroll
+      for (int v = 0; v < BV; ++v) {
+        const int i = lane + 64 * v, tl = i / (NS / 8), n0 = 8 * (i % (NS / 8));
+        bv[q][v] = (ok && i < Q * NS / 8)
+                       ? *reinterpret_cast<const u16x8_t*>(p.Bm + ((row0 + tl) * rowH + h) * NS + n0)
+                       : u16x8_t{};
+      }
+      dl[q] = (ok && lane < Q) ? bf_val(p.delta[(row0 + lane) * rowH + h]) : 0.f;
     }
-    rr::wave_lds_sync();
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int k = k0 + 4 * q;
+      if (k >= cstart) break;
+      const float cdv = prefix32(dl[q], lane);
+      const float c31 = __shfl(cdv, 31);
+      const float wgt = __expf(a * (c31 - cdv + sm.c.after[k])) * dl[q];
+#pragma unroll
+      for (int v = 0; v < UV; ++v) {
+        const int i = lane + 64 * v, tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sm.c.Ut[w][d0 + e][tl] = uv[q][v][e];
+      }
+#pragma unroll
+      for (int v = 0; v < BV; ++v) {
+        const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+        const float ws = __shfl(wgt, tl);
+        if (i < Q * NS / 8) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            uint16_t hi, lo;
+            bf_split(ws * bf_val(bv[q][v][e]), hi, lo);
+            sm.c.BwT_hi[w][n0 + e][tl] = hi;
+            sm.c.BwT_lo[w][n0 + e][tl] = lo;
+          }
+        }
+      }
+      rr::wave_lds_sync();
+#pragma unroll
+      for (int j = 0; j < K::NB; ++j) {
+        const int db = j / K::NBN, nb = j % K::NBN;
+        const u16x8_t fa = frag(&sm.c.Ut[w][16 * db + (lane & 15)][8 * (lane >> 4)]);
+        acc[j] = mfma16(fa, frag(&sm.c.BwT_hi[w][16 * nb + (lane & 15)][8 * (lane >> 4)]), acc[j]);
+        acc[j] = mfma16(fa, frag(&sm.c.BwT_lo[w][16 * nb + (lane & 15)][8 * (lane >> 4)]), acc[j]);
+      }
+      rr::wave_lds_sync();
+    }
   }
+  const float g0 = __expf(a * sm.c.total);
   __syncthreads();  // staging area is reused for the reduction
 #pragma unroll
   for (int j = 0; j < K::NB; ++j) {
@@ -167,7 +215,6 @@ __device__ void carry_in(const rr::Ssd2Args& p, FwdShared<DH, NS>& sm, int b, in
       sm.r.part[w][16 * db + 4 * (lane >> 4) + r][16 * nb + (lane & 15)] = acc[j][r];
   }
   __syncthreads();
-  const float g0 = expf(a * total);
 #pragma unroll
   for (int jj = 0; jj < K::NBW; ++jj) {
     const int j = w + 4 * jj;
@@ -176,9 +223,9 @@ __device__ void carry_in(const rr::Ssd2Args& p, FwdShared<DH, NS>& sm, int b, in
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
-        float s = sm.r.part[0][d][n] + sm.r.part[1][d][n] + sm.r.part[2][d][n] + sm.r.part[3][d][n];
-        if (p.h0 != nullptr) s += g0 * p.h0[(((int64_t)b * p.H + h) * DH + d) * NS + n];
-        hst[jj][r] = s;
+        float sum = sm.r.part[0][d][n] + sm.r.part[1][d][n] + sm.r.part[2][d][n] + sm.r.part[3][d][n];
+        if (p.h0 != nullptr) sum += g0 * p.h0[(((int64_t)b * p.H + h) * DH + d) * NS + n];
+        hst[jj][r] = sum;
       }
     }
   }
@@ -217,20 +264,42 @@ __global__ __launch_bounds__(256) void ssd2_fwd_kernel(rr::Ssd2Args p) {
 
   for (int c = cbeg; c < cend; ++c) {
     const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;  // first (b, t) row of the chunk
-    // ---- stage the chunk's inputs
-    for (int i = tid; i < Q * DH / 8; i += 256) {
-      const int tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
-      const u16x8_t v = *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0);
+    // ---- stage the chunk's inputs (all loads issued before any use)
+    {
+      constexpr int UV = (Q * DH / 8 + 255) / 256, BV = (Q * NS / 8 + 255) / 256;
+      u16x8_t uv[UV], bv[BV], cv[BV];
+      float dv = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sm.f.Ut[d0 + e][tl] = v[e];
+      for (int v = 0; v < UV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
+        uv[v] = i < Q * DH / 8 ? *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0) : u16x8_t{};
+      }
+#pragma unroll
+      for (int v = 0; v < BV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+        const int64_t g = ((row0 + tl) * rowH + h) * NS + n0;
+        bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Bm + g) : u16x8_t{};
+        cv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Cm + g) : u16x8_t{};
+      }
+      if (tid < Q) dv = bf_val(p.delta[(row0 + tid) * rowH + h]);
+#pragma unroll
+      for (int v = 0; v < UV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
+        if (i < Q * DH / 8) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sm.f.Ut[d0 + e][tl] = uv[v][e];
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < BV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+        if (i < Q * NS / 8) {
+          *reinterpret_cast<u16x8_t*>(&sm.f.B[tl][n0]) = bv[v];
+          *reinterpret_cast<u16x8_t*>(&sm.f.C[tl][n0]) = cv[v];
+        }
+      }
+      if (tid < Q) sm.f.del[tid] = dv;
     }
-    for (int i = tid; i < Q * NS / 8; i += 256) {
-      const int tl = i / (NS / 8), n0 = 8 * (i % (NS / 8));
-      const int64_t g = ((row0 + tl) * rowH + h) * NS + n0;
-      *reinterpret_cast<u16x8_t*>(&sm.f.B[tl][n0]) = *reinterpret_cast<const u16x8_t*>(p.Bm + g);
-      *reinterpret_cast<u16x8_t*>(&sm.f.C[tl][n0]) = *reinterpret_cast<const u16x8_t*>(p.Cm + g);
-    }
-    if (tid < Q) sm.f.del[tid] = bf_val(p.delta[(row0 + tid) * rowH + h]);
     __syncthreads();
     // ---- per-step scalars (wave 0) and h_in split (every wave, its blocks)
     if (w == 0) {
@@ -239,8 +308,8 @@ __global__ __launch_bounds__(256) void ssd2_fwd_kernel(rr::Ssd2Args p) {
       const float c31 = __shfl(cdv, 31);
       if (lane < Q) {
         sm.f.cd[lane] = cdv;
-        sm.f.gam[lane] = expf(a * cdv);
-        sm.f.wend[lane] = expf(a * (c31 - cdv)) * dv;
+        sm.f.gam[lane] = __expf(a * cdv);
+        sm.f.wend[lane] = __expf(a * (c31 - cdv)) * dv;
       }
     }
 #pragma unroll
@@ -271,7 +340,7 @@ __global__ __launch_bounds__(256) void ssd2_fwd_kernel(rr::Ssd2Args p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int t = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const float v = (s <= t) ? expf(a * (sm.f.cd[t] - cds)) * ds * cb[r] : 0.f;
+        const float v = (s <= t) ? __expf(a * (sm.f.cd[t] - cds)) * ds * cb[r] : 0.f;
         uint16_t hi, lo;
         bf_split(v, hi, lo);
         sm.f.W_hi[t][s] = hi;
@@ -429,7 +498,9 @@ struct BwdSmem {
   uint16_t MGd_hi[Q][PQ], MGd_lo[Q][PQ];
   uint16_t Km_hi[Q][PQ], Km_lo[Q][PQ];
   float del[Q], cd[Q], gam[Q], m31[Q], R[Q];
+  float kGH[Q], kUL[Q], kZ[Q];
   float t4[4][NS];
+  float dAp[4][4][NS];
 };
 
 template <int DH, int NS>
@@ -437,6 +508,8 @@ struct BwdCarrySmem {
   uint16_t GYw_hi[4][DH][PQ], GYw_lo[4][DH][PQ];
   uint16_t CT[4][NS][PQ];
   float tot[rr::kMaxCarryChunks];
+  float before[rr::kMaxCarryChunks];  // delta summed over the later chunks before chunk k
+  float total;
 };
 
 template <int DH, int NS>
@@ -446,64 +519,109 @@ union BwdShared {
   CarryRed<DH, NS> r;
 };
 
-// Adjoint entering chunk cend-1 from chunks cend .. nC-1 (and dfinal).
+// Adjoint entering chunk cend-1 from chunks cend .. nC-1 (and dfinal).  Same
+// scheme as carry_in: every 4th later chunk per wave, loads batched.
 template <int DH, int NS>
 __device__ void lam_carry(const rr::Ssd2Args& p, BwdShared<DH, NS>& sm, int b, int h, int cend,
                           float a, f32x4_t (&lam)[Cfg<DH, NS>::NBW]) {
   using K = Cfg<DH, NS>;
+  constexpr int kBatch = 2;
+  constexpr int GV = Q * DH / 4 / 64;               // float4 of dY per lane per chunk
+  constexpr int CV = (Q * NS / 8 + 63) / 64;        // u16x8 of C per lane per chunk
+  constexpr int KPW = rr::kMaxCarryChunks / 4;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t rowH = p.H;
-  for (int k = cend + w; k < p.nC; k += 4) {
-    float dv = 0.f;
-    if (lane < Q) dv = bf_val(p.delta[((int64_t)b * p.L + (int64_t)k * Q + lane) * rowH + h]);
+  const int nl = p.nC - cend;                       // number of later chunks
+  {
+    float dv[KPW];
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) dv += __shfl_xor(dv, o);
-    if (lane == 0) sm.c.tot[k - cend] = dv;
+    for (int j = 0; j < KPW; ++j) {
+      const int k = cend + w + 4 * j;
+      dv[j] = (k < p.nC && lane < Q) ? bf_val(p.delta[((int64_t)b * p.L + (int64_t)k * Q + lane) * rowH + h]) : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) dv[j] += __shfl_xor(dv[j], o);
+      if (lane == 0 && w + 4 * j < nl) sm.c.tot[w + 4 * j] = dv[j];
+    }
   }
   __syncthreads();
-  float total = 0.f;
-  for (int k = cend; k < p.nC; ++k) total += sm.c.tot[k - cend];
+  if (tid == 0) {
+    float acc = 0.f;
+    for (int k = 0; k < nl; ++k) {
+      sm.c.before[k] = acc;
+      acc += sm.c.tot[k];
+    }
+    sm.c.total = acc;
+  }
+  __syncthreads();
   f32x4_t acc[K::NB];
 #pragma unroll
   for (int j = 0; j < K::NB; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  for (int k = cend + w; k < p.nC; k += 4) {
-    float before = 0.f;  // delta over chunks cend .. k-1
-    for (int kk = cend; kk < k; ++kk) before += sm.c.tot[kk - cend];
-    const int64_t row0 = (int64_t)b * p.L + (int64_t)k * Q;
-    float dv = 0.f;
-    if (lane < Q) dv = bf_val(p.delta[(row0 + lane) * rowH + h]);
-    const float cdv = prefix32(dv, lane);
-    const float wgt = expf(a * (before + cdv));
-    // (w o dY)^T [d][t] split, C^T [n][t]
-    for (int i = lane; i < Q * DH / 4; i += 64) {
-      const int tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
-      const float4 g = *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0);
-      const float wt = __shfl(wgt, tl);
-      const float gv[4] = {g.x, g.y, g.z, g.w};
+  for (int k0 = w; k0 < nl; k0 += 4 * kBatch) {
+    float4 gv[kBatch][GV];
+    u16x8_t cv[kBatch][CV];
+    float dl[kBatch];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        uint16_t hi, lo;
-        bf_split(wt * gv[e], hi, lo);
-        sm.c.GYw_hi[w][d0 + e][tl] = hi;
-        sm.c.GYw_lo[w][d0 + e][tl] = lo;
+    for (int q = 0; q < kBatch; ++q) {
+      const int kk = k0 + 4 * q;
+      const bool ok = kk < nl;
+      const int64_t row0 = (int64_t)b * p.L + (int64_t)(cend + kk) * Q;
+#pragma unroll
+      for (int v = 0; v < GV; ++v) {
+        const int i = lane + 64 * v, tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
+        gv[q][v] = ok ? *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0)
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
       }
-    }
-    for (int i = lane; i < Q * NS / 8; i += 64) {
-      const int tl = i / (NS / 8), n0 = 8 * (i % (NS / 8));
-      const u16x8_t v = *reinterpret_cast<const u16x8_t*>(p.Cm + ((row0 + tl) * rowH + h) * NS + n0);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sm.c.CT[w][n0 + e][tl] = v[e];
+      for (int v = 0; v < CV; ++v) {
+        const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+        cv[q][v] = (ok && i < Q * NS / 8)
+                       ? *reinterpret_cast<const u16x8_t*>(p.Cm + ((row0 + tl) * rowH + h) * NS + n0)
+                       : u16x8_t{};
+      }
+      dl[q] = (ok && lane < Q) ? bf_val(p.delta[(row0 + lane) * rowH + h]) : 0.f;
     }
-    rr::wave_lds_sync();
 #pragma unroll
-    for (int j = 0; j < K::NB; ++j) {
-      const int db = j / K::NBN, nb = j % K::NBN;
-      const u16x8_t fb = frag(&sm.c.CT[w][16 * nb + (lane & 15)][8 * (lane >> 4)]);
-      acc[j] = mfma16(frag(&sm.c.GYw_hi[w][16 * db + (lane & 15)][8 * (lane >> 4)]), fb, acc[j]);
-      acc[j] = mfma16(frag(&sm.c.GYw_lo[w][16 * db + (lane & 15)][8 * (lane >> 4)]), fb, acc[j]);
+    for (int q = 0; q < kBatch; ++q) {
+      const int kk = k0 + 4 * q;
+      if (kk >= nl) break;
+      const float cdv = prefix32(dl[q], lane);
+      const float wgt = __expf(a * (sm.c.before[kk] + cdv));
+#pragma unroll
+      for (int v = 0; v < GV; ++v) {
+        const int i = lane + 64 * v, tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
+        const float wt = __shfl(wgt, tl);
+        const float g4[4] = {gv[q][v].x, gv[q][v].y, gv[q][v].z, gv[q][v].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          uint16_t hi, lo;
+          bf_split(wt * g4[e], hi, lo);
+          sm.c.GYw_hi[w][d0 + e][tl] = hi;
+          sm.c.GYw_lo[w][d0 + e][tl] = lo;
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < CV; ++v) {
+        const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+        if (i < Q * NS / 8) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sm.c.CT[w][n0 + e][tl] = cv[q][v][e];
+        }
+      }
+      rr::wave_lds_sync();
+#pragma unroll
+      for (int j = 0; j < K::NB; ++j) {
+        const int db = j / K::NBN, nb = j % K::NBN;
+        const u16x8_t fb = frag(&sm.c.CT[w][16 * nb + (lane & 15)][8 * (lane >> 4)]);
+        acc[j] = mfma16(frag(&sm.c.GYw_hi[w][16 * db + (lane & 15)][8 * (lane >> 4)]), fb, acc[j]);
+        acc[j] = mfma16(frag(&sm.c.GYw_lo[w][16 * db + (lane & 15)][8 * (lane >> 4)]), fb, acc[j]);
+      }
+      rr::wave_lds_sync();
     }
-    rr::wave_lds_sync();
   }
+  const float gf = __expf(a * sm.c.total);
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < K::NB; ++j) {
@@ -513,7 +631,6 @@ __device__ void lam_carry(const rr::Ssd2Args& p, BwdShared<DH, NS>& sm, int b, i
       sm.r.part[w][16 * db + 4 * (lane >> 4) + r][16 * nb + (lane & 15)] = acc[j][r];
   }
   __syncthreads();
-  const float gf = expf(a * total);
 #pragma unroll
   for (int jj = 0; jj < K::NBW; ++jj) {
     const int j = w + 4 * jj;
@@ -522,9 +639,9 @@ __device__ void lam_carry(const rr::Ssd2Args& p, BwdShared<DH, NS>& sm, int b, i
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
-        float s = sm.r.part[0][d][n] + sm.r.part[1][d][n] + sm.r.part[2][d][n] + sm.r.part[3][d][n];
-        if (p.dfinal != nullptr) s += gf * p.dfinal[(((int64_t)b * p.H + h) * DH + d) * NS + n];
-        lam[jj][r] = s;
+        float sum = sm.r.part[0][d][n] + sm.r.part[1][d][n] + sm.r.part[2][d][n] + sm.r.part[3][d][n];
+        if (p.dfinal != nullptr) sum += gf * p.dfinal[(((int64_t)b * p.H + h) * DH + d) * NS + n];
+        lam[jj][r] = sum;
       }
     }
   }
@@ -569,72 +686,112 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
 
   for (int c = cend - 1; c >= cbeg; --c) {
     const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;
-    // ------------------------------------------------ A: stage
-    for (int i = tid; i < Q * DH / 8; i += 256) {
-      const int tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
-      *reinterpret_cast<u16x8_t*>(&m.U[tl][d0]) =
-          *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0);
-    }
-    for (int i = tid; i < Q * NS / 8; i += 256) {
-      const int tl = i / (NS / 8), n0 = 8 * (i % (NS / 8));
-      const int64_t g = ((row0 + tl) * rowH + h) * NS + n0;
-      const u16x8_t vb = *reinterpret_cast<const u16x8_t*>(p.Bm + g);
-      const u16x8_t vc = *reinterpret_cast<const u16x8_t*>(p.Cm + g);
-      *reinterpret_cast<u16x8_t*>(&m.Bn[tl][n0]) = vb;
-      *reinterpret_cast<u16x8_t*>(&m.Cn[tl][n0]) = vc;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        m.BT[n0 + e][tl] = vb[e];
-        m.CT[n0 + e][tl] = vc[e];
-      }
-    }
-    for (int i = tid; i < Q * DH / 4; i += 256) {
-      const int tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
-      const float4 g = *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0);
-      const float gv[4] = {g.x, g.y, g.z, g.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        uint16_t hi, lo;
-        bf_split(gv[e], hi, lo);
-        m.GY_hi[tl][d0 + e] = hi;
-        m.GY_lo[tl][d0 + e] = lo;
-        m.GYT_hi[d0 + e][tl] = hi;
-        m.GYT_lo[d0 + e][tl] = lo;
-      }
-    }
-    if (w == 0) {
-      const float dv = lane < Q ? bf_val(p.delta[(row0 + (lane & 31)) * rowH + h]) : 0.f;
-      const float cdv = prefix32(dv, lane);
-      const float c31 = __shfl(cdv, 31);
-      if (lane < Q) {
-        m.del[lane] = dv;
-        m.cd[lane] = cdv;
-        m.gam[lane] = expf(a * cdv);
-        m.m31[lane] = expf(a * (c31 - cdv));
-      }
-    }
-    // lam (registers) and h_in (checkpoint) in the block layout
+    // ------------------------------------------------ A: stage (all loads first)
     f32x4_t hin[K::NBW];
+    {
+      constexpr int UV = (Q * DH / 8 + 255) / 256, BV = (Q * NS / 8 + 255) / 256, GV = (Q * DH / 4 + 255) / 256;
+      u16x8_t uv[UV], bv[BV], cv[BV];
+      float4 gv[GV];
+      float dv = 0.f;
 #pragma unroll
-    for (int jj = 0; jj < K::NBW; ++jj) {
-      const int j = w + 4 * jj;
-      hin[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      if (j < K::NB) {
-        const int db = j / NBN, nb = j % NBN;
+      for (int v = 0; v < UV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
+        uv[v] = i < Q * DH / 8 ? *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0) : u16x8_t{};
+      }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
-          if (c > 0) hin[jj][r] = p.ckpt[(((int64_t)b * p.H + h) * p.nC + (c - 1)) * DH * NS + d * NS + n];
-          else if (p.h0 != nullptr) hin[jj][r] = p.h0[sbase + d * NS + n];
-          uint16_t hi, lo;
-          bf_split(lam[jj][r], hi, lo);
-          m.LM_hi[d][n] = hi;
-          m.LM_lo[d][n] = lo;
-          m.LMT_hi[n][d] = hi;
-          m.LMT_lo[n][d] = lo;
-          bf_split(hin[jj][r], hi, lo);
-          m.HT_hi[n][d] = hi;
-          m.HT_lo[n][d] = lo;
+      for (int v = 0; v < BV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+        const int64_t g = ((row0 + tl) * rowH + h) * NS + n0;
+        bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Bm + g) : u16x8_t{};
+        cv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Cm + g) : u16x8_t{};
+      }
+#pragma unroll
+      for (int v = 0; v < GV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (DH / 4)) & (Q - 1), d0 = 4 * (i % (DH / 4));
+        gv[v] = i < Q * DH / 4 ? *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      if (w == 0 && lane < Q) dv = bf_val(p.delta[(row0 + lane) * rowH + h]);
+      const float* hsrc = c > 0 ? p.ckpt + (((int64_t)b * p.H + h) * p.nC + (c - 1)) * DH * NS
+                                : (p.h0 != nullptr ? p.h0 + sbase : nullptr);
+#pragma unroll
+      for (int jj = 0; jj < K::NBW; ++jj) {
+        const int j = w + 4 * jj;
+        hin[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        if (j < K::NB && hsrc != nullptr) {
+          const int db = j / NBN, nb = j % NBN;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) hin[jj][r] = hsrc[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)];
+        }
+      }
+      // LDS writes
+#pragma unroll
+      for (int v = 0; v < UV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
+        if (i < Q * DH / 8) *reinterpret_cast<u16x8_t*>(&m.U[tl][d0]) = uv[v];
+      }
+#pragma unroll
+      for (int v = 0; v < BV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+        if (i < Q * NS / 8) {
+          *reinterpret_cast<u16x8_t*>(&m.Bn[tl][n0]) = bv[v];
+          *reinterpret_cast<u16x8_t*>(&m.Cn[tl][n0]) = cv[v];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            m.BT[n0 + e][tl] = bv[v][e];
+            m.CT[n0 + e][tl] = cv[v][e];
+          }
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < GV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (DH / 4)) & (Q - 1), d0 = 4 * (i % (DH / 4));
+        if (i < Q * DH / 4) {
+          const float g4[4] = {gv[v].x, gv[v].y, gv[v].z, gv[v].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            uint16_t hi, lo;
+            bf_split(g4[e], hi, lo);
+            m.GY_hi[tl][d0 + e] = hi;
+            m.GY_lo[tl][d0 + e] = lo;
+            m.GYT_hi[d0 + e][tl] = hi;
+            m.GYT_lo[d0 + e][tl] = lo;
+          }
+        }
+      }
+      if (w == 0) {
+        const float cdv = prefix32(dv, lane);
+        const float c31 = __shfl(cdv, 31);
+        if (lane < Q) {
+          const float gt = __expf(a * cdv), mt = __expf(a * (c31 - cdv));
+          m.del[lane] = dv;
+          m.cd[lane] = cdv;
+          m.gam[lane] = gt;
+          m.m31[lane] = mt;
+          // per-step coefficients of the dA terms
+          m.kGH[lane] = gt * cdv;
+          m.kUL[lane] = mt * dv * (c31 - cdv + dv);
+          m.kZ[lane] = dv * dv;
+        }
+      }
+#pragma unroll
+      for (int jj = 0; jj < K::NBW; ++jj) {
+        const int j = w + 4 * jj;
+        if (j < K::NB) {
+          const int db = j / NBN, nb = j % NBN;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
+            uint16_t hi, lo;
+            bf_split(lam[jj][r], hi, lo);
+            m.LM_hi[d][n] = hi;
+            m.LM_lo[d][n] = lo;
+            m.LMT_hi[n][d] = hi;
+            m.LMT_lo[n][d] = lo;
+            bf_split(hin[jj][r], hi, lo);
+            m.HT_hi[n][d] = hi;
+            m.HT_lo[n][d] = lo;
+          }
         }
       }
     }
@@ -705,45 +862,63 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int tp = r32row(r, lane);
-        const float v = (s <= tp) ? expf(a * (m.cd[tp] - cds)) * m.CB[tp][s] : 0.f;
+        const float v = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * m.CB[tp][s] : 0.f;
         uint16_t hi, lo;
         bf_split(v, hi, lo);
         m.PT_hi[s][tp] = hi;
         m.PT_lo[s][tp] = lo;
       }
-    } else if (w == 1) {
+    } else if (w == 1 || w == 3) {
+      // M o G2 -> (M o G2)^T [t][t'] (wave 1); (M o G2 o delta_s) and K [t'][s] (wave 3)
       const int s = lane & 31;
       const float cds = m.cd[s], ds = m.del[s];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int tp = r32row(r, lane);
-        const float mg = (s <= tp) ? expf(a * (m.cd[tp] - cds)) * m.G2[tp][s] : 0.f;
+        const float mg = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * m.G2[tp][s] : 0.f;
         uint16_t hi, lo;
-        bf_split(mg, hi, lo);
-        m.MGT_hi[s][tp] = hi;
-        m.MGT_lo[s][tp] = lo;
-        bf_split(mg * ds, hi, lo);
-        m.MGd_hi[tp][s] = hi;
-        m.MGd_lo[tp][s] = lo;
-        bf_split(mg * ds * (m.cd[tp] - cds + ds), hi, lo);
-        m.Km_hi[tp][s] = hi;
-        m.Km_lo[tp][s] = lo;
+        if (w == 1) {
+          bf_split(mg, hi, lo);
+          m.MGT_hi[s][tp] = hi;
+          m.MGT_lo[s][tp] = lo;
+        } else {
+          bf_split(mg * ds, hi, lo);
+          m.MGd_hi[tp][s] = hi;
+          m.MGd_lo[tp][s] = lo;
+          bf_split(mg * ds * (m.cd[tp] - cds + ds), hi, lo);
+          m.Km_hi[tp][s] = hi;
+          m.Km_lo[tp][s] = lo;
+        }
       }
-    } else if (w == 2) {
-      // F[t'][t] = sum_{s <= t} E[t'][s]; lane t' < 32 walks its row
+    } else {
+      // E = M o delta_s o G2 o CB in the 32x32 layout; F = row prefix over s; R = column suffix over t'
+      const int s = lane & 31;
+      const float cds = m.cd[s], ds = m.del[s];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int tp = r32row(r, lane);
+        m.F[tp][s] = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * ds * m.G2[tp][s] * m.CB[tp][s] : 0.f;
+      }
+      rr::wave_lds_sync();
       if (lane < Q) {
-        const int tp = lane;
-        const float cdt = m.cd[tp];
+        float row[Q];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) row[q] = m.F[lane][q];
         float run = 0.f;
-        for (int s = 0; s < Q; ++s) {
-          if (s <= tp) run += expf(a * (cdt - m.cd[s])) * m.del[s] * m.G2[tp][s] * m.CB[tp][s];
-          m.F[tp][s] = run;
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+          run += row[q];
+          m.F[lane][q] = run;
         }
       }
       rr::wave_lds_sync();
       if (lane < Q) {
+        float col[Q];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) col[q] = m.F[q][lane];
         float rs = 0.f;
-        for (int tp = lane; tp < Q; ++tp) rs += m.F[tp][lane];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) rs += (q >= lane) ? col[q] : 0.f;
         m.R[lane] = rs;
       }
     }
@@ -874,19 +1049,27 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
       }
       const float T = m.R[t] + suf + pre + mt * gt * tr;
       if (lane < Q) rr::st_bf16(p.ddelta, (row0 + t) * rowH + h, a * T + (1.f - a * dt) * BZ);
-    } else if (w == 1 && lane < NS) {
-      const int n = lane;
-      const float cd31 = m.cd[Q - 1];
-      float s = gam31 * cd31 * (m.t4[0][n] + m.t4[1][n] + m.t4[2][n] + m.t4[3][n]);
-      for (int t = 0; t < Q; ++t) {
-        const float bv = bf_val(m.Bn[t][n]), cv = bf_val(m.Cn[t][n]);
-        const float dt = m.del[t];
-        s += cv * m.KB[t][n] + m.gam[t] * m.cd[t] * cv * m.GH[t][n] +
-             m.m31[t] * dt * (cd31 - m.cd[t] + dt) * bv * m.UL[t][n] - dt * dt * bv * m.Z[t][n];
+    } else {
+      // dA terms: lane -> (n = lane % 16 + 16 q, t in one of 12 row groups); waves 1..3
+      for (int n0 = 0; n0 < NS; n0 += 16) {
+        const int n = n0 + (lane & 15), tq = (w - 1) * 4 + (lane >> 4);
+        float sum = 0.f;
+        for (int t = tq; t < Q; t += 12) {
+          const float bv = bf_val(m.Bn[t][n]), cv = bf_val(m.Cn[t][n]);
+          sum += cv * (m.KB[t][n] + m.kGH[t] * m.GH[t][n]) + bv * (m.kUL[t] * m.UL[t][n] - m.kZ[t] * m.Z[t][n]);
+        }
+        sum += __shfl_xor(sum, 16);
+        sum += __shfl_xor(sum, 32);
+        if (lane < 16) m.dAp[w][0][n] = sum;
       }
-      dA_acc += s;
     }
+    // gam_31 cd_31 sum_d lam h_in (read before the barrier: the next chunk rewrites cd)
+    const float gc = gam31 * m.cd[Q - 1];
     __syncthreads();
+    if (w == 1 && lane < NS) {
+      dA_acc += m.dAp[1][0][lane] + m.dAp[2][0][lane] + m.dAp[3][0][lane] +
+                gc * (m.t4[0][lane] + m.t4[1][lane] + m.t4[2][lane] + m.t4[3][lane]);
+    }
   }
   // per-run dA partial and the initial-state gradient
   if (w == 1 && lane < NS) {
