@@ -60,32 +60,8 @@ struct FwdSmem {
   float del[Q], cd[Q], gam[Q], wend[Q];
 };
 
-// Per-wave staging for the entering-state sum, plus the fixed-order reduction.
 template <int DH, int NS>
-struct CarrySmem {
-  uint16_t Ut[4][DH][PQ];
-  uint16_t BwT_hi[4][NS][PQ];
-  uint16_t BwT_lo[4][NS][PQ];
-  float tot[rr::kMaxCarryChunks];
-  float after[rr::kMaxCarryChunks];   // delta summed over the later chunks before the start
-  float total;
-};
-
-template <int DH, int NS>
-struct CarryRed {
-  float part[4][DH][NS];
-};
-
-// The entering-state sum is used only with N <= 32 (see ssd2_pick_run), so the
-// larger shapes do not reserve LDS for it.
-template <int DH, int NS, bool kCarry = (NS <= 32)>
 union FwdShared {
-  FwdSmem<DH, NS> f;
-  CarrySmem<DH, NS> c;
-  CarryRed<DH, NS> r;
-};
-template <int DH, int NS>
-union FwdShared<DH, NS, false> {
   FwdSmem<DH, NS> f;
 };
 
@@ -99,140 +75,170 @@ __device__ __forceinline__ float prefix32(float v, int lane) {
   return v;
 }
 
-// Entering state of chunk `cstart` (>= 1): weighted sum over steps < start.
-// The four waves take every 4th earlier chunk; each wave issues the loads of
-// up to kBatch of its chunks at once (one memory latency per batch), then
-// stages and multiplies them one by one; the four partial sums are added in a
-// fixed order.
+// Pipelined mode (several workgroups per head).  Three kernels per pass:
+//  1. ssd2_agg_kernel, one wave per chunk k, writes the chunk's aggregate and
+//     its delta total tot_k:
+//       forward:  S_k = U_k^T diag(w) B_k, the state the chunk adds from a zero
+//                 start (into checkpoint slot k);
+//       backward: G_k = (gam o dY_k)^T C_k, the adjoint the chunk sends back to
+//                 its start (into the workspace).
+//  2. ssd2_pass_kernel, one thread per state element, walks the chunks in order:
+//       forward:  h_k = exp(a tot_k) h_{k-1} + S_k   (h_{-1} = h0), into slot k
+//       backward: lam_k = adjoint of the state leaving chunk k,
+//                 lam_{nC-1} = dfinal, lam_{k-1} = exp(a tot_k) lam_k + G_k,
+//                 and dh0 = exp(a tot_0) lam_0 + G_0.
+//  3. the main kernel, one workgroup per chunk, reads its entering state
+//     (and, backward, lam_k) and does the chunk's dense products.
 template <int DH, int NS>
-__device__ void carry_in(const rr::Ssd2Args& p, FwdShared<DH, NS>& sm, int b, int h, int cstart,
-                         float a, f32x4_t (&hst)[Cfg<DH, NS>::NBW]) {
-  using K = Cfg<DH, NS>;
-  constexpr int kBatch = 4;
-  constexpr int UV = Q * DH / 8 / 64;               // u16x8 of U per lane per chunk
-  constexpr int BV = (Q * NS / 8 + 63) / 64;        // u16x8 of B per lane per chunk
-  constexpr int KPW = rr::kMaxCarryChunks / 4;      // chunks per wave, at most
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t rowH = p.H;
-  // 1. per-chunk delta totals (all loads first), suffix sums by one thread
-  {
-    float dv[KPW];
+__global__ __launch_bounds__(64) void ssd2_agg_kernel(rr::Ssd2Args p, int kind) {
+  constexpr int NBN = NS / 16, NB = (DH / 16) * NBN;
+  __shared__ uint16_t XT_hi[DH][PQ], XT_lo[DH][PQ];   // kind 0: U^T [d][s] (hi only); kind 1: (gam o dY)^T
+  __shared__ uint16_t YT_hi[NS][PQ], YT_lo[NS][PQ];   // kind 0: (w o B)^T split; kind 1: C^T (hi only)
+  const int lane = threadIdx.x;
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const float a = p.A[(int64_t)h * p.A_stride_h];
+  const int64_t rowH = p.H, row0 = (int64_t)b * p.L + (int64_t)c * Q;
+  constexpr int UV = Q * DH / 8 / 64, GV = Q * DH / 4 / 64, BV = (Q * NS / 8 + 63) / 64;
+  // loads first
+  u16x8_t uv[UV], bv[BV];
+  float4 gv[GV];
+  if (kind == 0) {
 #pragma unroll
-    for (int j = 0; j < KPW; ++j) {
-      const int k = w + 4 * j;
-      dv[j] = (k < cstart && lane < Q) ? bf_val(p.delta[((int64_t)b * p.L + (int64_t)k * Q + lane) * rowH + h]) : 0.f;
+    for (int v = 0; v < UV; ++v) {
+      const int i = lane + 64 * v, tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
+      uv[v] = *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0);
     }
+  } else {
 #pragma unroll
-    for (int j = 0; j < KPW; ++j) {
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) dv[j] += __shfl_xor(dv[j], o);
-      const int k = w + 4 * j;
-      if (lane == 0 && k < cstart) sm.c.tot[k] = dv[j];
+    for (int v = 0; v < GV; ++v) {
+      const int i = lane + 64 * v, tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
+      gv[v] = *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0);
     }
   }
-  __syncthreads();
-  if (tid == 0) {
-    float acc = 0.f;
-    for (int k = cstart - 1; k >= 0; --k) {
-      sm.c.after[k] = acc;
-      acc += sm.c.tot[k];
-    }
-    sm.c.total = acc;
+  const uint16_t* bsrc = kind == 0 ? p.Bm : p.Cm;
+#pragma unroll
+  for (int v = 0; v < BV; ++v) {
+    const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+    bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(bsrc + ((row0 + tl) * rowH + h) * NS + n0) : u16x8_t{};
   }
-  __syncthreads();
-
-  f32x4_t acc[K::NB];
+  const float dv = lane < Q ? bf_val(p.delta[(row0 + lane) * rowH + h]) : 0.f;
+  const float cdv = prefix32(dv, lane);
+  const float c31 = __shfl(cdv, 31);
+  // kind 0: w_s = exp(a (c31 - cd_s)) delta_s ; kind 1: gam_t = exp(a cd_t)
+  const float wt = kind == 0 ? __expf(a * (c31 - cdv)) * dv : __expf(a * cdv);
+  if (kind == 0) {
 #pragma unroll
-  for (int j = 0; j < K::NB; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  for (int k0 = w; k0 < cstart; k0 += 4 * kBatch) {
-    u16x8_t uv[kBatch][UV], bv[kBatch][BV];
-    float dl[kBatch];
+    for (int v = 0; v < UV; ++v) {
+      const int i = lane + 64 * v, tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
 #pragma unroll
-    for (int q = 0; q < kBatch; ++q) {
-      const int k = k0 + 4 * q;
-      const bool ok = k < cstart;
-      const int64_t row0 = (int64_t)b * p.L + (int64_t)k * Q;
-#pragma unroll
-      for (int v = 0; v < UV; ++v) {
-        const int i = lane + 64 * v, tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
-        uv[q][v] = ok ? *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0) : u16x8_t{};
-      }
-#pragma unroll
-      for (int v = 0; v < BV; ++v) {
-        const int i = lane + 64 * v, tl = i / (NS / 8), n0 = 8 * (i % (NS / 8));
-        bv[q][v] = (ok && i < Q * NS / 8)
-                       ? *reinterpret_cast<const u16x8_t*>(p.Bm + ((row0 + tl) * rowH + h) * NS + n0)
-                       : u16x8_t{};
-      }
-      dl[q] = (ok && lane < Q) ? bf_val(p.delta[(row0 + lane) * rowH + h]) : 0.f;
+      for (int e = 0; e < 8; ++e) XT_hi[d0 + e][tl] = uv[v][e];
     }
+  } else {
 #pragma unroll
-    for (int q = 0; q < kBatch; ++q) {
-      const int k = k0 + 4 * q;
-      if (k >= cstart) break;
-      const float cdv = prefix32(dl[q], lane);
-      const float c31 = __shfl(cdv, 31);
-      const float wgt = __expf(a * (c31 - cdv + sm.c.after[k])) * dl[q];
+    for (int v = 0; v < GV; ++v) {
+      const int i = lane + 64 * v, tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
+      const float g4[4] = {gv[v].x, gv[v].y, gv[v].z, gv[v].w};
+      const float gt = __shfl(wt, tl);
 #pragma unroll
-      for (int v = 0; v < UV; ++v) {
-        const int i = lane + 64 * v, tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sm.c.Ut[w][d0 + e][tl] = uv[q][v][e];
+      for (int e = 0; e < 4; ++e) {
+        uint16_t hi, lo;
+        bf_split(gt * g4[e], hi, lo);
+        XT_hi[d0 + e][tl] = hi;
+        XT_lo[d0 + e][tl] = lo;
       }
+    }
+  }
 #pragma unroll
-      for (int v = 0; v < BV; ++v) {
-        const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
-        const float ws = __shfl(wgt, tl);
-        if (i < Q * NS / 8) {
+  for (int v = 0; v < BV; ++v) {
+    const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+    const float ws = __shfl(wt, tl);
+    if (i < Q * NS / 8) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            uint16_t hi, lo;
-            bf_split(ws * bf_val(bv[q][v][e]), hi, lo);
-            sm.c.BwT_hi[w][n0 + e][tl] = hi;
-            sm.c.BwT_lo[w][n0 + e][tl] = lo;
-          }
+      for (int e = 0; e < 8; ++e) {
+        if (kind == 0) {
+          uint16_t hi, lo;
+          bf_split(ws * bf_val(bv[v][e]), hi, lo);
+          YT_hi[n0 + e][tl] = hi;
+          YT_lo[n0 + e][tl] = lo;
+        } else {
+          YT_hi[n0 + e][tl] = bv[v][e];
         }
       }
-      rr::wave_lds_sync();
-#pragma unroll
-      for (int j = 0; j < K::NB; ++j) {
-        const int db = j / K::NBN, nb = j % K::NBN;
-        const u16x8_t fa = frag(&sm.c.Ut[w][16 * db + (lane & 15)][8 * (lane >> 4)]);
-        acc[j] = mfma16(fa, frag(&sm.c.BwT_hi[w][16 * nb + (lane & 15)][8 * (lane >> 4)]), acc[j]);
-        acc[j] = mfma16(fa, frag(&sm.c.BwT_lo[w][16 * nb + (lane & 15)][8 * (lane >> 4)]), acc[j]);
-      }
-      rr::wave_lds_sync();
     }
   }
-  const float g0 = __expf(a * sm.c.total);
-  __syncthreads();  // staging area is reused for the reduction
+  rr::wave_lds_sync();
+  float* dst = (kind == 0 ? p.ckpt : p.agg) + (((int64_t)b * p.H + h) * p.nC + c) * DH * NS;
 #pragma unroll
-  for (int j = 0; j < K::NB; ++j) {
-    const int db = j / K::NBN, nb = j % K::NBN;
+  for (int j = 0; j < NB; ++j) {
+    const int db = j / NBN, nb = j % NBN;
+    const u16x8_t fa = frag(&XT_hi[16 * db + (lane & 15)][8 * (lane >> 4)]);
+    const u16x8_t fb = frag(&YT_hi[16 * nb + (lane & 15)][8 * (lane >> 4)]);
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    acc = mfma16(fa, fb, acc);
+    if (kind == 0) acc = mfma16(fa, frag(&YT_lo[16 * nb + (lane & 15)][8 * (lane >> 4)]), acc);
+    else acc = mfma16(frag(&XT_lo[16 * db + (lane & 15)][8 * (lane >> 4)]), fb, acc);
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      sm.r.part[w][16 * db + 4 * (lane >> 4) + r][16 * nb + (lane & 15)] = acc[j][r];
+    for (int r = 0; r < 4; ++r) dst[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)] = acc[r];
   }
-  __syncthreads();
-#pragma unroll
-  for (int jj = 0; jj < K::NBW; ++jj) {
-    const int j = w + 4 * jj;
-    if (j < K::NB) {
-      const int db = j / K::NBN, nb = j % K::NBN;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
-        float sum = sm.r.part[0][d][n] + sm.r.part[1][d][n] + sm.r.part[2][d][n] + sm.r.part[3][d][n];
-        if (p.h0 != nullptr) sum += g0 * p.h0[(((int64_t)b * p.H + h) * DH + d) * NS + n];
-        hst[jj][r] = sum;
-      }
-    }
-  }
-  __syncthreads();
+  if (lane == 0) p.tot[((int64_t)b * p.H + h) * p.nC + c] = c31;
 }
 
+// Sequential pass over the chunks of one (batch, head), one state element per
+// thread; loads are issued kPass chunks ahead of their use.
 template <int DH, int NS>
+__global__ __launch_bounds__(256) void ssd2_pass_kernel(rr::Ssd2Args p, int kind) {
+  constexpr int kPass = 8;
+  const int e = blockIdx.x * 256 + threadIdx.x;   // element d * NS + n
+  const int h = blockIdx.y, b = blockIdx.z;
+  const float a = p.A[(int64_t)h * p.A_stride_h];
+  const int64_t bh = (int64_t)b * p.H + h;
+  const float* tot = p.tot + bh * p.nC;
+  const int nC = p.nC;
+  if (kind == 0) {
+    float* buf = p.ckpt + bh * nC * (DH * NS) + e;
+    float x = p.h0 != nullptr ? p.h0[bh * DH * NS + e] : 0.f;
+    for (int k0 = 0; k0 < nC; k0 += kPass) {
+      float sv[kPass], tv[kPass];
+#pragma unroll
+      for (int q = 0; q < kPass; ++q) {
+        const bool ok = k0 + q < nC;
+        sv[q] = ok ? buf[(int64_t)(k0 + q) * DH * NS] : 0.f;
+        tv[q] = ok ? tot[k0 + q] : 0.f;
+      }
+#pragma unroll
+      for (int q = 0; q < kPass; ++q) {
+        if (k0 + q < nC) {
+          x = __expf(a * tv[q]) * x + sv[q];
+          buf[(int64_t)(k0 + q) * DH * NS] = x;
+        }
+      }
+    }
+  } else {
+    float* buf = p.agg + bh * nC * (DH * NS) + e;
+    float x = p.dfinal != nullptr ? p.dfinal[bh * DH * NS + e] : 0.f;
+    for (int k0 = nC - 1; k0 >= 0; k0 -= kPass) {
+      float gv[kPass], tv[kPass];
+#pragma unroll
+      for (int q = 0; q < kPass; ++q) {
+        const bool ok = k0 - q >= 0;
+        gv[q] = ok ? buf[(int64_t)(k0 - q) * DH * NS] : 0.f;
+        tv[q] = ok ? tot[k0 - q] : 0.f;
+      }
+#pragma unroll
+      for (int q = 0; q < kPass; ++q) {
+        if (k0 - q >= 0) {
+          buf[(int64_t)(k0 - q) * DH * NS] = x;
+          x = __expf(a * tv[q]) * x + gv[q];
+        }
+      }
+    }
+    if (p.dh0 != nullptr) p.dh0[bh * DH * NS + e] = x;
+  }
+}
+
+// PIPE: one chunk per workgroup, entering state from checkpoint slot c - 1
+// (written by ssd2_pass_kernel); otherwise a whole head per workgroup.
+template <int DH, int NS, bool PIPE>
 __global__ __launch_bounds__(256) void ssd2_fwd_kernel(rr::Ssd2Args p) {
   using K = Cfg<DH, NS>;
   __shared__ FwdShared<DH, NS> sm;
@@ -246,9 +252,9 @@ __global__ __launch_bounds__(256) void ssd2_fwd_kernel(rr::Ssd2Args p) {
   f32x4_t hst[K::NBW];
 #pragma unroll
   for (int jj = 0; jj < K::NBW; ++jj) hst[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  if (cbeg > 0) {
-    if constexpr (NS <= 32) carry_in<DH, NS>(p, sm, b, h, cbeg, a, hst);
-  } else if (p.h0 != nullptr) {
+  const float* hsrc = cbeg > 0 ? p.ckpt + (((int64_t)b * p.H + h) * p.nC + cbeg - 1) * DH * NS
+                              : (p.h0 != nullptr ? p.h0 + ((int64_t)b * p.H + h) * DH * NS : nullptr);
+  if (hsrc != nullptr) {
 #pragma unroll
     for (int jj = 0; jj < K::NBW; ++jj) {
       const int j = w + 4 * jj;
@@ -256,8 +262,7 @@ __global__ __launch_bounds__(256) void ssd2_fwd_kernel(rr::Ssd2Args p) {
         const int db = j / K::NBN, nb = j % K::NBN;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          hst[jj][r] = p.h0[(((int64_t)b * p.H + h) * DH + 16 * db + 4 * (lane >> 4) + r) * NS +
-                            16 * nb + (lane & 15)];
+          hst[jj][r] = hsrc[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)];
       }
     }
   }
@@ -309,7 +314,7 @@ __global__ __launch_bounds__(256) void ssd2_fwd_kernel(rr::Ssd2Args p) {
       if (lane < Q) {
         sm.f.cd[lane] = cdv;
         sm.f.gam[lane] = __expf(a * cdv);
-        sm.f.wend[lane] = __expf(a * (c31 - cdv)) * dv;
+        if constexpr (!PIPE) sm.f.wend[lane] = __expf(a * (c31 - cdv)) * dv;
       }
     }
 #pragma unroll
@@ -346,7 +351,7 @@ __global__ __launch_bounds__(256) void ssd2_fwd_kernel(rr::Ssd2Args p) {
         sm.f.W_hi[t][s] = hi;
         sm.f.W_lo[t][s] = lo;
       }
-    } else {
+    } else if constexpr (!PIPE) {
       for (int i = tid - 64; i < Q * NS; i += 192) {
         const int n = i / Q, s = i % Q;
         uint16_t hi, lo;
@@ -380,6 +385,7 @@ __global__ __launch_bounds__(256) void ssd2_fwd_kernel(rr::Ssd2Args p) {
       }
     }
     // ---- h_end = Gam h_in + U^T (w o B): every wave, its blocks; checkpoint
+    if constexpr (PIPE) break;
     const float Gam = sm.f.gam[Q - 1];
 #pragma unroll
     for (int jj = 0; jj < K::NBW; ++jj) {
@@ -404,8 +410,16 @@ __global__ __launch_bounds__(256) void ssd2_fwd_kernel(rr::Ssd2Args p) {
 
 template <int DH, int NS>
 int launch_fwd(const rr::Ssd2Args& p, int64_t B, hipStream_t s) {
-  const int nR = (p.nC + p.R - 1) / p.R;
-  hipLaunchKernelGGL((ssd2_fwd_kernel<DH, NS>), dim3(nR, p.H, (unsigned)B), dim3(256), 0, s, p);
+  if (p.R < p.nC) {   // pipelined, R == 1
+    hipLaunchKernelGGL((ssd2_agg_kernel<DH, NS>), dim3(p.nC, p.H, (unsigned)B), dim3(64), 0, s, p, 0);
+    if (int rc = rr::check_launch("ssd chunked forward aggregates")) return rc;
+    hipLaunchKernelGGL((ssd2_pass_kernel<DH, NS>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0, s,
+                       p, 0);
+    if (int rc = rr::check_launch("ssd chunked forward state pass")) return rc;
+    hipLaunchKernelGGL((ssd2_fwd_kernel<DH, NS, true>), dim3(p.nC, p.H, (unsigned)B), dim3(256), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((ssd2_fwd_kernel<DH, NS, false>), dim3(1, p.H, (unsigned)B), dim3(256), 0, s, p);
+  }
   return rr::check_launch("ssd chunked forward");
 }
 
@@ -422,10 +436,10 @@ bool ssd2_supported(int dtype, int64_t L, int64_t seg, int64_t Dh, int64_t N, in
 }
 
 int ssd2_pick_run(int64_t B, int64_t H, int64_t nC, int64_t N) {
-  // One workgroup per chunk when the heads alone cannot fill the GPU, else a
-  // whole head per workgroup (no entering-state sum).  The entering-state
-  // reduction buffer limits R = 1 to N <= 32 and to kMaxCarryChunks chunks.
-  if (B * H >= 512 || N > 32 || nC > kMaxCarryChunks) return (int)nC;
+  // Pipelined (one workgroup per chunk) when the heads alone cannot fill the
+  // GPU, else a whole head per workgroup.  Only 1 and nC are valid.
+  (void)N;
+  if (B * H >= 512) return (int)nC;
   return 1;
 }
 
@@ -472,190 +486,61 @@ int ssd2_fwd(const Ssd2Args& p, int64_t B, hipStream_t s) {
 
 namespace {
 
-template <int DH, int NS>
+// LDS of the backward kernel.  Arrays live in phase order, so the operands
+// that die after phase B1 (x) share space with the masked products written in
+// B2 (y), and the B1/B2 fp32 products (p) with the phase-C results (q).
+template <int DH, int NS, bool PIPE>
 struct BwdSmem {
   static constexpr int PD = DH + 8, PN = NS + 8;
-  uint16_t U[Q][PD];
   uint16_t Bn[Q][PN];
   uint16_t Cn[Q][PN];
   uint16_t BT[NS][PQ];
   uint16_t CT[NS][PQ];
-  uint16_t CgT_hi[NS][PQ], CgT_lo[NS][PQ];
-  uint16_t GY_hi[Q][PD], GY_lo[Q][PD];
   uint16_t GYT_hi[DH][PQ], GYT_lo[DH][PQ];
   uint16_t LM_hi[DH][PN], LM_lo[DH][PN];
-  uint16_t LMT_hi[NS][PD], LMT_lo[NS][PD];
-  uint16_t HT_hi[NS][PD], HT_lo[NS][PD];
-  float CB[Q][Q + 1];
-  float G2[Q][Q + 1];
-  float F[Q][Q + 1];
   float GH[Q][NS + 1];
   float UL[Q][NS + 1];
-  float Z[Q][NS + 1];
-  float KB[Q][NS + 1];
-  uint16_t PT_hi[Q][PQ], PT_lo[Q][PQ];
-  uint16_t MGT_hi[Q][PQ], MGT_lo[Q][PQ];
-  uint16_t MGd_hi[Q][PQ], MGd_lo[Q][PQ];
-  uint16_t Km_hi[Q][PQ], Km_lo[Q][PQ];
+  union {
+    struct {                       // phase A -> B1
+      uint16_t U[Q][PD];
+      uint16_t GY_hi[Q][PD], GY_lo[Q][PD];
+      uint16_t LMT_hi[NS][PD], LMT_lo[NS][PD];
+      uint16_t HT_hi[NS][PD], HT_lo[NS][PD];
+    } x;
+    struct {                       // phase B2 -> C
+      uint16_t PT_hi[Q][PQ], PT_lo[Q][PQ];
+      uint16_t MGT_hi[Q][PQ], MGT_lo[Q][PQ];
+      uint16_t MGd_hi[Q][PQ], MGd_lo[Q][PQ];
+      uint16_t Km_hi[Q][PQ], Km_lo[Q][PQ];
+    } y;
+  };
+  union {
+    struct {                       // phase B1 -> B2
+      float CB[Q][Q + 1];
+      float G2[Q][Q + 1];
+      float F[Q][Q + 1];
+    } p;
+    struct {                       // phase C -> D
+      float Z[Q][NS + 1];
+      float KB[Q][NS + 1];
+    } q;
+  };
+  // (gam o C)^T, for the adjoint carried across chunks (whole-head mode only)
+  uint16_t CgT_hi[PIPE ? 1 : NS][PQ], CgT_lo[PIPE ? 1 : NS][PQ];
   float del[Q], cd[Q], gam[Q], m31[Q], R[Q];
   float kGH[Q], kUL[Q], kZ[Q];
   float t4[4][NS];
   float dAp[4][4][NS];
 };
 
-template <int DH, int NS>
-struct BwdCarrySmem {
-  uint16_t GYw_hi[4][DH][PQ], GYw_lo[4][DH][PQ];
-  uint16_t CT[4][NS][PQ];
-  float tot[rr::kMaxCarryChunks];
-  float before[rr::kMaxCarryChunks];  // delta summed over the later chunks before chunk k
-  float total;
-};
-
-template <int DH, int NS>
-union BwdShared {
-  BwdSmem<DH, NS> m;
-  BwdCarrySmem<DH, NS> c;
-  CarryRed<DH, NS> r;
-};
-
-// Adjoint entering chunk cend-1 from chunks cend .. nC-1 (and dfinal).  Same
-// scheme as carry_in: every 4th later chunk per wave, loads batched.
-template <int DH, int NS>
-__device__ void lam_carry(const rr::Ssd2Args& p, BwdShared<DH, NS>& sm, int b, int h, int cend,
-                          float a, f32x4_t (&lam)[Cfg<DH, NS>::NBW]) {
-  using K = Cfg<DH, NS>;
-  constexpr int kBatch = 2;
-  constexpr int GV = Q * DH / 4 / 64;               // float4 of dY per lane per chunk
-  constexpr int CV = (Q * NS / 8 + 63) / 64;        // u16x8 of C per lane per chunk
-  constexpr int KPW = rr::kMaxCarryChunks / 4;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t rowH = p.H;
-  const int nl = p.nC - cend;                       // number of later chunks
-  {
-    float dv[KPW];
-#pragma unroll
-    for (int j = 0; j < KPW; ++j) {
-      const int k = cend + w + 4 * j;
-      dv[j] = (k < p.nC && lane < Q) ? bf_val(p.delta[((int64_t)b * p.L + (int64_t)k * Q + lane) * rowH + h]) : 0.f;
-    }
-#pragma unroll
-    for (int j = 0; j < KPW; ++j) {
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) dv[j] += __shfl_xor(dv[j], o);
-      if (lane == 0 && w + 4 * j < nl) sm.c.tot[w + 4 * j] = dv[j];
-    }
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float acc = 0.f;
-    for (int k = 0; k < nl; ++k) {
-      sm.c.before[k] = acc;
-      acc += sm.c.tot[k];
-    }
-    sm.c.total = acc;
-  }
-  __syncthreads();
-  f32x4_t acc[K::NB];
-#pragma unroll
-  for (int j = 0; j < K::NB; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  for (int k0 = w; k0 < nl; k0 += 4 * kBatch) {
-    float4 gv[kBatch][GV];
-    u16x8_t cv[kBatch][CV];
-    float dl[kBatch];
-#pragma unroll
-    for (int q = 0; q < kBatch; ++q) {
-      const int kk = k0 + 4 * q;
-      const bool ok = kk < nl;
-      const int64_t row0 = (int64_t)b * p.L + (int64_t)(cend + kk) * Q;
-#pragma unroll
-      for (int v = 0; v < GV; ++v) {
-        const int i = lane + 64 * v, tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
-        gv[q][v] = ok ? *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0)
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-#pragma unroll
-      for (int v = 0; v < CV; ++v) {
-        const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
-        cv[q][v] = (ok && i < Q * NS / 8)
-                       ? *reinterpret_cast<const u16x8_t*>(p.Cm + ((row0 + tl) * rowH + h) * NS + n0)
-                       : u16x8_t{};
-      }
-      dl[q] = (ok && lane < Q) ? bf_val(p.delta[(row0 + lane) * rowH + h]) : 0.f;
-    }
-#pragma unroll
-    for (int q = 0; q < kBatch; ++q) {
-      const int kk = k0 + 4 * q;
-      if (kk >= nl) break;
-      const float cdv = prefix32(dl[q], lane);
-      const float wgt = __expf(a * (sm.c.before[kk] + cdv));
-#pragma unroll
-      for (int v = 0; v < GV; ++v) {
-        const int i = lane + 64 * v, tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
-        const float wt = __shfl(wgt, tl);
-        const float g4[4] = {gv[q][v].x, gv[q][v].y, gv[q][v].z, gv[q][v].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          uint16_t hi, lo;
-          bf_split(wt * g4[e], hi, lo);
-          sm.c.GYw_hi[w][d0 + e][tl] = hi;
-          sm.c.GYw_lo[w][d0 + e][tl] = lo;
-        }
-      }
-#pragma unroll
-      for (int v = 0; v < CV; ++v) {
-        const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
-        if (i < Q * NS / 8) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) sm.c.CT[w][n0 + e][tl] = cv[q][v][e];
-        }
-      }
-      rr::wave_lds_sync();
-#pragma unroll
-      for (int j = 0; j < K::NB; ++j) {
-        const int db = j / K::NBN, nb = j % K::NBN;
-        const u16x8_t fb = frag(&sm.c.CT[w][16 * nb + (lane & 15)][8 * (lane >> 4)]);
-        acc[j] = mfma16(frag(&sm.c.GYw_hi[w][16 * db + (lane & 15)][8 * (lane >> 4)]), fb, acc[j]);
-        acc[j] = mfma16(frag(&sm.c.GYw_lo[w][16 * db + (lane & 15)][8 * (lane >> 4)]), fb, acc[j]);
-      }
-      rr::wave_lds_sync();
-    }
-  }
-  const float gf = __expf(a * sm.c.total);
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < K::NB; ++j) {
-    const int db = j / K::NBN, nb = j % K::NBN;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      sm.r.part[w][16 * db + 4 * (lane >> 4) + r][16 * nb + (lane & 15)] = acc[j][r];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int jj = 0; jj < K::NBW; ++jj) {
-    const int j = w + 4 * jj;
-    if (j < K::NB) {
-      const int db = j / K::NBN, nb = j % K::NBN;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
-        float sum = sm.r.part[0][d][n] + sm.r.part[1][d][n] + sm.r.part[2][d][n] + sm.r.part[3][d][n];
-        if (p.dfinal != nullptr) sum += gf * p.dfinal[(((int64_t)b * p.H + h) * DH + d) * NS + n];
-        lam[jj][r] = sum;
-      }
-    }
-  }
-  __syncthreads();
-}
-
 __device__ __forceinline__ int r32row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
-template <int DH, int NS>
-__global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
+// PIPE: one chunk per workgroup, lam from the workspace (ssd2_pass_kernel);
+// otherwise a whole head per workgroup, lam carried backwards in registers.
+template <int DH, int NS, bool PIPE>
+__global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::Ssd2Args p) {
   using K = Cfg<DH, NS>;
-  using S = BwdSmem<DH, NS>;
-  __shared__ BwdShared<DH, NS> sm;
-  S& m = sm.m;
+  __shared__ BwdSmem<DH, NS, PIPE> m;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int h = blockIdx.y, b = blockIdx.z;
   const int cbeg = blockIdx.x * p.R;
@@ -668,9 +553,9 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
   f32x4_t lam[K::NBW];
 #pragma unroll
   for (int jj = 0; jj < K::NBW; ++jj) lam[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  if (cend < p.nC) {
-    lam_carry<DH, NS>(p, sm, b, h, cend, a, lam);
-  } else if (p.dfinal != nullptr) {
+  const float* lsrc = PIPE ? p.agg + (((int64_t)b * p.H + h) * p.nC + cbeg) * DH * NS
+                           : (p.dfinal != nullptr ? p.dfinal + sbase : nullptr);
+  if (lsrc != nullptr) {
 #pragma unroll
     for (int jj = 0; jj < K::NBW; ++jj) {
       const int j = w + 4 * jj;
@@ -678,7 +563,7 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
         const int db = j / NBN, nb = j % NBN;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          lam[jj][r] = p.dfinal[sbase + (16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)];
+          lam[jj][r] = lsrc[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)];
       }
     }
   }
@@ -728,7 +613,7 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
 #pragma unroll
       for (int v = 0; v < UV; ++v) {
         const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
-        if (i < Q * DH / 8) *reinterpret_cast<u16x8_t*>(&m.U[tl][d0]) = uv[v];
+        if (i < Q * DH / 8) *reinterpret_cast<u16x8_t*>(&m.x.U[tl][d0]) = uv[v];
       }
 #pragma unroll
       for (int v = 0; v < BV; ++v) {
@@ -752,8 +637,8 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
           for (int e = 0; e < 4; ++e) {
             uint16_t hi, lo;
             bf_split(g4[e], hi, lo);
-            m.GY_hi[tl][d0 + e] = hi;
-            m.GY_lo[tl][d0 + e] = lo;
+            m.x.GY_hi[tl][d0 + e] = hi;
+            m.x.GY_lo[tl][d0 + e] = lo;
             m.GYT_hi[d0 + e][tl] = hi;
             m.GYT_lo[d0 + e][tl] = lo;
           }
@@ -786,11 +671,11 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
             bf_split(lam[jj][r], hi, lo);
             m.LM_hi[d][n] = hi;
             m.LM_lo[d][n] = lo;
-            m.LMT_hi[n][d] = hi;
-            m.LMT_lo[n][d] = lo;
+            m.x.LMT_hi[n][d] = hi;
+            m.x.LMT_lo[n][d] = lo;
             bf_split(hin[jj][r], hi, lo);
-            m.HT_hi[n][d] = hi;
-            m.HT_lo[n][d] = lo;
+            m.x.HT_hi[n][d] = hi;
+            m.x.HT_lo[n][d] = lo;
           }
         }
       }
@@ -804,17 +689,17 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
         cb = mfma32(frag(&m.Cn[lane & 31][16 * kb + 8 * (lane >> 5)]),
                     frag(&m.Bn[lane & 31][16 * kb + 8 * (lane >> 5)]), cb);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) m.CB[r32row(r, lane)][lane & 31] = cb[r];
+      for (int r = 0; r < 16; ++r) m.p.CB[r32row(r, lane)][lane & 31] = cb[r];
     } else if (w == 1) {
       f32x16_t g2 = {};
 #pragma unroll
       for (int kb = 0; kb < DH / 16; ++kb) {
-        const u16x8_t fb = frag(&m.U[lane & 31][16 * kb + 8 * (lane >> 5)]);
-        g2 = mfma32(frag(&m.GY_hi[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, g2);
-        g2 = mfma32(frag(&m.GY_lo[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, g2);
+        const u16x8_t fb = frag(&m.x.U[lane & 31][16 * kb + 8 * (lane >> 5)]);
+        g2 = mfma32(frag(&m.x.GY_hi[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, g2);
+        g2 = mfma32(frag(&m.x.GY_lo[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, g2);
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) m.G2[r32row(r, lane)][lane & 31] = g2[r];
+      for (int r = 0; r < 16; ++r) m.p.G2[r32row(r, lane)][lane & 31] = g2[r];
     } else {
       // tasks: GH blocks (tb, nb) and UL blocks (sb, nb); waves 2 and 3
       for (int task = w - 2; task < 4 * NBN; task += 2) {
@@ -827,15 +712,15 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
         for (int kb = 0; kb < DH / 32; ++kb) {
           const int k0 = 32 * kb + 8 * (lane >> 4);
           if (isGH) {
-            const u16x8_t ah = frag(&m.GY_hi[row][k0]), al = frag(&m.GY_lo[row][k0]);
-            const u16x8_t bh = frag(&m.HT_hi[col][k0]), bl = frag(&m.HT_lo[col][k0]);
+            const u16x8_t ah = frag(&m.x.GY_hi[row][k0]), al = frag(&m.x.GY_lo[row][k0]);
+            const u16x8_t bh = frag(&m.x.HT_hi[col][k0]), bl = frag(&m.x.HT_lo[col][k0]);
             acc = mfma16(ah, bh, acc);
             acc = mfma16(ah, bl, acc);
             acc = mfma16(al, bh, acc);
           } else {
-            const u16x8_t fa = frag(&m.U[row][k0]);
-            acc = mfma16(fa, frag(&m.LMT_hi[col][k0]), acc);
-            acc = mfma16(fa, frag(&m.LMT_lo[col][k0]), acc);
+            const u16x8_t fa = frag(&m.x.U[row][k0]);
+            acc = mfma16(fa, frag(&m.x.LMT_hi[col][k0]), acc);
+            acc = mfma16(fa, frag(&m.x.LMT_lo[col][k0]), acc);
           }
         }
 #pragma unroll
@@ -845,12 +730,14 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
           else m.UL[t][col] = acc[r];
         }
       }
-      for (int i = tid - 128; i < NS * Q; i += 128) {
-        const int n = i / Q, t = i % Q;
-        uint16_t hi, lo;
-        bf_split(m.gam[t] * bf_val(m.Cn[t][n]), hi, lo);
-        m.CgT_hi[n][t] = hi;
-        m.CgT_lo[n][t] = lo;
+      if constexpr (!PIPE) {
+        for (int i = tid - 128; i < NS * Q; i += 128) {
+          const int n = i / Q, t = i % Q;
+          uint16_t hi, lo;
+          bf_split(m.gam[t] * bf_val(m.Cn[t][n]), hi, lo);
+          m.CgT_hi[n][t] = hi;
+          m.CgT_lo[n][t] = lo;
+        }
       }
     }
     __syncthreads();
@@ -862,11 +749,11 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int tp = r32row(r, lane);
-        const float v = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * m.CB[tp][s] : 0.f;
+        const float v = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * m.p.CB[tp][s] : 0.f;
         uint16_t hi, lo;
         bf_split(v, hi, lo);
-        m.PT_hi[s][tp] = hi;
-        m.PT_lo[s][tp] = lo;
+        m.y.PT_hi[s][tp] = hi;
+        m.y.PT_lo[s][tp] = lo;
       }
     } else if (w == 1 || w == 3) {
       // M o G2 -> (M o G2)^T [t][t'] (wave 1); (M o G2 o delta_s) and K [t'][s] (wave 3)
@@ -875,19 +762,19 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int tp = r32row(r, lane);
-        const float mg = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * m.G2[tp][s] : 0.f;
+        const float mg = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * m.p.G2[tp][s] : 0.f;
         uint16_t hi, lo;
         if (w == 1) {
           bf_split(mg, hi, lo);
-          m.MGT_hi[s][tp] = hi;
-          m.MGT_lo[s][tp] = lo;
+          m.y.MGT_hi[s][tp] = hi;
+          m.y.MGT_lo[s][tp] = lo;
         } else {
           bf_split(mg * ds, hi, lo);
-          m.MGd_hi[tp][s] = hi;
-          m.MGd_lo[tp][s] = lo;
+          m.y.MGd_hi[tp][s] = hi;
+          m.y.MGd_lo[tp][s] = lo;
           bf_split(mg * ds * (m.cd[tp] - cds + ds), hi, lo);
-          m.Km_hi[tp][s] = hi;
-          m.Km_lo[tp][s] = lo;
+          m.y.Km_hi[tp][s] = hi;
+          m.y.Km_lo[tp][s] = lo;
         }
       }
     } else {
@@ -897,25 +784,25 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int tp = r32row(r, lane);
-        m.F[tp][s] = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * ds * m.G2[tp][s] * m.CB[tp][s] : 0.f;
+        m.p.F[tp][s] = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * ds * m.p.G2[tp][s] * m.p.CB[tp][s] : 0.f;
       }
       rr::wave_lds_sync();
       if (lane < Q) {
         float row[Q];
 #pragma unroll
-        for (int q = 0; q < Q; ++q) row[q] = m.F[lane][q];
+        for (int q = 0; q < Q; ++q) row[q] = m.p.F[lane][q];
         float run = 0.f;
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
           run += row[q];
-          m.F[lane][q] = run;
+          m.p.F[lane][q] = run;
         }
       }
       rr::wave_lds_sync();
       if (lane < Q) {
         float col[Q];
 #pragma unroll
-        for (int q = 0; q < Q; ++q) col[q] = m.F[q][lane];
+        for (int q = 0; q < Q; ++q) col[q] = m.p.F[q][lane];
         float rs = 0.f;
 #pragma unroll
         for (int q = 0; q < Q; ++q) rs += (q >= lane) ? col[q] : 0.f;
@@ -931,7 +818,7 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const int k0 = 16 * kb + 8 * (lane >> 5);
-        const u16x8_t ph = frag(&m.PT_hi[lane & 31][k0]), pl = frag(&m.PT_lo[lane & 31][k0]);
+        const u16x8_t ph = frag(&m.y.PT_hi[lane & 31][k0]), pl = frag(&m.y.PT_lo[lane & 31][k0]);
         const u16x8_t gh = frag(&m.GYT_hi[d0 + (lane & 31)][k0]), gl = frag(&m.GYT_lo[d0 + (lane & 31)][k0]);
         a1 = mfma32(ph, gh, a1);
         a1 = mfma32(ph, gl, a1);
@@ -961,16 +848,16 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
         f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
         if (kind == 0) {
           const u16x8_t fb = frag(&m.CT[col][k0]);
-          acc = mfma16(frag(&m.MGT_hi[row][k0]), fb, acc);
-          acc = mfma16(frag(&m.MGT_lo[row][k0]), fb, acc);
+          acc = mfma16(frag(&m.y.MGT_hi[row][k0]), fb, acc);
+          acc = mfma16(frag(&m.y.MGT_lo[row][k0]), fb, acc);
         } else if (kind == 1) {
           const u16x8_t fb = frag(&m.BT[col][k0]);
-          acc = mfma16(frag(&m.MGd_hi[row][k0]), fb, acc);
-          acc = mfma16(frag(&m.MGd_lo[row][k0]), fb, acc);
+          acc = mfma16(frag(&m.y.MGd_hi[row][k0]), fb, acc);
+          acc = mfma16(frag(&m.y.MGd_lo[row][k0]), fb, acc);
         } else {
           const u16x8_t fb = frag(&m.BT[col][k0]);
-          acc = mfma16(frag(&m.Km_hi[row][k0]), fb, acc);
-          acc = mfma16(frag(&m.Km_lo[row][k0]), fb, acc);
+          acc = mfma16(frag(&m.y.Km_hi[row][k0]), fb, acc);
+          acc = mfma16(frag(&m.y.Km_lo[row][k0]), fb, acc);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -978,12 +865,12 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
           const int64_t gi = ((row0 + t) * rowH + h) * NS + col;
           if (kind == 0) {
             const float z = acc[r] + m.m31[t] * m.UL[t][col];
-            m.Z[t][col] = z;
+            m.q.Z[t][col] = z;
             rr::st_bf16(p.dB, gi, m.del[t] * z);
           } else if (kind == 1) {
             rr::st_bf16(p.dC, gi, m.gam[t] * m.GH[t][col] + acc[r]);
           } else {
-            m.KB[t][col] = acc[r];
+            m.q.KB[t][col] = acc[r];
           }
         }
       }
@@ -998,20 +885,21 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
         const int j = w + 4 * jj;
         if (j < K::NB) {
           const int db = j / NBN, nb = j % NBN;
-          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-          const int k0 = 8 * (lane >> 4);
-          const u16x8_t ah = frag(&m.GYT_hi[16 * db + (lane & 15)][k0]);
-          const u16x8_t al = frag(&m.GYT_lo[16 * db + (lane & 15)][k0]);
-          const u16x8_t bh = frag(&m.CgT_hi[16 * nb + (lane & 15)][k0]);
-          const u16x8_t bl = frag(&m.CgT_lo[16 * nb + (lane & 15)][k0]);
-          acc = mfma16(ah, bh, acc);
-          acc = mfma16(ah, bl, acc);
-          acc = mfma16(al, bh, acc);
           float part = 0.f;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            part += lam[jj][r] * hin[jj][r];
-            lam[jj][r] = acc[r] + gam31 * lam[jj][r];
+          for (int r = 0; r < 4; ++r) part += lam[jj][r] * hin[jj][r];
+          if constexpr (!PIPE) {
+            f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+            const int k0 = 8 * (lane >> 4);
+            const u16x8_t ah = frag(&m.GYT_hi[16 * db + (lane & 15)][k0]);
+            const u16x8_t al = frag(&m.GYT_lo[16 * db + (lane & 15)][k0]);
+            const u16x8_t bh = frag(&m.CgT_hi[16 * nb + (lane & 15)][k0]);
+            const u16x8_t bl = frag(&m.CgT_lo[16 * nb + (lane & 15)][k0]);
+            acc = mfma16(ah, bh, acc);
+            acc = mfma16(ah, bl, acc);
+            acc = mfma16(al, bh, acc);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) lam[jj][r] = acc[r] + gam31 * lam[jj][r];
           }
           part += __shfl_xor(part, 16);
           part += __shfl_xor(part, 32);
@@ -1034,7 +922,7 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
         const float bv = bf_val(m.Bn[t][n]);
         X += m.GH[t][n] * bf_val(m.Cn[t][n]);
         Y += m.UL[t][n] * bv;
-        BZ += bv * m.Z[t][n];
+        BZ += bv * m.q.Z[t][n];
         tr += m.t4[0][n] + m.t4[1][n] + m.t4[2][n] + m.t4[3][n];
       }
       const float dt = m.del[t], gt = m.gam[t], mt = m.m31[t];
@@ -1056,7 +944,7 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
         float sum = 0.f;
         for (int t = tq; t < Q; t += 12) {
           const float bv = bf_val(m.Bn[t][n]), cv = bf_val(m.Cn[t][n]);
-          sum += cv * (m.KB[t][n] + m.kGH[t] * m.GH[t][n]) + bv * (m.kUL[t] * m.UL[t][n] - m.kZ[t] * m.Z[t][n]);
+          sum += cv * (m.q.KB[t][n] + m.kGH[t] * m.GH[t][n]) + bv * (m.kUL[t] * m.UL[t][n] - m.kZ[t] * m.q.Z[t][n]);
         }
         sum += __shfl_xor(sum, 16);
         sum += __shfl_xor(sum, 32);
@@ -1072,11 +960,9 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
     }
   }
   // per-run dA partial and the initial-state gradient
-  if (w == 1 && lane < NS) {
-    const int nR = gridDim.x;
-    p.ws[(((int64_t)b * p.H + h) * nR + blockIdx.x) * NS + lane] = dA_acc;
-  }
-  if (cbeg == 0 && p.dh0 != nullptr) {
+  const int nR = gridDim.x;
+  if (w == 1 && lane < NS) p.ws[(((int64_t)b * p.H + h) * nR + blockIdx.x) * NS + lane] = dA_acc;
+  if (!PIPE && p.dh0 != nullptr) {
 #pragma unroll
     for (int jj = 0; jj < K::NBW; ++jj) {
       const int j = w + 4 * jj;
@@ -1090,26 +976,45 @@ __global__ __launch_bounds__(256) void ssd2_bwd_kernel(rr::Ssd2Args p) {
   }
 }
 
-// dA[h, n] = sum over batch rows and runs, in a fixed order.
-__global__ void ssd2_dA_kernel(const float* __restrict__ part, float* __restrict__ dA, int Bsz,
-                               int H, int nR, int NS) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= H * NS) return;
-  const int h = i / NS, n = i % NS;
+// dA[h, n] = sum over batch rows and runs of the per-run partials, in a fixed
+// order: one workgroup per head, thread (g, n) sums partials g, g + G, ...,
+// then the G per-thread sums are added in order.
+__global__ __launch_bounds__(256) void ssd2_dA_kernel(const float* __restrict__ part, float* __restrict__ dA,
+                                                      int Bsz, int H, int nR, int NS) {
+  __shared__ float red[256];
+  const int h = blockIdx.x, G = 256 / NS, n = threadIdx.x % NS, g = threadIdx.x / NS;
+  const int parts = Bsz * nR;
   float s = 0.f;
-  for (int b = 0; b < Bsz; ++b)
-    for (int r = 0; r < nR; ++r) s += part[(((int64_t)b * H + h) * nR + r) * NS + n];
-  dA[i] = s;
+  if (g < G) {
+    for (int i = g; i < parts; i += G) {
+      const int b = i / nR, r = i % nR;
+      s += part[(((int64_t)b * H + h) * nR + r) * NS + n];
+    }
+  }
+  red[threadIdx.x] = s;
+  __syncthreads();
+  if (threadIdx.x < NS) {
+    float t = 0.f;
+    for (int q = 0; q < G; ++q) t += red[q * NS + threadIdx.x];
+    dA[(int64_t)h * NS + threadIdx.x] = t;
+  }
 }
 
 template <int DH, int NS>
 int launch_bwd(const rr::Ssd2Args& p, int64_t B, hipStream_t s) {
   const int nR = (p.nC + p.R - 1) / p.R;
-  hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS>), dim3(nR, p.H, (unsigned)B), dim3(256), 0, s, p);
+  if (nR > 1) {   // pipelined, R == 1
+    hipLaunchKernelGGL((ssd2_agg_kernel<DH, NS>), dim3(p.nC, p.H, (unsigned)B), dim3(64), 0, s, p, 1);
+    if (int rc = rr::check_launch("ssd chunked backward aggregates")) return rc;
+    hipLaunchKernelGGL((ssd2_pass_kernel<DH, NS>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0, s,
+                       p, 1);
+    if (int rc = rr::check_launch("ssd chunked backward adjoint pass")) return rc;
+    hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, true>), dim3(nR, p.H, (unsigned)B), dim3(256), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, false>), dim3(1, p.H, (unsigned)B), dim3(256), 0, s, p);
+  }
   if (int rc = rr::check_launch("ssd chunked backward")) return rc;
-  const int n = p.H * p.NS;
-  hipLaunchKernelGGL(ssd2_dA_kernel, dim3((n + 127) / 128), dim3(128), 0, s, p.ws, p.dA, (int)B, p.H,
-                     nR, p.NS);
+  hipLaunchKernelGGL(ssd2_dA_kernel, dim3(p.H), dim3(256), 0, s, p.ws, p.dA, (int)B, p.H, nR, p.NS);
   return rr::check_launch("ssd chunked backward dA");
 }
 
@@ -1121,9 +1026,34 @@ bool ssd2_bwd_supported(int64_t Dh, int64_t N) {
   return (Dh == 32 || Dh == 64) && (N == 16 || N == 32);
 }
 
-size_t ssd2_bwd_ws_bytes(int64_t B, int64_t H, int64_t nC, int R, int64_t N) {
+// Workspace layout (floats, each part 256-byte aligned): per-chunk delta
+// totals [B,H,nC] (pipelined), dA partials [B,H,nR,N] (backward), backward
+// chunk aggregates / adjoints [B,H,nC,Dh,N] (pipelined backward).
+namespace {
+int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }
+}
+
+size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int R, int64_t Dh, int64_t N, int pass) {
   const int64_t nR = (nC + R - 1) / R;
-  return (size_t)(B * H * nR * N) * sizeof(float);
+  const bool pipe = nR > 1;
+  int64_t f = pipe ? align64(B * H * nC) : 0;
+  if (pass == 1) {
+    f += align64(B * H * nR * N);
+    if (pipe) f += align64(B * H * nC * Dh * N);
+  }
+  return (size_t)f * sizeof(float);
+}
+
+void ssd2_carve_ws(Ssd2Args& a, void* ws, int64_t B, int pass) {
+  float* f = static_cast<float*>(ws);
+  const int64_t nR = (a.nC + a.R - 1) / a.R;
+  const bool pipe = nR > 1;
+  a.tot = a.ws = a.agg = nullptr;
+  if (pipe) { a.tot = f; f += align64(B * a.H * a.nC); }
+  if (pass == 1) {
+    a.ws = f; f += align64(B * a.H * nR * a.NS);
+    if (pipe) a.agg = f;
+  }
 }
 
 int ssd2_bwd(const Ssd2Args& p, int64_t B, hipStream_t s) {

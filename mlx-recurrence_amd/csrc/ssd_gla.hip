@@ -553,11 +553,8 @@ int launch_bwd(Args<InT> a, FinArgs<InT> f, const Plan& q, int64_t B, hipStream_
 extern "C" size_t rr_ssd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N,
                                          int64_t seg, int64_t A_stride_n, int dtype, int pass) {
   if (B <= 0 || L <= 0 || H <= 0 || Dh <= 0 || N <= 0 || rr::chunk_len(L, seg) == 0) return 0;
-  if (rr::ssd2_supported(dtype, L, seg, Dh, N, A_stride_n)) {
-    if (pass == 0) return 0;
-    if (rr::ssd2_bwd_supported(Dh, N))
-      return rr::ssd2_bwd_ws_bytes(B, H, L / 32, rr::ssd2_pick_run(B, H, L / 32, N), N);
-  }
+  if (rr::ssd2_supported(dtype, L, seg, Dh, N, A_stride_n) && (pass == 0 || rr::ssd2_bwd_supported(Dh, N)))
+    return rr::ssd2_ws_bytes(B, H, L / 32, rr::ssd2_pick_run(B, H, L / 32, N), Dh, N, pass);
   const Plan q = make_plan(B, L, H, Dh, N, seg);
   return pass == 0 ? q.fwd_bytes : q.bwd_bytes;
 }
@@ -586,6 +583,10 @@ extern "C" int rr_ssd_fwd(const void* u, const void* delta, const void* Bm, cons
     a.ckpt = ckpt;
     a.L = (int)L; a.H = (int)H; a.DH = (int)Dh; a.NS = (int)N; a.nC = (int)(L / 32);
     a.R = rr::ssd2_pick_run(B, H, a.nC, N);
+    const size_t need = rr::ssd2_ws_bytes(B, H, a.nC, a.R, Dh, N, 0);
+    if (need && (!workspace || workspace_bytes < need))
+      return rr::fail(RR_EWORKSPACE, "ssd_fwd: workspace too small");
+    rr::ssd2_carve_ws(a, workspace, B, 0);
     return rr::ssd2_fwd(a, B, s);
   }
   const Plan q = make_plan(B, L, H, Dh, N, seg);
@@ -627,7 +628,7 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
   if (rr::ssd2_supported(dtype, L, seg, Dh, N, A_stride_n) && rr::ssd2_bwd_supported(Dh, N)) {
     const int nC = (int)(L / 32);
     const int R = rr::ssd2_pick_run(B, H, nC, N);
-    if (!workspace || workspace_bytes < rr::ssd2_bwd_ws_bytes(B, H, nC, R, N))
+    if (!workspace || workspace_bytes < rr::ssd2_ws_bytes(B, H, nC, R, Dh, N, 1))
       return rr::fail(RR_EWORKSPACE, "ssd_bwd: workspace too small");
     rr::Ssd2Args a{};
     a.u = static_cast<const uint16_t*>(u);
@@ -646,8 +647,8 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
     a.dC = static_cast<uint16_t*>(dC);
     a.dA = dA_neg;
     a.dh0 = dh0;
-    a.ws = static_cast<float*>(workspace);
     a.L = (int)L; a.H = (int)H; a.DH = (int)Dh; a.NS = (int)N; a.nC = nC; a.R = R;
+    rr::ssd2_carve_ws(a, workspace, B, 1);
     return rr::ssd2_bwd(a, B, static_cast<hipStream_t>(stream));
   }
   const Plan q = make_plan(B, L, H, Dh, N, seg);
