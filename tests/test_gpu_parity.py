@@ -199,6 +199,10 @@ SSD_CASES = [
     (1, 128, 2, 32, 32, 32, BF16, "cfg", True, False, 14),
     (1, 96, 2, 128, 64, 32, BF16, "cfg", False, True, 15),
     (2, 64, 2, 64, 16, 32, BF16, "ref", False, False, 16),  # dense A, bf16: VALU engine
+    # B*H >= 512: one workgroup walks a whole head (state carried in registers)
+    (1, 128, 512, 32, 16, 32, BF16, "cfg", True, True, 17),
+    (2, 96, 256, 64, 32, 32, BF16, "cfg", False, True, 18),
+    (2, 64, 256, 64, 16, 32, BF16, "cfg", True, False, 19),
 ]
 
 
