@@ -199,8 +199,8 @@ def make_gla(cfg, device, dtype):
         dk=torch.empty((B, L, H, Dh), dtype=dtype, device=device),
         dv=torch.empty((B, L, H, Dh), dtype=dtype, device=device),
         dg=torch.empty((B, L, H), dtype=dtype, device=device),
-        wsf=_lib.gla_workspace(B, L, H, Dh, seg, 0, device),
-        wsb=_lib.gla_workspace(B, L, H, Dh, seg, 1, device),
+        wsf=_lib.gla_workspace(B, L, H, Dh, seg, dtype, 0, device),
+        wsb=_lib.gla_workspace(B, L, H, Dh, seg, dtype, 1, device),
     )
     es = torch.tensor([], dtype=dtype).element_size()
     n_x, n_g, n_ck = B * L * H * Dh, B * L * H, B * H * nC * Dh * Dh

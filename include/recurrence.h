@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define RR_ABI_VERSION 2
+#define RR_ABI_VERSION 3
 
 enum rr_dtype { RR_F32 = 0, RR_BF16 = 1, RR_F16 = 2 };
 
@@ -102,9 +102,13 @@ int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, const void* 
  * ckpt [B,H,nC,Dh(j),Dh(i)] fp32: state S[i,j] stored with i fastest, so
  * ckpt[:,:,nC-1].transpose(-1,-2) is the final state [B,H,Dh(i),Dh(j)].
  * h0 / dfinal / dh0: [B,H,Dh(i),Dh(j)] fp32 (gla.py:321-329 layout).
+ * bf16 inputs with T = 32 run on the chunked MFMA kernels.
  */
+
+/* Workspace bytes needed by rr_gla_fwd (pass=0) or rr_gla_bwd (pass=1) for
+ * these arguments (the kernels chosen depend on dtype). */
 size_t rr_gla_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t seg,
-                              int pass);
+                              int dtype, int pass);
 
 /* Replaces _gla_forward_kernel (reference mlx_recurrence/gla.py:49-123). */
 int rr_gla_fwd(const void* q, const void* k, const void* v, const void* gates, int dtype,

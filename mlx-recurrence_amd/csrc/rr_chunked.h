@@ -1,0 +1,516 @@
+// rr_chunked.h — the chunked (MFMA) form shared by SSD with a head-uniform
+// decay rate and GLA: step scalars, the chunk-aggregate and state-pass
+// kernels, and the forward kernel.  Included by ssd_chunked.hip and
+// gla_chunked.hip; each instantiates what it launches.
+//
+// Both scans are, per (batch, head), the recurrence over a state h[d, n]
+//     h_t = dec_t h_{t-1} + w_t u_t B_t^T,     y_t = h_t C_t
+// with a scalar decay per step:
+//     SSD (reference ssd.py:85-111): dec_t = exp(a delta_t), w_t = delta_t,
+//         u = u, B = B_in, C = C_in, d = channel, n = state;
+//     GLA (reference gla.py:78-100): dec_t = g_t, w_t = 1,
+//         u = v, B = k, C = q, d = j (value index), n = i (key index).
+// Within a 32-step chunk, with M[t, s] = dec_{s+1} ... dec_t (s <= t),
+// gam_t = dec_0 ... dec_t and m31_s = M[31, s]:
+//     Y     = (M o C B^T o w_s) U  +  diag(gam) C h_in^T
+//     h_end = gam_31 h_in + U^T diag(m31 o w) B
+// Every product is a bf16 MFMA: inputs are exact in bf16, fp32 factors are
+// split into hi + lo bf16 halves (x = hi + lo + O(2^-17 |x|)).
+//
+// SSD forms its decays as exp(a (cd_t - cd_s)) of the in-chunk cumulative
+// delta cd; GLA forms them as running products of the gates, so gates of any
+// sign (and zero) are handled exactly.
+#pragma once
+
+#include "rr_common.h"
+#include "rr_internal.h"
+#include "rr_mfma.h"
+
+namespace rr {
+namespace chunked {
+
+constexpr int Q = 32;      // chunk length (steps)
+constexpr int PQ = Q + 8;  // LDS pitch (elements) of [*][s] arrays: 80 bytes
+
+template <int DH, int NS>
+struct Cfg {
+  static constexpr int PN = NS + 8;          // LDS pitch of [*][n] arrays
+  static constexpr int NBD = DH / 16, NBN = NS / 16, NB = NBD * NBN;
+  static constexpr int NBW = (NB + 3) / 4;   // 16x16 state blocks per wave (4 waves)
+  static constexpr int NYB = DH / 32;        // 32x32 output blocks of Y
+};
+
+// Row of element r of a 32x32 MFMA accumulator held by `lane` (its column is
+// lane % 32).
+__device__ __forceinline__ int r32row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+// Inclusive prefix sum / product over lanes 0..31 and, separately, 32..63.
+__device__ __forceinline__ float prefix32(float v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) {
+    const float x = __shfl_up(v, o, 32);
+    if ((lane & 31) >= o) v += x;
+  }
+  return v;
+}
+__device__ __forceinline__ float prefix_prod32(float v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) {
+    const float x = __shfl_up(v, o, 32);
+    if ((lane & 31) >= o) v *= x;
+  }
+  return v;
+}
+// Inclusive suffix product over lanes (lane..31) within each half-wave.
+__device__ __forceinline__ float suffix_prod32(float v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) {
+    const float x = __shfl_down(v, o, 32);
+    if ((lane & 31) + o < 32) v *= x;
+  }
+  return v;
+}
+
+// Step scalars of one chunk; lane s < 32 holds step s, whose raw step input
+// `x` (SSD delta_s, GLA g_s) it passes in.  Lanes >= 32 must pass the neutral
+// input (SSD 0, GLA 1).
+struct StepScalars {
+  float gam;   // decay over steps 0..s
+  float m31;   // decay over steps s+1..31
+  float w;     // input weight (SSD delta_s, GLA 1)
+  float cd;    // SSD: cumulative delta over steps 0..s (GLA: unused)
+  float tot;   // chunk decay gam_31 (every lane)
+};
+
+template <bool GLA>
+__device__ __forceinline__ StepScalars step_scalars(float x, float a, int lane) {
+  StepScalars r;
+  if constexpr (GLA) {
+    r.gam = prefix_prod32(x, lane);
+    const float suf = suffix_prod32(x, lane);
+    const float nxt = __shfl_down(suf, 1, 32);
+    r.m31 = (lane & 31) < 31 ? nxt : 1.f;
+    r.w = 1.f;
+    r.cd = 0.f;
+    r.tot = __shfl(r.gam, 31);
+  } else {
+    r.cd = prefix32(x, lane);
+    const float c31 = __shfl(r.cd, 31);
+    r.gam = __expf(a * r.cd);
+    r.m31 = __expf(a * (c31 - r.cd));
+    r.w = x;
+    r.tot = __expf(a * c31);
+  }
+  return r;
+}
+
+// The 16 decays M[t, s] held by `lane` in the 32x32 accumulator layout
+// (s = lane % 32, t = r32row(r, lane)), zero above the diagonal (s > t).
+// SSD reads the cumulative deltas cd[], GLA the gates g[] (both in LDS).
+template <bool GLA>
+__device__ __forceinline__ void decay_block32(const float* cd_or_g, float a, int lane, float (&m)[16]) {
+  const int s = lane & 31;
+  if constexpr (GLA) {
+    const int half = lane >> 5;
+    float run = 0.f;
+#pragma unroll
+    for (int t = 0; t < Q; ++t) {
+      run = t < s ? 0.f : (t == s ? 1.f : run * cd_or_g[t]);
+      if (((t >> 2) & 1) == half) m[4 * (t >> 3) + (t & 3)] = run;
+    }
+  } else {
+    const float cds = cd_or_g[s];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = r32row(r, lane);
+      m[r] = s <= t ? __expf(a * (cd_or_g[t] - cds)) : 0.f;
+    }
+  }
+}
+
+// Offset of state element (d, n) in a caller's initial state, final-state
+// cotangent or initial-state gradient: SSD keeps them [d][n] like the
+// checkpoints, GLA as S[i][j] = [n][d] (reference gla.py:321-329).
+template <bool GLA, int DH, int NS>
+__device__ __forceinline__ int state_off(int d, int n) {
+  if constexpr (GLA) return n * DH + d;
+  else return d * NS + n;
+}
+
+// Per-head decay rate (SSD); GLA has none.
+template <bool GLA>
+__device__ __forceinline__ float head_rate(const ChunkArgs& p, int h) {
+  if constexpr (GLA) return 0.f;
+  else return p.A[(int64_t)h * p.A_stride_h];
+}
+
+// ------------------------------------------------------------------ pipelined mode
+// Several workgroups per head.  Three kernels per pass:
+//  1. agg_kernel, one wave per chunk k, writes the chunk's aggregate and its
+//     decay tot_k = gam_31:
+//       forward:  S_k = U_k^T diag(m31 o w) B_k, the state the chunk adds from
+//                 a zero start (into checkpoint slot k);
+//       backward: G_k = (gam o dY_k)^T C_k, the adjoint the chunk sends back to
+//                 its start (into the workspace).
+//  2. pass_kernel, one thread per state element, walks the chunks in order:
+//       forward:  h_k = tot_k h_{k-1} + S_k   (h_{-1} = h0), into slot k
+//       backward: lam_k = adjoint of the state leaving chunk k,
+//                 lam_{nC-1} = dfinal, lam_{k-1} = tot_k lam_k + G_k,
+//                 and dh0 = tot_0 lam_0 + G_0.
+//  3. the main kernel, one workgroup per chunk, reads its entering state
+//     (and, backward, lam_k) and does the chunk's dense products.
+template <int DH, int NS, bool GLA>
+__global__ __launch_bounds__(64) void agg_kernel(ChunkArgs p, int kind) {
+  constexpr int NBN = NS / 16, NB = (DH / 16) * NBN;
+  __shared__ uint16_t XT_hi[DH][PQ], XT_lo[DH][PQ];   // kind 0: U^T [d][s] (hi only); kind 1: (gam o dY)^T
+  __shared__ uint16_t YT_hi[NS][PQ], YT_lo[NS][PQ];   // kind 0: (m31 o w o B)^T split; kind 1: C^T (hi only)
+  const int lane = threadIdx.x;
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const float a = head_rate<GLA>(p, h);
+  const int64_t rowH = p.H, row0 = (int64_t)b * p.L + (int64_t)c * Q;
+  constexpr int UV = Q * DH / 8 / 64, GV = Q * DH / 4 / 64, BV = (Q * NS / 8 + 63) / 64;
+  // loads first
+  u16x8_t uv[UV], bv[BV];
+  float4 gv[GV];
+  if (kind == 0) {
+#pragma unroll
+    for (int v = 0; v < UV; ++v) {
+      const int i = lane + 64 * v, tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
+      uv[v] = *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0);
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < GV; ++v) {
+      const int i = lane + 64 * v, tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
+      gv[v] = *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0);
+    }
+  }
+  const uint16_t* bsrc = kind == 0 ? p.Bm : p.Cm;
+#pragma unroll
+  for (int v = 0; v < BV; ++v) {
+    const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+    bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(bsrc + ((row0 + tl) * rowH + h) * NS + n0) : u16x8_t{};
+  }
+  const float xv = lane < Q ? bf_val(p.delta[(row0 + lane) * rowH + h]) : (GLA ? 1.f : 0.f);
+  const StepScalars sc = step_scalars<GLA>(xv, a, lane);
+  // kind 0: m31_s w_s ; kind 1: gam_t
+  const float wt = kind == 0 ? sc.m31 * sc.w : sc.gam;
+  if (kind == 0) {
+#pragma unroll
+    for (int v = 0; v < UV; ++v) {
+      const int i = lane + 64 * v, tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) XT_hi[d0 + e][tl] = uv[v][e];
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < GV; ++v) {
+      const int i = lane + 64 * v, tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
+      const float g4[4] = {gv[v].x, gv[v].y, gv[v].z, gv[v].w};
+      const float gt = __shfl(wt, tl);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint16_t hi, lo;
+        bf_split(gt * g4[e], hi, lo);
+        XT_hi[d0 + e][tl] = hi;
+        XT_lo[d0 + e][tl] = lo;
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < BV; ++v) {
+    const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+    const float ws = __shfl(wt, tl);
+    if (i < Q * NS / 8) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (kind == 0) {
+          uint16_t hi, lo;
+          bf_split(ws * bf_val(bv[v][e]), hi, lo);
+          YT_hi[n0 + e][tl] = hi;
+          YT_lo[n0 + e][tl] = lo;
+        } else {
+          YT_hi[n0 + e][tl] = bv[v][e];
+        }
+      }
+    }
+  }
+  wave_lds_sync();
+  float* dst = (kind == 0 ? p.ckpt : p.agg) + (((int64_t)b * p.H + h) * p.nC + c) * DH * NS;
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int db = j / NBN, nb = j % NBN;
+    const u16x8_t fa = frag(&XT_hi[16 * db + (lane & 15)][8 * (lane >> 4)]);
+    const u16x8_t fb = frag(&YT_hi[16 * nb + (lane & 15)][8 * (lane >> 4)]);
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    acc = mfma16(fa, fb, acc);
+    if (kind == 0) acc = mfma16(fa, frag(&YT_lo[16 * nb + (lane & 15)][8 * (lane >> 4)]), acc);
+    else acc = mfma16(frag(&XT_lo[16 * db + (lane & 15)][8 * (lane >> 4)]), fb, acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dst[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)] = acc[r];
+  }
+  if (lane == 0) p.tot[((int64_t)b * p.H + h) * p.nC + c] = sc.tot;
+}
+
+// Sequential pass over the chunks of one (batch, head), one state element per
+// thread; loads are issued kPass chunks ahead of their use.
+template <int DH, int NS, bool GLA>
+__global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
+  constexpr int kPass = 8;
+  const int e = blockIdx.x * 256 + threadIdx.x;   // element d * NS + n
+  const int es = state_off<GLA, DH, NS>(e / NS, e % NS);
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int64_t bh = (int64_t)b * p.H + h;
+  const float* tot = p.tot + bh * p.nC;
+  const int nC = p.nC;
+  if (kind == 0) {
+    float* buf = p.ckpt + bh * nC * (DH * NS) + e;
+    float x = p.h0 != nullptr ? p.h0[bh * DH * NS + es] : 0.f;
+    for (int k0 = 0; k0 < nC; k0 += kPass) {
+      float sv[kPass], tv[kPass];
+#pragma unroll
+      for (int q = 0; q < kPass; ++q) {
+        const bool ok = k0 + q < nC;
+        sv[q] = ok ? buf[(int64_t)(k0 + q) * DH * NS] : 0.f;
+        tv[q] = ok ? tot[k0 + q] : 0.f;
+      }
+#pragma unroll
+      for (int q = 0; q < kPass; ++q) {
+        if (k0 + q < nC) {
+          x = tv[q] * x + sv[q];
+          buf[(int64_t)(k0 + q) * DH * NS] = x;
+        }
+      }
+    }
+  } else {
+    float* buf = p.agg + bh * nC * (DH * NS) + e;
+    float x = p.dfinal != nullptr ? p.dfinal[bh * DH * NS + es] : 0.f;
+    for (int k0 = nC - 1; k0 >= 0; k0 -= kPass) {
+      float gv[kPass], tv[kPass];
+#pragma unroll
+      for (int q = 0; q < kPass; ++q) {
+        const bool ok = k0 - q >= 0;
+        gv[q] = ok ? buf[(int64_t)(k0 - q) * DH * NS] : 0.f;
+        tv[q] = ok ? tot[k0 - q] : 0.f;
+      }
+#pragma unroll
+      for (int q = 0; q < kPass; ++q) {
+        if (k0 - q >= 0) {
+          buf[(int64_t)(k0 - q) * DH * NS] = x;
+          x = tv[q] * x + gv[q];
+        }
+      }
+    }
+    if (p.dh0 != nullptr) p.dh0[bh * DH * NS + es] = x;
+  }
+}
+
+// ------------------------------------------------------------------ forward
+template <int DH, int NS>
+struct FwdSmem {
+  uint16_t Ut[DH][PQ];                 // U^T  [d][s]
+  uint16_t C[Q][Cfg<DH, NS>::PN];      // C    [t][n]
+  uint16_t B[Q][Cfg<DH, NS>::PN];      // B    [s][n]
+  uint16_t BwT_hi[NS][PQ];             // (m31 o w o B)^T [n][s]
+  uint16_t BwT_lo[NS][PQ];
+  uint16_t W_hi[Q][PQ];                // M o CB^T o w_s  [t][s]
+  uint16_t W_lo[Q][PQ];
+  uint16_t H_hi[DH][Cfg<DH, NS>::PN];  // h_in [d][n]
+  uint16_t H_lo[DH][Cfg<DH, NS>::PN];
+  float x[Q];      // step input (SSD delta, GLA gate)
+  float cd[Q];     // SSD: cumulative delta
+  float gam[Q], wend[Q];
+};
+
+// PIPE: one chunk per workgroup, entering state from checkpoint slot c - 1
+// (written by pass_kernel); otherwise a run of R chunks per workgroup (R = all
+// chunks of the head: the state is carried in registers).
+template <int DH, int NS, bool PIPE, bool GLA>
+__global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
+  using K = Cfg<DH, NS>;
+  __shared__ FwdSmem<DH, NS> sm;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int cbeg = blockIdx.x * p.R;
+  const int cend = min(cbeg + p.R, p.nC);
+  const float a = head_rate<GLA>(p, h);
+  const int64_t rowH = p.H;
+
+  f32x4_t hst[K::NBW];
+#pragma unroll
+  for (int jj = 0; jj < K::NBW; ++jj) hst[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const bool from_h0 = cbeg == 0;
+  const float* hsrc = !from_h0 ? p.ckpt + (((int64_t)b * p.H + h) * p.nC + cbeg - 1) * DH * NS
+                               : (p.h0 != nullptr ? p.h0 + ((int64_t)b * p.H + h) * DH * NS : nullptr);
+  if (hsrc != nullptr) {
+#pragma unroll
+    for (int jj = 0; jj < K::NBW; ++jj) {
+      const int j = w + 4 * jj;
+      if (j < K::NB) {
+        const int db = j / K::NBN, nb = j % K::NBN;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
+          hst[jj][r] = hsrc[from_h0 ? state_off<GLA, DH, NS>(d, n) : d * NS + n];
+        }
+      }
+    }
+  }
+
+  for (int c = cbeg; c < cend; ++c) {
+    const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;  // first (b, t) row of the chunk
+    // ---- stage the chunk's inputs (all loads issued before any use)
+    {
+      constexpr int UV = (Q * DH / 8 + 255) / 256, BV = (Q * NS / 8 + 255) / 256;
+      u16x8_t uv[UV], bv[BV], cv[BV];
+      float xv = 0.f;
+#pragma unroll
+      for (int v = 0; v < UV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
+        uv[v] = i < Q * DH / 8 ? *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0) : u16x8_t{};
+      }
+#pragma unroll
+      for (int v = 0; v < BV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+        const int64_t g = ((row0 + tl) * rowH + h) * NS + n0;
+        bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Bm + g) : u16x8_t{};
+        cv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Cm + g) : u16x8_t{};
+      }
+      if (tid < Q) xv = bf_val(p.delta[(row0 + tid) * rowH + h]);
+#pragma unroll
+      for (int v = 0; v < UV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
+        if (i < Q * DH / 8) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sm.Ut[d0 + e][tl] = uv[v][e];
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < BV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+        if (i < Q * NS / 8) {
+          *reinterpret_cast<u16x8_t*>(&sm.B[tl][n0]) = bv[v];
+          *reinterpret_cast<u16x8_t*>(&sm.C[tl][n0]) = cv[v];
+        }
+      }
+      if (tid < Q) sm.x[tid] = xv;
+    }
+    __syncthreads();
+    // ---- per-step scalars (wave 0) and h_in split (every wave, its blocks)
+    if (w == 0) {
+      const float xv = lane < Q ? sm.x[lane] : (GLA ? 1.f : 0.f);
+      const StepScalars sc = step_scalars<GLA>(xv, a, lane);
+      if (lane < Q) {
+        sm.cd[lane] = sc.cd;
+        sm.gam[lane] = sc.gam;
+        if constexpr (!PIPE) sm.wend[lane] = sc.m31 * sc.w;
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < K::NBW; ++jj) {
+      const int j = w + 4 * jj;
+      if (j < K::NB) {
+        const int db = j / K::NBN, nb = j % K::NBN;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          uint16_t hi, lo;
+          bf_split(hst[jj][r], hi, lo);
+          const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
+          sm.H_hi[d][n] = hi;
+          sm.H_lo[d][n] = lo;
+        }
+      }
+    }
+    __syncthreads();
+    // ---- W = M o CB^T o w_s (wave 0); (m31 o w o B)^T (waves 1..3)
+    if (w == 0) {
+      f32x16_t cb = {};
+#pragma unroll
+      for (int kb = 0; kb < NS / 16; ++kb)
+        cb = mfma32(frag(&sm.C[lane & 31][16 * kb + 8 * (lane >> 5)]),
+                    frag(&sm.B[lane & 31][16 * kb + 8 * (lane >> 5)]), cb);
+      const int s = lane & 31;
+      float m[16];
+      decay_block32<GLA>(GLA ? sm.x : sm.cd, a, lane, m);
+      const float ws = GLA ? 1.f : sm.x[s];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = r32row(r, lane);
+        uint16_t hi, lo;
+        bf_split(m[r] * ws * cb[r], hi, lo);
+        sm.W_hi[t][s] = hi;
+        sm.W_lo[t][s] = lo;
+      }
+    } else if constexpr (!PIPE) {
+      for (int i = tid - 64; i < Q * NS; i += 192) {
+        const int n = i / Q, s = i % Q;
+        uint16_t hi, lo;
+        bf_split(sm.wend[s] * bf_val(sm.B[s][n]), hi, lo);
+        sm.BwT_hi[n][s] = hi;
+        sm.BwT_lo[n][s] = lo;
+      }
+    }
+    __syncthreads();
+    // ---- Y blocks (waves < DH/32)
+    if (w < K::NYB) {
+      const int d0 = 32 * w;
+      f32x16_t yi = {}, ye = {};
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const u16x8_t fb = frag(&sm.Ut[d0 + (lane & 31)][16 * kb + 8 * (lane >> 5)]);
+        yi = mfma32(frag(&sm.W_hi[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, yi);
+        yi = mfma32(frag(&sm.W_lo[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, yi);
+      }
+#pragma unroll
+      for (int kb = 0; kb < NS / 16; ++kb) {
+        const u16x8_t fa = frag(&sm.C[lane & 31][16 * kb + 8 * (lane >> 5)]);
+        ye = mfma32(fa, frag(&sm.H_hi[d0 + (lane & 31)][16 * kb + 8 * (lane >> 5)]), ye);
+        ye = mfma32(fa, frag(&sm.H_lo[d0 + (lane & 31)][16 * kb + 8 * (lane >> 5)]), ye);
+      }
+      const int d = d0 + (lane & 31);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = r32row(r, lane);
+        p.y[((row0 + t) * rowH + h) * DH + d] = yi[r] + sm.gam[t] * ye[r];
+      }
+    }
+    // ---- h_end = gam_31 h_in + U^T (m31 o w o B): every wave, its blocks; checkpoint
+    if constexpr (PIPE) break;
+    const float Gam = sm.gam[Q - 1];
+#pragma unroll
+    for (int jj = 0; jj < K::NBW; ++jj) {
+      const int j = w + 4 * jj;
+      if (j < K::NB) {
+        const int db = j / K::NBN, nb = j % K::NBN;
+        const u16x8_t fa = frag(&sm.Ut[16 * db + (lane & 15)][8 * (lane >> 4)]);
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+        acc = mfma16(fa, frag(&sm.BwT_hi[16 * nb + (lane & 15)][8 * (lane >> 4)]), acc);
+        acc = mfma16(fa, frag(&sm.BwT_lo[16 * nb + (lane & 15)][8 * (lane >> 4)]), acc);
+        float* ck = p.ckpt + (((int64_t)b * p.H + h) * p.nC + c) * DH * NS;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          hst[jj][r] = Gam * hst[jj][r] + acc[r];
+          ck[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)] = hst[jj][r];
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <int DH, int NS, bool GLA>
+int launch_fwd(const ChunkArgs& p, int64_t B, hipStream_t s) {
+  if (p.R < p.nC) {   // pipelined, R == 1
+    hipLaunchKernelGGL((agg_kernel<DH, NS, GLA>), dim3(p.nC, p.H, (unsigned)B), dim3(64), 0, s, p, 0);
+    if (int rc = check_launch("chunked forward aggregates")) return rc;
+    hipLaunchKernelGGL((pass_kernel<DH, NS, GLA>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0, s, p, 0);
+    if (int rc = check_launch("chunked forward state pass")) return rc;
+    hipLaunchKernelGGL((fwd_kernel<DH, NS, true, GLA>), dim3(p.nC, p.H, (unsigned)B), dim3(256), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((fwd_kernel<DH, NS, false, GLA>), dim3(1, p.H, (unsigned)B), dim3(256), 0, s, p);
+  }
+  return check_launch("chunked forward");
+}
+
+}  // namespace chunked
+}  // namespace rr

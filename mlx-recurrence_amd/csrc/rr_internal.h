@@ -1,5 +1,5 @@
 // rr_internal.h — interfaces between the C-ABI entry points and the chunked
-// (MFMA) SSD kernels.  Not part of the public ABI.
+// (MFMA) SSD and GLA kernels.  Not part of the public ABI.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -7,8 +7,10 @@
 
 namespace rr {
 
-
-struct Ssd2Args {
+// Arguments of the chunked kernels, named for SSD.  GLA maps onto them as
+// u = v, delta = gates, Bm = k, Cm = q (du = dv, ddelta = dgates, dB = dk,
+// dC = dq); A, A_stride_h and dA are unused there.
+struct ChunkArgs {
   const uint16_t* u;       // [B,L,H,Dh] bf16
   const uint16_t* delta;   // [B,L,H]
   const uint16_t* Bm;      // [B,L,H,N]
@@ -27,12 +29,13 @@ struct Ssd2Args {
   uint16_t* dC;
   float* dA;               // [H,N]
   float* dh0;              // [B,H,Dh,N] or null
-  float* ws;               // backward: dA partials [B,H,nR,N]
-  float* tot;              // pipelined: per-chunk delta totals [B,H,nC]
+  float* ws;               // SSD backward: dA partials [B,H,nR,N]
+  float* tot;              // pipelined: per-chunk decay gam_31 [B,H,nC]
   float* agg;              // pipelined backward: chunk aggregates, then adjoints [B,H,nC,Dh,N]
   int L, H, DH, NS, nC, R;
 };
 
+// ------------------------------------------------------------------ SSD
 // True when the chunked kernels cover this call: bf16 inputs, a head-uniform A
 // (A_stride_n == 0), checkpoint interval 32, Dh in {32, 64, 128} and
 // N in {16, 32, 64, 128}.
@@ -40,14 +43,27 @@ bool ssd2_supported(int dtype, int64_t L, int64_t seg, int64_t Dh, int64_t N, in
 // Chunks per workgroup: 1 (pipelined: aggregate, pass and main kernels) or
 // nC (one workgroup walks a whole head).
 int ssd2_pick_run(int64_t B, int64_t H, int64_t nC, int64_t N);
-int ssd2_fwd(const Ssd2Args& p, int64_t B, hipStream_t s);
+int ssd2_fwd(const ChunkArgs& p, int64_t B, hipStream_t s);
 // The chunked backward covers Dh in {32, 64} and N in {16, 32} (on top of
 // ssd2_supported).
 bool ssd2_bwd_supported(int64_t Dh, int64_t N);
-// Workspace of the chunked passes: chunk aggregates + delta totals when runs
+// Workspace of the chunked passes: chunk aggregates + chunk decays when runs
 // are shorter than a head (pass 0 and 1), plus dA partials (pass 1).
 size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int R, int64_t Dh, int64_t N, int pass);
-void ssd2_carve_ws(Ssd2Args& a, void* ws, int64_t B, int pass);
-int ssd2_bwd(const Ssd2Args& p, int64_t B, hipStream_t s);
+void ssd2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass);
+int ssd2_bwd(const ChunkArgs& p, int64_t B, hipStream_t s);
+
+// ------------------------------------------------------------------ GLA
+// True when the chunked GLA kernels cover this call (pass 0 forward, 1
+// backward): bf16 inputs, checkpoint interval 32, Dh in {32, 64, 128}
+// (forward) or {32, 64} (backward).  Always pipelined (one chunk per
+// workgroup).
+bool gla2_supported(int dtype, int64_t L, int64_t seg, int64_t Dh, int pass);
+// Workspace: chunk decays [B,H,nC] (both passes) and the backward chunk
+// adjoints [B,H,nC,Dh,Dh] (pass 1).
+size_t gla2_ws_bytes(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass);
+void gla2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass);
+int gla2_fwd(const ChunkArgs& p, int64_t B, hipStream_t s);
+int gla2_bwd(const ChunkArgs& p, int64_t B, hipStream_t s);
 
 }  // namespace rr

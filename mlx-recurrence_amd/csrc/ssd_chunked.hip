@@ -4,25 +4,17 @@
 // configurations), the decay from step s to step t of a chunk is one scalar
 // per head, M[t, s] = exp(a (cd_t - cd_s)) (cd = in-chunk cumulative delta), and
 // a 32-step chunk of the recurrence (reference ssd.py:85-111) becomes dense
-// products (the "SSD dual" form):
-//     Y     = (M o C B^T o delta_s) U  +  diag(gam) C h_in^T
-//     h_end = Gam h_in + U^T diag(w) B,   gam_t = exp(a cd_t), w_s = M[31, s] delta_s
-// with U [32 x Dh], B/C [32 x N] the chunk's inputs.  Every product is a bf16
-// MFMA (inputs exact in bf16; fp32 factors split into hi + lo bf16 halves).
+// products (the "SSD dual" form, rr_chunked.h).  The forward kernels are the
+// shared ones of rr_chunked.h; this file holds the SSD backward.
 //
 // Work decomposition: a workgroup of 4 waves owns a run of R consecutive chunks
 // of one (batch, head) and walks them in order, keeping the state h [Dh x N]
-// in registers (16x16 MFMA accumulator blocks, block j owned by wave j % 4).
-// The state entering the run is the weighted sum over all earlier steps
-//     h_in = sum_{s < start} exp(a sum_{r=s+1}^{start-1} delta_r) delta_s u_s B_s^T (+ decayed h0)
-// computed as the same MFMA product over the earlier chunks (each wave takes
-// every 4th chunk; the four partial sums are added in a fixed order), so runs
-// are independent and the grid needs no inter-workgroup communication.  The
-// host picks R = 1 (one workgroup per chunk) when there are few heads and
-// R = all chunks when there are many.
-#include "rr_common.h"
-#include "rr_internal.h"
-#include "rr_mfma.h"
+// (forward) or the adjoint (backward) in registers as 16x16 MFMA accumulator
+// blocks, block j owned by wave j % 4.  The host picks R = all chunks of the
+// head when there are enough heads to fill the GPU, else R = 1: then the
+// chunk aggregates are formed first and one pass per state element carries
+// the state (adjoint) across chunks (the pipelined mode of rr_chunked.h).
+#include "rr_chunked.h"
 
 namespace {
 
@@ -34,394 +26,11 @@ using rr::frag;
 using rr::mfma16;
 using rr::mfma32;
 using rr::u16x8_t;
-
-constexpr int Q = 32;    // chunk length
-constexpr int PQ = Q + 8;  // LDS pitch (elements) of [*][s] arrays: 80 bytes
-
-template <int DH, int NS>
-struct Cfg {
-  static constexpr int PN = NS + 8;          // LDS pitch of [*][n] arrays
-  static constexpr int NBD = DH / 16, NBN = NS / 16, NB = NBD * NBN;
-  static constexpr int NBW = (NB + 3) / 4;   // state blocks per wave
-  static constexpr int NYB = DH / 32;        // 32x32 output blocks of Y
-};
-
-template <int DH, int NS>
-struct FwdSmem {
-  uint16_t Ut[DH][PQ];      // U^T  [d][s]
-  uint16_t C[Q][Cfg<DH, NS>::PN];   // C    [t][n]
-  uint16_t B[Q][Cfg<DH, NS>::PN];   // B    [s][n]
-  uint16_t BwT_hi[NS][PQ];  // (w o B)^T [n][s]
-  uint16_t BwT_lo[NS][PQ];
-  uint16_t W_hi[Q][PQ];     // M o CB^T o delta_s  [t][s]
-  uint16_t W_lo[Q][PQ];
-  uint16_t H_hi[DH][Cfg<DH, NS>::PN];  // h_in [d][n]
-  uint16_t H_lo[DH][Cfg<DH, NS>::PN];
-  float del[Q], cd[Q], gam[Q], wend[Q];
-};
-
-template <int DH, int NS>
-union FwdShared {
-  FwdSmem<DH, NS> f;
-};
-
-// Inclusive prefix sum over lanes 0..31 (values of lanes >= 32 ignored).
-__device__ __forceinline__ float prefix32(float v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 32; o <<= 1) {
-    const float x = __shfl_up(v, o, 32);
-    if ((lane & 31) >= o) v += x;
-  }
-  return v;
-}
-
-// Pipelined mode (several workgroups per head).  Three kernels per pass:
-//  1. ssd2_agg_kernel, one wave per chunk k, writes the chunk's aggregate and
-//     its delta total tot_k:
-//       forward:  S_k = U_k^T diag(w) B_k, the state the chunk adds from a zero
-//                 start (into checkpoint slot k);
-//       backward: G_k = (gam o dY_k)^T C_k, the adjoint the chunk sends back to
-//                 its start (into the workspace).
-//  2. ssd2_pass_kernel, one thread per state element, walks the chunks in order:
-//       forward:  h_k = exp(a tot_k) h_{k-1} + S_k   (h_{-1} = h0), into slot k
-//       backward: lam_k = adjoint of the state leaving chunk k,
-//                 lam_{nC-1} = dfinal, lam_{k-1} = exp(a tot_k) lam_k + G_k,
-//                 and dh0 = exp(a tot_0) lam_0 + G_0.
-//  3. the main kernel, one workgroup per chunk, reads its entering state
-//     (and, backward, lam_k) and does the chunk's dense products.
-template <int DH, int NS>
-__global__ __launch_bounds__(64) void ssd2_agg_kernel(rr::Ssd2Args p, int kind) {
-  constexpr int NBN = NS / 16, NB = (DH / 16) * NBN;
-  __shared__ uint16_t XT_hi[DH][PQ], XT_lo[DH][PQ];   // kind 0: U^T [d][s] (hi only); kind 1: (gam o dY)^T
-  __shared__ uint16_t YT_hi[NS][PQ], YT_lo[NS][PQ];   // kind 0: (w o B)^T split; kind 1: C^T (hi only)
-  const int lane = threadIdx.x;
-  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const float a = p.A[(int64_t)h * p.A_stride_h];
-  const int64_t rowH = p.H, row0 = (int64_t)b * p.L + (int64_t)c * Q;
-  constexpr int UV = Q * DH / 8 / 64, GV = Q * DH / 4 / 64, BV = (Q * NS / 8 + 63) / 64;
-  // loads first
-  u16x8_t uv[UV], bv[BV];
-  float4 gv[GV];
-  if (kind == 0) {
-#pragma unroll
-    for (int v = 0; v < UV; ++v) {
-      const int i = lane + 64 * v, tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
-      uv[v] = *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0);
-    }
-  } else {
-#pragma unroll
-    for (int v = 0; v < GV; ++v) {
-      const int i = lane + 64 * v, tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
-      gv[v] = *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0);
-    }
-  }
-  const uint16_t* bsrc = kind == 0 ? p.Bm : p.Cm;
-#pragma unroll
-  for (int v = 0; v < BV; ++v) {
-    const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
-    bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(bsrc + ((row0 + tl) * rowH + h) * NS + n0) : u16x8_t{};
-  }
-  const float dv = lane < Q ? bf_val(p.delta[(row0 + lane) * rowH + h]) : 0.f;
-  const float cdv = prefix32(dv, lane);
-  const float c31 = __shfl(cdv, 31);
-  // kind 0: w_s = exp(a (c31 - cd_s)) delta_s ; kind 1: gam_t = exp(a cd_t)
-  const float wt = kind == 0 ? __expf(a * (c31 - cdv)) * dv : __expf(a * cdv);
-  if (kind == 0) {
-#pragma unroll
-    for (int v = 0; v < UV; ++v) {
-      const int i = lane + 64 * v, tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
-#pragma unroll
-      for (int e = 0; e < 8; ++e) XT_hi[d0 + e][tl] = uv[v][e];
-    }
-  } else {
-#pragma unroll
-    for (int v = 0; v < GV; ++v) {
-      const int i = lane + 64 * v, tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
-      const float g4[4] = {gv[v].x, gv[v].y, gv[v].z, gv[v].w};
-      const float gt = __shfl(wt, tl);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        uint16_t hi, lo;
-        bf_split(gt * g4[e], hi, lo);
-        XT_hi[d0 + e][tl] = hi;
-        XT_lo[d0 + e][tl] = lo;
-      }
-    }
-  }
-#pragma unroll
-  for (int v = 0; v < BV; ++v) {
-    const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
-    const float ws = __shfl(wt, tl);
-    if (i < Q * NS / 8) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if (kind == 0) {
-          uint16_t hi, lo;
-          bf_split(ws * bf_val(bv[v][e]), hi, lo);
-          YT_hi[n0 + e][tl] = hi;
-          YT_lo[n0 + e][tl] = lo;
-        } else {
-          YT_hi[n0 + e][tl] = bv[v][e];
-        }
-      }
-    }
-  }
-  rr::wave_lds_sync();
-  float* dst = (kind == 0 ? p.ckpt : p.agg) + (((int64_t)b * p.H + h) * p.nC + c) * DH * NS;
-#pragma unroll
-  for (int j = 0; j < NB; ++j) {
-    const int db = j / NBN, nb = j % NBN;
-    const u16x8_t fa = frag(&XT_hi[16 * db + (lane & 15)][8 * (lane >> 4)]);
-    const u16x8_t fb = frag(&YT_hi[16 * nb + (lane & 15)][8 * (lane >> 4)]);
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    acc = mfma16(fa, fb, acc);
-    if (kind == 0) acc = mfma16(fa, frag(&YT_lo[16 * nb + (lane & 15)][8 * (lane >> 4)]), acc);
-    else acc = mfma16(frag(&XT_lo[16 * db + (lane & 15)][8 * (lane >> 4)]), fb, acc);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) dst[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)] = acc[r];
-  }
-  if (lane == 0) p.tot[((int64_t)b * p.H + h) * p.nC + c] = c31;
-}
-
-// Sequential pass over the chunks of one (batch, head), one state element per
-// thread; loads are issued kPass chunks ahead of their use.
-template <int DH, int NS>
-__global__ __launch_bounds__(256) void ssd2_pass_kernel(rr::Ssd2Args p, int kind) {
-  constexpr int kPass = 8;
-  const int e = blockIdx.x * 256 + threadIdx.x;   // element d * NS + n
-  const int h = blockIdx.y, b = blockIdx.z;
-  const float a = p.A[(int64_t)h * p.A_stride_h];
-  const int64_t bh = (int64_t)b * p.H + h;
-  const float* tot = p.tot + bh * p.nC;
-  const int nC = p.nC;
-  if (kind == 0) {
-    float* buf = p.ckpt + bh * nC * (DH * NS) + e;
-    float x = p.h0 != nullptr ? p.h0[bh * DH * NS + e] : 0.f;
-    for (int k0 = 0; k0 < nC; k0 += kPass) {
-      float sv[kPass], tv[kPass];
-#pragma unroll
-      for (int q = 0; q < kPass; ++q) {
-        const bool ok = k0 + q < nC;
-        sv[q] = ok ? buf[(int64_t)(k0 + q) * DH * NS] : 0.f;
-        tv[q] = ok ? tot[k0 + q] : 0.f;
-      }
-#pragma unroll
-      for (int q = 0; q < kPass; ++q) {
-        if (k0 + q < nC) {
-          x = __expf(a * tv[q]) * x + sv[q];
-          buf[(int64_t)(k0 + q) * DH * NS] = x;
-        }
-      }
-    }
-  } else {
-    float* buf = p.agg + bh * nC * (DH * NS) + e;
-    float x = p.dfinal != nullptr ? p.dfinal[bh * DH * NS + e] : 0.f;
-    for (int k0 = nC - 1; k0 >= 0; k0 -= kPass) {
-      float gv[kPass], tv[kPass];
-#pragma unroll
-      for (int q = 0; q < kPass; ++q) {
-        const bool ok = k0 - q >= 0;
-        gv[q] = ok ? buf[(int64_t)(k0 - q) * DH * NS] : 0.f;
-        tv[q] = ok ? tot[k0 - q] : 0.f;
-      }
-#pragma unroll
-      for (int q = 0; q < kPass; ++q) {
-        if (k0 - q >= 0) {
-          buf[(int64_t)(k0 - q) * DH * NS] = x;
-          x = __expf(a * tv[q]) * x + gv[q];
-        }
-      }
-    }
-    if (p.dh0 != nullptr) p.dh0[bh * DH * NS + e] = x;
-  }
-}
-
-// PIPE: one chunk per workgroup, entering state from checkpoint slot c - 1
-// (written by ssd2_pass_kernel); otherwise a whole head per workgroup.
-template <int DH, int NS, bool PIPE>
-__global__ __launch_bounds__(256) void ssd2_fwd_kernel(rr::Ssd2Args p) {
-  using K = Cfg<DH, NS>;
-  __shared__ FwdShared<DH, NS> sm;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int cbeg = blockIdx.x * p.R;
-  const int cend = min(cbeg + p.R, p.nC);
-  const float a = p.A[(int64_t)h * p.A_stride_h];
-  const int64_t rowH = p.H;
-
-  f32x4_t hst[K::NBW];
-#pragma unroll
-  for (int jj = 0; jj < K::NBW; ++jj) hst[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const float* hsrc = cbeg > 0 ? p.ckpt + (((int64_t)b * p.H + h) * p.nC + cbeg - 1) * DH * NS
-                              : (p.h0 != nullptr ? p.h0 + ((int64_t)b * p.H + h) * DH * NS : nullptr);
-  if (hsrc != nullptr) {
-#pragma unroll
-    for (int jj = 0; jj < K::NBW; ++jj) {
-      const int j = w + 4 * jj;
-      if (j < K::NB) {
-        const int db = j / K::NBN, nb = j % K::NBN;
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          hst[jj][r] = hsrc[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)];
-      }
-    }
-  }
-
-  for (int c = cbeg; c < cend; ++c) {
-    const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;  // first (b, t) row of the chunk
-    // ---- stage the chunk's inputs (all loads issued before any use)
-    {
-      constexpr int UV = (Q * DH / 8 + 255) / 256, BV = (Q * NS / 8 + 255) / 256;
-      u16x8_t uv[UV], bv[BV], cv[BV];
-      float dv = 0.f;
-#pragma unroll
-      for (int v = 0; v < UV; ++v) {
-        const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
-        uv[v] = i < Q * DH / 8 ? *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0) : u16x8_t{};
-      }
-#pragma unroll
-      for (int v = 0; v < BV; ++v) {
-        const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
-        const int64_t g = ((row0 + tl) * rowH + h) * NS + n0;
-        bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Bm + g) : u16x8_t{};
-        cv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Cm + g) : u16x8_t{};
-      }
-      if (tid < Q) dv = bf_val(p.delta[(row0 + tid) * rowH + h]);
-#pragma unroll
-      for (int v = 0; v < UV; ++v) {
-        const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
-        if (i < Q * DH / 8) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) sm.f.Ut[d0 + e][tl] = uv[v][e];
-        }
-      }
-#pragma unroll
-      for (int v = 0; v < BV; ++v) {
-        const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
-        if (i < Q * NS / 8) {
-          *reinterpret_cast<u16x8_t*>(&sm.f.B[tl][n0]) = bv[v];
-          *reinterpret_cast<u16x8_t*>(&sm.f.C[tl][n0]) = cv[v];
-        }
-      }
-      if (tid < Q) sm.f.del[tid] = dv;
-    }
-    __syncthreads();
-    // ---- per-step scalars (wave 0) and h_in split (every wave, its blocks)
-    if (w == 0) {
-      const float dv = lane < Q ? sm.f.del[lane] : 0.f;
-      const float cdv = prefix32(dv, lane);
-      const float c31 = __shfl(cdv, 31);
-      if (lane < Q) {
-        sm.f.cd[lane] = cdv;
-        sm.f.gam[lane] = __expf(a * cdv);
-        if constexpr (!PIPE) sm.f.wend[lane] = __expf(a * (c31 - cdv)) * dv;
-      }
-    }
-#pragma unroll
-    for (int jj = 0; jj < K::NBW; ++jj) {
-      const int j = w + 4 * jj;
-      if (j < K::NB) {
-        const int db = j / K::NBN, nb = j % K::NBN;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          uint16_t hi, lo;
-          bf_split(hst[jj][r], hi, lo);
-          const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
-          sm.f.H_hi[d][n] = hi;
-          sm.f.H_lo[d][n] = lo;
-        }
-      }
-    }
-    __syncthreads();
-    // ---- W = M o CB^T o delta_s (wave 0); (w o B)^T (waves 1..3)
-    if (w == 0) {
-      f32x16_t cb = {};
-#pragma unroll
-      for (int kb = 0; kb < NS / 16; ++kb)
-        cb = mfma32(frag(&sm.f.C[lane & 31][16 * kb + 8 * (lane >> 5)]),
-                    frag(&sm.f.B[lane & 31][16 * kb + 8 * (lane >> 5)]), cb);
-      const int s = lane & 31;
-      const float cds = sm.f.cd[s], ds = sm.f.del[s];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int t = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const float v = (s <= t) ? __expf(a * (sm.f.cd[t] - cds)) * ds * cb[r] : 0.f;
-        uint16_t hi, lo;
-        bf_split(v, hi, lo);
-        sm.f.W_hi[t][s] = hi;
-        sm.f.W_lo[t][s] = lo;
-      }
-    } else if constexpr (!PIPE) {
-      for (int i = tid - 64; i < Q * NS; i += 192) {
-        const int n = i / Q, s = i % Q;
-        uint16_t hi, lo;
-        bf_split(sm.f.wend[s] * bf_val(sm.f.B[s][n]), hi, lo);
-        sm.f.BwT_hi[n][s] = hi;
-        sm.f.BwT_lo[n][s] = lo;
-      }
-    }
-    __syncthreads();
-    // ---- Y blocks (waves < DH/32)
-    if (w < K::NYB) {
-      const int d0 = 32 * w;
-      f32x16_t yi = {}, ye = {};
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const u16x8_t fb = frag(&sm.f.Ut[d0 + (lane & 31)][16 * kb + 8 * (lane >> 5)]);
-        yi = mfma32(frag(&sm.f.W_hi[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, yi);
-        yi = mfma32(frag(&sm.f.W_lo[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, yi);
-      }
-#pragma unroll
-      for (int kb = 0; kb < NS / 16; ++kb) {
-        const u16x8_t fa = frag(&sm.f.C[lane & 31][16 * kb + 8 * (lane >> 5)]);
-        ye = mfma32(fa, frag(&sm.f.H_hi[d0 + (lane & 31)][16 * kb + 8 * (lane >> 5)]), ye);
-        ye = mfma32(fa, frag(&sm.f.H_lo[d0 + (lane & 31)][16 * kb + 8 * (lane >> 5)]), ye);
-      }
-      const int d = d0 + (lane & 31);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int t = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        p.y[((row0 + t) * rowH + h) * DH + d] = yi[r] + sm.f.gam[t] * ye[r];
-      }
-    }
-    // ---- h_end = Gam h_in + U^T (w o B): every wave, its blocks; checkpoint
-    if constexpr (PIPE) break;
-    const float Gam = sm.f.gam[Q - 1];
-#pragma unroll
-    for (int jj = 0; jj < K::NBW; ++jj) {
-      const int j = w + 4 * jj;
-      if (j < K::NB) {
-        const int db = j / K::NBN, nb = j % K::NBN;
-        const u16x8_t fa = frag(&sm.f.Ut[16 * db + (lane & 15)][8 * (lane >> 4)]);
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-        acc = mfma16(fa, frag(&sm.f.BwT_hi[16 * nb + (lane & 15)][8 * (lane >> 4)]), acc);
-        acc = mfma16(fa, frag(&sm.f.BwT_lo[16 * nb + (lane & 15)][8 * (lane >> 4)]), acc);
-        float* ck = p.ckpt + (((int64_t)b * p.H + h) * p.nC + c) * DH * NS;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          hst[jj][r] = Gam * hst[jj][r] + acc[r];
-          ck[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)] = hst[jj][r];
-        }
-      }
-    }
-    __syncthreads();
-  }
-}
-
-template <int DH, int NS>
-int launch_fwd(const rr::Ssd2Args& p, int64_t B, hipStream_t s) {
-  if (p.R < p.nC) {   // pipelined, R == 1
-    hipLaunchKernelGGL((ssd2_agg_kernel<DH, NS>), dim3(p.nC, p.H, (unsigned)B), dim3(64), 0, s, p, 0);
-    if (int rc = rr::check_launch("ssd chunked forward aggregates")) return rc;
-    hipLaunchKernelGGL((ssd2_pass_kernel<DH, NS>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0, s,
-                       p, 0);
-    if (int rc = rr::check_launch("ssd chunked forward state pass")) return rc;
-    hipLaunchKernelGGL((ssd2_fwd_kernel<DH, NS, true>), dim3(p.nC, p.H, (unsigned)B), dim3(256), 0, s, p);
-  } else {
-    hipLaunchKernelGGL((ssd2_fwd_kernel<DH, NS, false>), dim3(1, p.H, (unsigned)B), dim3(256), 0, s, p);
-  }
-  return rr::check_launch("ssd chunked forward");
-}
+using rr::chunked::Cfg;
+using rr::chunked::prefix32;
+using rr::chunked::PQ;
+using rr::chunked::Q;
+using rr::chunked::r32row;
 
 }  // namespace
 
@@ -443,20 +52,20 @@ int ssd2_pick_run(int64_t B, int64_t H, int64_t nC, int64_t N) {
   return 1;
 }
 
-int ssd2_fwd(const Ssd2Args& p, int64_t B, hipStream_t s) {
+int ssd2_fwd(const ChunkArgs& p, int64_t B, hipStream_t s) {
   switch (p.DH * 1000 + p.NS) {
-    case 32016: return launch_fwd<32, 16>(p, B, s);
-    case 32032: return launch_fwd<32, 32>(p, B, s);
-    case 32064: return launch_fwd<32, 64>(p, B, s);
-    case 32128: return launch_fwd<32, 128>(p, B, s);
-    case 64016: return launch_fwd<64, 16>(p, B, s);
-    case 64032: return launch_fwd<64, 32>(p, B, s);
-    case 64064: return launch_fwd<64, 64>(p, B, s);
-    case 64128: return launch_fwd<64, 128>(p, B, s);
-    case 128016: return launch_fwd<128, 16>(p, B, s);
-    case 128032: return launch_fwd<128, 32>(p, B, s);
-    case 128064: return launch_fwd<128, 64>(p, B, s);
-    case 128128: return launch_fwd<128, 128>(p, B, s);
+    case 32016: return chunked::launch_fwd<32, 16, false>(p, B, s);
+    case 32032: return chunked::launch_fwd<32, 32, false>(p, B, s);
+    case 32064: return chunked::launch_fwd<32, 64, false>(p, B, s);
+    case 32128: return chunked::launch_fwd<32, 128, false>(p, B, s);
+    case 64016: return chunked::launch_fwd<64, 16, false>(p, B, s);
+    case 64032: return chunked::launch_fwd<64, 32, false>(p, B, s);
+    case 64064: return chunked::launch_fwd<64, 64, false>(p, B, s);
+    case 64128: return chunked::launch_fwd<64, 128, false>(p, B, s);
+    case 128016: return chunked::launch_fwd<128, 16, false>(p, B, s);
+    case 128032: return chunked::launch_fwd<128, 32, false>(p, B, s);
+    case 128064: return chunked::launch_fwd<128, 64, false>(p, B, s);
+    case 128128: return chunked::launch_fwd<128, 128, false>(p, B, s);
     default: return fail(RR_EUNSUPPORTED, "ssd chunked: unsupported (Dh, N)");
   }
 }
@@ -481,8 +90,8 @@ int ssd2_fwd(const Ssd2Args& p, int64_t B, hipStream_t s) {
 //           + gam_31 cd_31 sum_d lam h_in - sum delta^2 B Z,  K = M o delta_s o G2 o span
 //   lam_prev = (gam o dY)^T C + gam_31 lam
 // (derived from the per-step adjoint; checked against the float64 oracle).
-// The adjoint entering a run from later chunks is the weighted sum
-//   lam = sum_{t >= end} exp(a sum_{r=end}^{t} delta_r) dy_t C_t^T + exp(a sum_{r>=end} delta_r) dfinal.
+// A whole-head run starts from lam = dfinal and carries lam_prev backwards in
+// registers; a pipelined workgroup reads its lam from pass_kernel.
 
 namespace {
 
@@ -533,12 +142,10 @@ struct BwdSmem {
   float dAp[4][4][NS];
 };
 
-__device__ __forceinline__ int r32row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
-
-// PIPE: one chunk per workgroup, lam from the workspace (ssd2_pass_kernel);
+// PIPE: one chunk per workgroup, lam from the workspace (pass_kernel);
 // otherwise a whole head per workgroup, lam carried backwards in registers.
 template <int DH, int NS, bool PIPE>
-__global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::Ssd2Args p) {
+__global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
   using K = Cfg<DH, NS>;
   __shared__ BwdSmem<DH, NS, PIPE> m;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -1001,12 +608,12 @@ __global__ __launch_bounds__(256) void ssd2_dA_kernel(const float* __restrict__ 
 }
 
 template <int DH, int NS>
-int launch_bwd(const rr::Ssd2Args& p, int64_t B, hipStream_t s) {
+int launch_bwd(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
   const int nR = (p.nC + p.R - 1) / p.R;
   if (nR > 1) {   // pipelined, R == 1
-    hipLaunchKernelGGL((ssd2_agg_kernel<DH, NS>), dim3(p.nC, p.H, (unsigned)B), dim3(64), 0, s, p, 1);
+    hipLaunchKernelGGL((rr::chunked::agg_kernel<DH, NS, false>), dim3(p.nC, p.H, (unsigned)B), dim3(64), 0, s, p, 1);
     if (int rc = rr::check_launch("ssd chunked backward aggregates")) return rc;
-    hipLaunchKernelGGL((ssd2_pass_kernel<DH, NS>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0, s,
+    hipLaunchKernelGGL((rr::chunked::pass_kernel<DH, NS, false>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0, s,
                        p, 1);
     if (int rc = rr::check_launch("ssd chunked backward adjoint pass")) return rc;
     hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, true>), dim3(nR, p.H, (unsigned)B), dim3(256), 0, s, p);
@@ -1044,7 +651,7 @@ size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int R, int64_t Dh, int64_
   return (size_t)f * sizeof(float);
 }
 
-void ssd2_carve_ws(Ssd2Args& a, void* ws, int64_t B, int pass) {
+void ssd2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass) {
   float* f = static_cast<float*>(ws);
   const int64_t nR = (a.nC + a.R - 1) / a.R;
   const bool pipe = nR > 1;
@@ -1056,7 +663,7 @@ void ssd2_carve_ws(Ssd2Args& a, void* ws, int64_t B, int pass) {
   }
 }
 
-int ssd2_bwd(const Ssd2Args& p, int64_t B, hipStream_t s) {
+int ssd2_bwd(const ChunkArgs& p, int64_t B, hipStream_t s) {
   switch (p.DH * 1000 + p.NS) {
     case 32016: return launch_bwd<32, 16>(p, B, s);
     case 32032: return launch_bwd<32, 32>(p, B, s);

@@ -571,7 +571,7 @@ extern "C" int rr_ssd_fwd(const void* u, const void* delta, const void* Bm, cons
     return rr::fail(RR_EINVAL, "ssd_fwd: A_stride_n must be 0 or 1");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (rr::ssd2_supported(dtype, L, seg, Dh, N, A_stride_n)) {
-    rr::Ssd2Args a{};
+    rr::ChunkArgs a{};
     a.u = static_cast<const uint16_t*>(u);
     a.delta = static_cast<const uint16_t*>(delta);
     a.Bm = static_cast<const uint16_t*>(Bm);
@@ -630,7 +630,7 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
     const int R = rr::ssd2_pick_run(B, H, nC, N);
     if (!workspace || workspace_bytes < rr::ssd2_ws_bytes(B, H, nC, R, Dh, N, 1))
       return rr::fail(RR_EWORKSPACE, "ssd_bwd: workspace too small");
-    rr::Ssd2Args a{};
+    rr::ChunkArgs a{};
     a.u = static_cast<const uint16_t*>(u);
     a.delta = static_cast<const uint16_t*>(delta);
     a.Bm = static_cast<const uint16_t*>(Bm);
@@ -695,9 +695,27 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
 }
 
 // ====================================================================== GLA
+namespace {
+// Chunked-kernel arguments of a GLA call (u = v, delta = gates, Bm = k, Cm = q).
+rr::ChunkArgs gla2_args(const void* qp, const void* kp, const void* vp, const void* gates, int64_t B,
+                        int64_t L, int64_t H, int64_t Dh, const float* h0) {
+  (void)B;
+  rr::ChunkArgs a{};
+  a.u = static_cast<const uint16_t*>(vp);
+  a.delta = static_cast<const uint16_t*>(gates);
+  a.Bm = static_cast<const uint16_t*>(kp);
+  a.Cm = static_cast<const uint16_t*>(qp);
+  a.h0 = h0;
+  a.L = (int)L; a.H = (int)H; a.DH = (int)Dh; a.NS = (int)Dh; a.nC = (int)(L / 32);
+  a.R = 1;
+  return a;
+}
+}  // namespace
+
 extern "C" size_t rr_gla_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh,
-                                         int64_t seg, int pass) {
+                                         int64_t seg, int dtype, int pass) {
   if (B <= 0 || L <= 0 || H <= 0 || Dh <= 0 || rr::chunk_len(L, seg) == 0) return 0;
+  if (rr::gla2_supported(dtype, L, seg, Dh, pass)) return rr::gla2_ws_bytes(B, H, L / 32, Dh, pass);
   const Plan q = make_plan(B, L, H, Dh, Dh, seg);
   return pass == 0 ? q.fwd_bytes : q.bwd_bytes;
 }
@@ -709,10 +727,19 @@ extern "C" int rr_gla_fwd(const void* qp, const void* kp, const void* vp, const 
   if (int rc = check_dims("gla_fwd", B, L, H, Dh, Dh, seg, dtype, "Dh")) return rc;
   if (!qp || !kp || !vp || !gates || !y || !ckpt)
     return rr::fail(RR_EINVAL, "gla_fwd: null pointer argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (rr::gla2_supported(dtype, L, seg, Dh, 0)) {
+    rr::ChunkArgs a = gla2_args(qp, kp, vp, gates, B, L, H, Dh, h0);
+    a.y = y;
+    a.ckpt = ckpt;
+    if (!workspace || workspace_bytes < rr::gla2_ws_bytes(B, H, a.nC, Dh, 0))
+      return rr::fail(RR_EWORKSPACE, "gla_fwd: workspace too small");
+    rr::gla2_carve_ws(a, workspace, B, 0);
+    return rr::gla2_fwd(a, B, s);
+  }
   const Plan q = make_plan(B, L, H, Dh, Dh, seg);
   if (workspace_bytes < q.fwd_bytes || (q.fwd_bytes && !workspace))
     return rr::fail(RR_EWORKSPACE, "gla_fwd: workspace too small");
-  hipStream_t s = static_cast<hipStream_t>(stream);
   RR_DISPATCH_DTYPE(dtype, {
     Args<InT> a{};
     a.lane_in = static_cast<const InT*>(vp);
@@ -737,6 +764,21 @@ extern "C" int rr_gla_bwd(const float* dy, const float* dfinal, const void* qp, 
   if (int rc = check_dims("gla_bwd", B, L, H, Dh, Dh, seg, dtype, "Dh")) return rc;
   if (!dy || !qp || !kp || !vp || !gates || !ckpt || !dq || !dk || !dv || !dgates)
     return rr::fail(RR_EINVAL, "gla_bwd: null pointer argument");
+  if (rr::gla2_supported(dtype, L, seg, Dh, 1)) {
+    rr::ChunkArgs a = gla2_args(qp, kp, vp, gates, B, L, H, Dh, h0);
+    a.ckpt = const_cast<float*>(ckpt);
+    a.dy = dy;
+    a.dfinal = dfinal;
+    a.du = static_cast<uint16_t*>(dv);
+    a.ddelta = static_cast<uint16_t*>(dgates);
+    a.dB = static_cast<uint16_t*>(dk);
+    a.dC = static_cast<uint16_t*>(dq);
+    a.dh0 = dh0;
+    if (!workspace || workspace_bytes < rr::gla2_ws_bytes(B, H, a.nC, Dh, 1))
+      return rr::fail(RR_EWORKSPACE, "gla_bwd: workspace too small");
+    rr::gla2_carve_ws(a, workspace, B, 1);
+    return rr::gla2_bwd(a, B, static_cast<hipStream_t>(stream));
+  }
   const Plan q = make_plan(B, L, H, Dh, Dh, seg);
   if (workspace_bytes < q.bwd_bytes || !workspace)
     return rr::fail(RR_EWORKSPACE, "gla_bwd: workspace too small");

@@ -39,7 +39,7 @@ _SIGS = {
     "rr_ssd_workspace_bytes": (_c_size, [_c_i64] * 7 + [_c_int, _c_int]),
     "rr_ssd_fwd": (_c_int, [_c_ptr] * 5 + [_c_i64, _c_int] + [_c_i64] * 6 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
     "rr_ssd_bwd": (_c_int, [_c_ptr] * 7 + [_c_i64, _c_int] + [_c_i64] * 6 + [_c_ptr] * 9 + [_c_size, _c_ptr]),
-    "rr_gla_workspace_bytes": (_c_size, [_c_i64] * 5 + [_c_int]),
+    "rr_gla_workspace_bytes": (_c_size, [_c_i64] * 5 + [_c_int, _c_int]),
     "rr_gla_fwd": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
     "rr_gla_bwd": (_c_int, [_c_ptr] * 6 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 8 + [_c_size, _c_ptr]),
     "rr_rglru_fwd": (_c_int, [_c_ptr] * 2 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 4),
@@ -166,8 +166,8 @@ def ssd_bwd(dy, dfinal, u, delta, Bm, Cm, A, a_stride_n, h0, ckpt, seg, du, ddel
 
 
 # ---------------------------------------------------------------- GLA
-def gla_workspace(B, L, H, Dh, seg, pass_, device) -> torch.Tensor | None:
-    n = int(load().rr_gla_workspace_bytes(B, L, H, Dh, seg, pass_))
+def gla_workspace(B, L, H, Dh, seg, dtype, pass_, device) -> torch.Tensor | None:
+    n = int(load().rr_gla_workspace_bytes(B, L, H, Dh, seg, DTYPE_CODE[dtype], pass_))
     return torch.empty(n, dtype=torch.uint8, device=device) if n else None
 
 

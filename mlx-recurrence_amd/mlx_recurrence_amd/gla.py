@@ -47,7 +47,7 @@ class _GLAScan(torch.autograd.Function):
         y = torch.empty((B, L, H, Dh), dtype=torch.float32, device=dev)
         ckpt = torch.empty((B, H, nC, Dh, Dh), dtype=torch.float32, device=dev)
         with torch.cuda.device(dev):
-            ws = _lib.gla_workspace(B, L, H, Dh, seg, 0, dev)
+            ws = _lib.gla_workspace(B, L, H, Dh, seg, dt, 0, dev)
             _lib.gla_fwd(q_, k_, v_, g_, h0_, seg, y, ckpt, ws)
         ctx.save_for_backward(q_, k_, v_, g_, h0_, ckpt)
         ctx.seg = seg
@@ -65,7 +65,7 @@ class _GLAScan(torch.autograd.Function):
         dq, dk, dv, dg = (torch.empty_like(t) for t in (q_, k_, v_, g_))
         dh0 = torch.empty((B, H, Dh, Dh), dtype=torch.float32, device=dev) if ctx.needs_input_grad[4] else None
         with torch.cuda.device(dev):
-            ws = _lib.gla_workspace(B, L, H, Dh, ctx.seg, 1, dev)
+            ws = _lib.gla_workspace(B, L, H, Dh, ctx.seg, q_.dtype, 1, dev)
             _lib.gla_bwd(dy, dfinal, q_, k_, v_, g_, h0_, ckpt, ctx.seg, dq, dk, dv, dg, dh0, ws)
         return dq, dk, dv, dg, dh0, None
 

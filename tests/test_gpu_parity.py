@@ -252,6 +252,10 @@ def _gla_inputs(rng, B, L, H, Dh, dist):
     else:
         q, k, v = (rng.standard_normal((B, L, H, Dh)) / np.sqrt(Dh) for _ in range(3))
     g = _sigmoid(rng.standard_normal((B, L, H)) + 2.0)
+    if dist == "signed":   # gates of either sign (the kernels take any real gate)
+        g = rng.uniform(-1.0, 1.0, (B, L, H))
+    elif dist == "zeros":  # exact zero gates cut the recurrence
+        g[:, ::7] = 0.0
     return q, k, v, g
 
 
@@ -264,6 +268,13 @@ GLA_CASES = [
     (1, 40, 1, 128, 8, F32, "ref", True, True, 4),      # Dh = 128, T = 8
     (3, 512, 12, 64, 32, BF16, "cfg", False, False, 12),  # BASELINE config 2, full size
     (2, 256, 4, 64, 32, F16, "cfg", True, True, 13),
+    # bf16 with T = 32: chunked MFMA kernels
+    (2, 256, 3, 64, 32, BF16, "cfg", True, True, 20),
+    (1, 128, 2, 32, 32, BF16, "ref", True, True, 21),
+    (1, 96, 2, 128, 32, BF16, "cfg", True, True, 22),   # chunked forward, VALU backward
+    (2, 32, 2, 64, 32, BF16, "cfg", True, True, 23),    # one chunk
+    (1, 160, 2, 64, 32, BF16, "signed", True, True, 24),
+    (1, 128, 2, 32, 32, BF16, "zeros", True, True, 25),
 ]
 
 
