@@ -32,8 +32,11 @@ using rr::bf_val;
 using rr::f32x16_t;
 using rr::f32x4_t;
 using rr::frag;
+using rr::frag4;
 using rr::mfma16;
+using rr::mfma16k16;
 using rr::mfma32;
+using rr::u16x4_t;
 using rr::u16x8_t;
 using rr::chunked::PQ;
 using rr::chunked::Q;
@@ -42,7 +45,7 @@ using rr::chunked::r32row;
 // LDS of the backward kernel.  The operands that die after phase B1 (x) share
 // space with the masked products written in phase B2 (y).
 template <int D>
-struct GlaBwdSmem {
+struct alignas(16) GlaBwdSmem {
   static constexpr int PD = D + 8;
   uint16_t Kn[Q][PD];                    // k   [s][i]
   uint16_t Qn[Q][PD];                    // q   [t][i]
@@ -50,14 +53,10 @@ struct GlaBwdSmem {
   uint16_t QT[D][PQ];                    // q^T [i][t]
   uint16_t GYT_hi[D][PQ], GYT_lo[D][PQ]; // dY^T [j][t]
   uint16_t LM_hi[D][PD], LM_lo[D][PD];   // lam [j][i]
-  float GH[Q][D + 1];                    // dY h_in [t][i]
-  float UL[Q][D + 1];                    // V lam   [s][i]
   union {
     struct {                             // phase A -> B1
-      uint16_t V[Q][PD];                     // v [s][j]
+      uint16_t V[Q][PD];                     // v  [s][j]
       uint16_t GY_hi[Q][PD], GY_lo[Q][PD];   // dY [t][j]
-      uint16_t LMT_hi[D][PD], LMT_lo[D][PD]; // lam^T [i][j]
-      uint16_t HT_hi[D][PD], HT_lo[D][PD];   // h_in^T [i][j]
     } x;
     struct {                             // phase B2 -> C
       uint16_t PT_hi[Q][PQ], PT_lo[Q][PQ];   // P^T  [s][t']
@@ -68,59 +67,70 @@ struct GlaBwdSmem {
   float CB[Q][Q + 1];
   float G2[Q][Q + 1];
   float Cc[Q + 1][Q + 1];                // dg contributions M'[r, t] F_t[r]
-  float XY[2][Q];                        // X, Y
+  float XYp[4][2][Q];                    // per-wave partial X, Y
   float g[Q], gam[Q], m31[Q];
   float trw[4];
 };
 
+// Work split (4 waves).  The state tile [j][i] is cut into 16x16 blocks; wave
+// w owns the column blocks nb = w, w + 4, ... (all row blocks db), holding
+// h_in and lam of those blocks in registers, where they are directly the B
+// operands of 16x16x16 MFMAs contracting over j: so each wave forms
+// GH = dY h_in and UL = V lam for its columns in registers and later writes
+// dq and dk of the same columns.  dv row block db goes to wave (db + NBN) % 4.
 template <int D>
-__global__ __launch_bounds__(256) void gla_bwd_kernel(rr::ChunkArgs p) {
-  constexpr int NBN = D / 16, NB = NBN * NBN, NBW = (NB + 3) / 4;
+__global__ __launch_bounds__(256, 2) void gla_bwd_kernel(rr::ChunkArgs p) {
+  constexpr int NBN = D / 16, NBD = D / 16;
+  constexpr int CPW = (NBN + 3) / 4;   // column blocks per wave
   __shared__ GlaBwdSmem<D> m;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int64_t rowH = p.H;
   const int64_t bh = (int64_t)b * p.H + h;
-  const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;  // first (b, t) row of the chunk
+  const int64_t base = (((int64_t)b * p.L + (int64_t)c * Q) * p.H + h) * D;  // element (b, t0, h, 0)
+  const int rs = p.H * D;                                                   // step stride (elements)
+  const int l15 = lane & 15, l4 = lane >> 4;
 
+  f32x4_t lam[CPW][NBD], hin[CPW][NBD];
+  u16x4_t lam_hi[CPW][NBD], lam_lo[CPW][NBD], hin_hi[CPW][NBD], hin_lo[CPW][NBD];
   // ------------------------------------------------ A: stage (all loads first)
   {
     constexpr int UV = (Q * D / 8 + 255) / 256, GV = (Q * D / 4 + 255) / 256;
     u16x8_t vv[UV], kv[UV], qv[UV];
     float4 gv[GV];
-    f32x4_t lam[NBW], hin[NBW];
     float xv = 1.f;
 #pragma unroll
     for (int v = 0; v < UV; ++v) {
       const int i = tid + 256 * v, tl = (i / (D / 8)) & (Q - 1), d0 = 8 * (i % (D / 8));
       const bool ok = i < Q * D / 8;
-      const int64_t g = ((row0 + tl) * rowH + h) * D + d0;
-      vv[v] = ok ? *reinterpret_cast<const u16x8_t*>(p.u + g) : u16x8_t{};
-      kv[v] = ok ? *reinterpret_cast<const u16x8_t*>(p.Bm + g) : u16x8_t{};
-      qv[v] = ok ? *reinterpret_cast<const u16x8_t*>(p.Cm + g) : u16x8_t{};
+      const int off = tl * rs + d0;
+      vv[v] = ok ? *reinterpret_cast<const u16x8_t*>(p.u + base + off) : u16x8_t{};
+      kv[v] = ok ? *reinterpret_cast<const u16x8_t*>(p.Bm + base + off) : u16x8_t{};
+      qv[v] = ok ? *reinterpret_cast<const u16x8_t*>(p.Cm + base + off) : u16x8_t{};
     }
 #pragma unroll
     for (int v = 0; v < GV; ++v) {
       const int i = tid + 256 * v, tl = (i / (D / 4)) & (Q - 1), d0 = 4 * (i % (D / 4));
-      gv[v] = i < Q * D / 4 ? *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * D + d0)
+      gv[v] = i < Q * D / 4 ? *reinterpret_cast<const float4*>(p.dy + base + tl * rs + d0)
                             : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    if (tid < Q) xv = bf_val(p.delta[(row0 + tid) * rowH + h]);
+    if (tid < Q) xv = bf_val(p.delta[(base / D) + tid * p.H]);
     const float* lsrc = p.agg + (bh * p.nC + c) * D * D;
     const float* hsrc = c > 0 ? p.ckpt + (bh * p.nC + c - 1) * D * D
                               : (p.h0 != nullptr ? p.h0 + bh * D * D : nullptr);
 #pragma unroll
-    for (int jj = 0; jj < NBW; ++jj) {
-      const int j = w + 4 * jj;
-      lam[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      hin[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      if (j < NB) {
-        const int db = j / NBN, nb = j % NBN;
+    for (int cc = 0; cc < CPW; ++cc) {
+      const int nb = w + 4 * cc;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
-          lam[jj][r] = lsrc[d * D + n];
-          if (hsrc != nullptr) hin[jj][r] = hsrc[c > 0 ? d * D + n : rr::chunked::state_off<true, D, D>(d, n)];
+      for (int db = 0; db < NBD; ++db) {
+        lam[cc][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        hin[cc][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        if (nb < NBN) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int d = 16 * db + 4 * l4 + r, n = 16 * nb + l15;
+            lam[cc][db][r] = lsrc[d * D + n];
+            if (hsrc != nullptr) hin[cc][db][r] = hsrc[c > 0 ? d * D + n : rr::chunked::state_off<true, D, D>(d, n)];
+          }
         }
       }
     }
@@ -144,15 +154,18 @@ __global__ __launch_bounds__(256) void gla_bwd_kernel(rr::ChunkArgs p) {
       const int i = tid + 256 * v, tl = (i / (D / 4)) & (Q - 1), d0 = 4 * (i % (D / 4));
       if (i < Q * D / 4) {
         const float g4[4] = {gv[v].x, gv[v].y, gv[v].z, gv[v].w};
+        u16x4_t hi4, lo4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           uint16_t hi, lo;
           bf_split(g4[e], hi, lo);
-          m.x.GY_hi[tl][d0 + e] = hi;
-          m.x.GY_lo[tl][d0 + e] = lo;
+          hi4[e] = hi;
+          lo4[e] = lo;
           m.GYT_hi[d0 + e][tl] = hi;
           m.GYT_lo[d0 + e][tl] = lo;
         }
+        *reinterpret_cast<u16x4_t*>(&m.x.GY_hi[tl][d0]) = hi4;
+        *reinterpret_cast<u16x4_t*>(&m.x.GY_lo[tl][d0]) = lo4;
       }
     }
     if (w == 0) {
@@ -165,23 +178,20 @@ __global__ __launch_bounds__(256) void gla_bwd_kernel(rr::ChunkArgs p) {
     }
     float part = 0.f;
 #pragma unroll
-    for (int jj = 0; jj < NBW; ++jj) {
-      const int j = w + 4 * jj;
-      if (j < NB) {
-        const int db = j / NBN, nb = j % NBN;
+    for (int cc = 0; cc < CPW; ++cc) {
+      const int nb = w + 4 * cc;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
-          uint16_t hi, lo;
-          bf_split(lam[jj][r], hi, lo);
-          m.LM_hi[d][n] = hi;
-          m.LM_lo[d][n] = lo;
-          m.x.LMT_hi[n][d] = hi;
-          m.x.LMT_lo[n][d] = lo;
-          bf_split(hin[jj][r], hi, lo);
-          m.x.HT_hi[n][d] = hi;
-          m.x.HT_lo[n][d] = lo;
-          part += lam[jj][r] * hin[jj][r];
+      for (int db = 0; db < NBD; ++db) {
+        rr::bf_split4(lam[cc][db], lam_hi[cc][db], lam_lo[cc][db]);
+        rr::bf_split4(hin[cc][db], hin_hi[cc][db], hin_lo[cc][db]);
+        if (nb < NBN) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int d = 16 * db + 4 * l4 + r, n = 16 * nb + l15;
+            m.LM_hi[d][n] = lam_hi[cc][db][r];
+            m.LM_lo[d][n] = lam_lo[cc][db][r];
+            part += lam[cc][db][r] * hin[cc][db][r];
+          }
         }
       }
     }
@@ -190,60 +200,82 @@ __global__ __launch_bounds__(256) void gla_bwd_kernel(rr::ChunkArgs p) {
     if (lane == 0) m.trw[w] = part;
   }
   __syncthreads();
-  // ------------------------------------------------ B1: CB, G2 (32x32), GH, UL (32 x D)
+  // ------------------------------------------------ B1: GH, UL (registers), CB, G2 (32x32)
+  f32x4_t gh[CPW][2], ul[CPW][2];
+#pragma unroll
+  for (int cc = 0; cc < CPW; ++cc) {
+    const int nb = w + 4 * cc;
+    float xp[2][4] = {}, yp[2][4] = {};
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      gh[cc][tb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      ul[cc][tb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if (nb < NBN) {
+#pragma unroll
+        for (int db = 0; db < NBD; ++db) {
+          const int row = 16 * tb + l15, k0 = 16 * db + 4 * l4;
+          const u16x4_t ah = frag4(&m.x.GY_hi[row][k0]), al = frag4(&m.x.GY_lo[row][k0]);
+          const u16x4_t av = frag4(&m.x.V[row][k0]);
+          gh[cc][tb] = mfma16k16(ah, hin_hi[cc][db], gh[cc][tb]);
+          gh[cc][tb] = mfma16k16(ah, hin_lo[cc][db], gh[cc][tb]);
+          gh[cc][tb] = mfma16k16(al, hin_hi[cc][db], gh[cc][tb]);
+          ul[cc][tb] = mfma16k16(av, lam_hi[cc][db], ul[cc][tb]);
+          ul[cc][tb] = mfma16k16(av, lam_lo[cc][db], ul[cc][tb]);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * tb + 4 * l4 + r, n = 16 * nb + l15;
+          xp[tb][r] = gh[cc][tb][r] * bf_val(m.Qn[t][n]);
+          yp[tb][r] = ul[cc][tb][r] * bf_val(m.Kn[t][n]);
+        }
+      }
+    }
+    // X, Y partials of this wave's columns: sum over the 16 lanes of a row group
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+          xp[tb][r] += __shfl_xor(xp[tb][r], o);
+          yp[tb][r] += __shfl_xor(yp[tb][r], o);
+        }
+        if (l15 == 0) {
+          const int t = 16 * tb + 4 * l4 + r;
+          if (cc == 0) {
+            m.XYp[w][0][t] = xp[tb][r];
+            m.XYp[w][1][t] = yp[tb][r];
+          } else {
+            m.XYp[w][0][t] += xp[tb][r];
+            m.XYp[w][1][t] += yp[tb][r];
+          }
+        }
+      }
+    }
+  }
+  f32x16_t cg = {};   // wave 0: CB = Q K^T; wave 1: G2 = dY V^T
   if (w == 0) {
-    f32x16_t cb = {};
 #pragma unroll
     for (int kb = 0; kb < D / 16; ++kb)
-      cb = mfma32(frag(&m.Qn[lane & 31][16 * kb + 8 * (lane >> 5)]),
-                  frag(&m.Kn[lane & 31][16 * kb + 8 * (lane >> 5)]), cb);
+      cg = mfma32(frag(&m.Qn[lane & 31][16 * kb + 8 * (lane >> 5)]),
+                  frag(&m.Kn[lane & 31][16 * kb + 8 * (lane >> 5)]), cg);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) m.CB[r32row(r, lane)][lane & 31] = cb[r];
+    for (int r = 0; r < 16; ++r) m.CB[r32row(r, lane)][lane & 31] = cg[r];
   } else if (w == 1) {
-    f32x16_t g2 = {};
 #pragma unroll
     for (int kb = 0; kb < D / 16; ++kb) {
       const u16x8_t fb = frag(&m.x.V[lane & 31][16 * kb + 8 * (lane >> 5)]);
-      g2 = mfma32(frag(&m.x.GY_hi[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, g2);
-      g2 = mfma32(frag(&m.x.GY_lo[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, g2);
+      cg = mfma32(frag(&m.x.GY_hi[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, cg);
+      cg = mfma32(frag(&m.x.GY_lo[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, cg);
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) m.G2[r32row(r, lane)][lane & 31] = g2[r];
-  } else {
-    // GH blocks (tb, nb) then UL blocks (sb, nb), 16x16 each, on waves 2 and 3
-    for (int task = w - 2; task < 4 * NBN; task += 2) {
-      const bool isGH = task < 2 * NBN;
-      const int tt = isGH ? task : task - 2 * NBN;
-      const int tb = tt / NBN, nb = tt % NBN;
-      const int row = 16 * tb + (lane & 15), col = 16 * nb + (lane & 15);
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kb = 0; kb < D / 32; ++kb) {
-        const int k0 = 32 * kb + 8 * (lane >> 4);
-        if (isGH) {
-          const u16x8_t ah = frag(&m.x.GY_hi[row][k0]), al = frag(&m.x.GY_lo[row][k0]);
-          const u16x8_t bh = frag(&m.x.HT_hi[col][k0]), bl = frag(&m.x.HT_lo[col][k0]);
-          acc = mfma16(ah, bh, acc);
-          acc = mfma16(ah, bl, acc);
-          acc = mfma16(al, bh, acc);
-        } else {
-          const u16x8_t fa = frag(&m.x.V[row][k0]);
-          acc = mfma16(fa, frag(&m.x.LMT_hi[col][k0]), acc);
-          acc = mfma16(fa, frag(&m.x.LMT_lo[col][k0]), acc);
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = 16 * tb + 4 * (lane >> 4) + r;
-        if (isGH) m.GH[t][col] = acc[r];
-        else m.UL[t][col] = acc[r];
-      }
-    }
+    for (int r = 0; r < 16; ++r) m.G2[r32row(r, lane)][lane & 31] = cg[r];
   }
   __syncthreads();
   // ------------------------------------------------ B2: masked products; dg
   if (w != 2) {
-    // wave 0: P^T; wave 1: MG^T; wave 3: MG
+    // wave 0: P^T (from its CB registers); wave 1: MG^T (from G2 registers);
+    // wave 3: MG (from G2 in LDS)
     float md[16];
     rr::chunked::decay_block32<true>(m.g, 0.f, lane, md);
     const int s = lane & 31;
@@ -252,46 +284,32 @@ __global__ __launch_bounds__(256) void gla_bwd_kernel(rr::ChunkArgs p) {
       const int tp = r32row(r, lane);
       uint16_t hi, lo;
       if (w == 0) {
-        bf_split(md[r] * m.CB[tp][s], hi, lo);
+        bf_split(md[r] * cg[r], hi, lo);
         m.y.PT_hi[s][tp] = hi;
         m.y.PT_lo[s][tp] = lo;
+      } else if (w == 1) {
+        bf_split(md[r] * cg[r], hi, lo);
+        m.y.MGT_hi[s][tp] = hi;
+        m.y.MGT_lo[s][tp] = lo;
       } else {
         bf_split(md[r] * m.G2[tp][s], hi, lo);
-        if (w == 1) {
-          m.y.MGT_hi[s][tp] = hi;
-          m.y.MGT_lo[s][tp] = lo;
-        } else {
-          m.y.MG_hi[tp][s] = hi;
-          m.y.MG_lo[tp][s] = lo;
-        }
+        m.y.MG_hi[tp][s] = hi;
+        m.y.MG_lo[tp][s] = lo;
       }
     }
   } else {
-    {
-      const int t = lane & 31;
-      float acc = 0.f;
-      if (lane < Q) {
-#pragma unroll 8
-        for (int n = 0; n < D; ++n) acc += m.GH[t][n] * bf_val(m.Qn[t][n]);
-      } else {
-#pragma unroll 8
-        for (int n = 0; n < D; ++n) acc += m.UL[t][n] * bf_val(m.Kn[t][n]);
-      }
-      m.XY[lane >> 5][t] = acc;
-    }
-    rr::wave_lds_sync();
     if (lane <= Q) {
       const int row = lane;
       float e[Q], fv[Q];
       float f;
       if (row < Q) {
-        f = m.XY[0][row];
+        f = m.XYp[0][0][row] + m.XYp[1][0][row] + m.XYp[2][0][row] + m.XYp[3][0][row];
 #pragma unroll
         for (int s = 0; s < Q; ++s) e[s] = s < row ? m.CB[row][s] * m.G2[row][s] : 0.f;
       } else {
         f = m.trw[0] + m.trw[1] + m.trw[2] + m.trw[3];
 #pragma unroll
-        for (int s = 0; s < Q; ++s) e[s] = m.XY[1][s];
+        for (int s = 0; s < Q; ++s) e[s] = m.XYp[0][1][s] + m.XYp[1][1][s] + m.XYp[2][1][s] + m.XYp[3][1][s];
       }
 #pragma unroll
       for (int t = 0; t < Q; ++t) {
@@ -312,60 +330,61 @@ __global__ __launch_bounds__(256) void gla_bwd_kernel(rr::ChunkArgs p) {
       float hp = 0.f;
 #pragma unroll
       for (int r = 0; r <= Q; ++r) hp += m.Cc[r][lane];
-      rr::st_bf16(p.ddelta, (row0 + lane) * rowH + h, hp);
+      rr::st_bf16(p.ddelta, base / D + lane * p.H, hp);
     }
   }
   __syncthreads();
   // ------------------------------------------------ C: dv, dk, dq
-  if (w < D / 32) {
-    const int d0 = 32 * w;
-    f32x16_t a1 = {}, a2 = {};
+  // dv row blocks db with (db + NBN) % 4 == w
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const int k0 = 16 * kb + 8 * (lane >> 5);
-      const u16x8_t ph = frag(&m.y.PT_hi[lane & 31][k0]), pl = frag(&m.y.PT_lo[lane & 31][k0]);
-      const u16x8_t gh = frag(&m.GYT_hi[d0 + (lane & 31)][k0]), gl = frag(&m.GYT_lo[d0 + (lane & 31)][k0]);
-      a1 = mfma32(ph, gh, a1);
-      a1 = mfma32(ph, gl, a1);
-      a1 = mfma32(pl, gh, a1);
-    }
+  for (int db = 0; db < NBD; ++db) {
+    if ((db + NBN) % 4 != w) continue;
 #pragma unroll
-    for (int kb = 0; kb < D / 16; ++kb) {
-      const int k0 = 16 * kb + 8 * (lane >> 5);
-      const u16x8_t fa = frag(&m.Kn[lane & 31][k0]);
-      a2 = mfma32(fa, frag(&m.LM_hi[d0 + (lane & 31)][k0]), a2);
-      a2 = mfma32(fa, frag(&m.LM_lo[d0 + (lane & 31)][k0]), a2);
-    }
-    const int d = d0 + (lane & 31);
+    for (int tb = 0; tb < 2; ++tb) {
+      f32x4_t a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
+      {
+        const int k0 = 8 * l4;
+        const u16x8_t ph = frag(&m.y.PT_hi[16 * tb + l15][k0]), pl = frag(&m.y.PT_lo[16 * tb + l15][k0]);
+        const u16x8_t gh8 = frag(&m.GYT_hi[16 * db + l15][k0]), gl8 = frag(&m.GYT_lo[16 * db + l15][k0]);
+        a1 = mfma16(ph, gh8, a1);
+        a1 = mfma16(ph, gl8, a1);
+        a1 = mfma16(pl, gh8, a1);
+      }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int t = r32row(r, lane);
-      rr::st_bf16(p.du, ((row0 + t) * rowH + h) * D + d, a1[r] + m.m31[t] * a2[r]);
-    }
-  } else {
-    // dk (kind 0) and dq (kind 1) blocks over the waves >= D/32
-    const int nw = 4 - D / 32;
-    for (int task = w - D / 32; task < 4 * NBN; task += nw) {
-      const int kind = task / (2 * NBN), tt = task % (2 * NBN);
-      const int tb = tt / NBN, nb = tt % NBN;
-      const int row = 16 * tb + (lane & 15), col = 16 * nb + (lane & 15);
-      const int k0 = 8 * (lane >> 4);
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-      if (kind == 0) {
-        const u16x8_t fb = frag(&m.QT[col][k0]);
-        acc = mfma16(frag(&m.y.MGT_hi[row][k0]), fb, acc);
-        acc = mfma16(frag(&m.y.MGT_lo[row][k0]), fb, acc);
-      } else {
-        const u16x8_t fb = frag(&m.KT[col][k0]);
-        acc = mfma16(frag(&m.y.MG_hi[row][k0]), fb, acc);
-        acc = mfma16(frag(&m.y.MG_lo[row][k0]), fb, acc);
+      for (int kk = 0; kk < D / 32; ++kk) {
+        const int k0 = 32 * kk + 8 * l4;
+        const u16x8_t fa = frag(&m.Kn[16 * tb + l15][k0]);
+        a2 = mfma16(fa, frag(&m.LM_hi[16 * db + l15][k0]), a2);
+        a2 = mfma16(fa, frag(&m.LM_lo[16 * db + l15][k0]), a2);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int t = 16 * tb + 4 * (lane >> 4) + r;
-        const int64_t gi = ((row0 + t) * rowH + h) * D + col;
-        if (kind == 0) rr::st_bf16(p.dB, gi, acc[r] + m.m31[t] * m.UL[t][col]);
-        else rr::st_bf16(p.dC, gi, m.gam[t] * m.GH[t][col] + acc[r]);
+        const int t = 16 * tb + 4 * l4 + r;
+        rr::st_bf16(p.du, base + t * rs + 16 * db + l15, a1[r] + m.m31[t] * a2[r]);
+      }
+    }
+  }
+  // dk, dq of this wave's columns
+#pragma unroll
+  for (int cc = 0; cc < CPW; ++cc) {
+    const int nb = w + 4 * cc;
+    if (nb >= NBN) continue;
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      const int row = 16 * tb + l15, k0 = 8 * l4;
+      f32x4_t ak = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
+      const u16x8_t fq = frag(&m.QT[16 * nb + l15][k0]);
+      ak = mfma16(frag(&m.y.MGT_hi[row][k0]), fq, ak);
+      ak = mfma16(frag(&m.y.MGT_lo[row][k0]), fq, ak);
+      const u16x8_t fk = frag(&m.KT[16 * nb + l15][k0]);
+      aq = mfma16(frag(&m.y.MG_hi[row][k0]), fk, aq);
+      aq = mfma16(frag(&m.y.MG_lo[row][k0]), fk, aq);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * tb + 4 * l4 + r;
+        const int64_t gi = base + t * rs + 16 * nb + l15;
+        rr::st_bf16(p.dB, gi, ak[r] + m.m31[t] * ul[cc][tb][r]);
+        rr::st_bf16(p.dC, gi, m.gam[t] * gh[cc][tb][r] + aq[r]);
       }
     }
   }
