@@ -78,13 +78,29 @@ struct alignas(16) GlaBwdSmem {
 // operands of 16x16x16 MFMAs contracting over j: so each wave forms
 // GH = dY h_in and UL = V lam for its columns in registers and later writes
 // dq and dk of the same columns.  dv row block db goes to wave (db + NBN) % 4.
+template <int D, int MODE>
+union GlaBwdShared {
+  GlaBwdSmem<D> m;
+};
 template <int D>
+union GlaBwdShared<D, rr::chunked::kDirect> {
+  GlaBwdSmem<D> m;
+  rr::chunked::DirectSmem<D, D, true> d;
+};
+
+// lam comes from pass_kernel (kPipe) or from the direct sum (kDirect); in the
+// direct mode the workgroup of chunk 0 also writes the initial-state gradient
+// dh0 = (gam o dY_0)^T Q_0 + gam_31 lam.
+template <int D, int MODE>
 __global__ __launch_bounds__(256, 2) void gla_bwd_kernel(rr::ChunkArgs p) {
   constexpr int NBN = D / 16, NBD = D / 16;
   constexpr int CPW = (NBN + 3) / 4;   // column blocks per wave
-  __shared__ GlaBwdSmem<D> m;
+  __shared__ GlaBwdShared<D, MODE> smu;
+  auto& m = smu.m;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const rr::chunked::ChunkId id = rr::chunked::chunk_id(p, false);
+  if (!id.valid) return;
+  const int c = id.c, h = id.h, b = id.b;
   const int64_t bh = (int64_t)b * p.H + h;
   const int64_t base = (((int64_t)b * p.L + (int64_t)c * Q) * p.H + h) * D;  // element (b, t0, h, 0)
   const int rs = p.H * D;                                                   // step stride (elements)
@@ -92,6 +108,25 @@ __global__ __launch_bounds__(256, 2) void gla_bwd_kernel(rr::ChunkArgs p) {
 
   f32x4_t lam[CPW][NBD], hin[CPW][NBD];
   u16x4_t lam_hi[CPW][NBD], lam_lo[CPW][NBD], hin_hi[CPW][NBD], hin_lo[CPW][NBD];
+  if constexpr (MODE == rr::chunked::kDirect) {
+    const float gam_all = rr::chunked::direct_sum<D, D, true, true>(p, c, b, h, 0.f, smu.d);
+    const float* dfb = p.dfinal != nullptr ? p.dfinal + bh * D * D : nullptr;
+#pragma unroll
+    for (int cc = 0; cc < CPW; ++cc) {
+      const int nb = w + 4 * cc;
+#pragma unroll
+      for (int db = 0; db < NBD; ++db) {
+        lam[cc][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        if (nb < NBN) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            lam[cc][db][r] = rr::chunked::direct_value<D, D, true, true>(smu.d, gam_all, dfb, 16 * db + 4 * l4 + r,
+                                                                         16 * nb + l15);
+        }
+      }
+    }
+    __syncthreads();   // the chunk below reuses the LDS of the sum
+  }
   // ------------------------------------------------ A: stage (all loads first)
   {
     constexpr int UV = (Q * D / 8 + 255) / 256, GV = (Q * D / 4 + 255) / 256;
@@ -114,7 +149,7 @@ __global__ __launch_bounds__(256, 2) void gla_bwd_kernel(rr::ChunkArgs p) {
                             : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     if (tid < Q) xv = bf_val(p.delta[(base / D) + tid * p.H]);
-    const float* lsrc = p.agg + (bh * p.nC + c) * D * D;
+    const float* lsrc = MODE == rr::chunked::kPipe ? p.agg + (bh * p.nC + c) * D * D : nullptr;
     const float* hsrc = c > 0 ? p.ckpt + (bh * p.nC + c - 1) * D * D
                               : (p.h0 != nullptr ? p.h0 + bh * D * D : nullptr);
 #pragma unroll
@@ -122,13 +157,13 @@ __global__ __launch_bounds__(256, 2) void gla_bwd_kernel(rr::ChunkArgs p) {
       const int nb = w + 4 * cc;
 #pragma unroll
       for (int db = 0; db < NBD; ++db) {
-        lam[cc][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        if constexpr (MODE == rr::chunked::kPipe) lam[cc][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         hin[cc][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         if (nb < NBN) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int d = 16 * db + 4 * l4 + r, n = 16 * nb + l15;
-            lam[cc][db][r] = lsrc[d * D + n];
+            if constexpr (MODE == rr::chunked::kPipe) lam[cc][db][r] = lsrc[d * D + n];
             if (hsrc != nullptr) hin[cc][db][r] = hsrc[c > 0 ? d * D + n : rr::chunked::state_off<true, D, D>(d, n)];
           }
         }
@@ -388,6 +423,40 @@ __global__ __launch_bounds__(256, 2) void gla_bwd_kernel(rr::ChunkArgs p) {
       }
     }
   }
+  if constexpr (MODE == rr::chunked::kDirect) {
+    if (c == 0 && p.dh0 != nullptr) {
+      // dh0 = (gam o dY_0)^T Q_0 + gam_31 lam, blocks of this wave's columns
+      const float g31 = m.gam[Q - 1];
+#pragma unroll
+      for (int cc = 0; cc < CPW; ++cc) {
+        const int nb = w + 4 * cc;
+        if (nb >= NBN) continue;
+        const int k0 = 8 * l4;
+        const u16x8_t qf = frag(&m.QT[16 * nb + l15][k0]);
+        u16x8_t qh, ql;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          uint16_t hi, lo;
+          bf_split(m.gam[k0 + e] * bf_val(qf[e]), hi, lo);
+          qh[e] = hi;
+          ql[e] = lo;
+        }
+#pragma unroll
+        for (int db = 0; db < NBD; ++db) {
+          const u16x8_t ah = frag(&m.GYT_hi[16 * db + l15][k0]), al = frag(&m.GYT_lo[16 * db + l15][k0]);
+          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+          acc = mfma16(ah, qh, acc);
+          acc = mfma16(ah, ql, acc);
+          acc = mfma16(al, qh, acc);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int d = 16 * db + 4 * l4 + r, n = 16 * nb + l15;
+            p.dh0[bh * D * D + rr::chunked::state_off<true, D, D>(d, n)] = acc[r] + g31 * lam[cc][db][r];
+          }
+        }
+      }
+    }
+  }
 }
 
 template <int D>
@@ -397,12 +466,20 @@ int launch_gla_fwd(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
 
 template <int D>
 int launch_gla_bwd(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
-  hipLaunchKernelGGL((rr::chunked::agg_kernel<D, D, true>), dim3(p.nC, p.H, (unsigned)B), dim3(64), 0, s, p, 1);
+  if (p.mode == rr::chunked::kDirect) {
+    if constexpr (D * D <= rr::chunked::kDirectMaxState) {
+      hipLaunchKernelGGL((gla_bwd_kernel<D, rr::chunked::kDirect>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
+      return rr::check_launch("gla chunked backward");
+    } else {
+      return rr::fail(RR_EUNSUPPORTED, "gla chunked backward: state too large for the direct mode");
+    }
+  }
+  hipLaunchKernelGGL((rr::chunked::agg_kernel<D, D, true>), rr::chunked::chunk_grid(p), dim3(64), 0, s, p, 1);
   if (int rc = rr::check_launch("gla chunked backward aggregates")) return rc;
   hipLaunchKernelGGL((rr::chunked::pass_kernel<D, D, true>), dim3(D * D / 256, p.H, (unsigned)B), dim3(256), 0, s,
                      p, 1);
   if (int rc = rr::check_launch("gla chunked backward adjoint pass")) return rc;
-  hipLaunchKernelGGL((gla_bwd_kernel<D>), dim3(p.nC, p.H, (unsigned)B), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((gla_bwd_kernel<D, rr::chunked::kPipe>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
   return rr::check_launch("gla chunked backward");
 }
 
@@ -412,13 +489,20 @@ int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }
 
 namespace rr {
 
-bool gla2_supported(int dtype, int64_t L, int64_t seg, int64_t Dh, int pass) {
+bool gla2_supported(int dtype, int64_t B, int64_t L, int64_t H, int64_t seg, int64_t Dh, int pass) {
   if (dtype != RR_BF16 || chunk_len(L, seg) != chunked::Q) return false;
+  if ((L / chunked::Q) * ((B * H + chunked::kXcds - 1) / chunked::kXcds * chunked::kXcds) >= ((int64_t)1 << 31))
+    return false;
   if (pass == 0) return Dh == 32 || Dh == 64 || Dh == 128;
   return Dh == 32 || Dh == 64;
 }
 
+int gla2_mode(int64_t nC, int64_t Dh) {
+  return nC <= chunked::kDirectMaxChunks && Dh * Dh <= chunked::kDirectMaxState ? chunked::kDirect : chunked::kPipe;
+}
+
 size_t gla2_ws_bytes(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass) {
+  if (gla2_mode(nC, Dh) == chunked::kDirect) return 0;
   int64_t f = align64(B * H * nC);
   if (pass == 1) f += align64(B * H * nC * Dh * Dh);
   return (size_t)f * sizeof(float);
@@ -426,7 +510,8 @@ size_t gla2_ws_bytes(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass) {
 
 void gla2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass) {
   float* f = static_cast<float*>(ws);
-  a.ws = nullptr;
+  a.ws = a.tot = a.agg = nullptr;
+  if (a.mode == chunked::kDirect) return;
   a.tot = f;
   f += align64(B * a.H * a.nC);
   a.agg = pass == 1 ? f : nullptr;

@@ -137,6 +137,27 @@ __device__ __forceinline__ int state_off(int d, int n) {
   else return d * NS + n;
 }
 
+// Per-chunk kernels run on a 1-D grid of chunk_grid(p) workgroups.  The GPU
+// hands workgroups to its 8 XCDs round-robin by linear index; the decode
+// gives every chunk of a head the same XCD, so whatever the head's
+// workgroups share (inputs, checkpoints, adjoints) is cached in one L2.
+// `reverse` numbers the chunks from the end (the costliest workgroups of the
+// direct forward, the late chunks, are then dispatched first).
+constexpr int kXcds = 8;
+struct ChunkId {
+  int c, h, b;
+  bool valid;   // false for the padding workgroups of the last head group
+};
+__device__ __forceinline__ ChunkId chunk_id(const ChunkArgs& p, bool reverse) {
+  const int id = blockIdx.x, x = id % kXcds, slot = id / kXcds;
+  const int bh = (slot / p.nC) * kXcds + x;
+  const int cs = slot % p.nC;
+  return ChunkId{reverse ? p.nC - 1 - cs : cs, bh % p.H, bh / p.H, bh < p.B * p.H};
+}
+inline dim3 chunk_grid(const ChunkArgs& p) {
+  return dim3((unsigned)(p.nC * ((p.B * p.H + kXcds - 1) / kXcds) * kXcds));
+}
+
 // Per-head decay rate (SSD); GLA has none.
 template <bool GLA>
 __device__ __forceinline__ float head_rate(const ChunkArgs& p, int h) {
@@ -165,7 +186,9 @@ __global__ __launch_bounds__(64) void agg_kernel(ChunkArgs p, int kind) {
   __shared__ uint16_t XT_hi[DH][PQ], XT_lo[DH][PQ];   // kind 0: U^T [d][s] (hi only); kind 1: (gam o dY)^T
   __shared__ uint16_t YT_hi[NS][PQ], YT_lo[NS][PQ];   // kind 0: (m31 o w o B)^T split; kind 1: C^T (hi only)
   const int lane = threadIdx.x;
-  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const ChunkId id = chunk_id(p, false);
+  if (!id.valid) return;
+  const int c = id.c, h = id.h, b = id.b;
   const float a = head_rate<GLA>(p, h);
   const int64_t rowH = p.H, row0 = (int64_t)b * p.L + (int64_t)c * Q;
   constexpr int UV = Q * DH / 8 / 64, GV = Q * DH / 4 / 64, BV = (Q * NS / 8 + 63) / 64;
@@ -305,6 +328,187 @@ __global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
   }
 }
 
+// ------------------------------------------------------------------ direct mode
+// Short sequences (nC <= kDirectMaxChunks): one workgroup per chunk forms the
+// state entering its chunk (forward) or the adjoint leaving it (backward)
+// itself, as a weighted sum over the inputs of all earlier (later) chunks, so
+// a pass is a single kernel with no aggregate or state-pass kernels:
+//   forward:  h_in(c) = Gam h0 + sum_{j<c} F_j U_j^T diag(m31 o w) B_j,
+//             F_j = tot_{j+1} ... tot_{c-1},   Gam = tot_0 ... tot_{c-1};
+//   backward: lam(c) = Gam dfinal + sum_{j>c} F_j (gam o dY_j)^T C_j,
+//             F_j = tot_{c+1} ... tot_{j-1},   Gam = tot_{c+1} ... tot_{nC-1}
+// (m31, w, gam and tot of chunk j as in step_scalars).  Wave w takes chunks
+// w, w + 4, ... of the range and accumulates every 16x16 block of the state;
+// the four partial sums are added in a fixed order (deterministic).
+enum Mode { kWhole = 0, kPipe = 1, kDirect = 2 };
+// The sum costs each workgroup up to nC - 1 chunks of extra reads; measured on
+// MI355X (B3 H12 Dh64), it beats the two extra launches of the pipelined mode
+// at 2 and 4 chunks and loses from 8 chunks on.
+constexpr int kDirectMaxChunks = 4;
+constexpr int kDirectMaxState = 64 * 64;   // Dh * N (the partial sums live in LDS)
+constexpr int kDirectPerWave = kDirectMaxChunks / 4;
+
+template <int DH, int NS, bool BWD>
+struct DirectSmem {
+  union {
+    struct {                                // one wave's staging area
+      uint16_t XT[BWD ? 2 : 1][DH][PQ];     // fwd: U^T; bwd: (coef o dY)^T hi, lo
+      uint16_t YT[BWD ? 1 : 2][NS][PQ];     // fwd: (coef o B)^T hi, lo; bwd: C^T
+    } st[4];
+    float red[4][DH * NS];                  // per-wave partial sums, [d][n]
+  };
+  float tot[kDirectMaxChunks];
+};
+
+// Runs the weighted sum; afterwards red[] holds the four partial sums and the
+// return value is Gam.  Every thread of the (256-thread) workgroup must call it.
+template <int DH, int NS, bool GLA, bool BWD>
+__device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, DirectSmem<DH, NS, BWD>& s) {
+  constexpr int NBN = NS / 16, NB = (DH / 16) * NBN;
+  constexpr int XV = BWD ? Q * DH / 4 / 64 : Q * DH / 8 / 64;  // float4 (dY) or u16x8 (U) per lane
+  constexpr int YV = (Q * NS / 8 + 63) / 64;                   // u16x8 of B (fwd) or C (bwd) per lane
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int l15 = lane & 15, l4 = lane >> 4;
+  const int64_t rowH = p.H;
+  const int j0 = BWD ? c + 1 : 0, j1 = BWD ? p.nC : c;   // chunks [j0, j1)
+  const float neutral = GLA ? 1.f : 0.f;
+
+  // 1. decays of the chunks in the range; per-step coefficients of this wave's
+  float coef[kDirectPerWave];
+#pragma unroll
+  for (int jj = 0; jj < kDirectPerWave; ++jj) {
+    const int j = j0 + w + 4 * jj;
+    coef[jj] = 0.f;
+    if (j < j1) {
+      const int64_t row0 = (int64_t)b * p.L + (int64_t)j * Q;
+      const float xv = lane < Q ? bf_val(p.delta[(row0 + lane) * rowH + h]) : neutral;
+      const StepScalars sc = step_scalars<GLA>(xv, a, lane);
+      coef[jj] = BWD ? sc.gam : sc.m31 * sc.w;
+      if (lane == 0) s.tot[j - j0] = sc.tot;
+    }
+  }
+  __syncthreads();
+  float gam_all = 1.f;
+  for (int k = j0; k < j1; ++k) gam_all *= s.tot[k - j0];
+#pragma unroll
+  for (int jj = 0; jj < kDirectPerWave; ++jj) {
+    const int j = j0 + w + 4 * jj;
+    if (j < j1) {
+      float f = 1.f;
+      const int kb = BWD ? j0 : j + 1, ke = BWD ? j : j1;
+      for (int k = kb; k < ke; ++k) f *= s.tot[k - j0];
+      coef[jj] *= f;
+    }
+  }
+
+  // 2. this wave's partial sum over its chunks (inputs of chunk jj + 1 are
+  //    loaded while chunk jj is staged and multiplied)
+  f32x4_t part[NB];
+#pragma unroll
+  for (int q = 0; q < NB; ++q) part[q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto& st = s.st[w];
+  const uint16_t* ysrc = BWD ? p.Cm : p.Bm;
+  u16x8_t xu[2][BWD ? 1 : XV], yv[2][YV];
+  float4 xf[2][BWD ? XV : 1];
+  auto load = [&](int buf, int j) {
+    const int64_t row0 = (int64_t)b * p.L + (int64_t)j * Q;
+#pragma unroll
+    for (int v = 0; v < XV; ++v) {
+      if constexpr (BWD) {
+        const int i = lane + 64 * v, tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
+        xf[buf][v] = *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0);
+      } else {
+        const int i = lane + 64 * v, tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
+        xu[buf][v] = *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0);
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < YV; ++v) {
+      const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+      yv[buf][v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(ysrc + ((row0 + tl) * rowH + h) * NS + n0)
+                                  : u16x8_t{};
+    }
+  };
+  if (j0 + w < j1) load(0, j0 + w);
+#pragma unroll
+  for (int jj = 0; jj < kDirectPerWave; ++jj) {
+    const int j = j0 + w + 4 * jj;
+    if (j >= j1) break;
+    const int cur = jj & 1;
+    if (j + 4 < j1) load(cur ^ 1, j + 4);
+    const float cf = coef[jj];
+#pragma unroll
+    for (int v = 0; v < XV; ++v) {
+      if constexpr (BWD) {
+        const int i = lane + 64 * v, tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
+        const float ct = __shfl(cf, tl);
+        const float g4[4] = {xf[cur][v].x, xf[cur][v].y, xf[cur][v].z, xf[cur][v].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          uint16_t hi, lo;
+          bf_split(ct * g4[e], hi, lo);
+          st.XT[0][d0 + e][tl] = hi;
+          st.XT[BWD ? 1 : 0][d0 + e][tl] = lo;
+        }
+      } else {
+        const int i = lane + 64 * v, tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) st.XT[0][d0 + e][tl] = xu[cur][v][e];
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < YV; ++v) {
+      const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+      const float ct = __shfl(cf, tl);
+      if (i < Q * NS / 8) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if constexpr (BWD) {
+            st.YT[0][n0 + e][tl] = yv[cur][v][e];
+          } else {
+            uint16_t hi, lo;
+            bf_split(ct * bf_val(yv[cur][v][e]), hi, lo);
+            st.YT[0][n0 + e][tl] = hi;
+            st.YT[BWD ? 0 : 1][n0 + e][tl] = lo;
+          }
+        }
+      }
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      const int db = q / NBN, nb = q % NBN;
+      const u16x8_t fa = frag(&st.XT[0][16 * db + l15][8 * l4]);
+      const u16x8_t fb = frag(&st.YT[0][16 * nb + l15][8 * l4]);
+      part[q] = mfma16(fa, fb, part[q]);
+      if constexpr (BWD) part[q] = mfma16(frag(&st.XT[BWD ? 1 : 0][16 * db + l15][8 * l4]), fb, part[q]);
+      else part[q] = mfma16(fa, frag(&st.YT[BWD ? 0 : 1][16 * nb + l15][8 * l4]), part[q]);
+    }
+    wave_lds_sync();
+  }
+  // 3. partial sums to LDS (the staging areas are dead once every wave is here)
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < NB; ++q) {
+    const int db = q / NBN, nb = q % NBN;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s.red[w][(16 * db + 4 * l4 + r) * NS + 16 * nb + l15] = part[q][r];
+  }
+  __syncthreads();
+  return gam_all;
+}
+
+// Element (d, n) of the direct sum: the four partials plus Gam times the
+// caller's h0 (forward) or dfinal (backward), read from red[] / `ext`.
+template <int DH, int NS, bool GLA, bool BWD>
+__device__ __forceinline__ float direct_value(const DirectSmem<DH, NS, BWD>& s, float gam_all, const float* ext,
+                                              int d, int n) {
+  const int e = d * NS + n;
+  float v = ((s.red[0][e] + s.red[1][e]) + s.red[2][e]) + s.red[3][e];
+  if (ext != nullptr) v += gam_all * ext[state_off<GLA, DH, NS>(d, n)];
+  return v;
+}
+
 // ------------------------------------------------------------------ forward
 template <int DH, int NS>
 struct FwdSmem {
@@ -322,16 +526,33 @@ struct FwdSmem {
   float gam[Q], wend[Q];
 };
 
-// PIPE: one chunk per workgroup, entering state from checkpoint slot c - 1
-// (written by pass_kernel); otherwise a run of R chunks per workgroup (R = all
-// chunks of the head: the state is carried in registers).
-template <int DH, int NS, bool PIPE, bool GLA>
+template <int DH, int NS, bool DIRECT>
+union FwdShared {
+  FwdSmem<DH, NS> f;
+};
+template <int DH, int NS>
+union FwdShared<DH, NS, true> {
+  FwdSmem<DH, NS> f;
+  DirectSmem<DH, NS, false> d;
+};
+
+// One chunk per workgroup with the entering state from checkpoint slot c - 1
+// (kPipe, written by pass_kernel) or from the direct sum (kDirect); or a run of
+// R = nC chunks per workgroup carrying the state in registers (kWhole).
+template <int DH, int NS, int MODE, bool GLA>
 __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
   using K = Cfg<DH, NS>;
-  __shared__ FwdSmem<DH, NS> sm;
+  __shared__ FwdShared<DH, NS, MODE == kDirect> smu;
+  auto& sm = smu.f;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int cbeg = blockIdx.x * p.R;
+  int h, b, cbeg;
+  if constexpr (MODE == kWhole) {
+    h = blockIdx.y, b = blockIdx.z, cbeg = 0;
+  } else {
+    const ChunkId id = chunk_id(p, MODE == kDirect);
+    if (!id.valid) return;
+    h = id.h, b = id.b, cbeg = id.c;
+  }
   const int cend = min(cbeg + p.R, p.nC);
   const float a = head_rate<GLA>(p, h);
   const int64_t rowH = p.H;
@@ -339,10 +560,26 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
   f32x4_t hst[K::NBW];
 #pragma unroll
   for (int jj = 0; jj < K::NBW; ++jj) hst[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if constexpr (MODE == kDirect) {
+    const float gam_all = direct_sum<DH, NS, GLA, false>(p, cbeg, b, h, a, smu.d);
+    const float* h0b = p.h0 != nullptr ? p.h0 + ((int64_t)b * p.H + h) * DH * NS : nullptr;
+#pragma unroll
+    for (int jj = 0; jj < K::NBW; ++jj) {
+      const int j = w + 4 * jj;
+      if (j < K::NB) {
+        const int db = j / K::NBN, nb = j % K::NBN;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          hst[jj][r] = direct_value<DH, NS, GLA, false>(smu.d, gam_all, h0b, 16 * db + 4 * (lane >> 4) + r,
+                                                        16 * nb + (lane & 15));
+      }
+    }
+    __syncthreads();   // the chunk below reuses the LDS of the sum
+  }
   const bool from_h0 = cbeg == 0;
   const float* hsrc = !from_h0 ? p.ckpt + (((int64_t)b * p.H + h) * p.nC + cbeg - 1) * DH * NS
                                : (p.h0 != nullptr ? p.h0 + ((int64_t)b * p.H + h) * DH * NS : nullptr);
-  if (hsrc != nullptr) {
+  if (MODE != kDirect && hsrc != nullptr) {
 #pragma unroll
     for (int jj = 0; jj < K::NBW; ++jj) {
       const int j = w + 4 * jj;
@@ -403,7 +640,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
       if (lane < Q) {
         sm.cd[lane] = sc.cd;
         sm.gam[lane] = sc.gam;
-        if constexpr (!PIPE) sm.wend[lane] = sc.m31 * sc.w;
+        if constexpr (MODE != kPipe) sm.wend[lane] = sc.m31 * sc.w;
       }
     }
 #pragma unroll
@@ -441,7 +678,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
         sm.W_hi[t][s] = hi;
         sm.W_lo[t][s] = lo;
       }
-    } else if constexpr (!PIPE) {
+    } else if constexpr (MODE != kPipe) {
       for (int i = tid - 64; i < Q * NS; i += 192) {
         const int n = i / Q, s = i % Q;
         uint16_t hi, lo;
@@ -475,7 +712,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
       }
     }
     // ---- h_end = gam_31 h_in + U^T (m31 o w o B): every wave, its blocks; checkpoint
-    if constexpr (PIPE) break;
+    if constexpr (MODE == kPipe) break;
     const float Gam = sm.gam[Q - 1];
 #pragma unroll
     for (int jj = 0; jj < K::NBW; ++jj) {
@@ -500,14 +737,19 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
 
 template <int DH, int NS, bool GLA>
 int launch_fwd(const ChunkArgs& p, int64_t B, hipStream_t s) {
-  if (p.R < p.nC) {   // pipelined, R == 1
-    hipLaunchKernelGGL((agg_kernel<DH, NS, GLA>), dim3(p.nC, p.H, (unsigned)B), dim3(64), 0, s, p, 0);
+  if (p.mode == kPipe) {   // R == 1
+    hipLaunchKernelGGL((agg_kernel<DH, NS, GLA>), chunk_grid(p), dim3(64), 0, s, p, 0);
     if (int rc = check_launch("chunked forward aggregates")) return rc;
     hipLaunchKernelGGL((pass_kernel<DH, NS, GLA>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0, s, p, 0);
     if (int rc = check_launch("chunked forward state pass")) return rc;
-    hipLaunchKernelGGL((fwd_kernel<DH, NS, true, GLA>), dim3(p.nC, p.H, (unsigned)B), dim3(256), 0, s, p);
-  } else {
-    hipLaunchKernelGGL((fwd_kernel<DH, NS, false, GLA>), dim3(1, p.H, (unsigned)B), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((fwd_kernel<DH, NS, kPipe, GLA>), chunk_grid(p), dim3(256), 0, s, p);
+  } else if (p.mode == kDirect) {   // R == 1
+    if constexpr (DH * NS <= kDirectMaxState)
+      hipLaunchKernelGGL((fwd_kernel<DH, NS, kDirect, GLA>), chunk_grid(p), dim3(256), 0, s, p);
+    else
+      return fail(RR_EUNSUPPORTED, "chunked forward: state too large for the direct mode");
+  } else {   // R == nC
+    hipLaunchKernelGGL((fwd_kernel<DH, NS, kWhole, GLA>), dim3(1, p.H, (unsigned)B), dim3(256), 0, s, p);
   }
   return check_launch("chunked forward");
 }

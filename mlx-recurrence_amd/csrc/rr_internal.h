@@ -32,35 +32,42 @@ struct ChunkArgs {
   float* ws;               // SSD backward: dA partials [B,H,nR,N]
   float* tot;              // pipelined: per-chunk decay gam_31 [B,H,nC]
   float* agg;              // pipelined backward: chunk aggregates, then adjoints [B,H,nC,Dh,N]
-  int L, H, DH, NS, nC, R;
+  int B, L, H, DH, NS, nC;
+  int R;                   // chunks per workgroup: nC (whole-head mode) or 1
+  int mode;                // 0 whole head, 1 pipelined, 2 direct (rr_chunked.h)
 };
+
+// Mode of the chunked kernels for B*H heads of nC chunks of a Dh x N state: a
+// whole head per workgroup when the heads alone fill the GPU; else one
+// workgroup per chunk, with the entering states formed directly (nC <= 4,
+// Dh * N <= 64 * 64) or by the pipelined aggregate and state-pass kernels.
+int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N);
 
 // ------------------------------------------------------------------ SSD
 // True when the chunked kernels cover this call: bf16 inputs, a head-uniform A
 // (A_stride_n == 0), checkpoint interval 32, Dh in {32, 64, 128} and
 // N in {16, 32, 64, 128}.
 bool ssd2_supported(int dtype, int64_t L, int64_t seg, int64_t Dh, int64_t N, int64_t A_stride_n);
-// Chunks per workgroup: 1 (pipelined: aggregate, pass and main kernels) or
-// nC (one workgroup walks a whole head).
-int ssd2_pick_run(int64_t B, int64_t H, int64_t nC, int64_t N);
 int ssd2_fwd(const ChunkArgs& p, int64_t B, hipStream_t s);
 // The chunked backward covers Dh in {32, 64} and N in {16, 32} (on top of
 // ssd2_supported).
 bool ssd2_bwd_supported(int64_t Dh, int64_t N);
-// Workspace of the chunked passes: chunk aggregates + chunk decays when runs
-// are shorter than a head (pass 0 and 1), plus dA partials (pass 1).
-size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int R, int64_t Dh, int64_t N, int pass);
+// Workspace of the chunked passes: chunk decays and (backward) chunk adjoints
+// in the pipelined mode, plus dA partials (pass 1).
+size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int mode, int64_t Dh, int64_t N, int pass);
 void ssd2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass);
 int ssd2_bwd(const ChunkArgs& p, int64_t B, hipStream_t s);
 
 // ------------------------------------------------------------------ GLA
 // True when the chunked GLA kernels cover this call (pass 0 forward, 1
 // backward): bf16 inputs, checkpoint interval 32, Dh in {32, 64, 128}
-// (forward) or {32, 64} (backward).  Always pipelined (one chunk per
-// workgroup).
-bool gla2_supported(int dtype, int64_t L, int64_t seg, int64_t Dh, int pass);
-// Workspace: chunk decays [B,H,nC] (both passes) and the backward chunk
-// adjoints [B,H,nC,Dh,Dh] (pass 1).
+// (forward) or {32, 64} (backward), and a 1-D grid of one workgroup per
+// chunk below 2^31 (direct or pipelined mode; the whole-head mode is not
+// used for GLA).
+bool gla2_supported(int dtype, int64_t B, int64_t L, int64_t H, int64_t seg, int64_t Dh, int pass);
+int gla2_mode(int64_t nC, int64_t Dh);
+// Workspace of the pipelined mode: chunk decays [B,H,nC] (both passes) and
+// the backward chunk adjoints [B,H,nC,Dh,Dh] (pass 1); none in direct mode.
 size_t gla2_ws_bytes(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass);
 void gla2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass);
 int gla2_fwd(const ChunkArgs& p, int64_t B, hipStream_t s);

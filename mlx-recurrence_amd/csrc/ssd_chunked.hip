@@ -31,6 +31,9 @@ using rr::chunked::prefix32;
 using rr::chunked::PQ;
 using rr::chunked::Q;
 using rr::chunked::r32row;
+using rr::chunked::kDirect;
+using rr::chunked::kPipe;
+using rr::chunked::kWhole;
 
 }  // namespace
 
@@ -42,14 +45,6 @@ bool ssd2_supported(int dtype, int64_t L, int64_t seg, int64_t Dh, int64_t N, in
   if (!(Dh == 32 || Dh == 64 || Dh == 128)) return false;
   if (!(N == 16 || N == 32 || N == 64 || N == 128)) return false;
   return true;
-}
-
-int ssd2_pick_run(int64_t B, int64_t H, int64_t nC, int64_t N) {
-  // Pipelined (one workgroup per chunk) when the heads alone cannot fill the
-  // GPU, else a whole head per workgroup.  Only 1 and nC are valid.
-  (void)N;
-  if (B * H >= 512) return (int)nC;
-  return 1;
 }
 
 int ssd2_fwd(const ChunkArgs& p, int64_t B, hipStream_t s) {
@@ -98,7 +93,7 @@ namespace {
 // LDS of the backward kernel.  Arrays live in phase order, so the operands
 // that die after phase B1 (x) share space with the masked products written in
 // B2 (y), and the B1/B2 fp32 products (p) with the phase-C results (q).
-template <int DH, int NS, bool PIPE>
+template <int DH, int NS, bool CARRY>
 struct BwdSmem {
   static constexpr int PD = DH + 8, PN = NS + 8;
   uint16_t Bn[Q][PN];
@@ -134,23 +129,43 @@ struct BwdSmem {
       float KB[Q][NS + 1];
     } q;
   };
-  // (gam o C)^T, for the adjoint carried across chunks (whole-head mode only)
-  uint16_t CgT_hi[PIPE ? 1 : NS][PQ], CgT_lo[PIPE ? 1 : NS][PQ];
+  // (gam o C)^T, for the adjoint carried to the previous chunk (whole-head
+  // mode; chunk 0 of the direct mode for the initial-state gradient)
+  uint16_t CgT_hi[CARRY ? NS : 1][PQ], CgT_lo[CARRY ? NS : 1][PQ];
   float del[Q], cd[Q], gam[Q], m31[Q], R[Q];
   float kGH[Q], kUL[Q], kZ[Q];
   float t4[4][NS];
   float dAp[4][4][NS];
 };
 
-// PIPE: one chunk per workgroup, lam from the workspace (pass_kernel);
-// otherwise a whole head per workgroup, lam carried backwards in registers.
-template <int DH, int NS, bool PIPE>
+template <int DH, int NS, int MODE>
+union BwdShared {
+  BwdSmem<DH, NS, MODE != kPipe> m;
+};
+template <int DH, int NS>
+union BwdShared<DH, NS, kDirect> {
+  BwdSmem<DH, NS, true> m;
+  rr::chunked::DirectSmem<DH, NS, true> d;
+};
+
+// One chunk per workgroup with lam from the workspace (kPipe, pass_kernel) or
+// from the direct sum (kDirect); or a whole head per workgroup, lam carried
+// backwards in registers (kWhole).
+template <int DH, int NS, int MODE>
 __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
   using K = Cfg<DH, NS>;
-  __shared__ BwdSmem<DH, NS, PIPE> m;
+  constexpr bool PIPE = MODE == kPipe;
+  __shared__ BwdShared<DH, NS, MODE> smu;
+  auto& m = smu.m;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int cbeg = blockIdx.x * p.R;
+  int h, b, cbeg;
+  if constexpr (MODE == kWhole) {
+    h = blockIdx.y, b = blockIdx.z, cbeg = 0;
+  } else {
+    const rr::chunked::ChunkId id = rr::chunked::chunk_id(p, false);
+    if (!id.valid) return;
+    h = id.h, b = id.b, cbeg = id.c;
+  }
   const int cend = min(cbeg + p.R, p.nC);
   const float a = p.A[(int64_t)h * p.A_stride_h];
   const int64_t rowH = p.H;
@@ -160,9 +175,28 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
   f32x4_t lam[K::NBW];
 #pragma unroll
   for (int jj = 0; jj < K::NBW; ++jj) lam[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if constexpr (MODE == kDirect) {
+    const float gam_all = rr::chunked::direct_sum<DH, NS, false, true>(p, cbeg, b, h, a, smu.d);
+    const float* dfb = p.dfinal != nullptr ? p.dfinal + sbase : nullptr;
+#pragma unroll
+    for (int jj = 0; jj < K::NBW; ++jj) {
+      const int j = w + 4 * jj;
+      if (j < K::NB) {
+        const int db = j / NBN, nb = j % NBN;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          lam[jj][r] = rr::chunked::direct_value<DH, NS, false, true>(smu.d, gam_all, dfb,
+                                                                      16 * db + 4 * (lane >> 4) + r, 16 * nb + (lane & 15));
+      }
+    }
+    __syncthreads();   // the chunk below reuses the LDS of the sum
+  }
+  // the adjoint entering chunk c - 1 is needed for the whole head, and for
+  // the initial-state gradient at chunk 0
+  const bool carry = MODE == kWhole || (MODE == kDirect && cbeg == 0 && p.dh0 != nullptr);
   const float* lsrc = PIPE ? p.agg + (((int64_t)b * p.H + h) * p.nC + cbeg) * DH * NS
                            : (p.dfinal != nullptr ? p.dfinal + sbase : nullptr);
-  if (lsrc != nullptr) {
+  if (MODE != kDirect && lsrc != nullptr) {
 #pragma unroll
     for (int jj = 0; jj < K::NBW; ++jj) {
       const int j = w + 4 * jj;
@@ -337,13 +371,15 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
           else m.UL[t][col] = acc[r];
         }
       }
-      if constexpr (!PIPE) {
-        for (int i = tid - 128; i < NS * Q; i += 128) {
-          const int n = i / Q, t = i % Q;
-          uint16_t hi, lo;
-          bf_split(m.gam[t] * bf_val(m.Cn[t][n]), hi, lo);
-          m.CgT_hi[n][t] = hi;
-          m.CgT_lo[n][t] = lo;
+      if constexpr (MODE != kPipe) {
+        if (carry) {
+          for (int i = tid - 128; i < NS * Q; i += 128) {
+            const int n = i / Q, t = i % Q;
+            uint16_t hi, lo;
+            bf_split(m.gam[t] * bf_val(m.Cn[t][n]), hi, lo);
+            m.CgT_hi[n][t] = hi;
+            m.CgT_lo[n][t] = lo;
+          }
         }
       }
     }
@@ -495,7 +531,7 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
           float part = 0.f;
 #pragma unroll
           for (int r = 0; r < 4; ++r) part += lam[jj][r] * hin[jj][r];
-          if constexpr (!PIPE) {
+          if constexpr (MODE != kPipe) if (carry) {
             f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
             const int k0 = 8 * (lane >> 4);
             const u16x8_t ah = frag(&m.GYT_hi[16 * db + (lane & 15)][k0]);
@@ -567,9 +603,10 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
     }
   }
   // per-run dA partial and the initial-state gradient
-  const int nR = gridDim.x;
-  if (w == 1 && lane < NS) p.ws[(((int64_t)b * p.H + h) * nR + blockIdx.x) * NS + lane] = dA_acc;
-  if (!PIPE && p.dh0 != nullptr) {
+  const int nR = MODE == kWhole ? 1 : p.nC;   // runs per head
+  const int run = MODE == kWhole ? 0 : cbeg;
+  if (w == 1 && lane < NS) p.ws[(((int64_t)b * p.H + h) * nR + run) * NS + lane] = dA_acc;
+  if (carry && p.dh0 != nullptr) {
 #pragma unroll
     for (int jj = 0; jj < K::NBW; ++jj) {
       const int j = w + 4 * jj;
@@ -610,15 +647,20 @@ __global__ __launch_bounds__(256) void ssd2_dA_kernel(const float* __restrict__ 
 template <int DH, int NS>
 int launch_bwd(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
   const int nR = (p.nC + p.R - 1) / p.R;
-  if (nR > 1) {   // pipelined, R == 1
-    hipLaunchKernelGGL((rr::chunked::agg_kernel<DH, NS, false>), dim3(p.nC, p.H, (unsigned)B), dim3(64), 0, s, p, 1);
+  if (p.mode == kPipe) {   // R == 1
+    hipLaunchKernelGGL((rr::chunked::agg_kernel<DH, NS, false>), rr::chunked::chunk_grid(p), dim3(64), 0, s, p, 1);
     if (int rc = rr::check_launch("ssd chunked backward aggregates")) return rc;
     hipLaunchKernelGGL((rr::chunked::pass_kernel<DH, NS, false>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0, s,
                        p, 1);
     if (int rc = rr::check_launch("ssd chunked backward adjoint pass")) return rc;
-    hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, true>), dim3(nR, p.H, (unsigned)B), dim3(256), 0, s, p);
-  } else {
-    hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, false>), dim3(1, p.H, (unsigned)B), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, kPipe>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
+  } else if (p.mode == kDirect) {   // R == 1
+    if constexpr (DH * NS <= rr::chunked::kDirectMaxState)
+      hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, kDirect>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
+    else
+      return rr::fail(RR_EUNSUPPORTED, "ssd chunked backward: state too large for the direct mode");
+  } else {   // R == nC
+    hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, kWhole>), dim3(1, p.H, (unsigned)B), dim3(256), 0, s, p);
   }
   if (int rc = rr::check_launch("ssd chunked backward")) return rc;
   hipLaunchKernelGGL(ssd2_dA_kernel, dim3(p.H), dim3(256), 0, s, p.ws, p.dA, (int)B, p.H, nR, p.NS);
@@ -633,16 +675,23 @@ bool ssd2_bwd_supported(int64_t Dh, int64_t N) {
   return (Dh == 32 || Dh == 64) && (N == 16 || N == 32);
 }
 
-// Workspace layout (floats, each part 256-byte aligned): per-chunk delta
-// totals [B,H,nC] (pipelined), dA partials [B,H,nR,N] (backward), backward
-// chunk aggregates / adjoints [B,H,nC,Dh,N] (pipelined backward).
+int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N) {
+  // (B * H < 512 keeps the 1-D per-chunk grid below 2^31 for any nC < 2^22)
+  if (B * H >= 512 || nC >= ((int64_t)1 << 22)) return chunked::kWhole;
+  if (nC <= chunked::kDirectMaxChunks && Dh * N <= chunked::kDirectMaxState) return chunked::kDirect;
+  return chunked::kPipe;
+}
+
+// Workspace layout (floats, each part 256-byte aligned): per-chunk decays
+// [B,H,nC] (pipelined), dA partials [B,H,nR,N] (backward), backward chunk
+// aggregates / adjoints [B,H,nC,Dh,N] (pipelined backward).
 namespace {
 int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }
 }
 
-size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int R, int64_t Dh, int64_t N, int pass) {
-  const int64_t nR = (nC + R - 1) / R;
-  const bool pipe = nR > 1;
+size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int mode, int64_t Dh, int64_t N, int pass) {
+  const int64_t nR = mode == chunked::kWhole ? 1 : nC;
+  const bool pipe = mode == chunked::kPipe;
   int64_t f = pipe ? align64(B * H * nC) : 0;
   if (pass == 1) {
     f += align64(B * H * nR * N);
@@ -654,7 +703,7 @@ size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int R, int64_t Dh, int64_
 void ssd2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass) {
   float* f = static_cast<float*>(ws);
   const int64_t nR = (a.nC + a.R - 1) / a.R;
-  const bool pipe = nR > 1;
+  const bool pipe = a.mode == chunked::kPipe;
   a.tot = a.ws = a.agg = nullptr;
   if (pipe) { a.tot = f; f += align64(B * a.H * a.nC); }
   if (pass == 1) {

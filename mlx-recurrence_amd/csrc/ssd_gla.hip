@@ -554,7 +554,7 @@ extern "C" size_t rr_ssd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_
                                          int64_t seg, int64_t A_stride_n, int dtype, int pass) {
   if (B <= 0 || L <= 0 || H <= 0 || Dh <= 0 || N <= 0 || rr::chunk_len(L, seg) == 0) return 0;
   if (rr::ssd2_supported(dtype, L, seg, Dh, N, A_stride_n) && (pass == 0 || rr::ssd2_bwd_supported(Dh, N)))
-    return rr::ssd2_ws_bytes(B, H, L / 32, rr::ssd2_pick_run(B, H, L / 32, N), Dh, N, pass);
+    return rr::ssd2_ws_bytes(B, H, L / 32, rr::chunked_mode(B, H, L / 32, Dh, N), Dh, N, pass);
   const Plan q = make_plan(B, L, H, Dh, N, seg);
   return pass == 0 ? q.fwd_bytes : q.bwd_bytes;
 }
@@ -581,9 +581,10 @@ extern "C" int rr_ssd_fwd(const void* u, const void* delta, const void* Bm, cons
     a.h0 = h0;
     a.y = y;
     a.ckpt = ckpt;
-    a.L = (int)L; a.H = (int)H; a.DH = (int)Dh; a.NS = (int)N; a.nC = (int)(L / 32);
-    a.R = rr::ssd2_pick_run(B, H, a.nC, N);
-    const size_t need = rr::ssd2_ws_bytes(B, H, a.nC, a.R, Dh, N, 0);
+    a.B = (int)B; a.L = (int)L; a.H = (int)H; a.DH = (int)Dh; a.NS = (int)N; a.nC = (int)(L / 32);
+    a.mode = rr::chunked_mode(B, H, a.nC, Dh, N);
+    a.R = a.mode == 0 ? a.nC : 1;
+    const size_t need = rr::ssd2_ws_bytes(B, H, a.nC, a.mode, Dh, N, 0);
     if (need && (!workspace || workspace_bytes < need))
       return rr::fail(RR_EWORKSPACE, "ssd_fwd: workspace too small");
     rr::ssd2_carve_ws(a, workspace, B, 0);
@@ -627,8 +628,8 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
     return rr::fail(RR_EINVAL, "ssd_bwd: A_stride_n must be 0 or 1");
   if (rr::ssd2_supported(dtype, L, seg, Dh, N, A_stride_n) && rr::ssd2_bwd_supported(Dh, N)) {
     const int nC = (int)(L / 32);
-    const int R = rr::ssd2_pick_run(B, H, nC, N);
-    if (!workspace || workspace_bytes < rr::ssd2_ws_bytes(B, H, nC, R, Dh, N, 1))
+    const int mode = rr::chunked_mode(B, H, nC, Dh, N);
+    if (!workspace || workspace_bytes < rr::ssd2_ws_bytes(B, H, nC, mode, Dh, N, 1))
       return rr::fail(RR_EWORKSPACE, "ssd_bwd: workspace too small");
     rr::ChunkArgs a{};
     a.u = static_cast<const uint16_t*>(u);
@@ -647,7 +648,9 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
     a.dC = static_cast<uint16_t*>(dC);
     a.dA = dA_neg;
     a.dh0 = dh0;
-    a.L = (int)L; a.H = (int)H; a.DH = (int)Dh; a.NS = (int)N; a.nC = nC; a.R = R;
+    a.B = (int)B; a.L = (int)L; a.H = (int)H; a.DH = (int)Dh; a.NS = (int)N; a.nC = nC;
+    a.mode = mode;
+    a.R = mode == 0 ? nC : 1;
     rr::ssd2_carve_ws(a, workspace, B, 1);
     return rr::ssd2_bwd(a, B, static_cast<hipStream_t>(stream));
   }
@@ -699,14 +702,15 @@ namespace {
 // Chunked-kernel arguments of a GLA call (u = v, delta = gates, Bm = k, Cm = q).
 rr::ChunkArgs gla2_args(const void* qp, const void* kp, const void* vp, const void* gates, int64_t B,
                         int64_t L, int64_t H, int64_t Dh, const float* h0) {
-  (void)B;
   rr::ChunkArgs a{};
+  a.B = (int)B;
   a.u = static_cast<const uint16_t*>(vp);
   a.delta = static_cast<const uint16_t*>(gates);
   a.Bm = static_cast<const uint16_t*>(kp);
   a.Cm = static_cast<const uint16_t*>(qp);
   a.h0 = h0;
   a.L = (int)L; a.H = (int)H; a.DH = (int)Dh; a.NS = (int)Dh; a.nC = (int)(L / 32);
+  a.mode = rr::gla2_mode(a.nC, Dh);
   a.R = 1;
   return a;
 }
@@ -715,7 +719,7 @@ rr::ChunkArgs gla2_args(const void* qp, const void* kp, const void* vp, const vo
 extern "C" size_t rr_gla_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh,
                                          int64_t seg, int dtype, int pass) {
   if (B <= 0 || L <= 0 || H <= 0 || Dh <= 0 || rr::chunk_len(L, seg) == 0) return 0;
-  if (rr::gla2_supported(dtype, L, seg, Dh, pass)) return rr::gla2_ws_bytes(B, H, L / 32, Dh, pass);
+  if (rr::gla2_supported(dtype, B, L, H, seg, Dh, pass)) return rr::gla2_ws_bytes(B, H, L / 32, Dh, pass);
   const Plan q = make_plan(B, L, H, Dh, Dh, seg);
   return pass == 0 ? q.fwd_bytes : q.bwd_bytes;
 }
@@ -728,11 +732,12 @@ extern "C" int rr_gla_fwd(const void* qp, const void* kp, const void* vp, const 
   if (!qp || !kp || !vp || !gates || !y || !ckpt)
     return rr::fail(RR_EINVAL, "gla_fwd: null pointer argument");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (rr::gla2_supported(dtype, L, seg, Dh, 0)) {
+  if (rr::gla2_supported(dtype, B, L, H, seg, Dh, 0)) {
     rr::ChunkArgs a = gla2_args(qp, kp, vp, gates, B, L, H, Dh, h0);
     a.y = y;
     a.ckpt = ckpt;
-    if (!workspace || workspace_bytes < rr::gla2_ws_bytes(B, H, a.nC, Dh, 0))
+    const size_t need = rr::gla2_ws_bytes(B, H, a.nC, Dh, 0);
+    if (need && (!workspace || workspace_bytes < need))
       return rr::fail(RR_EWORKSPACE, "gla_fwd: workspace too small");
     rr::gla2_carve_ws(a, workspace, B, 0);
     return rr::gla2_fwd(a, B, s);
@@ -764,7 +769,7 @@ extern "C" int rr_gla_bwd(const float* dy, const float* dfinal, const void* qp, 
   if (int rc = check_dims("gla_bwd", B, L, H, Dh, Dh, seg, dtype, "Dh")) return rc;
   if (!dy || !qp || !kp || !vp || !gates || !ckpt || !dq || !dk || !dv || !dgates)
     return rr::fail(RR_EINVAL, "gla_bwd: null pointer argument");
-  if (rr::gla2_supported(dtype, L, seg, Dh, 1)) {
+  if (rr::gla2_supported(dtype, B, L, H, seg, Dh, 1)) {
     rr::ChunkArgs a = gla2_args(qp, kp, vp, gates, B, L, H, Dh, h0);
     a.ckpt = const_cast<float*>(ckpt);
     a.dy = dy;
@@ -774,7 +779,8 @@ extern "C" int rr_gla_bwd(const float* dy, const float* dfinal, const void* qp, 
     a.dB = static_cast<uint16_t*>(dk);
     a.dC = static_cast<uint16_t*>(dq);
     a.dh0 = dh0;
-    if (!workspace || workspace_bytes < rr::gla2_ws_bytes(B, H, a.nC, Dh, 1))
+    const size_t need = rr::gla2_ws_bytes(B, H, a.nC, Dh, 1);
+    if (need && (!workspace || workspace_bytes < need))
       return rr::fail(RR_EWORKSPACE, "gla_bwd: workspace too small");
     rr::gla2_carve_ws(a, workspace, B, 1);
     return rr::gla2_bwd(a, B, static_cast<hipStream_t>(stream));

@@ -203,6 +203,9 @@ SSD_CASES = [
     (1, 128, 512, 32, 16, 32, BF16, "cfg", True, True, 17),
     (2, 96, 256, 64, 32, 32, BF16, "cfg", False, True, 18),
     (2, 64, 256, 64, 16, 32, BF16, "cfg", True, False, 19),
+    # more than 16 chunks: pipelined mode (aggregate, state-pass and chunk kernels)
+    (1, 1024, 3, 64, 16, 32, BF16, "cfg", True, True, 26),
+    (2, 640, 2, 32, 32, 32, BF16, "cfg", False, True, 27),
 ]
 
 
@@ -275,6 +278,8 @@ GLA_CASES = [
     (2, 32, 2, 64, 32, BF16, "cfg", True, True, 23),    # one chunk
     (1, 160, 2, 64, 32, BF16, "signed", True, True, 24),
     (1, 128, 2, 32, 32, BF16, "zeros", True, True, 25),
+    (1, 640, 3, 64, 32, BF16, "cfg", True, True, 28),      # pipelined mode
+    (2, 1024, 2, 32, 32, BF16, "signed", True, True, 29),
 ]
 
 
