@@ -254,17 +254,20 @@ def make_rglru(cfg, device, dtype):
     out = dict(y=torch.empty((B, L, D), dtype=f32, device=device),
                ckpt=torch.empty((B, nC, D), dtype=f32, device=device),
                da=torch.empty((B, L, D), dtype=dtype, device=device),
-               dx=torch.empty((B, L, D), dtype=dtype, device=device))
+               dx=torch.empty((B, L, D), dtype=dtype, device=device),
+               wsf=_lib.rglru_workspace(B, L, D, seg, dtype, 0, device),
+               wsb=_lib.rglru_workspace(B, L, D, seg, dtype, 1, device))
     es = torch.tensor([], dtype=dtype).element_size()
     n, n_ck = B * L * D, B * nC * D
     fwd_bytes = 2 * n * es + n * 4 + n_ck * 4
     bwd_bytes = n * 4 + n_ck * 4 + 2 * n * es + 2 * n * es
 
     def fwd():
-        _lib.rglru_fwd(d["a"], d["x"], None, seg, out["y"], out["ckpt"])
+        _lib.rglru_fwd(d["a"], d["x"], None, seg, out["y"], out["ckpt"], out["wsf"])
 
     def bwd():
-        _lib.rglru_bwd(d["dy"], None, d["a"], d["x"], None, out["ckpt"], seg, out["da"], out["dx"], None)
+        _lib.rglru_bwd(d["dy"], None, d["a"], d["x"], None, out["ckpt"], seg, out["da"], out["dx"], None,
+                       out["wsb"])
 
     def eager():
         import mlx_recurrence_amd as mr
@@ -305,7 +308,9 @@ def make_rotlru(cfg, device, dtype):
                da=torch.empty((B, L, Dp), dtype=dtype, device=device),
                dcs=torch.empty((B, L, Dp), dtype=dtype, device=device),
                dsn=torch.empty((B, L, Dp), dtype=dtype, device=device),
-               dx=torch.empty((B, L, 2 * Dp), dtype=dtype, device=device))
+               dx=torch.empty((B, L, 2 * Dp), dtype=dtype, device=device),
+               wsf=_lib.rotlru_workspace(B, L, Dp, seg, dtype, 0, device),
+               wsb=_lib.rotlru_workspace(B, L, Dp, seg, dtype, 1, device))
     es = torch.tensor([], dtype=dtype).element_size()
     n_p, n_x, n_ck = B * L * Dp, B * L * 2 * Dp, B * nC * 2 * Dp
     ins = (3 * n_p + n_x) * es
@@ -313,11 +318,11 @@ def make_rotlru(cfg, device, dtype):
     bwd_bytes = n_x * 4 + n_ck * 4 + ins + ins
 
     def fwd():
-        _lib.rotlru_fwd(d["a"], d["cs"], d["sn"], d["x"], None, seg, out["y"], out["ckpt"])
+        _lib.rotlru_fwd(d["a"], d["cs"], d["sn"], d["x"], None, seg, out["y"], out["ckpt"], out["wsf"])
 
     def bwd():
         _lib.rotlru_bwd(d["dy"], None, d["a"], d["cs"], d["sn"], d["x"], None, out["ckpt"], seg,
-                        out["da"], out["dcs"], out["dsn"], out["dx"], None)
+                        out["da"], out["dcs"], out["dsn"], out["dx"], None, out["wsb"])
 
     def eager():
         import mlx_recurrence_amd as mr
@@ -418,6 +423,7 @@ def measure(name, steps, warmup, dtype, device, with_cpu):
         for k in range(nk):
             us = pass_us[pname] if nk == 1 else chain_time(fn, keep=k)[0]
             kernels.append(dict(pass_=pname, index=k, us=us, pass_bytes=nbytes, n_kernels=nk))
+        print(f"[bench] {name} {pname}: {pass_us[pname]:.1f} us per pass, {nk} kernel(s)", file=sys.stderr, flush=True)
     dom = max(kernels, key=lambda r: r["us"])
     achieved = dom["pass_bytes"] / (dom["us"] * 1e-6) / 1e9  # GB/s
 

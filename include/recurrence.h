@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define RR_ABI_VERSION 3
+#define RR_ABI_VERSION 4
 
 enum rr_dtype { RR_F32 = 0, RR_BF16 = 1, RR_F16 = 2 };
 
@@ -126,32 +126,46 @@ int rr_gla_bwd(const float* dy, const float* dfinal, const void* q, const void* 
 
 /* --------------------------------------------------------------- RG-LRU --
  * a, x [B,L,D] (dtype).  y [B,L,D] fp32.  ckpt [B,nC,D] fp32.
- * h0 / dfinal / dh0: [B,D] fp32.  No workspace.
+ * h0 / dfinal / dh0: [B,D] fp32.
+ * The workspace carries the hand-off of states between the tiles of one pass
+ * (each call clears what it uses); calls that share a workspace must not run
+ * concurrently.
  */
+
+/* Workspace bytes needed by rr_rglru_fwd (pass=0) or rr_rglru_bwd (pass=1). */
+size_t rr_rglru_workspace_bytes(int64_t B, int64_t L, int64_t D, int64_t seg, int dtype, int pass);
+
 /* Replaces _rglru_forward_kernel (reference mlx_recurrence/rglru.py:64-123). */
 int rr_rglru_fwd(const void* a, const void* x, int dtype, int64_t B, int64_t L, int64_t D,
-                 int64_t seg, const float* h0, float* y, float* ckpt, void* stream);
+                 int64_t seg, const float* h0, float* y, float* ckpt, void* workspace,
+                 size_t workspace_bytes, void* stream);
 
 /* Replaces _rglru_backward_kernel (reference mlx_recurrence/rglru.py:130-203). */
 int rr_rglru_bwd(const float* dy, const float* dfinal, const void* a, const void* x,
                  int dtype, int64_t B, int64_t L, int64_t D, int64_t seg, const float* h0,
-                 const float* ckpt, void* da, void* dx, float* dh0, void* stream);
+                 const float* ckpt, void* da, void* dx, float* dh0, void* workspace,
+                 size_t workspace_bytes, void* stream);
 
 /* --------------------------------------------------------------- rotLRU --
  * a, cs, sn [B,L,Dp]; x [B,L,2*Dp] with (u,w) pairs interleaved (dtype).
  * y [B,L,2*Dp] fp32 (interleaved).  ckpt [B,nC,2*Dp] fp32.
- * h0 / dfinal / dh0: [B,2*Dp] fp32 (interleaved).  No workspace.
+ * h0 / dfinal / dh0: [B,2*Dp] fp32 (interleaved).  Workspace as for RG-LRU.
  */
+
+/* Workspace bytes needed by rr_rotlru_fwd (pass=0) or rr_rotlru_bwd (pass=1). */
+size_t rr_rotlru_workspace_bytes(int64_t B, int64_t L, int64_t Dp, int64_t seg, int dtype, int pass);
+
 /* Replaces _rotlru_forward_kernel (reference mlx_recurrence/rotlru.py:80-146). */
 int rr_rotlru_fwd(const void* a, const void* cs, const void* sn, const void* x, int dtype,
                   int64_t B, int64_t L, int64_t Dp, int64_t seg, const float* h0, float* y,
-                  float* ckpt, void* stream);
+                  float* ckpt, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Replaces _rotlru_backward_kernel (reference mlx_recurrence/rotlru.py:153-266). */
 int rr_rotlru_bwd(const float* dy, const float* dfinal, const void* a, const void* cs,
                   const void* sn, const void* x, int dtype, int64_t B, int64_t L,
                   int64_t Dp, int64_t seg, const float* h0, const float* ckpt, void* da,
-                  void* dcs, void* dsn, void* dx, float* dh0, void* stream);
+                  void* dcs, void* dsn, void* dx, float* dh0, void* workspace,
+                  size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

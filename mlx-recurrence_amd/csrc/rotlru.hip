@@ -4,333 +4,358 @@
 // i.e. h_t = z_t h_{t-1} + x_t with the complex gate z_t = a_t (c_t + i s_t).
 //
 // Reference: mlx_recurrence/rotlru.py (forward :80-146, backward :153-266, VJP
-// :317-322).  Same chunk-parallel workgroup structure as rglru.hip: a workgroup
-// owns 64 pairs of one batch row for all L steps; its waves take consecutive
-// chunks, fold them into complex affine maps (P, E), exchange the maps through
-// LDS, then replay their chunk from the composed entering state.  The adjoint
-// multiplies by conj(z_t) (the transpose of a_t R(theta_t)), so the backward
-// pass has the same map structure in reverse time.
-#include "rr_common.h"
+// :35-40, :206-235).  Same tiled chained scan as rglru.hip (rr_tiles.h): a
+// workgroup of NW waves owns a tile of 64 * CP pairs of one batch row and
+// NW * U steps; lane l holds pairs CP*l .. CP*l + CP - 1 (a/cs/sn: one CP-wide
+// access per step; x and y: one 2*CP-wide access).  The maps h -> P h + E are
+// complex; the adjoint multiplies by conj(z_t) (the transpose of a_t R(theta_t)),
+// so the backward pass has the same structure in reverse time.
+#include "rr_tiles.h"
 
 namespace {
 
-constexpr int kMaxT = 32;
+using rr::tiles::Pack;
+using rr::tiles::ld_pack;
+using rr::tiles::pack_fill;
 
-template <typename InT, int NW>
-__global__ __launch_bounds__(64 * NW) void rotlru_fwd_kernel(
-    const InT* __restrict__ a, const InT* __restrict__ cs, const InT* __restrict__ sn,
-    const InT* __restrict__ x, const float* __restrict__ h0, float* __restrict__ y,
-    float* __restrict__ ckpt, int L, int Dp, int T, int nC) {
-  __shared__ float sPr[NW][64], sPi[NW][64], sEu[NW][64], sEw[NW][64];
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int p = blockIdx.x * 64 + lane;
-  const int b = blockIdx.y;
-  const int D = 2 * Dp;
-  const bool pok = p < Dp;
-  const int64_t pbase = (int64_t)b * L * Dp + p;
-  const int64_t xbase = (int64_t)b * L * D + 2 * p;
-  float cu = 0.f, cw = 0.f;
-  if (h0 != nullptr && pok) {
-    cu = h0[(int64_t)b * D + 2 * p];
-    cw = h0[(int64_t)b * D + 2 * p + 1];
-  }
+constexpr int kNW = 8;
+constexpr int kCP = 2;   // pairs per lane
+constexpr int kU = 8;    // steps per wave
 
-  for (int c0 = 0; c0 < nC; c0 += NW) {
-    const int c = c0 + w;
-    const bool act = pok && c < nC;
-    float av[kMaxT], cv[kMaxT], sv[kMaxT], xu[kMaxT], xw[kMaxT];
+struct TileGrid {
+  int G;   // pair tiles per batch row
+  int K;   // step tiles
+  int64_t tiles() const { return (int64_t)G * K; }
+};
+inline TileGrid tile_grid(int64_t L, int64_t Dp) {
+  const int64_t S = (int64_t)kU * kNW;
+  return TileGrid{(int)((Dp + 64 * kCP - 1) / (64 * kCP)), (int)((L + S - 1) / S)};
+}
+
+struct cplx {
+  float r, i;
+};
+__device__ __forceinline__ cplx cmul(cplx p, cplx q) { return {p.r * q.r - p.i * q.i, p.r * q.i + p.i * q.r}; }
+__device__ __forceinline__ cplx cfma(cplx p, cplx q, cplx e) {   // p q + e
+  return {p.r * q.r - p.i * q.i + e.r, p.r * q.i + p.i * q.r + e.i};
+}
+__device__ __forceinline__ cplx conj(cplx p) { return {p.r, -p.i}; }
+
+// The inputs of one wave: U steps of CP pairs.
+template <typename InT, int U>
+struct WaveIn {
+  Pack<InT, kCP> a[U], c[U], s[U];
+  Pack<InT, 2 * kCP> x[U];
+  __device__ cplx z(int u, int q) const { return {a[u][q] * c[u][q], a[u][q] * s[u][q]}; }
+  __device__ cplx xin(int u, int q) const { return {x[u][2 * q], x[u][2 * q + 1]}; }
+};
+
+template <typename InT, int U>
+__device__ __forceinline__ void load_wave(WaveIn<InT, U>& in, const InT* a, const InT* cs, const InT* sn,
+                                          const InT* x, int64_t row0, int t0, int L, int Dp, int p, bool pok) {
 #pragma unroll
-    for (int t = 0; t < kMaxT; ++t) {
-      av[t] = 1.f;  // identity step past the end
-      cv[t] = 1.f;
-      sv[t] = 0.f;
-      xu[t] = 0.f;
-      xw[t] = 0.f;
-      if (t < T && act) {
-        const int64_t ip = pbase + (int64_t)(c * T + t) * Dp;
-        const int64_t ix = xbase + (int64_t)(c * T + t) * D;
-        av[t] = rr::ld(a, ip);
-        cv[t] = rr::ld(cs, ip);
-        sv[t] = rr::ld(sn, ip);
-        xu[t] = rr::ld(x, ix);
-        xw[t] = rr::ld(x, ix + 1);
-      }
+  for (int u = 0; u < U; ++u) {
+    const int t = t0 + u;
+    if (pok && t < L) {
+      const int64_t ip = (row0 + t) * Dp + p;
+      in.a[u] = ld_pack<InT, kCP>(a, ip);
+      in.c[u] = ld_pack<InT, kCP>(cs, ip);
+      in.s[u] = ld_pack<InT, kCP>(sn, ip);
+      in.x[u] = ld_pack<InT, 2 * kCP>(x, 2 * ip);
+    } else {   // identity step: z = 1, x = 0
+      in.a[u] = pack_fill<InT, kCP>(1.f);
+      in.c[u] = pack_fill<InT, kCP>(1.f);
+      in.s[u] = pack_fill<InT, kCP>(0.f);
+      in.x[u] = pack_fill<InT, 2 * kCP>(0.f);
     }
-    float pr = 1.f, pi = 0.f, eu = 0.f, ew = 0.f;
-#pragma unroll
-    for (int t = 0; t < kMaxT; ++t) {
-      if (t < T) {
-        const float un = av[t] * (cv[t] * eu - sv[t] * ew) + xu[t];
-        const float wn = av[t] * (sv[t] * eu + cv[t] * ew) + xw[t];
-        eu = un;
-        ew = wn;
-        const float zr = av[t] * cv[t], zi = av[t] * sv[t];
-        const float npr = zr * pr - zi * pi;
-        const float npi = zr * pi + zi * pr;
-        pr = npr;
-        pi = npi;
-      }
-    }
-    sPr[w][lane] = pr;
-    sPi[w][lane] = pi;
-    sEu[w][lane] = eu;
-    sEw[w][lane] = ew;
-    __syncthreads();
-    float hu = cu, hw = cw, nu = cu, nw = cw;
-#pragma unroll
-    for (int j = 0; j < NW; ++j) {
-      const float qr = sPr[j][lane], qi = sPi[j][lane], qu = sEu[j][lane], qw = sEw[j][lane];
-      if (j < w) {
-        const float tu = qr * hu - qi * hw + qu;
-        const float tw = qi * hu + qr * hw + qw;
-        hu = tu;
-        hw = tw;
-      }
-      const float tu = qr * nu - qi * nw + qu;
-      const float tw = qi * nu + qr * nw + qw;
-      nu = tu;
-      nw = tw;
-    }
-    float u = hu, v = hw;
-#pragma unroll
-    for (int t = 0; t < kMaxT; ++t) {
-      if (t < T) {
-        // same update and operation order as rotlru.py:101-104
-        const float un = av[t] * (cv[t] * u - sv[t] * v) + xu[t];
-        const float wn = av[t] * (sv[t] * u + cv[t] * v) + xw[t];
-        u = un;
-        v = wn;
-        if (act) {
-          const int64_t ix = xbase + (int64_t)(c * T + t) * D;
-          *reinterpret_cast<float2*>(y + ix) = make_float2(u, v);
-        }
-      }
-    }
-    if (act) {
-      *reinterpret_cast<float2*>(ckpt + ((int64_t)b * nC + c) * D + 2 * p) = make_float2(u, v);
-    }
-    __syncthreads();
-    cu = nu;
-    cw = nw;
   }
 }
 
-// Adjoint (rotlru.py:317-322, :212-234):
-//   lam += dy_t; dx_t = lam; da_t = lam . (R_t h_{t-1});
+template <typename InT>
+__global__ __launch_bounds__(64 * kNW, 4) void rotlru_fwd_kernel(
+    const InT* __restrict__ a, const InT* __restrict__ cs, const InT* __restrict__ sn,
+    const InT* __restrict__ x, const float* __restrict__ h0, float* __restrict__ y,
+    float* __restrict__ ckpt, uint32_t* counter, uint64_t* slots, int B, int L, int Dp, int T, int nC,
+    int G, int K) {
+  constexpr int GP = 64 * kCP, S = kU * kNW;
+  __shared__ cplx sP[kNW][GP], sE[kNW][GP];
+  __shared__ cplx sIn[GP];
+  __shared__ int sTicket;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int nGrp = B * G;
+  const int ticket = rr::tiles::take_ticket(counter, nGrp * K, &sTicket);
+  if (ticket < 0) return;
+  const int k = ticket / nGrp, grp = ticket % nGrp;
+  const int b = grp / G, g = grp % G;
+  const int p = g * GP + lane * kCP;
+  const bool pok = p < Dp;
+  const int D = 2 * Dp;
+  const int t0 = k * S + w * kU;
+  const int64_t row0 = (int64_t)b * L;
+
+  WaveIn<InT, kU> in;
+  load_wave<InT, kU>(in, a, cs, sn, x, row0, t0, L, Dp, p, pok);
+#pragma unroll
+  for (int q = 0; q < kCP; ++q) {
+    cplx P{1.f, 0.f}, E{0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const cplx z = in.z(u, q);
+      E = cfma(z, E, in.xin(u, q));
+      P = cmul(z, P);
+    }
+    sP[w][lane * kCP + q] = P;
+    sE[w][lane * kCP + q] = E;
+  }
+  __syncthreads();
+  if (w == 0) {
+    uint64_t* mine = slots + ((int64_t)grp * K + k) * (2 * GP) + 2 * lane * kCP;
+#pragma unroll
+    for (int q = 0; q < kCP; ++q) {
+      cplx hin{0.f, 0.f};
+      if (k > 0) {
+        hin.r = rr::tiles::take_value(mine - 2 * GP + 2 * q);
+        hin.i = rr::tiles::take_value(mine - 2 * GP + 2 * q + 1);
+      } else if (h0 != nullptr && pok) {
+        hin = {h0[(int64_t)b * D + 2 * (p + q)], h0[(int64_t)b * D + 2 * (p + q) + 1]};
+      }
+      sIn[lane * kCP + q] = hin;
+      if (k + 1 < K) {
+        cplx hout = hin;
+#pragma unroll
+        for (int j = 0; j < kNW; ++j) hout = cfma(sP[j][lane * kCP + q], hout, sE[j][lane * kCP + q]);
+        rr::tiles::publish(mine + 2 * q, hout.r);
+        rr::tiles::publish(mine + 2 * q + 1, hout.i);
+      }
+    }
+  }
+  __syncthreads();
+  cplx h[kCP];
+#pragma unroll
+  for (int q = 0; q < kCP; ++q) {
+    h[q] = sIn[lane * kCP + q];
+    for (int j = 0; j < w; ++j) h[q] = cfma(sP[j][lane * kCP + q], h[q], sE[j][lane * kCP + q]);
+  }
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const int t = t0 + u;
+    float out[2 * kCP];
+#pragma unroll
+    for (int q = 0; q < kCP; ++q) {
+      h[q] = cfma(in.z(u, q), h[q], in.xin(u, q));   // rotlru.py:101-122
+      out[2 * q] = h[q].r;
+      out[2 * q + 1] = h[q].i;
+    }
+    if (pok && t < L) {
+      rr::tiles::st_f32<2 * kCP>(y, (row0 + t) * D + 2 * p, out);
+      if ((t + 1) % T == 0) rr::tiles::st_f32<2 * kCP>(ckpt, ((int64_t)b * nC + (t + 1) / T - 1) * D + 2 * p, out);
+    }
+  }
+}
+
+// Adjoint (rotlru.py:35-40, :206-235), per step t going backwards with
+// r = R(theta_t) h_{t-1}:
+//   lam += dy_t; dx_t = lam; da_t = lam . r;
 //   dcs_t = a_t (lamU u_{t-1} + lamW w_{t-1}); dsn_t = a_t (lamW u_{t-1} - lamU w_{t-1});
-//   lam <- a_t R_t^T lam.
-template <typename InT, int NW>
-__global__ __launch_bounds__(64 * NW) void rotlru_bwd_kernel(
+//   lam = conj(z_t) lam.
+template <typename InT>
+__global__ __launch_bounds__(64 * kNW, 2) void rotlru_bwd_kernel(
     const float* __restrict__ dy, const float* __restrict__ dfinal, const InT* __restrict__ a,
     const InT* __restrict__ cs, const InT* __restrict__ sn, const InT* __restrict__ x,
     const float* __restrict__ h0, const float* __restrict__ ckpt, InT* __restrict__ da,
-    InT* __restrict__ dcs, InT* __restrict__ dsn, InT* __restrict__ dx,
-    float* __restrict__ dh0, int L, int Dp, int T, int nC) {
-  __shared__ float sPr[NW][64], sPi[NW][64], sEu[NW][64], sEw[NW][64];
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int p = blockIdx.x * 64 + lane;
-  const int b = blockIdx.y;
-  const int D = 2 * Dp;
+    InT* __restrict__ dcs, InT* __restrict__ dsn, InT* __restrict__ dx, float* __restrict__ dh0,
+    uint32_t* counter, uint64_t* slots, int B, int L, int Dp, int T, int nC, int G, int K) {
+  constexpr int GP = 64 * kCP, S = kU * kNW;
+  __shared__ cplx sP[kNW][GP], sEf[kNW][GP], sEb[kNW][GP];
+  __shared__ cplx sIn[GP];
+  __shared__ int sTicket;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int nGrp = B * G;
+  const int ticket = rr::tiles::take_ticket(counter, nGrp * K, &sTicket);
+  if (ticket < 0) return;
+  const int k = K - 1 - ticket / nGrp, grp = ticket % nGrp;
+  const int b = grp / G, g = grp % G;
+  const int p = g * GP + lane * kCP;
   const bool pok = p < Dp;
-  const int64_t pbase = (int64_t)b * L * Dp + p;
-  const int64_t xbase = (int64_t)b * L * D + 2 * p;
-  float cu = 0.f, cw = 0.f;
-  if (dfinal != nullptr && pok) {
-    cu = dfinal[(int64_t)b * D + 2 * p];
-    cw = dfinal[(int64_t)b * D + 2 * p + 1];
-  }
+  const int D = 2 * Dp;
+  const int t0 = k * S + w * kU;
+  const int64_t row0 = (int64_t)b * L;
 
-  for (int r0 = 0; r0 < nC; r0 += NW) {
-    const int c = nC - 1 - (r0 + w);
-    const bool act = pok && c >= 0;
-    float su = 0.f, sw = 0.f;  // state entering the chunk
-    if (act) {
-      if (c > 0) {
-        const float2 h = *reinterpret_cast<const float2*>(ckpt + ((int64_t)b * nC + (c - 1)) * D + 2 * p);
-        su = h.x;
-        sw = h.y;
-      } else if (h0 != nullptr) {
-        su = h0[(int64_t)b * D + 2 * p];
-        sw = h0[(int64_t)b * D + 2 * p + 1];
-      }
-    }
-    float av[kMaxT], cv[kMaxT], sv[kMaxT], hu[kMaxT], hw[kMaxT];
+  WaveIn<InT, kU> in;
+  load_wave<InT, kU>(in, a, cs, sn, x, row0, t0, L, Dp, p, pok);
+  cplx gy[kU][kCP];
 #pragma unroll
-    for (int t = 0; t < kMaxT; ++t) {
-      av[t] = 1.f;
-      cv[t] = 1.f;
-      sv[t] = 0.f;
-      hu[t] = 0.f;
-      hw[t] = 0.f;
-      if (t < T && act) {
-        const int64_t ip = pbase + (int64_t)(c * T + t) * Dp;
-        const int64_t ix = xbase + (int64_t)(c * T + t) * D;
-        av[t] = rr::ld(a, ip);
-        cv[t] = rr::ld(cs, ip);
-        sv[t] = rr::ld(sn, ip);
-        hu[t] = rr::ld(x, ix);
-        hw[t] = rr::ld(x, ix + 1);
-      }
-    }
-    // Recompute the chunk's states (hu/hw[t] = state after step t).
-    {
-      float u = su, v = sw;
+  for (int u = 0; u < kU; ++u) {
+    const int t = t0 + u;
+    if (pok && t < L) {
+      const Pack<float, 2 * kCP> g4 = ld_pack<float, 2 * kCP>(dy, (row0 + t) * D + 2 * p);
 #pragma unroll
-      for (int t = 0; t < kMaxT; ++t) {
-        if (t < T) {
-          const float un = av[t] * (cv[t] * u - sv[t] * v) + hu[t];
-          const float wn = av[t] * (sv[t] * u + cv[t] * v) + hw[t];
-          u = un;
-          v = wn;
-          hu[t] = u;
-          hw[t] = v;
-        }
-      }
-    }
-    // Chunk map of the adjoint from a zero carry: (P, E).
-    float pr = 1.f, pi = 0.f, eu = 0.f, ew = 0.f;
+      for (int q = 0; q < kCP; ++q) gy[u][q] = {g4[2 * q], g4[2 * q + 1]};
+    } else {
 #pragma unroll
-    for (int t = kMaxT - 1; t >= 0; --t) {
-      if (t < T) {
-        const float* g = dy + xbase + (int64_t)(c * T + t) * D;
-        float gu = 0.f, gw = 0.f;
-        if (act) {
-          const float2 gg = *reinterpret_cast<const float2*>(g);
-          gu = gg.x;
-          gw = gg.y;
-        }
-        eu += gu;
-        ew += gw;
-        const float nU = av[t] * (cv[t] * eu + sv[t] * ew);
-        const float nW = av[t] * (-sv[t] * eu + cv[t] * ew);
-        eu = nU;
-        ew = nW;
-        const float zr = av[t] * cv[t], zi = -av[t] * sv[t];
-        const float npr = zr * pr - zi * pi;
-        const float npi = zr * pi + zi * pr;
-        pr = npr;
-        pi = npi;
-      }
+      for (int q = 0; q < kCP; ++q) gy[u][q] = {0.f, 0.f};
     }
-    sPr[w][lane] = pr;
-    sPi[w][lane] = pi;
-    sEu[w][lane] = eu;
-    sEw[w][lane] = ew;
-    __syncthreads();
-    float lu = cu, lw = cw, nu = cu, nw = cw;
-#pragma unroll
-    for (int j = 0; j < NW; ++j) {
-      const float qr = sPr[j][lane], qi = sPi[j][lane], qu = sEu[j][lane], qw = sEw[j][lane];
-      if (j < w) {
-        const float tu = qr * lu - qi * lw + qu;
-        const float tw = qi * lu + qr * lw + qw;
-        lu = tu;
-        lw = tw;
-      }
-      const float tu = qr * nu - qi * nw + qu;
-      const float tw = qi * nu + qr * nw + qw;
-      nu = tu;
-      nw = tw;
-    }
-#pragma unroll
-    for (int t = kMaxT - 1; t >= 0; --t) {
-      if (t < T) {
-        const int64_t ip = pbase + (int64_t)(c * T + t) * Dp;
-        const int64_t ix = xbase + (int64_t)(c * T + t) * D;
-        float gu = 0.f, gw = 0.f;
-        if (act) {
-          const float2 gg = *reinterpret_cast<const float2*>(dy + ix);
-          gu = gg.x;
-          gw = gg.y;
-        }
-        lu += gu;
-        lw += gw;
-        const float up = (t > 0) ? hu[t - 1] : su;
-        const float wp = (t > 0) ? hw[t - 1] : sw;
-        const float ru = cv[t] * up - sv[t] * wp;
-        const float rw = sv[t] * up + cv[t] * wp;
-        if (act) {
-          rr::st(dx, ix, lu);
-          rr::st(dx, ix + 1, lw);
-          rr::st(da, ip, lu * ru + lw * rw);
-          rr::st(dcs, ip, av[t] * (lu * up + lw * wp));
-          rr::st(dsn, ip, av[t] * (lw * up - lu * wp));
-        }
-        const float nU = av[t] * (cv[t] * lu + sv[t] * lw);
-        const float nW = av[t] * (-sv[t] * lu + cv[t] * lw);
-        lu = nU;
-        lw = nW;
-      }
-    }
-    __syncthreads();
-    cu = nu;
-    cw = nw;
   }
-  if (dh0 != nullptr && pok && w == 0) {
-    dh0[(int64_t)b * D + 2 * p] = cu;
-    dh0[(int64_t)b * D + 2 * p + 1] = cw;
+  // forward map (from a zero state) and adjoint map (from a zero adjoint)
+#pragma unroll
+  for (int q = 0; q < kCP; ++q) {
+    cplx P{1.f, 0.f}, Ef{0.f, 0.f}, Eb{0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const cplx z = in.z(u, q);
+      Ef = cfma(z, Ef, in.xin(u, q));
+      P = cmul(z, P);
+    }
+#pragma unroll
+    for (int u = kU - 1; u >= 0; --u) {
+      Eb = {Eb.r + gy[u][q].r, Eb.i + gy[u][q].i};
+      Eb = cmul(conj(in.z(u, q)), Eb);
+    }
+    sP[w][lane * kCP + q] = P;
+    sEf[w][lane * kCP + q] = Ef;
+    sEb[w][lane * kCP + q] = Eb;
+  }
+  __syncthreads();
+  if (w == 0) {
+    uint64_t* mine = slots + ((int64_t)grp * K + k) * (2 * GP) + 2 * lane * kCP;
+#pragma unroll
+    for (int q = 0; q < kCP; ++q) {
+      cplx lin{0.f, 0.f};   // adjoint entering the tile from later steps
+      if (k + 1 < K) {
+        lin.r = rr::tiles::take_value(mine + 2 * GP + 2 * q);
+        lin.i = rr::tiles::take_value(mine + 2 * GP + 2 * q + 1);
+      } else if (dfinal != nullptr && pok) {
+        lin = {dfinal[(int64_t)b * D + 2 * (p + q)], dfinal[(int64_t)b * D + 2 * (p + q) + 1]};
+      }
+      sIn[lane * kCP + q] = lin;
+      cplx lout = lin;
+#pragma unroll
+      for (int j = kNW - 1; j >= 0; --j) lout = cfma(conj(sP[j][lane * kCP + q]), lout, sEb[j][lane * kCP + q]);
+      if (k > 0) {
+        rr::tiles::publish(mine + 2 * q, lout.r);
+        rr::tiles::publish(mine + 2 * q + 1, lout.i);
+      } else if (dh0 != nullptr && pok) {
+        dh0[(int64_t)b * D + 2 * (p + q)] = lout.r;
+        dh0[(int64_t)b * D + 2 * (p + q) + 1] = lout.i;
+      }
+    }
+  }
+  __syncthreads();
+  cplx lam[kCP], hin[kCP];
+  const int tb = t0 - t0 % T;   // start of the checkpoint interval (inside the tile: S % 32 == 0)
+#pragma unroll
+  for (int q = 0; q < kCP; ++q) {
+    lam[q] = sIn[lane * kCP + q];
+    for (int j = kNW - 1; j > w; --j) lam[q] = cfma(conj(sP[j][lane * kCP + q]), lam[q], sEb[j][lane * kCP + q]);
+    hin[q] = {0.f, 0.f};
+    if (pok) {
+      const int64_t e = 2 * (p + q);
+      if (tb > 0) hin[q] = {ckpt[((int64_t)b * nC + tb / T - 1) * D + e], ckpt[((int64_t)b * nC + tb / T - 1) * D + e + 1]};
+      else if (h0 != nullptr) hin[q] = {h0[(int64_t)b * D + e], h0[(int64_t)b * D + e + 1]};
+    }
+    for (int j = w - (t0 - tb) / kU; j < w; ++j) hin[q] = cfma(sP[j][lane * kCP + q], hin[q], sEf[j][lane * kCP + q]);
+  }
+  cplx hs[kU][kCP];   // hs[u] = h_{t0+u}
+#pragma unroll
+  for (int q = 0; q < kCP; ++q) {
+    cplx h = hin[q];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      h = cfma(in.z(u, q), h, in.xin(u, q));
+      hs[u][q] = h;
+    }
+  }
+#pragma unroll
+  for (int u = kU - 1; u >= 0; --u) {
+    const int t = t0 + u;
+    float gx[2 * kCP], ga[kCP], gc[kCP], gs[kCP];
+#pragma unroll
+    for (int q = 0; q < kCP; ++q) {
+      const cplx hp = u > 0 ? hs[u - 1][q] : hin[q];
+      const float av = in.a[u][q], cv = in.c[u][q], sv = in.s[u][q];
+      lam[q] = {lam[q].r + gy[u][q].r, lam[q].i + gy[u][q].i};
+      gx[2 * q] = lam[q].r;
+      gx[2 * q + 1] = lam[q].i;
+      const float ru = cv * hp.r - sv * hp.i, rw = sv * hp.r + cv * hp.i;
+      ga[q] = lam[q].r * ru + lam[q].i * rw;
+      gc[q] = av * (lam[q].r * hp.r + lam[q].i * hp.i);
+      gs[q] = av * (lam[q].i * hp.r - lam[q].r * hp.i);
+      lam[q] = cmul(conj(in.z(u, q)), lam[q]);
+    }
+    if (pok && t < L) {
+      const int64_t ip = (row0 + t) * Dp + p;
+      rr::tiles::st_pack<InT, kCP>(da, ip, ga);
+      rr::tiles::st_pack<InT, kCP>(dcs, ip, gc);
+      rr::tiles::st_pack<InT, kCP>(dsn, ip, gs);
+      rr::tiles::st_pack<InT, 2 * kCP>(dx, 2 * ip, gx);
+    }
   }
 }
 
 int check_common(int64_t B, int64_t L, int64_t Dp, int64_t seg, int dtype) {
-  if (B <= 0 || L <= 0 || Dp <= 0) {
-    return rr::fail(RR_EINVAL, "rotlru: B, L and Dp must be positive");
-  }
-  if (int rc = rr::check_segment_shape(L, seg, 2 * Dp, "D")) return rc;
+  if (B <= 0 || L <= 0 || Dp <= 0) return rr::fail(RR_EINVAL, "rotlru: B, L and Dp must be positive");
+  if (int rc = rr::check_segment_shape(L, seg, 2 * Dp, "D")) return rc;   // rotlru.py:283
   if (!rr::valid_dtype(dtype)) return rr::fail(RR_EINVAL, "rotlru: unsupported dtype");
-  if (B > 65535) return rr::fail(RR_EUNSUPPORTED, "rotlru: B > 65535 is not supported");
+  if (B * L * 2 * Dp >= ((int64_t)1 << 40)) return rr::fail(RR_EUNSUPPORTED, "rotlru: tensor too large");
   return RR_OK;
 }
 
-constexpr int kFwdWaves = 8;
-constexpr int kBwdWaves = 4;
+size_t ws_bytes_for(int64_t B, int64_t L, int64_t Dp) {
+  return rr::tiles::ws_bytes(B * tile_grid(L, Dp).tiles(), 2 * 64 * kCP);
+}
 
 }  // namespace
 
-extern "C" int rr_rotlru_fwd(const void* a, const void* cs, const void* sn, const void* x,
-                             int dtype, int64_t B, int64_t L, int64_t Dp, int64_t seg,
-                             const float* h0, float* y, float* ckpt, void* stream) {
+extern "C" size_t rr_rotlru_workspace_bytes(int64_t B, int64_t L, int64_t Dp, int64_t seg, int dtype,
+                                            int pass) {
+  (void)pass;
+  if (B <= 0 || L <= 0 || Dp <= 0 || rr::chunk_len(L, seg) == 0 || !rr::valid_dtype(dtype)) return 0;
+  return ws_bytes_for(B, L, Dp);
+}
+
+extern "C" int rr_rotlru_fwd(const void* a, const void* cs, const void* sn, const void* x, int dtype,
+                             int64_t B, int64_t L, int64_t Dp, int64_t seg, const float* h0, float* y,
+                             float* ckpt, void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_common(B, L, Dp, seg, dtype)) return rc;
-  if (!a || !cs || !sn || !x || !y || !ckpt) {
-    return rr::fail(RR_EINVAL, "rotlru_fwd: null pointer argument");
-  }
+  if (!a || !cs || !sn || !x || !y || !ckpt) return rr::fail(RR_EINVAL, "rotlru_fwd: null pointer argument");
+  const size_t need = ws_bytes_for(B, L, Dp);
+  if (!workspace || workspace_bytes < need) return rr::fail(RR_EWORKSPACE, "rotlru_fwd: workspace too small");
   const int T = (int)rr::chunk_len(L, seg);
   const int nC = (int)(L / T);
-  const dim3 grid((unsigned)((Dp + 63) / 64), (unsigned)B);
+  const TileGrid tg = tile_grid(L, Dp);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  RR_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((rotlru_fwd_kernel<InT, kFwdWaves>), grid,
-                                              dim3(64 * kFwdWaves), 0, s,
-                                              static_cast<const InT*>(a),
-                                              static_cast<const InT*>(cs),
-                                              static_cast<const InT*>(sn),
-                                              static_cast<const InT*>(x), h0, y, ckpt, (int)L,
-                                              (int)Dp, T, nC));
+  if (int rc = rr::tiles::launch_clear(workspace, need, s)) return rc;
+  RR_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((rotlru_fwd_kernel<InT>), dim3((unsigned)(B * tg.tiles())),
+                                              dim3(64 * kNW), 0, s, static_cast<const InT*>(a),
+                                              static_cast<const InT*>(cs), static_cast<const InT*>(sn),
+                                              static_cast<const InT*>(x), h0, y, ckpt,
+                                              rr::tiles::ws_counter(workspace), rr::tiles::ws_slots(workspace),
+                                              (int)B, (int)L, (int)Dp, T, nC, tg.G, tg.K));
   return rr::check_launch("rr_rotlru_fwd");
 }
 
-extern "C" int rr_rotlru_bwd(const float* dy, const float* dfinal, const void* a,
-                             const void* cs, const void* sn, const void* x, int dtype,
-                             int64_t B, int64_t L, int64_t Dp, int64_t seg, const float* h0,
-                             const float* ckpt, void* da, void* dcs, void* dsn, void* dx,
-                             float* dh0, void* stream) {
+extern "C" int rr_rotlru_bwd(const float* dy, const float* dfinal, const void* a, const void* cs,
+                             const void* sn, const void* x, int dtype, int64_t B, int64_t L,
+                             int64_t Dp, int64_t seg, const float* h0, const float* ckpt, void* da,
+                             void* dcs, void* dsn, void* dx, float* dh0, void* workspace,
+                             size_t workspace_bytes, void* stream) {
   if (int rc = check_common(B, L, Dp, seg, dtype)) return rc;
-  if (!dy || !a || !cs || !sn || !x || !ckpt || !da || !dcs || !dsn || !dx) {
+  if (!dy || !a || !cs || !sn || !x || !ckpt || !da || !dcs || !dsn || !dx)
     return rr::fail(RR_EINVAL, "rotlru_bwd: null pointer argument");
-  }
+  const size_t need = ws_bytes_for(B, L, Dp);
+  if (!workspace || workspace_bytes < need) return rr::fail(RR_EWORKSPACE, "rotlru_bwd: workspace too small");
   const int T = (int)rr::chunk_len(L, seg);
   const int nC = (int)(L / T);
-  const dim3 grid((unsigned)((Dp + 63) / 64), (unsigned)B);
+  const TileGrid tg = tile_grid(L, Dp);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  RR_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((rotlru_bwd_kernel<InT, kBwdWaves>), grid,
-                                              dim3(64 * kBwdWaves), 0, s, dy, dfinal,
-                                              static_cast<const InT*>(a),
-                                              static_cast<const InT*>(cs),
-                                              static_cast<const InT*>(sn),
-                                              static_cast<const InT*>(x), h0, ckpt,
-                                              static_cast<InT*>(da), static_cast<InT*>(dcs),
-                                              static_cast<InT*>(dsn), static_cast<InT*>(dx), dh0,
-                                              (int)L, (int)Dp, T, nC));
+  if (int rc = rr::tiles::launch_clear(workspace, need, s)) return rc;
+  RR_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((rotlru_bwd_kernel<InT>), dim3((unsigned)(B * tg.tiles())),
+                                              dim3(64 * kNW), 0, s, dy, dfinal, static_cast<const InT*>(a),
+                                              static_cast<const InT*>(cs), static_cast<const InT*>(sn),
+                                              static_cast<const InT*>(x), h0, ckpt, static_cast<InT*>(da),
+                                              static_cast<InT*>(dcs), static_cast<InT*>(dsn),
+                                              static_cast<InT*>(dx), dh0, rr::tiles::ws_counter(workspace),
+                                              rr::tiles::ws_slots(workspace), (int)B, (int)L, (int)Dp, T, nC,
+                                              tg.G, tg.K));
   return rr::check_launch("rr_rotlru_bwd");
 }

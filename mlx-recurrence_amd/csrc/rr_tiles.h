@@ -1,0 +1,185 @@
+// rr_tiles.h — tiled chained scan for the bandwidth-bound diagonal
+// recurrences (RG-LRU, rotLRU): packed vector loads and the cross-tile
+// state hand-off.
+//
+// A pass is one kernel over tiles of (channels x steps).  A tile loads its
+// inputs once into registers, folds them into the tile's affine map, receives
+// the state entering the tile from its predecessor, hands its own exit state
+// to its successor, and replays its steps from registers.  The hand-off:
+//   - tiles take tickets from an atomic counter in the caller's workspace and
+//     map tickets to tiles so that every predecessor of a tile holds a smaller
+//     ticket; a tile only ever waits for a workgroup that already runs (or has
+//     finished), so the waits always end;
+//   - a state value travels as one 64-bit word (float bits | tag << 32)
+//     written and read with agent-scope atomics: the word validates itself,
+//     so no cache-flushing fence is needed, and the chain is deterministic
+//     (each tile waits for exactly its predecessor);
+//   - the spin is bounded (kMaxSpin) so the kernel terminates whatever
+//     happens, and tickets beyond the tile count end their workgroup at once;
+//   - the workspace is cleared by clear_kernel before each pass, and a pass
+//     also leaves it clear: a consumer zeroes the slot it has read and the
+//     holder of the last ticket zeroes the counter (so a pass replayed
+//     without the clear, e.g. an isolated graph node, still runs correctly).
+#pragma once
+
+#include <algorithm>
+
+#include "rr_common.h"
+
+namespace rr {
+namespace tiles {
+
+constexpr uint32_t kTag = 1;           // "published in this pass"
+constexpr int kMaxSpin = 1 << 20;      // bounded wait (tens of ms): never reached in practice
+constexpr int kWsHeader = 64;          // u32 words before the hand-off slots (counter at [0])
+
+// ---------------------------------------------------------------- packed loads
+// N consecutive elements of an input, kept packed in registers.
+template <typename InT, int N> struct Pack;
+template <> struct Pack<bf16, 4> {
+  uint2 v;
+  __device__ float operator[](int i) const {
+    const uint32_t w = i < 2 ? v.x : v.y;
+    return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
+  }
+};
+template <> struct Pack<bf16, 2> {
+  uint32_t v;
+  __device__ float operator[](int i) const { return __uint_as_float(i ? (v & 0xffff0000u) : (v << 16)); }
+};
+template <> struct Pack<f16, 4> {
+  uint2 v;
+  __device__ float operator[](int i) const {
+    const uint32_t w = i < 2 ? v.x : v.y;
+    const uint16_t h = (i & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffffu);
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+  }
+};
+template <> struct Pack<f16, 2> {
+  uint32_t v;
+  __device__ float operator[](int i) const {
+    const uint16_t h = i ? (uint16_t)(v >> 16) : (uint16_t)(v & 0xffffu);
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+  }
+};
+template <> struct Pack<float, 4> {
+  float4 v;
+  __device__ float operator[](int i) const { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+};
+template <> struct Pack<float, 2> {
+  float2 v;
+  __device__ float operator[](int i) const { return i == 0 ? v.x : v.y; }
+};
+
+// fp32 -> the 16-bit input encoding (round to nearest even).
+template <typename InT>
+__device__ __forceinline__ uint16_t bits16(float v) {
+  if constexpr (__is_same(InT, bf16)) return from_f32<bf16>(v).bits;
+  else return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+
+// Loads elements [i, i + N) (i a multiple of N; the tensor 16-byte aligned).
+template <typename InT, int N>
+__device__ __forceinline__ Pack<InT, N> ld_pack(const InT* p, int64_t i) {
+  Pack<InT, N> r;
+  r.v = *reinterpret_cast<const decltype(r.v)*>(p + i);
+  return r;
+}
+// The identity step of a masked (out-of-range) position: value `one` everywhere.
+template <typename InT, int N>
+__device__ __forceinline__ Pack<InT, N> pack_fill(float one) {
+  Pack<InT, N> r;
+  if constexpr (sizeof(InT) == 4) {
+    float* f = reinterpret_cast<float*>(&r.v);
+#pragma unroll
+    for (int e = 0; e < N; ++e) f[e] = one;
+  } else {
+    const uint16_t bits = bits16<InT>(one);
+    uint16_t* h = reinterpret_cast<uint16_t*>(&r.v);
+#pragma unroll
+    for (int e = 0; e < N; ++e) h[e] = bits;
+  }
+  return r;
+}
+
+// Stores N fp32 values (16 or 8 bytes) at [i, i + N).
+template <int N>
+__device__ __forceinline__ void st_f32(float* p, int64_t i, const float (&v)[N]) {
+  if constexpr (N == 4) *reinterpret_cast<float4*>(p + i) = make_float4(v[0], v[1], v[2], v[3]);
+  else *reinterpret_cast<float2*>(p + i) = make_float2(v[0], v[1]);
+}
+// Stores N values in the input type at [i, i + N).
+template <typename InT, int N>
+__device__ __forceinline__ void st_pack(InT* p, int64_t i, const float (&v)[N]) {
+  if constexpr (sizeof(InT) == 4) {
+    st_f32<N>(reinterpret_cast<float*>(p), i, v);
+  } else {
+    uint16_t h[N];
+#pragma unroll
+    for (int e = 0; e < N; ++e) h[e] = bits16<InT>(v[e]);
+    if constexpr (N == 4) *reinterpret_cast<uint2*>(p + i) = make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16);
+    else *reinterpret_cast<uint32_t*>(p + i) = h[0] | (uint32_t)h[1] << 16;
+  }
+}
+
+// ---------------------------------------------------------------- hand-off
+__device__ __forceinline__ void publish(uint64_t* slot, float v) {
+  const uint64_t word = (uint64_t)__float_as_uint(v) | ((uint64_t)kTag << 32);
+  __hip_atomic_store(slot, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits (bounded) until `slot` holds a published value, clears the slot (its
+// only reader is the caller) and returns the value.
+__device__ __forceinline__ float take_value(uint64_t* slot) {
+  uint64_t word = 0;
+  for (int spin = 0; spin < kMaxSpin; ++spin) {
+    word = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((uint32_t)(word >> 32) == kTag) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  __hip_atomic_store(slot, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __uint_as_float((uint32_t)word);
+}
+
+// Ticket of this workgroup (thread 0 takes it; every thread returns it), or
+// -1 past the tile count.  The holder of the last ticket zeroes the counter:
+// every other workgroup of the pass has taken its ticket by then.
+__device__ __forceinline__ int take_ticket(uint32_t* counter, int ntiles, int* lds_slot) {
+  if (threadIdx.x == 0) {
+    const uint32_t t = atomicAdd(counter, 1u);
+    if (t == (uint32_t)ntiles - 1) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *lds_slot = t < (uint32_t)ntiles ? (int)t : -1;
+  }
+  __syncthreads();
+  return *lds_slot;
+}
+
+// Clears the ticket counter and the hand-off slots of a pass (a template so
+// that every translation unit including this header may instantiate it).
+template <typename W>
+__global__ void clear_kernel(W* ws, int64_t nwords32) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t j = i; j < nwords32 / 4; j += stride) reinterpret_cast<uint4*>(ws)[j] = make_uint4(0, 0, 0, 0);
+}
+
+inline int launch_clear(void* ws, size_t bytes, hipStream_t s) {
+  const int64_t n = (int64_t)(bytes / 4);
+  const int64_t blocks = std::min<int64_t>((n / 4 + 255) / 256, 1024);
+  hipLaunchKernelGGL(clear_kernel<uint32_t>, dim3((unsigned)std::max<int64_t>(blocks, 1)), dim3(256), 0, s,
+                     static_cast<uint32_t*>(ws), n);
+  return check_launch("clear hand-off workspace");
+}
+
+// Workspace bytes of a pass: header + one 64-bit slot per (tile, value),
+// rounded to 16 bytes.
+inline size_t ws_bytes(int64_t tiles, int64_t values_per_tile) {
+  return ((size_t)kWsHeader * 4 + (size_t)(tiles * values_per_tile) * 8 + 15) / 16 * 16;
+}
+inline uint32_t* ws_counter(void* ws) { return static_cast<uint32_t*>(ws); }
+inline uint64_t* ws_slots(void* ws) {
+  return reinterpret_cast<uint64_t*>(static_cast<uint32_t*>(ws) + kWsHeader);
+}
+
+}  // namespace tiles
+}  // namespace rr

@@ -42,10 +42,12 @@ _SIGS = {
     "rr_gla_workspace_bytes": (_c_size, [_c_i64] * 5 + [_c_int, _c_int]),
     "rr_gla_fwd": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
     "rr_gla_bwd": (_c_int, [_c_ptr] * 6 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 8 + [_c_size, _c_ptr]),
-    "rr_rglru_fwd": (_c_int, [_c_ptr] * 2 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 4),
-    "rr_rglru_bwd": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 6),
-    "rr_rotlru_fwd": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 4),
-    "rr_rotlru_bwd": (_c_int, [_c_ptr] * 6 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 8),
+    "rr_rglru_workspace_bytes": (_c_size, [_c_i64] * 4 + [_c_int, _c_int]),
+    "rr_rglru_fwd": (_c_int, [_c_ptr] * 2 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
+    "rr_rglru_bwd": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 6 + [_c_size, _c_ptr]),
+    "rr_rotlru_workspace_bytes": (_c_size, [_c_i64] * 4 + [_c_int, _c_int]),
+    "rr_rotlru_fwd": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
+    "rr_rotlru_bwd": (_c_int, [_c_ptr] * 6 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 8 + [_c_size, _c_ptr]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGS)
@@ -189,32 +191,43 @@ def gla_bwd(dy, dfinal, q, k, v, g, h0, ckpt, seg, dq, dk, dv, dg, dh0, ws):
 
 
 # ---------------------------------------------------------------- RG-LRU
-def rglru_fwd(a, x, h0, seg, y, ckpt):
+def rglru_workspace(B, L, D, seg, dtype, pass_, device) -> torch.Tensor:
+    n = int(load().rr_rglru_workspace_bytes(B, L, D, seg, DTYPE_CODE[dtype], pass_))
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def rglru_fwd(a, x, h0, seg, y, ckpt, ws):
     B, L, D = a.shape
     rc = load().rr_rglru_fwd(ptr(a), ptr(x), DTYPE_CODE[a.dtype], B, L, D, seg,
-                             ptr(h0), ptr(y), ptr(ckpt), stream_of(a))
+                             ptr(h0), ptr(y), ptr(ckpt), ptr(ws), ws.numel(), stream_of(a))
     _check(rc, "rr_rglru_fwd")
 
 
-def rglru_bwd(dy, dfinal, a, x, h0, ckpt, seg, da, dx, dh0):
+def rglru_bwd(dy, dfinal, a, x, h0, ckpt, seg, da, dx, dh0, ws):
     B, L, D = a.shape
     rc = load().rr_rglru_bwd(ptr(dy), ptr(dfinal), ptr(a), ptr(x), DTYPE_CODE[a.dtype],
                              B, L, D, seg, ptr(h0), ptr(ckpt), ptr(da), ptr(dx), ptr(dh0),
-                             stream_of(a))
+                             ptr(ws), ws.numel(), stream_of(a))
     _check(rc, "rr_rglru_bwd")
 
 
 # ---------------------------------------------------------------- rotLRU
-def rotlru_fwd(a, cs, sn, x, h0, seg, y, ckpt):
+def rotlru_workspace(B, L, Dp, seg, dtype, pass_, device) -> torch.Tensor:
+    n = int(load().rr_rotlru_workspace_bytes(B, L, Dp, seg, DTYPE_CODE[dtype], pass_))
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def rotlru_fwd(a, cs, sn, x, h0, seg, y, ckpt, ws):
     B, L, Dp = a.shape
     rc = load().rr_rotlru_fwd(ptr(a), ptr(cs), ptr(sn), ptr(x), DTYPE_CODE[a.dtype],
-                              B, L, Dp, seg, ptr(h0), ptr(y), ptr(ckpt), stream_of(a))
+                              B, L, Dp, seg, ptr(h0), ptr(y), ptr(ckpt), ptr(ws), ws.numel(), stream_of(a))
     _check(rc, "rr_rotlru_fwd")
 
 
-def rotlru_bwd(dy, dfinal, a, cs, sn, x, h0, ckpt, seg, da, dcs, dsn, dx, dh0):
+def rotlru_bwd(dy, dfinal, a, cs, sn, x, h0, ckpt, seg, da, dcs, dsn, dx, dh0, ws):
     B, L, Dp = a.shape
     rc = load().rr_rotlru_bwd(ptr(dy), ptr(dfinal), ptr(a), ptr(cs), ptr(sn), ptr(x),
                               DTYPE_CODE[a.dtype], B, L, Dp, seg, ptr(h0), ptr(ckpt),
-                              ptr(da), ptr(dcs), ptr(dsn), ptr(dx), ptr(dh0), stream_of(a))
+                              ptr(da), ptr(dcs), ptr(dsn), ptr(dx), ptr(dh0), ptr(ws), ws.numel(),
+                              stream_of(a))
     _check(rc, "rr_rotlru_bwd")

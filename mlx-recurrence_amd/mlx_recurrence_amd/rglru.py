@@ -42,7 +42,8 @@ class _RGLRUScan(torch.autograd.Function):
         y = torch.empty((B, L, D), dtype=torch.float32, device=dev)
         ckpt = torch.empty((B, nC, D), dtype=torch.float32, device=dev)
         with torch.cuda.device(dev):
-            _lib.rglru_fwd(a_, x_, h0_, seg, y, ckpt)
+            ws = _lib.rglru_workspace(B, L, D, seg, dt, 0, dev)
+            _lib.rglru_fwd(a_, x_, h0_, seg, y, ckpt, ws)
         ctx.save_for_backward(a_, x_, h0_, ckpt)
         ctx.seg = seg
         ctx.set_materialize_grads(False)
@@ -59,7 +60,8 @@ class _RGLRUScan(torch.autograd.Function):
         dx = torch.empty_like(x_)
         dh0 = torch.empty((B, D), dtype=torch.float32, device=dev) if ctx.needs_input_grad[2] else None
         with torch.cuda.device(dev):
-            _lib.rglru_bwd(dy, dfinal, a_, x_, h0_, ckpt, ctx.seg, da, dx, dh0)
+            ws = _lib.rglru_workspace(B, L, D, ctx.seg, a_.dtype, 1, dev)
+            _lib.rglru_bwd(dy, dfinal, a_, x_, h0_, ckpt, ctx.seg, da, dx, dh0, ws)
         return da, dx, dh0, None
 
 

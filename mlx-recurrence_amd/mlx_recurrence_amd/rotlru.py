@@ -54,7 +54,8 @@ class _RotLRUScan(torch.autograd.Function):
         y = torch.empty((B, L, D), dtype=torch.float32, device=dev)
         ckpt = torch.empty((B, nC, D), dtype=torch.float32, device=dev)
         with torch.cuda.device(dev):
-            _lib.rotlru_fwd(a_, cs_, sn_, x_, h0_, seg, y, ckpt)
+            ws = _lib.rotlru_workspace(B, L, Dp, seg, dt, 0, dev)
+            _lib.rotlru_fwd(a_, cs_, sn_, x_, h0_, seg, y, ckpt, ws)
         ctx.save_for_backward(a_, cs_, sn_, x_, h0_, ckpt)
         ctx.seg = seg
         ctx.set_materialize_grads(False)
@@ -72,7 +73,8 @@ class _RotLRUScan(torch.autograd.Function):
         dx = torch.empty_like(x_)
         dh0 = torch.empty((B, D), dtype=torch.float32, device=dev) if ctx.needs_input_grad[4] else None
         with torch.cuda.device(dev):
-            _lib.rotlru_bwd(dy, dfinal, a_, cs_, sn_, x_, h0_, ckpt, ctx.seg, da, dcs, dsn, dx, dh0)
+            ws = _lib.rotlru_workspace(B, L, Dp, ctx.seg, a_.dtype, 1, dev)
+            _lib.rotlru_bwd(dy, dfinal, a_, cs_, sn_, x_, h0_, ckpt, ctx.seg, da, dcs, dsn, dx, dh0, ws)
         return da, dcs, dsn, dx, dh0, None
 
 

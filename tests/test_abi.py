@@ -33,7 +33,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.rr_abi_version() == 3
+    assert lib.rr_abi_version() == 4
 
 
 @pytest.mark.parametrize("L,seg,T", [(512, 32, 32), (96, 16, 16), (128, 64, 32), (96, 48, 16),
@@ -44,7 +44,7 @@ def test_chunk_len(lib, L, seg, T):
 
 def _call_rglru_fwd(L, D, seg, dtype=0, null=False):
     p = None if null else ctypes.c_void_p(16)  # never dereferenced: validation fails first
-    return _lib.load().rr_rglru_fwd(p, p, dtype, 1, L, D, seg, None, p, p, None)
+    return _lib.load().rr_rglru_fwd(p, p, dtype, 1, L, D, seg, None, p, p, p, 1 << 30, None)
 
 
 def test_rejects_bad_shapes_before_launch(lib):
@@ -73,3 +73,7 @@ def test_ssd_gla_validation(lib):
         rc = lib.rr_ssd_bwd(p, None, p, p, p, p, p, 1, 0, 2, 64, 2, 64, 8, 32, None, p, p, p, p, p, p, None,
                             p, need - 1, None)
         assert rc == _lib.RR_EWORKSPACE
+    need = lib.rr_rglru_workspace_bytes(2, 256, 64, 32, 1, 0)
+    assert need > 0
+    rc = lib.rr_rglru_fwd(p, p, 1, 2, 256, 64, 32, None, p, p, p, need - 1, None)
+    assert rc == _lib.RR_EWORKSPACE
