@@ -174,7 +174,7 @@ def make_ssd(cfg, device, dtype):
 
     return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, tokens=B * L,
                 fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=B * L * H * Dh * N * 4,
-                ckpt_bytes=n_ck * 4)
+                ckpt_bytes=n_ck * 4, io_bytes=n_u * 4 + (n_u + n_d + 2 * n_bc) * es + H * 4)
 
 
 def make_gla(cfg, device, dtype):
@@ -229,7 +229,7 @@ def make_gla(cfg, device, dtype):
 
     return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, tokens=B * L,
                 fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=B * L * H * Dh * Dh * 4,
-                ckpt_bytes=n_ck * 4)
+                ckpt_bytes=n_ck * 4, io_bytes=n_x * 4 + (3 * n_x + n_g) * es)
 
 
 def make_rglru(cfg, device, dtype):
@@ -283,7 +283,8 @@ def make_rglru(cfg, device, dtype):
         orc.rglru_backward(d["dy"][:Bs].double().cpu().numpy(), aa, xx)
 
     return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, tokens=B * L, cpu_tokens=L,
-                fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=n * 4, ckpt_bytes=n_ck * 4)
+                fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=n * 4, ckpt_bytes=n_ck * 4,
+                io_bytes=n * 4 + 2 * n * es)
 
 
 def make_rotlru(cfg, device, dtype):
@@ -336,7 +337,8 @@ def make_rotlru(cfg, device, dtype):
         orc.rotlru_backward(d["dy"][:1].double().cpu().numpy(), *xs)
 
     return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, tokens=B * L, cpu_tokens=L,
-                fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=n_x * 4, ckpt_bytes=n_ck * 4)
+                fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=n_x * 4, ckpt_bytes=n_ck * 4,
+                io_bytes=n_x * 4 + (3 * n_p + n_x) * es)
 
 
 WORKLOADS = {
@@ -438,12 +440,13 @@ def measure(name, steps, warmup, dtype, device, with_cpu):
     torch.cuda.synchronize()
     eager_ms = (time.perf_counter() - e0) * 1e3 / ne
 
-    # transient memory of one eager fwd+bwd (beyond inputs)
+    # transient memory of one eager fwd+bwd: peak allocation beyond the inputs,
+    # minus the outputs and gradients the call returns (y, grads)
     torch.cuda.reset_peak_memory_stats(device)
     base = torch.cuda.memory_allocated(device)
     w["eager"]()
     torch.cuda.synchronize()
-    peak_extra = torch.cuda.max_memory_allocated(device) - base
+    peak_extra = torch.cuda.max_memory_allocated(device) - base - w["io_bytes"]
 
     res = dict(
         workload=desc, cfg=cfg, ms_per_step=ms_step, tokens_per_s=w["tokens"] / (ms_step * 1e-3),
@@ -472,6 +475,148 @@ def measure(name, steps, warmup, dtype, device, with_cpu):
     return res
 
 
+# ------------------------------------------------------------------ HBM traffic
+# roofline.traffic comes from two rocprofv3 counter runs of `--pmc-run`
+# (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the same
+# counter reads for a plain device copy of known size (`--calibrate-copy`).
+# `--pmc-summary DIR` turns those runs into profiles/pmc_traffic.json, which a
+# normal run reads for its dominant kernel.
+PMC_FILE = ROOT / "profiles" / "pmc_traffic.json"
+PROFILE_COMMANDS = [
+    "rocprofv3 --kernel-trace --stats -d $R/gpurun_out/prof_trace -o trace --output-format csv -- "
+    "python3 bench.py --steps 20 --warmup 3 --no-cpu --also gla,rglru,rotlru",
+    "rocprofv3 --pmc FETCH_SIZE -d $R/gpurun_out/pmc/cal_fetch -o cal --output-format csv -- "
+    "python3 bench.py --calibrate-copy 256",
+    "rocprofv3 --pmc WRITE_SIZE -d $R/gpurun_out/pmc/cal_write -o cal --output-format csv -- "
+    "python3 bench.py --calibrate-copy 256",
+    "for w in ssd gla rglru rotlru; do rocprofv3 --pmc FETCH_SIZE -d $R/gpurun_out/pmc/${w}_fetch -o $w "
+    "--output-format csv -- python3 bench.py --pmc-run $w; rocprofv3 --pmc WRITE_SIZE -d "
+    "$R/gpurun_out/pmc/${w}_write -o $w --output-format csv -- python3 bench.py --pmc-run $w; done",
+    "python3 bench.py --pmc-summary --trace-dir gpurun_out/prof_trace",
+]
+
+
+def pmc_run(name, out_dir):
+    """One warm forward + backward of `name`, preceded by two warm-up passes; the
+    kernel counts per pass go to out_dir/<name>_passes.json for the summary."""
+    import torch
+    desc, maker, cfg = WORKLOADS[name]
+    device = torch.device("cuda:0")
+    w = maker(cfg, device, torch.bfloat16)
+    hip = _Hip()
+    stream = torch.cuda.Stream(device)
+    sh = ctypes.c_void_p(stream.cuda_stream)
+    counts = {}
+    with torch.cuda.stream(stream):
+        for pname in ("fwd", "bwd"):
+            g = hip.capture(sh, w[pname])
+            counts[pname] = len(hip.kernel_nodes(g))
+            hip.lib.hipGraphDestroy(g)
+        for _ in range(2):
+            w["fwd"]()
+            w["bwd"]()
+        torch.cuda.synchronize()
+        w["fwd"]()
+        w["bwd"]()
+    torch.cuda.synchronize()
+    pathlib.Path(out_dir).mkdir(parents=True, exist_ok=True)
+    (pathlib.Path(out_dir) / f"{name}_passes.json").write_text(json.dumps(counts))
+
+
+def _counter_rows(run_dir):
+    import csv
+    rows = []
+    for f in sorted(pathlib.Path(run_dir).rglob("*counter_collection.csv")):
+        with open(f) as fh:
+            rows += list(csv.DictReader(fh))
+    return rows
+
+
+def pmc_summary(root):
+    """profiles/pmc_traffic.json from the counter runs under `root`:
+    root/cal_fetch, root/cal_write (calibration copy), root/<w>_fetch,
+    root/<w>_write and root/<w>_passes.json for each workload w."""
+    root = pathlib.Path(root)
+
+    def per_dispatch(run_dir, counter):
+        out = {}
+        for r in _counter_rows(run_dir):
+            if r["Counter_Name"] == counter:
+                d = int(r["Dispatch_Id"])
+                out[d] = (r["Kernel_Name"], out.get(d, ("", 0.0))[1] + float(r["Counter_Value"]))
+        return [out[k] for k in sorted(out)]
+
+    scale = {}
+    for counter, sub_dir, true_kib in (("FETCH_SIZE", "cal_fetch", 256 * 1024), ("WRITE_SIZE", "cal_write", 256 * 1024)):
+        copies = [v for n, v in per_dispatch(root / sub_dir, counter) if "copy" in n.lower()]
+        scale[counter] = true_kib / copies[-1] if copies else None
+    summary = {"scale": scale, "workloads": {}}
+    for w in WORKLOADS:
+        pj = root / f"{w}_passes.json"
+        if not pj.exists():
+            continue
+        counts = json.loads(pj.read_text())
+        fetch = per_dispatch(root / f"{w}_fetch", "FETCH_SIZE")
+        write = per_dispatch(root / f"{w}_write", "WRITE_SIZE")
+        n = counts["fwd"] + counts["bwd"]
+        fetch, write = fetch[-n:], write[-n:]
+        entry = {}
+        for pname, lo, hi in (("fwd", 0, counts["fwd"]), ("bwd", counts["fwd"], n)):
+            entry[pname] = [{"kernel": fetch[i][0],
+                             "fetch_bytes": fetch[i][1] * 1024 * (scale["FETCH_SIZE"] or 1.0),
+                             "write_bytes": write[i][1] * 1024 * (scale["WRITE_SIZE"] or 1.0)}
+                            for i in range(lo, hi)]
+        summary["workloads"][w] = entry
+    PMC_FILE.parent.mkdir(exist_ok=True)
+    PMC_FILE.write_text(json.dumps(summary, indent=1))
+    print(f"wrote {PMC_FILE}")
+    return summary
+
+
+def profile_markdown(summary, trace_dir, out_md, commands):
+    """Kernel durations (rocprofv3 --kernel-trace --stats) and per-dispatch HBM
+    traffic (the counter runs) beside each pass's algorithmic bytes."""
+    import csv
+    import torch
+    lines = ["# Default bench workloads (SSD config 1 headline; GLA config 2; RG-LRU / rotLRU config 3), bf16 inputs",
+             "", "Commands (from the repository root on one MI355X, `export TMPDIR=/tmp`, R = repository root):", ""]
+    lines += ["    " + c for c in commands]
+    lines += ["", "## Kernel durations (`rocprofv3 --kernel-trace --stats`)", "",
+              "| kernel | calls | average µs | min µs | max µs |", "|---|---|---|---|---|"]
+    stats = sorted(pathlib.Path(trace_dir).rglob("*kernel_stats.csv"))
+    if stats:
+        with open(stats[0]) as fh:
+            for r in sorted(csv.DictReader(fh), key=lambda r: -float(r["TotalDurationNs"])):
+                lines.append(f"| `{r['Name'][:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                             f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} |")
+    sc = summary["scale"]
+    lines += ["", "## HBM traffic per dispatch (`--pmc FETCH_SIZE`, `--pmc WRITE_SIZE`)", "",
+              f"Scale factors from a plain 256 MiB device copy (`bench.py --calibrate-copy 256`): FETCH_SIZE "
+              f"x{sc['FETCH_SIZE']:.3f}, WRITE_SIZE x{sc['WRITE_SIZE']:.3f}.  Algorithmic bytes are the pass's "
+              "(inputs, outputs and checkpoints at their API dtypes), all moved by its main kernel; the other "
+              "kernels of a pass move workspace data only.", "",
+              "| workload | pass | kernel | fetch MB | write MB | pass algorithmic MB |", "|---|---|---|---|---|---|"]
+    for wname, entry in summary["workloads"].items():
+        desc, maker, cfg = WORKLOADS[wname]
+        w = maker(cfg, torch.device("cpu"), torch.bfloat16)
+        for pname in ("fwd", "bwd"):
+            alg = w[f"{pname}_bytes"] / 1e6
+            for k in entry[pname]:
+                lines.append(f"| {wname} | {pname} | `{k['kernel'][:70]}` | {k['fetch_bytes'] / 1e6:.3f} | "
+                             f"{k['write_bytes'] / 1e6:.3f} | {alg:.3f} |")
+    pathlib.Path(out_md).write_text("\n".join(lines) + "\n")
+    print(f"wrote {out_md}")
+
+
+def traffic_of(name, dom):
+    """Measured HBM bytes per launch of the dominant kernel, or None."""
+    try:
+        k = json.loads(PMC_FILE.read_text())["workloads"][name][dom["pass"]][dom["index"]]
+        return k["fetch_bytes"] + k["write_bytes"]
+    except (OSError, KeyError, IndexError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -482,7 +627,19 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="only run a plain device-to-device copy of MB megabytes (PMC byte-counter scale)")
+    ap.add_argument("--pmc-run", default=None, metavar="WORKLOAD",
+                    help="only run one warm forward + backward of WORKLOAD (under rocprofv3 --pmc)")
+    ap.add_argument("--pmc-out", default="gpurun_out/pmc", help="directory for --pmc-run / --pmc-summary")
+    ap.add_argument("--pmc-summary", action="store_true",
+                    help="write profiles/pmc_traffic.json (and, with --trace-dir, the markdown summary) from "
+                         "the counter runs under --pmc-out (no GPU)")
+    ap.add_argument("--trace-dir", default=None, help="rocprofv3 --kernel-trace --stats output for --pmc-summary")
     args = ap.parse_args()
+    if args.pmc_summary:
+        summary = pmc_summary(args.pmc_out)
+        if args.trace_dir:
+            profile_markdown(summary, args.trace_dir, ROOT / "profiles" / "bench_default_scans.md", PROFILE_COMMANDS)
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every scan shards by "
@@ -497,6 +654,9 @@ def main():
     torch.cuda.set_device(device)
     dtype = torch.bfloat16
 
+    if args.pmc_run:
+        pmc_run(args.pmc_run, args.pmc_out)
+        return
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20) // 4
         src = torch.randn(n, device=device)
@@ -514,6 +674,7 @@ def main():
         extras[nm] = dict(workload=r["workload"], tokens_per_s=r["tokens_per_s"], ms_per_step=r["ms_per_step"],
                           fwd_us=r["fwd_us"], bwd_us=r["bwd_us"], eager_ms_per_step=r["eager_ms_per_step"],
                           roofline=dict(bound="hbm", achieved=r["achieved_gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
+                                        traffic=traffic_of(nm, r["dominant"]),
                                         frac=r["achieved_gbs"] / HBM_PEAK_GBS, kernel=r["dominant"]),
                           kernels=r["kernels"], peak_transient_bytes=r["peak_transient_bytes"],
                           state_history_bytes=r["state_history_bytes"])
@@ -540,7 +701,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": r["achieved_gbs"] / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": traffic_of(args.workload, r["dominant"]),
             "kernel": r["dominant"],
         },
         "cpu_baseline": r.get("cpu"),
