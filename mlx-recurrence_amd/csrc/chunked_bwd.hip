@@ -1,0 +1,626 @@
+// chunked_bwd.hip — backward of the chunked scans (rr_chunked.h) with the
+// state blocks owned by columns: GLA (any size) and SSD with N >= 64.
+//
+// Per 32-step chunk (reference adjoints ssd.py:203-268, gla.py:184-236 in
+// matrix form), with h_in the state entering the chunk (forward checkpoint),
+// lam the adjoint of the chunk's last state flowing in from later chunks,
+// M[t, s] = dec_{s+1} ... dec_t, gam_t = dec_0 ... dec_t, m31_t = M[31, t],
+// w_t the input weight (SSD delta_t, GLA 1) and rows d / columns n of the
+// state (SSD channel / state, GLA j / i):
+//   CB = C B^T, G2 = dY U^T, GH = dY h_in, UL = U lam, P = M o CB, MG = M o G2
+//   du = diag(w) (P^T dY + diag(m31) B lam^T)
+//   Z  = MG^T C + diag(m31) UL,  dB = diag(w) Z
+//   dC = diag(gam) GH + (MG o w_s) B
+//   Hp_t = sum_{d,n} lam_t h_{t-1}
+//        = sum_{r >= t} M'[r, t] F_t[r],   r = 0..32 (row 32 stands for lam):
+//          M'[r, t] = M[r, t] (r < 32), m31_t (r = 32);
+//          F_0[r] = X_r (r < 32), tr (r = 32);  F_{t+1}[r] = dec_t F_t[r] + E'[r, t];
+//          E'[r, s] = CB[r, s] G2[r, s] w_s (r < 32), Y_s (r = 32);
+//          X = rowsum(GH o C), Y = rowsum(UL o B) o w, tr = sum(lam o h_in)
+//        (division free: zero or negative GLA gates are exact)
+//   GLA: dg_t = Hp_t.
+//   SSD: d(delta)_t = a dec_t Hp_t + sum_n B_t Z_t, and per state n
+//        dA[n] = sum_t C (K B) + sum_t gam cd C GH + sum_t m31 (cd_31 - cd) w B UL
+//                + gam_31 cd_31 sum_d lam h_in,   K = M o w_s o G2 o (cd_t - cd_s)
+//        (cd = in-chunk cumulative delta; from d exp(a (cd_t - cd_s)) / da)
+//   lam_prev = (gam o dY)^T C + gam_31 lam   (adjoint handed to chunk c - 1)
+// (derived from the per-step adjoint; checked against the float64 oracle).
+//
+// Work split (4 waves).  The state tile [d][n] is cut into 16x16 blocks; wave
+// w owns the column blocks nb = w, w + 4, ... (all row blocks db) and holds
+// h_in and lam of those blocks in registers, where a 16x16 accumulator block
+// is directly the B operand of a 16x16x16 MFMA contracting over its rows: so
+// each wave forms GH and UL of its columns in registers and writes dB and dC
+// (and the dA of) those columns.  du row block db goes to wave (db + NBN) % 4.
+//
+// Modes as in the forward: kWhole (a head per workgroup, lam carried in
+// registers from chunk to chunk), kPipe (lam from pass_kernel), kDirect (lam
+// from the direct sum; the workgroup of chunk 0 also forms dh0).
+#include "rr_chunked.h"
+
+namespace {
+
+using rr::bf_split;
+using rr::bf_val;
+using rr::f32x16_t;
+using rr::f32x4_t;
+using rr::frag;
+using rr::frag4;
+using rr::mfma16;
+using rr::mfma16k16;
+using rr::mfma32;
+using rr::u16x4_t;
+using rr::u16x8_t;
+using rr::chunked::kDirect;
+using rr::chunked::kPipe;
+using rr::chunked::kWhole;
+using rr::chunked::PQ;
+using rr::chunked::Q;
+using rr::chunked::r32row;
+
+// LDS of the backward kernel.  The operands that die after phase B1 (x) share
+// space with the masked products written in phase B2 (y).
+template <int DH, int NS, bool GLA>
+struct alignas(16) ColBwdSmem {
+  static constexpr int PD = DH + 8, PN = NS + 8;
+  uint16_t Kn[Q][PN];                      // B [s][n]
+  uint16_t Qn[Q][PN];                      // C [t][n]
+  uint16_t KT[NS][PQ];                     // B^T [n][s]
+  uint16_t QT[NS][PQ];                     // C^T [n][t]
+  uint16_t GYT_hi[DH][PQ], GYT_lo[DH][PQ]; // dY^T [d][t]
+  uint16_t LM_hi[DH][PN], LM_lo[DH][PN];   // lam [d][n]
+  union {
+    struct {                               // phase A -> B1
+      uint16_t V[Q][PD];                       // U [s][d]
+      uint16_t GY_hi[Q][PD], GY_lo[Q][PD];     // dY [t][d]
+    } x;
+    struct {                               // phase B2 -> C
+      uint16_t PT_hi[Q][PQ], PT_lo[Q][PQ];     // P^T        [s][t']
+      uint16_t MGT_hi[Q][PQ], MGT_lo[Q][PQ];   // MG^T       [s][t']
+      uint16_t MG_hi[Q][PQ], MG_lo[Q][PQ];     // MG o w_s   [t'][s]
+      uint16_t Km_hi[GLA ? 1 : Q][PQ];         // SSD: K     [t'][s]
+      uint16_t Km_lo[GLA ? 1 : Q][PQ];
+    } y;
+  };
+  float CB[Q][Q + 1];
+  float G2[Q][Q + 1];
+  float Cc[Q + 1][Q + 1];                  // Hp contributions M'[r, t] F_t[r]
+  float XYp[4][2][Q];                      // per-wave partial X, Y
+  float BZp[GLA ? 1 : 4][Q];               // SSD: per-wave partial sum_n B Z
+  float xin[Q], dec[Q], gam[Q], m31[Q], w[Q], cd[Q], Hp[Q];
+  float trw[4];
+};
+
+template <int DH, int NS, int MODE, bool GLA>
+union ColBwdShared {
+  ColBwdSmem<DH, NS, GLA> m;
+};
+template <int DH, int NS, bool GLA>
+union ColBwdShared<DH, NS, kDirect, GLA> {
+  ColBwdSmem<DH, NS, GLA> m;
+  rr::chunked::DirectSmem<DH, NS, true> d;
+};
+
+template <int DH, int NS, int MODE, bool GLA>
+__global__ __launch_bounds__(256, 2) void col_bwd_kernel(rr::ChunkArgs p) {
+  constexpr int NBN = NS / 16, NBD = DH / 16;
+  constexpr int CPW = (NBN + 3) / 4;   // column blocks per wave
+  __shared__ ColBwdShared<DH, NS, MODE, GLA> smu;
+  auto& m = smu.m;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int h, b, cbeg, cend;
+  if constexpr (MODE == kWhole) {
+    h = blockIdx.y, b = blockIdx.z, cbeg = 0, cend = p.nC;
+  } else {
+    const rr::chunked::ChunkId id = rr::chunked::chunk_id(p, false);
+    if (!id.valid) return;
+    h = id.h, b = id.b, cbeg = id.c, cend = id.c + 1;
+  }
+  const float a = rr::chunked::head_rate<GLA>(p, h);
+  const int64_t bh = (int64_t)b * p.H + h;
+  const int rsD = p.H * DH, rsN = p.H * NS;   // step strides (elements) of [.., H, DH] / [.., H, NS]
+  const int l15 = lane & 15, l4 = lane >> 4;
+
+  f32x4_t lam[CPW][NBD];
+#pragma unroll
+  for (int cc = 0; cc < CPW; ++cc)
+#pragma unroll
+    for (int db = 0; db < NBD; ++db) lam[cc][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if constexpr (MODE == kDirect) {
+    const float gam_all = rr::chunked::direct_sum<DH, NS, GLA, true>(p, cbeg, b, h, a, smu.d);
+    const float* dfb = p.dfinal != nullptr ? p.dfinal + bh * DH * NS : nullptr;
+#pragma unroll
+    for (int cc = 0; cc < CPW; ++cc) {
+      const int nb = w + 4 * cc;
+      if (nb < NBN) {
+#pragma unroll
+        for (int db = 0; db < NBD; ++db)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            lam[cc][db][r] = rr::chunked::direct_value<DH, NS, GLA, true>(smu.d, gam_all, dfb, 16 * db + 4 * l4 + r,
+                                                                         16 * nb + l15);
+      }
+    }
+    __syncthreads();   // the chunk below reuses the LDS of the sum
+  } else if constexpr (MODE == kWhole) {
+    if (p.dfinal != nullptr) {
+#pragma unroll
+      for (int cc = 0; cc < CPW; ++cc) {
+        const int nb = w + 4 * cc;
+        if (nb < NBN) {
+#pragma unroll
+          for (int db = 0; db < NBD; ++db)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              lam[cc][db][r] = p.dfinal[bh * DH * NS +
+                                        rr::chunked::state_off<GLA, DH, NS>(16 * db + 4 * l4 + r, 16 * nb + l15)];
+        }
+      }
+    }
+  }
+  // the adjoint handed to chunk c - 1 is needed for the whole head, and for dh0
+  const bool carry = MODE == kWhole || (MODE == kDirect && cbeg == 0 && p.dh0 != nullptr);
+  float dA_acc[CPW];   // SSD: dA of this lane's column (every l4 group holds the same sum)
+#pragma unroll
+  for (int cc = 0; cc < CPW; ++cc) dA_acc[cc] = 0.f;
+
+  for (int c = cend - 1; c >= cbeg; --c) {
+    // a fresh copy of the thread index per chunk keeps the compiler from
+    // hoisting every per-lane LDS / global address of the body out of the loop
+    int tidv = tid;
+    asm volatile("" : "+v"(tidv));
+    const int lane = tidv & 63, l15 = lane & 15, l4 = lane >> 4, tid = tidv;
+    const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;   // first (b, t) row of the chunk
+    const int64_t baseD = (row0 * p.H + h) * DH, baseN = (row0 * p.H + h) * NS, baseX = row0 * p.H + h;
+    f32x4_t hin[CPW][NBD];
+    float trn[CPW];   // SSD: sum over this lane's rows of lam o h_in, per column
+    // ------------------------------------------------ A: stage (all loads first)
+    {
+      constexpr int UV = (Q * DH / 8 + 255) / 256, NV = (Q * NS / 8 + 255) / 256, GV = (Q * DH / 4 + 255) / 256;
+      u16x8_t uv[UV], bv[NV], cv[NV];
+      float4 gv[GV];
+      float xv = GLA ? 1.f : 0.f;
+#pragma unroll
+      for (int v = 0; v < UV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
+        uv[v] = i < Q * DH / 8 ? *reinterpret_cast<const u16x8_t*>(p.u + baseD + tl * rsD + d0) : u16x8_t{};
+      }
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+        const bool ok = i < Q * NS / 8;
+        bv[v] = ok ? *reinterpret_cast<const u16x8_t*>(p.Bm + baseN + tl * rsN + n0) : u16x8_t{};
+        cv[v] = ok ? *reinterpret_cast<const u16x8_t*>(p.Cm + baseN + tl * rsN + n0) : u16x8_t{};
+      }
+#pragma unroll
+      for (int v = 0; v < GV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (DH / 4)) & (Q - 1), d0 = 4 * (i % (DH / 4));
+        gv[v] = i < Q * DH / 4 ? *reinterpret_cast<const float4*>(p.dy + baseD + tl * rsD + d0)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      if (tid < Q) xv = bf_val(p.delta[baseX + tid * p.H]);
+      const float* hsrc = c > 0 ? p.ckpt + (bh * p.nC + c - 1) * DH * NS
+                                : (p.h0 != nullptr ? p.h0 + bh * DH * NS : nullptr);
+      const float* lsrc = MODE == kPipe ? p.agg + (bh * p.nC + c) * DH * NS : nullptr;
+#pragma unroll
+      for (int cc = 0; cc < CPW; ++cc) {
+        const int nb = w + 4 * cc;
+#pragma unroll
+        for (int db = 0; db < NBD; ++db) {
+          if constexpr (MODE == kPipe) lam[cc][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          hin[cc][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          if (nb < NBN) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int d = 16 * db + 4 * l4 + r, n = 16 * nb + l15;
+              if constexpr (MODE == kPipe) lam[cc][db][r] = lsrc[d * NS + n];
+              if (hsrc != nullptr)
+                hin[cc][db][r] = hsrc[c > 0 ? d * NS + n : rr::chunked::state_off<GLA, DH, NS>(d, n)];
+            }
+          }
+        }
+      }
+      // LDS writes
+#pragma unroll
+      for (int v = 0; v < UV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
+        if (i < Q * DH / 8) *reinterpret_cast<u16x8_t*>(&m.x.V[tl][d0]) = uv[v];
+      }
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+        if (i < Q * NS / 8) {
+          *reinterpret_cast<u16x8_t*>(&m.Kn[tl][n0]) = bv[v];
+          *reinterpret_cast<u16x8_t*>(&m.Qn[tl][n0]) = cv[v];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            m.KT[n0 + e][tl] = bv[v][e];
+            m.QT[n0 + e][tl] = cv[v][e];
+          }
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < GV; ++v) {
+        const int i = tid + 256 * v, tl = (i / (DH / 4)) & (Q - 1), d0 = 4 * (i % (DH / 4));
+        if (i < Q * DH / 4) {
+          const float g4[4] = {gv[v].x, gv[v].y, gv[v].z, gv[v].w};
+          u16x4_t hi4, lo4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            uint16_t hi, lo;
+            bf_split(g4[e], hi, lo);
+            hi4[e] = hi;
+            lo4[e] = lo;
+            m.GYT_hi[d0 + e][tl] = hi;
+            m.GYT_lo[d0 + e][tl] = lo;
+          }
+          *reinterpret_cast<u16x4_t*>(&m.x.GY_hi[tl][d0]) = hi4;
+          *reinterpret_cast<u16x4_t*>(&m.x.GY_lo[tl][d0]) = lo4;
+        }
+      }
+      if (w == 0) {
+        const rr::chunked::StepScalars sc = rr::chunked::step_scalars<GLA>(xv, a, lane);
+        if (lane < Q) {
+          m.xin[lane] = xv;
+          m.dec[lane] = GLA ? xv : __expf(a * xv);
+          m.gam[lane] = sc.gam;
+          m.m31[lane] = sc.m31;
+          m.w[lane] = sc.w;
+          m.cd[lane] = sc.cd;
+        }
+      }
+      float part = 0.f;
+#pragma unroll
+      for (int cc = 0; cc < CPW; ++cc) {
+        const int nb = w + 4 * cc;
+        trn[cc] = 0.f;
+        if (nb < NBN) {
+#pragma unroll
+          for (int db = 0; db < NBD; ++db) {
+            u16x4_t hi4, lo4;
+            rr::bf_split4(lam[cc][db], hi4, lo4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int d = 16 * db + 4 * l4 + r, n = 16 * nb + l15;
+              m.LM_hi[d][n] = hi4[r];
+              m.LM_lo[d][n] = lo4[r];
+              trn[cc] += lam[cc][db][r] * hin[cc][db][r];
+            }
+          }
+        }
+        part += trn[cc];
+        trn[cc] += __shfl_xor(trn[cc], 16);
+        trn[cc] += __shfl_xor(trn[cc], 32);
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o);
+      if (lane == 0) m.trw[w] = part;
+    }
+    __syncthreads();
+    // ------------------------------------------------ B1: GH, UL (registers), CB, G2 (32x32)
+    f32x4_t gh[CPW][2], ul[CPW][2];
+#pragma unroll
+    for (int cc = 0; cc < CPW; ++cc) {
+      const int nb = w + 4 * cc;
+      float xp[2][4] = {}, yp[2][4] = {};
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) {
+        gh[cc][tb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        ul[cc][tb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        if (nb < NBN) {
+#pragma unroll
+          for (int db = 0; db < NBD; ++db) {
+            const int row = 16 * tb + l15, k0 = 16 * db + 4 * l4;
+            const u16x4_t ah = frag4(&m.x.GY_hi[row][k0]), al = frag4(&m.x.GY_lo[row][k0]);
+            const u16x4_t av = frag4(&m.x.V[row][k0]);
+            u16x4_t hh, hl, lh, ll;
+            rr::bf_split4(hin[cc][db], hh, hl);
+            rr::bf_split4(lam[cc][db], lh, ll);
+            gh[cc][tb] = mfma16k16(ah, hh, gh[cc][tb]);
+            gh[cc][tb] = mfma16k16(ah, hl, gh[cc][tb]);
+            gh[cc][tb] = mfma16k16(al, hh, gh[cc][tb]);
+            ul[cc][tb] = mfma16k16(av, lh, ul[cc][tb]);
+            ul[cc][tb] = mfma16k16(av, ll, ul[cc][tb]);
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = 16 * tb + 4 * l4 + r, n = 16 * nb + l15;
+            xp[tb][r] = gh[cc][tb][r] * bf_val(m.Qn[t][n]);
+            yp[tb][r] = ul[cc][tb][r] * bf_val(m.Kn[t][n]);
+          }
+        }
+      }
+      // X, Y partials of this wave's columns: sum over the 16 lanes of a row group
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+          for (int o = 1; o < 16; o <<= 1) {
+            xp[tb][r] += __shfl_xor(xp[tb][r], o);
+            yp[tb][r] += __shfl_xor(yp[tb][r], o);
+          }
+          if (l15 == 0) {
+            const int t = 16 * tb + 4 * l4 + r;
+            m.XYp[w][0][t] = (cc == 0 ? 0.f : m.XYp[w][0][t]) + xp[tb][r];
+            m.XYp[w][1][t] = (cc == 0 ? 0.f : m.XYp[w][1][t]) + yp[tb][r];
+          }
+        }
+      }
+    }
+    f32x16_t cg = {};   // wave 0: CB = C B^T; wave 1: G2 = dY U^T
+    if (w == 0) {
+#pragma unroll
+      for (int kb = 0; kb < NS / 16; ++kb)
+        cg = mfma32(frag(&m.Qn[lane & 31][16 * kb + 8 * (lane >> 5)]),
+                    frag(&m.Kn[lane & 31][16 * kb + 8 * (lane >> 5)]), cg);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) m.CB[r32row(r, lane)][lane & 31] = cg[r];
+    } else if (w == 1) {
+#pragma unroll
+      for (int kb = 0; kb < DH / 16; ++kb) {
+        const u16x8_t fb = frag(&m.x.V[lane & 31][16 * kb + 8 * (lane >> 5)]);
+        cg = mfma32(frag(&m.x.GY_hi[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, cg);
+        cg = mfma32(frag(&m.x.GY_lo[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, cg);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) m.G2[r32row(r, lane)][lane & 31] = cg[r];
+    }
+    __syncthreads();
+    // ------------------------------------------------ B2: masked products; Hp
+    if (w != 2) {
+      // wave 0: P^T (CB registers); wave 1: MG^T (G2 registers); wave 3: MG o w_s
+      // and, for SSD, K (G2 from LDS)
+      float md[16];
+      rr::chunked::decay_block32<GLA>(GLA ? m.xin : m.cd, a, lane, md);
+      const int s = lane & 31;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int tp = r32row(r, lane);
+        uint16_t hi, lo;
+        if (w == 0) {
+          bf_split(md[r] * cg[r], hi, lo);
+          m.y.PT_hi[s][tp] = hi;
+          m.y.PT_lo[s][tp] = lo;
+        } else if (w == 1) {
+          bf_split(md[r] * cg[r], hi, lo);
+          m.y.MGT_hi[s][tp] = hi;
+          m.y.MGT_lo[s][tp] = lo;
+        } else {
+          const float mgw = md[r] * m.G2[tp][s] * m.w[s];
+          bf_split(mgw, hi, lo);
+          m.y.MG_hi[tp][s] = hi;
+          m.y.MG_lo[tp][s] = lo;
+          if constexpr (!GLA) {
+            bf_split(mgw * (m.cd[tp] - m.cd[s]), hi, lo);
+            m.y.Km_hi[tp][s] = hi;
+            m.y.Km_lo[tp][s] = lo;
+          }
+        }
+      }
+    } else {
+      if (lane <= Q) {
+        const int row = lane;
+        float e[Q], fv[Q];
+        float f;
+        if (row < Q) {
+          f = m.XYp[0][0][row] + m.XYp[1][0][row] + m.XYp[2][0][row] + m.XYp[3][0][row];
+#pragma unroll
+          for (int s = 0; s < Q; ++s) e[s] = s < row ? m.CB[row][s] * m.G2[row][s] * m.w[s] : 0.f;
+        } else {
+          f = m.trw[0] + m.trw[1] + m.trw[2] + m.trw[3];
+#pragma unroll
+          for (int s = 0; s < Q; ++s)
+            e[s] = (m.XYp[0][1][s] + m.XYp[1][1][s] + m.XYp[2][1][s] + m.XYp[3][1][s]) * m.w[s];
+        }
+#pragma unroll
+        for (int t = 0; t < Q; ++t) {
+          fv[t] = f;
+          f = m.dec[t] * f + e[t];
+        }
+        const int tmax = row < Q ? row : Q - 1;
+        float mm = 1.f;
+#pragma unroll
+        for (int t = Q - 1; t >= 0; --t) {
+          const bool act = t <= tmax;
+          m.Cc[row][t] = act ? mm * fv[t] : 0.f;
+          if (act) mm *= m.dec[t];
+        }
+      }
+      rr::wave_lds_sync();
+      if (lane < Q) {
+        float hp = 0.f;
+#pragma unroll
+        for (int r = 0; r <= Q; ++r) hp += m.Cc[r][lane];
+        if constexpr (GLA) rr::st_bf16(p.ddelta, baseX + lane * p.H, hp);
+        else m.Hp[lane] = hp;
+      }
+    }
+    __syncthreads();
+    // ------------------------------------------------ C: du, dB, dC (+ SSD dA terms, lam_prev)
+#pragma unroll
+    for (int db = 0; db < NBD; ++db) {
+      if ((db + NBN) % 4 != w) continue;
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) {
+        f32x4_t a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
+        {
+          const int k0 = 8 * l4;
+          const u16x8_t ph = frag(&m.y.PT_hi[16 * tb + l15][k0]), pl = frag(&m.y.PT_lo[16 * tb + l15][k0]);
+          const u16x8_t gh8 = frag(&m.GYT_hi[16 * db + l15][k0]), gl8 = frag(&m.GYT_lo[16 * db + l15][k0]);
+          a1 = mfma16(ph, gh8, a1);
+          a1 = mfma16(ph, gl8, a1);
+          a1 = mfma16(pl, gh8, a1);
+        }
+#pragma unroll
+        for (int kk = 0; kk < NS / 32; ++kk) {
+          const int k0 = 32 * kk + 8 * l4;
+          const u16x8_t fa = frag(&m.Kn[16 * tb + l15][k0]);
+          a2 = mfma16(fa, frag(&m.LM_hi[16 * db + l15][k0]), a2);
+          a2 = mfma16(fa, frag(&m.LM_lo[16 * db + l15][k0]), a2);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * tb + 4 * l4 + r;
+          rr::st_bf16(p.du, baseD + t * rsD + 16 * db + l15, m.w[t] * (a1[r] + m.m31[t] * a2[r]));
+        }
+      }
+    }
+    float bz[2][4] = {};
+    const float cd31 = m.cd[Q - 1], gam31 = m.gam[Q - 1];
+#pragma unroll
+    for (int cc = 0; cc < CPW; ++cc) {
+      const int nb = w + 4 * cc;
+      if (nb >= NBN) continue;
+      float dAp = 0.f;
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) {
+        const int row = 16 * tb + l15, k0 = 8 * l4;
+        f32x4_t ak = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f}, akb = {0.f, 0.f, 0.f, 0.f};
+        const u16x8_t fq = frag(&m.QT[16 * nb + l15][k0]);
+        ak = mfma16(frag(&m.y.MGT_hi[row][k0]), fq, ak);
+        ak = mfma16(frag(&m.y.MGT_lo[row][k0]), fq, ak);
+        const u16x8_t fk = frag(&m.KT[16 * nb + l15][k0]);
+        aq = mfma16(frag(&m.y.MG_hi[row][k0]), fk, aq);
+        aq = mfma16(frag(&m.y.MG_lo[row][k0]), fk, aq);
+        if constexpr (!GLA) {
+          akb = mfma16(frag(&m.y.Km_hi[row][k0]), fk, akb);
+          akb = mfma16(frag(&m.y.Km_lo[row][k0]), fk, akb);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * tb + 4 * l4 + r, n = 16 * nb + l15;
+          const int64_t gi = baseN + t * rsN + n;
+          const float z = ak[r] + m.m31[t] * ul[cc][tb][r];
+          rr::st_bf16(p.dB, gi, m.w[t] * z);
+          rr::st_bf16(p.dC, gi, m.gam[t] * gh[cc][tb][r] + aq[r]);
+          if constexpr (!GLA) {
+            const float bv = bf_val(m.Kn[t][n]), cv = bf_val(m.Qn[t][n]);
+            bz[tb][r] += bv * z;
+            dAp += cv * (akb[r] + m.gam[t] * m.cd[t] * gh[cc][tb][r]) +
+                   m.m31[t] * (cd31 - m.cd[t]) * m.w[t] * bv * ul[cc][tb][r];
+          }
+        }
+      }
+      if constexpr (!GLA) {
+        dAp += __shfl_xor(dAp, 16);
+        dAp += __shfl_xor(dAp, 32);
+        dA_acc[cc] += dAp + gam31 * cd31 * trn[cc];
+      }
+    }
+    if constexpr (!GLA) {
+      // sum_n B Z of this wave's columns
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+          for (int o = 1; o < 16; o <<= 1) bz[tb][r] += __shfl_xor(bz[tb][r], o);
+          if (l15 == 0) m.BZp[w][16 * tb + 4 * l4 + r] = bz[tb][r];
+        }
+      }
+    }
+    if (carry) {
+      // lam_prev = (gam o dY)^T C + gam_31 lam, blocks of this wave's columns
+#pragma unroll
+      for (int cc = 0; cc < CPW; ++cc) {
+        const int nb = w + 4 * cc;
+        if (nb >= NBN) continue;
+        const int k0 = 8 * l4;
+        const u16x8_t qf = frag(&m.QT[16 * nb + l15][k0]);
+        u16x8_t qh, ql;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          uint16_t hi, lo;
+          bf_split(m.gam[k0 + e] * bf_val(qf[e]), hi, lo);
+          qh[e] = hi;
+          ql[e] = lo;
+        }
+#pragma unroll
+        for (int db = 0; db < NBD; ++db) {
+          const u16x8_t ah = frag(&m.GYT_hi[16 * db + l15][k0]), al = frag(&m.GYT_lo[16 * db + l15][k0]);
+          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+          acc = mfma16(ah, qh, acc);
+          acc = mfma16(ah, ql, acc);
+          acc = mfma16(al, qh, acc);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) lam[cc][db][r] = acc[r] + gam31 * lam[cc][db][r];
+        }
+      }
+    }
+    if constexpr (!GLA) {
+      __syncthreads();
+      if (w == 0 && lane < Q) {
+        const float bzt = m.BZp[0][lane] + m.BZp[1][lane] + m.BZp[2][lane] + m.BZp[3][lane];
+        rr::st_bf16(p.ddelta, baseX + lane * p.H, a * m.dec[lane] * m.Hp[lane] + bzt);
+      }
+    }
+    if (MODE == kWhole) __syncthreads();   // the next chunk rewrites the LDS
+  }
+  if constexpr (!GLA) {
+    // per-run dA partial of this lane's column
+    const int nR = MODE == kWhole ? 1 : p.nC;
+    const int run = MODE == kWhole ? 0 : cbeg;
+#pragma unroll
+    for (int cc = 0; cc < CPW; ++cc) {
+      const int nb = w + 4 * cc;
+      if (nb < NBN && l4 == 0) p.ws[(bh * nR + run) * NS + 16 * nb + l15] = dA_acc[cc];
+    }
+  }
+  if (carry && p.dh0 != nullptr) {
+#pragma unroll
+    for (int cc = 0; cc < CPW; ++cc) {
+      const int nb = w + 4 * cc;
+      if (nb >= NBN) continue;
+#pragma unroll
+      for (int db = 0; db < NBD; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          p.dh0[bh * DH * NS + rr::chunked::state_off<GLA, DH, NS>(16 * db + 4 * l4 + r, 16 * nb + l15)] =
+              lam[cc][db][r];
+    }
+  }
+}
+
+template <int DH, int NS, bool GLA>
+int launch(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
+  if (p.mode == kPipe) {
+    hipLaunchKernelGGL((rr::chunked::agg_kernel<DH, NS, GLA>), rr::chunked::chunk_grid(p), dim3(64), 0, s, p, 1);
+    if (int rc = rr::check_launch("chunked backward aggregates")) return rc;
+    hipLaunchKernelGGL((rr::chunked::pass_kernel<DH, NS, GLA>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0,
+                       s, p, 1);
+    if (int rc = rr::check_launch("chunked backward adjoint pass")) return rc;
+    hipLaunchKernelGGL((col_bwd_kernel<DH, NS, kPipe, GLA>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
+  } else if (p.mode == kDirect) {
+    if constexpr (DH * NS <= rr::chunked::kDirectMaxState)
+      hipLaunchKernelGGL((col_bwd_kernel<DH, NS, kDirect, GLA>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
+    else
+      return rr::fail(RR_EUNSUPPORTED, "chunked backward: state too large for the direct mode");
+  } else {
+    hipLaunchKernelGGL((col_bwd_kernel<DH, NS, kWhole, GLA>), dim3(1, p.H, (unsigned)B), dim3(256), 0, s, p);
+  }
+  return rr::check_launch("chunked backward");
+}
+
+}  // namespace
+
+namespace rr {
+
+int chunked_bwd_cols(const ChunkArgs& p, int64_t B, hipStream_t s, bool gla) {
+  if (gla) {
+    switch (p.DH) {
+      case 32: return launch<32, 32, true>(p, B, s);
+      case 64: return launch<64, 64, true>(p, B, s);
+      default: return fail(RR_EUNSUPPORTED, "gla chunked backward: unsupported Dh");
+    }
+  }
+  switch (p.DH * 1000 + p.NS) {
+    case 32064: return launch<32, 64, false>(p, B, s);
+    case 32128: return launch<32, 128, false>(p, B, s);
+    case 64064: return launch<64, 64, false>(p, B, s);
+    case 64128: return launch<64, 128, false>(p, B, s);
+    default: return fail(RR_EUNSUPPORTED, "ssd chunked backward: unsupported (Dh, N)");
+  }
+}
+
+}  // namespace rr

@@ -49,8 +49,7 @@ int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N);
 // N in {16, 32, 64, 128}.
 bool ssd2_supported(int dtype, int64_t L, int64_t seg, int64_t Dh, int64_t N, int64_t A_stride_n);
 int ssd2_fwd(const ChunkArgs& p, int64_t B, hipStream_t s);
-// The chunked backward covers Dh in {32, 64} and N in {16, 32} (on top of
-// ssd2_supported).
+// The chunked backward covers Dh in {32, 64} (on top of ssd2_supported).
 bool ssd2_bwd_supported(int64_t Dh, int64_t N);
 // Workspace of the chunked passes: chunk decays and (backward) chunk adjoints
 // in the pipelined mode, plus dA partials (pass 1).
@@ -72,5 +71,10 @@ size_t gla2_ws_bytes(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass);
 void gla2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass);
 int gla2_fwd(const ChunkArgs& p, int64_t B, hipStream_t s);
 int gla2_bwd(const ChunkArgs& p, int64_t B, hipStream_t s);
+
+// Backward of the chunked kernels with column-owned state blocks (GLA: Dh in
+// {32, 64}; SSD: Dh in {32, 64}, N in {64, 128}; chunked_bwd.hip).  SSD
+// leaves per-run dA partials in p.ws for the caller's reduction.
+int chunked_bwd_cols(const ChunkArgs& p, int64_t B, hipStream_t s, bool gla);
 
 }  // namespace rr

@@ -644,9 +644,14 @@ __global__ __launch_bounds__(256) void ssd2_dA_kernel(const float* __restrict__ 
   }
 }
 
+int launch_dA(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
+  const int nR = p.mode == kWhole ? 1 : p.nC;
+  hipLaunchKernelGGL(ssd2_dA_kernel, dim3(p.H), dim3(256), 0, s, p.ws, p.dA, (int)B, p.H, nR, p.NS);
+  return rr::check_launch("ssd chunked backward dA");
+}
+
 template <int DH, int NS>
 int launch_bwd(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
-  const int nR = (p.nC + p.R - 1) / p.R;
   if (p.mode == kPipe) {   // R == 1
     hipLaunchKernelGGL((rr::chunked::agg_kernel<DH, NS, false>), rr::chunked::chunk_grid(p), dim3(64), 0, s, p, 1);
     if (int rc = rr::check_launch("ssd chunked backward aggregates")) return rc;
@@ -663,8 +668,7 @@ int launch_bwd(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
     hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, kWhole>), dim3(1, p.H, (unsigned)B), dim3(256), 0, s, p);
   }
   if (int rc = rr::check_launch("ssd chunked backward")) return rc;
-  hipLaunchKernelGGL(ssd2_dA_kernel, dim3(p.H), dim3(256), 0, s, p.ws, p.dA, (int)B, p.H, nR, p.NS);
-  return rr::check_launch("ssd chunked backward dA");
+  return launch_dA(p, B, s);
 }
 
 }  // namespace
@@ -672,7 +676,7 @@ int launch_bwd(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
 namespace rr {
 
 bool ssd2_bwd_supported(int64_t Dh, int64_t N) {
-  return (Dh == 32 || Dh == 64) && (N == 16 || N == 32);
+  return (Dh == 32 || Dh == 64) && (N == 16 || N == 32 || N == 64 || N == 128);
 }
 
 int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N) {
@@ -718,6 +722,9 @@ int ssd2_bwd(const ChunkArgs& p, int64_t B, hipStream_t s) {
     case 32032: return launch_bwd<32, 32>(p, B, s);
     case 64016: return launch_bwd<64, 16>(p, B, s);
     case 64032: return launch_bwd<64, 32>(p, B, s);
+    case 32064: case 32128: case 64064: case 64128:
+      if (int rc = chunked_bwd_cols(p, B, s, false)) return rc;
+      return launch_dA(p, B, s);
     default: return fail(RR_EUNSUPPORTED, "ssd chunked backward: unsupported (Dh, N)");
   }
 }

@@ -206,6 +206,13 @@ SSD_CASES = [
     # more than 16 chunks: pipelined mode (aggregate, state-pass and chunk kernels)
     (1, 1024, 3, 64, 16, 32, BF16, "cfg", True, True, 26),
     (2, 640, 2, 32, 32, 32, BF16, "cfg", False, True, 27),
+    # N = 64, 128: column-owned backward, in its three modes
+    (1, 128, 2, 64, 64, 32, BF16, "cfg", True, True, 30),    # direct (4 chunks)
+    (2, 96, 3, 32, 128, 32, BF16, "cfg", True, False, 31),   # direct (3 chunks)
+    (2, 320, 2, 32, 64, 32, BF16, "cfg", True, True, 32),    # pipelined (10 chunks)
+    (1, 192, 3, 64, 128, 32, BF16, "cfg", False, True, 33),  # pipelined
+    (1, 64, 512, 32, 64, 32, BF16, "cfg", True, True, 34),   # whole head
+    (2, 96, 256, 64, 128, 32, BF16, "cfg", True, True, 35),  # whole head, config 4's tile
 ]
 
 
