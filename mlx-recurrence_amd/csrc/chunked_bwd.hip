@@ -19,7 +19,10 @@
 //          X = rowsum(GH o C), Y = rowsum(UL o B) o w, tr = sum(lam o h_in)
 //        (division free: zero or negative GLA gates are exact)
 //   GLA: dg_t = Hp_t.
-//   SSD: d(delta)_t = a dec_t Hp_t + sum_n B_t Z_t, and per state n
+//   SSD: d(delta)_t = a dec_t Hp_t + sum_n B_t Z_t = a T_t + (1 - a delta_t) sum_n B_t Z_t
+//        with T_t = sum_{d,n} lam_t h_t = R_t + sum_{t' >= t} gam X + sum_{s <= t} m31 w Y
+//        + m31_t gam_t tr,  R_t = sum_{t' >= t, s <= t} (M o w_s o G2 o CB)[t', s]
+//        (h_t and lam_t both expand without dividing by a decay), and per state n
 //        dA[n] = sum_t C (K B) + sum_t gam cd C GH + sum_t m31 (cd_31 - cd) w B UL
 //                + gam_31 cd_31 sum_d lam h_in,   K = M o w_s o G2 o (cd_t - cd_s)
 //        (cd = in-chunk cumulative delta; from d exp(a (cd_t - cd_s)) / da)
@@ -84,10 +87,12 @@ struct alignas(16) ColBwdSmem {
   };
   float CB[Q][Q + 1];
   float G2[Q][Q + 1];
-  float Cc[Q + 1][Q + 1];                  // Hp contributions M'[r, t] F_t[r]
+  float Cc[GLA ? Q + 1 : 1][Q + 1];        // GLA: dg contributions M'[r, t] F_t[r]
   float XYp[4][2][Q];                      // per-wave partial X, Y
   float BZp[GLA ? 1 : 4][Q];               // SSD: per-wave partial sum_n B Z
-  float xin[Q], dec[Q], gam[Q], m31[Q], w[Q], cd[Q], Hp[Q];
+  float xin[Q], dec[Q], gam[Q], m31[Q], w[Q], cd[Q];
+  float HT[Q];                             // SSD: T_t = sum lam_t h_t
+  float Ts[GLA ? 1 : 2][Q];                // SSD: suffix of gam X, prefix of m31 w Y
   float trw[4];
 };
 
@@ -101,8 +106,12 @@ union ColBwdShared<DH, NS, kDirect, GLA> {
   rr::chunked::DirectSmem<DH, NS, true> d;
 };
 
+// Two workgroups per CU where the LDS allows it.
 template <int DH, int NS, int MODE, bool GLA>
-__global__ __launch_bounds__(256, 2) void col_bwd_kernel(rr::ChunkArgs p) {
+constexpr int kColBwdWgs = sizeof(ColBwdShared<DH, NS, MODE, GLA>) <= 80 * 1024 ? 2 : 1;
+
+template <int DH, int NS, int MODE, bool GLA>
+__global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_kernel(rr::ChunkArgs p) {
   constexpr int NBN = NS / 16, NBD = DH / 16;
   constexpr int CPW = (NBN + 3) / 4;   // column blocks per wave
   __shared__ ColBwdShared<DH, NS, MODE, GLA> smu;
@@ -289,65 +298,59 @@ __global__ __launch_bounds__(256, 2) void col_bwd_kernel(rr::ChunkArgs p) {
           }
         }
         part += trn[cc];
-        trn[cc] += __shfl_xor(trn[cc], 16);
-        trn[cc] += __shfl_xor(trn[cc], 32);
+        trn[cc] = rr::rows4_sum(trn[cc]);
       }
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o);
+      part = rr::wave_sum(part);
       if (lane == 0) m.trw[w] = part;
     }
     __syncthreads();
     // ------------------------------------------------ B1: GH, UL (registers), CB, G2 (32x32)
     f32x4_t gh[CPW][2], ul[CPW][2];
+    float xs[2][4] = {}, ys[2][4] = {};   // this lane's shares of the row sums X, Y
 #pragma unroll
     for (int cc = 0; cc < CPW; ++cc) {
       const int nb = w + 4 * cc;
-      float xp[2][4] = {}, yp[2][4] = {};
 #pragma unroll
-      for (int tb = 0; tb < 2; ++tb) {
-        gh[cc][tb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        ul[cc][tb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        if (nb < NBN) {
+      for (int tb = 0; tb < 2; ++tb) gh[cc][tb] = ul[cc][tb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if (nb >= NBN) continue;
 #pragma unroll
-          for (int db = 0; db < NBD; ++db) {
-            const int row = 16 * tb + l15, k0 = 16 * db + 4 * l4;
-            const u16x4_t ah = frag4(&m.x.GY_hi[row][k0]), al = frag4(&m.x.GY_lo[row][k0]);
-            const u16x4_t av = frag4(&m.x.V[row][k0]);
-            u16x4_t hh, hl, lh, ll;
-            rr::bf_split4(hin[cc][db], hh, hl);
-            rr::bf_split4(lam[cc][db], lh, ll);
-            gh[cc][tb] = mfma16k16(ah, hh, gh[cc][tb]);
-            gh[cc][tb] = mfma16k16(ah, hl, gh[cc][tb]);
-            gh[cc][tb] = mfma16k16(al, hh, gh[cc][tb]);
-            ul[cc][tb] = mfma16k16(av, lh, ul[cc][tb]);
-            ul[cc][tb] = mfma16k16(av, ll, ul[cc][tb]);
-          }
+      for (int db = 0; db < NBD; ++db) {
+        u16x4_t hh, hl, lh, ll;
+        rr::bf_split4(hin[cc][db], hh, hl);
+        rr::bf_split4(lam[cc][db], lh, ll);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int t = 16 * tb + 4 * l4 + r, n = 16 * nb + l15;
-            xp[tb][r] = gh[cc][tb][r] * bf_val(m.Qn[t][n]);
-            yp[tb][r] = ul[cc][tb][r] * bf_val(m.Kn[t][n]);
-          }
+        for (int tb = 0; tb < 2; ++tb) {
+          const int row = 16 * tb + l15, k0 = 16 * db + 4 * l4;
+          const u16x4_t ah = frag4(&m.x.GY_hi[row][k0]), al = frag4(&m.x.GY_lo[row][k0]);
+          const u16x4_t av = frag4(&m.x.V[row][k0]);
+          gh[cc][tb] = mfma16k16(ah, hh, gh[cc][tb]);
+          gh[cc][tb] = mfma16k16(ah, hl, gh[cc][tb]);
+          gh[cc][tb] = mfma16k16(al, hh, gh[cc][tb]);
+          ul[cc][tb] = mfma16k16(av, lh, ul[cc][tb]);
+          ul[cc][tb] = mfma16k16(av, ll, ul[cc][tb]);
         }
       }
-      // X, Y partials of this wave's columns: sum over the 16 lanes of a row group
 #pragma unroll
-      for (int tb = 0; tb < 2; ++tb) {
+      for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
+          const int t = 16 * tb + 4 * l4 + r, n = 16 * nb + l15;
+          xs[tb][r] += gh[cc][tb][r] * bf_val(m.Qn[t][n]);
+          ys[tb][r] += ul[cc][tb][r] * bf_val(m.Kn[t][n]);
+        }
+    }
+    // X, Y partials of this wave's columns: sums over the 16 lanes of a row group
 #pragma unroll
-          for (int o = 1; o < 16; o <<= 1) {
-            xp[tb][r] += __shfl_xor(xp[tb][r], o);
-            yp[tb][r] += __shfl_xor(yp[tb][r], o);
-          }
-          if (l15 == 0) {
-            const int t = 16 * tb + 4 * l4 + r;
-            m.XYp[w][0][t] = (cc == 0 ? 0.f : m.XYp[w][0][t]) + xp[tb][r];
-            m.XYp[w][1][t] = (cc == 0 ? 0.f : m.XYp[w][1][t]) + yp[tb][r];
-          }
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float xr = rr::row16_sum(xs[tb][r]), yr = rr::row16_sum(ys[tb][r]);
+        if (l15 == 0) {
+          const int t = 16 * tb + 4 * l4 + r;
+          m.XYp[w][0][t] = xr;
+          m.XYp[w][1][t] = yr;
         }
       }
-    }
     f32x16_t cg = {};   // wave 0: CB = C B^T; wave 1: G2 = dY U^T
     if (w == 0) {
 #pragma unroll
@@ -367,27 +370,34 @@ __global__ __launch_bounds__(256, 2) void col_bwd_kernel(rr::ChunkArgs p) {
       for (int r = 0; r < 16; ++r) m.G2[r32row(r, lane)][lane & 31] = cg[r];
     }
     __syncthreads();
-    // ------------------------------------------------ B2: masked products; Hp
+    // ------------------------------------------------ B2: masked products; GLA dg / SSD T
     if (w != 2) {
       // wave 0: P^T (CB registers); wave 1: MG^T (G2 registers); wave 3: MG o w_s
       // and, for SSD, K (G2 from LDS)
       float md[16];
       rr::chunked::decay_block32<GLA>(GLA ? m.xin : m.cd, a, lane, md);
       const int s = lane & 31;
+      if (w != 3) {
+        // rows r32row(4g .. 4g + 3) are consecutive: one 8-byte write per group
+        uint16_t(*dst_hi)[PQ] = w == 0 ? m.y.PT_hi : m.y.MGT_hi;
+        uint16_t(*dst_lo)[PQ] = w == 0 ? m.y.PT_lo : m.y.MGT_lo;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int tp = r32row(r, lane);
-        uint16_t hi, lo;
-        if (w == 0) {
-          bf_split(md[r] * cg[r], hi, lo);
-          m.y.PT_hi[s][tp] = hi;
-          m.y.PT_lo[s][tp] = lo;
-        } else if (w == 1) {
-          bf_split(md[r] * cg[r], hi, lo);
-          m.y.MGT_hi[s][tp] = hi;
-          m.y.MGT_lo[s][tp] = lo;
-        } else {
-          const float mgw = md[r] * m.G2[tp][s] * m.w[s];
+        for (int g = 0; g < 4; ++g) {
+          u16x4_t hi4, lo4;
+          rr::bf_split4(f32x4_t{md[4 * g] * cg[4 * g], md[4 * g + 1] * cg[4 * g + 1], md[4 * g + 2] * cg[4 * g + 2],
+                                md[4 * g + 3] * cg[4 * g + 3]},
+                        hi4, lo4);
+          const int tp = r32row(4 * g, lane);
+          *reinterpret_cast<u16x4_t*>(&dst_hi[s][tp]) = hi4;
+          *reinterpret_cast<u16x4_t*>(&dst_lo[s][tp]) = lo4;
+        }
+      } else {
+        const float wsv = m.w[s];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int tp = r32row(r, lane);
+          uint16_t hi, lo;
+          const float mgw = md[r] * m.G2[tp][s] * wsv;
           bf_split(mgw, hi, lo);
           m.y.MG_hi[tp][s] = hi;
           m.y.MG_lo[tp][s] = lo;
@@ -397,6 +407,33 @@ __global__ __launch_bounds__(256, 2) void col_bwd_kernel(rr::ChunkArgs p) {
             m.y.Km_lo[tp][s] = lo;
           }
         }
+      }
+    } else if constexpr (!GLA) {
+      // T_t = R_t + sum_{t' >= t} gam X + sum_{s <= t} m31 w Y + m31_t gam_t tr,
+      // R_t = sum_{t' >= t} sum_{s <= t} K[t', s], K = M o w_s o G2 o CB:
+      // prefix over s along the lanes, then the rows t' >= t of column t.
+      float md[16];
+      rr::chunked::decay_block32<false>(m.cd, a, lane, md);
+      const int s = lane & 31;
+      const float wsv = m.w[s];
+      float rs = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int tp = r32row(r, lane);
+        const float k = rr::prefix32_sum(md[r] * wsv * m.G2[tp][s] * m.CB[tp][s]);
+        rs += tp >= s ? k : 0.f;
+      }
+      rs = rr::halves_sum(rs);
+      // lanes 0..31: suffix of gam X in reversed lane order; lanes 32..63: prefix of m31 w Y
+      const int tq = lane < Q ? Q - 1 - lane : lane - Q;
+      const float xy = lane < Q
+          ? m.gam[tq] * (m.XYp[0][0][tq] + m.XYp[1][0][tq] + m.XYp[2][0][tq] + m.XYp[3][0][tq])
+          : m.m31[tq] * m.w[tq] * (m.XYp[0][1][tq] + m.XYp[1][1][tq] + m.XYp[2][1][tq] + m.XYp[3][1][tq]);
+      m.Ts[lane < Q ? 0 : 1][tq] = rr::prefix32_sum(xy);
+      rr::wave_lds_sync();
+      if (lane < Q) {
+        const float tr = m.trw[0] + m.trw[1] + m.trw[2] + m.trw[3];
+        m.HT[lane] = rs + m.Ts[0][lane] + m.Ts[1][lane] + m.m31[lane] * m.gam[lane] * tr;
       }
     } else {
       if (lane <= Q) {
@@ -432,8 +469,7 @@ __global__ __launch_bounds__(256, 2) void col_bwd_kernel(rr::ChunkArgs p) {
         float hp = 0.f;
 #pragma unroll
         for (int r = 0; r <= Q; ++r) hp += m.Cc[r][lane];
-        if constexpr (GLA) rr::st_bf16(p.ddelta, baseX + lane * p.H, hp);
-        else m.Hp[lane] = hp;
+        rr::st_bf16(p.ddelta, baseX + lane * p.H, hp);
       }
     }
     __syncthreads();
@@ -503,9 +539,7 @@ __global__ __launch_bounds__(256, 2) void col_bwd_kernel(rr::ChunkArgs p) {
         }
       }
       if constexpr (!GLA) {
-        dAp += __shfl_xor(dAp, 16);
-        dAp += __shfl_xor(dAp, 32);
-        dA_acc[cc] += dAp + gam31 * cd31 * trn[cc];
+        dA_acc[cc] += rr::rows4_sum(dAp) + gam31 * cd31 * trn[cc];
       }
     }
     if constexpr (!GLA) {
@@ -514,9 +548,8 @@ __global__ __launch_bounds__(256, 2) void col_bwd_kernel(rr::ChunkArgs p) {
       for (int tb = 0; tb < 2; ++tb) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-#pragma unroll
-          for (int o = 1; o < 16; o <<= 1) bz[tb][r] += __shfl_xor(bz[tb][r], o);
-          if (l15 == 0) m.BZp[w][16 * tb + 4 * l4 + r] = bz[tb][r];
+          const float v = rr::row16_sum(bz[tb][r]);
+          if (l15 == 0) m.BZp[w][16 * tb + 4 * l4 + r] = v;
         }
       }
     }
@@ -552,7 +585,7 @@ __global__ __launch_bounds__(256, 2) void col_bwd_kernel(rr::ChunkArgs p) {
       __syncthreads();
       if (w == 0 && lane < Q) {
         const float bzt = m.BZp[0][lane] + m.BZp[1][lane] + m.BZp[2][lane] + m.BZp[3][lane];
-        rr::st_bf16(p.ddelta, baseX + lane * p.H, a * m.dec[lane] * m.Hp[lane] + bzt);
+        rr::st_bf16(p.ddelta, baseX + lane * p.H, a * m.HT[lane] + (1.f - a * m.xin[lane]) * bzt);
       }
     }
     if (MODE == kWhole) __syncthreads();   // the next chunk rewrites the LDS

@@ -44,21 +44,20 @@ struct Cfg {
 // lane % 32).
 __device__ __forceinline__ int r32row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
-// Inclusive prefix sum / product over lanes 0..31 and, separately, 32..63.
-__device__ __forceinline__ float prefix32(float v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 32; o <<= 1) {
-    const float x = __shfl_up(v, o, 32);
-    if ((lane & 31) >= o) v += x;
-  }
-  return v;
+// Inclusive prefix sum / product over lanes 0..31 and, separately, 32..63
+// (DPP row shifts, then row 0 (2) hands its total to row 1 (3)).
+__device__ __forceinline__ float prefix32(float v, int /*lane*/) { return prefix32_sum(v); }
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_one(float v) {   // 1 where the source lane is outside the row
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, 1.f), __builtin_bit_cast(int, v),
+                                                               CTRL, ROWS, 0xF, false));
 }
-__device__ __forceinline__ float prefix_prod32(float v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 32; o <<= 1) {
-    const float x = __shfl_up(v, o, 32);
-    if ((lane & 31) >= o) v *= x;
-  }
+__device__ __forceinline__ float prefix_prod32(float v, int /*lane*/) {
+  v *= dpp_one<0x111, 0xF>(v);   // row_shr:1
+  v *= dpp_one<0x112, 0xF>(v);   // row_shr:2
+  v *= dpp_one<0x114, 0xF>(v);   // row_shr:4
+  v *= dpp_one<0x118, 0xF>(v);   // row_shr:8
+  v *= dpp_one<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
   return v;
 }
 // Inclusive suffix product over lanes (lane..31) within each half-wave.

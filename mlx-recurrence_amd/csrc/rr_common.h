@@ -3,8 +3,9 @@
 //
 // Element access: inputs arrive as fp32, bf16 or fp16 and are widened to fp32
 // on load; state and accumulation are always fp32.  bf16 is carried as raw
-// uint16_t bits (widening is a 16-bit shift; narrowing rounds to nearest even)
-// so the kernels do not depend on a vendor bf16 class.
+// uint16_t bits (widening is a 16-bit shift; narrowing is the hardware
+// conversion, round to nearest even) so the kernels do not depend on a vendor
+// bf16 class.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -26,16 +27,10 @@ __device__ __forceinline__ float to_f32(f16 v) { return static_cast<float>(v); }
 
 template <typename T> __device__ __forceinline__ T from_f32(float v);
 template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+// fp32 -> bf16 with gfx950's v_cvt_pk_bf16_f32 (round to nearest even, NaN
+// stays NaN).
 template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) {
-  uint32_t u = __float_as_uint(v);
-  bf16 r;
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
-    r.bits = static_cast<uint16_t>((u >> 16) | 0x40u);  // quiet NaN
-  } else {
-    u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even
-    r.bits = static_cast<uint16_t>(u >> 16);
-  }
-  return r;
+  return bf16{__builtin_bit_cast(uint16_t, static_cast<__bf16>(v))};
 }
 template <> __device__ __forceinline__ f16 from_f32<f16>(float v) { return static_cast<f16>(v); }
 

@@ -29,11 +29,9 @@ typedef __attribute__((__vector_size__(4 * sizeof(unsigned short)))) unsigned sh
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
 
-// fp32 -> bf16 bits, round to nearest even (finite inputs).
+// fp32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint16_t bf_bits(float x) {
-  uint32_t u = __float_as_uint(x);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
 }
 __device__ __forceinline__ float bf_val(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
@@ -57,15 +55,19 @@ __device__ __forceinline__ f32x4_t mfma16k16(const u16x4_t& a, const u16x4_t& b,
                                                    __builtin_bit_cast(i16x4_t, b), c, 0, 0, 0);
 }
 
+// Two fp32 values -> packed bf16 pair (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t bf_pack2(float a, float b) {
+  typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+  const bf16x2_v v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
 // Split four fp32 values into bf16 hi and lo operand fragments.
 __device__ __forceinline__ void bf_split4(const f32x4_t& x, u16x4_t& hi, u16x4_t& lo) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    uint16_t h, l;
-    bf_split(x[e], h, l);
-    hi[e] = h;
-    lo[e] = l;
-  }
+  const uint32_t h01 = bf_pack2(x[0], x[1]), h23 = bf_pack2(x[2], x[3]);
+  const uint32_t l01 = bf_pack2(x[0] - __uint_as_float(h01 << 16), x[1] - __uint_as_float(h01 & 0xffff0000u));
+  const uint32_t l23 = bf_pack2(x[2] - __uint_as_float(h23 << 16), x[3] - __uint_as_float(h23 & 0xffff0000u));
+  hi = __builtin_bit_cast(u16x4_t, make_uint2(h01, h23));
+  lo = __builtin_bit_cast(u16x4_t, make_uint2(l01, l23));
 }
 
 // Store an fp32 value as bf16 (round to nearest even).
@@ -79,6 +81,45 @@ __device__ __forceinline__ u16x8_t frag(const uint16_t* p) {
 // 8-byte fragment read from LDS (address must be 8-byte aligned).
 __device__ __forceinline__ u16x4_t frag4(const uint16_t* p) {
   return *reinterpret_cast<const u16x4_t*>(p);
+}
+
+// Cross-lane sums without LDS traffic.  Every lane of the group receives the
+// same value (each butterfly step adds two equal-valued pairs, so the
+// rounding is identical across the group).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Sum over the 16 lanes of a row (lanes 16k .. 16k + 15).
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+  v += dpp_mov<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+  v += dpp_mov<0x141>(v);   // row_half_mirror: quad q <-> quad q ^ 1
+  v += dpp_mov<0x140>(v);   // row_mirror: half h <-> half h ^ 1
+  return v;
+}
+// Sum over the four rows: lanes l, l ^ 16, l ^ 32, l ^ 48 (LDS-unit
+// permutes; used a few times per chunk).
+__device__ __forceinline__ float rows4_sum(float v) {
+  v += __shfl_xor(v, 16);
+  return v + __shfl_xor(v, 32);
+}
+__device__ __forceinline__ float wave_sum(float v) { return rows4_sum(row16_sum(v)); }
+// Sum of lanes l and l ^ 32.
+__device__ __forceinline__ float halves_sum(float v) { return v + __shfl_xor(v, 32); }
+// Inclusive prefix sum over lanes 0..31 and, separately, 32..63: shifts
+// within each 16-lane row, then row 0 (2) hands its total to row 1 (3).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_in(float v) {   // 0 where the source lane is outside the row
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, true));
+}
+__device__ __forceinline__ float prefix32_sum(float v) {
+  v += dpp_in<0x111, 0xF>(v);   // row_shr:1
+  v += dpp_in<0x112, 0xF>(v);   // row_shr:2
+  v += dpp_in<0x114, 0xF>(v);   // row_shr:4
+  v += dpp_in<0x118, 0xF>(v);   // row_shr:8
+  v += dpp_in<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
+  return v;
 }
 
 // Make one wave's LDS writes visible to its own later LDS reads.
