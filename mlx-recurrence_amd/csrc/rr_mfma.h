@@ -70,6 +70,15 @@ __device__ __forceinline__ void bf_split4(const f32x4_t& x, u16x4_t& hi, u16x4_t
   lo = __builtin_bit_cast(u16x4_t, make_uint2(l01, l23));
 }
 
+// Split eight fp32 values into bf16 hi and lo operand fragments.
+__device__ __forceinline__ void bf_split8(const float (&x)[8], u16x8_t& hi, u16x8_t& lo) {
+  u16x4_t h0, l0, h1, l1;
+  bf_split4(f32x4_t{x[0], x[1], x[2], x[3]}, h0, l0);
+  bf_split4(f32x4_t{x[4], x[5], x[6], x[7]}, h1, l1);
+  hi = u16x8_t{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+  lo = u16x8_t{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+}
+
 // Store an fp32 value as bf16 (round to nearest even).
 __device__ __forceinline__ void st_bf16(uint16_t* p, int64_t i, float v) { p[i] = bf_bits(v); }
 

@@ -25,6 +25,7 @@ using rr::f32x4_t;
 using rr::frag;
 using rr::mfma16;
 using rr::mfma32;
+using rr::u16x4_t;
 using rr::u16x8_t;
 using rr::chunked::Cfg;
 using rr::chunked::prefix32;
@@ -92,50 +93,45 @@ namespace {
 
 // LDS of the backward kernel.  Arrays live in phase order, so the operands
 // that die after phase B1 (x) share space with the masked products written in
-// B2 (y), and the B1/B2 fp32 products (p) with the phase-C results (q).
+// B2 (y).  The pipelined mode (CARRY false) takes dY^T, lam and the h_in / lam
+// columns as register fragments straight from global memory instead of the
+// transposed LDS copies (GYT, LM, LMT, HT), which keeps its LDS small enough
+// for three workgroups per CU.
 template <int DH, int NS, bool CARRY>
 struct BwdSmem {
   static constexpr int PD = DH + 8, PN = NS + 8;
+  static constexpr int TD = CARRY ? DH : 1, TN = CARRY ? NS : 1;
   uint16_t Bn[Q][PN];
   uint16_t Cn[Q][PN];
   uint16_t BT[NS][PQ];
   uint16_t CT[NS][PQ];
-  uint16_t GYT_hi[DH][PQ], GYT_lo[DH][PQ];
-  uint16_t LM_hi[DH][PN], LM_lo[DH][PN];
+  uint16_t GYT_hi[TD][PQ], GYT_lo[TD][PQ];
+  uint16_t LM_hi[TD][PN], LM_lo[TD][PN];
   float GH[Q][NS + 1];
   float UL[Q][NS + 1];
   union {
     struct {                       // phase A -> B1
       uint16_t U[Q][PD];
       uint16_t GY_hi[Q][PD], GY_lo[Q][PD];
-      uint16_t LMT_hi[NS][PD], LMT_lo[NS][PD];
-      uint16_t HT_hi[NS][PD], HT_lo[NS][PD];
+      uint16_t LMT_hi[TN][PD], LMT_lo[TN][PD];
+      uint16_t HT_hi[TN][PD], HT_lo[TN][PD];
     } x;
     struct {                       // phase B2 -> C
       uint16_t PT_hi[Q][PQ], PT_lo[Q][PQ];
       uint16_t MGT_hi[Q][PQ], MGT_lo[Q][PQ];
       uint16_t MGd_hi[Q][PQ], MGd_lo[Q][PQ];
-      uint16_t Km_hi[Q][PQ], Km_lo[Q][PQ];
     } y;
   };
-  union {
-    struct {                       // phase B1 -> B2
-      float CB[Q][Q + 1];
-      float G2[Q][Q + 1];
-      float F[Q][Q + 1];
-    } p;
-    struct {                       // phase C -> D
-      float Z[Q][NS + 1];
-      float KB[Q][NS + 1];
-    } q;
-  };
+  float CB[Q][Q + 1];              // phase B1 -> B2
+  float G2[Q][Q + 1];
   // (gam o C)^T, for the adjoint carried to the previous chunk (whole-head
   // mode; chunk 0 of the direct mode for the initial-state gradient)
   uint16_t CgT_hi[CARRY ? NS : 1][PQ], CgT_lo[CARRY ? NS : 1][PQ];
   float del[Q], cd[Q], gam[Q], m31[Q], R[Q];
-  float kGH[Q], kUL[Q], kZ[Q];
+  float Xs[NS / 16][Q], Ys[NS / 16][Q], BZs[NS / 16][Q];   // row sums over one 16-column block
+  float Ts[2][Q];                  // suffix of gam X, prefix of m31 delta Y
   float t4[4][NS];
-  float dAp[4][4][NS];
+  float dAq[2][2][NS];             // dA partials of the (kind, tb) tasks
 };
 
 template <int DH, int NS, int MODE>
@@ -152,12 +148,12 @@ union BwdShared<DH, NS, kDirect> {
 // from the direct sum (kDirect); or a whole head per workgroup, lam carried
 // backwards in registers (kWhole).
 template <int DH, int NS, int MODE>
-__global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
+__global__ __launch_bounds__(256, MODE == kPipe ? 3 : 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
   using K = Cfg<DH, NS>;
   constexpr bool PIPE = MODE == kPipe;
   __shared__ BwdShared<DH, NS, MODE> smu;
   auto& m = smu.m;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   int h, b, cbeg;
   if constexpr (MODE == kWhole) {
     h = blockIdx.y, b = blockIdx.z, cbeg = 0;
@@ -166,7 +162,9 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
     if (!id.valid) return;
     h = id.h, b = id.b, cbeg = id.c;
   }
-  const int cend = min(cbeg + p.R, p.nC);
+  // one chunk per workgroup except in the whole-head mode (a visible single
+  // iteration keeps the compiler from hoisting addresses out of the loop)
+  const int cend = MODE == kWhole ? min(cbeg + p.R, p.nC) : cbeg + 1;
   const float a = p.A[(int64_t)h * p.A_stride_h];
   const int64_t rowH = p.H;
   const int64_t sbase = ((int64_t)b * p.H + h) * DH * NS;
@@ -211,9 +209,18 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
   float dA_acc = 0.f;  // thread tid < NS accumulates dA[h, tid] over the run
 
   for (int c = cend - 1; c >= cbeg; --c) {
+    // a fresh copy of the thread index per chunk keeps the compiler from
+    // hoisting every per-lane address of the body out of the chunk loop
+    int tidv = tid;
+    if constexpr (MODE == kWhole) asm volatile("" : "+v"(tidv));
+    const int tid = tidv, lane = tidv & 63;
     const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;
     // ------------------------------------------------ A: stage (all loads first)
     f32x4_t hin[K::NBW];
+    // pipelined mode: register operand fragments (see BwdSmem)
+    constexpr int TPW = NBN;   // GH / UL tasks per task wave (waves 2 and 3 in phase B1)
+    float pdy[PIPE ? 2 : 1][8], plm[PIPE ? NS / 16 : 1][8];
+    f32x4_t pcol[PIPE ? TPW : 1][PIPE ? DH / 16 : 1];
     {
       constexpr int UV = (Q * DH / 8 + 255) / 256, BV = (Q * NS / 8 + 255) / 256, GV = (Q * DH / 4 + 255) / 256;
       u16x8_t uv[UV], bv[BV], cv[BV];
@@ -240,6 +247,24 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
       if (w == 0 && lane < Q) dv = bf_val(p.delta[(row0 + lane) * rowH + h]);
       const float* hsrc = c > 0 ? p.ckpt + (((int64_t)b * p.H + h) * p.nC + (c - 1)) * DH * NS
                                 : (p.h0 != nullptr ? p.h0 + sbase : nullptr);
+      if constexpr (PIPE) {
+        if (w >= 2) {
+          // GH / UL tasks: the h_in / lam column nb as 16x16x16 B fragments (k = d)
+#pragma unroll
+          for (int q = 0; q < TPW; ++q) {
+            const int task = (w - 2) + 2 * q;
+            const int kind = task / NBN, nb = task % NBN;
+            const float* src = kind == 0 ? hsrc : lsrc;
+#pragma unroll
+            for (int kb = 0; kb < DH / 16; ++kb)
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                pcol[q][kb][e] = (task < 2 * NBN && src != nullptr)
+                                     ? src[(16 * kb + 4 * (lane >> 4) + e) * NS + 16 * nb + (lane & 15)]
+                                     : 0.f;
+          }
+        }
+      }
 #pragma unroll
       for (int jj = 0; jj < K::NBW; ++jj) {
         const int j = w + 4 * jj;
@@ -280,8 +305,10 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
             bf_split(g4[e], hi, lo);
             m.x.GY_hi[tl][d0 + e] = hi;
             m.x.GY_lo[tl][d0 + e] = lo;
-            m.GYT_hi[d0 + e][tl] = hi;
-            m.GYT_lo[d0 + e][tl] = lo;
+            if constexpr (!PIPE) {
+              m.GYT_hi[d0 + e][tl] = hi;
+              m.GYT_lo[d0 + e][tl] = lo;
+            }
           }
         }
       }
@@ -294,16 +321,12 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
           m.cd[lane] = cdv;
           m.gam[lane] = gt;
           m.m31[lane] = mt;
-          // per-step coefficients of the dA terms
-          m.kGH[lane] = gt * cdv;
-          m.kUL[lane] = mt * dv * (c31 - cdv + dv);
-          m.kZ[lane] = dv * dv;
         }
       }
 #pragma unroll
       for (int jj = 0; jj < K::NBW; ++jj) {
         const int j = w + 4 * jj;
-        if (j < K::NB) {
+        if (!PIPE && j < K::NB) {
           const int db = j / NBN, nb = j % NBN;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
@@ -330,7 +353,7 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
         cb = mfma32(frag(&m.Cn[lane & 31][16 * kb + 8 * (lane >> 5)]),
                     frag(&m.Bn[lane & 31][16 * kb + 8 * (lane >> 5)]), cb);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) m.p.CB[r32row(r, lane)][lane & 31] = cb[r];
+      for (int r = 0; r < 16; ++r) m.CB[r32row(r, lane)][lane & 31] = cb[r];
     } else if (w == 1) {
       f32x16_t g2 = {};
 #pragma unroll
@@ -340,7 +363,44 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
         g2 = mfma32(frag(&m.x.GY_lo[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, g2);
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) m.p.G2[r32row(r, lane)][lane & 31] = g2[r];
+      for (int r = 0; r < 16; ++r) m.G2[r32row(r, lane)][lane & 31] = g2[r];
+    } else if constexpr (PIPE) {
+      // tasks (kind, nb): GH = dY h_in (kind 0) or UL = U lam (kind 1) for the
+      // 16 columns nb, B fragments from registers
+      const int l15 = lane & 15, l4 = lane >> 4;
+#pragma unroll
+      for (int q = 0; q < TPW; ++q) {
+        const int task = (w - 2) + 2 * q;
+        const int kind = task / NBN, nb = task % NBN;
+        u16x4_t bh[DH / 16], bl[DH / 16];
+#pragma unroll
+        for (int kb = 0; kb < DH / 16; ++kb) rr::bf_split4(pcol[q][kb], bh[kb], bl[kb]);
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+          const int row = 16 * tb + l15;
+          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kb = 0; kb < DH / 16; ++kb) {
+            const int k0 = 16 * kb + 4 * l4;
+            if (kind == 0) {
+              const u16x4_t ah = rr::frag4(&m.x.GY_hi[row][k0]), al = rr::frag4(&m.x.GY_lo[row][k0]);
+              acc = rr::mfma16k16(ah, bh[kb], acc);
+              acc = rr::mfma16k16(ah, bl[kb], acc);
+              acc = rr::mfma16k16(al, bh[kb], acc);
+            } else {
+              const u16x4_t av = rr::frag4(&m.x.U[row][k0]);
+              acc = rr::mfma16k16(av, bh[kb], acc);
+              acc = rr::mfma16k16(av, bl[kb], acc);
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = 16 * tb + 4 * l4 + r, col = 16 * nb + l15;
+            if (kind == 0) m.GH[t][col] = acc[r];
+            else m.UL[t][col] = acc[r];
+          }
+        }
+      }
     } else {
       // tasks: GH blocks (tb, nb) and UL blocks (sb, nb); waves 2 and 3
       for (int task = w - 2; task < 4 * NBN; task += 2) {
@@ -385,6 +445,25 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
     }
     __syncthreads();
     // ------------------------------------------------ B2: masked products, rectangle sums
+    if constexpr (PIPE) {
+      if (w < DH / 32) {
+        // du operands (used in phase C; the loads land while B2 runs): dY^T
+        // [t'][d] (B of a1) and lam [d][n] (B of a2), d = 32 w + lane % 32
+        const int d = 32 * w + (lane & 31);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            pdy[kb][e] = p.dy[((row0 + 16 * kb + 8 * (lane >> 5) + e) * rowH + h) * DH + d];
+#pragma unroll
+        for (int kb = 0; kb < NS / 16; ++kb) {
+          const float* src = lsrc + d * NS + 16 * kb + 8 * (lane >> 5);
+          const float4 l0 = *reinterpret_cast<const float4*>(src), l1 = *reinterpret_cast<const float4*>(src + 4);
+          plm[kb][0] = l0.x, plm[kb][1] = l0.y, plm[kb][2] = l0.z, plm[kb][3] = l0.w;
+          plm[kb][4] = l1.x, plm[kb][5] = l1.y, plm[kb][6] = l1.z, plm[kb][7] = l1.w;
+        }
+      }
+    }
     if (w == 0) {
       // P = M o CB, stored transposed [t][t']
       const int s = lane & 31;
@@ -392,20 +471,20 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int tp = r32row(r, lane);
-        const float v = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * m.p.CB[tp][s] : 0.f;
+        const float v = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * m.CB[tp][s] : 0.f;
         uint16_t hi, lo;
         bf_split(v, hi, lo);
         m.y.PT_hi[s][tp] = hi;
         m.y.PT_lo[s][tp] = lo;
       }
     } else if (w == 1 || w == 3) {
-      // M o G2 -> (M o G2)^T [t][t'] (wave 1); (M o G2 o delta_s) and K [t'][s] (wave 3)
+      // M o G2 -> (M o G2)^T [t][t'] (wave 1); M o G2 o delta_s [t'][s] (wave 3)
       const int s = lane & 31;
       const float cds = m.cd[s], ds = m.del[s];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int tp = r32row(r, lane);
-        const float mg = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * m.p.G2[tp][s] : 0.f;
+        const float mg = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * m.G2[tp][s] : 0.f;
         uint16_t hi, lo;
         if (w == 1) {
           bf_split(mg, hi, lo);
@@ -415,42 +494,23 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
           bf_split(mg * ds, hi, lo);
           m.y.MGd_hi[tp][s] = hi;
           m.y.MGd_lo[tp][s] = lo;
-          bf_split(mg * ds * (m.cd[tp] - cds + ds), hi, lo);
-          m.y.Km_hi[tp][s] = hi;
-          m.y.Km_lo[tp][s] = lo;
         }
       }
     } else {
-      // E = M o delta_s o G2 o CB in the 32x32 layout; F = row prefix over s; R = column suffix over t'
+      // R_t = sum_{t' >= t} sum_{s <= t} E[t', s], E = M o delta_s o G2 o CB: prefix
+      // over s along the lanes, then the rows t' >= t of column t
       const int s = lane & 31;
       const float cds = m.cd[s], ds = m.del[s];
+      float rs = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int tp = r32row(r, lane);
-        m.p.F[tp][s] = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * ds * m.p.G2[tp][s] * m.p.CB[tp][s] : 0.f;
+        const float e = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * ds * m.G2[tp][s] * m.CB[tp][s] : 0.f;
+        const float k = rr::prefix32_sum(e);
+        rs += tp >= s ? k : 0.f;
       }
-      rr::wave_lds_sync();
-      if (lane < Q) {
-        float row[Q];
-#pragma unroll
-        for (int q = 0; q < Q; ++q) row[q] = m.p.F[lane][q];
-        float run = 0.f;
-#pragma unroll
-        for (int q = 0; q < Q; ++q) {
-          run += row[q];
-          m.p.F[lane][q] = run;
-        }
-      }
-      rr::wave_lds_sync();
-      if (lane < Q) {
-        float col[Q];
-#pragma unroll
-        for (int q = 0; q < Q; ++q) col[q] = m.p.F[q][lane];
-        float rs = 0.f;
-#pragma unroll
-        for (int q = 0; q < Q; ++q) rs += (q >= lane) ? col[q] : 0.f;
-        m.R[lane] = rs;
-      }
+      rs = rr::halves_sum(rs);
+      if (lane < Q) m.R[lane] = rs;
     }
     __syncthreads();
     // ------------------------------------------------ C: du, Z/dB, dC, KB, lam_prev
@@ -462,7 +522,13 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
       for (int kb = 0; kb < 2; ++kb) {
         const int k0 = 16 * kb + 8 * (lane >> 5);
         const u16x8_t ph = frag(&m.y.PT_hi[lane & 31][k0]), pl = frag(&m.y.PT_lo[lane & 31][k0]);
-        const u16x8_t gh = frag(&m.GYT_hi[d0 + (lane & 31)][k0]), gl = frag(&m.GYT_lo[d0 + (lane & 31)][k0]);
+        u16x8_t gh, gl;
+        if constexpr (PIPE) {
+          rr::bf_split8(pdy[kb], gh, gl);
+        } else {
+          gh = frag(&m.GYT_hi[d0 + (lane & 31)][k0]);
+          gl = frag(&m.GYT_lo[d0 + (lane & 31)][k0]);
+        }
         a1 = mfma32(ph, gh, a1);
         a1 = mfma32(ph, gl, a1);
         a1 = mfma32(pl, gh, a1);
@@ -471,8 +537,15 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
       for (int kb = 0; kb < NS / 16; ++kb) {
         const int k0 = 16 * kb + 8 * (lane >> 5);
         const u16x8_t fa = frag(&m.Bn[lane & 31][k0]);
-        a2 = mfma32(fa, frag(&m.LM_hi[d0 + (lane & 31)][k0]), a2);
-        a2 = mfma32(fa, frag(&m.LM_lo[d0 + (lane & 31)][k0]), a2);
+        u16x8_t lh, ll;
+        if constexpr (PIPE) {
+          rr::bf_split8(plm[kb], lh, ll);
+        } else {
+          lh = frag(&m.LM_hi[d0 + (lane & 31)][k0]);
+          ll = frag(&m.LM_lo[d0 + (lane & 31)][k0]);
+        }
+        a2 = mfma32(fa, lh, a2);
+        a2 = mfma32(fa, ll, a2);
       }
       const int d = d0 + (lane & 31);
 #pragma unroll
@@ -481,9 +554,14 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
         rr::st_bf16(p.du, ((row0 + t) * rowH + h) * DH + d, m.del[t] * (a1[r] + m.m31[t] * a2[r]));
       }
     } else {
-      // Z, dC, KB blocks over the waves >= DH/32
+      // Z / dB and dC blocks over the waves >= DH/32, with their row sums
+      // (sum_n B Z, Y = sum_n UL B, X = sum_n GH C) and dA partials:
+      //   dA[n] = sum_t cd_t (C dC - B dB) + cd_31 (sum_t m31 delta B UL + gam_31 sum_d lam h_in)
+      // (dB, dC before rounding; the decay product of the dual form needs no
+      // extra matrix this way)
       const int nw = 4 - DH / 32;
-      for (int task = w - DH / 32; task < 6 * NBN; task += nw) {
+      const float cd31 = m.cd[Q - 1];
+      for (int task = w - DH / 32; task < 4 * NBN; task += nw) {
         const int kind = task / (2 * NBN), tt = task % (2 * NBN);
         const int tb = tt / NBN, nb = tt % NBN;
         const int row = 16 * tb + (lane & 15), col = 16 * nb + (lane & 15);
@@ -493,29 +571,45 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
           const u16x8_t fb = frag(&m.CT[col][k0]);
           acc = mfma16(frag(&m.y.MGT_hi[row][k0]), fb, acc);
           acc = mfma16(frag(&m.y.MGT_lo[row][k0]), fb, acc);
-        } else if (kind == 1) {
+        } else {
           const u16x8_t fb = frag(&m.BT[col][k0]);
           acc = mfma16(frag(&m.y.MGd_hi[row][k0]), fb, acc);
           acc = mfma16(frag(&m.y.MGd_lo[row][k0]), fb, acc);
-        } else {
-          const u16x8_t fb = frag(&m.BT[col][k0]);
-          acc = mfma16(frag(&m.y.Km_hi[row][k0]), fb, acc);
-          acc = mfma16(frag(&m.y.Km_lo[row][k0]), fb, acc);
         }
+        float da = 0.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = 16 * tb + 4 * (lane >> 4) + r;
           const int64_t gi = ((row0 + t) * rowH + h) * NS + col;
+          float s1, s2;
           if (kind == 0) {
-            const float z = acc[r] + m.m31[t] * m.UL[t][col];
-            m.q.Z[t][col] = z;
-            rr::st_bf16(p.dB, gi, m.del[t] * z);
-          } else if (kind == 1) {
-            rr::st_bf16(p.dC, gi, m.gam[t] * m.GH[t][col] + acc[r]);
+            const float bv = bf_val(m.Bn[t][col]), ul = m.UL[t][col], dt = m.del[t];
+            const float z = acc[r] + m.m31[t] * ul;
+            rr::st_bf16(p.dB, gi, dt * z);
+            s1 = bv * z;
+            s2 = ul * bv;
+            da += bv * dt * (cd31 * m.m31[t] * ul - m.cd[t] * z);
           } else {
-            m.q.KB[t][col] = acc[r];
+            const float cv = bf_val(m.Cn[t][col]), gh = m.GH[t][col];
+            const float dc = m.gam[t] * gh + acc[r];
+            rr::st_bf16(p.dC, gi, dc);
+            s1 = gh * cv;
+            s2 = 0.f;
+            da += m.cd[t] * cv * dc;
+          }
+          s1 = rr::row16_sum(s1);
+          s2 = rr::row16_sum(s2);
+          if ((lane & 15) == 0) {
+            if (kind == 0) {
+              m.BZs[nb][t] = s1;
+              m.Ys[nb][t] = s2;
+            } else {
+              m.Xs[nb][t] = s1;
+            }
           }
         }
+        da = rr::rows4_sum(da);
+        if (lane < 16) m.dAq[kind][tb][col] = da;
       }
     }
     // lam_prev = (gam o dY)^T C + gam31 lam; sum_d lam h_in per n (for tr and dA)
@@ -558,49 +652,32 @@ __global__ __launch_bounds__(256, 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
     }
     __syncthreads();
     // ------------------------------------------------ D: d(delta), dA
+    // d(delta)_t = a T_t + (1 - a delta_t) sum_n B_t Z_t,
+    // T_t = sum lam_t h_t = R_t + sum_{t' >= t} gam X + sum_{s <= t} m31 delta Y + m31_t gam_t tr
     if (w == 0) {
-      const int t = lane & 31;
-      float X = 0.f, Y = 0.f, BZ = 0.f, tr = 0.f;
-      for (int n = 0; n < NS; ++n) {
-        const float bv = bf_val(m.Bn[t][n]);
-        X += m.GH[t][n] * bf_val(m.Cn[t][n]);
-        Y += m.UL[t][n] * bv;
-        BZ += bv * m.q.Z[t][n];
-        tr += m.t4[0][n] + m.t4[1][n] + m.t4[2][n] + m.t4[3][n];
-      }
-      const float dt = m.del[t], gt = m.gam[t], mt = m.m31[t];
-      // suffix over t' >= t of gam X; prefix over s <= t of m31 delta Y
-      float suf = gt * X, pre = mt * dt * Y;
+      const float tn = lane < NS ? m.t4[0][lane] + m.t4[1][lane] + m.t4[2][lane] + m.t4[3][lane] : 0.f;
+      const float tr = rr::wave_sum(tn);
+      // lanes 0..31: suffix of gam X in reversed lane order; lanes 32..63: prefix of m31 delta Y
+      const int tq = lane < Q ? Q - 1 - lane : lane - Q;
+      float xy = 0.f;
 #pragma unroll
-      for (int o = 1; o < 32; o <<= 1) {
-        const float xs = __shfl_down(suf, o, 32);
-        const float xp = __shfl_up(pre, o, 32);
-        if (t + o < 32) suf += xs;
-        if (t >= o) pre += xp;
+      for (int nb = 0; nb < NBN; ++nb) xy += lane < Q ? m.Xs[nb][tq] : m.Ys[nb][tq];
+      xy *= lane < Q ? m.gam[tq] : m.m31[tq] * m.del[tq];
+      m.Ts[lane < Q ? 0 : 1][tq] = rr::prefix32_sum(xy);
+      rr::wave_lds_sync();
+      if (lane < Q) {
+        const int t = lane;
+        float bz = 0.f;
+#pragma unroll
+        for (int nb = 0; nb < NBN; ++nb) bz += m.BZs[nb][t];
+        const float T = m.R[t] + m.Ts[0][t] + m.Ts[1][t] + m.m31[t] * m.gam[t] * tr;
+        rr::st_bf16(p.ddelta, (row0 + t) * rowH + h, a * T + (1.f - a * m.del[t]) * bz);
       }
-      const float T = m.R[t] + suf + pre + mt * gt * tr;
-      if (lane < Q) rr::st_bf16(p.ddelta, (row0 + t) * rowH + h, a * T + (1.f - a * dt) * BZ);
-    } else {
-      // dA terms: lane -> (n = lane % 16 + 16 q, t in one of 12 row groups); waves 1..3
-      for (int n0 = 0; n0 < NS; n0 += 16) {
-        const int n = n0 + (lane & 15), tq = (w - 1) * 4 + (lane >> 4);
-        float sum = 0.f;
-        for (int t = tq; t < Q; t += 12) {
-          const float bv = bf_val(m.Bn[t][n]), cv = bf_val(m.Cn[t][n]);
-          sum += cv * (m.q.KB[t][n] + m.kGH[t] * m.GH[t][n]) + bv * (m.kUL[t] * m.UL[t][n] - m.kZ[t] * m.q.Z[t][n]);
-        }
-        sum += __shfl_xor(sum, 16);
-        sum += __shfl_xor(sum, 32);
-        if (lane < 16) m.dAp[w][0][n] = sum;
-      }
+    } else if (w == 1 && lane < NS) {
+      dA_acc += m.dAq[0][0][lane] + m.dAq[0][1][lane] + m.dAq[1][0][lane] + m.dAq[1][1][lane] +
+                gam31 * m.cd[Q - 1] * (m.t4[0][lane] + m.t4[1][lane] + m.t4[2][lane] + m.t4[3][lane]);
     }
-    // gam_31 cd_31 sum_d lam h_in (read before the barrier: the next chunk rewrites cd)
-    const float gc = gam31 * m.cd[Q - 1];
-    __syncthreads();
-    if (w == 1 && lane < NS) {
-      dA_acc += m.dAp[1][0][lane] + m.dAp[2][0][lane] + m.dAp[3][0][lane] +
-                gc * (m.t4[0][lane] + m.t4[1][lane] + m.t4[2][lane] + m.t4[3][lane]);
-    }
+    if constexpr (MODE == kWhole) __syncthreads();   // the next chunk rewrites the LDS
   }
   // per-run dA partial and the initial-state gradient
   const int nR = MODE == kWhole ? 1 : p.nC;   // runs per head

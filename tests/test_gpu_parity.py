@@ -206,6 +206,8 @@ SSD_CASES = [
     # more than 16 chunks: pipelined mode (aggregate, state-pass and chunk kernels)
     (1, 1024, 3, 64, 16, 32, BF16, "cfg", True, True, 26),
     (2, 640, 2, 32, 32, 32, BF16, "cfg", False, True, 27),
+    (1, 384, 3, 32, 16, 32, BF16, "cfg", True, True, 36),
+    (2, 192, 2, 64, 32, 32, BF16, "cfg", True, False, 37),
     # N = 64, 128: column-owned backward, in its three modes
     (1, 128, 2, 64, 64, 32, BF16, "cfg", True, True, 30),    # direct (4 chunks)
     (2, 96, 3, 32, 128, 32, BF16, "cfg", True, False, 31),   # direct (3 chunks)
