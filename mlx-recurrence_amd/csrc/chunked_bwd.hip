@@ -62,16 +62,18 @@ using rr::chunked::Q;
 using rr::chunked::r32row;
 
 // LDS of the backward kernel.  The operands that die after phase B1 (x) share
-// space with the masked products written in phase B2 (y).
-template <int DH, int NS, bool GLA>
+// space with the masked products written in phase B2 (y).  In the pipelined
+// mode (REG) the du operands dY^T and lam come from global memory as register
+// fragments, so GYT and LM shrink to a row.
+template <int DH, int NS, bool GLA, bool REG>
 struct alignas(16) ColBwdSmem {
-  static constexpr int PD = DH + 8, PN = NS + 8;
+  static constexpr int PD = DH + 8, PN = NS + 8, TD = REG ? 1 : DH;
   uint16_t Kn[Q][PN];                      // B [s][n]
   uint16_t Qn[Q][PN];                      // C [t][n]
   uint16_t KT[NS][PQ];                     // B^T [n][s]
   uint16_t QT[NS][PQ];                     // C^T [n][t]
-  uint16_t GYT_hi[DH][PQ], GYT_lo[DH][PQ]; // dY^T [d][t]
-  uint16_t LM_hi[DH][PN], LM_lo[DH][PN];   // lam [d][n]
+  uint16_t GYT_hi[TD][PQ], GYT_lo[TD][PQ]; // dY^T [d][t]
+  uint16_t LM_hi[TD][PN], LM_lo[TD][PN];   // lam [d][n]
   union {
     struct {                               // phase A -> B1
       uint16_t V[Q][PD];                       // U [s][d]
@@ -98,17 +100,19 @@ struct alignas(16) ColBwdSmem {
 
 template <int DH, int NS, int MODE, bool GLA>
 union ColBwdShared {
-  ColBwdSmem<DH, NS, GLA> m;
+  ColBwdSmem<DH, NS, GLA, MODE == kPipe> m;
 };
 template <int DH, int NS, bool GLA>
 union ColBwdShared<DH, NS, kDirect, GLA> {
-  ColBwdSmem<DH, NS, GLA> m;
+  ColBwdSmem<DH, NS, GLA, false> m;
   rr::chunked::DirectSmem<DH, NS, true> d;
 };
 
-// Two workgroups per CU where the LDS allows it.
+// Workgroups per CU the LDS allows (the register budget follows).
 template <int DH, int NS, int MODE, bool GLA>
-constexpr int kColBwdWgs = sizeof(ColBwdShared<DH, NS, MODE, GLA>) <= 80 * 1024 ? 2 : 1;
+constexpr int kColBwdWgs = (int)(160 * 1024 / sizeof(ColBwdShared<DH, NS, MODE, GLA>)) >= 3   ? 3
+                           : (int)(160 * 1024 / sizeof(ColBwdShared<DH, NS, MODE, GLA>)) >= 2 ? 2
+                                                                                                : 1;
 
 template <int DH, int NS, int MODE, bool GLA>
 __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_kernel(rr::ChunkArgs p) {
@@ -260,8 +264,10 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
             bf_split(g4[e], hi, lo);
             hi4[e] = hi;
             lo4[e] = lo;
-            m.GYT_hi[d0 + e][tl] = hi;
-            m.GYT_lo[d0 + e][tl] = lo;
+            if constexpr (MODE != kPipe) {
+              m.GYT_hi[d0 + e][tl] = hi;
+              m.GYT_lo[d0 + e][tl] = lo;
+            }
           }
           *reinterpret_cast<u16x4_t*>(&m.x.GY_hi[tl][d0]) = hi4;
           *reinterpret_cast<u16x4_t*>(&m.x.GY_lo[tl][d0]) = lo4;
@@ -291,8 +297,10 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int d = 16 * db + 4 * l4 + r, n = 16 * nb + l15;
-              m.LM_hi[d][n] = hi4[r];
-              m.LM_lo[d][n] = lo4[r];
+              if constexpr (MODE != kPipe) {
+                m.LM_hi[d][n] = hi4[r];
+                m.LM_lo[d][n] = lo4[r];
+              }
               trn[cc] += lam[cc][db][r] * hin[cc][db][r];
             }
           }
@@ -371,6 +379,25 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
     }
     __syncthreads();
     // ------------------------------------------------ B2: masked products; GLA dg / SSD T
+    // pipelined mode: this wave's du operands (row block mydb), used in phase C;
+    // the loads land while B2 runs
+    const int mydb = ((w - NBN) % 4 + 4) % 4;
+    float pdy[MODE == kPipe ? 8 : 1], plm[MODE == kPipe ? NS / 32 : 1][8];
+    if constexpr (MODE == kPipe) {
+      if (mydb < NBD) {
+        const int d = 16 * mydb + l15;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pdy[e] = p.dy[baseD + (8 * l4 + e) * rsD + d];
+        const float* lsrc = p.agg + ((bh * p.nC + c) * DH + d) * NS + 8 * l4;
+#pragma unroll
+        for (int kk = 0; kk < NS / 32; ++kk) {
+          const float4 l0 = *reinterpret_cast<const float4*>(lsrc + 32 * kk);
+          const float4 l1 = *reinterpret_cast<const float4*>(lsrc + 32 * kk + 4);
+          plm[kk][0] = l0.x, plm[kk][1] = l0.y, plm[kk][2] = l0.z, plm[kk][3] = l0.w;
+          plm[kk][4] = l1.x, plm[kk][5] = l1.y, plm[kk][6] = l1.z, plm[kk][7] = l1.w;
+        }
+      }
+    }
     if (w != 2) {
       // wave 0: P^T (CB registers); wave 1: MG^T (G2 registers); wave 3: MG o w_s
       // and, for SSD, K (G2 from LDS)
@@ -474,26 +501,40 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
     }
     __syncthreads();
     // ------------------------------------------------ C: du, dB, dC (+ SSD dA terms, lam_prev)
+    if (mydb < NBD) {
+      const int db = mydb;
+      u16x8_t gh8, gl8;   // dY^T fragment [t' = 8 l4 + e][d]
+      if constexpr (MODE == kPipe) {
+        rr::bf_split8(pdy, gh8, gl8);
+      } else {
+        gh8 = frag(&m.GYT_hi[16 * db + l15][8 * l4]);
+        gl8 = frag(&m.GYT_lo[16 * db + l15][8 * l4]);
+      }
+      u16x8_t lh8[NS / 32], ll8[NS / 32];   // lam fragments [n = 32 kk + 8 l4 + e][d]
 #pragma unroll
-    for (int db = 0; db < NBD; ++db) {
-      if ((db + NBN) % 4 != w) continue;
+      for (int kk = 0; kk < NS / 32; ++kk) {
+        if constexpr (MODE == kPipe) {
+          rr::bf_split8(plm[kk], lh8[kk], ll8[kk]);
+        } else {
+          lh8[kk] = frag(&m.LM_hi[16 * db + l15][32 * kk + 8 * l4]);
+          ll8[kk] = frag(&m.LM_lo[16 * db + l15][32 * kk + 8 * l4]);
+        }
+      }
 #pragma unroll
       for (int tb = 0; tb < 2; ++tb) {
         f32x4_t a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
         {
           const int k0 = 8 * l4;
           const u16x8_t ph = frag(&m.y.PT_hi[16 * tb + l15][k0]), pl = frag(&m.y.PT_lo[16 * tb + l15][k0]);
-          const u16x8_t gh8 = frag(&m.GYT_hi[16 * db + l15][k0]), gl8 = frag(&m.GYT_lo[16 * db + l15][k0]);
           a1 = mfma16(ph, gh8, a1);
           a1 = mfma16(ph, gl8, a1);
           a1 = mfma16(pl, gh8, a1);
         }
 #pragma unroll
         for (int kk = 0; kk < NS / 32; ++kk) {
-          const int k0 = 32 * kk + 8 * l4;
-          const u16x8_t fa = frag(&m.Kn[16 * tb + l15][k0]);
-          a2 = mfma16(fa, frag(&m.LM_hi[16 * db + l15][k0]), a2);
-          a2 = mfma16(fa, frag(&m.LM_lo[16 * db + l15][k0]), a2);
+          const u16x8_t fa = frag(&m.Kn[16 * tb + l15][32 * kk + 8 * l4]);
+          a2 = mfma16(fa, lh8[kk], a2);
+          a2 = mfma16(fa, ll8[kk], a2);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -528,8 +569,9 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
           const int t = 16 * tb + 4 * l4 + r, n = 16 * nb + l15;
           const int64_t gi = baseN + t * rsN + n;
           const float z = ak[r] + m.m31[t] * ul[cc][tb][r];
-          rr::st_bf16(p.dB, gi, m.w[t] * z);
-          rr::st_bf16(p.dC, gi, m.gam[t] * gh[cc][tb][r] + aq[r]);
+          const float dbv = m.w[t] * z, dcv = m.gam[t] * gh[cc][tb][r] + aq[r];
+          rr::st_bf16(p.dB, gi, dbv);
+          rr::st_bf16(p.dC, gi, dcv);
           if constexpr (!GLA) {
             const float bv = bf_val(m.Kn[t][n]), cv = bf_val(m.Qn[t][n]);
             bz[tb][r] += bv * z;

@@ -120,6 +120,7 @@ struct BwdSmem {
       uint16_t PT_hi[Q][PQ], PT_lo[Q][PQ];
       uint16_t MGT_hi[Q][PQ], MGT_lo[Q][PQ];
       uint16_t MGd_hi[Q][PQ], MGd_lo[Q][PQ];
+      uint16_t Km_hi[Q][PQ], Km_lo[Q][PQ];
     } y;
   };
   float CB[Q][Q + 1];              // phase B1 -> B2
@@ -478,7 +479,7 @@ __global__ __launch_bounds__(256, MODE == kPipe ? 3 : 2) void ssd2_bwd_kernel(rr
         m.y.PT_lo[s][tp] = lo;
       }
     } else if (w == 1 || w == 3) {
-      // M o G2 -> (M o G2)^T [t][t'] (wave 1); M o G2 o delta_s [t'][s] (wave 3)
+      // M o G2 -> (M o G2)^T [t][t'] (wave 1); M o G2 o delta_s and K [t'][s] (wave 3)
       const int s = lane & 31;
       const float cds = m.cd[s], ds = m.del[s];
 #pragma unroll
@@ -494,6 +495,9 @@ __global__ __launch_bounds__(256, MODE == kPipe ? 3 : 2) void ssd2_bwd_kernel(rr
           bf_split(mg * ds, hi, lo);
           m.y.MGd_hi[tp][s] = hi;
           m.y.MGd_lo[tp][s] = lo;
+          bf_split(mg * ds * (m.cd[tp] - cds + ds), hi, lo);
+          m.y.Km_hi[tp][s] = hi;
+          m.y.Km_lo[tp][s] = lo;
         }
       }
     } else {
@@ -554,11 +558,8 @@ __global__ __launch_bounds__(256, MODE == kPipe ? 3 : 2) void ssd2_bwd_kernel(rr
         rr::st_bf16(p.du, ((row0 + t) * rowH + h) * DH + d, m.del[t] * (a1[r] + m.m31[t] * a2[r]));
       }
     } else {
-      // Z / dB and dC blocks over the waves >= DH/32, with their row sums
-      // (sum_n B Z, Y = sum_n UL B, X = sum_n GH C) and dA partials:
-      //   dA[n] = sum_t cd_t (C dC - B dB) + cd_31 (sum_t m31 delta B UL + gam_31 sum_d lam h_in)
-      // (dB, dC before rounding; the decay product of the dual form needs no
-      // extra matrix this way)
+      // Z / dB and dC (+ K B) blocks over the waves >= DH/32, with their row
+      // sums (sum_n B Z, Y = sum_n UL B, X = sum_n GH C) and dA partials
       const int nw = 4 - DH / 32;
       const float cd31 = m.cd[Q - 1];
       for (int task = w - DH / 32; task < 4 * NBN; task += nw) {
@@ -566,7 +567,7 @@ __global__ __launch_bounds__(256, MODE == kPipe ? 3 : 2) void ssd2_bwd_kernel(rr
         const int tb = tt / NBN, nb = tt % NBN;
         const int row = 16 * tb + (lane & 15), col = 16 * nb + (lane & 15);
         const int k0 = 8 * (lane >> 4);
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f}, akb = {0.f, 0.f, 0.f, 0.f};
         if (kind == 0) {
           const u16x8_t fb = frag(&m.CT[col][k0]);
           acc = mfma16(frag(&m.y.MGT_hi[row][k0]), fb, acc);
@@ -575,6 +576,8 @@ __global__ __launch_bounds__(256, MODE == kPipe ? 3 : 2) void ssd2_bwd_kernel(rr
           const u16x8_t fb = frag(&m.BT[col][k0]);
           acc = mfma16(frag(&m.y.MGd_hi[row][k0]), fb, acc);
           acc = mfma16(frag(&m.y.MGd_lo[row][k0]), fb, acc);
+          akb = mfma16(frag(&m.y.Km_hi[row][k0]), fb, akb);
+          akb = mfma16(frag(&m.y.Km_lo[row][k0]), fb, akb);
         }
         float da = 0.f;
 #pragma unroll
@@ -588,14 +591,14 @@ __global__ __launch_bounds__(256, MODE == kPipe ? 3 : 2) void ssd2_bwd_kernel(rr
             rr::st_bf16(p.dB, gi, dt * z);
             s1 = bv * z;
             s2 = ul * bv;
-            da += bv * dt * (cd31 * m.m31[t] * ul - m.cd[t] * z);
+            da += bv * (m.m31[t] * dt * (cd31 - m.cd[t] + dt) * ul - dt * dt * z);
           } else {
             const float cv = bf_val(m.Cn[t][col]), gh = m.GH[t][col];
             const float dc = m.gam[t] * gh + acc[r];
             rr::st_bf16(p.dC, gi, dc);
             s1 = gh * cv;
             s2 = 0.f;
-            da += m.cd[t] * cv * dc;
+            da += cv * (akb[r] + m.gam[t] * m.cd[t] * gh);
           }
           s1 = rr::row16_sum(s1);
           s2 = rr::row16_sum(s2);
