@@ -12,12 +12,11 @@
 //   Z  = MG^T C + diag(m31) UL,  dB = diag(w) Z
 //   dC = diag(gam) GH + (MG o w_s) B
 //   Hp_t = sum_{d,n} lam_t h_{t-1}
-//        = sum_{r >= t} M'[r, t] F_t[r],   r = 0..32 (row 32 stands for lam):
-//          M'[r, t] = M[r, t] (r < 32), m31_t (r = 32);
-//          F_0[r] = X_r (r < 32), tr (r = 32);  F_{t+1}[r] = dec_t F_t[r] + E'[r, t];
-//          E'[r, s] = CB[r, s] G2[r, s] w_s (r < 32), Y_s (r = 32);
+//        = sum_{t'} (M o W)[t', t] + m31_t (P_t + gam_{t-1} tr),   W = E Mh + X gam_{t-1}
+//          E = CB o G2 o w_s,  Mh[s, t] = M[t-1, s] (s < t, else 0),  P_t = sum_s Mh[s, t] Y_s
 //          X = rowsum(GH o C), Y = rowsum(UL o B) o w, tr = sum(lam o h_in)
-//        (division free: zero or negative GLA gates are exact)
+//        (lam_t and h_{t-1} factor through M[t', t] and M[t-1, s]: division free,
+//        so zero or negative GLA gates are exact)
 //   GLA: dg_t = Hp_t.
 //   SSD: d(delta)_t = a dec_t Hp_t + sum_n B_t Z_t = a T_t + (1 - a delta_t) sum_n B_t Z_t
 //        with T_t = sum_{d,n} lam_t h_t = R_t + sum_{t' >= t} gam X + sum_{s <= t} m31 w Y
@@ -89,7 +88,7 @@ struct alignas(16) ColBwdSmem {
   };
   float CB[Q][Q + 1];
   float G2[Q][Q + 1];
-  float Cc[GLA ? Q + 1 : 1][Q + 1];        // GLA: dg contributions M'[r, t] F_t[r]
+  float XY[GLA ? 2 : 1][Q];                // GLA: X, Y (sums of the per-wave partials)
   float XYp[4][2][Q];                      // per-wave partial X, Y
   float BZp[GLA ? 1 : 4][Q];               // SSD: per-wave partial sum_n B Z
   float xin[Q], dec[Q], gam[Q], m31[Q], w[Q], cd[Q];
@@ -463,40 +462,56 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
         m.HT[lane] = rs + m.Ts[0][lane] + m.Ts[1][lane] + m.m31[lane] * m.gam[lane] * tr;
       }
     } else {
-      if (lane <= Q) {
-        const int row = lane;
-        float e[Q], fv[Q];
-        float f;
-        if (row < Q) {
-          f = m.XYp[0][0][row] + m.XYp[1][0][row] + m.XYp[2][0][row] + m.XYp[3][0][row];
+      // GLA: dg_t = sum_{t'} (M o W)[t', t] + m31_t (P_t + gam_{t-1} tr), division free:
+      //   W = E Mh + X gam_{t-1},  E = CB o G2,  Mh[s, t] = M[t-1, s] = g_{s+1} ... g_{t-1} (s < t),
+      //   P_t = sum_{s<t} Mh[s, t] Y_s
+      // (E Mh on MFMA: lane holds column t = lane % 32 of Mh for s = 16 kb + 8 (lane / 32) + e)
+      const int t = lane & 31, hf = lane >> 5;
+      if (lane < Q) {
+        m.XY[0][lane] = m.XYp[0][0][lane] + m.XYp[1][0][lane] + m.XYp[2][0][lane] + m.XYp[3][0][lane];
+        m.XY[1][lane] = m.XYp[0][1][lane] + m.XYp[1][1][lane] + m.XYp[2][1][lane] + m.XYp[3][1][lane];
+      }
+      float mh[2][8];
+      {
+        float run = 1.f;
 #pragma unroll
-          for (int s = 0; s < Q; ++s) e[s] = s < row ? m.CB[row][s] * m.G2[row][s] * m.w[s] : 0.f;
-        } else {
-          f = m.trw[0] + m.trw[1] + m.trw[2] + m.trw[3];
-#pragma unroll
-          for (int s = 0; s < Q; ++s)
-            e[s] = (m.XYp[0][1][s] + m.XYp[1][1][s] + m.XYp[2][1][s] + m.XYp[3][1][s]) * m.w[s];
-        }
-#pragma unroll
-        for (int t = 0; t < Q; ++t) {
-          fv[t] = f;
-          f = m.dec[t] * f + e[t];
-        }
-        const int tmax = row < Q ? row : Q - 1;
-        float mm = 1.f;
-#pragma unroll
-        for (int t = Q - 1; t >= 0; --t) {
-          const bool act = t <= tmax;
-          m.Cc[row][t] = act ? mm * fv[t] : 0.f;
-          if (act) mm *= m.dec[t];
+        for (int s = Q - 1; s >= 0; --s) {
+          run = s == t - 1 ? 1.f : run * m.xin[(s + 1) & (Q - 1)];
+          if (((s >> 3) & 1) == hf) mh[s >> 4][s & 7] = s < t ? run : 0.f;
         }
       }
-      rr::wave_lds_sync();
-      if (lane < Q) {
-        float hp = 0.f;
+      f32x16_t acc = {};
 #pragma unroll
-        for (int r = 0; r <= Q; ++r) hp += m.Cc[r][lane];
-        rr::st_bf16(p.ddelta, baseX + lane * p.H, hp);
+      for (int kb = 0; kb < 2; ++kb) {
+        float ev[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int sv = 16 * kb + 8 * hf + e;
+          ev[e] = m.CB[t][sv] * m.G2[t][sv];
+        }
+        u16x8_t eh, el, bh, bl;
+        rr::bf_split8(ev, eh, el);
+        rr::bf_split8(mh[kb], bh, bl);
+        acc = mfma32(eh, bh, acc);
+        acc = mfma32(eh, bl, acc);
+        acc = mfma32(el, bh, acc);
+      }
+      rr::wave_lds_sync();   // XY
+      float md[16];
+      rr::chunked::decay_block32<true>(m.xin, 0.f, lane, md);
+      const float gprev = t > 0 ? m.gam[t - 1] : 1.f;
+      float cs = 0.f, ps = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) cs += md[r] * (acc[r] + m.XY[0][r32row(r, lane)] * gprev);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ps += mh[kb][e] * m.XY[1][16 * kb + 8 * hf + e];
+      cs = rr::halves_sum(cs);
+      ps = rr::halves_sum(ps);
+      if (lane < Q) {
+        const float tr = m.trw[0] + m.trw[1] + m.trw[2] + m.trw[3];
+        rr::st_bf16(p.ddelta, baseX + lane * p.H, cs + m.m31[lane] * (ps + gprev * tr));
       }
     }
     __syncthreads();
@@ -660,7 +675,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
 template <int DH, int NS, bool GLA>
 int launch(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
   if (p.mode == kPipe) {
-    hipLaunchKernelGGL((rr::chunked::agg_kernel<DH, NS, GLA>), rr::chunked::chunk_grid(p), dim3(64), 0, s, p, 1);
+    hipLaunchKernelGGL((rr::chunked::agg_kernel<DH, NS, GLA>), rr::chunked::chunk_grid(p), dim3(rr::chunked::kAggThreads), 0, s, p, 1);
     if (int rc = rr::check_launch("chunked backward aggregates")) return rc;
     hipLaunchKernelGGL((rr::chunked::pass_kernel<DH, NS, GLA>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0,
                        s, p, 1);

@@ -166,7 +166,7 @@ __device__ __forceinline__ float head_rate(const ChunkArgs& p, int h) {
 
 // ------------------------------------------------------------------ pipelined mode
 // Several workgroups per head.  Three kernels per pass:
-//  1. agg_kernel, one wave per chunk k, writes the chunk's aggregate and its
+//  1. agg_kernel, one workgroup per chunk k, writes the chunk's aggregate and its
 //     decay tot_k = gam_31:
 //       forward:  S_k = U_k^T diag(m31 o w) B_k, the state the chunk adds from
 //                 a zero start (into checkpoint slot k);
@@ -179,71 +179,85 @@ __device__ __forceinline__ float head_rate(const ChunkArgs& p, int h) {
 //                 and dh0 = tot_0 lam_0 + G_0.
 //  3. the main kernel, one workgroup per chunk, reads its entering state
 //     (and, backward, lam_k) and does the chunk's dense products.
+// agg_kernel: a workgroup of four waves per chunk stages the operands (all
+// loads first), then wave w forms the 16x16 blocks j = w, w + 4, ... of the
+// aggregate.
+constexpr int kAggThreads = 256;
 template <int DH, int NS, bool GLA>
-__global__ __launch_bounds__(64) void agg_kernel(ChunkArgs p, int kind) {
+__global__ __launch_bounds__(kAggThreads) void agg_kernel(ChunkArgs p, int kind) {
   constexpr int NBN = NS / 16, NB = (DH / 16) * NBN;
   __shared__ uint16_t XT_hi[DH][PQ], XT_lo[DH][PQ];   // kind 0: U^T [d][s] (hi only); kind 1: (gam o dY)^T
   __shared__ uint16_t YT_hi[NS][PQ], YT_lo[NS][PQ];   // kind 0: (m31 o w o B)^T split; kind 1: C^T (hi only)
-  const int lane = threadIdx.x;
+  __shared__ float wsh[Q];                            // kind 0: m31_s w_s; kind 1: gam_t
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const ChunkId id = chunk_id(p, false);
   if (!id.valid) return;
   const int c = id.c, h = id.h, b = id.b;
   const float a = head_rate<GLA>(p, h);
   const int64_t rowH = p.H, row0 = (int64_t)b * p.L + (int64_t)c * Q;
-  constexpr int UV = Q * DH / 8 / 64, GV = Q * DH / 4 / 64, BV = (Q * NS / 8 + 63) / 64;
+  constexpr int T = kAggThreads;
+  constexpr int UV = (Q * DH / 8 + T - 1) / T, GV = (Q * DH / 4 + T - 1) / T, BV = (Q * NS / 8 + T - 1) / T;
   // loads first
   u16x8_t uv[UV], bv[BV];
   float4 gv[GV];
   if (kind == 0) {
 #pragma unroll
     for (int v = 0; v < UV; ++v) {
-      const int i = lane + 64 * v, tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
-      uv[v] = *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0);
+      const int i = tid + T * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
+      uv[v] = i < Q * DH / 8 ? *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0) : u16x8_t{};
     }
   } else {
 #pragma unroll
     for (int v = 0; v < GV; ++v) {
-      const int i = lane + 64 * v, tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
-      gv[v] = *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0);
+      const int i = tid + T * v, tl = (i / (DH / 4)) & (Q - 1), d0 = 4 * (i % (DH / 4));
+      gv[v] = i < Q * DH / 4 ? *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
   const uint16_t* bsrc = kind == 0 ? p.Bm : p.Cm;
 #pragma unroll
   for (int v = 0; v < BV; ++v) {
-    const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+    const int i = tid + T * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
     bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(bsrc + ((row0 + tl) * rowH + h) * NS + n0) : u16x8_t{};
   }
-  const float xv = lane < Q ? bf_val(p.delta[(row0 + lane) * rowH + h]) : (GLA ? 1.f : 0.f);
-  const StepScalars sc = step_scalars<GLA>(xv, a, lane);
-  // kind 0: m31_s w_s ; kind 1: gam_t
-  const float wt = kind == 0 ? sc.m31 * sc.w : sc.gam;
+  if (w == 0) {
+    const float xv = lane < Q ? bf_val(p.delta[(row0 + lane) * rowH + h]) : (GLA ? 1.f : 0.f);
+    const StepScalars sc = step_scalars<GLA>(xv, a, lane);
+    if (lane < Q) wsh[lane] = kind == 0 ? sc.m31 * sc.w : sc.gam;
+    if (lane == 0) p.tot[((int64_t)b * p.H + h) * p.nC + c] = sc.tot;
+  }
+  __syncthreads();
   if (kind == 0) {
 #pragma unroll
     for (int v = 0; v < UV; ++v) {
-      const int i = lane + 64 * v, tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
+      const int i = tid + T * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
+      if (i < Q * DH / 8) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) XT_hi[d0 + e][tl] = uv[v][e];
+        for (int e = 0; e < 8; ++e) XT_hi[d0 + e][tl] = uv[v][e];
+      }
     }
   } else {
 #pragma unroll
     for (int v = 0; v < GV; ++v) {
-      const int i = lane + 64 * v, tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
-      const float g4[4] = {gv[v].x, gv[v].y, gv[v].z, gv[v].w};
-      const float gt = __shfl(wt, tl);
+      const int i = tid + T * v, tl = (i / (DH / 4)) & (Q - 1), d0 = 4 * (i % (DH / 4));
+      if (i < Q * DH / 4) {
+        const float gt = wsh[tl];
+        const float g4[4] = {gv[v].x, gv[v].y, gv[v].z, gv[v].w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        uint16_t hi, lo;
-        bf_split(gt * g4[e], hi, lo);
-        XT_hi[d0 + e][tl] = hi;
-        XT_lo[d0 + e][tl] = lo;
+        for (int e = 0; e < 4; ++e) {
+          uint16_t hi, lo;
+          bf_split(gt * g4[e], hi, lo);
+          XT_hi[d0 + e][tl] = hi;
+          XT_lo[d0 + e][tl] = lo;
+        }
       }
     }
   }
 #pragma unroll
   for (int v = 0; v < BV; ++v) {
-    const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
-    const float ws = __shfl(wt, tl);
+    const int i = tid + T * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
     if (i < Q * NS / 8) {
+      const float ws = wsh[tl];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         if (kind == 0) {
@@ -257,10 +271,12 @@ __global__ __launch_bounds__(64) void agg_kernel(ChunkArgs p, int kind) {
       }
     }
   }
-  wave_lds_sync();
+  __syncthreads();
   float* dst = (kind == 0 ? p.ckpt : p.agg) + (((int64_t)b * p.H + h) * p.nC + c) * DH * NS;
 #pragma unroll
-  for (int j = 0; j < NB; ++j) {
+  for (int jj = 0; jj < (NB + 3) / 4; ++jj) {
+    const int j = w + 4 * jj;
+    if (j >= NB) break;
     const int db = j / NBN, nb = j % NBN;
     const u16x8_t fa = frag(&XT_hi[16 * db + (lane & 15)][8 * (lane >> 4)]);
     const u16x8_t fb = frag(&YT_hi[16 * nb + (lane & 15)][8 * (lane >> 4)]);
@@ -271,14 +287,13 @@ __global__ __launch_bounds__(64) void agg_kernel(ChunkArgs p, int kind) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) dst[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)] = acc[r];
   }
-  if (lane == 0) p.tot[((int64_t)b * p.H + h) * p.nC + c] = sc.tot;
 }
 
 // Sequential pass over the chunks of one (batch, head), one state element per
 // thread; loads are issued kPass chunks ahead of their use.
 template <int DH, int NS, bool GLA>
 __global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
-  constexpr int kPass = 8;
+  constexpr int kPass = 16;
   const int e = blockIdx.x * 256 + threadIdx.x;   // element d * NS + n
   const int es = state_off<GLA, DH, NS>(e / NS, e % NS);
   const int h = blockIdx.y, b = blockIdx.z;
@@ -737,7 +752,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
 template <int DH, int NS, bool GLA>
 int launch_fwd(const ChunkArgs& p, int64_t B, hipStream_t s) {
   if (p.mode == kPipe) {   // R == 1
-    hipLaunchKernelGGL((agg_kernel<DH, NS, GLA>), chunk_grid(p), dim3(64), 0, s, p, 0);
+    hipLaunchKernelGGL((agg_kernel<DH, NS, GLA>), chunk_grid(p), dim3(kAggThreads), 0, s, p, 0);
     if (int rc = check_launch("chunked forward aggregates")) return rc;
     hipLaunchKernelGGL((pass_kernel<DH, NS, GLA>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0, s, p, 0);
     if (int rc = check_launch("chunked forward state pass")) return rc;
