@@ -210,7 +210,8 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
         gv[v] = i < Q * DH / 4 ? *reinterpret_cast<const float4*>(p.dy + baseD + tl * rsD + d0)
                                : make_float4(0.f, 0.f, 0.f, 0.f);
       }
-      if (tid < Q) xv = bf_val(p.delta[baseX + tid * p.H]);
+      // unconditional (in-bounds) load, so no branch waits on it; only lanes < 32 of wave 0 use it
+      xv = bf_val(p.delta[baseX + (tid & (Q - 1)) * p.H]);
       const float* hsrc = c > 0 ? p.ckpt + (bh * p.nC + c - 1) * DH * NS
                                 : (p.h0 != nullptr ? p.h0 + bh * DH * NS : nullptr);
       const float* lsrc = MODE == kPipe ? p.agg + (bh * p.nC + c) * DH * NS : nullptr;
@@ -273,7 +274,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
         }
       }
       if (w == 0) {
-        const rr::chunked::StepScalars sc = rr::chunked::step_scalars<GLA>(xv, a, lane);
+        const rr::chunked::StepScalars sc = rr::chunked::step_scalars<GLA>(lane < Q ? xv : (GLA ? 1.f : 0.f), a, lane);
         if (lane < Q) {
           m.xin[lane] = xv;
           m.dec[lane] = GLA ? xv : __expf(a * xv);

@@ -136,6 +136,19 @@ __device__ __forceinline__ int state_off(int d, int n) {
   else return d * NS + n;
 }
 
+// Modes of the chunked kernels (ChunkArgs::mode):
+//   kWhole  a head per workgroup, state / adjoint carried in registers;
+//   kPipe   one workgroup per chunk; aggregate kernel, state-pass kernel
+//           (pass_kernel), chunk kernel;
+//   kDirect one workgroup per chunk forming its entering state from the raw
+//           inputs of the other chunks (nC <= kDirectMaxChunks);
+//   kSum    one workgroup per chunk forming its entering state from the
+//           chunk aggregates (agg_sum): aggregate kernel, chunk kernel.
+enum Mode { kWhole = 0, kPipe = 1, kDirect = 2, kSum = 3 };
+// kSum reads up to nC - 1 aggregates per workgroup (quadratic in nC), so it
+// serves the middle range of chunk counts; longer heads run kPipe.
+constexpr int kSumMaxChunks = 16;
+
 // Per-chunk kernels run on a 1-D grid of chunk_grid(p) workgroups.  The GPU
 // hands workgroups to its 8 XCDs round-robin by linear index; the decode
 // gives every chunk of a head the same XCD, so whatever the head's
@@ -169,7 +182,7 @@ __device__ __forceinline__ float head_rate(const ChunkArgs& p, int h) {
 //  1. agg_kernel, one workgroup per chunk k, writes the chunk's aggregate and its
 //     decay tot_k = gam_31:
 //       forward:  S_k = U_k^T diag(m31 o w) B_k, the state the chunk adds from
-//                 a zero start (into checkpoint slot k);
+//                 a zero start (into checkpoint slot k; kSum: the workspace);
 //       backward: G_k = (gam o dY_k)^T C_k, the adjoint the chunk sends back to
 //                 its start (into the workspace).
 //  2. pass_kernel, one thread per state element, walks the chunks in order:
@@ -221,7 +234,8 @@ __global__ __launch_bounds__(kAggThreads) void agg_kernel(ChunkArgs p, int kind)
     bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(bsrc + ((row0 + tl) * rowH + h) * NS + n0) : u16x8_t{};
   }
   if (w == 0) {
-    const float xv = lane < Q ? bf_val(p.delta[(row0 + lane) * rowH + h]) : (GLA ? 1.f : 0.f);
+    const float xl = bf_val(p.delta[(row0 + (lane & (Q - 1))) * rowH + h]);   // unconditional load
+    const float xv = lane < Q ? xl : (GLA ? 1.f : 0.f);
     const StepScalars sc = step_scalars<GLA>(xv, a, lane);
     if (lane < Q) wsh[lane] = kind == 0 ? sc.m31 * sc.w : sc.gam;
     if (lane == 0) p.tot[((int64_t)b * p.H + h) * p.nC + c] = sc.tot;
@@ -272,7 +286,7 @@ __global__ __launch_bounds__(kAggThreads) void agg_kernel(ChunkArgs p, int kind)
     }
   }
   __syncthreads();
-  float* dst = (kind == 0 ? p.ckpt : p.agg) + (((int64_t)b * p.H + h) * p.nC + c) * DH * NS;
+  float* dst = (kind == 0 && p.mode != kSum ? p.ckpt : p.agg) + (((int64_t)b * p.H + h) * p.nC + c) * DH * NS;
 #pragma unroll
   for (int jj = 0; jj < (NB + 3) / 4; ++jj) {
     const int j = w + 4 * jj;
@@ -342,6 +356,61 @@ __global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
   }
 }
 
+// ------------------------------------------------------------------ sum mode
+// kSum: the state entering chunk c (forward) or the adjoint leaving it
+// (backward), from the chunk aggregates in p.agg and decays in p.tot by
+// Horner's rule (the recursion pass_kernel runs, restricted to one chunk):
+//   forward:  x = h0;     x = tot_j x + S_j  for j = 0 .. c - 1
+//   backward: x = dfinal; x = tot_j x + G_j  for j = nC - 1 .. c + 1
+// for this lane's elements of the 16x16 blocks (db(j), nb(j)) listed by
+// `blk` (the caller's register layout: rows 4 (lane / 16) + r, column lane % 16).
+template <int DH, int NS, bool GLA, bool BWD, int NX, typename BLK>
+__device__ __forceinline__ void agg_sum(const ChunkArgs& p, int c, int64_t bh, int lane, BLK blk,
+                                        f32x4_t (&x)[NX]) {
+  constexpr int kBatch = NX == 1 ? 16 : NX == 2 ? 8 : 4;
+  const float* ext = BWD ? p.dfinal : p.h0;
+  // loads are unconditional (indices clamped into range) so that no branch
+  // waits on them; out-of-range terms are dropped in the fold
+  int off[NX];
+  bool has[NX];
+#pragma unroll
+  for (int q = 0; q < NX; ++q) {
+    int db, nb;
+    has[q] = blk(q, db, nb);
+    off[q] = has[q] ? (16 * db + 4 * (lane >> 4)) * NS + 16 * nb + (lane & 15) : 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int e = off[q] + r * NS, d = e / NS, n = e % NS;
+      x[q][r] = has[q] && ext != nullptr ? ext[bh * DH * NS + state_off<GLA, DH, NS>(d, n)] : 0.f;
+    }
+  }
+  const float* ag = p.agg + bh * p.nC * DH * NS;
+  const float* tt = p.tot + bh * p.nC;
+  const int cnt = BWD ? p.nC - 1 - c : c;
+  for (int k0 = 0; k0 < cnt; k0 += kBatch) {
+    float tv[kBatch];
+    f32x4_t v[kBatch][NX];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      int j = BWD ? p.nC - 1 - (k0 + k) : k0 + k;
+      j = j < 0 ? 0 : (j > p.nC - 1 ? p.nC - 1 : j);
+      tv[k] = tt[j];
+#pragma unroll
+      for (int q = 0; q < NX; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[k][q][r] = ag[(int64_t)j * DH * NS + off[q] + r * NS];
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const bool ok = k0 + k < cnt;
+#pragma unroll
+      for (int q = 0; q < NX; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[q][r] = ok && has[q] ? tv[k] * x[q][r] + v[k][q][r] : x[q][r];
+    }
+  }
+}
+
 // ------------------------------------------------------------------ direct mode
 // Short sequences (nC <= kDirectMaxChunks): one workgroup per chunk forms the
 // state entering its chunk (forward) or the adjoint leaving it (backward)
@@ -354,7 +423,6 @@ __global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
 // (m31, w, gam and tot of chunk j as in step_scalars).  Wave w takes chunks
 // w, w + 4, ... of the range and accumulates every 16x16 block of the state;
 // the four partial sums are added in a fixed order (deterministic).
-enum Mode { kWhole = 0, kPipe = 1, kDirect = 2 };
 // The sum costs each workgroup up to nC - 1 chunks of extra reads; measured on
 // MI355X (B3 H12 Dh64), it beats the two extra launches of the pipelined mode
 // at 2 and 4 chunks and loses from 8 chunks on.
@@ -395,7 +463,8 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
     coef[jj] = 0.f;
     if (j < j1) {
       const int64_t row0 = (int64_t)b * p.L + (int64_t)j * Q;
-      const float xv = lane < Q ? bf_val(p.delta[(row0 + lane) * rowH + h]) : neutral;
+      const float xl = bf_val(p.delta[(row0 + (lane & (Q - 1))) * rowH + h]);   // unconditional load
+      const float xv = lane < Q ? xl : neutral;
       const StepScalars sc = step_scalars<GLA>(xv, a, lane);
       coef[jj] = BWD ? sc.gam : sc.m31 * sc.w;
       if (lane == 0) s.tot[j - j0] = sc.tot;
@@ -551,8 +620,9 @@ union FwdShared<DH, NS, true> {
 };
 
 // One chunk per workgroup with the entering state from checkpoint slot c - 1
-// (kPipe, written by pass_kernel) or from the direct sum (kDirect); or a run of
-// R = nC chunks per workgroup carrying the state in registers (kWhole).
+// (kPipe, written by pass_kernel), from the direct sum (kDirect) or from the
+// aggregates (kSum); or a run of R = nC chunks per workgroup carrying the
+// state in registers (kWhole).
 template <int DH, int NS, int MODE, bool GLA>
 __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
   using K = Cfg<DH, NS>;
@@ -567,7 +637,9 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
     if (!id.valid) return;
     h = id.h, b = id.b, cbeg = id.c;
   }
-  const int cend = min(cbeg + p.R, p.nC);
+  // one chunk per workgroup except in the whole-head mode (a visible single
+  // iteration keeps the compiler from hoisting addresses out of the loop)
+  const int cend = MODE == kWhole ? min(cbeg + p.R, p.nC) : cbeg + 1;
   const float a = head_rate<GLA>(p, h);
   const int64_t rowH = p.H;
 
@@ -593,7 +665,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
   const bool from_h0 = cbeg == 0;
   const float* hsrc = !from_h0 ? p.ckpt + (((int64_t)b * p.H + h) * p.nC + cbeg - 1) * DH * NS
                                : (p.h0 != nullptr ? p.h0 + ((int64_t)b * p.H + h) * DH * NS : nullptr);
-  if (MODE != kDirect && hsrc != nullptr) {
+  if (MODE != kDirect && MODE != kSum && hsrc != nullptr) {
 #pragma unroll
     for (int jj = 0; jj < K::NBW; ++jj) {
       const int j = w + 4 * jj;
@@ -627,7 +699,34 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
         bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Bm + g) : u16x8_t{};
         cv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Cm + g) : u16x8_t{};
       }
-      if (tid < Q) xv = bf_val(p.delta[(row0 + tid) * rowH + h]);
+      // unconditional (in-bounds) load, so no branch waits on it
+      xv = bf_val(p.delta[(row0 + (tid & (Q - 1))) * rowH + h]);
+      // (kSum: the aggregate loads go out behind the chunk's own loads)
+      if constexpr (MODE == kSum) {
+        // entering state from the aggregates; this workgroup writes checkpoint
+        // slot c - 1 (its entering state) and the last one also slot nC - 1
+        const int64_t bh = (int64_t)b * p.H + h;
+        agg_sum<DH, NS, GLA, false>(p, cbeg, bh, lane, [&](int q, int& db, int& nb) {
+          const int j = w + 4 * q;
+          db = j / K::NBN, nb = j % K::NBN;
+          return j < K::NB;
+        }, hst);
+        const float* ag_last = p.agg + (bh * p.nC + p.nC - 1) * DH * NS;
+        const float t_last = p.tot[bh * p.nC + p.nC - 1];
+#pragma unroll
+        for (int jj = 0; jj < K::NBW; ++jj) {
+          const int j = w + 4 * jj;
+          if (j < K::NB) {
+            const int db = j / K::NBN, nb = j % K::NBN;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int e = (16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15);
+              if (cbeg > 0) p.ckpt[(bh * p.nC + cbeg - 1) * DH * NS + e] = hst[jj][r];
+              if (cbeg == p.nC - 1) p.ckpt[(bh * p.nC + cbeg) * DH * NS + e] = t_last * hst[jj][r] + ag_last[e];
+            }
+          }
+        }
+      }
 #pragma unroll
       for (int v = 0; v < UV; ++v) {
         const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
@@ -654,7 +753,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
       if (lane < Q) {
         sm.cd[lane] = sc.cd;
         sm.gam[lane] = sc.gam;
-        if constexpr (MODE != kPipe) sm.wend[lane] = sc.m31 * sc.w;
+        if constexpr (MODE != kPipe && MODE != kSum) sm.wend[lane] = sc.m31 * sc.w;
       }
     }
 #pragma unroll
@@ -692,7 +791,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
         sm.W_hi[t][s] = hi;
         sm.W_lo[t][s] = lo;
       }
-    } else if constexpr (MODE != kPipe) {
+    } else if constexpr (MODE != kPipe && MODE != kSum) {
       for (int i = tid - 64; i < Q * NS; i += 192) {
         const int n = i / Q, s = i % Q;
         uint16_t hi, lo;
@@ -726,7 +825,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
       }
     }
     // ---- h_end = gam_31 h_in + U^T (m31 o w o B): every wave, its blocks; checkpoint
-    if constexpr (MODE == kPipe) break;
+    if constexpr (MODE == kPipe || MODE == kSum) break;
     const float Gam = sm.gam[Q - 1];
 #pragma unroll
     for (int jj = 0; jj < K::NBW; ++jj) {
@@ -757,6 +856,10 @@ int launch_fwd(const ChunkArgs& p, int64_t B, hipStream_t s) {
     hipLaunchKernelGGL((pass_kernel<DH, NS, GLA>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0, s, p, 0);
     if (int rc = check_launch("chunked forward state pass")) return rc;
     hipLaunchKernelGGL((fwd_kernel<DH, NS, kPipe, GLA>), chunk_grid(p), dim3(256), 0, s, p);
+  } else if (p.mode == kSum) {   // R == 1
+    hipLaunchKernelGGL((agg_kernel<DH, NS, GLA>), chunk_grid(p), dim3(kAggThreads), 0, s, p, 0);
+    if (int rc = check_launch("chunked forward aggregates")) return rc;
+    hipLaunchKernelGGL((fwd_kernel<DH, NS, kSum, GLA>), chunk_grid(p), dim3(256), 0, s, p);
   } else if (p.mode == kDirect) {   // R == 1
     if constexpr (DH * NS <= kDirectMaxState)
       hipLaunchKernelGGL((fwd_kernel<DH, NS, kDirect, GLA>), chunk_grid(p), dim3(256), 0, s, p);

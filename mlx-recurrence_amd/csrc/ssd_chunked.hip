@@ -34,6 +34,7 @@ using rr::chunked::Q;
 using rr::chunked::r32row;
 using rr::chunked::kDirect;
 using rr::chunked::kPipe;
+using rr::chunked::kSum;
 using rr::chunked::kWhole;
 
 }  // namespace
@@ -97,10 +98,11 @@ namespace {
 // columns as register fragments straight from global memory instead of the
 // transposed LDS copies (GYT, LM, LMT, HT), which keeps its LDS small enough
 // for three workgroups per CU.
-template <int DH, int NS, bool CARRY>
+template <int DH, int NS, bool CARRY, bool SUM>
 struct BwdSmem {
   static constexpr int PD = DH + 8, PN = NS + 8;
   static constexpr int TD = CARRY ? DH : 1, TN = CARRY ? NS : 1;
+  float LS[SUM ? DH : 1][NS + 4];  // kSum: the summed lam [d][n], read back as register fragments
   uint16_t Bn[Q][PN];
   uint16_t Cn[Q][PN];
   uint16_t BT[NS][PQ];
@@ -137,11 +139,11 @@ struct BwdSmem {
 
 template <int DH, int NS, int MODE>
 union BwdShared {
-  BwdSmem<DH, NS, MODE != kPipe> m;
+  BwdSmem<DH, NS, MODE != kPipe && MODE != kSum, MODE == kSum> m;
 };
 template <int DH, int NS>
 union BwdShared<DH, NS, kDirect> {
-  BwdSmem<DH, NS, true> m;
+  BwdSmem<DH, NS, true, false> m;
   rr::chunked::DirectSmem<DH, NS, true> d;
 };
 
@@ -149,9 +151,13 @@ union BwdShared<DH, NS, kDirect> {
 // from the direct sum (kDirect); or a whole head per workgroup, lam carried
 // backwards in registers (kWhole).
 template <int DH, int NS, int MODE>
-__global__ __launch_bounds__(256, MODE == kPipe ? 3 : 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
+__global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
   using K = Cfg<DH, NS>;
-  constexpr bool PIPE = MODE == kPipe;
+  // PIPE: one chunk per workgroup with lam from the workspace (kPipe) or summed
+  // from the aggregates (kSum, SUM); the operands of du and of GH / UL are
+  // register fragments
+  constexpr bool SUM = MODE == kSum;
+  constexpr bool PIPE = MODE == kPipe || SUM;
   __shared__ BwdShared<DH, NS, MODE> smu;
   auto& m = smu.m;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -193,9 +199,9 @@ __global__ __launch_bounds__(256, MODE == kPipe ? 3 : 2) void ssd2_bwd_kernel(rr
   // the adjoint entering chunk c - 1 is needed for the whole head, and for
   // the initial-state gradient at chunk 0
   const bool carry = MODE == kWhole || (MODE == kDirect && cbeg == 0 && p.dh0 != nullptr);
-  const float* lsrc = PIPE ? p.agg + (((int64_t)b * p.H + h) * p.nC + cbeg) * DH * NS
-                           : (p.dfinal != nullptr ? p.dfinal + sbase : nullptr);
-  if (MODE != kDirect && lsrc != nullptr) {
+  const float* lsrc = MODE == kPipe ? p.agg + (((int64_t)b * p.H + h) * p.nC + cbeg) * DH * NS
+                                    : (p.dfinal != nullptr ? p.dfinal + sbase : nullptr);
+  if (MODE != kDirect && !SUM && lsrc != nullptr) {
 #pragma unroll
     for (int jj = 0; jj < K::NBW; ++jj) {
       const int j = w + 4 * jj;
@@ -245,7 +251,8 @@ __global__ __launch_bounds__(256, MODE == kPipe ? 3 : 2) void ssd2_bwd_kernel(rr
         gv[v] = i < Q * DH / 4 ? *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0)
                                : make_float4(0.f, 0.f, 0.f, 0.f);
       }
-      if (w == 0 && lane < Q) dv = bf_val(p.delta[(row0 + lane) * rowH + h]);
+      // unconditional (in-bounds) load, so no branch waits on it
+      dv = bf_val(p.delta[(row0 + (lane & (Q - 1))) * rowH + h]);   // lanes >= 32 masked at use
       const float* hsrc = c > 0 ? p.ckpt + (((int64_t)b * p.H + h) * p.nC + (c - 1)) * DH * NS
                                 : (p.h0 != nullptr ? p.h0 + sbase : nullptr);
       if constexpr (PIPE) {
@@ -256,6 +263,7 @@ __global__ __launch_bounds__(256, MODE == kPipe ? 3 : 2) void ssd2_bwd_kernel(rr
             const int task = (w - 2) + 2 * q;
             const int kind = task / NBN, nb = task % NBN;
             const float* src = kind == 0 ? hsrc : lsrc;
+            if (SUM && kind == 1) continue;   // from LDS after the staging barrier
 #pragma unroll
             for (int kb = 0; kb < DH / 16; ++kb)
 #pragma unroll
@@ -274,6 +282,32 @@ __global__ __launch_bounds__(256, MODE == kPipe ? 3 : 2) void ssd2_bwd_kernel(rr
           const int db = j / NBN, nb = j % NBN;
 #pragma unroll
           for (int r = 0; r < 4; ++r) hin[jj][r] = hsrc[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)];
+        }
+      }
+      // kSum: lam from the aggregates (their loads go out behind the chunk's own)
+      if constexpr (SUM) {
+        const int64_t bh = (int64_t)b * p.H + h;
+        rr::chunked::agg_sum<DH, NS, false, true>(p, cbeg, bh, lane, [&](int q, int& db, int& nb) {
+          const int j = w + 4 * q;
+          db = j / NBN, nb = j % NBN;
+          return j < K::NB;
+        }, lam);
+        // the summed lam for the register fragments (read after the staging barrier)
+        // and, at chunk 0, dh0 = tot_0 lam_0 + G_0
+        const float* g0 = p.agg + bh * p.nC * DH * NS;
+        const float t0 = p.tot[bh * p.nC];
+#pragma unroll
+        for (int jj = 0; jj < K::NBW; ++jj) {
+          const int j = w + 4 * jj;
+          if (j < K::NB) {
+            const int db = j / NBN, nb = j % NBN;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
+              m.LS[d][n] = lam[jj][r];
+              if (cbeg == 0 && p.dh0 != nullptr) p.dh0[sbase + d * NS + n] = t0 * lam[jj][r] + g0[d * NS + n];
+            }
+          }
         }
       }
       // LDS writes
@@ -314,7 +348,7 @@ __global__ __launch_bounds__(256, MODE == kPipe ? 3 : 2) void ssd2_bwd_kernel(rr
         }
       }
       if (w == 0) {
-        const float cdv = prefix32(dv, lane);
+        const float cdv = prefix32(lane < Q ? dv : 0.f, lane);
         const float c31 = __shfl(cdv, 31);
         if (lane < Q) {
           const float gt = __expf(a * cdv), mt = __expf(a * (c31 - cdv));
@@ -373,6 +407,12 @@ __global__ __launch_bounds__(256, MODE == kPipe ? 3 : 2) void ssd2_bwd_kernel(rr
       for (int q = 0; q < TPW; ++q) {
         const int task = (w - 2) + 2 * q;
         const int kind = task / NBN, nb = task % NBN;
+        if (SUM && kind == 1) {
+#pragma unroll
+          for (int kb = 0; kb < DH / 16; ++kb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pcol[q][kb][e] = m.LS[16 * kb + 4 * l4 + e][16 * nb + l15];
+        }
         u16x4_t bh[DH / 16], bl[DH / 16];
 #pragma unroll
         for (int kb = 0; kb < DH / 16; ++kb) rr::bf_split4(pcol[q][kb], bh[kb], bl[kb]);
@@ -458,7 +498,7 @@ __global__ __launch_bounds__(256, MODE == kPipe ? 3 : 2) void ssd2_bwd_kernel(rr
             pdy[kb][e] = p.dy[((row0 + 16 * kb + 8 * (lane >> 5) + e) * rowH + h) * DH + d];
 #pragma unroll
         for (int kb = 0; kb < NS / 16; ++kb) {
-          const float* src = lsrc + d * NS + 16 * kb + 8 * (lane >> 5);
+          const float* src = SUM ? &m.LS[d][16 * kb + 8 * (lane >> 5)] : lsrc + d * NS + 16 * kb + 8 * (lane >> 5);
           const float4 l0 = *reinterpret_cast<const float4*>(src), l1 = *reinterpret_cast<const float4*>(src + 4);
           plm[kb][0] = l0.x, plm[kb][1] = l0.y, plm[kb][2] = l0.z, plm[kb][3] = l0.w;
           plm[kb][4] = l1.x, plm[kb][5] = l1.y, plm[kb][6] = l1.z, plm[kb][7] = l1.w;
@@ -739,6 +779,11 @@ int launch_bwd(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
                        p, 1);
     if (int rc = rr::check_launch("ssd chunked backward adjoint pass")) return rc;
     hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, kPipe>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
+  } else if (p.mode == kSum) {   // R == 1
+    hipLaunchKernelGGL((rr::chunked::agg_kernel<DH, NS, false>), rr::chunked::chunk_grid(p),
+                       dim3(rr::chunked::kAggThreads), 0, s, p, 1);
+    if (int rc = rr::check_launch("ssd chunked backward aggregates")) return rc;
+    hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, kSum>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
   } else if (p.mode == kDirect) {   // R == 1
     if constexpr (DH * NS <= rr::chunked::kDirectMaxState)
       hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, kDirect>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
@@ -763,11 +808,14 @@ int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N) {
   // (B * H < 512 keeps the 1-D per-chunk grid below 2^31 for any nC < 2^22)
   if (B * H >= 512 || nC >= ((int64_t)1 << 22)) return chunked::kWhole;
   if (nC <= chunked::kDirectMaxChunks && Dh * N <= chunked::kDirectMaxState) return chunked::kDirect;
+  // the aggregate-sum mode where the backward's small-N kernel takes it
+  if (nC <= chunked::kSumMaxChunks && N <= 32) return chunked::kSum;
   return chunked::kPipe;
 }
 
 // Workspace layout (floats, each part 256-byte aligned): per-chunk decays
-// [B,H,nC] (pipelined), dA partials [B,H,nR,N] (backward), backward chunk
+// [B,H,nC] (pipelined and sum modes), chunk aggregates [B,H,nC,Dh,N] (sum
+// mode, both passes), dA partials [B,H,nR,N] (backward), backward chunk
 // aggregates / adjoints [B,H,nC,Dh,N] (pipelined backward).
 namespace {
 int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }
@@ -775,8 +823,9 @@ int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }
 
 size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int mode, int64_t Dh, int64_t N, int pass) {
   const int64_t nR = mode == chunked::kWhole ? 1 : nC;
-  const bool pipe = mode == chunked::kPipe;
-  int64_t f = pipe ? align64(B * H * nC) : 0;
+  const bool pipe = mode == chunked::kPipe, sum = mode == chunked::kSum;
+  int64_t f = pipe || sum ? align64(B * H * nC) : 0;
+  if (sum) f += align64(B * H * nC * Dh * N);
   if (pass == 1) {
     f += align64(B * H * nR * N);
     if (pipe) f += align64(B * H * nC * Dh * N);
@@ -787,9 +836,10 @@ size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int mode, int64_t Dh, int
 void ssd2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass) {
   float* f = static_cast<float*>(ws);
   const int64_t nR = (a.nC + a.R - 1) / a.R;
-  const bool pipe = a.mode == chunked::kPipe;
+  const bool pipe = a.mode == chunked::kPipe, sum = a.mode == chunked::kSum;
   a.tot = a.ws = a.agg = nullptr;
-  if (pipe) { a.tot = f; f += align64(B * a.H * a.nC); }
+  if (pipe || sum) { a.tot = f; f += align64(B * a.H * a.nC); }
+  if (sum) { a.agg = f; f += align64(B * a.H * a.nC * a.DH * a.NS); }
   if (pass == 1) {
     a.ws = f; f += align64(B * a.H * nR * a.NS);
     if (pipe) a.agg = f;
