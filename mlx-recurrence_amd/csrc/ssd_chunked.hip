@@ -741,21 +741,29 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
 }
 
 // dA[h, n] = sum over batch rows and runs of the per-run partials, in a fixed
-// order: one workgroup per head, thread (g, n) sums partials g, g + G, ...,
-// then the G per-thread sums are added in order.
-__global__ __launch_bounds__(256) void ssd2_dA_kernel(const float* __restrict__ part, float* __restrict__ dA,
-                                                      int Bsz, int H, int nR, int NS) {
-  __shared__ float red[256];
-  const int h = blockIdx.x, G = 256 / NS, n = threadIdx.x % NS, g = threadIdx.x / NS;
+// order: one workgroup per head, thread (g, n) sums partials g, g + G, ... in
+// four interleaved accumulators (four loads in flight), then the G per-thread
+// sums are added in order.
+template <int T>
+__global__ __launch_bounds__(T) void ssd2_dA_kernel(const float* __restrict__ part, float* __restrict__ dA, int Bsz,
+                                                    int H, int nR, int NS) {
+  __shared__ float red[T];
+  const int h = blockIdx.x, G = T / NS, n = threadIdx.x % NS, g = threadIdx.x / NS;
   const int parts = Bsz * nR;
-  float s = 0.f;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
   if (g < G) {
-    for (int i = g; i < parts; i += G) {
-      const int b = i / nR, r = i % nR;
-      s += part[(((int64_t)b * H + h) * nR + r) * NS + n];
+    for (int i0 = g; i0 < parts; i0 += 4 * G) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int i = i0 + q * G;
+        if (i < parts) {
+          const int b = i / nR, r = i % nR;
+          acc[q] += part[(((int64_t)b * H + h) * nR + r) * NS + n];
+        }
+      }
     }
   }
-  red[threadIdx.x] = s;
+  red[threadIdx.x] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   __syncthreads();
   if (threadIdx.x < NS) {
     float t = 0.f;
@@ -766,7 +774,11 @@ __global__ __launch_bounds__(256) void ssd2_dA_kernel(const float* __restrict__ 
 
 int launch_dA(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
   const int nR = p.mode == kWhole ? 1 : p.nC;
-  hipLaunchKernelGGL(ssd2_dA_kernel, dim3(p.H), dim3(256), 0, s, p.ws, p.dA, (int)B, p.H, nR, p.NS);
+  // (a larger workgroup only where there are many partials to sum)
+  if ((int64_t)B * nR * p.NS > 64 * 1024)
+    hipLaunchKernelGGL(ssd2_dA_kernel<1024>, dim3(p.H), dim3(1024), 0, s, p.ws, p.dA, (int)B, p.H, nR, p.NS);
+  else
+    hipLaunchKernelGGL(ssd2_dA_kernel<256>, dim3(p.H), dim3(256), 0, s, p.ws, p.dA, (int)B, p.H, nR, p.NS);
   return rr::check_launch("ssd chunked backward dA");
 }
 
@@ -804,9 +816,16 @@ bool ssd2_bwd_supported(int64_t Dh, int64_t N) {
   return (Dh == 32 || Dh == 64) && (N == 16 || N == 32 || N == 64 || N == 128);
 }
 
-int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N) {
-  // (B * H < 512 keeps the 1-D per-chunk grid below 2^31 for any nC < 2^22)
-  if (B * H >= 512 || nC >= ((int64_t)1 << 22)) return chunked::kWhole;
+int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N, int pass) {
+  const int64_t grid = nC * ((B * H + chunked::kXcds - 1) / chunked::kXcds * chunked::kXcds);
+  if (grid >= ((int64_t)1 << 31)) return chunked::kWhole;   // beyond a 1-D per-chunk grid
+  if (B * H >= 512) {
+    // Enough heads to fill the GPU with whole heads.  The backward of a large
+    // state (one workgroup per CU) is faster pipelined: at B8 H80 Dh64 N128
+    // L4096 (config 4) 5.1 ms pipelined against 7.5 ms whole-head on MI355X,
+    // while the whole-head forward (2.3 ms) beats the pipelined one (4.0 ms).
+    return pass == 1 && Dh * N > chunked::kDirectMaxState ? chunked::kPipe : chunked::kWhole;
+  }
   if (nC <= chunked::kDirectMaxChunks && Dh * N <= chunked::kDirectMaxState) return chunked::kDirect;
   // the aggregate-sum mode where the backward's small-N kernel takes it
   if (nC <= chunked::kSumMaxChunks && N <= 32) return chunked::kSum;

@@ -554,7 +554,7 @@ extern "C" size_t rr_ssd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_
                                          int64_t seg, int64_t A_stride_n, int dtype, int pass) {
   if (B <= 0 || L <= 0 || H <= 0 || Dh <= 0 || N <= 0 || rr::chunk_len(L, seg) == 0) return 0;
   if (rr::ssd2_supported(dtype, L, seg, Dh, N, A_stride_n) && (pass == 0 || rr::ssd2_bwd_supported(Dh, N)))
-    return rr::ssd2_ws_bytes(B, H, L / 32, rr::chunked_mode(B, H, L / 32, Dh, N), Dh, N, pass);
+    return rr::ssd2_ws_bytes(B, H, L / 32, rr::chunked_mode(B, H, L / 32, Dh, N, pass), Dh, N, pass);
   const Plan q = make_plan(B, L, H, Dh, N, seg);
   return pass == 0 ? q.fwd_bytes : q.bwd_bytes;
 }
@@ -582,7 +582,7 @@ extern "C" int rr_ssd_fwd(const void* u, const void* delta, const void* Bm, cons
     a.y = y;
     a.ckpt = ckpt;
     a.B = (int)B; a.L = (int)L; a.H = (int)H; a.DH = (int)Dh; a.NS = (int)N; a.nC = (int)(L / 32);
-    a.mode = rr::chunked_mode(B, H, a.nC, Dh, N);
+    a.mode = rr::chunked_mode(B, H, a.nC, Dh, N, 0);
     a.R = a.mode == 0 ? a.nC : 1;
     const size_t need = rr::ssd2_ws_bytes(B, H, a.nC, a.mode, Dh, N, 0);
     if (need && (!workspace || workspace_bytes < need))
@@ -628,7 +628,7 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
     return rr::fail(RR_EINVAL, "ssd_bwd: A_stride_n must be 0 or 1");
   if (rr::ssd2_supported(dtype, L, seg, Dh, N, A_stride_n) && rr::ssd2_bwd_supported(Dh, N)) {
     const int nC = (int)(L / 32);
-    const int mode = rr::chunked_mode(B, H, nC, Dh, N);
+    const int mode = rr::chunked_mode(B, H, nC, Dh, N, 1);
     if (!workspace || workspace_bytes < rr::ssd2_ws_bytes(B, H, nC, mode, Dh, N, 1))
       return rr::fail(RR_EWORKSPACE, "ssd_bwd: workspace too small");
     rr::ChunkArgs a{};
