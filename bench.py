@@ -349,6 +349,12 @@ WORKLOADS = {
     "rotlru": ("rotlru_scan fwd+bwd (BASELINE config 3)", make_rotlru, dict(B=8, L=4096, D=2560, seg=32)),
     "ssd_c4": ("ssd_scan fwd+bwd (BASELINE config 4)", make_ssd,
                dict(B=8, L=4096, H=80, Dh=64, N=128, seg=32)),
+    # configs 1 and 2 with 32x the batch: the same kernels with the GPU filled
+    # (at B = 3 the passes are latency-bound), reported beside the headline
+    "ssd_b96": ("ssd_scan fwd+bwd (BASELINE config 1 shape, B = 96)", make_ssd,
+                dict(B=96, L=512, H=12, Dh=64, N=16, seg=32)),
+    "gla_b96": ("gla_scan fwd+bwd (BASELINE config 2 shape, B = 96)", make_gla,
+                dict(B=96, L=512, H=12, Dh=64, seg=32)),
 }
 
 

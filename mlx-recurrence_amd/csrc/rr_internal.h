@@ -38,11 +38,12 @@ struct ChunkArgs {
 };
 
 // Mode of the SSD chunked kernels for pass 0 (forward) or 1 (backward), B*H
-// heads of nC chunks of a Dh x N state: a whole head per workgroup when the
-// heads alone fill the GPU (not for the backward of states above 64 x 64);
-// else one workgroup per chunk, with the entering states formed directly
-// (nC <= 4, Dh * N <= 64 * 64), from the chunk aggregates (nC <= 16, N <= 32)
-// or by the pipelined aggregate and state-pass kernels.
+// heads of nC chunks of a Dh x N state: a whole head per workgroup for the
+// forward when the heads alone fill the GPU (and for either pass when a 1-D
+// per-chunk grid would exceed 2^31 workgroups); else one workgroup per chunk,
+// with the entering states formed directly (nC <= 4, Dh * N <= 64 * 64), from
+// the chunk aggregates (nC <= 16, N <= 32) or by the pipelined aggregate and
+// state-pass kernels.
 int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N, int pass);
 
 // ------------------------------------------------------------------ SSD

@@ -775,7 +775,7 @@ __global__ __launch_bounds__(T) void ssd2_dA_kernel(const float* __restrict__ pa
 int launch_dA(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
   const int nR = p.mode == kWhole ? 1 : p.nC;
   // (a larger workgroup only where there are many partials to sum)
-  if ((int64_t)B * nR * p.NS > 64 * 1024)
+  if ((int64_t)B * nR * p.NS > 4096)
     hipLaunchKernelGGL(ssd2_dA_kernel<1024>, dim3(p.H), dim3(1024), 0, s, p.ws, p.dA, (int)B, p.H, nR, p.NS);
   else
     hipLaunchKernelGGL(ssd2_dA_kernel<256>, dim3(p.H), dim3(256), 0, s, p.ws, p.dA, (int)B, p.H, nR, p.NS);
@@ -819,13 +819,11 @@ bool ssd2_bwd_supported(int64_t Dh, int64_t N) {
 int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N, int pass) {
   const int64_t grid = nC * ((B * H + chunked::kXcds - 1) / chunked::kXcds * chunked::kXcds);
   if (grid >= ((int64_t)1 << 31)) return chunked::kWhole;   // beyond a 1-D per-chunk grid
-  if (B * H >= 512) {
-    // Enough heads to fill the GPU with whole heads.  The backward of a large
-    // state (one workgroup per CU) is faster pipelined: at B8 H80 Dh64 N128
-    // L4096 (config 4) 5.1 ms pipelined against 7.5 ms whole-head on MI355X,
-    // while the whole-head forward (2.3 ms) beats the pipelined one (4.0 ms).
-    return pass == 1 && Dh * N > chunked::kDirectMaxState ? chunked::kPipe : chunked::kWhole;
-  }
+  // Enough heads to fill the GPU: the forward runs whole heads; the backward
+  // stays per chunk (measured on MI355X, fwd / bwd µs, whole-head vs per chunk:
+  // B96 L512 H12 Dh64 N16 137 / 414 vs 194 / 357 (sum mode); B8 L4096 H80
+  // Dh64 N128 2308 / 7457 vs 4025 / 4873 (pipelined)).
+  if (B * H >= 512 && pass == 0) return chunked::kWhole;
   if (nC <= chunked::kDirectMaxChunks && Dh * N <= chunked::kDirectMaxState) return chunked::kDirect;
   // the aggregate-sum mode where the backward's small-N kernel takes it
   if (nC <= chunked::kSumMaxChunks && N <= 32) return chunked::kSum;
