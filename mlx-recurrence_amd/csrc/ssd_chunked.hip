@@ -505,21 +505,43 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
         }
       }
     }
-    if (w == 0) {
-      // P = M o CB, stored transposed [t][t']
+    if (w < 2) {
+      // wave 0: P = M o CB -> P^T [t][t'], and K = M o G2 o delta_s o span [t'][s];
+      // wave 1: M o G2 -> (M o G2)^T [t][t'].  Rows r32row(4g .. 4g + 3) are
+      // consecutive, so the transposed stores are one 8-byte write per group.
       const int s = lane & 31;
-      const float cds = m.cd[s];
+      const float cds = m.cd[s], ds = m.del[s];
+      float md[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int tp = r32row(r, lane);
-        const float v = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * m.CB[tp][s] : 0.f;
-        uint16_t hi, lo;
-        bf_split(v, hi, lo);
-        m.y.PT_hi[s][tp] = hi;
-        m.y.PT_lo[s][tp] = lo;
+        md[r] = s <= tp ? __expf(a * (m.cd[tp] - cds)) : 0.f;
       }
-    } else if (w == 1 || w == 3) {
-      // M o G2 -> (M o G2)^T [t][t'] (wave 1); M o G2 o delta_s and K [t'][s] (wave 3)
+      uint16_t(*dst_hi)[PQ] = w == 0 ? m.y.PT_hi : m.y.MGT_hi;
+      uint16_t(*dst_lo)[PQ] = w == 0 ? m.y.PT_lo : m.y.MGT_lo;
+      const float(*src)[Q + 1] = w == 0 ? m.CB : m.G2;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int tp = r32row(4 * g, lane);
+        u16x4_t hi4, lo4;
+        rr::bf_split4(f32x4_t{md[4 * g] * src[tp][s], md[4 * g + 1] * src[tp + 1][s], md[4 * g + 2] * src[tp + 2][s],
+                              md[4 * g + 3] * src[tp + 3][s]},
+                      hi4, lo4);
+        *reinterpret_cast<u16x4_t*>(&dst_hi[s][tp]) = hi4;
+        *reinterpret_cast<u16x4_t*>(&dst_lo[s][tp]) = lo4;
+      }
+      if (w == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int tp = r32row(r, lane);
+          uint16_t hi, lo;
+          bf_split(md[r] * m.G2[tp][s] * ds * (m.cd[tp] - cds + ds), hi, lo);
+          m.y.Km_hi[tp][s] = hi;
+          m.y.Km_lo[tp][s] = lo;
+        }
+      }
+    } else if (w == 3) {
+      // M o G2 o delta_s [t'][s]
       const int s = lane & 31;
       const float cds = m.cd[s], ds = m.del[s];
 #pragma unroll
@@ -527,18 +549,9 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
         const int tp = r32row(r, lane);
         const float mg = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * m.G2[tp][s] : 0.f;
         uint16_t hi, lo;
-        if (w == 1) {
-          bf_split(mg, hi, lo);
-          m.y.MGT_hi[s][tp] = hi;
-          m.y.MGT_lo[s][tp] = lo;
-        } else {
-          bf_split(mg * ds, hi, lo);
-          m.y.MGd_hi[tp][s] = hi;
-          m.y.MGd_lo[tp][s] = lo;
-          bf_split(mg * ds * (m.cd[tp] - cds + ds), hi, lo);
-          m.y.Km_hi[tp][s] = hi;
-          m.y.Km_lo[tp][s] = lo;
-        }
+        bf_split(mg * ds, hi, lo);
+        m.y.MGd_hi[tp][s] = hi;
+        m.y.MGd_lo[tp][s] = lo;
       }
     } else {
       // R_t = sum_{t' >= t} sum_{s <= t} E[t', s], E = M o delta_s o G2 o CB: prefix
