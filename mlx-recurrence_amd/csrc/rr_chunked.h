@@ -363,8 +363,10 @@ __global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
 //   forward:  x = h0;     x = tot_j x + S_j  for j = 0 .. c - 1
 //   backward: x = dfinal; x = tot_j x + G_j  for j = nC - 1 .. c + 1
 // for this lane's elements of the 16x16 blocks (db(j), nb(j)) listed by
-// `blk` (the caller's register layout: rows 4 (lane / 16) + r, column lane % 16).
-template <int DH, int NS, bool GLA, bool BWD, int NX, typename BLK>
+// `blk`, in the caller's register layout: element r at d = 16 db + 4 (lane / 16)
+// + r, n = 16 nb + lane % 16 (TRANS false), or at d = 16 db + lane % 16,
+// n = 16 nb + 4 (lane / 16) + r (TRANS true).
+template <int DH, int NS, bool GLA, bool BWD, bool TRANS = false, int NX, typename BLK>
 __device__ __forceinline__ void agg_sum(const ChunkArgs& p, int c, int64_t bh, int lane, BLK blk,
                                         f32x4_t (&x)[NX]) {
   constexpr int kBatch = NX == 1 ? 16 : NX == 2 ? 8 : 4;
@@ -377,10 +379,12 @@ __device__ __forceinline__ void agg_sum(const ChunkArgs& p, int c, int64_t bh, i
   for (int q = 0; q < NX; ++q) {
     int db, nb;
     has[q] = blk(q, db, nb);
-    off[q] = has[q] ? (16 * db + 4 * (lane >> 4)) * NS + 16 * nb + (lane & 15) : 0;
+    off[q] = !has[q] ? 0
+             : TRANS ? (16 * db + (lane & 15)) * NS + 16 * nb + 4 * (lane >> 4)
+                     : (16 * db + 4 * (lane >> 4)) * NS + 16 * nb + (lane & 15);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int e = off[q] + r * NS, d = e / NS, n = e % NS;
+      const int e = off[q] + (TRANS ? r : r * NS), d = e / NS, n = e % NS;
       x[q][r] = has[q] && ext != nullptr ? ext[bh * DH * NS + state_off<GLA, DH, NS>(d, n)] : 0.f;
     }
   }
@@ -398,7 +402,7 @@ __device__ __forceinline__ void agg_sum(const ChunkArgs& p, int c, int64_t bh, i
 #pragma unroll
       for (int q = 0; q < NX; ++q)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[k][q][r] = ag[(int64_t)j * DH * NS + off[q] + r * NS];
+        for (int r = 0; r < 4; ++r) v[k][q][r] = ag[(int64_t)j * DH * NS + off[q] + (TRANS ? r : r * NS)];
     }
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
@@ -602,11 +606,9 @@ struct FwdSmem {
   uint16_t BwT_lo[NS][PQ];
   uint16_t W_hi[Q][PQ];                // M o CB^T o w_s  [t][s]
   uint16_t W_lo[Q][PQ];
-  uint16_t H_hi[DH][Cfg<DH, NS>::PN];  // h_in [d][n]
-  uint16_t H_lo[DH][Cfg<DH, NS>::PN];
   float x[Q];      // step input (SSD delta, GLA gate)
   float cd[Q];     // SSD: cumulative delta
-  float gam[Q], wend[Q];
+  float gam[Q];
 };
 
 template <int DH, int NS, bool DIRECT>
@@ -623,12 +625,26 @@ union FwdShared<DH, NS, true> {
 // (kPipe, written by pass_kernel), from the direct sum (kDirect) or from the
 // aggregates (kSum); or a run of R = nC chunks per workgroup carrying the
 // state in registers (kWhole).
+//
+// Wave w owns the state rows d of the 16-row blocks db = w, w + 4, ... and
+// holds them transposed in registers: block (db, nb), element r at
+// n = 16 nb + 4 (lane / 16) + r, d = 16 db + lane % 16 — which is, element for
+// element, the B operand of v_mfma_f32_16x16x16_bf16 contracting over n (the
+// C h_in^T term of Y) and the accumulator of the state update
+// h^T += (m31 o w o B)^T U.  So every wave forms Y and the new state of its
+// rows with no cross-wave sum and no LDS copy of the state:
+//   Y[t, d] = (W U)[t, d] + gam_t (C h_in^T)[t, d],  W = M o C B^T o w_s
+//   h_end^T = gam_31 h_in^T + (m31 o w o B)^T U
 template <int DH, int NS, int MODE, bool GLA>
 __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
   using K = Cfg<DH, NS>;
+  constexpr int NBD = DH / 16, NBN = NS / 16;
+  constexpr int DBW = (NBD + 3) / 4;   // row blocks per wave
+  constexpr bool STATE = MODE == kWhole || MODE == kDirect;   // forms the chunk's end state
   __shared__ FwdShared<DH, NS, MODE == kDirect> smu;
   auto& sm = smu.f;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l15 = lane & 15, l4 = lane >> 4;
   int h, b, cbeg;
   if constexpr (MODE == kWhole) {
     h = blockIdx.y, b = blockIdx.z, cbeg = 0;
@@ -641,52 +657,66 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
   // iteration keeps the compiler from hoisting addresses out of the loop)
   const int cend = MODE == kWhole ? min(cbeg + p.R, p.nC) : cbeg + 1;
   const float a = head_rate<GLA>(p, h);
-  const int64_t rowH = p.H;
+  const int64_t rowH = p.H, bh = (int64_t)b * p.H + h;
 
-  f32x4_t hst[K::NBW];
+  f32x4_t hst[DBW][NBN];   // this wave's rows of the state, transposed blocks
 #pragma unroll
-  for (int jj = 0; jj < K::NBW; ++jj) hst[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < DBW; ++i)
+#pragma unroll
+    for (int nb = 0; nb < NBN; ++nb) hst[i][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   if constexpr (MODE == kDirect) {
     const float gam_all = direct_sum<DH, NS, GLA, false>(p, cbeg, b, h, a, smu.d);
-    const float* h0b = p.h0 != nullptr ? p.h0 + ((int64_t)b * p.H + h) * DH * NS : nullptr;
+    const float* h0b = p.h0 != nullptr ? p.h0 + bh * DH * NS : nullptr;
 #pragma unroll
-    for (int jj = 0; jj < K::NBW; ++jj) {
-      const int j = w + 4 * jj;
-      if (j < K::NB) {
-        const int db = j / K::NBN, nb = j % K::NBN;
+    for (int i = 0; i < DBW; ++i) {
+      const int db = w + 4 * i;
+      if (db < NBD) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          hst[jj][r] = direct_value<DH, NS, GLA, false>(smu.d, gam_all, h0b, 16 * db + 4 * (lane >> 4) + r,
-                                                        16 * nb + (lane & 15));
+        for (int nb = 0; nb < NBN; ++nb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            hst[i][nb][r] = direct_value<DH, NS, GLA, false>(smu.d, gam_all, h0b, 16 * db + l15, 16 * nb + 4 * l4 + r);
       }
     }
     __syncthreads();   // the chunk below reuses the LDS of the sum
-  }
-  const bool from_h0 = cbeg == 0;
-  const float* hsrc = !from_h0 ? p.ckpt + (((int64_t)b * p.H + h) * p.nC + cbeg - 1) * DH * NS
-                               : (p.h0 != nullptr ? p.h0 + ((int64_t)b * p.H + h) * DH * NS : nullptr);
-  if (MODE != kDirect && MODE != kSum && hsrc != nullptr) {
+  } else if constexpr (MODE == kPipe || MODE == kWhole) {
+    // entering state: checkpoint slot c - 1 ([d][n], four consecutive n per
+    // lane: one 16-byte load) or h0
+    const bool from_h0 = cbeg == 0;
+    const float* hsrc = !from_h0 ? p.ckpt + (bh * p.nC + cbeg - 1) * DH * NS
+                                 : (p.h0 != nullptr ? p.h0 + bh * DH * NS : nullptr);
+    if (hsrc != nullptr) {
 #pragma unroll
-    for (int jj = 0; jj < K::NBW; ++jj) {
-      const int j = w + 4 * jj;
-      if (j < K::NB) {
-        const int db = j / K::NBN, nb = j % K::NBN;
+      for (int i = 0; i < DBW; ++i) {
+        const int db = w + 4 * i;
+        if (db < NBD) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
-          hst[jj][r] = hsrc[from_h0 ? state_off<GLA, DH, NS>(d, n) : d * NS + n];
+          for (int nb = 0; nb < NBN; ++nb) {
+            const int d = 16 * db + l15, n0 = 16 * nb + 4 * l4;
+            if (from_h0) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) hst[i][nb][r] = hsrc[state_off<GLA, DH, NS>(d, n0 + r)];
+            } else {
+              const float4 v = *reinterpret_cast<const float4*>(hsrc + d * NS + n0);
+              hst[i][nb] = f32x4_t{v.x, v.y, v.z, v.w};
+            }
+          }
         }
       }
     }
   }
 
   for (int c = cbeg; c < cend; ++c) {
+    // a fresh copy of the thread index per chunk keeps the compiler from
+    // hoisting every per-lane address of the body out of the chunk loop
+    int tidv = tid;
+    if constexpr (MODE == kWhole) asm volatile("" : "+v"(tidv));
+    const int tid = tidv, lane = tidv & 63, l15 = lane & 15, l4 = lane >> 4;
     const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;  // first (b, t) row of the chunk
     // ---- stage the chunk's inputs (all loads issued before any use)
     {
       constexpr int UV = (Q * DH / 8 + 255) / 256, BV = (Q * NS / 8 + 255) / 256;
       u16x8_t uv[UV], bv[BV], cv[BV];
-      float xv = 0.f;
 #pragma unroll
       for (int v = 0; v < UV; ++v) {
         const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
@@ -700,29 +730,33 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
         cv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Cm + g) : u16x8_t{};
       }
       // unconditional (in-bounds) load, so no branch waits on it
-      xv = bf_val(p.delta[(row0 + (tid & (Q - 1))) * rowH + h]);
-      // (kSum: the aggregate loads go out behind the chunk's own loads)
+      const float xv = bf_val(p.delta[(row0 + (tid & (Q - 1))) * rowH + h]);
       if constexpr (MODE == kSum) {
-        // entering state from the aggregates; this workgroup writes checkpoint
-        // slot c - 1 (its entering state) and the last one also slot nC - 1
-        const int64_t bh = (int64_t)b * p.H + h;
-        agg_sum<DH, NS, GLA, false>(p, cbeg, bh, lane, [&](int q, int& db, int& nb) {
-          const int j = w + 4 * q;
-          db = j / K::NBN, nb = j % K::NBN;
-          return j < K::NB;
-        }, hst);
+        // entering state from the aggregates (their loads go out behind the
+        // chunk's own); this workgroup writes checkpoint slot c - 1 (its
+        // entering state) and the last one also slot nC - 1
+        agg_sum<DH, NS, GLA, false, true>(p, cbeg, bh, lane, [&](int q, int& db, int& nb) {
+          db = w + 4 * (q / NBN), nb = q % NBN;
+          return db < NBD;
+        }, reinterpret_cast<f32x4_t(&)[DBW * NBN]>(hst));
         const float* ag_last = p.agg + (bh * p.nC + p.nC - 1) * DH * NS;
         const float t_last = p.tot[bh * p.nC + p.nC - 1];
 #pragma unroll
-        for (int jj = 0; jj < K::NBW; ++jj) {
-          const int j = w + 4 * jj;
-          if (j < K::NB) {
-            const int db = j / K::NBN, nb = j % K::NBN;
+        for (int i = 0; i < DBW; ++i) {
+          const int db = w + 4 * i;
+          if (db < NBD) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int e = (16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15);
-              if (cbeg > 0) p.ckpt[(bh * p.nC + cbeg - 1) * DH * NS + e] = hst[jj][r];
-              if (cbeg == p.nC - 1) p.ckpt[(bh * p.nC + cbeg) * DH * NS + e] = t_last * hst[jj][r] + ag_last[e];
+            for (int nb = 0; nb < NBN; ++nb) {
+              const int e = (16 * db + l15) * NS + 16 * nb + 4 * l4;
+              const f32x4_t v = hst[i][nb];
+              if (cbeg > 0)
+                *reinterpret_cast<float4*>(p.ckpt + (bh * p.nC + cbeg - 1) * DH * NS + e) =
+                    make_float4(v[0], v[1], v[2], v[3]);
+              if (cbeg == p.nC - 1) {
+                const float4 g = *reinterpret_cast<const float4*>(ag_last + e);
+                *reinterpret_cast<float4*>(p.ckpt + (bh * p.nC + cbeg) * DH * NS + e) =
+                    make_float4(t_last * v[0] + g.x, t_last * v[1] + g.y, t_last * v[2] + g.z, t_last * v[3] + g.w);
+              }
             }
           }
         }
@@ -746,34 +780,15 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
       if (tid < Q) sm.x[tid] = xv;
     }
     __syncthreads();
-    // ---- per-step scalars (wave 0) and h_in split (every wave, its blocks)
+    // ---- step scalars (every wave; lanes s and s + 32 hold step s);
+    // W = M o C B^T o w_s (wave 0); (m31 o w o B)^T (the other waves)
+    const StepScalars sc = step_scalars<GLA>(sm.x[lane & (Q - 1)], a, lane);
     if (w == 0) {
-      const float xv = lane < Q ? sm.x[lane] : (GLA ? 1.f : 0.f);
-      const StepScalars sc = step_scalars<GLA>(xv, a, lane);
       if (lane < Q) {
         sm.cd[lane] = sc.cd;
         sm.gam[lane] = sc.gam;
-        if constexpr (MODE != kPipe && MODE != kSum) sm.wend[lane] = sc.m31 * sc.w;
       }
-    }
-#pragma unroll
-    for (int jj = 0; jj < K::NBW; ++jj) {
-      const int j = w + 4 * jj;
-      if (j < K::NB) {
-        const int db = j / K::NBN, nb = j % K::NBN;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          uint16_t hi, lo;
-          bf_split(hst[jj][r], hi, lo);
-          const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
-          sm.H_hi[d][n] = hi;
-          sm.H_lo[d][n] = lo;
-        }
-      }
-    }
-    __syncthreads();
-    // ---- W = M o CB^T o w_s (wave 0); (m31 o w o B)^T (waves 1..3)
-    if (w == 0) {
+      wave_lds_sync();   // cd for the decays below
       f32x16_t cb = {};
 #pragma unroll
       for (int kb = 0; kb < NS / 16; ++kb)
@@ -782,69 +797,68 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
       const int s = lane & 31;
       float m[16];
       decay_block32<GLA>(GLA ? sm.x : sm.cd, a, lane, m);
-      const float ws = GLA ? 1.f : sm.x[s];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int t = r32row(r, lane);
         uint16_t hi, lo;
-        bf_split(m[r] * ws * cb[r], hi, lo);
+        bf_split(m[r] * sc.w * cb[r], hi, lo);
         sm.W_hi[t][s] = hi;
         sm.W_lo[t][s] = lo;
       }
-    } else if constexpr (MODE != kPipe && MODE != kSum) {
+    } else if constexpr (STATE) {
+      // lane s (and s + 32) weights column s; 192 threads cover Q x NS
+      const float wend = sc.m31 * sc.w;
       for (int i = tid - 64; i < Q * NS; i += 192) {
         const int n = i / Q, s = i % Q;
         uint16_t hi, lo;
-        bf_split(sm.wend[s] * bf_val(sm.B[s][n]), hi, lo);
+        bf_split(wend * bf_val(sm.B[s][n]), hi, lo);
         sm.BwT_hi[n][s] = hi;
         sm.BwT_lo[n][s] = lo;
       }
     }
     __syncthreads();
-    // ---- Y blocks (waves < DH/32)
-    if (w < K::NYB) {
-      const int d0 = 32 * w;
-      f32x16_t yi = {}, ye = {};
+    // ---- Y and the end state of this wave's rows
+    const float Gam = sc.tot;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const u16x8_t fb = frag(&sm.Ut[d0 + (lane & 31)][16 * kb + 8 * (lane >> 5)]);
-        yi = mfma32(frag(&sm.W_hi[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, yi);
-        yi = mfma32(frag(&sm.W_lo[lane & 31][16 * kb + 8 * (lane >> 5)]), fb, yi);
-      }
+    for (int i = 0; i < DBW; ++i) {
+      const int db = w + 4 * i;
+      if (db >= NBD) continue;
+      u16x4_t hh[NBN], hl[NBN];
 #pragma unroll
-      for (int kb = 0; kb < NS / 16; ++kb) {
-        const u16x8_t fa = frag(&sm.C[lane & 31][16 * kb + 8 * (lane >> 5)]);
-        ye = mfma32(fa, frag(&sm.H_hi[d0 + (lane & 31)][16 * kb + 8 * (lane >> 5)]), ye);
-        ye = mfma32(fa, frag(&sm.H_lo[d0 + (lane & 31)][16 * kb + 8 * (lane >> 5)]), ye);
-      }
-      const int d = d0 + (lane & 31);
+      for (int nb = 0; nb < NBN; ++nb) rr::bf_split4(hst[i][nb], hh[nb], hl[nb]);
+      const u16x8_t fu = frag(&sm.Ut[16 * db + l15][8 * l4]);   // U [s][d]: B operand, k = s
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int t = r32row(r, lane);
-        p.y[((row0 + t) * rowH + h) * DH + d] = yi[r] + sm.gam[t] * ye[r];
-      }
-    }
-    // ---- h_end = gam_31 h_in + U^T (m31 o w o B): every wave, its blocks; checkpoint
-    if constexpr (MODE == kPipe || MODE == kSum) break;
-    const float Gam = sm.gam[Q - 1];
+      for (int tb = 0; tb < 2; ++tb) {
+        f32x4_t yi = {0.f, 0.f, 0.f, 0.f}, ye = {0.f, 0.f, 0.f, 0.f};
+        yi = mfma16(frag(&sm.W_hi[16 * tb + l15][8 * l4]), fu, yi);
+        yi = mfma16(frag(&sm.W_lo[16 * tb + l15][8 * l4]), fu, yi);
 #pragma unroll
-    for (int jj = 0; jj < K::NBW; ++jj) {
-      const int j = w + 4 * jj;
-      if (j < K::NB) {
-        const int db = j / K::NBN, nb = j % K::NBN;
-        const u16x8_t fa = frag(&sm.Ut[16 * db + (lane & 15)][8 * (lane >> 4)]);
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-        acc = mfma16(fa, frag(&sm.BwT_hi[16 * nb + (lane & 15)][8 * (lane >> 4)]), acc);
-        acc = mfma16(fa, frag(&sm.BwT_lo[16 * nb + (lane & 15)][8 * (lane >> 4)]), acc);
-        float* ck = p.ckpt + (((int64_t)b * p.H + h) * p.nC + c) * DH * NS;
+        for (int nb = 0; nb < NBN; ++nb) {
+          const u16x4_t fc = frag4(&sm.C[16 * tb + l15][16 * nb + 4 * l4]);
+          ye = mfma16k16(fc, hh[nb], ye);
+          ye = mfma16k16(fc, hl[nb], ye);
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          hst[jj][r] = Gam * hst[jj][r] + acc[r];
-          ck[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)] = hst[jj][r];
+          const int t = 16 * tb + 4 * l4 + r;
+          p.y[((row0 + t) * rowH + h) * DH + 16 * db + l15] = yi[r] + sm.gam[t] * ye[r];
+        }
+      }
+      if constexpr (STATE) {
+        float* ck = p.ckpt + (bh * p.nC + c) * DH * NS;
+#pragma unroll
+        for (int nb = 0; nb < NBN; ++nb) {
+          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+          acc = mfma16(frag(&sm.BwT_hi[16 * nb + l15][8 * l4]), fu, acc);
+          acc = mfma16(frag(&sm.BwT_lo[16 * nb + l15][8 * l4]), fu, acc);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) hst[i][nb][r] = Gam * hst[i][nb][r] + acc[r];
+          *reinterpret_cast<float4*>(ck + (16 * db + l15) * NS + 16 * nb + 4 * l4) =
+              make_float4(hst[i][nb][0], hst[i][nb][1], hst[i][nb][2], hst[i][nb][3]);
         }
       }
     }
-    __syncthreads();
+    if constexpr (MODE == kWhole) __syncthreads();   // the next chunk rewrites the LDS
   }
 }
 
