@@ -69,8 +69,6 @@ struct alignas(16) ColBwdSmem {
   static constexpr int PD = DH + 8, PN = NS + 8, TD = REG ? 1 : DH;
   uint16_t Kn[Q][PN];                      // B [s][n]
   uint16_t Qn[Q][PN];                      // C [t][n]
-  uint16_t KT[NS][PQ];                     // B^T [n][s]
-  uint16_t QT[NS][PQ];                     // C^T [n][t]
   uint16_t GYT_hi[TD][PQ], GYT_lo[TD][PQ]; // dY^T [d][t]
   uint16_t LM_hi[TD][PN], LM_lo[TD][PN];   // lam [d][n]
   union {
@@ -245,11 +243,6 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
         if (i < Q * NS / 8) {
           *reinterpret_cast<u16x8_t*>(&m.Kn[tl][n0]) = bv[v];
           *reinterpret_cast<u16x8_t*>(&m.Qn[tl][n0]) = cv[v];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            m.KT[n0 + e][tl] = bv[v][e];
-            m.QT[n0 + e][tl] = cv[v][e];
-          }
         }
       }
 #pragma unroll
@@ -570,10 +563,11 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
       for (int tb = 0; tb < 2; ++tb) {
         const int row = 16 * tb + l15, k0 = 8 * l4;
         f32x4_t ak = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f}, akb = {0.f, 0.f, 0.f, 0.f};
-        const u16x8_t fq = frag(&m.QT[16 * nb + l15][k0]);
+        // B and C as B operands over s / t' (transposing reads of Kn / Qn)
+        const u16x8_t fq = rr::frag_tr(&m.Qn[0][16 * nb], ColBwdSmem<DH, NS, GLA, MODE == kPipe>::PN, lane);
         ak = mfma16(frag(&m.y.MGT_hi[row][k0]), fq, ak);
         ak = mfma16(frag(&m.y.MGT_lo[row][k0]), fq, ak);
-        const u16x8_t fk = frag(&m.KT[16 * nb + l15][k0]);
+        const u16x8_t fk = rr::frag_tr(&m.Kn[0][16 * nb], ColBwdSmem<DH, NS, GLA, MODE == kPipe>::PN, lane);
         aq = mfma16(frag(&m.y.MG_hi[row][k0]), fk, aq);
         aq = mfma16(frag(&m.y.MG_lo[row][k0]), fk, aq);
         if constexpr (!GLA) {
@@ -618,7 +612,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
         const int nb = w + 4 * cc;
         if (nb >= NBN) continue;
         const int k0 = 8 * l4;
-        const u16x8_t qf = frag(&m.QT[16 * nb + l15][k0]);
+        const u16x8_t qf = rr::frag_tr(&m.Qn[0][16 * nb], ColBwdSmem<DH, NS, GLA, MODE == kPipe>::PN, lane);
         u16x8_t qh, ql;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {

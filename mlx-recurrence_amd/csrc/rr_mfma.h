@@ -131,6 +131,31 @@ __device__ __forceinline__ float prefix32_sum(float v) {
   return v;
 }
 
+// Operand fragments of a matrix stored k-major in LDS (X[k][col] at
+// base[k * pitch + col], col contiguous) with gfx950's transposing read
+// ds_read_b64_tr_b16: within each 16-lane group the lanes supply 16 4-element
+// row pieces and lane j receives element j % 4 of the pieces of lanes
+// 4 e + j / 4, e = 0..3 (checked on gfx950 by an in-bounds lane-layout probe).
+// Supplying &X[k0 + i / 4][4 (i % 4)] from lane i of group g gives lane j the
+// k-run X[k0 .. k0 + 3][j]: a fragment with k = 4 (lane / 16) + e (16x16x16)
+// or, two reads, k = 8 (lane / 16) + e (16x16x32), for columns col0 .. col0 + 15.
+// base must address X[0][col0]; pitch and col0 are multiples of 4.
+__device__ __forceinline__ u16x4_t tr_read4(const uint16_t* p) {
+  typedef short i16x4v __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(
+      u16x4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4v*)(p)));
+}
+__device__ __forceinline__ u16x4_t frag4_tr(const uint16_t* base, int pitch, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  return tr_read4(base + (4 * g + (i >> 2)) * pitch + 4 * (i & 3));
+}
+__device__ __forceinline__ u16x8_t frag_tr(const uint16_t* base, int pitch, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  const uint16_t* a = base + (8 * g + (i >> 2)) * pitch + 4 * (i & 3);
+  const u16x4_t lo = tr_read4(a), hi = tr_read4(a + 4 * pitch);
+  return u16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
 // Make one wave's LDS writes visible to its own later LDS reads.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
