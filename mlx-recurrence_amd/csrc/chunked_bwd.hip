@@ -122,7 +122,8 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
   if constexpr (MODE == kWhole) {
     h = blockIdx.y, b = blockIdx.z, cbeg = 0, cend = p.nC;
   } else {
-    const rr::chunked::ChunkId id = rr::chunked::chunk_id(p, false);
+    // early chunks cost most where the adjoint is a sum over the later ones
+    const rr::chunked::ChunkId id = rr::chunked::chunk_id(p, MODE == kDirect, false);
     if (!id.valid) return;
     h = id.h, b = id.b, cbeg = id.c, cend = id.c + 1;
   }
@@ -446,9 +447,10 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
       rs = rr::halves_sum(rs);
       // lanes 0..31: suffix of gam X in reversed lane order; lanes 32..63: prefix of m31 w Y
       const int tq = lane < Q ? Q - 1 - lane : lane - Q;
-      const float xy = lane < Q
-          ? m.gam[tq] * (m.XYp[0][0][tq] + m.XYp[1][0][tq] + m.XYp[2][0][tq] + m.XYp[3][0][tq])
-          : m.m31[tq] * m.w[tq] * (m.XYp[0][1][tq] + m.XYp[1][1][tq] + m.XYp[2][1][tq] + m.XYp[3][1][tq]);
+      // (every lane reads both factors and selects: no divergent branch)
+      const int kx = lane < Q ? 0 : 1;
+      const float gq = m.gam[tq], mw = m.m31[tq] * m.w[tq];
+      const float xy = (lane < Q ? gq : mw) * (m.XYp[0][kx][tq] + m.XYp[1][kx][tq] + m.XYp[2][kx][tq] + m.XYp[3][kx][tq]);
       m.Ts[lane < Q ? 0 : 1][tq] = rr::prefix32_sum(xy);
       rr::wave_lds_sync();
       if (lane < Q) {
@@ -470,7 +472,8 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
         float run = 1.f;
 #pragma unroll
         for (int s = Q - 1; s >= 0; --s) {
-          run = s == t - 1 ? 1.f : run * m.xin[(s + 1) & (Q - 1)];
+          const float g = m.xin[(s + 1) & (Q - 1)];   // read in every lane (no branch around it)
+          run = s == t - 1 ? 1.f : run * g;
           if (((s >> 3) & 1) == hf) mh[s >> 4][s & 7] = s < t ? run : 0.f;
         }
       }
@@ -493,7 +496,8 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
       rr::wave_lds_sync();   // XY
       float md[16];
       rr::chunked::decay_block32<true>(m.xin, 0.f, lane, md);
-      const float gprev = t > 0 ? m.gam[t - 1] : 1.f;
+      const float gp = m.gam[(t + Q - 1) & (Q - 1)];
+      const float gprev = t > 0 ? gp : 1.f;
       float cs = 0.f, ps = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) cs += md[r] * (acc[r] + m.XY[0][r32row(r, lane)] * gprev);

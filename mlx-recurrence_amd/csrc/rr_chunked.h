@@ -103,6 +103,16 @@ __device__ __forceinline__ StepScalars step_scalars(float x, float a, int lane) 
   return r;
 }
 
+// exp(x) where `keep`, else 0.  The exponential is formed in every lane and
+// then selected: written as a conditional expression it would compile to a
+// lane-divergent branch per element, which serialises the LDS reads and
+// exponentials it guards.  (A dropped lane may overflow to +inf; the select
+// discards it.)
+__device__ __forceinline__ float masked_exp(bool keep, float x) {
+  const float e = __expf(x);
+  return keep ? e : 0.f;
+}
+
 // The 16 decays M[t, s] held by `lane` in the 32x32 accumulator layout
 // (s = lane % 32, t = r32row(r, lane)), zero above the diagonal (s > t).
 // SSD reads the cumulative deltas cd[], GLA the gates g[] (both in LDS).
@@ -114,7 +124,8 @@ __device__ __forceinline__ void decay_block32(const float* cd_or_g, float a, int
     float run = 0.f;
 #pragma unroll
     for (int t = 0; t < Q; ++t) {
-      run = t < s ? 0.f : (t == s ? 1.f : run * cd_or_g[t]);
+      const float g = cd_or_g[t];   // read in every lane (no branch around it)
+      run = t < s ? 0.f : (t == s ? 1.f : run * g);
       if (((t >> 2) & 1) == half) m[4 * (t >> 3) + (t & 3)] = run;
     }
   } else {
@@ -122,7 +133,7 @@ __device__ __forceinline__ void decay_block32(const float* cd_or_g, float a, int
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int t = r32row(r, lane);
-      m[r] = s <= t ? __expf(a * (cd_or_g[t] - cds)) : 0.f;
+      m[r] = masked_exp(s <= t, a * (cd_or_g[t] - cds));
     }
   }
 }
@@ -151,20 +162,25 @@ constexpr int kSumMaxChunks = 16;
 
 // Per-chunk kernels run on a 1-D grid of chunk_grid(p) workgroups.  The GPU
 // hands workgroups to its 8 XCDs round-robin by linear index; the decode
-// gives every chunk of a head the same XCD, so whatever the head's
-// workgroups share (inputs, checkpoints, adjoints) is cached in one L2.
-// `reverse` numbers the chunks from the end (the costliest workgroups of the
-// direct forward, the late chunks, are then dispatched first).
+// gives every chunk of a head the same XCD (x = index % 8), so whatever the
+// head's workgroups share (inputs, checkpoints, adjoints) is cached in one L2.
+// Where the chunks cost the same (kPipe, kWhole's aggregates), a head's
+// chunks go out together.  Where they differ (kDirect and kSum sum over the
+// other chunks), the chunk position is the slowest-varying part of the index
+// and the costliest chunks of every head go out first (`late_first`: from the
+// last chunk, for forward sums; else from chunk 0); the cheap ones then take
+// the third slots of the CUs, which run slowest.
 constexpr int kXcds = 8;
 struct ChunkId {
   int c, h, b;
   bool valid;   // false for the padding workgroups of the last head group
 };
-__device__ __forceinline__ ChunkId chunk_id(const ChunkArgs& p, bool reverse) {
+__device__ __forceinline__ ChunkId chunk_id(const ChunkArgs& p, bool by_cost, bool late_first) {
   const int id = blockIdx.x, x = id % kXcds, slot = id / kXcds;
-  const int bh = (slot / p.nC) * kXcds + x;
-  const int cs = slot % p.nC;
-  return ChunkId{reverse ? p.nC - 1 - cs : cs, bh % p.H, bh / p.H, bh < p.B * p.H};
+  const int groups = (p.B * p.H + kXcds - 1) / kXcds;   // head groups of 8
+  const int cs = by_cost ? slot / groups : slot % p.nC;
+  const int bh = (by_cost ? slot % groups : slot / p.nC) * kXcds + x;
+  return ChunkId{late_first ? p.nC - 1 - cs : cs, bh % p.H, bh / p.H, bh < p.B * p.H};
 }
 inline dim3 chunk_grid(const ChunkArgs& p) {
   return dim3((unsigned)(p.nC * ((p.B * p.H + kXcds - 1) / kXcds) * kXcds));
@@ -203,7 +219,7 @@ __global__ __launch_bounds__(kAggThreads) void agg_kernel(ChunkArgs p, int kind)
   __shared__ uint16_t YT_hi[NS][PQ], YT_lo[NS][PQ];   // kind 0: (m31 o w o B)^T split; kind 1: C^T (hi only)
   __shared__ float wsh[Q];                            // kind 0: m31_s w_s; kind 1: gam_t
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const ChunkId id = chunk_id(p, false);
+  const ChunkId id = chunk_id(p, false, false);
   if (!id.valid) return;
   const int c = id.c, h = id.h, b = id.b;
   const float a = head_rate<GLA>(p, h);
@@ -357,6 +373,35 @@ __global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
 }
 
 // ------------------------------------------------------------------ sum mode
+// Folds the aggregates k0 .. k0 + KB - 1 of the run (chunk j(k) = k, or
+// nC - 1 - k backwards) into x.  All KB loads go out before the fold; the
+// surplus ones past `cnt` repeat the last needed chunk's addresses (cache
+// hits, dropped in the fold), so no branch waits on a load.
+template <int DH, int NS, bool BWD, bool TRANS, int NX, int KB>
+__device__ __forceinline__ void agg_fold(const ChunkArgs& p, const float* ag, const float* tt, int k0, int cnt,
+                                         const int (&off)[NX], const bool (&has)[NX], f32x4_t (&x)[NX]) {
+  float tv[KB];
+  f32x4_t v[KB][NX];
+#pragma unroll
+  for (int k = 0; k < KB; ++k) {
+    const int kk = min(k0 + k, cnt - 1);
+    const int j = BWD ? p.nC - 1 - kk : kk;
+    tv[k] = tt[j];
+#pragma unroll
+    for (int q = 0; q < NX; ++q)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[k][q][r] = ag[(int64_t)j * DH * NS + off[q] + (TRANS ? r : r * NS)];
+  }
+#pragma unroll
+  for (int k = 0; k < KB; ++k) {
+    const bool ok = k0 + k < cnt;
+#pragma unroll
+    for (int q = 0; q < NX; ++q)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[q][r] = ok && has[q] ? tv[k] * x[q][r] + v[k][q][r] : x[q][r];
+  }
+}
+
 // kSum: the state entering chunk c (forward) or the adjoint leaving it
 // (backward), from the chunk aggregates in p.agg and decays in p.tot by
 // Horner's rule (the recursion pass_kernel runs, restricted to one chunk):
@@ -365,14 +410,14 @@ __global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
 // for this lane's elements of the 16x16 blocks (db(j), nb(j)) listed by
 // `blk`, in the caller's register layout: element r at d = 16 db + 4 (lane / 16)
 // + r, n = 16 nb + lane % 16 (TRANS false), or at d = 16 db + lane % 16,
-// n = 16 nb + 4 (lane / 16) + r (TRANS true).
+// n = 16 nb + 4 (lane / 16) + r (TRANS true).  The number of aggregates is
+// uniform over the workgroup; a batch of 4, 8 or 16 (as registers allow)
+// covers it, so a workgroup reads little beyond the aggregates it needs.
 template <int DH, int NS, bool GLA, bool BWD, bool TRANS = false, int NX, typename BLK>
 __device__ __forceinline__ void agg_sum(const ChunkArgs& p, int c, int64_t bh, int lane, BLK blk,
                                         f32x4_t (&x)[NX]) {
   constexpr int kBatch = NX == 1 ? 16 : NX == 2 ? 8 : 4;
   const float* ext = BWD ? p.dfinal : p.h0;
-  // loads are unconditional (indices clamped into range) so that no branch
-  // waits on them; out-of-range terms are dropped in the fold
   int off[NX];
   bool has[NX];
 #pragma unroll
@@ -391,27 +436,13 @@ __device__ __forceinline__ void agg_sum(const ChunkArgs& p, int c, int64_t bh, i
   const float* ag = p.agg + bh * p.nC * DH * NS;
   const float* tt = p.tot + bh * p.nC;
   const int cnt = BWD ? p.nC - 1 - c : c;
-  for (int k0 = 0; k0 < cnt; k0 += kBatch) {
-    float tv[kBatch];
-    f32x4_t v[kBatch][NX];
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      int j = BWD ? p.nC - 1 - (k0 + k) : k0 + k;
-      j = j < 0 ? 0 : (j > p.nC - 1 ? p.nC - 1 : j);
-      tv[k] = tt[j];
-#pragma unroll
-      for (int q = 0; q < NX; ++q)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v[k][q][r] = ag[(int64_t)j * DH * NS + off[q] + (TRANS ? r : r * NS)];
-    }
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const bool ok = k0 + k < cnt;
-#pragma unroll
-      for (int q = 0; q < NX; ++q)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) x[q][r] = ok && has[q] ? tv[k] * x[q][r] + v[k][q][r] : x[q][r];
-    }
+  if (cnt <= 0) return;
+  if (cnt <= 4) {
+    agg_fold<DH, NS, BWD, TRANS, NX, 4>(p, ag, tt, 0, cnt, off, has, x);
+  } else if (kBatch >= 8 && cnt <= 8) {
+    agg_fold<DH, NS, BWD, TRANS, NX, (kBatch >= 8 ? 8 : 4)>(p, ag, tt, 0, cnt, off, has, x);
+  } else {
+    for (int k0 = 0; k0 < cnt; k0 += kBatch) agg_fold<DH, NS, BWD, TRANS, NX, kBatch>(p, ag, tt, k0, cnt, off, has, x);
   }
 }
 
@@ -649,7 +680,8 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
   if constexpr (MODE == kWhole) {
     h = blockIdx.y, b = blockIdx.z, cbeg = 0;
   } else {
-    const ChunkId id = chunk_id(p, MODE == kDirect);
+    constexpr bool kSums = MODE == kDirect || MODE == kSum;   // late chunks cost most
+    const ChunkId id = chunk_id(p, kSums, kSums);
     if (!id.valid) return;
     h = id.h, b = id.b, cbeg = id.c;
   }

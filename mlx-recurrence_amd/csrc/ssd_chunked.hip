@@ -165,7 +165,8 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
   if constexpr (MODE == kWhole) {
     h = blockIdx.y, b = blockIdx.z, cbeg = 0;
   } else {
-    const rr::chunked::ChunkId id = rr::chunked::chunk_id(p, false);
+    // early chunks cost most where the adjoint is a sum over the later ones
+    const rr::chunked::ChunkId id = rr::chunked::chunk_id(p, MODE == kDirect || MODE == kSum, false);
     if (!id.valid) return;
     h = id.h, b = id.b, cbeg = id.c;
   }
@@ -515,7 +516,7 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int tp = r32row(r, lane);
-        md[r] = s <= tp ? __expf(a * (m.cd[tp] - cds)) : 0.f;
+        md[r] = rr::chunked::masked_exp(s <= tp, a * (m.cd[tp] - cds));
       }
       uint16_t(*dst_hi)[PQ] = w == 0 ? m.y.PT_hi : m.y.MGT_hi;
       uint16_t(*dst_lo)[PQ] = w == 0 ? m.y.PT_lo : m.y.MGT_lo;
@@ -547,7 +548,7 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int tp = r32row(r, lane);
-        const float mg = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * m.G2[tp][s] : 0.f;
+        const float mg = rr::chunked::masked_exp(s <= tp, a * (m.cd[tp] - cds)) * m.G2[tp][s];
         uint16_t hi, lo;
         bf_split(mg * ds, hi, lo);
         m.y.MGd_hi[tp][s] = hi;
@@ -562,7 +563,7 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int tp = r32row(r, lane);
-        const float e = (s <= tp) ? __expf(a * (m.cd[tp] - cds)) * ds * m.G2[tp][s] * m.CB[tp][s] : 0.f;
+        const float e = rr::chunked::masked_exp(s <= tp, a * (m.cd[tp] - cds)) * ds * m.G2[tp][s] * m.CB[tp][s];
         const float k = rr::prefix32_sum(e);
         rs += tp >= s ? k : 0.f;
       }
@@ -711,14 +712,19 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
     // d(delta)_t = a T_t + (1 - a delta_t) sum_n B_t Z_t,
     // T_t = sum lam_t h_t = R_t + sum_{t' >= t} gam X + sum_{s <= t} m31 delta Y + m31_t gam_t tr
     if (w == 0) {
-      const float tn = lane < NS ? m.t4[0][lane] + m.t4[1][lane] + m.t4[2][lane] + m.t4[3][lane] : 0.f;
+      const int ln = lane & (NS - 1);   // every lane reads, lanes >= NS drop it (no branch)
+      const float tn = lane < NS ? m.t4[0][ln] + m.t4[1][ln] + m.t4[2][ln] + m.t4[3][ln] : 0.f;
       const float tr = rr::wave_sum(tn);
       // lanes 0..31: suffix of gam X in reversed lane order; lanes 32..63: prefix of m31 delta Y
       const int tq = lane < Q ? Q - 1 - lane : lane - Q;
       float xy = 0.f;
 #pragma unroll
-      for (int nb = 0; nb < NBN; ++nb) xy += lane < Q ? m.Xs[nb][tq] : m.Ys[nb][tq];
-      xy *= lane < Q ? m.gam[tq] : m.m31[tq] * m.del[tq];
+      for (int nb = 0; nb < NBN; ++nb) {
+        const float xs = m.Xs[nb][tq], ys = m.Ys[nb][tq];   // both read, then selected (no branch)
+        xy += lane < Q ? xs : ys;
+      }
+      const float gq = m.gam[tq], md = m.m31[tq] * m.del[tq];
+      xy *= lane < Q ? gq : md;
       m.Ts[lane < Q ? 0 : 1][tq] = rr::prefix32_sum(xy);
       rr::wave_lds_sync();
       if (lane < Q) {
