@@ -28,8 +28,12 @@ bool gla2_supported(int dtype, int64_t B, int64_t L, int64_t H, int64_t seg, int
   return Dh == 32 || Dh == 64;
 }
 
+// The direct mode for the shortest heads only (a Dh x Dh state makes each
+// workgroup's sum over the other chunks costly).
+constexpr int64_t kGlaDirectMaxChunks = 4;
+
 int gla2_mode(int64_t nC, int64_t Dh) {
-  return nC <= chunked::kDirectMaxChunks && Dh * Dh <= chunked::kDirectMaxState ? chunked::kDirect : chunked::kPipe;
+  return nC <= kGlaDirectMaxChunks && Dh * Dh <= chunked::kDirectMaxState ? chunked::kDirect : chunked::kPipe;
 }
 
 size_t gla2_ws_bytes(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass) {

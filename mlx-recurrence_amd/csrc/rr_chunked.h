@@ -151,14 +151,14 @@ __device__ __forceinline__ int state_off(int d, int n) {
 //   kWhole  a head per workgroup, state / adjoint carried in registers;
 //   kPipe   one workgroup per chunk; aggregate kernel, state-pass kernel
 //           (pass_kernel), chunk kernel;
-//   kDirect one workgroup per chunk forming its entering state from the raw
-//           inputs of the other chunks (nC <= kDirectMaxChunks);
-//   kSum    one workgroup per chunk forming its entering state from the
-//           chunk aggregates (agg_sum): aggregate kernel, chunk kernel.
+//   kDirect one workgroup per chunk forming its entering state (forward) or
+//           leaving adjoint (backward) from the raw inputs of the other chunks
+//           (direct_sum; nC <= kDirectMaxChunks): one kernel per pass;
+//   kSum    the same sum, for the backward's small-N kernel (its own
+//           instantiation); the forward runs the direct kernel.
+// Both read up to nC - 1 chunks of inputs per workgroup (quadratic in nC), so
+// they serve short heads; longer heads run kPipe.
 enum Mode { kWhole = 0, kPipe = 1, kDirect = 2, kSum = 3 };
-// kSum reads up to nC - 1 aggregates per workgroup (quadratic in nC), so it
-// serves the middle range of chunk counts; longer heads run kPipe.
-constexpr int kSumMaxChunks = 16;
 
 // Per-chunk kernels run on a 1-D grid of chunk_grid(p) workgroups.  The GPU
 // hands workgroups to its 8 XCDs round-robin by linear index; the decode
@@ -198,7 +198,7 @@ __device__ __forceinline__ float head_rate(const ChunkArgs& p, int h) {
 //  1. agg_kernel, one workgroup per chunk k, writes the chunk's aggregate and its
 //     decay tot_k = gam_31:
 //       forward:  S_k = U_k^T diag(m31 o w) B_k, the state the chunk adds from
-//                 a zero start (into checkpoint slot k; kSum: the workspace);
+//                 a zero start (into checkpoint slot k);
 //       backward: G_k = (gam o dY_k)^T C_k, the adjoint the chunk sends back to
 //                 its start (into the workspace).
 //  2. pass_kernel, one thread per state element, walks the chunks in order:
@@ -302,7 +302,7 @@ __global__ __launch_bounds__(kAggThreads) void agg_kernel(ChunkArgs p, int kind)
     }
   }
   __syncthreads();
-  float* dst = (kind == 0 && p.mode != kSum ? p.ckpt : p.agg) + (((int64_t)b * p.H + h) * p.nC + c) * DH * NS;
+  float* dst = (kind == 0 ? p.ckpt : p.agg) + (((int64_t)b * p.H + h) * p.nC + c) * DH * NS;
 #pragma unroll
   for (int jj = 0; jj < (NB + 3) / 4; ++jj) {
     const int j = w + 4 * jj;
@@ -372,257 +372,288 @@ __global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
   }
 }
 
-// ------------------------------------------------------------------ sum mode
-// Folds the aggregates k0 .. k0 + KB - 1 of the run (chunk j(k) = k, or
-// nC - 1 - k backwards) into x.  All KB loads go out before the fold; the
-// surplus ones past `cnt` repeat the last needed chunk's addresses (cache
-// hits, dropped in the fold), so no branch waits on a load.
-template <int DH, int NS, bool BWD, bool TRANS, int NX, int KB>
-__device__ __forceinline__ void agg_fold(const ChunkArgs& p, const float* ag, const float* tt, int k0, int cnt,
-                                         const int (&off)[NX], const bool (&has)[NX], f32x4_t (&x)[NX]) {
-  float tv[KB];
-  f32x4_t v[KB][NX];
-#pragma unroll
-  for (int k = 0; k < KB; ++k) {
-    const int kk = min(k0 + k, cnt - 1);
-    const int j = BWD ? p.nC - 1 - kk : kk;
-    tv[k] = tt[j];
-#pragma unroll
-    for (int q = 0; q < NX; ++q)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) v[k][q][r] = ag[(int64_t)j * DH * NS + off[q] + (TRANS ? r : r * NS)];
-  }
-#pragma unroll
-  for (int k = 0; k < KB; ++k) {
-    const bool ok = k0 + k < cnt;
-#pragma unroll
-    for (int q = 0; q < NX; ++q)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) x[q][r] = ok && has[q] ? tv[k] * x[q][r] + v[k][q][r] : x[q][r];
-  }
-}
-
-// kSum: the state entering chunk c (forward) or the adjoint leaving it
-// (backward), from the chunk aggregates in p.agg and decays in p.tot by
-// Horner's rule (the recursion pass_kernel runs, restricted to one chunk):
-//   forward:  x = h0;     x = tot_j x + S_j  for j = 0 .. c - 1
-//   backward: x = dfinal; x = tot_j x + G_j  for j = nC - 1 .. c + 1
-// for this lane's elements of the 16x16 blocks (db(j), nb(j)) listed by
-// `blk`, in the caller's register layout: element r at d = 16 db + 4 (lane / 16)
-// + r, n = 16 nb + lane % 16 (TRANS false), or at d = 16 db + lane % 16,
-// n = 16 nb + 4 (lane / 16) + r (TRANS true).  The number of aggregates is
-// uniform over the workgroup; a batch of 4, 8 or 16 (as registers allow)
-// covers it, so a workgroup reads little beyond the aggregates it needs.
-template <int DH, int NS, bool GLA, bool BWD, bool TRANS = false, int NX, typename BLK>
-__device__ __forceinline__ void agg_sum(const ChunkArgs& p, int c, int64_t bh, int lane, BLK blk,
-                                        f32x4_t (&x)[NX]) {
-  constexpr int kBatch = NX == 1 ? 16 : NX == 2 ? 8 : 4;
-  const float* ext = BWD ? p.dfinal : p.h0;
-  int off[NX];
-  bool has[NX];
-#pragma unroll
-  for (int q = 0; q < NX; ++q) {
-    int db, nb;
-    has[q] = blk(q, db, nb);
-    off[q] = !has[q] ? 0
-             : TRANS ? (16 * db + (lane & 15)) * NS + 16 * nb + 4 * (lane >> 4)
-                     : (16 * db + 4 * (lane >> 4)) * NS + 16 * nb + (lane & 15);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int e = off[q] + (TRANS ? r : r * NS), d = e / NS, n = e % NS;
-      x[q][r] = has[q] && ext != nullptr ? ext[bh * DH * NS + state_off<GLA, DH, NS>(d, n)] : 0.f;
-    }
-  }
-  const float* ag = p.agg + bh * p.nC * DH * NS;
-  const float* tt = p.tot + bh * p.nC;
-  const int cnt = BWD ? p.nC - 1 - c : c;
-  if (cnt <= 0) return;
-  if (cnt <= 4) {
-    agg_fold<DH, NS, BWD, TRANS, NX, 4>(p, ag, tt, 0, cnt, off, has, x);
-  } else if (kBatch >= 8 && cnt <= 8) {
-    agg_fold<DH, NS, BWD, TRANS, NX, (kBatch >= 8 ? 8 : 4)>(p, ag, tt, 0, cnt, off, has, x);
-  } else {
-    for (int k0 = 0; k0 < cnt; k0 += kBatch) agg_fold<DH, NS, BWD, TRANS, NX, kBatch>(p, ag, tt, k0, cnt, off, has, x);
-  }
-}
-
 // ------------------------------------------------------------------ direct mode
 // Short sequences (nC <= kDirectMaxChunks): one workgroup per chunk forms the
 // state entering its chunk (forward) or the adjoint leaving it (backward)
-// itself, as a weighted sum over the inputs of all earlier (later) chunks, so
-// a pass is a single kernel with no aggregate or state-pass kernels:
-//   forward:  h_in(c) = Gam h0 + sum_{j<c} F_j U_j^T diag(m31 o w) B_j,
+// itself, as a weighted sum over the raw inputs of all earlier (later)
+// chunks, so a pass is a single kernel with no aggregate or state-pass kernels:
+//   forward:  h_in(c) = Gam h0 + sum_{j<c} U_j^T diag(F_j m31 o w) B_j,
 //             F_j = tot_{j+1} ... tot_{c-1},   Gam = tot_0 ... tot_{c-1};
-//   backward: lam(c) = Gam dfinal + sum_{j>c} F_j (gam o dY_j)^T C_j,
+//   backward: lam(c) = Gam dfinal + sum_{j>c} (F_j gam o dY_j)^T C_j,
 //             F_j = tot_{c+1} ... tot_{j-1},   Gam = tot_{c+1} ... tot_{nC-1}
 // (m31, w, gam and tot of chunk j as in step_scalars).  Wave w takes chunks
-// w, w + 4, ... of the range and accumulates every 16x16 block of the state;
-// the four partial sums are added in a fixed order (deterministic).
-// The sum costs each workgroup up to nC - 1 chunks of extra reads; measured on
-// MI355X (B3 H12 Dh64), it beats the two extra launches of the pipelined mode
-// at 2 and 4 chunks and loses from 8 chunks on.
-constexpr int kDirectMaxChunks = 4;
+// j0 + w, j0 + w + 4, ... of the range (at most kDirectPerWave).  Their inputs
+// are loaded up to four chunks ahead, staged in the wave's own LDS area in
+// their natural [step][column] layout, the fp32 factor applied and split into
+// bf16 hi + lo, and read back as MFMA operands (k = step) by transposing LDS
+// reads; no transposed copies and no workgroup barriers in the loop.  Each
+// wave accumulates every 16x16 block of the state; the four partial sums are
+// added in a fixed order (deterministic).
+constexpr int kDirectMaxChunks = 16;
 constexpr int kDirectMaxState = 64 * 64;   // Dh * N (the partial sums live in LDS)
 constexpr int kDirectPerWave = kDirectMaxChunks / 4;
 
 template <int DH, int NS, bool BWD>
-struct DirectSmem {
+struct alignas(16) DirectSmem {
+  // Row pitches (elements): 32 or 96 bytes past a multiple of 128, so the
+  // four 32-byte row pieces that 16 lanes of a transposing read take hit
+  // distinct banks; 16-column rows (32 bytes) tile the banks unpadded.
+  static constexpr int PX = DH + 16;
+  static constexpr int PY = NS == 16 ? 16 : NS + 16;
   union {
-    struct {                                // one wave's staging area
-      uint16_t XT[BWD ? 2 : 1][DH][PQ];     // fwd: U^T; bwd: (coef o dY)^T hi, lo
-      uint16_t YT[BWD ? 1 : 2][NS][PQ];     // fwd: (coef o B)^T hi, lo; bwd: C^T
+    struct {
+      uint16_t X[BWD ? 2 : 1][Q][PX];   // fwd: U [s][d]; bwd: (F gam o dY) hi, lo [t][d]
+      uint16_t Y[BWD ? 1 : 2][Q][PY];   // fwd: (F m31 w o B) hi, lo [s][n]; bwd: C [t][n]
     } st[4];
-    float red[4][DH * NS];                  // per-wave partial sums, [d][n]
+    float red[2][DH * NS];              // partial sums of waves 0 + 2 and 1 + 3, [d][n]
   };
-  float tot[kDirectMaxChunks];
+  float tot[kDirectMaxChunks];          // decays of the chunks of the range
+  float g0[BWD ? DH * NS : 1];          // backward, chunk 0's own term G_0 (see direct_sum)
 };
 
-// Runs the weighted sum; afterwards red[] holds the four partial sums and the
-// return value is Gam.  Every thread of the (256-thread) workgroup must call it.
-template <int DH, int NS, bool GLA, bool BWD>
-__device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, DirectSmem<DH, NS, BWD>& s) {
-  constexpr int NBN = NS / 16, NB = (DH / 16) * NBN;
-  constexpr int XV = BWD ? Q * DH / 4 / 64 : Q * DH / 8 / 64;  // float4 (dY) or u16x8 (U) per lane
-  constexpr int YV = (Q * NS / 8 + 63) / 64;                   // u16x8 of B (fwd) or C (bwd) per lane
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int l15 = lane & 15, l4 = lane >> 4;
+struct NoLoads {
+  __device__ void operator()() const {}
+};
+
+// Runs the weighted sum; afterwards red[] holds the two partial sums and the
+// return value is Gam.  Every thread of the (256-thread) workgroup must call
+// it.  `pre` is called once per thread when its wave has staged its last
+// chunk: the caller issues its own chunk's loads there, so that they land
+// while the partial sums are added, without their registers being live in
+// the loop.  G0 (backward): the workgroup of chunk 0 also forms the
+// initial-state gradient dh0 = tot_0 lam(0) + G_0, G_0 = (gam o dY_0)^T C_0,
+// by taking chunk 0 into its range with a separate accumulator, and stores it
+// (when dh0 is given).
+template <int DH, int NS, bool GLA, bool BWD, bool G0 = false, typename PRE = NoLoads>
+__device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, DirectSmem<DH, NS, BWD>& s,
+                            float* dh0 = nullptr, PRE pre = PRE{}) {
+  using S = DirectSmem<DH, NS, BWD>;
+  constexpr int NBD = DH / 16, NBN = NS / 16;
+  constexpr int XV = BWD ? Q * DH / 4 / 64 : Q * DH / 8 / 64;   // per lane and chunk: float4 of dY / u16x8 of U
+  constexpr int YV = Q * NS / 8 / 64;                           // u16x8 of B (fwd) or C (bwd)
+  constexpr int VPC = 4 * (XV + YV);                            // registers per chunk in flight
+  constexpr int REGS = BWD && NS > 16 ? 48 : 80;                // budget for them
+  constexpr int PF = REGS / VPC >= 4 ? 4 : REGS / VPC >= 2 ? 2 : 1;   // chunks in flight per wave
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t rowH = p.H;
-  const int j0 = BWD ? c + 1 : 0, j1 = BWD ? p.nC : c;   // chunks [j0, j1)
+  const bool g0 = G0 && BWD && c == 0 && dh0 != nullptr;
+  const int kfirst = BWD ? c + 1 : 0;          // first chunk whose decay enters the factors
+  const int j0 = g0 ? 0 : kfirst;
+  const int j1 = BWD ? p.nC : c;               // the range: chunks [j0, j1)
+  const int cnt = j1 - j0;
+  const int nw = cnt > w ? (cnt - w + 3) / 4 : 0;   // this wave's chunks (uniform per wave)
   const float neutral = GLA ? 1.f : 0.f;
+  // chunk k of this wave, clamped into the range (surplus loads repeat a
+  // needed chunk; with an empty range, this workgroup's own chunk)
+  auto chunk = [&](int k) { return cnt > 0 ? min(j0 + w + 4 * k, j1 - 1) : c; };
 
-  // 1. decays of the chunks in the range; per-step coefficients of this wave's
-  float coef[kDirectPerWave];
+  // 1. step inputs of this wave's chunks, then the operands of the first PF
+  float xs[kDirectPerWave];
 #pragma unroll
-  for (int jj = 0; jj < kDirectPerWave; ++jj) {
-    const int j = j0 + w + 4 * jj;
-    coef[jj] = 0.f;
-    if (j < j1) {
-      const int64_t row0 = (int64_t)b * p.L + (int64_t)j * Q;
-      const float xl = bf_val(p.delta[(row0 + (lane & (Q - 1))) * rowH + h]);   // unconditional load
-      const float xv = lane < Q ? xl : neutral;
-      const StepScalars sc = step_scalars<GLA>(xv, a, lane);
-      coef[jj] = BWD ? sc.gam : sc.m31 * sc.w;
-      if (lane == 0) s.tot[j - j0] = sc.tot;
-    }
+  for (int k = 0; k < kDirectPerWave; ++k) {
+    const int64_t row0 = (int64_t)b * p.L + (int64_t)chunk(k) * Q;
+    xs[k] = bf_val(p.delta[(row0 + (lane & (Q - 1))) * rowH + h]);   // lanes >= 32 masked below
   }
-  __syncthreads();
-  float gam_all = 1.f;
-  for (int k = j0; k < j1; ++k) gam_all *= s.tot[k - j0];
-#pragma unroll
-  for (int jj = 0; jj < kDirectPerWave; ++jj) {
-    const int j = j0 + w + 4 * jj;
-    if (j < j1) {
-      float f = 1.f;
-      const int kb = BWD ? j0 : j + 1, ke = BWD ? j : j1;
-      for (int k = kb; k < ke; ++k) f *= s.tot[k - j0];
-      coef[jj] *= f;
-    }
-  }
-
-  // 2. this wave's partial sum over its chunks (inputs of chunk jj + 1 are
-  //    loaded while chunk jj is staged and multiplied)
-  f32x4_t part[NB];
-#pragma unroll
-  for (int q = 0; q < NB; ++q) part[q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  auto& st = s.st[w];
-  const uint16_t* ysrc = BWD ? p.Cm : p.Bm;
-  u16x8_t xu[2][BWD ? 1 : XV], yv[2][YV];
-  float4 xf[2][BWD ? XV : 1];
-  auto load = [&](int buf, int j) {
+  u16x8_t xu[PF][BWD ? 1 : XV], yv[PF][YV];
+  float4 xf[PF][BWD ? XV : 1];
+  auto load = [&](int slot, int j) {
     const int64_t row0 = (int64_t)b * p.L + (int64_t)j * Q;
 #pragma unroll
     for (int v = 0; v < XV; ++v) {
       if constexpr (BWD) {
-        const int i = lane + 64 * v, tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
-        xf[buf][v] = *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0);
+        const int i = lane + 64 * v, t = i / (DH / 4), d0 = 4 * (i % (DH / 4));
+        xf[slot][v] = *reinterpret_cast<const float4*>(p.dy + ((row0 + t) * rowH + h) * DH + d0);
       } else {
-        const int i = lane + 64 * v, tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
-        xu[buf][v] = *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0);
+        const int i = lane + 64 * v, t = i / (DH / 8), d0 = 8 * (i % (DH / 8));
+        xu[slot][v] = *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + t) * rowH + h) * DH + d0);
       }
     }
+    const uint16_t* ysrc = BWD ? p.Cm : p.Bm;
 #pragma unroll
     for (int v = 0; v < YV; ++v) {
-      const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
-      yv[buf][v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(ysrc + ((row0 + tl) * rowH + h) * NS + n0)
-                                  : u16x8_t{};
+      const int i = lane + 64 * v, t = i / (NS / 8), n0 = 8 * (i % (NS / 8));
+      yv[slot][v] = *reinterpret_cast<const u16x8_t*>(ysrc + ((row0 + t) * rowH + h) * NS + n0);
     }
   };
-  if (j0 + w < j1) load(0, j0 + w);
 #pragma unroll
-  for (int jj = 0; jj < kDirectPerWave; ++jj) {
-    const int j = j0 + w + 4 * jj;
-    if (j >= j1) break;
-    const int cur = jj & 1;
-    if (j + 4 < j1) load(cur ^ 1, j + 4);
-    const float cf = coef[jj];
+  for (int k = 0; k < PF; ++k) load(k, chunk(k));
+#pragma unroll
+  for (int k = 0; k < kDirectPerWave; ++k) rr::pin(xs[k]);   // waits for the step inputs only
+
+  // 2. step scalars; the chunk decays go to LDS
+  float coef[kDirectPerWave];
+#pragma unroll
+  for (int k = 0; k < kDirectPerWave; ++k) {
+    const StepScalars sc = step_scalars<GLA>(lane < Q ? xs[k] : neutral, a, lane);
+    coef[k] = BWD ? sc.gam : sc.m31 * sc.w;
+    if (k < nw && lane == 0) s.tot[chunk(k) - j0] = sc.tot;
+  }
+  __syncthreads();
+
+  // 3. chunk factors by a product scan over the range (lane i: chunk j0 + i)
+  //    fwd: F_j = tot_{j+1} ... tot_{j1-1} (exclusive suffix product);
+  //    bwd: F_j = tot_{kfirst} ... tot_{j-1} (exclusive prefix product; with
+  //    chunk 0 in the range for dh0, tot_0 is left out)
+  float gam_all;
+  float fk[kDirectPerWave];
+  {
+    const int i = lane & 31;
+    float v;
+    if constexpr (BWD) {
+      const int src = i - 1;   // exclusive: lane i takes chunk j0 + i - 1
+      const float t = s.tot[min(max(src, 0), kDirectMaxChunks - 1)];   // read in every lane
+      v = src >= 0 && src < cnt && j0 + src >= kfirst ? t : 1.f;
+    } else {
+      const int src = cnt - i;   // reversed, exclusive: lane i takes chunk j0 + cnt - i
+      const float t = s.tot[min(max(src, 0), kDirectMaxChunks - 1)];   // read in every lane
+      v = i > 0 && src >= 0 && src < cnt ? t : 1.f;
+    }
+    const float e = prefix_prod32(v, lane);   // lane i: product over lanes 0 .. i
+    gam_all = __shfl(e, min(cnt, 31));
+#pragma unroll
+    for (int k = 0; k < kDirectPerWave; ++k) {
+      const int idx = chunk(k) - j0;
+      fk[k] = __shfl(e, BWD ? idx : cnt - 1 - idx);
+    }
+  }
+
+  // 4. this wave's chunks: stage, then accumulate every block of the state
+  f32x4_t acc[NBD][NBN];
+#pragma unroll
+  for (int db = 0; db < NBD; ++db)
+#pragma unroll
+    for (int nb = 0; nb < NBN; ++nb) acc[db][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto& st = s.st[w];
+#pragma unroll
+  for (int k = 0; k < kDirectPerWave; ++k) {
+    if (k >= nw) break;
+    const int slot = k % PF;
+    const float cf = coef[k] * fk[k];   // lane s < 32: the factor of step s
 #pragma unroll
     for (int v = 0; v < XV; ++v) {
       if constexpr (BWD) {
-        const int i = lane + 64 * v, tl = i / (DH / 4), d0 = 4 * (i % (DH / 4));
-        const float ct = __shfl(cf, tl);
-        const float g4[4] = {xf[cur][v].x, xf[cur][v].y, xf[cur][v].z, xf[cur][v].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          uint16_t hi, lo;
-          bf_split(ct * g4[e], hi, lo);
-          st.XT[0][d0 + e][tl] = hi;
-          st.XT[BWD ? 1 : 0][d0 + e][tl] = lo;
-        }
+        const int i = lane + 64 * v, t = i / (DH / 4), d0 = 4 * (i % (DH / 4));
+        const float ct = __shfl(cf, t);
+        const float4 g = xf[slot][v];
+        u16x4_t hi, lo;
+        rr::bf_split4(f32x4_t{ct * g.x, ct * g.y, ct * g.z, ct * g.w}, hi, lo);
+        *reinterpret_cast<u16x4_t*>(&st.X[0][t][d0]) = hi;
+        *reinterpret_cast<u16x4_t*>(&st.X[BWD ? 1 : 0][t][d0]) = lo;
       } else {
-        const int i = lane + 64 * v, tl = i / (DH / 8), d0 = 8 * (i % (DH / 8));
-#pragma unroll
-        for (int e = 0; e < 8; ++e) st.XT[0][d0 + e][tl] = xu[cur][v][e];
+        const int i = lane + 64 * v, t = i / (DH / 8), d0 = 8 * (i % (DH / 8));
+        *reinterpret_cast<u16x8_t*>(&st.X[0][t][d0]) = xu[slot][v];
       }
     }
 #pragma unroll
     for (int v = 0; v < YV; ++v) {
-      const int i = lane + 64 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
-      const float ct = __shfl(cf, tl);
-      if (i < Q * NS / 8) {
+      const int i = lane + 64 * v, t = i / (NS / 8), n0 = 8 * (i % (NS / 8));
+      if constexpr (BWD) {
+        *reinterpret_cast<u16x8_t*>(&st.Y[0][t][n0]) = yv[slot][v];
+      } else {
+        const float ct = __shfl(cf, t);
+        float yw[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          if constexpr (BWD) {
-            st.YT[0][n0 + e][tl] = yv[cur][v][e];
-          } else {
-            uint16_t hi, lo;
-            bf_split(ct * bf_val(yv[cur][v][e]), hi, lo);
-            st.YT[0][n0 + e][tl] = hi;
-            st.YT[BWD ? 0 : 1][n0 + e][tl] = lo;
-          }
+        for (int e = 0; e < 8; ++e) yw[e] = ct * bf_val(yv[slot][v][e]);
+        u16x8_t hi, lo;
+        rr::bf_split8(yw, hi, lo);
+        *reinterpret_cast<u16x8_t*>(&st.Y[0][t][n0]) = hi;
+        *reinterpret_cast<u16x8_t*>(&st.Y[BWD ? 0 : 1][t][n0]) = lo;
+      }
+    }
+    // the registers of this slot are free: the loads of chunk k + PF (issued
+    // even past this wave's last chunk, as a repeat of it, so that the number
+    // of loads in flight is the same on every path and the waits for a slot
+    // stay exact)
+    if (k + PF < kDirectPerWave) load(slot, chunk(k + PF));
+    wave_lds_sync();
+    u16x8_t yf[BWD ? 1 : 2][NBN];
+#pragma unroll
+    for (int nb = 0; nb < NBN; ++nb)
+#pragma unroll
+      for (int hl = 0; hl < (BWD ? 1 : 2); ++hl) yf[hl][nb] = frag_tr(&st.Y[hl][0][16 * nb], S::PY, lane);
+#pragma unroll
+    for (int db = 0; db < NBD; ++db) {
+#pragma unroll
+      for (int hl = 0; hl < (BWD ? 2 : 1); ++hl) {
+        const u16x8_t xfr = frag_tr(&st.X[hl][0][16 * db], S::PX, lane);
+#pragma unroll
+        for (int nb = 0; nb < NBN; ++nb) {
+          acc[db][nb] = mfma16(xfr, yf[0][nb], acc[db][nb]);
+          if constexpr (!BWD) acc[db][nb] = mfma16(xfr, yf[BWD ? 0 : 1][nb], acc[db][nb]);
         }
       }
     }
-    wave_lds_sync();
+    if constexpr (G0) {
+      if (g0 && w == 0 && k == 0) {   // chunk 0: its own term, set aside in LDS
+        const int l15 = lane & 15, l4 = lane >> 4;
 #pragma unroll
-    for (int q = 0; q < NB; ++q) {
-      const int db = q / NBN, nb = q % NBN;
-      const u16x8_t fa = frag(&st.XT[0][16 * db + l15][8 * l4]);
-      const u16x8_t fb = frag(&st.YT[0][16 * nb + l15][8 * l4]);
-      part[q] = mfma16(fa, fb, part[q]);
-      if constexpr (BWD) part[q] = mfma16(frag(&st.XT[BWD ? 1 : 0][16 * db + l15][8 * l4]), fb, part[q]);
-      else part[q] = mfma16(fa, frag(&st.YT[BWD ? 0 : 1][16 * nb + l15][8 * l4]), part[q]);
+        for (int db = 0; db < NBD; ++db)
+#pragma unroll
+          for (int nb = 0; nb < NBN; ++nb) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s.g0[(16 * db + 4 * l4 + r) * NS + 16 * nb + l15] = acc[db][nb][r];
+            acc[db][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          }
+      }
     }
-    wave_lds_sync();
+    wave_lds_sync();   // the next chunk's staging rewrites the area
   }
-  // 3. partial sums to LDS (the staging areas are dead once every wave is here)
-  __syncthreads();
+  pre();
+
+  // 5. partial sums: red[0] = acc_0 + acc_2, red[1] = acc_1 + acc_3
+  __syncthreads();   // the staging areas are dead (red[] overlays them)
+  const int l15 = lane & 15, l4 = lane >> 4;
+  auto at = [&](int db, int nb, int r) { return (16 * db + 4 * l4 + r) * NS + 16 * nb + l15; };
+  if (w >= 2) {
 #pragma unroll
-  for (int q = 0; q < NB; ++q) {
-    const int db = q / NBN, nb = q % NBN;
+    for (int db = 0; db < NBD; ++db)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s.red[w][(16 * db + 4 * l4 + r) * NS + 16 * nb + l15] = part[q][r];
+      for (int nb = 0; nb < NBN; ++nb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s.red[w - 2][at(db, nb, r)] = acc[db][nb][r];
   }
   __syncthreads();
+  if (w < 2) {
+#pragma unroll
+    for (int db = 0; db < NBD; ++db)
+#pragma unroll
+      for (int nb = 0; nb < NBN; ++nb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int e = at(db, nb, r);
+          s.red[w][e] = acc[db][nb][r] + s.red[w][e];
+        }
+  }
+  __syncthreads();
+  if constexpr (G0) {
+    if (g0 && w == 0) {
+      // dh0 = tot_0 lam(0) + G_0, lam(0) = red0 + red1 + Gam dfinal
+      const float t0 = s.tot[0];
+      const float* ext = p.dfinal != nullptr ? p.dfinal + ((int64_t)b * p.H + h) * DH * NS : nullptr;
+      float* out = dh0 + ((int64_t)b * p.H + h) * DH * NS;
+#pragma unroll
+      for (int db = 0; db < NBD; ++db)
+#pragma unroll
+        for (int nb = 0; nb < NBN; ++nb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int e = at(db, nb, r), d = e / NS, n = e % NS;
+            float lam = s.red[0][e] + s.red[1][e];
+            if (ext != nullptr) lam += gam_all * ext[state_off<GLA, DH, NS>(d, n)];
+            out[state_off<GLA, DH, NS>(d, n)] = t0 * lam + s.g0[e];
+          }
+    }
+  }
   return gam_all;
 }
 
-// Element (d, n) of the direct sum: the four partials plus Gam times the
+// Element (d, n) of the direct sum: the two partials plus Gam times the
 // caller's h0 (forward) or dfinal (backward), read from red[] / `ext`.
 template <int DH, int NS, bool GLA, bool BWD>
 __device__ __forceinline__ float direct_value(const DirectSmem<DH, NS, BWD>& s, float gam_all, const float* ext,
                                               int d, int n) {
   const int e = d * NS + n;
-  float v = ((s.red[0][e] + s.red[1][e]) + s.red[2][e]) + s.red[3][e];
+  float v = s.red[0][e] + s.red[1][e];
   if (ext != nullptr) v += gam_all * ext[state_off<GLA, DH, NS>(d, n)];
   return v;
 }
@@ -680,8 +711,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
   if constexpr (MODE == kWhole) {
     h = blockIdx.y, b = blockIdx.z, cbeg = 0;
   } else {
-    constexpr bool kSums = MODE == kDirect || MODE == kSum;   // late chunks cost most
-    const ChunkId id = chunk_id(p, kSums, kSums);
+    const ChunkId id = chunk_id(p, MODE == kDirect, MODE == kDirect);   // late chunks cost most
     if (!id.valid) return;
     h = id.h, b = id.b, cbeg = id.c;
   }
@@ -696,8 +726,30 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
   for (int i = 0; i < DBW; ++i)
 #pragma unroll
     for (int nb = 0; nb < NBN; ++nb) hst[i][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // the chunk's own inputs (all loads issued before any use)
+  constexpr int UV = (Q * DH / 8 + 255) / 256, BV = (Q * NS / 8 + 255) / 256;
+  u16x8_t uv[UV], bv[BV], cv[BV];
+  float xv;
+  auto issue = [&](int c, int tid) {
+    const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;
+#pragma unroll
+    for (int v = 0; v < UV; ++v) {
+      const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
+      uv[v] = i < Q * DH / 8 ? *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0) : u16x8_t{};
+    }
+#pragma unroll
+    for (int v = 0; v < BV; ++v) {
+      const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+      const int64_t g = ((row0 + tl) * rowH + h) * NS + n0;
+      bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Bm + g) : u16x8_t{};
+      cv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Cm + g) : u16x8_t{};
+    }
+    // unconditional (in-bounds) load, so no branch waits on it
+    xv = bf_val(p.delta[(row0 + (tid & (Q - 1))) * rowH + h]);
+  };
   if constexpr (MODE == kDirect) {
-    const float gam_all = direct_sum<DH, NS, GLA, false>(p, cbeg, b, h, a, smu.d);
+    // the chunk's loads go out when each wave has staged its last summed chunk
+    const float gam_all = direct_sum<DH, NS, GLA, false>(p, cbeg, b, h, a, smu.d, nullptr, [&] { issue(cbeg, tid); });
     const float* h0b = p.h0 != nullptr ? p.h0 + bh * DH * NS : nullptr;
 #pragma unroll
     for (int i = 0; i < DBW; ++i) {
@@ -745,54 +797,9 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
     if constexpr (MODE == kWhole) asm volatile("" : "+v"(tidv));
     const int tid = tidv, lane = tidv & 63, l15 = lane & 15, l4 = lane >> 4;
     const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;  // first (b, t) row of the chunk
-    // ---- stage the chunk's inputs (all loads issued before any use)
+    // ---- stage the chunk's inputs
     {
-      constexpr int UV = (Q * DH / 8 + 255) / 256, BV = (Q * NS / 8 + 255) / 256;
-      u16x8_t uv[UV], bv[BV], cv[BV];
-#pragma unroll
-      for (int v = 0; v < UV; ++v) {
-        const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
-        uv[v] = i < Q * DH / 8 ? *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0) : u16x8_t{};
-      }
-#pragma unroll
-      for (int v = 0; v < BV; ++v) {
-        const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
-        const int64_t g = ((row0 + tl) * rowH + h) * NS + n0;
-        bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Bm + g) : u16x8_t{};
-        cv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Cm + g) : u16x8_t{};
-      }
-      // unconditional (in-bounds) load, so no branch waits on it
-      const float xv = bf_val(p.delta[(row0 + (tid & (Q - 1))) * rowH + h]);
-      if constexpr (MODE == kSum) {
-        // entering state from the aggregates (their loads go out behind the
-        // chunk's own); this workgroup writes checkpoint slot c - 1 (its
-        // entering state) and the last one also slot nC - 1
-        agg_sum<DH, NS, GLA, false, true>(p, cbeg, bh, lane, [&](int q, int& db, int& nb) {
-          db = w + 4 * (q / NBN), nb = q % NBN;
-          return db < NBD;
-        }, reinterpret_cast<f32x4_t(&)[DBW * NBN]>(hst));
-        const float* ag_last = p.agg + (bh * p.nC + p.nC - 1) * DH * NS;
-        const float t_last = p.tot[bh * p.nC + p.nC - 1];
-#pragma unroll
-        for (int i = 0; i < DBW; ++i) {
-          const int db = w + 4 * i;
-          if (db < NBD) {
-#pragma unroll
-            for (int nb = 0; nb < NBN; ++nb) {
-              const int e = (16 * db + l15) * NS + 16 * nb + 4 * l4;
-              const f32x4_t v = hst[i][nb];
-              if (cbeg > 0)
-                *reinterpret_cast<float4*>(p.ckpt + (bh * p.nC + cbeg - 1) * DH * NS + e) =
-                    make_float4(v[0], v[1], v[2], v[3]);
-              if (cbeg == p.nC - 1) {
-                const float4 g = *reinterpret_cast<const float4*>(ag_last + e);
-                *reinterpret_cast<float4*>(p.ckpt + (bh * p.nC + cbeg) * DH * NS + e) =
-                    make_float4(t_last * v[0] + g.x, t_last * v[1] + g.y, t_last * v[2] + g.z, t_last * v[3] + g.w);
-              }
-            }
-          }
-        }
-      }
+      if constexpr (MODE != kDirect) issue(c, tid);
 #pragma unroll
       for (int v = 0; v < UV; ++v) {
         const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
@@ -902,11 +909,7 @@ int launch_fwd(const ChunkArgs& p, int64_t B, hipStream_t s) {
     hipLaunchKernelGGL((pass_kernel<DH, NS, GLA>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0, s, p, 0);
     if (int rc = check_launch("chunked forward state pass")) return rc;
     hipLaunchKernelGGL((fwd_kernel<DH, NS, kPipe, GLA>), chunk_grid(p), dim3(256), 0, s, p);
-  } else if (p.mode == kSum) {   // R == 1
-    hipLaunchKernelGGL((agg_kernel<DH, NS, GLA>), chunk_grid(p), dim3(kAggThreads), 0, s, p, 0);
-    if (int rc = check_launch("chunked forward aggregates")) return rc;
-    hipLaunchKernelGGL((fwd_kernel<DH, NS, kSum, GLA>), chunk_grid(p), dim3(256), 0, s, p);
-  } else if (p.mode == kDirect) {   // R == 1
+  } else if (p.mode == kDirect || p.mode == kSum) {   // R == 1; kSum forward = direct
     if constexpr (DH * NS <= kDirectMaxState)
       hipLaunchKernelGGL((fwd_kernel<DH, NS, kDirect, GLA>), chunk_grid(p), dim3(256), 0, s, p);
     else

@@ -156,6 +156,13 @@ __device__ __forceinline__ u16x8_t frag_tr(const uint16_t* base, int pitch, int 
   return u16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// Pins a loaded value in a VGPR at this point, in every lane.  A value that
+// only some lanes use (a select on the lane index) lets the compiler move its
+// load into a divergent branch, where it then waits for every load in flight;
+// pinning it after the other loads are issued makes the wait cover only the
+// loads issued before it.
+__device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
+
 // Make one wave's LDS writes visible to its own later LDS reads.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -142,20 +142,20 @@ union BwdShared {
   BwdSmem<DH, NS, MODE != kPipe && MODE != kSum, MODE == kSum> m;
 };
 template <int DH, int NS>
-union BwdShared<DH, NS, kDirect> {
-  BwdSmem<DH, NS, true, false> m;
-  rr::chunked::DirectSmem<DH, NS, true> d;
+union BwdShared<DH, NS, kSum> {
+  BwdSmem<DH, NS, false, true> m;
+  rr::chunked::DirectSmem<DH, NS, true> d;   // the adjoint's sum, before the chunk's staging
 };
 
 // One chunk per workgroup with lam from the workspace (kPipe, pass_kernel) or
-// from the direct sum (kDirect); or a whole head per workgroup, lam carried
-// backwards in registers (kWhole).
+// summed over the later chunks' inputs in the kernel (kSum, direct_sum); or a
+// whole head per workgroup, lam carried backwards in registers (kWhole).
 template <int DH, int NS, int MODE>
 __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
   using K = Cfg<DH, NS>;
   // PIPE: one chunk per workgroup with lam from the workspace (kPipe) or summed
-  // from the aggregates (kSum, SUM); the operands of du and of GH / UL are
-  // register fragments
+  // in the kernel (kSum, SUM); the operands of du and of GH / UL are register
+  // fragments
   constexpr bool SUM = MODE == kSum;
   constexpr bool PIPE = MODE == kPipe || SUM;
   __shared__ BwdShared<DH, NS, MODE> smu;
@@ -166,7 +166,7 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
     h = blockIdx.y, b = blockIdx.z, cbeg = 0;
   } else {
     // early chunks cost most where the adjoint is a sum over the later ones
-    const rr::chunked::ChunkId id = rr::chunked::chunk_id(p, MODE == kDirect || MODE == kSum, false);
+    const rr::chunked::ChunkId id = rr::chunked::chunk_id(p, MODE == kSum, false);
     if (!id.valid) return;
     h = id.h, b = id.b, cbeg = id.c;
   }
@@ -181,28 +181,11 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
   f32x4_t lam[K::NBW];
 #pragma unroll
   for (int jj = 0; jj < K::NBW; ++jj) lam[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  if constexpr (MODE == kDirect) {
-    const float gam_all = rr::chunked::direct_sum<DH, NS, false, true>(p, cbeg, b, h, a, smu.d);
-    const float* dfb = p.dfinal != nullptr ? p.dfinal + sbase : nullptr;
-#pragma unroll
-    for (int jj = 0; jj < K::NBW; ++jj) {
-      const int j = w + 4 * jj;
-      if (j < K::NB) {
-        const int db = j / NBN, nb = j % NBN;
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          lam[jj][r] = rr::chunked::direct_value<DH, NS, false, true>(smu.d, gam_all, dfb,
-                                                                      16 * db + 4 * (lane >> 4) + r, 16 * nb + (lane & 15));
-      }
-    }
-    __syncthreads();   // the chunk below reuses the LDS of the sum
-  }
-  // the adjoint entering chunk c - 1 is needed for the whole head, and for
-  // the initial-state gradient at chunk 0
-  const bool carry = MODE == kWhole || (MODE == kDirect && cbeg == 0 && p.dh0 != nullptr);
+  // the adjoint entering chunk c - 1 is needed for the whole head
+  const bool carry = MODE == kWhole;
   const float* lsrc = MODE == kPipe ? p.agg + (((int64_t)b * p.H + h) * p.nC + cbeg) * DH * NS
                                     : (p.dfinal != nullptr ? p.dfinal + sbase : nullptr);
-  if (MODE != kDirect && !SUM && lsrc != nullptr) {
+  if (!SUM && lsrc != nullptr) {
 #pragma unroll
     for (int jj = 0; jj < K::NBW; ++jj) {
       const int j = w + 4 * jj;
@@ -234,82 +217,89 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
       u16x8_t uv[UV], bv[BV], cv[BV];
       float4 gv[GV];
       float dv = 0.f;
+      auto issue = [&]() {
 #pragma unroll
-      for (int v = 0; v < UV; ++v) {
-        const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
-        uv[v] = i < Q * DH / 8 ? *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0) : u16x8_t{};
-      }
+        for (int v = 0; v < UV; ++v) {
+          const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
+          uv[v] = i < Q * DH / 8 ? *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0) : u16x8_t{};
+        }
 #pragma unroll
-      for (int v = 0; v < BV; ++v) {
-        const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
-        const int64_t g = ((row0 + tl) * rowH + h) * NS + n0;
-        bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Bm + g) : u16x8_t{};
-        cv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Cm + g) : u16x8_t{};
-      }
+        for (int v = 0; v < BV; ++v) {
+          const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+          const int64_t g = ((row0 + tl) * rowH + h) * NS + n0;
+          bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Bm + g) : u16x8_t{};
+          cv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Cm + g) : u16x8_t{};
+        }
 #pragma unroll
-      for (int v = 0; v < GV; ++v) {
-        const int i = tid + 256 * v, tl = (i / (DH / 4)) & (Q - 1), d0 = 4 * (i % (DH / 4));
-        gv[v] = i < Q * DH / 4 ? *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-      // unconditional (in-bounds) load, so no branch waits on it
-      dv = bf_val(p.delta[(row0 + (lane & (Q - 1))) * rowH + h]);   // lanes >= 32 masked at use
-      const float* hsrc = c > 0 ? p.ckpt + (((int64_t)b * p.H + h) * p.nC + (c - 1)) * DH * NS
-                                : (p.h0 != nullptr ? p.h0 + sbase : nullptr);
-      if constexpr (PIPE) {
-        if (w >= 2) {
-          // GH / UL tasks: the h_in / lam column nb as 16x16x16 B fragments (k = d)
+        for (int v = 0; v < GV; ++v) {
+          const int i = tid + 256 * v, tl = (i / (DH / 4)) & (Q - 1), d0 = 4 * (i % (DH / 4));
+          gv[v] = i < Q * DH / 4 ? *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        // unconditional (in-bounds) load, so no branch waits on it
+        dv = bf_val(p.delta[(row0 + (lane & (Q - 1))) * rowH + h]);   // lanes >= 32 masked at use
+        const float* hsrc = c > 0 ? p.ckpt + (((int64_t)b * p.H + h) * p.nC + (c - 1)) * DH * NS
+                                  : (p.h0 != nullptr ? p.h0 + sbase : nullptr);
+        if constexpr (PIPE) {
+          if (w >= 2) {
+            // GH / UL tasks: the h_in / lam column nb as 16x16x16 B fragments (k = d)
 #pragma unroll
-          for (int q = 0; q < TPW; ++q) {
-            const int task = (w - 2) + 2 * q;
-            const int kind = task / NBN, nb = task % NBN;
-            const float* src = kind == 0 ? hsrc : lsrc;
-            if (SUM && kind == 1) continue;   // from LDS after the staging barrier
+            for (int q = 0; q < TPW; ++q) {
+              const int task = (w - 2) + 2 * q;
+              const int kind = task / NBN, nb = task % NBN;
+              const float* src = kind == 0 ? hsrc : lsrc;
+              if (SUM && kind == 1) continue;   // from LDS after the staging barrier
 #pragma unroll
-            for (int kb = 0; kb < DH / 16; ++kb)
+              for (int kb = 0; kb < DH / 16; ++kb)
 #pragma unroll
-              for (int e = 0; e < 4; ++e)
-                pcol[q][kb][e] = (task < 2 * NBN && src != nullptr)
-                                     ? src[(16 * kb + 4 * (lane >> 4) + e) * NS + 16 * nb + (lane & 15)]
-                                     : 0.f;
+                for (int e = 0; e < 4; ++e)
+                  pcol[q][kb][e] = (task < 2 * NBN && src != nullptr)
+                                       ? src[(16 * kb + 4 * (lane >> 4) + e) * NS + 16 * nb + (lane & 15)]
+                                       : 0.f;
+            }
           }
         }
-      }
 #pragma unroll
-      for (int jj = 0; jj < K::NBW; ++jj) {
-        const int j = w + 4 * jj;
-        hin[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        if (j < K::NB && hsrc != nullptr) {
-          const int db = j / NBN, nb = j % NBN;
+        for (int jj = 0; jj < K::NBW; ++jj) {
+          const int j = w + 4 * jj;
+          hin[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          if (j < K::NB && hsrc != nullptr) {
+            const int db = j / NBN, nb = j % NBN;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) hin[jj][r] = hsrc[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)];
+            for (int r = 0; r < 4; ++r) hin[jj][r] = hsrc[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)];
+          }
         }
-      }
-      // kSum: lam from the aggregates (their loads go out behind the chunk's own)
+      };
       if constexpr (SUM) {
-        const int64_t bh = (int64_t)b * p.H + h;
-        rr::chunked::agg_sum<DH, NS, false, true>(p, cbeg, bh, lane, [&](int q, int& db, int& nb) {
-          const int j = w + 4 * q;
-          db = j / NBN, nb = j % NBN;
-          return j < K::NB;
-        }, lam);
-        // the summed lam for the register fragments (read after the staging barrier)
-        // and, at chunk 0, dh0 = tot_0 lam_0 + G_0
-        const float* g0 = p.agg + bh * p.nC * DH * NS;
-        const float t0 = p.tot[bh * p.nC];
+        // lam summed over the later chunks' inputs; the chunk's own loads go
+        // out when each wave has staged its last summed chunk; the chunk-0
+        // workgroup also writes dh0
+        const float gam_all = rr::chunked::direct_sum<DH, NS, false, true, true>(p, cbeg, b, h, a, smu.d, p.dh0, issue);
+        const float* dfb = p.dfinal != nullptr ? p.dfinal + sbase : nullptr;
 #pragma unroll
         for (int jj = 0; jj < K::NBW; ++jj) {
           const int j = w + 4 * jj;
           if (j < K::NB) {
             const int db = j / NBN, nb = j % NBN;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int d = 16 * db + 4 * (lane >> 4) + r, n = 16 * nb + (lane & 15);
-              m.LS[d][n] = lam[jj][r];
-              if (cbeg == 0 && p.dh0 != nullptr) p.dh0[sbase + d * NS + n] = t0 * lam[jj][r] + g0[d * NS + n];
-            }
+            for (int r = 0; r < 4; ++r)
+              lam[jj][r] = rr::chunked::direct_value<DH, NS, false, true>(smu.d, gam_all, dfb, 16 * db + 4 * (lane >> 4) + r,
+                                                                          16 * nb + (lane & 15));
           }
         }
+        __syncthreads();   // the sum's LDS is dead: the staging below reuses it
+        // the summed lam for the register fragments (read after the staging barrier)
+#pragma unroll
+        for (int jj = 0; jj < K::NBW; ++jj) {
+          const int j = w + 4 * jj;
+          if (j < K::NB) {
+            const int db = j / NBN, nb = j % NBN;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) m.LS[16 * db + 4 * (lane >> 4) + r][16 * nb + (lane & 15)] = lam[jj][r];
+          }
+        }
+      } else {
+        issue();
       }
       // LDS writes
 #pragma unroll
@@ -810,16 +800,8 @@ int launch_bwd(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
                        p, 1);
     if (int rc = rr::check_launch("ssd chunked backward adjoint pass")) return rc;
     hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, kPipe>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
-  } else if (p.mode == kSum) {   // R == 1
-    hipLaunchKernelGGL((rr::chunked::agg_kernel<DH, NS, false>), rr::chunked::chunk_grid(p),
-                       dim3(rr::chunked::kAggThreads), 0, s, p, 1);
-    if (int rc = rr::check_launch("ssd chunked backward aggregates")) return rc;
+  } else if (p.mode == kSum || p.mode == kDirect) {   // R == 1; adjoint summed in the kernel
     hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, kSum>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
-  } else if (p.mode == kDirect) {   // R == 1
-    if constexpr (DH * NS <= rr::chunked::kDirectMaxState)
-      hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, kDirect>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
-    else
-      return rr::fail(RR_EUNSUPPORTED, "ssd chunked backward: state too large for the direct mode");
   } else {   // R == nC
     hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, kWhole>), dim3(1, p.H, (unsigned)B), dim3(256), 0, s, p);
   }
@@ -835,6 +817,11 @@ bool ssd2_bwd_supported(int64_t Dh, int64_t N) {
   return (Dh == 32 || Dh == 64) && (N == 16 || N == 32 || N == 64 || N == 128);
 }
 
+// Wider states (N >= 64: the column-owned backward) take the direct mode only
+// for the shortest heads.
+constexpr int64_t kDirectMaxChunksWide = 4;
+constexpr int64_t kDirectMaxWorkgroups = 4096;
+
 int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N, int pass) {
   const int64_t grid = nC * ((B * H + chunked::kXcds - 1) / chunked::kXcds * chunked::kXcds);
   if (grid >= ((int64_t)1 << 31)) return chunked::kWhole;   // beyond a 1-D per-chunk grid
@@ -843,25 +830,27 @@ int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N, int pa
   // B96 L512 H12 Dh64 N16 137 / 414 vs 194 / 357 (sum mode); B8 L4096 H80
   // Dh64 N128 2308 / 7457 vs 4025 / 4873 (pipelined)).
   if (B * H >= 512 && pass == 0) return chunked::kWhole;
-  if (nC <= chunked::kDirectMaxChunks && Dh * N <= chunked::kDirectMaxState) return chunked::kDirect;
-  // the aggregate-sum mode where the backward's small-N kernel takes it
-  if (nC <= chunked::kSumMaxChunks && N <= 32) return chunked::kSum;
+  // Short heads, few of them: every chunk's workgroup sums over the other
+  // chunks' inputs itself (a single kernel per pass; the sums' reads grow as
+  // nC^2 per head, so not once the workgroups fill the GPU several times
+  // over); kSum where the backward's small-N kernel takes it (its forward is
+  // the direct kernel)
+  if (nC <= chunked::kDirectMaxChunks && N <= 32 && B * H * nC <= kDirectMaxWorkgroups) return chunked::kSum;
+  if (nC <= kDirectMaxChunksWide && Dh * N <= chunked::kDirectMaxState) return chunked::kDirect;
   return chunked::kPipe;
 }
 
 // Workspace layout (floats, each part 256-byte aligned): per-chunk decays
-// [B,H,nC] (pipelined and sum modes), chunk aggregates [B,H,nC,Dh,N] (sum
-// mode, both passes), dA partials [B,H,nR,N] (backward), backward chunk
-// aggregates / adjoints [B,H,nC,Dh,N] (pipelined backward).
+// [B,H,nC] (pipelined mode), dA partials [B,H,nR,N] (backward), backward
+// chunk aggregates / adjoints [B,H,nC,Dh,N] (pipelined backward).
 namespace {
 int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }
 }
 
 size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int mode, int64_t Dh, int64_t N, int pass) {
   const int64_t nR = mode == chunked::kWhole ? 1 : nC;
-  const bool pipe = mode == chunked::kPipe, sum = mode == chunked::kSum;
-  int64_t f = pipe || sum ? align64(B * H * nC) : 0;
-  if (sum) f += align64(B * H * nC * Dh * N);
+  const bool pipe = mode == chunked::kPipe;
+  int64_t f = pipe ? align64(B * H * nC) : 0;
   if (pass == 1) {
     f += align64(B * H * nR * N);
     if (pipe) f += align64(B * H * nC * Dh * N);
@@ -872,10 +861,9 @@ size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int mode, int64_t Dh, int
 void ssd2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass) {
   float* f = static_cast<float*>(ws);
   const int64_t nR = (a.nC + a.R - 1) / a.R;
-  const bool pipe = a.mode == chunked::kPipe, sum = a.mode == chunked::kSum;
+  const bool pipe = a.mode == chunked::kPipe;
   a.tot = a.ws = a.agg = nullptr;
-  if (pipe || sum) { a.tot = f; f += align64(B * a.H * a.nC); }
-  if (sum) { a.agg = f; f += align64(B * a.H * a.nC * a.DH * a.NS); }
+  if (pipe) { a.tot = f; f += align64(B * a.H * a.nC); }
   if (pass == 1) {
     a.ws = f; f += align64(B * a.H * nR * a.NS);
     if (pipe) a.agg = f;
