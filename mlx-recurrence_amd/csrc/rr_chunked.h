@@ -383,12 +383,15 @@ __global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
 //             F_j = tot_{c+1} ... tot_{j-1},   Gam = tot_{c+1} ... tot_{nC-1}
 // (m31, w, gam and tot of chunk j as in step_scalars).  Wave w takes chunks
 // j0 + w, j0 + w + 4, ... of the range (at most kDirectPerWave).  Their inputs
-// are loaded up to four chunks ahead, staged in the wave's own LDS area in
-// their natural [step][column] layout, the fp32 factor applied and split into
-// bf16 hi + lo, and read back as MFMA operands (k = step) by transposing LDS
-// reads; no transposed copies and no workgroup barriers in the loop.  Each
-// wave accumulates every 16x16 block of the state; the four partial sums are
-// added in a fixed order (deterministic).
+// are loaded up to four chunks ahead.  The bf16 operands are staged in the
+// wave's own LDS area in their natural [step][column] layout (forward: B
+// with the fp32 factor applied, split into bf16 hi + lo) and read back as
+// MFMA operands (k = step) by transposing LDS reads; the backward's fp32 dY
+// is loaded straight into its operand layout (each lane eight steps of one
+// column) and weighted and split in registers, which keeps it out of LDS.
+// No transposed copies and no workgroup barriers in the loop.  Each wave
+// accumulates every 16x16 block of the state; the four partial sums are added
+// in a fixed order (deterministic).
 constexpr int kDirectMaxChunks = 16;
 constexpr int kDirectMaxState = 64 * 64;   // Dh * N (the partial sums live in LDS)
 constexpr int kDirectPerWave = kDirectMaxChunks / 4;
@@ -402,8 +405,9 @@ struct alignas(16) DirectSmem {
   static constexpr int PY = NS == 16 ? 16 : NS + 16;
   union {
     struct {
-      uint16_t X[BWD ? 2 : 1][Q][PX];   // fwd: U [s][d]; bwd: (F gam o dY) hi, lo [t][d]
+      uint16_t X[BWD ? 1 : Q][PX];      // fwd: U [s][d] (the backward's dY stays in registers)
       uint16_t Y[BWD ? 1 : 2][Q][PY];   // fwd: (F m31 w o B) hi, lo [s][n]; bwd: C [t][n]
+      float cw[BWD ? Q : 4];            // bwd: the chunk's step factors F gam_t
     } st[4];
     float red[2][DH * NS];              // partial sums of waves 0 + 2 and 1 + 3, [d][n]
   };
@@ -429,9 +433,9 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
                             float* dh0 = nullptr, PRE pre = PRE{}) {
   using S = DirectSmem<DH, NS, BWD>;
   constexpr int NBD = DH / 16, NBN = NS / 16;
-  constexpr int XV = BWD ? Q * DH / 4 / 64 : Q * DH / 8 / 64;   // per lane and chunk: float4 of dY / u16x8 of U
+  constexpr int XV = Q * DH / 8 / 64;                           // fwd, per lane and chunk: u16x8 of U
   constexpr int YV = Q * NS / 8 / 64;                           // u16x8 of B (fwd) or C (bwd)
-  constexpr int VPC = 4 * (XV + YV);                            // registers per chunk in flight
+  constexpr int VPC = BWD ? 8 * NBD + 4 * YV : 4 * (XV + YV);   // registers per chunk in flight
   constexpr int REGS = BWD && NS > 16 ? 48 : 80;                // budget for them
   constexpr int PF = REGS / VPC >= 4 ? 4 : REGS / VPC >= 2 ? 2 : 1;   // chunks in flight per wave
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -454,16 +458,21 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
     const int64_t row0 = (int64_t)b * p.L + (int64_t)chunk(k) * Q;
     xs[k] = bf_val(p.delta[(row0 + (lane & (Q - 1))) * rowH + h]);   // lanes >= 32 masked below
   }
+  // forward: U rows as 16-byte pieces; backward: dY in the A-operand layout
+  // of 16x16x32, lane (j, g) = (lane % 16, lane / 16) holding dY[8 g + e][16 db + j]
   u16x8_t xu[PF][BWD ? 1 : XV], yv[PF][YV];
-  float4 xf[PF][BWD ? XV : 1];
+  float xg[PF][BWD ? NBD : 1][BWD ? 8 : 1];
+  const int jl = lane & 15, gl = lane >> 4;
   auto load = [&](int slot, int j) {
     const int64_t row0 = (int64_t)b * p.L + (int64_t)j * Q;
+    if constexpr (BWD) {
 #pragma unroll
-    for (int v = 0; v < XV; ++v) {
-      if constexpr (BWD) {
-        const int i = lane + 64 * v, t = i / (DH / 4), d0 = 4 * (i % (DH / 4));
-        xf[slot][v] = *reinterpret_cast<const float4*>(p.dy + ((row0 + t) * rowH + h) * DH + d0);
-      } else {
+      for (int db = 0; db < NBD; ++db)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xg[slot][db][e] = p.dy[((row0 + 8 * gl + e) * rowH + h) * DH + 16 * db + jl];
+    } else {
+#pragma unroll
+      for (int v = 0; v < XV; ++v) {
         const int i = lane + 64 * v, t = i / (DH / 8), d0 = 8 * (i % (DH / 8));
         xu[slot][v] = *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + t) * rowH + h) * DH + d0);
       }
@@ -529,27 +538,48 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
     if (k >= nw) break;
     const int slot = k % PF;
     const float cf = coef[k] * fk[k];   // lane s < 32: the factor of step s
+    if constexpr (BWD) {
+      if (lane < Q) st.cw[lane] = cf;
 #pragma unroll
-    for (int v = 0; v < XV; ++v) {
-      if constexpr (BWD) {
-        const int i = lane + 64 * v, t = i / (DH / 4), d0 = 4 * (i % (DH / 4));
-        const float ct = __shfl(cf, t);
-        const float4 g = xf[slot][v];
-        u16x4_t hi, lo;
-        rr::bf_split4(f32x4_t{ct * g.x, ct * g.y, ct * g.z, ct * g.w}, hi, lo);
-        *reinterpret_cast<u16x4_t*>(&st.X[0][t][d0]) = hi;
-        *reinterpret_cast<u16x4_t*>(&st.X[BWD ? 1 : 0][t][d0]) = lo;
-      } else {
-        const int i = lane + 64 * v, t = i / (DH / 8), d0 = 8 * (i % (DH / 8));
-        *reinterpret_cast<u16x8_t*>(&st.X[0][t][d0]) = xu[slot][v];
-      }
-    }
-#pragma unroll
-    for (int v = 0; v < YV; ++v) {
-      const int i = lane + 64 * v, t = i / (NS / 8), n0 = 8 * (i % (NS / 8));
-      if constexpr (BWD) {
+      for (int v = 0; v < YV; ++v) {
+        const int i = lane + 64 * v, t = i / (NS / 8), n0 = 8 * (i % (NS / 8));
         *reinterpret_cast<u16x8_t*>(&st.Y[0][t][n0]) = yv[slot][v];
-      } else {
+      }
+      wave_lds_sync();
+      // this lane's step factors (steps 8 g .. 8 g + 7; broadcast reads)
+      const float4 c0 = *reinterpret_cast<const float4*>(&st.cw[8 * gl]);
+      const float4 c1 = *reinterpret_cast<const float4*>(&st.cw[8 * gl + 4]);
+      const float cwl[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+      u16x8_t yf[NBN];
+#pragma unroll
+      for (int nb = 0; nb < NBN; ++nb) yf[nb] = frag_tr(&st.Y[0][0][16 * nb], S::PY, lane);
+#pragma unroll
+      for (int db = 0; db < NBD; ++db) {
+        float xw[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xw[e] = cwl[e] * xg[slot][db][e];
+        u16x8_t xh, xl;
+        rr::bf_split8(xw, xh, xl);
+#pragma unroll
+        for (int nb = 0; nb < NBN; ++nb) {
+          acc[db][nb] = mfma16(xh, yf[nb], acc[db][nb]);
+          acc[db][nb] = mfma16(xl, yf[nb], acc[db][nb]);
+        }
+      }
+      // the registers of this slot are free: the loads of chunk k + PF
+      // (issued even past this wave's last chunk, as a repeat of it, so that
+      // the number of loads in flight is the same on every path and the
+      // waits for a slot stay exact)
+      if (k + PF < kDirectPerWave) load(slot, chunk(k + PF));
+    } else {
+#pragma unroll
+      for (int v = 0; v < XV; ++v) {
+        const int i = lane + 64 * v, t = i / (DH / 8), d0 = 8 * (i % (DH / 8));
+        *reinterpret_cast<u16x8_t*>(&st.X[t][d0]) = xu[slot][v];
+      }
+#pragma unroll
+      for (int v = 0; v < YV; ++v) {
+        const int i = lane + 64 * v, t = i / (NS / 8), n0 = 8 * (i % (NS / 8));
         const float ct = __shfl(cf, t);
         float yw[8];
 #pragma unroll
@@ -559,27 +589,21 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
         *reinterpret_cast<u16x8_t*>(&st.Y[0][t][n0]) = hi;
         *reinterpret_cast<u16x8_t*>(&st.Y[BWD ? 0 : 1][t][n0]) = lo;
       }
-    }
-    // the registers of this slot are free: the loads of chunk k + PF (issued
-    // even past this wave's last chunk, as a repeat of it, so that the number
-    // of loads in flight is the same on every path and the waits for a slot
-    // stay exact)
-    if (k + PF < kDirectPerWave) load(slot, chunk(k + PF));
-    wave_lds_sync();
-    u16x8_t yf[BWD ? 1 : 2][NBN];
+      // the registers of this slot are free: the loads of chunk k + PF (see above)
+      if (k + PF < kDirectPerWave) load(slot, chunk(k + PF));
+      wave_lds_sync();
+      u16x8_t yf[2][NBN];
 #pragma unroll
-    for (int nb = 0; nb < NBN; ++nb)
+      for (int nb = 0; nb < NBN; ++nb)
 #pragma unroll
-      for (int hl = 0; hl < (BWD ? 1 : 2); ++hl) yf[hl][nb] = frag_tr(&st.Y[hl][0][16 * nb], S::PY, lane);
+        for (int hl = 0; hl < 2; ++hl) yf[hl][nb] = frag_tr(&st.Y[hl][0][16 * nb], S::PY, lane);
 #pragma unroll
-    for (int db = 0; db < NBD; ++db) {
-#pragma unroll
-      for (int hl = 0; hl < (BWD ? 2 : 1); ++hl) {
-        const u16x8_t xfr = frag_tr(&st.X[hl][0][16 * db], S::PX, lane);
+      for (int db = 0; db < NBD; ++db) {
+        const u16x8_t xfr = frag_tr(&st.X[0][16 * db], S::PX, lane);
 #pragma unroll
         for (int nb = 0; nb < NBN; ++nb) {
           acc[db][nb] = mfma16(xfr, yf[0][nb], acc[db][nb]);
-          if constexpr (!BWD) acc[db][nb] = mfma16(xfr, yf[BWD ? 0 : 1][nb], acc[db][nb]);
+          acc[db][nb] = mfma16(xfr, yf[1][nb], acc[db][nb]);
         }
       }
     }
