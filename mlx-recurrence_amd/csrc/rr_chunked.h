@@ -208,27 +208,43 @@ __device__ __forceinline__ float head_rate(const ChunkArgs& p, int h) {
 //                 and dh0 = tot_0 lam_0 + G_0.
 //  3. the main kernel, one workgroup per chunk, reads its entering state
 //     (and, backward, lam_k) and does the chunk's dense products.
-// agg_kernel: a workgroup of four waves per chunk stages the operands (all
-// loads first), then wave w forms the 16x16 blocks j = w, w + 4, ... of the
-// aggregate.
+// agg_kernel: a workgroup of four waves per chunk; wave w forms the 16x16
+// blocks w NBW .. w NBW + NBW - 1 of the aggregate (one row block of the state
+// for Dh = 64).  The operands are read with k = step: U (forward) and the
+// N-wide B / C are staged in LDS in their natural [step][column] layout and
+// read back by transposing reads; the backward's fp32 dY goes straight into
+// A-operand registers (lane (j, g) = (lane % 16, lane / 16): dY[8 g + e][16 db
+// + j]), is weighted by gam and split into bf16 hi + lo there.  The forward's
+// factor m31 w is applied to the B fragments in registers.
 constexpr int kAggThreads = 256;
 template <int DH, int NS, bool GLA>
+struct AggSmem {
+  static constexpr int PX = DH + 16, PY = NS == 16 ? 16 : NS + 16;   // see DirectSmem
+  uint16_t X[Q][PX];    // kind 0: U [s][d]
+  uint16_t Y[Q][PY];    // B [s][n] (kind 0) or C [t][n] (kind 1)
+  float wsh[Q];         // kind 0: m31_s w_s; kind 1: gam_t
+};
+template <int DH, int NS, bool GLA>
 __global__ __launch_bounds__(kAggThreads) void agg_kernel(ChunkArgs p, int kind) {
-  constexpr int NBN = NS / 16, NB = (DH / 16) * NBN;
-  __shared__ uint16_t XT_hi[DH][PQ], XT_lo[DH][PQ];   // kind 0: U^T [d][s] (hi only); kind 1: (gam o dY)^T
-  __shared__ uint16_t YT_hi[NS][PQ], YT_lo[NS][PQ];   // kind 0: (m31 o w o B)^T split; kind 1: C^T (hi only)
-  __shared__ float wsh[Q];                            // kind 0: m31_s w_s; kind 1: gam_t
+  using S = AggSmem<DH, NS, GLA>;
+  constexpr int NBN = NS / 16, NB = (DH / 16) * NBN, NBW = (NB + 3) / 4;
+  constexpr int NDB = NBW > NBN ? NBW / NBN : 1;   // row blocks per wave
+  __shared__ __attribute__((aligned(16))) S sm;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int jl = lane & 15, gl = lane >> 4;
   const ChunkId id = chunk_id(p, false, false);
   if (!id.valid) return;
   const int c = id.c, h = id.h, b = id.b;
   const float a = head_rate<GLA>(p, h);
   const int64_t rowH = p.H, row0 = (int64_t)b * p.L + (int64_t)c * Q;
   constexpr int T = kAggThreads;
-  constexpr int UV = (Q * DH / 8 + T - 1) / T, GV = (Q * DH / 4 + T - 1) / T, BV = (Q * NS / 8 + T - 1) / T;
+  constexpr int UV = (Q * DH / 8 + T - 1) / T, BV = (Q * NS / 8 + T - 1) / T;
+  const int jw0 = w * NBW;                       // this wave's first block
+  const bool busy = jw0 < NB;
+  const int db0 = busy ? jw0 / NBN : 0;          // its first row block
   // loads first
   u16x8_t uv[UV], bv[BV];
-  float4 gv[GV];
+  float dyv[NDB][8];
   if (kind == 0) {
 #pragma unroll
     for (int v = 0; v < UV; ++v) {
@@ -237,11 +253,10 @@ __global__ __launch_bounds__(kAggThreads) void agg_kernel(ChunkArgs p, int kind)
     }
   } else {
 #pragma unroll
-    for (int v = 0; v < GV; ++v) {
-      const int i = tid + T * v, tl = (i / (DH / 4)) & (Q - 1), d0 = 4 * (i % (DH / 4));
-      gv[v] = i < Q * DH / 4 ? *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0)
-                             : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    for (int q = 0; q < NDB; ++q)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        dyv[q][e] = p.dy[((row0 + 8 * gl + e) * rowH + h) * DH + 16 * min(db0 + q, DH / 16 - 1) + jl];
   }
   const uint16_t* bsrc = kind == 0 ? p.Bm : p.Cm;
 #pragma unroll
@@ -250,72 +265,66 @@ __global__ __launch_bounds__(kAggThreads) void agg_kernel(ChunkArgs p, int kind)
     bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(bsrc + ((row0 + tl) * rowH + h) * NS + n0) : u16x8_t{};
   }
   if (w == 0) {
-    const float xl = bf_val(p.delta[(row0 + (lane & (Q - 1))) * rowH + h]);   // unconditional load
+    float xl = bf_val(p.delta[(row0 + (lane & (Q - 1))) * rowH + h]);   // unconditional load
+    rr::pin(xl);
     const float xv = lane < Q ? xl : (GLA ? 1.f : 0.f);
     const StepScalars sc = step_scalars<GLA>(xv, a, lane);
-    if (lane < Q) wsh[lane] = kind == 0 ? sc.m31 * sc.w : sc.gam;
+    if (lane < Q) sm.wsh[lane] = kind == 0 ? sc.m31 * sc.w : sc.gam;
     if (lane == 0) p.tot[((int64_t)b * p.H + h) * p.nC + c] = sc.tot;
   }
-  __syncthreads();
   if (kind == 0) {
 #pragma unroll
     for (int v = 0; v < UV; ++v) {
       const int i = tid + T * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
-      if (i < Q * DH / 8) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) XT_hi[d0 + e][tl] = uv[v][e];
-      }
-    }
-  } else {
-#pragma unroll
-    for (int v = 0; v < GV; ++v) {
-      const int i = tid + T * v, tl = (i / (DH / 4)) & (Q - 1), d0 = 4 * (i % (DH / 4));
-      if (i < Q * DH / 4) {
-        const float gt = wsh[tl];
-        const float g4[4] = {gv[v].x, gv[v].y, gv[v].z, gv[v].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          uint16_t hi, lo;
-          bf_split(gt * g4[e], hi, lo);
-          XT_hi[d0 + e][tl] = hi;
-          XT_lo[d0 + e][tl] = lo;
-        }
-      }
+      if (i < Q * DH / 8) *reinterpret_cast<u16x8_t*>(&sm.X[tl][d0]) = uv[v];
     }
   }
 #pragma unroll
   for (int v = 0; v < BV; ++v) {
     const int i = tid + T * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
-    if (i < Q * NS / 8) {
-      const float ws = wsh[tl];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if (kind == 0) {
-          uint16_t hi, lo;
-          bf_split(ws * bf_val(bv[v][e]), hi, lo);
-          YT_hi[n0 + e][tl] = hi;
-          YT_lo[n0 + e][tl] = lo;
-        } else {
-          YT_hi[n0 + e][tl] = bv[v][e];
-        }
-      }
-    }
+    if (i < Q * NS / 8) *reinterpret_cast<u16x8_t*>(&sm.Y[tl][n0]) = bv[v];
   }
   __syncthreads();
+  if (!busy) return;
+  // this lane's step factors (steps 8 g .. 8 g + 7; broadcast reads)
+  const float4 c0 = *reinterpret_cast<const float4*>(&sm.wsh[8 * gl]);
+  const float4 c1 = *reinterpret_cast<const float4*>(&sm.wsh[8 * gl + 4]);
+  const float cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
   float* dst = (kind == 0 ? p.ckpt : p.agg) + (((int64_t)b * p.H + h) * p.nC + c) * DH * NS;
 #pragma unroll
-  for (int jj = 0; jj < (NB + 3) / 4; ++jj) {
-    const int j = w + 4 * jj;
-    if (j >= NB) break;
-    const int db = j / NBN, nb = j % NBN;
-    const u16x8_t fa = frag(&XT_hi[16 * db + (lane & 15)][8 * (lane >> 4)]);
-    const u16x8_t fb = frag(&YT_hi[16 * nb + (lane & 15)][8 * (lane >> 4)]);
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    acc = mfma16(fa, fb, acc);
-    if (kind == 0) acc = mfma16(fa, frag(&YT_lo[16 * nb + (lane & 15)][8 * (lane >> 4)]), acc);
-    else acc = mfma16(frag(&XT_lo[16 * db + (lane & 15)][8 * (lane >> 4)]), fb, acc);
+  for (int q = 0; q < NDB; ++q) {
+    const int db = db0 + q;
+    if (db * NBN >= NB || db * NBN >= jw0 + NBW) break;
+    u16x8_t xh, xl;   // A operand (rows d, k = step): U (kind 0: hi only) or gam o dY hi, lo
+    if (kind == 0) {
+      xh = frag_tr(&sm.X[0][16 * db], S::PX, lane);
+    } else {
+      float xw[8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) dst[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)] = acc[r];
+      for (int e = 0; e < 8; ++e) xw[e] = cw[e] * dyv[q][e];
+      rr::bf_split8(xw, xh, xl);
+    }
+#pragma unroll
+    for (int nb = 0; nb < NBN; ++nb) {
+      const int j = db * NBN + nb;
+      if (j < jw0 || j >= jw0 + NBW) continue;
+      const u16x8_t yr = frag_tr(&sm.Y[0][16 * nb], S::PY, lane);   // B operand (k = step, columns n)
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      if (kind == 0) {
+        float yw[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) yw[e] = cw[e] * bf_val(yr[e]);
+        u16x8_t yh, yl;
+        rr::bf_split8(yw, yh, yl);
+        acc = mfma16(xh, yh, acc);
+        acc = mfma16(xh, yl, acc);
+      } else {
+        acc = mfma16(xh, yr, acc);
+        acc = mfma16(xl, yr, acc);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dst[(16 * db + 4 * gl + r) * NS + 16 * nb + jl] = acc[r];
+    }
   }
 }
 
