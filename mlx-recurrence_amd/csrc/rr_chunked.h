@@ -329,7 +329,9 @@ __global__ __launch_bounds__(kAggThreads) void agg_kernel(ChunkArgs p, int kind)
 }
 
 // Sequential pass over the chunks of one (batch, head), one state element per
-// thread; loads are issued kPass chunks ahead of their use.
+// thread.  The loads of kPass chunks go out together, unconditionally (chunk
+// indices clamped into range; out-of-range terms are dropped in the fold), so
+// that no branch waits on a load.
 template <int DH, int NS, bool GLA>
 __global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
   constexpr int kPass = 16;
@@ -346,9 +348,9 @@ __global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
       float sv[kPass], tv[kPass];
 #pragma unroll
       for (int q = 0; q < kPass; ++q) {
-        const bool ok = k0 + q < nC;
-        sv[q] = ok ? buf[(int64_t)(k0 + q) * DH * NS] : 0.f;
-        tv[q] = ok ? tot[k0 + q] : 0.f;
+        const int k = min(k0 + q, nC - 1);
+        sv[q] = buf[(int64_t)k * DH * NS];
+        tv[q] = tot[k];
       }
 #pragma unroll
       for (int q = 0; q < kPass; ++q) {
@@ -365,9 +367,9 @@ __global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
       float gv[kPass], tv[kPass];
 #pragma unroll
       for (int q = 0; q < kPass; ++q) {
-        const bool ok = k0 - q >= 0;
-        gv[q] = ok ? buf[(int64_t)(k0 - q) * DH * NS] : 0.f;
-        tv[q] = ok ? tot[k0 - q] : 0.f;
+        const int k = max(k0 - q, 0);
+        gv[q] = buf[(int64_t)k * DH * NS];
+        tv[q] = tot[k];
       }
 #pragma unroll
       for (int q = 0; q < kPass; ++q) {
