@@ -203,7 +203,8 @@ SSD_CASES = [
     (1, 128, 512, 32, 16, 32, BF16, "cfg", True, True, 17),
     (2, 96, 256, 64, 32, 32, BF16, "cfg", False, True, 18),
     (2, 64, 256, 64, 16, 32, BF16, "cfg", True, False, 19),
-    # more than 16 chunks: pipelined mode (aggregate, state-pass and chunk kernels)
+    # more than 16 chunks: pipelined mode (aggregate, state-pass and chunk kernels);
+    # 36, 37: 12 and 6 chunks (one kernel per pass, sums over the other chunks)
     (1, 1024, 3, 64, 16, 32, BF16, "cfg", True, True, 26),
     (2, 640, 2, 32, 32, 32, BF16, "cfg", False, True, 27),
     (1, 384, 3, 32, 16, 32, BF16, "cfg", True, True, 36),
