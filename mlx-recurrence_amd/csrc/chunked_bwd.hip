@@ -674,11 +674,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
 template <int DH, int NS, bool GLA>
 int launch(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
   if (p.mode == kPipe) {
-    hipLaunchKernelGGL((rr::chunked::agg_kernel<DH, NS, GLA>), rr::chunked::chunk_grid(p), dim3(rr::chunked::kAggThreads), 0, s, p, 1);
-    if (int rc = rr::check_launch("chunked backward aggregates")) return rc;
-    hipLaunchKernelGGL((rr::chunked::pass_kernel<DH, NS, GLA>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0,
-                       s, p, 1);
-    if (int rc = rr::check_launch("chunked backward adjoint pass")) return rc;
+    if (int rc = rr::chunked::launch_scan<DH, NS, GLA>(p, B, s, true)) return rc;
     hipLaunchKernelGGL((col_bwd_kernel<DH, NS, kPipe, GLA>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
   } else if (p.mode == kDirect) {
     if constexpr (DH * NS <= rr::chunked::kDirectMaxState)

@@ -22,6 +22,8 @@
 // sign (and zero) are handled exactly.
 #pragma once
 
+#include <type_traits>
+
 #include "rr_common.h"
 #include "rr_internal.h"
 #include "rr_mfma.h"
@@ -60,14 +62,21 @@ __device__ __forceinline__ float prefix_prod32(float v, int /*lane*/) {
   v *= dpp_one<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
   return v;
 }
-// Inclusive suffix product over lanes (lane..31) within each half-wave.
+// The value of lane `src` (a constant), in every lane (v_readlane).
+__device__ __forceinline__ float lane_value(float v, int src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
+}
+// Inclusive suffix product over lanes (lane..31) within each half-wave:
+// row_shl shifts within each 16-lane row, then rows 0 and 2 take the totals
+// of rows 1 and 3 (their first lanes).  No LDS-unit permutes.
 __device__ __forceinline__ float suffix_prod32(float v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 32; o <<= 1) {
-    const float x = __shfl_down(v, o, 32);
-    if ((lane & 31) + o < 32) v *= x;
-  }
-  return v;
+  v *= dpp_one<0x101, 0xF>(v);   // row_shl:1
+  v *= dpp_one<0x102, 0xF>(v);   // row_shl:2
+  v *= dpp_one<0x104, 0xF>(v);   // row_shl:4
+  v *= dpp_one<0x108, 0xF>(v);   // row_shl:8
+  const float r1 = lane_value(v, 16), r3 = lane_value(v, 48);
+  const int row = lane >> 4;
+  return row == 0 ? v * r1 : row == 2 ? v * r3 : v;
 }
 
 // Step scalars of one chunk; lane s < 32 holds step s, whose raw step input
@@ -86,15 +95,18 @@ __device__ __forceinline__ StepScalars step_scalars(float x, float a, int lane) 
   StepScalars r;
   if constexpr (GLA) {
     r.gam = prefix_prod32(x, lane);
-    const float suf = suffix_prod32(x, lane);
-    const float nxt = __shfl_down(suf, 1, 32);
-    r.m31 = (lane & 31) < 31 ? nxt : 1.f;
+    // m31_s = g_{s+1} ... g_31: the suffix product of the inputs shifted by
+    // one lane (lane 15 of each half takes lane 16's input across the row)
+    float x1 = dpp_one<0x101, 0xF>(x);   // row_shl:1
+    const float x16 = lane_value(x, 16), x48 = lane_value(x, 48);
+    x1 = (lane & 31) == 15 ? (lane < 32 ? x16 : x48) : x1;
+    r.m31 = suffix_prod32(x1, lane);
     r.w = 1.f;
     r.cd = 0.f;
-    r.tot = __shfl(r.gam, 31);
+    r.tot = lane_value(r.gam, 31);
   } else {
     r.cd = prefix32(x, lane);
-    const float c31 = __shfl(r.cd, 31);
+    const float c31 = lane_value(r.cd, 31);
     r.gam = __expf(a * r.cd);
     r.m31 = __expf(a * (c31 - r.cd));
     r.w = x;
@@ -381,6 +393,216 @@ __global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
     }
     if (p.dh0 != nullptr) p.dh0[bh * DH * NS + es] = x;
   }
+}
+
+// ------------------------------------------------------------------ state scan
+// The state of the pipelined mode: one workgroup per (batch, head) walks the
+// chunks in order (the backward from the last chunk), carrying the state
+// (forward) or adjoint (backward) in registers and writing it once per chunk:
+//   forward:  h_k = tot_k h_{k-1} + U_k^T diag(m31 o w) B_k (h_{-1} = h0),
+//             into checkpoint slot k;
+//   backward: slot k of the workspace <- lam_k (lam_{nC-1} = dfinal),
+//             lam_{k-1} = tot_k lam_k + (gam o dY_k)^T C_k, dh0 = lam_{-1}.
+// A chunk's update is a rank-32 MFMA product on the running state.  All 256
+// threads load the chunk's inputs kScanPF chunks ahead and stage them in a
+// double-buffered LDS area in natural [step][column] layout (the fp32 factor
+// applied and split into bf16 hi + lo on the way: forward on B, backward on
+// dY); the operands are read back by transposing LDS reads (k = step); one
+// workgroup barrier per chunk.  Wave w owns the 16x16 state blocks w, w + 4,
+// ...  Its traffic is the inputs it reads and the states it writes, nothing
+// else (no per-chunk aggregates in HBM).
+constexpr int kScanPF = 4;
+template <int DH, int NS, bool BWD>
+struct ScanSmem {
+  static constexpr int PX = DH + 16, PY = NS == 16 ? 16 : NS + 16;   // see DirectSmem
+  uint16_t X[2][BWD ? 2 : 1][Q][PX];   // fwd: U; bwd: (gam o dY) hi, lo   [step][d]
+  uint16_t Y[2][BWD ? 1 : 2][Q][PY];   // fwd: (m31 w o B) hi, lo; bwd: C   [step][n]
+};
+template <int DH, int NS, bool GLA, bool BWD>
+__global__ __launch_bounds__(256) void scan_kernel(ChunkArgs p) {
+  using S = ScanSmem<DH, NS, BWD>;
+  constexpr int NBN = NS / 16, NB = (DH / 16) * NBN, NBW = (NB + 3) / 4;
+  constexpr int XN = BWD ? Q * DH / 4 : Q * DH / 8;   // X pieces per chunk (float4 of dY / u16x8 of U)
+  constexpr int YN = Q * NS / 8;                      // Y pieces (u16x8 of B / C)
+  constexpr int XV = (XN + 255) / 256, YV = (YN + 255) / 256;
+  __shared__ __attribute__((aligned(16))) S sm;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l15 = lane & 15, l4 = lane >> 4;
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int64_t bh = (int64_t)b * p.H + h, rowH = p.H;
+  const float a = head_rate<GLA>(p, h);
+  const int nC = p.nC;
+  const float neutral = GLA ? 1.f : 0.f;
+
+  // the running state, this wave's blocks in the [d][n] accumulator layout
+  f32x4_t st[NBW];
+  {
+    const float* ext = BWD ? p.dfinal : p.h0;
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+      const int j = w + 4 * i, db = j / NBN, nb = j % NBN;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        st[i][r] = j < NB && ext != nullptr
+                       ? ext[bh * DH * NS + state_off<GLA, DH, NS>(16 * db + 4 * l4 + r, 16 * nb + l15)]
+                       : 0.f;
+    }
+  }
+  // chunk of walk position k (clamped: the surplus prefetches repeat the last)
+  auto chunk_at = [&](int k) {
+    k = min(k, nC - 1);
+    return BWD ? nC - 1 - k : k;
+  };
+  u16x8_t xu[kScanPF][BWD ? 1 : XV], yv[kScanPF][YV];
+  float4 xf[kScanPF][BWD ? XV : 1];
+  float xs[kScanPF];
+  auto load = [&](int slot, int k) {
+    const int64_t row0 = (int64_t)b * p.L + (int64_t)chunk_at(k) * Q;
+    xs[slot] = bf_val(p.delta[(row0 + (lane & (Q - 1))) * rowH + h]);   // lanes >= 32 masked at use
+#pragma unroll
+    for (int v = 0; v < XV; ++v) {
+      const int i = min(tid + 256 * v, XN - 1);   // in range (surplus threads repeat a piece)
+      if constexpr (BWD) {
+        const int t = i / (DH / 4), d0 = 4 * (i % (DH / 4));
+        xf[slot][v] = *reinterpret_cast<const float4*>(p.dy + ((row0 + t) * rowH + h) * DH + d0);
+      } else {
+        const int t = i / (DH / 8), d0 = 8 * (i % (DH / 8));
+        xu[slot][v] = *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + t) * rowH + h) * DH + d0);
+      }
+    }
+    const uint16_t* ysrc = BWD ? p.Cm : p.Bm;
+#pragma unroll
+    for (int v = 0; v < YV; ++v) {
+      const int i = min(tid + 256 * v, YN - 1), t = i / (NS / 8), n0 = 8 * (i % (NS / 8));
+      yv[slot][v] = *reinterpret_cast<const u16x8_t*>(ysrc + ((row0 + t) * rowH + h) * NS + n0);
+    }
+  };
+#pragma unroll
+  for (int q = 0; q < kScanPF; ++q) load(q, q);
+
+  float* out = (BWD ? p.agg : p.ckpt) + bh * nC * DH * NS;
+  auto store_state = [&](float* dst) {
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+      const int j = w + 4 * i, db = j / NBN, nb = j % NBN;
+      if (NB % 4 == 0 || j < NB) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[(16 * db + 4 * l4 + r) * NS + 16 * nb + l15] = st[i][r];
+      }
+    }
+  };
+  // walk position k, prefetch slot q (a compile-time index)
+  auto step = [&](int k, auto qc) {
+    constexpr int q = decltype(qc)::value;
+    const int buf = k & 1;
+    const int c = chunk_at(k);
+    // step scalars (every wave; lanes s and s + 32 hold step s)
+    const StepScalars sc = step_scalars<GLA>(lane < Q ? xs[q] : neutral, a, lane);
+    const float cf = BWD ? sc.gam : sc.m31 * sc.w;
+    // stage the chunk (the factor applied on the way)
+#pragma unroll
+    for (int v = 0; v < XV; ++v) {
+      const int i = tid + 256 * v;
+      if constexpr (BWD) {
+        const int t = (i / (DH / 4)) & (Q - 1), d0 = 4 * (i % (DH / 4));
+        const float ct = __shfl(cf, t);   // every lane (the shuffle reads other lanes)
+        if (i < XN) {
+          const float4 g = xf[q][v];
+          u16x4_t hi, lo;
+          rr::bf_split4(f32x4_t{ct * g.x, ct * g.y, ct * g.z, ct * g.w}, hi, lo);
+          *reinterpret_cast<u16x4_t*>(&sm.X[buf][0][t][d0]) = hi;
+          *reinterpret_cast<u16x4_t*>(&sm.X[buf][BWD ? 1 : 0][t][d0]) = lo;
+        }
+      } else {
+        const int t = i / (DH / 8), d0 = 8 * (i % (DH / 8));
+        if (i < XN) *reinterpret_cast<u16x8_t*>(&sm.X[buf][0][t][d0]) = xu[q][v];
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < YV; ++v) {
+      const int i = tid + 256 * v, t = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+      if constexpr (BWD) {
+        if (i < YN) *reinterpret_cast<u16x8_t*>(&sm.Y[buf][0][t][n0]) = yv[q][v];
+      } else {
+        const float ct = __shfl(cf, t);
+        if (i < YN) {
+          float yw[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) yw[e] = ct * bf_val(yv[q][v][e]);
+          u16x8_t hi, lo;
+          rr::bf_split8(yw, hi, lo);
+          *reinterpret_cast<u16x8_t*>(&sm.Y[buf][0][t][n0]) = hi;
+          *reinterpret_cast<u16x8_t*>(&sm.Y[buf][BWD ? 0 : 1][t][n0]) = lo;
+        }
+      }
+    }
+    // this slot's registers are free: the loads of walk position k + kScanPF
+    load(q, k + kScanPF);
+    if constexpr (BWD) store_state(out + (int64_t)c * DH * NS);   // lam_c, the adjoint leaving chunk c
+    __syncthreads();
+    // state = tot_c state + X^T Y
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+      const int j = w + 4 * i, db = j / NBN, nb = j % NBN;
+      if (NB % 4 == 0 || j < NB) {
+        f32x4_t acc = st[i] * sc.tot;
+        if constexpr (BWD) {
+          const u16x8_t yr = frag_tr(&sm.Y[buf][0][0][16 * nb], S::PY, lane);
+          acc = mfma16(frag_tr(&sm.X[buf][0][0][16 * db], S::PX, lane), yr, acc);
+          acc = mfma16(frag_tr(&sm.X[buf][BWD ? 1 : 0][0][16 * db], S::PX, lane), yr, acc);
+        } else {
+          const u16x8_t xa = frag_tr(&sm.X[buf][0][0][16 * db], S::PX, lane);
+          acc = mfma16(xa, frag_tr(&sm.Y[buf][0][0][16 * nb], S::PY, lane), acc);
+          acc = mfma16(xa, frag_tr(&sm.Y[buf][BWD ? 0 : 1][0][16 * nb], S::PY, lane), acc);
+        }
+        st[i] = acc;
+      }
+    }
+    if constexpr (!BWD) store_state(out + (int64_t)c * DH * NS);   // h_c, the state leaving chunk c
+  };
+  // groups of kScanPF chunks with no exit inside (the waits for a slot's
+  // loads then stay exact), then the remainder
+  static_assert(kScanPF == 4, "the walk below is unrolled by four");
+  const int nMain = nC - nC % kScanPF;
+  for (int k0 = 0; k0 < nMain; k0 += kScanPF) {
+    step(k0 + 0, std::integral_constant<int, 0>{});
+    step(k0 + 1, std::integral_constant<int, 1>{});
+    step(k0 + 2, std::integral_constant<int, 2>{});
+    step(k0 + 3, std::integral_constant<int, 3>{});
+  }
+  if (nMain + 0 < nC) step(nMain + 0, std::integral_constant<int, 0>{});
+  if (nMain + 1 < nC) step(nMain + 1, std::integral_constant<int, 1>{});
+  if (nMain + 2 < nC) step(nMain + 2, std::integral_constant<int, 2>{});
+  if (BWD && p.dh0 != nullptr) {
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+      const int j = w + 4 * i, db = j / NBN, nb = j % NBN;
+      if (j < NB) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          p.dh0[bh * DH * NS + state_off<GLA, DH, NS>(16 * db + 4 * l4 + r, 16 * nb + l15)] = st[i][r];
+      }
+    }
+  }
+}
+
+// The states of the pipelined mode: with enough heads to fill the GPU, the
+// per-head scan (HBM traffic: inputs and states only); with few heads, whose
+// serial walks would leave most CUs idle (measured at B3 H12 nC16: 14.7 µs
+// against 9.5 µs), the aggregate kernel and the per-element state pass.
+constexpr int64_t kScanMinHeads = 320;
+template <int DH, int NS, bool GLA>
+int launch_scan(const ChunkArgs& p, int64_t B, hipStream_t s, bool bwd) {
+  const int kind = bwd ? 1 : 0;
+  if (B * p.H < kScanMinHeads) {
+    hipLaunchKernelGGL((agg_kernel<DH, NS, GLA>), chunk_grid(p), dim3(kAggThreads), 0, s, p, kind);
+    if (int rc = check_launch(bwd ? "chunked backward aggregates" : "chunked forward aggregates")) return rc;
+    hipLaunchKernelGGL((pass_kernel<DH, NS, GLA>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0, s, p, kind);
+    return check_launch(bwd ? "chunked backward adjoint pass" : "chunked forward state pass");
+  }
+  if (bwd) hipLaunchKernelGGL((scan_kernel<DH, NS, GLA, true>), dim3(p.H, (unsigned)B), dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((scan_kernel<DH, NS, GLA, false>), dim3(p.H, (unsigned)B), dim3(256), 0, s, p);
+  return check_launch(bwd ? "chunked backward adjoint scan" : "chunked forward state scan");
 }
 
 // ------------------------------------------------------------------ direct mode
@@ -939,10 +1161,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
 template <int DH, int NS, bool GLA>
 int launch_fwd(const ChunkArgs& p, int64_t B, hipStream_t s) {
   if (p.mode == kPipe) {   // R == 1
-    hipLaunchKernelGGL((agg_kernel<DH, NS, GLA>), chunk_grid(p), dim3(kAggThreads), 0, s, p, 0);
-    if (int rc = check_launch("chunked forward aggregates")) return rc;
-    hipLaunchKernelGGL((pass_kernel<DH, NS, GLA>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0, s, p, 0);
-    if (int rc = check_launch("chunked forward state pass")) return rc;
+    if (int rc = launch_scan<DH, NS, GLA>(p, B, s, false)) return rc;
     hipLaunchKernelGGL((fwd_kernel<DH, NS, kPipe, GLA>), chunk_grid(p), dim3(256), 0, s, p);
   } else if (p.mode == kDirect || p.mode == kSum) {   // R == 1; kSum forward = direct
     if constexpr (DH * NS <= kDirectMaxState)

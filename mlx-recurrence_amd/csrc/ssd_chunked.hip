@@ -794,11 +794,7 @@ int launch_dA(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
 template <int DH, int NS>
 int launch_bwd(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
   if (p.mode == kPipe) {   // R == 1
-    hipLaunchKernelGGL((rr::chunked::agg_kernel<DH, NS, false>), rr::chunked::chunk_grid(p), dim3(rr::chunked::kAggThreads), 0, s, p, 1);
-    if (int rc = rr::check_launch("ssd chunked backward aggregates")) return rc;
-    hipLaunchKernelGGL((rr::chunked::pass_kernel<DH, NS, false>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0, s,
-                       p, 1);
-    if (int rc = rr::check_launch("ssd chunked backward adjoint pass")) return rc;
+    if (int rc = rr::chunked::launch_scan<DH, NS, false>(p, B, s, true)) return rc;
     hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, kPipe>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
   } else if (p.mode == kSum || p.mode == kDirect) {   // R == 1; adjoint summed in the kernel
     hipLaunchKernelGGL((ssd2_bwd_kernel<DH, NS, kSum>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);

@@ -216,6 +216,9 @@ SSD_CASES = [
     (1, 192, 3, 64, 128, 32, BF16, "cfg", False, True, 33),  # pipelined
     (1, 64, 512, 32, 64, 32, BF16, "cfg", True, True, 34),   # whole head
     (2, 96, 256, 64, 128, 32, BF16, "cfg", True, True, 35),  # whole head, config 4's tile
+    # pipelined with B*H >= 320: the per-head state / adjoint scan kernel
+    (1, 640, 320, 32, 16, 32, BF16, "cfg", True, True, 38),
+    (2, 320, 160, 32, 64, 32, BF16, "cfg", True, True, 39),
 ]
 
 
@@ -290,6 +293,7 @@ GLA_CASES = [
     (1, 128, 2, 32, 32, BF16, "zeros", True, True, 25),
     (1, 640, 3, 64, 32, BF16, "cfg", True, True, 28),      # pipelined mode
     (2, 1024, 2, 32, 32, BF16, "signed", True, True, 29),
+    (2, 192, 160, 32, 32, BF16, "signed", True, True, 30),  # pipelined, B*H >= 320: head scan
 ]
 
 
