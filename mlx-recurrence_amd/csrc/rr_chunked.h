@@ -491,15 +491,15 @@ __global__ __launch_bounds__(256) void scan_kernel(ChunkArgs p) {
       }
     }
   };
-  // walk position k, prefetch slot q (a compile-time index)
-  auto step = [&](int k, auto qc) {
+  // Stage walk position k from prefetch slot q (a compile-time index) into
+  // LDS buffer k & 1, the factor applied on the way, then refill slot q with
+  // position k + kScanPF; returns tot_k.
+  auto stage = [&](int k, auto qc) {
     constexpr int q = decltype(qc)::value;
     const int buf = k & 1;
-    const int c = chunk_at(k);
     // step scalars (every wave; lanes s and s + 32 hold step s)
     const StepScalars sc = step_scalars<GLA>(lane < Q ? xs[q] : neutral, a, lane);
     const float cf = BWD ? sc.gam : sc.m31 * sc.w;
-    // stage the chunk (the factor applied on the way)
 #pragma unroll
     for (int v = 0; v < XV; ++v) {
       const int i = tid + 256 * v;
@@ -536,16 +536,19 @@ __global__ __launch_bounds__(256) void scan_kernel(ChunkArgs p) {
         }
       }
     }
-    // this slot's registers are free: the loads of walk position k + kScanPF
-    load(q, k + kScanPF);
+    load(q, k + kScanPF);   // this slot's registers are free
+    return sc.tot;
+  };
+  // The update of walk position k from LDS buffer k & 1: state = tot_k state + X^T Y.
+  auto update = [&](int k, float tot) {
+    const int buf = k & 1;
+    const int c = chunk_at(k);
     if constexpr (BWD) store_state(out + (int64_t)c * DH * NS);   // lam_c, the adjoint leaving chunk c
-    __syncthreads();
-    // state = tot_c state + X^T Y
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
       const int j = w + 4 * i, db = j / NBN, nb = j % NBN;
       if (NB % 4 == 0 || j < NB) {
-        f32x4_t acc = st[i] * sc.tot;
+        f32x4_t acc = st[i] * tot;
         if constexpr (BWD) {
           const u16x8_t yr = frag_tr(&sm.Y[buf][0][0][16 * nb], S::PY, lane);
           acc = mfma16(frag_tr(&sm.X[buf][0][0][16 * db], S::PX, lane), yr, acc);
@@ -560,19 +563,55 @@ __global__ __launch_bounds__(256) void scan_kernel(ChunkArgs p) {
     }
     if constexpr (!BWD) store_state(out + (int64_t)c * DH * NS);   // h_c, the state leaving chunk c
   };
-  // groups of kScanPF chunks with no exit inside (the waits for a slot's
-  // loads then stay exact), then the remainder
+  // Software pipeline: position k + 1 is staged (into the other LDS buffer)
+  // while position k's update runs, one barrier per position.  In groups of
+  // kScanPF positions with no exit inside (the waits for a slot's loads then
+  // stay exact), then the remainder; staging past the last position repeats
+  // the last chunk into a buffer nobody reads.
   static_assert(kScanPF == 4, "the walk below is unrolled by four");
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  float tot_next = stage(0, I0{});
+  __syncthreads();
   const int nMain = nC - nC % kScanPF;
   for (int k0 = 0; k0 < nMain; k0 += kScanPF) {
-    step(k0 + 0, std::integral_constant<int, 0>{});
-    step(k0 + 1, std::integral_constant<int, 1>{});
-    step(k0 + 2, std::integral_constant<int, 2>{});
-    step(k0 + 3, std::integral_constant<int, 3>{});
+    float tot = tot_next;
+    tot_next = stage(k0 + 1, I1{});
+    update(k0 + 0, tot);
+    __syncthreads();
+    tot = tot_next;
+    tot_next = stage(k0 + 2, I2{});
+    update(k0 + 1, tot);
+    __syncthreads();
+    tot = tot_next;
+    tot_next = stage(k0 + 3, I3{});
+    update(k0 + 2, tot);
+    __syncthreads();
+    tot = tot_next;
+    tot_next = stage(k0 + 4, I0{});
+    update(k0 + 3, tot);
+    __syncthreads();
   }
-  if (nMain + 0 < nC) step(nMain + 0, std::integral_constant<int, 0>{});
-  if (nMain + 1 < nC) step(nMain + 1, std::integral_constant<int, 1>{});
-  if (nMain + 2 < nC) step(nMain + 2, std::integral_constant<int, 2>{});
+  if (nMain + 0 < nC) {
+    const float tot = tot_next;
+    tot_next = stage(nMain + 1, I1{});
+    update(nMain + 0, tot);
+    __syncthreads();
+  }
+  if (nMain + 1 < nC) {
+    const float tot = tot_next;
+    tot_next = stage(nMain + 2, I2{});
+    update(nMain + 1, tot);
+    __syncthreads();
+  }
+  if (nMain + 2 < nC) {
+    const float tot = tot_next;
+    tot_next = stage(nMain + 3, I3{});
+    update(nMain + 2, tot);
+    __syncthreads();
+  }
   if (BWD && p.dh0 != nullptr) {
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
