@@ -38,6 +38,8 @@
 // Modes as in the forward: kWhole (a head per workgroup, lam carried in
 // registers from chunk to chunk), kPipe (lam from pass_kernel), kDirect (lam
 // from the direct sum; the workgroup of chunk 0 also forms dh0).
+#include <utility>
+
 #include "rr_chunked.h"
 
 namespace {
@@ -61,9 +63,10 @@ using rr::chunked::Q;
 using rr::chunked::r32row;
 
 // LDS of the backward kernel.  The operands that die after phase B1 (x) share
-// space with the masked products written in phase B2 (y).  In the pipelined
-// mode (REG) the du operands dY^T and lam come from global memory as register
-// fragments, so GYT and LM shrink to a row.
+// space with the masked products written in phase B2 (y).  In the one-chunk
+// modes (REG: kPipe, kDirect) the du operands dY^T and lam are register
+// fragments (dY^T from global memory; lam from the pass's output, or from the
+// direct sum's LDS before the chunk reuses it), so GYT and LM shrink to a row.
 template <int DH, int NS, bool GLA, bool REG>
 struct alignas(16) ColBwdSmem {
   static constexpr int PD = DH + 8, PN = NS + 8, TD = REG ? 1 : DH;
@@ -97,24 +100,26 @@ struct alignas(16) ColBwdSmem {
 
 template <int DH, int NS, int MODE, bool GLA>
 union ColBwdShared {
-  ColBwdSmem<DH, NS, GLA, MODE == kPipe> m;
+  ColBwdSmem<DH, NS, GLA, MODE != kWhole> m;
 };
 template <int DH, int NS, bool GLA>
 union ColBwdShared<DH, NS, kDirect, GLA> {
-  ColBwdSmem<DH, NS, GLA, false> m;
+  ColBwdSmem<DH, NS, GLA, true> m;
   rr::chunked::DirectSmem<DH, NS, true> d;
 };
 
-// Workgroups per CU the LDS allows (the register budget follows).
+// Workgroups per CU the LDS allows (the register budget follows); SSD's
+// direct mode (short sequences, few workgroups) keeps the registers of two.
 template <int DH, int NS, int MODE, bool GLA>
-constexpr int kColBwdWgs = (int)(160 * 1024 / sizeof(ColBwdShared<DH, NS, MODE, GLA>)) >= 3   ? 3
-                           : (int)(160 * 1024 / sizeof(ColBwdShared<DH, NS, MODE, GLA>)) >= 2 ? 2
-                                                                                                : 1;
+constexpr int kColBwdWgs = (int)(160 * 1024 / sizeof(ColBwdShared<DH, NS, MODE, GLA>)) >= 3 && (GLA || MODE != kDirect) ? 3
+                           : (int)(160 * 1024 / sizeof(ColBwdShared<DH, NS, MODE, GLA>)) >= 2                          ? 2
+                                                                                                                      : 1;
 
 template <int DH, int NS, int MODE, bool GLA>
 __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_kernel(rr::ChunkArgs p) {
   constexpr int NBN = NS / 16, NBD = DH / 16;
   constexpr int CPW = (NBN + 3) / 4;   // column blocks per wave
+  constexpr bool REG = MODE != kWhole;   // du operands as register fragments
   __shared__ ColBwdShared<DH, NS, MODE, GLA> smu;
   auto& m = smu.m;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -131,25 +136,63 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
   const int64_t bh = (int64_t)b * p.H + h;
   const int rsD = p.H * DH, rsN = p.H * NS;   // step strides (elements) of [.., H, DH] / [.., H, NS]
   const int l15 = lane & 15, l4 = lane >> 4;
+  const int mydb = ((w - NBN) % 4 + 4) % 4;   // the row block of du this wave forms
 
   f32x4_t lam[CPW][NBD];
+  float plm[REG ? NS / 32 : 1][8];   // du operand: lam[16 mydb + l15][32 kk + 8 l4 + e]
 #pragma unroll
   for (int cc = 0; cc < CPW; ++cc)
 #pragma unroll
     for (int db = 0; db < NBD; ++db) lam[cc][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   if constexpr (MODE == kDirect) {
-    const float gam_all = rr::chunked::direct_sum<DH, NS, GLA, true>(p, cbeg, b, h, a, smu.d);
+    // the adjoint leaving the chunk; chunk 0's workgroup also stores dh0
+    const float gam_all = rr::chunked::direct_sum<DH, NS, GLA, true, true>(p, cbeg, b, h, a, smu.d, p.dh0);
     const float* dfb = p.dfinal != nullptr ? p.dfinal + bh * DH * NS : nullptr;
+    // lam of this wave's columns, and its du operand (rows of block mydb)
+    auto lam_at = [&](int cc, int db, int r) { return std::make_pair(16 * db + 4 * l4 + r, 16 * (w + 4 * cc) + l15); };
+    auto plm_at = [&](int kk, int e) { return std::make_pair(16 * mydb + l15, 32 * kk + 8 * l4 + e); };
 #pragma unroll
     for (int cc = 0; cc < CPW; ++cc) {
-      const int nb = w + 4 * cc;
-      if (nb < NBN) {
+      if (w + 4 * cc < NBN) {
 #pragma unroll
         for (int db = 0; db < NBD; ++db)
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            lam[cc][db][r] = rr::chunked::direct_value<DH, NS, GLA, true>(smu.d, gam_all, dfb, 16 * db + 4 * l4 + r,
-                                                                         16 * nb + l15);
+          for (int r = 0; r < 4; ++r) {
+            const auto [d, n] = lam_at(cc, db, r);
+            lam[cc][db][r] = rr::chunked::direct_partial(smu.d, d, n);
+          }
+      }
+    }
+    if (mydb < NBD) {
+#pragma unroll
+      for (int kk = 0; kk < NS / 32; ++kk)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const auto [d, n] = plm_at(kk, e);
+          plm[kk][e] = rr::chunked::direct_partial(smu.d, d, n);
+        }
+    }
+    if (dfb != nullptr) {
+#pragma unroll
+      for (int cc = 0; cc < CPW; ++cc) {
+        if (w + 4 * cc < NBN) {
+#pragma unroll
+          for (int db = 0; db < NBD; ++db)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const auto [d, n] = lam_at(cc, db, r);
+              lam[cc][db][r] += rr::chunked::direct_ext<DH, NS, GLA>(gam_all, dfb, d, n);
+            }
+        }
+      }
+      if (mydb < NBD) {
+#pragma unroll
+        for (int kk = 0; kk < NS / 32; ++kk)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const auto [d, n] = plm_at(kk, e);
+            plm[kk][e] += rr::chunked::direct_ext<DH, NS, GLA>(gam_all, dfb, d, n);
+          }
       }
     }
     __syncthreads();   // the chunk below reuses the LDS of the sum
@@ -170,7 +213,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
     }
   }
   // the adjoint handed to chunk c - 1 is needed for the whole head, and for dh0
-  const bool carry = MODE == kWhole || (MODE == kDirect && cbeg == 0 && p.dh0 != nullptr);
+  constexpr bool carry = MODE == kWhole;
   float dA_acc[CPW];   // SSD: dA of this lane's column (every l4 group holds the same sum)
 #pragma unroll
   for (int cc = 0; cc < CPW; ++cc) dA_acc[cc] = 0.f;
@@ -258,7 +301,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
             bf_split(g4[e], hi, lo);
             hi4[e] = hi;
             lo4[e] = lo;
-            if constexpr (MODE != kPipe) {
+            if constexpr (!REG) {
               m.GYT_hi[d0 + e][tl] = hi;
               m.GYT_lo[d0 + e][tl] = lo;
             }
@@ -291,7 +334,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int d = 16 * db + 4 * l4 + r, n = 16 * nb + l15;
-              if constexpr (MODE != kPipe) {
+              if constexpr (!REG) {
                 m.LM_hi[d][n] = hi4[r];
                 m.LM_lo[d][n] = lo4[r];
               }
@@ -373,15 +416,19 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
     }
     __syncthreads();
     // ------------------------------------------------ B2: masked products; GLA dg / SSD T
-    // pipelined mode: this wave's du operands (row block mydb), used in phase C;
-    // the loads land while B2 runs
-    const int mydb = ((w - NBN) % 4 + 4) % 4;
-    float pdy[MODE == kPipe ? 8 : 1], plm[MODE == kPipe ? NS / 32 : 1][8];
-    if constexpr (MODE == kPipe) {
+    // one-chunk modes: this wave's du operands (row block mydb), used in
+    // phase C; the loads land while B2 runs
+    float pdy[REG ? 8 : 1];
+    if constexpr (REG) {
       if (mydb < NBD) {
         const int d = 16 * mydb + l15;
 #pragma unroll
         for (int e = 0; e < 8; ++e) pdy[e] = p.dy[baseD + (8 * l4 + e) * rsD + d];
+      }
+    }
+    if constexpr (MODE == kPipe) {
+      if (mydb < NBD) {
+        const int d = 16 * mydb + l15;
         const float* lsrc = p.agg + ((bh * p.nC + c) * DH + d) * NS + 8 * l4;
 #pragma unroll
         for (int kk = 0; kk < NS / 32; ++kk) {
@@ -517,7 +564,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
     if (mydb < NBD) {
       const int db = mydb;
       u16x8_t gh8, gl8;   // dY^T fragment [t' = 8 l4 + e][d]
-      if constexpr (MODE == kPipe) {
+      if constexpr (REG) {
         rr::bf_split8(pdy, gh8, gl8);
       } else {
         gh8 = frag(&m.GYT_hi[16 * db + l15][8 * l4]);
@@ -526,7 +573,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
       u16x8_t lh8[NS / 32], ll8[NS / 32];   // lam fragments [n = 32 kk + 8 l4 + e][d]
 #pragma unroll
       for (int kk = 0; kk < NS / 32; ++kk) {
-        if constexpr (MODE == kPipe) {
+        if constexpr (REG) {
           rr::bf_split8(plm[kk], lh8[kk], ll8[kk]);
         } else {
           lh8[kk] = frag(&m.LM_hi[16 * db + l15][32 * kk + 8 * l4]);
@@ -568,10 +615,10 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
         const int row = 16 * tb + l15, k0 = 8 * l4;
         f32x4_t ak = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f}, akb = {0.f, 0.f, 0.f, 0.f};
         // B and C as B operands over s / t' (transposing reads of Kn / Qn)
-        const u16x8_t fq = rr::frag_tr(&m.Qn[0][16 * nb], ColBwdSmem<DH, NS, GLA, MODE == kPipe>::PN, lane);
+        const u16x8_t fq = rr::frag_tr(&m.Qn[0][16 * nb], ColBwdSmem<DH, NS, GLA, REG>::PN, lane);
         ak = mfma16(frag(&m.y.MGT_hi[row][k0]), fq, ak);
         ak = mfma16(frag(&m.y.MGT_lo[row][k0]), fq, ak);
-        const u16x8_t fk = rr::frag_tr(&m.Kn[0][16 * nb], ColBwdSmem<DH, NS, GLA, MODE == kPipe>::PN, lane);
+        const u16x8_t fk = rr::frag_tr(&m.Kn[0][16 * nb], ColBwdSmem<DH, NS, GLA, REG>::PN, lane);
         aq = mfma16(frag(&m.y.MG_hi[row][k0]), fk, aq);
         aq = mfma16(frag(&m.y.MG_lo[row][k0]), fk, aq);
         if constexpr (!GLA) {
@@ -609,14 +656,14 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
         }
       }
     }
-    if (carry) {
+    if constexpr (carry) {
       // lam_prev = (gam o dY)^T C + gam_31 lam, blocks of this wave's columns
 #pragma unroll
       for (int cc = 0; cc < CPW; ++cc) {
         const int nb = w + 4 * cc;
         if (nb >= NBN) continue;
         const int k0 = 8 * l4;
-        const u16x8_t qf = rr::frag_tr(&m.Qn[0][16 * nb], ColBwdSmem<DH, NS, GLA, MODE == kPipe>::PN, lane);
+        const u16x8_t qf = rr::frag_tr(&m.Qn[0][16 * nb], ColBwdSmem<DH, NS, GLA, REG>::PN, lane);
         u16x8_t qh, ql;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -656,7 +703,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
       if (nb < NBN && l4 == 0) p.ws[(bh * nR + run) * NS + 16 * nb + l15] = dA_acc[cc];
     }
   }
-  if (carry && p.dh0 != nullptr) {
+  if (carry && p.dh0 != nullptr) {   // kWhole (kDirect stores dh0 in the direct sum)
 #pragma unroll
     for (int cc = 0; cc < CPW; ++cc) {
       const int nb = w + 4 * cc;

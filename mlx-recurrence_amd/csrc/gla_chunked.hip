@@ -28,16 +28,22 @@ bool gla2_supported(int dtype, int64_t B, int64_t L, int64_t H, int64_t seg, int
   return Dh == 32 || Dh == 64;
 }
 
-// The direct mode for the shortest heads only (a Dh x Dh state makes each
-// workgroup's sum over the other chunks costly).
+// The direct mode (one kernel per pass, each chunk's workgroup summing over
+// the other chunks' inputs) for short heads: up to 4 chunks always; up to 16
+// while every workgroup can be resident at once (three per CU on 256 CUs; a
+// second round of workgroups costs more than the aggregate and state-pass
+// kernels it saves).
 constexpr int64_t kGlaDirectMaxChunks = 4;
+constexpr int64_t kGlaDirectMaxWorkgroups = 3 * 256;
 
-int gla2_mode(int64_t nC, int64_t Dh) {
-  return nC <= kGlaDirectMaxChunks && Dh * Dh <= chunked::kDirectMaxState ? chunked::kDirect : chunked::kPipe;
+int gla2_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh) {
+  if (Dh * Dh > chunked::kDirectMaxState) return chunked::kPipe;
+  if (nC <= kGlaDirectMaxChunks) return chunked::kDirect;
+  return nC <= chunked::kDirectMaxChunks && B * H * nC <= kGlaDirectMaxWorkgroups ? chunked::kDirect : chunked::kPipe;
 }
 
 size_t gla2_ws_bytes(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass) {
-  if (gla2_mode(nC, Dh) == chunked::kDirect) return 0;
+  if (gla2_mode(B, H, nC, Dh) == chunked::kDirect) return 0;
   int64_t f = align64(B * H * nC);
   if (pass == 1) f += align64(B * H * nC * Dh * Dh);
   return (size_t)f * sizeof(float);

@@ -670,16 +670,14 @@ constexpr int kDirectPerWave = kDirectMaxChunks / 4;
 
 template <int DH, int NS, bool BWD>
 struct alignas(16) DirectSmem {
-  // Row pitches (elements): 32 or 96 bytes past a multiple of 128, so the
-  // four 32-byte row pieces that 16 lanes of a transposing read take hit
-  // distinct banks; 16-column rows (32 bytes) tile the banks unpadded.
-  static constexpr int PX = DH + 16;
-  static constexpr int PY = NS == 16 ? 16 : NS + 16;
+  // a 64 x 64 state's staging areas packed, so that three workgroups fit a CU
+  using SX = Staged<DH, DH * NS >= 4096>;
+  using SY = Staged<NS, DH * NS >= 4096>;
   union {
-    struct {
-      uint16_t X[BWD ? 1 : Q][PX];      // fwd: U [s][d] (the backward's dY stays in registers)
-      uint16_t Y[BWD ? 1 : 2][Q][PY];   // fwd: (F m31 w o B) hi, lo [s][n]; bwd: C [t][n]
-      float cw[BWD ? Q : 4];            // bwd: the chunk's step factors F gam_t
+    struct {   // every member 16-byte aligned (16-byte and transposing LDS accesses)
+      alignas(16) uint16_t X[BWD ? 8 : SX::SIZE];      // fwd: U [s][d] (the backward's dY stays in registers)
+      alignas(16) uint16_t Y[BWD ? 1 : 2][SY::SIZE];   // fwd: (F m31 w o B) hi, lo [s][n]; bwd: C [t][n]
+      alignas(16) float cw[BWD ? Q : 4];               // bwd: the chunk's step factors F gam_t
     } st[4];
     float red[2][DH * NS];              // partial sums of waves 0 + 2 and 1 + 3, [d][n]
   };
@@ -708,7 +706,9 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
   constexpr int XV = Q * DH / 8 / 64;                           // fwd, per lane and chunk: u16x8 of U
   constexpr int YV = Q * NS / 8 / 64;                           // u16x8 of B (fwd) or C (bwd)
   constexpr int VPC = BWD ? 8 * NBD + 4 * YV : 4 * (XV + YV);   // registers per chunk in flight
-  constexpr int REGS = BWD && NS > 16 ? 48 : 80;                // budget for them
+  // budget for them (GLA's 64 x 64 forward: one chunk, its accumulators
+  // taking 64 of the 168 registers that three workgroups per CU leave)
+  constexpr int REGS = GLA && !BWD && DH * NS >= 4096 ? VPC : BWD && NS > 16 ? 48 : 80;
   constexpr int PF = REGS / VPC >= 4 ? 4 : REGS / VPC >= 2 ? 2 : 1;   // chunks in flight per wave
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t rowH = p.H;
@@ -815,7 +815,7 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
 #pragma unroll
       for (int v = 0; v < YV; ++v) {
         const int i = lane + 64 * v, t = i / (NS / 8), n0 = 8 * (i % (NS / 8));
-        *reinterpret_cast<u16x8_t*>(&st.Y[0][t][n0]) = yv[slot][v];
+        *reinterpret_cast<u16x8_t*>(&st.Y[0][S::SY::off(t, n0)]) = yv[slot][v];
       }
       wave_lds_sync();
       // this lane's step factors (steps 8 g .. 8 g + 7; broadcast reads)
@@ -824,7 +824,7 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
       const float cwl[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
       u16x8_t yf[NBN];
 #pragma unroll
-      for (int nb = 0; nb < NBN; ++nb) yf[nb] = frag_tr(&st.Y[0][0][16 * nb], S::PY, lane);
+      for (int nb = 0; nb < NBN; ++nb) yf[nb] = frag_tr_st<typename S::SY>(st.Y[0], 16 * nb, lane);
 #pragma unroll
       for (int db = 0; db < NBD; ++db) {
         float xw[8];
@@ -847,7 +847,7 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
 #pragma unroll
       for (int v = 0; v < XV; ++v) {
         const int i = lane + 64 * v, t = i / (DH / 8), d0 = 8 * (i % (DH / 8));
-        *reinterpret_cast<u16x8_t*>(&st.X[t][d0]) = xu[slot][v];
+        *reinterpret_cast<u16x8_t*>(&st.X[S::SX::off(t, d0)]) = xu[slot][v];
       }
 #pragma unroll
       for (int v = 0; v < YV; ++v) {
@@ -858,8 +858,8 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
         for (int e = 0; e < 8; ++e) yw[e] = ct * bf_val(yv[slot][v][e]);
         u16x8_t hi, lo;
         rr::bf_split8(yw, hi, lo);
-        *reinterpret_cast<u16x8_t*>(&st.Y[0][t][n0]) = hi;
-        *reinterpret_cast<u16x8_t*>(&st.Y[BWD ? 0 : 1][t][n0]) = lo;
+        *reinterpret_cast<u16x8_t*>(&st.Y[0][S::SY::off(t, n0)]) = hi;
+        *reinterpret_cast<u16x8_t*>(&st.Y[BWD ? 0 : 1][S::SY::off(t, n0)]) = lo;
       }
       // the registers of this slot are free: the loads of chunk k + PF (see above)
       if (k + PF < kDirectPerWave) load(slot, chunk(k + PF));
@@ -868,10 +868,10 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
 #pragma unroll
       for (int nb = 0; nb < NBN; ++nb)
 #pragma unroll
-        for (int hl = 0; hl < 2; ++hl) yf[hl][nb] = frag_tr(&st.Y[hl][0][16 * nb], S::PY, lane);
+        for (int hl = 0; hl < 2; ++hl) yf[hl][nb] = frag_tr_st<typename S::SY>(st.Y[hl], 16 * nb, lane);
 #pragma unroll
       for (int db = 0; db < NBD; ++db) {
-        const u16x8_t xfr = frag_tr(&st.X[0][16 * db], S::PX, lane);
+        const u16x8_t xfr = frag_tr_st<typename S::SX>(st.X, 16 * db, lane);
 #pragma unroll
         for (int nb = 0; nb < NBN; ++nb) {
           acc[db][nb] = mfma16(xfr, yf[0][nb], acc[db][nb]);
@@ -922,36 +922,50 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
   }
   __syncthreads();
   if constexpr (G0) {
-    if (g0 && w == 0) {
-      // dh0 = tot_0 lam(0) + G_0, lam(0) = red0 + red1 + Gam dfinal
+    if (g0) {
+      // dh0 = tot_0 lam(0) + G_0, lam(0) = red0 + red1 + Gam dfinal; every
+      // thread takes elements e = tid + 256 k (the LDS reads first, the
+      // dfinal terms in one branch)
+      constexpr int PER = DH * NS / 256;
       const float t0 = s.tot[0];
       const float* ext = p.dfinal != nullptr ? p.dfinal + ((int64_t)b * p.H + h) * DH * NS : nullptr;
       float* out = dh0 + ((int64_t)b * p.H + h) * DH * NS;
+      float lam[PER];
 #pragma unroll
-      for (int db = 0; db < NBD; ++db)
+      for (int k = 0; k < PER; ++k) {
+        const int e = tid + 256 * k;
+        lam[k] = s.red[0][e] + s.red[1][e];
+      }
+      if (ext != nullptr) {
 #pragma unroll
-        for (int nb = 0; nb < NBN; ++nb)
+        for (int k = 0; k < PER; ++k) {
+          const int e = tid + 256 * k;
+          lam[k] += gam_all * ext[state_off<GLA, DH, NS>(e / NS, e % NS)];
+        }
+      }
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int e = at(db, nb, r), d = e / NS, n = e % NS;
-            float lam = s.red[0][e] + s.red[1][e];
-            if (ext != nullptr) lam += gam_all * ext[state_off<GLA, DH, NS>(d, n)];
-            out[state_off<GLA, DH, NS>(d, n)] = t0 * lam + s.g0[e];
-          }
+      for (int k = 0; k < PER; ++k) {
+        const int e = tid + 256 * k;
+        out[state_off<GLA, DH, NS>(e / NS, e % NS)] = t0 * lam[k] + s.g0[e];
+      }
     }
   }
   return gam_all;
 }
 
-// Element (d, n) of the direct sum: the two partials plus Gam times the
-// caller's h0 (forward) or dfinal (backward), read from red[] / `ext`.
-template <int DH, int NS, bool GLA, bool BWD>
-__device__ __forceinline__ float direct_value(const DirectSmem<DH, NS, BWD>& s, float gam_all, const float* ext,
-                                              int d, int n) {
+// Element (d, n) of the direct sum is direct_partial (the two partials in
+// red[]) plus, where the caller has an h0 (forward) or dfinal (backward),
+// direct_ext (Gam times that element).  Callers read all their partials
+// first and add the ext terms in one separate branch: a branch per element
+// would wait for each LDS read before the next is issued.
+template <int DH, int NS, bool BWD>
+__device__ __forceinline__ float direct_partial(const DirectSmem<DH, NS, BWD>& s, int d, int n) {
   const int e = d * NS + n;
-  float v = s.red[0][e] + s.red[1][e];
-  if (ext != nullptr) v += gam_all * ext[state_off<GLA, DH, NS>(d, n)];
-  return v;
+  return s.red[0][e] + s.red[1][e];
+}
+template <int DH, int NS, bool GLA>
+__device__ __forceinline__ float direct_ext(float gam_all, const float* ext, int d, int n) {
+  return gam_all * ext[state_off<GLA, DH, NS>(d, n)];
 }
 
 // ------------------------------------------------------------------ forward
@@ -993,8 +1007,14 @@ union FwdShared<DH, NS, true> {
 // rows with no cross-wave sum and no LDS copy of the state:
 //   Y[t, d] = (W U)[t, d] + gam_t (C h_in^T)[t, d],  W = M o C B^T o w_s
 //   h_end^T = gam_31 h_in^T + (m31 o w o B)^T U
+// GLA's direct mode: three workgroups per CU where the LDS allows it (a chunk
+// per workgroup, so every workgroup of a 16-chunk sequence at batch 3 can be
+// resident); the register budget follows.
 template <int DH, int NS, int MODE, bool GLA>
-__global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
+constexpr int kFwdWgs = GLA && MODE == kDirect && 160 * 1024 / sizeof(FwdShared<DH, NS, true>) >= 3 ? 3 : 1;
+
+template <int DH, int NS, int MODE, bool GLA>
+__global__ __launch_bounds__(256, (kFwdWgs<DH, NS, MODE, GLA>)) void fwd_kernel(ChunkArgs p) {
   using K = Cfg<DH, NS>;
   constexpr int NBD = DH / 16, NBN = NS / 16;
   constexpr int DBW = (NBD + 3) / 4;   // row blocks per wave
@@ -1054,8 +1074,20 @@ __global__ __launch_bounds__(256) void fwd_kernel(ChunkArgs p) {
 #pragma unroll
         for (int nb = 0; nb < NBN; ++nb)
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            hst[i][nb][r] = direct_value<DH, NS, GLA, false>(smu.d, gam_all, h0b, 16 * db + l15, 16 * nb + 4 * l4 + r);
+          for (int r = 0; r < 4; ++r) hst[i][nb][r] = direct_partial(smu.d, 16 * db + l15, 16 * nb + 4 * l4 + r);
+      }
+    }
+    if (h0b != nullptr) {
+#pragma unroll
+      for (int i = 0; i < DBW; ++i) {
+        const int db = w + 4 * i;
+        if (db < NBD) {
+#pragma unroll
+          for (int nb = 0; nb < NBN; ++nb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              hst[i][nb][r] += direct_ext<DH, NS, GLA>(gam_all, h0b, 16 * db + l15, 16 * nb + 4 * l4 + r);
+        }
       }
     }
     __syncthreads();   // the chunk below reuses the LDS of the sum

@@ -163,6 +163,31 @@ __device__ __forceinline__ u16x8_t frag_tr(const uint16_t* base, int pitch, int 
 // loads issued before it.
 __device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
 
+// A bf16 matrix X[step][col] (W columns) staged in LDS for transposing reads.
+// Rows are padded to 32 or 96 bytes past a multiple of 128, so the four rows
+// that 16 lanes of a transposing read take hit four distinct 32-byte bank
+// groups (16-column rows, 32 bytes, tile the banks unpadded).  With PACK, rows
+// of a multiple of 64 columns are stored unpadded instead, their 16-column
+// pieces permuted by row (piece p of row t at p ^ (t % 4)): 20 % less LDS, for
+// a few more address registers (the piece offsets differ per lane).
+template <int W, bool PACK = false>
+struct Staged {
+  static constexpr bool SWZ = PACK && W % 64 == 0;
+  static constexpr int P = SWZ ? W : W == 16 ? 16 : W + 16;   // row pitch (elements)
+  static constexpr int SIZE = 32 * P;                          // elements of 32 rows
+  // element offset of X[t][col]; an 8-aligned run of 8 columns stays contiguous
+  static __device__ __forceinline__ int off(int t, int col) { return t * P + (SWZ ? col ^ (16 * (t & 3)) : col); }
+};
+// frag_tr for a Staged matrix: columns col0 .. col0 + 15 (col0 % 16 == 0),
+// k-runs from row 0.
+template <typename S>
+__device__ __forceinline__ u16x8_t frag_tr_st(const uint16_t* x, int col0, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  const uint16_t* a = x + S::off(8 * g + (i >> 2), col0) + 4 * (i & 3);   // rows r and r + 4 share r % 4
+  const u16x4_t lo = tr_read4(a), hi = tr_read4(a + 4 * S::P);
+  return u16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
 // Make one wave's LDS writes visible to its own later LDS reads.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

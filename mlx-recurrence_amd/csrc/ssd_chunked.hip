@@ -283,8 +283,20 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
             const int db = j / NBN, nb = j % NBN;
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-              lam[jj][r] = rr::chunked::direct_value<DH, NS, false, true>(smu.d, gam_all, dfb, 16 * db + 4 * (lane >> 4) + r,
-                                                                          16 * nb + (lane & 15));
+              lam[jj][r] = rr::chunked::direct_partial(smu.d, 16 * db + 4 * (lane >> 4) + r, 16 * nb + (lane & 15));
+          }
+        }
+        if (dfb != nullptr) {
+#pragma unroll
+          for (int jj = 0; jj < K::NBW; ++jj) {
+            const int j = w + 4 * jj;
+            if (j < K::NB) {
+              const int db = j / NBN, nb = j % NBN;
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                lam[jj][r] += rr::chunked::direct_ext<DH, NS, false>(gam_all, dfb, 16 * db + 4 * (lane >> 4) + r,
+                                                                     16 * nb + (lane & 15));
+            }
           }
         }
         __syncthreads();   // the sum's LDS is dead: the staging below reuses it

@@ -710,7 +710,7 @@ rr::ChunkArgs gla2_args(const void* qp, const void* kp, const void* vp, const vo
   a.Cm = static_cast<const uint16_t*>(qp);
   a.h0 = h0;
   a.L = (int)L; a.H = (int)H; a.DH = (int)Dh; a.NS = (int)Dh; a.nC = (int)(L / 32);
-  a.mode = rr::gla2_mode(a.nC, Dh);
+  a.mode = rr::gla2_mode(B, H, a.nC, Dh);
   a.R = 1;
   return a;
 }

@@ -294,6 +294,10 @@ GLA_CASES = [
     (1, 640, 3, 64, 32, BF16, "cfg", True, True, 28),      # pipelined mode
     (2, 1024, 2, 32, 32, BF16, "signed", True, True, 29),
     (2, 192, 160, 32, 32, BF16, "signed", True, True, 30),  # pipelined, B*H >= 320: head scan
+    (1, 512, 3, 64, 32, BF16, "signed", True, True, 31),    # direct mode, 16 chunks
+    (2, 512, 4, 32, 32, BF16, "cfg", True, True, 32),       # direct mode, 16 chunks, Dh = 32
+    (1, 480, 2, 64, 32, BF16, "zeros", True, True, 33),     # direct mode, 15 chunks, zero gates
+    (5, 512, 12, 64, 32, BF16, "cfg", False, True, 34),     # 960 workgroups: pipelined
 ]
 
 
