@@ -1015,7 +1015,6 @@ constexpr int kFwdWgs = GLA && MODE == kDirect && 160 * 1024 / sizeof(FwdShared<
 
 template <int DH, int NS, int MODE, bool GLA>
 __global__ __launch_bounds__(256, (kFwdWgs<DH, NS, MODE, GLA>)) void fwd_kernel(ChunkArgs p) {
-  using K = Cfg<DH, NS>;
   constexpr int NBD = DH / 16, NBN = NS / 16;
   constexpr int DBW = (NBD + 3) / 4;   // row blocks per wave
   constexpr bool STATE = MODE == kWhole || MODE == kDirect;   // forms the chunk's end state

@@ -188,6 +188,15 @@ __device__ __forceinline__ u16x8_t frag_tr_st(const uint16_t* x, int col0, int l
   return u16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// A pointer into global memory as such: loads through it are global (not
+// flat) loads, which count only against vmcnt, so waits for LDS traffic
+// (lgkmcnt, e.g. at a barrier) do not also wait for them.  For pointers the
+// compiler cannot trace to a kernel argument (selected between several).
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* as_global(const T* p) {
+  return (const __attribute__((address_space(1))) T*)p;
+}
+
 // Make one wave's LDS writes visible to its own later LDS reads.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -130,7 +130,8 @@ struct BwdSmem {
   // (gam o C)^T, for the adjoint carried to the previous chunk (whole-head
   // mode; chunk 0 of the direct mode for the initial-state gradient)
   uint16_t CgT_hi[CARRY ? NS : 1][PQ], CgT_lo[CARRY ? NS : 1][PQ];
-  float del[Q], cd[Q], gam[Q], m31[Q], R[Q];
+  float del[Q], cd[Q], gam[Q], m31[Q];
+  float Rp[4][Q];                  // per-wave partials of R_t (phase B2)
   float Xs[NS / 16][Q], Ys[NS / 16][Q], BZs[NS / 16][Q];   // row sums over one 16-column block
   float Ts[2][Q];                  // suffix of gam X, prefix of m31 delta Y
   float t4[4][NS];
@@ -177,6 +178,8 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
   const int64_t rowH = p.H;
   const int64_t sbase = ((int64_t)b * p.H + h) * DH * NS;
   constexpr int NBN = K::NBN;
+  constexpr int NBD = DH / 16;   // du column blocks (phase C: one per wave w < NBD)
+  static_assert(NBD == 2 || NBD == 4, "the du blocks map onto the four waves");
 
   f32x4_t lam[K::NBW];
 #pragma unroll
@@ -210,63 +213,68 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
     f32x4_t hin[K::NBW];
     // pipelined mode: register operand fragments (see BwdSmem)
     constexpr int TPW = NBN;   // GH / UL tasks per task wave (waves 2 and 3 in phase B1)
-    float pdy[PIPE ? 2 : 1][8], plm[PIPE ? NS / 16 : 1][8];
+    float pdy[PIPE ? 8 : 1], plm[PIPE ? NS / 16 : 1][4];
     f32x4_t pcol[PIPE ? TPW : 1][PIPE ? DH / 16 : 1];
     {
       constexpr int UV = (Q * DH / 8 + 255) / 256, BV = (Q * NS / 8 + 255) / 256, GV = (Q * DH / 4 + 255) / 256;
       u16x8_t uv[UV], bv[BV], cv[BV];
       float4 gv[GV];
       float dv = 0.f;
+      // Every load below is issued by every thread, unconditionally and in
+      // bounds (clamped indices; surplus values are multiplied by 0, which
+      // the compiler cannot turn into a branch around the load): a load
+      // under a branch makes the branch's join wait for all of them.
       auto issue = [&]() {
 #pragma unroll
         for (int v = 0; v < UV; ++v) {
           const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
-          uv[v] = i < Q * DH / 8 ? *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0) : u16x8_t{};
+          uv[v] = *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0);
         }
 #pragma unroll
         for (int v = 0; v < BV; ++v) {
           const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
           const int64_t g = ((row0 + tl) * rowH + h) * NS + n0;
-          bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Bm + g) : u16x8_t{};
-          cv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Cm + g) : u16x8_t{};
+          bv[v] = *reinterpret_cast<const u16x8_t*>(p.Bm + g);
+          cv[v] = *reinterpret_cast<const u16x8_t*>(p.Cm + g);
         }
 #pragma unroll
         for (int v = 0; v < GV; ++v) {
           const int i = tid + 256 * v, tl = (i / (DH / 4)) & (Q - 1), d0 = 4 * (i % (DH / 4));
-          gv[v] = i < Q * DH / 4 ? *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0)
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+          gv[v] = *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0);
         }
-        // unconditional (in-bounds) load, so no branch waits on it
         dv = bf_val(p.delta[(row0 + (lane & (Q - 1))) * rowH + h]);   // lanes >= 32 masked at use
-        const float* hsrc = c > 0 ? p.ckpt + (((int64_t)b * p.H + h) * p.nC + (c - 1)) * DH * NS
-                                  : (p.h0 != nullptr ? p.h0 + sbase : nullptr);
+        // the entering state (checkpoint slot c - 1, or h0; none: zero, read
+        // from the checkpoint buffer and dropped)
+        const float has_h = c > 0 || p.h0 != nullptr ? 1.f : 0.f;   // the slot read is finite
+        const auto hsrc = rr::as_global(c > 0 ? p.ckpt + (((int64_t)b * p.H + h) * p.nC + (c - 1)) * DH * NS
+                                              : (p.h0 != nullptr ? p.h0 + sbase : p.ckpt));
         if constexpr (PIPE) {
-          if (w >= 2) {
-            // GH / UL tasks: the h_in / lam column nb as 16x16x16 B fragments (k = d)
+          // GH / UL tasks of waves 2 and 3: the h_in / lam column nb as
+          // 16x16x16 B fragments (k = d); waves 0 and 1 load and drop them
 #pragma unroll
-            for (int q = 0; q < TPW; ++q) {
-              const int task = (w - 2) + 2 * q;
-              const int kind = task / NBN, nb = task % NBN;
-              const float* src = kind == 0 ? hsrc : lsrc;
-              if (SUM && kind == 1) continue;   // from LDS after the staging barrier
+          for (int q = 0; q < TPW; ++q) {
+            const int task = (w & 1) + 2 * q;
+            const int kind = task / NBN, nb = task % NBN;
+            // lam (kind 1) comes from LDS after the staging barrier in the sum mode
+            const float use = task < 2 * NBN ? (kind == 0 ? has_h : SUM ? 0.f : 1.f) : 0.f;
+            const auto src = kind == 0 || SUM ? hsrc : rr::as_global(lsrc);
 #pragma unroll
-              for (int kb = 0; kb < DH / 16; ++kb)
+            for (int kb = 0; kb < DH / 16; ++kb)
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                  pcol[q][kb][e] = (task < 2 * NBN && src != nullptr)
-                                       ? src[(16 * kb + 4 * (lane >> 4) + e) * NS + 16 * nb + (lane & 15)]
-                                       : 0.f;
-            }
+              for (int e = 0; e < 4; ++e) {
+                const float v = src[(16 * kb + 4 * (lane >> 4) + e) * NS + 16 * (nb & (NBN - 1)) + (lane & 15)];
+                pcol[q][kb][e] = use * v;
+              }
           }
         }
 #pragma unroll
         for (int jj = 0; jj < K::NBW; ++jj) {
           const int j = w + 4 * jj;
-          hin[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-          if (j < K::NB && hsrc != nullptr) {
-            const int db = j / NBN, nb = j % NBN;
+          const int jc = min(j, K::NB - 1), db = jc / NBN, nb = jc % NBN;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) hin[jj][r] = hsrc[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)];
+          for (int r = 0; r < 4; ++r) {
+            const float v = hsrc[(16 * db + 4 * (lane >> 4) + r) * NS + 16 * nb + (lane & 15)];
+            hin[jj][r] = (j < K::NB ? has_h : 0.f) * v;
           }
         }
       };
@@ -490,135 +498,112 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
     __syncthreads();
     // ------------------------------------------------ B2: masked products, rectangle sums
     if constexpr (PIPE) {
-      if (w < DH / 32) {
-        // du operands (used in phase C; the loads land while B2 runs): dY^T
-        // [t'][d] (B of a1) and lam [d][n] (B of a2), d = 32 w + lane % 32
-        const int d = 32 * w + (lane & 31);
+      // du operands (used in phase C by waves w < NBD; the loads land while
+      // B2 runs): the 16x16 B fragments of du's column block d = 16 w + l15,
+      // dY^T [t' = 8 l4 + e][d] and lam^T [n = 16 kk + 4 l4 + e][d].  Every
+      // wave issues them (waves without a du block repeat one), so no branch
+      // join waits for the loads.
+      const int d = 16 * (w & (NBD - 1)) + (lane & 15), l4 = lane >> 4;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+      for (int e = 0; e < 8; ++e) pdy[e] = p.dy[((row0 + 8 * l4 + e) * rowH + h) * DH + d];
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            pdy[kb][e] = p.dy[((row0 + 16 * kb + 8 * (lane >> 5) + e) * rowH + h) * DH + d];
-#pragma unroll
-        for (int kb = 0; kb < NS / 16; ++kb) {
-          const float* src = SUM ? &m.LS[d][16 * kb + 8 * (lane >> 5)] : lsrc + d * NS + 16 * kb + 8 * (lane >> 5);
-          const float4 l0 = *reinterpret_cast<const float4*>(src), l1 = *reinterpret_cast<const float4*>(src + 4);
-          plm[kb][0] = l0.x, plm[kb][1] = l0.y, plm[kb][2] = l0.z, plm[kb][3] = l0.w;
-          plm[kb][4] = l1.x, plm[kb][5] = l1.y, plm[kb][6] = l1.z, plm[kb][7] = l1.w;
-        }
+      for (int kk = 0; kk < NS / 16; ++kk) {
+        const float* src = SUM ? &m.LS[d][16 * kk + 4 * l4] : lsrc + d * NS + 16 * kk + 4 * l4;
+        const float4 l0 = *reinterpret_cast<const float4*>(src);
+        plm[kk][0] = l0.x, plm[kk][1] = l0.y, plm[kk][2] = l0.z, plm[kk][3] = l0.w;
       }
     }
-    if (w < 2) {
-      // wave 0: P = M o CB -> P^T [t][t'], and K = M o G2 o delta_s o span [t'][s];
-      // wave 1: M o G2 -> (M o G2)^T [t][t'].  Rows r32row(4g .. 4g + 3) are
-      // consecutive, so the transposed stores are one 8-byte write per group.
-      const int s = lane & 31;
+    {
+      // Wave w forms rows t' = t0 + q, q < 4, t0 = 8 w + 4 (lane / 32), of
+      // every 32 x 32 product, column s = lane % 32 (one decay per element):
+      //   P^T = (M o CB)^T and (M o G2)^T, [s][t'] (four consecutive t': one
+      //   8-byte write each); M o G2 o delta_s and K = M o G2 o delta_s o
+      //   (cd_t' - cd_s + delta_s), [t'][s];
+      //   R_t = sum_{t' >= t} sum_{s <= t} E[t', s], E = M o delta_s o G2 o CB:
+      //   a prefix over s along the lanes, the rows t' >= s of column s, and
+      //   this wave's partial over its rows (summed in phase D).
+      const int s = lane & 31, t0 = 8 * w + 4 * (lane >> 5);
       const float cds = m.cd[s], ds = m.del[s];
-      float md[16];
+      float pt[4], mg[4], rs = 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int tp = r32row(r, lane);
-        md[r] = rr::chunked::masked_exp(s <= tp, a * (m.cd[tp] - cds));
-      }
-      uint16_t(*dst_hi)[PQ] = w == 0 ? m.y.PT_hi : m.y.MGT_hi;
-      uint16_t(*dst_lo)[PQ] = w == 0 ? m.y.PT_lo : m.y.MGT_lo;
-      const float(*src)[Q + 1] = w == 0 ? m.CB : m.G2;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int tp = r32row(4 * g, lane);
-        u16x4_t hi4, lo4;
-        rr::bf_split4(f32x4_t{md[4 * g] * src[tp][s], md[4 * g + 1] * src[tp + 1][s], md[4 * g + 2] * src[tp + 2][s],
-                              md[4 * g + 3] * src[tp + 3][s]},
-                      hi4, lo4);
-        *reinterpret_cast<u16x4_t*>(&dst_hi[s][tp]) = hi4;
-        *reinterpret_cast<u16x4_t*>(&dst_lo[s][tp]) = lo4;
-      }
-      if (w == 0) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int tp = r32row(r, lane);
-          uint16_t hi, lo;
-          bf_split(md[r] * m.G2[tp][s] * ds * (m.cd[tp] - cds + ds), hi, lo);
-          m.y.Km_hi[tp][s] = hi;
-          m.y.Km_lo[tp][s] = lo;
-        }
-      }
-    } else if (w == 3) {
-      // M o G2 o delta_s [t'][s]
-      const int s = lane & 31;
-      const float cds = m.cd[s], ds = m.del[s];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int tp = r32row(r, lane);
-        const float mg = rr::chunked::masked_exp(s <= tp, a * (m.cd[tp] - cds)) * m.G2[tp][s];
+      for (int q = 0; q < 4; ++q) {
+        const int tp = t0 + q;
+        const float ctp = m.cd[tp];
+        const float md = rr::chunked::masked_exp(s <= tp, a * (ctp - cds));
+        const float cb = m.CB[tp][s];
+        pt[q] = md * cb;
+        mg[q] = md * m.G2[tp][s];
+        const float mgd = mg[q] * ds;
         uint16_t hi, lo;
-        bf_split(mg * ds, hi, lo);
+        bf_split(mgd, hi, lo);
         m.y.MGd_hi[tp][s] = hi;
         m.y.MGd_lo[tp][s] = lo;
-      }
-    } else {
-      // R_t = sum_{t' >= t} sum_{s <= t} E[t', s], E = M o delta_s o G2 o CB: prefix
-      // over s along the lanes, then the rows t' >= t of column t
-      const int s = lane & 31;
-      const float cds = m.cd[s], ds = m.del[s];
-      float rs = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int tp = r32row(r, lane);
-        const float e = rr::chunked::masked_exp(s <= tp, a * (m.cd[tp] - cds)) * ds * m.G2[tp][s] * m.CB[tp][s];
-        const float k = rr::prefix32_sum(e);
+        bf_split(mgd * (ctp - cds + ds), hi, lo);
+        m.y.Km_hi[tp][s] = hi;
+        m.y.Km_lo[tp][s] = lo;
+        const float k = rr::prefix32_sum(mgd * cb);
         rs += tp >= s ? k : 0.f;
       }
+      u16x4_t hi4, lo4;
+      rr::bf_split4(f32x4_t{pt[0], pt[1], pt[2], pt[3]}, hi4, lo4);
+      *reinterpret_cast<u16x4_t*>(&m.y.PT_hi[s][t0]) = hi4;
+      *reinterpret_cast<u16x4_t*>(&m.y.PT_lo[s][t0]) = lo4;
+      rr::bf_split4(f32x4_t{mg[0], mg[1], mg[2], mg[3]}, hi4, lo4);
+      *reinterpret_cast<u16x4_t*>(&m.y.MGT_hi[s][t0]) = hi4;
+      *reinterpret_cast<u16x4_t*>(&m.y.MGT_lo[s][t0]) = lo4;
       rs = rr::halves_sum(rs);
-      if (lane < Q) m.R[lane] = rs;
+      if (lane < Q) m.Rp[w][lane] = rs;
     }
     __syncthreads();
     // ------------------------------------------------ C: du, Z/dB, dC, KB, lam_prev
     const float gam31 = m.gam[Q - 1];
-    if (w < DH / 32) {
-      const int d0 = 32 * w;
-      f32x16_t a1 = {}, a2 = {};
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const int k0 = 16 * kb + 8 * (lane >> 5);
-        const u16x8_t ph = frag(&m.y.PT_hi[lane & 31][k0]), pl = frag(&m.y.PT_lo[lane & 31][k0]);
-        u16x8_t gh, gl;
+    {
+      const int l15 = lane & 15, l4 = lane >> 4;
+      if (w < NBD) {
+        // du, column block d = 16 w + l15:
+        // du = diag(delta) (P^T dY + diag(m31) B lam^T)
+        const int d = 16 * w + l15;
+        u16x8_t gh, gl;   // dY^T [t' = 8 l4 + e][d]
         if constexpr (PIPE) {
-          rr::bf_split8(pdy[kb], gh, gl);
+          rr::bf_split8(pdy, gh, gl);
         } else {
-          gh = frag(&m.GYT_hi[d0 + (lane & 31)][k0]);
-          gl = frag(&m.GYT_lo[d0 + (lane & 31)][k0]);
+          gh = frag(&m.GYT_hi[d][8 * l4]);
+          gl = frag(&m.GYT_lo[d][8 * l4]);
         }
-        a1 = mfma32(ph, gh, a1);
-        a1 = mfma32(ph, gl, a1);
-        a1 = mfma32(pl, gh, a1);
-      }
+        u16x4_t lh[NS / 16], ll[NS / 16];   // lam^T [n = 16 kk + 4 l4 + e][d]
 #pragma unroll
-      for (int kb = 0; kb < NS / 16; ++kb) {
-        const int k0 = 16 * kb + 8 * (lane >> 5);
-        const u16x8_t fa = frag(&m.Bn[lane & 31][k0]);
-        u16x8_t lh, ll;
-        if constexpr (PIPE) {
-          rr::bf_split8(plm[kb], lh, ll);
-        } else {
-          lh = frag(&m.LM_hi[d0 + (lane & 31)][k0]);
-          ll = frag(&m.LM_lo[d0 + (lane & 31)][k0]);
+        for (int kk = 0; kk < NS / 16; ++kk) {
+          if constexpr (PIPE) {
+            rr::bf_split4(f32x4_t{plm[kk][0], plm[kk][1], plm[kk][2], plm[kk][3]}, lh[kk], ll[kk]);
+          } else {
+            lh[kk] = rr::frag4(&m.LM_hi[d][16 * kk + 4 * l4]);
+            ll[kk] = rr::frag4(&m.LM_lo[d][16 * kk + 4 * l4]);
+          }
         }
-        a2 = mfma32(fa, lh, a2);
-        a2 = mfma32(fa, ll, a2);
-      }
-      const int d = d0 + (lane & 31);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int t = r32row(r, lane);
-        rr::st_bf16(p.du, ((row0 + t) * rowH + h) * DH + d, m.del[t] * (a1[r] + m.m31[t] * a2[r]));
+        for (int tb = 0; tb < 2; ++tb) {
+          f32x4_t a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
+          const u16x8_t ph = frag(&m.y.PT_hi[16 * tb + l15][8 * l4]), pl = frag(&m.y.PT_lo[16 * tb + l15][8 * l4]);
+          a1 = mfma16(ph, gh, a1);
+          a1 = mfma16(ph, gl, a1);
+          a1 = mfma16(pl, gh, a1);
+#pragma unroll
+          for (int kk = 0; kk < NS / 16; ++kk) {
+            const u16x4_t fb = rr::frag4(&m.Bn[16 * tb + l15][16 * kk + 4 * l4]);
+            a2 = rr::mfma16k16(fb, lh[kk], a2);
+            a2 = rr::mfma16k16(fb, ll[kk], a2);
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = 16 * tb + 4 * l4 + r;
+            rr::st_bf16(p.du, ((row0 + t) * rowH + h) * DH + d, m.del[t] * (a1[r] + m.m31[t] * a2[r]));
+          }
+        }
       }
-    } else {
-      // Z / dB and dC (+ K B) blocks over the waves >= DH/32, with their row
-      // sums (sum_n B Z, Y = sum_n UL B, X = sum_n GH C) and dA partials
-      const int nw = 4 - DH / 32;
+      // Z / dB and dC (+ K B) blocks, spread over the four waves, with their
+      // row sums (sum_n B Z, Y = sum_n UL B, X = sum_n GH C) and dA partials
       const float cd31 = m.cd[Q - 1];
-      for (int task = w - DH / 32; task < 4 * NBN; task += nw) {
+      for (int task = w; task < 4 * NBN; task += 4) {
         const int kind = task / (2 * NBN), tt = task % (2 * NBN);
         const int tb = tt / NBN, nb = tt % NBN;
         const int row = 16 * tb + (lane & 15), col = 16 * nb + (lane & 15);
@@ -734,7 +719,8 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
         float bz = 0.f;
 #pragma unroll
         for (int nb = 0; nb < NBN; ++nb) bz += m.BZs[nb][t];
-        const float T = m.R[t] + m.Ts[0][t] + m.Ts[1][t] + m.m31[t] * m.gam[t] * tr;
+        const float T = (m.Rp[0][t] + m.Rp[1][t]) + (m.Rp[2][t] + m.Rp[3][t]) + m.Ts[0][t] + m.Ts[1][t] +
+                        m.m31[t] * m.gam[t] * tr;
         rr::st_bf16(p.ddelta, (row0 + t) * rowH + h, a * T + (1.f - a * m.del[t]) * bz);
       }
     } else if (w == 1 && lane < NS) {
