@@ -144,6 +144,59 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
   for (int cc = 0; cc < CPW; ++cc)
 #pragma unroll
     for (int db = 0; db < NBD; ++db) lam[cc][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // the chunk's inputs (phase A), loaded by `issue` at the start of the
+  // chunk.  (Issued during the direct sum's reduction instead, they delay the
+  // sum loops of the costliest workgroups more than they save: measured.)
+  // Every load is issued by every thread, unconditionally and in bounds
+  // (clamped indices; dropped values multiplied by 0, which the compiler
+  // cannot turn into a branch around the load): a load under a branch makes
+  // the branch's join wait for all of them.
+  constexpr int UV = (Q * DH / 8 + 255) / 256, NV = (Q * NS / 8 + 255) / 256, GV = (Q * DH / 4 + 255) / 256;
+  u16x8_t uv[UV], bv[NV], cv[NV];
+  float4 gv[GV];
+  float xv;
+  f32x4_t hin[CPW][NBD];
+  auto issue = [&](int c, int tid) {
+    const int lane = tid & 63, l15 = lane & 15, l4 = lane >> 4;
+    const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;
+    const int64_t baseD = (row0 * p.H + h) * DH, baseN = (row0 * p.H + h) * NS, baseX = row0 * p.H + h;
+#pragma unroll
+    for (int v = 0; v < UV; ++v) {
+      const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
+      uv[v] = *reinterpret_cast<const u16x8_t*>(p.u + baseD + tl * rsD + d0);
+    }
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
+      bv[v] = *reinterpret_cast<const u16x8_t*>(p.Bm + baseN + tl * rsN + n0);
+      cv[v] = *reinterpret_cast<const u16x8_t*>(p.Cm + baseN + tl * rsN + n0);
+    }
+#pragma unroll
+    for (int v = 0; v < GV; ++v) {
+      const int i = tid + 256 * v, tl = (i / (DH / 4)) & (Q - 1), d0 = 4 * (i % (DH / 4));
+      gv[v] = *reinterpret_cast<const float4*>(p.dy + baseD + tl * rsD + d0);
+    }
+    xv = bf_val(p.delta[baseX + (tid & (Q - 1)) * p.H]);   // only lanes < 32 of wave 0 use it
+    // h_in: checkpoint slot c - 1 ([d][n]), h0 (state layout) or, with
+    // neither, zero (the checkpoint buffer read and dropped; its values are finite)
+    const float has_h = c > 0 || p.h0 != nullptr ? 1.f : 0.f;
+    const auto hsrc = rr::as_global(c > 0 ? p.ckpt + (bh * p.nC + c - 1) * DH * NS
+                                          : (p.h0 != nullptr ? p.h0 + bh * DH * NS : p.ckpt));
+    const auto lsrc = rr::as_global(MODE == kPipe ? p.agg + (bh * p.nC + c) * DH * NS : p.ckpt);
+#pragma unroll
+    for (int cc = 0; cc < CPW; ++cc) {
+      const int nb = min(w + 4 * cc, NBN - 1);
+      const float use = w + 4 * cc < NBN ? 1.f : 0.f;
+#pragma unroll
+      for (int db = 0; db < NBD; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int d = 16 * db + 4 * l4 + r, n = 16 * nb + l15;
+          if constexpr (MODE == kPipe) lam[cc][db][r] = use * lsrc[d * NS + n];
+          hin[cc][db][r] = use * has_h * hsrc[c > 0 ? d * NS + n : rr::chunked::state_off<GLA, DH, NS>(d, n)];
+        }
+    }
+  };
   if constexpr (MODE == kDirect) {
     // the adjoint leaving the chunk; chunk 0's workgroup also stores dh0
     const float gam_all = rr::chunked::direct_sum<DH, NS, GLA, true, true>(p, cbeg, b, h, a, smu.d, p.dh0);
@@ -226,55 +279,10 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
     const int lane = tidv & 63, l15 = lane & 15, l4 = lane >> 4, tid = tidv;
     const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;   // first (b, t) row of the chunk
     const int64_t baseD = (row0 * p.H + h) * DH, baseN = (row0 * p.H + h) * NS, baseX = row0 * p.H + h;
-    f32x4_t hin[CPW][NBD];
     float trn[CPW];   // SSD: sum over this lane's rows of lam o h_in, per column
-    // ------------------------------------------------ A: stage (all loads first)
+    // ------------------------------------------------ A: stage
     {
-      constexpr int UV = (Q * DH / 8 + 255) / 256, NV = (Q * NS / 8 + 255) / 256, GV = (Q * DH / 4 + 255) / 256;
-      u16x8_t uv[UV], bv[NV], cv[NV];
-      float4 gv[GV];
-      float xv = GLA ? 1.f : 0.f;
-#pragma unroll
-      for (int v = 0; v < UV; ++v) {
-        const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
-        uv[v] = i < Q * DH / 8 ? *reinterpret_cast<const u16x8_t*>(p.u + baseD + tl * rsD + d0) : u16x8_t{};
-      }
-#pragma unroll
-      for (int v = 0; v < NV; ++v) {
-        const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
-        const bool ok = i < Q * NS / 8;
-        bv[v] = ok ? *reinterpret_cast<const u16x8_t*>(p.Bm + baseN + tl * rsN + n0) : u16x8_t{};
-        cv[v] = ok ? *reinterpret_cast<const u16x8_t*>(p.Cm + baseN + tl * rsN + n0) : u16x8_t{};
-      }
-#pragma unroll
-      for (int v = 0; v < GV; ++v) {
-        const int i = tid + 256 * v, tl = (i / (DH / 4)) & (Q - 1), d0 = 4 * (i % (DH / 4));
-        gv[v] = i < Q * DH / 4 ? *reinterpret_cast<const float4*>(p.dy + baseD + tl * rsD + d0)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-      // unconditional (in-bounds) load, so no branch waits on it; only lanes < 32 of wave 0 use it
-      xv = bf_val(p.delta[baseX + (tid & (Q - 1)) * p.H]);
-      const float* hsrc = c > 0 ? p.ckpt + (bh * p.nC + c - 1) * DH * NS
-                                : (p.h0 != nullptr ? p.h0 + bh * DH * NS : nullptr);
-      const float* lsrc = MODE == kPipe ? p.agg + (bh * p.nC + c) * DH * NS : nullptr;
-#pragma unroll
-      for (int cc = 0; cc < CPW; ++cc) {
-        const int nb = w + 4 * cc;
-#pragma unroll
-        for (int db = 0; db < NBD; ++db) {
-          if constexpr (MODE == kPipe) lam[cc][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-          hin[cc][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-          if (nb < NBN) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int d = 16 * db + 4 * l4 + r, n = 16 * nb + l15;
-              if constexpr (MODE == kPipe) lam[cc][db][r] = lsrc[d * NS + n];
-              if (hsrc != nullptr)
-                hin[cc][db][r] = hsrc[c > 0 ? d * NS + n : rr::chunked::state_off<GLA, DH, NS>(d, n)];
-            }
-          }
-        }
-      }
+      issue(c, tid);
       // LDS writes
 #pragma unroll
       for (int v = 0; v < UV; ++v) {
@@ -417,18 +425,17 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
     __syncthreads();
     // ------------------------------------------------ B2: masked products; GLA dg / SSD T
     // one-chunk modes: this wave's du operands (row block mydb), used in
-    // phase C; the loads land while B2 runs
+    // phase C; the loads land while B2 runs (issued by every wave, clamped:
+    // no branch join waits for them)
     float pdy[REG ? 8 : 1];
     if constexpr (REG) {
-      if (mydb < NBD) {
-        const int d = 16 * mydb + l15;
+      const int d = 16 * min(mydb, NBD - 1) + l15;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pdy[e] = p.dy[baseD + (8 * l4 + e) * rsD + d];
-      }
+      for (int e = 0; e < 8; ++e) pdy[e] = p.dy[baseD + (8 * l4 + e) * rsD + d];
     }
     if constexpr (MODE == kPipe) {
-      if (mydb < NBD) {
-        const int d = 16 * mydb + l15;
+      {
+        const int d = 16 * min(mydb, NBD - 1) + l15;
         const float* lsrc = p.agg + ((bh * p.nC + c) * DH + d) * NS + 8 * l4;
 #pragma unroll
         for (int kk = 0; kk < NS / 32; ++kk) {
