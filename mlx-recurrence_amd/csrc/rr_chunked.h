@@ -680,6 +680,9 @@ struct alignas(16) DirectSmem {
       alignas(16) float cw[BWD ? Q : 4];               // bwd: the chunk's step factors F gam_t
     } st[4];
     float red[2][DH * NS];              // partial sums of waves 0 + 2 and 1 + 3, [d][n]
+    // forward, DH = 64 (row-owned reduction): wave w's partials of the row
+    // blocks db != w (slot db - (db > w)), 16x16 blocks as [lane][4]
+    float xch[!BWD && DH == 64 ? 4 : 1][3][NS / 16][256];
   };
   float tot[kDirectMaxChunks];          // decays of the chunks of the range
   float g0[BWD ? DH * NS : 1];          // backward, chunk 0's own term G_0 (see direct_sum)
@@ -700,9 +703,15 @@ struct NoLoads {
 // (when dh0 is given).
 template <int DH, int NS, bool GLA, bool BWD, bool G0 = false, typename PRE = NoLoads>
 __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, DirectSmem<DH, NS, BWD>& s,
-                            float* dh0 = nullptr, PRE pre = PRE{}) {
+                            float* dh0 = nullptr, PRE pre = PRE{}, f32x4_t* own = nullptr) {
   using S = DirectSmem<DH, NS, BWD>;
   constexpr int NBD = DH / 16, NBN = NS / 16;
+  // forward with DH = 64: row-owned.  The blocks are accumulated transposed
+  // (element r at n = 16 nb + 4 (lane / 16) + r, d = 16 db + lane % 16: the
+  // layout of the forward's state registers) and wave w ends up with the
+  // full sum of row block db = w in `own` (one exchange through LDS, one
+  // barrier); red[] is not used.
+  constexpr bool ROWS = !BWD && DH == 64;
   constexpr int XV = Q * DH / 8 / 64;                           // fwd, per lane and chunk: u16x8 of U
   constexpr int YV = Q * NS / 8 / 64;                           // u16x8 of B (fwd) or C (bwd)
   constexpr int VPC = BWD ? 8 * NBD + 4 * YV : 4 * (XV + YV);   // registers per chunk in flight
@@ -874,8 +883,13 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
         const u16x8_t xfr = frag_tr_st<typename S::SX>(st.X, 16 * db, lane);
 #pragma unroll
         for (int nb = 0; nb < NBN; ++nb) {
-          acc[db][nb] = mfma16(xfr, yf[0][nb], acc[db][nb]);
-          acc[db][nb] = mfma16(xfr, yf[1][nb], acc[db][nb]);
+          if constexpr (ROWS) {   // transposed block: (B^T U)[n][d]
+            acc[db][nb] = mfma16(yf[0][nb], xfr, acc[db][nb]);
+            acc[db][nb] = mfma16(yf[1][nb], xfr, acc[db][nb]);
+          } else {
+            acc[db][nb] = mfma16(xfr, yf[0][nb], acc[db][nb]);
+            acc[db][nb] = mfma16(xfr, yf[1][nb], acc[db][nb]);
+          }
         }
       }
     }
@@ -895,6 +909,37 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
     wave_lds_sync();   // the next chunk's staging rewrites the area
   }
   pre();
+
+  if constexpr (ROWS) {
+    // 5. row-owned: wave w hands its partials of the other row blocks over,
+    // then sums row block w over the four waves in a fixed order
+    __syncthreads();   // the staging areas are dead (xch[] overlays them)
+    f32x4_t mine[NBN];
+#pragma unroll
+    for (int db = 0; db < NBD; ++db) {
+      if (db == w) {
+#pragma unroll
+        for (int nb = 0; nb < NBN; ++nb) mine[nb] = acc[db][nb];
+      } else {
+#pragma unroll
+        for (int nb = 0; nb < NBN; ++nb)
+          *reinterpret_cast<f32x4_t*>(&s.xch[w][db - (db > w ? 1 : 0)][nb][4 * lane]) = acc[db][nb];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int nb = 0; nb < NBN; ++nb) own[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int src = 0; src < 4; ++src) {
+      const int slot = min(w - (w > src ? 1 : 0), 2);   // in bounds; unused for src == w
+#pragma unroll
+      for (int nb = 0; nb < NBN; ++nb) {
+        const f32x4_t v = *reinterpret_cast<const f32x4_t*>(&s.xch[src][slot][nb][4 * lane]);
+        own[nb] += src == w ? mine[nb] : v;
+      }
+    }
+    return gam_all;
+  }
 
   // 5. partial sums: red[0] = acc_0 + acc_2, red[1] = acc_1 + acc_3
   __syncthreads();   // the staging areas are dead (red[] overlays them)
@@ -1064,16 +1109,23 @@ __global__ __launch_bounds__(256, (kFwdWgs<DH, NS, MODE, GLA>)) void fwd_kernel(
   };
   if constexpr (MODE == kDirect) {
     // the chunk's loads go out when each wave has staged its last summed chunk
-    const float gam_all = direct_sum<DH, NS, GLA, false>(p, cbeg, b, h, a, smu.d, nullptr, [&] { issue(cbeg, tid); });
+    f32x4_t own[DH == 64 ? NBN : 1];
+    const float gam_all =
+        direct_sum<DH, NS, GLA, false>(p, cbeg, b, h, a, smu.d, nullptr, [&] { issue(cbeg, tid); }, own);
     const float* h0b = p.h0 != nullptr ? p.h0 + bh * DH * NS : nullptr;
+    if constexpr (DH == 64) {   // row block w, summed in registers
 #pragma unroll
-    for (int i = 0; i < DBW; ++i) {
-      const int db = w + 4 * i;
-      if (db < NBD) {
+      for (int nb = 0; nb < NBN; ++nb) hst[0][nb] = own[nb];
+    } else {
 #pragma unroll
-        for (int nb = 0; nb < NBN; ++nb)
+      for (int i = 0; i < DBW; ++i) {
+        const int db = w + 4 * i;
+        if (db < NBD) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) hst[i][nb][r] = direct_partial(smu.d, 16 * db + l15, 16 * nb + 4 * l4 + r);
+          for (int nb = 0; nb < NBN; ++nb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) hst[i][nb][r] = direct_partial(smu.d, 16 * db + l15, 16 * nb + 4 * l4 + r);
+        }
       }
     }
     if (h0b != nullptr) {
