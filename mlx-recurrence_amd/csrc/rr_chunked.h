@@ -1014,27 +1014,30 @@ __device__ __forceinline__ float direct_ext(float gam_all, const float* ext, int
 }
 
 // ------------------------------------------------------------------ forward
-template <int DH, int NS>
-struct FwdSmem {
-  uint16_t Ut[DH][PQ];                 // U^T  [d][s]
-  uint16_t C[Q][Cfg<DH, NS>::PN];      // C    [t][n]
-  uint16_t B[Q][Cfg<DH, NS>::PN];      // B    [s][n]
-  uint16_t BwT_hi[NS][PQ];             // (m31 o w o B)^T [n][s]
-  uint16_t BwT_lo[NS][PQ];
-  uint16_t W_hi[Q][PQ];                // M o CB^T o w_s  [t][s]
+// TRB (SSD with N <= 32): the end state reads B transposed from LDS and
+// weights it in registers; otherwise (m31 o w o B)^T is staged as BwT.
+template <int DH, int NS, bool TRB>
+struct alignas(16) FwdSmem {
+  uint16_t Ut[DH][PQ];                                     // U^T  [d][s]
+  uint16_t C[Q][Cfg<DH, NS>::PN];                          // C    [t][n]
+  uint16_t B[Q][TRB ? Staged<NS>::P : Cfg<DH, NS>::PN];    // B    [s][n]
+  uint16_t BwT_hi[TRB ? 1 : NS][PQ];                       // (m31 o w o B)^T [n][s]
+  uint16_t BwT_lo[TRB ? 1 : NS][PQ];
+  uint16_t W_hi[Q][PQ];                                    // M o CB^T o w_s  [t][s]
   uint16_t W_lo[Q][PQ];
-  float x[Q];      // step input (SSD delta, GLA gate)
-  float cd[Q];     // SSD: cumulative delta
+  float x[Q];       // step input (SSD delta, GLA gate)
+  float cd[4][Q];   // SSD: cumulative delta (a copy per wave)
   float gam[Q];
+  float wend[Q];    // TRB: m31 o w, the step factors of the end state
 };
 
-template <int DH, int NS, bool DIRECT>
+template <int DH, int NS, bool DIRECT, bool TRB>
 union FwdShared {
-  FwdSmem<DH, NS> f;
+  FwdSmem<DH, NS, TRB> f;
 };
-template <int DH, int NS>
-union FwdShared<DH, NS, true> {
-  FwdSmem<DH, NS> f;
+template <int DH, int NS, bool TRB>
+union FwdShared<DH, NS, true, TRB> {
+  FwdSmem<DH, NS, TRB> f;
   DirectSmem<DH, NS, false> d;
 };
 
@@ -1056,14 +1059,15 @@ union FwdShared<DH, NS, true> {
 // per workgroup, so every workgroup of a 16-chunk sequence at batch 3 can be
 // resident); the register budget follows.
 template <int DH, int NS, int MODE, bool GLA>
-constexpr int kFwdWgs = GLA && MODE == kDirect && 160 * 1024 / sizeof(FwdShared<DH, NS, true>) >= 3 ? 3 : 1;
+constexpr int kFwdWgs = GLA && MODE == kDirect && 160 * 1024 / sizeof(FwdShared<DH, NS, true, false>) >= 3 ? 3 : 1;
 
 template <int DH, int NS, int MODE, bool GLA>
 __global__ __launch_bounds__(256, (kFwdWgs<DH, NS, MODE, GLA>)) void fwd_kernel(ChunkArgs p) {
   constexpr int NBD = DH / 16, NBN = NS / 16;
   constexpr int DBW = (NBD + 3) / 4;   // row blocks per wave
   constexpr bool STATE = MODE == kWhole || MODE == kDirect;   // forms the chunk's end state
-  __shared__ FwdShared<DH, NS, MODE == kDirect> smu;
+  constexpr bool TRB = !GLA && NS <= 32;
+  __shared__ FwdShared<DH, NS, MODE == kDirect, TRB> smu;
   auto& sm = smu.f;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l15 = lane & 15, l4 = lane >> 4;
@@ -1198,41 +1202,77 @@ __global__ __launch_bounds__(256, (kFwdWgs<DH, NS, MODE, GLA>)) void fwd_kernel(
       if (tid < Q) sm.x[tid] = xv;
     }
     __syncthreads();
-    // ---- step scalars (every wave; lanes s and s + 32 hold step s);
-    // W = M o C B^T o w_s (wave 0); (m31 o w o B)^T (the other waves)
+    // ---- step scalars (every wave; lanes s and s + 32 hold step s), then
+    // W = M o C B^T o w_s and, unless TRB, (m31 o w o B)^T.  SSD: W's rows
+    // split over the waves (t = 8 w + 4 (lane / 32) + q, the r32row rows
+    // r = 4 w + q), BwT over all threads.  GLA: wave 0 forms W while the
+    // others stage BwT (measured: the split's redundant C B^T products and
+    // decay chains cost GLA more than they save).
     const StepScalars sc = step_scalars<GLA>(sm.x[lane & (Q - 1)], a, lane);
-    if (w == 0) {
-      if (lane < Q) {
-        sm.cd[lane] = sc.cd;
+    if (lane < Q) {
+      if constexpr (!GLA) sm.cd[w][lane] = sc.cd;   // this wave's copy, for its decays
+      if (w == 0) {
         sm.gam[lane] = sc.gam;
+        if constexpr (TRB) sm.wend[lane] = sc.m31 * sc.w;
       }
-      wave_lds_sync();   // cd for the decays below
-      f32x16_t cb = {};
+    }
+    auto stage_bwt = [&](int first, int stride) {
+      // lane s (and s + 32) weights column s
+      const float wend = sc.m31 * sc.w;
+      for (int i = first; i < Q * NS; i += stride) {
+        const int n = i / Q, s2 = i % Q;
+        uint16_t hi, lo;
+        bf_split(wend * bf_val(sm.B[s2][n]), hi, lo);
+        sm.BwT_hi[n][s2] = hi;
+        sm.BwT_lo[n][s2] = lo;
+      }
+    };
+    if constexpr (GLA) {
+      if (w == 0) {
+        f32x16_t cb = {};
+#pragma unroll
+        for (int kb = 0; kb < NS / 16; ++kb)
+          cb = mfma32(frag(&sm.C[lane & 31][16 * kb + 8 * (lane >> 5)]),
+                      frag(&sm.B[lane & 31][16 * kb + 8 * (lane >> 5)]), cb);
+        const int s = lane & 31;
+        float m[16];
+        decay_block32<true>(sm.x, a, lane, m);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int t = r32row(r, lane);
+          uint16_t hi, lo;
+          bf_split(m[r] * sc.w * cb[r], hi, lo);
+          sm.W_hi[t][s] = hi;
+          sm.W_lo[t][s] = lo;
+        }
+      } else if constexpr (STATE) {
+        stage_bwt(tid - 64, 192);
+      }
+    } else {
+      wave_lds_sync();   // this wave's cd
+      f32x16_t cb = {};   // C B^T, every wave (its rows picked below)
 #pragma unroll
       for (int kb = 0; kb < NS / 16; ++kb)
         cb = mfma32(frag(&sm.C[lane & 31][16 * kb + 8 * (lane >> 5)]),
                     frag(&sm.B[lane & 31][16 * kb + 8 * (lane >> 5)]), cb);
-      const int s = lane & 31;
-      float m[16];
-      decay_block32<GLA>(GLA ? sm.x : sm.cd, a, lane, m);
+      float cq[4];
+      switch (w) {   // uniform
+        case 0: cq[0] = cb[0], cq[1] = cb[1], cq[2] = cb[2], cq[3] = cb[3]; break;
+        case 1: cq[0] = cb[4], cq[1] = cb[5], cq[2] = cb[6], cq[3] = cb[7]; break;
+        case 2: cq[0] = cb[8], cq[1] = cb[9], cq[2] = cb[10], cq[3] = cb[11]; break;
+        default: cq[0] = cb[12], cq[1] = cb[13], cq[2] = cb[14], cq[3] = cb[15]; break;
+      }
+      const int s = lane & 31, t0 = 8 * w + 4 * (lane >> 5);
+      const float cds = sm.cd[w][s];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int t = r32row(r, lane);
+      for (int q = 0; q < 4; ++q) {
+        const float mq = masked_exp(s <= t0 + q, a * (sm.cd[w][t0 + q] - cds));   // M[t0 + q][s]
         uint16_t hi, lo;
-        bf_split(m[r] * sc.w * cb[r], hi, lo);
-        sm.W_hi[t][s] = hi;
-        sm.W_lo[t][s] = lo;
+        bf_split(mq * sc.w * cq[q], hi, lo);
+        sm.W_hi[t0 + q][s] = hi;
+        sm.W_lo[t0 + q][s] = lo;
       }
-    } else if constexpr (STATE) {
-      // lane s (and s + 32) weights column s; 192 threads cover Q x NS
-      const float wend = sc.m31 * sc.w;
-      for (int i = tid - 64; i < Q * NS; i += 192) {
-        const int n = i / Q, s = i % Q;
-        uint16_t hi, lo;
-        bf_split(wend * bf_val(sm.B[s][n]), hi, lo);
-        sm.BwT_hi[n][s] = hi;
-        sm.BwT_lo[n][s] = lo;
-      }
+      if constexpr (STATE && !TRB) stage_bwt(tid, 256);
     }
     __syncthreads();
     // ---- Y and the end state of this wave's rows
@@ -1264,11 +1304,31 @@ __global__ __launch_bounds__(256, (kFwdWgs<DH, NS, MODE, GLA>)) void fwd_kernel(
       }
       if constexpr (STATE) {
         float* ck = p.ckpt + (bh * p.nC + c) * DH * NS;
+        // TRB: the (m31 o w o B)^T operands from B's k-runs (transposing LDS
+        // reads), weighted per step and split in registers (steps
+        // s = 8 (lane / 16) + e); else from BwT
+        float wl[8];
+        if constexpr (TRB) {
+          const float4 w0 = *reinterpret_cast<const float4*>(&sm.wend[8 * l4]);
+          const float4 w1 = *reinterpret_cast<const float4*>(&sm.wend[8 * l4 + 4]);
+          wl[0] = w0.x, wl[1] = w0.y, wl[2] = w0.z, wl[3] = w0.w, wl[4] = w1.x, wl[5] = w1.y, wl[6] = w1.z, wl[7] = w1.w;
+        }
 #pragma unroll
         for (int nb = 0; nb < NBN; ++nb) {
+          u16x8_t bh, bl;
+          if constexpr (TRB) {
+            const u16x8_t braw = frag_tr(&sm.B[0][16 * nb], Staged<NS>::P, lane);
+            float bw[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) bw[e] = wl[e] * bf_val(braw[e]);
+            rr::bf_split8(bw, bh, bl);
+          } else {
+            bh = frag(&sm.BwT_hi[16 * nb + l15][8 * l4]);
+            bl = frag(&sm.BwT_lo[16 * nb + l15][8 * l4]);
+          }
           f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-          acc = mfma16(frag(&sm.BwT_hi[16 * nb + l15][8 * l4]), fu, acc);
-          acc = mfma16(frag(&sm.BwT_lo[16 * nb + l15][8 * l4]), fu, acc);
+          acc = mfma16(bh, fu, acc);
+          acc = mfma16(bl, fu, acc);
 #pragma unroll
           for (int r = 0; r < 4; ++r) hst[i][nb][r] = Gam * hst[i][nb][r] + acc[r];
           *reinterpret_cast<float4*>(ck + (16 * db + l15) * NS + 16 * nb + 4 * l4) =
