@@ -93,7 +93,7 @@ struct alignas(16) ColBwdSmem {
   float XYp[4][2][Q];                      // per-wave partial X, Y
   float BZp[GLA ? 1 : 4][Q];               // SSD: per-wave partial sum_n B Z
   float xin[Q], dec[Q], gam[Q], m31[Q], w[Q], cd[Q];
-  float HT[Q];                             // SSD: T_t = sum lam_t h_t
+  float Rp[GLA ? 1 : 4][Q];                // SSD: per-wave partials of R_t (T_t = sum lam_t h_t)
   float Ts[GLA ? 1 : 2][Q];                // SSD: suffix of gam X, prefix of m31 w Y
   float trw[4];
 };
@@ -446,11 +446,58 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
         }
       }
     }
-    if (w != 2) {
-      // wave 0: P^T (CB registers); wave 1: MG^T (G2 registers); wave 3: MG o w_s
-      // and, for SSD, K (G2 from LDS)
+    if constexpr (!GLA) {
+      // Wave w forms rows t' = t0 + q, q < 4, t0 = 8 w + 4 (lane / 32), of
+      // every 32 x 32 product, column s = lane % 32 (one decay per element):
+      // P^T and MG^T [s][t'] (four consecutive t': one 8-byte write each),
+      // MG o w_s and K = MG o w_s o (cd_t' - cd_s) [t'][s], and its partial of
+      // R_t = sum_{t' >= t} sum_{s <= t} (M o w_s o G2 o CB)[t', s] (prefix
+      // over s along the lanes, then the rows t' >= s of column s).
+      const int s = lane & 31, t0 = 8 * w + 4 * (lane >> 5);
+      const float cds = m.cd[s], wsv = m.w[s];
+      float pt[4], mg[4], rs = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int tp = t0 + q;
+        const float ctp = m.cd[tp];
+        const float md = rr::chunked::masked_exp(s <= tp, a * (ctp - cds));
+        const float cb = m.CB[tp][s];
+        pt[q] = md * cb;
+        mg[q] = md * m.G2[tp][s];
+        const float mgw = mg[q] * wsv;
+        uint16_t hi, lo;
+        bf_split(mgw, hi, lo);
+        m.y.MG_hi[tp][s] = hi;
+        m.y.MG_lo[tp][s] = lo;
+        bf_split(mgw * (ctp - cds), hi, lo);
+        m.y.Km_hi[tp][s] = hi;
+        m.y.Km_lo[tp][s] = lo;
+        const float k = rr::prefix32_sum(mgw * cb);
+        rs += tp >= s ? k : 0.f;
+      }
+      u16x4_t hi4, lo4;
+      rr::bf_split4(f32x4_t{pt[0], pt[1], pt[2], pt[3]}, hi4, lo4);
+      *reinterpret_cast<u16x4_t*>(&m.y.PT_hi[s][t0]) = hi4;
+      *reinterpret_cast<u16x4_t*>(&m.y.PT_lo[s][t0]) = lo4;
+      rr::bf_split4(f32x4_t{mg[0], mg[1], mg[2], mg[3]}, hi4, lo4);
+      *reinterpret_cast<u16x4_t*>(&m.y.MGT_hi[s][t0]) = hi4;
+      *reinterpret_cast<u16x4_t*>(&m.y.MGT_lo[s][t0]) = lo4;
+      rs = rr::halves_sum(rs);
+      if (lane < Q) m.Rp[w][lane] = rs;
+      if (w == 2) {
+        // lanes 0..31: suffix of gam X in reversed lane order; lanes 32..63: prefix of m31 w Y
+        const int tq = lane < Q ? Q - 1 - lane : lane - Q;
+        // (every lane reads both factors and selects: no divergent branch)
+        const int kx = lane < Q ? 0 : 1;
+        const float gq = m.gam[tq], mw = m.m31[tq] * m.w[tq];
+        const float xy =
+            (lane < Q ? gq : mw) * (m.XYp[0][kx][tq] + m.XYp[1][kx][tq] + m.XYp[2][kx][tq] + m.XYp[3][kx][tq]);
+        m.Ts[lane < Q ? 0 : 1][tq] = rr::prefix32_sum(xy);
+      }
+    } else if (w != 2) {
+      // GLA: wave 0: P^T (CB registers); wave 1: MG^T (G2 registers); wave 3: MG o w_s
       float md[16];
-      rr::chunked::decay_block32<GLA>(GLA ? m.xin : m.cd, a, lane, md);
+      rr::chunked::decay_block32<true>(m.xin, a, lane, md);
       const int s = lane & 31;
       if (w != 3) {
         // rows r32row(4g .. 4g + 3) are consecutive: one 8-byte write per group
@@ -476,40 +523,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
           bf_split(mgw, hi, lo);
           m.y.MG_hi[tp][s] = hi;
           m.y.MG_lo[tp][s] = lo;
-          if constexpr (!GLA) {
-            bf_split(mgw * (m.cd[tp] - m.cd[s]), hi, lo);
-            m.y.Km_hi[tp][s] = hi;
-            m.y.Km_lo[tp][s] = lo;
-          }
         }
-      }
-    } else if constexpr (!GLA) {
-      // T_t = R_t + sum_{t' >= t} gam X + sum_{s <= t} m31 w Y + m31_t gam_t tr,
-      // R_t = sum_{t' >= t} sum_{s <= t} K[t', s], K = M o w_s o G2 o CB:
-      // prefix over s along the lanes, then the rows t' >= t of column t.
-      float md[16];
-      rr::chunked::decay_block32<false>(m.cd, a, lane, md);
-      const int s = lane & 31;
-      const float wsv = m.w[s];
-      float rs = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int tp = r32row(r, lane);
-        const float k = rr::prefix32_sum(md[r] * wsv * m.G2[tp][s] * m.CB[tp][s]);
-        rs += tp >= s ? k : 0.f;
-      }
-      rs = rr::halves_sum(rs);
-      // lanes 0..31: suffix of gam X in reversed lane order; lanes 32..63: prefix of m31 w Y
-      const int tq = lane < Q ? Q - 1 - lane : lane - Q;
-      // (every lane reads both factors and selects: no divergent branch)
-      const int kx = lane < Q ? 0 : 1;
-      const float gq = m.gam[tq], mw = m.m31[tq] * m.w[tq];
-      const float xy = (lane < Q ? gq : mw) * (m.XYp[0][kx][tq] + m.XYp[1][kx][tq] + m.XYp[2][kx][tq] + m.XYp[3][kx][tq]);
-      m.Ts[lane < Q ? 0 : 1][tq] = rr::prefix32_sum(xy);
-      rr::wave_lds_sync();
-      if (lane < Q) {
-        const float tr = m.trw[0] + m.trw[1] + m.trw[2] + m.trw[3];
-        m.HT[lane] = rs + m.Ts[0][lane] + m.Ts[1][lane] + m.m31[lane] * m.gam[lane] * tr;
       }
     } else {
       // GLA: dg_t = sum_{t'} (M o W)[t', t] + m31_t (P_t + gam_{t-1} tr), division free:
@@ -695,7 +709,11 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
       __syncthreads();
       if (w == 0 && lane < Q) {
         const float bzt = m.BZp[0][lane] + m.BZp[1][lane] + m.BZp[2][lane] + m.BZp[3][lane];
-        rr::st_bf16(p.ddelta, baseX + lane * p.H, a * m.HT[lane] + (1.f - a * m.xin[lane]) * bzt);
+        // T_t = R_t + sum_{t' >= t} gam X + sum_{s <= t} m31 w Y + m31_t gam_t tr
+        const float tr = m.trw[0] + m.trw[1] + m.trw[2] + m.trw[3];
+        const float T = (m.Rp[0][lane] + m.Rp[1][lane]) + (m.Rp[2][lane] + m.Rp[3][lane]) + m.Ts[0][lane] +
+                        m.Ts[1][lane] + m.m31[lane] * m.gam[lane] * tr;
+        rr::st_bf16(p.ddelta, baseX + lane * p.H, a * T + (1.f - a * m.xin[lane]) * bzt);
       }
     }
     if (MODE == kWhole) __syncthreads();   // the next chunk rewrites the LDS
