@@ -160,21 +160,26 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
     const int lane = tid & 63, l15 = lane & 15, l4 = lane >> 4;
     const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;
     const int64_t baseD = (row0 * p.H + h) * DH, baseN = (row0 * p.H + h) * NS, baseX = row0 * p.H + h;
+    // uniform chunk bases, 32-bit unsigned per-lane offsets
+    const uint16_t* const uB = p.u + baseD;
+    const uint16_t* const bB = p.Bm + baseN;
+    const uint16_t* const cB = p.Cm + baseN;
+    const float* const dyB = p.dy + baseD;
 #pragma unroll
     for (int v = 0; v < UV; ++v) {
       const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
-      uv[v] = *reinterpret_cast<const u16x8_t*>(p.u + baseD + tl * rsD + d0);
+      uv[v] = rr::ld32<u16x8_t>(uB, (uint32_t)(tl * rsD + d0));
     }
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
-      bv[v] = *reinterpret_cast<const u16x8_t*>(p.Bm + baseN + tl * rsN + n0);
-      cv[v] = *reinterpret_cast<const u16x8_t*>(p.Cm + baseN + tl * rsN + n0);
+      bv[v] = rr::ld32<u16x8_t>(bB, (uint32_t)(tl * rsN + n0));
+      cv[v] = rr::ld32<u16x8_t>(cB, (uint32_t)(tl * rsN + n0));
     }
 #pragma unroll
     for (int v = 0; v < GV; ++v) {
       const int i = tid + 256 * v, tl = (i / (DH / 4)) & (Q - 1), d0 = 4 * (i % (DH / 4));
-      gv[v] = *reinterpret_cast<const float4*>(p.dy + baseD + tl * rsD + d0);
+      gv[v] = rr::ld32<float4>(dyB, (uint32_t)(tl * rsD + d0));
     }
     xv = bf_val(p.delta[baseX + (tid & (Q - 1)) * p.H]);   // only lanes < 32 of wave 0 use it
     // h_in: checkpoint slot c - 1 ([d][n]), h0 (state layout) or, with
@@ -192,8 +197,9 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int d = 16 * db + 4 * l4 + r, n = 16 * nb + l15;
-          if constexpr (MODE == kPipe) lam[cc][db][r] = use * lsrc[d * NS + n];
-          hin[cc][db][r] = use * has_h * hsrc[c > 0 ? d * NS + n : rr::chunked::state_off<GLA, DH, NS>(d, n)];
+          if constexpr (MODE == kPipe) lam[cc][db][r] = use * rr::ld32<float>(lsrc, (uint32_t)(d * NS + n));
+          hin[cc][db][r] =
+              use * has_h * rr::ld32<float>(hsrc, (uint32_t)(c > 0 ? d * NS + n : rr::chunked::state_off<GLA, DH, NS>(d, n)));
         }
     }
   };
@@ -279,6 +285,9 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
     const int lane = tidv & 63, l15 = lane & 15, l4 = lane >> 4, tid = tidv;
     const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;   // first (b, t) row of the chunk
     const int64_t baseD = (row0 * p.H + h) * DH, baseN = (row0 * p.H + h) * NS, baseX = row0 * p.H + h;
+    uint16_t* const duB = p.du + baseD;
+    uint16_t* const dBB = p.dB + baseN;
+    uint16_t* const dCB = p.dC + baseN;
     float trn[CPW];   // SSD: sum over this lane's rows of lam o h_in, per column
     // ------------------------------------------------ A: stage
     {
@@ -431,7 +440,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
     if constexpr (REG) {
       const int d = 16 * min(mydb, NBD - 1) + l15;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pdy[e] = p.dy[baseD + (8 * l4 + e) * rsD + d];
+      for (int e = 0; e < 8; ++e) pdy[e] = rr::ld32<float>(p.dy + baseD, (uint32_t)((8 * l4 + e) * rsD + d));
     }
     if constexpr (MODE == kPipe) {
       {
@@ -620,7 +629,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = 16 * tb + 4 * l4 + r;
-          rr::st_bf16(p.du, baseD + t * rsD + 16 * db + l15, m.w[t] * (a1[r] + m.m31[t] * a2[r]));
+          rr::st_bf16_u32(duB, (uint32_t)(t * rsD + 16 * db + l15), m.w[t] * (a1[r] + m.m31[t] * a2[r]));
         }
       }
     }
@@ -649,11 +658,11 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = 16 * tb + 4 * l4 + r, n = 16 * nb + l15;
-          const int64_t gi = baseN + t * rsN + n;
+          const uint32_t gi = (uint32_t)(t * rsN + n);
           const float z = ak[r] + m.m31[t] * ul[cc][tb][r];
           const float dbv = m.w[t] * z, dcv = m.gam[t] * gh[cc][tb][r] + aq[r];
-          rr::st_bf16(p.dB, gi, dbv);
-          rr::st_bf16(p.dC, gi, dcv);
+          rr::st_bf16_u32(dBB, gi, dbv);
+          rr::st_bf16_u32(dCB, gi, dcv);
           if constexpr (!GLA) {
             const float bv = bf_val(m.Kn[t][n]), cv = bf_val(m.Qn[t][n]);
             bz[tb][r] += bv * z;

@@ -81,6 +81,23 @@ __device__ __forceinline__ void bf_split8(const float (&x)[8], u16x8_t& hi, u16x
 
 // Store an fp32 value as bf16 (round to nearest even).
 __device__ __forceinline__ void st_bf16(uint16_t* p, int64_t i, float v) { p[i] = bf_bits(v); }
+// Accesses at a uniform base plus a 32-bit per-lane offset: the byte offset
+// is formed in 32 bits (element i of a chunk, i * sizeof(E) < 2^32), so the
+// address is the SGPR base plus a VGPR offset with no 64-bit math per element.
+// ld32<T>: a T (e.g. a 16-byte vector) starting at element i.
+template <typename T, typename E>
+__device__ __forceinline__ T ld32(const E* base, uint32_t i) {
+  return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + i * (uint32_t)sizeof(E));
+}
+template <typename T, typename E>
+__device__ __forceinline__ T ld32(const __attribute__((address_space(1))) E* base, uint32_t i) {
+  typedef const __attribute__((address_space(1))) char gchar;
+  typedef const __attribute__((address_space(1))) T gT;
+  return *(gT*)((gchar*)base + i * (uint32_t)sizeof(E));
+}
+__device__ __forceinline__ void st_bf16_u32(uint16_t* base, uint32_t i, float v) {
+  *reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(base) + i * 2u) = bf_bits(v);
+}
 
 // 16-byte fragment read from LDS (address must be 16-byte aligned).
 __device__ __forceinline__ u16x8_t frag(const uint16_t* p) {
