@@ -680,9 +680,10 @@ struct alignas(16) DirectSmem {
       alignas(16) float cw[BWD ? Q : 4];               // bwd: the chunk's step factors F gam_t
     } st[4];
     float red[2][DH * NS];              // partial sums of waves 0 + 2 and 1 + 3, [d][n]
-    // forward, DH = 64 (row-owned reduction): wave w's partials of the row
-    // blocks db != w (slot db - (db > w)), 16x16 blocks as [lane][4]
-    float xch[!BWD && DH == 64 ? 4 : 1][3][NS / 16][256];
+    // DH = 64 (row-owned reduction; backward with NS = 16): wave w's
+    // partials of the row blocks db != w (slot db - (db > w)), 16x16 blocks
+    // as [lane][4]
+    float xch[DH == 64 && (!BWD || NS == 16) ? 4 : 1][3][NS / 16][256];
   };
   float tot[kDirectMaxChunks];          // decays of the chunks of the range
   float g0[BWD ? DH * NS : 1];          // backward, chunk 0's own term G_0 (see direct_sum)
@@ -706,12 +707,14 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
                             float* dh0 = nullptr, PRE pre = PRE{}, f32x4_t* own = nullptr) {
   using S = DirectSmem<DH, NS, BWD>;
   constexpr int NBD = DH / 16, NBN = NS / 16;
-  // forward with DH = 64: row-owned.  The blocks are accumulated transposed
-  // (element r at n = 16 nb + 4 (lane / 16) + r, d = 16 db + lane % 16: the
-  // layout of the forward's state registers) and wave w ends up with the
-  // full sum of row block db = w in `own` (one exchange through LDS, one
-  // barrier); red[] is not used.
-  constexpr bool ROWS = !BWD && DH == 64;
+  // DH = 64, forward or backward with NS = 16: row-owned.  Wave w ends up
+  // with the full sum of row block db = w in `own` (one exchange through LDS,
+  // one barrier; red[] is not used).  The forward accumulates its blocks
+  // transposed (element r at n = 16 nb + 4 (lane / 16) + r, d = 16 db +
+  // lane % 16: the layout of its state registers); the backward's are in the
+  // natural layout (d = 16 db + 4 (lane / 16) + r, n = 16 nb + lane % 16),
+  // that of its adjoint registers.
+  constexpr bool ROWS = DH == 64 && (!BWD || NS == 16);
   constexpr int XV = Q * DH / 8 / 64;                           // fwd, per lane and chunk: u16x8 of U
   constexpr int YV = Q * NS / 8 / 64;                           // u16x8 of B (fwd) or C (bwd)
   constexpr int VPC = BWD ? 8 * NBD + 4 * YV : 4 * (XV + YV);   // registers per chunk in flight
@@ -936,6 +939,32 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
       for (int nb = 0; nb < NBN; ++nb) {
         const f32x4_t v = *reinterpret_cast<const f32x4_t*>(&s.xch[src][slot][nb][4 * lane]);
         own[nb] += src == w ? mine[nb] : v;
+      }
+    }
+    if constexpr (G0) {
+      if (g0) {
+        // dh0 = tot_0 lam(0) + G_0 for this wave's rows (natural layout)
+        const int l15 = lane & 15, l4 = lane >> 4;
+        const float t0 = s.tot[0];
+        const float* ext = p.dfinal != nullptr ? p.dfinal + ((int64_t)b * p.H + h) * DH * NS : nullptr;
+        float* out = dh0 + ((int64_t)b * p.H + h) * DH * NS;
+        f32x4_t lam[NBN];
+#pragma unroll
+        for (int nb = 0; nb < NBN; ++nb) lam[nb] = own[nb];
+        if (ext != nullptr) {
+#pragma unroll
+          for (int nb = 0; nb < NBN; ++nb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              lam[nb][r] += gam_all * ext[state_off<GLA, DH, NS>(16 * w + 4 * l4 + r, 16 * nb + l15)];
+        }
+#pragma unroll
+        for (int nb = 0; nb < NBN; ++nb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int d = 16 * w + 4 * l4 + r, n = 16 * nb + l15;
+            out[state_off<GLA, DH, NS>(d, n)] = t0 * lam[nb][r] + s.g0[d * NS + n];
+          }
       }
     }
     return gam_all;

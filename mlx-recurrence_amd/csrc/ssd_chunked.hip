@@ -282,16 +282,24 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
         // lam summed over the later chunks' inputs; the chunk's own loads go
         // out when each wave has staged its last summed chunk; the chunk-0
         // workgroup also writes dh0
-        const float gam_all = rr::chunked::direct_sum<DH, NS, false, true, true>(p, cbeg, b, h, a, smu.d, p.dh0, issue);
+        // (DH = 64, NS = 16: wave w's block j = w comes back summed in `own`)
+        constexpr bool OWN = DH == 64 && NS == 16;
+        f32x4_t own[1];
+        const float gam_all =
+            rr::chunked::direct_sum<DH, NS, false, true, true>(p, cbeg, b, h, a, smu.d, p.dh0, issue, own);
         const float* dfb = p.dfinal != nullptr ? p.dfinal + sbase : nullptr;
+        if constexpr (OWN) {
+          lam[0] = own[0];
+        } else {
 #pragma unroll
-        for (int jj = 0; jj < K::NBW; ++jj) {
-          const int j = w + 4 * jj;
-          if (j < K::NB) {
-            const int db = j / NBN, nb = j % NBN;
+          for (int jj = 0; jj < K::NBW; ++jj) {
+            const int j = w + 4 * jj;
+            if (j < K::NB) {
+              const int db = j / NBN, nb = j % NBN;
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              lam[jj][r] = rr::chunked::direct_partial(smu.d, 16 * db + 4 * (lane >> 4) + r, 16 * nb + (lane & 15));
+              for (int r = 0; r < 4; ++r)
+                lam[jj][r] = rr::chunked::direct_partial(smu.d, 16 * db + 4 * (lane >> 4) + r, 16 * nb + (lane & 15));
+            }
           }
         }
         if (dfb != nullptr) {
