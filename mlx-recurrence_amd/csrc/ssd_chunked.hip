@@ -209,6 +209,10 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
     if constexpr (MODE == kWhole) asm volatile("" : "+v"(tidv));
     const int tid = tidv, lane = tidv & 63;
     const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;
+    // uniform chunk bases ([.., H, DH] and [.., H, NS] rows of step 0) and
+    // 32-bit per-lane offsets (no 64-bit address math per element)
+    const int64_t baseD = (row0 * rowH + h) * DH, baseN = (row0 * rowH + h) * NS;
+    const uint32_t rsD = (uint32_t)(rowH * DH), rsN = (uint32_t)(rowH * NS);
     // ------------------------------------------------ A: stage (all loads first)
     f32x4_t hin[K::NBW];
     // pipelined mode: register operand fragments (see BwdSmem)
@@ -228,19 +232,18 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
 #pragma unroll
         for (int v = 0; v < UV; ++v) {
           const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
-          uv[v] = *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0);
+          uv[v] = rr::ld32<u16x8_t>(p.u + baseD, tl * rsD + d0);
         }
 #pragma unroll
         for (int v = 0; v < BV; ++v) {
           const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
-          const int64_t g = ((row0 + tl) * rowH + h) * NS + n0;
-          bv[v] = *reinterpret_cast<const u16x8_t*>(p.Bm + g);
-          cv[v] = *reinterpret_cast<const u16x8_t*>(p.Cm + g);
+          bv[v] = rr::ld32<u16x8_t>(p.Bm + baseN, tl * rsN + n0);
+          cv[v] = rr::ld32<u16x8_t>(p.Cm + baseN, tl * rsN + n0);
         }
 #pragma unroll
         for (int v = 0; v < GV; ++v) {
           const int i = tid + 256 * v, tl = (i / (DH / 4)) & (Q - 1), d0 = 4 * (i % (DH / 4));
-          gv[v] = *reinterpret_cast<const float4*>(p.dy + ((row0 + tl) * rowH + h) * DH + d0);
+          gv[v] = rr::ld32<float4>(p.dy + baseD, tl * rsD + d0);
         }
         dv = bf_val(p.delta[(row0 + (lane & (Q - 1))) * rowH + h]);   // lanes >= 32 masked at use
         // the entering state (checkpoint slot c - 1, or h0; none: zero, read
@@ -513,7 +516,7 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
       // join waits for the loads.
       const int d = 16 * (w & (NBD - 1)) + (lane & 15), l4 = lane >> 4;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pdy[e] = p.dy[((row0 + 8 * l4 + e) * rowH + h) * DH + d];
+      for (int e = 0; e < 8; ++e) pdy[e] = rr::ld32<float>(p.dy + baseD, (8 * l4 + e) * rsD + d);
 #pragma unroll
       for (int kk = 0; kk < NS / 16; ++kk) {
         const float* src = SUM ? &m.LS[d][16 * kk + 4 * l4] : lsrc + d * NS + 16 * kk + 4 * l4;
@@ -604,7 +607,7 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int t = 16 * tb + 4 * l4 + r;
-            rr::st_bf16(p.du, ((row0 + t) * rowH + h) * DH + d, m.del[t] * (a1[r] + m.m31[t] * a2[r]));
+            rr::st_bf16_u32(p.du + baseD, t * rsD + d, m.del[t] * (a1[r] + m.m31[t] * a2[r]));
           }
         }
       }
@@ -632,19 +635,19 @@ __global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ss
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = 16 * tb + 4 * (lane >> 4) + r;
-          const int64_t gi = ((row0 + t) * rowH + h) * NS + col;
+          const uint32_t gi = t * rsN + col;
           float s1, s2;
           if (kind == 0) {
             const float bv = bf_val(m.Bn[t][col]), ul = m.UL[t][col], dt = m.del[t];
             const float z = acc[r] + m.m31[t] * ul;
-            rr::st_bf16(p.dB, gi, dt * z);
+            rr::st_bf16_u32(p.dB + baseN, gi, dt * z);
             s1 = bv * z;
             s2 = ul * bv;
             da += bv * (m.m31[t] * dt * (cd31 - m.cd[t] + dt) * ul - dt * dt * z);
           } else {
             const float cv = bf_val(m.Cn[t][col]), gh = m.GH[t][col];
             const float dc = m.gam[t] * gh + acc[r];
-            rr::st_bf16(p.dC, gi, dc);
+            rr::st_bf16_u32(p.dC + baseN, gi, dc);
             s1 = gh * cv;
             s2 = 0.f;
             da += cv * (akb[r] + m.gam[t] * m.cd[t] * gh);
