@@ -467,8 +467,8 @@ def measure(name, steps, warmup, dtype, device, with_cpu):
         nthreads = 1
         t_cpu = []
         w["cpu"]()  # warm
-        deadline = time.perf_counter() + 12.0
-        while len(t_cpu) < 9 and (len(t_cpu) < 3 or time.perf_counter() < deadline):
+        # about 10 s of CPU work (at least 3 runs): the bounded sample
+        while len(t_cpu) < 3 or (sum(t_cpu) < 10.0 and len(t_cpu) < 400):
             c0 = time.perf_counter()
             w["cpu"]()
             t_cpu.append(time.perf_counter() - c0)
@@ -477,7 +477,8 @@ def measure(name, steps, warmup, dtype, device, with_cpu):
         ctok = w.get("cpu_tokens", w["tokens"])
         res["cpu"] = dict(value=ctok / med, unit="tokens/s", cores=nthreads, kind="port",
                           sample=f"float64 oracle forward + explicit adjoint over {ctok} tokens of the "
-                                 f"workload, median of {len(t_cpu)} runs ({med:.2f} s each)")
+                                 f"workload, median of {len(t_cpu)} runs ({med:.2f} s each, "
+                                 f"{sum(t_cpu):.1f} s in all)")
     return res
 
 
