@@ -1123,19 +1123,27 @@ __global__ __launch_bounds__(256, (kFwdWgs<DH, NS, MODE, GLA>)) void fwd_kernel(
   constexpr int UV = (Q * DH / 8 + 255) / 256, BV = (Q * NS / 8 + 255) / 256;
   u16x8_t uv[UV], bv[BV], cv[BV];
   float xv;
+  // (direct mode, where the loads are issued during the sum and consumed
+  // after it: every load unconditional and in bounds, threads past the
+  // chunk's pieces repeating one (the LDS writes below skip them), since a
+  // load under a branch makes the branch's join wait for all loads in flight;
+  // the other modes consume them at once and skip the surplus loads)
   auto issue = [&](int c, int tid) {
     const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;
 #pragma unroll
     for (int v = 0; v < UV; ++v) {
       const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
-      uv[v] = i < Q * DH / 8 ? *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0) : u16x8_t{};
+      uv[v] = MODE == kDirect || i < Q * DH / 8
+                  ? *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + tl) * rowH + h) * DH + d0)
+                  : u16x8_t{};
     }
 #pragma unroll
     for (int v = 0; v < BV; ++v) {
       const int i = tid + 256 * v, tl = (i / (NS / 8)) & (Q - 1), n0 = 8 * (i % (NS / 8));
       const int64_t g = ((row0 + tl) * rowH + h) * NS + n0;
-      bv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Bm + g) : u16x8_t{};
-      cv[v] = i < Q * NS / 8 ? *reinterpret_cast<const u16x8_t*>(p.Cm + g) : u16x8_t{};
+      const bool ld = MODE == kDirect || i < Q * NS / 8;
+      bv[v] = ld ? *reinterpret_cast<const u16x8_t*>(p.Bm + g) : u16x8_t{};
+      cv[v] = ld ? *reinterpret_cast<const u16x8_t*>(p.Cm + g) : u16x8_t{};
     }
     // unconditional (in-bounds) load, so no branch waits on it
     xv = bf_val(p.delta[(row0 + (tid & (Q - 1))) * rowH + h]);
@@ -1211,6 +1219,8 @@ __global__ __launch_bounds__(256, (kFwdWgs<DH, NS, MODE, GLA>)) void fwd_kernel(
     const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;  // first (b, t) row of the chunk
     // ---- stage the chunk's inputs
     {
+      // (whole head: issuing the next chunk's loads here instead, during this
+      // chunk, measured slower: B96 forward 95 -> 108 us)
       if constexpr (MODE != kDirect) issue(c, tid);
 #pragma unroll
       for (int v = 0; v < UV; ++v) {
