@@ -298,6 +298,7 @@ GLA_CASES = [
     (2, 512, 4, 32, 32, BF16, "cfg", True, True, 32),       # direct mode, 16 chunks, Dh = 32
     (1, 480, 2, 64, 32, BF16, "zeros", True, True, 33),     # direct mode, 15 chunks, zero gates
     (5, 512, 12, 64, 32, BF16, "cfg", False, True, 34),     # 960 workgroups: pipelined
+    (4, 512, 12, 64, 32, BF16, "cfg", True, False, 35),     # 768 workgroups: direct, the largest
 ]
 
 
