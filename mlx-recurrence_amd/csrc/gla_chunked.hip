@@ -35,15 +35,21 @@ bool gla2_supported(int dtype, int64_t B, int64_t L, int64_t H, int64_t seg, int
 // kernels it saves).
 constexpr int64_t kGlaDirectMaxChunks = 4;
 constexpr int64_t kGlaDirectMaxWorkgroups = 3 * 256;
+// The forward with enough heads to fill the GPU runs whole heads (the state
+// in registers from chunk to chunk: no aggregates, no state pass, no
+// checkpoint re-read).
+constexpr int64_t kGlaWholeMinHeads = 512;
 
-int gla2_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh) {
+int gla2_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass) {
+  if (pass == 0 && B * H >= kGlaWholeMinHeads) return chunked::kWhole;
   if (Dh * Dh > chunked::kDirectMaxState) return chunked::kPipe;
   if (nC <= kGlaDirectMaxChunks) return chunked::kDirect;
   return nC <= chunked::kDirectMaxChunks && B * H * nC <= kGlaDirectMaxWorkgroups ? chunked::kDirect : chunked::kPipe;
 }
 
 size_t gla2_ws_bytes(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass) {
-  if (gla2_mode(B, H, nC, Dh) == chunked::kDirect) return 0;
+  const int mode = gla2_mode(B, H, nC, Dh, pass);
+  if (mode == chunked::kDirect || mode == chunked::kWhole) return 0;
   int64_t f = align64(B * H * nC);
   if (pass == 1) f += align64(B * H * nC * Dh * Dh);
   return (size_t)f * sizeof(float);
@@ -52,7 +58,7 @@ size_t gla2_ws_bytes(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass) {
 void gla2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass) {
   float* f = static_cast<float*>(ws);
   a.ws = a.tot = a.agg = nullptr;
-  if (a.mode == chunked::kDirect) return;
+  if (a.mode == chunked::kDirect || a.mode == chunked::kWhole) return;
   a.tot = f;
   f += align64(B * a.H * a.nC);
   a.agg = pass == 1 ? f : nullptr;

@@ -67,7 +67,7 @@ int ssd2_bwd(const ChunkArgs& p, int64_t B, hipStream_t s);
 // chunk below 2^31 (direct or pipelined mode; the whole-head mode is not
 // used for GLA).
 bool gla2_supported(int dtype, int64_t B, int64_t L, int64_t H, int64_t seg, int64_t Dh, int pass);
-int gla2_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh);
+int gla2_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass);
 // Workspace of the pipelined mode: chunk decays [B,H,nC] (both passes) and
 // the backward chunk adjoints [B,H,nC,Dh,Dh] (pass 1); none in direct mode.
 size_t gla2_ws_bytes(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass);

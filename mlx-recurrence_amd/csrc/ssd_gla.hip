@@ -701,7 +701,7 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
 namespace {
 // Chunked-kernel arguments of a GLA call (u = v, delta = gates, Bm = k, Cm = q).
 rr::ChunkArgs gla2_args(const void* qp, const void* kp, const void* vp, const void* gates, int64_t B,
-                        int64_t L, int64_t H, int64_t Dh, const float* h0) {
+                        int64_t L, int64_t H, int64_t Dh, const float* h0, int pass) {
   rr::ChunkArgs a{};
   a.B = (int)B;
   a.u = static_cast<const uint16_t*>(vp);
@@ -710,8 +710,8 @@ rr::ChunkArgs gla2_args(const void* qp, const void* kp, const void* vp, const vo
   a.Cm = static_cast<const uint16_t*>(qp);
   a.h0 = h0;
   a.L = (int)L; a.H = (int)H; a.DH = (int)Dh; a.NS = (int)Dh; a.nC = (int)(L / 32);
-  a.mode = rr::gla2_mode(B, H, a.nC, Dh);
-  a.R = 1;
+  a.mode = rr::gla2_mode(B, H, a.nC, Dh, pass);
+  a.R = a.mode == 0 ? a.nC : 1;   // whole-head mode (0): one run of nC chunks
   return a;
 }
 }  // namespace
@@ -733,7 +733,7 @@ extern "C" int rr_gla_fwd(const void* qp, const void* kp, const void* vp, const 
     return rr::fail(RR_EINVAL, "gla_fwd: null pointer argument");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (rr::gla2_supported(dtype, B, L, H, seg, Dh, 0)) {
-    rr::ChunkArgs a = gla2_args(qp, kp, vp, gates, B, L, H, Dh, h0);
+    rr::ChunkArgs a = gla2_args(qp, kp, vp, gates, B, L, H, Dh, h0, 0);
     a.y = y;
     a.ckpt = ckpt;
     const size_t need = rr::gla2_ws_bytes(B, H, a.nC, Dh, 0);
@@ -770,7 +770,7 @@ extern "C" int rr_gla_bwd(const float* dy, const float* dfinal, const void* qp, 
   if (!dy || !qp || !kp || !vp || !gates || !ckpt || !dq || !dk || !dv || !dgates)
     return rr::fail(RR_EINVAL, "gla_bwd: null pointer argument");
   if (rr::gla2_supported(dtype, B, L, H, seg, Dh, 1)) {
-    rr::ChunkArgs a = gla2_args(qp, kp, vp, gates, B, L, H, Dh, h0);
+    rr::ChunkArgs a = gla2_args(qp, kp, vp, gates, B, L, H, Dh, h0, 1);
     a.ckpt = const_cast<float*>(ckpt);
     a.dy = dy;
     a.dfinal = dfinal;

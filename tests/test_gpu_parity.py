@@ -299,6 +299,8 @@ GLA_CASES = [
     (1, 480, 2, 64, 32, BF16, "zeros", True, True, 33),     # direct mode, 15 chunks, zero gates
     (5, 512, 12, 64, 32, BF16, "cfg", False, True, 34),     # 960 workgroups: pipelined
     (4, 512, 12, 64, 32, BF16, "cfg", True, False, 35),     # 768 workgroups: direct, the largest
+    (1, 160, 512, 64, 32, BF16, "signed", True, True, 36),  # B*H >= 512: whole-head forward
+    (2, 64, 256, 32, 32, BF16, "zeros", True, True, 37),    # whole-head forward, Dh = 32
 ]
 
 
