@@ -64,12 +64,13 @@ int ssd2_bwd(const ChunkArgs& p, int64_t B, hipStream_t s);
 // True when the chunked GLA kernels cover this call (pass 0 forward, 1
 // backward): bf16 inputs, checkpoint interval 32, Dh in {32, 64, 128}
 // (forward) or {32, 64} (backward), and a 1-D grid of one workgroup per
-// chunk below 2^31 (direct or pipelined mode; the whole-head mode is not
-// used for GLA).
+// chunk below 2^31 (the backward's direct or pipelined mode; the forward
+// runs whole heads when B * H >= 512).
 bool gla2_supported(int dtype, int64_t B, int64_t L, int64_t H, int64_t seg, int64_t Dh, int pass);
 int gla2_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass);
 // Workspace of the pipelined mode: chunk decays [B,H,nC] (both passes) and
-// the backward chunk adjoints [B,H,nC,Dh,Dh] (pass 1); none in direct mode.
+// the backward chunk adjoints [B,H,nC,Dh,Dh] (pass 1); none in the direct and
+// whole-head modes.
 size_t gla2_ws_bytes(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass);
 void gla2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass);
 int gla2_fwd(const ChunkArgs& p, int64_t B, hipStream_t s);
