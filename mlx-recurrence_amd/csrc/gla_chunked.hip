@@ -35,13 +35,16 @@ bool gla2_supported(int dtype, int64_t B, int64_t L, int64_t H, int64_t seg, int
 // kernels it saves).
 constexpr int64_t kGlaDirectMaxChunks = 4;
 constexpr int64_t kGlaDirectMaxWorkgroups = 3 * 256;
-// The forward with enough heads to fill the GPU runs whole heads (the state
-// in registers from chunk to chunk: no aggregates, no state pass, no
-// checkpoint re-read).
+// With enough heads to fill the GPU, whole heads: the forward always (the
+// state in registers from chunk to chunk: no aggregates, no state pass, no
+// checkpoint re-read; B96 L512 H12: 238 -> 175 us), the backward for short
+// heads (the adjoint carried likewise, no adjoint scan or workspace: 383 ->
+// 365 us; long heads serialise too many chunks per workgroup).
 constexpr int64_t kGlaWholeMinHeads = 512;
+constexpr int64_t kGlaWholeBwdMaxChunks = 16;
 
 int gla2_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass) {
-  if (pass == 0 && B * H >= kGlaWholeMinHeads) return chunked::kWhole;
+  if (B * H >= kGlaWholeMinHeads && (pass == 0 || nC <= kGlaWholeBwdMaxChunks)) return chunked::kWhole;
   if (Dh * Dh > chunked::kDirectMaxState) return chunked::kPipe;
   if (nC <= kGlaDirectMaxChunks) return chunked::kDirect;
   return nC <= chunked::kDirectMaxChunks && B * H * nC <= kGlaDirectMaxWorkgroups ? chunked::kDirect : chunked::kPipe;

@@ -64,8 +64,8 @@ int ssd2_bwd(const ChunkArgs& p, int64_t B, hipStream_t s);
 // True when the chunked GLA kernels cover this call (pass 0 forward, 1
 // backward): bf16 inputs, checkpoint interval 32, Dh in {32, 64, 128}
 // (forward) or {32, 64} (backward), and a 1-D grid of one workgroup per
-// chunk below 2^31 (the backward's direct or pipelined mode; the forward
-// runs whole heads when B * H >= 512).
+// chunk below 2^31 (direct or pipelined modes; whole heads run with
+// B * H >= 512: the forward always, the backward up to 16 chunks).
 bool gla2_supported(int dtype, int64_t B, int64_t L, int64_t H, int64_t seg, int64_t Dh, int pass);
 int gla2_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass);
 // Workspace of the pipelined mode: chunk decays [B,H,nC] (both passes) and
