@@ -301,6 +301,7 @@ GLA_CASES = [
     (4, 512, 12, 64, 32, BF16, "cfg", True, False, 35),     # 768 workgroups: direct, the largest
     (1, 160, 512, 64, 32, BF16, "signed", True, True, 36),  # B*H >= 512: whole-head forward
     (2, 64, 256, 32, 32, BF16, "zeros", True, True, 37),    # whole-head forward, Dh = 32
+    (1, 32, 512, 128, 32, BF16, "cfg", True, True, 38),     # whole-head forward, Dh = 128 (VALU backward)
 ]
 
 
