@@ -97,12 +97,13 @@ namespace {
 // B2 (y).  The pipelined mode (CARRY false) takes dY^T, lam and the h_in / lam
 // columns as register fragments straight from global memory instead of the
 // transposed LDS copies (GYT, LM, LMT, HT), which keeps its LDS small enough
-// for three workgroups per CU.
+// for four workgroups per CU (N = 16; three with the sum mode's LS).  Arrays a
+// mode does not use have no rows.
 template <int DH, int NS, bool CARRY, bool SUM>
 struct BwdSmem {
   static constexpr int PD = DH + 8, PN = NS + 8;
-  static constexpr int TD = CARRY ? DH : 1, TN = CARRY ? NS : 1;
-  float LS[SUM ? DH : 1][NS + 4];  // kSum: the summed lam [d][n], read back as register fragments
+  static constexpr int TD = CARRY ? DH : 0, TN = CARRY ? NS : 0;
+  float LS[SUM ? DH : 0][NS + 4];  // kSum: the summed lam [d][n], read back as register fragments
   uint16_t Bn[Q][PN];
   uint16_t Cn[Q][PN];
   uint16_t BT[NS][PQ];
@@ -125,11 +126,11 @@ struct BwdSmem {
       uint16_t Km_hi[Q][PQ], Km_lo[Q][PQ];
     } y;
   };
-  float CB[Q][Q + 1];              // phase B1 -> B2
-  float G2[Q][Q + 1];
+  float CB[Q][Q];                  // phase B1 -> B2 (rows read whole: unpadded)
+  float G2[Q][Q];
   // (gam o C)^T, for the adjoint carried to the previous chunk (whole-head
   // mode; chunk 0 of the direct mode for the initial-state gradient)
-  uint16_t CgT_hi[CARRY ? NS : 1][PQ], CgT_lo[CARRY ? NS : 1][PQ];
+  uint16_t CgT_hi[CARRY ? NS : 0][PQ], CgT_lo[CARRY ? NS : 0][PQ];
   float del[Q], cd[Q], gam[Q], m31[Q];
   float Rp[4][Q];                  // per-wave partials of R_t (phase B2)
   float Xs[NS / 16][Q], Ys[NS / 16][Q], BZs[NS / 16][Q];   // row sums over one 16-column block
@@ -151,8 +152,15 @@ union BwdShared<DH, NS, kSum> {
 // One chunk per workgroup with lam from the workspace (kPipe, pass_kernel) or
 // summed over the later chunks' inputs in the kernel (kSum, direct_sum); or a
 // whole head per workgroup, lam carried backwards in registers (kWhole).
+// Workgroups per CU: the pipelined mode as many as its LDS allows (up to 4),
+// the sum mode 3, the whole-head mode 2.
 template <int DH, int NS, int MODE>
-__global__ __launch_bounds__(256, MODE == kPipe || MODE == kSum ? 3 : 2) void ssd2_bwd_kernel(rr::ChunkArgs p) {
+constexpr int kBwdWgs = MODE == kPipe  ? (160 * 1024 / sizeof(BwdShared<DH, NS, MODE>) >= 4 ? 4 : 3)
+                        : MODE == kSum ? 3
+                                       : 2;
+
+template <int DH, int NS, int MODE>
+__global__ __launch_bounds__(256, (kBwdWgs<DH, NS, MODE>)) void ssd2_bwd_kernel(rr::ChunkArgs p) {
   using K = Cfg<DH, NS>;
   // PIPE: one chunk per workgroup with lam from the workspace (kPipe) or summed
   // in the kernel (kSum, SUM); the operands of du and of GH / UL are register
