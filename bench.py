@@ -287,6 +287,63 @@ def make_rglru(cfg, device, dtype):
                 io_bytes=n * 4 + 2 * n * es)
 
 
+def make_rglru_gated(cfg, device, dtype):
+    """BASELINE config 3 shape, RG-LRU with the gate math in the kernels:
+    x ~ N(0,1); r ~ N(0,1) (pre-activation); i = sigmoid(N(0,1)); lam chosen so
+    that exp(-softplus(lam)) = U(0.9, 0.999), i.e. a_t = U^(8 sigmoid(r_t)) as in
+    the config; the kernels read (r, i, x, lam) and form a_t, x'_t themselves."""
+    import torch
+    from mlx_recurrence_amd import _lib
+    B, L, D, seg = cfg["B"], cfg["L"], cfg["D"], cfg["seg"]
+    g = torch.Generator().manual_seed(cfg.get("seed", 3))
+    x = _gen((B, L, D), g)
+    r = _gen((B, L, D), g)
+    i = torch.sigmoid(_gen((B, L, D), g))
+    base = _gen((D,), g, "uniform") * 0.099 + 0.9
+    lam = torch.log(torch.expm1(-torch.log(base)))
+    dy = _gen((B, L, D), g)
+    d = dict(r=r.to(dtype).to(device), i=i.to(dtype).to(device), x=x.to(dtype).to(device),
+             lam=lam.to(device), dy=dy.to(device))
+    T = _lib.chunk_len(L, seg)
+    nC = L // T
+    f32 = torch.float32
+    out = dict(y=torch.empty((B, L, D), dtype=f32, device=device),
+               ckpt=torch.empty((B, nC, D), dtype=f32, device=device),
+               dr=torch.empty((B, L, D), dtype=dtype, device=device),
+               di=torch.empty((B, L, D), dtype=dtype, device=device),
+               dx=torch.empty((B, L, D), dtype=dtype, device=device),
+               dlam=torch.empty((D,), dtype=f32, device=device),
+               wsf=_lib.rglru_gated_workspace(B, L, D, seg, dtype, 0, device),
+               wsb=_lib.rglru_gated_workspace(B, L, D, seg, dtype, 1, device))
+    es = torch.tensor([], dtype=dtype).element_size()
+    n, n_ck = B * L * D, B * nC * D
+    fwd_bytes = 3 * n * es + n * 4 + n_ck * 4
+    bwd_bytes = n * 4 + n_ck * 4 + 3 * n * es + 3 * n * es
+
+    def fwd():
+        _lib.rglru_gated_fwd(d["r"], d["i"], d["x"], d["lam"], 8.0, None, seg, out["y"], out["ckpt"], out["wsf"])
+
+    def bwd():
+        _lib.rglru_gated_bwd(d["dy"], None, d["r"], d["i"], d["x"], d["lam"], 8.0, None, out["ckpt"], seg,
+                             out["dr"], out["di"], out["dx"], out["dlam"], None, out["wsb"])
+
+    def eager():
+        import mlx_recurrence_amd as mr
+        xs = [d[kk].detach().requires_grad_(True) for kk in ("r", "i", "x", "lam")]
+        mr.rglru_gated_scan(*xs, 8.0, seg=seg).backward(d["dy"])
+
+    def cpu_sample():
+        from oracle import recurrence_oracle as orc
+        xs = [d[kk][:1].double().cpu().numpy() for kk in ("r", "i", "x")]
+        lm = d["lam"].double().cpu().numpy()
+        orc.rglru_gated_forward(*xs, lm)
+        orc.rglru_gated_backward(d["dy"][:1].double().cpu().numpy(), *xs, lm)
+
+    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, tokens=B * L, cpu_tokens=L,
+                fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=n * 4, ckpt_bytes=n_ck * 4,
+                io_bytes=n * 4 + 3 * n * es)
+
+
 def make_rotlru(cfg, device, dtype):
     """BASELINE config 3 (rotLRU): a = sigmoid(N(2,1)) [B,L,Dp];
     theta = U(-pi, pi) * 0.1; cs, sn = cos, sin; x ~ N(0,1) [B,L,2Dp]."""
@@ -347,6 +404,8 @@ WORKLOADS = {
     "gla": ("gla_scan fwd+bwd (BASELINE config 2)", make_gla, dict(B=3, L=512, H=12, Dh=64, seg=32)),
     "rglru": ("rglru_scan fwd+bwd (BASELINE config 3)", make_rglru, dict(B=8, L=4096, D=2560, seg=32)),
     "rotlru": ("rotlru_scan fwd+bwd (BASELINE config 3)", make_rotlru, dict(B=8, L=4096, D=2560, seg=32)),
+    "rglru_gated": ("rglru_gated_scan fwd+bwd, gate math in the kernels (BASELINE config 3 shape)",
+                    make_rglru_gated, dict(B=8, L=4096, D=2560, seg=32)),
     "ssd_c4": ("ssd_scan fwd+bwd (BASELINE config 4)", make_ssd,
                dict(B=8, L=4096, H=80, Dh=64, N=128, seg=32)),
     # configs 1 and 2 with 32x the batch: the same kernels with the GPU filled

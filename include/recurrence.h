@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define RR_ABI_VERSION 4
+#define RR_ABI_VERSION 5
 
 enum rr_dtype { RR_F32 = 0, RR_BF16 = 1, RR_F16 = 2 };
 
@@ -145,6 +145,35 @@ int rr_rglru_bwd(const float* dy, const float* dfinal, const void* a, const void
                  int dtype, int64_t B, int64_t L, int64_t D, int64_t seg, const float* h0,
                  const float* ckpt, void* da, void* dx, float* dh0, void* workspace,
                  size_t workspace_bytes, void* stream);
+
+/* --------------------------------------------------------- RG-LRU, gated --
+ * The RG-LRU gate math fused into the scan.  The reference computes it in MLX
+ * host code before its scan kernel (mlx_recurrence/rglru.py:10-27); here the
+ * kernels read the raw gates, so a(t) and x'(t) never travel through HBM.
+ * Per channel d and step t:
+ *   a_t = exp(-c * softplus(lam[d]) * sigmoid(r_t)),
+ *   x'_t = sqrt(1 - a_t^2) * (i_t * x_t),   h_t = a_t h_{t-1} + x'_t,  y_t = h_t.
+ * r, i, x [B,L,D] (dtype); lam [D] fp32; c > 0 (Griffin uses 8).  y, ckpt,
+ * h0, dfinal, dh0 as for rr_rglru_*.  Gradients dr, di, dx [B,L,D] (dtype)
+ * and dlam [D] fp32 (summed over batch and steps, in a fixed order).
+ */
+
+/* Workspace bytes needed by rr_rglru_gated_fwd (pass=0) or _bwd (pass=1). */
+size_t rr_rglru_gated_workspace_bytes(int64_t B, int64_t L, int64_t D, int64_t seg, int dtype, int pass);
+
+/* Replaces the gate math of rglru.py:13-14 (MLX host ops) followed by
+ * _rglru_forward_kernel (rglru.py:64-123). */
+int rr_rglru_gated_fwd(const void* r, const void* i, const void* x, const float* lam, float c,
+                       int dtype, int64_t B, int64_t L, int64_t D, int64_t seg, const float* h0,
+                       float* y, float* ckpt, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Replaces _rglru_backward_kernel (rglru.py:130-203) followed by MLX's
+ * autodiff of the gate math of rglru.py:13-14. */
+int rr_rglru_gated_bwd(const float* dy, const float* dfinal, const void* r, const void* i,
+                       const void* x, const float* lam, float c, int dtype, int64_t B, int64_t L,
+                       int64_t D, int64_t seg, const float* h0, const float* ckpt, void* dr,
+                       void* di, void* dx, float* dlam, float* dh0, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 /* --------------------------------------------------------------- rotLRU --
  * a, cs, sn [B,L,Dp]; x [B,L,2*Dp] with (u,w) pairs interleaved (dtype).

@@ -26,9 +26,13 @@ using rr::tiles::pack_fill;
 
 // Tile shapes (measured on MI355X at BASELINE config 3): CH = 2 channels per
 // lane; U steps per wave: forward 16 for 16-bit inputs, otherwise 8 (the
-// backward also holds dy and the recomputed states); NW = 8 waves, two
-// workgroups per CU.
-template <typename InT, bool BWD> constexpr int steps_per_wave() { return sizeof(InT) == 4 || BWD ? 8 : 16; }
+// backward also holds dy and the recomputed states; the gated passes hold
+// the gates in fp32, the gated backward 4 steps); NW = 8 waves, two
+// workgroups per CU.  A tile's NW * U steps are a multiple of 32, so it holds
+// whole checkpoint intervals.
+template <typename InT, bool BWD, bool GATED> constexpr int steps_per_wave() {
+  return BWD && GATED ? 4 : sizeof(InT) == 4 || BWD || GATED ? 8 : 16;
+}
 constexpr int kNW = 8;
 constexpr int kFwdCh = 2, kBwdCh = 2;
 
@@ -37,17 +41,75 @@ struct TileGrid {
   int K;   // step tiles
   int64_t tiles() const { return (int64_t)G * K; }
 };
-inline int steps_per_wave(int dtype, int pass) { return dtype == RR_F32 || pass == 1 ? 8 : 16; }
-inline TileGrid tile_grid(int64_t L, int64_t D, int ch, int dtype, int pass) {
-  const int64_t S = (int64_t)steps_per_wave(dtype, pass) * kNW;
+inline int steps_per_wave(int dtype, int pass, bool gated) {
+  return pass == 1 && gated ? 4 : dtype == RR_F32 || pass == 1 || gated ? 8 : 16;
+}
+inline TileGrid tile_grid(int64_t L, int64_t D, int ch, int dtype, int pass, bool gated = false) {
+  const int64_t S = (int64_t)steps_per_wave(dtype, pass, gated) * kNW;
   return TileGrid{(int)((D + 64 * ch - 1) / (64 * ch)), (int)((L + S - 1) / S)};
 }
 
-template <typename InT, int CH, int U>
+// Gated RG-LRU (the Griffin gate math of reference rglru.py:13-14, which the
+// reference computes in MLX before its scan kernel): with c' = c softplus(lam)
+// per channel, a = exp(-c' sigmoid(r)) and x' = sqrt(1 - a^2) (i x).  The
+// per-element math uses the hardware exp / reciprocal / square root (about
+// 1 ulp each; the correctly rounded library forms made the passes VALU-bound),
+// and 1 - a^2 = -expm1(2z), z = -c' sigmoid(r), takes its Taylor series
+// through z^5 where 1 - a^2 would cancel (2z > -1/8; truncation < 1e-7
+// relative), so s = sqrt(1 - a^2) keeps its relative accuracy as a -> 1.
+__device__ __forceinline__ float softplus_f(float v) { return v > 20.f ? v : log1pf(expf(v)); }
+__device__ __forceinline__ float sigmoid_f(float v) { return __builtin_amdgcn_rcpf(1.f + __expf(-v)); }
+__device__ __forceinline__ void gate(float r, float csp, float& a, float& s) {
+  const float z = -csp * sigmoid_f(r);
+  a = __expf(z);
+  const float t = 2.f * z;
+  const float om = t > -0.125f ? -t * (1.f + t * (0.5f + t * (1.f / 6 + t * (1.f / 24 + t * (1.f / 120)))))
+                               : 1.f - a * a;
+  s = __builtin_amdgcn_sqrtf(om);
+}
+
+// Loads a wave's U steps of the scan inputs.  Plain: pa = a, px = x.  Gated:
+// pa = r, px = x, pi = i, and the fp32 gates av = a, sv = sqrt(1 - a^2).
+// Steps past L or D are identity steps (a = 1, x' = 0).
+template <typename InT, int CH, int U, bool GATED>
+__device__ __forceinline__ void load_steps(const InT* a, const InT* x, const InT* gi, const float (&csp)[CH],
+                                           bool cok, int t0, int L, int64_t row0, int D, int ch,
+                                           Pack<InT, CH> (&pa)[U], Pack<InT, CH> (&px)[U],
+                                           Pack<InT, CH> (&pi)[GATED ? U : 1], float (&av)[GATED ? U : 1][CH],
+                                           float (&sv)[GATED ? U : 1][CH]) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int t = t0 + u;
+    if (cok && t < L) {
+      const int64_t i = (row0 + t) * D + ch;
+      pa[u] = ld_pack<InT, CH>(a, i);
+      px[u] = ld_pack<InT, CH>(x, i);
+      if constexpr (GATED) pi[u] = ld_pack<InT, CH>(gi, i);
+    } else {   // identity step
+      pa[u] = pack_fill<InT, CH>(1.f);
+      px[u] = pack_fill<InT, CH>(0.f);
+      if constexpr (GATED) pi[u] = pack_fill<InT, CH>(0.f);
+    }
+  }
+  if constexpr (GATED) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool ok = cok && t0 + u < L;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        gate(pa[u][c], csp[c], av[u][c], sv[u][c]);
+        if (!ok) av[u][c] = 1.f, sv[u][c] = 0.f;
+      }
+    }
+  }
+}
+
+template <typename InT, int CH, int U, bool GATED>
 __global__ __launch_bounds__(64 * kNW, 4) void rglru_fwd_kernel(
-    const InT* __restrict__ a, const InT* __restrict__ x, const float* __restrict__ h0,
-    float* __restrict__ y, float* __restrict__ ckpt, uint32_t* counter, uint64_t* slots, int B, int L,
-    int D, int T, int nC, int G, int K) {
+    const InT* __restrict__ a, const InT* __restrict__ x, const InT* __restrict__ gi,
+    const float* __restrict__ glam, float gc, const float* __restrict__ h0, float* __restrict__ y,
+    float* __restrict__ ckpt, uint32_t* counter, uint64_t* slots, int B, int L, int D, int T, int nC, int G,
+    int K) {
   constexpr int GCH = 64 * CH, S = U * kNW;
   __shared__ float sP[kNW][GCH], sE[kNW][GCH];
   __shared__ float sIn[GCH];
@@ -65,19 +127,21 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_fwd_kernel(
   const int t0 = k * S + w * U;
   const int64_t row0 = (int64_t)b * L;
 
-  Pack<InT, CH> pa[U], px[U];
+  float csp[CH];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int t = t0 + u;
-    if (cok && t < L) {
-      const int64_t i = (row0 + t) * D + ch;
-      pa[u] = ld_pack<InT, CH>(a, i);
-      px[u] = ld_pack<InT, CH>(x, i);
-    } else {   // identity step
-      pa[u] = pack_fill<InT, CH>(1.f);
-      px[u] = pack_fill<InT, CH>(0.f);
-    }
-  }
+  for (int c = 0; c < CH; ++c) csp[c] = GATED && cok ? gc * softplus_f(glam[ch + c]) : 0.f;
+  Pack<InT, CH> pa[U], px[U], pi[GATED ? U : 1];
+  float av[GATED ? U : 1][CH], sv[GATED ? U : 1][CH];
+  load_steps<InT, CH, U, GATED>(a, x, gi, csp, cok, t0, L, row0, D, ch, pa, px, pi, av, sv);
+  // the step's decay and input
+  auto A = [&](int u, int c) -> float {
+    if constexpr (GATED) return av[u][c];
+    else return pa[u][c];
+  };
+  auto X = [&](int u, int c) -> float {
+    if constexpr (GATED) return sv[u][c] * (pi[u][c] * px[u][c]);
+    else return px[u][c];
+  };
   float P[CH], E[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
@@ -85,8 +149,8 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_fwd_kernel(
     E[c] = 0.f;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      E[c] = pa[u][c] * E[c] + px[u][c];
-      P[c] *= pa[u][c];
+      E[c] = A(u, c) * E[c] + X(u, c);
+      P[c] *= A(u, c);
     }
     sP[w][lane * CH + c] = P[c];
     sE[w][lane * CH + c] = E[c];
@@ -119,7 +183,7 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_fwd_kernel(
   for (int u = 0; u < U; ++u) {
     const int t = t0 + u;
 #pragma unroll
-    for (int c = 0; c < CH; ++c) h[c] = pa[u][c] * h[c] + px[u][c];   // rglru.py:92
+    for (int c = 0; c < CH; ++c) h[c] = A(u, c) * h[c] + X(u, c);   // rglru.py:92
     if (cok && t < L) {
       rr::tiles::st_f32<CH>(y, (row0 + t) * D + ch, h);
       if ((t + 1) % T == 0) rr::tiles::st_f32<CH>(ckpt, ((int64_t)b * nC + (t + 1) / T - 1) * D + ch, h);
@@ -127,14 +191,19 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_fwd_kernel(
   }
 }
 
-template <typename InT, int CH, int U>
+// Backward.  Plain: da, dx.  Gated: da receives dr, dx dx, dgi di, and dpart
+// the tile's sums over its steps of dz * sigmoid(r) per channel (z = log a),
+// row b * K + k of a [B * K, D] array that rglru_dlam_kernel reduces.
+template <typename InT, int CH, int U, bool GATED>
 __global__ __launch_bounds__(64 * kNW, 4) void rglru_bwd_kernel(
     const float* __restrict__ dy, const float* __restrict__ dfinal, const InT* __restrict__ a,
-    const InT* __restrict__ x, const float* __restrict__ h0, const float* __restrict__ ckpt,
-    InT* __restrict__ da, InT* __restrict__ dx, float* __restrict__ dh0, uint32_t* counter,
+    const InT* __restrict__ x, const InT* __restrict__ gi, const float* __restrict__ glam, float gc,
+    const float* __restrict__ h0, const float* __restrict__ ckpt, InT* __restrict__ da, InT* __restrict__ dx,
+    InT* __restrict__ dgi, float* __restrict__ dpart, float* __restrict__ dh0, uint32_t* counter,
     uint64_t* slots, int B, int L, int D, int T, int nC, int G, int K) {
   constexpr int GCH = 64 * CH, S = U * kNW;
   __shared__ float sP[kNW][GCH], sEf[kNW][GCH], sEb[kNW][GCH];
+  __shared__ float sD[GATED ? kNW : 1][GCH];
   __shared__ float sIn[GCH];
   __shared__ int sTicket;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -150,36 +219,44 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_bwd_kernel(
   const int t0 = k * S + w * U;
   const int64_t row0 = (int64_t)b * L;
 
-  Pack<InT, CH> pa[U], px[U];
   float gy[U][CH];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int t = t0 + u;
     if (cok && t < L) {
-      const int64_t i = (row0 + t) * D + ch;
-      pa[u] = ld_pack<InT, CH>(a, i);
-      px[u] = ld_pack<InT, CH>(x, i);
-      const Pack<float, CH> g2 = ld_pack<float, CH>(dy, i);
+      const Pack<float, CH> g2 = ld_pack<float, CH>(dy, (row0 + t) * D + ch);
 #pragma unroll
       for (int c = 0; c < CH; ++c) gy[u][c] = g2[c];
     } else {
-      pa[u] = pack_fill<InT, CH>(1.f);
-      px[u] = pack_fill<InT, CH>(0.f);
 #pragma unroll
       for (int c = 0; c < CH; ++c) gy[u][c] = 0.f;
     }
   }
+  float csp[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) csp[c] = GATED && cok ? gc * softplus_f(glam[ch + c]) : 0.f;
+  Pack<InT, CH> pa[U], px[U], pi[GATED ? U : 1];
+  float av[GATED ? U : 1][CH], sv[GATED ? U : 1][CH];
+  load_steps<InT, CH, U, GATED>(a, x, gi, csp, cok, t0, L, row0, D, ch, pa, px, pi, av, sv);
+  auto A = [&](int u, int c) -> float {
+    if constexpr (GATED) return av[u][c];
+    else return pa[u][c];
+  };
+  auto X = [&](int u, int c) -> float {
+    if constexpr (GATED) return sv[u][c] * (pi[u][c] * px[u][c]);
+    else return px[u][c];
+  };
   // forward map (from a zero state) and adjoint map (from a zero adjoint)
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     float P = 1.f, Ef = 0.f, Eb = 0.f;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      Ef = pa[u][c] * Ef + px[u][c];
-      P *= pa[u][c];
+      Ef = A(u, c) * Ef + X(u, c);
+      P *= A(u, c);
     }
 #pragma unroll
-    for (int u = U - 1; u >= 0; --u) Eb = pa[u][c] * (Eb + gy[u][c]);
+    for (int u = U - 1; u >= 0; --u) Eb = A(u, c) * (Eb + gy[u][c]);
     sP[w][lane * CH + c] = P;
     sEf[w][lane * CH + c] = Ef;
     sEb[w][lane * CH + c] = Eb;
@@ -229,10 +306,13 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_bwd_kernel(
     float h = hin[c];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      h = pa[u][c] * h + px[u][c];
+      h = A(u, c) * h + X(u, c);
       hs[u][c] = h;
     }
   }
+  float dsum[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) dsum[c] = 0.f;
 #pragma unroll
   for (int u = U - 1; u >= 0; --u) {
     const int t = t0 + u;
@@ -242,13 +322,79 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_bwd_kernel(
       lam[c] += gy[u][c];
       gx[c] = lam[c];
       ga[c] = lam[c] * (u > 0 ? hs[u - 1][c] : hin[c]);
-      lam[c] *= pa[u][c];
+      lam[c] *= A(u, c);
     }
-    if (cok && t < L) {
+    const bool ok = cok && t < L;
+    if constexpr (GATED) {
+      // x' = s (i x), s = sqrt(1 - a^2): ds/da = -a / s; a = exp(z),
+      // z = -c' sigmoid(r).  (At a = 1, s = 0, where the s branch has no
+      // finite derivative, its term is dropped.)
+      float gr[CH], gi2[CH], gxx[CH];
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const float sr = sigmoid_f(pa[u][c]), iv = pi[u][c], xv = px[u][c], av_ = av[u][c], s = sv[u][c];
+        const float ds = gx[c] * (iv * xv);
+        const float dz = (ga[c] - (s > 0.f ? ds * av_ * __builtin_amdgcn_rcpf(s) : 0.f)) * av_;
+        gr[c] = dz * -csp[c] * (sr * (1.f - sr));
+        gi2[c] = gx[c] * s * xv;
+        gxx[c] = gx[c] * s * iv;
+        if (ok) dsum[c] += dz * sr;
+      }
+      if (ok) {
+        const int64_t i = (row0 + t) * D + ch;
+        rr::tiles::st_pack<InT, CH>(da, i, gr);
+        rr::tiles::st_pack<InT, CH>(dgi, i, gi2);
+        rr::tiles::st_pack<InT, CH>(dx, i, gxx);
+      }
+    } else if (ok) {
       const int64_t i = (row0 + t) * D + ch;
       rr::tiles::st_pack<InT, CH>(dx, i, gx);
       rr::tiles::st_pack<InT, CH>(da, i, ga);
     }
+  }
+  if constexpr (GATED) {   // the tile's dz * sigmoid(r) sums, waves added in order
+#pragma unroll
+    for (int c = 0; c < CH; ++c) sD[w][lane * CH + c] = dsum[c];
+    __syncthreads();
+    if (w == 0 && cok) {
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        float t = 0.f;
+#pragma unroll
+        for (int j = 0; j < kNW; ++j) t += sD[j][lane * CH + c];
+        dpart[((int64_t)b * K + k) * D + ch + c] = t;
+      }
+    }
+  }
+}
+
+// dlam[d] = -c sigmoid(lam[d]) * sum over rows of dpart[row, d] (d softplus /
+// d lam = sigmoid), rows in a fixed order: wave w of a workgroup of 16 sums
+// rows w, w + 16, ... of 64 channels with 8 loads in flight, then the waves'
+// sums are added in order.
+constexpr int kDlamWaves = 16;
+__global__ __launch_bounds__(64 * kDlamWaves) void rglru_dlam_kernel(const float* __restrict__ dpart,
+                                                                     const float* __restrict__ glam, float gc,
+                                                                     float* __restrict__ dlam, int rows, int D) {
+  __shared__ float red[kDlamWaves][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int d = blockIdx.x * 64 + lane;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (d < D) {
+    for (int j0 = w; j0 < rows; j0 += 8 * kDlamWaves) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int j = j0 + q * kDlamWaves;
+        if (j < rows) acc[q] += dpart[(int64_t)j * D + d];
+      }
+    }
+  }
+  red[w][lane] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+  __syncthreads();
+  if (w == 0 && d < D) {
+    float t = 0.f;
+    for (int j = 0; j < kDlamWaves; ++j) t += red[j][lane];
+    dlam[d] = -gc * t * sigmoid_f(glam[d]);
   }
 }
 
@@ -262,9 +408,18 @@ int check_common(int64_t B, int64_t L, int64_t D, int64_t seg, int dtype) {
   return RR_OK;
 }
 
-size_t ws_bytes_for(int64_t B, int64_t L, int64_t D, int dtype, int pass) {
+size_t ws_bytes_for(int64_t B, int64_t L, int64_t D, int dtype, int pass, bool gated = false) {
   const int ch = pass == 0 ? kFwdCh : kBwdCh;
-  return rr::tiles::ws_bytes(B * tile_grid(L, D, ch, dtype, pass).tiles(), 64 * ch);
+  return rr::tiles::ws_bytes(B * tile_grid(L, D, ch, dtype, pass, gated).tiles(), 64 * ch);
+}
+// Gated backward: the hand-off words, then the [B * K, D] fp32 tile sums.
+size_t gated_part_offset(int64_t B, int64_t L, int64_t D, int dtype) {
+  return (ws_bytes_for(B, L, D, dtype, 1, true) + 255) / 256 * 256;
+}
+size_t gated_ws_bytes(int64_t B, int64_t L, int64_t D, int dtype, int pass) {
+  if (pass == 0) return ws_bytes_for(B, L, D, dtype, 0, true);
+  const int K = tile_grid(L, D, kBwdCh, dtype, 1, true).K;
+  return gated_part_offset(B, L, D, dtype) + (size_t)(B * K * D) * 4;
 }
 
 }  // namespace
@@ -287,12 +442,12 @@ extern "C" int rr_rglru_fwd(const void* a, const void* x, int dtype, int64_t B, 
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (int rc = rr::tiles::launch_clear(workspace, need, s)) return rc;
   RR_DISPATCH_DTYPE(dtype, {
-    constexpr int U = steps_per_wave<InT, false>();
+    constexpr int U = steps_per_wave<InT, false, false>();
     const TileGrid tg = tile_grid(L, D, kFwdCh, dtype, 0);
-    hipLaunchKernelGGL((rglru_fwd_kernel<InT, kFwdCh, U>), dim3((unsigned)(B * tg.tiles())), dim3(64 * kNW), 0, s,
-                       static_cast<const InT*>(a), static_cast<const InT*>(x), h0, y, ckpt,
-                       rr::tiles::ws_counter(workspace), rr::tiles::ws_slots(workspace), (int)B, (int)L, (int)D,
-                       T, nC, tg.G, tg.K);
+    hipLaunchKernelGGL((rglru_fwd_kernel<InT, kFwdCh, U, false>), dim3((unsigned)(B * tg.tiles())), dim3(64 * kNW),
+                       0, s, static_cast<const InT*>(a), static_cast<const InT*>(x), nullptr, nullptr, 0.f, h0, y,
+                       ckpt, rr::tiles::ws_counter(workspace), rr::tiles::ws_slots(workspace), (int)B, (int)L,
+                       (int)D, T, nC, tg.G, tg.K);
   });
   return rr::check_launch("rr_rglru_fwd");
 }
@@ -312,12 +467,76 @@ extern "C" int rr_rglru_bwd(const float* dy, const float* dfinal, const void* a,
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (int rc = rr::tiles::launch_clear(workspace, need, s)) return rc;
   RR_DISPATCH_DTYPE(dtype, {
-    constexpr int U = steps_per_wave<InT, true>();
+    constexpr int U = steps_per_wave<InT, true, false>();
     const TileGrid tg = tile_grid(L, D, kBwdCh, dtype, 1);
-    hipLaunchKernelGGL((rglru_bwd_kernel<InT, kBwdCh, U>), dim3((unsigned)(B * tg.tiles())), dim3(64 * kNW), 0, s,
-                       dy, dfinal, static_cast<const InT*>(a), static_cast<const InT*>(x), h0, ckpt,
-                       static_cast<InT*>(da), static_cast<InT*>(dx), dh0, rr::tiles::ws_counter(workspace),
-                       rr::tiles::ws_slots(workspace), (int)B, (int)L, (int)D, T, nC, tg.G, tg.K);
+    hipLaunchKernelGGL((rglru_bwd_kernel<InT, kBwdCh, U, false>), dim3((unsigned)(B * tg.tiles())), dim3(64 * kNW),
+                       0, s, dy, dfinal, static_cast<const InT*>(a), static_cast<const InT*>(x), nullptr, nullptr,
+                       0.f, h0, ckpt, static_cast<InT*>(da), static_cast<InT*>(dx), nullptr, nullptr, dh0,
+                       rr::tiles::ws_counter(workspace), rr::tiles::ws_slots(workspace), (int)B, (int)L, (int)D, T,
+                       nC, tg.G, tg.K);
   });
   return rr::check_launch("rr_rglru_bwd");
+}
+
+extern "C" size_t rr_rglru_gated_workspace_bytes(int64_t B, int64_t L, int64_t D, int64_t seg, int dtype,
+                                                 int pass) {
+  if (B <= 0 || L <= 0 || D <= 0 || rr::chunk_len(L, seg) == 0 || !rr::valid_dtype(dtype)) return 0;
+  return gated_ws_bytes(B, L, D, dtype, pass);
+}
+
+extern "C" int rr_rglru_gated_fwd(const void* r, const void* i, const void* x, const float* lam, float c,
+                                  int dtype, int64_t B, int64_t L, int64_t D, int64_t seg, const float* h0,
+                                  float* y, float* ckpt, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  if (int rc = check_common(B, L, D, seg, dtype)) return rc;
+  if (!r || !i || !x || !lam || !y || !ckpt) return rr::fail(RR_EINVAL, "rglru_gated_fwd: null pointer argument");
+  if (!(c > 0.f) || !(c < INFINITY)) return rr::fail(RR_EINVAL, "rglru_gated_fwd: c must be positive and finite");
+  const size_t need = gated_ws_bytes(B, L, D, dtype, 0);
+  if (!workspace || workspace_bytes < need) return rr::fail(RR_EWORKSPACE, "rglru_gated_fwd: workspace too small");
+  const int T = (int)rr::chunk_len(L, seg);
+  const int nC = (int)(L / T);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (int rc = rr::tiles::launch_clear(workspace, need, s)) return rc;
+  RR_DISPATCH_DTYPE(dtype, {
+    constexpr int U = steps_per_wave<InT, false, true>();
+    const TileGrid tg = tile_grid(L, D, kFwdCh, dtype, 0, true);
+    hipLaunchKernelGGL((rglru_fwd_kernel<InT, kFwdCh, U, true>), dim3((unsigned)(B * tg.tiles())), dim3(64 * kNW), 0,
+                       s, static_cast<const InT*>(r), static_cast<const InT*>(x), static_cast<const InT*>(i), lam,
+                       c, h0, y, ckpt, rr::tiles::ws_counter(workspace), rr::tiles::ws_slots(workspace), (int)B,
+                       (int)L, (int)D, T, nC, tg.G, tg.K);
+  });
+  return rr::check_launch("rr_rglru_gated_fwd");
+}
+
+extern "C" int rr_rglru_gated_bwd(const float* dy, const float* dfinal, const void* r, const void* i,
+                                  const void* x, const float* lam, float c, int dtype, int64_t B, int64_t L,
+                                  int64_t D, int64_t seg, const float* h0, const float* ckpt, void* dr, void* di,
+                                  void* dx, float* dlam, float* dh0, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  if (int rc = check_common(B, L, D, seg, dtype)) return rc;
+  if (!dy || !r || !i || !x || !lam || !ckpt || !dr || !di || !dx || !dlam) {
+    return rr::fail(RR_EINVAL, "rglru_gated_bwd: null pointer argument");
+  }
+  if (!(c > 0.f) || !(c < INFINITY)) return rr::fail(RR_EINVAL, "rglru_gated_bwd: c must be positive and finite");
+  const size_t need = gated_ws_bytes(B, L, D, dtype, 1);
+  if (!workspace || workspace_bytes < need) return rr::fail(RR_EWORKSPACE, "rglru_gated_bwd: workspace too small");
+  const int T = (int)rr::chunk_len(L, seg);
+  const int nC = (int)(L / T);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // only the hand-off words need clearing; every tile writes its row of sums
+  if (int rc = rr::tiles::launch_clear(workspace, ws_bytes_for(B, L, D, dtype, 1, true), s)) return rc;
+  float* dpart = reinterpret_cast<float*>(static_cast<char*>(workspace) + gated_part_offset(B, L, D, dtype));
+  const TileGrid tg = tile_grid(L, D, kBwdCh, dtype, 1, true);
+  RR_DISPATCH_DTYPE(dtype, {
+    constexpr int U = steps_per_wave<InT, true, true>();
+    hipLaunchKernelGGL((rglru_bwd_kernel<InT, kBwdCh, U, true>), dim3((unsigned)(B * tg.tiles())), dim3(64 * kNW), 0,
+                       s, dy, dfinal, static_cast<const InT*>(r), static_cast<const InT*>(x),
+                       static_cast<const InT*>(i), lam, c, h0, ckpt, static_cast<InT*>(dr), static_cast<InT*>(dx),
+                       static_cast<InT*>(di), dpart, dh0, rr::tiles::ws_counter(workspace),
+                       rr::tiles::ws_slots(workspace), (int)B, (int)L, (int)D, T, nC, tg.G, tg.K);
+  });
+  if (int rc = rr::check_launch("rr_rglru_gated_bwd")) return rc;
+  hipLaunchKernelGGL(rglru_dlam_kernel, dim3((unsigned)((D + 63) / 64)), dim3(64 * kDlamWaves), 0, s, dpart, lam, c,
+                     dlam, (int)(B * tg.K), (int)D);
+  return rr::check_launch("rr_rglru_gated_bwd dlam");
 }

@@ -45,6 +45,11 @@ _SIGS = {
     "rr_rglru_workspace_bytes": (_c_size, [_c_i64] * 4 + [_c_int, _c_int]),
     "rr_rglru_fwd": (_c_int, [_c_ptr] * 2 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
     "rr_rglru_bwd": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 6 + [_c_size, _c_ptr]),
+    "rr_rglru_gated_workspace_bytes": (_c_size, [_c_i64] * 4 + [_c_int, _c_int]),
+    "rr_rglru_gated_fwd": (_c_int, [_c_ptr] * 4 + [ctypes.c_float, _c_int] + [_c_i64] * 4 + [_c_ptr] * 4
+                           + [_c_size, _c_ptr]),
+    "rr_rglru_gated_bwd": (_c_int, [_c_ptr] * 6 + [ctypes.c_float, _c_int] + [_c_i64] * 4 + [_c_ptr] * 8
+                           + [_c_size, _c_ptr]),
     "rr_rotlru_workspace_bytes": (_c_size, [_c_i64] * 4 + [_c_int, _c_int]),
     "rr_rotlru_fwd": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
     "rr_rotlru_bwd": (_c_int, [_c_ptr] * 6 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 8 + [_c_size, _c_ptr]),
@@ -209,6 +214,28 @@ def rglru_bwd(dy, dfinal, a, x, h0, ckpt, seg, da, dx, dh0, ws):
                              B, L, D, seg, ptr(h0), ptr(ckpt), ptr(da), ptr(dx), ptr(dh0),
                              ptr(ws), ws.numel(), stream_of(a))
     _check(rc, "rr_rglru_bwd")
+
+
+def rglru_gated_workspace(B, L, D, seg, dtype, pass_, device) -> torch.Tensor:
+    n = int(load().rr_rglru_gated_workspace_bytes(B, L, D, seg, DTYPE_CODE[dtype], pass_))
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def rglru_gated_fwd(r, i, x, lam, c, h0, seg, y, ckpt, ws):
+    B, L, D = r.shape
+    rc = load().rr_rglru_gated_fwd(ptr(r), ptr(i), ptr(x), ptr(lam), float(c), DTYPE_CODE[r.dtype],
+                                   B, L, D, seg, ptr(h0), ptr(y), ptr(ckpt), ptr(ws), ws.numel(),
+                                   stream_of(r))
+    _check(rc, "rr_rglru_gated_fwd")
+
+
+def rglru_gated_bwd(dy, dfinal, r, i, x, lam, c, h0, ckpt, seg, dr, di, dx, dlam, dh0, ws):
+    B, L, D = r.shape
+    rc = load().rr_rglru_gated_bwd(ptr(dy), ptr(dfinal), ptr(r), ptr(i), ptr(x), ptr(lam), float(c),
+                                   DTYPE_CODE[r.dtype], B, L, D, seg, ptr(h0), ptr(ckpt), ptr(dr),
+                                   ptr(di), ptr(dx), ptr(dlam), ptr(dh0), ptr(ws), ws.numel(),
+                                   stream_of(r))
+    _check(rc, "rr_rglru_gated_bwd")
 
 
 # ---------------------------------------------------------------- rotLRU

@@ -44,6 +44,9 @@ __all__ = [
     "gla_backward",
     "rglru_forward",
     "rglru_backward",
+    "rglru_gates",
+    "rglru_gated_forward",
+    "rglru_gated_backward",
     "rotlru_forward",
     "rotlru_backward",
     "ssd_dual_form",
@@ -210,6 +213,40 @@ def rglru_backward(dy, a, x, h0=None, dfinal=None):
         da[:, t] = lam * hprev[:, t]
         lam = lam * a[:, t]
     return da, dx, lam
+
+
+def rglru_gates(r, i, x, lam, c=8.0):
+    """RG-LRU gate math (rglru.py:13-14, the Griffin formulas the reference
+    leaves to MLX host code, rglru.py:19-27): a = exp(-c softplus(lam)
+    sigmoid(r)), x' = sqrt(1 - a^2) (i x).  lam is per channel [D]."""
+    r, i, x, lam = _f64(r, i, x, lam)
+    sp = np.logaddexp(0.0, lam)
+    sr = 1.0 / (1.0 + np.exp(-r))
+    a = np.exp(-c * sp * sr)
+    return a, np.sqrt(1.0 - a * a) * (i * x)
+
+
+def rglru_gated_forward(r, i, x, lam, c=8.0, h0=None):
+    """Scan of the gated inputs: rglru_forward(*rglru_gates(...), h0)."""
+    a, xg = rglru_gates(r, i, x, lam, c)
+    return rglru_forward(a, xg, h0)
+
+
+def rglru_gated_backward(dy, r, i, x, lam, c=8.0, h0=None, dfinal=None):
+    """Chain rule of rglru_gates through rglru_backward.
+    Returns (dr, di, dx, dlam [D], dh0)."""
+    r, i, x, lam = _f64(r, i, x, lam)
+    a, xg = rglru_gates(r, i, x, lam, c)
+    da, dxg, dh0 = rglru_backward(dy, a, xg, h0, dfinal)
+    sp = np.logaddexp(0.0, lam)
+    sr = 1.0 / (1.0 + np.exp(-r))
+    s = np.sqrt(1.0 - a * a)
+    # x' = s (i x): d/ds, d/di, d/dx; s = sqrt(1 - a^2): ds/da = -a / s
+    ds = dxg * i * x
+    dz = (da - ds * a / s) * a                 # a = exp(z), z = -c sp sr
+    dr = dz * (-c * sp) * sr * (1.0 - sr)
+    dlam = (dz * (-c * sr)).sum(axis=(0, 1)) / (1.0 + np.exp(-lam))
+    return dr, dxg * s * x, dxg * s * i, dlam, dh0
 
 
 def rglru_discounted_sum(a_const, x):

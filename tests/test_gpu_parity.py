@@ -86,6 +86,65 @@ def test_rglru_parity(B, L, D, seg, dtype, gates, h0, dfinal, seed):
     print(rep, flush=True)
 
 
+RGLRU_GATED_CASES = [
+    # (B, L, D, seg, dtype, h0, dfinal, seed)
+    (2, 64, 64, 32, F32, False, False, 20),
+    (1, 32, 32, 32, F32, True, True, 21),        # L == seg, one tile
+    (3, 200, 96, 8, F32, True, True, 22),        # T = 8; D and L not tile multiples
+    (2, 1024, 320, 32, BF16, True, True, 23),
+    (2, 512, 128, 16, F16, False, True, 24),
+    (8, 4096, 2560, 32, BF16, False, False, 25),  # BASELINE config 3 shape, full size
+]
+
+
+@pytest.mark.parametrize("B,L,D,seg,dtype,h0,dfinal,seed", RGLRU_GATED_CASES)
+def test_rglru_gated_parity(B, L, D, seg, dtype, h0, dfinal, seed):
+    """Fused gate math + scan against the oracle's gates composed with its scan."""
+    _announce("rglru_gated", B=B, L=L, D=D, seg=seg, dtype=dtype, h0=h0, seed=seed)
+    rng = np.random.default_rng(seed)
+    r = rng.standard_normal((B, L, D))
+    i = _sigmoid(rng.standard_normal((B, L, D)))
+    x = rng.standard_normal((B, L, D))
+    lam = np.log(rng.uniform(0.9, 0.999, D))     # BASELINE config 3's Lambda
+    rt, it, xt = (to_dev(v, dtype, True) for v in (r, i, x))
+    lt = to_dev(lam, F32, True)
+    h0t = to_dev(rng.standard_normal((B, D)), F32, True) if h0 else None
+    y, fs = mr.rglru_gated_scan_with_state(rt, it, xt, lt, 8.0, seg=seg, initial_state=h0t)
+    W = _w(rng, (B, L, D))
+    Wf = _w(rng, (B, D)) if dfinal else None
+    loss = (y * torch.tensor(W, dtype=F32, device=y.device)).sum()
+    if dfinal:
+        loss = loss + (fs * torch.tensor(Wf, dtype=F32, device=y.device)).sum()
+    loss.backward()
+    rr_, ri, rx, rl = rounded(rt), rounded(it), rounded(xt), rounded(lt)
+    rh0 = rounded(h0t) if h0 else None
+    y_o, fs_o = orc.rglru_gated_forward(rr_, ri, rx, rl, 8.0, rh0)
+    dr_o, di_o, dx_o, dl_o, dh0_o = orc.rglru_gated_backward(W, rr_, ri, rx, rl, 8.0, rh0, Wf)
+    tol, rep = TOL[dtype], {}
+    check("y", y, y_o, TOL[F32] if dtype == F32 else tol, rep)
+    check("final", fs, fs_o, TOL[F32] if dtype == F32 else tol, rep)
+    check("grad_r", rt.grad, dr_o, tol, rep)
+    check("grad_i", it.grad, di_o, tol, rep)
+    check("grad_x", xt.grad, dx_o, tol, rep)
+    check("grad_lam", lt.grad, dl_o, TOL[F32] if dtype == F32 else tol, rep)
+    if h0:
+        check("grad_h0", h0t.grad, dh0_o, tol, rep)
+    print(rep, flush=True)
+
+
+def test_rglru_gated_matches_plain_scan_of_gates():
+    """The fused path against rglru_scan of torch-computed gates (same kernels'
+    scan, gates formed on the host as the reference does)."""
+    rng = np.random.default_rng(26)
+    B, L, D = 2, 256, 192
+    r, i, x = (to_dev(rng.standard_normal((B, L, D)), F32) for _ in range(3))
+    lam = to_dev(rng.standard_normal(D), F32)
+    y = mr.rglru_gated_scan(r, i, x, lam, 8.0)
+    a = torch.exp(-8.0 * torch.nn.functional.softplus(lam) * torch.sigmoid(r))
+    y_ref = mr.rglru_scan(a, torch.sqrt(1 - a * a) * (i * x))
+    assert (y - y_ref).abs().max().item() <= 1e-5 * y_ref.abs().max().item()
+
+
 def test_rglru_final_equals_last_step():
     rng = np.random.default_rng(11)
     a = to_dev(_sigmoid(rng.standard_normal((2, 64, 64)) + 2), F32)

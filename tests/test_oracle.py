@@ -229,6 +229,48 @@ def test_rglru_backward_finite_differences():
         _close(gr, _fd_grad(loss, arr), rtol=1e-6, atol=1e-8)
 
 
+def test_rglru_gates_known_answers():
+    # sigmoid(0) = 1/2 and softplus(0) = ln 2: a = 2^(-c/2), x' = sqrt(1 - a^2) i x
+    a, xg = orc.rglru_gates(np.zeros((1, 1, 2)), np.full((1, 1, 2), 0.5), np.full((1, 1, 2), 3.0),
+                            np.zeros(2), c=8.0)
+    _close(a, np.full((1, 1, 2), 1 / 16), rtol=1e-15)
+    _close(xg, np.full((1, 1, 2), 1.5 * np.sqrt(255) / 16), rtol=1e-15)
+    # Griffin's form a^(c r') of a base decay a0 = exp(-softplus(lam)) with r' = sigmoid(r)
+    rng = RNG(12)
+    r, lam = rng.standard_normal((2, 5, 4)), rng.standard_normal(4)
+    a, _ = orc.rglru_gates(r, np.ones_like(r), np.ones_like(r), lam, c=8.0)
+    a0 = 1 / (1 + np.exp(lam))
+    _close(a, a0 ** (8.0 / (1 + np.exp(-r))), rtol=1e-12)
+    # the gated scan is the plain scan of the gated inputs, brute force on one step
+    y, fs = orc.rglru_gated_forward(r[:, :1], np.ones_like(r[:, :1]), np.ones_like(r[:, :1]), lam)
+    _close(y[:, 0], np.sqrt(1 - a[:, 0] ** 2), rtol=1e-12)
+    _close(fs, y[:, -1])
+
+
+def test_rglru_gated_backward_finite_differences():
+    rng = RNG(13)
+    r = rng.standard_normal((2, 6, 3))
+    i = 1 / (1 + np.exp(-rng.standard_normal(r.shape)))
+    x = rng.standard_normal(r.shape)
+    lam = rng.standard_normal(3)
+    h0 = rng.standard_normal((2, 3))
+    W = rng.standard_normal(r.shape)
+    Wf = rng.standard_normal(h0.shape)
+    args = [r, i, x, lam]
+
+    def loss():
+        y, fs = orc.rglru_gated_forward(*args, c=8.0, h0=h0)
+        return float((y * W).sum() + (fs * Wf).sum())
+
+    grads = orc.rglru_gated_backward(W, *args, c=8.0, h0=h0, dfinal=Wf)
+    for arr, gr in zip(args + [h0], grads):
+        _close(gr, _fd_grad(loss, arr), rtol=1e-6, atol=1e-8)
+    # a planted mistake (sigmoid' taken as sigmoid in dr) fails the same check
+    sr = 1 / (1 + np.exp(-r))
+    bad = grads[0] / (1 - sr)
+    assert not np.allclose(bad, _fd_grad(loss, r), rtol=1e-4)
+
+
 def test_rotlru_backward_finite_differences():
     rng = RNG(8)
     B, L, Dp = 2, 6, 2
