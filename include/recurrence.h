@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define RR_ABI_VERSION 5
+#define RR_ABI_VERSION 6
 
 enum rr_dtype { RR_F32 = 0, RR_BF16 = 1, RR_F16 = 2 };
 
@@ -195,6 +195,20 @@ int rr_rotlru_bwd(const float* dy, const float* dfinal, const void* a, const voi
                   int64_t Dp, int64_t seg, const float* h0, const float* ckpt, void* da,
                   void* dcs, void* dsn, void* dx, float* dh0, void* workspace,
                   size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------- rotLRU, theta --
+ * The rotation passed as its angle: theta [B,L,Dp] (dtype) replaces cs and
+ * sn, the kernels form cos / sin in registers (the reference computes them in
+ * MLX host code, mlx_recurrence/rotlru.py:18-23, 306-317, and its kernel reads
+ * both).  Other arguments and the workspace (rr_rotlru_workspace_bytes) as
+ * for rr_rotlru_*; dtheta [B,L,Dp] (dtype) = -sin * dcs + cos * dsn. */
+int rr_rotlru_theta_fwd(const void* a, const void* theta, const void* x, int dtype, int64_t B,
+                        int64_t L, int64_t Dp, int64_t seg, const float* h0, float* y, float* ckpt,
+                        void* workspace, size_t workspace_bytes, void* stream);
+int rr_rotlru_theta_bwd(const float* dy, const float* dfinal, const void* a, const void* theta,
+                        const void* x, int dtype, int64_t B, int64_t L, int64_t Dp, int64_t seg,
+                        const float* h0, const float* ckpt, void* da, void* dtheta, void* dx,
+                        float* dh0, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

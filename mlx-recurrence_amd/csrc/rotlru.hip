@@ -42,16 +42,28 @@ __device__ __forceinline__ cplx cfma(cplx p, cplx q, cplx e) {   // p q + e
 __device__ __forceinline__ cplx conj(cplx p) { return {p.r, -p.i}; }
 
 // The inputs of one wave: U steps of CP pairs.
-template <typename InT, int U>
+// TH: the rotation comes as the angle theta (one input instead of cos and
+// sin; the reference forms cos / sin in MLX host code, rotlru.py:18-23), and
+// the kernel takes sincosf of it in registers.
+template <typename InT, int U, bool TH>
 struct WaveIn {
-  Pack<InT, kCP> a[U], c[U], s[U];
+  Pack<InT, kCP> a[U], c[U], s[TH ? 1 : U];   // TH: c holds theta
+  float cf[TH ? U : 1][kCP], sf[TH ? U : 1][kCP];
   Pack<InT, 2 * kCP> x[U];
-  __device__ cplx z(int u, int q) const { return {a[u][q] * c[u][q], a[u][q] * s[u][q]}; }
+  __device__ float cosv(int u, int q) const {
+    if constexpr (TH) return cf[u][q];
+    else return c[u][q];
+  }
+  __device__ float sinv(int u, int q) const {
+    if constexpr (TH) return sf[u][q];
+    else return s[u][q];
+  }
+  __device__ cplx z(int u, int q) const { return {a[u][q] * cosv(u, q), a[u][q] * sinv(u, q)}; }
   __device__ cplx xin(int u, int q) const { return {x[u][2 * q], x[u][2 * q + 1]}; }
 };
 
-template <typename InT, int U>
-__device__ __forceinline__ void load_wave(WaveIn<InT, U>& in, const InT* a, const InT* cs, const InT* sn,
+template <typename InT, int U, bool TH>
+__device__ __forceinline__ void load_wave(WaveIn<InT, U, TH>& in, const InT* a, const InT* cs, const InT* sn,
                                           const InT* x, int64_t row0, int t0, int L, int Dp, int p, bool pok) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -60,18 +72,24 @@ __device__ __forceinline__ void load_wave(WaveIn<InT, U>& in, const InT* a, cons
       const int64_t ip = (row0 + t) * Dp + p;
       in.a[u] = ld_pack<InT, kCP>(a, ip);
       in.c[u] = ld_pack<InT, kCP>(cs, ip);
-      in.s[u] = ld_pack<InT, kCP>(sn, ip);
+      if constexpr (!TH) in.s[u] = ld_pack<InT, kCP>(sn, ip);
       in.x[u] = ld_pack<InT, 2 * kCP>(x, 2 * ip);
-    } else {   // identity step: z = 1, x = 0
+    } else {   // identity step: z = 1, x = 0 (theta = 0)
       in.a[u] = pack_fill<InT, kCP>(1.f);
-      in.c[u] = pack_fill<InT, kCP>(1.f);
-      in.s[u] = pack_fill<InT, kCP>(0.f);
+      in.c[u] = pack_fill<InT, kCP>(TH ? 0.f : 1.f);
+      if constexpr (!TH) in.s[u] = pack_fill<InT, kCP>(0.f);
       in.x[u] = pack_fill<InT, 2 * kCP>(0.f);
     }
   }
+  if constexpr (TH) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int q = 0; q < kCP; ++q) sincosf(in.c[u][q], &in.sf[u][q], &in.cf[u][q]);
+  }
 }
 
-template <typename InT>
+template <typename InT, bool TH>
 __global__ __launch_bounds__(64 * kNW, 4) void rotlru_fwd_kernel(
     const InT* __restrict__ a, const InT* __restrict__ cs, const InT* __restrict__ sn,
     const InT* __restrict__ x, const float* __restrict__ h0, float* __restrict__ y,
@@ -93,8 +111,8 @@ __global__ __launch_bounds__(64 * kNW, 4) void rotlru_fwd_kernel(
   const int t0 = k * S + w * kU;
   const int64_t row0 = (int64_t)b * L;
 
-  WaveIn<InT, kU> in;
-  load_wave<InT, kU>(in, a, cs, sn, x, row0, t0, L, Dp, p, pok);
+  WaveIn<InT, kU, TH> in;
+  load_wave<InT, kU, TH>(in, a, cs, sn, x, row0, t0, L, Dp, p, pok);
 #pragma unroll
   for (int q = 0; q < kCP; ++q) {
     cplx P{1.f, 0.f}, E{0.f, 0.f};
@@ -158,7 +176,7 @@ __global__ __launch_bounds__(64 * kNW, 4) void rotlru_fwd_kernel(
 //   lam += dy_t; dx_t = lam; da_t = lam . r;
 //   dcs_t = a_t (lamU u_{t-1} + lamW w_{t-1}); dsn_t = a_t (lamW u_{t-1} - lamU w_{t-1});
 //   lam = conj(z_t) lam.
-template <typename InT>
+template <typename InT, bool TH>
 __global__ __launch_bounds__(64 * kNW, 2) void rotlru_bwd_kernel(
     const float* __restrict__ dy, const float* __restrict__ dfinal, const InT* __restrict__ a,
     const InT* __restrict__ cs, const InT* __restrict__ sn, const InT* __restrict__ x,
@@ -181,8 +199,8 @@ __global__ __launch_bounds__(64 * kNW, 2) void rotlru_bwd_kernel(
   const int t0 = k * S + w * kU;
   const int64_t row0 = (int64_t)b * L;
 
-  WaveIn<InT, kU> in;
-  load_wave<InT, kU>(in, a, cs, sn, x, row0, t0, L, Dp, p, pok);
+  WaveIn<InT, kU, TH> in;
+  load_wave<InT, kU, TH>(in, a, cs, sn, x, row0, t0, L, Dp, p, pok);
   cplx gy[kU][kCP];
 #pragma unroll
   for (int u = 0; u < kU; ++u) {
@@ -272,7 +290,7 @@ __global__ __launch_bounds__(64 * kNW, 2) void rotlru_bwd_kernel(
 #pragma unroll
     for (int q = 0; q < kCP; ++q) {
       const cplx hp = u > 0 ? hs[u - 1][q] : hin[q];
-      const float av = in.a[u][q], cv = in.c[u][q], sv = in.s[u][q];
+      const float av = in.a[u][q], cv = in.cosv(u, q), sv = in.sinv(u, q);
       lam[q] = {lam[q].r + gy[u][q].r, lam[q].i + gy[u][q].i};
       gx[2 * q] = lam[q].r;
       gx[2 * q + 1] = lam[q].i;
@@ -285,8 +303,15 @@ __global__ __launch_bounds__(64 * kNW, 2) void rotlru_bwd_kernel(
     if (pok && t < L) {
       const int64_t ip = (row0 + t) * Dp + p;
       rr::tiles::st_pack<InT, kCP>(da, ip, ga);
-      rr::tiles::st_pack<InT, kCP>(dcs, ip, gc);
-      rr::tiles::st_pack<InT, kCP>(dsn, ip, gs);
+      if constexpr (TH) {   // d theta = -sin * dcos + cos * dsin
+        float gt[kCP];
+#pragma unroll
+        for (int q = 0; q < kCP; ++q) gt[q] = in.cosv(u, q) * gs[q] - in.sinv(u, q) * gc[q];
+        rr::tiles::st_pack<InT, kCP>(dcs, ip, gt);
+      } else {
+        rr::tiles::st_pack<InT, kCP>(dcs, ip, gc);
+        rr::tiles::st_pack<InT, kCP>(dsn, ip, gs);
+      }
       rr::tiles::st_pack<InT, 2 * kCP>(dx, 2 * ip, gx);
     }
   }
@@ -325,7 +350,7 @@ extern "C" int rr_rotlru_fwd(const void* a, const void* cs, const void* sn, cons
   const TileGrid tg = tile_grid(L, Dp);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (int rc = rr::tiles::launch_clear(workspace, need, s)) return rc;
-  RR_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((rotlru_fwd_kernel<InT>), dim3((unsigned)(B * tg.tiles())),
+  RR_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((rotlru_fwd_kernel<InT, false>), dim3((unsigned)(B * tg.tiles())),
                                               dim3(64 * kNW), 0, s, static_cast<const InT*>(a),
                                               static_cast<const InT*>(cs), static_cast<const InT*>(sn),
                                               static_cast<const InT*>(x), h0, y, ckpt,
@@ -349,7 +374,7 @@ extern "C" int rr_rotlru_bwd(const float* dy, const float* dfinal, const void* a
   const TileGrid tg = tile_grid(L, Dp);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (int rc = rr::tiles::launch_clear(workspace, need, s)) return rc;
-  RR_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((rotlru_bwd_kernel<InT>), dim3((unsigned)(B * tg.tiles())),
+  RR_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((rotlru_bwd_kernel<InT, false>), dim3((unsigned)(B * tg.tiles())),
                                               dim3(64 * kNW), 0, s, dy, dfinal, static_cast<const InT*>(a),
                                               static_cast<const InT*>(cs), static_cast<const InT*>(sn),
                                               static_cast<const InT*>(x), h0, ckpt, static_cast<InT*>(da),
@@ -358,4 +383,49 @@ extern "C" int rr_rotlru_bwd(const float* dy, const float* dfinal, const void* a
                                               rr::tiles::ws_slots(workspace), (int)B, (int)L, (int)Dp, T, nC,
                                               tg.G, tg.K));
   return rr::check_launch("rr_rotlru_bwd");
+}
+
+extern "C" int rr_rotlru_theta_fwd(const void* a, const void* theta, const void* x, int dtype, int64_t B,
+                                   int64_t L, int64_t Dp, int64_t seg, const float* h0, float* y, float* ckpt,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_common(B, L, Dp, seg, dtype)) return rc;
+  if (!a || !theta || !x || !y || !ckpt) return rr::fail(RR_EINVAL, "rotlru_theta_fwd: null pointer argument");
+  const size_t need = ws_bytes_for(B, L, Dp);
+  if (!workspace || workspace_bytes < need) return rr::fail(RR_EWORKSPACE, "rotlru_theta_fwd: workspace too small");
+  const int T = (int)rr::chunk_len(L, seg);
+  const int nC = (int)(L / T);
+  const TileGrid tg = tile_grid(L, Dp);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (int rc = rr::tiles::launch_clear(workspace, need, s)) return rc;
+  RR_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((rotlru_fwd_kernel<InT, true>), dim3((unsigned)(B * tg.tiles())),
+                                              dim3(64 * kNW), 0, s, static_cast<const InT*>(a),
+                                              static_cast<const InT*>(theta), nullptr, static_cast<const InT*>(x),
+                                              h0, y, ckpt, rr::tiles::ws_counter(workspace),
+                                              rr::tiles::ws_slots(workspace), (int)B, (int)L, (int)Dp, T, nC,
+                                              tg.G, tg.K));
+  return rr::check_launch("rr_rotlru_theta_fwd");
+}
+
+extern "C" int rr_rotlru_theta_bwd(const float* dy, const float* dfinal, const void* a, const void* theta,
+                                   const void* x, int dtype, int64_t B, int64_t L, int64_t Dp, int64_t seg,
+                                   const float* h0, const float* ckpt, void* da, void* dtheta, void* dx,
+                                   float* dh0, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_common(B, L, Dp, seg, dtype)) return rc;
+  if (!dy || !a || !theta || !x || !ckpt || !da || !dtheta || !dx)
+    return rr::fail(RR_EINVAL, "rotlru_theta_bwd: null pointer argument");
+  const size_t need = ws_bytes_for(B, L, Dp);
+  if (!workspace || workspace_bytes < need) return rr::fail(RR_EWORKSPACE, "rotlru_theta_bwd: workspace too small");
+  const int T = (int)rr::chunk_len(L, seg);
+  const int nC = (int)(L / T);
+  const TileGrid tg = tile_grid(L, Dp);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (int rc = rr::tiles::launch_clear(workspace, need, s)) return rc;
+  RR_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((rotlru_bwd_kernel<InT, true>), dim3((unsigned)(B * tg.tiles())),
+                                              dim3(64 * kNW), 0, s, dy, dfinal, static_cast<const InT*>(a),
+                                              static_cast<const InT*>(theta), nullptr, static_cast<const InT*>(x),
+                                              h0, ckpt, static_cast<InT*>(da), static_cast<InT*>(dtheta), nullptr,
+                                              static_cast<InT*>(dx), dh0, rr::tiles::ws_counter(workspace),
+                                              rr::tiles::ws_slots(workspace), (int)B, (int)L, (int)Dp, T, nC,
+                                              tg.G, tg.K));
+  return rr::check_launch("rr_rotlru_theta_bwd");
 }

@@ -22,7 +22,8 @@ from .ssd import ssd_scan, ssd_scan_with_state, ssd_scan_reference
 from .gla import gla_scan, gla_scan_with_state, gla_scan_reference
 from .rglru import (rglru_scan, rglru_scan_with_state, rglru_scan_reference, rglru_gated_scan,
                     rglru_gated_scan_with_state, rglru_gated_reference)
-from .rotlru import rotlru_scan, rotlru_scan_with_state, rotlru_scan_reference
+from .rotlru import (rotlru_scan, rotlru_scan_with_state, rotlru_scan_reference, rotlru_theta_scan,
+                     rotlru_theta_scan_with_state)
 from ._chassis import DEFAULT_SEG, SIMD_WIDTH, get_or_build_kernel, check_segment_shape, parity_check
 
 __all__ = [
@@ -41,6 +42,8 @@ __all__ = [
     "rotlru_scan",
     "rotlru_scan_with_state",
     "rotlru_scan_reference",
+    "rotlru_theta_scan",
+    "rotlru_theta_scan_with_state",
     "DEFAULT_SEG",
     "SIMD_WIDTH",
     "get_or_build_kernel",

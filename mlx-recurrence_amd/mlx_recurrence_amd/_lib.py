@@ -53,6 +53,8 @@ _SIGS = {
     "rr_rotlru_workspace_bytes": (_c_size, [_c_i64] * 4 + [_c_int, _c_int]),
     "rr_rotlru_fwd": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
     "rr_rotlru_bwd": (_c_int, [_c_ptr] * 6 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 8 + [_c_size, _c_ptr]),
+    "rr_rotlru_theta_fwd": (_c_int, [_c_ptr] * 3 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
+    "rr_rotlru_theta_bwd": (_c_int, [_c_ptr] * 5 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 7 + [_c_size, _c_ptr]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGS)
@@ -258,3 +260,18 @@ def rotlru_bwd(dy, dfinal, a, cs, sn, x, h0, ckpt, seg, da, dcs, dsn, dx, dh0, w
                               ptr(da), ptr(dcs), ptr(dsn), ptr(dx), ptr(dh0), ptr(ws), ws.numel(),
                               stream_of(a))
     _check(rc, "rr_rotlru_bwd")
+
+
+def rotlru_theta_fwd(a, th, x, h0, seg, y, ckpt, ws):
+    B, L, Dp = a.shape
+    rc = load().rr_rotlru_theta_fwd(ptr(a), ptr(th), ptr(x), DTYPE_CODE[a.dtype], B, L, Dp, seg,
+                                    ptr(h0), ptr(y), ptr(ckpt), ptr(ws), ws.numel(), stream_of(a))
+    _check(rc, "rr_rotlru_theta_fwd")
+
+
+def rotlru_theta_bwd(dy, dfinal, a, th, x, h0, ckpt, seg, da, dth, dx, dh0, ws):
+    B, L, Dp = a.shape
+    rc = load().rr_rotlru_theta_bwd(ptr(dy), ptr(dfinal), ptr(a), ptr(th), ptr(x), DTYPE_CODE[a.dtype],
+                                    B, L, Dp, seg, ptr(h0), ptr(ckpt), ptr(da), ptr(dth), ptr(dx),
+                                    ptr(dh0), ptr(ws), ws.numel(), stream_of(a))
+    _check(rc, "rr_rotlru_theta_bwd")

@@ -132,3 +132,62 @@ def rotlru_scan_reference(a, cs, sn, x, *, initial_state=None):
         u, w = un, wn
         ys.append(torch.stack([u, w], dim=-1).reshape(B, 2 * Dp))
     return torch.stack(ys, dim=1)
+
+
+# ------------------------------------------------------ rotLRU from theta
+class _RotLRUThetaScan(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, a, th, x, h0, seg):
+        dev = _lib.require_device(a, th, x, h0)
+        dt = _lib.common_dtype(a, th, x)
+        a_, th_, x_ = (_lib.prep(t, dt) for t in (a, th, x))
+        B, L, Dp = a_.shape
+        D = 2 * Dp
+        h0_ = None if h0 is None else _lib.prep(h0.reshape(B, D), torch.float32)
+        nC = L // _lib.chunk_len(L, seg)
+        y = torch.empty((B, L, D), dtype=torch.float32, device=dev)
+        ckpt = torch.empty((B, nC, D), dtype=torch.float32, device=dev)
+        with torch.cuda.device(dev):
+            ws = _lib.rotlru_workspace(B, L, Dp, seg, dt, 0, dev)
+            _lib.rotlru_theta_fwd(a_, th_, x_, h0_, seg, y, ckpt, ws)
+        ctx.save_for_backward(a_, th_, x_, h0_, ckpt)
+        ctx.seg = seg
+        ctx.set_materialize_grads(False)
+        return y, ckpt[:, -1]
+
+    @staticmethod
+    def backward(ctx, dy, dfinal):
+        a_, th_, x_, h0_, ckpt = ctx.saved_tensors
+        B, L, Dp = a_.shape
+        D = 2 * Dp
+        dev = a_.device
+        dy = torch.zeros((B, L, D), dtype=torch.float32, device=dev) if dy is None else _lib.prep(dy, torch.float32)
+        dfinal = None if dfinal is None else _lib.prep(dfinal, torch.float32)
+        da, dth, dx = torch.empty_like(a_), torch.empty_like(th_), torch.empty_like(x_)
+        dh0 = torch.empty((B, D), dtype=torch.float32, device=dev) if ctx.needs_input_grad[3] else None
+        with torch.cuda.device(dev):
+            ws = _lib.rotlru_workspace(B, L, Dp, ctx.seg, a_.dtype, 1, dev)
+            _lib.rotlru_theta_bwd(dy, dfinal, a_, th_, x_, h0_, ckpt, ctx.seg, da, dth, dx, dh0, ws)
+        return da, dth, dx, dh0, None
+
+
+def _run_theta(a, theta, x, seg, initial_state):
+    B, L, Dp = _validate(a, theta, theta, x)
+    check_segment_shape(L, seg, 2 * Dp, "D")
+    if initial_state is not None and tuple(initial_state.shape) != (B, 2 * Dp):
+        raise ValueError(f"initial_state must be [B, 2*Dp] = [{B}, {2 * Dp}], got {tuple(initial_state.shape)}")
+    return _RotLRUThetaScan.apply(a, theta, x, initial_state, seg)
+
+
+def rotlru_theta_scan(a, theta, x, seg=DEFAULT_SEG, *, initial_state=None):
+    """rotlru_scan with the rotation given by its angle: the kernels form
+    cos(theta) and sin(theta) in registers (the reference forms them in MLX
+    host code, rotlru.py:18-23) and return d theta = -sin * dcs + cos * dsn.
+    a, theta [B, L, Dp]; x [B, L, 2*Dp] interleaved (u, w) pairs."""
+    y, _ = _run_theta(a, theta, x, seg, initial_state)
+    return y
+
+
+def rotlru_theta_scan_with_state(a, theta, x, seg=DEFAULT_SEG, *, initial_state=None):
+    """rotlru_theta_scan that also returns the final state [B, 2*Dp]."""
+    return _run_theta(a, theta, x, seg, initial_state)

@@ -49,6 +49,8 @@ __all__ = [
     "rglru_gated_backward",
     "rotlru_forward",
     "rotlru_backward",
+    "rotlru_theta_forward",
+    "rotlru_theta_backward",
     "ssd_dual_form",
     "gla_causal_linear_attention",
     "rglru_discounted_sum",
@@ -296,6 +298,19 @@ def rotlru_forward(a, cs, sn, x, h0=None):
         y[:, t, :, 1] = w
     y = y.reshape(B, L, 2 * Dp)
     return y, y[:, -1].copy()
+
+
+def rotlru_theta_forward(a, theta, x, h0=None):
+    """rotLRU with the rotation as its angle (cos / sin of rotlru.py:18-23)."""
+    theta = np.asarray(theta, dtype=np.float64)
+    return rotlru_forward(a, np.cos(theta), np.sin(theta), x, h0)
+
+
+def rotlru_theta_backward(dy, a, theta, x, h0=None, dfinal=None):
+    """Chain rule of (cos, sin) through rotlru_backward: (da, dtheta, dx, dh0)."""
+    theta = np.asarray(theta, dtype=np.float64)
+    da, dcs, dsn, dx, dh0 = rotlru_backward(dy, a, np.cos(theta), np.sin(theta), x, h0, dfinal)
+    return da, np.cos(theta) * dsn - np.sin(theta) * dcs, dx, dh0
 
 
 def rotlru_backward(dy, a, cs, sn, x, h0=None, dfinal=None):

@@ -153,6 +153,47 @@ def test_rglru_final_equals_last_step():
     assert torch.equal(fs, y[:, -1])
 
 
+# ------------------------------------------------------- rotLRU from theta
+ROTLRU_THETA_CASES = [
+    # (B, L, Dp, seg, dtype, h0, dfinal, seed)
+    (2, 64, 32, 32, F32, False, False, 30),
+    (2, 160, 48, 16, F32, True, True, 31),     # Dp not a tile multiple, T = 16
+    (2, 1024, 160, 32, BF16, True, True, 32),
+    (8, 4096, 1280, 32, BF16, False, False, 33),  # BASELINE config 3 shape, full size
+]
+
+
+@pytest.mark.parametrize("B,L,Dp,seg,dtype,h0,dfinal,seed", ROTLRU_THETA_CASES)
+def test_rotlru_theta_parity(B, L, Dp, seg, dtype, h0, dfinal, seed):
+    _announce("rotlru_theta", B=B, L=L, Dp=Dp, seg=seg, dtype=dtype, h0=h0, seed=seed)
+    rng = np.random.default_rng(seed)
+    a = _sigmoid(rng.standard_normal((B, L, Dp)) + 2.0)
+    th = rng.uniform(-np.pi, np.pi, (B, L, Dp))
+    x = rng.standard_normal((B, L, 2 * Dp))
+    at, tt, xt = (to_dev(v, dtype, True) for v in (a, th, x))
+    h0t = to_dev(rng.standard_normal((B, 2 * Dp)), F32, True) if h0 else None
+    y, fs = mr.rotlru_theta_scan_with_state(at, tt, xt, seg=seg, initial_state=h0t)
+    W = _w(rng, (B, L, 2 * Dp))
+    Wf = _w(rng, (B, 2 * Dp)) if dfinal else None
+    loss = (y * torch.tensor(W, dtype=F32, device=y.device)).sum()
+    if dfinal:
+        loss = loss + (fs * torch.tensor(Wf, dtype=F32, device=y.device)).sum()
+    loss.backward()
+    ra, rt, rx = rounded(at), rounded(tt), rounded(xt)
+    rh0 = rounded(h0t) if h0 else None
+    y_o, fs_o = orc.rotlru_theta_forward(ra, rt, rx, rh0)
+    da_o, dt_o, dx_o, dh0_o = orc.rotlru_theta_backward(W, ra, rt, rx, rh0, Wf)
+    tol, rep = TOL[dtype], {}
+    check("y", y, y_o, TOL[F32] if dtype == F32 else tol, rep)
+    check("final", fs, fs_o, TOL[F32] if dtype == F32 else tol, rep)
+    check("grad_a", at.grad, da_o, tol, rep)
+    check("grad_theta", tt.grad, dt_o, tol, rep)
+    check("grad_x", xt.grad, dx_o, tol, rep)
+    if h0:
+        check("grad_h0", h0t.grad, dh0_o, tol, rep)
+    print(rep, flush=True)
+
+
 # ----------------------------------------------------------------- rotLRU
 ROTLRU_CASES = [
     # (B, L, Dp, seg, dtype, a_range, h0, dfinal, seed)

@@ -271,6 +271,33 @@ def test_rglru_gated_backward_finite_differences():
     assert not np.allclose(bad, _fd_grad(loss, r), rtol=1e-4)
 
 
+def test_rotlru_theta_known_answers_and_finite_differences():
+    rng = RNG(14)
+    a = rng.uniform(0.3, 0.99, (2, 6, 3))
+    th = rng.uniform(-3.0, 3.0, a.shape)
+    x = rng.standard_normal((2, 6, 6))
+    h0 = rng.standard_normal((2, 6))
+    # theta = 0: the pairs decouple into two RG-LRU scans with the same a
+    y0, _ = orc.rotlru_theta_forward(a, np.zeros_like(a), x)
+    yr, _ = orc.rglru_forward(np.repeat(a, 2, axis=-1), x)
+    _close(y0, yr, rtol=1e-13)
+    W = rng.standard_normal(x.shape)
+    Wf = rng.standard_normal(h0.shape)
+    args = [a, th, x, h0]
+
+    def loss():
+        y, fs = orc.rotlru_theta_forward(*args)
+        return float((y * W).sum() + (fs * Wf).sum())
+
+    grads = orc.rotlru_theta_backward(W, *args, dfinal=Wf)
+    for arr, gr in zip(args, grads):
+        _close(gr, _fd_grad(loss, arr), rtol=1e-6, atol=1e-8)
+    # a planted sign mistake in d theta fails the same check
+    da, dcs, dsn, _, _ = orc.rotlru_backward(W, a, np.cos(th), np.sin(th), x, h0, Wf)
+    bad = np.cos(th) * dsn + np.sin(th) * dcs
+    assert not np.allclose(bad, _fd_grad(loss, th), rtol=1e-4)
+
+
 def test_rotlru_backward_finite_differences():
     rng = RNG(8)
     B, L, Dp = 2, 6, 2
