@@ -344,6 +344,58 @@ def make_rglru_gated(cfg, device, dtype):
                 io_bytes=n * 4 + 3 * n * es)
 
 
+def make_rotlru_theta(cfg, device, dtype):
+    """BASELINE config 3 shape, rotLRU given the angle: the kernels read
+    theta and form cos / sin themselves (inputs as make_rotlru)."""
+    import math
+    import torch
+    from mlx_recurrence_amd import _lib
+    B, L, Dp, seg = cfg["B"], cfg["L"], cfg["D"] // 2, cfg["seg"]
+    g = torch.Generator().manual_seed(cfg.get("seed", 4))
+    a = torch.sigmoid(_gen((B, L, Dp), g) + 2.0)
+    th = (_gen((B, L, Dp), g, "uniform") * 2 - 1) * math.pi * 0.1
+    x = _gen((B, L, 2 * Dp), g)
+    dy = _gen((B, L, 2 * Dp), g)
+    d = dict(a=a.to(dtype).to(device), th=th.to(dtype).to(device), x=x.to(dtype).to(device), dy=dy.to(device))
+    T = _lib.chunk_len(L, seg)
+    nC = L // T
+    f32 = torch.float32
+    out = dict(y=torch.empty((B, L, 2 * Dp), dtype=f32, device=device),
+               ckpt=torch.empty((B, nC, 2 * Dp), dtype=f32, device=device),
+               da=torch.empty((B, L, Dp), dtype=dtype, device=device),
+               dth=torch.empty((B, L, Dp), dtype=dtype, device=device),
+               dx=torch.empty((B, L, 2 * Dp), dtype=dtype, device=device),
+               wsf=_lib.rotlru_workspace(B, L, Dp, seg, dtype, 0, device),
+               wsb=_lib.rotlru_workspace(B, L, Dp, seg, dtype, 1, device))
+    es = torch.tensor([], dtype=dtype).element_size()
+    n_p, n_x, n_ck = B * L * Dp, B * L * 2 * Dp, B * nC * 2 * Dp
+    ins = (2 * n_p + n_x) * es
+    fwd_bytes = ins + n_x * 4 + n_ck * 4
+    bwd_bytes = n_x * 4 + n_ck * 4 + ins + ins
+
+    def fwd():
+        _lib.rotlru_theta_fwd(d["a"], d["th"], d["x"], None, seg, out["y"], out["ckpt"], out["wsf"])
+
+    def bwd():
+        _lib.rotlru_theta_bwd(d["dy"], None, d["a"], d["th"], d["x"], None, out["ckpt"], seg, out["da"],
+                              out["dth"], out["dx"], None, out["wsb"])
+
+    def eager():
+        import mlx_recurrence_amd as mr
+        xs = [d[kk].detach().requires_grad_(True) for kk in ("a", "th", "x")]
+        mr.rotlru_theta_scan(*xs, seg=seg).backward(d["dy"])
+
+    def cpu_sample():
+        from oracle import recurrence_oracle as orc
+        xs = [d[kk][:1].double().cpu().numpy() for kk in ("a", "th", "x")]
+        orc.rotlru_theta_forward(*xs)
+        orc.rotlru_theta_backward(d["dy"][:1].double().cpu().numpy(), *xs)
+
+    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, tokens=B * L, cpu_tokens=L,
+                fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=n_x * 4, ckpt_bytes=n_ck * 4,
+                io_bytes=n_x * 4 + ins)
+
+
 def make_rotlru(cfg, device, dtype):
     """BASELINE config 3 (rotLRU): a = sigmoid(N(2,1)) [B,L,Dp];
     theta = U(-pi, pi) * 0.1; cs, sn = cos, sin; x ~ N(0,1) [B,L,2Dp]."""
@@ -404,6 +456,8 @@ WORKLOADS = {
     "gla": ("gla_scan fwd+bwd (BASELINE config 2)", make_gla, dict(B=3, L=512, H=12, Dh=64, seg=32)),
     "rglru": ("rglru_scan fwd+bwd (BASELINE config 3)", make_rglru, dict(B=8, L=4096, D=2560, seg=32)),
     "rotlru": ("rotlru_scan fwd+bwd (BASELINE config 3)", make_rotlru, dict(B=8, L=4096, D=2560, seg=32)),
+    "rotlru_theta": ("rotlru_theta_scan fwd+bwd, cos/sin in the kernels (BASELINE config 3 shape)",
+                     make_rotlru_theta, dict(B=8, L=4096, D=2560, seg=32)),
     "rglru_gated": ("rglru_gated_scan fwd+bwd, gate math in the kernels (BASELINE config 3 shape)",
                     make_rglru_gated, dict(B=8, L=4096, D=2560, seg=32)),
     "ssd_c4": ("ssd_scan fwd+bwd (BASELINE config 4)", make_ssd,
