@@ -604,12 +604,12 @@ def measure(name, steps, warmup, dtype, device, with_cpu):
 PMC_FILE = ROOT / "profiles" / "pmc_traffic.json"
 PROFILE_COMMANDS = [
     "rocprofv3 --kernel-trace --stats -d $R/gpurun_out/prof_trace -o trace --output-format csv -- "
-    "python3 bench.py --steps 20 --warmup 3 --no-cpu --also gla,rglru,rotlru,rglru_gated",
+    "python3 bench.py --steps 20 --warmup 3 --no-cpu --also gla,rglru,rotlru,rglru_gated,rotlru_theta",
     "rocprofv3 --pmc FETCH_SIZE -d $R/gpurun_out/pmc/cal_fetch -o cal --output-format csv -- "
     "python3 bench.py --calibrate-copy 256",
     "rocprofv3 --pmc WRITE_SIZE -d $R/gpurun_out/pmc/cal_write -o cal --output-format csv -- "
     "python3 bench.py --calibrate-copy 256",
-    "for w in ssd gla rglru rotlru rglru_gated; do rocprofv3 --pmc FETCH_SIZE -d $R/gpurun_out/pmc/${w}_fetch -o $w "
+    "for w in ssd gla rglru rotlru rglru_gated rotlru_theta; do rocprofv3 --pmc FETCH_SIZE -d $R/gpurun_out/pmc/${w}_fetch -o $w "
     "--output-format csv -- python3 bench.py --pmc-run $w; rocprofv3 --pmc WRITE_SIZE -d "
     "$R/gpurun_out/pmc/${w}_write -o $w --output-format csv -- python3 bench.py --pmc-run $w; done",
     "python3 bench.py --pmc-summary --trace-dir gpurun_out/prof_trace",
@@ -698,8 +698,8 @@ def profile_markdown(summary, trace_dir, out_md, commands):
     traffic (the counter runs) beside each pass's algorithmic bytes."""
     import csv
     import torch
-    lines = ["# Default bench workloads (SSD config 1 headline; GLA config 2; RG-LRU / rotLRU / gated RG-LRU "
-             "config 3), bf16 inputs",
+    lines = ["# Default bench workloads (SSD config 1 headline; GLA config 2; RG-LRU / rotLRU / gated RG-LRU / "
+             "rotLRU from theta, config 3), bf16 inputs",
              "", "Commands (from the repository root on one MI355X, `export TMPDIR=/tmp`, R = repository root):", ""]
     lines += ["    " + c for c in commands]
     lines += ["", "## Kernel durations (`rocprofv3 --kernel-trace --stats`)", "",
