@@ -172,7 +172,7 @@ def make_ssd(cfg, device, dtype):
         orc.ssd_forward(c["u"], c["delta"], c["Bm"], c["Cm"], c["A_neg"])
         orc.ssd_backward(c["dy"], c["u"], c["delta"], c["Bm"], c["Cm"], c["A_neg"])
 
-    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, tokens=B * L,
+    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L,
                 fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=B * L * H * Dh * N * 4,
                 ckpt_bytes=n_ck * 4, io_bytes=n_u * 4 + (n_u + n_d + 2 * n_bc) * es + H * 4)
 
@@ -227,7 +227,7 @@ def make_gla(cfg, device, dtype):
         orc.gla_forward(c["q"], c["k"], c["v"], c["g"])
         orc.gla_backward(c["dy"], c["q"], c["k"], c["v"], c["g"])
 
-    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, tokens=B * L,
+    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L,
                 fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=B * L * H * Dh * Dh * 4,
                 ckpt_bytes=n_ck * 4, io_bytes=n_x * 4 + (3 * n_x + n_g) * es)
 
@@ -282,7 +282,7 @@ def make_rglru(cfg, device, dtype):
         orc.rglru_forward(aa, xx)
         orc.rglru_backward(d["dy"][:Bs].double().cpu().numpy(), aa, xx)
 
-    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, tokens=B * L, cpu_tokens=L,
+    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L, cpu_tokens=L,
                 fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=n * 4, ckpt_bytes=n_ck * 4,
                 io_bytes=n * 4 + 2 * n * es)
 
@@ -339,7 +339,7 @@ def make_rglru_gated(cfg, device, dtype):
         orc.rglru_gated_forward(*xs, lm)
         orc.rglru_gated_backward(d["dy"][:1].double().cpu().numpy(), *xs, lm)
 
-    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, tokens=B * L, cpu_tokens=L,
+    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L, cpu_tokens=L,
                 fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=n * 4, ckpt_bytes=n_ck * 4,
                 io_bytes=n * 4 + 3 * n * es)
 
@@ -391,7 +391,7 @@ def make_rotlru_theta(cfg, device, dtype):
         orc.rotlru_theta_forward(*xs)
         orc.rotlru_theta_backward(d["dy"][:1].double().cpu().numpy(), *xs)
 
-    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, tokens=B * L, cpu_tokens=L,
+    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L, cpu_tokens=L,
                 fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=n_x * 4, ckpt_bytes=n_ck * 4,
                 io_bytes=n_x * 4 + ins)
 
@@ -445,7 +445,7 @@ def make_rotlru(cfg, device, dtype):
         orc.rotlru_forward(*xs)
         orc.rotlru_backward(d["dy"][:1].double().cpu().numpy(), *xs)
 
-    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, tokens=B * L, cpu_tokens=L,
+    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L, cpu_tokens=L,
                 fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=n_x * 4, ckpt_bytes=n_ck * 4,
                 io_bytes=n_x * 4 + (3 * n_p + n_x) * es)
 

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define RR_ABI_VERSION 6
+#define RR_ABI_VERSION 7
 
 enum rr_dtype { RR_F32 = 0, RR_BF16 = 1, RR_F16 = 2 };
 
@@ -63,6 +63,25 @@ const char* rr_last_error(void);
 /* Checkpoint interval T used for (L, seg); 0 if seg/L are invalid.
  * The reference checkpoints every `seg` steps (ssd.py:103-110). */
 int64_t rr_chunk_len(int64_t L, int64_t seg);
+
+/* Errors that kernels report after their launch returned, on the current
+ * device.  No reference counterpart (Metal kernels there have no runtime error
+ * channel).  Waits for the device to finish (hipDeviceSynchronize), then
+ * returns RR_OK, or RR_EHIP if a pass since the last call met an error whose
+ * results it marked invalid (an RG-LRU / rotLRU tile hand-off wait that
+ * expired: the values handed on are NaN); the message names it and the status
+ * is cleared. */
+int rr_async_status(void);
+
+/* Tile schedule of the RG-LRU / rotLRU passes, for tests of the hand-off order.
+ * No reference counterpart.  scan: 0 RG-LRU, 1 gated RG-LRU, 2 rotLRU (D = the
+ * pair count Dp); pass 0 forward, 1 backward.  Returns the number n of
+ * workgroup tickets, or -1 for invalid arguments.  When cap >= n, ticket t runs
+ * step tile tile_k[t] of channel group tile_grp[t] (group = batch row * G +
+ * channel tile), and *max_ckpt_row (nullable) receives the largest checkpoint
+ * row b * nC + c that the backward pass reads (-1 if none or pass 0). */
+int64_t rr_tile_schedule(int scan, int pass, int64_t B, int64_t L, int64_t D, int64_t seg, int dtype,
+                         int32_t* tile_k, int32_t* tile_grp, int64_t* max_ckpt_row, int64_t cap);
 
 /* ------------------------------------------------------------------ SSD --
  * u [B,L,H,Dh], delta [B,L,H], Bm/Cm [B,L,H,N] (dtype); A_neg fp32, element

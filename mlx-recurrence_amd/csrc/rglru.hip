@@ -108,8 +108,8 @@ template <typename InT, int CH, int U, bool GATED>
 __global__ __launch_bounds__(64 * kNW, 4) void rglru_fwd_kernel(
     const InT* __restrict__ a, const InT* __restrict__ x, const InT* __restrict__ gi,
     const float* __restrict__ glam, float gc, const float* __restrict__ h0, float* __restrict__ y,
-    float* __restrict__ ckpt, uint32_t* counter, uint64_t* slots, int B, int L, int D, int T, int nC, int G,
-    int K) {
+    float* __restrict__ ckpt, uint32_t* counter, uint64_t* slots, uint32_t* status, int B, int L, int D, int T,
+    int nC, int G, int K) {
   constexpr int GCH = 64 * CH, S = U * kNW;
   __shared__ float sP[kNW][GCH], sE[kNW][GCH];
   __shared__ float sIn[GCH];
@@ -120,7 +120,8 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_fwd_kernel(
   const int nGrp = B * G;
   const int ticket = rr::tiles::take_ticket(counter, nGrp * K, &sTicket);
   if (ticket < 0) return;
-  const int k = ticket / nGrp, grp = ticket % nGrp;
+  const rr::tiles::TileOfTicket tt = rr::tiles::tile_of_ticket(ticket, nGrp, K, false);
+  const int k = tt.k, grp = tt.grp;
   const int b = grp / G, g = grp % G;
   const int ch = g * GCH + lane * CH;
   const bool cok = ch < D;
@@ -161,7 +162,7 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_fwd_kernel(
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       float hin = 0.f;
-      if (k > 0) hin = rr::tiles::take_value(mine - GCH + c);   // exit state of tile k - 1
+      if (k > 0) hin = rr::tiles::take_value(mine - GCH + c, status);   // exit state of tile k - 1
       else if (h0 != nullptr && cok) hin = h0[(int64_t)b * D + ch + c];
       sIn[lane * CH + c] = hin;
       if (k + 1 < K) {
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_bwd_kernel(
     const InT* __restrict__ x, const InT* __restrict__ gi, const float* __restrict__ glam, float gc,
     const float* __restrict__ h0, const float* __restrict__ ckpt, InT* __restrict__ da, InT* __restrict__ dx,
     InT* __restrict__ dgi, float* __restrict__ dpart, float* __restrict__ dh0, uint32_t* counter,
-    uint64_t* slots, int B, int L, int D, int T, int nC, int G, int K) {
+    uint64_t* slots, uint32_t* status, int B, int L, int D, int T, int nC, int G, int K) {
   constexpr int GCH = 64 * CH, S = U * kNW;
   __shared__ float sP[kNW][GCH], sEf[kNW][GCH], sEb[kNW][GCH];
   __shared__ float sD[GATED ? kNW : 1][GCH];
@@ -212,7 +213,8 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_bwd_kernel(
   const int nGrp = B * G;
   const int ticket = rr::tiles::take_ticket(counter, nGrp * K, &sTicket);
   if (ticket < 0) return;
-  const int k = K - 1 - ticket / nGrp, grp = ticket % nGrp;
+  const rr::tiles::TileOfTicket tt = rr::tiles::tile_of_ticket(ticket, nGrp, K, true);
+  const int k = tt.k, grp = tt.grp;
   const int b = grp / G, g = grp % G;
   const int ch = g * GCH + lane * CH;
   const bool cok = ch < D;
@@ -267,7 +269,7 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_bwd_kernel(
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       float lin = 0.f;   // adjoint entering the tile from later steps
-      if (k + 1 < K) lin = rr::tiles::take_value(mine + GCH + c);
+      if (k + 1 < K) lin = rr::tiles::take_value(mine + GCH + c, status);
       else if (dfinal != nullptr && cok) lin = dfinal[(int64_t)b * D + ch + c];
       sIn[lane * CH + c] = lin;
       float lout = lin;
@@ -289,13 +291,14 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_bwd_kernel(
   // checkpoint interval, then the earlier waves of the interval (the tile
   // holds whole intervals: S is a multiple of 32 >= T)
   const int tb = t0 - t0 % T;
+  const int crow = rr::tiles::bwd_ckpt_row(t0, T, L);
   float hin[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     hin[c] = 0.f;
     if (cok) {
-      if (tb > 0) hin[c] = ckpt[((int64_t)b * nC + tb / T - 1) * D + ch + c];
-      else if (h0 != nullptr) hin[c] = h0[(int64_t)b * D + ch + c];
+      if (crow >= 0) hin[c] = ckpt[((int64_t)b * nC + crow) * D + ch + c];
+      else if (tb == 0 && h0 != nullptr) hin[c] = h0[(int64_t)b * D + ch + c];
     }
     for (int j = w - (t0 - tb) / U; j < w; ++j) hin[c] = sP[j][lane * CH + c] * hin[c] + sEf[j][lane * CH + c];
   }
@@ -424,6 +427,11 @@ size_t gated_ws_bytes(int64_t B, int64_t L, int64_t D, int dtype, int pass) {
 
 }  // namespace
 
+rr::tiles::Geometry rr::rglru_geometry(int64_t L, int64_t D, int dtype, int pass, bool gated) {
+  const TileGrid tg = tile_grid(L, D, pass == 0 ? kFwdCh : kBwdCh, dtype, pass, gated);
+  return rr::tiles::Geometry{tg.G, tg.K, steps_per_wave(dtype, pass, gated), kNW};
+}
+
 extern "C" size_t rr_rglru_workspace_bytes(int64_t B, int64_t L, int64_t D, int64_t seg, int dtype,
                                            int pass) {
   if (B <= 0 || L <= 0 || D <= 0 || rr::chunk_len(L, seg) == 0 || !rr::valid_dtype(dtype)) return 0;
@@ -440,14 +448,16 @@ extern "C" int rr_rglru_fwd(const void* a, const void* x, int dtype, int64_t B, 
   const int T = (int)rr::chunk_len(L, seg);
   const int nC = (int)(L / T);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* status = rr::status_word();
+  if (status == nullptr) return RR_EHIP;
   if (int rc = rr::tiles::launch_clear(workspace, need, s)) return rc;
   RR_DISPATCH_DTYPE(dtype, {
     constexpr int U = steps_per_wave<InT, false, false>();
     const TileGrid tg = tile_grid(L, D, kFwdCh, dtype, 0);
     hipLaunchKernelGGL((rglru_fwd_kernel<InT, kFwdCh, U, false>), dim3((unsigned)(B * tg.tiles())), dim3(64 * kNW),
                        0, s, static_cast<const InT*>(a), static_cast<const InT*>(x), nullptr, nullptr, 0.f, h0, y,
-                       ckpt, rr::tiles::ws_counter(workspace), rr::tiles::ws_slots(workspace), (int)B, (int)L,
-                       (int)D, T, nC, tg.G, tg.K);
+                       ckpt, rr::tiles::ws_counter(workspace), rr::tiles::ws_slots(workspace), status, (int)B,
+                       (int)L, (int)D, T, nC, tg.G, tg.K);
   });
   return rr::check_launch("rr_rglru_fwd");
 }
@@ -465,6 +475,8 @@ extern "C" int rr_rglru_bwd(const float* dy, const float* dfinal, const void* a,
   const int T = (int)rr::chunk_len(L, seg);
   const int nC = (int)(L / T);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* status = rr::status_word();
+  if (status == nullptr) return RR_EHIP;
   if (int rc = rr::tiles::launch_clear(workspace, need, s)) return rc;
   RR_DISPATCH_DTYPE(dtype, {
     constexpr int U = steps_per_wave<InT, true, false>();
@@ -472,8 +484,8 @@ extern "C" int rr_rglru_bwd(const float* dy, const float* dfinal, const void* a,
     hipLaunchKernelGGL((rglru_bwd_kernel<InT, kBwdCh, U, false>), dim3((unsigned)(B * tg.tiles())), dim3(64 * kNW),
                        0, s, dy, dfinal, static_cast<const InT*>(a), static_cast<const InT*>(x), nullptr, nullptr,
                        0.f, h0, ckpt, static_cast<InT*>(da), static_cast<InT*>(dx), nullptr, nullptr, dh0,
-                       rr::tiles::ws_counter(workspace), rr::tiles::ws_slots(workspace), (int)B, (int)L, (int)D, T,
-                       nC, tg.G, tg.K);
+                       rr::tiles::ws_counter(workspace), rr::tiles::ws_slots(workspace), status, (int)B, (int)L, (int)D,
+                       T, nC, tg.G, tg.K);
   });
   return rr::check_launch("rr_rglru_bwd");
 }
@@ -496,14 +508,16 @@ extern "C" int rr_rglru_gated_fwd(const void* r, const void* i, const void* x, c
   const int T = (int)rr::chunk_len(L, seg);
   const int nC = (int)(L / T);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* status = rr::status_word();
+  if (status == nullptr) return RR_EHIP;
   if (int rc = rr::tiles::launch_clear(workspace, need, s)) return rc;
   RR_DISPATCH_DTYPE(dtype, {
     constexpr int U = steps_per_wave<InT, false, true>();
     const TileGrid tg = tile_grid(L, D, kFwdCh, dtype, 0, true);
     hipLaunchKernelGGL((rglru_fwd_kernel<InT, kFwdCh, U, true>), dim3((unsigned)(B * tg.tiles())), dim3(64 * kNW), 0,
                        s, static_cast<const InT*>(r), static_cast<const InT*>(x), static_cast<const InT*>(i), lam,
-                       c, h0, y, ckpt, rr::tiles::ws_counter(workspace), rr::tiles::ws_slots(workspace), (int)B,
-                       (int)L, (int)D, T, nC, tg.G, tg.K);
+                       c, h0, y, ckpt, rr::tiles::ws_counter(workspace), rr::tiles::ws_slots(workspace), status,
+                       (int)B, (int)L, (int)D, T, nC, tg.G, tg.K);
   });
   return rr::check_launch("rr_rglru_gated_fwd");
 }
@@ -523,6 +537,8 @@ extern "C" int rr_rglru_gated_bwd(const float* dy, const float* dfinal, const vo
   const int T = (int)rr::chunk_len(L, seg);
   const int nC = (int)(L / T);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* status = rr::status_word();
+  if (status == nullptr) return RR_EHIP;
   // only the hand-off words need clearing; every tile writes its row of sums
   if (int rc = rr::tiles::launch_clear(workspace, ws_bytes_for(B, L, D, dtype, 1, true), s)) return rc;
   float* dpart = reinterpret_cast<float*>(static_cast<char*>(workspace) + gated_part_offset(B, L, D, dtype));
@@ -533,7 +549,7 @@ extern "C" int rr_rglru_gated_bwd(const float* dy, const float* dfinal, const vo
                        s, dy, dfinal, static_cast<const InT*>(r), static_cast<const InT*>(x),
                        static_cast<const InT*>(i), lam, c, h0, ckpt, static_cast<InT*>(dr), static_cast<InT*>(dx),
                        static_cast<InT*>(di), dpart, dh0, rr::tiles::ws_counter(workspace),
-                       rr::tiles::ws_slots(workspace), (int)B, (int)L, (int)D, T, nC, tg.G, tg.K);
+                       rr::tiles::ws_slots(workspace), status, (int)B, (int)L, (int)D, T, nC, tg.G, tg.K);
   });
   if (int rc = rr::check_launch("rr_rglru_gated_bwd")) return rc;
   hipLaunchKernelGGL(rglru_dlam_kernel, dim3((unsigned)((D + 63) / 64)), dim3(64 * kDlamWaves), 0, s, dpart, lam, c,

@@ -93,8 +93,8 @@ template <typename InT, bool TH>
 __global__ __launch_bounds__(64 * kNW, 4) void rotlru_fwd_kernel(
     const InT* __restrict__ a, const InT* __restrict__ cs, const InT* __restrict__ sn,
     const InT* __restrict__ x, const float* __restrict__ h0, float* __restrict__ y,
-    float* __restrict__ ckpt, uint32_t* counter, uint64_t* slots, int B, int L, int Dp, int T, int nC,
-    int G, int K) {
+    float* __restrict__ ckpt, uint32_t* counter, uint64_t* slots, uint32_t* status, int B, int L, int Dp, int T,
+    int nC, int G, int K) {
   constexpr int GP = 64 * kCP, S = kU * kNW;
   __shared__ cplx sP[kNW][GP], sE[kNW][GP];
   __shared__ cplx sIn[GP];
@@ -103,7 +103,8 @@ __global__ __launch_bounds__(64 * kNW, 4) void rotlru_fwd_kernel(
   const int nGrp = B * G;
   const int ticket = rr::tiles::take_ticket(counter, nGrp * K, &sTicket);
   if (ticket < 0) return;
-  const int k = ticket / nGrp, grp = ticket % nGrp;
+  const rr::tiles::TileOfTicket tt = rr::tiles::tile_of_ticket(ticket, nGrp, K, false);
+  const int k = tt.k, grp = tt.grp;
   const int b = grp / G, g = grp % G;
   const int p = g * GP + lane * kCP;
   const bool pok = p < Dp;
@@ -132,8 +133,8 @@ __global__ __launch_bounds__(64 * kNW, 4) void rotlru_fwd_kernel(
     for (int q = 0; q < kCP; ++q) {
       cplx hin{0.f, 0.f};
       if (k > 0) {
-        hin.r = rr::tiles::take_value(mine - 2 * GP + 2 * q);
-        hin.i = rr::tiles::take_value(mine - 2 * GP + 2 * q + 1);
+        hin.r = rr::tiles::take_value(mine - 2 * GP + 2 * q, status);
+        hin.i = rr::tiles::take_value(mine - 2 * GP + 2 * q + 1, status);
       } else if (h0 != nullptr && pok) {
         hin = {h0[(int64_t)b * D + 2 * (p + q)], h0[(int64_t)b * D + 2 * (p + q) + 1]};
       }
@@ -182,7 +183,7 @@ __global__ __launch_bounds__(64 * kNW, 2) void rotlru_bwd_kernel(
     const InT* __restrict__ cs, const InT* __restrict__ sn, const InT* __restrict__ x,
     const float* __restrict__ h0, const float* __restrict__ ckpt, InT* __restrict__ da,
     InT* __restrict__ dcs, InT* __restrict__ dsn, InT* __restrict__ dx, float* __restrict__ dh0,
-    uint32_t* counter, uint64_t* slots, int B, int L, int Dp, int T, int nC, int G, int K) {
+    uint32_t* counter, uint64_t* slots, uint32_t* status, int B, int L, int Dp, int T, int nC, int G, int K) {
   constexpr int GP = 64 * kCP, S = kU * kNW;
   __shared__ cplx sP[kNW][GP], sEf[kNW][GP], sEb[kNW][GP];
   __shared__ cplx sIn[GP];
@@ -191,7 +192,8 @@ __global__ __launch_bounds__(64 * kNW, 2) void rotlru_bwd_kernel(
   const int nGrp = B * G;
   const int ticket = rr::tiles::take_ticket(counter, nGrp * K, &sTicket);
   if (ticket < 0) return;
-  const int k = K - 1 - ticket / nGrp, grp = ticket % nGrp;
+  const rr::tiles::TileOfTicket tt = rr::tiles::tile_of_ticket(ticket, nGrp, K, true);
+  const int k = tt.k, grp = tt.grp;
   const int b = grp / G, g = grp % G;
   const int p = g * GP + lane * kCP;
   const bool pok = p < Dp;
@@ -240,8 +242,8 @@ __global__ __launch_bounds__(64 * kNW, 2) void rotlru_bwd_kernel(
     for (int q = 0; q < kCP; ++q) {
       cplx lin{0.f, 0.f};   // adjoint entering the tile from later steps
       if (k + 1 < K) {
-        lin.r = rr::tiles::take_value(mine + 2 * GP + 2 * q);
-        lin.i = rr::tiles::take_value(mine + 2 * GP + 2 * q + 1);
+        lin.r = rr::tiles::take_value(mine + 2 * GP + 2 * q, status);
+        lin.i = rr::tiles::take_value(mine + 2 * GP + 2 * q + 1, status);
       } else if (dfinal != nullptr && pok) {
         lin = {dfinal[(int64_t)b * D + 2 * (p + q)], dfinal[(int64_t)b * D + 2 * (p + q) + 1]};
       }
@@ -261,6 +263,7 @@ __global__ __launch_bounds__(64 * kNW, 2) void rotlru_bwd_kernel(
   __syncthreads();
   cplx lam[kCP], hin[kCP];
   const int tb = t0 - t0 % T;   // start of the checkpoint interval (inside the tile: S % 32 == 0)
+  const int crow = rr::tiles::bwd_ckpt_row(t0, T, L);
 #pragma unroll
   for (int q = 0; q < kCP; ++q) {
     lam[q] = sIn[lane * kCP + q];
@@ -268,8 +271,8 @@ __global__ __launch_bounds__(64 * kNW, 2) void rotlru_bwd_kernel(
     hin[q] = {0.f, 0.f};
     if (pok) {
       const int64_t e = 2 * (p + q);
-      if (tb > 0) hin[q] = {ckpt[((int64_t)b * nC + tb / T - 1) * D + e], ckpt[((int64_t)b * nC + tb / T - 1) * D + e + 1]};
-      else if (h0 != nullptr) hin[q] = {h0[(int64_t)b * D + e], h0[(int64_t)b * D + e + 1]};
+      if (crow >= 0) hin[q] = {ckpt[((int64_t)b * nC + crow) * D + e], ckpt[((int64_t)b * nC + crow) * D + e + 1]};
+      else if (tb == 0 && h0 != nullptr) hin[q] = {h0[(int64_t)b * D + e], h0[(int64_t)b * D + e + 1]};
     }
     for (int j = w - (t0 - tb) / kU; j < w; ++j) hin[q] = cfma(sP[j][lane * kCP + q], hin[q], sEf[j][lane * kCP + q]);
   }
@@ -331,6 +334,11 @@ size_t ws_bytes_for(int64_t B, int64_t L, int64_t Dp) {
 
 }  // namespace
 
+rr::tiles::Geometry rr::rotlru_geometry(int64_t L, int64_t Dp) {
+  const TileGrid tg = tile_grid(L, Dp);
+  return rr::tiles::Geometry{tg.G, tg.K, kU, kNW};
+}
+
 extern "C" size_t rr_rotlru_workspace_bytes(int64_t B, int64_t L, int64_t Dp, int64_t seg, int dtype,
                                             int pass) {
   (void)pass;
@@ -349,13 +357,15 @@ extern "C" int rr_rotlru_fwd(const void* a, const void* cs, const void* sn, cons
   const int nC = (int)(L / T);
   const TileGrid tg = tile_grid(L, Dp);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* status = rr::status_word();
+  if (status == nullptr) return RR_EHIP;
   if (int rc = rr::tiles::launch_clear(workspace, need, s)) return rc;
   RR_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((rotlru_fwd_kernel<InT, false>), dim3((unsigned)(B * tg.tiles())),
                                               dim3(64 * kNW), 0, s, static_cast<const InT*>(a),
                                               static_cast<const InT*>(cs), static_cast<const InT*>(sn),
                                               static_cast<const InT*>(x), h0, y, ckpt,
                                               rr::tiles::ws_counter(workspace), rr::tiles::ws_slots(workspace),
-                                              (int)B, (int)L, (int)Dp, T, nC, tg.G, tg.K));
+                                              status, (int)B, (int)L, (int)Dp, T, nC, tg.G, tg.K));
   return rr::check_launch("rr_rotlru_fwd");
 }
 
@@ -373,6 +383,8 @@ extern "C" int rr_rotlru_bwd(const float* dy, const float* dfinal, const void* a
   const int nC = (int)(L / T);
   const TileGrid tg = tile_grid(L, Dp);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* status = rr::status_word();
+  if (status == nullptr) return RR_EHIP;
   if (int rc = rr::tiles::launch_clear(workspace, need, s)) return rc;
   RR_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((rotlru_bwd_kernel<InT, false>), dim3((unsigned)(B * tg.tiles())),
                                               dim3(64 * kNW), 0, s, dy, dfinal, static_cast<const InT*>(a),
@@ -380,7 +392,7 @@ extern "C" int rr_rotlru_bwd(const float* dy, const float* dfinal, const void* a
                                               static_cast<const InT*>(x), h0, ckpt, static_cast<InT*>(da),
                                               static_cast<InT*>(dcs), static_cast<InT*>(dsn),
                                               static_cast<InT*>(dx), dh0, rr::tiles::ws_counter(workspace),
-                                              rr::tiles::ws_slots(workspace), (int)B, (int)L, (int)Dp, T, nC,
+                                              rr::tiles::ws_slots(workspace), status, (int)B, (int)L, (int)Dp, T, nC,
                                               tg.G, tg.K));
   return rr::check_launch("rr_rotlru_bwd");
 }
@@ -396,12 +408,14 @@ extern "C" int rr_rotlru_theta_fwd(const void* a, const void* theta, const void*
   const int nC = (int)(L / T);
   const TileGrid tg = tile_grid(L, Dp);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* status = rr::status_word();
+  if (status == nullptr) return RR_EHIP;
   if (int rc = rr::tiles::launch_clear(workspace, need, s)) return rc;
   RR_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((rotlru_fwd_kernel<InT, true>), dim3((unsigned)(B * tg.tiles())),
                                               dim3(64 * kNW), 0, s, static_cast<const InT*>(a),
                                               static_cast<const InT*>(theta), nullptr, static_cast<const InT*>(x),
                                               h0, y, ckpt, rr::tiles::ws_counter(workspace),
-                                              rr::tiles::ws_slots(workspace), (int)B, (int)L, (int)Dp, T, nC,
+                                              rr::tiles::ws_slots(workspace), status, (int)B, (int)L, (int)Dp, T, nC,
                                               tg.G, tg.K));
   return rr::check_launch("rr_rotlru_theta_fwd");
 }
@@ -419,13 +433,15 @@ extern "C" int rr_rotlru_theta_bwd(const float* dy, const float* dfinal, const v
   const int nC = (int)(L / T);
   const TileGrid tg = tile_grid(L, Dp);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* status = rr::status_word();
+  if (status == nullptr) return RR_EHIP;
   if (int rc = rr::tiles::launch_clear(workspace, need, s)) return rc;
   RR_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((rotlru_bwd_kernel<InT, true>), dim3((unsigned)(B * tg.tiles())),
                                               dim3(64 * kNW), 0, s, dy, dfinal, static_cast<const InT*>(a),
                                               static_cast<const InT*>(theta), nullptr, static_cast<const InT*>(x),
                                               h0, ckpt, static_cast<InT*>(da), static_cast<InT*>(dtheta), nullptr,
                                               static_cast<InT*>(dx), dh0, rr::tiles::ws_counter(workspace),
-                                              rr::tiles::ws_slots(workspace), (int)B, (int)L, (int)Dp, T, nC,
+                                              rr::tiles::ws_slots(workspace), status, (int)B, (int)L, (int)Dp, T, nC,
                                               tg.G, tg.K));
   return rr::check_launch("rr_rotlru_theta_bwd");
 }

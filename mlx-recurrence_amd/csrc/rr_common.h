@@ -44,6 +44,12 @@ void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int check_launch(const char* what);
 
+// Device address of the library's status word on the current device (a
+// 32-bit __device__ variable; kernels OR error bits into it, rr_async_status
+// reads and clears it), or nullptr with the error set.  Looked up once per
+// device.
+uint32_t* status_word();
+
 // Checkpoint interval: the largest power of two <= 32 that divides seg.
 inline int64_t chunk_len(int64_t L, int64_t seg) {
   if (seg <= 0 || L <= 0 || L % seg != 0) return 0;

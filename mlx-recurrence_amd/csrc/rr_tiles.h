@@ -16,6 +16,9 @@
 //     (each tile waits for exactly its predecessor);
 //   - the spin is bounded (kMaxSpin) so the kernel terminates whatever
 //     happens, and tickets beyond the tile count end their workgroup at once;
+//     a wait that expires sets a bit in the library's device status word
+//     (read by rr_async_status) and hands on NaN, so the pass's results are
+//     visibly invalid instead of silently wrong;
 //   - the workspace is cleared by clear_kernel before each pass, and a pass
 //     also leaves it clear: a consumer zeroes the slot it has read and the
 //     holder of the last ticket zeroes the counter (so a pass replayed
@@ -30,8 +33,36 @@ namespace rr {
 namespace tiles {
 
 constexpr uint32_t kTag = 1;           // "published in this pass"
-constexpr int kMaxSpin = 1 << 20;      // bounded wait (tens of ms): never reached in practice
+constexpr int kMaxSpin = 1 << 20;      // bounded wait (about a second): never reached in practice
 constexpr int kWsHeader = 64;          // u32 words before the hand-off slots (counter at [0])
+constexpr uint32_t kStatusSpinExpired = 1;   // bit of the device status word (rr_async_status)
+
+// ---------------------------------------------------------------- schedule
+// Tickets map to tiles so that a tile's predecessor (the tile of the same
+// channels one step tile earlier, or later in a reverse-time pass) always
+// holds a smaller ticket: tickets run over the nGrp channel groups fastest and
+// over the K step tiles slowest.  A workgroup takes its ticket only once it
+// runs, so every workgroup it waits for has started and, by induction over
+// the tickets, finishes: no wait depends on a workgroup that is not resident.
+struct TileOfTicket {
+  int k;     // step tile
+  int grp;   // channel group (batch row * G + channel tile)
+};
+__host__ __device__ inline TileOfTicket tile_of_ticket(int ticket, int nGrp, int K, bool reverse_time) {
+  const int slow = ticket / nGrp;
+  return TileOfTicket{reverse_time ? K - 1 - slow : slow, ticket % nGrp};
+}
+
+// Checkpoint interval start of the backward: the steps t0 .. of a wave resume
+// from the checkpoint written after step tb - 1, tb = t0 - t0 % T (row
+// tb / T - 1 of the batch row's nC checkpoints), or from the initial state
+// when tb = 0.  Waves wholly past L (padding of the last step tile) read
+// nothing.  Returns the checkpoint row, or -1 when no checkpoint is read.
+__host__ __device__ inline int bwd_ckpt_row(int t0, int T, int L) {
+  if (t0 >= L) return -1;
+  const int tb = t0 - t0 % T;
+  return tb > 0 ? tb / T - 1 : -1;
+}
 
 // ---------------------------------------------------------------- packed loads
 // N consecutive elements of an input, kept packed in registers.
@@ -129,15 +160,24 @@ __device__ __forceinline__ void publish(uint64_t* slot, float v) {
 }
 
 // Waits (bounded) until `slot` holds a published value, clears the slot (its
-// only reader is the caller) and returns the value.
-__device__ __forceinline__ float take_value(uint64_t* slot) {
+// only reader is the caller) and returns the value.  If the wait expires, the
+// expiry is recorded in *status and the value returned is NaN.
+__device__ __forceinline__ float take_value(uint64_t* slot, uint32_t* status) {
   uint64_t word = 0;
+  bool got = false;
   for (int spin = 0; spin < kMaxSpin; ++spin) {
     word = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((uint32_t)(word >> 32) == kTag) break;
+    if ((uint32_t)(word >> 32) == kTag) {
+      got = true;
+      break;
+    }
     __builtin_amdgcn_s_sleep(1);
   }
   __hip_atomic_store(slot, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (!got) {
+    __hip_atomic_fetch_or(status, kStatusSpinExpired, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __builtin_nanf("");
+  }
   return __uint_as_float((uint32_t)word);
 }
 
@@ -181,5 +221,17 @@ inline uint64_t* ws_slots(void* ws) {
   return reinterpret_cast<uint64_t*>(static_cast<uint32_t*>(ws) + kWsHeader);
 }
 
+// Geometry of a pass: G channel tiles per batch row, K step tiles, U steps
+// per wave, NW waves per workgroup (a tile spans NW * U steps).
+struct Geometry {
+  int G, K, U, NW;
+};
+
 }  // namespace tiles
+
+// Pass geometries of rglru.hip (gated: the fused-gate kernels) and
+// rotlru.hip (Dp pairs), as their entry points launch them.
+tiles::Geometry rglru_geometry(int64_t L, int64_t D, int dtype, int pass, bool gated);
+tiles::Geometry rotlru_geometry(int64_t L, int64_t Dp);
+
 }  // namespace rr

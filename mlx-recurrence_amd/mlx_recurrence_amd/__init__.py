@@ -25,6 +25,7 @@ from .rglru import (rglru_scan, rglru_scan_with_state, rglru_scan_reference, rgl
 from .rotlru import (rotlru_scan, rotlru_scan_with_state, rotlru_scan_reference, rotlru_theta_scan,
                      rotlru_theta_scan_with_state)
 from ._chassis import DEFAULT_SEG, SIMD_WIDTH, get_or_build_kernel, check_segment_shape, parity_check
+from ._lib import async_status
 
 __all__ = [
     "ssd_scan",
@@ -49,6 +50,7 @@ __all__ = [
     "get_or_build_kernel",
     "check_segment_shape",
     "parity_check",
+    "async_status",
 ]
 
 __version__ = "0.3.0+gfx950"

@@ -36,6 +36,8 @@ _SIGS = {
     "rr_abi_version": (_c_int, []),
     "rr_last_error": (ctypes.c_char_p, []),
     "rr_chunk_len": (_c_i64, [_c_i64, _c_i64]),
+    "rr_async_status": (_c_int, []),
+    "rr_tile_schedule": (_c_i64, [_c_int, _c_int] + [_c_i64] * 4 + [_c_int] + [_c_ptr] * 3 + [_c_i64]),
     "rr_ssd_workspace_bytes": (_c_size, [_c_i64] * 7 + [_c_int, _c_int]),
     "rr_ssd_fwd": (_c_int, [_c_ptr] * 5 + [_c_i64, _c_int] + [_c_i64] * 6 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
     "rr_ssd_bwd": (_c_int, [_c_ptr] * 7 + [_c_i64, _c_int] + [_c_i64] * 6 + [_c_ptr] * 9 + [_c_size, _c_ptr]),
@@ -87,6 +89,29 @@ def abi_version() -> int:
 
 def chunk_len(L: int, seg: int) -> int:
     return int(load().rr_chunk_len(L, seg))
+
+
+def async_status() -> None:
+    """Synchronise the current device and raise RuntimeError if a kernel since
+    the last check reported an error after its launch returned (an expired
+    tile hand-off wait: that pass's results are NaN)."""
+    _check(load().rr_async_status(), "rr_async_status")
+
+
+def tile_schedule(scan: int, pass_: int, B: int, L: int, D: int, seg: int, dtype: int):
+    """(tile_k, tile_grp, max_ckpt_row) per workgroup ticket of an RG-LRU
+    (scan 0), gated RG-LRU (1) or rotLRU (2, D = pairs) pass, as numpy arrays."""
+    import numpy as np
+    lib = load()
+    n = int(lib.rr_tile_schedule(scan, pass_, B, L, D, seg, dtype, None, None, None, 0))
+    if n < 0:
+        raise ValueError(lib.rr_last_error().decode())
+    k = np.empty(n, dtype=np.int32)
+    g = np.empty(n, dtype=np.int32)
+    worst = ctypes.c_int64(0)
+    lib.rr_tile_schedule(scan, pass_, B, L, D, seg, dtype, k.ctypes.data_as(_c_ptr), g.ctypes.data_as(_c_ptr),
+                         ctypes.byref(worst), n)
+    return k, g, int(worst.value)
 
 
 def _check(rc: int, what: str) -> None:

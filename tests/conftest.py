@@ -14,3 +14,21 @@ for p in (ROOT, ROOT / "mlx-recurrence_amd"):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a ROCm GPU (MI355X) and the built HIP library")
+
+
+import pytest  # noqa: E402
+
+
+@pytest.fixture(autouse=True)
+def _kernel_status_after_gpu_tests(request):
+    """After every GPU test: synchronise and fail the test if a kernel reported
+    an error after its launch returned (rr_async_status, e.g. an expired tile
+    hand-off wait whose results were NaN-marked)."""
+    yield
+    if request.node.get_closest_marker("gpu") is None:
+        return
+    import torch
+    if not torch.cuda.is_available():
+        return
+    from mlx_recurrence_amd import _lib
+    _lib.async_status()

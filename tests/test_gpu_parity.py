@@ -87,25 +87,46 @@ def test_rglru_parity(B, L, D, seg, dtype, gates, h0, dfinal, seed):
 
 
 RGLRU_GATED_CASES = [
-    # (B, L, D, seg, dtype, h0, dfinal, seed)
-    (2, 64, 64, 32, F32, False, False, 20),
-    (1, 32, 32, 32, F32, True, True, 21),        # L == seg, one tile
-    (3, 200, 96, 8, F32, True, True, 22),        # T = 8; D and L not tile multiples
-    (2, 1024, 320, 32, BF16, True, True, 23),
-    (2, 512, 128, 16, F16, False, True, 24),
-    (8, 4096, 2560, 32, BF16, False, False, 25),  # BASELINE config 3 shape, full size
+    # (B, L, D, seg, dtype, lam, h0, dfinal, seed); lam "cfg": BASELINE config 3's
+    # a_t = U(0.9, 0.999)^(8 sigmoid(r)), i.e. softplus(lam) = -log U (most
+    # elements in the kernel's 1 - a^2 series branch, 2z > -1/8); "raw":
+    # lam = log U passed straight in (a_t = exp(-8 softplus(log U) sigmoid(r)),
+    # mostly the direct branch); "near1": a -> 1 (very negative lam or r, so
+    # sqrt(1 - a^2) -> 0 and its derivative grows)
+    (2, 64, 64, 32, F32, "raw", False, False, 20),
+    (2, 64, 64, 32, F32, "cfg", False, False, 27),
+    (1, 32, 32, 32, F32, "cfg", True, True, 21),        # L == seg, one tile
+    (3, 200, 96, 8, F32, "cfg", True, True, 22),        # T = 8; D and L not tile multiples
+    (2, 1024, 320, 32, BF16, "cfg", True, True, 23),
+    (2, 512, 128, 16, F16, "raw", False, True, 24),
+    (2, 256, 192, 32, F32, "near1", True, True, 28),
+    (2, 256, 192, 32, BF16, "near1", False, True, 29),
+    (8, 4096, 2560, 32, BF16, "cfg", False, False, 25),  # BASELINE config 3, full size
 ]
 
 
-@pytest.mark.parametrize("B,L,D,seg,dtype,h0,dfinal,seed", RGLRU_GATED_CASES)
-def test_rglru_gated_parity(B, L, D, seg, dtype, h0, dfinal, seed):
-    """Fused gate math + scan against the oracle's gates composed with its scan."""
-    _announce("rglru_gated", B=B, L=L, D=D, seg=seg, dtype=dtype, h0=h0, seed=seed)
-    rng = np.random.default_rng(seed)
+def _gated_inputs(rng, B, L, D, lam_kind):
     r = rng.standard_normal((B, L, D))
     i = _sigmoid(rng.standard_normal((B, L, D)))
     x = rng.standard_normal((B, L, D))
-    lam = np.log(rng.uniform(0.9, 0.999, D))     # BASELINE config 3's Lambda
+    base = rng.uniform(0.9, 0.999, D)
+    if lam_kind == "raw":
+        lam = np.log(base)
+    else:   # softplus(lam) = -log(base): the inverse softplus, as bench.py's config-3 workload
+        lam = np.log(np.expm1(-np.log(base)))
+    if lam_kind == "near1":
+        lam[0::3] = -12.0                        # c softplus(lam) ~ 5e-5: a within 5e-5 of 1
+        lam[1::3] = -25.0                        # ~ 1e-10: a rounds to 1 in fp32 for most r
+        r[:, :, 2::3] = -16.0 + r[:, :, 2::3]   # sigmoid(r) ~ 1e-7
+    return r, i, x, lam
+
+
+@pytest.mark.parametrize("B,L,D,seg,dtype,lam_kind,h0,dfinal,seed", RGLRU_GATED_CASES)
+def test_rglru_gated_parity(B, L, D, seg, dtype, lam_kind, h0, dfinal, seed):
+    """Fused gate math + scan against the oracle's gates composed with its scan."""
+    _announce("rglru_gated", B=B, L=L, D=D, seg=seg, dtype=dtype, lam=lam_kind, h0=h0, seed=seed)
+    rng = np.random.default_rng(seed)
+    r, i, x, lam = _gated_inputs(rng, B, L, D, lam_kind)
     rt, it, xt = (to_dev(v, dtype, True) for v in (r, i, x))
     lt = to_dev(lam, F32, True)
     h0t = to_dev(rng.standard_normal((B, D)), F32, True) if h0 else None
@@ -129,6 +150,15 @@ def test_rglru_gated_parity(B, L, D, seg, dtype, h0, dfinal, seed):
     check("grad_lam", lt.grad, dl_o, TOL[F32] if dtype == F32 else tol, rep)
     if h0:
         check("grad_h0", h0t.grad, dh0_o, tol, rep)
+    if lam_kind == "near1":
+        # the a -> 1 channels on their own scale (normalised over the whole
+        # tensor, their small gradients would hide behind the others)
+        for grp in range(3):
+            sl = (Ellipsis, slice(grp, None, 3))
+            check(f"y[{grp}::3]", y[sl], y_o[sl], TOL[F32] if dtype == F32 else tol, rep)
+            check(f"grad_r[{grp}::3]", rt.grad[sl], dr_o[sl], tol, rep)
+            check(f"grad_x[{grp}::3]", xt.grad[sl], dx_o[sl], tol, rep)
+            check(f"grad_lam[{grp}::3]", lt.grad[sl], dl_o[sl], TOL[F32] if dtype == F32 else tol, rep)
     print(rep, flush=True)
 
 
