@@ -45,6 +45,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "SSD/GLA fwd+bwd tokens/s at B3·L512·H12·Dh64; achieved HBM GB/s % of peak"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # dense bf16 MFMA, MI355X
 
 
 # ------------------------------------------------------------------ HIP graph
@@ -105,6 +106,16 @@ class _Hip:
 
 
 # ------------------------------------------------------------------ workloads
+def _host_copies(cache, d, keys, steps=None):
+    """fp32 host copies of device inputs, optionally their first `steps` steps
+    (made once, outside the timed CPU runs)."""
+    for k in keys:
+        if k not in cache:
+            v = d[k] if steps is None else d[k][:, :steps]
+            cache[k] = v.float().cpu().contiguous()
+    return {k: cache[k].detach() for k in keys}
+
+
 def _gen(shape, gen, kind="normal"):
     import torch
     if kind == "normal":
@@ -166,13 +177,21 @@ def make_ssd(cfg, device, dtype):
         y = mr.ssd_scan(*xs, A_[:, None].expand(H, N), seg=seg)
         y.backward(d["dy"])
 
-    def cpu_sample():
-        from oracle import recurrence_oracle as orc
-        c = {k: v.to(dtype).double().numpy() if k not in ("A_neg", "dy") else v.double().numpy() for k, v in cpu.items()}
-        orc.ssd_forward(c["u"], c["delta"], c["Bm"], c["Cm"], c["A_neg"])
-        orc.ssd_backward(c["dy"], c["u"], c["delta"], c["Bm"], c["Cm"], c["A_neg"])
+    # CPU leg: the reference's per-step loop (ssd_scan_reference, fp32 torch on
+    # the host) with autograd, on the same input values; config 4's sample is
+    # one batch row and 256 steps (its full autograd tape would hold ~86 GB)
+    cb, cl = (1, 256) if B * L * H * Dh * N > (1 << 28) else (B, L)
 
-    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L,
+    def cpu_sample():
+        import mlx_recurrence_amd as mr
+        xs = [cpu[k][:cb, :cl].to(dtype).float().requires_grad_(True) for k in ("u", "delta", "Bm", "Cm")]
+        A_ = cpu["A_neg"][:, 0].clone().requires_grad_(True)
+        y = mr.ssd_scan_reference(*xs, A_[:, None].expand(H, N))
+        y.backward(cpu["dy"][:cb, :cl])
+
+    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L, cpu_tokens=cb * cl,
+                cpu_desc=f"B={cb} L={cl}" + (" of the workload (full batch and length)" if (cb, cl) == (B, L)
+                                              else f" of the workload's B={B} L={L} (same H, Dh, N)"),
                 fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=B * L * H * Dh * N * 4,
                 ckpt_bytes=n_ck * 4, io_bytes=n_u * 4 + (n_u + n_d + 2 * n_bc) * es + H * 4)
 
@@ -221,13 +240,13 @@ def make_gla(cfg, device, dtype):
         y = mr.gla_scan(*xs, seg=seg)
         y.backward(d["dy"])
 
-    def cpu_sample():
-        from oracle import recurrence_oracle as orc
-        c = {kk: vv.to(dtype).double().numpy() if kk != "dy" else vv.double().numpy() for kk, vv in cpu.items()}
-        orc.gla_forward(c["q"], c["k"], c["v"], c["g"])
-        orc.gla_backward(c["dy"], c["q"], c["k"], c["v"], c["g"])
+    def cpu_sample():   # gla_scan_reference (fp32 torch, host) with autograd, full shape
+        import mlx_recurrence_amd as mr
+        xs = [cpu[kk].to(dtype).float().requires_grad_(True) for kk in ("q", "k", "v", "g")]
+        mr.gla_scan_reference(*xs).backward(cpu["dy"])
 
-    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L,
+    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L, cpu_tokens=B * L,
+                cpu_desc=f"B={B} L={L} of the workload (full batch and length)",
                 fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=B * L * H * Dh * Dh * 4,
                 ckpt_bytes=n_ck * 4, io_bytes=n_x * 4 + (3 * n_x + n_g) * es)
 
@@ -274,15 +293,17 @@ def make_rglru(cfg, device, dtype):
         a_, x_ = (d[kk].detach().requires_grad_(True) for kk in ("a", "x"))
         mr.rglru_scan(a_, x_, seg=seg).backward(d["dy"])
 
-    def cpu_sample():
-        from oracle import recurrence_oracle as orc
-        Bs = 1  # one batch row of the workload
-        aa = d["a"][:Bs].double().cpu().numpy()
-        xx = d["x"][:Bs].double().cpu().numpy()
-        orc.rglru_forward(aa, xx)
-        orc.rglru_backward(d["dy"][:Bs].double().cpu().numpy(), aa, xx)
+    host = {}
+    cl = min(L, 512)   # CPU sample: the first 512 steps (per-token cost of the loop does not depend on L)
 
-    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L, cpu_tokens=L,
+    def cpu_sample():   # rglru_scan_reference (fp32 torch, host) with autograd, full shape
+        import mlx_recurrence_amd as mr
+        h = _host_copies(host, d, ("a", "x"), cl)
+        a_, x_ = (h[kk].requires_grad_(True) for kk in ("a", "x"))
+        mr.rglru_scan_reference(a_, x_).backward(dy[:, :cl])
+
+    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L, cpu_tokens=B * cl,
+                cpu_desc=f"B={B}, the first L={cl} of L={L} steps",
                 fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=n * 4, ckpt_bytes=n_ck * 4,
                 io_bytes=n * 4 + 2 * n * es)
 
@@ -332,14 +353,18 @@ def make_rglru_gated(cfg, device, dtype):
         xs = [d[kk].detach().requires_grad_(True) for kk in ("r", "i", "x", "lam")]
         mr.rglru_gated_scan(*xs, 8.0, seg=seg).backward(d["dy"])
 
-    def cpu_sample():
-        from oracle import recurrence_oracle as orc
-        xs = [d[kk][:1].double().cpu().numpy() for kk in ("r", "i", "x")]
-        lm = d["lam"].double().cpu().numpy()
-        orc.rglru_gated_forward(*xs, lm)
-        orc.rglru_gated_backward(d["dy"][:1].double().cpu().numpy(), *xs, lm)
+    host = {}
+    cl = min(L, 512)
 
-    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L, cpu_tokens=L,
+    def cpu_sample():   # rglru_gated_reference (gate math + per-step loop, fp32 torch) with autograd
+        import mlx_recurrence_amd as mr
+        h = _host_copies(host, d, ("r", "i", "x"), cl)
+        h.update(_host_copies(host, d, ("lam",)))
+        xs = [h[kk].requires_grad_(True) for kk in ("r", "i", "x", "lam")]
+        mr.rglru_gated_reference(*xs, 8.0).backward(dy[:, :cl])
+
+    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L, cpu_tokens=B * cl,
+                cpu_desc=f"B={B}, the first L={cl} of L={L} steps",
                 fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=n * 4, ckpt_bytes=n_ck * 4,
                 io_bytes=n * 4 + 3 * n * es)
 
@@ -385,13 +410,17 @@ def make_rotlru_theta(cfg, device, dtype):
         xs = [d[kk].detach().requires_grad_(True) for kk in ("a", "th", "x")]
         mr.rotlru_theta_scan(*xs, seg=seg).backward(d["dy"])
 
-    def cpu_sample():
-        from oracle import recurrence_oracle as orc
-        xs = [d[kk][:1].double().cpu().numpy() for kk in ("a", "th", "x")]
-        orc.rotlru_theta_forward(*xs)
-        orc.rotlru_theta_backward(d["dy"][:1].double().cpu().numpy(), *xs)
+    host = {}
+    cl = min(L, 512)
 
-    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L, cpu_tokens=L,
+    def cpu_sample():   # cos / sin in torch, rotlru_scan_reference (fp32, host) with autograd
+        import mlx_recurrence_amd as mr
+        h = _host_copies(host, d, ("a", "th", "x"), cl)
+        a_, th_, x_ = (h[kk].requires_grad_(True) for kk in ("a", "th", "x"))
+        mr.rotlru_scan_reference(a_, torch.cos(th_), torch.sin(th_), x_).backward(dy[:, :cl])
+
+    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L, cpu_tokens=B * cl,
+                cpu_desc=f"B={B}, the first L={cl} of L={L} steps",
                 fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=n_x * 4, ckpt_bytes=n_ck * 4,
                 io_bytes=n_x * 4 + ins)
 
@@ -439,13 +468,17 @@ def make_rotlru(cfg, device, dtype):
         xs = [d[kk].detach().requires_grad_(True) for kk in ("a", "cs", "sn", "x")]
         mr.rotlru_scan(*xs, seg=seg).backward(d["dy"])
 
-    def cpu_sample():
-        from oracle import recurrence_oracle as orc
-        xs = [d[kk][:1].double().cpu().numpy() for kk in ("a", "cs", "sn", "x")]
-        orc.rotlru_forward(*xs)
-        orc.rotlru_backward(d["dy"][:1].double().cpu().numpy(), *xs)
+    host = {}
+    cl = min(L, 512)
 
-    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L, cpu_tokens=L,
+    def cpu_sample():   # rotlru_scan_reference (fp32 torch, host) with autograd, full shape
+        import mlx_recurrence_amd as mr
+        h = _host_copies(host, d, ("a", "cs", "sn", "x"), cl)
+        xs = [h[kk].requires_grad_(True) for kk in ("a", "cs", "sn", "x")]
+        mr.rotlru_scan_reference(*xs).backward(dy[:, :cl])
+
+    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L, cpu_tokens=B * cl,
+                cpu_desc=f"B={B}, the first L={cl} of L={L} steps",
                 fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes, state_hist_bytes=n_x * 4, ckpt_bytes=n_ck * 4,
                 io_bytes=n_x * 4 + (3 * n_p + n_x) * es)
 
@@ -472,7 +505,7 @@ WORKLOADS = {
 
 
 # ------------------------------------------------------------------ measure
-def measure(name, steps, warmup, dtype, device, with_cpu):
+def measure(name, steps, warmup, dtype, device, cpu_seconds):
     import torch
     desc, maker, cfg = WORKLOADS[name]
     w = maker(cfg, device, dtype)
@@ -576,42 +609,78 @@ def measure(name, steps, warmup, dtype, device, with_cpu):
         achieved_gbs=achieved, eager_ms_per_step=eager_ms,
         peak_transient_bytes=int(peak_extra), state_history_bytes=int(w["state_hist_bytes"]),
     )
-    if with_cpu:
-        nthreads = 1
-        t_cpu = []
-        w["cpu"]()  # warm
-        # about 10 s of CPU work (at least 3 runs): the bounded sample
-        while len(t_cpu) < 3 or (sum(t_cpu) < 10.0 and len(t_cpu) < 400):
-            c0 = time.perf_counter()
-            w["cpu"]()
-            t_cpu.append(time.perf_counter() - c0)
-        t_cpu.sort()
-        med = t_cpu[len(t_cpu) // 2]
-        ctok = w.get("cpu_tokens", w["tokens"])
-        res["cpu"] = dict(value=ctok / med, unit="tokens/s", cores=nthreads, kind="port",
-                          sample=f"float64 oracle forward + explicit adjoint over {ctok} tokens of the "
-                                 f"workload, median of {len(t_cpu)} runs ({med:.2f} s each, "
-                                 f"{sum(t_cpu):.1f} s in all)")
+    if cpu_seconds > 0:
+        res["cpu"] = cpu_baseline(w, cpu_seconds)
     return res
 
 
-# ------------------------------------------------------------------ HBM traffic
+def cpu_threads():
+    """Host threads for the CPU leg: every core this process may run on, capped
+    by OMP_NUM_THREADS where the launcher sets it (the share of a shared box)."""
+    n = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS")
+    if cap and cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return n, len(os.sched_getaffinity(0))
+
+
+def cpu_baseline(w, seconds):
+    """The reference's CPU path as restated in this package: the fp32 torch
+    per-step *_scan_reference loop with autograd (the counterpart of the
+    reference's pure-MLX loop under mx.grad, reference ssd.py:382-394,
+    gla.py:336-346, rglru.py:274-282, rotlru.py:338-351) on the host, on the
+    same input values.  Repeated for about `seconds` of CPU work (at least 3
+    runs); the median run gives tokens/s."""
+    import platform
+    import torch
+    n, n_aff = cpu_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(n)
+    try:
+        t_cpu = []
+        w["cpu"]()  # warm (and host copies of the inputs)
+        while len(t_cpu) < 3 or (sum(t_cpu) < seconds and len(t_cpu) < 400):
+            c0 = time.perf_counter()
+            w["cpu"]()
+            t_cpu.append(time.perf_counter() - c0)
+            print(f"[bench] cpu leg run {len(t_cpu)}: {t_cpu[-1]:.3f} s", file=sys.stderr, flush=True)
+    finally:
+        torch.set_num_threads(prev)
+    t_cpu.sort()
+    med = t_cpu[len(t_cpu) // 2]
+    ctok = w["cpu_tokens"]
+    return dict(value=ctok / med, unit="tokens/s", cores=n, kind="port",
+                sample=f"fp32 torch per-step *_scan_reference forward + autograd backward on the host, "
+                       f"{w['cpu_desc']} ({ctok} tokens), {n} threads (of {n_aff} cores in the affinity mask; "
+                       f"{platform.processor() or platform.machine()}), median of {len(t_cpu)} runs "
+                       f"({med:.3f} s each, {sum(t_cpu):.1f} s in all)")
+
+
+# ------------------------------------------------------------------ counters
 # roofline.traffic comes from two rocprofv3 counter runs of `--pmc-run`
 # (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the same
-# counter reads for a plain device copy of known size (`--calibrate-copy`).
-# `--pmc-summary DIR` turns those runs into profiles/pmc_traffic.json, which a
-# normal run reads for its dominant kernel.
+# counter reads for a plain device copy of known size (`--calibrate-copy`); a
+# third run reads the MFMA counters (busy cycles, bf16 MOPS, instruction
+# counts).  `--pmc-summary` turns the runs into profiles/pmc_traffic.json, which
+# a normal run reads for its dominant kernel.
 PMC_FILE = ROOT / "profiles" / "pmc_traffic.json"
+COUNTER_SETS = {
+    "fetch": ["FETCH_SIZE"],
+    "write": ["WRITE_SIZE"],
+    "mfma": ["SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU",
+             "SQ_INSTS_MFMA", "SQ_BUSY_CU_CYCLES"],
+}
+PROFILED_WORKLOADS = ["ssd", "gla", "rglru", "rotlru", "rglru_gated", "rotlru_theta", "ssd_c4", "ssd_b96", "gla_b96"]
 PROFILE_COMMANDS = [
     "rocprofv3 --kernel-trace --stats -d $R/gpurun_out/prof_trace -o trace --output-format csv -- "
-    "python3 bench.py --steps 20 --warmup 3 --no-cpu --also gla,rglru,rotlru,rglru_gated,rotlru_theta",
+    "python3 bench.py --steps 20 --warmup 3 --no-cpu --also " + ",".join(PROFILED_WORKLOADS[1:]),
     "rocprofv3 --pmc FETCH_SIZE -d $R/gpurun_out/pmc/cal_fetch -o cal --output-format csv -- "
     "python3 bench.py --calibrate-copy 256",
     "rocprofv3 --pmc WRITE_SIZE -d $R/gpurun_out/pmc/cal_write -o cal --output-format csv -- "
     "python3 bench.py --calibrate-copy 256",
-    "for w in ssd gla rglru rotlru rglru_gated rotlru_theta; do rocprofv3 --pmc FETCH_SIZE -d $R/gpurun_out/pmc/${w}_fetch -o $w "
-    "--output-format csv -- python3 bench.py --pmc-run $w; rocprofv3 --pmc WRITE_SIZE -d "
-    "$R/gpurun_out/pmc/${w}_write -o $w --output-format csv -- python3 bench.py --pmc-run $w; done",
+    "for w in " + " ".join(PROFILED_WORKLOADS) + "; do for c in fetch write mfma; do rocprofv3 --pmc <counters of "
+    "set c> -d $R/gpurun_out/pmc/${w}_$c -o $w --output-format csv -- python3 bench.py --pmc-run $w; done; done "
+    "(sets: " + "; ".join(f"{k}: {' '.join(v)}" for k, v in COUNTER_SETS.items()) + ")",
     "python3 bench.py --pmc-summary --trace-dir gpurun_out/prof_trace",
 ]
 
@@ -652,10 +721,23 @@ def _counter_rows(run_dir):
     return rows
 
 
+def _simd_count(run_dir, default=1024):
+    import csv
+    for f in sorted(pathlib.Path(run_dir).rglob("*agent_info.csv")):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                if r.get("Agent_Type", r.get("Type", "")) == "GPU" or r.get("Name", "").startswith("gfx"):
+                    try:
+                        return int(r["Simd_Count"])
+                    except (KeyError, ValueError):
+                        pass
+    return default
+
+
 def pmc_summary(root):
     """profiles/pmc_traffic.json from the counter runs under `root`:
-    root/cal_fetch, root/cal_write (calibration copy), root/<w>_fetch,
-    root/<w>_write and root/<w>_passes.json for each workload w."""
+    root/cal_fetch, root/cal_write (calibration copy), root/<w>_{fetch,write,mfma}
+    and root/<w>_passes.json for each workload w."""
     root = pathlib.Path(root)
 
     def per_dispatch(run_dir, counter):
@@ -676,17 +758,29 @@ def pmc_summary(root):
         if not pj.exists():
             continue
         counts = json.loads(pj.read_text())
-        fetch = per_dispatch(root / f"{w}_fetch", "FETCH_SIZE")
-        write = per_dispatch(root / f"{w}_write", "WRITE_SIZE")
         n = counts["fwd"] + counts["bwd"]
-        fetch, write = fetch[-n:], write[-n:]
+        fetch = per_dispatch(root / f"{w}_fetch", "FETCH_SIZE")[-n:]
+        write = per_dispatch(root / f"{w}_write", "WRITE_SIZE")[-n:]
+        mf = {c: per_dispatch(root / f"{w}_mfma", c)[-n:] for c in COUNTER_SETS["mfma"]}
+        simd = _simd_count(root / f"{w}_mfma")
         entry = {}
         for pname, lo, hi in (("fwd", 0, counts["fwd"]), ("bwd", counts["fwd"], n)):
-            entry[pname] = [{"kernel": fetch[i][0],
-                             "fetch_bytes": fetch[i][1] * 1024 * (scale["FETCH_SIZE"] or 1.0),
-                             "write_bytes": write[i][1] * 1024 * (scale["WRITE_SIZE"] or 1.0)}
-                            for i in range(lo, hi)]
+            rows = []
+            for i in range(lo, hi):
+                k = {"kernel": fetch[i][0] if i < len(fetch) else "",
+                     "fetch_bytes": fetch[i][1] * 1024 * (scale["FETCH_SIZE"] or 1.0) if i < len(fetch) else None,
+                     "write_bytes": write[i][1] * 1024 * (scale["WRITE_SIZE"] or 1.0) if i < len(write) else None}
+                if all(len(mf[c]) == n for c in mf):
+                    busy, gui = mf["SQ_VALU_MFMA_BUSY_CYCLES"][i][1], mf["GRBM_GUI_ACTIVE"][i][1]
+                    k.update(mfma_busy_cycles=busy, gui_active_cycles=gui,
+                             mfma_util=busy / (gui * simd) if gui else None,
+                             mfma_flops=mf["SQ_INSTS_VALU_MFMA_MOPS_BF16"][i][1] * 512,
+                             insts_valu=mf["SQ_INSTS_VALU"][i][1], insts_mfma=mf["SQ_INSTS_MFMA"][i][1],
+                             busy_cu_cycles=mf["SQ_BUSY_CU_CYCLES"][i][1])
+                rows.append(k)
+            entry[pname] = rows
         summary["workloads"][w] = entry
+    summary["simd_count"] = _simd_count(root / "ssd_mfma") if (root / "ssd_mfma").exists() else 1024
     PMC_FILE.parent.mkdir(exist_ok=True)
     PMC_FILE.write_text(json.dumps(summary, indent=1))
     print(f"wrote {PMC_FILE}")
@@ -694,12 +788,12 @@ def pmc_summary(root):
 
 
 def profile_markdown(summary, trace_dir, out_md, commands):
-    """Kernel durations (rocprofv3 --kernel-trace --stats) and per-dispatch HBM
-    traffic (the counter runs) beside each pass's algorithmic bytes."""
+    """Kernel durations (rocprofv3 --kernel-trace --stats), per-dispatch HBM
+    traffic and MFMA counters beside each pass's algorithmic bytes."""
     import csv
     import torch
-    lines = ["# Default bench workloads (SSD config 1 headline; GLA config 2; RG-LRU / rotLRU / gated RG-LRU / "
-             "rotLRU from theta, config 3), bf16 inputs",
+    lines = ["# Bench workloads: SSD config 1 (headline), GLA config 2, RG-LRU / rotLRU / gated RG-LRU / rotLRU from "
+             "theta at config 3, SSD config 4, SSD and GLA at B = 96; bf16 inputs",
              "", "Commands (from the repository root on one MI355X, `export TMPDIR=/tmp`, R = repository root):", ""]
     lines += ["    " + c for c in commands]
     lines += ["", "## Kernel durations (`rocprofv3 --kernel-trace --stats`)", "",
@@ -711,31 +805,71 @@ def profile_markdown(summary, trace_dir, out_md, commands):
                 lines.append(f"| `{r['Name'][:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
                              f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} |")
     sc = summary["scale"]
-    lines += ["", "## HBM traffic per dispatch (`--pmc FETCH_SIZE`, `--pmc WRITE_SIZE`)", "",
+    lines += ["", "## HBM traffic and MFMA per dispatch (`--pmc` runs)", "",
               f"Scale factors from a plain 256 MiB device copy (`bench.py --calibrate-copy 256`): FETCH_SIZE "
               f"x{sc['FETCH_SIZE']:.3f}, WRITE_SIZE x{sc['WRITE_SIZE']:.3f}.  Algorithmic bytes are the pass's "
               "(inputs, outputs and checkpoints at their API dtypes), all moved by its main kernel; the other "
-              "kernels of a pass move workspace data only.", "",
-              "| workload | pass | kernel | fetch MB | write MB | pass algorithmic MB |", "|---|---|---|---|---|---|"]
+              "kernels of a pass move workspace data only.  MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / "
+              "(GRBM_GUI_ACTIVE x SIMDs); MFMA GFLOP = SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 per dispatch; "
+              "VALU / MFMA = SQ_INSTS_VALU, SQ_INSTS_MFMA (instructions per dispatch).", "",
+              "| workload | pass | kernel | fetch MB | write MB | pass algorithmic MB | MFMA busy | MFMA GFLOP | "
+              "VALU insts | MFMA insts |", "|---|---|---|---|---|---|---|---|---|---|"]
+
+    def fmt(v, f):
+        return "—" if v is None else f.format(v)
+
     for wname, entry in summary["workloads"].items():
         desc, maker, cfg = WORKLOADS[wname]
-        w = maker(cfg, torch.device("cpu"), torch.bfloat16)
+        w = maker(cfg, torch.device("cpu"), torch.bfloat16) if "c4" not in wname else None
         for pname in ("fwd", "bwd"):
-            alg = w[f"{pname}_bytes"] / 1e6
+            alg = (w[f"{pname}_bytes"] if w else _c4_bytes()[pname]) / 1e6
             for k in entry[pname]:
-                lines.append(f"| {wname} | {pname} | `{k['kernel'][:70]}` | {k['fetch_bytes'] / 1e6:.3f} | "
-                             f"{k['write_bytes'] / 1e6:.3f} | {alg:.3f} |")
+                lines.append(f"| {wname} | {pname} | `{k['kernel'][:60]}` | {fmt(k['fetch_bytes'] and k['fetch_bytes'] / 1e6, '{:.3f}')} | "
+                             f"{fmt(k['write_bytes'] and k['write_bytes'] / 1e6, '{:.3f}')} | {alg:.3f} | "
+                             f"{fmt(k.get('mfma_util') and 100 * k['mfma_util'], '{:.1f} %')} | "
+                             f"{fmt(k.get('mfma_flops') and k['mfma_flops'] / 1e9, '{:.2f}')} | "
+                             f"{fmt(k.get('insts_valu'), '{:.3g}')} | {fmt(k.get('insts_mfma'), '{:.3g}')} |")
     pathlib.Path(out_md).write_text("\n".join(lines) + "\n")
     print(f"wrote {out_md}")
 
 
-def traffic_of(name, dom):
-    """Measured HBM bytes per launch of the dominant kernel, or None."""
+def _c4_bytes():
+    """Algorithmic bytes of config 4's passes (bf16 inputs), without allocating it."""
+    B, L, H, Dh, N, T = 8, 4096, 80, 64, 128, 32
+    es = 2
+    n_u, n_d, n_bc, n_ck = B * L * H * Dh, B * L * H, B * L * H * N, B * H * (L // T) * Dh * N
+    inputs = (n_u + n_d + 2 * n_bc) * es + H * N * 4
+    return {"fwd": inputs + n_u * 4 + n_ck * 4,
+            "bwd": n_u * 4 + n_ck * 4 + inputs + (n_u + n_d + 2 * n_bc) * es + H * N * 4}
+
+
+def _pmc_kernel(name, dom):
     try:
-        k = json.loads(PMC_FILE.read_text())["workloads"][name][dom["pass"]][dom["index"]]
-        return k["fetch_bytes"] + k["write_bytes"]
+        return json.loads(PMC_FILE.read_text())["workloads"][name][dom["pass"]][dom["index"]]
     except (OSError, KeyError, IndexError, ValueError):
         return None
+
+
+def traffic_of(name, dom):
+    """Measured HBM bytes per launch of the dominant kernel, or None."""
+    k = _pmc_kernel(name, dom)
+    if k is None or k.get("fetch_bytes") is None or k.get("write_bytes") is None:
+        return None
+    return k["fetch_bytes"] + k["write_bytes"]
+
+
+def mfma_of(name, dom):
+    """MFMA figures of the dominant kernel: busy fraction of the MFMA units
+    (counters) and bf16 MFMA TFLOP/s (counted flops / the live-measured
+    average launch duration) against MI355X's dense bf16 peak; None where the
+    kernel issues no MFMA."""
+    k = _pmc_kernel(name, dom)
+    if k is None or not k.get("mfma_flops"):
+        return None
+    tflops = k["mfma_flops"] / (dom["us"] * 1e-6) / 1e12
+    return {"util": k.get("mfma_util"), "achieved": tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": tflops / MFMA_BF16_PEAK_TFLOPS, "flops_per_launch": k["mfma_flops"],
+            "valu_insts": k.get("insts_valu"), "mfma_insts": k.get("insts_mfma")}
 
 
 def main():
@@ -744,8 +878,11 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="ssd", choices=sorted(WORKLOADS))
-    ap.add_argument("--also", default="gla", help="comma-separated extra workloads reported beside")
+    ap.add_argument("--also", default="gla,rglru,rotlru,ssd_c4",
+                    help="comma-separated extra workloads reported beside (each with its roofline and CPU leg)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="CPU work per CPU baseline (the headline workload; the extra workloads get half)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="only run a plain device-to-device copy of MB megabytes (PMC byte-counter scale)")
     ap.add_argument("--pmc-run", default=None, metavar="WORKLOAD",
@@ -788,17 +925,22 @@ def main():
         print(json.dumps({"calibrate_copy": {"bytes_read": 4 * n, "bytes_written": 4 * n, "launches": 5}}))
         return
 
-    main_res = measure(args.workload, args.steps, args.warmup, dtype, device, not args.no_cpu)
+    cpu_s = 0.0 if args.no_cpu else args.cpu_seconds
+    main_res = measure(args.workload, args.steps, args.warmup, dtype, device, cpu_s)
     extras = {}
     for nm in [s for s in args.also.split(",") if s and s != args.workload]:
-        r = measure(nm, args.steps, args.warmup, dtype, device, False)
-        extras[nm] = dict(workload=r["workload"], tokens_per_s=r["tokens_per_s"], ms_per_step=r["ms_per_step"],
-                          fwd_us=r["fwd_us"], bwd_us=r["bwd_us"], eager_ms_per_step=r["eager_ms_per_step"],
+        r = measure(nm, args.steps, args.warmup, dtype, device, cpu_s / 2)
+        extras[nm] = dict(workload=r["workload"], config=r["cfg"], tokens_per_s=r["tokens_per_s"],
+                          ms_per_step=r["ms_per_step"], fwd_us=r["fwd_us"], bwd_us=r["bwd_us"],
+                          eager_ms_per_step=r["eager_ms_per_step"],
                           roofline=dict(bound="hbm", achieved=r["achieved_gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
                                         traffic=traffic_of(nm, r["dominant"]),
                                         frac=r["achieved_gbs"] / HBM_PEAK_GBS, kernel=r["dominant"]),
+                          mfma=mfma_of(nm, r["dominant"]), cpu_baseline=r.get("cpu"),
                           kernels=r["kernels"], peak_transient_bytes=r["peak_transient_bytes"],
                           state_history_bytes=r["state_history_bytes"])
+        print(f"[bench] {nm}: {r['ms_per_step'] * 1e3:.1f} us per step, {r['tokens_per_s']:.4g} tokens/s",
+              file=sys.stderr, flush=True)
 
     r = main_res
     cfg = dict(workload=r["workload"], **r["cfg"], input_dtype="bf16", state_dtype="f32")
@@ -826,6 +968,7 @@ def main():
             "kernel": r["dominant"],
         },
         "cpu_baseline": r.get("cpu"),
+        "mfma": mfma_of(args.workload, r["dominant"]),
         "fwd_us": r["fwd_us"],
         "bwd_us": r["bwd_us"],
         "kernels": r["kernels"],

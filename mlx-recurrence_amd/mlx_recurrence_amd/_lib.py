@@ -10,6 +10,7 @@ passes raw device pointers plus the current stream of the tensors' device.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 import pathlib
 
@@ -88,7 +89,7 @@ def abi_version() -> int:
 
 
 def chunk_len(L: int, seg: int) -> int:
-    return int(load().rr_chunk_len(L, seg))
+    return chunk_len_cached(int(L), int(seg))
 
 
 def async_status() -> None:
@@ -124,11 +125,37 @@ def _check(rc: int, what: str) -> None:
 
 
 def ptr(t: torch.Tensor | None):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    """Device address of a tensor (an int; ctypes passes it as void*), or None."""
+    return None if t is None else t.data_ptr()
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def stream_of(t: torch.Tensor):
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    """The current stream of t's device as a raw hipStream_t address."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index if t.device.index is not None else torch.cuda.current_device())
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+class _NoGuard:
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+_NO_GUARD = _NoGuard()
+
+
+def device_guard(dev: torch.device):
+    """torch.cuda.device(dev) when dev is not the current device (the library
+    looks up per-device addresses on the current device), else a no-op."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return _NO_GUARD
+    return torch.cuda.device(dev)
 
 
 def require_device(*tensors: torch.Tensor) -> torch.device:
@@ -171,10 +198,24 @@ def common_dtype(*tensors: torch.Tensor) -> torch.dtype:
     return dt
 
 
+@functools.lru_cache(maxsize=1024)
+def _ws_bytes(fn_name: str, args: tuple) -> int:
+    return int(getattr(load(), fn_name)(*args))
+
+
+@functools.lru_cache(maxsize=1024)
+def chunk_len_cached(L: int, seg: int) -> int:
+    return int(load().rr_chunk_len(L, seg))
+
+
+def _alloc_ws(n: int, device) -> torch.Tensor | None:
+    return torch.empty(n, dtype=torch.uint8, device=device) if n else None
+
+
 # ---------------------------------------------------------------- SSD
 def ssd_workspace(B, L, H, Dh, N, seg, a_stride_n, dtype, pass_, device) -> torch.Tensor | None:
-    n = int(load().rr_ssd_workspace_bytes(B, L, H, Dh, N, seg, a_stride_n, DTYPE_CODE[dtype], pass_))
-    return torch.empty(n, dtype=torch.uint8, device=device) if n else None
+    n = _ws_bytes("rr_ssd_workspace_bytes", (B, L, H, Dh, N, seg, a_stride_n, DTYPE_CODE[dtype], pass_))
+    return _alloc_ws(n, device)
 
 
 def ssd_fwd(u, delta, Bm, Cm, A, a_stride_n, h0, seg, y, ckpt, ws):
@@ -201,8 +242,8 @@ def ssd_bwd(dy, dfinal, u, delta, Bm, Cm, A, a_stride_n, h0, ckpt, seg, du, ddel
 
 # ---------------------------------------------------------------- GLA
 def gla_workspace(B, L, H, Dh, seg, dtype, pass_, device) -> torch.Tensor | None:
-    n = int(load().rr_gla_workspace_bytes(B, L, H, Dh, seg, DTYPE_CODE[dtype], pass_))
-    return torch.empty(n, dtype=torch.uint8, device=device) if n else None
+    n = _ws_bytes("rr_gla_workspace_bytes", (B, L, H, Dh, seg, DTYPE_CODE[dtype], pass_))
+    return _alloc_ws(n, device)
 
 
 def gla_fwd(q, k, v, g, h0, seg, y, ckpt, ws):
@@ -224,7 +265,7 @@ def gla_bwd(dy, dfinal, q, k, v, g, h0, ckpt, seg, dq, dk, dv, dg, dh0, ws):
 
 # ---------------------------------------------------------------- RG-LRU
 def rglru_workspace(B, L, D, seg, dtype, pass_, device) -> torch.Tensor:
-    n = int(load().rr_rglru_workspace_bytes(B, L, D, seg, DTYPE_CODE[dtype], pass_))
+    n = _ws_bytes("rr_rglru_workspace_bytes", (B, L, D, seg, DTYPE_CODE[dtype], pass_))
     return torch.empty(n, dtype=torch.uint8, device=device)
 
 
@@ -244,7 +285,7 @@ def rglru_bwd(dy, dfinal, a, x, h0, ckpt, seg, da, dx, dh0, ws):
 
 
 def rglru_gated_workspace(B, L, D, seg, dtype, pass_, device) -> torch.Tensor:
-    n = int(load().rr_rglru_gated_workspace_bytes(B, L, D, seg, DTYPE_CODE[dtype], pass_))
+    n = _ws_bytes("rr_rglru_gated_workspace_bytes", (B, L, D, seg, DTYPE_CODE[dtype], pass_))
     return torch.empty(n, dtype=torch.uint8, device=device)
 
 
@@ -267,7 +308,7 @@ def rglru_gated_bwd(dy, dfinal, r, i, x, lam, c, h0, ckpt, seg, dr, di, dx, dlam
 
 # ---------------------------------------------------------------- rotLRU
 def rotlru_workspace(B, L, Dp, seg, dtype, pass_, device) -> torch.Tensor:
-    n = int(load().rr_rotlru_workspace_bytes(B, L, Dp, seg, DTYPE_CODE[dtype], pass_))
+    n = _ws_bytes("rr_rotlru_workspace_bytes", (B, L, Dp, seg, DTYPE_CODE[dtype], pass_))
     return torch.empty(n, dtype=torch.uint8, device=device)
 
 

@@ -46,7 +46,7 @@ class _GLAScan(torch.autograd.Function):
         nC = L // _lib.chunk_len(L, seg)
         y = torch.empty((B, L, H, Dh), dtype=torch.float32, device=dev)
         ckpt = torch.empty((B, H, nC, Dh, Dh), dtype=torch.float32, device=dev)
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             ws = _lib.gla_workspace(B, L, H, Dh, seg, dt, 0, dev)
             _lib.gla_fwd(q_, k_, v_, g_, h0_, seg, y, ckpt, ws)
         ctx.save_for_backward(q_, k_, v_, g_, h0_, ckpt)
@@ -64,7 +64,7 @@ class _GLAScan(torch.autograd.Function):
         dfinal = None if dfinal is None else _lib.prep(dfinal, torch.float32)
         dq, dk, dv, dg = (torch.empty_like(t) for t in (q_, k_, v_, g_))
         dh0 = torch.empty((B, H, Dh, Dh), dtype=torch.float32, device=dev) if ctx.needs_input_grad[4] else None
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             ws = _lib.gla_workspace(B, L, H, Dh, ctx.seg, q_.dtype, 1, dev)
             _lib.gla_bwd(dy, dfinal, q_, k_, v_, g_, h0_, ckpt, ctx.seg, dq, dk, dv, dg, dh0, ws)
         return dq, dk, dv, dg, dh0, None
@@ -112,9 +112,10 @@ def gla_scan_reference(q, k, v, gates, *, initial_state=None):
     q, k, v, gates = (t.to(ct) for t in (q, k, v, gates))
     h = torch.zeros((B, H, Dh, Dh), dtype=ct, device=q.device) if initial_state is None else initial_state.to(ct)
     ys = []
-    for t in range(L):
-        g = gates[:, t, :, None, None]
-        kv = k[:, t, :, :, None] * v[:, t, :, None, :]
+    # per-step slices from unbind (one backward stack, not a scatter per step)
+    for g_t, k_t, v_t, q_t in zip(gates.unbind(1), k.unbind(1), v.unbind(1), q.unbind(1)):
+        g = g_t[:, :, None, None]
+        kv = k_t[:, :, :, None] * v_t[:, :, None, :]
         h = g * h + kv
-        ys.append((q[:, t, :, :, None] * h).sum(-2))
+        ys.append((q_t[:, :, :, None] * h).sum(-2))
     return torch.stack(ys, dim=1)

@@ -45,7 +45,7 @@ class _RGLRUScan(torch.autograd.Function):
         nC = L // _lib.chunk_len(L, seg)
         y = torch.empty((B, L, D), dtype=torch.float32, device=dev)
         ckpt = torch.empty((B, nC, D), dtype=torch.float32, device=dev)
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             ws = _lib.rglru_workspace(B, L, D, seg, dt, 0, dev)
             _lib.rglru_fwd(a_, x_, h0_, seg, y, ckpt, ws)
         ctx.save_for_backward(a_, x_, h0_, ckpt)
@@ -63,7 +63,7 @@ class _RGLRUScan(torch.autograd.Function):
         da = torch.empty_like(a_)
         dx = torch.empty_like(x_)
         dh0 = torch.empty((B, D), dtype=torch.float32, device=dev) if ctx.needs_input_grad[2] else None
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             ws = _lib.rglru_workspace(B, L, D, ctx.seg, a_.dtype, 1, dev)
             _lib.rglru_bwd(dy, dfinal, a_, x_, h0_, ckpt, ctx.seg, da, dx, dh0, ws)
         return da, dx, dh0, None
@@ -110,8 +110,9 @@ def rglru_scan_reference(a, x, *, initial_state=None):
     ct = torch.promote_types(torch.promote_types(a.dtype, x.dtype), torch.float32)
     h = torch.zeros((B, D), dtype=ct, device=a.device) if initial_state is None else initial_state.to(ct)
     ys = []
-    for t in range(L):
-        h = a[:, t, :].to(ct) * h + x[:, t, :].to(ct)
+    # per-step slices from unbind (one backward stack, not a scatter per step)
+    for a_t, x_t in zip(a.to(ct).unbind(1), x.to(ct).unbind(1)):
+        h = a_t * h + x_t
         ys.append(h)
     return torch.stack(ys, dim=1)
 
@@ -129,7 +130,7 @@ class _RGLRUGatedScan(torch.autograd.Function):
         nC = L // _lib.chunk_len(L, seg)
         y = torch.empty((B, L, D), dtype=torch.float32, device=dev)
         ckpt = torch.empty((B, nC, D), dtype=torch.float32, device=dev)
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             ws = _lib.rglru_gated_workspace(B, L, D, seg, dt, 0, dev)
             _lib.rglru_gated_fwd(r_, i_, x_, lam_, c, h0_, seg, y, ckpt, ws)
         ctx.save_for_backward(r_, i_, x_, lam_, h0_, ckpt)
@@ -147,7 +148,7 @@ class _RGLRUGatedScan(torch.autograd.Function):
         dr, di, dx = (torch.empty_like(t) for t in (r_, i_, x_))
         dlam = torch.empty((D,), dtype=torch.float32, device=dev)
         dh0 = torch.empty((B, D), dtype=torch.float32, device=dev) if ctx.needs_input_grad[4] else None
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             ws = _lib.rglru_gated_workspace(B, L, D, ctx.seg, r_.dtype, 1, dev)
             _lib.rglru_gated_bwd(dy, dfinal, r_, i_, x_, lam_, ctx.c, h0_, ckpt, ctx.seg, dr, di, dx, dlam, dh0, ws)
         return dr, di, dx, dlam, dh0, None, None

@@ -53,7 +53,7 @@ class _RotLRUScan(torch.autograd.Function):
         nC = L // _lib.chunk_len(L, seg)
         y = torch.empty((B, L, D), dtype=torch.float32, device=dev)
         ckpt = torch.empty((B, nC, D), dtype=torch.float32, device=dev)
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             ws = _lib.rotlru_workspace(B, L, Dp, seg, dt, 0, dev)
             _lib.rotlru_fwd(a_, cs_, sn_, x_, h0_, seg, y, ckpt, ws)
         ctx.save_for_backward(a_, cs_, sn_, x_, h0_, ckpt)
@@ -72,7 +72,7 @@ class _RotLRUScan(torch.autograd.Function):
         da, dcs, dsn = torch.empty_like(a_), torch.empty_like(cs_), torch.empty_like(sn_)
         dx = torch.empty_like(x_)
         dh0 = torch.empty((B, D), dtype=torch.float32, device=dev) if ctx.needs_input_grad[4] else None
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             ws = _lib.rotlru_workspace(B, L, Dp, ctx.seg, a_.dtype, 1, dev)
             _lib.rotlru_bwd(dy, dfinal, a_, cs_, sn_, x_, h0_, ckpt, ctx.seg, da, dcs, dsn, dx, dh0, ws)
         return da, dcs, dsn, dx, dh0, None
@@ -125,10 +125,10 @@ def rotlru_scan_reference(a, cs, sn, x, *, initial_state=None):
         h0 = initial_state.to(ct).reshape(B, Dp, 2)
         u, w = h0[..., 0], h0[..., 1]
     ys = []
-    for t in range(L):
-        at, c, s = a[:, t, :].to(ct), cs[:, t, :].to(ct), sn[:, t, :].to(ct)
-        un = at * (c * u - s * w) + xp[:, t, :, 0]
-        wn = at * (s * u + c * w) + xp[:, t, :, 1]
+    # per-step slices from unbind (one backward stack, not a scatter per step)
+    for at, c, s, x_t in zip(a.to(ct).unbind(1), cs.to(ct).unbind(1), sn.to(ct).unbind(1), xp.unbind(1)):
+        un = at * (c * u - s * w) + x_t[:, :, 0]
+        wn = at * (s * u + c * w) + x_t[:, :, 1]
         u, w = un, wn
         ys.append(torch.stack([u, w], dim=-1).reshape(B, 2 * Dp))
     return torch.stack(ys, dim=1)
@@ -147,7 +147,7 @@ class _RotLRUThetaScan(torch.autograd.Function):
         nC = L // _lib.chunk_len(L, seg)
         y = torch.empty((B, L, D), dtype=torch.float32, device=dev)
         ckpt = torch.empty((B, nC, D), dtype=torch.float32, device=dev)
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             ws = _lib.rotlru_workspace(B, L, Dp, seg, dt, 0, dev)
             _lib.rotlru_theta_fwd(a_, th_, x_, h0_, seg, y, ckpt, ws)
         ctx.save_for_backward(a_, th_, x_, h0_, ckpt)
@@ -165,7 +165,7 @@ class _RotLRUThetaScan(torch.autograd.Function):
         dfinal = None if dfinal is None else _lib.prep(dfinal, torch.float32)
         da, dth, dx = torch.empty_like(a_), torch.empty_like(th_), torch.empty_like(x_)
         dh0 = torch.empty((B, D), dtype=torch.float32, device=dev) if ctx.needs_input_grad[3] else None
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             ws = _lib.rotlru_workspace(B, L, Dp, ctx.seg, a_.dtype, 1, dev)
             _lib.rotlru_theta_bwd(dy, dfinal, a_, th_, x_, h0_, ckpt, ctx.seg, da, dth, dx, dh0, ws)
         return da, dth, dx, dh0, None

@@ -66,7 +66,7 @@ class _SSDScan(torch.autograd.Function):
         nC = L // _lib.chunk_len(L, seg)
         y = torch.empty((Bsz, L, H, Dh), dtype=torch.float32, device=dev)
         ckpt = torch.empty((Bsz, H, nC, Dh, N), dtype=torch.float32, device=dev)
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             ws = _lib.ssd_workspace(Bsz, L, H, Dh, N, seg, a_sn, dt, 0, dev)
             _lib.ssd_fwd(u_, d_, B_, C_, A_, a_sn, h0_, seg, y, ckpt, ws)
         ctx.save_for_backward(u_, d_, B_, C_, A_, h0_, ckpt)
@@ -86,7 +86,7 @@ class _SSDScan(torch.autograd.Function):
         du, dd, dB, dC = (torch.empty_like(t) for t in (u_, d_, B_, C_))
         dA = torch.empty((H, N), dtype=torch.float32, device=dev)
         dh0 = torch.empty((Bsz, H, Dh, N), dtype=torch.float32, device=dev) if ctx.needs_input_grad[5] else None
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             ws = _lib.ssd_workspace(Bsz, L, H, Dh, N, ctx.seg, ctx.a_sn, u_.dtype, 1, dev)
             _lib.ssd_bwd(dy, dfinal, u_, d_, B_, C_, A_, ctx.a_sn, h0_, ckpt, ctx.seg, du, dd, dB, dC, dA, dh0, ws)
         return du, dd, dB, dC, dA, dh0, None
@@ -138,10 +138,12 @@ def ssd_scan_reference(u, delta, B, C, A_neg, *, initial_state=None):
     u, delta, B, C, A_neg = (t.to(ct) for t in (u, delta, B, C, A_neg))
     h = torch.zeros((Bsz, H, Dh, N), dtype=ct, device=u.device) if initial_state is None else initial_state.to(ct)
     ys = []
-    for t in range(L):
-        dt = delta[:, t, :, None, None]
+    # the per-step slices come from unbind (one backward stack for all steps,
+    # where indexing [:, t] would scatter a full-size gradient per step)
+    for dl_t, B_t, C_t, u_t in zip(delta.unbind(1), B.unbind(1), C.unbind(1), u.unbind(1)):
+        dt = dl_t[:, :, None, None]
         decay = torch.exp(dt * A_neg[None, :, None, :])
-        inp = dt * B[:, t, :, None, :] * u[:, t, :, :, None]
+        inp = dt * B_t[:, :, None, :] * u_t[:, :, :, None]
         h = decay * h + inp
-        ys.append((h * C[:, t, :, None, :]).sum(-1))
+        ys.append((h * C_t[:, :, None, :]).sum(-1))
     return torch.stack(ys, dim=1)
