@@ -116,6 +116,21 @@ int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, const void* 
                void* dC, float* dA_neg, float* dh0, void* workspace,
                size_t workspace_bytes, void* stream);
 
+/* rr_ssd_bwd without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  The workspace is
+ * a 16 MiB static device array of the library (one per device, held until the
+ * process ends); the call allocates nothing.  A call whose
+ * rr_ssd_workspace_bytes(..., pass = 1) exceeds 16 MiB returns
+ * RR_EUNSUPPORTED (config 1 needs 36 KiB).  Every call on one device shares
+ * that array: calls that overlap on one GPU (other streams or threads) race.
+ * Arguments and results otherwise as rr_ssd_bwd. */
+int rr_ssd_bwd_noalloc(const float* dy, const float* dfinal, const void* u, const void* delta,
+                       const void* Bm, const void* Cm, const float* A_neg, int64_t A_stride_n, int dtype,
+                       int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N, int64_t seg,
+                       const float* h0, const float* ckpt, void* du, void* ddelta, void* dB,
+                       void* dC, float* dA_neg, float* dh0, void* stream);
+
 /* ------------------------------------------------------------------ GLA --
  * q/k/v [B,L,H,Dh], gates [B,L,H] (dtype).  y [B,L,H,Dh] fp32.
  * ckpt [B,H,nC,Dh(j),Dh(i)] fp32: state S[i,j] stored with i fastest, so

@@ -35,6 +35,9 @@
 #include "rr_common.h"
 #include "rr_internal.h"
 
+#include <atomic>
+#include <string>
+
 namespace {
 
 constexpr int kMaxT = 32;
@@ -695,6 +698,61 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
     return launch_bwd<InT, false>(a, f, q, B, s, dA_neg);
   });
   return RR_OK;
+}
+
+// ============================================== SSD backward, no allocation
+// rr_ssd_bwd for callers that cannot allocate device memory: the workspace is
+// `scratch`, a static device array of this library (one copy per device, held
+// until the process ends), whose address is looked up once per device.  The
+// SSD backward kernels write every workspace word before they read it (their
+// results do not depend on its prior contents), so nothing is cleared between
+// calls; calls that overlap on one device share the array and race.
+namespace {
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;   // 16 MiB
+constexpr int kNoAllocMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+std::atomic<void*> g_scratch_ptr[kNoAllocMaxDevices];
+
+// Device address of `scratch` on the current device (nullptr with the error set).
+void* scratch_ptr() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNoAllocMaxDevices) {
+    rr::fail(RR_EHIP, "ssd_bwd_noalloc: no current HIP device");
+    return nullptr;
+  }
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    void* addr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || addr == nullptr) {
+      rr::fail(RR_EHIP, std::string("ssd_bwd_noalloc: hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev].store(addr, std::memory_order_release);
+    p = addr;
+  }
+  return p;
+}
+}  // namespace
+
+extern "C" int rr_ssd_bwd_noalloc(const float* dy, const float* dfinal, const void* u, const void* delta,
+                                  const void* Bm, const void* Cm, const float* A_neg, int64_t A_stride_n,
+                                  int dtype, int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N,
+                                  int64_t seg, const float* h0, const float* ckpt, void* du, void* ddelta,
+                                  void* dB, void* dC, float* dA_neg, float* dh0, void* stream) {
+  if (int rc = check_dims("ssd_bwd_noalloc", B, L, H, Dh, N, seg, dtype, "Dh")) return rc;
+  if (A_stride_n != 0 && A_stride_n != 1)
+    return rr::fail(RR_EINVAL, "ssd_bwd_noalloc: A_stride_n must be 0 or 1");
+  const size_t need = rr_ssd_workspace_bytes(B, L, H, Dh, N, seg, A_stride_n, dtype, 1);
+  if (need > kNoAllocScratchBytes)
+    return rr::fail(RR_EUNSUPPORTED, "ssd_bwd_noalloc: this call needs " + std::to_string(need) +
+                                         " bytes of workspace, more than the library's " +
+                                         std::to_string(kNoAllocScratchBytes) +
+                                         "-byte device scratch; use rr_ssd_bwd with a caller workspace");
+  void* ws = scratch_ptr();
+  if (ws == nullptr) return RR_EHIP;
+  return rr_ssd_bwd(dy, dfinal, u, delta, Bm, Cm, A_neg, A_stride_n, dtype, B, L, H, Dh, N, seg, h0, ckpt, du,
+                    ddelta, dB, dC, dA_neg, dh0, ws, kNoAllocScratchBytes, stream);
 }
 
 // ====================================================================== GLA

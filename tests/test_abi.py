@@ -77,3 +77,18 @@ def test_ssd_gla_validation(lib):
     assert need > 0
     rc = lib.rr_rglru_fwd(p, p, 1, 2, 256, 64, 32, None, p, p, p, need - 1, None)
     assert rc == _lib.RR_EWORKSPACE
+
+
+def test_ssd_bwd_noalloc_rejects_beyond_its_scratch(lib):
+    """The no-allocation SSD backward refuses calls whose workspace exceeds its
+    16 MiB static scratch, before touching the device (B = 96: 75 MB)."""
+    p = ctypes.c_void_p(16)  # never dereferenced: the size check fails first
+    need = lib.rr_ssd_workspace_bytes(96, 512, 12, 64, 16, 32, 0, 1, 1)
+    assert need > (16 << 20)
+    rc = lib.rr_ssd_bwd_noalloc(p, None, p, p, p, p, p, 0, 1, 96, 512, 12, 64, 16, 32, None, p, p, p, p, p, p,
+                                None, None)
+    assert rc == _lib.RR_EUNSUPPORTED and b"16777216-byte device scratch" in lib.rr_last_error()
+    assert lib.rr_ssd_workspace_bytes(3, 512, 12, 64, 16, 32, 0, 1, 1) <= (16 << 20)   # config 1 fits
+    rc = lib.rr_ssd_bwd_noalloc(p, None, p, p, p, p, p, 0, 1, 3, 30, 12, 64, 16, 32, None, p, p, p, p, p, p,
+                                None, None)
+    assert rc == _lib.RR_EINVAL and b"L=30" in lib.rr_last_error()
