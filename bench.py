@@ -504,6 +504,119 @@ WORKLOADS = {
 }
 
 
+# ------------------------------------------------------------------ decode
+# One token of the single-step decode kernels on the cached states of the
+# BASELINE shapes; bytes per token = state read + written (fp32) + token
+# inputs (dtype) + y (fp32).
+DECODE = {
+    "ssd_c1": dict(kind="ssd", B=3, H=12, Dh=64, N=16),
+    "ssd_c4": dict(kind="ssd", B=8, H=80, Dh=64, N=128),
+    "gla_c2": dict(kind="gla", B=3, H=12, Dh=64),
+    "rglru_c3": dict(kind="rglru", B=8, D=2560),
+    "rotlru_c3": dict(kind="rotlru", B=8, D=2560),
+}
+
+
+def make_decode(cfg, device, dtype):
+    import torch
+    import mlx_recurrence_amd as mr
+    from mlx_recurrence_amd import _lib
+    g = torch.Generator().manual_seed(7)
+    es = torch.tensor([], dtype=dtype).element_size()
+    k = cfg["kind"]
+    B = cfg["B"]
+
+    def rnd(*shape):
+        return torch.randn(shape, generator=g).to(dtype).to(device)
+
+    if k == "ssd":
+        H, Dh, N = cfg["H"], cfg["Dh"], cfg["N"]
+        u, dl = rnd(B, H, Dh), (torch.rand((B, H), generator=g) * 0.1 + 0.01).to(dtype).to(device)
+        Bm, Cm = rnd(B, H, N), rnd(B, H, N)
+        A = -torch.rand((H,), generator=g).to(device) - 0.1
+        state = torch.zeros((B, H, Dh, N), device=device)
+        y = torch.empty((B, H, Dh), device=device)
+        nbytes = 2 * state.numel() * 4 + (u.numel() + dl.numel() + 2 * Bm.numel()) * es + H * 4 + y.numel() * 4
+        raw = (lambda: _lib.ssd_step(u, dl, Bm, Cm, A, 0, state, y))
+        eager = (lambda: mr.ssd_step(u, dl, Bm, Cm, A[:, None].expand(H, N), state))
+    elif k == "gla":
+        H, Dh = cfg["H"], cfg["Dh"]
+        q, kk, v = rnd(B, H, Dh), rnd(B, H, Dh), rnd(B, H, Dh)
+        gt = torch.sigmoid(torch.randn((B, H), generator=g) + 2).to(dtype).to(device)
+        state = torch.zeros((B, H, Dh, Dh), device=device)
+        y = torch.empty((B, H, Dh), device=device)
+        nbytes = 2 * state.numel() * 4 + (3 * q.numel() + gt.numel()) * es + y.numel() * 4
+        raw = (lambda: _lib.gla_step(q, kk, v, gt, state, y))
+        eager = (lambda: mr.gla_step(q, kk, v, gt, state))
+    elif k == "rglru":
+        D = cfg["D"]
+        a = torch.sigmoid(torch.randn((B, D), generator=g) + 2).to(dtype).to(device)
+        x = rnd(B, D)
+        state = torch.zeros((B, D), device=device)
+        y = torch.empty((B, D), device=device)
+        nbytes = 2 * state.numel() * 4 + 2 * a.numel() * es + y.numel() * 4
+        raw = (lambda: _lib.rglru_step(a, x, state, y))
+        eager = (lambda: mr.rglru_step(a, x, state))
+    else:
+        Dp = cfg["D"] // 2
+        a = torch.sigmoid(torch.randn((B, Dp), generator=g) + 2).to(dtype).to(device)
+        th = torch.rand((B, Dp), generator=g) * 0.2 - 0.1
+        cs, sn = torch.cos(th).to(dtype).to(device), torch.sin(th).to(dtype).to(device)
+        x = rnd(B, 2 * Dp)
+        state = torch.zeros((B, 2 * Dp), device=device)
+        y = torch.empty((B, 2 * Dp), device=device)
+        nbytes = 2 * state.numel() * 4 + (3 * a.numel() + x.numel()) * es + y.numel() * 4
+        raw = (lambda: _lib.rotlru_step(a, cs, sn, x, state, y))
+        eager = (lambda: mr.rotlru_step(a, cs, sn, x, state))
+    return dict(raw=raw, eager=eager, bytes=nbytes, batch=B)
+
+
+def measure_decode(name, dtype, device, tokens=200):
+    """Per-token latency of a decode step: `tokens` consecutive steps captured
+    in one HIP graph (the way a decode loop runs them), timed between HIP
+    events on the launch stream; and the eager Python call (mr.*_step) per
+    token."""
+    import torch
+    w = make_decode(DECODE[name], device, dtype)
+    hip = _Hip()
+    stream = torch.cuda.Stream(device)
+    sh = ctypes.c_void_p(stream.cuda_stream)
+    with torch.cuda.stream(stream):
+        w["raw"]()
+        torch.cuda.synchronize()
+        g = hip.capture(sh, lambda: [w["raw"]() for _ in range(tokens)])
+    ex = ctypes.c_void_p()
+    hip.ok(hip.lib.hipGraphInstantiate(ctypes.byref(ex), g, None, None, 0), "hipGraphInstantiate")
+    hip.launch(ex, sh)
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(5):
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st.record(stream)
+        hip.launch(ex, sh)
+        en.record(stream)
+        en.synchronize()
+        us = st.elapsed_time(en) * 1e3 / tokens
+        best = us if best is None else min(best, us)
+    hip.lib.hipGraphExecDestroy(ex)
+    hip.lib.hipGraphDestroy(g)
+    with torch.no_grad():
+        for _ in range(10):
+            w["eager"]()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(tokens):
+            w["eager"]()
+        torch.cuda.synchronize()
+    eager_us = (time.perf_counter() - t0) * 1e6 / tokens
+    gbs = w["bytes"] / (best * 1e-6) / 1e9
+    print(f"[bench] decode {name}: {best:.2f} us per token (graph), {eager_us:.1f} us eager", file=sys.stderr,
+          flush=True)
+    return dict(config=DECODE[name], us_per_token=best, eager_us_per_token=eager_us,
+                tokens_per_s=w["batch"] / (best * 1e-6), bytes_per_token=w["bytes"],
+                roofline=dict(bound="hbm", achieved=gbs, peak=HBM_PEAK_GBS, unit="GB/s", frac=gbs / HBM_PEAK_GBS))
+
+
 # ------------------------------------------------------------------ measure
 def measure(name, steps, warmup, dtype, device, cpu_seconds):
     import torch
@@ -881,6 +994,7 @@ def main():
     ap.add_argument("--also", default="gla,rglru,rotlru,ssd_c4",
                     help="comma-separated extra workloads reported beside (each with its roofline and CPU leg)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true", help="skip the single-token decode step lines")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU work per CPU baseline (the headline workload; the extra workloads get half)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
@@ -942,6 +1056,8 @@ def main():
         print(f"[bench] {nm}: {r['ms_per_step'] * 1e3:.1f} us per step, {r['tokens_per_s']:.4g} tokens/s",
               file=sys.stderr, flush=True)
 
+    decode = {} if args.no_decode else {nm: measure_decode(nm, dtype, device) for nm in DECODE}
+
     r = main_res
     cfg = dict(workload=r["workload"], **r["cfg"], input_dtype="bf16", state_dtype="f32")
     line = {
@@ -976,6 +1092,7 @@ def main():
         "peak_transient_bytes": r["peak_transient_bytes"],
         "state_history_bytes": r["state_history_bytes"],
         "also": extras,
+        "decode": decode,
     }
     print(json.dumps(line), flush=True)
 

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define RR_ABI_VERSION 7
+#define RR_ABI_VERSION 8
 
 enum rr_dtype { RR_F32 = 0, RR_BF16 = 1, RR_F16 = 2 };
 
@@ -243,6 +243,40 @@ int rr_rotlru_theta_bwd(const float* dy, const float* dfinal, const void* a, con
                         const void* x, int dtype, int64_t B, int64_t L, int64_t Dp, int64_t seg,
                         const float* h0, const float* ckpt, void* da, void* dtheta, void* dx,
                         float* dh0, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------- decode: one token --
+ * The recurrent update of one token on a cached state, updated in place, one
+ * launch per call.  The reference lists this as its next inference step
+ * (docs/validation/BOTTLENECK_ANALYSIS.md:105-119: one fused kernel per layer
+ * type on the final-state cache layouts of the *_scan_with_state functions,
+ * ssd.py:365-375, gla.py:321-329, rglru.py:259-267, rotlru.py:323-331); the
+ * arithmetic is one step of the reference recurrences (ssd.py:85-111,
+ * gla.py:78-100, rglru.py:88-99, rotlru.py:101-122).  Token inputs are in
+ * `dtype`; the state (fp32) is the scans' final-state layout, so a scan's
+ * final state continues directly; y is fp32.  Not differentiable.
+ */
+
+/* SSD: u [B,H,Dh], delta [B,H], Bm / Cm [B,H,N] (dtype); A_neg as for
+ * rr_ssd_fwd (A_stride_n 0: [H], 1: [H,N]); state [B,H,Dh,N]; y [B,H,Dh].
+ * N <= 256. */
+int rr_ssd_step(const void* u, const void* delta, const void* Bm, const void* Cm, const float* A_neg,
+                int64_t A_stride_n, int dtype, int64_t B, int64_t H, int64_t Dh, int64_t N, float* state,
+                float* y, void* stream);
+
+/* GLA: q / k / v [B,H,Dh], gates [B,H] (dtype); state [B,H,Dh(i),Dh(j)];
+ * y [B,H,Dh] (y[j] = sum_i q[i] S'[i,j], the post-update state).  Dh <= 256. */
+int rr_gla_step(const void* q, const void* k, const void* v, const void* gates, int dtype, int64_t B,
+                int64_t H, int64_t Dh, float* state, float* y, void* stream);
+
+/* RG-LRU: a, x [B,D] (dtype; x the gated input, as for rr_rglru_fwd);
+ * state [B,D]; y [B,D]. */
+int rr_rglru_step(const void* a, const void* x, int dtype, int64_t B, int64_t D, float* state, float* y,
+                  void* stream);
+
+/* rotLRU: a, cs, sn [B,Dp]; x [B,2*Dp] interleaved (dtype); state [B,2*Dp]
+ * interleaved (8-byte aligned); y [B,2*Dp]. */
+int rr_rotlru_step(const void* a, const void* cs, const void* sn, const void* x, int dtype, int64_t B,
+                   int64_t Dp, float* state, float* y, void* stream);
 
 #ifdef __cplusplus
 }

@@ -26,6 +26,7 @@ from .rotlru import (rotlru_scan, rotlru_scan_with_state, rotlru_scan_reference,
                      rotlru_theta_scan_with_state)
 from ._chassis import DEFAULT_SEG, SIMD_WIDTH, get_or_build_kernel, check_segment_shape, parity_check
 from ._lib import async_status
+from .step import ssd_step, gla_step, rglru_step, rotlru_step
 
 __all__ = [
     "ssd_scan",
@@ -51,6 +52,10 @@ __all__ = [
     "check_segment_shape",
     "parity_check",
     "async_status",
+    "ssd_step",
+    "gla_step",
+    "rglru_step",
+    "rotlru_step",
 ]
 
 __version__ = "0.3.0+gfx950"

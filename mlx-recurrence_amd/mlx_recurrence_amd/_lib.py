@@ -59,6 +59,10 @@ _SIGS = {
     "rr_rotlru_bwd": (_c_int, [_c_ptr] * 6 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 8 + [_c_size, _c_ptr]),
     "rr_rotlru_theta_fwd": (_c_int, [_c_ptr] * 3 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
     "rr_rotlru_theta_bwd": (_c_int, [_c_ptr] * 5 + [_c_int] + [_c_i64] * 4 + [_c_ptr] * 7 + [_c_size, _c_ptr]),
+    "rr_ssd_step": (_c_int, [_c_ptr] * 5 + [_c_i64, _c_int] + [_c_i64] * 4 + [_c_ptr] * 3),
+    "rr_gla_step": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 3 + [_c_ptr] * 3),
+    "rr_rglru_step": (_c_int, [_c_ptr] * 2 + [_c_int] + [_c_i64] * 2 + [_c_ptr] * 3),
+    "rr_rotlru_step": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 2 + [_c_ptr] * 3),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGS)
@@ -354,3 +358,29 @@ def rotlru_theta_bwd(dy, dfinal, a, th, x, h0, ckpt, seg, da, dth, dx, dh0, ws):
                                     B, L, Dp, seg, ptr(h0), ptr(ckpt), ptr(da), ptr(dth), ptr(dx),
                                     ptr(dh0), ptr(ws), ws.numel(), stream_of(a))
     _check(rc, "rr_rotlru_theta_bwd")
+
+
+# ---------------------------------------------------------------- decode steps
+def ssd_step(u, delta, Bm, Cm, A, a_stride_n, state, y):
+    B, H, Dh = u.shape
+    N = Bm.shape[-1]
+    _check(load().rr_ssd_step(ptr(u), ptr(delta), ptr(Bm), ptr(Cm), ptr(A), a_stride_n, DTYPE_CODE[u.dtype],
+                              B, H, Dh, N, ptr(state), ptr(y), stream_of(u)), "rr_ssd_step")
+
+
+def gla_step(q, k, v, g, state, y):
+    B, H, Dh = q.shape
+    _check(load().rr_gla_step(ptr(q), ptr(k), ptr(v), ptr(g), DTYPE_CODE[q.dtype], B, H, Dh, ptr(state), ptr(y),
+                              stream_of(q)), "rr_gla_step")
+
+
+def rglru_step(a, x, state, y):
+    B, D = a.shape
+    _check(load().rr_rglru_step(ptr(a), ptr(x), DTYPE_CODE[a.dtype], B, D, ptr(state), ptr(y), stream_of(a)),
+           "rr_rglru_step")
+
+
+def rotlru_step(a, cs, sn, x, state, y):
+    B, Dp = a.shape
+    _check(load().rr_rotlru_step(ptr(a), ptr(cs), ptr(sn), ptr(x), DTYPE_CODE[a.dtype], B, Dp, ptr(state), ptr(y),
+                                 stream_of(a)), "rr_rotlru_step")
