@@ -131,18 +131,22 @@ def make_ssd(cfg, device, dtype):
     import torch
     from mlx_recurrence_amd import _lib
     B, L, H, Dh, N, seg = cfg["B"], cfg["L"], cfg["H"], cfg["Dh"], cfg["N"], cfg["seg"]
+    dense = cfg.get("dense", False)   # A_neg [H, N] varying over n (the reference tests' A): VALU engine
+    dtype = torch.float32 if cfg.get("dtype") == "f32" else dtype
     g = torch.Generator().manual_seed(cfg.get("seed", 1))
     u = _gen((B, L, H, Dh), g)
     delta = _gen((B, L, H), g).abs() * 0.1 + 0.01
     Bm = _gen((B, L, H, N), g)
     Cm = _gen((B, L, H, N), g)
-    A = -torch.exp(_gen((H,), g, "uniform") * math.log(16.0))
+    A = -torch.exp(_gen((H, N) if dense else (H,), g, "uniform") * math.log(16.0))
     dy = _gen((B, L, H, Dh), g)
-    cpu = dict(u=u, delta=delta, Bm=Bm, Cm=Cm, A_neg=A[:, None].expand(H, N).contiguous(), dy=dy)
+    cpu = dict(u=u, delta=delta, Bm=Bm, Cm=Cm, A_neg=A.contiguous() if dense else A[:, None].expand(H, N).contiguous(),
+               dy=dy)
     d = {k: (v.to(dtype) if k not in ("A_neg", "dy") else v).to(device) for k, v in cpu.items()}
     # A per head, broadcast over N (stride 0): the layout the kernels take as A_stride_n = 0
+    a_sn = 1 if dense else 0
     d["A"] = A.to(device)
-    d["A_neg"] = d["A"][:, None].expand(H, N)
+    d["A_neg"] = d["A"] if dense else d["A"][:, None].expand(H, N)
     T = _lib.chunk_len(L, seg)
     nC = L // T
     f32 = torch.float32
@@ -154,8 +158,8 @@ def make_ssd(cfg, device, dtype):
         dB=torch.empty((B, L, H, N), dtype=dtype, device=device),
         dC=torch.empty((B, L, H, N), dtype=dtype, device=device),
         dA=torch.empty((H, N), dtype=f32, device=device),
-        wsf=_lib.ssd_workspace(B, L, H, Dh, N, seg, 0, dtype, 0, device),
-        wsb=_lib.ssd_workspace(B, L, H, Dh, N, seg, 0, dtype, 1, device),
+        wsf=_lib.ssd_workspace(B, L, H, Dh, N, seg, a_sn, dtype, 0, device),
+        wsb=_lib.ssd_workspace(B, L, H, Dh, N, seg, a_sn, dtype, 1, device),
     )
     es = torch.tensor([], dtype=dtype).element_size()
     n_u, n_d, n_bc, n_ck = B * L * H * Dh, B * L * H, B * L * H * N, B * H * nC * Dh * N
@@ -164,17 +168,17 @@ def make_ssd(cfg, device, dtype):
     bwd_bytes = n_u * 4 + n_ck * 4 + inputs + (n_u + n_d + 2 * n_bc) * es + H * N * 4
 
     def fwd():
-        _lib.ssd_fwd(d["u"], d["delta"], d["Bm"], d["Cm"], d["A"], 0, None, seg, out["y"], out["ckpt"], out["wsf"])
+        _lib.ssd_fwd(d["u"], d["delta"], d["Bm"], d["Cm"], d["A"], a_sn, None, seg, out["y"], out["ckpt"], out["wsf"])
 
     def bwd():
-        _lib.ssd_bwd(d["dy"], None, d["u"], d["delta"], d["Bm"], d["Cm"], d["A"], 0, None, out["ckpt"], seg,
+        _lib.ssd_bwd(d["dy"], None, d["u"], d["delta"], d["Bm"], d["Cm"], d["A"], a_sn, None, out["ckpt"], seg,
                      out["du"], out["dd"], out["dB"], out["dC"], out["dA"], None, out["wsb"])
 
     def eager():
         import mlx_recurrence_amd as mr
         xs = [d[k].detach().requires_grad_(True) for k in ("u", "delta", "Bm", "Cm")]
         A_ = d["A"].detach().requires_grad_(True)
-        y = mr.ssd_scan(*xs, A_[:, None].expand(H, N), seg=seg)
+        y = mr.ssd_scan(*xs, A_ if dense else A_[:, None].expand(H, N), seg=seg)
         y.backward(d["dy"])
 
     # CPU leg: the reference's per-step loop (ssd_scan_reference, fp32 torch on
@@ -185,8 +189,8 @@ def make_ssd(cfg, device, dtype):
     def cpu_sample():
         import mlx_recurrence_amd as mr
         xs = [cpu[k][:cb, :cl].to(dtype).float().requires_grad_(True) for k in ("u", "delta", "Bm", "Cm")]
-        A_ = cpu["A_neg"][:, 0].clone().requires_grad_(True)
-        y = mr.ssd_scan_reference(*xs, A_[:, None].expand(H, N))
+        A_ = (cpu["A_neg"] if dense else cpu["A_neg"][:, 0]).clone().requires_grad_(True)
+        y = mr.ssd_scan_reference(*xs, A_ if dense else A_[:, None].expand(H, N))
         y.backward(cpu["dy"][:cb, :cl])
 
     return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L, cpu_tokens=cb * cl,
@@ -202,6 +206,7 @@ def make_gla(cfg, device, dtype):
     import torch
     from mlx_recurrence_amd import _lib
     B, L, H, Dh, seg = cfg["B"], cfg["L"], cfg["H"], cfg["Dh"], cfg["seg"]
+    dtype = torch.float32 if cfg.get("dtype") == "f32" else dtype
     g = torch.Generator().manual_seed(cfg.get("seed", 2))
     q, k, v = (_gen((B, L, H, Dh), g) / math.sqrt(Dh) for _ in range(3))
     gates = torch.sigmoid(_gen((B, L, H), g) + 2.0)
@@ -497,6 +502,18 @@ WORKLOADS = {
                dict(B=8, L=4096, H=80, Dh=64, N=128, seg=32)),
     # configs 1 and 2 with 32x the batch: the same kernels with the GPU filled
     # (at B = 3 the passes are latency-bound), reported beside the headline
+    # the reference's general input contract on the VALU engine: A_neg [H, N]
+    # varying over n (its tests' draw), fp32 inputs, and its production SSD
+    # shape Dh 128, N 64 (chunked forward, VALU backward)
+    "ssd_dense": ("ssd_scan fwd+bwd, dense A_neg [H, N] (BASELINE config 1 shape)", make_ssd,
+                  dict(B=3, L=512, H=12, Dh=64, N=16, seg=32, dense=True)),
+    "ssd_f32": ("ssd_scan fwd+bwd, fp32 inputs (BASELINE config 1 shape)", make_ssd,
+                dict(B=3, L=512, H=12, Dh=64, N=16, seg=32, dtype="f32")),
+    "ssd_dh128": ("ssd_scan fwd+bwd at Dh 128, N 64 (B3 L512 H12)", make_ssd,
+                  dict(B=3, L=512, H=12, Dh=128, N=64, seg=32)),
+    "gla_f32": ("gla_scan fwd+bwd, fp32 inputs (BASELINE config 2 shape)", make_gla,
+                dict(B=3, L=512, H=12, Dh=64, seg=32, dtype="f32")),
+    "gla_dh128": ("gla_scan fwd+bwd at Dh 128 (B3 L512 H12)", make_gla, dict(B=3, L=512, H=12, Dh=128, seg=32)),
     "ssd_b96": ("ssd_scan fwd+bwd (BASELINE config 1 shape, B = 96)", make_ssd,
                 dict(B=96, L=512, H=12, Dh=64, N=16, seg=32)),
     "gla_b96": ("gla_scan fwd+bwd (BASELINE config 2 shape, B = 96)", make_gla,
@@ -783,7 +800,8 @@ COUNTER_SETS = {
     "mfma": ["SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU",
              "SQ_INSTS_MFMA", "SQ_BUSY_CU_CYCLES"],
 }
-PROFILED_WORKLOADS = ["ssd", "gla", "rglru", "rotlru", "rglru_gated", "rotlru_theta", "ssd_c4", "ssd_b96", "gla_b96"]
+PROFILED_WORKLOADS = ["ssd", "gla", "rglru", "rotlru", "rglru_gated", "rotlru_theta", "ssd_c4", "ssd_b96", "gla_b96",
+                      "ssd_dense", "ssd_f32", "ssd_dh128", "gla_f32", "gla_dh128"]
 PROFILE_COMMANDS = [
     "rocprofv3 --kernel-trace --stats -d $R/gpurun_out/prof_trace -o trace --output-format csv -- "
     "python3 bench.py --steps 20 --warmup 3 --no-cpu --also " + ",".join(PROFILED_WORKLOADS[1:]),
