@@ -27,6 +27,7 @@ from .rotlru import (rotlru_scan, rotlru_scan_with_state, rotlru_scan_reference,
 from ._chassis import DEFAULT_SEG, SIMD_WIDTH, get_or_build_kernel, check_segment_shape, parity_check
 from ._lib import async_status
 from .step import ssd_step, gla_step, rglru_step, rotlru_step
+from .gdn import gated_deltanet_scan, gated_deltanet_scan_with_state, gated_deltanet_reference
 
 __all__ = [
     "ssd_scan",
@@ -56,6 +57,9 @@ __all__ = [
     "gla_step",
     "rglru_step",
     "rotlru_step",
+    "gated_deltanet_scan",
+    "gated_deltanet_scan_with_state",
+    "gated_deltanet_reference",
 ]
 
 __version__ = "0.3.0+gfx950"

@@ -63,6 +63,8 @@ _SIGS = {
     "rr_gla_step": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 3 + [_c_ptr] * 3),
     "rr_rglru_step": (_c_int, [_c_ptr] * 2 + [_c_int] + [_c_i64] * 2 + [_c_ptr] * 3),
     "rr_rotlru_step": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 2 + [_c_ptr] * 3),
+    "rr_gdn_fwd": (_c_int, [_c_ptr] * 5 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 4),
+    "rr_gdn_bwd": (_c_int, [_c_ptr] * 7 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 9),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGS)
@@ -384,3 +386,17 @@ def rotlru_step(a, cs, sn, x, state, y):
     B, Dp = a.shape
     _check(load().rr_rotlru_step(ptr(a), ptr(cs), ptr(sn), ptr(x), DTYPE_CODE[a.dtype], B, Dp, ptr(state), ptr(y),
                                  stream_of(a)), "rr_rotlru_step")
+
+
+# ---------------------------------------------------------------- Gated DeltaNet
+def gdn_fwd(q, k, v, alpha, beta, h0, seg, y, ckpt):
+    B, L, H, Dh = q.shape
+    _check(load().rr_gdn_fwd(ptr(q), ptr(k), ptr(v), ptr(alpha), ptr(beta), DTYPE_CODE[q.dtype], B, L, H, Dh, seg,
+                             ptr(h0), ptr(y), ptr(ckpt), stream_of(q)), "rr_gdn_fwd")
+
+
+def gdn_bwd(dy, dfinal, q, k, v, alpha, beta, h0, ckpt, seg, dq, dk, dv, dalpha, dbeta, dh0):
+    B, L, H, Dh = q.shape
+    _check(load().rr_gdn_bwd(ptr(dy), ptr(dfinal), ptr(q), ptr(k), ptr(v), ptr(alpha), ptr(beta),
+                             DTYPE_CODE[q.dtype], B, L, H, Dh, seg, ptr(h0), ptr(ckpt), ptr(dq), ptr(dk), ptr(dv),
+                             ptr(dalpha), ptr(dbeta), ptr(dh0), stream_of(q)), "rr_gdn_bwd")

@@ -13,6 +13,10 @@ adjoints (D-CSIL/mlx-recurrence v0.3.0):
           gla.py:321-329, adjoint gla.py:184-236
   RG-LRU  forward rglru.py:274-282, adjoint rglru.py:36-39 and :166-180
   rotLRU  forward rotlru.py:338-351, adjoint rotlru.py:317-322 and :205-235
+  Gated DeltaNet (the reference's designed next plug-in, not code there):
+          recurrence and output docs/DESIGN_gated_deltanet.md:56-90 (R1'',
+          R2'), adjoint :334-440 (B0, Bq, Bp', Bv, grad_k terms A + B, Bbeta,
+          Balpha)
 
 Extensions beyond the reference, present in the kernels and checked here:
 an optional initial state h0 and a cotangent ``dfinal`` on the final state
@@ -55,6 +59,8 @@ __all__ = [
     "gla_causal_linear_attention",
     "rglru_discounted_sum",
     "chunked_cumsum_scan",
+    "gdn_forward",
+    "gdn_backward",
 ]
 
 
@@ -343,3 +349,59 @@ def rotlru_backward(dy, a, cs, sn, x, h0=None, dfinal=None):
         lu, lw = at * (c * lu + s * lw), at * (-s * lu + c * lw)
     dh0 = np.stack([lu, lw], axis=-1).reshape(B, 2 * Dp)
     return da, dcs, dsn, dx.reshape(B, L, 2 * Dp), dh0
+
+
+# ------------------------------------------------------------ Gated DeltaNet
+def _gdn_states(q, k, v, alpha, beta, h0):
+    B, L, H, Dh = q.shape
+    hs = np.empty((L + 1, B, H, Dh, Dh))
+    hs[0] = 0.0 if h0 is None else h0
+    y = np.empty((B, L, H, Dh))
+    for t in range(L):
+        kt, vt = k[:, t], v[:, t]                                   # [B,H,Dh]
+        a, b = alpha[:, t, :, None, None], beta[:, t, :, None, None]
+        p = np.einsum("bhi,bhij->bhj", kt, hs[t])                   # k^T S_{t-1}
+        hs[t + 1] = a * (hs[t] - b * kt[..., :, None] * p[..., None, :]) + b * kt[..., :, None] * vt[..., None, :]
+        y[:, t] = np.einsum("bhi,bhij->bhj", q[:, t], hs[t + 1])     # o_t = S_t^T q_t
+    return y, hs
+
+
+def gdn_forward(q, k, v, alpha, beta, h0=None):
+    """Gated DeltaNet, per (b, h): S_t = alpha_t (I - beta_t k_t k_t^T) S_{t-1}
+    + beta_t k_t v_t^T, o_t = S_t^T q_t (DESIGN_gated_deltanet.md:56-90, the
+    reference's pinned convention: S[i, j], k and q on the row axis i, v and o
+    on the column axis j).  q, k, v [B,L,H,Dh], alpha, beta [B,L,H] (already
+    activated).  Returns y [B,L,H,Dh] and the final state [B,H,Dh(i),Dh(j)]."""
+    q, k, v, alpha, beta, h0 = _f64(q, k, v, alpha, beta, h0)
+    y, hs = _gdn_states(q, k, v, alpha, beta, h0)
+    return y, hs[-1].copy()
+
+
+def gdn_backward(dy, q, k, v, alpha, beta, h0=None, dfinal=None):
+    """Explicit float64 adjoint (DESIGN_gated_deltanet.md:334-440), newest to
+    oldest with dS the adjoint of S_t:
+      dS += q_t go_t^T;  dq_t = S_t go_t;  d = k_t^T dS;  p = k_t^T S_{t-1};
+      dv_t = beta d;  dk_t = dS (beta v - alpha beta p) - alpha beta S_{t-1} d;
+      dbeta_t = d . (v - alpha p);  dalpha_t = <dS, S_{t-1}> - beta d . p;
+      dS <- alpha (dS - beta k_t d^T).
+    Returns (dq, dk, dv, dalpha, dbeta, dh0)."""
+    dy, q, k, v, alpha, beta, h0, dfinal = _f64(dy, q, k, v, alpha, beta, h0, dfinal)
+    B, L, H, Dh = q.shape
+    _, hs = _gdn_states(q, k, v, alpha, beta, h0)
+    lam = np.zeros((B, H, Dh, Dh)) if dfinal is None else dfinal.copy()
+    dq, dk, dv = np.empty_like(q), np.empty_like(k), np.empty_like(v)
+    da, db = np.empty_like(alpha), np.empty_like(beta)
+    for t in range(L - 1, -1, -1):
+        kt, vt, go = k[:, t], v[:, t], dy[:, t]
+        a, b = alpha[:, t, :, None], beta[:, t, :, None]            # [B,H,1]
+        sp, sc = hs[t], hs[t + 1]
+        lam = lam + q[:, t, :, :, None] * go[:, :, None, :]          # (B0)
+        dq[:, t] = np.einsum("bhij,bhj->bhi", sc, go)                # (Bq)
+        d = np.einsum("bhi,bhij->bhj", kt, lam)
+        p = np.einsum("bhi,bhij->bhj", kt, sp)
+        dv[:, t] = b * d                                             # (Bv)
+        dk[:, t] = np.einsum("bhij,bhj->bhi", lam, b * vt - a * b * p) - a * b * np.einsum("bhij,bhj->bhi", sp, d)
+        db[:, t] = (d * (vt - a * p)).sum(-1)                        # (Bbeta)
+        da[:, t] = (lam * sp).sum((-1, -2)) - beta[:, t] * (d * p).sum(-1)   # (Balpha)
+        lam = a[..., None] * (lam - b[..., None] * kt[..., :, None] * d[..., None, :])   # (Bp')
+    return dq, dk, dv, da, db, lam

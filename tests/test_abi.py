@@ -33,7 +33,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.rr_abi_version() == 8
+    assert lib.rr_abi_version() == 9
 
 
 @pytest.mark.parametrize("L,seg,T", [(512, 32, 32), (96, 16, 16), (128, 64, 32), (96, 48, 16),
@@ -92,3 +92,19 @@ def test_ssd_bwd_noalloc_rejects_beyond_its_scratch(lib):
     rc = lib.rr_ssd_bwd_noalloc(p, None, p, p, p, p, p, 0, 1, 3, 30, 12, 64, 16, 32, None, p, p, p, p, p, p,
                                 None, None)
     assert rc == _lib.RR_EINVAL and b"L=30" in lib.rr_last_error()
+
+
+def test_gdn_validation(lib):
+    """Gated DeltaNet entry points: shape rules and the kernels' Dh / interval
+    limits are reported before any launch."""
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    rc = lib.rr_gdn_fwd(p, p, p, p, p, 0, 1, 30, 2, 64, 32, None, p, p, None)
+    assert rc == _lib.RR_EINVAL and b"L=30" in lib.rr_last_error()
+    rc = lib.rr_gdn_fwd(p, p, p, p, p, 0, 1, 64, 2, 128, 32, None, p, p, None)
+    assert rc == _lib.RR_EUNSUPPORTED and b"Dh must be 32 or 64" in lib.rr_last_error()
+    rc = lib.rr_gdn_fwd(p, p, p, p, p, 0, 1, 12, 2, 64, 4, None, p, p, None)
+    assert rc == _lib.RR_EUNSUPPORTED and b"multiple of 8" in lib.rr_last_error()
+    rc = lib.rr_gdn_fwd(p, p, p, p, None, 0, 1, 64, 2, 64, 32, None, p, p, None)
+    assert rc == _lib.RR_EINVAL and b"null pointer" in lib.rr_last_error()
+    rc = lib.rr_gdn_bwd(p, None, p, p, p, p, p, 0, 1, 64, 2, 64, 32, None, p, p, p, None, p, p, None, None)
+    assert rc == _lib.RR_EINVAL and b"null pointer" in lib.rr_last_error()
