@@ -488,6 +488,65 @@ def make_rotlru(cfg, device, dtype):
                 io_bytes=n_x * 4 + (3 * n_p + n_x) * es)
 
 
+
+def make_gdn(cfg, device, dtype):
+    """Gated DeltaNet at config 2's shape: q, k unit-normalised N(0,1) rows;
+    v ~ N(0,1); alpha = exp(-U(0.01, 0.5)); beta = sigmoid(N(0,1)); dO ~ N(0,1)."""
+    import torch
+    from mlx_recurrence_amd import _lib
+    B, L, H, Dh, seg = cfg["B"], cfg["L"], cfg["H"], cfg["Dh"], cfg["seg"]
+    g = torch.Generator().manual_seed(cfg.get("seed", 5))
+    q, k = (torch.nn.functional.normalize(_gen((B, L, H, Dh), g), dim=-1) for _ in range(2))
+    v = _gen((B, L, H, Dh), g)
+    alpha = torch.exp(-(0.01 + 0.49 * _gen((B, L, H), g, "uniform")))
+    beta = torch.sigmoid(_gen((B, L, H), g))
+    dy = _gen((B, L, H, Dh), g)
+    cpu = dict(q=q, k=k, v=v, alpha=alpha, beta=beta, dy=dy)
+    d = {kk: (vv.to(dtype) if kk != "dy" else vv).to(device) for kk, vv in cpu.items()}
+    T = _lib.chunk_len(L, seg)
+    nC = L // T
+    f32 = torch.float32
+    out = dict(
+        y=torch.empty((B, L, H, Dh), dtype=f32, device=device),
+        ckpt=torch.empty((B, H, nC, Dh, Dh), dtype=f32, device=device),
+        dq=torch.empty((B, L, H, Dh), dtype=dtype, device=device),
+        dk=torch.empty((B, L, H, Dh), dtype=dtype, device=device),
+        dv=torch.empty((B, L, H, Dh), dtype=dtype, device=device),
+        da=torch.empty((B, L, H), dtype=dtype, device=device),
+        db=torch.empty((B, L, H), dtype=dtype, device=device),
+    )
+    es = torch.tensor([], dtype=dtype).element_size()
+    n_x, n_g, n_ck = B * L * H * Dh, B * L * H, B * H * nC * Dh * Dh
+    inputs = (3 * n_x + 2 * n_g) * es
+    fwd_bytes = inputs + n_x * 4 + n_ck * 4
+    bwd_bytes = n_x * 4 + n_ck * 4 + inputs + (3 * n_x + 2 * n_g) * es
+
+    def fwd():
+        _lib.gdn_fwd(d["q"], d["k"], d["v"], d["alpha"], d["beta"], None, seg, out["y"], out["ckpt"])
+
+    def bwd():
+        _lib.gdn_bwd(d["dy"], None, d["q"], d["k"], d["v"], d["alpha"], d["beta"], None, out["ckpt"], seg,
+                     out["dq"], out["dk"], out["dv"], out["da"], out["db"], None)
+
+    def eager():
+        import mlx_recurrence_amd as mr
+        xs = [d[kk].detach().requires_grad_(True) for kk in ("q", "k", "v", "alpha", "beta")]
+        y = mr.gated_deltanet_scan(*xs, seg=seg)
+        y.backward(d["dy"])
+
+    cl = min(L, 128)
+
+    def cpu_sample():   # gated_deltanet_reference (fp32 torch, host) with autograd, first cl steps
+        import mlx_recurrence_amd as mr
+        xs = [cpu[kk][:, :cl].to(dtype).float().requires_grad_(True) for kk in ("q", "k", "v", "alpha", "beta")]
+        mr.gated_deltanet_reference(*xs).backward(cpu["dy"][:, :cl])
+
+    return dict(fwd=fwd, bwd=bwd, eager=eager, cpu=cpu_sample, out=out, tokens=B * L, cpu_tokens=B * cl,
+                cpu_desc=f"B={B}, the first {cl} of L={L} steps", fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes,
+                state_hist_bytes=B * L * H * Dh * Dh * 4, ckpt_bytes=n_ck * 4,
+                io_bytes=n_x * 4 + (3 * n_x + 2 * n_g) * es)
+
+
 WORKLOADS = {
     "ssd": ("ssd_scan fwd+bwd (BASELINE config 1)", make_ssd,
             dict(B=3, L=512, H=12, Dh=64, N=16, seg=32)),
@@ -518,6 +577,8 @@ WORKLOADS = {
                 dict(B=96, L=512, H=12, Dh=64, N=16, seg=32)),
     "gla_b96": ("gla_scan fwd+bwd (BASELINE config 2 shape, B = 96)", make_gla,
                 dict(B=96, L=512, H=12, Dh=64, seg=32)),
+    "gdn": ("gated_deltanet_scan fwd+bwd, sequential kernels (BASELINE config 2 shape)", make_gdn,
+            dict(B=3, L=512, H=12, Dh=64, seg=32)),
 }
 
 
