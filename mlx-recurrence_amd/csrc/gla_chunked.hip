@@ -45,6 +45,7 @@ constexpr int64_t kGlaWholeBwdMaxChunks = 16;
 
 int gla2_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass) {
   if (B * H >= kGlaWholeMinHeads && (pass == 0 || nC <= kGlaWholeBwdMaxChunks)) return chunked::kWhole;
+  if (pass == 0 && res_fwd_supported(B, H, nC, Dh, Dh)) return chunked::kRes;   // short heads, resident
   if (Dh * Dh > chunked::kDirectMaxState) return chunked::kPipe;
   if (nC <= kGlaDirectMaxChunks) return chunked::kDirect;
   return nC <= chunked::kDirectMaxChunks && B * H * nC <= kGlaDirectMaxWorkgroups ? chunked::kDirect : chunked::kPipe;
@@ -52,7 +53,7 @@ int gla2_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass) {
 
 size_t gla2_ws_bytes(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass) {
   const int mode = gla2_mode(B, H, nC, Dh, pass);
-  if (mode == chunked::kDirect || mode == chunked::kWhole) return 0;
+  if (mode == chunked::kDirect || mode == chunked::kWhole || mode == chunked::kRes) return 0;
   int64_t f = align64(B * H * nC);
   if (pass == 1) f += align64(B * H * nC * Dh * Dh);
   return (size_t)f * sizeof(float);
@@ -61,13 +62,14 @@ size_t gla2_ws_bytes(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass) {
 void gla2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass) {
   float* f = static_cast<float*>(ws);
   a.ws = a.tot = a.agg = nullptr;
-  if (a.mode == chunked::kDirect || a.mode == chunked::kWhole) return;
+  if (a.mode == chunked::kDirect || a.mode == chunked::kWhole || a.mode == chunked::kRes) return;
   a.tot = f;
   f += align64(B * a.H * a.nC);
   a.agg = pass == 1 ? f : nullptr;
 }
 
 int gla2_fwd(const ChunkArgs& p, int64_t B, hipStream_t s) {
+  if (p.mode == chunked::kRes) return res_fwd(p, B, s, true);
   switch (p.DH) {
     case 32: return launch_gla_fwd<32>(p, B, s);
     case 64: return launch_gla_fwd<64>(p, B, s);

@@ -133,11 +133,20 @@ __device__ __forceinline__ void decay_block32(const float* cd_or_g, float a, int
   const int s = lane & 31;
   if constexpr (GLA) {
     const int half = lane >> 5;
+    // All 32 gates are read (and pinned) before the chain: a read that the
+    // chain's selects need in only some lanes was otherwise moved into a
+    // divergent branch per step, serialising 32 LDS round trips.
+    float gv[Q];
+#pragma unroll
+    for (int t = 0; t < Q; ++t) gv[t] = cd_or_g[t];
+#pragma unroll
+    for (int t = 0; t < Q; ++t) pin(gv[t]);
     float run = 0.f;
 #pragma unroll
     for (int t = 0; t < Q; ++t) {
-      const float g = cd_or_g[t];   // read in every lane (no branch around it)
-      run = t < s ? 0.f : (t == s ? 1.f : run * g);
+      const float prod = run * gv[t];
+      const float diag = t == s ? 1.f : prod;
+      run = t < s ? 0.f : diag;
       if (((t >> 2) & 1) == half) m[4 * (t >> 3) + (t & 3)] = run;
     }
   } else {
@@ -170,7 +179,9 @@ __device__ __forceinline__ int state_off(int d, int n) {
 //           instantiation); the forward runs the direct kernel.
 // Both read up to nC - 1 chunks of inputs per workgroup (quadratic in nC), so
 // they serve short heads; longer heads run kPipe.
-enum Mode { kWhole = 0, kPipe = 1, kDirect = 2, kSum = 3 };
+//   kRes    forward only: every chunk of a head resident in one workgroup
+//           per 16-column slice of d (resident.hip), nC <= 16.
+enum Mode { kWhole = 0, kPipe = 1, kDirect = 2, kSum = 3, kRes = 4 };
 
 // Per-chunk kernels run on a 1-D grid of chunk_grid(p) workgroups.  The GPU
 // hands workgroups to its 8 XCDs round-robin by linear index; the decode

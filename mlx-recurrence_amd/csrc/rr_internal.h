@@ -34,7 +34,7 @@ struct ChunkArgs {
   float* agg;              // pipelined backward: chunk aggregates, then adjoints [B,H,nC,Dh,N]
   int B, L, H, DH, NS, nC;
   int R;                   // chunks per workgroup: nC (whole-head mode) or 1
-  int mode;                // 0 whole head, 1 pipelined, 2 direct (rr_chunked.h)
+  int mode;                // rr::chunked::Mode (rr_chunked.h)
 };
 
 // Mode of the SSD chunked kernels for pass 0 (forward) or 1 (backward), B*H
@@ -75,6 +75,12 @@ size_t gla2_ws_bytes(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass);
 void gla2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass);
 int gla2_fwd(const ChunkArgs& p, int64_t B, hipStream_t s);
 int gla2_bwd(const ChunkArgs& p, int64_t B, hipStream_t s);
+
+// Forward with every chunk of a head resident in one workgroup per 16-column
+// slice of the state's d axis (resident.hip): nC <= 16, Dh % 16 == 0,
+// N in {16, 32, 64} (GLA: N = Dh in {32, 64}), 16 nC >= N.
+bool res_fwd_supported(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N);
+int res_fwd(const ChunkArgs& p, int64_t B, hipStream_t s, bool gla);
 
 // Backward of the chunked kernels with column-owned state blocks (GLA: Dh in
 // {32, 64}; SSD: Dh in {32, 64}, N in {64, 128}; chunked_bwd.hip).  SSD

@@ -36,6 +36,7 @@ using rr::chunked::kDirect;
 using rr::chunked::kPipe;
 using rr::chunked::kSum;
 using rr::chunked::kWhole;
+using rr::chunked::kRes;
 
 }  // namespace
 
@@ -50,6 +51,7 @@ bool ssd2_supported(int dtype, int64_t L, int64_t seg, int64_t Dh, int64_t N, in
 }
 
 int ssd2_fwd(const ChunkArgs& p, int64_t B, hipStream_t s) {
+  if (p.mode == kRes) return res_fwd(p, B, s, false);
   switch (p.DH * 1000 + p.NS) {
     case 32016: return chunked::launch_fwd<32, 16, false>(p, B, s);
     case 32032: return chunked::launch_fwd<32, 32, false>(p, B, s);
@@ -843,6 +845,9 @@ int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N, int pa
   // B96 L512 H12 Dh64 N16 137 / 414 vs 194 / 357 (sum mode); B8 L4096 H80
   // Dh64 N128 2308 / 7457 vs 4025 / 4873 (pipelined)).
   if (B * H >= 512 && pass == 0) return chunked::kWhole;
+  // Short heads: the forward holds all chunks of a head in one workgroup per
+  // 16-column slice of d (no re-reads, no cross-workgroup carry)
+  if (pass == 0 && res_fwd_supported(B, H, nC, Dh, N)) return chunked::kRes;
   // Short heads, few of them: every chunk's workgroup sums over the other
   // chunks' inputs itself (a single kernel per pass; the sums' reads grow as
   // nC^2 per head, so not once the workgroups fill the GPU several times
