@@ -178,7 +178,7 @@ def make_ssd(cfg, device, dtype):
         import mlx_recurrence_amd as mr
         xs = [d[k].detach().requires_grad_(True) for k in ("u", "delta", "Bm", "Cm")]
         A_ = d["A"].detach().requires_grad_(True)
-        y = mr.ssd_scan(*xs, A_ if dense else A_[:, None].expand(H, N), seg=seg)
+        y = mr.ssd_scan(*xs, A_, seg=seg)   # [H, N] dense, or the per-head rates [H]
         y.backward(d["dy"])
 
     # CPU leg: the reference's per-step loop (ssd_scan_reference, fp32 torch on

@@ -1,11 +1,12 @@
-"""Build librecurrence_gfx950.so from csrc/*.hip with hipcc (AOT, gfx950 only).
+"""Build librecurrence_gfx950.so from csrc/*.hip with hipcc (AOT, gfx950 only),
+then the C++ autograd bindings (csrc_torch/autograd.cpp -> the Python module
+mlx_recurrence_amd._autograd, linked against that library).
 
 Usage:  python mlx-recurrence_amd/build.py [--jobs N] [--verbose]
 
-Objects go to mlx-recurrence_amd/_build/; the shared library is written next
-to the Python package (mlx_recurrence_amd/librecurrence_gfx950.so), where the
-ctypes loader looks for it.  Every call recompiles (the build check must see
-the current sources).
+Objects go to mlx-recurrence_amd/_build/; the shared libraries are written next
+to the Python package (mlx_recurrence_amd/), where the loaders look for them.
+Every call recompiles (the build check must see the current sources).
 """
 from __future__ import annotations
 
@@ -22,6 +23,7 @@ CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 PKG = HERE / "mlx_recurrence_amd"
 LIB_NAME = "librecurrence_gfx950.so"
+EXT_SRC = HERE / "csrc_torch" / "autograd.cpp"
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -73,6 +75,38 @@ def build(jobs: int | None = None, verbose: bool = False) -> pathlib.Path:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"linking {LIB_NAME} failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, out)
+    build_autograd(verbose)
+    return out
+
+
+def build_autograd(verbose: bool = False) -> pathlib.Path:
+    """The torch C++ extension mlx_recurrence_amd._autograd (host code only,
+    g++ against the installed torch; links librecurrence_gfx950.so by rpath)."""
+    import sysconfig
+
+    import torch
+
+    tdir = pathlib.Path(torch.__file__).resolve().parent
+    suffix = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
+    out = PKG / ("_autograd" + suffix)
+    tmp = PKG / ("_autograd" + suffix + ".tmp")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [
+        os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-w",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DTORCH_API_INCLUDE_EXTENSION_H", "-DTORCH_EXTENSION_NAME=_autograd",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        "-isystem", str(tdir / "include"), "-isystem", str(tdir / "include" / "torch" / "csrc" / "api" / "include"),
+        "-isystem", "/opt/rocm/include", "-isystem", sysconfig.get_paths()["include"],
+        str(EXT_SRC), "-o", str(tmp),
+        "-L", str(tdir / "lib"), "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python",
+        "-L", str(PKG), "-l:" + LIB_NAME, "-Wl,-rpath,$ORIGIN",
+    ]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"building the autograd bindings failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, out)
     return out
 

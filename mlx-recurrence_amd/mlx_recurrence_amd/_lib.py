@@ -95,6 +95,27 @@ def abi_version() -> int:
     return load().rr_abi_version()
 
 
+_AUTOGRAD_UNSET = object()
+_autograd_mod = _AUTOGRAD_UNSET
+
+
+def autograd_ext():
+    """The C++ autograd bindings (module mlx_recurrence_amd._autograd, built by
+    build.py next to the library), or None where they are not built.  Both
+    bindings call the same kernels through the same C ABI."""
+    global _autograd_mod
+    if _autograd_mod is _AUTOGRAD_UNSET:
+        load()   # the library first: the extension links this same file
+        try:
+            from . import _autograd as mod
+        except ImportError:
+            mod = None
+        if mod is not None and mod.abi_version() != load().rr_abi_version():
+            mod = None   # built against another revision of the library
+        _autograd_mod = mod
+    return _autograd_mod
+
+
 def chunk_len(L: int, seg: int) -> int:
     return chunk_len_cached(int(L), int(seg))
 

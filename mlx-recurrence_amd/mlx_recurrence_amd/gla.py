@@ -77,6 +77,9 @@ def _run(q, k, v, gates, seg, initial_state):
         raise ValueError(
             f"initial_state must be [B, H, Dh, Dh] = [{B}, {H}, {Dh}, {Dh}], got {tuple(initial_state.shape)}"
         )
+    ext = _lib.autograd_ext()
+    if ext is not None:   # the same forward / backward as one C++ autograd node
+        return ext.gla_scan(q, k, v, gates, initial_state, seg)
     return _GLAScan.apply(q, k, v, gates, initial_state, seg)
 
 

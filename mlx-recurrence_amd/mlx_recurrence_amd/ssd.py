@@ -12,9 +12,10 @@ Public API (reference ssd.py:344-394):
     ssd_scan_with_state(u, delta, B, C, A_neg, seg=32)   -> (y, final_state [B, H, Dh, N])
     ssd_scan_reference(u, delta, B, C, A_neg)            -> y (per-step torch loop)
 
-``A_neg`` is [H, N] as in the reference (ssd.py:62); a per-head A of shape [H]
-is passed as ``A[:, None].expand(H, N)`` and its gradient then sums over n
-through autograd.  Beyond the reference: keyword-only ``initial_state``
+``A_neg`` is [H, N] as in the reference (ssd.py:62); a per-head A (Mamba-2)
+is passed either as ``A[:, None].expand(H, N)`` (its gradient then sums over n
+through autograd) or, beyond the reference, as the [H] vector itself (the
+gradient is then [H]).  Beyond the reference: keyword-only ``initial_state``
 [B, H, Dh, N] and the gradient of a loss that uses ``final_state`` (the
 reference VJP reads only the cotangent of y, ssd.py:334).
 """
@@ -30,9 +31,9 @@ def _validate(u, delta, B, C, A_neg):
     if u.ndim != 4:
         raise ValueError(f"u must be [B, L, H, Dh], got shape {tuple(u.shape)}")
     Bsz, L, H, Dh = u.shape
-    if A_neg.ndim != 2 or A_neg.shape[0] != H:
-        raise ValueError(f"A_neg must be [H, N] with H={H}, got {tuple(A_neg.shape)}")
-    N = A_neg.shape[1]
+    if A_neg.ndim not in (1, 2) or A_neg.shape[0] != H:
+        raise ValueError(f"A_neg must be [H, N] (or [H], one rate per head) with H={H}, got {tuple(A_neg.shape)}")
+    N = A_neg.shape[1] if A_neg.ndim == 2 else B.shape[-1]
     if tuple(delta.shape) != (Bsz, L, H):
         raise ValueError(f"delta must be [B, L, H] = [{Bsz}, {L}, {H}], got {tuple(delta.shape)}")
     for name, t in (("B", B), ("C", C)):
@@ -47,7 +48,10 @@ def _decay_rates(A_neg):
     An ``A_neg`` that is one rate per head broadcast over N (stride 0 along N,
     e.g. ``A[:, None].expand(H, N)``) is passed as the [H] vector with flag 0,
     which selects the chunked MFMA kernels; any other [H, N] array is passed
-    dense with flag 1.  Both give the same results; the gradient is [H, N]."""
+    dense with flag 1.  Both give the same results; the gradient is [H, N].
+    A 1-D A_neg [H] is the per-head vector itself."""
+    if A_neg.ndim == 1:
+        return _lib.prep(A_neg, torch.float32), 0
     if A_neg.shape[1] > 1 and A_neg.stride(1) == 0:
         return _lib.prep(A_neg[:, 0], torch.float32), 0
     return _lib.prep(A_neg, torch.float32), 1
@@ -72,6 +76,7 @@ class _SSDScan(torch.autograd.Function):
         ctx.save_for_backward(u_, d_, B_, C_, A_, h0_, ckpt)
         ctx.seg = seg
         ctx.a_sn = a_sn
+        ctx.a_dim = A_neg.ndim
         ctx.set_materialize_grads(False)
         return y, ckpt[:, :, -1]
 
@@ -89,7 +94,7 @@ class _SSDScan(torch.autograd.Function):
         with _lib.device_guard(dev):
             ws = _lib.ssd_workspace(Bsz, L, H, Dh, N, ctx.seg, ctx.a_sn, u_.dtype, 1, dev)
             _lib.ssd_bwd(dy, dfinal, u_, d_, B_, C_, A_, ctx.a_sn, h0_, ckpt, ctx.seg, du, dd, dB, dC, dA, dh0, ws)
-        return du, dd, dB, dC, dA, dh0, None
+        return du, dd, dB, dC, dA.sum(1) if ctx.a_dim == 1 else dA, dh0, None
 
 
 def _run(u, delta, B, C, A_neg, seg, initial_state):
@@ -99,6 +104,9 @@ def _run(u, delta, B, C, A_neg, seg, initial_state):
         raise ValueError(
             f"initial_state must be [B, H, Dh, N] = [{Bsz}, {H}, {Dh}, {N}], got {tuple(initial_state.shape)}"
         )
+    ext = _lib.autograd_ext()
+    if ext is not None:   # the same forward / backward as one C++ autograd node
+        return ext.ssd_scan(u, delta, B, C, A_neg, initial_state, seg)
     return _SSDScan.apply(u, delta, B, C, A_neg, initial_state, seg)
 
 
@@ -110,7 +118,7 @@ def ssd_scan(u, delta, B, C, A_neg, seg=DEFAULT_SEG, *, initial_state=None):
         delta:  [B, L, H]       per-token, per-head step size
         B:      [B, L, H, N]    input projection
         C:      [B, L, H, N]    output projection
-        A_neg:  [H, N]          decay rates (negative)
+        A_neg:  [H, N]          decay rates (negative); [H] for one rate per head
         seg:    checkpoint segment length (L % seg == 0; default 32)
 
     Returns:
@@ -131,7 +139,9 @@ def ssd_scan_reference(u, delta, B, C, A_neg, *, initial_state=None):
     """Per-step torch loop, op for op as the reference's ssd_scan_reference
     (ssd.py:382-394).  Differentiable; runs on any device."""
     Bsz, L, H, Dh = u.shape
-    N = A_neg.shape[-1]
+    N = B.shape[-1]
+    if A_neg.ndim == 1:   # one rate per head
+        A_neg = A_neg[:, None].expand(H, N)
     ct = torch.float32
     for t in (u, delta, B, C, A_neg):
         ct = torch.promote_types(ct, t.dtype)

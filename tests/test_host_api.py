@@ -68,7 +68,9 @@ def test_invalid_shapes_raise_value_error():
         mr.rotlru_scan(a, a[:, :, :8], a, torch.rand(1, 64, 32))
     with pytest.raises(ValueError, match="A_neg must be"):
         u, d, B, C, _ = _ssd(1, 32, 2, 32, 8)
-        mr.ssd_scan(u, d, B, C, -torch.rand(2))
+        mr.ssd_scan(u, d, B, C, -torch.rand(3))        # H = 2
+    with pytest.raises(ValueError, match="A_neg must be"):
+        mr.ssd_scan(u, d, B, C, -torch.rand(2, 8, 1))
 
 
 def test_cpu_tensors_are_refused():
@@ -88,3 +90,19 @@ def test_parity_check_reference_vs_itself():
     ok, rep = mr.parity_check(mr.rglru_scan_reference, mr.rglru_scan_reference, (a, x),
                               ["a", "x"], (0, 1), verbose=False)
     assert ok and rep["y"]["abs"] == 0.0 and rep["grad_a"]["rel"] == 0.0
+
+
+def test_ssd_reference_takes_per_head_rates():
+    """A 1-D A_neg [H] is one rate per head: the reference loop gives the same
+    y as with A[:, None].expand(H, N), and its gradient is the per-head sum."""
+    u, d, B, C, _ = _ssd(2, 16, 3, 32, 8)
+    A = -torch.rand(3, dtype=torch.float64) - 0.1
+    A1 = A.clone().requires_grad_(True)
+    A2 = A.clone().requires_grad_(True)
+    y1 = mr.ssd_scan_reference(u.double(), d.double(), B.double(), C.double(), A1)
+    y2 = mr.ssd_scan_reference(u.double(), d.double(), B.double(), C.double(), A2[:, None].expand(3, 8))
+    assert torch.equal(y1, y2)
+    w = torch.randn_like(y1)
+    (y1 * w).sum().backward()
+    (y2 * w).sum().backward()
+    torch.testing.assert_close(A1.grad, A2.grad, rtol=1e-12, atol=1e-12)
