@@ -772,16 +772,19 @@ def measure(name, steps, warmup, dtype, device, cpu_seconds):
     dom = max(kernels, key=lambda r: r["us"])
     achieved = dom["pass_bytes"] / (dom["us"] * 1e-6) / 1e9  # GB/s
 
-    # eager autograd API
-    for _ in range(3):
+    # eager autograd API: median of 5 timed runs of ne steps each, after warm-up
+    for _ in range(10):
         w["eager"]()
     torch.cuda.synchronize()
-    e0 = time.perf_counter()
-    ne = max(5, min(steps, 50))
-    for _ in range(ne):
-        w["eager"]()
-    torch.cuda.synchronize()
-    eager_ms = (time.perf_counter() - e0) * 1e3 / ne
+    ne = max(10, min(steps, 50))
+    runs = []
+    for _ in range(5):
+        e0 = time.perf_counter()
+        for _ in range(ne):
+            w["eager"]()
+        torch.cuda.synchronize()
+        runs.append((time.perf_counter() - e0) * 1e3 / ne)
+    eager_ms = sorted(runs)[len(runs) // 2]
 
     # transient memory of one eager fwd+bwd: peak allocation beyond the inputs,
     # minus the outputs and gradients the call returns (y, grads)

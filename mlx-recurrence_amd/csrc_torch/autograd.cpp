@@ -79,8 +79,36 @@ void check(int rc, const char* what) {
   throw std::runtime_error(std::string(what) + " failed (code " + std::to_string(rc) + "): " + msg);
 }
 
-Tensor workspace(size_t n, const Tensor& like) {
-  return n ? at::empty({(int64_t)n}, like.options().dtype(at::kByte)) : Tensor();
+// The outputs and workspace of one pass carved out of a single allocation (one
+// caching-allocator call instead of one per buffer): tensors are strided
+// views of it, the workspace a byte offset.  Pieces start 256-byte aligned.
+class Arena {
+ public:
+  // reserve a piece of `bytes`; returns its byte offset
+  int64_t reserve(int64_t bytes) {
+    const int64_t off = total_;
+    total_ += (bytes + 255) / 256 * 256;
+    return off;
+  }
+  void allocate(const at::TensorOptions& opts, at::ScalarType dt) {
+    esize_ = (int64_t)c10::elementSize(dt);
+    buf_ = at::empty({(total_ + esize_ - 1) / esize_}, opts.dtype(dt));
+  }
+  // a contiguous tensor of the arena's dtype at byte offset `off`
+  Tensor view(int64_t off, at::IntArrayRef sizes) const {
+    return buf_.as_strided(sizes, c10::contiguous_strides(sizes), off / esize_);
+  }
+  void* ptr(int64_t off) const { return static_cast<char*>(buf_.data_ptr()) + off; }
+
+ private:
+  int64_t total_ = 0, esize_ = 1;
+  Tensor buf_;
+};
+
+int64_t numel(at::IntArrayRef sizes) {
+  int64_t n = 1;
+  for (int64_t v : sizes) n *= v;
+  return n;
 }
 
 // ------------------------------------------------------------------ SSD
@@ -109,13 +137,14 @@ struct SSDFn : public torch::autograd::Function<SSDFn> {
     }
     const Tensor h0_ = h0.defined() ? prep(h0, at::kFloat) : Tensor();
     const int64_t nC = L / rr_chunk_len(L, seg);
-    const auto f32 = u_.options().dtype(at::kFloat);
-    Tensor y = at::empty({Bsz, L, H, Dh}, f32);
-    Tensor ckpt = at::empty({Bsz, H, nC, Dh, N}, f32);
     const size_t wsb = rr_ssd_workspace_bytes(Bsz, L, H, Dh, N, seg, a_sn, dtype_code(dt), 0);
-    Tensor ws = workspace(wsb, u_);
+    Arena ar;
+    const int64_t oy = ar.reserve(Bsz * L * H * Dh * 4), ock = ar.reserve(Bsz * H * nC * Dh * N * 4);
+    const int64_t ows = ar.reserve((int64_t)wsb);
+    ar.allocate(u_.options(), at::kFloat);
+    Tensor y = ar.view(oy, {Bsz, L, H, Dh}), ckpt = ar.view(ock, {Bsz, H, nC, Dh, N});
     check(rr_ssd_fwd(P(u_), P(d_), P(B_), P(C_), PF(A_), a_sn, dtype_code(dt), Bsz, L, H, Dh, N, seg, PF(h0_),
-                     MF(y), MF(ckpt), P(ws), wsb, stream_of(u_)),
+                     MF(y), MF(ckpt), wsb ? ar.ptr(ows) : nullptr, wsb, stream_of(u_)),
           "rr_ssd_fwd");
     ctx->save_for_backward({u_, d_, B_, C_, A_, h0_, ckpt});
     ctx->saved_data["seg"] = seg;
@@ -135,18 +164,31 @@ struct SSDFn : public torch::autograd::Function<SSDFn> {
     const auto f32 = u_.options().dtype(at::kFloat);
     const Tensor dy = grads[0].defined() ? prep(grads[0], at::kFloat) : at::zeros({Bsz, L, H, Dh}, f32);
     const Tensor dfinal = grads[1].defined() ? prep(grads[1], at::kFloat) : Tensor();
-    Tensor du = at::empty_like(u_), dd = at::empty_like(d_), dB = at::empty_like(B_), dC = at::empty_like(C_);
-    Tensor dA = at::empty({H, N}, f32);
     // (autograd edges exist only for the tensors passed: h0, when given, is the sixth)
     const bool want_dh0 = ctx->saved_data["has_h0"].toBool() && ctx->needs_input_grad(5);
     Tensor dh0 = want_dh0 ? at::empty({Bsz, H, Dh, N}, f32) : Tensor();
-    const int dtc = dtype_code(u_.scalar_type());
+    const at::ScalarType dt = u_.scalar_type();
+    const int64_t es = (int64_t)c10::elementSize(dt);
+    const int dtc = dtype_code(dt);
     const size_t wsb = rr_ssd_workspace_bytes(Bsz, L, H, Dh, N, seg, a_sn, dtc, 1);
-    Tensor ws = workspace(wsb, u_);
+    const bool heads = ctx->saved_data["a_dim"].toInt() == 1;   // A_neg [H]: its gradient sums dA over n
+    Arena ar;   // du, ddelta, dB, dC in the inputs' dtype; dA (fp32, [H] case) and the workspace as bytes
+    const int64_t odu = ar.reserve(u_.numel() * es), odd = ar.reserve(d_.numel() * es);
+    const int64_t odB = ar.reserve(B_.numel() * es), odC = ar.reserve(C_.numel() * es);
+    const int64_t odA = heads ? ar.reserve(H * N * 4) : 0, ows = ar.reserve((int64_t)wsb);
+    ar.allocate(u_.options(), dt);
+    Tensor du = ar.view(odu, u_.sizes()), dd = ar.view(odd, d_.sizes());
+    Tensor dB = ar.view(odB, B_.sizes()), dC = ar.view(odC, C_.sizes());
+    Tensor dA_full = heads ? Tensor() : at::empty({H, N}, f32);
+    float* dA = heads ? static_cast<float*>(ar.ptr(odA)) : MF(dA_full);
     check(rr_ssd_bwd(PF(dy), PF(dfinal), P(u_), P(d_), P(B_), P(C_), PF(A_), a_sn, dtc, Bsz, L, H, Dh, N, seg,
-                     PF(h0_), PF(ckpt), P(du), P(dd), P(dB), P(dC), MF(dA), MF(dh0), P(ws), wsb, stream_of(u_)),
+                     PF(h0_), PF(ckpt), P(du), P(dd), P(dB), P(dC), dA, MF(dh0), wsb ? ar.ptr(ows) : nullptr, wsb,
+                     stream_of(u_)),
           "rr_ssd_bwd");
-    Tensor dA_out = ctx->saved_data["a_dim"].toInt() == 1 ? dA.sum(1) : dA;
+    // [H] case: the sum over n reads the arena's piece through a non-owning
+    // tensor; the arena outlives the enqueue, and a block freed to the caching
+    // allocator is reused only by work ordered after it on this stream
+    Tensor dA_out = heads ? at::from_blob(dA, {H, N}, f32).sum(1) : dA_full;
     return {du, dd, dB, dC, dA_out, dh0, Tensor()};
   }
 };
@@ -169,13 +211,14 @@ struct GLAFn : public torch::autograd::Function<GLAFn> {
     const int64_t B = q_.size(0), L = q_.size(1), H = q_.size(2), Dh = q_.size(3);
     const Tensor h0_ = h0.defined() ? prep(h0, at::kFloat) : Tensor();
     const int64_t nC = L / rr_chunk_len(L, seg);
-    const auto f32 = q_.options().dtype(at::kFloat);
-    Tensor y = at::empty({B, L, H, Dh}, f32);
-    Tensor ckpt = at::empty({B, H, nC, Dh, Dh}, f32);
     const size_t wsb = rr_gla_workspace_bytes(B, L, H, Dh, seg, dtype_code(dt), 0);
-    Tensor ws = workspace(wsb, q_);
-    check(rr_gla_fwd(P(q_), P(k_), P(v_), P(g_), dtype_code(dt), B, L, H, Dh, seg, PF(h0_), MF(y), MF(ckpt), P(ws),
-                     wsb, stream_of(q_)),
+    Arena ar;
+    const int64_t oy = ar.reserve(B * L * H * Dh * 4), ock = ar.reserve(B * H * nC * Dh * Dh * 4);
+    const int64_t ows = ar.reserve((int64_t)wsb);
+    ar.allocate(q_.options(), at::kFloat);
+    Tensor y = ar.view(oy, {B, L, H, Dh}), ckpt = ar.view(ock, {B, H, nC, Dh, Dh});
+    check(rr_gla_fwd(P(q_), P(k_), P(v_), P(g_), dtype_code(dt), B, L, H, Dh, seg, PF(h0_), MF(y), MF(ckpt),
+                     wsb ? ar.ptr(ows) : nullptr, wsb, stream_of(q_)),
           "rr_gla_fwd");
     ctx->save_for_backward({q_, k_, v_, g_, h0_, ckpt});
     ctx->saved_data["seg"] = seg;
@@ -194,15 +237,22 @@ struct GLAFn : public torch::autograd::Function<GLAFn> {
     const auto f32 = q_.options().dtype(at::kFloat);
     const Tensor dy = grads[0].defined() ? prep(grads[0], at::kFloat) : at::zeros({B, L, H, Dh}, f32);
     const Tensor dfinal = grads[1].defined() ? prep(grads[1], at::kFloat) : Tensor();
-    Tensor dq = at::empty_like(q_), dk = at::empty_like(k_), dv = at::empty_like(v_), dg = at::empty_like(g_);
     // (autograd edges exist only for the tensors passed: h0, when given, is the fifth)
     const bool want_dh0 = ctx->saved_data["has_h0"].toBool() && ctx->needs_input_grad(4);
     Tensor dh0 = want_dh0 ? at::empty({B, H, Dh, Dh}, f32) : Tensor();
-    const int dtc = dtype_code(q_.scalar_type());
+    const at::ScalarType dt = q_.scalar_type();
+    const int64_t es = (int64_t)c10::elementSize(dt);
+    const int dtc = dtype_code(dt);
     const size_t wsb = rr_gla_workspace_bytes(B, L, H, Dh, seg, dtc, 1);
-    Tensor ws = workspace(wsb, q_);
+    Arena ar;   // dq, dk, dv, dgates in the inputs' dtype; the workspace as bytes
+    const int64_t n4 = q_.numel() * es;
+    const int64_t odq = ar.reserve(n4), odk = ar.reserve(n4), odv = ar.reserve(n4), odg = ar.reserve(g_.numel() * es);
+    const int64_t ows = ar.reserve((int64_t)wsb);
+    ar.allocate(q_.options(), dt);
+    Tensor dq = ar.view(odq, q_.sizes()), dk = ar.view(odk, k_.sizes()), dv = ar.view(odv, v_.sizes());
+    Tensor dg = ar.view(odg, g_.sizes());
     check(rr_gla_bwd(PF(dy), PF(dfinal), P(q_), P(k_), P(v_), P(g_), dtc, B, L, H, Dh, seg, PF(h0_), PF(ckpt), P(dq),
-                     P(dk), P(dv), P(dg), MF(dh0), P(ws), wsb, stream_of(q_)),
+                     P(dk), P(dv), P(dg), MF(dh0), wsb ? ar.ptr(ows) : nullptr, wsb, stream_of(q_)),
           "rr_gla_bwd");
     return {dq, dk, dv, dg, dh0, Tensor()};
   }
