@@ -514,6 +514,7 @@ def make_gdn(cfg, device, dtype):
         dv=torch.empty((B, L, H, Dh), dtype=dtype, device=device),
         da=torch.empty((B, L, H), dtype=dtype, device=device),
         db=torch.empty((B, L, H), dtype=dtype, device=device),
+        wsb=_lib.gdn_workspace(B, L, H, Dh, seg, dtype, device),
     )
     es = torch.tensor([], dtype=dtype).element_size()
     n_x, n_g, n_ck = B * L * H * Dh, B * L * H, B * H * nC * Dh * Dh
@@ -526,7 +527,7 @@ def make_gdn(cfg, device, dtype):
 
     def bwd():
         _lib.gdn_bwd(d["dy"], None, d["q"], d["k"], d["v"], d["alpha"], d["beta"], None, out["ckpt"], seg,
-                     out["dq"], out["dk"], out["dv"], out["da"], out["db"], None)
+                     out["dq"], out["dk"], out["dv"], out["da"], out["db"], None, out["wsb"])
 
     def eager():
         import mlx_recurrence_amd as mr
@@ -577,7 +578,7 @@ WORKLOADS = {
                 dict(B=96, L=512, H=12, Dh=64, N=16, seg=32)),
     "gla_b96": ("gla_scan fwd+bwd (BASELINE config 2 shape, B = 96)", make_gla,
                 dict(B=96, L=512, H=12, Dh=64, seg=32)),
-    "gdn": ("gated_deltanet_scan fwd+bwd, sequential kernels (BASELINE config 2 shape)", make_gdn,
+    "gdn": ("gated_deltanet_scan fwd+bwd, sequential form (BASELINE config 2 shape)", make_gdn,
             dict(B=3, L=512, H=12, Dh=64, seg=32)),
 }
 

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define RR_ABI_VERSION 9
+#define RR_ABI_VERSION 10
 
 enum rr_dtype { RR_F32 = 0, RR_BF16 = 1, RR_F16 = 2 };
 
@@ -280,19 +280,24 @@ int rr_rotlru_step(const void* a, const void* cs, const void* sn, const void* x,
 
 /* ------------------------------------------------------ Gated DeltaNet --
  * The reference's designed next plug-in (docs/DESIGN_gated_deltanet.md; not
- * code in the reference): the sequential kernel of its Phase 2 (:270-440,
+ * code in the reference): the sequential kernels of its Phase 2 (:270-440,
  * :528-536), as a C entry pair instead of a Metal launcher.  Per (b, h):
  *   S_t = alpha_t (S_{t-1} - beta_t k_t (k_t^T S_{t-1})) + beta_t k_t v_t^T,
  *   y_t[j] = sum_i q_t[i] S_t[i,j]                           (:56-90)
  * q, k, v [B,L,H,Dh] and alpha, beta [B,L,H] (dtype; q and k L2-normalised,
- * alpha and beta pre-activated by the caller, :461-464); h0 [B,H,Dh(i),Dh(j)]
- * (nullable); y [B,L,H,Dh] fp32; ckpt [B,H,L/T,Dh,Dh] fp32, the state after
- * every T = rr_chunk_len(L, seg) steps (the last is the final state).
- * Dh 32 or 64; T 8, 16 or 32 (seg a multiple of 8).  No workspace.
+ * alpha and beta pre-activated by the caller, :461-464; q and k 16-byte
+ * aligned); h0 [B,H,Dh(i),Dh(j)] (nullable); y [B,L,H,Dh] fp32;
+ * ckpt [B,H,L/T,Dh,Dh] fp32, the state after every T = rr_chunk_len(L, seg)
+ * steps (the last is the final state).  Dh 32 or 64; T 8, 16 or 32 (seg a
+ * multiple of 8).
  */
 int rr_gdn_fwd(const void* q, const void* k, const void* v, const void* alpha, const void* beta, int dtype,
                int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t seg, const float* h0, float* y, float* ckpt,
                void* stream);
+
+/* Workspace bytes of rr_gdn_bwd (the adjoint at every checkpoint,
+ * [B,H,L/T,Dh,Dh] fp32); 0 for invalid arguments. */
+size_t rr_gdn_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t seg, int dtype);
 
 /* Backward (:334-440): dy [B,L,H,Dh] fp32, dfinal [B,H,Dh,Dh] fp32 (nullable);
  * ckpt from rr_gdn_fwd on the same inputs; writes dq, dk, dv [B,L,H,Dh] and
@@ -301,7 +306,7 @@ int rr_gdn_fwd(const void* q, const void* k, const void* v, const void* alpha, c
 int rr_gdn_bwd(const float* dy, const float* dfinal, const void* q, const void* k, const void* v,
                const void* alpha, const void* beta, int dtype, int64_t B, int64_t L, int64_t H, int64_t Dh,
                int64_t seg, const float* h0, const float* ckpt, void* dq, void* dk, void* dv, void* dalpha,
-               void* dbeta, float* dh0, void* stream);
+               void* dbeta, float* dh0, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

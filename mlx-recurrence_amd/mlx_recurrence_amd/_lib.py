@@ -64,7 +64,8 @@ _SIGS = {
     "rr_rglru_step": (_c_int, [_c_ptr] * 2 + [_c_int] + [_c_i64] * 2 + [_c_ptr] * 3),
     "rr_rotlru_step": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 2 + [_c_ptr] * 3),
     "rr_gdn_fwd": (_c_int, [_c_ptr] * 5 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 4),
-    "rr_gdn_bwd": (_c_int, [_c_ptr] * 7 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 9),
+    "rr_gdn_workspace_bytes": (_c_size, [_c_i64] * 5 + [_c_int]),
+    "rr_gdn_bwd": (_c_int, [_c_ptr] * 7 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 9 + [_c_size, _c_ptr]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGS)
@@ -416,8 +417,13 @@ def gdn_fwd(q, k, v, alpha, beta, h0, seg, y, ckpt):
                              ptr(h0), ptr(y), ptr(ckpt), stream_of(q)), "rr_gdn_fwd")
 
 
-def gdn_bwd(dy, dfinal, q, k, v, alpha, beta, h0, ckpt, seg, dq, dk, dv, dalpha, dbeta, dh0):
+def gdn_workspace(B, L, H, Dh, seg, dtype, device) -> torch.Tensor | None:
+    return _alloc_ws(_ws_bytes("rr_gdn_workspace_bytes", (B, L, H, Dh, seg, DTYPE_CODE[dtype])), device)
+
+
+def gdn_bwd(dy, dfinal, q, k, v, alpha, beta, h0, ckpt, seg, dq, dk, dv, dalpha, dbeta, dh0, ws):
     B, L, H, Dh = q.shape
     _check(load().rr_gdn_bwd(ptr(dy), ptr(dfinal), ptr(q), ptr(k), ptr(v), ptr(alpha), ptr(beta),
                              DTYPE_CODE[q.dtype], B, L, H, Dh, seg, ptr(h0), ptr(ckpt), ptr(dq), ptr(dk), ptr(dv),
-                             ptr(dalpha), ptr(dbeta), ptr(dh0), stream_of(q)), "rr_gdn_bwd")
+                             ptr(dalpha), ptr(dbeta), ptr(dh0), ptr(ws), 0 if ws is None else ws.numel(),
+                             stream_of(q)), "rr_gdn_bwd")

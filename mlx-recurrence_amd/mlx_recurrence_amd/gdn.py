@@ -70,7 +70,8 @@ class _GDNScan(torch.autograd.Function):
         dq, dk, dv, da, db = (torch.empty_like(t) for t in (q_, k_, v_, a_, b_))
         dh0 = torch.empty((B, H, Dh, Dh), dtype=torch.float32, device=dev) if ctx.needs_input_grad[5] else None
         with _lib.device_guard(dev):
-            _lib.gdn_bwd(dy, dfinal, q_, k_, v_, a_, b_, h0_, ckpt, ctx.seg, dq, dk, dv, da, db, dh0)
+            ws = _lib.gdn_workspace(B, L, H, Dh, ctx.seg, q_.dtype, dev)
+            _lib.gdn_bwd(dy, dfinal, q_, k_, v_, a_, b_, h0_, ckpt, ctx.seg, dq, dk, dv, da, db, dh0, ws)
         return dq, dk, dv, da, db, dh0, None
 
 

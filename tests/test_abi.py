@@ -33,7 +33,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.rr_abi_version() == 9
+    assert lib.rr_abi_version() == 10
 
 
 @pytest.mark.parametrize("L,seg,T", [(512, 32, 32), (96, 16, 16), (128, 64, 32), (96, 48, 16),
@@ -106,5 +106,13 @@ def test_gdn_validation(lib):
     assert rc == _lib.RR_EUNSUPPORTED and b"multiple of 8" in lib.rr_last_error()
     rc = lib.rr_gdn_fwd(p, p, p, p, None, 0, 1, 64, 2, 64, 32, None, p, p, None)
     assert rc == _lib.RR_EINVAL and b"null pointer" in lib.rr_last_error()
-    rc = lib.rr_gdn_bwd(p, None, p, p, p, p, p, 0, 1, 64, 2, 64, 32, None, p, p, p, None, p, p, None, None)
+    rc = lib.rr_gdn_bwd(p, None, p, p, p, p, p, 0, 1, 64, 2, 64, 32, None, p, p, p, None, p, p, None, p, 1 << 30,
+                        None)
     assert rc == _lib.RR_EINVAL and b"null pointer" in lib.rr_last_error()
+    need = lib.rr_gdn_workspace_bytes(1, 64, 2, 64, 32, 0)
+    assert need == 1 * 2 * 2 * 64 * 64 * 4
+    rc = lib.rr_gdn_bwd(p, None, p, p, p, p, p, 0, 1, 64, 2, 64, 32, None, p, p, p, p, p, p, None, p, need - 1, None)
+    assert rc == _lib.RR_EWORKSPACE
+    q_odd = ctypes.c_void_p(24)
+    rc = lib.rr_gdn_fwd(q_odd, p, p, p, p, 0, 1, 64, 2, 64, 32, None, p, p, None)
+    assert rc == _lib.RR_EINVAL and b"16-byte aligned" in lib.rr_last_error()
