@@ -21,12 +21,12 @@
 //   * only the gradients couple the columns (dq, dk are row sums over j;
 //     dalpha, dbeta sums over j).
 // Hence three kernels:
-//   1. forward: one single-wave workgroup per (head, 8 columns); lane l holds
-//      rows R (l % 8) .. R (l % 8) + R - 1 (R = Dh / 8) of column
-//      8 jb + l / 8, so a column dot over i is R in-lane products plus a sum
-//      over 8 adjacent lanes (three DPP steps, no LDS); the step inputs are
-//      staged through the wave's LDS 32 steps at a time, a block ahead; the
-//      state is checkpointed every T steps;
+//   1. forward: one single-wave workgroup per (head, CPW columns); a column's
+//      64 / CPW adjacent lanes hold R rows each, so a column dot over i is R
+//      in-lane products plus a sum over those lanes (DPP steps within a
+//      16-lane row, no LDS); the step inputs are staged through the wave's
+//      LDS 32 steps at a time, a block ahead; the state is checkpointed every
+//      T steps;
 //   2. the adjoint pass, with the same decomposition, walks the steps
 //      backwards from dL/dS_{L-1} and writes the adjoint entering every
 //      interval from its right (workspace [B,H,nC,Dh,Dh]) and dh0;
@@ -54,6 +54,15 @@ __device__ __forceinline__ float col_sum(float v) {
   v += rr::dpp_mov<0x4E>(v);    // quad_perm [2, 3, 0, 1]
   v += rr::dpp_mov<0x141>(v);   // row_half_mirror: quad 0 <-> quad 1 of each 8
   return v;
+}
+
+// Sum over the 16 lanes of a column (lanes 16 c .. 16 c + 15) for the
+// four-column waves of the column-split passes; same rounding in every lane.
+__device__ __forceinline__ float col_sum16(float v) { return rr::row16_sum(v); }
+template <int LPC>
+__device__ __forceinline__ float col_sum_n(float v) {
+  if constexpr (LPC == 16) return col_sum16(v);
+  else return col_sum(v);
 }
 
 // R consecutive elements (a row run of q or k) into fp32.
@@ -110,9 +119,9 @@ __device__ __forceinline__ float dot(const float (&x)[R], const float (&y)[R]) {
 }
 
 // One step of the recurrence on this lane's R entries of column j; returns p.
-template <int R>
+template <int R, int LPC = 8>
 __device__ __forceinline__ float step(float (&S)[R], const StepIn<R>& in) {
-  const float p = col_sum(dot<R>(in.k, S));              // p_j = k^T S_{t-1} (reference :75-84)
+  const float p = col_sum_n<LPC>(dot<R>(in.k, S));       // p_j = k^T S_{t-1} (reference :75-84)
   // S <- alpha (S - beta k p) + beta k v = alpha S + k (beta v - alpha beta p)
   const float cc = in.b * in.x - in.a * (in.b * p);
 #pragma unroll
@@ -122,12 +131,12 @@ __device__ __forceinline__ float step(float (&S)[R], const StepIn<R>& in) {
 
 // One step of the adjoint recursion on this lane's R entries of column j
 // (dS += q go^T; d = k^T dS; dS <- alpha (dS - beta k d^T)); returns d.
-template <int R>
+template <int R, int LPC = 8>
 __device__ __forceinline__ float adjoint_step(float (&adj)[R], const float (&q)[R], const float (&k)[R], float go,
                                               float a, float b) {
 #pragma unroll
   for (int r = 0; r < R; ++r) adj[r] += q[r] * go;
-  const float d = col_sum(dot<R>(k, adj));
+  const float d = col_sum_n<LPC>(dot<R>(k, adj));
   const float abd = a * (b * d);
 #pragma unroll
   for (int r = 0; r < R; ++r) adj[r] = a * adj[r] - k[r] * abd;   // alpha (dS - beta k d^T)
@@ -135,18 +144,20 @@ __device__ __forceinline__ float adjoint_step(float (&adj)[R], const float (&q)[
 }
 
 // The forward and adjoint passes run one single-wave workgroup per (head,
-// 8-column block): B H Dh/8 waves spread over the GPU, since a step's work
-// is issue-bound (a few dozen VALU instructions per lane) and a lone wave
-// issues every cycle it can.  The wave's step inputs are staged through
-// LDS kTS steps at a time, double-buffered: the next block's loads are issued
-// into registers a whole block ahead and written to LDS at the block's end.
-// The column blocks of one head share an XCD (their inputs stay in one L2).
+// CPW-column block): B H Dh/CPW waves spread over the GPU.  A step is a chain
+// of dependent instructions per lane, so the split that gives each lane the
+// fewest (R = Dh CPW / 64 rows of one column, the column's 64 / CPW lanes
+// adjacent, CPW = 4 for Dh = 64) runs fastest.  The wave's step inputs are
+// staged through LDS kTS steps at a time, double-buffered: the next block's
+// loads are issued into registers a whole block ahead and written to LDS at
+// the block's end.  The column blocks of one head share an XCD (their inputs
+// stay in one L2).
 constexpr int kTS = 32;
 
-template <int DH>
+template <int DH, int CPW>
 struct StageSmem {
   float k[2][kTS][DH], q[2][kTS][DH];
-  float x[2][kTS][8];   // v or dy of this wave's 8 columns
+  float x[2][kTS][CPW];   // v or dy of this wave's columns
   float a[2][kTS], b[2][kTS];
 };
 
@@ -161,29 +172,28 @@ __device__ __forceinline__ ColId col_id(int NJ, int BH) {
 }
 inline unsigned col_grid(int64_t BH, int NJ) { return (unsigned)((BH + 7) / 8 * 8 * NJ); }
 
-// Raw 8-element chunk (16 bytes of 16-bit inputs, 32 bytes of fp32).
-template <typename E>
-__device__ __forceinline__ void ld8(const E* p, uint4 (&r)[2]) {
-  const uint4* v = reinterpret_cast<const uint4*>(p);
-  r[0] = v[0];
-  if constexpr (sizeof(E) == 4) r[1] = v[1];
+// A raw run of N elements (N = 4 or 8: 8 to 32 bytes), then widened into LDS.
+template <typename E, int N>
+__device__ __forceinline__ void ldn(const E* p, uint4 (&r)[2]) {
+  constexpr int BYTES = N * (int)sizeof(E), AL = BYTES >= 16 ? 16 : BYTES;
+  __builtin_memcpy(r, __builtin_assume_aligned(p, AL), BYTES);
 }
-template <typename E>
-__device__ __forceinline__ void st8(float* dst, const uint4 (&r)[2]) {
-  E tmp[8];
-  __builtin_memcpy(tmp, r, 8 * sizeof(E));
-  float o[8];
+template <typename E, int N>
+__device__ __forceinline__ void stn(float* dst, const uint4 (&r)[2]) {
+  E tmp[N];
+  __builtin_memcpy(tmp, r, N * sizeof(E));
 #pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = rr::to_f32(tmp[e]);
-  reinterpret_cast<float4*>(dst)[0] = make_float4(o[0], o[1], o[2], o[3]);
-  reinterpret_cast<float4*>(dst)[1] = make_float4(o[4], o[5], o[6], o[7]);
+  for (int e = 0; e < N; e += 4)
+    reinterpret_cast<float4*>(dst)[e / 4] =
+        make_float4(rr::to_f32(tmp[e]), rr::to_f32(tmp[e + 1]), rr::to_f32(tmp[e + 2]), rr::to_f32(tmp[e + 3]));
 }
 
 // One block's loads held by the wave's lanes: the k and q rows (kTS DH / 8
-// chunks each), the 8 columns of x per step (kTS chunks) and the step scalars.
-template <typename InT, typename XT, int DH>
+// runs of 8 each), the wave's CPW columns of x per step (kTS runs) and the
+// step scalars.
+template <typename InT, typename XT, int DH, int CPW>
 struct Stager {
-  static constexpr int CPA = kTS * DH / 8;                 // chunks per k / q block
+  static constexpr int CPA = kTS * DH / 8;                 // runs per k / q block
   static constexpr int NCH = 2 * CPA + kTS;
   static constexpr int PER = (NCH + 63) / 64;
   uint4 raw[PER][2];
@@ -195,34 +205,34 @@ struct Stager {
       const int id = lane + 64 * i;
       if (id < 2 * CPA) {
         const int rem = id % CPA, st = rem / (DH / 8), ch = rem % (DH / 8), t = blk * kTS + st;
-        if (t < L) ld8<InT>((id < CPA ? k : q) + (row0 + (int64_t)t * H) * DH + 8 * ch, raw[i]);
+        if (t < L) ldn<InT, 8>((id < CPA ? k : q) + (row0 + (int64_t)t * H) * DH + 8 * ch, raw[i]);
       } else if (id < NCH) {
         const int st = id - 2 * CPA, t = blk * kTS + st;
-        if (t < L) ld8<XT>(x + (row0 + (int64_t)t * H) * DH + j0, raw[i]);
+        if (t < L) ldn<XT, CPW>(x + (row0 + (int64_t)t * H) * DH + j0, raw[i]);
       }
     }
     sc = 0.f;
     const int t = blk * kTS + (lane % kTS);
     if (t < L) sc = rr::ld(lane < kTS ? alpha : beta, row0 + (int64_t)t * H);
   }
-  __device__ __forceinline__ void commit(StageSmem<DH>& sm, int buf, int blk, int L, int lane) const {
+  __device__ __forceinline__ void commit(StageSmem<DH, CPW>& sm, int buf, int blk, int L, int lane) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int id = lane + 64 * i;
       if (id < 2 * CPA) {
         const int rem = id % CPA, st = rem / (DH / 8), ch = rem % (DH / 8);
-        if (blk * kTS + st < L) st8<InT>(id < CPA ? &sm.k[buf][st][8 * ch] : &sm.q[buf][st][8 * ch], raw[i]);
+        if (blk * kTS + st < L) stn<InT, 8>(id < CPA ? &sm.k[buf][st][8 * ch] : &sm.q[buf][st][8 * ch], raw[i]);
       } else if (id < NCH) {
         const int st = id - 2 * CPA;
-        if (blk * kTS + st < L) st8<XT>(&sm.x[buf][st][0], raw[i]);
+        if (blk * kTS + st < L) stn<XT, CPW>(&sm.x[buf][st][0], raw[i]);
       }
     }
     (lane < kTS ? sm.a : sm.b)[buf][lane % kTS] = sc;
   }
 };
 
-template <int R, int DH>
-__device__ __forceinline__ StepIn<R> stage_step(const StageSmem<DH>& sm, int buf, int st, int i0, int c) {
+template <int R, int DH, int CPW>
+__device__ __forceinline__ StepIn<R> stage_step(const StageSmem<DH, CPW>& sm, int buf, int st, int i0, int c) {
   StepIn<R> in;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -235,48 +245,55 @@ __device__ __forceinline__ StepIn<R> stage_step(const StageSmem<DH>& sm, int buf
   return in;
 }
 
+template <int DH>
+constexpr int kCpw = DH == 64 ? 4 : 8;   // columns per wave of the column-split passes
+
 template <typename InT, int DH>
 __global__ __launch_bounds__(64) void gdn_fwd_kernel(const InT* __restrict__ q, const InT* __restrict__ k,
                                                      const InT* __restrict__ v, const InT* __restrict__ alpha,
                                                      const InT* __restrict__ beta, const float* __restrict__ h0,
                                                      float* __restrict__ y, float* __restrict__ ckpt, int BH, int H,
                                                      int L, int T, int nC) {
-  constexpr int R = DH / 8, NJ = DH / 8;
-  __shared__ StageSmem<DH> sm;
+  constexpr int CPW = kCpw<DH>, LPC = 64 / CPW, R = DH / LPC, NJ = DH / CPW;
+  __shared__ StageSmem<DH, CPW> sm;
   const ColId id = col_id(NJ, BH);
   if (!id.valid) return;
   const int bh = id.bh, b = bh / H, h = bh % H;
-  const int lane = threadIdx.x, g = lane & 7, c = lane >> 3, j = 8 * id.jb + c, i0 = R * g;
+  const int lane = threadIdx.x, g = lane % LPC, c = lane / LPC, j = CPW * id.jb + c, i0 = R * g;
   const int64_t row0 = (int64_t)b * L * H + h;   // (b, t = 0, h); step t adds t H
   const int logT = __builtin_ctz(T);
-  Stager<InT, InT, DH> stg;
+  Stager<InT, InT, DH, CPW> stg;
   float S[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) S[r] = h0 != nullptr ? h0[((int64_t)bh * DH + i0 + r) * DH + j] : 0.f;
   const int nblk = (L + kTS - 1) / kTS;
-  stg.issue(q, k, v, alpha, beta, 0, row0, H, L, 8 * id.jb, lane);
+  stg.issue(q, k, v, alpha, beta, 0, row0, H, L, CPW * id.jb, lane);
   stg.commit(sm, 0, 0, L, lane);
-  if (nblk > 1) stg.issue(q, k, v, alpha, beta, 1, row0, H, L, 8 * id.jb, lane);
+  if (nblk > 1) stg.issue(q, k, v, alpha, beta, 1, row0, H, L, CPW * id.jb, lane);
   rr::wave_lds_sync();
   for (int blk = 0; blk < nblk; ++blk) {
     const int buf = blk & 1, tn = min(kTS, L - blk * kTS);
-    StepIn<R> nxt = stage_step<R, DH>(sm, buf, 0, i0, c);
-    for (int st = 0; st < tn; ++st) {
-      const int t = blk * kTS + st;
-      const StepIn<R> in = nxt;
-      nxt = stage_step<R, DH>(sm, buf, min(st + 1, tn - 1), i0, c);   // the next step's reads go out first
-      step<R>(S, in);
-      const float o = col_sum(dot<R>(in.q, S));          // o_t[j] = sum_i q_t[i] S_t[i][j] (:86-90)
-      if (g == 0) y[(row0 + (int64_t)t * H) * DH + j] = o;
-      if (((t + 1) & (T - 1)) == 0) {                    // T is a power of two
-        float* ck = ckpt + (((int64_t)bh * nC + ((t + 1) >> logT) - 1) * DH + i0) * DH + j;
+    // four steps per pass (tn is a multiple of 8): their LDS reads all go out first
+    for (int st0 = 0; st0 < tn; st0 += 4) {
+      StepIn<R> in[4];
 #pragma unroll
-        for (int r = 0; r < R; ++r) ck[r * DH] = S[r];
+      for (int u = 0; u < 4; ++u) in[u] = stage_step<R, DH, CPW>(sm, buf, st0 + u, i0, c);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int t = blk * kTS + st0 + u;
+        step<R, LPC>(S, in[u]);
+        const float o = col_sum_n<LPC>(dot<R>(in[u].q, S));   // o_t[j] = sum_i q_t[i] S_t[i][j] (:86-90)
+        if (g == 0) y[(row0 + (int64_t)t * H) * DH + j] = o;
+        if (((t + 1) & (T - 1)) == 0) {                  // T is a power of two
+          float* ck = ckpt + (((int64_t)bh * nC + ((t + 1) >> logT) - 1) * DH + i0) * DH + j;
+#pragma unroll
+          for (int r = 0; r < R; ++r) ck[r * DH] = S[r];
+        }
       }
     }
     if (blk + 1 < nblk) {
       stg.commit(sm, buf ^ 1, blk + 1, L, lane);
-      if (blk + 2 < nblk) stg.issue(q, k, v, alpha, beta, blk + 2, row0, H, L, 8 * id.jb, lane);
+      if (blk + 2 < nblk) stg.issue(q, k, v, alpha, beta, blk + 2, row0, H, L, CPW * id.jb, lane);
     }
     rr::wave_lds_sync();
   }
@@ -291,40 +308,43 @@ __global__ __launch_bounds__(64) void gdn_adj_kernel(const float* __restrict__ d
                                                      const InT* __restrict__ alpha, const InT* __restrict__ beta,
                                                      float* __restrict__ adjck, float* __restrict__ dh0, int BH,
                                                      int H, int L, int T, int nC) {
-  constexpr int R = DH / 8, NJ = DH / 8;
-  __shared__ StageSmem<DH> sm;
+  constexpr int CPW = kCpw<DH>, LPC = 64 / CPW, R = DH / LPC, NJ = DH / CPW;
+  __shared__ StageSmem<DH, CPW> sm;
   const ColId id = col_id(NJ, BH);
   if (!id.valid) return;
   const int bh = id.bh, b = bh / H, h = bh % H;
-  const int lane = threadIdx.x, g = lane & 7, c = lane >> 3, j = 8 * id.jb + c, i0 = R * g;
+  const int lane = threadIdx.x, g = lane % LPC, c = lane / LPC, j = CPW * id.jb + c, i0 = R * g;
   const int64_t row0 = (int64_t)b * L * H + h;
   const int logT = __builtin_ctz(T);
-  Stager<InT, float, DH> stg;
+  Stager<InT, float, DH, CPW> stg;
   float adj[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) adj[r] = dfinal != nullptr ? dfinal[((int64_t)bh * DH + i0 + r) * DH + j] : 0.f;
   const int nblk = (L + kTS - 1) / kTS;
-  stg.issue(q, k, dy, alpha, beta, nblk - 1, row0, H, L, 8 * id.jb, lane);
+  stg.issue(q, k, dy, alpha, beta, nblk - 1, row0, H, L, CPW * id.jb, lane);
   stg.commit(sm, 0, nblk - 1, L, lane);
-  if (nblk > 1) stg.issue(q, k, dy, alpha, beta, nblk - 2, row0, H, L, 8 * id.jb, lane);
+  if (nblk > 1) stg.issue(q, k, dy, alpha, beta, nblk - 2, row0, H, L, CPW * id.jb, lane);
   rr::wave_lds_sync();
   for (int n = 0; n < nblk; ++n) {
     const int blk = nblk - 1 - n, buf = n & 1, tn = min(kTS, L - blk * kTS);
-    StepIn<R> nxt = stage_step<R, DH>(sm, buf, tn - 1, i0, c);
-    for (int st = tn - 1; st >= 0; --st) {
-      const int t = blk * kTS + st;
-      if (((t + 1) & (T - 1)) == 0) {   // the end of interval (t + 1) / T - 1, before its own steps
-        float* ac = adjck + (((int64_t)bh * nC + ((t + 1) >> logT) - 1) * DH + i0) * DH + j;
+    for (int st0 = tn - 1; st0 >= 0; st0 -= 4) {   // four steps per pass, reads first
+      StepIn<R> in[4];
 #pragma unroll
-        for (int r = 0; r < R; ++r) ac[r * DH] = adj[r];
+      for (int u = 0; u < 4; ++u) in[u] = stage_step<R, DH, CPW>(sm, buf, st0 - u, i0, c);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int t = blk * kTS + st0 - u;
+        if (((t + 1) & (T - 1)) == 0) {   // the end of interval (t + 1) / T - 1, before its own steps
+          float* ac = adjck + (((int64_t)bh * nC + ((t + 1) >> logT) - 1) * DH + i0) * DH + j;
+#pragma unroll
+          for (int r = 0; r < R; ++r) ac[r * DH] = adj[r];
+        }
+        adjoint_step<R, LPC>(adj, in[u].q, in[u].k, in[u].x, in[u].a, in[u].b);
       }
-      const StepIn<R> in = nxt;
-      nxt = stage_step<R, DH>(sm, buf, max(st - 1, 0), i0, c);
-      adjoint_step<R>(adj, in.q, in.k, in.x, in.a, in.b);
     }
     if (n + 1 < nblk) {
       stg.commit(sm, buf ^ 1, blk - 1, L, lane);
-      if (n + 2 < nblk) stg.issue(q, k, dy, alpha, beta, blk - 2, row0, H, L, 8 * id.jb, lane);
+      if (n + 2 < nblk) stg.issue(q, k, dy, alpha, beta, blk - 2, row0, H, L, CPW * id.jb, lane);
     }
     rr::wave_lds_sync();
   }
@@ -559,7 +579,7 @@ void launch_bwd_dh(int64_t T, const float* dy, const float* dfinal, const void* 
                    const void* alpha, const void* beta, const float* h0, const float* ckpt, float* adjck, void* dq,
                    void* dk, void* dv, void* dalpha, void* dbeta, float* dh0, int64_t B, int64_t H, int64_t L,
                    int64_t nC, hipStream_t s) {
-  hipLaunchKernelGGL((gdn_adj_kernel<InT, DH>), dim3(col_grid(B * H, DH / 8)), dim3(64), 0, s, dy, dfinal,
+  hipLaunchKernelGGL((gdn_adj_kernel<InT, DH>), dim3(col_grid(B * H, DH / kCpw<DH>)), dim3(64), 0, s, dy, dfinal,
                      static_cast<const InT*>(q), static_cast<const InT*>(k), static_cast<const InT*>(alpha),
                      static_cast<const InT*>(beta), adjck, dh0, (int)(B * H), (int)H, (int)L, (int)T, (int)nC);
   if (T == 32)
@@ -588,12 +608,12 @@ extern "C" int rr_gdn_fwd(const void* q, const void* k, const void* v, const voi
   hipStream_t s = static_cast<hipStream_t>(stream);
   RR_DISPATCH_DTYPE(dtype, {
     if (Dh == 64)
-      hipLaunchKernelGGL((gdn_fwd_kernel<InT, 64>), dim3(col_grid(B * H, 8)), dim3(64), 0, s,
+      hipLaunchKernelGGL((gdn_fwd_kernel<InT, 64>), dim3(col_grid(B * H, 64 / kCpw<64>)), dim3(64), 0, s,
                          static_cast<const InT*>(q), static_cast<const InT*>(k), static_cast<const InT*>(v),
                          static_cast<const InT*>(alpha), static_cast<const InT*>(beta), h0, y, ckpt, (int)(B * H),
                          (int)H, (int)L, (int)T, (int)nC);
     else
-      hipLaunchKernelGGL((gdn_fwd_kernel<InT, 32>), dim3(col_grid(B * H, 4)), dim3(64), 0, s,
+      hipLaunchKernelGGL((gdn_fwd_kernel<InT, 32>), dim3(col_grid(B * H, 32 / kCpw<32>)), dim3(64), 0, s,
                          static_cast<const InT*>(q), static_cast<const InT*>(k), static_cast<const InT*>(v),
                          static_cast<const InT*>(alpha), static_cast<const InT*>(beta), h0, y, ckpt, (int)(B * H),
                          (int)H, (int)L, (int)T, (int)nC);
