@@ -124,7 +124,7 @@ def _gen(shape, gen, kind="normal"):
 
 
 def make_ssd(cfg, device, dtype):
-    """BASELINE config 0/1/4 distributions: u ~ N(0,1); delta =
+    """BASELINE config 0/1/4 input distributions: u ~ N(0,1); delta =
     |N(0,1)|*0.1 + 0.01; B, C ~ N(0,1); A = -exp(U(0, ln 16)) per head,
     broadcast over N; dy ~ N(0,1)."""
     import math
@@ -866,7 +866,7 @@ COUNTER_SETS = {
              "SQ_INSTS_MFMA", "SQ_BUSY_CU_CYCLES"],
 }
 PROFILED_WORKLOADS = ["ssd", "gla", "rglru", "rotlru", "rglru_gated", "rotlru_theta", "ssd_c4", "ssd_b96", "gla_b96",
-                      "ssd_dense", "ssd_f32", "ssd_dh128", "gla_f32", "gla_dh128"]
+                      "ssd_dense", "ssd_f32", "ssd_dh128", "gla_f32", "gla_dh128", "gdn"]
 PROFILE_COMMANDS = [
     "rocprofv3 --kernel-trace --stats -d $R/gpurun_out/prof_trace -o trace --output-format csv -- "
     "python3 bench.py --steps 20 --warmup 3 --no-cpu --also " + ",".join(PROFILED_WORKLOADS[1:]),
@@ -1098,7 +1098,7 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every scan shards by "
-              "batch/head with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "batch/head with no exchange between GPUs). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
