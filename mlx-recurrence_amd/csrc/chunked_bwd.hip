@@ -33,7 +33,8 @@
 // h_in and lam of those blocks in registers, where a 16x16 accumulator block
 // is directly the B operand of a 16x16x16 MFMA contracting over its rows: so
 // each wave forms GH and UL of its columns in registers and writes dB and dC
-// (and the dA of) those columns.  du row block db goes to wave (db + NBN) % 4.
+// (and the dA of) those columns.  du row block db goes to wave (db + NBN) % 4
+// (two blocks per wave with Dh = 128).
 //
 // Modes as in the forward: kWhole (a head per workgroup, lam carried in
 // registers from chunk to chunk), kPipe (lam from pass_kernel), kDirect (lam
@@ -136,10 +137,11 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
   const int64_t bh = (int64_t)b * p.H + h;
   const int rsD = p.H * DH, rsN = p.H * NS;   // step strides (elements) of [.., H, DH] / [.., H, NS]
   const int l15 = lane & 15, l4 = lane >> 4;
-  const int mydb = ((w - NBN) % 4 + 4) % 4;   // the row block of du this wave forms
+  const int mydb = ((w - NBN) % 4 + 4) % 4;   // the first row block of du this wave forms
+  constexpr int DPW = (NBD + 3) / 4;           // du row blocks per wave: mydb, mydb + 4, ...
 
   f32x4_t lam[CPW][NBD];
-  float plm[REG ? NS / 32 : 1][8];   // du operand: lam[16 mydb + l15][32 kk + 8 l4 + e]
+  float plm[REG ? DPW : 1][REG ? NS / 32 : 1][8];   // du operand: lam[16 (mydb + 4 k) + l15][32 kk + 8 l4 + e]
 #pragma unroll
   for (int cc = 0; cc < CPW; ++cc)
 #pragma unroll
@@ -207,9 +209,11 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
     // the adjoint leaving the chunk; chunk 0's workgroup also stores dh0
     const float gam_all = rr::chunked::direct_sum<DH, NS, GLA, true, true>(p, cbeg, b, h, a, smu.d, p.dh0);
     const float* dfb = p.dfinal != nullptr ? p.dfinal + bh * DH * NS : nullptr;
-    // lam of this wave's columns, and its du operand (rows of block mydb)
+    // lam of this wave's columns, and its du operands (rows of blocks mydb + 4 k)
     auto lam_at = [&](int cc, int db, int r) { return std::make_pair(16 * db + 4 * l4 + r, 16 * (w + 4 * cc) + l15); };
-    auto plm_at = [&](int kk, int e) { return std::make_pair(16 * mydb + l15, 32 * kk + 8 * l4 + e); };
+    auto plm_at = [&](int k, int kk, int e) {
+      return std::make_pair(16 * (mydb + 4 * k) + l15, 32 * kk + 8 * l4 + e);
+    };
 #pragma unroll
     for (int cc = 0; cc < CPW; ++cc) {
       if (w + 4 * cc < NBN) {
@@ -222,14 +226,17 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
           }
       }
     }
-    if (mydb < NBD) {
 #pragma unroll
-      for (int kk = 0; kk < NS / 32; ++kk)
+    for (int k = 0; k < DPW; ++k) {
+      if (mydb + 4 * k < NBD) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const auto [d, n] = plm_at(kk, e);
-          plm[kk][e] = rr::chunked::direct_partial(smu.d, d, n);
-        }
+        for (int kk = 0; kk < NS / 32; ++kk)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const auto [d, n] = plm_at(k, kk, e);
+            plm[k][kk][e] = rr::chunked::direct_partial(smu.d, d, n);
+          }
+      }
     }
     if (dfb != nullptr) {
 #pragma unroll
@@ -244,14 +251,17 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
             }
         }
       }
-      if (mydb < NBD) {
 #pragma unroll
-        for (int kk = 0; kk < NS / 32; ++kk)
+      for (int k = 0; k < DPW; ++k) {
+        if (mydb + 4 * k < NBD) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const auto [d, n] = plm_at(kk, e);
-            plm[kk][e] += rr::chunked::direct_ext<DH, NS, GLA>(gam_all, dfb, d, n);
-          }
+          for (int kk = 0; kk < NS / 32; ++kk)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const auto [d, n] = plm_at(k, kk, e);
+              plm[k][kk][e] += rr::chunked::direct_ext<DH, NS, GLA>(gam_all, dfb, d, n);
+            }
+        }
       }
     }
     __syncthreads();   // the chunk below reuses the LDS of the sum
@@ -433,25 +443,29 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
     }
     __syncthreads();
     // ------------------------------------------------ B2: masked products; GLA dg / SSD T
-    // one-chunk modes: this wave's du operands (row block mydb), used in
-    // phase C; the loads land while B2 runs (issued by every wave, clamped:
+    // one-chunk modes: this wave's du operands (row blocks mydb + 4 k), used
+    // in phase C; the loads land while B2 runs (issued by every wave, clamped:
     // no branch join waits for them)
-    float pdy[REG ? 8 : 1];
+    float pdy[REG ? DPW : 1][REG ? 8 : 1];
     if constexpr (REG) {
-      const int d = 16 * min(mydb, NBD - 1) + l15;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pdy[e] = rr::ld32<float>(p.dy + baseD, (uint32_t)((8 * l4 + e) * rsD + d));
+      for (int k = 0; k < DPW; ++k) {
+        const int d = 16 * min(mydb + 4 * k, NBD - 1) + l15;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pdy[k][e] = rr::ld32<float>(p.dy + baseD, (uint32_t)((8 * l4 + e) * rsD + d));
+      }
     }
     if constexpr (MODE == kPipe) {
-      {
-        const int d = 16 * min(mydb, NBD - 1) + l15;
+#pragma unroll
+      for (int k = 0; k < DPW; ++k) {
+        const int d = 16 * min(mydb + 4 * k, NBD - 1) + l15;
         const float* lsrc = p.agg + ((bh * p.nC + c) * DH + d) * NS + 8 * l4;
 #pragma unroll
         for (int kk = 0; kk < NS / 32; ++kk) {
           const float4 l0 = *reinterpret_cast<const float4*>(lsrc + 32 * kk);
           const float4 l1 = *reinterpret_cast<const float4*>(lsrc + 32 * kk + 4);
-          plm[kk][0] = l0.x, plm[kk][1] = l0.y, plm[kk][2] = l0.z, plm[kk][3] = l0.w;
-          plm[kk][4] = l1.x, plm[kk][5] = l1.y, plm[kk][6] = l1.z, plm[kk][7] = l1.w;
+          plm[k][kk][0] = l0.x, plm[k][kk][1] = l0.y, plm[k][kk][2] = l0.z, plm[k][kk][3] = l0.w;
+          plm[k][kk][4] = l1.x, plm[k][kk][5] = l1.y, plm[k][kk][6] = l1.z, plm[k][kk][7] = l1.w;
         }
       }
     }
@@ -591,11 +605,13 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
     }
     __syncthreads();
     // ------------------------------------------------ C: du, dB, dC (+ SSD dA terms, lam_prev)
-    if (mydb < NBD) {
-      const int db = mydb;
+#pragma unroll
+    for (int k = 0; k < DPW; ++k) {
+      const int db = mydb + 4 * k;
+      if (db >= NBD) continue;
       u16x8_t gh8, gl8;   // dY^T fragment [t' = 8 l4 + e][d]
       if constexpr (REG) {
-        rr::bf_split8(pdy, gh8, gl8);
+        rr::bf_split8(pdy[k], gh8, gl8);
       } else {
         gh8 = frag(&m.GYT_hi[16 * db + l15][8 * l4]);
         gl8 = frag(&m.GYT_lo[16 * db + l15][8 * l4]);
@@ -604,7 +620,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
 #pragma unroll
       for (int kk = 0; kk < NS / 32; ++kk) {
         if constexpr (REG) {
-          rr::bf_split8(plm[kk], lh8[kk], ll8[kk]);
+          rr::bf_split8(plm[k][kk], lh8[kk], ll8[kk]);
         } else {
           lh8[kk] = frag(&m.LM_hi[16 * db + l15][32 * kk + 8 * l4]);
           ll8[kk] = frag(&m.LM_lo[16 * db + l15][32 * kk + 8 * l4]);
@@ -777,6 +793,7 @@ int chunked_bwd_cols(const ChunkArgs& p, int64_t B, hipStream_t s, bool gla) {
     switch (p.DH) {
       case 32: return launch<32, 32, true>(p, B, s);
       case 64: return launch<64, 64, true>(p, B, s);
+      case 128: return launch<128, 128, true>(p, B, s);
       default: return fail(RR_EUNSUPPORTED, "gla chunked backward: unsupported Dh");
     }
   }
@@ -785,6 +802,8 @@ int chunked_bwd_cols(const ChunkArgs& p, int64_t B, hipStream_t s, bool gla) {
     case 32128: return launch<32, 128, false>(p, B, s);
     case 64064: return launch<64, 64, false>(p, B, s);
     case 64128: return launch<64, 128, false>(p, B, s);
+    case 128064: return launch<128, 64, false>(p, B, s);
+    case 128128: return launch<128, 128, false>(p, B, s);
     default: return fail(RR_EUNSUPPORTED, "ssd chunked backward: unsupported (Dh, N)");
   }
 }

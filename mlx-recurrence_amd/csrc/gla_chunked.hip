@@ -24,8 +24,7 @@ bool gla2_supported(int dtype, int64_t B, int64_t L, int64_t H, int64_t seg, int
   if (dtype != RR_BF16 || chunk_len(L, seg) != chunked::Q) return false;
   if ((L / chunked::Q) * ((B * H + chunked::kXcds - 1) / chunked::kXcds * chunked::kXcds) >= ((int64_t)1 << 31))
     return false;
-  if (pass == 0) return Dh == 32 || Dh == 64 || Dh == 128;
-  return Dh == 32 || Dh == 64;
+  return Dh == 32 || Dh == 64 || Dh == 128;
 }
 
 // The direct mode (one kernel per pass, each chunk's workgroup summing over

@@ -52,7 +52,8 @@ int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N, int pa
 // N in {16, 32, 64, 128}.
 bool ssd2_supported(int dtype, int64_t L, int64_t seg, int64_t Dh, int64_t N, int64_t A_stride_n);
 int ssd2_fwd(const ChunkArgs& p, int64_t B, hipStream_t s);
-// The chunked backward covers Dh in {32, 64} (on top of ssd2_supported).
+// The chunked backward covers Dh in {32, 64}, and Dh = 128 with N in {64, 128}
+// (on top of ssd2_supported).
 bool ssd2_bwd_supported(int64_t Dh, int64_t N);
 // Workspace of the chunked passes: chunk decays and (backward) chunk adjoints
 // in the pipelined mode, plus dA partials (pass 1).
@@ -62,8 +63,8 @@ int ssd2_bwd(const ChunkArgs& p, int64_t B, hipStream_t s);
 
 // ------------------------------------------------------------------ GLA
 // True when the chunked GLA kernels cover this call (pass 0 forward, 1
-// backward): bf16 inputs, checkpoint interval 32, Dh in {32, 64, 128}
-// (forward) or {32, 64} (backward), and a 1-D grid of one workgroup per
+// backward): bf16 inputs, checkpoint interval 32, Dh in {32, 64, 128}, and a
+// 1-D grid of one workgroup per
 // chunk below 2^31 (direct or pipelined modes; whole heads run with
 // B * H >= 512: the forward always, the backward up to 16 chunks).
 bool gla2_supported(int dtype, int64_t B, int64_t L, int64_t H, int64_t seg, int64_t Dh, int pass);
@@ -83,7 +84,7 @@ bool res_fwd_supported(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N);
 int res_fwd(const ChunkArgs& p, int64_t B, hipStream_t s, bool gla);
 
 // Backward of the chunked kernels with column-owned state blocks (GLA: Dh in
-// {32, 64}; SSD: Dh in {32, 64}, N in {64, 128}; chunked_bwd.hip).  SSD
+// {32, 64, 128}; SSD: Dh in {32, 64, 128}, N in {64, 128}; chunked_bwd.hip).  SSD
 // leaves per-run dA partials in p.ws for the caller's reduction.
 int chunked_bwd_cols(const ChunkArgs& p, int64_t B, hipStream_t s, bool gla);
 

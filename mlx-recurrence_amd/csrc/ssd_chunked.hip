@@ -829,6 +829,7 @@ int launch_bwd(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
 namespace rr {
 
 bool ssd2_bwd_supported(int64_t Dh, int64_t N) {
+  if (Dh == 128) return N == 64 || N == 128;   // the column-owned kernel
   return (Dh == 32 || Dh == 64) && (N == 16 || N == 32 || N == 64 || N == 128);
 }
 
@@ -894,7 +895,7 @@ int ssd2_bwd(const ChunkArgs& p, int64_t B, hipStream_t s) {
     case 32032: return launch_bwd<32, 32>(p, B, s);
     case 64016: return launch_bwd<64, 16>(p, B, s);
     case 64032: return launch_bwd<64, 32>(p, B, s);
-    case 32064: case 32128: case 64064: case 64128:
+    case 32064: case 32128: case 64064: case 64128: case 128064: case 128128:
       if (int rc = chunked_bwd_cols(p, B, s, false)) return rc;
       return launch_dA(p, B, s);
     default: return fail(RR_EUNSUPPORTED, "ssd chunked backward: unsupported (Dh, N)");

@@ -346,6 +346,10 @@ SSD_CASES = [
     (1, 192, 3, 64, 128, 32, BF16, "cfg", False, True, 33),  # pipelined
     (1, 64, 512, 32, 64, 32, BF16, "cfg", True, True, 34),   # whole head
     (2, 96, 256, 64, 128, 32, BF16, "cfg", True, True, 35),  # whole head, config 4's tile
+    # Dh = 128 (column-owned backward, two du row blocks per wave)
+    (3, 512, 12, 128, 64, 32, BF16, "cfg", True, True, 40),   # the reference's production shape: pipelined
+    (1, 160, 3, 128, 128, 32, BF16, "cfg", True, True, 41),   # N = 128, pipelined
+    (2, 192, 160, 128, 64, 32, BF16, "cfg", False, True, 42), # B*H >= 320: per-head adjoint scan
     # pipelined with B*H >= 320: the per-head state / adjoint scan kernel
     (1, 640, 320, 32, 16, 32, BF16, "cfg", True, True, 38),
     (2, 320, 160, 32, 64, 32, BF16, "cfg", True, True, 39),
@@ -417,7 +421,8 @@ GLA_CASES = [
     # bf16 with T = 32: chunked MFMA kernels
     (2, 256, 3, 64, 32, BF16, "cfg", True, True, 20),
     (1, 128, 2, 32, 32, BF16, "ref", True, True, 21),
-    (1, 96, 2, 128, 32, BF16, "cfg", True, True, 22),   # chunked forward, VALU backward
+    (1, 96, 2, 128, 32, BF16, "cfg", True, True, 22),   # Dh = 128: resident forward, pipelined backward
+    (1, 256, 3, 128, 32, BF16, "signed", True, True, 39),  # Dh = 128, 8 chunks, gates of either sign
     (2, 32, 2, 64, 32, BF16, "cfg", True, True, 23),    # one chunk
     (1, 160, 2, 64, 32, BF16, "signed", True, True, 24),
     (1, 128, 2, 32, 32, BF16, "zeros", True, True, 25),
@@ -431,7 +436,8 @@ GLA_CASES = [
     (4, 512, 12, 64, 32, BF16, "cfg", True, False, 35),     # 768 workgroups: direct, the largest
     (1, 160, 512, 64, 32, BF16, "signed", True, True, 36),  # B*H >= 512: whole-head forward
     (2, 64, 256, 32, 32, BF16, "zeros", True, True, 37),    # whole-head forward, Dh = 32
-    (1, 32, 512, 128, 32, BF16, "cfg", True, True, 38),     # whole-head forward, Dh = 128 (VALU backward)
+    (1, 32, 512, 128, 32, BF16, "cfg", True, True, 38),     # whole-head forward and backward, Dh = 128
+    (1, 64, 512, 128, 32, BF16, "zeros", True, True, 40),   # whole head, Dh = 128, 2 chunks, zero gates
 ]
 
 
