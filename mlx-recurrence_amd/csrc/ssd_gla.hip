@@ -20,8 +20,9 @@
 //     lam *= dec_t[n]
 //
 // Work decomposition.  A workgroup owns a 16(d) x 16(n) tile of one head's
-// state for the whole sequence; lane = 4*dl + ng holds d = 16*dt + dl and the
-// four states n = 16*nt + 4*ng + k.  Its NW waves take NW consecutive chunks of
+// state for the whole sequence; lane = 16*ng + dl holds d = 16*dt + dl and the
+// four states n = 16*nt + 4*ng + k (a row of 16 lanes is one n-group, so sums
+// over d stay within a row: DPP, no LDS traffic).  Its NW waves take NW consecutive chunks of
 // T steps at once (chunk-parallel scan): each wave stages its chunk's per-step
 // coefficients (dec, inB, outC; one exp per (t, n) instead of one per lane)
 // in LDS, folds the chunk into the affine map h -> P*h + E, the maps are
@@ -34,8 +35,10 @@
 // recurrence-specific epilogue (dB = delta*Gin, d(delta), dA, dgates).
 #include "rr_common.h"
 #include "rr_internal.h"
+#include "rr_mfma.h"
 
 #include <atomic>
+#include <type_traits>
 #include <string>
 
 namespace {
@@ -43,28 +46,37 @@ namespace {
 constexpr int kMaxT = 32;
 constexpr int kTile = 16;
 constexpr int kFwdWaves = 8;
-constexpr int kBwdWaves = 4;
+constexpr int kBwdWaves = 8;
 constexpr int kFinRows = 32;  // (b, t) rows per finalize workgroup
 
-__device__ __forceinline__ float qxor1(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+// Sum over the 4 rows (the 4 n-groups of one d: lanes l, l ^ 16, l ^ 32,
+// l ^ 48) with gfx950's row-swapping permutes (VALU, no LDS traffic); every
+// lane of the group gets the same value.
+__device__ __forceinline__ float ngroup_sum(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto h = __builtin_amdgcn_permlane32_swap(u, u, false, false);   // lanes l % 32, l % 32 + 32
+  v = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+  const uint32_t x = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);   // rows 2k, 2k + 1
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
-__device__ __forceinline__ float qxor2(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+// Sums over the 16 lanes of a row (the 16 d of a tile) of N values at once,
+// butterfly level by level across the values (independent DPP adds back to
+// back, none waiting on the one before); every lane of the row gets the sum.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
 }
-// Sum over the 4 lanes of a quad (the 4 n-groups of one d).
-__device__ __forceinline__ float quad_sum(float v) {
-  v += qxor1(v);
-  v += qxor2(v);
-  return v;
-}
-// Sum over the 16 lanes sharing (lane & 3) (the 16 d of a tile).
-__device__ __forceinline__ float dsum16(float v) {
-  v += __shfl_xor(v, 4);
-  v += __shfl_xor(v, 8);
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+template <int N>
+__device__ __forceinline__ void dsum16(float (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = dpp_add<0xB1>(v[i]);    // quad_perm [1, 0, 3, 2]
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = dpp_add<0x4E>(v[i]);    // quad_perm [2, 3, 0, 1]
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = dpp_add<0x141>(v[i]);   // row_half_mirror
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = dpp_add<0x140>(v[i]);   // row_mirror
 }
 
 template <typename InT>
@@ -134,7 +146,7 @@ __global__ __launch_bounds__(64 * NW) void r1_fwd_kernel(Args<InT> p) {
   __shared__ float4 sE[NW][64];
   __shared__ float4 sP[NW][4];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int ng = lane & 3, dl = lane >> 2;
+  const int ng = lane >> 4, dl = lane & 15;
   const int dt = blockIdx.x / p.NN, nt = blockIdx.x % p.NN;
   const int h = blockIdx.y, b = blockIdx.z;
   const int d = dt * kTile + dl;
@@ -209,7 +221,7 @@ __global__ __launch_bounds__(64 * NW) void r1_fwd_kernel(Args<InT> p) {
           hs[k] = dec[k] * hs[k] + inb[k] * uv[t];
           yp += outc[k] * hs[k];
         }
-        yp = quad_sum(yp);
+        yp = ngroup_sum(yp);
         if (act && dok && ng == (t & 3))
           yout[(((int64_t)b * p.L + (int64_t)c * p.T + t) * p.H + h) * p.DL + d] = yp;
       }
@@ -234,7 +246,7 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
   __shared__ float4 sE[NW][64];
   __shared__ float4 sP[NW][4];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int ng = lane & 3, dl = lane >> 2;
+  const int ng = lane >> 4, dl = lane & 15;
   const int dt = blockIdx.x / p.NN, nt = blockIdx.x % p.NN;
   const int h = blockIdx.y, b = blockIdx.z;
   const int d = dt * kTile + dl;
@@ -279,21 +291,20 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
       }
     }
     __syncthreads();
-    // Recompute the chunk's states: hs[t][k] = h_t.
-    float hs[kMaxT][4];
-    {
-      float hc[4] = {hst[0], hst[1], hst[2], hst[3]};
+    // The chunk's states are recomputed from its checkpoint in two halves of
+    // 16 steps (16 x 4 registers at a time): here the state after step 15,
+    // below each half again from its entering state as the adjoint walks it.
+    constexpr int kHalf = kMaxT / 2;
+    float hmid[4] = {hst[0], hst[1], hst[2], hst[3]};
 #pragma unroll
-      for (int t = 0; t < kMaxT; ++t) {
-        if (t < p.T) {
-          float dec[4], inb[4];
-          unpack(sCoef[w][0][t][ng], dec);
-          unpack(sCoef[w][1][t][ng], inb);
+    for (int t = 0; t < kHalf; ++t) {
+      if (t < p.T) {
+        float dec[4], inb[4];
+        unpack(sCoef[w][0][t][ng], dec);
+        unpack(sCoef[w][1][t][ng], inb);
+        const float uvt = sU[w][t][dl];
 #pragma unroll
-          for (int k = 0; k < 4; ++k) hc[k] = dec[k] * hc[k] + inb[k] * sU[w][t][dl];
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) hs[t][k] = hc[k];
+        for (int k = 0; k < 4; ++k) hmid[k] = dec[k] * hmid[k] + inb[k] * uvt;
       }
     }
     // Chunk map of the adjoint from a zero carry.
@@ -328,43 +339,81 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
         nxt[k] = pj[k] * nxt[k] + ej[k];
       }
     }
+    // Steps t0 .. t0 + 15 of the adjoint, backwards, beside their states
+    // recomputed from hbeg (the state entering step t0).
+    // Gin, Gout, Hp of a lane's four states as one 16-byte store each
+    const bool st4 = p.NS % 4 == 0 && (reinterpret_cast<uintptr_t>(p.g3) & 15) == 0;
+    auto adjoint_half = [&](auto half, const float (&hbeg)[4]) {
+      constexpr int t0 = decltype(half)::value;
+      float hs[kHalf][4];
+      {
+        float hc[4] = {hbeg[0], hbeg[1], hbeg[2], hbeg[3]};
 #pragma unroll
-    for (int t = kMaxT - 1; t >= 0; --t) {
-      if (t < p.T) {
-        float dec[4], inb[4], outc[4];
-        unpack(sCoef[w][0][t][ng], dec);
-        unpack(sCoef[w][1][t][ng], inb);
-        unpack(sCoef[w][2][t][ng], outc);
-        const float uvt = sU[w][t][dl], gyt = sG[w][t][dl];
-        float gup = 0.f, gin[4], gout[4], hp[4];
+        for (int i = 0; i < kHalf; ++i) {
+          const int t = t0 + i;
+          if (t < p.T) {
+            float dec[4], inb[4];
+            unpack(sCoef[w][0][t][ng], dec);
+            unpack(sCoef[w][1][t][ng], inb);
+            const float uvt = sU[w][t][dl];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          lam[k] += gyt * outc[k];
-          gup += lam[k] * inb[k];
-          gin[k] = dsum16(lam[k] * uvt);
-          gout[k] = dsum16(hs[t][k] * gyt);
-          const float hprev = (t > 0) ? hs[t - 1][k] : hst[k];
-          hp[k] = dsum16(lam[k] * hprev);
-          lam[k] *= dec[k];
-        }
-        gup = quad_sum(gup);
-        const int64_t row = ((int64_t)b * p.L + (int64_t)c * p.T + t) * p.H + h;
-        if (act && dl == 0) {
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            if (nb + k < p.NS) {
-              gin_p[row * p.NS + nb + k] = gin[k];
-              gout_p[row * p.NS + nb + k] = gout[k];
-              hp_p[row * p.NS + nb + k] = hp[k];
-            }
+            for (int k = 0; k < 4; ++k) hc[k] = dec[k] * hc[k] + inb[k] * uvt;
           }
-        }
-        if (act && dok && ng == (t & 3)) {
-          if (p.NN > 1) p.gu_part[((int64_t)nt * p.rows + row) * p.DL + d] = gup;
-          else rr::st(p.gu, row * p.DL + d, gup);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) hs[i][k] = hc[k];
         }
       }
-    }
+#pragma unroll
+      for (int i = kHalf - 1; i >= 0; --i) {
+        const int t = t0 + i;
+        if (t < p.T) {
+          float dec[4], inb[4], outc[4];
+          unpack(sCoef[w][0][t][ng], dec);
+          unpack(sCoef[w][1][t][ng], inb);
+          unpack(sCoef[w][2][t][ng], outc);
+          const float uvt = sU[w][t][dl], gyt = sG[w][t][dl];
+          float gup = 0.f, g12[12];   // Gin, Gout, Hp of the four states, summed over d
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            lam[k] += gyt * outc[k];
+            gup += lam[k] * inb[k];
+            g12[k] = lam[k] * uvt;
+            g12[4 + k] = hs[i][k] * gyt;
+            const float hprev = i > 0 ? hs[i - 1][k] : hbeg[k];
+            g12[8 + k] = lam[k] * hprev;
+            lam[k] *= dec[k];
+          }
+          dsum16(g12);
+          gup = ngroup_sum(gup);
+          const int64_t row = ((int64_t)b * p.L + (int64_t)c * p.T + t) * p.H + h;
+          if (st4) {
+            // lanes dl = 0, 1, 2 of each row store Gin, Gout, Hp (n-groups
+            // past NS hold no states)
+            if (act && dl < 3 && nb < p.NS) {
+              const float4 v = dl == 0 ? make_float4(g12[0], g12[1], g12[2], g12[3])
+                               : dl == 1 ? make_float4(g12[4], g12[5], g12[6], g12[7])
+                                         : make_float4(g12[8], g12[9], g12[10], g12[11]);
+              *reinterpret_cast<float4*>(gin_p + (int64_t)dl * p.ND * p.rows * p.NS + row * p.NS + nb) = v;
+            }
+          } else if (act && dl == 0) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              if (nb + k < p.NS) {
+                gin_p[row * p.NS + nb + k] = g12[k];
+                gout_p[row * p.NS + nb + k] = g12[4 + k];
+                hp_p[row * p.NS + nb + k] = g12[8 + k];
+              }
+            }
+          }
+          if (act && dok && ng == (t & 3)) {
+            if (p.NN > 1) p.gu_part[((int64_t)nt * p.rows + row) * p.DL + d] = gup;
+            else rr::st(p.gu, row * p.DL + d, gup);
+          }
+        }
+      }
+    };
+    adjoint_half(std::integral_constant<int, kHalf>{}, hmid);
+    adjoint_half(std::integral_constant<int, 0>{}, hst);
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 4; ++k) carry[k] = nxt[k];

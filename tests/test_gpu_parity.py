@@ -333,6 +333,9 @@ SSD_CASES = [
     (1, 128, 512, 32, 16, 32, BF16, "cfg", True, True, 17),
     (2, 96, 256, 64, 32, 32, BF16, "cfg", False, True, 18),
     (2, 64, 256, 64, 16, 32, BF16, "cfg", True, False, 19),
+    # Dh 64, N 16 sums row-owned: ranges shorter and longer than the loads in flight
+    (1, 224, 3, 64, 16, 32, BF16, "cfg", True, True, 43),
+    (2, 32, 2, 64, 16, 32, BF16, "cfg", True, True, 44),
     # more than 16 chunks: pipelined mode (aggregate, state-pass and chunk kernels);
     # 36, 37: 12 and 6 chunks (one kernel per pass, sums over the other chunks)
     (1, 1024, 3, 64, 16, 32, BF16, "cfg", True, True, 26),
