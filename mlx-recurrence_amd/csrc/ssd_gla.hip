@@ -109,27 +109,38 @@ __device__ __forceinline__ int64_t state_idx(int d, int n, int DL, int NS) {
   return GLA ? (int64_t)n * DL + d : (int64_t)d * NS + n;
 }
 
+// Every staging load below is issued first, at a clamped in-bounds index, and
+// masked afterwards: loads under a branch would each wait out a full memory
+// latency in turn.
+constexpr int kStageIt = kMaxT * kTile / 64;   // (step, column) pairs per lane
+
+// The chunk's per-step coefficients of state columns nt*16 .. nt*16 + 15:
+// lane holds column nn = lane % 16 of steps lane / 16 + 4 j.
 template <typename InT, bool GLA>
 __device__ __forceinline__ void stage_chunk(const Args<InT>& p, float4 (*coef)[kMaxT][4],
                                             int b, int h, int c, bool act, int nt, int lane) {
-  for (int i = lane; i < kMaxT * kTile; i += 64) {
-    const int t = i >> 4, nn = i & 15, n = nt * kTile + nn;
-    float dec = 1.f, inb = 0.f, outc = 0.f;
-    if (act && t < p.T && n < p.NS) {
-      const int64_t row = ((int64_t)b * p.L + (int64_t)c * p.T + t) * p.H + h;
-      const float sv = rr::ld(p.step, row);
-      if (GLA) {
-        dec = sv;
-        inb = rr::ld(p.in_coef, row * p.NS + n);
-      } else {
-        dec = expf(sv * p.A[(int64_t)h * p.a_sh + (int64_t)n * p.a_sn]);
-        inb = sv * rr::ld(p.in_coef, row * p.NS + n);
-      }
-      outc = rr::ld(p.out_coef, row * p.NS + n);
-    }
-    reinterpret_cast<float*>(&coef[0][t][0])[nn] = dec;
-    reinterpret_cast<float*>(&coef[1][t][0])[nn] = inb;
-    reinterpret_cast<float*>(&coef[2][t][0])[nn] = outc;
+  const int nn = lane & 15, n = nt * kTile + nn;
+  const bool nok = n < p.NS;
+  const int nc = min(n, p.NS - 1), cc = act ? c : 0;
+  const float an = GLA ? 0.f : p.A[(int64_t)h * p.a_sh + (int64_t)nc * p.a_sn];
+  float sv[kStageIt], bv[kStageIt], cv[kStageIt];
+#pragma unroll
+  for (int j = 0; j < kStageIt; ++j) {
+    const int t = (lane >> 4) + 4 * j, tc = min(t, p.T - 1);
+    const int64_t row = ((int64_t)b * p.L + (int64_t)cc * p.T + tc) * p.H + h;
+    sv[j] = rr::ld(p.step, row);
+    bv[j] = rr::ld(p.in_coef, row * p.NS + nc);
+    cv[j] = rr::ld(p.out_coef, row * p.NS + nc);
+  }
+#pragma unroll
+  for (int j = 0; j < kStageIt; ++j) {
+    const int t = (lane >> 4) + 4 * j;
+    const bool ok = act && t < p.T && nok;
+    const float dec = GLA ? sv[j] : expf(sv[j] * an);
+    const float inb = GLA ? bv[j] : sv[j] * bv[j];
+    reinterpret_cast<float*>(&coef[0][t][0])[nn] = ok ? dec : 1.f;
+    reinterpret_cast<float*>(&coef[1][t][0])[nn] = ok ? inb : 0.f;
+    reinterpret_cast<float*>(&coef[2][t][0])[nn] = ok ? cv[j] : 0.f;
   }
 }
 
@@ -167,11 +178,13 @@ __global__ __launch_bounds__(64 * NW) void r1_fwd_kernel(Args<InT> p) {
     const bool act = c < p.nC;
     stage_chunk<InT, GLA>(p, sCoef[w], b, h, c, act, nt, lane);
     float uv[kMaxT];
+    {
+      const int cc = act ? c : 0, dc = min(d, p.DL - 1);
 #pragma unroll
-    for (int t = 0; t < kMaxT; ++t) {
-      uv[t] = 0.f;
-      if (t < p.T && act && dok)
-        uv[t] = rr::ld(p.lane_in, (((int64_t)b * p.L + (int64_t)c * p.T + t) * p.H + h) * p.DL + d);
+      for (int t = 0; t < kMaxT; ++t)
+        uv[t] = rr::ld(p.lane_in, (((int64_t)b * p.L + (int64_t)cc * p.T + min(t, p.T - 1)) * p.H + h) * p.DL + dc);
+#pragma unroll
+      for (int t = 0; t < kMaxT; ++t) uv[t] = t < p.T && act && dok ? uv[t] : 0.f;
     }
     __syncthreads();
     float e[4] = {0.f, 0.f, 0.f, 0.f}, P[4] = {1.f, 1.f, 1.f, 1.f};
@@ -238,14 +251,25 @@ __global__ __launch_bounds__(64 * NW) void r1_fwd_kernel(Args<InT> p) {
   }
 }
 
-template <typename InT, bool GLA, int NW>
+// g[i] for i < 12 (a select tree over the bits of i; i >= 12: any of them).
+__device__ __forceinline__ float pick12(const float (&g)[12], int i) {
+  const bool b0 = i & 1, b1 = i & 2, b2 = i & 4, b3 = i & 8;
+  const float a0 = b0 ? g[1] : g[0], a1 = b0 ? g[3] : g[2], a2 = b0 ? g[5] : g[4];
+  const float a3 = b0 ? g[7] : g[6], a4 = b0 ? g[9] : g[8], a5 = b0 ? g[11] : g[10];
+  const float c0 = b1 ? a1 : a0, c1 = b1 ? a3 : a2, c2 = b1 ? a5 : a4;
+  return b3 ? c2 : b2 ? c1 : c0;
+}
+
+// PART: the grid has several n-tiles (NN > 1) and du / dv goes to per-tile
+// fp32 partials, else straight to gu.
+template <typename InT, bool GLA, int NW, bool PART>
 __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
   __shared__ float4 sCoef[NW][3][kMaxT][4];
   __shared__ float sU[NW][kMaxT][kTile];   // u_t[d] of the wave's chunk
   __shared__ float sG[NW][kMaxT][kTile];   // dy_t[d]
   __shared__ float4 sE[NW][64];
   __shared__ float4 sP[NW][4];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ng = lane >> 4, dl = lane & 15;
   const int dt = blockIdx.x / p.NN, nt = blockIdx.x % p.NN;
   const int h = blockIdx.y, b = blockIdx.z;
@@ -254,9 +278,7 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
   const int nb = nt * kTile + ng * 4;
   const int64_t bh = (int64_t)b * p.H + h;
   const int64_t sbase = bh * p.DL * p.NS;
-  float* gin_p = p.g3 + (int64_t)dt * p.rows * p.NS;
-  float* gout_p = gin_p + (int64_t)p.ND * p.rows * p.NS;
-  float* hp_p = gout_p + (int64_t)p.ND * p.rows * p.NS;
+  float* gin_p = p.g3 + (int64_t)dt * p.rows * p.NS;   // then Gout, Hp, ND * rows * NS apart
 
   float carry[4] = {0.f, 0.f, 0.f, 0.f};
   if (p.dfinal != nullptr && dok) {
@@ -269,26 +291,39 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
     const int c = p.nC - 1 - (r0 + w);
     const bool act = c >= 0;
     stage_chunk<InT, GLA>(p, sCoef[w], b, h, c, act, nt, lane);
-    for (int i = lane; i < kMaxT * kTile; i += 64) {
-      const int t = i >> 4, dd = dt * kTile + (i & 15);
-      float uvv = 0.f, gyv = 0.f;
-      if (act && t < p.T && dd < p.DL) {
-        const int64_t j = (((int64_t)b * p.L + (int64_t)c * p.T + t) * p.H + h) * p.DL + dd;
-        uvv = rr::ld(p.lane_in, j);
-        gyv = p.dy[j];
+    float hst[4];
+    {
+      // u and dy of columns dt*16 + lane % 16, steps lane / 16 + 4 j
+      const int cc = act ? c : 0, dd = dt * kTile + (lane & 15), ddc = min(dd, p.DL - 1);
+      float uvv[kStageIt], gyv[kStageIt];
+#pragma unroll
+      for (int j = 0; j < kStageIt; ++j) {
+        const int t = (lane >> 4) + 4 * j;
+        const int64_t i = (((int64_t)b * p.L + (int64_t)cc * p.T + min(t, p.T - 1)) * p.H + h) * p.DL + ddc;
+        uvv[j] = rr::ld(p.lane_in, i);
+        gyv[j] = p.dy[i];
       }
-      sU[w][t][i & 15] = uvv;
-      sG[w][t][i & 15] = gyv;
-    }
-    float hst[4] = {0.f, 0.f, 0.f, 0.f};
-    if (act && dok) {
+      // the entering state: checkpoint slot c - 1, else h0, else zero
+      const bool from_ck = c > 0, has = from_ck || p.h0 != nullptr;
+      const float* hsrc = from_ck ? p.ckpt : has ? p.h0 : p.ckpt;
+      const int dc = min(d, p.DL - 1);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        if (nb + k < p.NS) {
-          if (c > 0) hst[k] = p.ckpt[((bh * p.nC + (c - 1)) * p.DL + d) * p.NS + nb + k];
-          else if (p.h0 != nullptr) hst[k] = p.h0[sbase + state_idx<GLA>(d, nb + k, p.DL, p.NS)];
-        }
+        const int ncl = min(nb + k, p.NS - 1);
+        const int64_t i = from_ck ? ((bh * p.nC + (cc - 1)) * p.DL + dc) * p.NS + ncl
+                          : has   ? sbase + state_idx<GLA>(dc, ncl, p.DL, p.NS)
+                                  : 0;
+        hst[k] = hsrc[i];
       }
+#pragma unroll
+      for (int j = 0; j < kStageIt; ++j) {
+        const int t = (lane >> 4) + 4 * j;
+        const bool ok = act && t < p.T && dd < p.DL;
+        sU[w][t][lane & 15] = ok ? uvv[j] : 0.f;
+        sG[w][t][lane & 15] = ok ? gyv[j] : 0.f;
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) hst[k] = act && dok && has && nb + k < p.NS ? hst[k] : 0.f;
     }
     __syncthreads();
     // The chunk's states are recomputed from its checkpoint in two halves of
@@ -340,9 +375,15 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
       }
     }
     // Steps t0 .. t0 + 15 of the adjoint, backwards, beside their states
-    // recomputed from hbeg (the state entering step t0).
-    // Gin, Gout, Hp of a lane's four states as one 16-byte store each
-    const bool st4 = p.NS % 4 == 0 && (reinterpret_cast<uintptr_t>(p.g3) & 15) == 0;
+    // recomputed from hbeg (the state entering step t0).  Per step, lane
+    // dl < 12 of each row stores quantity dl / 4 (Gin, Gout, Hp) of state
+    // nb + dl % 4, and the row ng == t % 4 stores du / dv of its 16 columns:
+    // per-lane bases here, a uniform row offset per step.
+    const int64_t crow = ((int64_t)b * p.L + (int64_t)(act ? c : 0) * p.T) * p.H + h;   // step 0's row
+    float* const gq = gin_p + (int64_t)(dl >> 2) * p.ND * p.rows * p.NS + nb + (dl & 3);
+    const bool gq_ok = act && dl < 12 && nb + (dl & 3) < p.NS;
+    float* const gu_f = PART ? p.gu_part + (int64_t)nt * p.rows * p.DL + d : nullptr;
+    InT* const gu_t = PART ? nullptr : p.gu + d;
     auto adjoint_half = [&](auto half, const float (&hbeg)[4]) {
       constexpr int t0 = decltype(half)::value;
       float hs[kHalf][4];
@@ -385,29 +426,14 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
           }
           dsum16(g12);
           gup = ngroup_sum(gup);
-          const int64_t row = ((int64_t)b * p.L + (int64_t)c * p.T + t) * p.H + h;
-          if (st4) {
-            // lanes dl = 0, 1, 2 of each row store Gin, Gout, Hp (n-groups
-            // past NS hold no states)
-            if (act && dl < 3 && nb < p.NS) {
-              const float4 v = dl == 0 ? make_float4(g12[0], g12[1], g12[2], g12[3])
-                               : dl == 1 ? make_float4(g12[4], g12[5], g12[6], g12[7])
-                                         : make_float4(g12[8], g12[9], g12[10], g12[11]);
-              *reinterpret_cast<float4*>(gin_p + (int64_t)dl * p.ND * p.rows * p.NS + row * p.NS + nb) = v;
-            }
-          } else if (act && dl == 0) {
+          const int64_t row = crow + (int64_t)t * p.H;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              if (nb + k < p.NS) {
-                gin_p[row * p.NS + nb + k] = g12[k];
-                gout_p[row * p.NS + nb + k] = g12[4 + k];
-                hp_p[row * p.NS + nb + k] = g12[8 + k];
-              }
-            }
-          }
+          for (int i = 0; i < 12; ++i) asm volatile("" : "+v"(g12[i]));   // formed here, selected below
+          const float gv = pick12(g12, dl);
+          if (gq_ok) gq[row * p.NS] = gv;
           if (act && dok && ng == (t & 3)) {
-            if (p.NN > 1) p.gu_part[((int64_t)nt * p.rows + row) * p.DL + d] = gup;
-            else rr::st(p.gu, row * p.DL + d, gup);
+            if constexpr (PART) gu_f[row * p.DL] = gup;
+            else rr::st(gu_t, row * p.DL, gup);
           }
         }
       }
@@ -457,7 +483,7 @@ struct FinArgs {
 template <typename InT, bool GLA>
 __global__ __launch_bounds__(256) void r1_finalize_kernel(FinArgs<InT> p) {
   __shared__ float sA[4][256];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = blockIdx.y;
   const int64_t rows = p.BL * p.H;
   const int64_t plane = (int64_t)p.ND * rows * p.NS;
@@ -585,7 +611,10 @@ template <typename InT, bool GLA>
 int launch_bwd(Args<InT> a, FinArgs<InT> f, const Plan& q, int64_t B, hipStream_t s,
                float* dA) {
   const dim3 grid((unsigned)(q.ND * q.NN), (unsigned)a.H, (unsigned)B);
-  hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kBwdWaves>), grid, dim3(64 * kBwdWaves), 0, s, a);
+  if (q.NN > 1)
+    hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kBwdWaves, true>), grid, dim3(64 * kBwdWaves), 0, s, a);
+  else
+    hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kBwdWaves, false>), grid, dim3(64 * kBwdWaves), 0, s, a);
   if (int rc = rr::check_launch("scan backward")) return rc;
   const dim3 fgrid((unsigned)q.nblk, (unsigned)a.H);
   hipLaunchKernelGGL((r1_finalize_kernel<InT, GLA>), fgrid, dim3(256), 0, s, f);
