@@ -478,24 +478,46 @@ struct FinArgs {
   int H, DL, NS, ND, NN;
 };
 
-// One workgroup = one head h and kFinRows consecutive (b, t) rows; wave w takes
-// rows w, w+4, ...; lanes stride over n (and over d for the gu sum).
-template <typename InT, bool GLA>
+// Sum over the P lanes of a group (P = 16: a row, 32: two rows, 64: the
+// wave); every lane of the group gets the sum.
+template <int P>
+__device__ __forceinline__ float group_sum(float v) {
+  v = rr::row16_sum(v);
+  if constexpr (P == 32) {
+    const uint32_t x = __float_as_uint(v);
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);   // rows 2k, 2k + 1
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else if constexpr (P == 64) {
+    v = ngroup_sum(v);
+  }
+  return v;
+}
+
+// One workgroup = one head h and kFinRows consecutive (b, t) rows.  A group of
+// P lanes takes one row (lanes over n, then over d for the du sum), so a wave
+// takes 64 / P rows at a time: P = 16 for NS <= 16, 32 for NS <= 32, else 64
+// (n strided by 64).
+template <typename InT, bool GLA, int P>
 __global__ __launch_bounds__(256) void r1_finalize_kernel(FinArgs<InT> p) {
-  __shared__ float sA[4][256];
+  constexpr int G = 64 / P;   // rows per wave at a time
+  __shared__ float sA[4][G][P == 64 ? 256 : P];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int sub = lane / P, ln = lane % P;
   const int h = blockIdx.y;
   const int64_t rows = p.BL * p.H;
   const int64_t plane = (int64_t)p.ND * rows * p.NS;
-  float gacc[4] = {0.f, 0.f, 0.f, 0.f};  // SSD dA partial for n = lane + 64*q
-  for (int r = w; r < kFinRows; r += 4) {
+  constexpr int QA = P == 64 ? 4 : 1;   // SSD dA partials of n = ln + P q
+  float gacc[QA];
+#pragma unroll
+  for (int q = 0; q < QA; ++q) gacc[q] = 0.f;
+  for (int r = w * G + sub; r < kFinRows; r += 4 * G) {
     const int64_t bt = (int64_t)blockIdx.x * kFinRows + r;
-    if (bt >= p.BL) break;
+    if (bt >= p.BL) break;   // (uniform within the group; the groups after it stop too)
     const int64_t row = bt * p.H + h;
     const float sv = rr::ld(p.step, row);
     float acc = 0.f;
-    for (int q = 0; q * 64 < p.NS; ++q) {
-      const int n = q * 64 + lane;
+    for (int q = 0; q * P < p.NS; ++q) {
+      const int n = q * P + ln;
       if (n < p.NS) {
         float gin = 0.f, gout = 0.f, hp = 0.f;
         for (int j = 0; j < p.ND; ++j) {
@@ -514,15 +536,14 @@ __global__ __launch_bounds__(256) void r1_finalize_kernel(FinArgs<InT> p) {
           rr::st(p.g_in, row * p.NS + n, sv * gin);
           rr::st(p.g_out, row * p.NS + n, gout);
           acc += a * dec * hp + rr::ld(p.in_coef, row * p.NS + n) * gin;
-          if (q < 4) gacc[q] += sv * dec * hp;
+          if (q < QA) gacc[q] += sv * dec * hp;
         }
       }
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
-    if (lane == 0) rr::st(p.g_step, row, acc);
+    acc = group_sum<P>(acc);
+    if (ln == 0) rr::st(p.g_step, row, acc);
     if (p.NN > 1) {
-      for (int d = lane; d < p.DL; d += 64) {
+      for (int d = ln; d < p.DL; d += P) {
         float s = 0.f;
         for (int j = 0; j < p.NN; ++j) s += p.gu_part[((int64_t)j * rows + row) * p.DL + d];
         rr::st(p.gu, row * p.DL + d, s);
@@ -531,10 +552,14 @@ __global__ __launch_bounds__(256) void r1_finalize_kernel(FinArgs<InT> p) {
   }
   if (!GLA) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) sA[w][q * 64 + lane] = gacc[q];
+    for (int q = 0; q < QA; ++q) sA[w][sub][q * P + ln] = gacc[q];
     __syncthreads();
     for (int n = threadIdx.x; n < p.NS; n += 256) {
-      const float s = sA[0][n] + sA[1][n] + sA[2][n] + sA[3][n];
+      float s = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww)
+#pragma unroll
+        for (int g = 0; g < G; ++g) s += sA[ww][g][n];
       p.gA_part[((int64_t)h * gridDim.x + blockIdx.x) * p.NS + n] = s;
     }
   }
@@ -617,7 +642,12 @@ int launch_bwd(Args<InT> a, FinArgs<InT> f, const Plan& q, int64_t B, hipStream_
     hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kBwdWaves, false>), grid, dim3(64 * kBwdWaves), 0, s, a);
   if (int rc = rr::check_launch("scan backward")) return rc;
   const dim3 fgrid((unsigned)q.nblk, (unsigned)a.H);
-  hipLaunchKernelGGL((r1_finalize_kernel<InT, GLA>), fgrid, dim3(256), 0, s, f);
+  if (a.NS <= 16)
+    hipLaunchKernelGGL((r1_finalize_kernel<InT, GLA, 16>), fgrid, dim3(256), 0, s, f);
+  else if (a.NS <= 32)
+    hipLaunchKernelGGL((r1_finalize_kernel<InT, GLA, 32>), fgrid, dim3(256), 0, s, f);
+  else
+    hipLaunchKernelGGL((r1_finalize_kernel<InT, GLA, 64>), fgrid, dim3(256), 0, s, f);
   if (int rc = rr::check_launch("scan backward finalize")) return rc;
   if (!GLA) {
     const int n = (int)(a.H * a.NS);
