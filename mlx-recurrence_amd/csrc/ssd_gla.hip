@@ -221,6 +221,9 @@ __global__ __launch_bounds__(64 * NW) void r1_fwd_kernel(Args<InT> p) {
     float hs[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) hs[k] = hin[k];
+    // this lane's y of step 0 of the chunk; step t is t * H * DL further
+    float* const ylane = yout + (((int64_t)b * p.L + (int64_t)(act ? c : 0) * p.T) * p.H + h) * p.DL + d;
+    const int64_t ystep = (int64_t)p.H * p.DL;
 #pragma unroll
     for (int t = 0; t < kMaxT; ++t) {
       if (t < p.T) {
@@ -235,8 +238,7 @@ __global__ __launch_bounds__(64 * NW) void r1_fwd_kernel(Args<InT> p) {
           yp += outc[k] * hs[k];
         }
         yp = ngroup_sum(yp);
-        if (act && dok && ng == (t & 3))
-          yout[(((int64_t)b * p.L + (int64_t)c * p.T + t) * p.H + h) * p.DL + d] = yp;
+        if (act && dok && ng == (t & 3)) ylane[t * ystep] = yp;
       }
     }
     if (act && dok) {
