@@ -515,6 +515,7 @@ def make_gdn(cfg, device, dtype):
         da=torch.empty((B, L, H), dtype=dtype, device=device),
         db=torch.empty((B, L, H), dtype=dtype, device=device),
         wsb=_lib.gdn_workspace(B, L, H, Dh, seg, dtype, device),
+        wsf=_lib.gdn_fwd_workspace(B, L, H, Dh, seg, dtype, device),
     )
     es = torch.tensor([], dtype=dtype).element_size()
     n_x, n_g, n_ck = B * L * H * Dh, B * L * H, B * H * nC * Dh * Dh
@@ -523,7 +524,7 @@ def make_gdn(cfg, device, dtype):
     bwd_bytes = n_x * 4 + n_ck * 4 + inputs + (3 * n_x + 2 * n_g) * es
 
     def fwd():
-        _lib.gdn_fwd(d["q"], d["k"], d["v"], d["alpha"], d["beta"], None, seg, out["y"], out["ckpt"])
+        _lib.gdn_fwd(d["q"], d["k"], d["v"], d["alpha"], d["beta"], None, seg, out["y"], out["ckpt"], out["wsf"])
 
     def bwd():
         _lib.gdn_bwd(d["dy"], None, d["q"], d["k"], d["v"], d["alpha"], d["beta"], None, out["ckpt"], seg,
@@ -578,7 +579,7 @@ WORKLOADS = {
                 dict(B=96, L=512, H=12, Dh=64, N=16, seg=32)),
     "gla_b96": ("gla_scan fwd+bwd (BASELINE config 2 shape, B = 96)", make_gla,
                 dict(B=96, L=512, H=12, Dh=64, seg=32)),
-    "gdn": ("gated_deltanet_scan fwd+bwd, sequential form (BASELINE config 2 shape)", make_gdn,
+    "gdn": ("gated_deltanet_scan fwd+bwd, chunkwise forward, sequential backward (BASELINE config 2 shape)", make_gdn,
             dict(B=3, L=512, H=12, Dh=64, seg=32)),
 }
 

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define RR_ABI_VERSION 10
+#define RR_ABI_VERSION 11
 
 enum rr_dtype { RR_F32 = 0, RR_BF16 = 1, RR_F16 = 2 };
 
@@ -289,11 +289,19 @@ int rr_rotlru_step(const void* a, const void* cs, const void* sn, const void* x,
  * aligned); h0 [B,H,Dh(i),Dh(j)] (nullable); y [B,L,H,Dh] fp32;
  * ckpt [B,H,L/T,Dh,Dh] fp32, the state after every T = rr_chunk_len(L, seg)
  * steps (the last is the final state).  Dh 32 or 64; T 8, 16 or 32 (seg a
- * multiple of 8).
+ * multiple of 8).  With bf16 inputs, Dh 64 and T 32 and a workspace of
+ * rr_gdn_fwd_workspace_bytes (16-byte aligned), the forward runs in the
+ * chunkwise-parallel (WY) form of the design's :139-238 (its Phase 3); with
+ * no workspace (NULL, 0), or for other shapes, in the sequential form.
  */
 int rr_gdn_fwd(const void* q, const void* k, const void* v, const void* alpha, const void* beta, int dtype,
                int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t seg, const float* h0, float* y, float* ckpt,
-               void* stream);
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of rr_gdn_fwd's chunkwise form (operand fragments of every
+ * chunk, 33 KB per chunk); 0 where the forward runs sequentially (no
+ * workspace needed) or for invalid arguments. */
+size_t rr_gdn_fwd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t seg, int dtype);
 
 /* Workspace bytes of rr_gdn_bwd (the adjoint at every checkpoint,
  * [B,H,L/T,Dh,Dh] fp32); 0 for invalid arguments. */

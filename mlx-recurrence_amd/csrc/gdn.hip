@@ -39,6 +39,7 @@
 //      through LDS, dalpha and dbeta over columns and waves likewise, in a
 //      fixed order (deterministic).
 #include "rr_common.h"
+#include "rr_internal.h"
 #include "rr_mfma.h"
 
 #include <string>
@@ -597,15 +598,27 @@ extern "C" size_t rr_gdn_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_
   return adj_bytes(B, L, H, Dh, seg);
 }
 
+extern "C" size_t rr_gdn_fwd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t seg, int dtype) {
+  if (check_gdn("gdn_fwd", B, L, H, Dh, seg, dtype) != RR_OK) return 0;
+  return rr::gdn_chunk_supported(dtype, Dh, rr::chunk_len(L, seg)) ? rr::gdn_chunk_ws_bytes(B, L, H) : 0;
+}
+
 extern "C" int rr_gdn_fwd(const void* q, const void* k, const void* v, const void* alpha, const void* beta, int dtype,
                           int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t seg, const float* h0, float* y,
-                          float* ckpt, void* stream) {
+                          float* ckpt, void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_gdn("gdn_fwd", B, L, H, Dh, seg, dtype)) return rc;
   if (!q || !k || !v || !alpha || !beta || !y || !ckpt) return rr::fail(RR_EINVAL, "gdn_fwd: null pointer argument");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v))
     return rr::fail(RR_EINVAL, "gdn_fwd: q, k and v must be 16-byte aligned");
   const int64_t T = rr::chunk_len(L, seg), nC = L / T;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (workspace != nullptr || workspace_bytes != 0) {   // the chunkwise form was asked for
+    if (!rr::gdn_chunk_supported(dtype, Dh, T))
+      return rr::fail(RR_EINVAL, "gdn_fwd: a workspace is only taken by the chunkwise form (bf16, Dh 64, T 32)");
+    if (workspace == nullptr || !aligned16(workspace) || workspace_bytes < rr::gdn_chunk_ws_bytes(B, L, H))
+      return rr::fail(RR_EWORKSPACE, "gdn_fwd: workspace smaller than rr_gdn_fwd_workspace_bytes or misaligned");
+    return rr::gdn_chunk_fwd(q, k, v, alpha, beta, B, L, H, h0, y, ckpt, workspace, s);
+  }
   RR_DISPATCH_DTYPE(dtype, {
     if (Dh == 64)
       hipLaunchKernelGGL((gdn_fwd_kernel<InT, 64>), dim3(col_grid(B * H, 64 / kCpw<64>)), dim3(64), 0, s,

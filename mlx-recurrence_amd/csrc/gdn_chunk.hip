@@ -1,0 +1,430 @@
+// gdn_chunk.hip — Gated DeltaNet forward in chunkwise-parallel (WY) form on
+// gfx950 MFMA: bf16 inputs, Dh = 64, checkpoint interval T = 32 (one chunk).
+//
+// Per (batch, head) and chunk of Q = 32 steps r (S_in the state entering it),
+// with lg_r = sum_{m <= r} log alpha_m, gam_r = exp(lg_r) and the decay ratios
+// R[r][c] = gam_r / gam_c = exp(lg_r - lg_c) <= 1 for c <= r, the recurrence
+// S_r = alpha_r (I - beta_r k_r k_r^T) S_{r-1} + beta_r k_r v_r^T
+// (docs/DESIGN_gated_deltanet.md:56-90 of the reference; its chunkwise
+// section :139-238 gives the structure, the weights below are derived here)
+// is, with u_r = S_r - alpha_r S_{r-1} + alpha_r beta_r k_r (k_r^T S_{r-1})
+// written as S_r = gam_r S_in + sum_{c <= r} R[r][c] k_c U[c]^T:
+//   (I + A) U = diag(beta) (V - diag(gam) K S_in),
+//   A[r][c] = beta_r R[r][c] (k_r . k_c)  (c < r; strictly lower),
+// so with T = (I + A)^-1 (unit lower triangular):
+//   U    = U0 - W S_in,   U0 = T diag(beta) V,   W = T diag(beta gam) K
+//   O    = diag(gam) Q S_in + P U,   P[r][c] = R[r][c] (q_r . k_c) (c <= r)
+//   S_out = gam_31 S_in + Kbar^T U,  Kbar[r] = (gam_31 / gam_r) k_r.
+// W, U0, P and Kbar need no state: kernel 1 forms them for every chunk at
+// once (one wave per chunk) and stores them as MFMA operand fragments; the
+// state then only crosses the chunks in kernel 2, one wave per (head,
+// 16 state columns j), which per chunk forms U (12 MFMAs), the output (14)
+// and the next state (12) with the state in accumulator registers.
+//
+// Fragments (v_mfma_f32_16x16x32_bf16): A[m][k] with lane (m, g) = (lane %
+// 16, lane / 16) holding k = 8 g + e, B[k][n] with lane (n, g) holding the
+// same k, D[4 g + r][n].  Kernel 2 feeds accumulators back as B operands: a
+// 32-row operand held as two 16-row accumulator blocks gives lane (n, g) the
+// rows pi(g, e) = e < 4 ? 4 g + e : 16 + 4 g + e - 4, so every A operand of
+// kernel 2 is packed by kernel 1 with its k index in that order (the product
+// sums over k, any order shared by A and B gives it).  fp32 operands are
+// split into bf16 hi + lo halves (three products), bf16 inputs are exact.
+#include "rr_common.h"
+#include "rr_internal.h"
+#include "rr_mfma.h"
+
+namespace {
+
+using rr::f32x4_t;
+using rr::u16x4_t;
+using rr::u16x8_t;
+
+constexpr int kQ = 32;      // steps per chunk (= checkpoint interval)
+constexpr int kD = 64;      // Dh
+constexpr int kXcd = 8;     // XCDs: a head's workgroups share one (and its L2)
+
+// One chunk's operand fragments (kernel 1 -> kernel 2), 16 bytes per lane.
+struct alignas(16) ChunkPack {
+  uint4 W[2][2][2][64];    // [rb][kb][hi, lo]: W[16 rb + m][32 kb + pi]
+  float4 U0[4][2][64];     // [slice][rb]: U0[16 rb + 4 g + r][16 slice + n] (accumulator layout)
+  uint4 Kb[4][2][64];      // [ib][hi, lo]: Kbar^T[16 ib + m][pi]
+  uint4 P[2][2][64];       // [rb][hi, lo]: P[16 rb + m][pi]
+  uint4 Qf[2][2][64];      // [rb][kb]: q[16 rb + m][32 kb + pi] (bf16, exact)
+  float gam[kQ];           // gam_r
+  float pad[kQ];
+};
+
+__device__ __forceinline__ int pi_k(int g, int e) { return e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4); }
+
+__device__ __forceinline__ uint4 as_u4(const u16x8_t& v) { return __builtin_bit_cast(uint4, v); }
+__device__ __forceinline__ u16x8_t as_u8(const uint4& v) { return __builtin_bit_cast(u16x8_t, v); }
+
+// 8 fp32 values -> bf16 hi and lo fragments.
+__device__ __forceinline__ void split8(const float (&x)[8], uint4& hi, uint4& lo) {
+  u16x8_t h, l;
+  rr::bf_split8(x, h, l);
+  hi = as_u4(h);
+  lo = as_u4(l);
+}
+
+__device__ __forceinline__ f32x4_t mfma(const u16x8_t& a, const u16x8_t& b, f32x4_t c) { return rr::mfma16(a, b, c); }
+
+// ------------------------------------------------------------------ kernel 1
+// LDS of one chunk's wave: inputs as bf16 rows (pitch 72: 16-byte aligned
+// rows; transposing reads need pitch % 4 == 0), fp32 matrices with padded rows.
+struct alignas(16) WySmem {
+  uint16_t k[kQ][72], v[kQ][72], q[kQ][72];
+  float a[kQ][36];     // A (strictly lower)
+  float t[kQ][36];     // T = (I + A)^-1
+  float x[16][20];     // A21 T11
+  float p[kQ][36];     // P
+  float w[kQ][68];     // W
+  float lg[kQ], gam[kQ], beta[kQ];
+};
+
+template <int ROWS>
+__device__ __forceinline__ void load_rows(uint16_t (*dst)[72], const uint16_t* src, int64_t row0, int64_t rs, int lane) {
+  // 32 rows x 64 bf16: 8 pieces of 16 bytes per row, 4 passes of 64 lanes
+#pragma unroll
+  for (int v = 0; v < ROWS * 8 / 64; ++v) {
+    const int i = lane + 64 * v, r = i >> 3, c8 = 8 * (i & 7);
+    *reinterpret_cast<uint4*>(&dst[r][c8]) = *reinterpret_cast<const uint4*>(src + (row0 + r) * rs + c8);
+  }
+}
+
+__global__ __launch_bounds__(64) void gdn_wy_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                                    const uint16_t* __restrict__ v, const uint16_t* __restrict__ alpha,
+                                                    const uint16_t* __restrict__ beta, ChunkPack* __restrict__ pack,
+                                                    int BH, int H, int L, int nC) {
+  __shared__ WySmem sm;
+  const int id = blockIdx.x, xcd = id % kXcd, kk = id / kXcd;
+  const int c = kk % nC, bh = (kk / nC) * kXcd + xcd;
+  if (bh >= BH) return;
+  const int b = bh / H, h = bh % H;
+  const int lane = threadIdx.x, l15 = lane & 15, g = lane >> 4, l31 = lane & 31;
+  const int64_t row0 = (int64_t)b * L + (int64_t)c * kQ;   // (b, t) row of step 0
+  // inputs [B, L, H, Dh]: the chunk's rows of this head
+  load_rows<kQ>(sm.k, k + (row0 * H + h) * kD, 0, (int64_t)H * kD, lane);
+  load_rows<kQ>(sm.v, v + (row0 * H + h) * kD, 0, (int64_t)H * kD, lane);
+  load_rows<kQ>(sm.q, q + (row0 * H + h) * kD, 0, (int64_t)H * kD, lane);
+  const float al = rr::bf_val(alpha[(row0 + l31) * H + h]), be = rr::bf_val(beta[(row0 + l31) * H + h]);
+  // lg_r = sum_{m <= r} log alpha_m (alpha = 0 taken as 1e-30: its products vanish)
+  const float lg = rr::prefix32_sum(__logf(fmaxf(al, 1e-30f)));
+  if (lane < kQ) {
+    sm.lg[lane] = lg;
+    sm.gam[lane] = __expf(lg);
+    sm.beta[lane] = be;
+  }
+  __syncthreads();
+
+  // G = K K^T and K Q^T ... Q K^T: 32 x 32 blocks, contraction over 64
+  f32x4_t G[2][2], QK[2][2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) G[rb][cb] = QK[rb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    u16x8_t ka[2], qa[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      ka[rb] = *reinterpret_cast<const u16x8_t*>(&sm.k[16 * rb + l15][32 * kb + 8 * g]);
+      qa[rb] = *reinterpret_cast<const u16x8_t*>(&sm.q[16 * rb + l15][32 * kb + 8 * g]);
+    }
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+        G[rb][cb] = mfma(ka[rb], ka[cb], G[rb][cb]);     // B[k][n] = K[16 cb + n][k]
+        QK[rb][cb] = mfma(qa[rb], ka[cb], QK[rb][cb]);
+      }
+  }
+  // A[r][c] = beta_r R[r][c] G[r][c] (c < r), P[r][c] = R[r][c] QK[r][c] (c <= r)
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * rb + 4 * g + r, col = 16 * cb + l15;
+        const bool low = col <= row;
+        const float rat = __expf(low ? sm.lg[row] - sm.lg[col] : 0.f);
+        sm.a[row][col] = col < row ? sm.beta[row] * rat * G[rb][cb][r] : 0.f;
+        sm.p[row][col] = low ? rat * QK[rb][cb][r] : 0.f;
+      }
+  __syncthreads();
+
+  // T = (I + A)^-1 by 16 x 16 blocks: the diagonal blocks by forward
+  // substitution (lanes 16 h + c: column c of block h; lanes 32-63 repeat
+  // 0-31), T[r][c] = (r == c) - sum_{m < r} A[r][m] T[m][c]; then
+  // T21 = -T22 (A21 T11)
+  {
+    const int hb = 16 * ((lane >> 4) & 1), cl = l15;
+    float tc[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float s0 = r == cl ? 1.f : 0.f, s1 = 0.f;
+#pragma unroll
+      for (int m = 0; m + 1 < r; m += 2) {
+        s0 -= sm.a[hb + r][hb + m] * tc[m];
+        s1 -= sm.a[hb + r][hb + m + 1] * tc[m + 1];
+      }
+      if (r & 1) s0 -= sm.a[hb + r][hb + r - 1] * tc[r - 1];
+      tc[r] = s0 + s1;
+    }
+    if (lane < kQ) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sm.t[hb + r][hb + cl] = tc[r];
+        sm.t[hb + r][16 - hb + cl] = 0.f;   // the upper block is zero; the lower is written below
+      }
+    }
+  }
+  __syncthreads();
+  {
+    // lane: column c = lane % 16 of rows 4 (lane / 16) + i of the 16 x 16 products
+    const int r0 = 4 * g;
+    float xs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const float tm = sm.t[m][l15];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xs[i] += sm.a[16 + r0 + i][m] * tm;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sm.x[r0 + i][l15] = xs[i];
+    __syncthreads();
+    float ts[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const float xm = sm.x[m][l15];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ts[i] -= sm.t[16 + r0 + i][16 + m] * xm;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sm.t[16 + r0 + i][l15] = ts[i];
+  }
+  __syncthreads();
+
+  // W = T diag(beta gam) K, U0 = T diag(beta) V: A operand T rows (k = c),
+  // column factors applied before the split; B operands by transposing reads
+  ChunkPack& pk = pack[(int64_t)bh * nC + c];
+  {
+    u16x8_t tw[2][2], tu[2][2];   // [rb][hi, lo]
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const float4 t0 = *reinterpret_cast<const float4*>(&sm.t[16 * rb + l15][8 * g]);
+      const float4 t1 = *reinterpret_cast<const float4*>(&sm.t[16 * rb + l15][8 * g + 4]);
+      const float tv[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
+      float xw[8], xu[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int cc = 8 * g + e;
+        xu[e] = tv[e] * sm.beta[cc];
+        xw[e] = xu[e] * sm.gam[cc];
+      }
+      rr::bf_split8(xw, tw[rb][0], tw[rb][1]);
+      rr::bf_split8(xu, tu[rb][0], tu[rb][1]);
+    }
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const u16x8_t kf = rr::frag_tr(&sm.k[0][16 * nb], 72, lane);   // K[8 g + e][16 nb + n]
+      const u16x8_t vf = rr::frag_tr(&sm.v[0][16 * nb], 72, lane);
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        f32x4_t w = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+        w = mfma(tw[rb][0], kf, w);
+        w = mfma(tw[rb][1], kf, w);
+        u = mfma(tu[rb][0], vf, u);
+        u = mfma(tu[rb][1], vf, u);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sm.w[16 * rb + 4 * g + r][16 * nb + l15] = w[r];
+        pk.U0[nb][rb][lane] = make_float4(u[0], u[1], u[2], u[3]);   // slice nb, accumulator layout
+      }
+    }
+  }
+  __syncthreads();
+
+  // packed A operands of kernel 2 (k in pi order)
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int row = 16 * rb + l15;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const float4 w0 = *reinterpret_cast<const float4*>(&sm.w[row][32 * kb + 4 * g]);
+      const float4 w1 = *reinterpret_cast<const float4*>(&sm.w[row][32 * kb + 16 + 4 * g]);
+      const float x[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+      split8(x, pk.W[rb][kb][0][lane], pk.W[rb][kb][1][lane]);
+      const uint2 q0 = *reinterpret_cast<const uint2*>(&sm.q[row][32 * kb + 4 * g]);
+      const uint2 q1 = *reinterpret_cast<const uint2*>(&sm.q[row][32 * kb + 16 + 4 * g]);
+      pk.Qf[rb][kb][lane] = make_uint4(q0.x, q0.y, q1.x, q1.y);
+    }
+    const float4 p0 = *reinterpret_cast<const float4*>(&sm.p[row][4 * g]);
+    const float4 p1 = *reinterpret_cast<const float4*>(&sm.p[row][16 + 4 * g]);
+    const float x[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+    split8(x, pk.P[rb][0][lane], pk.P[rb][1][lane]);
+  }
+  {
+    // Kbar^T[16 ib + m][t] = (gam_31 / gam_t) k_t[16 ib + m], t = pi(g, e)
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = __expf(sm.lg[kQ - 1] - sm.lg[pi_k(g, e)]);
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+      const u16x4_t lo = rr::frag4_tr(&sm.k[0][16 * ib], 72, lane);    // K[4 g + e][16 ib + m]
+      const u16x4_t hi = rr::frag4_tr(&sm.k[16][16 * ib], 72, lane);   // K[16 + 4 g + e][..]
+      const float x[8] = {f[0] * rr::bf_val(lo[0]), f[1] * rr::bf_val(lo[1]), f[2] * rr::bf_val(lo[2]),
+                          f[3] * rr::bf_val(lo[3]), f[4] * rr::bf_val(hi[0]), f[5] * rr::bf_val(hi[1]),
+                          f[6] * rr::bf_val(hi[2]), f[7] * rr::bf_val(hi[3])};
+      split8(x, pk.Kb[ib][0][lane], pk.Kb[ib][1][lane]);
+    }
+  }
+  if (lane < kQ) pk.gam[lane] = sm.gam[lane];
+}
+
+// ------------------------------------------------------------------ kernel 2
+// One wave per (head, 16 state columns j = 16 s + n): the state block
+// S[0..63][16 s .. 16 s + 15] as four 16-row accumulator blocks, carried
+// through the chunks in order.  Per chunk: U = U0 - W S_in, the output
+// O = diag(gam) Q S_in + P U, then S_out = gam_31 S_in + Kbar^T U, written as
+// the chunk's checkpoint.
+struct Frags {
+  uint4 W[2][2][2], Kb[4][2], P[2][2], Qf[2][2];
+  float4 U0[2], gam[2];
+  float gend;
+};
+
+__device__ __forceinline__ void load_frags(Frags& f, const ChunkPack& pk, int s, int lane) {
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      f.W[rb][kb][0] = pk.W[rb][kb][0][lane];
+      f.W[rb][kb][1] = pk.W[rb][kb][1][lane];
+      f.Qf[rb][kb] = pk.Qf[rb][kb][lane];
+    }
+    f.P[rb][0] = pk.P[rb][0][lane];
+    f.P[rb][1] = pk.P[rb][1][lane];
+    f.U0[rb] = pk.U0[s][rb][lane];
+    f.gam[rb] = *reinterpret_cast<const float4*>(&pk.gam[16 * rb + 4 * (lane >> 4)]);
+  }
+#pragma unroll
+  for (int ib = 0; ib < 4; ++ib) {
+    f.Kb[ib][0] = pk.Kb[ib][0][lane];
+    f.Kb[ib][1] = pk.Kb[ib][1][lane];
+  }
+  f.gend = pk.gam[kQ - 1];
+}
+
+// Two 16-row accumulator blocks -> bf16 hi / lo B-operand fragments (k = pi).
+__device__ __forceinline__ void split_pair(const f32x4_t& a0, const f32x4_t& a1, u16x8_t& hi, u16x8_t& lo) {
+  const float x[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+  rr::bf_split8(x, hi, lo);
+}
+
+__global__ __launch_bounds__(64) void gdn_state_kernel(const ChunkPack* __restrict__ pack, const float* __restrict__ h0,
+                                                       float* __restrict__ y, float* __restrict__ ckpt, int BH, int H,
+                                                       int L, int nC) {
+  const int id = blockIdx.x, xcd = id % kXcd, kk = id / kXcd;
+  const int s = kk & 3, bh = (kk >> 2) * kXcd + xcd;
+  if (bh >= BH) return;
+  const int b = bh / H, h = bh % H;
+  const int lane = threadIdx.x, n = lane & 15, g = lane >> 4;
+  const int j = 16 * s + n;
+  f32x4_t S[4];
+#pragma unroll
+  for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      S[ib][r] = h0 != nullptr ? h0[((int64_t)bh * kD + 16 * ib + 4 * g + r) * kD + j] : 0.f;
+  const ChunkPack* pk = pack + (int64_t)bh * nC;
+  Frags f;
+  load_frags(f, pk[0], s, lane);
+  for (int c = 0; c < nC; ++c) {
+    // the state as B operands of its two 32-row k blocks
+    u16x8_t sh[2], sl[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) split_pair(S[2 * kb], S[2 * kb + 1], sh[kb], sl[kb]);
+    // U = U0 - W S_in
+    f32x4_t U[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      f32x4_t a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        a = mfma(as_u8(f.W[rb][kb][0]), sh[kb], a);
+        a = mfma(as_u8(f.W[rb][kb][0]), sl[kb], a);
+        a = mfma(as_u8(f.W[rb][kb][1]), sh[kb], a);
+      }
+      const float4 u0 = f.U0[rb];
+      U[rb] = f32x4_t{u0.x - a[0], u0.y - a[1], u0.z - a[2], u0.w - a[3]};
+    }
+    u16x8_t uh, ul;
+    split_pair(U[0], U[1], uh, ul);
+    // O = diag(gam) Q S_in + P U
+    f32x4_t O[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      f32x4_t a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        a = mfma(as_u8(f.Qf[rb][kb]), sh[kb], a);
+        a = mfma(as_u8(f.Qf[rb][kb]), sl[kb], a);
+      }
+      const float4 gm = f.gam[rb];
+      a = f32x4_t{gm.x * a[0], gm.y * a[1], gm.z * a[2], gm.w * a[3]};
+      a = mfma(as_u8(f.P[rb][0]), uh, a);
+      a = mfma(as_u8(f.P[rb][0]), ul, a);
+      a = mfma(as_u8(f.P[rb][1]), uh, a);
+      O[rb] = a;
+    }
+    // S_out = gam_31 S_in + Kbar^T U
+    const float gend = f.gend;
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+      f32x4_t a = {gend * S[ib][0], gend * S[ib][1], gend * S[ib][2], gend * S[ib][3]};
+      a = mfma(as_u8(f.Kb[ib][0]), uh, a);
+      a = mfma(as_u8(f.Kb[ib][0]), ul, a);
+      a = mfma(as_u8(f.Kb[ib][1]), uh, a);
+      S[ib] = a;
+    }
+    // the next chunk's fragments go out before this chunk's stores
+    if (c + 1 < nC) load_frags(f, pk[c + 1], s, lane);
+    const int64_t row0 = (int64_t)b * L + (int64_t)c * kQ;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) y[((row0 + 16 * rb + 4 * g + r) * H + h) * kD + j] = O[rb][r];
+    float* ck = ckpt + ((int64_t)bh * nC + c) * kD * kD;
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ck[(16 * ib + 4 * g + r) * kD + j] = S[ib][r];
+  }
+}
+
+}  // namespace
+
+namespace rr {
+
+bool gdn_chunk_supported(int dtype, int64_t Dh, int64_t T) { return dtype == RR_BF16 && Dh == kD && T == kQ; }
+
+size_t gdn_chunk_ws_bytes(int64_t B, int64_t L, int64_t H) {
+  return (size_t)(B * H) * (size_t)(L / kQ) * sizeof(ChunkPack);
+}
+
+int gdn_chunk_fwd(const void* q, const void* k, const void* v, const void* alpha, const void* beta, int64_t B,
+                  int64_t L, int64_t H, const float* h0, float* y, float* ckpt, void* workspace, hipStream_t s) {
+  const int64_t BH = B * H, nC = L / kQ, groups = (BH + kXcd - 1) / kXcd;
+  ChunkPack* pack = static_cast<ChunkPack*>(workspace);
+  hipLaunchKernelGGL(gdn_wy_kernel, dim3((unsigned)(groups * kXcd * nC)), dim3(64), 0, s,
+                     static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                     static_cast<const uint16_t*>(alpha), static_cast<const uint16_t*>(beta), pack, (int)BH, (int)H,
+                     (int)L, (int)nC);
+  if (int rc = check_launch("gdn chunked forward (WY)")) return rc;
+  hipLaunchKernelGGL(gdn_state_kernel, dim3((unsigned)(groups * kXcd * 4)), dim3(64), 0, s, pack, h0, y, ckpt,
+                     (int)BH, (int)H, (int)L, (int)nC);
+  return check_launch("gdn chunked forward (state)");
+}
+
+}  // namespace rr

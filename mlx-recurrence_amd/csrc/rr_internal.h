@@ -83,6 +83,13 @@ int gla2_bwd(const ChunkArgs& p, int64_t B, hipStream_t s);
 bool res_fwd_supported(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N);
 int res_fwd(const ChunkArgs& p, int64_t B, hipStream_t s, bool gla);
 
+// Gated DeltaNet forward in chunkwise (WY) form (gdn_chunk.hip): bf16, Dh 64,
+// checkpoint interval 32; the workspace holds every chunk's operand fragments.
+bool gdn_chunk_supported(int dtype, int64_t Dh, int64_t T);
+size_t gdn_chunk_ws_bytes(int64_t B, int64_t L, int64_t H);
+int gdn_chunk_fwd(const void* q, const void* k, const void* v, const void* alpha, const void* beta, int64_t B,
+                  int64_t L, int64_t H, const float* h0, float* y, float* ckpt, void* workspace, hipStream_t s);
+
 // Backward of the chunked kernels with column-owned state blocks (GLA: Dh in
 // {32, 64, 128}; SSD: Dh in {32, 64, 128}, N in {64, 128}; chunked_bwd.hip).  SSD
 // leaves per-run dA partials in p.ws for the caller's reduction.

@@ -63,7 +63,8 @@ _SIGS = {
     "rr_gla_step": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 3 + [_c_ptr] * 3),
     "rr_rglru_step": (_c_int, [_c_ptr] * 2 + [_c_int] + [_c_i64] * 2 + [_c_ptr] * 3),
     "rr_rotlru_step": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 2 + [_c_ptr] * 3),
-    "rr_gdn_fwd": (_c_int, [_c_ptr] * 5 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 4),
+    "rr_gdn_fwd": (_c_int, [_c_ptr] * 5 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
+    "rr_gdn_fwd_workspace_bytes": (_c_size, [_c_i64] * 5 + [_c_int]),
     "rr_gdn_workspace_bytes": (_c_size, [_c_i64] * 5 + [_c_int]),
     "rr_gdn_bwd": (_c_int, [_c_ptr] * 7 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 9 + [_c_size, _c_ptr]),
 }
@@ -411,10 +412,16 @@ def rotlru_step(a, cs, sn, x, state, y):
 
 
 # ---------------------------------------------------------------- Gated DeltaNet
-def gdn_fwd(q, k, v, alpha, beta, h0, seg, y, ckpt):
+def gdn_fwd(q, k, v, alpha, beta, h0, seg, y, ckpt, ws=None):
+    """ws: gdn_fwd_workspace(...) for the chunkwise form (None: sequential)."""
     B, L, H, Dh = q.shape
     _check(load().rr_gdn_fwd(ptr(q), ptr(k), ptr(v), ptr(alpha), ptr(beta), DTYPE_CODE[q.dtype], B, L, H, Dh, seg,
-                             ptr(h0), ptr(y), ptr(ckpt), stream_of(q)), "rr_gdn_fwd")
+                             ptr(h0), ptr(y), ptr(ckpt), ptr(ws), 0 if ws is None else ws.numel(), stream_of(q)),
+           "rr_gdn_fwd")
+
+
+def gdn_fwd_workspace(B, L, H, Dh, seg, dtype, device) -> torch.Tensor | None:
+    return _alloc_ws(_ws_bytes("rr_gdn_fwd_workspace_bytes", (B, L, H, Dh, seg, DTYPE_CODE[dtype])), device)
 
 
 def gdn_workspace(B, L, H, Dh, seg, dtype, device) -> torch.Tensor | None:

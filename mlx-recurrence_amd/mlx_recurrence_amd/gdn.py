@@ -54,7 +54,8 @@ class _GDNScan(torch.autograd.Function):
         y = torch.empty((B, L, H, Dh), dtype=torch.float32, device=dev)
         ckpt = torch.empty((B, H, nC, Dh, Dh), dtype=torch.float32, device=dev)
         with _lib.device_guard(dev):
-            _lib.gdn_fwd(q_, k_, v_, a_, b_, h0_, seg, y, ckpt)
+            ws = _lib.gdn_fwd_workspace(B, L, H, Dh, seg, q_.dtype, dev)
+            _lib.gdn_fwd(q_, k_, v_, a_, b_, h0_, seg, y, ckpt, ws)
         ctx.save_for_backward(q_, k_, v_, a_, b_, h0_, ckpt)
         ctx.seg = seg
         ctx.set_materialize_grads(False)

@@ -33,7 +33,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.rr_abi_version() == 10
+    assert lib.rr_abi_version() == 11
 
 
 @pytest.mark.parametrize("L,seg,T", [(512, 32, 32), (96, 16, 16), (128, 64, 32), (96, 48, 16),
@@ -98,13 +98,13 @@ def test_gdn_validation(lib):
     """Gated DeltaNet entry points: shape rules and the kernels' Dh / interval
     limits are reported before any launch."""
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
-    rc = lib.rr_gdn_fwd(p, p, p, p, p, 0, 1, 30, 2, 64, 32, None, p, p, None)
+    rc = lib.rr_gdn_fwd(p, p, p, p, p, 0, 1, 30, 2, 64, 32, None, p, p, None, 0, None)
     assert rc == _lib.RR_EINVAL and b"L=30" in lib.rr_last_error()
-    rc = lib.rr_gdn_fwd(p, p, p, p, p, 0, 1, 64, 2, 128, 32, None, p, p, None)
+    rc = lib.rr_gdn_fwd(p, p, p, p, p, 0, 1, 64, 2, 128, 32, None, p, p, None, 0, None)
     assert rc == _lib.RR_EUNSUPPORTED and b"Dh must be 32 or 64" in lib.rr_last_error()
-    rc = lib.rr_gdn_fwd(p, p, p, p, p, 0, 1, 12, 2, 64, 4, None, p, p, None)
+    rc = lib.rr_gdn_fwd(p, p, p, p, p, 0, 1, 12, 2, 64, 4, None, p, p, None, 0, None)
     assert rc == _lib.RR_EUNSUPPORTED and b"multiple of 8" in lib.rr_last_error()
-    rc = lib.rr_gdn_fwd(p, p, p, p, None, 0, 1, 64, 2, 64, 32, None, p, p, None)
+    rc = lib.rr_gdn_fwd(p, p, p, p, None, 0, 1, 64, 2, 64, 32, None, p, p, None, 0, None)
     assert rc == _lib.RR_EINVAL and b"null pointer" in lib.rr_last_error()
     rc = lib.rr_gdn_bwd(p, None, p, p, p, p, p, 0, 1, 64, 2, 64, 32, None, p, p, p, None, p, p, None, p, 1 << 30,
                         None)
@@ -114,5 +114,18 @@ def test_gdn_validation(lib):
     rc = lib.rr_gdn_bwd(p, None, p, p, p, p, p, 0, 1, 64, 2, 64, 32, None, p, p, p, p, p, p, None, p, need - 1, None)
     assert rc == _lib.RR_EWORKSPACE
     q_odd = ctypes.c_void_p(24)
-    rc = lib.rr_gdn_fwd(q_odd, p, p, p, p, 0, 1, 64, 2, 64, 32, None, p, p, None)
+    rc = lib.rr_gdn_fwd(q_odd, p, p, p, p, 0, 1, 64, 2, 64, 32, None, p, p, None, 0, None)
     assert rc == _lib.RR_EINVAL and b"16-byte aligned" in lib.rr_last_error()
+    # the chunkwise forward's workspace: bf16, Dh 64, T 32 only (one pack per chunk)
+    fneed = lib.rr_gdn_fwd_workspace_bytes(2, 64, 3, 64, 32, 1)
+    assert fneed > 0 and fneed % (2 * 3 * 2) == 0
+    assert lib.rr_gdn_fwd_workspace_bytes(2, 64, 3, 64, 32, 0) == 0     # fp32: sequential
+    assert lib.rr_gdn_fwd_workspace_bytes(2, 64, 3, 32, 32, 1) == 0     # Dh 32
+    assert lib.rr_gdn_fwd_workspace_bytes(2, 64, 3, 64, 16, 1) == 0     # T 16
+    assert lib.rr_gdn_fwd_workspace_bytes(2, 30, 3, 64, 32, 1) == 0     # invalid L
+    rc = lib.rr_gdn_fwd(p, p, p, p, p, 1, 2, 64, 3, 64, 32, None, p, p, p, fneed - 1, None)
+    assert rc == _lib.RR_EWORKSPACE
+    rc = lib.rr_gdn_fwd(p, p, p, p, p, 1, 2, 64, 3, 64, 32, None, p, p, ctypes.c_void_p(24), fneed, None)
+    assert rc == _lib.RR_EWORKSPACE and b"misaligned" in lib.rr_last_error()
+    rc = lib.rr_gdn_fwd(p, p, p, p, p, 0, 2, 64, 3, 64, 32, None, p, p, p, 1 << 30, None)
+    assert rc == _lib.RR_EINVAL and b"chunkwise form" in lib.rr_last_error()

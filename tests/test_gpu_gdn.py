@@ -132,3 +132,34 @@ def test_gdn_deterministic():
         outs.append([y.detach(), fs.detach()] + [t.grad for t in ts])
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("B,L,H,dist,h0,seed", [(3, 512, 12, "plain", True, 60), (2, 96, 3, "edges", True, 61),
+                                                  (1, 32, 2, "plain", False, 62)])
+def test_gdn_chunkwise_forward_matches_sequential(B, L, H, dist, h0, seed):
+    """The chunkwise (WY) forward (bf16, Dh 64, T 32, with its workspace)
+    against the sequential forward (no workspace) on the same inputs through
+    the C ABI: y and every checkpoint, at fp32 accuracy (the chunkwise
+    products split fp32 operands into bf16 halves: about 1e-6); both are
+    checked against the float64 oracle by the parity cases above."""
+    from mlx_recurrence_amd import _lib
+    Dh, seg = 64, 32
+    _announce("gdn_chunkwise", B=B, L=L, H=H, dist=dist, h0=h0, seed=seed)
+    rng = np.random.default_rng(seed)
+    q, k, v, a, b = (to_dev(t, BF16) for t in _inputs(rng, B, L, H, Dh, dist))
+    h0t = to_dev(rng.standard_normal((B, H, Dh, Dh)) * 0.5, F32) if h0 else None
+    nC = L // 32
+    ws = _lib.gdn_fwd_workspace(B, L, H, Dh, seg, BF16, q.device)
+    assert ws is not None
+    res = []
+    for w in (None, ws):
+        y = torch.full((B, L, H, Dh), float("nan"), dtype=F32, device=q.device)
+        ck = torch.full((B, H, nC, Dh, Dh), float("nan"), dtype=F32, device=q.device)
+        _lib.gdn_fwd(q, k, v, a, b, h0t, seg, y, ck, w)
+        torch.cuda.synchronize()
+        res.append((y, ck))
+    (ys, cs), (yc, cc) = res
+    ey = ((yc - ys).abs().max() / ys.abs().max()).item()
+    ec = ((cc - cs).abs().max() / cs.abs().max()).item()
+    print({"y": ey, "ckpt": ec}, flush=True)
+    assert np.isfinite(ey) and ey < 2e-5 and np.isfinite(ec) and ec < 2e-5
