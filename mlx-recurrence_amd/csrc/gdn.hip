@@ -564,6 +564,16 @@ size_t adj_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t seg) {
   return (size_t)(B * H * (L / rr::chunk_len(L, seg)) * Dh * Dh) * sizeof(float);
 }
 
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// The backward's workspace: the adjoint checkpoints, then (chunkwise adjoint
+// pass) every chunk's fragments.
+size_t bwd_ws_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t seg, int dtype) {
+  const size_t n = adj_bytes(B, L, H, Dh, seg);
+  return rr::gdn_chunk_supported(dtype, Dh, rr::chunk_len(L, seg)) ? align256(n) + rr::gdn_chunk_bwd_ws_bytes(B, L, H)
+                                                                    : n;
+}
+
 template <typename InT, int DH, int T>
 void launch_grad_t(const float* dy, const void* q, const void* k, const void* v, const void* alpha, const void* beta,
                    const float* h0, const float* ckpt, const float* adjck, void* dq, void* dk, void* dv, void* dalpha,
@@ -595,7 +605,7 @@ void launch_bwd_dh(int64_t T, const float* dy, const float* dfinal, const void* 
 
 extern "C" size_t rr_gdn_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t seg, int dtype) {
   if (B <= 0 || L <= 0 || H <= 0 || Dh <= 0 || rr::chunk_len(L, seg) == 0 || !rr::valid_dtype(dtype)) return 0;
-  return adj_bytes(B, L, H, Dh, seg);
+  return bwd_ws_bytes(B, L, H, Dh, seg, dtype);
 }
 
 extern "C" size_t rr_gdn_fwd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t seg, int dtype) {
@@ -644,13 +654,22 @@ extern "C" int rr_gdn_bwd(const float* dy, const float* dfinal, const void* q, c
     return rr::fail(RR_EINVAL, "gdn_bwd: null pointer argument");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dy))
     return rr::fail(RR_EINVAL, "gdn_bwd: q, k, v and dy must be 16-byte aligned");
-  if (!workspace || workspace_bytes < adj_bytes(B, L, H, Dh, seg))
+  if (!workspace || workspace_bytes < bwd_ws_bytes(B, L, H, Dh, seg, dtype))
     return rr::fail(RR_EWORKSPACE, "gdn_bwd: workspace too small");
   const int64_t T = rr::chunk_len(L, seg), nC = L / T;
   hipStream_t s = static_cast<hipStream_t>(stream);
   float* adjck = static_cast<float*>(workspace);
+  // bf16, Dh 64, T 32: the adjoint pass in chunkwise form, then the same
+  // interval-parallel gradient pass
+  const bool chunked = rr::gdn_chunk_supported(dtype, Dh, T);
+  if (chunked && !aligned16(workspace)) return rr::fail(RR_EWORKSPACE, "gdn_bwd: workspace must be 16-byte aligned");
   RR_DISPATCH_DTYPE(dtype, {
-    if (Dh == 64)
+    if (chunked) {
+      void* packs = static_cast<char*>(workspace) + align256(adj_bytes(B, L, H, Dh, seg));
+      if (int rc = rr::gdn_chunk_adjoint(q, k, v, alpha, beta, dy, dfinal, B, L, H, adjck, dh0, packs, s)) return rc;
+      launch_grad_t<InT, 64, 32>(dy, q, k, v, alpha, beta, h0, ckpt, adjck, dq, dk, dv, dalpha, dbeta, B, H, L, nC,
+                                 s);
+    } else if (Dh == 64)
       launch_bwd_dh<InT, 64>(T, dy, dfinal, q, k, v, alpha, beta, h0, ckpt, adjck, dq, dk, dv, dalpha, dbeta, dh0, B,
                              H, L, nC, s);
     else

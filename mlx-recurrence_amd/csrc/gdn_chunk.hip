@@ -54,6 +54,19 @@ struct alignas(16) ChunkPack {
   float pad[kQ];
 };
 
+// The backward's fragments of a chunk (kernel 1 in its backward mode ->
+// the reverse state pass): the transposed products of the adjoint
+//   dU = P^T dO + Kbar dS_out,
+//   dS_in = gam_31 dS_out + (diag(gam) Q)^T dO - W^T dU.
+struct alignas(16) BwdPack {
+  uint4 Pt[2][2][64];      // [rb][hi, lo]: P^T[16 rb + m][pi] = P[pi][16 rb + m]
+  uint4 Kb[2][2][2][64];   // [rb][kb][hi, lo]: Kbar[16 rb + m][32 kb + pi]
+  uint4 Qg[4][2][64];      // [ib][hi, lo]: gam_pi q_pi[16 ib + m]
+  uint4 Wn[4][2][64];      // [ib][hi, lo]: -W[pi][16 ib + m]
+  float gend;
+  float pad[63];
+};
+
 __device__ __forceinline__ int pi_k(int g, int e) { return e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4); }
 
 __device__ __forceinline__ uint4 as_u4(const u16x8_t& v) { return __builtin_bit_cast(uint4, v); }
@@ -92,9 +105,11 @@ __device__ __forceinline__ void load_rows(uint16_t (*dst)[72], const uint16_t* s
   }
 }
 
+// BWD: the backward's fragments (BwdPack) instead of the forward's.
+template <bool BWD>
 __global__ __launch_bounds__(64) void gdn_wy_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                     const uint16_t* __restrict__ v, const uint16_t* __restrict__ alpha,
-                                                    const uint16_t* __restrict__ beta, ChunkPack* __restrict__ pack,
+                                                    const uint16_t* __restrict__ beta, void* __restrict__ packs,
                                                     int BH, int H, int L, int nC) {
   __shared__ WySmem sm;
   const int id = blockIdx.x, xcd = id % kXcd, kk = id / kXcd;
@@ -208,7 +223,8 @@ __global__ __launch_bounds__(64) void gdn_wy_kernel(const uint16_t* __restrict__
 
   // W = T diag(beta gam) K, U0 = T diag(beta) V: A operand T rows (k = c),
   // column factors applied before the split; B operands by transposing reads
-  ChunkPack& pk = pack[(int64_t)bh * nC + c];
+  ChunkPack& pk = static_cast<ChunkPack*>(packs)[(int64_t)bh * nC + c];
+  BwdPack& bp = static_cast<BwdPack*>(packs)[(int64_t)bh * nC + c];
   {
     u16x8_t tw[2][2], tu[2][2];   // [rb][hi, lo]
 #pragma unroll
@@ -232,54 +248,96 @@ __global__ __launch_bounds__(64) void gdn_wy_kernel(const uint16_t* __restrict__
       const u16x8_t vf = rr::frag_tr(&sm.v[0][16 * nb], 72, lane);
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
-        f32x4_t w = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+        f32x4_t w = {0.f, 0.f, 0.f, 0.f};
         w = mfma(tw[rb][0], kf, w);
         w = mfma(tw[rb][1], kf, w);
-        u = mfma(tu[rb][0], vf, u);
-        u = mfma(tu[rb][1], vf, u);
 #pragma unroll
         for (int r = 0; r < 4; ++r) sm.w[16 * rb + 4 * g + r][16 * nb + l15] = w[r];
-        pk.U0[nb][rb][lane] = make_float4(u[0], u[1], u[2], u[3]);   // slice nb, accumulator layout
+        if constexpr (!BWD) {
+          f32x4_t u = {0.f, 0.f, 0.f, 0.f};
+          u = mfma(tu[rb][0], vf, u);
+          u = mfma(tu[rb][1], vf, u);
+          pk.U0[nb][rb][lane] = make_float4(u[0], u[1], u[2], u[3]);   // slice nb, accumulator layout
+        }
       }
     }
   }
   __syncthreads();
 
-  // packed A operands of kernel 2 (k in pi order)
+  if constexpr (BWD) {
+    // packed A operands of the reverse state pass (k in pi order)
+    float gp[8];   // gam_t, t = pi(g, e)
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int row = 16 * rb + l15;
+    for (int e = 0; e < 8; ++e) gp[e] = sm.gam[pi_k(g, e)];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const float4 w0 = *reinterpret_cast<const float4*>(&sm.w[row][32 * kb + 4 * g]);
-      const float4 w1 = *reinterpret_cast<const float4*>(&sm.w[row][32 * kb + 16 + 4 * g]);
-      const float x[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-      split8(x, pk.W[rb][kb][0][lane], pk.W[rb][kb][1][lane]);
-      const uint2 q0 = *reinterpret_cast<const uint2*>(&sm.q[row][32 * kb + 4 * g]);
-      const uint2 q1 = *reinterpret_cast<const uint2*>(&sm.q[row][32 * kb + 16 + 4 * g]);
-      pk.Qf[rb][kb][lane] = make_uint4(q0.x, q0.y, q1.x, q1.y);
+    for (int rb = 0; rb < 2; ++rb) {
+      const int row = 16 * rb + l15;
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = sm.p[pi_k(g, e)][row];
+      split8(x, bp.Pt[rb][0][lane], bp.Pt[rb][1][lane]);
+      const float fr = __expf(sm.lg[kQ - 1] - sm.lg[row]);   // Kbar row factor
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const u16x4_t k0 = *reinterpret_cast<const u16x4_t*>(&sm.k[row][32 * kb + 4 * g]);
+        const u16x4_t k1 = *reinterpret_cast<const u16x4_t*>(&sm.k[row][32 * kb + 16 + 4 * g]);
+        const float y[8] = {fr * rr::bf_val(k0[0]), fr * rr::bf_val(k0[1]), fr * rr::bf_val(k0[2]),
+                            fr * rr::bf_val(k0[3]), fr * rr::bf_val(k1[0]), fr * rr::bf_val(k1[1]),
+                            fr * rr::bf_val(k1[2]), fr * rr::bf_val(k1[3])};
+        split8(y, bp.Kb[rb][kb][0][lane], bp.Kb[rb][kb][1][lane]);
+      }
     }
-    const float4 p0 = *reinterpret_cast<const float4*>(&sm.p[row][4 * g]);
-    const float4 p1 = *reinterpret_cast<const float4*>(&sm.p[row][16 + 4 * g]);
-    const float x[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-    split8(x, pk.P[rb][0][lane], pk.P[rb][1][lane]);
-  }
-  {
-    // Kbar^T[16 ib + m][t] = (gam_31 / gam_t) k_t[16 ib + m], t = pi(g, e)
-    float f[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = __expf(sm.lg[kQ - 1] - sm.lg[pi_k(g, e)]);
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib) {
-      const u16x4_t lo = rr::frag4_tr(&sm.k[0][16 * ib], 72, lane);    // K[4 g + e][16 ib + m]
-      const u16x4_t hi = rr::frag4_tr(&sm.k[16][16 * ib], 72, lane);   // K[16 + 4 g + e][..]
-      const float x[8] = {f[0] * rr::bf_val(lo[0]), f[1] * rr::bf_val(lo[1]), f[2] * rr::bf_val(lo[2]),
-                          f[3] * rr::bf_val(lo[3]), f[4] * rr::bf_val(hi[0]), f[5] * rr::bf_val(hi[1]),
-                          f[6] * rr::bf_val(hi[2]), f[7] * rr::bf_val(hi[3])};
-      split8(x, pk.Kb[ib][0][lane], pk.Kb[ib][1][lane]);
+      const u16x4_t lo = rr::frag4_tr(&sm.q[0][16 * ib], 72, lane);    // q[4 g + e][16 ib + m]
+      const u16x4_t hi = rr::frag4_tr(&sm.q[16][16 * ib], 72, lane);   // q[16 + 4 g + e][..]
+      const float x[8] = {gp[0] * rr::bf_val(lo[0]), gp[1] * rr::bf_val(lo[1]), gp[2] * rr::bf_val(lo[2]),
+                          gp[3] * rr::bf_val(lo[3]), gp[4] * rr::bf_val(hi[0]), gp[5] * rr::bf_val(hi[1]),
+                          gp[6] * rr::bf_val(hi[2]), gp[7] * rr::bf_val(hi[3])};
+      split8(x, bp.Qg[ib][0][lane], bp.Qg[ib][1][lane]);
+      float w[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w[e] = -sm.w[pi_k(g, e)][16 * ib + l15];
+      split8(w, bp.Wn[ib][0][lane], bp.Wn[ib][1][lane]);
     }
-  }
-  if (lane < kQ) pk.gam[lane] = sm.gam[lane];
+    if (lane == 0) bp.gend = sm.gam[kQ - 1];
+  } else {
+    // packed A operands of kernel 2 (k in pi order)
+  #pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int row = 16 * rb + l15;
+  #pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const float4 w0 = *reinterpret_cast<const float4*>(&sm.w[row][32 * kb + 4 * g]);
+        const float4 w1 = *reinterpret_cast<const float4*>(&sm.w[row][32 * kb + 16 + 4 * g]);
+        const float x[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        split8(x, pk.W[rb][kb][0][lane], pk.W[rb][kb][1][lane]);
+        const uint2 q0 = *reinterpret_cast<const uint2*>(&sm.q[row][32 * kb + 4 * g]);
+        const uint2 q1 = *reinterpret_cast<const uint2*>(&sm.q[row][32 * kb + 16 + 4 * g]);
+        pk.Qf[rb][kb][lane] = make_uint4(q0.x, q0.y, q1.x, q1.y);
+      }
+      const float4 p0 = *reinterpret_cast<const float4*>(&sm.p[row][4 * g]);
+      const float4 p1 = *reinterpret_cast<const float4*>(&sm.p[row][16 + 4 * g]);
+      const float x[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+      split8(x, pk.P[rb][0][lane], pk.P[rb][1][lane]);
+    }
+    {
+      // Kbar^T[16 ib + m][t] = (gam_31 / gam_t) k_t[16 ib + m], t = pi(g, e)
+      float f[8];
+  #pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = __expf(sm.lg[kQ - 1] - sm.lg[pi_k(g, e)]);
+  #pragma unroll
+      for (int ib = 0; ib < 4; ++ib) {
+        const u16x4_t lo = rr::frag4_tr(&sm.k[0][16 * ib], 72, lane);    // K[4 g + e][16 ib + m]
+        const u16x4_t hi = rr::frag4_tr(&sm.k[16][16 * ib], 72, lane);   // K[16 + 4 g + e][..]
+        const float x[8] = {f[0] * rr::bf_val(lo[0]), f[1] * rr::bf_val(lo[1]), f[2] * rr::bf_val(lo[2]),
+                            f[3] * rr::bf_val(lo[3]), f[4] * rr::bf_val(hi[0]), f[5] * rr::bf_val(hi[1]),
+                            f[6] * rr::bf_val(hi[2]), f[7] * rr::bf_val(hi[3])};
+        split8(x, pk.Kb[ib][0][lane], pk.Kb[ib][1][lane]);
+      }
+    }
+    if (lane < kQ) pk.gam[lane] = sm.gam[lane];
+}
 }
 
 // ------------------------------------------------------------------ kernel 2
@@ -403,6 +461,115 @@ __global__ __launch_bounds__(64) void gdn_state_kernel(const ChunkPack* __restri
   }
 }
 
+// ------------------------------------------------------------------ kernel 3
+// The adjoint across the chunks, newest first: one wave per (head, 16
+// adjoint columns j), dS = dL/dS at the end of the chunk from the later
+// steps as four 16-row accumulator blocks.  Per chunk it writes dS as the
+// chunk's adjoint checkpoint (before the chunk's own steps: what the
+// gradient pass starts each interval from), then
+//   dU = P^T dO + Kbar dS,   dS <- gam_31 dS + (diag(gam) Q)^T dO - W^T dU.
+struct BFrags {
+  uint4 Pt[2][2], Kb[2][2][2], Qg[4][2], Wn[4][2];
+  float gend;
+  float dO[8];   // dO[pi(g, e)][j]
+};
+
+__device__ __forceinline__ void load_bfrags(BFrags& f, const BwdPack& pk, const float* dy, int64_t row0, int H, int h,
+                                            int j, int lane) {
+  const int g = lane >> 4;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    f.Pt[rb][0] = pk.Pt[rb][0][lane];
+    f.Pt[rb][1] = pk.Pt[rb][1][lane];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      f.Kb[rb][kb][0] = pk.Kb[rb][kb][0][lane];
+      f.Kb[rb][kb][1] = pk.Kb[rb][kb][1][lane];
+    }
+  }
+#pragma unroll
+  for (int ib = 0; ib < 4; ++ib) {
+    f.Qg[ib][0] = pk.Qg[ib][0][lane];
+    f.Qg[ib][1] = pk.Qg[ib][1][lane];
+    f.Wn[ib][0] = pk.Wn[ib][0][lane];
+    f.Wn[ib][1] = pk.Wn[ib][1][lane];
+  }
+  f.gend = pk.gend;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f.dO[e] = dy[((row0 + pi_k(g, e)) * H + h) * kD + j];
+}
+
+__global__ __launch_bounds__(64) void gdn_rstate_kernel(const BwdPack* __restrict__ pack, const float* __restrict__ dy,
+                                                        const float* __restrict__ dfinal, float* __restrict__ adjck,
+                                                        float* __restrict__ dh0, int BH, int H, int L, int nC) {
+  const int id = blockIdx.x, xcd = id % kXcd, kk = id / kXcd;
+  const int s = kk & 3, bh = (kk >> 2) * kXcd + xcd;
+  if (bh >= BH) return;
+  const int b = bh / H, h = bh % H;
+  const int lane = threadIdx.x, n = lane & 15, g = lane >> 4;
+  const int j = 16 * s + n;
+  f32x4_t S[4];
+#pragma unroll
+  for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      S[ib][r] = dfinal != nullptr ? dfinal[((int64_t)bh * kD + 16 * ib + 4 * g + r) * kD + j] : 0.f;
+  const BwdPack* pk = pack + (int64_t)bh * nC;
+  auto row0 = [&](int c) { return (int64_t)b * L + (int64_t)c * kQ; };
+  BFrags f;
+  load_bfrags(f, pk[nC - 1], dy, row0(nC - 1), H, h, j, lane);
+  for (int c = nC - 1; c >= 0; --c) {
+    float* ac = adjck + ((int64_t)bh * nC + c) * kD * kD;
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ac[(16 * ib + 4 * g + r) * kD + j] = S[ib][r];
+    u16x8_t oh, ol;
+    rr::bf_split8(f.dO, oh, ol);
+    u16x8_t sh[2], sl[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) split_pair(S[2 * kb], S[2 * kb + 1], sh[kb], sl[kb]);
+    // dU = P^T dO + Kbar dS
+    f32x4_t U[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      f32x4_t a = {0.f, 0.f, 0.f, 0.f};
+      a = mfma(as_u8(f.Pt[rb][0]), oh, a);
+      a = mfma(as_u8(f.Pt[rb][0]), ol, a);
+      a = mfma(as_u8(f.Pt[rb][1]), oh, a);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        a = mfma(as_u8(f.Kb[rb][kb][0]), sh[kb], a);
+        a = mfma(as_u8(f.Kb[rb][kb][0]), sl[kb], a);
+        a = mfma(as_u8(f.Kb[rb][kb][1]), sh[kb], a);
+      }
+      U[rb] = a;
+    }
+    u16x8_t uh, ul;
+    split_pair(U[0], U[1], uh, ul);
+    // dS_in = gam_31 dS + (diag(gam) Q)^T dO - W^T dU
+    const float gend = f.gend;
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+      f32x4_t a = {gend * S[ib][0], gend * S[ib][1], gend * S[ib][2], gend * S[ib][3]};
+      a = mfma(as_u8(f.Qg[ib][0]), oh, a);
+      a = mfma(as_u8(f.Qg[ib][0]), ol, a);
+      a = mfma(as_u8(f.Qg[ib][1]), oh, a);
+      a = mfma(as_u8(f.Wn[ib][0]), uh, a);
+      a = mfma(as_u8(f.Wn[ib][0]), ul, a);
+      a = mfma(as_u8(f.Wn[ib][1]), uh, a);
+      S[ib] = a;
+    }
+    if (c > 0) load_bfrags(f, pk[c - 1], dy, row0(c - 1), H, h, j, lane);
+  }
+  if (dh0 != nullptr) {
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dh0[((int64_t)bh * kD + 16 * ib + 4 * g + r) * kD + j] = S[ib][r];
+  }
+}
+
 }  // namespace
 
 namespace rr {
@@ -417,7 +584,7 @@ int gdn_chunk_fwd(const void* q, const void* k, const void* v, const void* alpha
                   int64_t L, int64_t H, const float* h0, float* y, float* ckpt, void* workspace, hipStream_t s) {
   const int64_t BH = B * H, nC = L / kQ, groups = (BH + kXcd - 1) / kXcd;
   ChunkPack* pack = static_cast<ChunkPack*>(workspace);
-  hipLaunchKernelGGL(gdn_wy_kernel, dim3((unsigned)(groups * kXcd * nC)), dim3(64), 0, s,
+  hipLaunchKernelGGL(gdn_wy_kernel<false>, dim3((unsigned)(groups * kXcd * nC)), dim3(64), 0, s,
                      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
                      static_cast<const uint16_t*>(alpha), static_cast<const uint16_t*>(beta), pack, (int)BH, (int)H,
                      (int)L, (int)nC);
@@ -425,6 +592,28 @@ int gdn_chunk_fwd(const void* q, const void* k, const void* v, const void* alpha
   hipLaunchKernelGGL(gdn_state_kernel, dim3((unsigned)(groups * kXcd * 4)), dim3(64), 0, s, pack, h0, y, ckpt,
                      (int)BH, (int)H, (int)L, (int)nC);
   return check_launch("gdn chunked forward (state)");
+}
+
+}  // namespace rr
+
+namespace rr {
+
+size_t gdn_chunk_bwd_ws_bytes(int64_t B, int64_t L, int64_t H) {
+  return (size_t)(B * H) * (size_t)(L / kQ) * sizeof(BwdPack);
+}
+
+int gdn_chunk_adjoint(const void* q, const void* k, const void* v, const void* alpha, const void* beta, const float* dy,
+                      const float* dfinal, int64_t B, int64_t L, int64_t H, float* adjck, float* dh0, void* packs,
+                      hipStream_t s) {
+  const int64_t BH = B * H, nC = L / kQ, groups = (BH + kXcd - 1) / kXcd;
+  hipLaunchKernelGGL(gdn_wy_kernel<true>, dim3((unsigned)(groups * kXcd * nC)), dim3(64), 0, s,
+                     static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                     static_cast<const uint16_t*>(alpha), static_cast<const uint16_t*>(beta), packs, (int)BH, (int)H,
+                     (int)L, (int)nC);
+  if (int rc = check_launch("gdn chunked adjoint (WY)")) return rc;
+  hipLaunchKernelGGL(gdn_rstate_kernel, dim3((unsigned)(groups * kXcd * 4)), dim3(64), 0, s,
+                     static_cast<const BwdPack*>(packs), dy, dfinal, adjck, dh0, (int)BH, (int)H, (int)L, (int)nC);
+  return check_launch("gdn chunked adjoint (state)");
 }
 
 }  // namespace rr

@@ -89,6 +89,12 @@ bool gdn_chunk_supported(int dtype, int64_t Dh, int64_t T);
 size_t gdn_chunk_ws_bytes(int64_t B, int64_t L, int64_t H);
 int gdn_chunk_fwd(const void* q, const void* k, const void* v, const void* alpha, const void* beta, int64_t B,
                   int64_t L, int64_t H, const float* h0, float* y, float* ckpt, void* workspace, hipStream_t s);
+// The backward's adjoint pass in the same form: the adjoint at every chunk
+// end (adjck [B,H,nC,Dh,Dh], as the sequential pass writes it) and dh0.
+size_t gdn_chunk_bwd_ws_bytes(int64_t B, int64_t L, int64_t H);
+int gdn_chunk_adjoint(const void* q, const void* k, const void* v, const void* alpha, const void* beta, const float* dy,
+                      const float* dfinal, int64_t B, int64_t L, int64_t H, float* adjck, float* dh0, void* packs,
+                      hipStream_t s);
 
 // Backward of the chunked kernels with column-owned state blocks (GLA: Dh in
 // {32, 64, 128}; SSD: Dh in {32, 64, 128}, N in {64, 128}; chunked_bwd.hip).  SSD
