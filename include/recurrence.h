@@ -281,7 +281,8 @@ int rr_rotlru_step(const void* a, const void* cs, const void* sn, const void* x,
 /* ------------------------------------------------------ Gated DeltaNet --
  * The reference's designed next plug-in (docs/DESIGN_gated_deltanet.md; not
  * code in the reference): the sequential kernels of its Phase 2 (:270-440,
- * :528-536), as a C entry pair instead of a Metal launcher.  Per (b, h):
+ * :528-536) and, for bf16 / Dh 64 / T 32, the chunkwise form of its Phase 3
+ * (:139-266), as a C entry pair instead of a Metal launcher.  Per (b, h):
  *   S_t = alpha_t (S_{t-1} - beta_t k_t (k_t^T S_{t-1})) + beta_t k_t v_t^T,
  *   y_t[j] = sum_i q_t[i] S_t[i,j]                           (:56-90)
  * q, k, v [B,L,H,Dh] and alpha, beta [B,L,H] (dtype; q and k L2-normalised,
@@ -304,7 +305,8 @@ int rr_gdn_fwd(const void* q, const void* k, const void* v, const void* alpha, c
 size_t rr_gdn_fwd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t seg, int dtype);
 
 /* Workspace bytes of rr_gdn_bwd (the adjoint at every checkpoint,
- * [B,H,L/T,Dh,Dh] fp32); 0 for invalid arguments. */
+ * [B,H,L/T,Dh,Dh] fp32, then for bf16 / Dh 64 / T 32 the chunk fragments of
+ * the chunkwise adjoint pass; 16-byte aligned); 0 for invalid arguments. */
 size_t rr_gdn_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t seg, int dtype);
 
 /* Backward (:334-440): dy [B,L,H,Dh] fp32, dfinal [B,H,Dh,Dh] fp32 (nullable);
