@@ -659,16 +659,15 @@ extern "C" int rr_gdn_bwd(const float* dy, const float* dfinal, const void* q, c
   const int64_t T = rr::chunk_len(L, seg), nC = L / T;
   hipStream_t s = static_cast<hipStream_t>(stream);
   float* adjck = static_cast<float*>(workspace);
-  // bf16, Dh 64, T 32: the adjoint pass in chunkwise form, then the same
-  // interval-parallel gradient pass
+  // bf16, Dh 64, T 32: the adjoint pass and the gradient pass in chunkwise form
   const bool chunked = rr::gdn_chunk_supported(dtype, Dh, T);
   if (chunked && !aligned16(workspace)) return rr::fail(RR_EWORKSPACE, "gdn_bwd: workspace must be 16-byte aligned");
   RR_DISPATCH_DTYPE(dtype, {
     if (chunked) {
       void* packs = static_cast<char*>(workspace) + align256(adj_bytes(B, L, H, Dh, seg));
       if (int rc = rr::gdn_chunk_adjoint(q, k, v, alpha, beta, dy, dfinal, B, L, H, adjck, dh0, packs, s)) return rc;
-      launch_grad_t<InT, 64, 32>(dy, q, k, v, alpha, beta, h0, ckpt, adjck, dq, dk, dv, dalpha, dbeta, B, H, L, nC,
-                                 s);
+      if (int rc = rr::gdn_chunk_grad(dy, q, k, v, alpha, beta, h0, ckpt, adjck, dq, dk, dv, dalpha, dbeta, B, L, H, s))
+        return rc;
     } else if (Dh == 64)
       launch_bwd_dh<InT, 64>(T, dy, dfinal, q, k, v, alpha, beta, h0, ckpt, adjck, dq, dk, dv, dalpha, dbeta, dh0, B,
                              H, L, nC, s);

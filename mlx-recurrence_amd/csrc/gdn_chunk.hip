@@ -570,6 +570,438 @@ __global__ __launch_bounds__(64) void gdn_rstate_kernel(const BwdPack* __restric
   }
 }
 
+// ------------------------------------------------------------------ kernel 4
+// The gradient pass in chunkwise form: one workgroup (4 waves) per chunk, all
+// chunks at once, from the forward checkpoint S_in, the adjoint checkpoint
+// dS_out and dO.  With the forward quantities above (recomputed) and
+// dU = P^T dO + Kbar dS_out:
+//   dQ = diag(gam) dO S_in^T + dQK K,   dQK = tril(R) o dP,   dP = dO U^T
+//   dK = dQK^T Q + diag(f) Kbar' + diag(beta gam) T^T dW + (dG + dG^T) K,
+//        Kbar' = U dS_out^T,  f = gam_31 / gam,  dW = -dU S_in^T
+//   dV = diag(beta) T^T dU
+//   dT = dU V^T diag(beta) + dW K^T diag(beta gam),  dA = -T^T dT T^T (strictly lower)
+//   dG = diag(beta) R o dA
+//   dbeta = rows(T^T dU o V) + gam o rows(T^T dW o K) + rows(R o G o dA)
+// and the decays through lg (gam_r = e^lg_r, R = e^(lg_r - lg_c), f):
+//   dlg = rows(E) - cols(E) + gam o (rows(dO o Q S_in) + beta o rows(T^T dW o K))
+//         - f o rows(Kbar' o K) + [r = 31] (gam_31 <dS_out, S_in> + sum f o rows(Kbar' o K)),
+//   E = (QK o dP (lower, diagonal included) + diag(beta) G o dA) o R,
+//   dalpha_m = (sum_{r >= m} dlg_r) / alpha_m.
+// (Derived from the chunk equations and checked in float64 against the
+// sequential adjoint before this kernel.)  Every product runs on MFMA from
+// fp32 matrices in LDS (bf16 hi / lo terms; bf16 inputs one term), its 16x16
+// output blocks dealt to the four waves.
+constexpr int kP68 = 68, kP36 = 36;   // LDS row pitches (fp32): 64 + 4, 32 + 4
+
+struct alignas(16) GradSm {
+  float k[kQ][kP68], v[kQ][kP68], q[kQ][kP68], dO[kQ][kP68];
+  float sin[kD][kP68], dso[kD][kP68];
+  float u[kQ][kP68], du[kQ][kP68], w[kQ][kP68];   // U (then dK), dU, W (then dW)
+  float dq[kQ][kP68];
+  float A[kQ][kP36], T[kQ][kP36], P[kQ][kP36], G[kQ][kP36];   // P: QK, then dQK; G: G, then dG + dG^T
+  float dR[kQ][kP36], dT[kQ][kP36], X[kQ][kP36];
+  float x16[16][20];
+  float lg[kQ], gam[kQ], beta[kQ], f[kQ], al[kQ];
+  float part[6][kQ][4];   // per-row partial sums of the elementwise reductions, [quantity][row][column block]
+};
+
+// Reads op(M)[row][k0 .. k0 + 7] (TR: M[k][row]) times the optional k and
+// row scales into x[8].
+template <bool TR>
+__device__ __forceinline__ void rd8(const float* M, int ld, int row, int k0, const float* ks, float rs, float (&x)[8]) {
+  if constexpr (TR) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = M[(k0 + e) * ld + row];
+  } else {
+    const float4 a = *reinterpret_cast<const float4*>(&M[row * ld + k0]);
+    const float4 b = *reinterpret_cast<const float4*>(&M[row * ld + k0 + 4]);
+    x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] *= (ks != nullptr ? ks[k0 + e] : 1.f) * rs;
+}
+
+// C = op(A) op(B) (M x N, contraction K) from LDS; each 16 x 16 block goes to
+// out(mb, nb, acc) with acc[r] = C[16 mb + 4 (lane / 16) + r][16 nb + lane % 16].
+// A: A[m][k] (TA: A[k][m]); B: B[k][n] (TB: B[n][k]); ka / kb scale the
+// contraction index of A / B, ma the rows of A; AX / BX: bf16-exact operand.
+template <int M, int N, int K, bool TA, bool TB, bool AX, bool BX, typename OUT>
+__device__ __forceinline__ void mm(const float* A, int lda, const float* B, int ldb, OUT out,
+                                   const float* ka = nullptr, const float* ma = nullptr, const float* kb = nullptr) {
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l15 = lane & 15, g = lane >> 4;
+  constexpr int MB = M / 16, NB = N / 16, KB = K / 32;
+  for (int blk = w; blk < MB * NB; blk += 4) {
+    const int mbk = blk / NB, nbk = blk % NB;
+    const int ar = 16 * mbk + l15, bc = 16 * nbk + l15;
+    const float rs = ma != nullptr ? ma[ar] : 1.f;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KB; ++kk) {
+      const int k0 = 32 * kk + 8 * g;
+      float a[8], b[8];
+      rd8<TA>(A, lda, ar, k0, ka, rs, a);
+      rd8<!TB>(B, ldb, bc, k0, kb, 1.f, b);   // B[k][n]: column n of rows k0.. = transposed read
+      u16x8_t ah, al, bh, bl;
+      rr::bf_split8(a, ah, al);
+      rr::bf_split8(b, bh, bl);
+      acc = mfma(ah, bh, acc);
+      if constexpr (!BX) acc = mfma(ah, bl, acc);
+      if constexpr (!AX) acc = mfma(al, bh, acc);
+    }
+    out(mbk, nbk, acc);
+  }
+}
+
+__device__ __forceinline__ float bfv(uint16_t x) { return rr::bf_val(x); }
+
+__global__ __launch_bounds__(256) void gdn_cgrad_kernel(const float* __restrict__ dy, const uint16_t* __restrict__ q,
+                                                        const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                                                        const uint16_t* __restrict__ alpha,
+                                                        const uint16_t* __restrict__ beta, const float* __restrict__ h0,
+                                                        const float* __restrict__ ckpt, const float* __restrict__ adjck,
+                                                        uint16_t* __restrict__ dq, uint16_t* __restrict__ dk,
+                                                        uint16_t* __restrict__ dv, uint16_t* __restrict__ dalpha,
+                                                        uint16_t* __restrict__ dbeta, int BH, int H, int L, int nC) {
+  __shared__ GradSm sm;
+  const int id = blockIdx.x, xcd = id % kXcd, kk = id / kXcd;
+  const int c = kk % nC, bh = (kk / nC) * kXcd + xcd;
+  if (bh >= BH) return;
+  const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l15 = lane & 15, g = lane >> 4;
+  const int64_t row0 = (int64_t)b * L + (int64_t)c * kQ;
+  const int64_t rs = (int64_t)H * kD;   // element stride of a step in [B, L, H, Dh]
+  // ---- loads: the chunk's inputs (fp32 in LDS), dO, S_in, dS_out
+  {
+    const uint16_t* kp = k + (row0 * H + h) * kD;
+    const uint16_t* vp = v + (row0 * H + h) * kD;
+    const uint16_t* qp = q + (row0 * H + h) * kD;
+    const float* dp = dy + (row0 * H + h) * kD;
+    {   // 32 rows x 8 pieces of 8 elements: one per thread
+      const int r = tid >> 3, c8 = 8 * (tid & 7);
+      const u16x8_t kx = *reinterpret_cast<const u16x8_t*>(kp + r * rs + c8);
+      const u16x8_t vx = *reinterpret_cast<const u16x8_t*>(vp + r * rs + c8);
+      const u16x8_t qx = *reinterpret_cast<const u16x8_t*>(qp + r * rs + c8);
+      const float4 d0 = *reinterpret_cast<const float4*>(dp + r * rs + c8);
+      const float4 d1 = *reinterpret_cast<const float4*>(dp + r * rs + c8 + 4);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sm.k[r][c8 + e] = bfv(kx[e]);
+        sm.v[r][c8 + e] = bfv(vx[e]);
+        sm.q[r][c8 + e] = bfv(qx[e]);
+      }
+      *reinterpret_cast<float4*>(&sm.dO[r][c8]) = d0;
+      *reinterpret_cast<float4*>(&sm.dO[r][c8 + 4]) = d1;
+    }
+    // S_in: checkpoint c - 1, else h0, else zero; dS_out: adjoint checkpoint c
+    const float* sp = c > 0 ? ckpt + ((int64_t)bh * nC + c - 1) * kD * kD
+                            : (h0 != nullptr ? h0 + (int64_t)bh * kD * kD : nullptr);
+    const float* ap = adjck + ((int64_t)bh * nC + c) * kD * kD;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {   // 64 x 64: 1024 float4, four passes
+      const int i = tid + 256 * it, r = i >> 4, c4 = 4 * (i & 15);
+      const float4 sv = sp != nullptr ? *reinterpret_cast<const float4*>(sp + r * kD + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      *reinterpret_cast<float4*>(&sm.sin[r][c4]) = sv;
+      *reinterpret_cast<float4*>(&sm.dso[r][c4]) = *reinterpret_cast<const float4*>(ap + r * kD + c4);
+    }
+    if (tid < kQ) {
+      const float al = fmaxf(bfv(alpha[(row0 + tid) * H + h]), 1e-30f);   // alpha = 0 taken as 1e-30
+      sm.al[tid] = al;
+      sm.beta[tid] = bfv(beta[(row0 + tid) * H + h]);
+      sm.lg[tid] = __logf(al);   // prefix-summed below
+    }
+  }
+  __syncthreads();
+  if (w == 0) {
+    const float lgv = rr::prefix32_sum(sm.lg[lane & 31]);
+    rr::wave_lds_sync();
+    if (lane < kQ) {
+      sm.lg[lane] = lgv;
+      sm.gam[lane] = __expf(lgv);
+    }
+    rr::wave_lds_sync();
+    if (lane < kQ) sm.f[lane] = __expf(sm.lg[kQ - 1] - lgv);
+  }
+  __syncthreads();
+
+  // ---- G = K K^T, QK = Q K^T; A, P
+  mm<32, 32, 64, false, true, true, true>(&sm.k[0][0], kP68, &sm.k[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm.G[16 * mb + 4 * g + r][16 * nb + l15] = acc[r];
+  });
+  mm<32, 32, 64, false, true, true, true>(&sm.q[0][0], kP68, &sm.k[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm.P[16 * mb + 4 * g + r][16 * nb + l15] = acc[r];
+  });
+  __syncthreads();
+  for (int i = tid; i < kQ * kQ; i += 256) {
+    const int r = i >> 5, cc = i & 31;
+    const float rat = __expf(cc <= r ? sm.lg[r] - sm.lg[cc] : 0.f);
+    sm.A[r][cc] = cc < r ? sm.beta[r] * rat * sm.G[r][cc] : 0.f;
+    sm.dR[r][cc] = cc <= r ? rat : 0.f;   // R on the lower triangle (kept for the decay terms)
+  }
+  __syncthreads();
+  // ---- T = (I + A)^-1 (wave 0; 16 x 16 blocks as in the WY kernel)
+  if (w == 0) {
+    const int hb = 16 * ((lane >> 4) & 1), cl = l15;
+    float tc[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float s0 = r == cl ? 1.f : 0.f, s1 = 0.f;
+#pragma unroll
+      for (int m = 0; m + 1 < r; m += 2) {
+        s0 -= sm.A[hb + r][hb + m] * tc[m];
+        s1 -= sm.A[hb + r][hb + m + 1] * tc[m + 1];
+      }
+      if (r & 1) s0 -= sm.A[hb + r][hb + r - 1] * tc[r - 1];
+      tc[r] = s0 + s1;
+    }
+    if (lane < kQ) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sm.T[hb + r][hb + cl] = tc[r];
+        sm.T[hb + r][16 - hb + cl] = 0.f;
+      }
+    }
+    rr::wave_lds_sync();
+    const int r0 = 4 * g;
+    float xs[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const float tm = sm.T[m][l15];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xs[i] += sm.A[16 + r0 + i][m] * tm;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sm.x16[r0 + i][l15] = xs[i];
+    rr::wave_lds_sync();
+    float ts[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const float xm = sm.x16[m][l15];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ts[i] -= sm.T[16 + r0 + i][16 + m] * xm;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sm.T[16 + r0 + i][l15] = ts[i];
+  }
+  // P = tril(R) o QK (each thread its own elements)
+  for (int i = tid; i < kQ * kQ; i += 256) {
+    const int r = i >> 5, cc = i & 31;
+    sm.P[r][cc] *= sm.dR[r][cc];
+  }
+  __syncthreads();
+
+  // ---- W = T diag(beta gam) K; U = T diag(beta) V - W S_in
+  {
+    float* bgam = &sm.part[5][0][0];   // beta gam per step, 32 floats
+    if (tid < kQ) bgam[tid] = sm.beta[tid] * sm.gam[tid];
+    __syncthreads();
+    mm<32, 64, 32, false, false, false, true>(&sm.T[0][0], kP36, &sm.k[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sm.w[16 * mb + 4 * g + r][16 * nb + l15] = acc[r];
+    }, bgam);
+    mm<32, 64, 32, false, false, false, true>(&sm.T[0][0], kP36, &sm.v[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sm.u[16 * mb + 4 * g + r][16 * nb + l15] = acc[r];
+    }, sm.beta);
+    __syncthreads();
+    mm<32, 64, 64, false, false, false, false>(&sm.w[0][0], kP68, &sm.sin[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sm.u[16 * mb + 4 * g + r][16 * nb + l15] -= acc[r];
+    });
+  }
+  // rows(dO o Q S_in) -> part[0]
+  mm<32, 64, 64, false, false, true, false>(&sm.q[0][0], kP68, &sm.sin[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * mb + 4 * g + r;
+      const float s = rr::row16_sum(acc[r] * sm.dO[row][16 * nb + l15]);
+      if (l15 == 0) sm.part[0][row][nb] = s;
+    }
+  });
+  __syncthreads();
+
+  // ---- dU = P^T dO + Kbar dS_out
+  mm<32, 64, 32, true, false, false, false>(&sm.P[0][0], kP36, &sm.dO[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm.du[16 * mb + 4 * g + r][16 * nb + l15] = acc[r];
+  });
+  __syncthreads();
+  mm<32, 64, 64, false, false, false, false>(&sm.k[0][0], kP68, &sm.dso[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm.du[16 * mb + 4 * g + r][16 * nb + l15] += acc[r];
+  }, nullptr, sm.f);
+  // dQ = diag(gam) dO S_in^T
+  mm<32, 64, 64, false, true, false, false>(&sm.dO[0][0], kP68, &sm.sin[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * mb + 4 * g + r;
+      sm.dq[row][16 * nb + l15] = sm.gam[row] * acc[r];
+    }
+  });
+  // dP = dO U^T: dQK = tril(R) o dP into P's place is below (P still read above);
+  // the decay term QK o dP (lower) is formed from G's place after QK is rebuilt
+  __syncthreads();
+  mm<32, 32, 64, false, true, false, false>(&sm.dO[0][0], kP68, &sm.u[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm.X[16 * mb + 4 * g + r][16 * nb + l15] = acc[r];   // dP
+  });
+  __syncthreads();
+  // E (decay) += QK o dP o R on the lower triangle: QK = P / R there (R > 0);
+  // recomputing QK avoids the division: P holds tril(R) o QK
+  for (int i = tid; i < kQ * kQ; i += 256) {
+    const int r = i >> 5, cc = i & 31;
+    const float dp = sm.X[r][cc], R = sm.dR[r][cc];
+    sm.dT[r][cc] = cc <= r ? sm.P[r][cc] * dp : 0.f;   // E_P = (R o QK) o dP = P o dP
+    sm.X[r][cc] = cc <= r ? R * dp : 0.f;              // dQK = tril(R) o dP
+  }
+  __syncthreads();
+  // dQ += dQK K -> global; dK = dQK^T Q (into U's place after Kbar' below)
+  mm<32, 64, 32, false, false, false, true>(&sm.X[0][0], kP36, &sm.k[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * mb + 4 * g + r, col = 16 * nb + l15;
+      dq[((row0 + row) * H + h) * kD + col] = rr::bf_bits(sm.dq[row][col] + acc[r]);
+    }
+  });
+  __syncthreads();
+  // Kbar' = U dS_out^T: dK += f o Kbar', rows(Kbar' o K) -> part[1]
+  mm<32, 64, 64, false, true, false, false>(&sm.u[0][0], kP68, &sm.dso[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * mb + 4 * g + r, col = 16 * nb + l15;
+      sm.dq[row][col] = sm.f[row] * acc[r];   // dK partial (dq's place is free after its store)
+      const float s = rr::row16_sum(acc[r] * sm.k[row][col]);
+      if (l15 == 0) sm.part[1][row][nb] = s;
+    }
+  });
+  __syncthreads();
+  mm<32, 64, 32, true, false, false, true>(&sm.X[0][0], kP36, &sm.q[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm.dq[16 * mb + 4 * g + r][16 * nb + l15] += acc[r];   // dK += dQK^T Q
+  });
+  // dW = -dU S_in^T (into W's place)
+  __syncthreads();
+  mm<32, 64, 64, false, true, false, false>(&sm.du[0][0], kP68, &sm.sin[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm.w[16 * mb + 4 * g + r][16 * nb + l15] = -acc[r];
+  });
+  // T^T dU: dV = diag(beta) T^T dU -> global, rows(T^T dU o V) -> part[2]
+  mm<32, 64, 32, true, false, false, false>(&sm.T[0][0], kP36, &sm.du[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * mb + 4 * g + r, col = 16 * nb + l15;
+      dv[((row0 + row) * H + h) * kD + col] = rr::bf_bits(sm.beta[row] * acc[r]);
+      const float s = rr::row16_sum(acc[r] * sm.v[row][col]);
+      if (l15 == 0) sm.part[2][row][nb] = s;
+    }
+  });
+  // dT = dU V^T diag(beta)
+  mm<32, 32, 64, false, true, false, true>(&sm.du[0][0], kP68, &sm.v[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int col = 16 * nb + l15;
+      sm.A[16 * mb + 4 * g + r][col] = sm.beta[col] * acc[r];   // A's place holds dT from here
+    }
+  });
+  __syncthreads();
+  // T^T dW: dK += diag(beta gam) T^T dW, rows(T^T dW o K) -> part[3]
+  mm<32, 64, 32, true, false, false, false>(&sm.T[0][0], kP36, &sm.w[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * mb + 4 * g + r, col = 16 * nb + l15;
+      sm.dq[row][col] += sm.beta[row] * sm.gam[row] * acc[r];
+      const float s = rr::row16_sum(acc[r] * sm.k[row][col]);
+      if (l15 == 0) sm.part[3][row][nb] = s;
+    }
+  });
+  // dT += dW K^T diag(beta gam)
+  mm<32, 32, 64, false, true, false, true>(&sm.w[0][0], kP68, &sm.k[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int col = 16 * nb + l15;
+      sm.A[16 * mb + 4 * g + r][col] += sm.beta[col] * sm.gam[col] * acc[r];
+    }
+  });
+  __syncthreads();
+  // dA = -T^T (dT T^T), strictly lower: X = dT T^T
+  mm<32, 32, 32, false, true, false, false>(&sm.A[0][0], kP36, &sm.T[0][0], kP36, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm.X[16 * mb + 4 * g + r][16 * nb + l15] = acc[r];
+  });
+  __syncthreads();
+  mm<32, 32, 32, true, false, false, false>(&sm.T[0][0], kP36, &sm.X[0][0], kP36, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * mb + 4 * g + r, col = 16 * nb + l15;
+      const float da = col < row ? -acc[r] : 0.f;
+      const float R = sm.dR[row][col], Gv = sm.G[row][col];
+      // E += diag(beta) G o dA o R; dG = diag(beta) R o dA; rows(R o G o dA) -> part[4]
+      sm.dT[row][col] += sm.beta[row] * Gv * da * R;
+      sm.A[row][col] = sm.beta[row] * R * da;   // dG (dT no longer needed)
+      const float s = rr::row16_sum(R * Gv * da);
+      if (l15 == 0) sm.part[4][row][nb] = s;
+    }
+  });
+  __syncthreads();
+  // dGs = dG + dG^T (into G's place); dK += dGs K -> global
+  for (int i = tid; i < kQ * kQ; i += 256) {
+    const int r = i >> 5, cc = i & 31;
+    sm.G[r][cc] = sm.A[r][cc] + sm.A[cc][r];
+  }
+  __syncthreads();
+  mm<32, 64, 32, false, false, false, true>(&sm.G[0][0], kP36, &sm.k[0][0], kP68, [&](int mb, int nb, f32x4_t acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * mb + 4 * g + r, col = 16 * nb + l15;
+      dk[((row0 + row) * H + h) * kD + col] = rr::bf_bits(sm.dq[row][col] + acc[r]);
+    }
+  });
+  // ---- the step scalars (wave 0, lane t < 32): dbeta, dlg -> dalpha
+  if (w == 0) {
+    const int t = lane & 31;
+    float rowE = 0.f, colE = 0.f;   // E = dT's place: (P o dP + diag(beta) G o dA o R)
+    for (int m = 0; m < kQ; ++m) {
+      rowE += sm.dT[t][m];
+      colE += sm.dT[m][t];
+    }
+    auto rows = [&](int qn) { return (sm.part[qn][t][0] + sm.part[qn][t][1]) + (sm.part[qn][t][2] + sm.part[qn][t][3]); };
+    const float p0 = rows(0), p1 = rows(1), p2 = rows(2), p3 = rows(3);
+    const float p4 = (sm.part[4][t][0] + sm.part[4][t][1]);   // 32 columns: two blocks
+    const float gm = sm.gam[t], be = sm.beta[t], ft = sm.f[t];
+    const float dbe = p2 + gm * p3 + p4;
+    float dlg = rowE - colE + gm * (p0 + be * p3) - ft * p1;
+    // the chunk end: gam_31 <dS_out, S_in> and sum_t f_t rows(Kbar' o K)_t
+    float fsum = ft * p1;
+    fsum += __shfl_xor(fsum, 1, 32);
+    fsum += __shfl_xor(fsum, 2, 32);
+    fsum += __shfl_xor(fsum, 4, 32);
+    fsum += __shfl_xor(fsum, 8, 32);
+    fsum += __shfl_xor(fsum, 16, 32);
+    float dot = 0.f;
+    for (int i = t; i < kD * kD; i += 32) dot += sm.dso[i >> 6][i & 63] * sm.sin[i >> 6][i & 63];
+    dot += __shfl_xor(dot, 1, 32);
+    dot += __shfl_xor(dot, 2, 32);
+    dot += __shfl_xor(dot, 4, 32);
+    dot += __shfl_xor(dot, 8, 32);
+    dot += __shfl_xor(dot, 16, 32);
+    if (t == kQ - 1) dlg += sm.gam[kQ - 1] * dot + fsum;
+    // dalpha_m = (sum_{r >= m} dlg_r) / alpha_m: suffix sum over the lanes
+    float suf = dlg;
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) {
+      const float x = __shfl_down(suf, o, 32);
+      if (t + o < 32) suf += x;
+    }
+    if (lane < kQ) {
+      dalpha[(row0 + t) * H + h] = rr::bf_bits(suf / sm.al[t]);
+      dbeta[(row0 + t) * H + h] = rr::bf_bits(dbe);
+    }
+  }
+}
+
 }  // namespace
 
 namespace rr {
@@ -614,6 +1046,22 @@ int gdn_chunk_adjoint(const void* q, const void* k, const void* v, const void* a
   hipLaunchKernelGGL(gdn_rstate_kernel, dim3((unsigned)(groups * kXcd * 4)), dim3(64), 0, s,
                      static_cast<const BwdPack*>(packs), dy, dfinal, adjck, dh0, (int)BH, (int)H, (int)L, (int)nC);
   return check_launch("gdn chunked adjoint (state)");
+}
+
+}  // namespace rr
+
+namespace rr {
+
+int gdn_chunk_grad(const float* dy, const void* q, const void* k, const void* v, const void* alpha, const void* beta,
+                   const float* h0, const float* ckpt, const float* adjck, void* dq, void* dk, void* dv, void* dalpha,
+                   void* dbeta, int64_t B, int64_t L, int64_t H, hipStream_t s) {
+  const int64_t BH = B * H, nC = L / kQ, groups = (BH + kXcd - 1) / kXcd;
+  hipLaunchKernelGGL(gdn_cgrad_kernel, dim3((unsigned)(groups * kXcd * nC)), dim3(256), 0, s, dy,
+                     static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                     static_cast<const uint16_t*>(alpha), static_cast<const uint16_t*>(beta), h0, ckpt, adjck,
+                     static_cast<uint16_t*>(dq), static_cast<uint16_t*>(dk), static_cast<uint16_t*>(dv),
+                     static_cast<uint16_t*>(dalpha), static_cast<uint16_t*>(dbeta), (int)BH, (int)H, (int)L, (int)nC);
+  return check_launch("gdn chunked gradients");
 }
 
 }  // namespace rr

@@ -95,6 +95,11 @@ size_t gdn_chunk_bwd_ws_bytes(int64_t B, int64_t L, int64_t H);
 int gdn_chunk_adjoint(const void* q, const void* k, const void* v, const void* alpha, const void* beta, const float* dy,
                       const float* dfinal, int64_t B, int64_t L, int64_t H, float* adjck, float* dh0, void* packs,
                       hipStream_t s);
+// The gradient pass in chunkwise form, every chunk at once, from the forward
+// and adjoint checkpoints.
+int gdn_chunk_grad(const float* dy, const void* q, const void* k, const void* v, const void* alpha, const void* beta,
+                   const float* h0, const float* ckpt, const float* adjck, void* dq, void* dk, void* dv, void* dalpha,
+                   void* dbeta, int64_t B, int64_t L, int64_t H, hipStream_t s);
 
 // Backward of the chunked kernels with column-owned state blocks (GLA: Dh in
 // {32, 64, 128}; SSD: Dh in {32, 64, 128}, N in {64, 128}; chunked_bwd.hip).  SSD

@@ -189,3 +189,35 @@ def test_gdn_chunkwise_adjoint_matches_sequential():
         err = ((a - b).abs().max() / b.abs().max()).item()
         print({name: err}, flush=True)
         assert np.isfinite(err) and err < 1e-4, (name, err)
+
+
+@pytest.mark.parametrize("dist,seed", [("plain", 64), ("edges", 65)])
+def test_gdn_chunkwise_gradients_match_sequential(dist, seed):
+    """The chunkwise gradient pass (bf16 outputs) against the sequential
+    kernels in fp32 on the same bf16-rounded inputs, rounded to bf16: at
+    fp32 accuracy of the chunkwise form (about 1e-5) the two roundings
+    differ by one bf16 step at most, and only where the exact value lies
+    next to a rounding boundary (a small fraction of the elements); an error
+    of even 1e-3 would move a large fraction."""
+    B, L, H, Dh = 2, 128, 3, 64
+    _announce("gdn_chunkwise_grads", B=B, L=L, H=H, Dh=Dh, dist=dist, seed=seed)
+    rng = np.random.default_rng(seed)
+    ins = [rounded(to_dev(t, BF16)) for t in _inputs(rng, B, L, H, Dh, dist)]
+    h0 = rng.standard_normal((B, H, Dh, Dh)) * 0.5
+    W = torch.tensor(_w(rng, (B, L, H, Dh)), device="cuda:0")
+    Wf = torch.tensor(_w(rng, (B, H, Dh, Dh)), device="cuda:0")
+    res = []
+    for dt in (BF16, F32):
+        ts = [to_dev(t, dt, True) for t in ins]
+        h0t = to_dev(h0, F32, True)
+        y, fs = mr.gated_deltanet_scan_with_state(*ts, initial_state=h0t)
+        ((y * W).sum() + (fs * Wf).sum()).backward()
+        res.append([t.grad.float() for t in ts])
+    for name, a, b in zip(("dq", "dk", "dv", "dalpha", "dbeta"), *res):
+        b16 = b.to(BF16).float()
+        step = b16.abs() * 2.0 ** -7 + b16.abs().max() * 1e-5   # one bf16 step (floor near zero)
+        diff = (a - b16).abs()
+        frac = (diff > 0).float().mean().item()
+        worst = (diff / step).max().item()
+        print({name: {"moved": frac, "worst_steps": worst}}, flush=True)
+        assert worst <= 1.0 and frac < 0.05, (name, frac, worst)
