@@ -571,7 +571,7 @@ __global__ __launch_bounds__(64) void gdn_rstate_kernel(const BwdPack* __restric
 }
 
 // ------------------------------------------------------------------ kernel 4
-// The gradient pass in chunkwise form: one workgroup (4 waves) per chunk, all
+// The gradient pass in chunkwise form: one workgroup (8 waves) per chunk, all
 // chunks at once, from the forward checkpoint S_in, the adjoint checkpoint
 // dS_out and dO.  With the forward quantities above (recomputed) and
 // dU = P^T dO + Kbar dS_out:
@@ -590,8 +590,9 @@ __global__ __launch_bounds__(64) void gdn_rstate_kernel(const BwdPack* __restric
 // (Derived from the chunk equations and checked in float64 against the
 // sequential adjoint before this kernel.)  Every product runs on MFMA from
 // fp32 matrices in LDS (bf16 hi / lo terms; bf16 inputs one term), its 16x16
-// output blocks dealt to the four waves.
+// output blocks dealt to the eight waves.
 constexpr int kP68 = 68, kP36 = 36;   // LDS row pitches (fp32): 64 + 4, 32 + 4
+constexpr int kGW = 8;                 // waves of a gradient workgroup
 
 struct alignas(16) GradSm {
   float k[kQ][kP68], v[kQ][kP68], q[kQ][kP68], dO[kQ][kP68];
@@ -602,6 +603,7 @@ struct alignas(16) GradSm {
   float dR[kQ][kP36], dT[kQ][kP36], X[kQ][kP36];
   float x16[16][20];
   float lg[kQ], gam[kQ], beta[kQ], f[kQ], al[kQ];
+  float dotp[kGW];        // per-wave partial sums of <dS_out, S_in>
   float part[6][kQ][4];   // per-row partial sums of the elementwise reductions, [quantity][row][column block]
 };
 
@@ -631,7 +633,7 @@ __device__ __forceinline__ void mm(const float* A, int lda, const float* B, int 
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l15 = lane & 15, g = lane >> 4;
   constexpr int MB = M / 16, NB = N / 16, KB = K / 32;
-  for (int blk = w; blk < MB * NB; blk += 4) {
+  for (int blk = w; blk < MB * NB; blk += kGW) {
     const int mbk = blk / NB, nbk = blk % NB;
     const int ar = 16 * mbk + l15, bc = 16 * nbk + l15;
     const float rs = ma != nullptr ? ma[ar] : 1.f;
@@ -655,7 +657,7 @@ __device__ __forceinline__ void mm(const float* A, int lda, const float* B, int 
 
 __device__ __forceinline__ float bfv(uint16_t x) { return rr::bf_val(x); }
 
-__global__ __launch_bounds__(256) void gdn_cgrad_kernel(const float* __restrict__ dy, const uint16_t* __restrict__ q,
+__global__ __launch_bounds__(64 * kGW) void gdn_cgrad_kernel(const float* __restrict__ dy, const uint16_t* __restrict__ q,
                                                         const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                                                         const uint16_t* __restrict__ alpha,
                                                         const uint16_t* __restrict__ beta, const float* __restrict__ h0,
@@ -678,7 +680,7 @@ __global__ __launch_bounds__(256) void gdn_cgrad_kernel(const float* __restrict_
     const uint16_t* vp = v + (row0 * H + h) * kD;
     const uint16_t* qp = q + (row0 * H + h) * kD;
     const float* dp = dy + (row0 * H + h) * kD;
-    {   // 32 rows x 8 pieces of 8 elements: one per thread
+    if (tid < 256) {   // 32 rows x 8 pieces of 8 elements
       const int r = tid >> 3, c8 = 8 * (tid & 7);
       const u16x8_t kx = *reinterpret_cast<const u16x8_t*>(kp + r * rs + c8);
       const u16x8_t vx = *reinterpret_cast<const u16x8_t*>(vp + r * rs + c8);
@@ -698,13 +700,18 @@ __global__ __launch_bounds__(256) void gdn_cgrad_kernel(const float* __restrict_
     const float* sp = c > 0 ? ckpt + ((int64_t)bh * nC + c - 1) * kD * kD
                             : (h0 != nullptr ? h0 + (int64_t)bh * kD * kD : nullptr);
     const float* ap = adjck + ((int64_t)bh * nC + c) * kD * kD;
+    float dot = 0.f;   // <dS_out, S_in>, this thread's share
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {   // 64 x 64: 1024 float4, four passes
-      const int i = tid + 256 * it, r = i >> 4, c4 = 4 * (i & 15);
+    for (int it = 0; it < 2; ++it) {   // 64 x 64: 1024 float4, two passes
+      const int i = tid + 512 * it, r = i >> 4, c4 = 4 * (i & 15);
       const float4 sv = sp != nullptr ? *reinterpret_cast<const float4*>(sp + r * kD + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 av = *reinterpret_cast<const float4*>(ap + r * kD + c4);
       *reinterpret_cast<float4*>(&sm.sin[r][c4]) = sv;
-      *reinterpret_cast<float4*>(&sm.dso[r][c4]) = *reinterpret_cast<const float4*>(ap + r * kD + c4);
+      *reinterpret_cast<float4*>(&sm.dso[r][c4]) = av;
+      dot += (sv.x * av.x + sv.y * av.y) + (sv.z * av.z + sv.w * av.w);
     }
+    dot = rr::wave_sum(dot);
+    if (lane == 0) sm.dotp[w] = dot;
     if (tid < kQ) {
       const float al = fmaxf(bfv(alpha[(row0 + tid) * H + h]), 1e-30f);   // alpha = 0 taken as 1e-30
       sm.al[tid] = al;
@@ -735,7 +742,7 @@ __global__ __launch_bounds__(256) void gdn_cgrad_kernel(const float* __restrict_
     for (int r = 0; r < 4; ++r) sm.P[16 * mb + 4 * g + r][16 * nb + l15] = acc[r];
   });
   __syncthreads();
-  for (int i = tid; i < kQ * kQ; i += 256) {
+  for (int i = tid; i < kQ * kQ; i += 64 * kGW) {
     const int r = i >> 5, cc = i & 31;
     const float rat = __expf(cc <= r ? sm.lg[r] - sm.lg[cc] : 0.f);
     sm.A[r][cc] = cc < r ? sm.beta[r] * rat * sm.G[r][cc] : 0.f;
@@ -787,7 +794,7 @@ __global__ __launch_bounds__(256) void gdn_cgrad_kernel(const float* __restrict_
     for (int i = 0; i < 4; ++i) sm.T[16 + r0 + i][l15] = ts[i];
   }
   // P = tril(R) o QK (each thread its own elements)
-  for (int i = tid; i < kQ * kQ; i += 256) {
+  for (int i = tid; i < kQ * kQ; i += 64 * kGW) {
     const int r = i >> 5, cc = i & 31;
     sm.P[r][cc] *= sm.dR[r][cc];
   }
@@ -851,7 +858,7 @@ __global__ __launch_bounds__(256) void gdn_cgrad_kernel(const float* __restrict_
   __syncthreads();
   // E (decay) += QK o dP o R on the lower triangle: QK = P / R there (R > 0);
   // recomputing QK avoids the division: P holds tril(R) o QK
-  for (int i = tid; i < kQ * kQ; i += 256) {
+  for (int i = tid; i < kQ * kQ; i += 64 * kGW) {
     const int r = i >> 5, cc = i & 31;
     const float dp = sm.X[r][cc], R = sm.dR[r][cc];
     sm.dT[r][cc] = cc <= r ? sm.P[r][cc] * dp : 0.f;   // E_P = (R o QK) o dP = P o dP
@@ -947,7 +954,7 @@ __global__ __launch_bounds__(256) void gdn_cgrad_kernel(const float* __restrict_
   });
   __syncthreads();
   // dGs = dG + dG^T (into G's place); dK += dGs K -> global
-  for (int i = tid; i < kQ * kQ; i += 256) {
+  for (int i = tid; i < kQ * kQ; i += 64 * kGW) {
     const int r = i >> 5, cc = i & 31;
     sm.G[r][cc] = sm.A[r][cc] + sm.A[cc][r];
   }
@@ -981,12 +988,8 @@ __global__ __launch_bounds__(256) void gdn_cgrad_kernel(const float* __restrict_
     fsum += __shfl_xor(fsum, 8, 32);
     fsum += __shfl_xor(fsum, 16, 32);
     float dot = 0.f;
-    for (int i = t; i < kD * kD; i += 32) dot += sm.dso[i >> 6][i & 63] * sm.sin[i >> 6][i & 63];
-    dot += __shfl_xor(dot, 1, 32);
-    dot += __shfl_xor(dot, 2, 32);
-    dot += __shfl_xor(dot, 4, 32);
-    dot += __shfl_xor(dot, 8, 32);
-    dot += __shfl_xor(dot, 16, 32);
+#pragma unroll
+    for (int ww = 0; ww < kGW; ++ww) dot += sm.dotp[ww];
     if (t == kQ - 1) dlg += sm.gam[kQ - 1] * dot + fsum;
     // dalpha_m = (sum_{r >= m} dlg_r) / alpha_m: suffix sum over the lanes
     float suf = dlg;
@@ -1056,7 +1059,7 @@ int gdn_chunk_grad(const float* dy, const void* q, const void* k, const void* v,
                    const float* h0, const float* ckpt, const float* adjck, void* dq, void* dk, void* dv, void* dalpha,
                    void* dbeta, int64_t B, int64_t L, int64_t H, hipStream_t s) {
   const int64_t BH = B * H, nC = L / kQ, groups = (BH + kXcd - 1) / kXcd;
-  hipLaunchKernelGGL(gdn_cgrad_kernel, dim3((unsigned)(groups * kXcd * nC)), dim3(256), 0, s, dy,
+  hipLaunchKernelGGL(gdn_cgrad_kernel, dim3((unsigned)(groups * kXcd * nC)), dim3(64 * kGW), 0, s, dy,
                      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
                      static_cast<const uint16_t*>(alpha), static_cast<const uint16_t*>(beta), h0, ckpt, adjck,
                      static_cast<uint16_t*>(dq), static_cast<uint16_t*>(dk), static_cast<uint16_t*>(dv),
