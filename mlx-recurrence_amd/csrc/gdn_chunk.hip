@@ -396,9 +396,8 @@ __global__ __launch_bounds__(64) void gdn_state_kernel(const ChunkPack* __restri
     for (int r = 0; r < 4; ++r)
       S[ib][r] = h0 != nullptr ? h0[((int64_t)bh * kD + 16 * ib + 4 * g + r) * kD + j] : 0.f;
   const ChunkPack* pk = pack + (int64_t)bh * nC;
-  Frags f;
-  load_frags(f, pk[0], s, lane);
-  for (int c = 0; c < nC; ++c) {
+  // one chunk; its fragments were loaded two chunks ahead
+  auto step = [&](const Frags& f, int c) {
     // the state as B operands of its two 32-row k blocks
     u16x8_t sh[2], sl[2];
 #pragma unroll
@@ -446,8 +445,6 @@ __global__ __launch_bounds__(64) void gdn_state_kernel(const ChunkPack* __restri
       a = mfma(as_u8(f.Kb[ib][1]), uh, a);
       S[ib] = a;
     }
-    // the next chunk's fragments go out before this chunk's stores
-    if (c + 1 < nC) load_frags(f, pk[c + 1], s, lane);
     const int64_t row0 = (int64_t)b * L + (int64_t)c * kQ;
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
@@ -458,6 +455,22 @@ __global__ __launch_bounds__(64) void gdn_state_kernel(const ChunkPack* __restri
     for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
       for (int r = 0; r < 4; ++r) ck[(16 * ib + 4 * g + r) * kD + j] = S[ib][r];
+  };
+  // three fragment sets in a ring, loads two chunks ahead (issued whatever
+  // the chunk count, at clamped indices: the waits for a set stay exact)
+  auto ld = [&](Frags& f, int c) { load_frags(f, pk[min(c, nC - 1)], s, lane); };
+  Frags fa, fb, fc;
+  ld(fa, 0);
+  ld(fb, 1);
+  for (int c = 0; c < nC; c += 3) {
+    ld(fc, c + 2);
+    step(fa, c);
+    if (c + 1 >= nC) break;
+    ld(fa, c + 3);
+    step(fb, c + 1);
+    if (c + 2 >= nC) break;
+    ld(fb, c + 4);
+    step(fc, c + 2);
   }
 }
 
@@ -516,9 +529,7 @@ __global__ __launch_bounds__(64) void gdn_rstate_kernel(const BwdPack* __restric
       S[ib][r] = dfinal != nullptr ? dfinal[((int64_t)bh * kD + 16 * ib + 4 * g + r) * kD + j] : 0.f;
   const BwdPack* pk = pack + (int64_t)bh * nC;
   auto row0 = [&](int c) { return (int64_t)b * L + (int64_t)c * kQ; };
-  BFrags f;
-  load_bfrags(f, pk[nC - 1], dy, row0(nC - 1), H, h, j, lane);
-  for (int c = nC - 1; c >= 0; --c) {
+  auto step = [&](const BFrags& f, int c) {
     float* ac = adjck + ((int64_t)bh * nC + c) * kD * kD;
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib)
@@ -560,7 +571,24 @@ __global__ __launch_bounds__(64) void gdn_rstate_kernel(const BwdPack* __restric
       a = mfma(as_u8(f.Wn[ib][1]), uh, a);
       S[ib] = a;
     }
-    if (c > 0) load_bfrags(f, pk[c - 1], dy, row0(c - 1), H, h, j, lane);
+  };
+  // three fragment sets in a ring, loads two chunks ahead (clamped indices)
+  auto ld = [&](BFrags& f, int c) {
+    const int cc = max(c, 0);
+    load_bfrags(f, pk[cc], dy, row0(cc), H, h, j, lane);
+  };
+  BFrags fa, fb, fc;
+  ld(fa, nC - 1);
+  ld(fb, nC - 2);
+  for (int c = nC - 1; c >= 0; c -= 3) {
+    ld(fc, c - 2);
+    step(fa, c);
+    if (c - 1 < 0) break;
+    ld(fa, c - 3);
+    step(fb, c - 1);
+    if (c - 2 < 0) break;
+    ld(fb, c - 4);
+    step(fc, c - 2);
   }
   if (dh0 != nullptr) {
 #pragma unroll
