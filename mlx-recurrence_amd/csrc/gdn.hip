@@ -11,10 +11,13 @@
 //   dbeta_t = d . (v - alpha p);  dalpha_t = <dS, S_{t-1}> - beta d . p;
 //   dS <- alpha (dS - beta k_t d^T).
 //
-// The transition alpha (I - beta k k^T) is a full Dh x Dh matrix, so there is
-// no cheap chunk composition: this is the sequential form (the reference's
-// own first landing, its "Phase 2").  Its parallelism is across state
-// columns and, given checkpoints, across time intervals:
+// The transition alpha (I - beta k k^T) is a full Dh x Dh matrix, so chunks do
+// not compose by scalar decays: this file is the sequential form (the
+// reference's own first landing, its "Phase 2"), used for fp32 / fp16 inputs,
+// Dh 32 and intervals of 8 or 16; bf16 inputs at Dh 64 and T 32 run the
+// chunkwise (WY) form of gdn_chunk.hip instead.  The sequential form's
+// parallelism is across state columns and, given checkpoints, across time
+// intervals:
 //   * every column j of S evolves on its own (p_j, S[:, j] and y[j] need only
 //     column j), and so does every column of the adjoint (the dS recursion
 //     involves neither S nor p);
