@@ -579,7 +579,7 @@ WORKLOADS = {
                 dict(B=96, L=512, H=12, Dh=64, N=16, seg=32)),
     "gla_b96": ("gla_scan fwd+bwd (BASELINE config 2 shape, B = 96)", make_gla,
                 dict(B=96, L=512, H=12, Dh=64, seg=32)),
-    "gdn": ("gated_deltanet_scan fwd+bwd, chunkwise forward, sequential backward (BASELINE config 2 shape)", make_gdn,
+    "gdn": ("gated_deltanet_scan fwd+bwd, chunkwise WY form both ways (BASELINE config 2 shape)", make_gdn,
             dict(B=3, L=512, H=12, Dh=64, seg=32)),
 }
 
