@@ -158,18 +158,20 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_fwd_kernel(
   }
   __syncthreads();
   if (w == 0) {
-    uint64_t* mine = slots + ((int64_t)grp * K + k) * GCH + lane * CH;
+    // slot of (tile, lane, c): tile * GCH + 64 c + lane (a wave's hand-off
+    // stores and loads cover whole 32-byte sectors)
+    uint64_t* mine = slots + ((int64_t)grp * K + k) * GCH + lane;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       float hin = 0.f;
-      if (k > 0) hin = rr::tiles::take_value(mine - GCH + c, status);   // exit state of tile k - 1
+      if (k > 0) hin = rr::tiles::take_value(mine - GCH + 64 * c, status);   // exit state of tile k - 1
       else if (h0 != nullptr && cok) hin = h0[(int64_t)b * D + ch + c];
       sIn[lane * CH + c] = hin;
       if (k + 1 < K) {
         float hout = hin;
 #pragma unroll
         for (int j = 0; j < kNW; ++j) hout = sP[j][lane * CH + c] * hout + sE[j][lane * CH + c];
-        rr::tiles::publish(mine + c, hout);
+        rr::tiles::publish(mine + 64 * c, hout);
       }
     }
   }
@@ -265,17 +267,17 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_bwd_kernel(
   }
   __syncthreads();
   if (w == 0) {
-    uint64_t* mine = slots + ((int64_t)grp * K + k) * GCH + lane * CH;
+    uint64_t* mine = slots + ((int64_t)grp * K + k) * GCH + lane;   // slot layout as in the forward
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       float lin = 0.f;   // adjoint entering the tile from later steps
-      if (k + 1 < K) lin = rr::tiles::take_value(mine + GCH + c, status);
+      if (k + 1 < K) lin = rr::tiles::take_value(mine + GCH + 64 * c, status);
       else if (dfinal != nullptr && cok) lin = dfinal[(int64_t)b * D + ch + c];
       sIn[lane * CH + c] = lin;
       float lout = lin;
 #pragma unroll
       for (int j = kNW - 1; j >= 0; --j) lout = sP[j][lane * CH + c] * lout + sEb[j][lane * CH + c];
-      if (k > 0) rr::tiles::publish(mine + c, lout);
+      if (k > 0) rr::tiles::publish(mine + 64 * c, lout);
       else if (dh0 != nullptr && cok) dh0[(int64_t)b * D + ch + c] = lout;
     }
   }

@@ -128,13 +128,16 @@ __global__ __launch_bounds__(64 * kNW, 4) void rotlru_fwd_kernel(
   }
   __syncthreads();
   if (w == 0) {
-    uint64_t* mine = slots + ((int64_t)grp * K + k) * (2 * GP) + 2 * lane * kCP;
+    // slot of (tile, lane, q, real / imaginary part j): tile * 2 GP +
+    // 64 (2 q + j) + lane (a wave's hand-off stores and loads cover whole
+    // 32-byte sectors)
+    uint64_t* mine = slots + ((int64_t)grp * K + k) * (2 * GP) + lane;
 #pragma unroll
     for (int q = 0; q < kCP; ++q) {
       cplx hin{0.f, 0.f};
       if (k > 0) {
-        hin.r = rr::tiles::take_value(mine - 2 * GP + 2 * q, status);
-        hin.i = rr::tiles::take_value(mine - 2 * GP + 2 * q + 1, status);
+        hin.r = rr::tiles::take_value(mine - 2 * GP + 128 * q, status);
+        hin.i = rr::tiles::take_value(mine - 2 * GP + 128 * q + 64, status);
       } else if (h0 != nullptr && pok) {
         hin = {h0[(int64_t)b * D + 2 * (p + q)], h0[(int64_t)b * D + 2 * (p + q) + 1]};
       }
@@ -143,8 +146,8 @@ __global__ __launch_bounds__(64 * kNW, 4) void rotlru_fwd_kernel(
         cplx hout = hin;
 #pragma unroll
         for (int j = 0; j < kNW; ++j) hout = cfma(sP[j][lane * kCP + q], hout, sE[j][lane * kCP + q]);
-        rr::tiles::publish(mine + 2 * q, hout.r);
-        rr::tiles::publish(mine + 2 * q + 1, hout.i);
+        rr::tiles::publish(mine + 128 * q, hout.r);
+        rr::tiles::publish(mine + 128 * q + 64, hout.i);
       }
     }
   }
@@ -237,13 +240,13 @@ __global__ __launch_bounds__(64 * kNW, 2) void rotlru_bwd_kernel(
   }
   __syncthreads();
   if (w == 0) {
-    uint64_t* mine = slots + ((int64_t)grp * K + k) * (2 * GP) + 2 * lane * kCP;
+    uint64_t* mine = slots + ((int64_t)grp * K + k) * (2 * GP) + lane;   // slot layout as in the forward
 #pragma unroll
     for (int q = 0; q < kCP; ++q) {
       cplx lin{0.f, 0.f};   // adjoint entering the tile from later steps
       if (k + 1 < K) {
-        lin.r = rr::tiles::take_value(mine + 2 * GP + 2 * q, status);
-        lin.i = rr::tiles::take_value(mine + 2 * GP + 2 * q + 1, status);
+        lin.r = rr::tiles::take_value(mine + 2 * GP + 128 * q, status);
+        lin.i = rr::tiles::take_value(mine + 2 * GP + 128 * q + 64, status);
       } else if (dfinal != nullptr && pok) {
         lin = {dfinal[(int64_t)b * D + 2 * (p + q)], dfinal[(int64_t)b * D + 2 * (p + q) + 1]};
       }
@@ -252,8 +255,8 @@ __global__ __launch_bounds__(64 * kNW, 2) void rotlru_bwd_kernel(
 #pragma unroll
       for (int j = kNW - 1; j >= 0; --j) lout = cfma(conj(sP[j][lane * kCP + q]), lout, sEb[j][lane * kCP + q]);
       if (k > 0) {
-        rr::tiles::publish(mine + 2 * q, lout.r);
-        rr::tiles::publish(mine + 2 * q + 1, lout.i);
+        rr::tiles::publish(mine + 128 * q, lout.r);
+        rr::tiles::publish(mine + 128 * q + 64, lout.i);
       } else if (dh0 != nullptr && pok) {
         dh0[(int64_t)b * D + 2 * (p + q)] = lout.r;
         dh0[(int64_t)b * D + 2 * (p + q) + 1] = lout.i;
