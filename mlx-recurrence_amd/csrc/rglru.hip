@@ -59,37 +59,72 @@ inline TileGrid tile_grid(int64_t L, int64_t D, int ch, int dtype, int pass, boo
 // relative), so s = sqrt(1 - a^2) keeps its relative accuracy as a -> 1.
 __device__ __forceinline__ float softplus_f(float v) { return v > 20.f ? v : log1pf(expf(v)); }
 __device__ __forceinline__ float sigmoid_f(float v) { return __builtin_amdgcn_rcpf(1.f + __expf(-v)); }
-__device__ __forceinline__ void gate(float r, float csp, float& a, float& s) {
-  const float z = -csp * sigmoid_f(r);
+// (from sr = sigmoid(r))
+__device__ __forceinline__ void gate_s(float sr, float csp, float& a, float& s) {
+  const float z = -csp * sr;
   a = __expf(z);
   const float t = 2.f * z;
-  const float om = t > -0.125f ? -t * (1.f + t * (0.5f + t * (1.f / 6 + t * (1.f / 24 + t * (1.f / 120)))))
-                               : 1.f - a * a;
-  s = __builtin_amdgcn_sqrtf(om);
+  float p = -t * (1.f + t * (0.5f + t * (1.f / 6 + t * (1.f / 24 + t * (1.f / 120)))));
+  float q = 1.f - a * a;
+  asm volatile("" : "+v"(p));   // both forms, then a select (no divergent branch per element)
+  asm volatile("" : "+v"(q));
+  s = __builtin_amdgcn_sqrtf(t > -0.125f ? p : q);
 }
 
-// Loads a wave's U steps of the scan inputs.  Plain: pa = a, px = x.  Gated:
-// pa = r, px = x, pi = i, and the fp32 gates av = a, sv = sqrt(1 - a^2).
-// Steps past L or D are identity steps (a = 1, x' = 0).
+// c' = c softplus(lam) of a lane's CH channels, formed once per workgroup:
+// the waves w < CH form channel 64 w + lane of the tile from lv (its lam,
+// loaded by every wave before the step inputs) into sC; after a workgroup
+// barrier each lane reads its own.  Channels past D read 0.
+template <int CH, bool GATED>
+__device__ __forceinline__ void tile_csp(float lv, float gc, int w, int lane, bool cok, float* sC, float (&csp)[CH]) {
+  if constexpr (GATED) {
+    if (w < CH) sC[64 * w + lane] = gc * softplus_f(lv);
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < CH; ++c) csp[c] = cok ? sC[lane * CH + c] : 0.f;
+  } else {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) csp[c] = 0.f;
+  }
+}
+
+// A wave's U steps of the scan inputs.  Plain: pa = a, px = x.  Gated:
+// pa = r, px = x, pi = i, and the fp32 gates av = a, sv = sqrt(1 - a^2),
+// sr = sigmoid(r).  Steps past L or D are identity steps (a = 1, x' = 0).
+// rb: element offset of the wave's first step row (uniform), so step u of
+// channel ch is at rb + u D + ch.  issue_steps loads every step in every lane
+// at a clamped step and channel (in bounds); finish_steps, called once all
+// of the wave's loads are issued, gives masked positions the identity values
+// and forms the gates.
+__device__ __forceinline__ uint32_t step_off(int u, int t0, int L, int D, int chc) {
+  return (uint32_t)((min(t0 + u, L - 1) - min(t0, L - 1)) * D + chc);   // the step clamped to L - 1
+}
 template <typename InT, int CH, int U, bool GATED>
-__device__ __forceinline__ void load_steps(const InT* a, const InT* x, const InT* gi, const float (&csp)[CH],
-                                           bool cok, int t0, int L, int64_t row0, int D, int ch,
-                                           Pack<InT, CH> (&pa)[U], Pack<InT, CH> (&px)[U],
-                                           Pack<InT, CH> (&pi)[GATED ? U : 1], float (&av)[GATED ? U : 1][CH],
-                                           float (&sv)[GATED ? U : 1][CH]) {
+__device__ __forceinline__ void issue_steps(const InT* a, const InT* x, const InT* gi, int t0, int L, int64_t rb,
+                                            int D, int chc, Pack<InT, CH> (&pa)[U], Pack<InT, CH> (&px)[U],
+                                            Pack<InT, CH> (&pi)[GATED ? U : 1]) {
+  const InT* const aw = a + rb;
+  const InT* const xw = x + rb;
+  const InT* const iw = GATED ? gi + rb : nullptr;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int t = t0 + u;
-    if (cok && t < L) {
-      const int64_t i = (row0 + t) * D + ch;
-      pa[u] = ld_pack<InT, CH>(a, i);
-      px[u] = ld_pack<InT, CH>(x, i);
-      if constexpr (GATED) pi[u] = ld_pack<InT, CH>(gi, i);
-    } else {   // identity step
-      pa[u] = pack_fill<InT, CH>(1.f);
-      px[u] = pack_fill<InT, CH>(0.f);
-      if constexpr (GATED) pi[u] = pack_fill<InT, CH>(0.f);
-    }
+    const uint32_t i = step_off(u, t0, L, D, chc);
+    pa[u] = rr::tiles::ld_pack_at<InT, CH>(aw, i);
+    px[u] = rr::tiles::ld_pack_at<InT, CH>(xw, i);
+    if constexpr (GATED) pi[u] = rr::tiles::ld_pack_at<InT, CH>(iw, i);
+  }
+}
+template <typename InT, int CH, int U, bool GATED>
+__device__ __forceinline__ void finish_steps(const float (&csp)[CH], bool cok, int t0, int L,
+                                             Pack<InT, CH> (&pa)[U], Pack<InT, CH> (&px)[U],
+                                             Pack<InT, CH> (&pi)[GATED ? U : 1], float (&av)[GATED ? U : 1][CH],
+                                             float (&sv)[GATED ? U : 1][CH], float (&sr)[GATED ? U : 1][CH]) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {   // identity steps past L or D
+    const bool ok = cok && t0 + u < L;
+    pa[u] = rr::tiles::pick<InT, CH>(ok, pa[u], pack_fill<InT, CH>(1.f));
+    px[u] = rr::tiles::pick<InT, CH>(ok, px[u], pack_fill<InT, CH>(0.f));
+    if constexpr (GATED) pi[u] = rr::tiles::pick<InT, CH>(ok, pi[u], pack_fill<InT, CH>(0.f));
   }
   if constexpr (GATED) {
 #pragma unroll
@@ -97,7 +132,8 @@ __device__ __forceinline__ void load_steps(const InT* a, const InT* x, const InT
       const bool ok = cok && t0 + u < L;
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
-        gate(pa[u][c], csp[c], av[u][c], sv[u][c]);
+        sr[u][c] = sigmoid_f(pa[u][c]);
+        gate_s(sr[u][c], csp[c], av[u][c], sv[u][c]);
         if (!ok) av[u][c] = 1.f, sv[u][c] = 0.f;
       }
     }
@@ -113,8 +149,9 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_fwd_kernel(
   constexpr int GCH = 64 * CH, S = U * kNW;
   __shared__ float sP[kNW][GCH], sE[kNW][GCH];
   __shared__ float sIn[GCH];
+  __shared__ float sC[GATED ? GCH : 1];
   __shared__ int sTicket;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   // tickets run over step tiles slowest, so the tile before (same channels,
   // previous steps) always holds a smaller ticket
   const int nGrp = B * G;
@@ -127,13 +164,18 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_fwd_kernel(
   const bool cok = ch < D;
   const int t0 = k * S + w * U;
   const int64_t row0 = (int64_t)b * L;
+  // the wave's first step row (clamped: a wave wholly past L touches nothing)
+  const int64_t rb = (row0 + min(t0, L - 1)) * D;
 
-  float csp[CH];
-#pragma unroll
-  for (int c = 0; c < CH; ++c) csp[c] = GATED && cok ? gc * softplus_f(glam[ch + c]) : 0.f;
+  // every load first (clamped channel: every lane loads), then masks and gates
+  const int chc = min(ch, D - CH);
+  const float lv = GATED ? glam[min(g * GCH + 64 * (w % CH) + lane, D - 1)] : 0.f;
   Pack<InT, CH> pa[U], px[U], pi[GATED ? U : 1];
-  float av[GATED ? U : 1][CH], sv[GATED ? U : 1][CH];
-  load_steps<InT, CH, U, GATED>(a, x, gi, csp, cok, t0, L, row0, D, ch, pa, px, pi, av, sv);
+  issue_steps<InT, CH, U, GATED>(a, x, gi, t0, L, rb, D, chc, pa, px, pi);
+  float csp[CH];
+  tile_csp<CH, GATED>(lv, gc, w, lane, cok, sC, csp);
+  float av[GATED ? U : 1][CH], sv[GATED ? U : 1][CH], sr[GATED ? U : 1][CH];
+  finish_steps<InT, CH, U, GATED>(csp, cok, t0, L, pa, px, pi, av, sv, sr);
   // the step's decay and input
   auto A = [&](int u, int c) -> float {
     if constexpr (GATED) return av[u][c];
@@ -188,8 +230,8 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_fwd_kernel(
 #pragma unroll
     for (int c = 0; c < CH; ++c) h[c] = A(u, c) * h[c] + X(u, c);   // rglru.py:92
     if (cok && t < L) {
-      rr::tiles::st_f32<CH>(y, (row0 + t) * D + ch, h);
-      if ((t + 1) % T == 0) rr::tiles::st_f32<CH>(ckpt, ((int64_t)b * nC + (t + 1) / T - 1) * D + ch, h);
+      rr::tiles::st_f32_at<CH>(y + rb, (uint32_t)(u * D + ch), h);
+      if ((t + 1) % T == 0) rr::tiles::st_f32_at<CH>(ckpt + ((int64_t)b * nC + (t + 1) / T - 1) * D, (uint32_t)ch, h);
     }
   }
 }
@@ -208,8 +250,9 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_bwd_kernel(
   __shared__ float sP[kNW][GCH], sEf[kNW][GCH], sEb[kNW][GCH];
   __shared__ float sD[GATED ? kNW : 1][GCH];
   __shared__ float sIn[GCH];
+  __shared__ float sC[GATED ? GCH : 1];
   __shared__ int sTicket;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   // step tiles are taken from the end: the tile after (same channels, later
   // steps) always holds a smaller ticket
   const int nGrp = B * G;
@@ -222,26 +265,39 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_bwd_kernel(
   const bool cok = ch < D;
   const int t0 = k * S + w * U;
   const int64_t row0 = (int64_t)b * L;
+  // the wave's first step row (clamped: a wave wholly past L touches nothing)
+  const int64_t rb = (row0 + min(t0, L - 1)) * D;
 
+  // every load first (clamped channel: every lane loads), then masks and
+  // gates: dy, the inputs, lam, and the state entering the wave's checkpoint
+  // interval (checkpoint row crow, or h0 at tb = 0, or zero: then any valid
+  // row is read and dropped)
+  const int chc = min(ch, D - CH);
+  const float lv = GATED ? glam[min(g * GCH + 64 * (w % CH) + lane, D - 1)] : 0.f;
+  Pack<float, CH> g2[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) g2[u] = rr::tiles::ld_pack_at<float, CH>(dy + rb, step_off(u, t0, L, D, chc));
+  Pack<InT, CH> pa[U], px[U], pi[GATED ? U : 1];
+  issue_steps<InT, CH, U, GATED>(a, x, gi, t0, L, rb, D, chc, pa, px, pi);
+  const int tb = t0 - t0 % T;
+  const int crow = rr::tiles::bwd_ckpt_row(t0, T, L);
+  const bool from_h0 = crow < 0 && tb == 0 && h0 != nullptr;
+  const bool huse = crow >= 0 || from_h0;
+  const float* const hsrc = crow >= 0 ? ckpt + ((int64_t)b * nC + crow) * D : (from_h0 ? h0 + (int64_t)b * D : ckpt);
+  float hin[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) hin[c] = hsrc[chc + c];
   float gy[U][CH];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int t = t0 + u;
-    if (cok && t < L) {
-      const Pack<float, CH> g2 = ld_pack<float, CH>(dy, (row0 + t) * D + ch);
+    g2[u] = rr::tiles::pick<float, CH>(cok && t0 + u < L, g2[u], pack_fill<float, CH>(0.f));
 #pragma unroll
-      for (int c = 0; c < CH; ++c) gy[u][c] = g2[c];
-    } else {
-#pragma unroll
-      for (int c = 0; c < CH; ++c) gy[u][c] = 0.f;
-    }
+    for (int c = 0; c < CH; ++c) gy[u][c] = g2[u][c];
   }
   float csp[CH];
-#pragma unroll
-  for (int c = 0; c < CH; ++c) csp[c] = GATED && cok ? gc * softplus_f(glam[ch + c]) : 0.f;
-  Pack<InT, CH> pa[U], px[U], pi[GATED ? U : 1];
-  float av[GATED ? U : 1][CH], sv[GATED ? U : 1][CH];
-  load_steps<InT, CH, U, GATED>(a, x, gi, csp, cok, t0, L, row0, D, ch, pa, px, pi, av, sv);
+  tile_csp<CH, GATED>(lv, gc, w, lane, cok, sC, csp);
+  float av[GATED ? U : 1][CH], sv[GATED ? U : 1][CH], sr[GATED ? U : 1][CH];
+  finish_steps<InT, CH, U, GATED>(csp, cok, t0, L, pa, px, pi, av, sv, sr);
   auto A = [&](int u, int c) -> float {
     if constexpr (GATED) return av[u][c];
     else return pa[u][c];
@@ -292,16 +348,10 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_bwd_kernel(
   // state entering this wave's steps: checkpoint at the start of the
   // checkpoint interval, then the earlier waves of the interval (the tile
   // holds whole intervals: S is a multiple of 32 >= T)
-  const int tb = t0 - t0 % T;
-  const int crow = rr::tiles::bwd_ckpt_row(t0, T, L);
-  float hin[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    hin[c] = 0.f;
-    if (cok) {
-      if (crow >= 0) hin[c] = ckpt[((int64_t)b * nC + crow) * D + ch + c];
-      else if (tb == 0 && h0 != nullptr) hin[c] = h0[(int64_t)b * D + ch + c];
-    }
+    asm volatile("" : "+v"(hin[c]));
+    hin[c] = huse && cok ? hin[c] : 0.f;
     for (int j = w - (t0 - tb) / U; j < w; ++j) hin[c] = sP[j][lane * CH + c] * hin[c] + sEf[j][lane * CH + c];
   }
   // recompute the states (hs[u] = h_{t0+u}), then sweep the adjoint backwards
@@ -337,24 +387,26 @@ __global__ __launch_bounds__(64 * kNW, 4) void rglru_bwd_kernel(
       float gr[CH], gi2[CH], gxx[CH];
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
-        const float sr = sigmoid_f(pa[u][c]), iv = pi[u][c], xv = px[u][c], av_ = av[u][c], s = sv[u][c];
+        const float sg = sr[u][c], iv = pi[u][c], xv = px[u][c], av_ = av[u][c], s = sv[u][c];
         const float ds = gx[c] * (iv * xv);
-        const float dz = (ga[c] - (s > 0.f ? ds * av_ * __builtin_amdgcn_rcpf(s) : 0.f)) * av_;
-        gr[c] = dz * -csp[c] * (sr * (1.f - sr));
+        float q = ds * av_ * __builtin_amdgcn_rcpf(s);
+        asm volatile("" : "+v"(q));
+        const float dz = (ga[c] - (s > 0.f ? q : 0.f)) * av_;
+        gr[c] = dz * -csp[c] * (sg * (1.f - sg));
         gi2[c] = gx[c] * s * xv;
         gxx[c] = gx[c] * s * iv;
-        if (ok) dsum[c] += dz * sr;
+        if (ok) dsum[c] += dz * sg;
       }
       if (ok) {
-        const int64_t i = (row0 + t) * D + ch;
-        rr::tiles::st_pack<InT, CH>(da, i, gr);
-        rr::tiles::st_pack<InT, CH>(dgi, i, gi2);
-        rr::tiles::st_pack<InT, CH>(dx, i, gxx);
+        const uint32_t i = (uint32_t)(u * D + ch);
+        rr::tiles::st_pack_at<InT, CH>(da + rb, i, gr);
+        rr::tiles::st_pack_at<InT, CH>(dgi + rb, i, gi2);
+        rr::tiles::st_pack_at<InT, CH>(dx + rb, i, gxx);
       }
     } else if (ok) {
-      const int64_t i = (row0 + t) * D + ch;
-      rr::tiles::st_pack<InT, CH>(dx, i, gx);
-      rr::tiles::st_pack<InT, CH>(da, i, ga);
+      const uint32_t i = (uint32_t)(u * D + ch);
+      rr::tiles::st_pack_at<InT, CH>(dx + rb, i, gx);
+      rr::tiles::st_pack_at<InT, CH>(da + rb, i, ga);
     }
   }
   if constexpr (GATED) {   // the tile's dz * sigmoid(r) sums, waves added in order

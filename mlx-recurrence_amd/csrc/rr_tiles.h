@@ -116,6 +116,22 @@ __device__ __forceinline__ Pack<InT, N> ld_pack(const InT* p, int64_t i) {
   r.v = *reinterpret_cast<const decltype(r.v)*>(p + i);
   return r;
 }
+// v where ok, else alt.  The loaded words are pinned first, so the load they
+// come from stays unconditional (a load moved under a branch makes the
+// branch's join wait for every load in flight).
+template <typename InT, int N>
+__device__ __forceinline__ Pack<InT, N> pick(bool ok, Pack<InT, N> v, const Pack<InT, N>& alt) {
+  constexpr int W = (int)(sizeof(v.v) / 4);
+  uint32_t* pv = reinterpret_cast<uint32_t*>(&v.v);
+  const uint32_t* pa = reinterpret_cast<const uint32_t*>(&alt.v);
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    asm volatile("" : "+v"(pv[w]));
+    pv[w] = ok ? pv[w] : pa[w];
+  }
+  return v;
+}
+
 // The identity step of a masked (out-of-range) position: value `one` everywhere.
 template <typename InT, int N>
 __device__ __forceinline__ Pack<InT, N> pack_fill(float one) {
@@ -133,11 +149,27 @@ __device__ __forceinline__ Pack<InT, N> pack_fill(float one) {
   return r;
 }
 
+// The same accesses at a 32-bit element offset from a wave-uniform base (the
+// address is then one scalar base plus one 32-bit lane offset, no 64-bit
+// arithmetic per lane).
+template <typename InT, int N>
+__device__ __forceinline__ Pack<InT, N> ld_pack_at(const InT* base, uint32_t i) {
+  Pack<InT, N> r;
+  r.v = *reinterpret_cast<const decltype(r.v)*>(reinterpret_cast<const char*>(base) + i * (uint32_t)sizeof(InT));
+  return r;
+}
+
 // Stores N fp32 values (16 or 8 bytes) at [i, i + N).
 template <int N>
 __device__ __forceinline__ void st_f32(float* p, int64_t i, const float (&v)[N]) {
   if constexpr (N == 4) *reinterpret_cast<float4*>(p + i) = make_float4(v[0], v[1], v[2], v[3]);
   else *reinterpret_cast<float2*>(p + i) = make_float2(v[0], v[1]);
+}
+template <int N>
+__device__ __forceinline__ void st_f32_at(float* base, uint32_t i, const float (&v)[N]) {
+  float* p = reinterpret_cast<float*>(reinterpret_cast<char*>(base) + i * 4u);
+  if constexpr (N == 4) *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  else *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
 }
 // Stores N values in the input type at [i, i + N).
 template <typename InT, int N>
@@ -151,6 +183,11 @@ __device__ __forceinline__ void st_pack(InT* p, int64_t i, const float (&v)[N]) 
     if constexpr (N == 4) *reinterpret_cast<uint2*>(p + i) = make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16);
     else *reinterpret_cast<uint32_t*>(p + i) = h[0] | (uint32_t)h[1] << 16;
   }
+}
+template <typename InT, int N>
+__device__ __forceinline__ void st_pack_at(InT* base, uint32_t i, const float (&v)[N]) {
+  InT* p = reinterpret_cast<InT*>(reinterpret_cast<char*>(base) + i * (uint32_t)sizeof(InT));
+  st_pack<InT, N>(p, 0, v);
 }
 
 // ---------------------------------------------------------------- hand-off
@@ -191,7 +228,7 @@ __device__ __forceinline__ int take_ticket(uint32_t* counter, int ntiles, int* l
     *lds_slot = t < (uint32_t)ntiles ? (int)t : -1;
   }
   __syncthreads();
-  return *lds_slot;
+  return __builtin_amdgcn_readfirstlane(*lds_slot);   // uniform: tile indices and bases in scalar registers
 }
 
 // Clears the ticket counter and the hand-off slots of a pass (a template so
