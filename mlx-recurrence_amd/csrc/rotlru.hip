@@ -62,24 +62,35 @@ struct WaveIn {
   __device__ cplx xin(int u, int q) const { return {x[u][2 * q], x[u][2 * q + 1]}; }
 };
 
+// Step u of pair p sits at element rb + u Dp + p of a / cs / sn and at twice
+// that in x (rb: the wave's first step row, uniform).  issue_wave loads every
+// step in every lane at a clamped step and pair (in bounds); finish_wave,
+// called once all of the wave's loads are issued, gives the steps past L or
+// Dp the identity (z = 1, x = 0, theta = 0) and forms cos / sin of theta.
+__device__ __forceinline__ uint32_t step_off(int u, int t0, int L, int Dp, int pc) {
+  return (uint32_t)((min(t0 + u, L - 1) - min(t0, L - 1)) * Dp + pc);   // the step clamped to L - 1
+}
 template <typename InT, int U, bool TH>
-__device__ __forceinline__ void load_wave(WaveIn<InT, U, TH>& in, const InT* a, const InT* cs, const InT* sn,
-                                          const InT* x, int64_t row0, int t0, int L, int Dp, int p, bool pok) {
+__device__ __forceinline__ void issue_wave(WaveIn<InT, U, TH>& in, const InT* a, const InT* cs, const InT* sn,
+                                           const InT* x, int64_t rb, int t0, int L, int Dp, int pc) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int t = t0 + u;
-    if (pok && t < L) {
-      const int64_t ip = (row0 + t) * Dp + p;
-      in.a[u] = ld_pack<InT, kCP>(a, ip);
-      in.c[u] = ld_pack<InT, kCP>(cs, ip);
-      if constexpr (!TH) in.s[u] = ld_pack<InT, kCP>(sn, ip);
-      in.x[u] = ld_pack<InT, 2 * kCP>(x, 2 * ip);
-    } else {   // identity step: z = 1, x = 0 (theta = 0)
-      in.a[u] = pack_fill<InT, kCP>(1.f);
-      in.c[u] = pack_fill<InT, kCP>(TH ? 0.f : 1.f);
-      if constexpr (!TH) in.s[u] = pack_fill<InT, kCP>(0.f);
-      in.x[u] = pack_fill<InT, 2 * kCP>(0.f);
-    }
+    const uint32_t ip = step_off(u, t0, L, Dp, pc);
+    in.a[u] = rr::tiles::ld_pack_at<InT, kCP>(a + rb, ip);
+    in.c[u] = rr::tiles::ld_pack_at<InT, kCP>(cs + rb, ip);
+    if constexpr (!TH) in.s[u] = rr::tiles::ld_pack_at<InT, kCP>(sn + rb, ip);
+    in.x[u] = rr::tiles::ld_pack_at<InT, 2 * kCP>(x + 2 * rb, 2 * ip);
+  }
+}
+template <typename InT, int U, bool TH>
+__device__ __forceinline__ void finish_wave(WaveIn<InT, U, TH>& in, int t0, int L, bool pok) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const bool ok = pok && t0 + u < L;
+    in.a[u] = rr::tiles::pick<InT, kCP>(ok, in.a[u], pack_fill<InT, kCP>(1.f));
+    in.c[u] = rr::tiles::pick<InT, kCP>(ok, in.c[u], pack_fill<InT, kCP>(TH ? 0.f : 1.f));
+    if constexpr (!TH) in.s[u] = rr::tiles::pick<InT, kCP>(ok, in.s[u], pack_fill<InT, kCP>(0.f));
+    in.x[u] = rr::tiles::pick<InT, 2 * kCP>(ok, in.x[u], pack_fill<InT, 2 * kCP>(0.f));
   }
   if constexpr (TH) {
 #pragma unroll
@@ -99,7 +110,7 @@ __global__ __launch_bounds__(64 * kNW, 4) void rotlru_fwd_kernel(
   __shared__ cplx sP[kNW][GP], sE[kNW][GP];
   __shared__ cplx sIn[GP];
   __shared__ int sTicket;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nGrp = B * G;
   const int ticket = rr::tiles::take_ticket(counter, nGrp * K, &sTicket);
   if (ticket < 0) return;
@@ -111,9 +122,12 @@ __global__ __launch_bounds__(64 * kNW, 4) void rotlru_fwd_kernel(
   const int D = 2 * Dp;
   const int t0 = k * S + w * kU;
   const int64_t row0 = (int64_t)b * L;
+  const int64_t rb = (row0 + min(t0, L - 1)) * Dp;   // the wave's first step row (clamped)
+  const int pc = min(p, Dp - kCP);                    // clamped pair: every lane loads
 
   WaveIn<InT, kU, TH> in;
-  load_wave<InT, kU, TH>(in, a, cs, sn, x, row0, t0, L, Dp, p, pok);
+  issue_wave<InT, kU, TH>(in, a, cs, sn, x, rb, t0, L, Dp, pc);
+  finish_wave<InT, kU, TH>(in, t0, L, pok);
 #pragma unroll
   for (int q = 0; q < kCP; ++q) {
     cplx P{1.f, 0.f}, E{0.f, 0.f};
@@ -169,7 +183,7 @@ __global__ __launch_bounds__(64 * kNW, 4) void rotlru_fwd_kernel(
       out[2 * q + 1] = h[q].i;
     }
     if (pok && t < L) {
-      rr::tiles::st_f32<2 * kCP>(y, (row0 + t) * D + 2 * p, out);
+      rr::tiles::st_f32_at<2 * kCP>(y + 2 * rb, (uint32_t)(u * D + 2 * p), out);
       if ((t + 1) % T == 0) rr::tiles::st_f32<2 * kCP>(ckpt, ((int64_t)b * nC + (t + 1) / T - 1) * D + 2 * p, out);
     }
   }
@@ -191,7 +205,7 @@ __global__ __launch_bounds__(64 * kNW, 2) void rotlru_bwd_kernel(
   __shared__ cplx sP[kNW][GP], sEf[kNW][GP], sEb[kNW][GP];
   __shared__ cplx sIn[GP];
   __shared__ int sTicket;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nGrp = B * G;
   const int ticket = rr::tiles::take_ticket(counter, nGrp * K, &sTicket);
   if (ticket < 0) return;
@@ -203,21 +217,30 @@ __global__ __launch_bounds__(64 * kNW, 2) void rotlru_bwd_kernel(
   const int D = 2 * Dp;
   const int t0 = k * S + w * kU;
   const int64_t row0 = (int64_t)b * L;
+  const int64_t rb = (row0 + min(t0, L - 1)) * Dp;   // the wave's first step row (clamped)
+  const int pc = min(p, Dp - kCP);                    // clamped pair: every lane loads
 
+  // every load first: dy, the inputs, and the state entering the wave's
+  // checkpoint interval (checkpoint row crow, or h0 at tb = 0, or zero: then
+  // any valid row is read and dropped)
+  Pack<float, 2 * kCP> g4[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) g4[u] = rr::tiles::ld_pack_at<float, 2 * kCP>(dy + 2 * rb, 2 * step_off(u, t0, L, Dp, pc));
   WaveIn<InT, kU, TH> in;
-  load_wave<InT, kU, TH>(in, a, cs, sn, x, row0, t0, L, Dp, p, pok);
+  issue_wave<InT, kU, TH>(in, a, cs, sn, x, rb, t0, L, Dp, pc);
+  const int tb = t0 - t0 % T;   // start of the checkpoint interval (inside the tile: S % 32 == 0)
+  const int crow = rr::tiles::bwd_ckpt_row(t0, T, L);
+  const bool from_h0 = crow < 0 && tb == 0 && h0 != nullptr;
+  const bool huse = crow >= 0 || from_h0;
+  const float* const hsrc = crow >= 0 ? ckpt + ((int64_t)b * nC + crow) * D : (from_h0 ? h0 + (int64_t)b * D : ckpt);
+  Pack<float, 2 * kCP> h4 = rr::tiles::ld_pack_at<float, 2 * kCP>(hsrc, (uint32_t)(2 * pc));
+  finish_wave<InT, kU, TH>(in, t0, L, pok);
   cplx gy[kU][kCP];
 #pragma unroll
   for (int u = 0; u < kU; ++u) {
-    const int t = t0 + u;
-    if (pok && t < L) {
-      const Pack<float, 2 * kCP> g4 = ld_pack<float, 2 * kCP>(dy, (row0 + t) * D + 2 * p);
+    g4[u] = rr::tiles::pick<float, 2 * kCP>(pok && t0 + u < L, g4[u], pack_fill<float, 2 * kCP>(0.f));
 #pragma unroll
-      for (int q = 0; q < kCP; ++q) gy[u][q] = {g4[2 * q], g4[2 * q + 1]};
-    } else {
-#pragma unroll
-      for (int q = 0; q < kCP; ++q) gy[u][q] = {0.f, 0.f};
-    }
+    for (int q = 0; q < kCP; ++q) gy[u][q] = {g4[u][2 * q], g4[u][2 * q + 1]};
   }
   // forward map (from a zero state) and adjoint map (from a zero adjoint)
 #pragma unroll
@@ -265,18 +288,12 @@ __global__ __launch_bounds__(64 * kNW, 2) void rotlru_bwd_kernel(
   }
   __syncthreads();
   cplx lam[kCP], hin[kCP];
-  const int tb = t0 - t0 % T;   // start of the checkpoint interval (inside the tile: S % 32 == 0)
-  const int crow = rr::tiles::bwd_ckpt_row(t0, T, L);
+  h4 = rr::tiles::pick<float, 2 * kCP>(huse && pok, h4, pack_fill<float, 2 * kCP>(0.f));
 #pragma unroll
   for (int q = 0; q < kCP; ++q) {
     lam[q] = sIn[lane * kCP + q];
     for (int j = kNW - 1; j > w; --j) lam[q] = cfma(conj(sP[j][lane * kCP + q]), lam[q], sEb[j][lane * kCP + q]);
-    hin[q] = {0.f, 0.f};
-    if (pok) {
-      const int64_t e = 2 * (p + q);
-      if (crow >= 0) hin[q] = {ckpt[((int64_t)b * nC + crow) * D + e], ckpt[((int64_t)b * nC + crow) * D + e + 1]};
-      else if (tb == 0 && h0 != nullptr) hin[q] = {h0[(int64_t)b * D + e], h0[(int64_t)b * D + e + 1]};
-    }
+    hin[q] = {h4[2 * q], h4[2 * q + 1]};
     for (int j = w - (t0 - tb) / kU; j < w; ++j) hin[q] = cfma(sP[j][lane * kCP + q], hin[q], sEf[j][lane * kCP + q]);
   }
   cplx hs[kU][kCP];   // hs[u] = h_{t0+u}
@@ -307,18 +324,18 @@ __global__ __launch_bounds__(64 * kNW, 2) void rotlru_bwd_kernel(
       lam[q] = cmul(conj(in.z(u, q)), lam[q]);
     }
     if (pok && t < L) {
-      const int64_t ip = (row0 + t) * Dp + p;
-      rr::tiles::st_pack<InT, kCP>(da, ip, ga);
+      const uint32_t ip = (uint32_t)(u * Dp + p);
+      rr::tiles::st_pack_at<InT, kCP>(da + rb, ip, ga);
       if constexpr (TH) {   // d theta = -sin * dcos + cos * dsin
         float gt[kCP];
 #pragma unroll
         for (int q = 0; q < kCP; ++q) gt[q] = in.cosv(u, q) * gs[q] - in.sinv(u, q) * gc[q];
-        rr::tiles::st_pack<InT, kCP>(dcs, ip, gt);
+        rr::tiles::st_pack_at<InT, kCP>(dcs + rb, ip, gt);
       } else {
-        rr::tiles::st_pack<InT, kCP>(dcs, ip, gc);
-        rr::tiles::st_pack<InT, kCP>(dsn, ip, gs);
+        rr::tiles::st_pack_at<InT, kCP>(dcs + rb, ip, gc);
+        rr::tiles::st_pack_at<InT, kCP>(dsn + rb, ip, gs);
       }
-      rr::tiles::st_pack<InT, 2 * kCP>(dx, 2 * ip, gx);
+      rr::tiles::st_pack_at<InT, 2 * kCP>(dx + 2 * rb, 2 * ip, gx);
     }
   }
 }
