@@ -41,71 +41,97 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-// Loads 4 consecutive fp32 values at p[i..i+3] (columns c..c+3 of a row of
-// length n): one 16-byte access when VEC (rows a multiple of 4 long), else
-// element by element with the columns past n read as 0.
+// Loads the 4 consecutive fp32 values of a row at columns c .. c + 3 (row
+// length n): every lane loads, at columns clamped into the row, and columns
+// past n read as 0 (a select on the loaded registers; a load under a branch
+// makes the branch's join wait for every load in flight).  VEC: rows a
+// multiple of 4 long, one 16-byte access.
 template <bool VEC>
-__device__ __forceinline__ void ld4(const float* p, int64_t i, int c, int n, float (&v)[4]) {
+__device__ __forceinline__ void ld4(const float* row, int c, int n, float (&v)[4]) {
   if constexpr (VEC) {
-    if (c < n) {
-      const float4 q = *reinterpret_cast<const float4*>(p + i);
-      v[0] = q.x, v[1] = q.y, v[2] = q.z, v[3] = q.w;
-    } else {
-      v[0] = v[1] = v[2] = v[3] = 0.f;
-    }
+    const float4 q = *reinterpret_cast<const float4*>(row + min(c, n - 4));
+    v[0] = q.x, v[1] = q.y, v[2] = q.z, v[3] = q.w;
   } else {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = c + e < n ? p[i + e] : 0.f;
+    for (int e = 0; e < 4; ++e) v[e] = row[min(c + e, n - 1)];
+  }
+}
+__device__ __forceinline__ void mask4(int c, int n, float (&v)[4]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    asm volatile("" : "+v"(v[e]));
+    v[e] = c + e < n ? v[e] : 0.f;
   }
 }
 template <bool VEC>
-__device__ __forceinline__ void st4(float* p, int64_t i, int c, int n, const float (&v)[4]) {
+__device__ __forceinline__ void st4(float* row, int c, int n, const float (&v)[4]) {
   if constexpr (VEC) {
-    if (c < n) *reinterpret_cast<float4*>(p + i) = make_float4(v[0], v[1], v[2], v[3]);
+    if (c < n) *reinterpret_cast<float4*>(row + c) = make_float4(v[0], v[1], v[2], v[3]);
   } else {
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      if (c + e < n) p[i + e] = v[e];
+      if (c + e < n) row[c + e] = v[e];
   }
 }
 
 // ------------------------------------------------------------------ SSD
 // Lane l of a wave: column group col = l % G (states n = 4 col .. 4 col + 3),
-// row slot l / G; the workgroup walks the Dh rows 4 * (64 / G) at a time.
+// row slot l / G; the workgroup walks the Dh rows 4 * (64 / G) at a time, the
+// next row's u and state loaded while the current one is updated.
 template <typename InT, int G, bool VEC>
 __global__ __launch_bounds__(kThreads) void ssd_step_kernel(const InT* __restrict__ u, const InT* __restrict__ delta,
                                                             const InT* __restrict__ Bm, const InT* __restrict__ Cm,
                                                             const float* __restrict__ A, int a_sn, int H, int Dh,
                                                             int N, float* __restrict__ state, float* __restrict__ y) {
-  constexpr int kRowsPerWave = 64 / G;
+  constexpr int kRowsPerWave = 64 / G, kStep = kWaves * kRowsPerWave;
   const int bh = blockIdx.x, h = bh % H;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane % G, c0 = 4 * col;
+  float* S = state + (int64_t)bh * Dh * N;
+  // every load of the token and of the first row first (clamped indices)
   const float dt = rr::ld(delta, bh);
-  float dA[4], dB[4], Cn[4];
+  float Av[4], Bv[4], Cv[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const int n = c0 + e;
-    const bool ok = n < N;
-    const int nn = ok ? n : 0;
-    dA[e] = ok ? __expf(dt * A[(int64_t)h * (a_sn ? N : 1) + (int64_t)nn * a_sn]) : 0.f;
-    dB[e] = ok ? dt * rr::ld(Bm, (int64_t)bh * N + nn) : 0.f;
-    Cn[e] = ok ? rr::ld(Cm, (int64_t)bh * N + nn) : 0.f;
+    const int nn = min(c0 + e, N - 1);
+    Av[e] = A[(int64_t)h * (a_sn ? N : 1) + (int64_t)nn * a_sn];
+    Bv[e] = rr::ld(Bm, (int64_t)bh * N + nn);
+    Cv[e] = rr::ld(Cm, (int64_t)bh * N + nn);
   }
-  float* S = state + (int64_t)bh * Dh * N;
-  for (int d = wave * kRowsPerWave + lane / G; d < Dh; d += kWaves * kRowsPerWave) {
-    const float ud = rr::ld(u, (int64_t)bh * Dh + d);
-    float s[4];
-    ld4<VEC>(S, (int64_t)d * N + c0, c0, N, s);
+  int d = wave * kRowsPerWave + lane / G;
+  float ud = rr::ld(u, (int64_t)bh * Dh + min(d, Dh - 1));
+  float s[4];
+  ld4<VEC>(S + (int64_t)min(d, Dh - 1) * N, c0, N, s);
+  float dA[4], dB[4], Cn[4];
+  mask4(c0, N, Av);
+  mask4(c0, N, Bv);
+  mask4(c0, N, Cv);
+  mask4(c0, N, s);   // states past N read as 0 (they enter the row sum)
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    dA[e] = c0 + e < N ? __expf(dt * Av[e]) : 0.f;
+    dB[e] = dt * Bv[e];
+    Cn[e] = Cv[e];
+  }
+  for (; d < Dh; d += kStep) {
+    // the next row's loads (clamped; dropped past the last row)
+    const int dn = min(d + kStep, Dh - 1);
+    const float un = rr::ld(u, (int64_t)bh * Dh + dn);
+    float sn[4];
+    ld4<VEC>(S + (int64_t)dn * N, c0, N, sn);
     float acc = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       s[e] = dA[e] * s[e] + dB[e] * ud;   // ssd.py:97-98 for one step
       acc += s[e] * Cn[e];
     }
-    st4<VEC>(S, (int64_t)d * N + c0, c0, N, s);
+    st4<VEC>(S + (int64_t)d * N, c0, N, s);
     acc = group_sum<G>(acc);              // y[d] = sum_n h[d,n] C[n] (ssd.py:99-101)
     if (col == 0) y[(int64_t)bh * Dh + d] = acc;
+    ud = un;
+    mask4(c0, N, sn);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s[e] = sn[e];
   }
 }
 
@@ -115,30 +141,41 @@ __global__ __launch_bounds__(kThreads) void ssd_step_kernel(const InT* __restric
 // waves (LDS) in a fixed order.
 template <typename InT, int G, bool VEC>
 __global__ __launch_bounds__(kThreads) void gla_step_kernel(const InT* __restrict__ q, const InT* __restrict__ k,
-                                                            const InT* __restrict__ v, const InT* __restrict__ gates,
-                                                            int Dh, float* __restrict__ state,
-                                                            float* __restrict__ y) {
-  constexpr int kRowsPerWave = 64 / G;
+                                                                  const InT* __restrict__ v, const InT* __restrict__ gates,
+                                                                  int Dh, float* __restrict__ state,
+                                                                  float* __restrict__ y) {
+  constexpr int kRowsPerWave = 64 / G, kStep = kWaves * kRowsPerWave;
   __shared__ float part[kWaves][4 * G];
   const int bh = blockIdx.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane % G, c0 = 4 * col;
+  float* S = state + (int64_t)bh * Dh * Dh;
+  // every load of the token and of the first row first (clamped indices)
   const float g = rr::ld(gates, bh);
   float vj[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) vj[e] = c0 + e < Dh ? rr::ld(v, (int64_t)bh * Dh + c0 + e) : 0.f;
-  float* S = state + (int64_t)bh * Dh * Dh;
+  for (int e = 0; e < 4; ++e) vj[e] = rr::ld(v, (int64_t)bh * Dh + min(c0 + e, Dh - 1));
+  int i = wave * kRowsPerWave + lane / G;
+  float ki = rr::ld(k, (int64_t)bh * Dh + min(i, Dh - 1)), qi = rr::ld(q, (int64_t)bh * Dh + min(i, Dh - 1));
+  float s[4];
+  ld4<VEC>(S + (int64_t)min(i, Dh - 1) * Dh, c0, Dh, s);
+  mask4(c0, Dh, vj);
   float o[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int i = wave * kRowsPerWave + lane / G; i < Dh; i += kWaves * kRowsPerWave) {
-    const float ki = rr::ld(k, (int64_t)bh * Dh + i), qi = rr::ld(q, (int64_t)bh * Dh + i);
-    float s[4];
-    ld4<VEC>(S, (int64_t)i * Dh + c0, c0, Dh, s);
+  for (; i < Dh; i += kStep) {
+    // the next row's loads (clamped; dropped past the last row)
+    const int in = min(i + kStep, Dh - 1);
+    const float kn = rr::ld(k, (int64_t)bh * Dh + in), qn = rr::ld(q, (int64_t)bh * Dh + in);
+    float sn[4];
+    ld4<VEC>(S + (int64_t)in * Dh, c0, Dh, sn);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       s[e] = g * s[e] + ki * vj[e];       // gla.py:86-87 for one step
       o[e] += qi * s[e];
     }
-    st4<VEC>(S, (int64_t)i * Dh + c0, c0, Dh, s);
+    st4<VEC>(S + (int64_t)i * Dh, c0, Dh, s);
+    ki = kn, qi = qn;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s[e] = sn[e];
   }
   // column sums: over the row slots of the wave (lanes col, col + G, ...) ...
 #pragma unroll

@@ -41,6 +41,7 @@ SSD_CASES = [
     (2, 12, 2, 96, 128, F16, True, 2),
     (1, 8, 2, 32, 256, F32, False, 3),      # N = 256: 64 lanes per row
     (8, 3, 80, 64, 128, BF16, True, 4),     # BASELINE config 4's state [8, 80, 64, 128]
+    (1, 6, 2, 32, 24, F32, True, 5),        # N = 24: 8 lane groups, the last two past N
 ]
 
 
@@ -72,6 +73,8 @@ GLA_CASES = [
     (1, 16, 2, 24, F32, 11),     # Dh not a multiple of 4 (scalar rows)
     (1, 12, 2, 128, F16, 12),
     (1, 6, 1, 256, F32, 13),     # Dh = 256: 64 lanes per row
+    (1, 8, 2, 20, F32, 14),      # Dh = 20: lane groups past Dh
+    (1, 8, 2, 18, BF16, 15),     # Dh = 18: scalar rows, lane groups past Dh
 ]
 
 
