@@ -708,42 +708,58 @@ __global__ __launch_bounds__(64 * kGW) void gdn_cgrad_kernel(const float* __rest
     const uint16_t* vp = v + (row0 * H + h) * kD;
     const uint16_t* qp = q + (row0 * H + h) * kD;
     const float* dp = dy + (row0 * H + h) * kD;
-    if (tid < 256) {   // 32 rows x 8 pieces of 8 elements
-      const int r = tid >> 3, c8 = 8 * (tid & 7);
-      const u16x8_t kx = *reinterpret_cast<const u16x8_t*>(kp + r * rs + c8);
-      const u16x8_t vx = *reinterpret_cast<const u16x8_t*>(vp + r * rs + c8);
-      const u16x8_t qx = *reinterpret_cast<const u16x8_t*>(qp + r * rs + c8);
-      const float4 d0 = *reinterpret_cast<const float4*>(dp + r * rs + c8);
-      const float4 d1 = *reinterpret_cast<const float4*>(dp + r * rs + c8 + 4);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        sm.k[r][c8 + e] = bfv(kx[e]);
-        sm.v[r][c8 + e] = bfv(vx[e]);
-        sm.q[r][c8 + e] = bfv(qx[e]);
-      }
-      *reinterpret_cast<float4*>(&sm.dO[r][c8]) = d0;
-      *reinterpret_cast<float4*>(&sm.dO[r][c8 + 4]) = d1;
-    }
-    // S_in: checkpoint c - 1, else h0, else zero; dS_out: adjoint checkpoint c
-    const float* sp = c > 0 ? ckpt + ((int64_t)bh * nC + c - 1) * kD * kD
-                            : (h0 != nullptr ? h0 + (int64_t)bh * kD * kD : nullptr);
+    // every load first, unconditional (a load under a branch makes the
+    // branch's join wait for every load in flight): the chunk's rows (32 rows
+    // x 8 pieces of 8 elements; threads >= 256 repeat rows 0-31 and drop
+    // them), S_in (checkpoint c - 1, else h0, else zero: a valid matrix read
+    // and dropped), dS_out (adjoint checkpoint c), alpha and beta
+    const int r8 = (tid >> 3) & (kQ - 1), c8 = 8 * (tid & 7);
+    const u16x8_t kx = *reinterpret_cast<const u16x8_t*>(kp + r8 * rs + c8);
+    const u16x8_t vx = *reinterpret_cast<const u16x8_t*>(vp + r8 * rs + c8);
+    const u16x8_t qx = *reinterpret_cast<const u16x8_t*>(qp + r8 * rs + c8);
+    const float4 d0 = *reinterpret_cast<const float4*>(dp + r8 * rs + c8);
+    const float4 d1 = *reinterpret_cast<const float4*>(dp + r8 * rs + c8 + 4);
     const float* ap = adjck + ((int64_t)bh * nC + c) * kD * kD;
-    float dot = 0.f;   // <dS_out, S_in>, this thread's share
+    const bool has_s = c > 0 || h0 != nullptr;
+    const float* sp = c > 0 ? ckpt + ((int64_t)bh * nC + c - 1) * kD * kD
+                            : (h0 != nullptr ? h0 + (int64_t)bh * kD * kD : ap);
+    float4 sv[2], av[2];
 #pragma unroll
     for (int it = 0; it < 2; ++it) {   // 64 x 64: 1024 float4, two passes
       const int i = tid + 512 * it, r = i >> 4, c4 = 4 * (i & 15);
-      const float4 sv = sp != nullptr ? *reinterpret_cast<const float4*>(sp + r * kD + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float4 av = *reinterpret_cast<const float4*>(ap + r * kD + c4);
-      *reinterpret_cast<float4*>(&sm.sin[r][c4]) = sv;
-      *reinterpret_cast<float4*>(&sm.dso[r][c4]) = av;
-      dot += (sv.x * av.x + sv.y * av.y) + (sv.z * av.z + sv.w * av.w);
+      sv[it] = *reinterpret_cast<const float4*>(sp + r * kD + c4);
+      av[it] = *reinterpret_cast<const float4*>(ap + r * kD + c4);
+    }
+    const int tq = tid & (kQ - 1);
+    const float alv = bfv(alpha[(row0 + tq) * H + h]), bev = bfv(beta[(row0 + tq) * H + h]);
+    if (tid < 256) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sm.k[r8][c8 + e] = bfv(kx[e]);
+        sm.v[r8][c8 + e] = bfv(vx[e]);
+        sm.q[r8][c8 + e] = bfv(qx[e]);
+      }
+      *reinterpret_cast<float4*>(&sm.dO[r8][c8]) = d0;
+      *reinterpret_cast<float4*>(&sm.dO[r8][c8 + 4]) = d1;
+    }
+    float dot = 0.f;   // <dS_out, S_in>, this thread's share
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int i = tid + 512 * it, r = i >> 4, c4 = 4 * (i & 15);
+      float4 s4 = sv[it];
+      asm volatile("" : "+v"(s4.x), "+v"(s4.y), "+v"(s4.z), "+v"(s4.w));
+      if (!has_s) s4 = make_float4(0.f, 0.f, 0.f, 0.f);   // uniform
+      const float4 a4 = av[it];
+      *reinterpret_cast<float4*>(&sm.sin[r][c4]) = s4;
+      *reinterpret_cast<float4*>(&sm.dso[r][c4]) = a4;
+      dot += (s4.x * a4.x + s4.y * a4.y) + (s4.z * a4.z + s4.w * a4.w);
     }
     dot = rr::wave_sum(dot);
     if (lane == 0) sm.dotp[w] = dot;
     if (tid < kQ) {
-      const float al = fmaxf(bfv(alpha[(row0 + tid) * H + h]), 1e-30f);   // alpha = 0 taken as 1e-30
+      const float al = fmaxf(alv, 1e-30f);   // alpha = 0 taken as 1e-30
       sm.al[tid] = al;
-      sm.beta[tid] = bfv(beta[(row0 + tid) * H + h]);
+      sm.beta[tid] = bev;
       sm.lg[tid] = __logf(al);   // prefix-summed below
     }
   }
