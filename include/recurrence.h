@@ -87,7 +87,8 @@ int64_t rr_tile_schedule(int scan, int pass, int64_t B, int64_t L, int64_t D, in
  * u [B,L,H,Dh], delta [B,L,H], Bm/Cm [B,L,H,N] (dtype); A_neg fp32, element
  * (h, n) at A_neg[h * (A_stride_n ? N : 1) + n * A_stride_n]: A_stride_n = 1 for a
  * dense [H,N] array, 0 for one rate per head broadcast over N (Mamba-2's A,
- * the BASELINE configurations; these calls run on the chunked MFMA kernels).
+ * as in the benchmarked SSD configurations; these calls run on the chunked
+ * MFMA kernels).
  * y [B,L,H,Dh] fp32.  ckpt [B,H,nC,Dh,N] fp32, nC = L/T: the state after the
  * last step of each chunk (ckpt[:,:,nC-1] is the final state [B,H,Dh,N]).
  * h0 / dfinal / dh0: [B,H,Dh,N] fp32 (the Mamba-2 state layout of

@@ -24,7 +24,7 @@ using rr::tiles::Pack;
 using rr::tiles::ld_pack;
 using rr::tiles::pack_fill;
 
-// Tile shapes (measured on MI355X at BASELINE config 3): CH = 2 channels per
+// Tile shapes (measured on MI355X at B8 L4096 D2560): CH = 2 channels per
 // lane; U steps per wave: forward 16 for 16-bit inputs, otherwise 8 (the
 // backward also holds dy and the recomputed states; the gated passes hold
 // the gates in fp32, the gated backward 4 steps); NW = 8 waves, two

@@ -1,7 +1,7 @@
 // ssd_chunked.hip — SSD scan with a head-uniform decay rate on bf16 MFMA.
 //
-// When A_neg[h, n] is the same for every n (Mamba-2's per-head A, the BASELINE
-// configurations), the decay from step s to step t of a chunk is one scalar
+// When A_neg[h, n] is the same for every n (Mamba-2's per-head A, as in the
+// benchmarked SSD configurations), the decay from step s to step t of a chunk is one scalar
 // per head, M[t, s] = exp(a (cd_t - cd_s)) (cd = in-chunk cumulative delta), and
 // a 32-step chunk of the recurrence (reference ssd.py:85-111) becomes dense
 // products (the "SSD dual" form, rr_chunked.h).  The forward kernels are the
