@@ -23,9 +23,10 @@ the stream it runs on; achieved = algorithmic bytes of the kernel's pass
 the workload) / that kernel's average duration (which therefore includes the
 dispatch gap between dependent launches).
 
-CPU baseline: the float64 oracle (oracle/recurrence_oracle.py, forward +
-explicit adjoint) on the same workload's shape, on the host cores, rank 0
-only, over a bounded sample.
+CPU baseline: the reference's CPU path as this package restates it — the fp32
+torch per-step *_scan_reference loop, forward + autograd backward — on the same
+input values, on the host cores (affinity mask, capped by OMP_NUM_THREADS),
+rank 0 only, over a bounded sample of the workload (see cpu_baseline).
 
 One GPU only: --gpus N > 1 exits with a message.
 """

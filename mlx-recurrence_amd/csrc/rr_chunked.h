@@ -742,8 +742,13 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
   const int cnt = j1 - j0;
   const int nw = cnt > w ? (cnt - w + 3) / 4 : 0;   // this wave's chunks (uniform per wave)
   const float neutral = GLA ? 1.f : 0.f;
-  // chunk k of this wave, clamped into the range (surplus loads repeat a
-  // needed chunk; with an empty range, this workgroup's own chunk)
+  // chunk k of this wave, clamped into the range (with an empty range, this
+  // workgroup's own chunk).  Every wave issues the loads of kDirectPerWave
+  // chunks whatever its count nw, so that every path has the same loads in
+  // flight and the waits for a slot stay exact; a surplus chunk's loads
+  // (k >= nw, never read) take one address in every lane (`on` = 0 drops the
+  // lane's part of the offset): one cache line per load instead of a chunk's
+  // worth of L2 traffic in the start-up burst of every workgroup.
   auto chunk = [&](int k) { return cnt > 0 ? min(j0 + w + 4 * k, j1 - 1) : c; };
 
   // 1. step inputs of this wave's chunks, then the operands of the first PF
@@ -751,36 +756,39 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
 #pragma unroll
   for (int k = 0; k < kDirectPerWave; ++k) {
     const int64_t row0 = (int64_t)b * p.L + (int64_t)chunk(k) * Q;
-    xs[k] = bf_val(p.delta[(row0 + (lane & (Q - 1))) * rowH + h]);   // lanes >= 32 masked below
+    const int tl = k < nw ? lane & (Q - 1) : 0;
+    xs[k] = bf_val(p.delta[(row0 + tl) * rowH + h]);   // lanes >= 32 masked below
   }
   // forward: U rows as 16-byte pieces; backward: dY in the A-operand layout
   // of 16x16x32, lane (j, g) = (lane % 16, lane / 16) holding dY[8 g + e][16 db + j]
   u16x8_t xu[PF][BWD ? 1 : XV], yv[PF][YV];
   float xg[PF][BWD ? NBD : 1][BWD ? 8 : 1];
   const int jl = lane & 15, gl = lane >> 4;
-  auto load = [&](int slot, int j) {
-    const int64_t row0 = (int64_t)b * p.L + (int64_t)j * Q;
+  auto load = [&](int slot, int k) {
+    const int64_t row0 = (int64_t)b * p.L + (int64_t)chunk(k) * Q;
+    const int on = k < nw ? 1 : 0;   // wave-uniform
     if constexpr (BWD) {
+      const int64_t lo = on * ((int64_t)8 * gl * rowH * DH + jl);
 #pragma unroll
       for (int db = 0; db < NBD; ++db)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xg[slot][db][e] = p.dy[((row0 + 8 * gl + e) * rowH + h) * DH + 16 * db + jl];
+        for (int e = 0; e < 8; ++e) xg[slot][db][e] = p.dy[((row0 + e) * rowH + h) * DH + 16 * db + lo];
     } else {
 #pragma unroll
       for (int v = 0; v < XV; ++v) {
-        const int i = lane + 64 * v, t = i / (DH / 8), d0 = 8 * (i % (DH / 8));
+        const int i = on * (lane + 64 * v), t = i / (DH / 8), d0 = 8 * (i % (DH / 8));
         xu[slot][v] = *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + t) * rowH + h) * DH + d0);
       }
     }
     const uint16_t* ysrc = BWD ? p.Cm : p.Bm;
 #pragma unroll
     for (int v = 0; v < YV; ++v) {
-      const int i = lane + 64 * v, t = i / (NS / 8), n0 = 8 * (i % (NS / 8));
+      const int i = on * (lane + 64 * v), t = i / (NS / 8), n0 = 8 * (i % (NS / 8));
       yv[slot][v] = *reinterpret_cast<const u16x8_t*>(ysrc + ((row0 + t) * rowH + h) * NS + n0);
     }
   };
 #pragma unroll
-  for (int k = 0; k < PF; ++k) load(k, chunk(k));
+  for (int k = 0; k < PF; ++k) load(k, k);
 #pragma unroll
   for (int k = 0; k < kDirectPerWave; ++k) rr::pin(xs[k]);   // waits for the step inputs only
 
@@ -862,10 +870,9 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
         }
       }
       // the registers of this slot are free: the loads of chunk k + PF
-      // (issued even past this wave's last chunk, as a repeat of it, so that
-      // the number of loads in flight is the same on every path and the
-      // waits for a slot stay exact)
-      if (k + PF < kDirectPerWave) load(slot, chunk(k + PF));
+      // (issued even past this wave's last chunk, as single-address surplus
+      // loads, so that the waits for a slot stay exact)
+      if (k + PF < kDirectPerWave) load(slot, k + PF);
     } else {
 #pragma unroll
       for (int v = 0; v < XV; ++v) {
@@ -885,7 +892,7 @@ __device__ float direct_sum(const ChunkArgs& p, int c, int b, int h, float a, Di
         *reinterpret_cast<u16x8_t*>(&st.Y[BWD ? 0 : 1][S::SY::off(t, n0)]) = lo;
       }
       // the registers of this slot are free: the loads of chunk k + PF (see above)
-      if (k + PF < kDirectPerWave) load(slot, chunk(k + PF));
+      if (k + PF < kDirectPerWave) load(slot, k + PF);
       wave_lds_sync();
       u16x8_t yf[2][NBN];
 #pragma unroll
