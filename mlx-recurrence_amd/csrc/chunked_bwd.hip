@@ -38,7 +38,14 @@
 //
 // Modes as in the forward: kWhole (a head per workgroup, lam carried in
 // registers from chunk to chunk), kPipe (lam from pass_kernel), kDirect (lam
-// from the direct sum; the workgroup of chunk 0 also forms dh0).
+// from the direct sum; the workgroup of chunk 0 also forms dh0), kPair (a
+// workgroup per pair of chunks, lam of the pair's last chunk from the
+// adjoint scan, which stores every second adjoint only; the workgroup forms
+// the adjoint entering the pair's first chunk itself, in the layouts of both
+// of its uses: the column blocks, lam_prev = gam_31 lam + (gam o dY)^T C,
+// at the end of phase B1 while dY is staged, and du's operand rows, the
+// same sum transposed, C^T diag(gam) dY, in phase C).
+#include <type_traits>
 #include <utility>
 
 #include "rr_chunked.h"
@@ -57,6 +64,7 @@ using rr::mfma32;
 using rr::u16x4_t;
 using rr::u16x8_t;
 using rr::chunked::kDirect;
+using rr::chunked::kPair;
 using rr::chunked::kPipe;
 using rr::chunked::kWhole;
 using rr::chunked::PQ;
@@ -112,7 +120,8 @@ union ColBwdShared<DH, NS, kDirect, GLA> {
 // Workgroups per CU the LDS allows (the register budget follows); SSD's
 // direct mode (short sequences, few workgroups) keeps the registers of two.
 template <int DH, int NS, int MODE, bool GLA>
-constexpr int kColBwdWgs = (int)(160 * 1024 / sizeof(ColBwdShared<DH, NS, MODE, GLA>)) >= 3 && (GLA || MODE != kDirect) ? 3
+constexpr int kColBwdWgs = MODE == kPair ? 2   // the carried du operands: the registers of two
+                           : (int)(160 * 1024 / sizeof(ColBwdShared<DH, NS, MODE, GLA>)) >= 3 && (GLA || MODE != kDirect) ? 3
                            : (int)(160 * 1024 / sizeof(ColBwdShared<DH, NS, MODE, GLA>)) >= 2                          ? 2
                                                                                                                       : 1;
 
@@ -127,6 +136,10 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
   int h, b, cbeg, cend;
   if constexpr (MODE == kWhole) {
     h = blockIdx.y, b = blockIdx.z, cbeg = 0, cend = p.nC;
+  } else if constexpr (MODE == kPair) {
+    const rr::chunked::ChunkId id = rr::chunked::pair_id(p);
+    if (!id.valid) return;
+    h = id.h, b = id.b, cbeg = 2 * id.c, cend = 2 * id.c + 2;
   } else {
     // early chunks cost most where the adjoint is a sum over the later ones
     const rr::chunked::ChunkId id = rr::chunked::chunk_id(p, MODE == kDirect, false);
@@ -141,7 +154,10 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
   constexpr int DPW = (NBD + 3) / 4;           // du row blocks per wave: mydb, mydb + 4, ...
 
   f32x4_t lam[CPW][NBD];
-  float plm[REG ? DPW : 1][REG ? NS / 32 : 1][8];   // du operand: lam[16 (mydb + 4 k) + l15][32 kk + 8 l4 + e]
+  float plm[REG && MODE != kPair ? DPW : 1][REG && MODE != kPair ? NS / 32 : 1][8];   // du operand: lam[16 (mydb + 4 k) + l15][32 kk + 8 l4 + e]
+  // kPair's du operand: lam[16 (mydb + 4 k) + l15][16 nb + 4 l4 + r] (the layout
+  // of the accumulator that carries it across the pair)
+  f32x4_t plm4[MODE == kPair ? DPW : 1][MODE == kPair ? NBN : 1];
 #pragma unroll
   for (int cc = 0; cc < CPW; ++cc)
 #pragma unroll
@@ -286,8 +302,27 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
   float dA_acc[CPW];   // SSD: dA of this lane's column (every l4 group holds the same sum)
 #pragma unroll
   for (int cc = 0; cc < CPW; ++cc) dA_acc[cc] = 0.f;
+  if constexpr (MODE == kPair) {
+    // lam leaving the pair (slot cbeg / 2 of the scan's output), this wave's column blocks
+    const auto lsrc = rr::as_global(p.agg + (bh * (p.nC / 2) + cbeg / 2) * DH * NS);
+#pragma unroll
+    for (int cc = 0; cc < CPW; ++cc) {
+      const int nb = min(w + 4 * cc, NBN - 1);
+      const float use = w + 4 * cc < NBN ? 1.f : 0.f;
+#pragma unroll
+      for (int db = 0; db < NBD; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          lam[cc][db][r] = use * rr::ld32<float>(lsrc, (uint32_t)((16 * db + 4 * l4 + r) * NS + 16 * nb + l15));
+    }
+  }
 
-  for (int c = cend - 1; c >= cbeg; --c) {
+  // One chunk (FIRST: the first chunk of a kPair workgroup, whose adjoint
+  // comes from memory; the second takes the carried one).  A lambda forced
+  // inline, so kPair runs it twice with its loads and carries resolved at
+  // compile time (no branch around a load).
+  auto chunk_body = [&](const int c, auto first_tag) __attribute__((always_inline)) {
+    constexpr bool FIRST = decltype(first_tag)::value;
     // a fresh copy of the thread index per chunk keeps the compiler from
     // hoisting every per-lane LDS / global address of the body out of the loop
     int tidv = tid;
@@ -423,6 +458,37 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
           m.XYp[w][1][t] = yr;
         }
       }
+    if constexpr (MODE == kPair && FIRST) {
+      // the adjoint entering this chunk, for the pair's other chunk (lam is
+      // dead here: UL above was its last use): lam <- gam_31 lam + (gam o dY)^T C,
+      // dY^T [d][t] by transposing reads of the staged dY, (gam o C) [t][n]
+      const float g31 = m.gam[Q - 1];
+#pragma unroll
+      for (int cc = 0; cc < CPW; ++cc) {
+        const int nb = w + 4 * cc;
+        if (nb >= NBN) continue;
+        const u16x8_t qf = rr::frag_tr(&m.Qn[0][16 * nb], ColBwdSmem<DH, NS, GLA, REG>::PN, lane);
+        float qw[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qw[e] = m.gam[8 * l4 + e] * bf_val(qf[e]);
+        u16x8_t qh, ql;
+        rr::bf_split8(qw, qh, ql);
+#pragma unroll
+        for (int db = 0; db < NBD; ++db) {
+          constexpr int PD = ColBwdSmem<DH, NS, GLA, REG>::PD;
+          const u16x8_t ah = rr::frag_tr(&m.x.GY_hi[0][16 * db], PD, lane);
+          const u16x8_t al = rr::frag_tr(&m.x.GY_lo[0][16 * db], PD, lane);
+          // all four hi / lo products: both factors are split fp32 values, and
+          // the carried adjoint keeps the scan's 2^-17 relative accuracy
+          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+          acc = mfma16(al, ql, acc);
+          acc = mfma16(ah, ql, acc);
+          acc = mfma16(al, qh, acc);
+          acc = mfma16(ah, qh, acc);
+          lam[cc][db] = acc + g31 * lam[cc][db];
+        }
+      }
+    }
     f32x16_t cg = {};   // wave 0: CB = C B^T; wave 1: G2 = dY U^T
     if (w == 0) {
 #pragma unroll
@@ -453,6 +519,18 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
         const int d = 16 * min(mydb + 4 * k, NBD - 1) + l15;
 #pragma unroll
         for (int e = 0; e < 8; ++e) pdy[k][e] = rr::ld32<float>(p.dy + baseD, (uint32_t)((8 * l4 + e) * rsD + d));
+      }
+    }
+    if constexpr (MODE == kPair && FIRST) {
+#pragma unroll
+      for (int k = 0; k < DPW; ++k) {
+        const int d = 16 * min(mydb + 4 * k, NBD - 1) + l15;
+        const float* lsrc = p.agg + ((bh * (p.nC / 2) + cbeg / 2) * DH + d) * NS + 4 * l4;
+#pragma unroll
+        for (int nb = 0; nb < NBN; ++nb) {
+          const float4 l0 = *reinterpret_cast<const float4*>(lsrc + 16 * nb);
+          plm4[k][nb] = f32x4_t{l0.x, l0.y, l0.z, l0.w};
+        }
       }
     }
     if constexpr (MODE == kPipe) {
@@ -617,9 +695,15 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
         gl8 = frag(&m.GYT_lo[16 * db + l15][8 * l4]);
       }
       u16x8_t lh8[NS / 32], ll8[NS / 32];   // lam fragments [n = 32 kk + 8 l4 + e][d]
+      u16x4_t lh4[MODE == kPair ? NBN : 1], ll4[MODE == kPair ? NBN : 1];   // kPair: [n = 16 nb + 4 l4 + e][d]
+      if constexpr (MODE == kPair) {
+#pragma unroll
+        for (int nb = 0; nb < NBN; ++nb) rr::bf_split4(plm4[k][nb], lh4[nb], ll4[nb]);
+      }
 #pragma unroll
       for (int kk = 0; kk < NS / 32; ++kk) {
-        if constexpr (REG) {
+        if constexpr (MODE == kPair) {
+        } else if constexpr (REG) {
           rr::bf_split8(plm[k][kk], lh8[kk], ll8[kk]);
         } else {
           lh8[kk] = frag(&m.LM_hi[16 * db + l15][32 * kk + 8 * l4]);
@@ -636,16 +720,46 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
           a1 = mfma16(ph, gl8, a1);
           a1 = mfma16(pl, gh8, a1);
         }
+        if constexpr (MODE == kPair) {
 #pragma unroll
-        for (int kk = 0; kk < NS / 32; ++kk) {
-          const u16x8_t fa = frag(&m.Kn[16 * tb + l15][32 * kk + 8 * l4]);
-          a2 = mfma16(fa, lh8[kk], a2);
-          a2 = mfma16(fa, ll8[kk], a2);
+          for (int nb = 0; nb < NBN; ++nb) {
+            const u16x4_t fa = frag4(&m.Kn[16 * tb + l15][16 * nb + 4 * l4]);
+            a2 = mfma16k16(fa, lh4[nb], a2);
+            a2 = mfma16k16(fa, ll4[nb], a2);
+          }
+        } else {
+#pragma unroll
+          for (int kk = 0; kk < NS / 32; ++kk) {
+            const u16x8_t fa = frag(&m.Kn[16 * tb + l15][32 * kk + 8 * l4]);
+            a2 = mfma16(fa, lh8[kk], a2);
+            a2 = mfma16(fa, ll8[kk], a2);
+          }
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = 16 * tb + 4 * l4 + r;
           rr::st_bf16_u32(duB, (uint32_t)(t * rsD + 16 * db + l15), m.w[t] * (a1[r] + m.m31[t] * a2[r]));
+        }
+      }
+      if constexpr (MODE == kPair && FIRST) {
+        // du's operand rows of the adjoint entering this chunk, for the
+        // pair's other chunk: plm4 <- gam_31 plm4 + C^T diag(gam) dY (rows n,
+        // columns d = this wave's du block; dY^T is the fragment above)
+        const float g31 = m.gam[Q - 1];
+#pragma unroll
+        for (int nb = 0; nb < NBN; ++nb) {
+          const u16x8_t qf = rr::frag_tr(&m.Qn[0][16 * nb], ColBwdSmem<DH, NS, GLA, REG>::PN, lane);
+          float qw[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) qw[e] = m.gam[8 * l4 + e] * bf_val(qf[e]);
+          u16x8_t qh, ql;
+          rr::bf_split8(qw, qh, ql);
+          f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+          acc = mfma16(ql, gl8, acc);
+          acc = mfma16(qh, gl8, acc);
+          acc = mfma16(ql, gh8, acc);
+          acc = mfma16(qh, gh8, acc);
+          plm4[k][nb] = acc + g31 * plm4[k][nb];
         }
       }
     }
@@ -741,12 +855,18 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
         rr::st_bf16(p.ddelta, baseX + lane * p.H, a * T + (1.f - a * m.xin[lane]) * bzt);
       }
     }
-    if (MODE == kWhole) __syncthreads();   // the next chunk rewrites the LDS
+    if (MODE == kWhole || (MODE == kPair && FIRST)) __syncthreads();   // the next chunk rewrites the LDS
+  };
+  if constexpr (MODE == kPair) {
+    chunk_body(cend - 1, std::true_type{});
+    chunk_body(cbeg, std::false_type{});
+  } else {
+    for (int c = cend - 1; c >= cbeg; --c) chunk_body(c, std::false_type{});
   }
   if constexpr (!GLA) {
     // per-run dA partial of this lane's column
-    const int nR = MODE == kWhole ? 1 : p.nC;
-    const int run = MODE == kWhole ? 0 : cbeg;
+    const int nR = MODE == kWhole ? 1 : MODE == kPair ? p.nC / 2 : p.nC;
+    const int run = MODE == kWhole ? 0 : MODE == kPair ? cbeg / 2 : cbeg;
 #pragma unroll
     for (int cc = 0; cc < CPW; ++cc) {
       const int nb = w + 4 * cc;
@@ -773,6 +893,15 @@ int launch(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
   if (p.mode == kPipe) {
     if (int rc = rr::chunked::launch_scan<DH, NS, GLA>(p, B, s, true)) return rc;
     hipLaunchKernelGGL((col_bwd_kernel<DH, NS, kPipe, GLA>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
+  } else if (p.mode == rr::chunked::kPair) {
+    if constexpr (GLA) {
+      return rr::fail(RR_EUNSUPPORTED, "gla chunked backward: no pair mode");
+    } else {
+      if (p.R != 2 || p.nC % 2 != 0) return rr::fail(RR_EINVAL, "chunked backward: pair mode needs R = 2, even nC");
+      if (int rc = rr::chunked::launch_scan<DH, NS, GLA>(p, B, s, true)) return rc;
+      hipLaunchKernelGGL((col_bwd_kernel<DH, NS, rr::chunked::kPair, GLA>), rr::chunked::pair_grid(p), dim3(256), 0, s,
+                         p);
+    }
   } else if (p.mode == kDirect) {
     if constexpr (DH * NS <= rr::chunked::kDirectMaxState)
       hipLaunchKernelGGL((col_bwd_kernel<DH, NS, kDirect, GLA>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);

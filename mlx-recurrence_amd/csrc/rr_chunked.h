@@ -180,8 +180,12 @@ __device__ __forceinline__ int state_off(int d, int n) {
 // Both read up to nC - 1 chunks of inputs per workgroup (quadratic in nC), so
 // they serve short heads; longer heads run kPipe.
 //   kRes    forward only: every chunk of a head resident in one workgroup
-//           per 16-column slice of d (resident.hip), nC <= 16.
-enum Mode { kWhole = 0, kPipe = 1, kDirect = 2, kSum = 3, kRes = 4 };
+//           per 16-column slice of d (resident.hip), nC <= 16;
+//   kPair   backward of the column-owned kernel with the per-head adjoint
+//           scan: one workgroup per pair of chunks (2j, 2j + 1); the scan
+//           stores the adjoint leaving every second chunk only (R = 2), and
+//           the workgroup carries it across the pair's boundary itself.
+enum Mode { kWhole = 0, kPipe = 1, kDirect = 2, kSum = 3, kRes = 4, kPair = 5 };
 
 // Per-chunk kernels run on a 1-D grid of chunk_grid(p) workgroups.  The GPU
 // hands workgroups to its 8 XCDs round-robin by linear index; the decode
@@ -207,6 +211,15 @@ __device__ __forceinline__ ChunkId chunk_id(const ChunkArgs& p, bool by_cost, bo
 }
 inline dim3 chunk_grid(const ChunkArgs& p) {
   return dim3((unsigned)(p.nC * ((p.B * p.H + kXcds - 1) / kXcds) * kXcds));
+}
+// kPair: the same decode over the nC / 2 pairs of a head (c = pair index)
+__device__ __forceinline__ ChunkId pair_id(const ChunkArgs& p) {
+  const int id = blockIdx.x, x = id % kXcds, slot = id / kXcds, nP = p.nC / 2;
+  const int bh = (slot / nP) * kXcds + x;
+  return ChunkId{slot % nP, bh % p.H, bh / p.H, bh < p.B * p.H};
+}
+inline dim3 pair_grid(const ChunkArgs& p) {
+  return dim3((unsigned)(p.nC / 2 * ((p.B * p.H + kXcds - 1) / kXcds) * kXcds));
 }
 
 // Per-head decay rate (SSD); GLA has none.
@@ -413,7 +426,8 @@ __global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
 //   forward:  h_k = tot_k h_{k-1} + U_k^T diag(m31 o w) B_k (h_{-1} = h0),
 //             into checkpoint slot k;
 //   backward: slot k of the workspace <- lam_k (lam_{nC-1} = dfinal),
-//             lam_{k-1} = tot_k lam_k + (gam o dY_k)^T C_k, dh0 = lam_{-1}.
+//             lam_{k-1} = tot_k lam_k + (gam o dY_k)^T C_k, dh0 = lam_{-1};
+//             with R = 2 (kPair) only the odd chunks' lam_k, into slot k / 2.
 // A chunk's update is a rank-32 MFMA product on the running state.  All 256
 // threads load the chunk's inputs kScanPF chunks ahead and stage them in a
 // double-buffered LDS area in natural [step][column] layout (the fp32 factor
@@ -491,7 +505,9 @@ __global__ __launch_bounds__(256) void scan_kernel(ChunkArgs p) {
 #pragma unroll
   for (int q = 0; q < kScanPF; ++q) load(q, q);
 
-  float* out = (BWD ? p.agg : p.ckpt) + bh * nC * DH * NS;
+  // this head's slots: nC checkpoints (forward), or one adjoint per run of
+  // R chunks (backward; the workspace holds ceil(nC / R) per head)
+  float* out = BWD ? p.agg + bh * ((nC + p.R - 1) / p.R) * DH * NS : p.ckpt + bh * nC * DH * NS;
   auto store_state = [&](float* dst) {
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
@@ -554,7 +570,10 @@ __global__ __launch_bounds__(256) void scan_kernel(ChunkArgs p) {
   auto update = [&](int k, float tot) {
     const int buf = k & 1;
     const int c = chunk_at(k);
-    if constexpr (BWD) store_state(out + (int64_t)c * DH * NS);   // lam_c, the adjoint leaving chunk c
+    if constexpr (BWD) {   // lam_c, the adjoint leaving chunk c (every R-th chunk: uniform branch, no loads)
+      if (p.R == 1) store_state(out + (int64_t)c * DH * NS);
+      else if (c % p.R == p.R - 1) store_state(out + (int64_t)(c / p.R) * DH * NS);
+    }
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
       const int j = w + 4 * i, db = j / NBN, nb = j % NBN;
@@ -645,6 +664,7 @@ template <int DH, int NS, bool GLA>
 int launch_scan(const ChunkArgs& p, int64_t B, hipStream_t s, bool bwd) {
   const int kind = bwd ? 1 : 0;
   if (B * p.H < kScanMinHeads) {
+    if (p.R != 1) return fail(RR_EINVAL, "chunked adjoint pass: one adjoint per chunk only");
     hipLaunchKernelGGL((agg_kernel<DH, NS, GLA>), chunk_grid(p), dim3(kAggThreads), 0, s, p, kind);
     if (int rc = check_launch(bwd ? "chunked backward aggregates" : "chunked forward aggregates")) return rc;
     hipLaunchKernelGGL((pass_kernel<DH, NS, GLA>), dim3(DH * NS / 256, p.H, (unsigned)B), dim3(256), 0, s, p, kind);

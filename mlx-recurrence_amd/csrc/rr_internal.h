@@ -45,6 +45,7 @@ struct ChunkArgs {
 // the chunk aggregates (nC <= 16, N <= 32) or by the pipelined aggregate and
 // state-pass kernels.
 int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N, int pass);
+int chunked_run(int mode, int64_t nC);   // ChunkArgs::R of a mode
 
 // ------------------------------------------------------------------ SSD
 // True when the chunked kernels cover this call: bf16 inputs, a head-uniform A

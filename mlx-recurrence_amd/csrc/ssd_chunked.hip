@@ -801,7 +801,7 @@ __global__ __launch_bounds__(T) void ssd2_dA_kernel(const float* __restrict__ pa
 }
 
 int launch_dA(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
-  const int nR = p.mode == kWhole ? 1 : p.nC;
+  const int nR = (p.nC + p.R - 1) / p.R;   // runs per head
   // (a larger workgroup only where there are many partials to sum)
   if ((int64_t)B * nR * p.NS > 4096)
     hipLaunchKernelGGL(ssd2_dA_kernel<1024>, dim3(p.H), dim3(1024), 0, s, p.ws, p.dA, (int)B, p.H, nR, p.NS);
@@ -856,7 +856,16 @@ int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N, int pa
   // the direct kernel)
   if (nC <= chunked::kDirectMaxChunks && N <= 32 && B * H * nC <= kDirectMaxWorkgroups) return chunked::kSum;
   if (nC <= kDirectMaxChunksWide && Dh * N <= chunked::kDirectMaxState) return chunked::kDirect;
+  // Wide states (the column-owned backward) with the per-head adjoint scan:
+  // a workgroup per pair of chunks, half the adjoints through memory
+  if (pass == 1 && N >= 64 && Dh <= 64 && nC % 2 == 0 && B * H >= chunked::kScanMinHeads)
+    return chunked::kPair;
   return chunked::kPipe;
+}
+
+// Chunks per workgroup (ChunkArgs::R) of a mode.
+int chunked_run(int mode, int64_t nC) {
+  return mode == chunked::kWhole ? (int)nC : mode == chunked::kPair ? 2 : 1;
 }
 
 // Workspace layout (floats, each part 256-byte aligned): per-chunk decays
@@ -867,12 +876,12 @@ int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }
 }
 
 size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int mode, int64_t Dh, int64_t N, int pass) {
-  const int64_t nR = mode == chunked::kWhole ? 1 : nC;
-  const bool pipe = mode == chunked::kPipe;
+  const int64_t R = chunked_run(mode, nC), nR = (nC + R - 1) / R;
+  const bool pipe = mode == chunked::kPipe || mode == chunked::kPair;
   int64_t f = pipe ? align64(B * H * nC) : 0;
   if (pass == 1) {
     f += align64(B * H * nR * N);
-    if (pipe) f += align64(B * H * nC * Dh * N);
+    if (pipe) f += align64(B * H * nR * Dh * N);   // one adjoint per run
   }
   return (size_t)f * sizeof(float);
 }
@@ -880,7 +889,7 @@ size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int mode, int64_t Dh, int
 void ssd2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass) {
   float* f = static_cast<float*>(ws);
   const int64_t nR = (a.nC + a.R - 1) / a.R;
-  const bool pipe = a.mode == chunked::kPipe;
+  const bool pipe = a.mode == chunked::kPipe || a.mode == chunked::kPair;
   a.tot = a.ws = a.agg = nullptr;
   if (pipe) { a.tot = f; f += align64(B * a.H * a.nC); }
   if (pass == 1) {

@@ -763,7 +763,7 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
     a.dh0 = dh0;
     a.B = (int)B; a.L = (int)L; a.H = (int)H; a.DH = (int)Dh; a.NS = (int)N; a.nC = nC;
     a.mode = mode;
-    a.R = mode == 0 ? nC : 1;
+    a.R = rr::chunked_run(mode, nC);
     rr::ssd2_carve_ws(a, workspace, B, 1);
     return rr::ssd2_bwd(a, B, static_cast<hipStream_t>(stream));
   }
