@@ -39,12 +39,12 @@
 // Modes as in the forward: kWhole (a head per workgroup, lam carried in
 // registers from chunk to chunk), kPipe (lam from pass_kernel), kDirect (lam
 // from the direct sum; the workgroup of chunk 0 also forms dh0), kPair (a
-// workgroup per pair of chunks, lam of the pair's last chunk from the
-// adjoint scan, which stores every second adjoint only; the workgroup forms
-// the adjoint entering the pair's first chunk itself, in the layouts of both
-// of its uses: the column blocks, lam_prev = gam_31 lam + (gam o dY)^T C,
-// at the end of phase B1 while dY is staged, and du's operand rows, the
-// same sum transposed, C^T diag(gam) dY, in phase C).
+// workgroup per run of R = 2 or 4 chunks, lam of the run's last chunk from
+// the adjoint scan, which stores every R-th adjoint only; the workgroup forms
+// the adjoint entering each earlier chunk of the run itself, in the layouts
+// of both of its uses: the column blocks, lam_prev = gam_31 lam + (gam o
+// dY)^T C, at the end of phase B1 while dY is staged, and du's operand rows,
+// the same sum transposed, C^T diag(gam) dY, in phase C).
 #include <type_traits>
 #include <utility>
 
@@ -137,9 +137,9 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
   if constexpr (MODE == kWhole) {
     h = blockIdx.y, b = blockIdx.z, cbeg = 0, cend = p.nC;
   } else if constexpr (MODE == kPair) {
-    const rr::chunked::ChunkId id = rr::chunked::pair_id(p);
+    const rr::chunked::ChunkId id = rr::chunked::run_id(p);
     if (!id.valid) return;
-    h = id.h, b = id.b, cbeg = 2 * id.c, cend = 2 * id.c + 2;
+    h = id.h, b = id.b, cbeg = p.R * id.c, cend = p.R * id.c + p.R;
   } else {
     // early chunks cost most where the adjoint is a sum over the later ones
     const rr::chunked::ChunkId id = rr::chunked::chunk_id(p, MODE == kDirect, false);
@@ -303,8 +303,8 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
 #pragma unroll
   for (int cc = 0; cc < CPW; ++cc) dA_acc[cc] = 0.f;
   if constexpr (MODE == kPair) {
-    // lam leaving the pair (slot cbeg / 2 of the scan's output), this wave's column blocks
-    const auto lsrc = rr::as_global(p.agg + (bh * (p.nC / 2) + cbeg / 2) * DH * NS);
+    // lam leaving the run (slot cbeg / R of the scan's output), this wave's column blocks
+    const auto lsrc = rr::as_global(p.agg + (bh * (p.nC / p.R) + cbeg / p.R) * DH * NS);
 #pragma unroll
     for (int cc = 0; cc < CPW; ++cc) {
       const int nb = min(w + 4 * cc, NBN - 1);
@@ -317,12 +317,12 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
     }
   }
 
-  // One chunk (FIRST: the first chunk of a kPair workgroup, whose adjoint
-  // comes from memory; the second takes the carried one).  A lambda forced
-  // inline, so kPair runs it twice with its loads and carries resolved at
-  // compile time (no branch around a load).
-  auto chunk_body = [&](const int c, auto first_tag) __attribute__((always_inline)) {
-    constexpr bool FIRST = decltype(first_tag)::value;
+  // One chunk.  kPair: LOAD for the run's last chunk (its adjoint from
+  // memory), CARRY for every chunk but the run's first (it forms the adjoint
+  // entering the chunk before it).  A lambda forced inline, so the loads and
+  // carries are resolved at compile time (no branch around a load).
+  auto chunk_body = [&](const int c, auto load_tag, auto carry_tag) __attribute__((always_inline)) {
+    constexpr bool LOAD = decltype(load_tag)::value, CARRY = decltype(carry_tag)::value;
     // a fresh copy of the thread index per chunk keeps the compiler from
     // hoisting every per-lane LDS / global address of the body out of the loop
     int tidv = tid;
@@ -458,8 +458,8 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
           m.XYp[w][1][t] = yr;
         }
       }
-    if constexpr (MODE == kPair && FIRST) {
-      // the adjoint entering this chunk, for the pair's other chunk (lam is
+    if constexpr (MODE == kPair && CARRY) {
+      // the adjoint entering this chunk, for the run's chunk before it (lam is
       // dead here: UL above was its last use): lam <- gam_31 lam + (gam o dY)^T C,
       // dY^T [d][t] by transposing reads of the staged dY, (gam o C) [t][n]
       const float g31 = m.gam[Q - 1];
@@ -521,11 +521,11 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
         for (int e = 0; e < 8; ++e) pdy[k][e] = rr::ld32<float>(p.dy + baseD, (uint32_t)((8 * l4 + e) * rsD + d));
       }
     }
-    if constexpr (MODE == kPair && FIRST) {
+    if constexpr (MODE == kPair && LOAD) {
 #pragma unroll
       for (int k = 0; k < DPW; ++k) {
         const int d = 16 * min(mydb + 4 * k, NBD - 1) + l15;
-        const float* lsrc = p.agg + ((bh * (p.nC / 2) + cbeg / 2) * DH + d) * NS + 4 * l4;
+        const float* lsrc = p.agg + ((bh * (p.nC / p.R) + cbeg / p.R) * DH + d) * NS + 4 * l4;
 #pragma unroll
         for (int nb = 0; nb < NBN; ++nb) {
           const float4 l0 = *reinterpret_cast<const float4*>(lsrc + 16 * nb);
@@ -741,9 +741,9 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
           rr::st_bf16_u32(duB, (uint32_t)(t * rsD + 16 * db + l15), m.w[t] * (a1[r] + m.m31[t] * a2[r]));
         }
       }
-      if constexpr (MODE == kPair && FIRST) {
+      if constexpr (MODE == kPair && CARRY) {
         // du's operand rows of the adjoint entering this chunk, for the
-        // pair's other chunk: plm4 <- gam_31 plm4 + C^T diag(gam) dY (rows n,
+        // run's chunk before it: plm4 <- gam_31 plm4 + C^T diag(gam) dY (rows n,
         // columns d = this wave's du block; dY^T is the fragment above)
         const float g31 = m.gam[Q - 1];
 #pragma unroll
@@ -855,18 +855,19 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
         rr::st_bf16(p.ddelta, baseX + lane * p.H, a * T + (1.f - a * m.xin[lane]) * bzt);
       }
     }
-    if (MODE == kWhole || (MODE == kPair && FIRST)) __syncthreads();   // the next chunk rewrites the LDS
+    if (MODE == kWhole || (MODE == kPair && CARRY)) __syncthreads();   // the next chunk rewrites the LDS
   };
   if constexpr (MODE == kPair) {
-    chunk_body(cend - 1, std::true_type{});
-    chunk_body(cbeg, std::false_type{});
+    chunk_body(cend - 1, std::true_type{}, std::true_type{});
+    for (int c = cend - 2; c > cbeg; --c) chunk_body(c, std::false_type{}, std::true_type{});
+    chunk_body(cbeg, std::false_type{}, std::false_type{});
   } else {
-    for (int c = cend - 1; c >= cbeg; --c) chunk_body(c, std::false_type{});
+    for (int c = cend - 1; c >= cbeg; --c) chunk_body(c, std::false_type{}, std::false_type{});
   }
   if constexpr (!GLA) {
     // per-run dA partial of this lane's column
-    const int nR = MODE == kWhole ? 1 : MODE == kPair ? p.nC / 2 : p.nC;
-    const int run = MODE == kWhole ? 0 : MODE == kPair ? cbeg / 2 : cbeg;
+    const int nR = MODE == kWhole ? 1 : MODE == kPair ? p.nC / p.R : p.nC;
+    const int run = MODE == kWhole ? 0 : MODE == kPair ? cbeg / p.R : cbeg;
 #pragma unroll
     for (int cc = 0; cc < CPW; ++cc) {
       const int nb = w + 4 * cc;
@@ -894,12 +895,12 @@ int launch(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
     if (int rc = rr::chunked::launch_scan<DH, NS, GLA>(p, B, s, true)) return rc;
     hipLaunchKernelGGL((col_bwd_kernel<DH, NS, kPipe, GLA>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
   } else if (p.mode == rr::chunked::kPair) {
-    if constexpr (GLA) {
-      return rr::fail(RR_EUNSUPPORTED, "gla chunked backward: no pair mode");
+    if constexpr (GLA || DH > 64) {   // (the host picks it for SSD with Dh <= 64 only)
+      return rr::fail(RR_EUNSUPPORTED, "chunked backward: no pair mode for this state");
     } else {
-      if (p.R != 2 || p.nC % 2 != 0) return rr::fail(RR_EINVAL, "chunked backward: pair mode needs R = 2, even nC");
+      if (p.R < 2 || p.nC % p.R != 0) return rr::fail(RR_EINVAL, "chunked backward: runs of R > 1 chunks dividing nC");
       if (int rc = rr::chunked::launch_scan<DH, NS, GLA>(p, B, s, true)) return rc;
-      hipLaunchKernelGGL((col_bwd_kernel<DH, NS, rr::chunked::kPair, GLA>), rr::chunked::pair_grid(p), dim3(256), 0, s,
+      hipLaunchKernelGGL((col_bwd_kernel<DH, NS, rr::chunked::kPair, GLA>), rr::chunked::run_grid(p), dim3(256), 0, s,
                          p);
     }
   } else if (p.mode == kDirect) {

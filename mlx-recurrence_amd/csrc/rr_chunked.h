@@ -182,9 +182,9 @@ __device__ __forceinline__ int state_off(int d, int n) {
 //   kRes    forward only: every chunk of a head resident in one workgroup
 //           per 16-column slice of d (resident.hip), nC <= 16;
 //   kPair   backward of the column-owned kernel with the per-head adjoint
-//           scan: one workgroup per pair of chunks (2j, 2j + 1); the scan
-//           stores the adjoint leaving every second chunk only (R = 2), and
-//           the workgroup carries it across the pair's boundary itself.
+//           scan: one workgroup per run of R = 2 or 4 consecutive chunks;
+//           the scan stores the adjoint leaving every R-th chunk only, and
+//           the workgroup carries it across the run's inner boundaries.
 enum Mode { kWhole = 0, kPipe = 1, kDirect = 2, kSum = 3, kRes = 4, kPair = 5 };
 
 // Per-chunk kernels run on a 1-D grid of chunk_grid(p) workgroups.  The GPU
@@ -212,14 +212,14 @@ __device__ __forceinline__ ChunkId chunk_id(const ChunkArgs& p, bool by_cost, bo
 inline dim3 chunk_grid(const ChunkArgs& p) {
   return dim3((unsigned)(p.nC * ((p.B * p.H + kXcds - 1) / kXcds) * kXcds));
 }
-// kPair: the same decode over the nC / 2 pairs of a head (c = pair index)
-__device__ __forceinline__ ChunkId pair_id(const ChunkArgs& p) {
-  const int id = blockIdx.x, x = id % kXcds, slot = id / kXcds, nP = p.nC / 2;
+// kPair: the same decode over the nC / R runs of a head (c = run index)
+__device__ __forceinline__ ChunkId run_id(const ChunkArgs& p) {
+  const int id = blockIdx.x, x = id % kXcds, slot = id / kXcds, nP = p.nC / p.R;
   const int bh = (slot / nP) * kXcds + x;
   return ChunkId{slot % nP, bh % p.H, bh / p.H, bh < p.B * p.H};
 }
-inline dim3 pair_grid(const ChunkArgs& p) {
-  return dim3((unsigned)(p.nC / 2 * ((p.B * p.H + kXcds - 1) / kXcds) * kXcds));
+inline dim3 run_grid(const ChunkArgs& p) {
+  return dim3((unsigned)(p.nC / p.R * ((p.B * p.H + kXcds - 1) / kXcds) * kXcds));
 }
 
 // Per-head decay rate (SSD); GLA has none.
@@ -427,7 +427,7 @@ __global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
 //             into checkpoint slot k;
 //   backward: slot k of the workspace <- lam_k (lam_{nC-1} = dfinal),
 //             lam_{k-1} = tot_k lam_k + (gam o dY_k)^T C_k, dh0 = lam_{-1};
-//             with R = 2 (kPair) only the odd chunks' lam_k, into slot k / 2.
+//             with R > 1 (kPair) only lam_k of every R-th chunk, into slot k / R.
 // A chunk's update is a rank-32 MFMA product on the running state.  All 256
 // threads load the chunk's inputs kScanPF chunks ahead and stage them in a
 // double-buffered LDS area in natural [step][column] layout (the fp32 factor

@@ -858,6 +858,9 @@ int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N, int pa
   if (nC <= kDirectMaxChunksWide && Dh * N <= chunked::kDirectMaxState) return chunked::kDirect;
   // Wide states (the column-owned backward) with the per-head adjoint scan:
   // a workgroup per pair of chunks, half the adjoints through memory
+  // (measured at config 4: runs of 2 3.98 ms against 4.45 ms per chunk; runs
+  // of 4 3.92 ms, but the carried adjoint's rounding then reaches 8e-6 of dA
+  // where pairs keep 6e-6, so pairs)
   if (pass == 1 && N >= 64 && Dh <= 64 && nC % 2 == 0 && B * H >= chunked::kScanMinHeads)
     return chunked::kPair;
   return chunked::kPipe;
@@ -865,7 +868,9 @@ int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N, int pa
 
 // Chunks per workgroup (ChunkArgs::R) of a mode.
 int chunked_run(int mode, int64_t nC) {
-  return mode == chunked::kWhole ? (int)nC : mode == chunked::kPair ? 2 : 1;
+  if (mode == chunked::kWhole) return (int)nC;
+  if (mode == chunked::kPair) return 2;
+  return 1;
 }
 
 // Workspace layout (floats, each part 256-byte aligned): per-chunk decays

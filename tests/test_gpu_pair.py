@@ -3,8 +3,9 @@
 scan storing the adjoint leaving every second chunk only, and one workgroup
 per pair of chunks that carries the adjoint across the pair itself.
 
-Shape: B=4 L=128 H=80 Dh=64 N=128 bf16 (320 heads, 4 chunks per head), the
-smallest that takes the mode.
+Shapes: B=4 L=128 H=80 Dh=64 N=128 bf16 (320 heads, 4 chunks per head: two
+pairs), the smallest that takes the mode with more than one pair per head;
+the guard test also at L=64 (one pair per head).
   - Through the C ABI, with guard regions after the workspace (as large as the
     workspace itself) and after every output, filled with a byte pattern:
     nothing may be written past the sizes the library states
@@ -36,7 +37,7 @@ PATTERN = 0x5A
 GUARD_OUT = 4096   # bytes past each output
 
 
-def _inputs(seed):
+def _inputs(seed, L=L):
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(seed)
     bf = torch.bfloat16
@@ -57,9 +58,10 @@ def _guarded(shape, dtype, guard_bytes):
     return buf[:n].view(dtype).view(shape), buf[n:]
 
 
-def test_pair_mode_writes_inside_its_buffers():
+@pytest.mark.parametrize("L", [L, 64], ids=["two_pairs", "one_pair"])
+def test_pair_mode_writes_inside_its_buffers(L):
     print(f"[case] ssd pair-mode guards B={B} L={L} H={H} Dh={Dh} N={N} bf16", flush=True)
-    u, delta, Bm, Cm, A, dy = _inputs(11)
+    u, delta, Bm, Cm, A, dy = _inputs(11, L)
     nC = L // _lib.chunk_len(L, SEG)
     y = torch.empty((B, L, H, Dh), dtype=torch.float32, device=u.device)
     ckpt = torch.empty((B, H, nC, Dh, N), dtype=torch.float32, device=u.device)
