@@ -29,6 +29,8 @@ from mlx_recurrence_amd import _lib
 from oracle import recurrence_oracle as orc
 from tests.gpu_util import rel_err
 
+import mlx_recurrence_amd as mr
+
 pytestmark = pytest.mark.gpu
 
 B, L, H, Dh, N, SEG = 4, 128, 80, 64, 128, 32
@@ -50,6 +52,21 @@ def _inputs(seed, L=L):
     return u, delta, Bm, Cm, A, W
 
 
+def _a64(n):
+    return (n + 63) // 64 * 64
+
+
+def _assert_pair_mode(Bsz, seq, Hh, dh, n_st):
+    """The backward workspace the library asks for at this shape is the pair
+    mode's (per-chunk decays, dA partials and one adjoint per pair of chunks,
+    each part 256-byte aligned), which tells the mode apart from the
+    per-chunk pipelined one (an adjoint per chunk) and the direct one."""
+    nC = seq // 32
+    want = 4 * (_a64(Bsz * Hh * nC) + _a64(Bsz * Hh * (nC // 2) * n_st) + _a64(Bsz * Hh * (nC // 2) * dh * n_st))
+    got = _lib.load().rr_ssd_workspace_bytes(Bsz, seq, Hh, dh, n_st, SEG, 0, _lib.DTYPE_CODE[torch.bfloat16], 1)
+    assert got == want, f"not the pair mode at B={Bsz} L={seq} H={Hh} Dh={dh} N={n_st}: {got} != {want}"
+
+
 def _guarded(shape, dtype, guard_bytes):
     """An output tensor of `shape` that is the prefix of a larger buffer whose
     tail (guard_bytes) holds PATTERN; returns (tensor, guard bytes view)."""
@@ -61,6 +78,7 @@ def _guarded(shape, dtype, guard_bytes):
 @pytest.mark.parametrize("L", [L, 64], ids=["two_pairs", "one_pair"])
 def test_pair_mode_writes_inside_its_buffers(L):
     print(f"[case] ssd pair-mode guards B={B} L={L} H={H} Dh={Dh} N={N} bf16", flush=True)
+    _assert_pair_mode(B, L, H, Dh, N)
     u, delta, Bm, Cm, A, dy = _inputs(11, L)
     nC = L // _lib.chunk_len(L, SEG)
     y = torch.empty((B, L, H, Dh), dtype=torch.float32, device=u.device)
@@ -88,6 +106,7 @@ def pair_run():
     [H, N], as the kernels form it); returns float64 CPU slices of the
     selected heads."""
     print(f"[case] ssd pair-mode parity B={B} L={L} H={H} Dh={Dh} N={N} bf16", flush=True)
+    _assert_pair_mode(B, L, H, Dh, N)
     u, delta, Bm, Cm, A, W = _inputs(12)
     nC = L // _lib.chunk_len(L, SEG)
     y = torch.empty((B, L, H, Dh), dtype=torch.float32, device=u.device)
@@ -128,3 +147,48 @@ def test_pair_mode_parity(pair_run, j):
         assert errs[k] < 1e-5, (k, errs)
     for k in ("grad_u", "grad_delta", "grad_B", "grad_C"):
         assert errs[k] < 2e-2, (k, errs)
+
+
+def test_pair_mode_initial_state_and_final_cotangent():
+    """N = 64, three pairs per head (L = 192: more than the four chunks of the
+    direct mode), with an initial state and a loss on the final state: the
+    entering state of the first chunk, the final-state cotangent through the
+    adjoint scan and dh0 (through the public API; heads 0 and 79 against
+    the oracle)."""
+    n_st, seq = 64, 192
+    print(f"[case] ssd pair-mode h0 + dfinal B={B} L={seq} H={H} Dh={Dh} N={n_st} bf16", flush=True)
+    _assert_pair_mode(B, seq, H, Dh, n_st)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(13)
+    bf = torch.bfloat16
+    u = torch.randn((B, seq, H, Dh), generator=g, device=dev).to(bf)
+    delta = (torch.randn((B, seq, H), generator=g, device=dev).abs() * 0.1 + 0.01).to(bf)
+    Bm = torch.randn((B, seq, H, n_st), generator=g, device=dev).to(bf)
+    Cm = torch.randn((B, seq, H, n_st), generator=g, device=dev).to(bf)
+    A = -torch.exp(torch.rand((H,), generator=g, device=dev) * math.log(16.0))
+    h0 = torch.randn((B, H, Dh, n_st), generator=g, device=dev)
+    W = torch.randn((B, seq, H, Dh), generator=g, device=dev)
+    V = torch.randn((B, H, Dh, n_st), generator=g, device=dev)
+    xs = [t.requires_grad_(True) for t in (u, delta, Bm, Cm, A, h0)]
+    y, fs = mr.ssd_scan_with_state(xs[0], xs[1], xs[2], xs[3], xs[4], seg=SEG, initial_state=xs[5])
+    ((y * W).sum() + (fs * V).sum()).backward()
+    torch.cuda.synchronize()
+    for h in (0, 79):
+        def sel(t, axis):
+            return t.detach().select(axis, h).unsqueeze(axis).double().cpu().numpy()
+        ui, di, bi, ci = sel(u, 2), sel(delta, 2), sel(Bm, 2), sel(Cm, 2)
+        Ai = np.repeat(A.detach()[h].double().cpu().numpy().reshape(1, 1), n_st, axis=1)
+        h0i, Vi, Wi = sel(h0, 1), sel(V, 1), sel(W, 2)
+        y_o, fs_o = orc.ssd_forward(ui, di, bi, ci, Ai, h0=h0i)
+        du_o, dd_o, dB_o, dC_o, dA_o, dh0_o = orc.ssd_backward(Wi, ui, di, bi, ci, Ai, h0=h0i, dfinal=Vi)
+        errs = {
+            "y": rel_err(sel(y, 2), y_o), "final": rel_err(sel(fs, 1), fs_o),
+            "grad_h0": rel_err(sel(xs[5].grad, 1), dh0_o),
+            "grad_u": rel_err(sel(xs[0].grad, 2), du_o), "grad_delta": rel_err(sel(xs[1].grad, 2), dd_o),
+            "grad_B": rel_err(sel(xs[2].grad, 2), dB_o), "grad_C": rel_err(sel(xs[3].grad, 2), dC_o),
+        }
+        print(f"ssd pair h0/dfinal head {h}: " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()), flush=True)
+        for k in ("y", "final", "grad_h0"):
+            assert errs[k] < 1e-5, (h, k, errs)
+        for k in ("grad_u", "grad_delta", "grad_B", "grad_C"):
+            assert errs[k] < 2e-2, (h, k, errs)
