@@ -1248,6 +1248,14 @@ __global__ __launch_bounds__(256, (kFwdWgs<DH, NS, MODE, GLA>)) void fwd_kernel(
     }
   }
 
+  // whole head with a 64-column state: the next chunk's loads are issued as
+  // soon as this chunk's are staged (the first before the loop; the last
+  // chunk repeats itself, so the count of loads in flight is the same every
+  // time).  Measured on one box: GLA B96 L512 H12 forward 161 -> 152 us; SSD
+  // config 4 (N = 128) 1110 -> 1127 us, so not there; N = 16 (SSD B96)
+  // 95 -> 108 us.
+  constexpr bool PREF = MODE == kWhole && NS == 64;
+  if constexpr (PREF) issue(cbeg, tid);
   for (int c = cbeg; c < cend; ++c) {
     // a fresh copy of the thread index per chunk keeps the compiler from
     // hoisting every per-lane address of the body out of the chunk loop
@@ -1257,9 +1265,7 @@ __global__ __launch_bounds__(256, (kFwdWgs<DH, NS, MODE, GLA>)) void fwd_kernel(
     const int64_t row0 = (int64_t)b * p.L + (int64_t)c * Q;  // first (b, t) row of the chunk
     // ---- stage the chunk's inputs
     {
-      // (whole head: issuing the next chunk's loads here instead, during this
-      // chunk, measured slower: B96 forward 95 -> 108 us)
-      if constexpr (MODE != kDirect) issue(c, tid);
+      if constexpr (MODE != kDirect && !PREF) issue(c, tid);
 #pragma unroll
       for (int v = 0; v < UV; ++v) {
         const int i = tid + 256 * v, tl = (i / (DH / 8)) & (Q - 1), d0 = 8 * (i % (DH / 8));
@@ -1277,6 +1283,7 @@ __global__ __launch_bounds__(256, (kFwdWgs<DH, NS, MODE, GLA>)) void fwd_kernel(
         }
       }
       if (tid < Q) sm.x[tid] = xv;
+      if constexpr (PREF) issue(min(c + 1, cend - 1), tid);
     }
     __syncthreads();
     // ---- step scalars (every wave; lanes s and s + 32 hold step s), then
