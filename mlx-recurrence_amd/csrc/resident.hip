@@ -82,20 +82,27 @@ __global__ __launch_bounds__(64 * kResMaxChunks) void res_fwd_kernel(ChunkArgs p
     cfr[kb] = *reinterpret_cast<const u16x8_t*>(p.Cm + off);
   }
   const u16x8_t ufr = *reinterpret_cast<const u16x8_t*>(p.u + rowp(lane >> 1) * DH + d0 + 8 * (lane & 1));
-  // C^T operand of the state term: column t = 16 tb + lane % 16, n-run
+  // C^T operand of the state term: column t = 16 tb + lane % 16, n-run.
+  // N = 16: loaded here with the rest (8 bytes per lane); wider: a second
+  // read of the C rows loaded above for C B^T, issued only when phase 2
+  // starts (from L2 then), which keeps it out of the start-up burst
   constexpr int KC = NS == 16 ? 1 : NS / 32;
   u16x8_t ctf[2][KC];
   u16x4_t ctf4[2];
+  auto load_ct = [&]() {
 #pragma unroll
-  for (int tb = 0; tb < 2; ++tb) {
-    const int64_t base = rowp(16 * tb + l15) * NS;
-    if constexpr (NS == 16) {
-      ctf4[tb] = *reinterpret_cast<const u16x4_t*>(p.Cm + base + 4 * l4);
-    } else {
+    for (int tb = 0; tb < 2; ++tb) {
+      const int64_t base = rowp(16 * tb + l15) * NS;
+      if constexpr (NS == 16) {
+        ctf4[tb] = *reinterpret_cast<const u16x4_t*>(p.Cm + base + 4 * l4);
+      } else {
 #pragma unroll
-      for (int kk = 0; kk < KC; ++kk) ctf[tb][kk] = *reinterpret_cast<const u16x8_t*>(p.Cm + base + 32 * kk + 8 * l4);
+        for (int kk = 0; kk < KC; ++kk)
+          ctf[tb][kk] = *reinterpret_cast<const u16x8_t*>(p.Cm + base + 32 * kk + 8 * l4);
+      }
     }
-  }
+  };
+  if constexpr (NS == 16) load_ct();
   const float xv = bf_val(p.delta[rowp(s32)]);
 
   // entering state of the carry below (one element per pass of its loop)
@@ -163,6 +170,7 @@ __global__ __launch_bounds__(64 * kResMaxChunks) void res_fwd_kernel(ChunkArgs p
     }
   }
   __syncthreads();
+  if constexpr (NS != 16) load_ct();
 
   // ---- 2. chunk-to-chunk carry, one thread per state element: all LDS
   // reads, then the chain, then the LDS writes, then the checkpoint stores,
