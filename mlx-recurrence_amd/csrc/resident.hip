@@ -73,7 +73,10 @@ __global__ __launch_bounds__(64 * kResMaxChunks) void res_fwd_kernel(ChunkArgs p
   auto rowp = [&](int s) -> int64_t { return (row0 + s) * H + h; };
   ResWave<NS>& wv = sm.wv[c];
 
-  // ---- 1. loads (all issued before any use)
+  // ---- 1. loads (all issued before any use), in the order of their use:
+  // the step input, B and C (step scalars, decays and C B^T need nothing
+  // else, so they run while U is in flight), U last
+  const float xv = bf_val(p.delta[rowp(s32)]);
   u16x8_t bfr[KB], cfr[KB];   // B, C rows s = lane % 32, n = 16 kb + 8 (lane / 32) + e
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
@@ -81,7 +84,6 @@ __global__ __launch_bounds__(64 * kResMaxChunks) void res_fwd_kernel(ChunkArgs p
     bfr[kb] = *reinterpret_cast<const u16x8_t*>(p.Bm + off);
     cfr[kb] = *reinterpret_cast<const u16x8_t*>(p.Cm + off);
   }
-  const u16x8_t ufr = *reinterpret_cast<const u16x8_t*>(p.u + rowp(lane >> 1) * DH + d0 + 8 * (lane & 1));
   // C^T operand of the state term: column t = 16 tb + lane % 16, n-run.
   // N = 16: loaded here with the rest (8 bytes per lane); wider: a second
   // read of the C rows loaded above for C B^T, issued only when phase 2
@@ -103,7 +105,7 @@ __global__ __launch_bounds__(64 * kResMaxChunks) void res_fwd_kernel(ChunkArgs p
     }
   };
   if constexpr (NS == 16) load_ct();
-  const float xv = bf_val(p.delta[rowp(s32)]);
+  const u16x8_t ufr = *reinterpret_cast<const u16x8_t*>(p.u + rowp(lane >> 1) * DH + d0 + 8 * (lane & 1));
 
   // entering state of the carry below (one element per pass of its loop)
   float h0v[4] = {0.f, 0.f, 0.f, 0.f};
@@ -118,10 +120,9 @@ __global__ __launch_bounds__(64 * kResMaxChunks) void res_fwd_kernel(ChunkArgs p
     }
   }
 
-  // ---- stage U and B; step scalars (lanes s and s + 32 both hold step s)
-  *reinterpret_cast<u16x8_t*>(&wv.u[SU::off(lane >> 1, 8 * (lane & 1))]) = ufr;
-#pragma unroll
-  for (int kb = 0; kb < KB; ++kb) *reinterpret_cast<u16x8_t*>(&wv.x.b[SB::off(s32, 16 * kb + 8 * hi32)]) = bfr[kb];
+  // ---- step scalars (lanes s and s + 32 both hold step s) and the
+  // elements of W = M o C B^T o w_s (registers: they are stored over the B
+  // staging once the aggregate has read it)
   const StepScalars sc = step_scalars<GLA>(xv, a, lane);
   if (lane < Q) {
     wv.g[lane] = GLA ? xv : sc.cd;
@@ -129,6 +130,21 @@ __global__ __launch_bounds__(64 * kResMaxChunks) void res_fwd_kernel(ChunkArgs p
     wv.gam[lane] = sc.gam;
   }
   if (lane == 0) sm.tot[c] = sc.tot;
+  float wel[16];
+  {
+    f32x16_t cb = {};
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) cb = mfma32(cfr[kb], bfr[kb], cb);
+    wave_lds_sync();   // the step scalars above, for the decays
+    float m[16];
+    decay_block32<GLA>(wv.g, a, lane, m);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) wel[r] = m[r] * sc.w * cb[r];
+  }
+  // ---- stage U and B
+  *reinterpret_cast<u16x8_t*>(&wv.u[SU::off(lane >> 1, 8 * (lane & 1))]) = ufr;
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) *reinterpret_cast<u16x8_t*>(&wv.x.b[SB::off(s32, 16 * kb + 8 * hi32)]) = bfr[kb];
   wave_lds_sync();
 
   // ---- chunk aggregate S_c[d][n] = sum_s U[s][d] wend_s B[s][n]
@@ -152,22 +168,15 @@ __global__ __launch_bounds__(64 * kResMaxChunks) void res_fwd_kernel(ChunkArgs p
       for (int r = 0; r < 4; ++r) sm.st[c][4 * l4 + r][16 * nb + l15] = acc[r];   // D: row d, col n
     }
   }
-  // ---- W = M o C B^T o w_s (over the B staging: this wave's reads are done)
-  {
-    f32x16_t cb = {};
+  // ---- W, hi and lo (over the B staging: this wave's reads are done)
+  wave_lds_sync();   // the transposing reads of B above precede the W stores
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) cb = mfma32(cfr[kb], bfr[kb], cb);
-    float m[16];
-    decay_block32<GLA>(wv.g, a, lane, m);
-    wave_lds_sync();   // the transposing reads of B above precede the W stores
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int t = r32row(r, lane);
-      uint16_t whi, wlo;
-      bf_split(m[r] * sc.w * cb[r], whi, wlo);
-      wv.x.w[0][w_off(t, s32)] = whi;
-      wv.x.w[1][w_off(t, s32)] = wlo;
-    }
+  for (int r = 0; r < 16; ++r) {
+    const int t = r32row(r, lane);
+    uint16_t whi, wlo;
+    bf_split(wel[r], whi, wlo);
+    wv.x.w[0][w_off(t, s32)] = whi;
+    wv.x.w[1][w_off(t, s32)] = wlo;
   }
   __syncthreads();
   if constexpr (NS != 16) load_ct();
