@@ -383,6 +383,12 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
           m.cd[lane] = sc.cd;
         }
       }
+    }
+    // sum lam o h_in per column (trn) and per wave (trw, read in phase B2);
+    // whole head: with lam's LDS copy, before the barrier; register modes:
+    // after it, so that the staging above does not wait for h_in (the
+    // chunk's largest load)
+    auto lam_hin = [&]() __attribute__((always_inline)) {
       float part = 0.f;
 #pragma unroll
       for (int cc = 0; cc < CPW; ++cc) {
@@ -409,8 +415,10 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
       }
       part = rr::wave_sum(part);
       if (lane == 0) m.trw[w] = part;
-    }
+    };
+    if constexpr (!REG) lam_hin();
     __syncthreads();
+    if constexpr (REG) lam_hin();
     // ------------------------------------------------ B1: GH, UL (registers), CB, G2 (32x32)
     f32x4_t gh[CPW][2], ul[CPW][2];
     float xs[2][4] = {}, ys[2][4] = {};   // this lane's shares of the row sums X, Y
