@@ -356,6 +356,15 @@ SSD_CASES = [
     # pipelined with B*H >= 320: the per-head state / adjoint scan kernel
     (1, 640, 320, 32, 16, 32, BF16, "cfg", True, True, 38),
     (2, 320, 160, 32, 64, 32, BF16, "cfg", True, True, 39),
+    # VALU engine (fp32 / fp16 inputs, dense A_neg [H, N], T < 32) past one
+    # round of 8 chunks per workgroup: the state and the adjoint cross rounds
+    (2, 512, 3, 64, 16, 32, F32, "ref", True, True, 50),    # the reference's contract, 16 chunks
+    (1, 320, 2, 32, 16, 16, F32, "ref", True, True, 51),    # seg 16: 20 chunks, ragged last round
+    (3, 512, 12, 64, 16, 32, BF16, "ref", True, True, 52),  # config 1's shape with a dense A
+    (1, 1024, 2, 32, 8, 32, F32, "cfg", True, True, 53),    # 32 chunks, four rounds
+    (1, 200, 2, 32, 16, 8, F16, "ref", True, True, 54),     # T = 8: 25 chunks
+    (1, 320, 2, 64, 16, 16, BF16, "cfg", True, True, 55),   # bf16 with T = 16: 20 chunks
+    (2, 512, 2, 64, 40, 32, F32, "ref", False, True, 56),   # N = 40: three n-tiles, partial sums
 ]
 
 
@@ -441,6 +450,12 @@ GLA_CASES = [
     (2, 64, 256, 32, 32, BF16, "zeros", True, True, 37),    # whole-head forward, Dh = 32
     (1, 32, 512, 128, 32, BF16, "cfg", True, True, 38),     # whole-head forward and backward, Dh = 128
     (1, 64, 512, 128, 32, BF16, "zeros", True, True, 40),   # whole head, Dh = 128, 2 chunks, zero gates
+    # VALU engine past one round of 8 chunks (fp32 / fp16 inputs, T < 32)
+    (2, 512, 3, 64, 32, F32, "ref", True, True, 50),        # the reference's contract, 16 chunks
+    (1, 512, 2, 64, 32, F16, "cfg", True, True, 51),
+    (1, 320, 2, 32, 16, F32, "signed", True, True, 52),     # T = 16: 20 chunks
+    (2, 200, 2, 32, 8, F32, "zeros", True, True, 53),       # T = 8: 25 chunks, zero gates
+    (1, 320, 2, 64, 16, BF16, "cfg", True, True, 54),       # bf16 with T = 16
 ]
 
 
