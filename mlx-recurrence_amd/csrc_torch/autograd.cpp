@@ -79,9 +79,13 @@ void check(int rc, const char* what) {
   throw std::runtime_error(std::string(what) + " failed (code " + std::to_string(rc) + "): " + msg);
 }
 
-// The outputs and workspace of one pass carved out of a single allocation (one
-// caching-allocator call instead of one per buffer): tensors are strided
-// views of it, the workspace a byte offset.  Pieces start 256-byte aligned.
+// The outputs of one pass that the caller receives together (the backward's
+// gradients) carved out of a single allocation (one caching-allocator call
+// instead of one per buffer): tensors are strided views of it.  Pieces start
+// 256-byte aligned.  The workspace and the forward's checkpoints are separate
+// allocations, so that the workspace is released (stream-ordered) when the
+// pass returns and the checkpoints live exactly as long as the autograd node
+// that saved them, whatever the caller keeps of y or of the gradients.
 class Arena {
  public:
   // reserve a piece of `bytes`; returns its byte offset
@@ -104,6 +108,13 @@ class Arena {
   int64_t total_ = 0, esize_ = 1;
   Tensor buf_;
 };
+
+// A pass's workspace: `bytes` of device memory (undefined when 0), released to
+// the caching allocator when the tensor goes out of scope; the allocator
+// reuses the block only for work ordered after this pass on the stream.
+Tensor workspace(size_t bytes, const at::TensorOptions& opts) {
+  return bytes ? at::empty({(int64_t)bytes}, opts.dtype(at::kByte)) : Tensor();
+}
 
 int64_t numel(at::IntArrayRef sizes) {
   int64_t n = 1;
@@ -138,13 +149,11 @@ struct SSDFn : public torch::autograd::Function<SSDFn> {
     const Tensor h0_ = h0.defined() ? prep(h0, at::kFloat) : Tensor();
     const int64_t nC = L / rr_chunk_len(L, seg);
     const size_t wsb = rr_ssd_workspace_bytes(Bsz, L, H, Dh, N, seg, a_sn, dtype_code(dt), 0);
-    Arena ar;
-    const int64_t oy = ar.reserve(Bsz * L * H * Dh * 4), ock = ar.reserve(Bsz * H * nC * Dh * N * 4);
-    const int64_t ows = ar.reserve((int64_t)wsb);
-    ar.allocate(u_.options(), at::kFloat);
-    Tensor y = ar.view(oy, {Bsz, L, H, Dh}), ckpt = ar.view(ock, {Bsz, H, nC, Dh, N});
+    const auto f32 = u_.options().dtype(at::kFloat);
+    Tensor y = at::empty({Bsz, L, H, Dh}, f32), ckpt = at::empty({Bsz, H, nC, Dh, N}, f32);
+    const Tensor ws = workspace(wsb, u_.options());
     check(rr_ssd_fwd(P(u_), P(d_), P(B_), P(C_), PF(A_), a_sn, dtype_code(dt), Bsz, L, H, Dh, N, seg, PF(h0_),
-                     MF(y), MF(ckpt), wsb ? ar.ptr(ows) : nullptr, wsb, stream_of(u_)),
+                     MF(y), MF(ckpt), P(ws), wsb, stream_of(u_)),
           "rr_ssd_fwd");
     ctx->save_for_backward({u_, d_, B_, C_, A_, h0_, ckpt});
     ctx->saved_data["seg"] = seg;
@@ -172,18 +181,18 @@ struct SSDFn : public torch::autograd::Function<SSDFn> {
     const int dtc = dtype_code(dt);
     const size_t wsb = rr_ssd_workspace_bytes(Bsz, L, H, Dh, N, seg, a_sn, dtc, 1);
     const bool heads = ctx->saved_data["a_dim"].toInt() == 1;   // A_neg [H]: its gradient sums dA over n
-    Arena ar;   // du, ddelta, dB, dC in the inputs' dtype; dA (fp32, [H] case) and the workspace as bytes
+    Arena ar;   // du, ddelta, dB, dC in the inputs' dtype; dA (fp32, [H] case) as bytes
     const int64_t odu = ar.reserve(u_.numel() * es), odd = ar.reserve(d_.numel() * es);
     const int64_t odB = ar.reserve(B_.numel() * es), odC = ar.reserve(C_.numel() * es);
-    const int64_t odA = heads ? ar.reserve(H * N * 4) : 0, ows = ar.reserve((int64_t)wsb);
+    const int64_t odA = heads ? ar.reserve(H * N * 4) : 0;
     ar.allocate(u_.options(), dt);
+    const Tensor ws = workspace(wsb, u_.options());
     Tensor du = ar.view(odu, u_.sizes()), dd = ar.view(odd, d_.sizes());
     Tensor dB = ar.view(odB, B_.sizes()), dC = ar.view(odC, C_.sizes());
     Tensor dA_full = heads ? Tensor() : at::empty({H, N}, f32);
     float* dA = heads ? static_cast<float*>(ar.ptr(odA)) : MF(dA_full);
     check(rr_ssd_bwd(PF(dy), PF(dfinal), P(u_), P(d_), P(B_), P(C_), PF(A_), a_sn, dtc, Bsz, L, H, Dh, N, seg,
-                     PF(h0_), PF(ckpt), P(du), P(dd), P(dB), P(dC), dA, MF(dh0), wsb ? ar.ptr(ows) : nullptr, wsb,
-                     stream_of(u_)),
+                     PF(h0_), PF(ckpt), P(du), P(dd), P(dB), P(dC), dA, MF(dh0), P(ws), wsb, stream_of(u_)),
           "rr_ssd_bwd");
     // [H] case: the sum over n reads the arena's piece through a non-owning
     // tensor; the arena outlives the enqueue, and a block freed to the caching
@@ -212,13 +221,11 @@ struct GLAFn : public torch::autograd::Function<GLAFn> {
     const Tensor h0_ = h0.defined() ? prep(h0, at::kFloat) : Tensor();
     const int64_t nC = L / rr_chunk_len(L, seg);
     const size_t wsb = rr_gla_workspace_bytes(B, L, H, Dh, seg, dtype_code(dt), 0);
-    Arena ar;
-    const int64_t oy = ar.reserve(B * L * H * Dh * 4), ock = ar.reserve(B * H * nC * Dh * Dh * 4);
-    const int64_t ows = ar.reserve((int64_t)wsb);
-    ar.allocate(q_.options(), at::kFloat);
-    Tensor y = ar.view(oy, {B, L, H, Dh}), ckpt = ar.view(ock, {B, H, nC, Dh, Dh});
+    const auto f32 = q_.options().dtype(at::kFloat);
+    Tensor y = at::empty({B, L, H, Dh}, f32), ckpt = at::empty({B, H, nC, Dh, Dh}, f32);
+    const Tensor ws = workspace(wsb, q_.options());
     check(rr_gla_fwd(P(q_), P(k_), P(v_), P(g_), dtype_code(dt), B, L, H, Dh, seg, PF(h0_), MF(y), MF(ckpt),
-                     wsb ? ar.ptr(ows) : nullptr, wsb, stream_of(q_)),
+                     P(ws), wsb, stream_of(q_)),
           "rr_gla_fwd");
     ctx->save_for_backward({q_, k_, v_, g_, h0_, ckpt});
     ctx->saved_data["seg"] = seg;
@@ -244,15 +251,15 @@ struct GLAFn : public torch::autograd::Function<GLAFn> {
     const int64_t es = (int64_t)c10::elementSize(dt);
     const int dtc = dtype_code(dt);
     const size_t wsb = rr_gla_workspace_bytes(B, L, H, Dh, seg, dtc, 1);
-    Arena ar;   // dq, dk, dv, dgates in the inputs' dtype; the workspace as bytes
+    Arena ar;   // dq, dk, dv, dgates in the inputs' dtype
     const int64_t n4 = q_.numel() * es;
     const int64_t odq = ar.reserve(n4), odk = ar.reserve(n4), odv = ar.reserve(n4), odg = ar.reserve(g_.numel() * es);
-    const int64_t ows = ar.reserve((int64_t)wsb);
     ar.allocate(q_.options(), dt);
+    const Tensor ws = workspace(wsb, q_.options());
     Tensor dq = ar.view(odq, q_.sizes()), dk = ar.view(odk, k_.sizes()), dv = ar.view(odv, v_.sizes());
     Tensor dg = ar.view(odg, g_.sizes());
     check(rr_gla_bwd(PF(dy), PF(dfinal), P(q_), P(k_), P(v_), P(g_), dtc, B, L, H, Dh, seg, PF(h0_), PF(ckpt), P(dq),
-                     P(dk), P(dv), P(dg), MF(dh0), wsb ? ar.ptr(ows) : nullptr, wsb, stream_of(q_)),
+                     P(dk), P(dv), P(dg), MF(dh0), P(ws), wsb, stream_of(q_)),
           "rr_gla_bwd");
     return {dq, dk, dv, dg, dh0, Tensor()};
   }
@@ -270,5 +277,7 @@ PYBIND11_MODULE(_autograd, m) {
   m.doc() = "C++ autograd bindings of the gfx950 SSD and GLA scans";
   m.def("ssd_scan", &ssd_scan, "SSD scan (y, final state) as one C++ autograd node");
   m.def("gla_scan", &gla_scan, "GLA scan (y, final state) as one C++ autograd node");
-  m.def("abi_version", [] { return rr_abi_version(); });
+  // the header revision this module was compiled against (not the loaded
+  // library's, which the Python loader compares it with)
+  m.def("abi_version", [] { return RR_ABI_VERSION; });
 }

@@ -95,3 +95,58 @@ def test_gla_bindings_agree(h0, dfinal):
     for i, (x, y_) in enumerate(zip(a_ext, a_py)):
         assert x.shape == y_.shape and x.dtype == y_.dtype, i
         assert torch.equal(x, y_), f"output {i} differs"
+
+
+@pytest.mark.parametrize("kind", ["ssd", "gla"])
+def test_bindings_release_workspace_and_checkpoints(kind):
+    """The C++ bindings' allocations end with their use: after backward, with
+    the gradients and y alive, the device holds the gradients, y and the
+    inputs only (the backward's workspace is released when the pass returns,
+    and the checkpoints with the autograd graph); y alone does not hold the
+    checkpoints."""
+    ext = _lib.autograd_ext()
+    assert ext is not None, "the C++ autograd bindings are not built"
+    print(f"[case] bindings memory {kind}", flush=True)
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(9)
+    # more than 16 chunks: the pipelined backward, whose workspace holds every chunk's adjoint
+    B, L, H, Dh, N = 1, 1024, 3, 64, 16
+    if kind == "ssd":
+        xs = [torch.randn(B, L, H, Dh, generator=g), torch.rand(B, L, H, generator=g) * 0.1 + 0.01,
+              torch.randn(B, L, H, N, generator=g), torch.randn(B, L, H, N, generator=g)]
+        xs = [x.bfloat16().to(dev).requires_grad_(True) for x in xs]
+        A = (-torch.rand(H, generator=g) - 0.5).to(dev).requires_grad_(True)
+        ws = _lib.ssd_workspace(B, L, H, Dh, N, 32, 0, torch.bfloat16, 1, dev)
+        ck_bytes = B * H * (L // 32) * Dh * N * 4
+        xs.append(A)
+
+        def call(ys):
+            return ext.ssd_scan(*ys, None, 32)
+    else:
+        xs = [(torch.randn(B, L, H, Dh, generator=g) / 8).bfloat16().to(dev).requires_grad_(True) for _ in range(3)]
+        xs.append(torch.sigmoid(torch.randn(B, L, H, generator=g) + 2).bfloat16().to(dev).requires_grad_(True))
+        ws = _lib.gla_workspace(B, L, H, Dh, 32, torch.bfloat16, 1, dev)
+        ck_bytes = B * H * (L // 32) * Dh * Dh * 4
+
+        def call(ys):
+            return ext.gla_scan(*ys, None, 32)
+    ws_bytes = 0 if ws is None else ws.numel()
+    del ws
+    assert ws_bytes > 256 * 1024, "the case is meant to have a sizeable backward workspace"
+    w_y = torch.randn(B, L, H, Dh, generator=g).to(dev)
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated(dev)
+    y, fs = call(xs)
+    del fs
+    torch.cuda.synchronize()
+    held = torch.cuda.memory_allocated(dev) - base
+    y_bytes = y.numel() * 4
+    # forward: y and the checkpoints (saved by the graph), no workspace
+    assert held <= y_bytes + ck_bytes + 64 * 1024, (held, y_bytes, ck_bytes)
+    (y * w_y).sum().backward()
+    torch.cuda.synchronize()
+    held = torch.cuda.memory_allocated(dev) - base
+    grad_bytes = sum(x.grad.numel() * x.grad.element_size() for x in xs)
+    # graph freed: y and the gradients remain (256-byte piece alignment, allocator rounding)
+    assert held <= y_bytes + grad_bytes + 64 * 1024, (held, y_bytes, grad_bytes, ws_bytes)
+    assert held < y_bytes + grad_bytes + ws_bytes // 2
