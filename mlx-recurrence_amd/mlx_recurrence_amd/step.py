@@ -9,7 +9,7 @@ output.  The states are the final-state layouts of the scans
     y, state = mr.ssd_scan_with_state(u, delta, B, C, A_neg)     # prompt
     y_t = mr.ssd_step(u_t, delta_t, B_t, C_t, A_neg, state)      # then per token
 
-    ssd_step(u [B,H,Dh], delta [B,H], B [B,H,N], C [B,H,N], A_neg [H,N], state [B,H,Dh,N]) -> y [B,H,Dh]
+    ssd_step(u [B,H,Dh], delta [B,H], B [B,H,N], C [B,H,N], A_neg [H,N] or [H], state [B,H,Dh,N]) -> y [B,H,Dh]
     gla_step(q, k, v [B,H,Dh], gates [B,H], state [B,H,Dh,Dh])                           -> y [B,H,Dh]
     rglru_step(a, x [B,D], state [B,D])                                                   -> y [B,D]
     rotlru_step(a, cs, sn [B,Dp], x [B,2Dp], state [B,2Dp])                               -> y [B,2Dp]
@@ -27,9 +27,12 @@ from . import _lib
 from .ssd import _decay_rates
 
 
-def _prepare(name, state, inputs, state_shape):
-    dev = _lib.require_device(state, *inputs)
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (state, *inputs)):
+def _prepare(name, state, inputs, state_shape, params=()):
+    """Device and compute dtype of one step.  The dtype comes from the token
+    inputs alone; `params` (SSD's fp32 A_neg) are checked for device and
+    autograd but do not promote the token inputs."""
+    dev = _lib.require_device(state, *inputs, *params)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (state, *inputs, *params)):
         raise ValueError(f"{name} is not differentiable (inference only); call it under torch.no_grad()")
     if tuple(state.shape) != tuple(state_shape):
         raise ValueError(f"{name}: state must be {list(state_shape)}, got {tuple(state.shape)}")
@@ -41,19 +44,23 @@ def _prepare(name, state, inputs, state_shape):
 
 def ssd_step(u, delta, B, C, A_neg, state):
     """One SSD token: state[b,h,d,n] = exp(delta A_neg[h,n]) state + delta B[n] u[d];
-    returns y[b,h,d] = sum_n state[b,h,d,n] C[n] (reference ssd.py:97-101)."""
+    returns y[b,h,d] = sum_n state[b,h,d,n] C[n] (reference ssd.py:97-101).
+    A_neg is [H, N] or one rate per head [H], as for ssd_scan; the token
+    inputs run in their own dtype (A_neg, fp32, does not promote them)."""
     if u.ndim != 3:
         raise ValueError(f"u must be [B, H, Dh], got shape {tuple(u.shape)}")
     Bsz, H, Dh = u.shape
-    if A_neg.ndim != 2 or A_neg.shape[0] != H:
-        raise ValueError(f"A_neg must be [H, N] with H={H}, got {tuple(A_neg.shape)}")
-    N = A_neg.shape[1]
+    if B.ndim != 3:
+        raise ValueError(f"B must be [B, H, N], got shape {tuple(B.shape)}")
+    N = B.shape[-1]
+    if A_neg.ndim not in (1, 2) or A_neg.shape[0] != H or (A_neg.ndim == 2 and A_neg.shape[1] != N):
+        raise ValueError(f"A_neg must be [H, N] or [H] with H={H}, N={N}, got {tuple(A_neg.shape)}")
     if tuple(delta.shape) != (Bsz, H):
         raise ValueError(f"delta must be [B, H] = [{Bsz}, {H}], got {tuple(delta.shape)}")
     for nm, t in (("B", B), ("C", C)):
         if tuple(t.shape) != (Bsz, H, N):
             raise ValueError(f"{nm} must be [B, H, N] = [{Bsz}, {H}, {N}], got {tuple(t.shape)}")
-    dev, dt = _prepare("ssd_step", state, (u, delta, B, C, A_neg), (Bsz, H, Dh, N))
+    dev, dt = _prepare("ssd_step", state, (u, delta, B, C), (Bsz, H, Dh, N), params=(A_neg,))
     u_, d_, B_, C_ = (_lib.prep(t, dt) for t in (u, delta, B, C))
     A_, a_sn = _decay_rates(A_neg)
     y = torch.empty((Bsz, H, Dh), dtype=torch.float32, device=dev)

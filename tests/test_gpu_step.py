@@ -42,6 +42,8 @@ SSD_CASES = [
     (1, 8, 2, 32, 256, F32, False, 3),      # N = 256: 64 lanes per row
     (8, 3, 80, 64, 128, BF16, True, 4),     # BASELINE config 4's state [8, 80, 64, 128]
     (1, 6, 2, 32, 24, F32, True, 5),        # N = 24: 8 lane groups, the last two past N
+    (2, 10, 3, 64, 16, BF16, "1d", 6),      # A_neg [H], as ssd_scan takes it
+    (1, 7, 2, 32, 32, F16, "1d", 7),
 ]
 
 
@@ -55,16 +57,47 @@ def test_ssd_step(B, L, H, Dh, N, dtype, per_head, seed):
     A = -np.exp(rng.uniform(0, np.log(16), (H, 1 if per_head else N)))
     h0 = rng.standard_normal((B, H, Dh, N)) * 0.5
     ut, dt_, Bt, Ct = (to_dev(v, dtype) for v in (u, dl, Bm, Cm))
-    At = to_dev(A[:, 0], F32)[:, None].expand(H, N) if per_head else to_dev(A, F32)
+    if per_head == "1d":
+        At = to_dev(A[:, 0], F32)
+    else:
+        At = to_dev(A[:, 0], F32)[:, None].expand(H, N) if per_head else to_dev(A, F32)
     state = to_dev(h0, F32).contiguous()
     with torch.no_grad():
         ys = torch.stack([mr.ssd_step(ut[:, t], dt_[:, t], Bt[:, t], Ct[:, t], At, state) for t in range(L)], 1)
-    r = [rounded(t) for t in (ut, dt_, Bt, Ct)] + [np.broadcast_to(rounded(At), (H, N))]
+    r = [rounded(t) for t in (ut, dt_, Bt, Ct)] + [np.broadcast_to(rounded(At).reshape(H, -1), (H, N))]
     y_o, fs_o = orc.ssd_forward(*r, h0.astype(np.float32).astype(np.float64))
     rep = {}
     check("y", ys, y_o, BAR, rep)
     check("state", state, fs_o, BAR, rep)
     print(rep, flush=True)
+
+
+def test_ssd_step_keeps_input_dtype(monkeypatch):
+    """A bf16 token runs the kernel's bf16 path: the fp32 A_neg does not
+    promote u / delta / B / C, so the step launches no cast."""
+    from mlx_recurrence_amd import _lib
+    seen = []
+    real = _lib.ssd_step
+
+    def spy(u, delta, Bm, Cm, A, a_sn, state, y):
+        seen.append((u, delta, Bm, Cm, A, a_sn))
+        return real(u, delta, Bm, Cm, A, a_sn, state, y)
+
+    monkeypatch.setattr(_lib, "ssd_step", spy)
+    dev = torch.device("cuda:0")
+    Bsz, H, Dh, N = 2, 3, 64, 16
+    u, Bm, Cm = (torch.randn(s_, device=dev).bfloat16() for s_ in ((Bsz, H, Dh), (Bsz, H, N), (Bsz, H, N)))
+    d = (torch.rand(Bsz, H, device=dev) * 0.1 + 0.01).bfloat16()
+    state = torch.zeros(Bsz, H, Dh, N, device=dev)
+    for A in (-torch.rand(H, device=dev) - 0.1, (-torch.rand(H, 1, device=dev) - 0.1).expand(H, N)):
+        seen.clear()
+        with torch.no_grad():
+            mr.ssd_step(u, d, Bm, Cm, A, state)
+        (u_, d_, B_, C_, A_, a_sn), = seen
+        assert all(t.dtype == torch.bfloat16 for t in (u_, d_, B_, C_))
+        assert (u_.data_ptr(), d_.data_ptr(), B_.data_ptr(), C_.data_ptr()) == \
+            (u.data_ptr(), d.data_ptr(), Bm.data_ptr(), Cm.data_ptr())
+        assert A_.dtype == torch.float32 and A_.shape == (H,) and a_sn == 0
 
 
 GLA_CASES = [
@@ -151,7 +184,7 @@ def test_steps_continue_a_chunked_prefill():
         y0, state = mr.ssd_scan_with_state(ut[:, :L0], dt_[:, :L0], Bt[:, :L0], Ct[:, :L0], At)
         state = state.contiguous()
         y1 = torch.stack([mr.ssd_step(ut[:, t], dt_[:, t], Bt[:, t], Ct[:, t], At, state) for t in range(L0, L)], 1)
-    r = [rounded(t) for t in (ut, dt_, Bt, Ct)] + [np.broadcast_to(rounded(At), (H, N))]
+    r = [rounded(t) for t in (ut, dt_, Bt, Ct)] + [np.broadcast_to(rounded(At).reshape(H, -1), (H, N))]
     y_o, fs_o = orc.ssd_forward(*r)
     rep = {}
     check("y", torch.cat([y0, y1], 1), y_o, BAR, rep)
