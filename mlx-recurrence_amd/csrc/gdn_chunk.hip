@@ -1011,37 +1011,58 @@ __global__ __launch_bounds__(64 * kGW) void gdn_cgrad_kernel(const float* __rest
     }
   });
   // ---- the step scalars (wave 0, lane t < 32): dbeta, dlg -> dalpha
+  //
+  // dL/dlog(alpha_m) is the suffix sum over r >= m of dlg_r = dL/dlg_r, with
+  //   dlg_r = rowE_r - colE_r + gam_r (p0 + beta_r p3)_r - f_r p1_r
+  //           (+ gam_31 <dS_out, S_in> + sum_t f_t p1_t at r = 31).
+  // Summed as written it cancels: the entries of E inside the block
+  // rows, columns >= m, and the f_r p1_r with r >= m, are O(1) whatever
+  // alpha_m, and appear with both signs, while the sum is O(alpha_m), so its
+  // rounding divided by a small alpha_m swamps dalpha_m.  The same sum,
+  // regrouped (E is lower triangular):
+  //   sum_{r >= m} dlg_r = sum_{r >= m, c < m} E[r][c] + sum_{r >= m} gam_r (p0 + beta_r p3)_r
+  //                        + sum_{t < m} f_t p1_t + gam_31 <dS_out, S_in>,
+  // where every term carries alpha_m as a factor (R[r][c] = gam_r / gam_c for
+  // c < m <= r, gam_r for r >= m, f_t = gam_31 / gam_t for t < m), so it keeps
+  // fp32 relative accuracy down to alpha_m = 0 (taken as 1e-30 above).
   if (w == 0) {
-    const int t = lane & 31;
-    float rowE = 0.f, colE = 0.f;   // E = dT's place: (P o dP + diag(beta) G o dA o R)
-    for (int m = 0; m < kQ; ++m) {
-      rowE += sm.dT[t][m];
-      colE += sm.dT[m][t];
+    const int t = lane & 31, half = lane >> 5;
+    // this lane's half of the rows (16 * half .. 16 * half + 15) of the block sum for m = t
+    float blk = 0.f;
+#pragma unroll 4
+    for (int rr_ = 0; rr_ < kQ / 2; ++rr_) {
+      const int r = 16 * half + rr_;
+      const float4* row = reinterpret_cast<const float4*>(&sm.dT[r][0]);
+      float acc = 0.f;
+#pragma unroll
+      for (int c4 = 0; c4 < kQ / 4; ++c4) {
+        const float4 e = row[c4];
+        acc += (4 * c4 + 0 < t ? e.x : 0.f) + (4 * c4 + 1 < t ? e.y : 0.f) + (4 * c4 + 2 < t ? e.z : 0.f) +
+               (4 * c4 + 3 < t ? e.w : 0.f);
+      }
+      blk += r >= t ? acc : 0.f;
     }
+    blk += __shfl_xor(blk, 32);
     auto rows = [&](int qn) { return (sm.part[qn][t][0] + sm.part[qn][t][1]) + (sm.part[qn][t][2] + sm.part[qn][t][3]); };
     const float p0 = rows(0), p1 = rows(1), p2 = rows(2), p3 = rows(3);
     const float p4 = (sm.part[4][t][0] + sm.part[4][t][1]);   // 32 columns: two blocks
     const float gm = sm.gam[t], be = sm.beta[t], ft = sm.f[t];
     const float dbe = p2 + gm * p3 + p4;
-    float dlg = rowE - colE + gm * (p0 + be * p3) - ft * p1;
-    // the chunk end: gam_31 <dS_out, S_in> and sum_t f_t rows(Kbar' o K)_t
-    float fsum = ft * p1;
-    fsum += __shfl_xor(fsum, 1, 32);
-    fsum += __shfl_xor(fsum, 2, 32);
-    fsum += __shfl_xor(fsum, 4, 32);
-    fsum += __shfl_xor(fsum, 8, 32);
-    fsum += __shfl_xor(fsum, 16, 32);
+    // suffix sum over r >= t of gam_r (p0 + beta_r p3)_r; prefix over t' < t of
+    // f p1, shifted by one lane first (f_t p1_t itself does not carry alpha_t,
+    // so an inclusive prefix minus it would cancel again)
+    float suf = gm * (p0 + be * p3), pre = __shfl_up(ft * p1, 1, 32);
+    pre = t > 0 ? pre : 0.f;
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) {
+      const float x = __shfl_down(suf, o, 32), y = __shfl_up(pre, o, 32);
+      if (t + o < 32) suf += x;
+      if (t >= o) pre += y;
+    }
     float dot = 0.f;
 #pragma unroll
     for (int ww = 0; ww < kGW; ++ww) dot += sm.dotp[ww];
-    if (t == kQ - 1) dlg += sm.gam[kQ - 1] * dot + fsum;
-    // dalpha_m = (sum_{r >= m} dlg_r) / alpha_m: suffix sum over the lanes
-    float suf = dlg;
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) {
-      const float x = __shfl_down(suf, o, 32);
-      if (t + o < 32) suf += x;
-    }
+    suf += blk + pre + sm.gam[kQ - 1] * dot;
     if (lane < kQ) {
       dalpha[(row0 + t) * H + h] = rr::bf_bits(suf / sm.al[t]);
       dbeta[(row0 + t) * H + h] = rr::bf_bits(dbe);

@@ -45,6 +45,10 @@ def _inputs(rng, B, L, H, Dh, dist):
         beta[:, ::7] = 0.0
         beta[:, 3::11] = 1.0
         alpha[:, 2::13] = 0.01
+    elif dist == "tiny":  # strong decays down to none of the state kept: the dalpha of small alpha
+        alpha[:, 3::9] = 1e-4
+        alpha[:, 5::11] = 1e-8
+        alpha[:, 7::13] = 0.0
     return q, k, v, alpha, beta
 
 
@@ -63,6 +67,9 @@ GDN_CASES = [
     (3, 512, 12, 64, 32, BF16, "plain", False, False, 6),  # bench shape (config 2's B, L, H, Dh)
     (2, 256, 4, 32, 32, F16, "edges", True, True, 7),
     (1, 128, 2, 64, 32, BF16, "edges", True, True, 8),
+    # alpha of 1e-4, 1e-8 and 0: dalpha at a strong decay (chunkwise form, then sequential)
+    (2, 128, 3, 64, 32, BF16, "tiny", True, True, 9),
+    (1, 96, 2, 64, 32, F32, "tiny", True, True, 10),
 ]
 
 
@@ -191,7 +198,7 @@ def test_gdn_chunkwise_adjoint_matches_sequential():
         assert np.isfinite(err) and err < 1e-4, (name, err)
 
 
-@pytest.mark.parametrize("dist,seed", [("plain", 64), ("edges", 65)])
+@pytest.mark.parametrize("dist,seed", [("plain", 64), ("edges", 65), ("tiny", 66)])
 def test_gdn_chunkwise_gradients_match_sequential(dist, seed):
     """The chunkwise gradient pass (bf16 outputs) against the sequential
     kernels in fp32 on the same bf16-rounded inputs, rounded to bf16: at
