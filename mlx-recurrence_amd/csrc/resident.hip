@@ -62,7 +62,9 @@ __global__ __launch_bounds__(64 * kResMaxChunks) void res_fwd_kernel(ChunkArgs p
   __shared__ ResSmem<NS> sm;
   const int nDQ = p.DH / DQ;
   const int id = blockIdx.x, xcd = id % kXcds, k = id / kXcds;
-  const int dq = k % nDQ, bh = (k / nDQ) * kXcds + xcd;   // a head's slices share an XCD
+  // a head's slices share an XCD, and so do heads whose B / C rows share lines
+  const int groups = (p.B * p.H + kXcds - 1) / kXcds;
+  const int dq = k % nDQ, bh = head_on_xcd(k / nDQ, xcd, groups, line_heads(NS));
   if (bh >= p.B * p.H) return;
   const int b = bh / p.H, h = bh % p.H;
   const int tid = threadIdx.x, lane = tid & 63, c = __builtin_amdgcn_readfirstlane(tid >> 6);

@@ -202,11 +202,24 @@ struct ChunkId {
   int c, h, b;
   bool valid;   // false for the padding workgroups of the last head group
 };
+// Heads whose B / C rows share a 128-byte line: a step's row of one head is
+// NS bf16 values, so G = 128 / (2 NS) consecutive heads read the same lines
+// (N = 16: four heads per line).  Every read request fills a whole line, so
+// such heads placed on different XCDs fetch each line once per XCD.
+__host__ __device__ inline int line_heads(int NS) { return NS >= 64 ? 1 : 64 / NS; }
+// The (batch * H + head) index of head group j (of `groups`, 8 heads each) on
+// XCD x: runs of G consecutive heads on one XCD, as long as whole runs of G
+// groups remain; the rest one head per XCD in turn.  A bijection of
+// [0, 8 groups); every XCD gets `groups` heads, as with bh = 8 j + x.
+__host__ __device__ inline int head_on_xcd(int j, int x, int groups, int G) {
+  const int q = groups / G * G;
+  return j < q ? G * (kXcds * (j / G) + x) + j % G : kXcds * j + x;
+}
 __device__ __forceinline__ ChunkId chunk_id(const ChunkArgs& p, bool by_cost, bool late_first) {
   const int id = blockIdx.x, x = id % kXcds, slot = id / kXcds;
   const int groups = (p.B * p.H + kXcds - 1) / kXcds;   // head groups of 8
   const int cs = by_cost ? slot / groups : slot % p.nC;
-  const int bh = (by_cost ? slot % groups : slot / p.nC) * kXcds + x;
+  const int bh = head_on_xcd(by_cost ? slot % groups : slot / p.nC, x, groups, line_heads(p.NS));
   return ChunkId{late_first ? p.nC - 1 - cs : cs, bh % p.H, bh / p.H, bh < p.B * p.H};
 }
 inline dim3 chunk_grid(const ChunkArgs& p) {
@@ -215,7 +228,8 @@ inline dim3 chunk_grid(const ChunkArgs& p) {
 // kPair: the same decode over the nC / R runs of a head (c = run index)
 __device__ __forceinline__ ChunkId run_id(const ChunkArgs& p) {
   const int id = blockIdx.x, x = id % kXcds, slot = id / kXcds, nP = p.nC / p.R;
-  const int bh = (slot / nP) * kXcds + x;
+  const int groups = (p.B * p.H + kXcds - 1) / kXcds;
+  const int bh = head_on_xcd(slot / nP, x, groups, line_heads(p.NS));
   return ChunkId{slot % nP, bh % p.H, bh / p.H, bh < p.B * p.H};
 }
 inline dim3 run_grid(const ChunkArgs& p) {

@@ -33,7 +33,7 @@ struct ChunkArgs {
   float* tot;              // pipelined: per-chunk decay gam_31 [B,H,nC]
   float* agg;              // pipelined backward: chunk aggregates, then adjoints [B,H,nC,Dh,N]
   int B, L, H, DH, NS, nC;
-  int R;                   // chunks per workgroup: nC (whole-head mode) or 1
+  int R;                   // chunks per workgroup: nC (whole-head mode), 2 (pair mode) or 1
   int mode;                // rr::chunked::Mode (rr_chunked.h)
 };
 
