@@ -802,6 +802,8 @@ def measure(name, steps, warmup, dtype, device, cpu_seconds):
         fwd_us=pass_us["fwd"], bwd_us=pass_us["bwd"],
         kernels=[{"pass": r["pass_"], "index": r["index"], "us": round(r["us"], 3)} for r in kernels],
         dominant={"pass": dom["pass_"], "index": dom["index"], "us": dom["us"], "bytes": dom["pass_bytes"],
+                  "pass_us": pass_us[dom["pass_"]],
+                  "pass_frac": dom["pass_bytes"] / (pass_us[dom["pass_"]] * 1e-6) / 1e9 / HBM_PEAK_GBS,
                   "n_kernels_in_pass": dom["n_kernels"]},
         achieved_gbs=achieved, eager_ms_per_step=eager_ms,
         peak_transient_bytes=int(peak_extra), state_history_bytes=int(w["state_hist_bytes"]),
@@ -854,33 +856,79 @@ def cpu_baseline(w, seconds):
 
 
 # ------------------------------------------------------------------ counters
-# roofline.traffic comes from two rocprofv3 counter runs of `--pmc-run`
-# (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the same
-# counter reads for a plain device copy of known size (`--calibrate-copy`); a
-# third run reads the MFMA counters (busy cycles, bf16 MOPS, instruction
-# counts).  `--pmc-summary` turns the runs into profiles/pmc_traffic.json, which
-# a normal run reads for its dominant kernel.
+# roofline.traffic comes from two rocprofv3 counter runs of `--pmc-run`: the
+# raw TCC request counters behind FETCH_SIZE (read requests sent to memory, by
+# size: 128-byte = TCC_BUBBLE, 32-byte = TCC_EA0_RDREQ_32B, the rest of
+# TCC_EA0_RDREQ 64-byte) and WRITE_SIZE (TCC_EA0_WRREQ, of which
+# TCC_EA0_WRREQ_64B are 64-byte, the rest 32-byte), turned into bytes by the
+# gfx950 FETCH_SIZE / WRITE_SIZE formulas.  Three calibrations check the
+# counters against kernels whose bytes and flops are known: a plain device copy
+# (`--calibrate copy`), a read of one 32-byte sector per 128-byte line
+# (`--calibrate sector`) and a bf16 GEMM of known size (`--calibrate gemm`).  A
+# third run per workload reads the MFMA counters (busy cycles, bf16 MOPS,
+# instruction counts).  `--pmc-summary` turns the runs into
+# profiles/pmc_traffic.json, which a normal run reads for its dominant kernel.
 PMC_FILE = ROOT / "profiles" / "pmc_traffic.json"
 COUNTER_SETS = {
-    "fetch": ["FETCH_SIZE"],
-    "write": ["WRITE_SIZE"],
+    "fetch": ["TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum", "TCC_BUBBLE_sum"],
+    "write": ["TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum"],
     "mfma": ["SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU",
              "SQ_INSTS_MFMA", "SQ_BUSY_CU_CYCLES"],
 }
-PROFILED_WORKLOADS = ["ssd", "gla", "rglru", "rotlru", "rglru_gated", "rotlru_theta", "ssd_c4", "ssd_b96", "gla_b96",
-                      "ssd_dense", "ssd_f32", "ssd_dh128", "gla_f32", "gla_dh128", "gdn"]
+CALIBRATIONS = {"copy": ("fetch", "write"), "sector": ("fetch", "write"), "gemm": ("mfma",)}
+CAL_MB = 256          # copy / sector read source size
+CAL_GEMM = 8192       # M = N = K of the calibration GEMM
+PROFILED_WORKLOADS = ["ssd", "gla", "rglru", "rotlru", "ssd_c4", "ssd_dh128", "gla_dh128", "rglru_gated",
+                      "rotlru_theta", "ssd_b96", "gla_b96", "ssd_dense", "ssd_f32", "gla_f32", "gdn"]
 PROFILE_COMMANDS = [
     "rocprofv3 --kernel-trace --stats -d $R/gpurun_out/prof_trace -o trace --output-format csv -- "
-    "python3 bench.py --steps 20 --warmup 3 --no-cpu --also " + ",".join(PROFILED_WORKLOADS[1:]),
-    "rocprofv3 --pmc FETCH_SIZE -d $R/gpurun_out/pmc/cal_fetch -o cal --output-format csv -- "
-    "python3 bench.py --calibrate-copy 256",
-    "rocprofv3 --pmc WRITE_SIZE -d $R/gpurun_out/pmc/cal_write -o cal --output-format csv -- "
-    "python3 bench.py --calibrate-copy 256",
+    "python3 bench.py --steps 20 --warmup 3 --no-cpu --no-decode --also " + ",".join(PROFILED_WORKLOADS[1:]),
+    "for k in " + " ".join(CALIBRATIONS) + "; do for c in <sets of k>; do rocprofv3 --pmc <counters of set c> "
+    "-d $R/gpurun_out/pmc/cal_${k}_$c -o cal --output-format csv -- python3 bench.py --calibrate $k; done; done "
+    "(copy, sector: fetch write; gemm: mfma)",
     "for w in " + " ".join(PROFILED_WORKLOADS) + "; do for c in fetch write mfma; do rocprofv3 --pmc <counters of "
     "set c> -d $R/gpurun_out/pmc/${w}_$c -o $w --output-format csv -- python3 bench.py --pmc-run $w; done; done "
     "(sets: " + "; ".join(f"{k}: {' '.join(v)}" for k, v in COUNTER_SETS.items()) + ")",
     "python3 bench.py --pmc-summary --trace-dir gpurun_out/prof_trace",
 ]
+
+
+def calibrate(kind, device):
+    """Kernels whose HBM bytes / MFMA flops are known, for the counter runs.
+    copy: 5 device copies of CAL_MB MiB (fp32), each reads and writes CAL_MB MiB.
+    sector: 5 reads of one 32-byte sector of every 128-byte line of a CAL_MB MiB
+    fp32 tensor (sum over 8 of every 32 floats; CAL_MB/4 MiB of sectors touched,
+    CAL_MB/128 MiB written).  gemm: 5 bf16 GEMMs M = N = K = CAL_GEMM
+    (2 CAL_GEMM^3 flops each), timed with HIP events."""
+    import torch
+    out = {"kind": kind}
+    if kind == "gemm":
+        a = torch.randn((CAL_GEMM, CAL_GEMM), device=device, dtype=torch.bfloat16)
+        b = torch.randn((CAL_GEMM, CAL_GEMM), device=device, dtype=torch.bfloat16)
+        torch.matmul(a, b)
+        torch.cuda.synchronize()
+        us = []
+        for _ in range(5):
+            st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            st.record()
+            torch.matmul(a, b)
+            en.record()
+            en.synchronize()
+            us.append(st.elapsed_time(en) * 1e3)
+        out.update(flops=2 * CAL_GEMM ** 3, us=us)
+    else:
+        n = CAL_MB * (1 << 20) // 4
+        src = torch.randn(n, device=device)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            if kind == "copy":
+                torch.empty_like(src).copy_(src)
+            else:
+                src.view(-1, 32)[:, :8].sum(dim=1)
+        torch.cuda.synchronize()
+        out.update(read_bytes=4 * n if kind == "copy" else n,
+                   write_bytes=4 * n if kind == "copy" else n // 32 * 4, launches=5)
+    print(json.dumps({"calibrate": out}), flush=True)
 
 
 def pmc_run(name, out_dir):
@@ -919,66 +967,128 @@ def _counter_rows(run_dir):
     return rows
 
 
-def _simd_count(run_dir, default=1024):
+def _agent_info(run_dir):
+    """SIMD count, XCD count and compute clock (MHz) of the GPU agent the counter
+    run saw (rocprofv3's agent_info.csv), with MI355X's values as defaults."""
     import csv
+    info = {"simd": 1024, "xcc": 8, "clk_mhz": 2400}
     for f in sorted(pathlib.Path(run_dir).rglob("*agent_info.csv")):
         with open(f) as fh:
             for r in csv.DictReader(fh):
-                if r.get("Agent_Type", r.get("Type", "")) == "GPU" or r.get("Name", "").startswith("gfx"):
-                    try:
-                        return int(r["Simd_Count"])
-                    except (KeyError, ValueError):
-                        pass
-    return default
+                if r.get("Agent_Type", "") == "GPU" or r.get("Name", "").startswith("gfx"):
+                    for key, col in (("simd", "Simd_Count"), ("xcc", "Num_Xcc"), ("clk_mhz", "Max_Engine_Clk_Fcompute")):
+                        try:
+                            info[key] = int(r[col])
+                        except (KeyError, ValueError):
+                            pass
+                    return info
+    return info
+
+
+def _per_dispatch(run_dir, counters):
+    """[(kernel name, {counter: value})] per dispatch, in dispatch order."""
+    out = {}
+    for r in _counter_rows(run_dir):
+        if r["Counter_Name"] in counters:
+            d = int(r["Dispatch_Id"])
+            name, vals = out.setdefault(d, (r["Kernel_Name"], {}))
+            vals[r["Counter_Name"]] = vals.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    return [out[k] for k in sorted(out)]
+
+
+def _fetch_bytes(v):
+    """gfx950's FETCH_SIZE formula in bytes: 128-byte requests (TCC_BUBBLE), the
+    32-byte ones, and the rest of TCC_EA0_RDREQ at 64 bytes."""
+    rd, r32, bub = v["TCC_EA0_RDREQ_sum"], v["TCC_EA0_RDREQ_32B_sum"], v["TCC_BUBBLE_sum"]
+    return 128.0 * bub + 64.0 * (rd - bub - r32) + 32.0 * r32
+
+
+def _write_bytes(v):
+    """gfx950's WRITE_SIZE formula in bytes: 64-byte write requests, the rest at 32."""
+    wr, w64 = v["TCC_EA0_WRREQ_sum"], v["TCC_EA0_WRREQ_64B_sum"]
+    return 64.0 * w64 + 32.0 * (wr - w64)
+
+
+def _calibration(root, kind):
+    """Counters of the calibration kernel `kind` (the last 5 dispatches of its
+    runs: the measured launches), per launch, beside the known figures."""
+    res = {}
+    for cset in CALIBRATIONS[kind]:
+        rows = _per_dispatch(root / f"cal_{kind}_{cset}", COUNTER_SETS[cset])[-5:]
+        if not rows:
+            return None
+        mean = {c: sum(v.get(c, 0.0) for _, v in rows) / len(rows) for c in COUNTER_SETS[cset]}
+        res.update(mean)
+        res["kernel"] = rows[-1][0]
+    if kind != "gemm":
+        n = CAL_MB * (1 << 20)
+        res["fetch_bytes"] = _fetch_bytes(res)
+        res["write_bytes"] = _write_bytes(res)
+        res["true_read_bytes"] = n if kind == "copy" else n // 4
+        res["true_write_bytes"] = n if kind == "copy" else n // 32
+    else:
+        info = _agent_info(root / "cal_gemm_mfma")
+        flops = 2.0 * CAL_GEMM ** 3
+        t_gui = res["GRBM_GUI_ACTIVE"] / info["xcc"] / (info["clk_mhz"] * 1e6)
+        res.update(true_flops=flops, counted_flops=res["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512,
+                   gui_us=t_gui * 1e6,
+                   mfma_util=res["SQ_VALU_MFMA_BUSY_CYCLES"] / (res["GRBM_GUI_ACTIVE"] / info["xcc"] * info["simd"]),
+                   flops_frac=flops / t_gui / (MFMA_BF16_PEAK_TFLOPS * 1e12))
+    return res
 
 
 def pmc_summary(root):
-    """profiles/pmc_traffic.json from the counter runs under `root`:
-    root/cal_fetch, root/cal_write (calibration copy), root/<w>_{fetch,write,mfma}
-    and root/<w>_passes.json for each workload w."""
+    """profiles/pmc_traffic.json from the counter runs under `root`: the
+    calibration runs root/cal_<kind>_<set>, and root/<w>_{fetch,write,mfma} and
+    root/<w>_passes.json for each workload w.
+
+    Per dispatch: fetch_bytes / write_bytes by the gfx950 FETCH_SIZE /
+    WRITE_SIZE formulas from the raw request counters, each times the factor
+    `scale` that makes the plain copy's counted bytes equal its true bytes
+    (stated beside the sector read's counted / true ratio, which tests that
+    factor on 32-byte requests); mfma_util = SQ_VALU_MFMA_BUSY_CYCLES /
+    (GRBM_GUI_ACTIVE / XCDs x SIMDs): GRBM_GUI_ACTIVE is summed over the XCDs,
+    each of which counts the whole dispatch."""
     root = pathlib.Path(root)
-
-    def per_dispatch(run_dir, counter):
-        out = {}
-        for r in _counter_rows(run_dir):
-            if r["Counter_Name"] == counter:
-                d = int(r["Dispatch_Id"])
-                out[d] = (r["Kernel_Name"], out.get(d, ("", 0.0))[1] + float(r["Counter_Value"]))
-        return [out[k] for k in sorted(out)]
-
-    scale = {}
-    for counter, sub_dir, true_kib in (("FETCH_SIZE", "cal_fetch", 256 * 1024), ("WRITE_SIZE", "cal_write", 256 * 1024)):
-        copies = [v for n, v in per_dispatch(root / sub_dir, counter) if "copy" in n.lower()]
-        scale[counter] = true_kib / copies[-1] if copies else None
-    summary = {"scale": scale, "workloads": {}}
+    cal = {k: _calibration(root, k) for k in CALIBRATIONS}
+    scale = {"fetch": 1.0, "write": 1.0}
+    if cal["copy"]:
+        scale["fetch"] = cal["copy"]["true_read_bytes"] / cal["copy"]["fetch_bytes"]
+        scale["write"] = cal["copy"]["true_write_bytes"] / cal["copy"]["write_bytes"]
+    summary = {"scale": scale, "calibration": cal, "workloads": {}}
     for w in WORKLOADS:
         pj = root / f"{w}_passes.json"
         if not pj.exists():
             continue
         counts = json.loads(pj.read_text())
         n = counts["fwd"] + counts["bwd"]
-        fetch = per_dispatch(root / f"{w}_fetch", "FETCH_SIZE")[-n:]
-        write = per_dispatch(root / f"{w}_write", "WRITE_SIZE")[-n:]
-        mf = {c: per_dispatch(root / f"{w}_mfma", c)[-n:] for c in COUNTER_SETS["mfma"]}
-        simd = _simd_count(root / f"{w}_mfma")
+        fetch = _per_dispatch(root / f"{w}_fetch", COUNTER_SETS["fetch"])[-n:]
+        write = _per_dispatch(root / f"{w}_write", COUNTER_SETS["write"])[-n:]
+        mf = _per_dispatch(root / f"{w}_mfma", COUNTER_SETS["mfma"])[-n:]
+        info = _agent_info(root / f"{w}_mfma")
         entry = {}
         for pname, lo, hi in (("fwd", 0, counts["fwd"]), ("bwd", counts["fwd"], n)):
             rows = []
             for i in range(lo, hi):
-                k = {"kernel": fetch[i][0] if i < len(fetch) else "",
-                     "fetch_bytes": fetch[i][1] * 1024 * (scale["FETCH_SIZE"] or 1.0) if i < len(fetch) else None,
-                     "write_bytes": write[i][1] * 1024 * (scale["WRITE_SIZE"] or 1.0) if i < len(write) else None}
-                if all(len(mf[c]) == n for c in mf):
-                    busy, gui = mf["SQ_VALU_MFMA_BUSY_CYCLES"][i][1], mf["GRBM_GUI_ACTIVE"][i][1]
+                k = {"kernel": fetch[i][0] if i < len(fetch) else ""}
+                if i < len(fetch):
+                    k["fetch_req"] = fetch[i][1]
+                    k["fetch_bytes"] = _fetch_bytes(fetch[i][1]) * scale["fetch"]
+                if i < len(write):
+                    k["write_req"] = write[i][1]
+                    k["write_bytes"] = _write_bytes(write[i][1]) * scale["write"]
+                if len(mf) == n:
+                    v = mf[i][1]
+                    busy, gui = v["SQ_VALU_MFMA_BUSY_CYCLES"], v["GRBM_GUI_ACTIVE"]
                     k.update(mfma_busy_cycles=busy, gui_active_cycles=gui,
-                             mfma_util=busy / (gui * simd) if gui else None,
-                             mfma_flops=mf["SQ_INSTS_VALU_MFMA_MOPS_BF16"][i][1] * 512,
-                             insts_valu=mf["SQ_INSTS_VALU"][i][1], insts_mfma=mf["SQ_INSTS_MFMA"][i][1],
-                             busy_cu_cycles=mf["SQ_BUSY_CU_CYCLES"][i][1])
+                             mfma_util=busy / (gui / info["xcc"] * info["simd"]) if gui else None,
+                             mfma_flops=v["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512,
+                             insts_valu=v["SQ_INSTS_VALU"], insts_mfma=v["SQ_INSTS_MFMA"],
+                             busy_cu_cycles=v["SQ_BUSY_CU_CYCLES"])
                 rows.append(k)
             entry[pname] = rows
         summary["workloads"][w] = entry
-    summary["simd_count"] = _simd_count(root / "ssd_mfma") if (root / "ssd_mfma").exists() else 1024
+        summary["agent"] = info
     PMC_FILE.parent.mkdir(exist_ok=True)
     PMC_FILE.write_text(json.dumps(summary, indent=1))
     print(f"wrote {PMC_FILE}")
@@ -991,7 +1101,8 @@ def profile_markdown(summary, trace_dir, out_md, commands):
     import csv
     import torch
     lines = ["# Bench workloads: SSD config 1 (headline), GLA config 2, RG-LRU / rotLRU / gated RG-LRU / rotLRU from "
-             "theta at config 3, SSD config 4, SSD and GLA at B = 96; bf16 inputs",
+             "theta at config 3, SSD config 4, SSD and GLA at Dh 128 (B3 L512 H12) and at B = 96, the general "
+             "input contract (dense A_neg, fp32 inputs), Gated DeltaNet; bf16 inputs unless named",
              "", "Commands (from the repository root on one MI355X, `export TMPDIR=/tmp`, R = repository root):", ""]
     lines += ["    " + c for c in commands]
     lines += ["", "## Kernel durations (`rocprofv3 --kernel-trace --stats`)", "",
@@ -1002,16 +1113,42 @@ def profile_markdown(summary, trace_dir, out_md, commands):
             for r in sorted(csv.DictReader(fh), key=lambda r: -float(r["TotalDurationNs"])):
                 lines.append(f"| `{r['Name'][:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
                              f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} |")
-    sc = summary["scale"]
+    sc, cal, info = summary["scale"], summary.get("calibration", {}), summary.get("agent", {})
+    lines += ["", "## Counter calibration", "",
+              "Kernels whose bytes and flops are known, run under the same counter sets (`bench.py --calibrate "
+              "copy|sector|gemm`; per launch, mean of 5).  Bytes by the gfx950 FETCH_SIZE / WRITE_SIZE formulas "
+              "from the raw request counters, before scaling.", "",
+              "| calibration | kernel | true read MB | counted read MB | 128 B / 64 B / 32 B read requests | "
+              "true write MB | counted write MB | 64 B / 32 B write requests |", "|---|---|---|---|---|---|---|---|"]
+    for kind in ("copy", "sector"):
+        c = cal.get(kind)
+        if not c:
+            continue
+        rd, r32, bub = c["TCC_EA0_RDREQ_sum"], c["TCC_EA0_RDREQ_32B_sum"], c["TCC_BUBBLE_sum"]
+        wr, w64 = c["TCC_EA0_WRREQ_sum"], c["TCC_EA0_WRREQ_64B_sum"]
+        lines.append(f"| {kind} | `{c['kernel'][:50]}` | {c['true_read_bytes'] / 1e6:.2f} | {c['fetch_bytes'] / 1e6:.2f} | "
+                     f"{bub:.4g} / {rd - bub - r32:.4g} / {r32:.4g} | {c['true_write_bytes'] / 1e6:.2f} | "
+                     f"{c['write_bytes'] / 1e6:.2f} | {w64:.4g} / {wr - w64:.4g} |")
+    g = cal.get("gemm")
+    if g:
+        lines += ["", f"bf16 GEMM {CAL_GEMM}^3 (`{g['kernel'][:60]}`): true {g['true_flops'] / 1e9:.1f} GFLOP, "
+                      f"counted (SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512) {g['counted_flops'] / 1e9:.1f} GFLOP; "
+                      f"GRBM_GUI_ACTIVE / XCDs = {g['gui_us']:.1f} µs at {info.get('clk_mhz', 2400)} MHz; "
+                      f"MFMA busy (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCDs x SIMDs)) "
+                      f"{100 * g['mfma_util']:.1f} % against flops / that time / 2.5 PFLOP/s = "
+                      f"{100 * g['flops_frac']:.1f} %."]
     lines += ["", "## HBM traffic and MFMA per dispatch (`--pmc` runs)", "",
-              f"Scale factors from a plain 256 MiB device copy (`bench.py --calibrate-copy 256`): FETCH_SIZE "
-              f"x{sc['FETCH_SIZE']:.3f}, WRITE_SIZE x{sc['WRITE_SIZE']:.3f}.  Algorithmic bytes are the pass's "
+              f"Traffic = the counted bytes times the copy's factors (read x{sc['fetch']:.3f}, write "
+              f"x{sc['write']:.3f}).  Algorithmic bytes are the pass's "
               "(inputs, outputs and checkpoints at their API dtypes), all moved by its main kernel; the other "
               "kernels of a pass move workspace data only.  MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / "
-              "(GRBM_GUI_ACTIVE x SIMDs); MFMA GFLOP = SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 per dispatch; "
+              f"(GRBM_GUI_ACTIVE / {info.get('xcc', 8)} XCDs x {info.get('simd', 1024)} SIMDs); MFMA GFLOP = "
+              "SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 per dispatch; MOPS / MFMA inst = that count over SQ_INSTS_MFMA "
+              "(64 for 32x32x16, 32 for 16x16x32, 16 for 16x16x16 bf16: the K = 16 shapes issue at half the "
+              "peak rate, so their busy share exceeds their share of the 2.5 PFLOP/s peak); "
               "VALU / MFMA = SQ_INSTS_VALU, SQ_INSTS_MFMA (instructions per dispatch).", "",
               "| workload | pass | kernel | fetch MB | write MB | pass algorithmic MB | MFMA busy | MFMA GFLOP | "
-              "VALU insts | MFMA insts |", "|---|---|---|---|---|---|---|---|---|---|"]
+              "MOPS / MFMA inst | VALU insts | MFMA insts |", "|---|---|---|---|---|---|---|---|---|---|---|"]
 
     def fmt(v, f):
         return "—" if v is None else f.format(v)
@@ -1026,6 +1163,7 @@ def profile_markdown(summary, trace_dir, out_md, commands):
                              f"{fmt(k['write_bytes'] and k['write_bytes'] / 1e6, '{:.3f}')} | {alg:.3f} | "
                              f"{fmt(k.get('mfma_util') and 100 * k['mfma_util'], '{:.1f} %')} | "
                              f"{fmt(k.get('mfma_flops') and k['mfma_flops'] / 1e9, '{:.2f}')} | "
+                             f"{fmt(k.get('insts_mfma') and k['mfma_flops'] / 512 / k['insts_mfma'], '{:.1f}')} | "
                              f"{fmt(k.get('insts_valu'), '{:.3g}')} | {fmt(k.get('insts_mfma'), '{:.3g}')} |")
     pathlib.Path(out_md).write_text("\n".join(lines) + "\n")
     print(f"wrote {out_md}")
@@ -1057,17 +1195,40 @@ def traffic_of(name, dom):
 
 
 def mfma_of(name, dom):
-    """MFMA figures of the dominant kernel: busy fraction of the MFMA units
-    (counters) and bf16 MFMA TFLOP/s (counted flops / the live-measured
-    average launch duration) against MI355X's dense bf16 peak; None where the
+    """MFMA figures of the dominant kernel against MI355X's dense bf16 peak
+    (2.5 PFLOP/s = 1024 SIMDs x 1024 flops per cycle x 2.4 GHz):
+      util      busy share of the MFMA units, SQ_VALU_MFMA_BUSY_CYCLES / (the
+                live-measured average launch duration x 2.4 GHz x SIMDs);
+      frac      bf16 MFMA flops (SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512) / that
+                duration / the peak;
+      util_grbm busy cycles / (GRBM_GUI_ACTIVE / XCDs x SIMDs): cycles of the
+                actual clock (lower than 2.4 GHz under a heavy MFMA load), and
+                for launches of a few microseconds inflated by the counter
+                window.
+    The bf16 GEMM calibration checks these: its counted flops are its true
+    flops, and util = frac there.  util > frac where a kernel issues the K = 16
+    shapes (16x16x16, 32x32x8 bf16), which take as many busy cycles per
+    instruction as the K = 32 shapes for half the flops; mops_per_mfma_inst
+    shows the mix (32 for 16x16x32 bf16, 16 for 16x16x16).  None where the
     kernel issues no MFMA."""
     k = _pmc_kernel(name, dom)
     if k is None or not k.get("mfma_flops"):
         return None
     tflops = k["mfma_flops"] / (dom["us"] * 1e-6) / 1e12
-    return {"util": k.get("mfma_util"), "achieved": tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": tflops / MFMA_BF16_PEAK_TFLOPS, "flops_per_launch": k["mfma_flops"],
-            "valu_insts": k.get("insts_valu"), "mfma_insts": k.get("insts_mfma")}
+    try:
+        info = json.loads(PMC_FILE.read_text()).get("agent", {})
+    except (OSError, ValueError):
+        info = {}
+    simd, clk = info.get("simd", 1024), info.get("clk_mhz", 2400)
+    util = k["mfma_busy_cycles"] / (dom["us"] * 1e-6 * clk * 1e6 * simd) if k.get("mfma_busy_cycles") else None
+    mops_inst = k["mfma_flops"] / 512 / k["insts_mfma"] if k.get("insts_mfma") else None
+    return {"util": util, "achieved": tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": tflops / MFMA_BF16_PEAK_TFLOPS, "util_grbm": k.get("mfma_util"),
+            "flops_per_launch": k["mfma_flops"], "mops_per_mfma_inst": mops_inst,
+            "valu_insts": k.get("insts_valu"), "mfma_insts": k.get("insts_mfma"),
+            "formula": "util = SQ_VALU_MFMA_BUSY_CYCLES / (live launch duration x 2.4 GHz x 1024 SIMDs); "
+                       "frac = SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 / live duration / 2.5 PFLOP/s; util_grbm = busy "
+                       "cycles / (GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs)"}
 
 
 def main():
@@ -1076,14 +1237,14 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="ssd", choices=sorted(WORKLOADS))
-    ap.add_argument("--also", default="gla,rglru,rotlru,ssd_c4",
+    ap.add_argument("--also", default="gla,rglru,rotlru,ssd_c4,ssd_dh128,gla_dh128",
                     help="comma-separated extra workloads reported beside (each with its roofline and CPU leg)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the single-token decode step lines")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU work per CPU baseline (the headline workload; the extra workloads get half)")
-    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
-                    help="only run a plain device-to-device copy of MB megabytes (PMC byte-counter scale)")
+    ap.add_argument("--calibrate", default=None, choices=sorted(CALIBRATIONS),
+                    help="only run a calibration kernel of known bytes / flops (under rocprofv3 --pmc)")
     ap.add_argument("--pmc-run", default=None, metavar="WORKLOAD",
                     help="only run one warm forward + backward of WORKLOAD (under rocprofv3 --pmc)")
     ap.add_argument("--pmc-out", default="gpurun_out/pmc", help="directory for --pmc-run / --pmc-summary")
@@ -1114,14 +1275,8 @@ def main():
     if args.pmc_run:
         pmc_run(args.pmc_run, args.pmc_out)
         return
-    if args.calibrate_copy:
-        n = args.calibrate_copy * (1 << 20) // 4
-        src = torch.randn(n, device=device)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"calibrate_copy": {"bytes_read": 4 * n, "bytes_written": 4 * n, "launches": 5}}))
+    if args.calibrate:
+        calibrate(args.calibrate, device)
         return
 
     cpu_s = 0.0 if args.no_cpu else args.cpu_seconds
@@ -1144,7 +1299,9 @@ def main():
     decode = {} if args.no_decode else {nm: measure_decode(nm, dtype, device) for nm in DECODE}
 
     r = main_res
-    cfg = dict(workload=r["workload"], **r["cfg"], input_dtype="bf16", state_dtype="f32")
+    cfg = dict(workload=r["workload"], **r["cfg"], input_dtype="bf16", state_dtype="f32",
+               arithmetic="bf16 inputs (exact MFMA operands); fp32 state, decays, adjoints and dy split into "
+                          "bf16 hi + lo MFMA operands (2^-17 relative per product term); fp32 accumulation")
     line = {
         "metric": METRIC,
         "value": r["tokens_per_s"],
@@ -1156,7 +1313,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16-in/f32-accum",
         "data": "synthetic",
         "config": cfg,
         "roofline": {
