@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define RR_ABI_VERSION 11
+#define RR_ABI_VERSION 12
 
 enum rr_dtype { RR_F32 = 0, RR_BF16 = 1, RR_F16 = 2 };
 
@@ -99,6 +99,14 @@ int64_t rr_tile_schedule(int scan, int pass, int64_t B, int64_t L, int64_t D, in
  * these arguments (the kernels chosen depend on A_stride_n and dtype). */
 size_t rr_ssd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N,
                               int64_t seg, int64_t A_stride_n, int dtype, int pass);
+
+/* One past the largest workspace byte that the chunked (MFMA) SSD kernels of
+ * this call write or read: the library walks the grids of the pass's kernels
+ * with their own workgroup decode and slot arithmetic.  For tests that the
+ * kernels stay inside rr_ssd_workspace_bytes.  No reference counterpart.
+ * Returns -1 for invalid arguments or a call that runs on the VALU engine. */
+int64_t rr_ssd_workspace_extent(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N, int64_t seg,
+                                int64_t A_stride_n, int dtype, int pass);
 
 /* Replaces _ssd_forward_kernel (reference mlx_recurrence/ssd.py:54-135). */
 int rr_ssd_fwd(const void* u, const void* delta, const void* Bm, const void* Cm,

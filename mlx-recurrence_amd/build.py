@@ -2,7 +2,7 @@
 then the C++ autograd bindings (csrc_torch/autograd.cpp -> the Python module
 mlx_recurrence_amd._autograd, linked against that library).
 
-Usage:  python mlx-recurrence_amd/build.py [--jobs N] [--verbose]
+Usage:  python mlx-recurrence_amd/build.py [--jobs N] [--verbose] [--host-sanitize]
 
 Objects go to mlx-recurrence_amd/_build/; the shared libraries are written next
 to the Python package (mlx_recurrence_amd/), where the loaders look for them.
@@ -37,6 +37,56 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-ffp-contract=fast",
 ]
+
+
+# Host-sanitizer build (--host-sanitize): the host side of the C ABI
+# (argument validation, workspace sizing, the tile schedule and workspace
+# bound walks) under AddressSanitizer + UndefinedBehaviorSanitizer, for the
+# CPU tests.  Only host code is instrumented (each -fsanitize= behind
+# -Xarch_host); the device code is built unoptimised, since this library never
+# launches a kernel.  Loaded by setting MLX_RECURRENCE_AMD_LIB to its path with
+# the ASan runtime preloaded (tests/test_host_sanitize.py).
+SANITIZE_DIR = BUILD / "sanitize"
+SANITIZERS = ("address", "undefined")
+SANITIZE_LINK = [arg for name in SANITIZERS for arg in ("-Xarch_host", "-fsanitize=" + name)]
+SANITIZE_FLAGS = [
+    f"--offload-arch={ARCH}", "-O1", "-g", "-std=c++17", "-fPIC", "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    *SANITIZE_LINK, "-Xarch_host", "-fno-omit-frame-pointer", "-Xarch_device", "-O0",
+]
+
+
+def asan_runtime() -> pathlib.Path:
+    """The clang ASan runtime that a host-sanitizer build needs preloaded."""
+    root = pathlib.Path(hipcc()).resolve().parents[1] / "llvm" / "lib" / "clang"
+    for cand in sorted(root.glob("*/lib/linux/libclang_rt.asan-x86_64.so"), reverse=True):
+        return cand
+    raise RuntimeError(f"libclang_rt.asan-x86_64.so not found under {root}")
+
+
+def build_sanitized(jobs: int | None = None, verbose: bool = False) -> pathlib.Path:
+    SANITIZE_DIR.mkdir(parents=True, exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    jobs = jobs or min(len(sources), os.cpu_count() or 1, 8)
+
+    def one(src: pathlib.Path) -> pathlib.Path:
+        obj = SANITIZE_DIR / (src.stem + ".o")
+        cmd = [hipcc(), *SANITIZE_FLAGS, "-c", str(src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"compiling {src.name} (host sanitizers) failed:\n{res.stdout}\n{res.stderr}")
+        return obj
+
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(one, sources))
+    out = SANITIZE_DIR / LIB_NAME
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *SANITIZE_LINK, *map(str, objs), "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"linking the host-sanitizer {LIB_NAME} failed:\n{res.stdout}\n{res.stderr}")
+    return out
 
 
 def hipcc() -> str:
@@ -115,8 +165,13 @@ def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--host-sanitize", action="store_true",
+                    help="build only the host-sanitizer library (_build/sanitize/) for the CPU tests")
     args = ap.parse_args()
-    print(build(args.jobs, args.verbose))
+    if args.host_sanitize:
+        print(build_sanitized(args.jobs, args.verbose))
+    else:
+        print(build(args.jobs, args.verbose))
 
 
 if __name__ == "__main__":

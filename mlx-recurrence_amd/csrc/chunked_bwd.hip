@@ -205,7 +205,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
     const float has_h = c > 0 || p.h0 != nullptr ? 1.f : 0.f;
     const auto hsrc = rr::as_global(c > 0 ? p.ckpt + (bh * p.nC + c - 1) * DH * NS
                                           : (p.h0 != nullptr ? p.h0 + bh * DH * NS : p.ckpt));
-    const auto lsrc = rr::as_global(MODE == kPipe ? p.agg + (bh * p.nC + c) * DH * NS : p.ckpt);
+    const auto lsrc = rr::as_global(MODE == kPipe ? p.agg + rr::chunked::adj_slot(bh, p.nC, 1, c) * DH * NS : p.ckpt);
 #pragma unroll
     for (int cc = 0; cc < CPW; ++cc) {
       const int nb = min(w + 4 * cc, NBN - 1);
@@ -304,7 +304,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
   for (int cc = 0; cc < CPW; ++cc) dA_acc[cc] = 0.f;
   if constexpr (MODE == kPair) {
     // lam leaving the run (slot cbeg / R of the scan's output), this wave's column blocks
-    const auto lsrc = rr::as_global(p.agg + (bh * (p.nC / p.R) + cbeg / p.R) * DH * NS);
+    const auto lsrc = rr::as_global(p.agg + rr::chunked::adj_slot(bh, p.nC, p.R, cbeg / p.R) * DH * NS);
 #pragma unroll
     for (int cc = 0; cc < CPW; ++cc) {
       const int nb = min(w + 4 * cc, NBN - 1);
@@ -533,7 +533,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
 #pragma unroll
       for (int k = 0; k < DPW; ++k) {
         const int d = 16 * min(mydb + 4 * k, NBD - 1) + l15;
-        const float* lsrc = p.agg + ((bh * (p.nC / p.R) + cbeg / p.R) * DH + d) * NS + 4 * l4;
+        const float* lsrc = p.agg + (rr::chunked::adj_slot(bh, p.nC, p.R, cbeg / p.R) * DH + d) * NS + 4 * l4;
 #pragma unroll
         for (int nb = 0; nb < NBN; ++nb) {
           const float4 l0 = *reinterpret_cast<const float4*>(lsrc + 16 * nb);
@@ -545,7 +545,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
 #pragma unroll
       for (int k = 0; k < DPW; ++k) {
         const int d = 16 * min(mydb + 4 * k, NBD - 1) + l15;
-        const float* lsrc = p.agg + ((bh * p.nC + c) * DH + d) * NS + 8 * l4;
+        const float* lsrc = p.agg + (rr::chunked::adj_slot(bh, p.nC, 1, c) * DH + d) * NS + 8 * l4;
 #pragma unroll
         for (int kk = 0; kk < NS / 32; ++kk) {
           const float4 l0 = *reinterpret_cast<const float4*>(lsrc + 32 * kk);
@@ -879,7 +879,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
 #pragma unroll
     for (int cc = 0; cc < CPW; ++cc) {
       const int nb = w + 4 * cc;
-      if (nb < NBN && l4 == 0) p.ws[(bh * nR + run) * NS + 16 * nb + l15] = dA_acc[cc];
+      if (nb < NBN && l4 == 0) p.ws[rr::chunked::dA_slot(bh, nR, run) * NS + 16 * nb + l15] = dA_acc[cc];
     }
   }
   if (carry && p.dh0 != nullptr) {   // kWhole (kDirect stores dh0 in the direct sum)

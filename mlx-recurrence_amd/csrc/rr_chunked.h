@@ -215,26 +215,48 @@ __host__ __device__ inline int head_on_xcd(int j, int x, int groups, int G) {
   const int q = groups / G * G;
   return j < q ? G * (kXcds * (j / G) + x) + j % G : kXcds * j + x;
 }
+// Chunk (or, for kPair, run) of workgroup `id` of a per-chunk grid: the
+// decode of chunk_id / run_id below, callable on the host so that the
+// workspace bound (rr_ssd_workspace_extent) walks the grid the kernels run.
+__host__ __device__ inline ChunkId decode_chunk(int id, int B, int H, int nC, int NS, bool by_cost, bool late_first) {
+  const int x = id % kXcds, slot = id / kXcds;
+  const int groups = (B * H + kXcds - 1) / kXcds;   // head groups of 8
+  const int cs = by_cost ? slot / groups : slot % nC;
+  const int bh = head_on_xcd(by_cost ? slot % groups : slot / nC, x, groups, line_heads(NS));
+  return ChunkId{late_first ? nC - 1 - cs : cs, bh % H, bh / H, bh < B * H};
+}
+__host__ __device__ inline ChunkId decode_run(int id, int B, int H, int nC, int R, int NS) {
+  const int x = id % kXcds, slot = id / kXcds, nP = nC / R;
+  const int groups = (B * H + kXcds - 1) / kXcds;
+  const int bh = head_on_xcd(slot / nP, x, groups, line_heads(NS));
+  return ChunkId{slot % nP, bh % H, bh / H, bh < B * H};
+}
 __device__ __forceinline__ ChunkId chunk_id(const ChunkArgs& p, bool by_cost, bool late_first) {
-  const int id = blockIdx.x, x = id % kXcds, slot = id / kXcds;
-  const int groups = (p.B * p.H + kXcds - 1) / kXcds;   // head groups of 8
-  const int cs = by_cost ? slot / groups : slot % p.nC;
-  const int bh = head_on_xcd(by_cost ? slot % groups : slot / p.nC, x, groups, line_heads(p.NS));
-  return ChunkId{late_first ? p.nC - 1 - cs : cs, bh % p.H, bh / p.H, bh < p.B * p.H};
+  return decode_chunk(blockIdx.x, p.B, p.H, p.nC, p.NS, by_cost, late_first);
 }
-inline dim3 chunk_grid(const ChunkArgs& p) {
-  return dim3((unsigned)(p.nC * ((p.B * p.H + kXcds - 1) / kXcds) * kXcds));
+__host__ __device__ inline int64_t chunk_grid_size(int B, int H, int nC) {
+  return (int64_t)nC * ((B * H + kXcds - 1) / kXcds) * kXcds;
 }
+inline dim3 chunk_grid(const ChunkArgs& p) { return dim3((unsigned)chunk_grid_size(p.B, p.H, p.nC)); }
 // kPair: the same decode over the nC / R runs of a head (c = run index)
-__device__ __forceinline__ ChunkId run_id(const ChunkArgs& p) {
-  const int id = blockIdx.x, x = id % kXcds, slot = id / kXcds, nP = p.nC / p.R;
-  const int groups = (p.B * p.H + kXcds - 1) / kXcds;
-  const int bh = head_on_xcd(slot / nP, x, groups, line_heads(p.NS));
-  return ChunkId{slot % nP, bh % p.H, bh / p.H, bh < p.B * p.H};
+__device__ __forceinline__ ChunkId run_id(const ChunkArgs& p) { return decode_run(blockIdx.x, p.B, p.H, p.nC, p.R, p.NS); }
+__host__ __device__ inline int64_t run_grid_size(int B, int H, int nC, int R) {
+  return (int64_t)(nC / R) * ((B * H + kXcds - 1) / kXcds) * kXcds;
 }
-inline dim3 run_grid(const ChunkArgs& p) {
-  return dim3((unsigned)(p.nC / p.R * ((p.B * p.H + kXcds - 1) / kXcds) * kXcds));
+inline dim3 run_grid(const ChunkArgs& p) { return dim3((unsigned)run_grid_size(p.B, p.H, p.nC, p.R)); }
+
+// Backward workspace slot (in units of one Dh x N state) of the adjoint
+// leaving run `run` (R chunks) of head bh = b * H + h: each head holds
+// ceil(nC / R) slots.  The adjoint scan and the aggregate / state-pass
+// kernels write these slots, the pipelined and pair chunk kernels read them,
+// and rr_ssd_workspace_extent bounds them on the host.
+__host__ __device__ inline int64_t adj_slot(int64_t bh, int nC, int R, int run) {
+  return bh * ((nC + R - 1) / R) + run;
 }
+// Backward dA partial slot (N floats) of run `run` of head bh, nR runs per
+// head: each backward workgroup writes one (the whole-head mode one run per
+// head, the pair mode nC / R, the per-chunk modes nC).
+__host__ __device__ inline int64_t dA_slot(int64_t bh, int nR, int run) { return bh * nR + run; }
 
 // Per-head decay rate (SSD); GLA has none.
 template <bool GLA>
@@ -340,7 +362,8 @@ __global__ __launch_bounds__(kAggThreads) void agg_kernel(ChunkArgs p, int kind)
   const float4 c0 = *reinterpret_cast<const float4*>(&sm.wsh[8 * gl]);
   const float4 c1 = *reinterpret_cast<const float4*>(&sm.wsh[8 * gl + 4]);
   const float cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-  float* dst = (kind == 0 ? p.ckpt : p.agg) + (((int64_t)b * p.H + h) * p.nC + c) * DH * NS;
+  float* dst = kind == 0 ? p.ckpt + (((int64_t)b * p.H + h) * p.nC + c) * DH * NS
+                          : p.agg + adj_slot((int64_t)b * p.H + h, p.nC, 1, c) * DH * NS;
 #pragma unroll
   for (int q = 0; q < NDB; ++q) {
     const int db = db0 + q;
@@ -411,7 +434,7 @@ __global__ __launch_bounds__(256) void pass_kernel(ChunkArgs p, int kind) {
       }
     }
   } else {
-    float* buf = p.agg + bh * nC * (DH * NS) + e;
+    float* buf = p.agg + adj_slot(bh, nC, 1, 0) * (DH * NS) + e;
     float x = p.dfinal != nullptr ? p.dfinal[bh * DH * NS + es] : 0.f;
     for (int k0 = nC - 1; k0 >= 0; k0 -= kPass) {
       float gv[kPass], tv[kPass];
@@ -521,7 +544,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ChunkArgs p) {
 
   // this head's slots: nC checkpoints (forward), or one adjoint per run of
   // R chunks (backward; the workspace holds ceil(nC / R) per head)
-  float* out = BWD ? p.agg + bh * ((nC + p.R - 1) / p.R) * DH * NS : p.ckpt + bh * nC * DH * NS;
+  float* out = BWD ? p.agg + adj_slot(bh, nC, p.R, 0) * DH * NS : p.ckpt + bh * nC * DH * NS;
   auto store_state = [&](float* dst) {
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {

@@ -60,6 +60,10 @@ bool ssd2_bwd_supported(int64_t Dh, int64_t N);
 // in the pipelined mode, plus dA partials (pass 1).
 size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int mode, int64_t Dh, int64_t N, int pass);
 void ssd2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass);
+// One past the largest workspace byte that the chunked SSD kernels of a pass
+// write or read, walked over their grids with the kernels' own decode and slot
+// arithmetic (a host-side bound for tests).
+int64_t ssd2_ws_extent(int64_t B, int64_t H, int64_t nC, int mode, int64_t Dh, int64_t N, int pass);
 int ssd2_bwd(const ChunkArgs& p, int64_t B, hipStream_t s);
 
 // ------------------------------------------------------------------ GLA

@@ -16,6 +16,8 @@
 // the state (adjoint) across chunks (the pipelined mode of rr_chunked.h).
 #include "rr_chunked.h"
 
+#include <algorithm>
+
 namespace {
 
 using rr::bf_split;
@@ -196,7 +198,7 @@ __global__ __launch_bounds__(256, (kBwdWgs<DH, NS, MODE>)) void ssd2_bwd_kernel(
   for (int jj = 0; jj < K::NBW; ++jj) lam[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // the adjoint entering chunk c - 1 is needed for the whole head
   const bool carry = MODE == kWhole;
-  const float* lsrc = MODE == kPipe ? p.agg + (((int64_t)b * p.H + h) * p.nC + cbeg) * DH * NS
+  const float* lsrc = MODE == kPipe ? p.agg + rr::chunked::adj_slot((int64_t)b * p.H + h, p.nC, 1, cbeg) * DH * NS
                                     : (p.dfinal != nullptr ? p.dfinal + sbase : nullptr);
   if (!SUM && lsrc != nullptr) {
 #pragma unroll
@@ -753,7 +755,7 @@ __global__ __launch_bounds__(256, (kBwdWgs<DH, NS, MODE>)) void ssd2_bwd_kernel(
   // per-run dA partial and the initial-state gradient
   const int nR = MODE == kWhole ? 1 : p.nC;   // runs per head
   const int run = MODE == kWhole ? 0 : cbeg;
-  if (w == 1 && lane < NS) p.ws[(((int64_t)b * p.H + h) * nR + run) * NS + lane] = dA_acc;
+  if (w == 1 && lane < NS) p.ws[rr::chunked::dA_slot((int64_t)b * p.H + h, nR, run) * NS + lane] = dA_acc;
   if (carry && p.dh0 != nullptr) {
 #pragma unroll
     for (int jj = 0; jj < K::NBW; ++jj) {
@@ -901,6 +903,61 @@ void ssd2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass) {
     a.ws = f; f += align64(B * a.H * nR * a.NS);
     if (pipe) a.agg = f;
   }
+}
+
+int64_t ssd2_ws_extent(int64_t B, int64_t H, int64_t nC, int mode, int64_t Dh, int64_t N, int pass) {
+  using namespace chunked;
+  ChunkArgs a{};
+  a.B = (int)B; a.H = (int)H; a.nC = (int)nC; a.DH = (int)Dh; a.NS = (int)N; a.mode = mode;
+  a.R = chunked_run(mode, nC);
+  // carve from a stand-in base address (never dereferenced) and measure offsets
+  char* const base = reinterpret_cast<char*>(uintptr_t(1) << 44);
+  ssd2_carve_ws(a, base, B, pass);
+  int64_t ext = 0;
+  auto touch = [&](const float* region, int64_t first, int64_t count) {
+    if (region == nullptr) return;
+    ext = std::max<int64_t>(ext, reinterpret_cast<const char*>(region + first + count) - base);
+  };
+  const int64_t state = Dh * N, BH = B * H;
+  const bool pipe = mode == kPipe || mode == kPair;
+  if (pipe && BH < kScanMinHeads) {
+    // aggregate kernel and state / adjoint pass: per-chunk decays and states
+    for (int64_t id = 0; id < chunk_grid_size(a.B, a.H, a.nC); ++id) {
+      const ChunkId c = decode_chunk((int)id, a.B, a.H, a.nC, a.NS, false, false);
+      if (!c.valid) continue;
+      const int64_t bh = (int64_t)c.b * H + c.h;
+      touch(a.tot, bh * nC + c.c, 1);
+      if (pass == 1) touch(a.agg, adj_slot(bh, a.nC, 1, c.c) * state, state);
+    }
+  } else if (pipe && pass == 1) {
+    // adjoint scan: the adjoint leaving every R-th chunk of each head
+    for (int64_t bh = 0; bh < BH; ++bh)
+      for (int c = 0; c < a.nC; ++c)
+        if (a.R == 1 || c % a.R == a.R - 1) touch(a.agg, adj_slot(bh, a.nC, a.R, c / a.R) * state, state);
+  }
+  if (pass != 1) return ext;
+  // the chunk kernels: the adjoint each reads, the dA partial each writes
+  const int nR = mode == kWhole ? 1 : mode == kPair ? a.nC / a.R : a.nC;
+  if (mode == kWhole) {
+    for (int64_t bh = 0; bh < BH; ++bh) touch(a.ws, dA_slot(bh, nR, 0) * N, N);
+  } else if (mode == kPair) {
+    for (int64_t id = 0; id < run_grid_size(a.B, a.H, a.nC, a.R); ++id) {
+      const ChunkId r = decode_run((int)id, a.B, a.H, a.nC, a.R, a.NS);
+      if (!r.valid) continue;
+      const int64_t bh = (int64_t)r.b * H + r.h;
+      touch(a.agg, adj_slot(bh, a.nC, a.R, r.c) * state, state);
+      touch(a.ws, dA_slot(bh, nR, r.c) * N, N);
+    }
+  } else {
+    for (int64_t id = 0; id < chunk_grid_size(a.B, a.H, a.nC); ++id) {
+      const ChunkId c = decode_chunk((int)id, a.B, a.H, a.nC, a.NS, mode == kSum, false);
+      if (!c.valid) continue;
+      const int64_t bh = (int64_t)c.b * H + c.h;
+      if (mode == kPipe) touch(a.agg, adj_slot(bh, a.nC, 1, c.c) * state, state);
+      touch(a.ws, dA_slot(bh, nR, c.c) * N, N);
+    }
+  }
+  return ext;
 }
 
 int ssd2_bwd(const ChunkArgs& p, int64_t B, hipStream_t s) {

@@ -672,6 +672,17 @@ extern "C" size_t rr_ssd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_
   return pass == 0 ? q.fwd_bytes : q.bwd_bytes;
 }
 
+extern "C" int64_t rr_ssd_workspace_extent(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N, int64_t seg,
+                                           int64_t A_stride_n, int dtype, int pass) {
+  if (B <= 0 || L <= 0 || H <= 0 || Dh <= 0 || N <= 0 || rr::chunk_len(L, seg) == 0 || (pass != 0 && pass != 1)) {
+    rr::fail(RR_EINVAL, "rr_ssd_workspace_extent: invalid arguments");
+    return -1;
+  }
+  if (!rr::ssd2_supported(dtype, L, seg, Dh, N, A_stride_n) || (pass == 1 && !rr::ssd2_bwd_supported(Dh, N))) return -1;
+  const int64_t nC = L / 32;
+  return rr::ssd2_ws_extent(B, H, nC, rr::chunked_mode(B, H, nC, Dh, N, pass), Dh, N, pass);
+}
+
 extern "C" int rr_ssd_fwd(const void* u, const void* delta, const void* Bm, const void* Cm,
                           const float* A_neg, int64_t A_stride_n, int dtype, int64_t B, int64_t L, int64_t H,
                           int64_t Dh, int64_t N, int64_t seg, const float* h0, float* y,

@@ -17,7 +17,10 @@ import pathlib
 import torch
 
 LIB_NAME = "librecurrence_gfx950.so"
-LIB_PATH = pathlib.Path(__file__).resolve().parent / LIB_NAME
+# MLX_RECURRENCE_AMD_LIB names another build of the library to load instead
+# (the host-sanitizer build that the CPU tests of the C ABI run against).
+LIB_PATH = pathlib.Path(os.environ.get("MLX_RECURRENCE_AMD_LIB") or
+                        pathlib.Path(__file__).resolve().parent / LIB_NAME)
 
 RR_OK = 0
 RR_EINVAL = 1
@@ -40,6 +43,7 @@ _SIGS = {
     "rr_async_status": (_c_int, []),
     "rr_tile_schedule": (_c_i64, [_c_int, _c_int] + [_c_i64] * 4 + [_c_int] + [_c_ptr] * 3 + [_c_i64]),
     "rr_ssd_workspace_bytes": (_c_size, [_c_i64] * 7 + [_c_int, _c_int]),
+    "rr_ssd_workspace_extent": (_c_i64, [_c_i64] * 7 + [_c_int, _c_int]),
     "rr_ssd_fwd": (_c_int, [_c_ptr] * 5 + [_c_i64, _c_int] + [_c_i64] * 6 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
     "rr_ssd_bwd": (_c_int, [_c_ptr] * 7 + [_c_i64, _c_int] + [_c_i64] * 6 + [_c_ptr] * 9 + [_c_size, _c_ptr]),
     "rr_ssd_bwd_noalloc": (_c_int, [_c_ptr] * 7 + [_c_i64, _c_int] + [_c_i64] * 6 + [_c_ptr] * 9),
@@ -143,6 +147,14 @@ def tile_schedule(scan: int, pass_: int, B: int, L: int, D: int, seg: int, dtype
     lib.rr_tile_schedule(scan, pass_, B, L, D, seg, dtype, k.ctypes.data_as(_c_ptr), g.ctypes.data_as(_c_ptr),
                          ctypes.byref(worst), n)
     return k, g, int(worst.value)
+
+
+def ssd_workspace_extent(B: int, L: int, H: int, Dh: int, N: int, seg: int, a_stride_n: int, dtype: int,
+                         pass_: int) -> int:
+    """One past the largest workspace byte the chunked SSD kernels of a pass
+    touch (walked over their grids by the library), or -1 where the call runs
+    on the VALU engine."""
+    return int(load().rr_ssd_workspace_extent(B, L, H, Dh, N, seg, a_stride_n, dtype, pass_))
 
 
 def _check(rc: int, what: str) -> None:

@@ -33,7 +33,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.rr_abi_version() == 11
+    assert lib.rr_abi_version() == 12
 
 
 @pytest.mark.parametrize("L,seg,T", [(512, 32, 32), (96, 16, 16), (128, 64, 32), (96, 48, 16),
