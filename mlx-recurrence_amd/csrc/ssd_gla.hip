@@ -45,8 +45,7 @@ namespace {
 
 constexpr int kMaxT = 32;
 constexpr int kTile = 16;
-constexpr int kFwdWaves = 8;
-constexpr int kBwdWaves = 8;
+constexpr int kChunkWaves = 4;    // chunks per workgroup of the chunk-parallel kernels
 constexpr int kFinRows = 32;  // (b, t) rows per finalize workgroup
 
 // Sum over the 4 rows (the 4 n-groups of one d: lanes l, l ^ 16, l ^ 32,
@@ -98,6 +97,9 @@ struct Args {
   float* gu_part;       // bwd: per-n-tile partials of gu when NN > 1
   float* g3;            // bwd: [3][ND][B*L*H][NS] partial Gin, Gout, Hp
   float* dh0;           // bwd: gradient of the initial state (nullable)
+  float* lamws;         // bwd: adjoint flowing into each chunk [B,H,nC,DL,NS] (workspace)
+  float* mapE;          // chunk maps x -> P x + E (workspace): E [B,H,nC,DL,NS]
+  float* mapP;          //   P [B,H,nC,NS]
   int L, H, DL, NS, T, nC, ND, NN;
   int64_t rows;         // B*L*H
 };
@@ -151,105 +153,226 @@ __device__ __forceinline__ void unpack(float4 v, float (&a)[4]) {
   a[3] = v.w;
 }
 
-template <typename InT, bool GLA, int NW>
-__global__ __launch_bounds__(64 * NW) void r1_fwd_kernel(Args<InT> p) {
+// FULL: the chunk is kMaxT steps (the checkpoint interval of the default
+// seg = 32), so the per-step loops carry no run-time bound and the compiler
+// can issue each step's LDS reads ahead of the steps before it.
+
+// Each pass runs in three kernels:
+//   r1_fold_kernel (every chunk at once, NW chunks per workgroup): each wave
+//     folds its chunk into the affine map x -> P x + E of the state (forward,
+//     from the coefficients and u) or of the adjoint (backward, from the
+//     coefficients and dy, walking the steps backwards), P per state column,
+//     E per state element, into the workspace;
+//   r1_compose_kernel (one wave per state tile of a (head, batch row)): walks
+//     the maps in order, writing the state after each chunk to the checkpoints
+//     (forward) or the adjoint flowing into each chunk from the later ones to
+//     `lamws` (backward; the last one is dh0): the only serial part of the
+//     scan, and a cheap one (a multiply-add per state element per chunk);
+//   r1_out_kernel / r1_bwd_kernel (every chunk at once): each wave replays its
+//     chunk from its entering state (checkpoint c - 1, h0 or zero) and writes
+//     y, or recomputes its states and walks the adjoint back from lamws,
+//     writing the per-step partial sums.
+template <typename InT, bool GLA, int NW, bool BWD>
+__global__ __launch_bounds__(64 * NW) void r1_fold_kernel(Args<InT> p) {
+  constexpr bool FULL = false;   // (a run-time bound keeps the read-ahead, and the registers, in check)
   __shared__ float4 sCoef[NW][3][kMaxT][4];
-  __shared__ float4 sE[NW][64];
-  __shared__ float4 sP[NW][4];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ng = lane >> 4, dl = lane & 15;
-  const int dt = blockIdx.x / p.NN, nt = blockIdx.x % p.NN;
+  const int tiles = p.ND * p.NN, tile = blockIdx.x % tiles, grp = blockIdx.x / tiles;
+  const int dt = tile / p.NN, nt = tile % p.NN;
   const int h = blockIdx.y, b = blockIdx.z;
   const int d = dt * kTile + dl;
   const bool dok = d < p.DL;
   const int nb = nt * kTile + ng * 4;
   const int64_t bh = (int64_t)b * p.H + h;
-
-  float carry[4] = {0.f, 0.f, 0.f, 0.f};
-  if (p.h0 != nullptr && dok) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (nb + k < p.NS) carry[k] = p.h0[bh * p.DL * p.NS + state_idx<GLA>(d, nb + k, p.DL, p.NS)];
-  }
-  float* yout = p.y + (p.NN > 1 ? (int64_t)nt * p.rows * p.DL : 0);
-
-  for (int c0 = 0; c0 < p.nC; c0 += NW) {
-    const int c = c0 + w;
-    const bool act = c < p.nC;
-    stage_chunk<InT, GLA>(p, sCoef[w], b, h, c, act, nt, lane);
-    float uv[kMaxT];
-    {
-      const int cc = act ? c : 0, dc = min(d, p.DL - 1);
-#pragma unroll
-      for (int t = 0; t < kMaxT; ++t)
-        uv[t] = rr::ld(p.lane_in, (((int64_t)b * p.L + (int64_t)cc * p.T + min(t, p.T - 1)) * p.H + h) * p.DL + dc);
-#pragma unroll
-      for (int t = 0; t < kMaxT; ++t) uv[t] = t < p.T && act && dok ? uv[t] : 0.f;
-    }
-    __syncthreads();
-    float e[4] = {0.f, 0.f, 0.f, 0.f}, P[4] = {1.f, 1.f, 1.f, 1.f};
+  const int c = grp * NW + w;
+  const bool act = c < p.nC;
+  stage_chunk<InT, GLA>(p, sCoef[w], b, h, c, act, nt, lane);
+  float xv[kMaxT];   // forward: u_t[d]; backward: dy_t[d]
+  {
+    const int cc = act ? c : 0, dc = min(d, p.DL - 1);
 #pragma unroll
     for (int t = 0; t < kMaxT; ++t) {
-      if (t < p.T) {
+      const int64_t i = (((int64_t)b * p.L + (int64_t)cc * p.T + min(t, p.T - 1)) * p.H + h) * p.DL + dc;
+      xv[t] = BWD ? p.dy[i] : rr::ld(p.lane_in, i);
+    }
+#pragma unroll
+    for (int t = 0; t < kMaxT; ++t) xv[t] = t < p.T && act && dok ? xv[t] : 0.f;
+  }
+  __syncthreads();
+  float e[4] = {0.f, 0.f, 0.f, 0.f}, P[4] = {1.f, 1.f, 1.f, 1.f};
+  if constexpr (BWD) {
+#pragma unroll
+    for (int t = kMaxT - 1; t >= 0; --t) {
+      if (FULL || t < p.T) {
+        float dec[4], outc[4];
+        unpack(sCoef[w][0][t][ng], dec);
+        unpack(sCoef[w][2][t][ng], outc);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          e[k] = (e[k] + xv[t] * outc[k]) * dec[k];
+          P[k] *= dec[k];
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < kMaxT; ++t) {
+      if (FULL || t < p.T) {
         float dec[4], inb[4];
         unpack(sCoef[w][0][t][ng], dec);
         unpack(sCoef[w][1][t][ng], inb);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          e[k] = dec[k] * e[k] + inb[k] * uv[t];
+          e[k] = dec[k] * e[k] + inb[k] * xv[t];
           P[k] *= dec[k];
         }
       }
     }
-    sE[w][lane] = make_float4(e[0], e[1], e[2], e[3]);
-    if (dl == 0) sP[w][ng] = make_float4(P[0], P[1], P[2], P[3]);
-    __syncthreads();
-    float hin[4], nxt[4];
+  }
+  if (act && dok) {
+    float* em = p.mapE + ((bh * p.nC + c) * p.DL + d) * p.NS;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) hin[k] = nxt[k] = carry[k];
+    for (int k = 0; k < 4; ++k)
+      if (nb + k < p.NS) em[nb + k] = e[k];
+  }
+  if (act && dl == 0) {
+    float* pm = p.mapP + (bh * p.nC + c) * p.NS;
 #pragma unroll
-    for (int j = 0; j < NW; ++j) {
-      float pj[4], ej[4];
-      unpack(sP[j][ng], pj);
-      unpack(sE[j][lane], ej);
+    for (int k = 0; k < 4; ++k)
+      if (nb + k < p.NS) pm[nb + k] = P[k];
+  }
+}
+
+// One wave per (tile, head, batch row): x_c = P_c x_{c-1} + E_c over the chunks
+// (forward from h0, in order; backward from dfinal, in reverse), maps loaded
+// kCompPF chunks ahead.
+constexpr int kCompPF = 8;
+template <bool GLA, bool BWD>
+__global__ __launch_bounds__(64) void r1_compose_kernel(const float* __restrict__ mapE, const float* __restrict__ mapP,
+                                                        const float* __restrict__ x0, float* __restrict__ out,
+                                                        float* __restrict__ xlast, int H, int DL, int NS, int nC,
+                                                        int NN) {
+  const int lane = threadIdx.x, ng = lane >> 4, dl = lane & 15;
+  const int dt = blockIdx.x / NN, nt = blockIdx.x % NN;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int d = dt * kTile + dl, dc = min(d, DL - 1);
+  const bool dok = d < DL;
+  const int nb = nt * kTile + ng * 4;
+  const int64_t bh = (int64_t)b * H + h;
+  int ncl[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) ncl[k] = min(nb + k, NS - 1);
+  float x[4] = {0.f, 0.f, 0.f, 0.f};
+  if (x0 != nullptr) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) x[k] = x0[bh * DL * NS + state_idx<GLA>(dc, ncl[k], DL, NS)];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) x[k] = dok && nb + k < NS ? x[k] : 0.f;
+  }
+  for (int i0 = 0; i0 < nC; i0 += kCompPF) {
+    float ev[kCompPF][4], pv[kCompPF][4];
+#pragma unroll
+    for (int q = 0; q < kCompPF; ++q) {
+      const int i = min(i0 + q, nC - 1), c = BWD ? nC - 1 - i : i;
+      const float* em = mapE + ((bh * nC + c) * DL + dc) * NS;
+      const float* pm = mapP + (bh * nC + c) * NS;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        if (j < w) hin[k] = pj[k] * hin[k] + ej[k];
-        nxt[k] = pj[k] * nxt[k] + ej[k];
+        ev[q][k] = em[ncl[k]];
+        pv[q][k] = pm[ncl[k]];
       }
     }
-    float hs[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) hs[k] = hin[k];
-    // this lane's y of step 0 of the chunk; step t is t * H * DL further
-    float* const ylane = yout + (((int64_t)b * p.L + (int64_t)(act ? c : 0) * p.T) * p.H + h) * p.DL + d;
-    const int64_t ystep = (int64_t)p.H * p.DL;
+    for (int q = 0; q < kCompPF; ++q) {
+      const int i = i0 + q, c = BWD ? nC - 1 - i : i;
+      if (i < nC) {
+        // backward: the adjoint flowing into chunk c, before its own map
+        if (BWD && dok) {
+          float* o = out + ((bh * nC + c) * DL + d) * NS;
 #pragma unroll
-    for (int t = 0; t < kMaxT; ++t) {
-      if (t < p.T) {
-        float dec[4], inb[4], outc[4];
-        unpack(sCoef[w][0][t][ng], dec);
-        unpack(sCoef[w][1][t][ng], inb);
-        unpack(sCoef[w][2][t][ng], outc);
-        float yp = 0.f;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          hs[k] = dec[k] * hs[k] + inb[k] * uv[t];
-          yp += outc[k] * hs[k];
+          for (int k = 0; k < 4; ++k)
+            if (nb + k < NS) o[nb + k] = x[k];
         }
-        yp = ngroup_sum(yp);
-        if (act && dok && ng == (t & 3)) ylane[t * ystep] = yp;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x[k] = pv[q][k] * x[k] + ev[q][k];
+        // forward: the state after chunk c
+        if (!BWD && dok) {
+          float* o = out + ((bh * nC + c) * DL + d) * NS;
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            if (nb + k < NS) o[nb + k] = x[k];
+        }
       }
     }
-    if (act && dok) {
-      float* ck = p.ckpt + ((bh * p.nC + c) * p.DL + d) * p.NS;
+  }
+  if (xlast != nullptr && dok) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (nb + k < p.NS) ck[nb + k] = hs[k];
+    for (int k = 0; k < 4; ++k)
+      if (nb + k < NS) xlast[bh * DL * NS + state_idx<GLA>(d, nb + k, DL, NS)] = x[k];
+  }
+}
+
+// Grid of the chunk-parallel kernels: x = tile + (ND * NN) * group, where
+// group g holds chunks NW g .. NW g + NW - 1 (one per wave).
+template <typename InT, bool GLA, int NW, bool FULL>
+__global__ __launch_bounds__(64 * NW) void r1_out_kernel(Args<InT> p) {
+  __shared__ float4 sCoef[NW][3][kMaxT][4];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ng = lane >> 4, dl = lane & 15;
+  const int tiles = p.ND * p.NN, tile = blockIdx.x % tiles, grp = blockIdx.x / tiles;
+  const int dt = tile / p.NN, nt = tile % p.NN;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int d = dt * kTile + dl;
+  const bool dok = d < p.DL;
+  const int nb = nt * kTile + ng * 4;
+  const int64_t bh = (int64_t)b * p.H + h;
+  const int c = grp * NW + w;
+  const bool act = c < p.nC;
+  stage_chunk<InT, GLA>(p, sCoef[w], b, h, c, act, nt, lane);
+  float uv[kMaxT], hs[4];
+  {
+    const int cc = act ? c : 0, dc = min(d, p.DL - 1);
+#pragma unroll
+    for (int t = 0; t < kMaxT; ++t)
+      uv[t] = rr::ld(p.lane_in, (((int64_t)b * p.L + (int64_t)cc * p.T + min(t, p.T - 1)) * p.H + h) * p.DL + dc);
+    // the entering state: checkpoint slot c - 1, else h0, else zero
+    const bool from_ck = cc > 0, has = from_ck || p.h0 != nullptr;
+    const float* hsrc = from_ck ? p.ckpt : has ? p.h0 : p.ckpt;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int ncl = min(nb + k, p.NS - 1);
+      const int64_t i = from_ck ? ((bh * p.nC + (cc - 1)) * p.DL + dc) * p.NS + ncl
+                        : has   ? bh * p.DL * p.NS + state_idx<GLA>(dc, ncl, p.DL, p.NS)
+                                : 0;
+      hs[k] = hsrc[i];
     }
-    __syncthreads();
 #pragma unroll
-    for (int k = 0; k < 4; ++k) carry[k] = nxt[k];
+    for (int t = 0; t < kMaxT; ++t) uv[t] = t < p.T && act && dok ? uv[t] : 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) hs[k] = act && dok && has && nb + k < p.NS ? hs[k] : 0.f;
+  }
+  __syncthreads();
+  float* yout = p.y + (p.NN > 1 ? (int64_t)nt * p.rows * p.DL : 0);
+  // this lane's y of step 0 of the chunk; step t is t * H * DL further
+  float* const ylane = yout + (((int64_t)b * p.L + (int64_t)(act ? c : 0) * p.T) * p.H + h) * p.DL + d;
+  const int64_t ystep = (int64_t)p.H * p.DL;
+#pragma unroll
+  for (int t = 0; t < kMaxT; ++t) {
+    if (FULL || t < p.T) {
+      float dec[4], inb[4], outc[4];
+      unpack(sCoef[w][0][t][ng], dec);
+      unpack(sCoef[w][1][t][ng], inb);
+      unpack(sCoef[w][2][t][ng], outc);
+      float yp = 0.f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        hs[k] = dec[k] * hs[k] + inb[k] * uv[t];
+        yp += outc[k] * hs[k];
+      }
+      yp = ngroup_sum(yp);
+      if (act && dok && ng == (t & 3)) ylane[t * ystep] = yp;
+    }
   }
 }
 
@@ -264,16 +387,15 @@ __device__ __forceinline__ float pick12(const float (&g)[12], int i) {
 
 // PART: the grid has several n-tiles (NN > 1) and du / dv goes to per-tile
 // fp32 partials, else straight to gu.
-template <typename InT, bool GLA, int NW, bool PART>
+template <typename InT, bool GLA, int NW, bool PART, bool FULL>
 __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
   __shared__ float4 sCoef[NW][3][kMaxT][4];
   __shared__ float sU[NW][kMaxT][kTile];   // u_t[d] of the wave's chunk
   __shared__ float sG[NW][kMaxT][kTile];   // dy_t[d]
-  __shared__ float4 sE[NW][64];
-  __shared__ float4 sP[NW][4];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ng = lane >> 4, dl = lane & 15;
-  const int dt = blockIdx.x / p.NN, nt = blockIdx.x % p.NN;
+  const int tiles = p.ND * p.NN, tile = blockIdx.x % tiles, grp = blockIdx.x / tiles;
+  const int dt = tile / p.NN, nt = tile % p.NN;
   const int h = blockIdx.y, b = blockIdx.z;
   const int d = dt * kTile + dl;
   const bool dok = d < p.DL;
@@ -282,18 +404,11 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
   const int64_t sbase = bh * p.DL * p.NS;
   float* gin_p = p.g3 + (int64_t)dt * p.rows * p.NS;   // then Gout, Hp, ND * rows * NS apart
 
-  float carry[4] = {0.f, 0.f, 0.f, 0.f};
-  if (p.dfinal != nullptr && dok) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (nb + k < p.NS) carry[k] = p.dfinal[sbase + state_idx<GLA>(d, nb + k, p.DL, p.NS)];
-  }
-
-  for (int r0 = 0; r0 < p.nC; r0 += NW) {
-    const int c = p.nC - 1 - (r0 + w);
-    const bool act = c >= 0;
+  {
+    const int c = grp * NW + w;
+    const bool act = c < p.nC;
     stage_chunk<InT, GLA>(p, sCoef[w], b, h, c, act, nt, lane);
-    float hst[4];
+    float hst[4], lam[4];
     {
       // u and dy of columns dt*16 + lane % 16, steps lane / 16 + 4 j
       const int cc = act ? c : 0, dd = dt * kTile + (lane & 15), ddc = min(dd, p.DL - 1);
@@ -305,8 +420,9 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
         uvv[j] = rr::ld(p.lane_in, i);
         gyv[j] = p.dy[i];
       }
-      // the entering state: checkpoint slot c - 1, else h0, else zero
-      const bool from_ck = c > 0, has = from_ck || p.h0 != nullptr;
+      // the entering state: checkpoint slot c - 1, else h0, else zero (an
+      // inactive wave, c >= nC, reads chunk 0's and drops it)
+      const bool from_ck = cc > 0, has = from_ck || p.h0 != nullptr;
       const float* hsrc = from_ck ? p.ckpt : has ? p.h0 : p.ckpt;
       const int dc = min(d, p.DL - 1);
 #pragma unroll
@@ -326,6 +442,12 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
       }
 #pragma unroll
       for (int k = 0; k < 4; ++k) hst[k] = act && dok && has && nb + k < p.NS ? hst[k] : 0.f;
+      // the adjoint flowing into the chunk from the later ones (r1_compose_kernel)
+      const float* lsrc = p.lamws + ((bh * p.nC + cc) * p.DL + dc) * p.NS;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) lam[k] = lsrc[min(nb + k, p.NS - 1)];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) lam[k] = act && dok && nb + k < p.NS ? lam[k] : 0.f;
     }
     __syncthreads();
     // The chunk's states are recomputed from its checkpoint in two halves of
@@ -335,45 +457,13 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
     float hmid[4] = {hst[0], hst[1], hst[2], hst[3]};
 #pragma unroll
     for (int t = 0; t < kHalf; ++t) {
-      if (t < p.T) {
+      if (FULL || t < p.T) {
         float dec[4], inb[4];
         unpack(sCoef[w][0][t][ng], dec);
         unpack(sCoef[w][1][t][ng], inb);
         const float uvt = sU[w][t][dl];
 #pragma unroll
         for (int k = 0; k < 4; ++k) hmid[k] = dec[k] * hmid[k] + inb[k] * uvt;
-      }
-    }
-    // Chunk map of the adjoint from a zero carry.
-    float e[4] = {0.f, 0.f, 0.f, 0.f}, P[4] = {1.f, 1.f, 1.f, 1.f};
-#pragma unroll
-    for (int t = kMaxT - 1; t >= 0; --t) {
-      if (t < p.T) {
-        float dec[4], outc[4];
-        unpack(sCoef[w][0][t][ng], dec);
-        unpack(sCoef[w][2][t][ng], outc);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          e[k] = (e[k] + sG[w][t][dl] * outc[k]) * dec[k];
-          P[k] *= dec[k];
-        }
-      }
-    }
-    sE[w][lane] = make_float4(e[0], e[1], e[2], e[3]);
-    if (dl == 0) sP[w][ng] = make_float4(P[0], P[1], P[2], P[3]);
-    __syncthreads();
-    float lam[4], nxt[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) lam[k] = nxt[k] = carry[k];
-#pragma unroll
-    for (int j = 0; j < NW; ++j) {
-      float pj[4], ej[4];
-      unpack(sP[j][ng], pj);
-      unpack(sE[j][lane], ej);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        if (j < w) lam[k] = pj[k] * lam[k] + ej[k];
-        nxt[k] = pj[k] * nxt[k] + ej[k];
       }
     }
     // Steps t0 .. t0 + 15 of the adjoint, backwards, beside their states
@@ -394,7 +484,7 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
 #pragma unroll
         for (int i = 0; i < kHalf; ++i) {
           const int t = t0 + i;
-          if (t < p.T) {
+          if (FULL || t < p.T) {
             float dec[4], inb[4];
             unpack(sCoef[w][0][t][ng], dec);
             unpack(sCoef[w][1][t][ng], inb);
@@ -409,7 +499,7 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
 #pragma unroll
       for (int i = kHalf - 1; i >= 0; --i) {
         const int t = t0 + i;
-        if (t < p.T) {
+        if (FULL || t < p.T) {
           float dec[4], inb[4], outc[4];
           unpack(sCoef[w][0][t][ng], dec);
           unpack(sCoef[w][1][t][ng], inb);
@@ -442,14 +532,6 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
     };
     adjoint_half(std::integral_constant<int, kHalf>{}, hmid);
     adjoint_half(std::integral_constant<int, 0>{}, hst);
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < 4; ++k) carry[k] = nxt[k];
-  }
-  if (p.dh0 != nullptr && dok && w == 0) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (nb + k < p.NS) p.dh0[sbase + state_idx<GLA>(d, nb + k, p.DL, p.NS)] = carry[k];
   }
 }
 
@@ -580,8 +662,9 @@ __global__ void sum_gA_kernel(const float* __restrict__ part, float* __restrict_
 
 // ------------------------------------------------------------------ host
 struct Plan {
-  int64_t T, nC, ND, NN, rows, nblk;
-  size_t off_y, off_g3, off_gu, off_gA, fwd_bytes, bwd_bytes;
+  int64_t T, nC, ND, NN, rows, nblk, groups;
+  size_t off_y, off_g3, off_gu, off_gA, off_lam, fwd_bytes, bwd_bytes;
+  size_t fwd_mapE, fwd_mapP, bwd_mapE, bwd_mapP;   // chunk maps of each pass
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -594,15 +677,26 @@ Plan make_plan(int64_t B, int64_t L, int64_t H, int64_t DL, int64_t NS, int64_t 
   q.NN = (NS + kTile - 1) / kTile;
   q.rows = B * L * H;
   q.nblk = (B * L + kFinRows - 1) / kFinRows;
+  q.groups = (q.nC + kChunkWaves - 1) / kChunkWaves;
   const size_t f = sizeof(float);
+  const size_t mapE = align256(B * H * q.nC * DL * NS * f), mapP = align256(B * H * q.nC * NS * f);
   q.off_y = 0;
   q.fwd_bytes = q.NN > 1 ? align256(q.NN * q.rows * DL * f) : 0;
+  q.fwd_mapE = q.fwd_bytes;
+  q.fwd_mapP = q.fwd_mapE + mapE;
+  q.fwd_bytes = q.fwd_mapP + mapP;
   q.off_g3 = 0;
   size_t o = align256(3 * q.ND * q.rows * NS * f);
   q.off_gu = o;
   o += q.NN > 1 ? align256(q.NN * q.rows * DL * f) : 0;
   q.off_gA = o;
   o += align256(H * q.nblk * NS * f);
+  q.off_lam = o;
+  o += align256(B * H * q.nC * DL * NS * f);
+  q.bwd_mapE = o;
+  o += mapE;
+  q.bwd_mapP = o;
+  o += mapP;
   q.bwd_bytes = o;
   return q;
 }
@@ -622,9 +716,20 @@ int check_dims(const char* who, int64_t B, int64_t L, int64_t H, int64_t DL, int
 
 template <typename InT, bool GLA>
 int launch_fwd(Args<InT> a, const Plan& q, int64_t B, void* ws, hipStream_t s, float* y) {
+  if (q.ND * q.NN * q.groups >= ((int64_t)1 << 31))
+    return rr::fail(RR_EUNSUPPORTED, "scan: too many (tile, chunk group) workgroups");
   const dim3 grid((unsigned)(q.ND * q.NN), (unsigned)a.H, (unsigned)B);
-  hipLaunchKernelGGL((r1_fwd_kernel<InT, GLA, kFwdWaves>), grid, dim3(64 * kFwdWaves), 0, s, a);
-  if (int rc = rr::check_launch("scan forward")) return rc;
+  const dim3 cgrid((unsigned)(q.ND * q.NN * q.groups), (unsigned)a.H, (unsigned)B), cblk(64 * kChunkWaves);
+  a.mapE = reinterpret_cast<float*>(static_cast<char*>(ws) + q.fwd_mapE);
+  a.mapP = reinterpret_cast<float*>(static_cast<char*>(ws) + q.fwd_mapP);
+  hipLaunchKernelGGL((r1_fold_kernel<InT, GLA, kChunkWaves, false>), cgrid, cblk, 0, s, a);
+  if (int rc = rr::check_launch("scan forward chunk maps")) return rc;
+  hipLaunchKernelGGL((r1_compose_kernel<GLA, false>), grid, dim3(64), 0, s, a.mapE, a.mapP, a.h0, a.ckpt, nullptr,
+                     a.H, a.DL, a.NS, a.nC, a.NN);
+  if (int rc = rr::check_launch("scan forward states")) return rc;
+  if (q.T == kMaxT) hipLaunchKernelGGL((r1_out_kernel<InT, GLA, kChunkWaves, true>), cgrid, cblk, 0, s, a);
+  else hipLaunchKernelGGL((r1_out_kernel<InT, GLA, kChunkWaves, false>), cgrid, cblk, 0, s, a);
+  if (int rc = rr::check_launch("scan forward outputs")) return rc;
   if (q.NN > 1) {
     const int64_t n = q.rows * a.DL;
     hipLaunchKernelGGL(sum_tiles_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
@@ -637,11 +742,22 @@ int launch_fwd(Args<InT> a, const Plan& q, int64_t B, void* ws, hipStream_t s, f
 template <typename InT, bool GLA>
 int launch_bwd(Args<InT> a, FinArgs<InT> f, const Plan& q, int64_t B, hipStream_t s,
                float* dA) {
+  if (q.ND * q.NN * q.groups >= ((int64_t)1 << 31))
+    return rr::fail(RR_EUNSUPPORTED, "scan: too many (tile, chunk group) workgroups");
   const dim3 grid((unsigned)(q.ND * q.NN), (unsigned)a.H, (unsigned)B);
-  if (q.NN > 1)
-    hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kBwdWaves, true>), grid, dim3(64 * kBwdWaves), 0, s, a);
-  else
-    hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kBwdWaves, false>), grid, dim3(64 * kBwdWaves), 0, s, a);
+  const dim3 cgrid((unsigned)(q.ND * q.NN * q.groups), (unsigned)a.H, (unsigned)B), cblk(64 * kChunkWaves);
+  hipLaunchKernelGGL((r1_fold_kernel<InT, GLA, kChunkWaves, true>), cgrid, cblk, 0, s, a);
+  if (int rc = rr::check_launch("scan backward chunk maps")) return rc;
+  hipLaunchKernelGGL((r1_compose_kernel<GLA, true>), grid, dim3(64), 0, s, a.mapE, a.mapP, a.dfinal, a.lamws, a.dh0,
+                     a.H, a.DL, a.NS, a.nC, a.NN);
+  if (int rc = rr::check_launch("scan backward adjoints")) return rc;
+  if (q.T == kMaxT) {
+    if (q.NN > 1) hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kChunkWaves, true, true>), cgrid, cblk, 0, s, a);
+    else hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kChunkWaves, false, true>), cgrid, cblk, 0, s, a);
+  } else {
+    if (q.NN > 1) hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kChunkWaves, true, false>), cgrid, cblk, 0, s, a);
+    else hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kChunkWaves, false, false>), cgrid, cblk, 0, s, a);
+  }
   if (int rc = rr::check_launch("scan backward")) return rc;
   const dim3 fgrid((unsigned)q.nblk, (unsigned)a.H);
   if (a.NS <= 16)
@@ -799,6 +915,9 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
     a.gu = static_cast<InT*>(du);
     a.gu_part = reinterpret_cast<float*>(ws + q.off_gu);
     a.g3 = reinterpret_cast<float*>(ws + q.off_g3);
+    a.lamws = reinterpret_cast<float*>(ws + q.off_lam);
+    a.mapE = reinterpret_cast<float*>(ws + q.bwd_mapE);
+    a.mapP = reinterpret_cast<float*>(ws + q.bwd_mapP);
     a.dh0 = dh0;
     a.L = (int)L; a.H = (int)H; a.DL = (int)Dh; a.NS = (int)N; a.T = (int)q.T;
     a.nC = (int)q.nC; a.ND = (int)q.ND; a.NN = (int)q.NN; a.rows = q.rows;
@@ -982,6 +1101,9 @@ extern "C" int rr_gla_bwd(const float* dy, const float* dfinal, const void* qp, 
     a.gu = static_cast<InT*>(dv);
     a.gu_part = reinterpret_cast<float*>(ws + q.off_gu);
     a.g3 = reinterpret_cast<float*>(ws + q.off_g3);
+    a.lamws = reinterpret_cast<float*>(ws + q.off_lam);
+    a.mapE = reinterpret_cast<float*>(ws + q.bwd_mapE);
+    a.mapP = reinterpret_cast<float*>(ws + q.bwd_mapP);
     a.dh0 = dh0;
     a.L = (int)L; a.H = (int)H; a.DL = (int)Dh; a.NS = (int)Dh; a.T = (int)q.T;
     a.nC = (int)q.nC; a.ND = (int)q.ND; a.NN = (int)q.NN; a.rows = q.rows;
