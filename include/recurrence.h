@@ -116,13 +116,15 @@ int rr_ssd_fwd(const void* u, const void* delta, const void* Bm, const void* Cm,
 
 /* Replaces _ssd_backward_kernel and the host mx.sum epilogue
  * (reference mlx_recurrence/ssd.py:142-307).  dy [B,L,H,Dh] fp32; gradients
- * du/ddelta/dB/dC in `dtype` with the shapes of their inputs; dA_neg [H,N] fp32
- * (summed over the batch, ssd.py:305), dense even when A_stride_n == 0. */
+ * du/ddelta/dB/dC in `dtype` with the shapes of their inputs; dA_neg fp32,
+ * summed over the batch (ssd.py:305): with dA_stride_n = 1 the dense [H,N]
+ * gradient (whatever A_stride_n is), with dA_stride_n = 0 the [H] gradient of a
+ * per-head rate (the [H,N] one summed over n, in order of n). */
 int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, const void* delta,
                const void* Bm, const void* Cm, const float* A_neg, int64_t A_stride_n, int dtype,
                int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N, int64_t seg,
                const float* h0, const float* ckpt, void* du, void* ddelta, void* dB,
-               void* dC, float* dA_neg, float* dh0, void* workspace,
+               void* dC, float* dA_neg, int64_t dA_stride_n, float* dh0, void* workspace,
                size_t workspace_bytes, void* stream);
 
 /* rr_ssd_bwd without a workspace argument, for callers that cannot allocate
@@ -138,7 +140,7 @@ int rr_ssd_bwd_noalloc(const float* dy, const float* dfinal, const void* u, cons
                        const void* Bm, const void* Cm, const float* A_neg, int64_t A_stride_n, int dtype,
                        int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N, int64_t seg,
                        const float* h0, const float* ckpt, void* du, void* ddelta, void* dB,
-                       void* dC, float* dA_neg, float* dh0, void* stream);
+                       void* dC, float* dA_neg, int64_t dA_stride_n, float* dh0, void* stream);
 
 /* ------------------------------------------------------------------ GLA --
  * q/k/v [B,L,H,Dh], gates [B,L,H] (dtype).  y [B,L,H,Dh] fp32.

@@ -27,7 +27,8 @@ struct ChunkArgs {
   uint16_t* ddelta;
   uint16_t* dB;
   uint16_t* dC;
-  float* dA;               // [H,N]
+  float* dA;               // [H,N], or [H] (summed over n) when dA_sn == 0
+  int dA_sn;               // n-stride of dA: 1 dense [H,N], 0 per head [H]
   float* dh0;              // [B,H,Dh,N] or null
   float* ws;               // SSD backward: dA partials [B,H,nR,N]
   float* tot;              // pipelined: per-chunk decay gam_31 [B,H,nC]

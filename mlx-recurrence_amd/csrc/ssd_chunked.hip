@@ -773,10 +773,11 @@ __global__ __launch_bounds__(256, (kBwdWgs<DH, NS, MODE>)) void ssd2_bwd_kernel(
 // dA[h, n] = sum over batch rows and runs of the per-run partials, in a fixed
 // order: one workgroup per head, thread (g, n) sums partials g, g + G, ... in
 // four interleaved accumulators (four loads in flight), then the G per-thread
-// sums are added in order.
+// sums are added in order.  Per head (dA_sn == 0): dA[h] = the sum of those
+// over n, in order of n.
 template <int T>
 __global__ __launch_bounds__(T) void ssd2_dA_kernel(const float* __restrict__ part, float* __restrict__ dA, int Bsz,
-                                                    int H, int nR, int NS) {
+                                                    int H, int nR, int NS, int dA_sn) {
   __shared__ float red[T];
   const int h = blockIdx.x, G = T / NS, n = threadIdx.x % NS, g = threadIdx.x / NS;
   const int parts = Bsz * nR;
@@ -795,10 +796,20 @@ __global__ __launch_bounds__(T) void ssd2_dA_kernel(const float* __restrict__ pa
   }
   red[threadIdx.x] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   __syncthreads();
+  float t = 0.f;
   if (threadIdx.x < NS) {
-    float t = 0.f;
     for (int q = 0; q < G; ++q) t += red[q * NS + threadIdx.x];
-    dA[(int64_t)h * NS + threadIdx.x] = t;
+    if (dA_sn != 0) dA[(int64_t)h * NS + threadIdx.x] = t;
+  }
+  if (dA_sn == 0) {
+    __syncthreads();   // every partial read; red[] takes the per-n sums
+    if (threadIdx.x < NS) red[threadIdx.x] = t;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float s = 0.f;
+      for (int n2 = 0; n2 < NS; ++n2) s += red[n2];
+      dA[h] = s;
+    }
   }
 }
 
@@ -806,9 +817,9 @@ int launch_dA(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
   const int nR = (p.nC + p.R - 1) / p.R;   // runs per head
   // (a larger workgroup only where there are many partials to sum)
   if ((int64_t)B * nR * p.NS > 4096)
-    hipLaunchKernelGGL(ssd2_dA_kernel<1024>, dim3(p.H), dim3(1024), 0, s, p.ws, p.dA, (int)B, p.H, nR, p.NS);
+    hipLaunchKernelGGL(ssd2_dA_kernel<1024>, dim3(p.H), dim3(1024), 0, s, p.ws, p.dA, (int)B, p.H, nR, p.NS, p.dA_sn);
   else
-    hipLaunchKernelGGL(ssd2_dA_kernel<256>, dim3(p.H), dim3(256), 0, s, p.ws, p.dA, (int)B, p.H, nR, p.NS);
+    hipLaunchKernelGGL(ssd2_dA_kernel<256>, dim3(p.H), dim3(256), 0, s, p.ws, p.dA, (int)B, p.H, nR, p.NS, p.dA_sn);
   return rr::check_launch("ssd chunked backward dA");
 }
 

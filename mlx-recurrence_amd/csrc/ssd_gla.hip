@@ -649,15 +649,20 @@ __global__ __launch_bounds__(256) void r1_finalize_kernel(FinArgs<InT> p) {
   }
 }
 
-// dA_neg[h, n] = sum over finalize blocks (fixed order: deterministic).
+// dA_neg[h, n] = sum over finalize blocks (fixed order: deterministic); per
+// head (dA_sn == 0) dA_neg[h] = the sum of those over n, in order of n.
 __global__ void sum_gA_kernel(const float* __restrict__ part, float* __restrict__ dA, int H,
-                              int NS, int nblk) {
+                              int NS, int nblk, int dA_sn) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= H * NS) return;
-  const int h = i / NS, n = i % NS;
-  float s = 0.f;
-  for (int j = 0; j < nblk; ++j) s += part[((int64_t)h * nblk + j) * NS + n];
-  dA[i] = s;
+  if (i >= (dA_sn != 0 ? H * NS : H)) return;
+  const int h = dA_sn != 0 ? i / NS : i, n0 = dA_sn != 0 ? i % NS : 0, n1 = dA_sn != 0 ? n0 + 1 : NS;
+  float t = 0.f;
+  for (int n = n0; n < n1; ++n) {
+    float s = 0.f;
+    for (int j = 0; j < nblk; ++j) s += part[((int64_t)h * nblk + j) * NS + n];
+    t += s;
+  }
+  dA[i] = t;
 }
 
 // ------------------------------------------------------------------ host
@@ -741,7 +746,7 @@ int launch_fwd(Args<InT> a, const Plan& q, int64_t B, void* ws, hipStream_t s, f
 
 template <typename InT, bool GLA>
 int launch_bwd(Args<InT> a, FinArgs<InT> f, const Plan& q, int64_t B, hipStream_t s,
-               float* dA) {
+               float* dA, int dA_sn) {
   if (q.ND * q.NN * q.groups >= ((int64_t)1 << 31))
     return rr::fail(RR_EUNSUPPORTED, "scan: too many (tile, chunk group) workgroups");
   const dim3 grid((unsigned)(q.ND * q.NN), (unsigned)a.H, (unsigned)B);
@@ -770,7 +775,7 @@ int launch_bwd(Args<InT> a, FinArgs<InT> f, const Plan& q, int64_t B, hipStream_
   if (!GLA) {
     const int n = (int)(a.H * a.NS);
     hipLaunchKernelGGL(sum_gA_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                       f.gA_part, dA, a.H, a.NS, (int)q.nblk);
+                       f.gA_part, dA, a.H, a.NS, (int)q.nblk, dA_sn);
     if (int rc = rr::check_launch("scan backward dA")) return rc;
   }
   return RR_OK;
@@ -857,7 +862,7 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
                           int dtype,
                           int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N, int64_t seg,
                           const float* h0, const float* ckpt, void* du, void* ddelta, void* dB,
-                          void* dC, float* dA_neg, float* dh0, void* workspace,
+                          void* dC, float* dA_neg, int64_t dA_stride_n, float* dh0, void* workspace,
                           size_t workspace_bytes, void* stream) {
   if (int rc = check_dims("ssd_bwd", B, L, H, Dh, N, seg, dtype, "Dh")) return rc;
   if (N > 256) return rr::fail(RR_EUNSUPPORTED, "ssd_bwd: N > 256 is not supported");
@@ -866,6 +871,8 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
     return rr::fail(RR_EINVAL, "ssd_bwd: null pointer argument");
   if (A_stride_n != 0 && A_stride_n != 1)
     return rr::fail(RR_EINVAL, "ssd_bwd: A_stride_n must be 0 or 1");
+  if (dA_stride_n != 0 && dA_stride_n != 1)
+    return rr::fail(RR_EINVAL, "ssd_bwd: dA_stride_n must be 0 or 1");
   if (rr::ssd2_supported(dtype, L, seg, Dh, N, A_stride_n) && rr::ssd2_bwd_supported(Dh, N)) {
     const int nC = (int)(L / 32);
     const int mode = rr::chunked_mode(B, H, nC, Dh, N, 1);
@@ -887,6 +894,7 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
     a.dB = static_cast<uint16_t*>(dB);
     a.dC = static_cast<uint16_t*>(dC);
     a.dA = dA_neg;
+    a.dA_sn = (int)dA_stride_n;
     a.dh0 = dh0;
     a.B = (int)B; a.L = (int)L; a.H = (int)H; a.DH = (int)Dh; a.NS = (int)N; a.nC = nC;
     a.mode = mode;
@@ -935,7 +943,7 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
     f.gu = static_cast<InT*>(du);
     f.gA_part = reinterpret_cast<float*>(ws + q.off_gA);
     f.BL = B * L; f.H = (int)H; f.DL = (int)Dh; f.NS = (int)N; f.ND = (int)q.ND; f.NN = (int)q.NN;
-    return launch_bwd<InT, false>(a, f, q, B, s, dA_neg);
+    return launch_bwd<InT, false>(a, f, q, B, s, dA_neg, (int)dA_stride_n);
   });
   return RR_OK;
 }
@@ -979,7 +987,8 @@ extern "C" int rr_ssd_bwd_noalloc(const float* dy, const float* dfinal, const vo
                                   const void* Bm, const void* Cm, const float* A_neg, int64_t A_stride_n,
                                   int dtype, int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N,
                                   int64_t seg, const float* h0, const float* ckpt, void* du, void* ddelta,
-                                  void* dB, void* dC, float* dA_neg, float* dh0, void* stream) {
+                                  void* dB, void* dC, float* dA_neg, int64_t dA_stride_n, float* dh0,
+                                  void* stream) {
   if (int rc = check_dims("ssd_bwd_noalloc", B, L, H, Dh, N, seg, dtype, "Dh")) return rc;
   if (A_stride_n != 0 && A_stride_n != 1)
     return rr::fail(RR_EINVAL, "ssd_bwd_noalloc: A_stride_n must be 0 or 1");
@@ -992,7 +1001,7 @@ extern "C" int rr_ssd_bwd_noalloc(const float* dy, const float* dfinal, const vo
   void* ws = scratch_ptr();
   if (ws == nullptr) return RR_EHIP;
   return rr_ssd_bwd(dy, dfinal, u, delta, Bm, Cm, A_neg, A_stride_n, dtype, B, L, H, Dh, N, seg, h0, ckpt, du,
-                    ddelta, dB, dC, dA_neg, dh0, ws, kNoAllocScratchBytes, stream);
+                    ddelta, dB, dC, dA_neg, dA_stride_n, dh0, ws, kNoAllocScratchBytes, stream);
 }
 
 // ====================================================================== GLA
@@ -1116,7 +1125,7 @@ extern "C" int rr_gla_bwd(const float* dy, const float* dfinal, const void* qp, 
     f.g_step = static_cast<InT*>(dgates);
     f.gu = static_cast<InT*>(dv);
     f.BL = B * L; f.H = (int)H; f.DL = (int)Dh; f.NS = (int)Dh; f.ND = (int)q.ND; f.NN = (int)q.NN;
-    return launch_bwd<InT, true>(a, f, q, B, s, nullptr);
+    return launch_bwd<InT, true>(a, f, q, B, s, nullptr, 1);
   });
   return RR_OK;
 }

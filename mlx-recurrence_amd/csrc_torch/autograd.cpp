@@ -181,24 +181,20 @@ struct SSDFn : public torch::autograd::Function<SSDFn> {
     const int dtc = dtype_code(dt);
     const size_t wsb = rr_ssd_workspace_bytes(Bsz, L, H, Dh, N, seg, a_sn, dtc, 1);
     const bool heads = ctx->saved_data["a_dim"].toInt() == 1;   // A_neg [H]: its gradient sums dA over n
-    Arena ar;   // du, ddelta, dB, dC in the inputs' dtype; dA (fp32, [H] case) as bytes
+    Arena ar;   // du, ddelta, dB, dC in the inputs' dtype
     const int64_t odu = ar.reserve(u_.numel() * es), odd = ar.reserve(d_.numel() * es);
     const int64_t odB = ar.reserve(B_.numel() * es), odC = ar.reserve(C_.numel() * es);
-    const int64_t odA = heads ? ar.reserve(H * N * 4) : 0;
     ar.allocate(u_.options(), dt);
     const Tensor ws = workspace(wsb, u_.options());
     Tensor du = ar.view(odu, u_.sizes()), dd = ar.view(odd, d_.sizes());
     Tensor dB = ar.view(odB, B_.sizes()), dC = ar.view(odC, C_.sizes());
-    Tensor dA_full = heads ? Tensor() : at::empty({H, N}, f32);
-    float* dA = heads ? static_cast<float*>(ar.ptr(odA)) : MF(dA_full);
+    // A_neg [H]: the library sums the gradient over n itself (dA_stride_n 0)
+    Tensor dA = heads ? at::empty({H}, f32) : at::empty({H, N}, f32);
     check(rr_ssd_bwd(PF(dy), PF(dfinal), P(u_), P(d_), P(B_), P(C_), PF(A_), a_sn, dtc, Bsz, L, H, Dh, N, seg,
-                     PF(h0_), PF(ckpt), P(du), P(dd), P(dB), P(dC), dA, MF(dh0), P(ws), wsb, stream_of(u_)),
+                     PF(h0_), PF(ckpt), P(du), P(dd), P(dB), P(dC), MF(dA), heads ? 0 : 1, MF(dh0), P(ws), wsb,
+                     stream_of(u_)),
           "rr_ssd_bwd");
-    // [H] case: the sum over n reads the arena's piece through a non-owning
-    // tensor; the arena outlives the enqueue, and a block freed to the caching
-    // allocator is reused only by work ordered after it on this stream
-    Tensor dA_out = heads ? at::from_blob(dA, {H, N}, f32).sum(1) : dA_full;
-    return {du, dd, dB, dC, dA_out, dh0, Tensor()};
+    return {du, dd, dB, dC, dA, dh0, Tensor()};
   }
 };
 

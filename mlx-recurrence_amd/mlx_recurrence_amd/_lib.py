@@ -45,8 +45,10 @@ _SIGS = {
     "rr_ssd_workspace_bytes": (_c_size, [_c_i64] * 7 + [_c_int, _c_int]),
     "rr_ssd_workspace_extent": (_c_i64, [_c_i64] * 7 + [_c_int, _c_int]),
     "rr_ssd_fwd": (_c_int, [_c_ptr] * 5 + [_c_i64, _c_int] + [_c_i64] * 6 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
-    "rr_ssd_bwd": (_c_int, [_c_ptr] * 7 + [_c_i64, _c_int] + [_c_i64] * 6 + [_c_ptr] * 9 + [_c_size, _c_ptr]),
-    "rr_ssd_bwd_noalloc": (_c_int, [_c_ptr] * 7 + [_c_i64, _c_int] + [_c_i64] * 6 + [_c_ptr] * 9),
+    "rr_ssd_bwd": (_c_int, [_c_ptr] * 7 + [_c_i64, _c_int] + [_c_i64] * 6 + [_c_ptr] * 7 + [_c_i64]
+                   + [_c_ptr] * 2 + [_c_size, _c_ptr]),
+    "rr_ssd_bwd_noalloc": (_c_int, [_c_ptr] * 7 + [_c_i64, _c_int] + [_c_i64] * 6 + [_c_ptr] * 7 + [_c_i64]
+                           + [_c_ptr] * 2),
     "rr_gla_workspace_bytes": (_c_size, [_c_i64] * 5 + [_c_int, _c_int]),
     "rr_gla_fwd": (_c_int, [_c_ptr] * 4 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 4 + [_c_size, _c_ptr]),
     "rr_gla_bwd": (_c_int, [_c_ptr] * 6 + [_c_int] + [_c_i64] * 5 + [_c_ptr] * 8 + [_c_size, _c_ptr]),
@@ -272,12 +274,14 @@ def ssd_fwd(u, delta, Bm, Cm, A, a_stride_n, h0, seg, y, ckpt, ws):
 
 
 def ssd_bwd(dy, dfinal, u, delta, Bm, Cm, A, a_stride_n, h0, ckpt, seg, du, ddelta, dB, dC, dA, dh0, ws):
+    """rr_ssd_bwd; dA is [H, N] (dense gradient) or [H] (per-head gradient,
+    summed over n by the library)."""
     B, L, H, Dh = u.shape
     N = Bm.shape[-1]
     rc = load().rr_ssd_bwd(
         ptr(dy), ptr(dfinal), ptr(u), ptr(delta), ptr(Bm), ptr(Cm), ptr(A), a_stride_n,
         DTYPE_CODE[u.dtype], B, L, H, Dh, N, seg, ptr(h0), ptr(ckpt), ptr(du),
-        ptr(ddelta), ptr(dB), ptr(dC), ptr(dA), ptr(dh0), ptr(ws),
+        ptr(ddelta), ptr(dB), ptr(dC), ptr(dA), 0 if dA.ndim == 1 else 1, ptr(dh0), ptr(ws),
         0 if ws is None else ws.numel(), stream_of(u))
     _check(rc, "rr_ssd_bwd")
 
@@ -290,7 +294,7 @@ def ssd_bwd_noalloc(dy, dfinal, u, delta, Bm, Cm, A, a_stride_n, h0, ckpt, seg, 
     rc = load().rr_ssd_bwd_noalloc(
         ptr(dy), ptr(dfinal), ptr(u), ptr(delta), ptr(Bm), ptr(Cm), ptr(A), a_stride_n,
         DTYPE_CODE[u.dtype], B, L, H, Dh, N, seg, ptr(h0), ptr(ckpt), ptr(du),
-        ptr(ddelta), ptr(dB), ptr(dC), ptr(dA), ptr(dh0), stream_of(u))
+        ptr(ddelta), ptr(dB), ptr(dC), ptr(dA), 0 if dA.ndim == 1 else 1, ptr(dh0), stream_of(u))
     _check(rc, "rr_ssd_bwd_noalloc")
 
 

@@ -89,12 +89,13 @@ class _SSDScan(torch.autograd.Function):
         dy = torch.zeros((Bsz, L, H, Dh), dtype=torch.float32, device=dev) if dy is None else _lib.prep(dy, torch.float32)
         dfinal = None if dfinal is None else _lib.prep(dfinal, torch.float32)
         du, dd, dB, dC = (torch.empty_like(t) for t in (u_, d_, B_, C_))
-        dA = torch.empty((H, N), dtype=torch.float32, device=dev)
+        # [H]: the library sums the gradient over n itself (one rate per head)
+        dA = torch.empty((H,) if ctx.a_dim == 1 else (H, N), dtype=torch.float32, device=dev)
         dh0 = torch.empty((Bsz, H, Dh, N), dtype=torch.float32, device=dev) if ctx.needs_input_grad[5] else None
         with _lib.device_guard(dev):
             ws = _lib.ssd_workspace(Bsz, L, H, Dh, N, ctx.seg, ctx.a_sn, u_.dtype, 1, dev)
             _lib.ssd_bwd(dy, dfinal, u_, d_, B_, C_, A_, ctx.a_sn, h0_, ckpt, ctx.seg, du, dd, dB, dC, dA, dh0, ws)
-        return du, dd, dB, dC, dA.sum(1) if ctx.a_dim == 1 else dA, dh0, None
+        return du, dd, dB, dC, dA, dh0, None
 
 
 def _run(u, delta, B, C, A_neg, seg, initial_state):

@@ -70,9 +70,12 @@ def test_ssd_gla_validation(lib):
     # too-small workspace is reported, not overrun
     need = lib.rr_ssd_workspace_bytes(2, 64, 2, 64, 8, 32, 1, 0, 1)
     if need:
-        rc = lib.rr_ssd_bwd(p, None, p, p, p, p, p, 1, 0, 2, 64, 2, 64, 8, 32, None, p, p, p, p, p, p, None,
+        rc = lib.rr_ssd_bwd(p, None, p, p, p, p, p, 1, 0, 2, 64, 2, 64, 8, 32, None, p, p, p, p, p, p, 1, None,
                             p, need - 1, None)
         assert rc == _lib.RR_EWORKSPACE
+        rc = lib.rr_ssd_bwd(p, None, p, p, p, p, p, 1, 0, 2, 64, 2, 64, 8, 32, None, p, p, p, p, p, p, 2, None,
+                            p, need, None)
+        assert rc == _lib.RR_EINVAL and b"dA_stride_n" in lib.rr_last_error()
     need = lib.rr_rglru_workspace_bytes(2, 256, 64, 32, 1, 0)
     assert need > 0
     rc = lib.rr_rglru_fwd(p, p, 1, 2, 256, 64, 32, None, p, p, p, need - 1, None)
@@ -86,11 +89,11 @@ def test_ssd_bwd_noalloc_rejects_beyond_its_scratch(lib):
     need = lib.rr_ssd_workspace_bytes(96, 512, 12, 64, 16, 32, 0, 1, 1)
     assert need > (16 << 20)
     rc = lib.rr_ssd_bwd_noalloc(p, None, p, p, p, p, p, 0, 1, 96, 512, 12, 64, 16, 32, None, p, p, p, p, p, p,
-                                None, None)
+                                1, None, None)
     assert rc == _lib.RR_EUNSUPPORTED and b"16777216-byte device scratch" in lib.rr_last_error()
     assert lib.rr_ssd_workspace_bytes(3, 512, 12, 64, 16, 32, 0, 1, 1) <= (16 << 20)   # config 1 fits
     rc = lib.rr_ssd_bwd_noalloc(p, None, p, p, p, p, p, 0, 1, 3, 30, 12, 64, 16, 32, None, p, p, p, p, p, p,
-                                None, None)
+                                1, None, None)
     assert rc == _lib.RR_EINVAL and b"L=30" in lib.rr_last_error()
 
 

@@ -405,6 +405,38 @@ def test_ssd_parity(B, L, H, Dh, N, seg, dtype, dist, h0, dfinal, seed):
     print(rep, flush=True)
 
 
+SSD_HEAD_VECTOR_CASES = [
+    # (B, L, H, Dh, N, seg, dtype, seed): A_neg passed as the [H] vector itself
+    (3, 512, 12, 64, 16, 32, BF16, 60),   # BASELINE config 1 (sum-mode chunk kernel + dA reduction)
+    (1, 256, 4, 64, 128, 32, BF16, 61),   # column-owned backward
+    (1, 128, 2, 32, 16, 32, F32, 62),     # fp32: the VALU engine
+    (2, 96, 2, 32, 24, 16, F32, 63),      # VALU engine, N = 24, T = 16
+]
+
+
+@pytest.mark.parametrize("B,L,H,Dh,N,seg,dtype,seed", SSD_HEAD_VECTOR_CASES)
+def test_ssd_per_head_rate_vector(B, L, H, Dh, N, seg, dtype, seed):
+    """A_neg as the [H] vector: its gradient is [H], the library's dA summed over
+    n in the kernel (dA_stride_n = 0), against the oracle's [H, N] one summed."""
+    _announce("ssd_head_vector", B=B, L=L, H=H, Dh=Dh, N=N, seg=seg, dtype=dtype, seed=seed)
+    rng = np.random.default_rng(seed)
+    u, delta, Bm, Cm, A = _ssd_inputs(rng, B, L, H, Dh, N, "cfg")
+    ut, dt, Bt, Ct = (to_dev(v, dtype, True) for v in (u, delta, Bm, Cm))
+    Ah = to_dev(A[:, 0], F32, True)
+    y = mr.ssd_scan(ut, dt, Bt, Ct, Ah, seg=seg)
+    W = _w(rng, (B, L, H, Dh))
+    (y * torch.tensor(W, dtype=F32, device=y.device)).sum().backward()
+    r = [rounded(t) for t in (ut, dt, Bt, Ct)] + [np.repeat(rounded(Ah)[:, None], N, axis=1)]
+    y_o, _ = orc.ssd_forward(*r)
+    grads_o = orc.ssd_backward(W, *r)
+    assert Ah.grad.shape == (H,)
+    tol, rep = TOL[dtype], {}
+    check("y", y, y_o, TOL[F32] if dtype == F32 else tol, rep)
+    check("grad_A", Ah.grad, grads_o[4].sum(1), max(tol, 1e-5) if dtype != F32 else TOL[F32], rep)
+    check("grad_delta", dt.grad, grads_o[1], tol, rep)
+    print(rep, flush=True)
+
+
 # -------------------------------------------------------------------- GLA
 def _gla_inputs(rng, B, L, H, Dh, dist):
     if dist == "ref":   # test_v2_gla.py:11-18
