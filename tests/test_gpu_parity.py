@@ -465,7 +465,7 @@ GLA_CASES = [
     # bf16 with T = 32: chunked MFMA kernels
     (2, 256, 3, 64, 32, BF16, "cfg", True, True, 20),
     (1, 128, 2, 32, 32, BF16, "ref", True, True, 21),
-    (1, 96, 2, 128, 32, BF16, "cfg", True, True, 22),   # Dh = 128: resident forward, pipelined backward
+    (1, 96, 2, 128, 32, BF16, "cfg", True, True, 22),   # Dh = 128: pipelined forward and backward (a 128 x 128 state)
     (1, 256, 3, 128, 32, BF16, "signed", True, True, 39),  # Dh = 128, 8 chunks, gates of either sign
     (2, 32, 2, 64, 32, BF16, "cfg", True, True, 23),    # one chunk
     (1, 160, 2, 64, 32, BF16, "signed", True, True, 24),
