@@ -315,9 +315,54 @@ __global__ __launch_bounds__(64) void r1_compose_kernel(const float* __restrict_
 
 // Grid of the chunk-parallel kernels: x = tile + (ND * NN) * group, where
 // group g holds chunks NW g .. NW g + NW - 1 (one per wave).
-template <typename InT, bool GLA, int NW, bool FULL>
+// Short heads (nC <= kDirectMaxChunks): the replay kernels compose the chunk
+// maps themselves instead of reading the compose kernel's output.  The
+// workgroup loads the maps of chunks j0 .. j0 + cnt - 1 of its tile into LDS
+// (wave w takes maps w, w + NW, ...; every load issued first, at a clamped
+// chunk), and each wave then walks the ones it needs from LDS.
+constexpr int kDirectMaxChunks = 16;
+struct MapSmem {
+  float4 E[kDirectMaxChunks][64];   // E of the tile, this lane's four states
+  float4 P[kDirectMaxChunks][4];    // P of the tile's 16 columns, by n-group
+};
+template <bool DIRECT>
+struct MaybeMaps {
+  MapSmem m;
+};
+template <>
+struct MaybeMaps<false> {};
+template <int NW, typename InT>
+__device__ __forceinline__ void load_maps(const Args<InT>& p, MapSmem& sm, int64_t bh, int d, int nb, int lane, int w,
+                                          int j0, int cnt) {
+  const int ng = lane >> 4, dl = lane & 15, dc = min(d, p.DL - 1);
+  constexpr int PER = kDirectMaxChunks / NW;
+  float ev[PER][4], pv[PER][4];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int j = min(j0 + w + NW * i, p.nC - 1);
+    const float* em = p.mapE + ((bh * p.nC + j) * p.DL + dc) * p.NS;
+    const float* pm = p.mapP + (bh * p.nC + j) * p.NS;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int ncl = min(nb + k, p.NS - 1);
+      ev[i][k] = em[ncl];
+      pv[i][k] = pm[ncl];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int jj = w + NW * i;
+    if (jj < cnt) {
+      sm.E[jj][lane] = make_float4(ev[i][0], ev[i][1], ev[i][2], ev[i][3]);
+      if (dl == 0) sm.P[jj][ng] = make_float4(pv[i][0], pv[i][1], pv[i][2], pv[i][3]);
+    }
+  }
+}
+
+template <typename InT, bool GLA, int NW, bool FULL, bool DIRECT>
 __global__ __launch_bounds__(64 * NW) void r1_out_kernel(Args<InT> p) {
   __shared__ float4 sCoef[NW][3][kMaxT][4];
+  __shared__ MaybeMaps<DIRECT> sMap;
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ng = lane >> 4, dl = lane & 15;
   const int tiles = p.ND * p.NN, tile = blockIdx.x % tiles, grp = blockIdx.x / tiles;
@@ -336,8 +381,9 @@ __global__ __launch_bounds__(64 * NW) void r1_out_kernel(Args<InT> p) {
 #pragma unroll
     for (int t = 0; t < kMaxT; ++t)
       uv[t] = rr::ld(p.lane_in, (((int64_t)b * p.L + (int64_t)cc * p.T + min(t, p.T - 1)) * p.H + h) * p.DL + dc);
-    // the entering state: checkpoint slot c - 1, else h0, else zero
-    const bool from_ck = cc > 0, has = from_ck || p.h0 != nullptr;
+    // the entering state: checkpoint slot c - 1, else h0, else zero (DIRECT:
+    // h0 or zero here, the maps of chunks 0 .. c - 1 applied below)
+    const bool from_ck = !DIRECT && cc > 0, has = from_ck || p.h0 != nullptr;
     const float* hsrc = from_ck ? p.ckpt : has ? p.h0 : p.ckpt;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -347,12 +393,25 @@ __global__ __launch_bounds__(64 * NW) void r1_out_kernel(Args<InT> p) {
                                 : 0;
       hs[k] = hsrc[i];
     }
+    if constexpr (DIRECT) load_maps<NW>(p, sMap.m, bh, d, nb, lane, w, 0, min(grp * NW + NW - 1, p.nC - 1));
 #pragma unroll
     for (int t = 0; t < kMaxT; ++t) uv[t] = t < p.T && act && dok ? uv[t] : 0.f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) hs[k] = act && dok && has && nb + k < p.NS ? hs[k] : 0.f;
   }
   __syncthreads();
+  if constexpr (DIRECT) {
+    // x <- P_j x + E_j over the chunks before this one
+    for (int j = 0; j < (act ? c : 0); ++j) {
+      float pj[4], ej[4];
+      unpack(sMap.m.P[j][ng], pj);
+      unpack(sMap.m.E[j][lane], ej);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) hs[k] = pj[k] * hs[k] + ej[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) hs[k] = act && dok && nb + k < p.NS ? hs[k] : 0.f;
+  }
   float* yout = p.y + (p.NN > 1 ? (int64_t)nt * p.rows * p.DL : 0);
   // this lane's y of step 0 of the chunk; step t is t * H * DL further
   float* const ylane = yout + (((int64_t)b * p.L + (int64_t)(act ? c : 0) * p.T) * p.H + h) * p.DL + d;
@@ -374,6 +433,12 @@ __global__ __launch_bounds__(64 * NW) void r1_out_kernel(Args<InT> p) {
       if (act && dok && ng == (t & 3)) ylane[t * ystep] = yp;
     }
   }
+  if (DIRECT && act && dok) {   // the state after the chunk: its checkpoint
+    float* ck = p.ckpt + ((bh * p.nC + c) * p.DL + d) * p.NS;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (nb + k < p.NS) ck[nb + k] = hs[k];
+  }
 }
 
 // g[i] for i < 12 (a select tree over the bits of i; i >= 12: any of them).
@@ -387,11 +452,33 @@ __device__ __forceinline__ float pick12(const float (&g)[12], int i) {
 
 // PART: the grid has several n-tiles (NN > 1) and du / dv goes to per-tile
 // fp32 partials, else straight to gu.
-template <typename InT, bool GLA, int NW, bool PART, bool FULL>
+// LDS of the backward replay: u_t[d] and dy_t[d] of each wave's chunk, and
+// (DIRECT) the chunk maps, which are dead before u and dy are staged.
+template <int NW, bool DIRECT>
+struct BwdLds {
+  struct UG {
+    float U[NW][kMaxT][kTile];
+    float G[NW][kMaxT][kTile];
+  };
+  union {
+    UG x;
+    MapSmem m;
+  };
+};
+template <int NW>
+struct BwdLds<NW, false> {
+  struct UG {
+    float U[NW][kMaxT][kTile];
+    float G[NW][kMaxT][kTile];
+  } x;
+};
+
+template <typename InT, bool GLA, int NW, bool PART, bool FULL, bool DIRECT>
 __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
   __shared__ float4 sCoef[NW][3][kMaxT][4];
-  __shared__ float sU[NW][kMaxT][kTile];   // u_t[d] of the wave's chunk
-  __shared__ float sG[NW][kMaxT][kTile];   // dy_t[d]
+  __shared__ BwdLds<NW, DIRECT> sx;
+  auto& sU = sx.x.U;
+  auto& sG = sx.x.G;
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ng = lane >> 4, dl = lane & 15;
   const int tiles = p.ND * p.NN, tile = blockIdx.x % tiles, grp = blockIdx.x / tiles;
@@ -409,10 +496,20 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
     const bool act = c < p.nC;
     stage_chunk<InT, GLA>(p, sCoef[w], b, h, c, act, nt, lane);
     float hst[4], lam[4];
+    // u and dy of columns dt*16 + lane % 16, steps lane / 16 + 4 j
+    const int dd = dt * kTile + (lane & 15);
+    float uvv[kStageIt], gyv[kStageIt];
+    auto stage_ug = [&]() {
+#pragma unroll
+      for (int j = 0; j < kStageIt; ++j) {
+        const int t = (lane >> 4) + 4 * j;
+        const bool ok = act && t < p.T && dd < p.DL;
+        sU[w][t][lane & 15] = ok ? uvv[j] : 0.f;
+        sG[w][t][lane & 15] = ok ? gyv[j] : 0.f;
+      }
+    };
     {
-      // u and dy of columns dt*16 + lane % 16, steps lane / 16 + 4 j
-      const int cc = act ? c : 0, dd = dt * kTile + (lane & 15), ddc = min(dd, p.DL - 1);
-      float uvv[kStageIt], gyv[kStageIt];
+      const int cc = act ? c : 0, ddc = min(dd, p.DL - 1);
 #pragma unroll
       for (int j = 0; j < kStageIt; ++j) {
         const int t = (lane >> 4) + 4 * j;
@@ -433,23 +530,44 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
                                   : 0;
         hst[k] = hsrc[i];
       }
-#pragma unroll
-      for (int j = 0; j < kStageIt; ++j) {
-        const int t = (lane >> 4) + 4 * j;
-        const bool ok = act && t < p.T && dd < p.DL;
-        sU[w][t][lane & 15] = ok ? uvv[j] : 0.f;
-        sG[w][t][lane & 15] = ok ? gyv[j] : 0.f;
-      }
+      if constexpr (!DIRECT) stage_ug();
 #pragma unroll
       for (int k = 0; k < 4; ++k) hst[k] = act && dok && has && nb + k < p.NS ? hst[k] : 0.f;
-      // the adjoint flowing into the chunk from the later ones (r1_compose_kernel)
-      const float* lsrc = p.lamws + ((bh * p.nC + cc) * p.DL + dc) * p.NS;
+      // the adjoint flowing into the chunk from the later ones (r1_compose_kernel;
+      // DIRECT: dfinal, the maps of chunks nC - 1 .. c + 1 applied below)
+      if constexpr (DIRECT) {
+        const float* fsrc = p.dfinal != nullptr ? p.dfinal : p.ckpt;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) lam[k] = lsrc[min(nb + k, p.NS - 1)];
+        for (int k = 0; k < 4; ++k)
+          lam[k] = fsrc[p.dfinal != nullptr ? sbase + state_idx<GLA>(dc, min(nb + k, p.NS - 1), p.DL, p.NS) : 0];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) lam[k] = act && dok && nb + k < p.NS ? lam[k] : 0.f;
+        for (int k = 0; k < 4; ++k) lam[k] = act && dok && p.dfinal != nullptr && nb + k < p.NS ? lam[k] : 0.f;
+        // maps grp * NW + 1 .. nC - 1
+        load_maps<NW>(p, sx.m, bh, d, nb, lane, w, grp * NW + 1, p.nC - 1 - grp * NW);
+      } else {
+        const float* lsrc = p.lamws + ((bh * p.nC + cc) * p.DL + dc) * p.NS;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) lam[k] = lsrc[min(nb + k, p.NS - 1)];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) lam[k] = act && dok && nb + k < p.NS ? lam[k] : 0.f;
+      }
     }
     __syncthreads();
+    if constexpr (DIRECT) {
+      // lam <- P_j lam + E_j over the later chunks, last first
+      for (int j = p.nC - 1; j > (act ? c : p.nC - 1); --j) {
+        const int jj = j - (grp * NW + 1);
+        float pj[4], ej[4];
+        unpack(sx.m.P[jj][ng], pj);
+        unpack(sx.m.E[jj][lane], ej);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) lam[k] = pj[k] * lam[k] + ej[k];
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) lam[k] = act && dok && nb + k < p.NS ? lam[k] : 0.f;
+      __syncthreads();   // every wave has read the maps: u and dy take their place
+      stage_ug();        // (a wave reads back only its own rows: no barrier after)
+    }
     // The chunk's states are recomputed from its checkpoint in two halves of
     // 16 steps (16 x 4 registers at a time): here the state after step 15,
     // below each half again from its entering state as the adjoint walks it.
@@ -532,6 +650,12 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
     };
     adjoint_half(std::integral_constant<int, kHalf>{}, hmid);
     adjoint_half(std::integral_constant<int, 0>{}, hst);
+    // DIRECT: chunk 0's wave ends with the adjoint of the initial state
+    if (DIRECT && c == 0 && p.dh0 != nullptr && dok) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (nb + k < p.NS) p.dh0[sbase + state_idx<GLA>(d, nb + k, p.DL, p.NS)] = lam[k];
+    }
   }
 }
 
@@ -729,11 +853,15 @@ int launch_fwd(Args<InT> a, const Plan& q, int64_t B, void* ws, hipStream_t s, f
   a.mapP = reinterpret_cast<float*>(static_cast<char*>(ws) + q.fwd_mapP);
   hipLaunchKernelGGL((r1_fold_kernel<InT, GLA, kChunkWaves, false>), cgrid, cblk, 0, s, a);
   if (int rc = rr::check_launch("scan forward chunk maps")) return rc;
-  hipLaunchKernelGGL((r1_compose_kernel<GLA, false>), grid, dim3(64), 0, s, a.mapE, a.mapP, a.h0, a.ckpt, nullptr,
-                     a.H, a.DL, a.NS, a.nC, a.NN);
-  if (int rc = rr::check_launch("scan forward states")) return rc;
-  if (q.T == kMaxT) hipLaunchKernelGGL((r1_out_kernel<InT, GLA, kChunkWaves, true>), cgrid, cblk, 0, s, a);
-  else hipLaunchKernelGGL((r1_out_kernel<InT, GLA, kChunkWaves, false>), cgrid, cblk, 0, s, a);
+  if (q.T == kMaxT && q.nC <= kDirectMaxChunks) {   // short heads: the maps composed in the replay kernel
+    hipLaunchKernelGGL((r1_out_kernel<InT, GLA, kChunkWaves, true, true>), cgrid, cblk, 0, s, a);
+  } else {
+    hipLaunchKernelGGL((r1_compose_kernel<GLA, false>), grid, dim3(64), 0, s, a.mapE, a.mapP, a.h0, a.ckpt, nullptr,
+                       a.H, a.DL, a.NS, a.nC, a.NN);
+    if (int rc = rr::check_launch("scan forward states")) return rc;
+    if (q.T == kMaxT) hipLaunchKernelGGL((r1_out_kernel<InT, GLA, kChunkWaves, true, false>), cgrid, cblk, 0, s, a);
+    else hipLaunchKernelGGL((r1_out_kernel<InT, GLA, kChunkWaves, false, false>), cgrid, cblk, 0, s, a);
+  }
   if (int rc = rr::check_launch("scan forward outputs")) return rc;
   if (q.NN > 1) {
     const int64_t n = q.rows * a.DL;
@@ -753,15 +881,20 @@ int launch_bwd(Args<InT> a, FinArgs<InT> f, const Plan& q, int64_t B, hipStream_
   const dim3 cgrid((unsigned)(q.ND * q.NN * q.groups), (unsigned)a.H, (unsigned)B), cblk(64 * kChunkWaves);
   hipLaunchKernelGGL((r1_fold_kernel<InT, GLA, kChunkWaves, true>), cgrid, cblk, 0, s, a);
   if (int rc = rr::check_launch("scan backward chunk maps")) return rc;
-  hipLaunchKernelGGL((r1_compose_kernel<GLA, true>), grid, dim3(64), 0, s, a.mapE, a.mapP, a.dfinal, a.lamws, a.dh0,
-                     a.H, a.DL, a.NS, a.nC, a.NN);
-  if (int rc = rr::check_launch("scan backward adjoints")) return rc;
-  if (q.T == kMaxT) {
-    if (q.NN > 1) hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kChunkWaves, true, true>), cgrid, cblk, 0, s, a);
-    else hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kChunkWaves, false, true>), cgrid, cblk, 0, s, a);
+  if (q.T == kMaxT && q.nC <= kDirectMaxChunks) {   // short heads: the maps composed in the replay kernel
+    if (q.NN > 1) hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kChunkWaves, true, true, true>), cgrid, cblk, 0, s, a);
+    else hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kChunkWaves, false, true, true>), cgrid, cblk, 0, s, a);
   } else {
-    if (q.NN > 1) hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kChunkWaves, true, false>), cgrid, cblk, 0, s, a);
-    else hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kChunkWaves, false, false>), cgrid, cblk, 0, s, a);
+    hipLaunchKernelGGL((r1_compose_kernel<GLA, true>), grid, dim3(64), 0, s, a.mapE, a.mapP, a.dfinal, a.lamws,
+                       a.dh0, a.H, a.DL, a.NS, a.nC, a.NN);
+    if (int rc = rr::check_launch("scan backward adjoints")) return rc;
+    if (q.T == kMaxT) {
+      if (q.NN > 1) hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kChunkWaves, true, true, false>), cgrid, cblk, 0, s, a);
+      else hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kChunkWaves, false, true, false>), cgrid, cblk, 0, s, a);
+    } else {
+      if (q.NN > 1) hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kChunkWaves, true, false, false>), cgrid, cblk, 0, s, a);
+      else hipLaunchKernelGGL((r1_bwd_kernel<InT, GLA, kChunkWaves, false, false, false>), cgrid, cblk, 0, s, a);
+    }
   }
   if (int rc = rr::check_launch("scan backward")) return rc;
   const dim3 fgrid((unsigned)q.nblk, (unsigned)a.H);
