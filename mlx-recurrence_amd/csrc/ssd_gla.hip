@@ -101,6 +101,7 @@ struct Args {
   float* mapE;          // chunk maps x -> P x + E (workspace): E [B,H,nC,DL,NS]
   float* mapP;          //   P [B,H,nC,NS]
   int L, H, DL, NS, T, nC, ND, NN;
+  int Bsz;              // batch rows
   int64_t rows;         // B*L*H
 };
 
@@ -178,9 +179,10 @@ __global__ __launch_bounds__(64 * NW) void r1_fold_kernel(Args<InT> p) {
   __shared__ float4 sCoef[NW][3][kMaxT][4];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ng = lane >> 4, dl = lane & 15;
-  const int tiles = p.ND * p.NN, tile = blockIdx.x % tiles, grp = blockIdx.x / tiles;
+  const TileUnit tu = tile_unit<NW>(p);
+  if (!tu.valid) return;
+  const int tile = tu.tile, grp = tu.grp, h = tu.h, b = tu.b;
   const int dt = tile / p.NN, nt = tile % p.NN;
-  const int h = blockIdx.y, b = blockIdx.z;
   const int d = dt * kTile + dl;
   const bool dok = d < p.DL;
   const int nb = nt * kTile + ng * 4;
@@ -315,6 +317,27 @@ __global__ __launch_bounds__(64) void r1_compose_kernel(const float* __restrict_
 
 // Grid of the chunk-parallel kernels: x = tile + (ND * NN) * group, where
 // group g holds chunks NW g .. NW g + NW - 1 (one per wave).
+// Workgroup of a chunk-parallel kernel (fold, replay): a 1-D grid over the
+// units u = (b * H + h) * groups + g (chunk group g: NW chunks) times the
+// ND * NN state tiles, decoded so that every tile of a unit runs on the same
+// XCD (the GPU hands workgroups to its 8 XCDs round-robin by linear index):
+// the tiles of a unit read the same step inputs, B and C rows, which one L2
+// then holds once.
+struct TileUnit {
+  int tile, grp, h, b;
+  bool valid;   // false for the padding workgroups of the last unit group
+};
+template <int NW, typename InT>
+__device__ __forceinline__ TileUnit tile_unit(const Args<InT>& p) {
+  const int id = blockIdx.x, x = id % 8, rest = id / 8, tiles = p.ND * p.NN;
+  const int groups = (p.nC + NW - 1) / NW;
+  const int u = (rest / tiles) * 8 + x, bh = u / groups;
+  return TileUnit{rest % tiles, u % groups, bh % p.H, bh / p.H, (int64_t)bh < (int64_t)p.Bsz * p.H};
+}
+inline int64_t tile_grid(int64_t B, int64_t H, int64_t groups, int64_t tiles) {
+  return (B * H * groups + 7) / 8 * 8 * tiles;
+}
+
 // Short heads (nC <= kDirectMaxChunks): the replay kernels compose the chunk
 // maps themselves instead of reading the compose kernel's output.  The
 // workgroup loads the maps of chunks j0 .. j0 + cnt - 1 of its tile into LDS
@@ -365,9 +388,10 @@ __global__ __launch_bounds__(64 * NW) void r1_out_kernel(Args<InT> p) {
   __shared__ MaybeMaps<DIRECT> sMap;
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ng = lane >> 4, dl = lane & 15;
-  const int tiles = p.ND * p.NN, tile = blockIdx.x % tiles, grp = blockIdx.x / tiles;
+  const TileUnit tu = tile_unit<NW>(p);
+  if (!tu.valid) return;
+  const int tile = tu.tile, grp = tu.grp, h = tu.h, b = tu.b;
   const int dt = tile / p.NN, nt = tile % p.NN;
-  const int h = blockIdx.y, b = blockIdx.z;
   const int d = dt * kTile + dl;
   const bool dok = d < p.DL;
   const int nb = nt * kTile + ng * 4;
@@ -481,9 +505,10 @@ __global__ __launch_bounds__(64 * NW) void r1_bwd_kernel(Args<InT> p) {
   auto& sG = sx.x.G;
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ng = lane >> 4, dl = lane & 15;
-  const int tiles = p.ND * p.NN, tile = blockIdx.x % tiles, grp = blockIdx.x / tiles;
+  const TileUnit tu = tile_unit<NW>(p);
+  if (!tu.valid) return;
+  const int tile = tu.tile, grp = tu.grp, h = tu.h, b = tu.b;
   const int dt = tile / p.NN, nt = tile % p.NN;
-  const int h = blockIdx.y, b = blockIdx.z;
   const int d = dt * kTile + dl;
   const bool dok = d < p.DL;
   const int nb = nt * kTile + ng * 4;
@@ -845,10 +870,10 @@ int check_dims(const char* who, int64_t B, int64_t L, int64_t H, int64_t DL, int
 
 template <typename InT, bool GLA>
 int launch_fwd(Args<InT> a, const Plan& q, int64_t B, void* ws, hipStream_t s, float* y) {
-  if (q.ND * q.NN * q.groups >= ((int64_t)1 << 31))
+  if (tile_grid(B, a.H, q.groups, q.ND * q.NN) >= ((int64_t)1 << 31))
     return rr::fail(RR_EUNSUPPORTED, "scan: too many (tile, chunk group) workgroups");
   const dim3 grid((unsigned)(q.ND * q.NN), (unsigned)a.H, (unsigned)B);
-  const dim3 cgrid((unsigned)(q.ND * q.NN * q.groups), (unsigned)a.H, (unsigned)B), cblk(64 * kChunkWaves);
+  const dim3 cgrid((unsigned)tile_grid(B, a.H, q.groups, q.ND * q.NN)), cblk(64 * kChunkWaves);
   a.mapE = reinterpret_cast<float*>(static_cast<char*>(ws) + q.fwd_mapE);
   a.mapP = reinterpret_cast<float*>(static_cast<char*>(ws) + q.fwd_mapP);
   hipLaunchKernelGGL((r1_fold_kernel<InT, GLA, kChunkWaves, false>), cgrid, cblk, 0, s, a);
@@ -875,10 +900,10 @@ int launch_fwd(Args<InT> a, const Plan& q, int64_t B, void* ws, hipStream_t s, f
 template <typename InT, bool GLA>
 int launch_bwd(Args<InT> a, FinArgs<InT> f, const Plan& q, int64_t B, hipStream_t s,
                float* dA, int dA_sn) {
-  if (q.ND * q.NN * q.groups >= ((int64_t)1 << 31))
+  if (tile_grid(B, a.H, q.groups, q.ND * q.NN) >= ((int64_t)1 << 31))
     return rr::fail(RR_EUNSUPPORTED, "scan: too many (tile, chunk group) workgroups");
   const dim3 grid((unsigned)(q.ND * q.NN), (unsigned)a.H, (unsigned)B);
-  const dim3 cgrid((unsigned)(q.ND * q.NN * q.groups), (unsigned)a.H, (unsigned)B), cblk(64 * kChunkWaves);
+  const dim3 cgrid((unsigned)tile_grid(B, a.H, q.groups, q.ND * q.NN)), cblk(64 * kChunkWaves);
   hipLaunchKernelGGL((r1_fold_kernel<InT, GLA, kChunkWaves, true>), cgrid, cblk, 0, s, a);
   if (int rc = rr::check_launch("scan backward chunk maps")) return rc;
   if (q.T == kMaxT && q.nC <= kDirectMaxChunks) {   // short heads: the maps composed in the replay kernel
@@ -984,6 +1009,7 @@ extern "C" int rr_ssd_fwd(const void* u, const void* delta, const void* Bm, cons
     a.y = q.NN > 1 ? static_cast<float*>(workspace) : y;
     a.ckpt = ckpt;
     a.L = (int)L; a.H = (int)H; a.DL = (int)Dh; a.NS = (int)N; a.T = (int)q.T;
+    a.Bsz = (int)B;
     a.nC = (int)q.nC; a.ND = (int)q.ND; a.NN = (int)q.NN; a.rows = q.rows;
     return launch_fwd<InT, false>(a, q, B, workspace, s, y);
   });
@@ -1061,6 +1087,7 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
     a.mapP = reinterpret_cast<float*>(ws + q.bwd_mapP);
     a.dh0 = dh0;
     a.L = (int)L; a.H = (int)H; a.DL = (int)Dh; a.NS = (int)N; a.T = (int)q.T;
+    a.Bsz = (int)B;
     a.nC = (int)q.nC; a.ND = (int)q.ND; a.NN = (int)q.NN; a.rows = q.rows;
     FinArgs<InT> f{};
     f.g3 = a.g3;
@@ -1195,6 +1222,7 @@ extern "C" int rr_gla_fwd(const void* qp, const void* kp, const void* vp, const 
     a.y = q.NN > 1 ? static_cast<float*>(workspace) : y;
     a.ckpt = ckpt;
     a.L = (int)L; a.H = (int)H; a.DL = (int)Dh; a.NS = (int)Dh; a.T = (int)q.T;
+    a.Bsz = (int)B;
     a.nC = (int)q.nC; a.ND = (int)q.ND; a.NN = (int)q.NN; a.rows = q.rows;
     return launch_fwd<InT, true>(a, q, B, workspace, s, y);
   });
@@ -1248,6 +1276,7 @@ extern "C" int rr_gla_bwd(const float* dy, const float* dfinal, const void* qp, 
     a.mapP = reinterpret_cast<float*>(ws + q.bwd_mapP);
     a.dh0 = dh0;
     a.L = (int)L; a.H = (int)H; a.DL = (int)Dh; a.NS = (int)Dh; a.T = (int)q.T;
+    a.Bsz = (int)B;
     a.nC = (int)q.nC; a.ND = (int)q.ND; a.NN = (int)q.NN; a.rows = q.rows;
     FinArgs<InT> f{};
     f.g3 = a.g3;
