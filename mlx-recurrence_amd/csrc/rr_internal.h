@@ -107,6 +107,44 @@ int gdn_chunk_grad(const float* dy, const void* q, const void* k, const void* v,
                    const float* h0, const float* ckpt, const float* adjck, void* dq, void* dk, void* dv, void* dalpha,
                    void* dbeta, int64_t B, int64_t L, int64_t H, hipStream_t s);
 
+// ------------------------------------------------------------------ SSD, rate per (head, n)
+// Chunked SSD for A_neg [H, N] (any input dtype) and for fp32 / fp16 inputs
+// with a per-head rate (ssd_dense.hip): one workgroup per 32-step chunk,
+// contractions on the fp32 MFMA.  It writes every chunk's map (mapE
+// [B,H,nC,Dh,N], mapP [B,H,nC,N]), and ssd_dense_compose walks them into ckpt
+// (forward) and lamws (backward).
+struct DenseArgs {
+  const void* u;           // [B,L,H,Dh] of the input dtype
+  const void* delta;       // [B,L,H]
+  const void* Bm;          // [B,L,H,N]
+  const void* Cm;          // [B,L,H,N]
+  const float* A;          // A[h * a_sh + n * a_sn]
+  int64_t a_sh, a_sn;
+  const float* h0;         // [B,H,Dh,N] or null
+  const float* ckpt;       // [B,H,nC,Dh,N]: the state after each chunk
+  const float* lamws;      // [B,H,nC,Dh,N]: the adjoint flowing into each chunk's end
+  const float* dy;         // [B,L,H,Dh]
+  float* y;                // [B,L,H,Dh]
+  void* du;                // gradients, of the input dtype
+  void* ddelta;
+  void* dB;
+  void* dC;
+  float* gA_part;          // [H][B * nC][N]: dA of each chunk
+  float* mapE;
+  float* mapP;
+  int B, L, H, DH, NS, nC;
+};
+enum DenseKernel { kDenseMapsFwd = 0, kDenseMapsBwd = 1, kDenseOut = 2, kDenseGrad = 3 };
+// True when the chunk kernels cover the call: checkpoint interval T = 32,
+// Dh in {32, 64}, N in {16, 32}, and a 1-D grid of one workgroup per chunk.
+bool ssd_dense_supported(int64_t T, int64_t Dh, int64_t N, int64_t B, int64_t H, int64_t nC);
+int ssd_dense_launch(const DenseArgs& a, int dtype, int what, hipStream_t s);
+// The walk over the chunk maps: forward x0 = h0, out = ckpt (the state after
+// each chunk); backward x0 = dfinal, out = lamws (the adjoint flowing into
+// each chunk's end), xlast = dh0.  x0 and xlast may be null.
+int ssd_dense_compose(const float* mapE, const float* mapP, const float* x0, float* out, float* xlast, int64_t B,
+                      int64_t H, int64_t Dh, int64_t N, int64_t nC, bool bwd, hipStream_t s);
+
 // Backward of the chunked kernels with column-owned state blocks (GLA: Dh in
 // {32, 64, 128}; SSD: Dh in {32, 64, 128}, N in {64, 128}; chunked_bwd.hip).  SSD
 // leaves per-run dA partials in p.ws for the caller's reduction.

@@ -1,0 +1,580 @@
+// ssd_dense.hip — SSD with a decay rate per (head, state column n) — the
+// reference's own A_neg [H, N] — in chunked form, contractions on the fp32
+// MFMA, for chunks of 32 steps.  Also taken by fp32 / fp16
+// inputs with a per-head rate (the chunked kernels of rr_chunked.h take bf16
+// only).
+//
+// Per chunk of one (batch, head), steps t, s < 32, cd = in-chunk cumulative
+// delta, E[t,n] = exp(A_n cd_t), m31[s,n] = exp(A_n (cd_31 - cd_s)) and
+// M_n[t,s] = exp(A_n (cd_t - cd_s)) for t >= s (0 else) — the matrix form of
+// the reference's per-step recurrence and adjoint (ssd.py:85-111, 203-268):
+//   chunk map, forward:  S  = U^T diag(delta) (m31 o B); the state after the
+//                        chunk is E_31 o h_in + S
+//   chunk map, backward: S' = dY^T (E o C); the adjoint handed to the chunk
+//                        before is E_31 o lam + S'
+//   Y   = (W o delta_s) U + (C o E) h_in^T,   W[t,s] = sum_n C_t[n] B_s[n] M_n[t,s]
+//   du  = diag(delta) (W^T dY + (B o m31) lam^T)
+//   with G2 = dY U^T, GH = dY h_in, UL = U lam, F_n[t,s] = M_n[t,s] G2[t,s]:
+//   ZF[s,n]  = sum_t F_n[t,s] C_t[n];          Z = ZF + m31 o UL;  dB = diag(delta) Z
+//   dC2[t,n] = sum_s F_n[t,s] delta_s B_s[n];  dC = E o GH + dC2
+//   D[t,n]   = sum_{t'>=t} (E C GH)[t',n] + R[t,n] + E_31[n] tr[n] + sum_{s<t} (m31 delta B UL)[s,n],
+//     R[t,n] = sum_{tau>=t} (C dC2 - delta B ZF)[tau,n]  (the dominance sum
+//              sum_{t'>=t>s} F_n[t',s] delta_s B_s[n] C_t'[n], telescoped), tr = sum_d lam o h_in
+//   d(delta)_t = sum_n (A_n D[t,n] + B_t[n] Z[t,n])
+//   dA[n]    = sum_t delta_t D[t,n], summed here with each term's weight formed
+//              exactly:  sum_t (E C GH)[t,n] cd_t + cd_31 E_31[n] tr[n]
+//              + sum_s (m31 delta B UL)[s,n] (cd_31 - cd_s) + sum_s delta_s B_s[n] ZW[s,n],
+//     ZW[s,n] = sum_t F_n[t,s] C_t[n] (cd_t - cd_s).  (The suffix sum R cancels
+//     to R[0] = 0 from O(1) terms; summed over t for dA that cancellation would
+//     cost ~1e-5 of dA's scale in fp32, the weighted form none.)
+// where h_in is the state entering the chunk and lam the adjoint flowing into
+// its end from the later chunks, both from dense_compose_kernel's walk over
+// the chunk maps.  D[t,n] is dec_t[n] sum_d lam_t h_{t-1}, the
+// quantity both d(delta) and dA need, formed without dividing by a decay.
+// (Derived from the per-step adjoint and checked in float64 against the oracle
+// before this code; the GPU parity tests check it against the oracle.)
+//
+// Work split: a workgroup of four waves per chunk, in three kernels per pass
+// (chunk maps; the walk over them, one thread per state element; every
+// chunk's outputs or gradients).  Each workgroup issues all of its global
+// loads before it writes any of them to LDS (one memory latency per chunk, not
+// one per staged row).  The inputs and the
+// intermediates live in LDS as fp32, and the contractions run on the fp32 MFMA
+// (fp32 products and sums: fp32 inputs keep fp32 accuracy, where a bf16 hi + lo
+// operand split would leave ~2^-18 per product).  The per-n masked sums W, ZF and dC2
+// run on the VALU, one thread per output element, with the decay of each
+// (t, s, n) formed by its own exponential (exact for any rate and step size:
+// no rescaled factors that could overflow).
+#include "rr_common.h"
+#include "rr_internal.h"
+#include "rr_mfma.h"
+
+namespace {
+
+using rr::f32x4_t;
+
+constexpr int Q = 32;   // chunk length (steps)
+
+template <typename InT>
+struct DenseArgsT {
+  const InT* u;
+  const InT* delta;
+  const InT* Bm;
+  const InT* Cm;
+  const float* A;
+  int64_t a_sh, a_sn;      // A[h * a_sh + n * a_sn]
+  const float* h0;         // [B,H,Dh,N] or null
+  const float* ckpt;       // [B,H,nC,Dh,N]: the state after each chunk
+  const float* lamws;      // [B,H,nC,Dh,N]: the adjoint flowing into each chunk's end
+  const float* dy;         // [B,L,H,Dh]
+  float* y;
+  InT* du;
+  InT* ddelta;
+  InT* dB;
+  InT* dC;
+  float* gA_part;          // [H][B * nC][N]: dA of each chunk
+  float* mapE;             // [B,H,nC,Dh,N]
+  float* mapP;             // [B,H,nC,N]
+  int B, L, H, DH, NS, nC;
+};
+
+// acc += A . B over K (a multiple of 4) for the 16 x 16 output block whose
+// lane holds column lane % 16 of rows 4 (lane / 16) + r, on the fp32 MFMA
+// v_mfma_f32_16x16x4_f32 (A[row = lane % 16][k = lane / 16],
+// B[k = lane / 16][col = lane % 16]): products and sums in fp32, no operand
+// splitting.  fa(row, k) and fb(k, col) read the operands (rows and columns
+// relative to the block).
+template <int K, class FA, class FB>
+__device__ __forceinline__ f32x4_t mm16(FA fa, FB fb, int lane, f32x4_t acc) {
+  const int r = lane & 15, kq = lane >> 4;
+#pragma unroll
+  for (int k0 = 0; k0 < K; k0 += 4) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(fa(r, k0 + kq), fb(k0 + kq, r), acc, 0, 0, 0);
+  return acc;
+}
+
+// exp(x) where keep, else 0 (formed in every lane, then selected: no branch,
+// and an overflowing exponential of a masked element is dropped, not multiplied).
+__device__ __forceinline__ float kept_exp(bool keep, float x) {
+  const float e = __expf(x);
+  return keep ? e : 0.f;
+}
+
+// Chunk (b, h, c) of workgroup blockIdx.x = (b * H + h) * nC + c.
+struct ChunkPos {
+  int b, h, c;
+  int64_t bh, row0;   // b * H + h; first (b, t) row of the chunk
+};
+template <typename InT>
+__device__ __forceinline__ ChunkPos chunk_pos(const DenseArgsT<InT>& p) {
+  const int id = blockIdx.x, c = id % p.nC, bh = id / p.nC;
+  return ChunkPos{bh / p.H, bh % p.H, c, (int64_t)bh, (int64_t)(bh / p.H) * p.L + (int64_t)c * Q};
+}
+
+// A [ROWS][W] fp32 slab staged through registers: load() issues one global
+// load per element (row r at src + r * stride, element w at + w; every
+// thread takes elements tid, tid + 256, ...), store() writes them to LDS.  A
+// kernel calls every load() before the first store(), so all of its loads are
+// in flight at once.
+template <int ROWS, int W>
+struct Slab {
+  static constexpr int N = ROWS * W / 256;
+  static_assert(ROWS * W % 256 == 0, "slab must split evenly over 256 threads");
+  float v[N];
+  template <typename T>
+  __device__ __forceinline__ void load(const T* src, int64_t stride, int tid) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int i = tid + 256 * j;
+      v[j] = rr::ld(src, (int64_t)(i / W) * stride + i % W);
+    }
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = 0.f;
+  }
+  template <int P>
+  __device__ __forceinline__ void store(float (&dst)[ROWS][P], int tid) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int i = tid + 256 * j;
+      dst[i / W][i % W] = v[j];
+    }
+  }
+};
+
+// Step scalars of the chunk: delta (thread t < 32) and the rates (thread
+// n < NS) are loaded by the caller with the other inputs; this writes them to
+// LDS, forms cd (wave 0's prefix sum), then E[t,n] and / or m31[t,n].
+template <int NS, int PN, bool WANT_E, bool WANT_M31>
+__device__ __forceinline__ void step_scalars(float dv, float av, float* del, float* cd, float* a, float (*E)[PN],
+                                             float (*m31)[PN], int tid) {
+  if (tid < Q) del[tid] = dv;
+  if (tid < NS) a[tid] = av;
+  if (tid < 64) {   // wave 0
+    const float c = rr::prefix32_sum(tid < Q ? dv : 0.f);
+    if (tid < Q) cd[tid] = c;
+  }
+  __syncthreads();
+  const float c31 = cd[Q - 1];
+#pragma unroll
+  for (int j = 0; j < Q * NS / 256; ++j) {
+    const int i = tid + 256 * j, t = i / NS, n = i % NS;
+    const float an = a[n], ct = cd[t];
+    if constexpr (WANT_E) E[t][n] = __expf(an * ct);
+    if constexpr (WANT_M31) m31[t][n] = __expf(an * (c31 - ct));
+  }
+}
+
+// The chunk's delta (thread t < 32) and rate (thread n < NS), loaded with the
+// slabs.
+template <int NS, typename InT>
+__device__ __forceinline__ void load_step(const DenseArgsT<InT>& p, const ChunkPos& cp, int tid, float& dv, float& av) {
+  dv = rr::ld(p.delta, (cp.row0 + (tid & (Q - 1))) * p.H + cp.h);
+  av = p.A[(int64_t)cp.h * p.a_sh + (int64_t)(tid & (NS - 1)) * p.a_sn];
+}
+
+// W[t,s] = sum_n C_t[n] B_s[n] M_n[t,s] (t >= s; 0 else): one thread per (t, s).
+template <int NS, int PN, int PQ>
+__device__ __forceinline__ void form_w(float (*W)[PQ], const float (*Cm)[PN], const float (*Bm)[PN], const float* cd,
+                                       const float* a, int tid) {
+#pragma unroll
+  for (int j = 0; j < Q * Q / 256; ++j) {
+    const int i = tid + 256 * j, t = i / Q, s = i % Q;
+    const bool keep = t >= s;
+    const float dc = cd[t] - cd[s];
+    float w = 0.f;
+#pragma unroll
+    for (int n = 0; n < NS; ++n) w += Cm[t][n] * Bm[s][n] * kept_exp(keep, a[n] * dc);
+    W[t][s] = w;
+  }
+}
+
+// ------------------------------------------------------------------ chunk maps
+// Forward: S[d][n] = sum_s u_s[d] delta_s m31[s,n] B_s[n]; backward:
+// S'[d][n] = sum_t dY_t[d] E[t,n] C_t[n]; P[n] = E[31, n].  (The layout
+// dense_compose_kernel walks.)
+template <int DH, int NS>
+struct alignas(16) MapSmem {
+  static constexpr int PD = DH + 4, PN = NS + 4;
+  float X[Q][PD];    // u (forward) or dY (backward) [t][d]
+  float V[Q][PN];    // B (forward) or C (backward)
+  float F[Q][PN];    // m31 (forward) or E (backward)
+  float del[Q], cd[Q], a[NS];
+};
+
+template <typename InT, int DH, int NS, bool BWD>
+__global__ __launch_bounds__(256) void dense_map_kernel(DenseArgsT<InT> p) {
+  using S = MapSmem<DH, NS>;
+  __shared__ S sm;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const ChunkPos cp = chunk_pos(p);
+  const int64_t xoff = (cp.row0 * p.H + cp.h) * DH, voff = (cp.row0 * p.H + cp.h) * NS;
+  Slab<Q, DH> X;
+  Slab<Q, NS> V;
+  float dv, av;
+  if constexpr (BWD) {
+    X.load(p.dy + xoff, (int64_t)p.H * DH, tid);
+    V.load(p.Cm + voff, (int64_t)p.H * NS, tid);
+  } else {
+    X.load(p.u + xoff, (int64_t)p.H * DH, tid);
+    V.load(p.Bm + voff, (int64_t)p.H * NS, tid);
+  }
+  load_step<NS>(p, cp, tid, dv, av);
+  X.store(sm.X, tid);
+  V.store(sm.V, tid);
+  if constexpr (BWD) step_scalars<NS, S::PN, true, false>(dv, av, sm.del, sm.cd, sm.a, sm.F, nullptr, tid);
+  else step_scalars<NS, S::PN, false, true>(dv, av, sm.del, sm.cd, sm.a, nullptr, sm.F, tid);
+  __syncthreads();
+  constexpr int NBD = DH / 16, NBN = NS / 16;
+  float* dst = p.mapE + ((cp.bh * p.nC + cp.c) * DH) * NS;
+  for (int blk = w; blk < NBD * NBN; blk += 4) {
+    const int d0 = 16 * (blk / NBN), n0 = 16 * (blk % NBN);
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (BWD) {
+      acc = mm16<Q>([&](int r, int k) { return sm.X[k][d0 + r]; },
+                    [&](int k, int c) { return sm.F[k][n0 + c] * sm.V[k][n0 + c]; }, lane, acc);
+    } else {
+      acc = mm16<Q>([&](int r, int k) { return sm.X[k][d0 + r]; },
+                    [&](int k, int c) { return sm.del[k] * sm.F[k][n0 + c] * sm.V[k][n0 + c]; }, lane, acc);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dst[(d0 + 4 * (lane >> 4) + r) * NS + n0 + (lane & 15)] = acc[r];
+  }
+  if (tid < NS) p.mapP[(cp.bh * p.nC + cp.c) * NS + tid] = __expf(sm.a[tid] * sm.cd[Q - 1]);
+}
+
+// ------------------------------------------------------------------ the walk over chunks
+// One thread per state element (b, h, d, n): x_c = P_c x_{c-1} + E_c over the
+// chunks (forward from h0, in order, writing the state after each chunk;
+// backward from dfinal, in reverse, writing the adjoint flowing into each
+// chunk before its own map, and dh0 at the end).  The maps of kWalkBatch
+// chunks are loaded at once.
+constexpr int kWalkBatch = 16;
+template <bool BWD>
+__global__ __launch_bounds__(256) void dense_compose_kernel(const float* __restrict__ mapE,
+                                                            const float* __restrict__ mapP,
+                                                            const float* __restrict__ x0, float* __restrict__ out,
+                                                            float* __restrict__ xlast, int64_t total, int DN, int NS,
+                                                            int nC) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int64_t bh = i / DN;
+  const int e = (int)(i % DN), n = e % NS;
+  float x = x0 != nullptr ? x0[i] : 0.f;
+  for (int i0 = 0; i0 < nC; i0 += kWalkBatch) {
+    float ev[kWalkBatch], pv[kWalkBatch];
+#pragma unroll
+    for (int q = 0; q < kWalkBatch; ++q) {
+      const int k = min(i0 + q, nC - 1), c = BWD ? nC - 1 - k : k;
+      ev[q] = mapE[(bh * nC + c) * DN + e];
+      pv[q] = mapP[(bh * nC + c) * NS + n];
+    }
+#pragma unroll
+    for (int q = 0; q < kWalkBatch; ++q) {
+      const int k = i0 + q, c = BWD ? nC - 1 - k : k;
+      if (k < nC) {
+        if (BWD) out[(bh * nC + c) * DN + e] = x;
+        x = pv[q] * x + ev[q];
+        if (!BWD) out[(bh * nC + c) * DN + e] = x;
+      }
+    }
+  }
+  if (xlast != nullptr) xlast[i] = x;
+}
+
+// ------------------------------------------------------------------ forward y
+template <int DH, int NS>
+struct alignas(16) OutSmem {
+  static constexpr int PD = DH + 4, PN = NS + 4, PQ = Q + 4;
+  float U[Q][PD];
+  float Bm[Q][PN], Cm[Q][PN], E[Q][PN];
+  float hin[DH][PN];
+  float W[Q][PQ];
+  float del[Q], cd[Q], a[NS];
+};
+
+template <typename InT, int DH, int NS>
+__global__ __launch_bounds__(256) void dense_out_kernel(DenseArgsT<InT> p) {
+  using S = OutSmem<DH, NS>;
+  __shared__ S sm;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const ChunkPos cp = chunk_pos(p);
+  const int64_t xoff = (cp.row0 * p.H + cp.h) * DH, voff = (cp.row0 * p.H + cp.h) * NS;
+  Slab<Q, DH> U;
+  Slab<Q, NS> Bv, Cv;
+  Slab<DH, NS> Hs;   // the state entering the chunk: checkpoint c - 1, h0 or zero
+  float dv, av;
+  U.load(p.u + xoff, (int64_t)p.H * DH, tid);
+  Bv.load(p.Bm + voff, (int64_t)p.H * NS, tid);
+  Cv.load(p.Cm + voff, (int64_t)p.H * NS, tid);
+  if (cp.c > 0) Hs.load(p.ckpt + (cp.bh * p.nC + cp.c - 1) * DH * NS, NS, tid);
+  else if (p.h0 != nullptr) Hs.load(p.h0 + cp.bh * DH * NS, NS, tid);
+  else Hs.zero();
+  load_step<NS>(p, cp, tid, dv, av);
+  U.store(sm.U, tid);
+  Bv.store(sm.Bm, tid);
+  Cv.store(sm.Cm, tid);
+  Hs.store(sm.hin, tid);
+  step_scalars<NS, S::PN, true, false>(dv, av, sm.del, sm.cd, sm.a, sm.E, nullptr, tid);
+  __syncthreads();
+  form_w<NS, S::PN, S::PQ>(sm.W, sm.Cm, sm.Bm, sm.cd, sm.a, tid);
+  __syncthreads();
+  // Y [t][d] = sum_s W[t][s] delta_s U[s][d] + sum_n C[t][n] E[t][n] hin[d][n]
+  constexpr int NBD = DH / 16;
+  for (int blk = w; blk < 2 * NBD; blk += 4) {
+    const int t0 = 16 * (blk / NBD), d0 = 16 * (blk % NBD);
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    acc = mm16<Q>([&](int r, int k) { return sm.W[t0 + r][k] * sm.del[k]; },
+                  [&](int k, int c) { return sm.U[k][d0 + c]; }, lane, acc);
+    acc = mm16<NS>([&](int r, int k) { return sm.Cm[t0 + r][k] * sm.E[t0 + r][k]; },
+                   [&](int k, int c) { return sm.hin[d0 + c][k]; }, lane, acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = t0 + 4 * (lane >> 4) + r;
+      p.y[((cp.row0 + t) * p.H + cp.h) * DH + d0 + (lane & 15)] = acc[r];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ backward
+template <int DH, int NS>
+struct alignas(16) GradSmem {
+  static constexpr int PD = DH + 4, PN = NS + 4, PQ = Q + 4;
+  float U[Q][PD];       // u [s][d]
+  float G[Q][PD];       // dY [t][d]
+  float Bm[Q][PN], Cm[Q][PN];
+  float E[Q][PN], m31[Q][PN];
+  float hin[DH][PN], lam[DH][PN];
+  float G2[Q][PQ];      // dY U^T [t][s]
+  float W[Q][PQ];       // W [t][s]
+  float GH[Q][PN], UL[Q][PN], ZF[Q][PN], ZW[Q][PN], dC2[Q][PN];
+  float del[Q], cd[Q], a[NS], trp[256 / NS][NS], tr[NS];
+  float ddp[4][2][Q];   // per-(wave, half) partials of d(delta)
+};
+
+template <typename InT, int DH, int NS>
+__global__ __launch_bounds__(256) void dense_grad_kernel(DenseArgsT<InT> p) {
+  using S = GradSmem<DH, NS>;
+  __shared__ S sm;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const ChunkPos cp = chunk_pos(p);
+  // ---- A: inputs, the entering state and the adjoint flowing in
+  {
+    const int64_t xoff = (cp.row0 * p.H + cp.h) * DH, voff = (cp.row0 * p.H + cp.h) * NS;
+    Slab<Q, DH> U, G;
+    Slab<Q, NS> Bv, Cv;
+    Slab<DH, NS> Hs, Ls;
+    float dv, av;
+    U.load(p.u + xoff, (int64_t)p.H * DH, tid);
+    G.load(p.dy + xoff, (int64_t)p.H * DH, tid);
+    Bv.load(p.Bm + voff, (int64_t)p.H * NS, tid);
+    Cv.load(p.Cm + voff, (int64_t)p.H * NS, tid);
+    if (cp.c > 0) Hs.load(p.ckpt + (cp.bh * p.nC + cp.c - 1) * DH * NS, NS, tid);
+    else if (p.h0 != nullptr) Hs.load(p.h0 + cp.bh * DH * NS, NS, tid);
+    else Hs.zero();
+    Ls.load(p.lamws + (cp.bh * p.nC + cp.c) * DH * NS, NS, tid);
+    load_step<NS>(p, cp, tid, dv, av);
+    U.store(sm.U, tid);
+    G.store(sm.G, tid);
+    Bv.store(sm.Bm, tid);
+    Cv.store(sm.Cm, tid);
+    Hs.store(sm.hin, tid);
+    Ls.store(sm.lam, tid);
+    step_scalars<NS, S::PN, true, true>(dv, av, sm.del, sm.cd, sm.a, sm.E, sm.m31, tid);
+  }
+  __syncthreads();
+  // ---- B1: G2 = dY U^T, GH = dY h_in, UL = U lam (MFMA); tr partials; W
+  {
+    // wave w: G2 block (w / 2, w % 2)
+    const int t0 = 16 * (w >> 1), s0 = 16 * (w & 1);
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    acc = mm16<DH>([&](int r, int k) { return sm.G[t0 + r][k]; }, [&](int k, int c) { return sm.U[s0 + c][k]; },
+                   lane, acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm.G2[t0 + 4 * (lane >> 4) + r][s0 + (lane & 15)] = acc[r];
+  }
+  constexpr int NBN = NS / 16;
+  for (int blk = w; blk < 2 * 2 * NBN; blk += 4) {   // (kind, t-block, n-block)
+    const int kind = blk / (2 * NBN), t0 = 16 * ((blk / NBN) & 1), n0 = 16 * (blk % NBN);
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    if (kind == 0) {
+      acc = mm16<DH>([&](int r, int k) { return sm.G[t0 + r][k]; },
+                     [&](int k, int c) { return sm.hin[k][n0 + c]; }, lane, acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sm.GH[t0 + 4 * (lane >> 4) + r][n0 + (lane & 15)] = acc[r];
+    } else {
+      acc = mm16<DH>([&](int r, int k) { return sm.U[t0 + r][k]; },
+                     [&](int k, int c) { return sm.lam[k][n0 + c]; }, lane, acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sm.UL[t0 + 4 * (lane >> 4) + r][n0 + (lane & 15)] = acc[r];
+    }
+  }
+  {
+    // tr[n] = sum_d lam o h_in: thread (part, n) sums d = part, part + P, ...
+    constexpr int P = 256 / NS;
+    const int n = tid % NS, part = tid / NS;
+    float s = 0.f;
+#pragma unroll
+    for (int d = part; d < DH; d += P) s += sm.lam[d][n] * sm.hin[d][n];
+    sm.trp[part][n] = s;
+  }
+  form_w<NS, S::PN, S::PQ>(sm.W, sm.Cm, sm.Bm, sm.cd, sm.a, tid);
+  __syncthreads();
+  if (tid < NS) {
+    float s = 0.f;
+#pragma unroll
+    for (int part = 0; part < 256 / NS; ++part) s += sm.trp[part][tid];
+    sm.tr[tid] = s;
+  }
+  // ---- B2: ZF[s,n] = sum_{t>=s} F_n[t,s] C_t[n], ZW (the same weighted by cd_t - cd_s);
+  //          dC2[t,n] = sum_{s<=t} F_n[t,s] delta_s B_s[n]
+#pragma unroll
+  for (int jj = 0; jj < Q * NS / 256; ++jj) {
+    const int i = tid + 256 * jj, j = i / NS, n = i % NS;
+    const float an = sm.a[n], cj = sm.cd[j];
+    float zf = 0.f, zw = 0.f, dc2 = 0.f;
+#pragma unroll 8
+    for (int k = 0; k < Q; ++k) {
+      // ZF, ZW: s = j, t = k; dC2: t = j, s = k
+      const float dk = sm.cd[k] - cj;
+      const float g = sm.G2[k][j] * kept_exp(k >= j, an * dk) * sm.Cm[k][n];
+      zf += g;
+      zw += g * dk;
+      dc2 += sm.G2[j][k] * kept_exp(k <= j, -an * dk) * sm.del[k] * sm.Bm[k][n];
+    }
+    sm.ZF[j][n] = zf;
+    sm.ZW[j][n] = zw;
+    sm.dC2[j][n] = dc2;
+  }
+  __syncthreads();
+  // ---- C: du = diag(delta) (W^T dY + (B o m31) lam^T) (MFMA)
+  constexpr int NBD = DH / 16;
+  for (int blk = w; blk < 2 * NBD; blk += 4) {
+    const int s0 = 16 * (blk / NBD), d0 = 16 * (blk % NBD);
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    acc = mm16<Q>([&](int r, int k) { return sm.W[k][s0 + r]; }, [&](int k, int c) { return sm.G[k][d0 + c]; }, lane,
+                  acc);
+    acc = mm16<NS>([&](int r, int k) { return sm.Bm[s0 + r][k] * sm.m31[s0 + r][k]; },
+                   [&](int k, int c) { return sm.lam[d0 + c][k]; }, lane, acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int s = s0 + 4 * (lane >> 4) + r;
+      rr::st(p.du, ((cp.row0 + s) * p.H + cp.h) * DH + d0 + (lane & 15), sm.del[s] * acc[r]);
+    }
+  }
+  // dB = delta Z, dC = E GH + dC2
+#pragma unroll
+  for (int jj = 0; jj < Q * NS / 256; ++jj) {
+    const int i = tid + 256 * jj, t = i / NS, n = i % NS;
+    const int64_t gi = ((cp.row0 + t) * p.H + cp.h) * NS + n;
+    rr::st(p.dB, gi, sm.del[t] * (sm.ZF[t][n] + sm.m31[t][n] * sm.UL[t][n]));
+    rr::st(p.dC, gi, sm.E[t][n] * sm.GH[t][n] + sm.dC2[t][n]);
+  }
+  // D[t,n] by scans over t (lanes t of a half-wave, one n per half-wave); dA
+  // of this chunk and the per-(wave, half) partials of d(delta)
+  {
+    const int t = lane & (Q - 1), hf = lane >> 5;
+    float ddp = 0.f;
+    for (int n2 = 2 * w; n2 < NS; n2 += 8) {
+      const int n = n2 + hf;   // NS even: n < NS
+      const float e = sm.E[t][n], c = sm.Cm[t][n], bd = sm.del[t] * sm.Bm[t][n], zf = sm.ZF[t][n];
+      const float x = e * c * sm.GH[t][n];
+      const float rt = c * sm.dC2[t][n] - bd * zf;
+      const float yv = sm.m31[t][n] * bd * sm.UL[t][n];
+      const float px = rr::prefix32_sum(x), pr = rr::prefix32_sum(rt), py = rr::prefix32_sum(yv);
+      const float tx = __shfl(px, 31 + 32 * hf), trr = __shfl(pr, 31 + 32 * hf);
+      const float D = (tx - px + x) + (trr - pr + rt) + sm.E[Q - 1][n] * sm.tr[n] + (py - yv);
+      const float ct = sm.cd[t], c31 = sm.cd[Q - 1];
+      const float da = rr::prefix32_sum(x * ct + yv * (c31 - ct) + bd * sm.ZW[t][n]);
+      if (t == Q - 1)
+        p.gA_part[((int64_t)cp.h * (p.B * p.nC) + (int64_t)cp.b * p.nC + cp.c) * NS + n] =
+            da + c31 * sm.E[Q - 1][n] * sm.tr[n];
+      ddp += sm.a[n] * D + sm.Bm[t][n] * (zf + sm.m31[t][n] * sm.UL[t][n]);
+    }
+    sm.ddp[w][hf][t] = ddp;
+  }
+  __syncthreads();
+  if (tid < Q) {
+    float s = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) s += sm.ddp[ww][0][tid] + sm.ddp[ww][1][tid];
+    rr::st(p.ddelta, (cp.row0 + tid) * p.H + cp.h, s);
+  }
+}
+
+template <typename InT, int DH, int NS>
+int launch(const rr::DenseArgs& a, int what, hipStream_t s) {
+  DenseArgsT<InT> p;
+  p.u = static_cast<const InT*>(a.u);
+  p.delta = static_cast<const InT*>(a.delta);
+  p.Bm = static_cast<const InT*>(a.Bm);
+  p.Cm = static_cast<const InT*>(a.Cm);
+  p.A = a.A;
+  p.a_sh = a.a_sh;
+  p.a_sn = a.a_sn;
+  p.h0 = a.h0;
+  p.ckpt = a.ckpt;
+  p.lamws = a.lamws;
+  p.dy = a.dy;
+  p.y = a.y;
+  p.du = static_cast<InT*>(a.du);
+  p.ddelta = static_cast<InT*>(a.ddelta);
+  p.dB = static_cast<InT*>(a.dB);
+  p.dC = static_cast<InT*>(a.dC);
+  p.gA_part = a.gA_part;
+  p.mapE = a.mapE;
+  p.mapP = a.mapP;
+  p.B = a.B; p.L = a.L; p.H = a.H; p.DH = a.DH; p.NS = a.NS; p.nC = a.nC;
+  const dim3 grid((unsigned)((int64_t)a.B * a.H * a.nC)), blk(256);
+  switch (what) {
+    case rr::kDenseMapsFwd: hipLaunchKernelGGL((dense_map_kernel<InT, DH, NS, false>), grid, blk, 0, s, p); break;
+    case rr::kDenseMapsBwd: hipLaunchKernelGGL((dense_map_kernel<InT, DH, NS, true>), grid, blk, 0, s, p); break;
+    case rr::kDenseOut: hipLaunchKernelGGL((dense_out_kernel<InT, DH, NS>), grid, blk, 0, s, p); break;
+    default: hipLaunchKernelGGL((dense_grad_kernel<InT, DH, NS>), grid, blk, 0, s, p); break;
+  }
+  return rr::check_launch(what == rr::kDenseOut ? "ssd dense forward" : what == rr::kDenseGrad ? "ssd dense backward"
+                                                                                               : "ssd dense chunk maps");
+}
+
+template <typename InT>
+int launch_shape(const rr::DenseArgs& a, int what, hipStream_t s) {
+  switch (a.DH * 1000 + a.NS) {
+    case 32016: return launch<InT, 32, 16>(a, what, s);
+    case 32032: return launch<InT, 32, 32>(a, what, s);
+    case 64016: return launch<InT, 64, 16>(a, what, s);
+    case 64032: return launch<InT, 64, 32>(a, what, s);
+    default: return rr::fail(RR_EUNSUPPORTED, "ssd dense: unsupported (Dh, N)");
+  }
+}
+
+}  // namespace
+
+namespace rr {
+
+bool ssd_dense_supported(int64_t T, int64_t Dh, int64_t N, int64_t B, int64_t H, int64_t nC) {
+  return T == Q && (Dh == 32 || Dh == 64) && (N == 16 || N == 32) && B * H * nC < ((int64_t)1 << 31);
+}
+
+int ssd_dense_launch(const DenseArgs& a, int dtype, int what, hipStream_t s) {
+  switch (dtype) {
+    case RR_F32: return launch_shape<float>(a, what, s);
+    case RR_BF16: return launch_shape<bf16>(a, what, s);
+    case RR_F16: return launch_shape<f16>(a, what, s);
+    default: return fail(RR_EINVAL, "ssd dense: unsupported dtype");
+  }
+}
+
+int ssd_dense_compose(const float* mapE, const float* mapP, const float* x0, float* out, float* xlast, int64_t B,
+                      int64_t H, int64_t Dh, int64_t N, int64_t nC, bool bwd, hipStream_t s) {
+  const int64_t total = B * H * Dh * N;
+  const dim3 grid((unsigned)((total + 255) / 256)), blk(256);
+  if (bwd)
+    hipLaunchKernelGGL((dense_compose_kernel<true>), grid, blk, 0, s, mapE, mapP, x0, out, xlast, total,
+                       (int)(Dh * N), (int)N, (int)nC);
+  else
+    hipLaunchKernelGGL((dense_compose_kernel<false>), grid, blk, 0, s, mapE, mapP, x0, out, xlast, total,
+                       (int)(Dh * N), (int)N, (int)nC);
+  return check_launch(bwd ? "ssd dense backward adjoints" : "ssd dense forward states");
+}
+
+}  // namespace rr

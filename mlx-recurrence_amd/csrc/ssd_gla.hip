@@ -158,6 +158,27 @@ __device__ __forceinline__ void unpack(float4 v, float (&a)[4]) {
 // seg = 32), so the per-step loops carry no run-time bound and the compiler
 // can issue each step's LDS reads ahead of the steps before it.
 
+// Workgroup of a chunk-parallel kernel (fold, replay): a 1-D grid over the
+// units u = (b * H + h) * groups + g (chunk group g: NW chunks) times the
+// ND * NN state tiles, decoded so that every tile of a unit runs on the same
+// XCD (the GPU hands workgroups to its 8 XCDs round-robin by linear index):
+// the tiles of a unit read the same step inputs, B and C rows, which one L2
+// then holds once.
+struct TileUnit {
+  int tile, grp, h, b;
+  bool valid;   // false for the padding workgroups of the last unit group
+};
+template <int NW, typename InT>
+__device__ __forceinline__ TileUnit tile_unit(const Args<InT>& p) {
+  const int id = blockIdx.x, x = id % 8, rest = id / 8, tiles = p.ND * p.NN;
+  const int groups = (p.nC + NW - 1) / NW;
+  const int u = (rest / tiles) * 8 + x, bh = u / groups;
+  return TileUnit{rest % tiles, u % groups, bh % p.H, bh / p.H, (int64_t)bh < (int64_t)p.Bsz * p.H};
+}
+inline int64_t tile_grid(int64_t B, int64_t H, int64_t groups, int64_t tiles) {
+  return (B * H * groups + 7) / 8 * 8 * tiles;
+}
+
 // Each pass runs in three kernels:
 //   r1_fold_kernel (every chunk at once, NW chunks per workgroup): each wave
 //     folds its chunk into the affine map x -> P x + E of the state (forward,
@@ -315,28 +336,6 @@ __global__ __launch_bounds__(64) void r1_compose_kernel(const float* __restrict_
   }
 }
 
-// Grid of the chunk-parallel kernels: x = tile + (ND * NN) * group, where
-// group g holds chunks NW g .. NW g + NW - 1 (one per wave).
-// Workgroup of a chunk-parallel kernel (fold, replay): a 1-D grid over the
-// units u = (b * H + h) * groups + g (chunk group g: NW chunks) times the
-// ND * NN state tiles, decoded so that every tile of a unit runs on the same
-// XCD (the GPU hands workgroups to its 8 XCDs round-robin by linear index):
-// the tiles of a unit read the same step inputs, B and C rows, which one L2
-// then holds once.
-struct TileUnit {
-  int tile, grp, h, b;
-  bool valid;   // false for the padding workgroups of the last unit group
-};
-template <int NW, typename InT>
-__device__ __forceinline__ TileUnit tile_unit(const Args<InT>& p) {
-  const int id = blockIdx.x, x = id % 8, rest = id / 8, tiles = p.ND * p.NN;
-  const int groups = (p.nC + NW - 1) / NW;
-  const int u = (rest / tiles) * 8 + x, bh = u / groups;
-  return TileUnit{rest % tiles, u % groups, bh % p.H, bh / p.H, (int64_t)bh < (int64_t)p.Bsz * p.H};
-}
-inline int64_t tile_grid(int64_t B, int64_t H, int64_t groups, int64_t tiles) {
-  return (B * H * groups + 7) / 8 * 8 * tiles;
-}
 
 // Short heads (nC <= kDirectMaxChunks): the replay kernels compose the chunk
 // maps themselves instead of reading the compose kernel's output.  The
@@ -798,20 +797,22 @@ __global__ __launch_bounds__(256) void r1_finalize_kernel(FinArgs<InT> p) {
   }
 }
 
-// dA_neg[h, n] = sum over finalize blocks (fixed order: deterministic); per
-// head (dA_sn == 0) dA_neg[h] = the sum of those over n, in order of n.
-__global__ void sum_gA_kernel(const float* __restrict__ part, float* __restrict__ dA, int H,
-                              int NS, int nblk, int dA_sn) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (dA_sn != 0 ? H * NS : H)) return;
-  const int h = dA_sn != 0 ? i / NS : i, n0 = dA_sn != 0 ? i % NS : 0, n1 = dA_sn != 0 ? n0 + 1 : NS;
-  float t = 0.f;
-  for (int n = n0; n < n1; ++n) {
-    float s = 0.f;
-    for (int j = 0; j < nblk; ++j) s += part[((int64_t)h * nblk + j) * NS + n];
-    t += s;
-  }
-  dA[i] = t;
+// dA_neg[h, n] = the sum of part[h][j][n] over the nblk blocks j; per head
+// (dA_sn == 0) dA_neg[h] = the sum over j and n.  One wave per output: lane l
+// sums terms l, l + 64, ... in order, then a fixed butterfly sums the lanes
+// (deterministic; every load of a lane is independent, so they overlap).
+__global__ __launch_bounds__(256) void sum_gA_kernel(const float* __restrict__ part, float* __restrict__ dA, int H,
+                                                     int NS, int nblk, int dA_sn) {
+  const int o = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (o >= (dA_sn != 0 ? H * NS : H)) return;   // whole waves
+  const int h = dA_sn != 0 ? o / NS : o, n0 = dA_sn != 0 ? o % NS : 0, nn = dA_sn != 0 ? 1 : NS;
+  const int64_t terms = (int64_t)nn * nblk;
+  const float* ph = part + (int64_t)h * nblk * NS;
+  float s = 0.f;
+#pragma unroll 4
+  for (int64_t q = lane; q < terms; q += 64) s += ph[(q % nblk) * NS + n0 + q / nblk];
+  s = rr::wave_sum(s);
+  if (lane == 0) dA[o] = s;
 }
 
 // ------------------------------------------------------------------ host
@@ -931,12 +932,55 @@ int launch_bwd(Args<InT> a, FinArgs<InT> f, const Plan& q, int64_t B, hipStream_
     hipLaunchKernelGGL((r1_finalize_kernel<InT, GLA, 64>), fgrid, dim3(256), 0, s, f);
   if (int rc = rr::check_launch("scan backward finalize")) return rc;
   if (!GLA) {
-    const int n = (int)(a.H * a.NS);
-    hipLaunchKernelGGL(sum_gA_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+    const int n = dA_sn != 0 ? (int)(a.H * a.NS) : a.H;
+    hipLaunchKernelGGL(sum_gA_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s,
                        f.gA_part, dA, a.H, a.NS, (int)q.nblk, dA_sn);
     if (int rc = rr::check_launch("scan backward dA")) return rc;
   }
   return RR_OK;
+}
+
+// SSD through the per-chunk kernels of ssd_dense.hip (a rate per (head, n), or
+// fp32 / fp16 inputs, at T = 32): chunk maps, the walk over chunks, then every
+// chunk's outputs or gradients at once.
+rr::DenseArgs dense_args(const void* u, const void* delta, const void* Bm, const void* Cm, const float* A_neg,
+                         int64_t A_stride_n, int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N, int64_t nC) {
+  rr::DenseArgs d{};
+  d.u = u;
+  d.delta = delta;
+  d.Bm = Bm;
+  d.Cm = Cm;
+  d.A = A_neg;
+  d.a_sh = A_stride_n ? N : 1;
+  d.a_sn = A_stride_n;
+  d.B = (int)B; d.L = (int)L; d.H = (int)H; d.DH = (int)Dh; d.NS = (int)N; d.nC = (int)nC;
+  return d;
+}
+
+int dense_fwd(rr::DenseArgs d, int dtype, const Plan& q, char* ws, float* ckpt, hipStream_t s) {
+  d.mapE = reinterpret_cast<float*>(ws + q.fwd_mapE);
+  d.mapP = reinterpret_cast<float*>(ws + q.fwd_mapP);
+  d.ckpt = ckpt;
+  if (int rc = rr::ssd_dense_launch(d, dtype, rr::kDenseMapsFwd, s)) return rc;
+  if (int rc = rr::ssd_dense_compose(d.mapE, d.mapP, d.h0, ckpt, nullptr, d.B, d.H, d.DH, d.NS, d.nC, false, s))
+    return rc;
+  return rr::ssd_dense_launch(d, dtype, rr::kDenseOut, s);
+}
+
+int dense_bwd(rr::DenseArgs d, int dtype, const Plan& q, char* ws, const float* dfinal, float* dh0, float* dA,
+              int dA_sn, hipStream_t s) {
+  d.mapE = reinterpret_cast<float*>(ws + q.bwd_mapE);
+  d.mapP = reinterpret_cast<float*>(ws + q.bwd_mapP);
+  float* lam = reinterpret_cast<float*>(ws + q.off_lam);
+  d.lamws = lam;
+  d.gA_part = reinterpret_cast<float*>(ws + q.off_gA);   // H * (B * nC) * N floats: nblk == B * nC at T = 32
+  if (int rc = rr::ssd_dense_launch(d, dtype, rr::kDenseMapsBwd, s)) return rc;
+  if (int rc = rr::ssd_dense_compose(d.mapE, d.mapP, dfinal, lam, dh0, d.B, d.H, d.DH, d.NS, d.nC, true, s)) return rc;
+  if (int rc = rr::ssd_dense_launch(d, dtype, rr::kDenseGrad, s)) return rc;
+  const int n = dA_sn != 0 ? d.H * d.NS : d.H;
+  hipLaunchKernelGGL(sum_gA_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, d.gA_part, dA, d.H, d.NS,
+                     d.B * d.nC, dA_sn);
+  return rr::check_launch("ssd dense backward dA");
 }
 
 }  // namespace
@@ -996,6 +1040,12 @@ extern "C" int rr_ssd_fwd(const void* u, const void* delta, const void* Bm, cons
   const Plan q = make_plan(B, L, H, Dh, N, seg);
   if (workspace_bytes < q.fwd_bytes || (q.fwd_bytes && !workspace))
     return rr::fail(RR_EWORKSPACE, "ssd_fwd: workspace too small");
+  if (rr::ssd_dense_supported(q.T, Dh, N, B, H, q.nC)) {
+    rr::DenseArgs d = dense_args(u, delta, Bm, Cm, A_neg, A_stride_n, B, L, H, Dh, N, q.nC);
+    d.h0 = h0;
+    d.y = y;
+    return dense_fwd(d, dtype, q, static_cast<char*>(workspace), ckpt, s);
+  }
   RR_DISPATCH_DTYPE(dtype, {
     Args<InT> a{};
     a.lane_in = static_cast<const InT*>(u);
@@ -1066,6 +1116,17 @@ extern "C" int rr_ssd_bwd(const float* dy, const float* dfinal, const void* u, c
     return rr::fail(RR_EWORKSPACE, "ssd_bwd: workspace too small");
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
+  if (rr::ssd_dense_supported(q.T, Dh, N, B, H, q.nC)) {
+    rr::DenseArgs d = dense_args(u, delta, Bm, Cm, A_neg, A_stride_n, B, L, H, Dh, N, q.nC);
+    d.h0 = h0;
+    d.ckpt = ckpt;
+    d.dy = dy;
+    d.du = du;
+    d.ddelta = ddelta;
+    d.dB = dB;
+    d.dC = dC;
+    return dense_bwd(d, dtype, q, ws, dfinal, dh0, dA_neg, (int)dA_stride_n, s);
+  }
   RR_DISPATCH_DTYPE(dtype, {
     Args<InT> a{};
     a.lane_in = static_cast<const InT*>(u);

@@ -304,6 +304,12 @@ def _ssd_inputs(rng, B, L, H, Dh, N, dist):
         Bm = rng.standard_normal((B, L, H, N)) * 0.5
         Cm = rng.standard_normal((B, L, H, N)) * 0.5
         A = -np.abs(rng.standard_normal((H, N))) - 0.1
+    elif dist == "steep":   # large steps and rates: in-chunk decays far below fp32's range
+        u = rng.standard_normal((B, L, H, Dh))
+        delta = np.abs(rng.standard_normal((B, L, H))) * 0.5 + 0.05
+        Bm = rng.standard_normal((B, L, H, N))
+        Cm = rng.standard_normal((B, L, H, N))
+        A = -np.abs(rng.standard_normal((H, N))) * 4.0 - 0.5
     else:               # BASELINE configs 0/1/4: A per head, broadcast over n
         u = rng.standard_normal((B, L, H, Dh))
         delta = np.abs(rng.standard_normal((B, L, H))) * 0.1 + 0.01
@@ -365,6 +371,14 @@ SSD_CASES = [
     (1, 200, 2, 32, 16, 8, F16, "ref", True, True, 54),     # T = 8: 25 chunks
     (1, 320, 2, 64, 16, 16, BF16, "cfg", True, True, 55),   # bf16 with T = 16: 20 chunks
     (2, 512, 2, 64, 40, 32, F32, "ref", False, True, 56),   # N = 40: three n-tiles, partial sums
+    # per-chunk MFMA kernels (a rate per (head, n), or fp32 / fp16 inputs, at
+    # T = 32, Dh 32 / 64, N 16 / 32): both N, both Dh, the three dtypes
+    (2, 128, 3, 32, 32, 32, F16, "ref", True, True, 57),
+    (1, 160, 2, 64, 32, 32, F32, "ref", True, True, 58),    # 5 chunks
+    (1, 1280, 2, 64, 16, 32, F32, "ref", True, False, 59),  # 40 chunks: compose walks past its read-ahead
+    (2, 96, 2, 32, 32, 32, BF16, "ref", True, True, 64),    # bf16 with a rate per (head, n)
+    (1, 256, 2, 64, 16, 32, F32, "steep", True, True, 65),  # in-chunk decays that underflow fp32
+    (2, 64, 3, 32, 16, 32, F16, "cfg", False, True, 66),    # fp16, per-head rate
 ]
 
 
