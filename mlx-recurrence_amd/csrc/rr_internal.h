@@ -139,11 +139,36 @@ enum DenseKernel { kDenseMapsFwd = 0, kDenseMapsBwd = 1, kDenseOut = 2, kDenseGr
 // Dh in {32, 64}, N in {16, 32}, and a 1-D grid of one workgroup per chunk.
 bool ssd_dense_supported(int64_t T, int64_t Dh, int64_t N, int64_t B, int64_t H, int64_t nC);
 int ssd_dense_launch(const DenseArgs& a, int dtype, int what, hipStream_t s);
-// The walk over the chunk maps: forward x0 = h0, out = ckpt (the state after
-// each chunk); backward x0 = dfinal, out = lamws (the adjoint flowing into
-// each chunk's end), xlast = dh0.  x0 and xlast may be null.
-int ssd_dense_compose(const float* mapE, const float* mapP, const float* x0, float* out, float* xlast, int64_t B,
-                      int64_t H, int64_t Dh, int64_t N, int64_t nC, bool bwd, hipStream_t s);
+// GLA for fp32 / fp16 inputs (and bf16 where the chunked kernels do not run),
+// T = 32, Dh in {32, 64} (gla_dense.hip): the same three-kernel scheme, the
+// maps in the layout dense_compose walks (mapP: gam_31 in every column).
+struct GlaDenseArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  const float* h0;      // [B,H,Dh,Dh] as [i][j], or null
+  const float* ckpt;    // [B,H,nC,Dh,Dh] as [j][i]
+  const float* lamws;   // [B,H,nC,Dh,Dh] as [j][i]
+  const float* dy;      // [B,L,H,Dh]
+  float* y;
+  void* dq;
+  void* dk;
+  void* dv;
+  void* dg;
+  float* mapE;
+  float* mapP;
+  int B, L, H, D, nC;
+};
+bool gla_dense_supported(int64_t T, int64_t Dh, int64_t B, int64_t H, int64_t nC);
+int gla_dense_launch(const GlaDenseArgs& a, int dtype, int what, hipStream_t s);
+
+// The walk over the chunk maps (SSD and GLA): forward x0 = h0, out = ckpt (the
+// state after each chunk); backward x0 = dfinal, out = lamws (the adjoint
+// flowing into each chunk's end), xlast = dh0.  x0 and xlast may be null; they
+// are [n][d] for GLA (the reference's [i, j]), [d][n] for SSD.
+int dense_compose(const float* mapE, const float* mapP, const float* x0, float* out, float* xlast, int64_t B,
+                  int64_t H, int64_t Dh, int64_t N, int64_t nC, bool bwd, bool gla, hipStream_t s);
 
 // Backward of the chunked kernels with column-owned state blocks (GLA: Dh in
 // {32, 64, 128}; SSD: Dh in {32, 64, 128}, N in {64, 128}; chunked_bwd.hip).  SSD

@@ -46,14 +46,13 @@
 // (t, s, n) formed by its own exponential (exact for any rate and step size:
 // no rescaled factors that could overflow).
 #include "rr_common.h"
+#include "rr_dense.h"
 #include "rr_internal.h"
 #include "rr_mfma.h"
 
 namespace {
 
-using rr::f32x4_t;
-
-constexpr int Q = 32;   // chunk length (steps)
+using namespace rr::dense;
 
 template <typename InT>
 struct DenseArgsT {
@@ -78,90 +77,59 @@ struct DenseArgsT {
   int B, L, H, DH, NS, nC;
 };
 
-// acc += A . B over K (a multiple of 4) for the 16 x 16 output block whose
-// lane holds column lane % 16 of rows 4 (lane / 16) + r, on the fp32 MFMA
-// v_mfma_f32_16x16x4_f32 (A[row = lane % 16][k = lane / 16],
-// B[k = lane / 16][col = lane % 16]): products and sums in fp32, no operand
-// splitting.  fa(row, k) and fb(k, col) read the operands (rows and columns
-// relative to the block).
-template <int K, class FA, class FB>
-__device__ __forceinline__ f32x4_t mm16(FA fa, FB fb, int lane, f32x4_t acc) {
-  const int r = lane & 15, kq = lane >> 4;
-#pragma unroll
-  for (int k0 = 0; k0 < K; k0 += 4) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(fa(r, k0 + kq), fb(k0 + kq, r), acc, 0, 0, 0);
-  return acc;
-}
-
-// exp(x) where keep, else 0 (formed in every lane, then selected: no branch,
-// and an overflowing exponential of a masked element is dropped, not multiplied).
-__device__ __forceinline__ float kept_exp(bool keep, float x) {
-  const float e = __expf(x);
-  return keep ? e : 0.f;
-}
-
-// Chunk (b, h, c) of workgroup blockIdx.x = (b * H + h) * nC + c.
-struct ChunkPos {
-  int b, h, c;
-  int64_t bh, row0;   // b * H + h; first (b, t) row of the chunk
-};
 template <typename InT>
 __device__ __forceinline__ ChunkPos chunk_pos(const DenseArgsT<InT>& p) {
-  const int id = blockIdx.x, c = id % p.nC, bh = id / p.nC;
-  return ChunkPos{bh / p.H, bh % p.H, c, (int64_t)bh, (int64_t)(bh / p.H) * p.L + (int64_t)c * Q};
+  return rr::dense::chunk_pos(p.H, p.L, p.nC);
 }
 
-// A [ROWS][W] fp32 slab staged through registers: load() issues one global
-// load per element (row r at src + r * stride, element w at + w; every
-// thread takes elements tid, tid + 256, ...), store() writes them to LDS.  A
-// kernel calls every load() before the first store(), so all of its loads are
-// in flight at once.
-template <int ROWS, int W>
-struct Slab {
-  static constexpr int N = ROWS * W / 256;
-  static_assert(ROWS * W % 256 == 0, "slab must split evenly over 256 threads");
-  float v[N];
-  template <typename T>
-  __device__ __forceinline__ void load(const T* src, int64_t stride, int tid) {
-#pragma unroll
-    for (int j = 0; j < N; ++j) {
-      const int i = tid + 256 * j;
-      v[j] = rr::ld(src, (int64_t)(i / W) * stride + i % W);
-    }
-  }
-  __device__ __forceinline__ void zero() {
-#pragma unroll
-    for (int j = 0; j < N; ++j) v[j] = 0.f;
-  }
-  template <int P>
-  __device__ __forceinline__ void store(float (&dst)[ROWS][P], int tid) const {
-#pragma unroll
-    for (int j = 0; j < N; ++j) {
-      const int i = tid + 256 * j;
-      dst[i / W][i % W] = v[j];
-    }
-  }
+// The decays of a chunk factor as M_n[t,s] = Ef[t,n] / Ef[s,n] with
+// Ef[t,n] = exp(a_n (cd_t - cm)), cm the middle of the range of cd (and 0).
+// Where every Ef and 1 / Ef lies within e^{+-80} (far inside fp32's normal
+// range), the masked sums over s, t of the backward and W are MFMA products of
+// ECt = Ef o C and BEi = B / Ef; else ("steep" chunks) they are formed with an
+// exponential per (t, s, n).  kFactorLimit bounds max_n |a_n| * half-range.
+constexpr float kFactorLimit = 80.f;
+struct Factor {
+  float cm;
+  float fast;   // 1: the factored form holds
 };
 
 // Step scalars of the chunk: delta (thread t < 32) and the rates (thread
 // n < NS) are loaded by the caller with the other inputs; this writes them to
-// LDS, forms cd (wave 0's prefix sum), then E[t,n] and / or m31[t,n].
-template <int NS, int PN, bool WANT_E, bool WANT_M31>
-__device__ __forceinline__ void step_scalars(float dv, float av, float* del, float* cd, float* a, float (*E)[PN],
-                                             float (*m31)[PN], int tid) {
+// LDS, forms cd (wave 0's prefix sum) and the factor scale, then E[t,n],
+// m31[t,n] and (in factored chunks) ECt, BEi, as requested (null: not wanted).
+// Cm and Bm must be in LDS before the call when ECt / BEi are wanted.
+template <int NS, int PN, int NT = 256>
+__device__ __forceinline__ void step_scalars(float dv, float av, float* del, float* cd, float* a, Factor* fac,
+                                             float (*E)[PN], float (*m31)[PN], float (*ECt)[PN], float (*BEi)[PN],
+                                             const float (*Cm)[PN], const float (*Bm)[PN], int tid) {
   if (tid < Q) del[tid] = dv;
   if (tid < NS) a[tid] = av;
-  if (tid < 64) {   // wave 0
+  if (tid < 64) {   // wave 0; lanes >= 32 take cd = 0 (the chunk's start)
     const float c = rr::prefix32_sum(tid < Q ? dv : 0.f);
     if (tid < Q) cd[tid] = c;
+    if (fac != nullptr) {
+      const float cmax = wave_max(c), cmin = -wave_max(-c), amax = wave_max(fabsf(av));
+      if (tid == 0) {
+        fac->cm = 0.5f * (cmax + cmin);
+        fac->fast = amax * (0.5f * (cmax - cmin)) <= kFactorLimit ? 1.f : 0.f;
+      }
+    }
   }
   __syncthreads();
   const float c31 = cd[Q - 1];
+  const bool fast = fac != nullptr && __builtin_amdgcn_readfirstlane(__float_as_int(fac->fast)) != 0;
+  const float cm = fac != nullptr ? fac->cm : 0.f;
 #pragma unroll
-  for (int j = 0; j < Q * NS / 256; ++j) {
-    const int i = tid + 256 * j, t = i / NS, n = i % NS;
+  for (int j = 0; j < Q * NS / NT; ++j) {
+    const int i = tid + NT * j, t = i / NS, n = i % NS;
     const float an = a[n], ct = cd[t];
-    if constexpr (WANT_E) E[t][n] = __expf(an * ct);
-    if constexpr (WANT_M31) m31[t][n] = __expf(an * (c31 - ct));
+    if (E != nullptr) E[t][n] = __expf(an * ct);
+    if (m31 != nullptr) m31[t][n] = __expf(an * (c31 - ct));
+    if (ECt != nullptr && fast) {
+      ECt[t][n] = __expf(an * (ct - cm)) * Cm[t][n];
+      BEi[t][n] = __expf(-an * (ct - cm)) * Bm[t][n];
+    }
   }
 }
 
@@ -173,19 +141,36 @@ __device__ __forceinline__ void load_step(const DenseArgsT<InT>& p, const ChunkP
   av = p.A[(int64_t)cp.h * p.a_sh + (int64_t)(tid & (NS - 1)) * p.a_sn];
 }
 
-// W[t,s] = sum_n C_t[n] B_s[n] M_n[t,s] (t >= s; 0 else): one thread per (t, s).
-template <int NS, int PN, int PQ>
+// W[t,s] = sum_n C_t[n] B_s[n] M_n[t,s] (t >= s; 0 else) with an exponential
+// per (t, s, n): one thread per (t, s).
+template <int NS, int PN, int PQ, int NT = 256>
 __device__ __forceinline__ void form_w(float (*W)[PQ], const float (*Cm)[PN], const float (*Bm)[PN], const float* cd,
                                        const float* a, int tid) {
 #pragma unroll
-  for (int j = 0; j < Q * Q / 256; ++j) {
-    const int i = tid + 256 * j, t = i / Q, s = i % Q;
+  for (int j = 0; j < Q * Q / NT; ++j) {
+    const int i = tid + NT * j, t = i / Q, s = i % Q;
     const bool keep = t >= s;
     const float dc = cd[t] - cd[s];
     float w = 0.f;
 #pragma unroll
     for (int n = 0; n < NS; ++n) w += Cm[t][n] * Bm[s][n] * kept_exp(keep, a[n] * dc);
     W[t][s] = w;
+  }
+}
+
+// W of a factored chunk: W[t,s] = sum_n ECt[t,n] BEi[s,n] (t >= s; 0 else) on
+// MFMA, 16 x 16 block (t0, s0) by one wave.
+template <int NS, int PN, int PQ>
+__device__ __forceinline__ void form_w_block(float (*W)[PQ], const float (*ECt)[PN], const float (*BEi)[PN], int t0,
+                                             int s0, int lane) {
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  if (t0 >= s0)
+    acc = mm16<NS>([&](int r, int k) { return ECt[t0 + r][k]; }, [&](int k, int c) { return BEi[s0 + c][k]; }, lane,
+                   acc);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = t0 + 4 * (lane >> 4) + r, s = s0 + (lane & 15);
+    W[t][s] = t >= s ? acc[r] : 0.f;
   }
 }
 
@@ -222,8 +207,10 @@ __global__ __launch_bounds__(256) void dense_map_kernel(DenseArgsT<InT> p) {
   load_step<NS>(p, cp, tid, dv, av);
   X.store(sm.X, tid);
   V.store(sm.V, tid);
-  if constexpr (BWD) step_scalars<NS, S::PN, true, false>(dv, av, sm.del, sm.cd, sm.a, sm.F, nullptr, tid);
-  else step_scalars<NS, S::PN, false, true>(dv, av, sm.del, sm.cd, sm.a, nullptr, sm.F, tid);
+  if constexpr (BWD)
+    step_scalars<NS, S::PN>(dv, av, sm.del, sm.cd, sm.a, nullptr, sm.F, nullptr, nullptr, nullptr, nullptr, nullptr, tid);
+  else
+    step_scalars<NS, S::PN>(dv, av, sm.del, sm.cd, sm.a, nullptr, nullptr, sm.F, nullptr, nullptr, nullptr, nullptr, tid);
   __syncthreads();
   constexpr int NBD = DH / 16, NBN = NS / 16;
   float* dst = p.mapE + ((cp.bh * p.nC + cp.c) * DH) * NS;
@@ -243,45 +230,6 @@ __global__ __launch_bounds__(256) void dense_map_kernel(DenseArgsT<InT> p) {
   if (tid < NS) p.mapP[(cp.bh * p.nC + cp.c) * NS + tid] = __expf(sm.a[tid] * sm.cd[Q - 1]);
 }
 
-// ------------------------------------------------------------------ the walk over chunks
-// One thread per state element (b, h, d, n): x_c = P_c x_{c-1} + E_c over the
-// chunks (forward from h0, in order, writing the state after each chunk;
-// backward from dfinal, in reverse, writing the adjoint flowing into each
-// chunk before its own map, and dh0 at the end).  The maps of kWalkBatch
-// chunks are loaded at once.
-constexpr int kWalkBatch = 16;
-template <bool BWD>
-__global__ __launch_bounds__(256) void dense_compose_kernel(const float* __restrict__ mapE,
-                                                            const float* __restrict__ mapP,
-                                                            const float* __restrict__ x0, float* __restrict__ out,
-                                                            float* __restrict__ xlast, int64_t total, int DN, int NS,
-                                                            int nC) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= total) return;
-  const int64_t bh = i / DN;
-  const int e = (int)(i % DN), n = e % NS;
-  float x = x0 != nullptr ? x0[i] : 0.f;
-  for (int i0 = 0; i0 < nC; i0 += kWalkBatch) {
-    float ev[kWalkBatch], pv[kWalkBatch];
-#pragma unroll
-    for (int q = 0; q < kWalkBatch; ++q) {
-      const int k = min(i0 + q, nC - 1), c = BWD ? nC - 1 - k : k;
-      ev[q] = mapE[(bh * nC + c) * DN + e];
-      pv[q] = mapP[(bh * nC + c) * NS + n];
-    }
-#pragma unroll
-    for (int q = 0; q < kWalkBatch; ++q) {
-      const int k = i0 + q, c = BWD ? nC - 1 - k : k;
-      if (k < nC) {
-        if (BWD) out[(bh * nC + c) * DN + e] = x;
-        x = pv[q] * x + ev[q];
-        if (!BWD) out[(bh * nC + c) * DN + e] = x;
-      }
-    }
-  }
-  if (xlast != nullptr) xlast[i] = x;
-}
-
 // ------------------------------------------------------------------ forward y
 template <int DH, int NS>
 struct alignas(16) OutSmem {
@@ -290,7 +238,9 @@ struct alignas(16) OutSmem {
   float Bm[Q][PN], Cm[Q][PN], E[Q][PN];
   float hin[DH][PN];
   float W[Q][PQ];
+  float ECt[Q][PN], BEi[Q][PN];
   float del[Q], cd[Q], a[NS];
+  Factor fac;
 };
 
 template <typename InT, int DH, int NS>
@@ -315,9 +265,12 @@ __global__ __launch_bounds__(256) void dense_out_kernel(DenseArgsT<InT> p) {
   Bv.store(sm.Bm, tid);
   Cv.store(sm.Cm, tid);
   Hs.store(sm.hin, tid);
-  step_scalars<NS, S::PN, true, false>(dv, av, sm.del, sm.cd, sm.a, sm.E, nullptr, tid);
+  step_scalars<NS, S::PN>(dv, av, sm.del, sm.cd, sm.a, &sm.fac, sm.E, nullptr, sm.ECt, sm.BEi, sm.Cm, sm.Bm, tid);
   __syncthreads();
-  form_w<NS, S::PN, S::PQ>(sm.W, sm.Cm, sm.Bm, sm.cd, sm.a, tid);
+  if (__builtin_amdgcn_readfirstlane(__float_as_int(sm.fac.fast)) != 0)
+    form_w_block<NS, S::PN, S::PQ>(sm.W, sm.ECt, sm.BEi, 16 * (w >> 1), 16 * (w & 1), lane);
+  else
+    form_w<NS, S::PN, S::PQ>(sm.W, sm.Cm, sm.Bm, sm.cd, sm.a, tid);
   __syncthreads();
   // Y [t][d] = sum_s W[t][s] delta_s U[s][d] + sum_n C[t][n] E[t][n] hin[d][n]
   constexpr int NBD = DH / 16;
@@ -337,6 +290,10 @@ __global__ __launch_bounds__(256) void dense_out_kernel(DenseArgsT<InT> p) {
 }
 
 // ------------------------------------------------------------------ backward
+// Eight waves per chunk: the LDS of a chunk allows two workgroups per CU, and
+// the phases below are LDS-latency bound, so more waves per workgroup keep the
+// SIMDs busy.
+constexpr int kGradThreads = 512, kGradWaves = kGradThreads / 64;
 template <int DH, int NS>
 struct alignas(16) GradSmem {
   static constexpr int PD = DH + 4, PN = NS + 4, PQ = Q + 4;
@@ -348,12 +305,15 @@ struct alignas(16) GradSmem {
   float G2[Q][PQ];      // dY U^T [t][s]
   float W[Q][PQ];       // W [t][s]
   float GH[Q][PN], UL[Q][PN], ZF[Q][PN], ZW[Q][PN], dC2[Q][PN];
-  float del[Q], cd[Q], a[NS], trp[256 / NS][NS], tr[NS];
-  float ddp[4][2][Q];   // per-(wave, half) partials of d(delta)
+  float ECt[Q][PN], BEi[Q][PN];
+  float del[Q], cd[Q], a[NS], trp[kGradThreads / NS][NS], tr[NS];
+  float ddp[kGradWaves][2][Q];   // per-(wave, half) partials of d(delta)
+  Factor fac;
 };
 
 template <typename InT, int DH, int NS>
-__global__ __launch_bounds__(256) void dense_grad_kernel(DenseArgsT<InT> p) {
+__global__ __launch_bounds__(kGradThreads) void dense_grad_kernel(DenseArgsT<InT> p) {
+  constexpr int NT = kGradThreads, NW = kGradWaves;
   using S = GradSmem<DH, NS>;
   __shared__ S sm;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -361,9 +321,9 @@ __global__ __launch_bounds__(256) void dense_grad_kernel(DenseArgsT<InT> p) {
   // ---- A: inputs, the entering state and the adjoint flowing in
   {
     const int64_t xoff = (cp.row0 * p.H + cp.h) * DH, voff = (cp.row0 * p.H + cp.h) * NS;
-    Slab<Q, DH> U, G;
-    Slab<Q, NS> Bv, Cv;
-    Slab<DH, NS> Hs, Ls;
+    Slab<Q, DH, NT> U, G;
+    Slab<Q, NS, NT> Bv, Cv;
+    Slab<DH, NS, NT> Hs, Ls;
     float dv, av;
     U.load(p.u + xoff, (int64_t)p.H * DH, tid);
     G.load(p.dy + xoff, (int64_t)p.H * DH, tid);
@@ -380,23 +340,24 @@ __global__ __launch_bounds__(256) void dense_grad_kernel(DenseArgsT<InT> p) {
     Cv.store(sm.Cm, tid);
     Hs.store(sm.hin, tid);
     Ls.store(sm.lam, tid);
-    step_scalars<NS, S::PN, true, true>(dv, av, sm.del, sm.cd, sm.a, sm.E, sm.m31, tid);
+    step_scalars<NS, S::PN, NT>(dv, av, sm.del, sm.cd, sm.a, &sm.fac, sm.E, sm.m31, sm.ECt, sm.BEi, sm.Cm, sm.Bm, tid);
   }
   __syncthreads();
-  // ---- B1: G2 = dY U^T, GH = dY h_in, UL = U lam (MFMA); tr partials; W
-  {
-    // wave w: G2 block (w / 2, w % 2)
-    const int t0 = 16 * (w >> 1), s0 = 16 * (w & 1);
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    acc = mm16<DH>([&](int r, int k) { return sm.G[t0 + r][k]; }, [&](int k, int c) { return sm.U[s0 + c][k]; },
-                   lane, acc);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sm.G2[t0 + 4 * (lane >> 4) + r][s0 + (lane & 15)] = acc[r];
-  }
+  // ---- B1: G2 = dY U^T, GH = dY h_in, UL = U lam (MFMA blocks: G2's four,
+  //          then GH and UL, 2 NBN each); tr partials; W of a steep chunk
   constexpr int NBN = NS / 16;
-  for (int blk = w; blk < 2 * 2 * NBN; blk += 4) {   // (kind, t-block, n-block)
-    const int kind = blk / (2 * NBN), t0 = 16 * ((blk / NBN) & 1), n0 = 16 * (blk % NBN);
+  for (int blk = w; blk < 4 + 4 * NBN; blk += NW) {
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    if (blk < 4) {
+      const int t0 = 16 * (blk >> 1), s0 = 16 * (blk & 1);
+      acc = mm16<DH>([&](int r, int k) { return sm.G[t0 + r][k]; }, [&](int k, int c) { return sm.U[s0 + c][k]; },
+                     lane, acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sm.G2[t0 + 4 * (lane >> 4) + r][s0 + (lane & 15)] = acc[r];
+      continue;
+    }
+    const int kind = (blk - 4) / (2 * NBN), rem = (blk - 4) % (2 * NBN);
+    const int t0 = 16 * (rem / NBN), n0 = 16 * (rem % NBN);
     if (kind == 0) {
       acc = mm16<DH>([&](int r, int k) { return sm.G[t0 + r][k]; },
                      [&](int k, int c) { return sm.hin[k][n0 + c]; }, lane, acc);
@@ -411,45 +372,87 @@ __global__ __launch_bounds__(256) void dense_grad_kernel(DenseArgsT<InT> p) {
   }
   {
     // tr[n] = sum_d lam o h_in: thread (part, n) sums d = part, part + P, ...
-    constexpr int P = 256 / NS;
+    constexpr int P = NT / NS;
     const int n = tid % NS, part = tid / NS;
     float s = 0.f;
 #pragma unroll
     for (int d = part; d < DH; d += P) s += sm.lam[d][n] * sm.hin[d][n];
     sm.trp[part][n] = s;
   }
-  form_w<NS, S::PN, S::PQ>(sm.W, sm.Cm, sm.Bm, sm.cd, sm.a, tid);
+  const bool fast = __builtin_amdgcn_readfirstlane(__float_as_int(sm.fac.fast)) != 0;
+  if (!fast) form_w<NS, S::PN, S::PQ, NT>(sm.W, sm.Cm, sm.Bm, sm.cd, sm.a, tid);
   __syncthreads();
   if (tid < NS) {
     float s = 0.f;
 #pragma unroll
-    for (int part = 0; part < 256 / NS; ++part) s += sm.trp[part][tid];
+    for (int part = 0; part < NT / NS; ++part) s += sm.trp[part][tid];
     sm.tr[tid] = s;
   }
   // ---- B2: ZF[s,n] = sum_{t>=s} F_n[t,s] C_t[n], ZW (the same weighted by cd_t - cd_s);
-  //          dC2[t,n] = sum_{s<=t} F_n[t,s] delta_s B_s[n]
+  //          dC2[t,n] = sum_{s<=t} F_n[t,s] delta_s B_s[n]; W of a factored chunk
+  if (fast) {
+    // Ef_s^-1 G2m^T ECt, the same with G2m o (cd_t - cd_s), Ef_t G2m (delta BEi):
+    // masked MFMA products (G2m: G2 for t >= s, 0 else; the k-range of a block
+    // skips its all-zero part).  Blocks: W's four, then ZF, ZW, dC2 (2 NBN each).
+    const float cm = sm.fac.cm;
+    for (int blk = w; blk < 4 + 6 * NBN; blk += NW) {
+      if (blk < 4) {
+        form_w_block<NS, S::PN, S::PQ>(sm.W, sm.ECt, sm.BEi, 16 * (blk >> 1), 16 * (blk & 1), lane);
+        continue;
+      }
+      const int kind = (blk - 4) / (2 * NBN), rem = (blk - 4) % (2 * NBN);
+      const int r0 = 16 * (rem / NBN), n0 = 16 * (rem % NBN);
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      const auto ect = [&](int k, int c) { return sm.ECt[k][n0 + c]; };
+      if (kind == 0) {          // ZF, rows s
+        const auto fa = [&](int r, int k) { return k >= r0 + r ? sm.G2[k][r0 + r] : 0.f; };
+        acc = r0 == 0 ? mm16r<0, Q>(fa, ect, lane, acc) : mm16r<16, Q>(fa, ect, lane, acc);
+      } else if (kind == 1) {   // ZW, rows s
+        const auto fa = [&](int r, int k) {
+          const int s = r0 + r;
+          return k >= s ? sm.G2[k][s] * (sm.cd[k] - sm.cd[s]) : 0.f;
+        };
+        acc = r0 == 0 ? mm16r<0, Q>(fa, ect, lane, acc) : mm16r<16, Q>(fa, ect, lane, acc);
+      } else {                  // dC2, rows t
+        const auto fa = [&](int r, int k) { return k <= r0 + r ? sm.G2[r0 + r][k] : 0.f; };
+        const auto fb = [&](int k, int c) { return sm.del[k] * sm.BEi[k][n0 + c]; };
+        acc = r0 == 0 ? mm16r<0, 16>(fa, fb, lane, acc) : mm16r<0, Q>(fa, fb, lane, acc);
+      }
+      const int n = n0 + (lane & 15);
+      const float an = sm.a[n];
 #pragma unroll
-  for (int jj = 0; jj < Q * NS / 256; ++jj) {
-    const int i = tid + 256 * jj, j = i / NS, n = i % NS;
-    const float an = sm.a[n], cj = sm.cd[j];
-    float zf = 0.f, zw = 0.f, dc2 = 0.f;
-#pragma unroll 8
-    for (int k = 0; k < Q; ++k) {
-      // ZF, ZW: s = j, t = k; dC2: t = j, s = k
-      const float dk = sm.cd[k] - cj;
-      const float g = sm.G2[k][j] * kept_exp(k >= j, an * dk) * sm.Cm[k][n];
-      zf += g;
-      zw += g * dk;
-      dc2 += sm.G2[j][k] * kept_exp(k <= j, -an * dk) * sm.del[k] * sm.Bm[k][n];
+      for (int r = 0; r < 4; ++r) {
+        const int row = r0 + 4 * (lane >> 4) + r;
+        const float x = an * (sm.cd[row] - cm);
+        if (kind == 0) sm.ZF[row][n] = acc[r] * __expf(-x);
+        else if (kind == 1) sm.ZW[row][n] = acc[r] * __expf(-x);
+        else sm.dC2[row][n] = acc[r] * __expf(x);
+      }
     }
-    sm.ZF[j][n] = zf;
-    sm.ZW[j][n] = zw;
-    sm.dC2[j][n] = dc2;
+  } else {
+#pragma unroll
+    for (int jj = 0; jj < Q * NS / NT; ++jj) {
+      const int i = tid + NT * jj, j = i / NS, n = i % NS;
+      const float an = sm.a[n], cj = sm.cd[j];
+      float zf = 0.f, zw = 0.f, dc2 = 0.f;
+#pragma unroll 8
+      for (int k = 0; k < Q; ++k) {
+        // ZF, ZW: s = j, t = k; dC2: t = j, s = k
+        const float dk = sm.cd[k] - cj;
+        const float g = sm.G2[k][j] * kept_exp(k >= j, an * dk) * sm.Cm[k][n];
+        zf += g;
+        zw += g * dk;
+        dc2 += sm.G2[j][k] * kept_exp(k <= j, -an * dk) * sm.del[k] * sm.Bm[k][n];
+      }
+      sm.ZF[j][n] = zf;
+      sm.ZW[j][n] = zw;
+      sm.dC2[j][n] = dc2;
+    }
   }
   __syncthreads();
   // ---- C: du = diag(delta) (W^T dY + (B o m31) lam^T) (MFMA)
   constexpr int NBD = DH / 16;
-  for (int blk = w; blk < 2 * NBD; blk += 4) {
+  for (int blk = w; blk < 2 * NBD; blk += NW) {
     const int s0 = 16 * (blk / NBD), d0 = 16 * (blk % NBD);
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
     acc = mm16<Q>([&](int r, int k) { return sm.W[k][s0 + r]; }, [&](int k, int c) { return sm.G[k][d0 + c]; }, lane,
@@ -464,8 +467,8 @@ __global__ __launch_bounds__(256) void dense_grad_kernel(DenseArgsT<InT> p) {
   }
   // dB = delta Z, dC = E GH + dC2
 #pragma unroll
-  for (int jj = 0; jj < Q * NS / 256; ++jj) {
-    const int i = tid + 256 * jj, t = i / NS, n = i % NS;
+  for (int jj = 0; jj < Q * NS / NT; ++jj) {
+    const int i = tid + NT * jj, t = i / NS, n = i % NS;
     const int64_t gi = ((cp.row0 + t) * p.H + cp.h) * NS + n;
     rr::st(p.dB, gi, sm.del[t] * (sm.ZF[t][n] + sm.m31[t][n] * sm.UL[t][n]));
     rr::st(p.dC, gi, sm.E[t][n] * sm.GH[t][n] + sm.dC2[t][n]);
@@ -475,7 +478,7 @@ __global__ __launch_bounds__(256) void dense_grad_kernel(DenseArgsT<InT> p) {
   {
     const int t = lane & (Q - 1), hf = lane >> 5;
     float ddp = 0.f;
-    for (int n2 = 2 * w; n2 < NS; n2 += 8) {
+    for (int n2 = 2 * w; n2 < NS; n2 += 2 * NW) {
       const int n = n2 + hf;   // NS even: n < NS
       const float e = sm.E[t][n], c = sm.Cm[t][n], bd = sm.del[t] * sm.Bm[t][n], zf = sm.ZF[t][n];
       const float x = e * c * sm.GH[t][n];
@@ -497,7 +500,7 @@ __global__ __launch_bounds__(256) void dense_grad_kernel(DenseArgsT<InT> p) {
   if (tid < Q) {
     float s = 0.f;
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww) s += sm.ddp[ww][0][tid] + sm.ddp[ww][1][tid];
+    for (int ww = 0; ww < NW; ++ww) s += sm.ddp[ww][0][tid] + sm.ddp[ww][1][tid];
     rr::st(p.ddelta, (cp.row0 + tid) * p.H + cp.h, s);
   }
 }
@@ -530,7 +533,7 @@ int launch(const rr::DenseArgs& a, int what, hipStream_t s) {
     case rr::kDenseMapsFwd: hipLaunchKernelGGL((dense_map_kernel<InT, DH, NS, false>), grid, blk, 0, s, p); break;
     case rr::kDenseMapsBwd: hipLaunchKernelGGL((dense_map_kernel<InT, DH, NS, true>), grid, blk, 0, s, p); break;
     case rr::kDenseOut: hipLaunchKernelGGL((dense_out_kernel<InT, DH, NS>), grid, blk, 0, s, p); break;
-    default: hipLaunchKernelGGL((dense_grad_kernel<InT, DH, NS>), grid, blk, 0, s, p); break;
+    default: hipLaunchKernelGGL((dense_grad_kernel<InT, DH, NS>), grid, dim3(kGradThreads), 0, s, p); break;
   }
   return rr::check_launch(what == rr::kDenseOut ? "ssd dense forward" : what == rr::kDenseGrad ? "ssd dense backward"
                                                                                                : "ssd dense chunk maps");
@@ -564,17 +567,20 @@ int ssd_dense_launch(const DenseArgs& a, int dtype, int what, hipStream_t s) {
   }
 }
 
-int ssd_dense_compose(const float* mapE, const float* mapP, const float* x0, float* out, float* xlast, int64_t B,
-                      int64_t H, int64_t Dh, int64_t N, int64_t nC, bool bwd, hipStream_t s) {
+int dense_compose(const float* mapE, const float* mapP, const float* x0, float* out, float* xlast, int64_t B,
+                  int64_t H, int64_t Dh, int64_t N, int64_t nC, bool bwd, bool gla, hipStream_t s) {
   const int64_t total = B * H * Dh * N;
   const dim3 grid((unsigned)((total + 255) / 256)), blk(256);
-  if (bwd)
-    hipLaunchKernelGGL((dense_compose_kernel<true>), grid, blk, 0, s, mapE, mapP, x0, out, xlast, total,
-                       (int)(Dh * N), (int)N, (int)nC);
+  const int dl = (int)Dh, ns = (int)N, nc = (int)nC;
+  if (bwd && gla)
+    hipLaunchKernelGGL((dense_compose_kernel<true, true>), grid, blk, 0, s, mapE, mapP, x0, out, xlast, total, dl, ns, nc);
+  else if (bwd)
+    hipLaunchKernelGGL((dense_compose_kernel<true, false>), grid, blk, 0, s, mapE, mapP, x0, out, xlast, total, dl, ns, nc);
+  else if (gla)
+    hipLaunchKernelGGL((dense_compose_kernel<false, true>), grid, blk, 0, s, mapE, mapP, x0, out, xlast, total, dl, ns, nc);
   else
-    hipLaunchKernelGGL((dense_compose_kernel<false>), grid, blk, 0, s, mapE, mapP, x0, out, xlast, total,
-                       (int)(Dh * N), (int)N, (int)nC);
-  return check_launch(bwd ? "ssd dense backward adjoints" : "ssd dense forward states");
+    hipLaunchKernelGGL((dense_compose_kernel<false, false>), grid, blk, 0, s, mapE, mapP, x0, out, xlast, total, dl, ns, nc);
+  return check_launch(bwd ? "dense backward adjoints" : "dense forward states");
 }
 
 }  // namespace rr

@@ -962,7 +962,7 @@ int dense_fwd(rr::DenseArgs d, int dtype, const Plan& q, char* ws, float* ckpt, 
   d.mapP = reinterpret_cast<float*>(ws + q.fwd_mapP);
   d.ckpt = ckpt;
   if (int rc = rr::ssd_dense_launch(d, dtype, rr::kDenseMapsFwd, s)) return rc;
-  if (int rc = rr::ssd_dense_compose(d.mapE, d.mapP, d.h0, ckpt, nullptr, d.B, d.H, d.DH, d.NS, d.nC, false, s))
+  if (int rc = rr::dense_compose(d.mapE, d.mapP, d.h0, ckpt, nullptr, d.B, d.H, d.DH, d.NS, d.nC, false, false, s))
     return rc;
   return rr::ssd_dense_launch(d, dtype, rr::kDenseOut, s);
 }
@@ -975,7 +975,8 @@ int dense_bwd(rr::DenseArgs d, int dtype, const Plan& q, char* ws, const float* 
   d.lamws = lam;
   d.gA_part = reinterpret_cast<float*>(ws + q.off_gA);   // H * (B * nC) * N floats: nblk == B * nC at T = 32
   if (int rc = rr::ssd_dense_launch(d, dtype, rr::kDenseMapsBwd, s)) return rc;
-  if (int rc = rr::ssd_dense_compose(d.mapE, d.mapP, dfinal, lam, dh0, d.B, d.H, d.DH, d.NS, d.nC, true, s)) return rc;
+  if (int rc = rr::dense_compose(d.mapE, d.mapP, dfinal, lam, dh0, d.B, d.H, d.DH, d.NS, d.nC, true, false, s))
+    return rc;
   if (int rc = rr::ssd_dense_launch(d, dtype, rr::kDenseGrad, s)) return rc;
   const int n = dA_sn != 0 ? d.H * d.NS : d.H;
   hipLaunchKernelGGL(sum_gA_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, d.gA_part, dA, d.H, d.NS,
@@ -1244,6 +1245,19 @@ rr::ChunkArgs gla2_args(const void* qp, const void* kp, const void* vp, const vo
 }
 }  // namespace
 
+namespace {
+rr::GlaDenseArgs gla_dense_args(const void* qp, const void* kp, const void* vp, const void* gates, int64_t B,
+                                int64_t L, int64_t H, int64_t Dh, int64_t nC) {
+  rr::GlaDenseArgs d{};
+  d.q = qp;
+  d.k = kp;
+  d.v = vp;
+  d.g = gates;
+  d.B = (int)B; d.L = (int)L; d.H = (int)H; d.D = (int)Dh; d.nC = (int)nC;
+  return d;
+}
+}  // namespace
+
 extern "C" size_t rr_gla_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh,
                                          int64_t seg, int dtype, int pass) {
   if (B <= 0 || L <= 0 || H <= 0 || Dh <= 0 || rr::chunk_len(L, seg) == 0) return 0;
@@ -1273,6 +1287,18 @@ extern "C" int rr_gla_fwd(const void* qp, const void* kp, const void* vp, const 
   const Plan q = make_plan(B, L, H, Dh, Dh, seg);
   if (workspace_bytes < q.fwd_bytes || (q.fwd_bytes && !workspace))
     return rr::fail(RR_EWORKSPACE, "gla_fwd: workspace too small");
+  if (rr::gla_dense_supported(q.T, Dh, B, H, q.nC)) {
+    rr::GlaDenseArgs d = gla_dense_args(qp, kp, vp, gates, B, L, H, Dh, q.nC);
+    char* ws = static_cast<char*>(workspace);
+    d.h0 = h0;
+    d.y = y;
+    d.ckpt = ckpt;
+    d.mapE = reinterpret_cast<float*>(ws + q.fwd_mapE);
+    d.mapP = reinterpret_cast<float*>(ws + q.fwd_mapP);
+    if (int rc = rr::gla_dense_launch(d, dtype, rr::kDenseMapsFwd, s)) return rc;
+    if (int rc = rr::dense_compose(d.mapE, d.mapP, h0, ckpt, nullptr, B, H, Dh, Dh, q.nC, false, true, s)) return rc;
+    return rr::gla_dense_launch(d, dtype, rr::kDenseOut, s);
+  }
   RR_DISPATCH_DTYPE(dtype, {
     Args<InT> a{};
     a.lane_in = static_cast<const InT*>(vp);
@@ -1319,6 +1345,23 @@ extern "C" int rr_gla_bwd(const float* dy, const float* dfinal, const void* qp, 
     return rr::fail(RR_EWORKSPACE, "gla_bwd: workspace too small");
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
+  if (rr::gla_dense_supported(q.T, Dh, B, H, q.nC)) {
+    rr::GlaDenseArgs d = gla_dense_args(qp, kp, vp, gates, B, L, H, Dh, q.nC);
+    float* lam = reinterpret_cast<float*>(ws + q.off_lam);
+    d.h0 = h0;
+    d.ckpt = ckpt;
+    d.lamws = lam;
+    d.dy = dy;
+    d.dq = dq;
+    d.dk = dk;
+    d.dv = dv;
+    d.dg = dgates;
+    d.mapE = reinterpret_cast<float*>(ws + q.bwd_mapE);
+    d.mapP = reinterpret_cast<float*>(ws + q.bwd_mapP);
+    if (int rc = rr::gla_dense_launch(d, dtype, rr::kDenseMapsBwd, s)) return rc;
+    if (int rc = rr::dense_compose(d.mapE, d.mapP, dfinal, lam, dh0, B, H, Dh, Dh, q.nC, true, true, s)) return rc;
+    return rr::gla_dense_launch(d, dtype, rr::kDenseGrad, s);
+  }
   RR_DISPATCH_DTYPE(dtype, {
     Args<InT> a{};
     a.lane_in = static_cast<const InT*>(vp);

@@ -304,9 +304,9 @@ def _ssd_inputs(rng, B, L, H, Dh, N, dist):
         Bm = rng.standard_normal((B, L, H, N)) * 0.5
         Cm = rng.standard_normal((B, L, H, N)) * 0.5
         A = -np.abs(rng.standard_normal((H, N))) - 0.1
-    elif dist == "steep":   # large steps and rates: in-chunk decays far below fp32's range
+    elif dist in ("steep", "cliff"):   # large steps and rates: in-chunk decays far below fp32's range
         u = rng.standard_normal((B, L, H, Dh))
-        delta = np.abs(rng.standard_normal((B, L, H))) * 0.5 + 0.05
+        delta = np.abs(rng.standard_normal((B, L, H))) * (0.5 if dist == "steep" else 2.0) + 0.05
         Bm = rng.standard_normal((B, L, H, N))
         Cm = rng.standard_normal((B, L, H, N))
         A = -np.abs(rng.standard_normal((H, N))) * 4.0 - 0.5
@@ -377,7 +377,11 @@ SSD_CASES = [
     (1, 160, 2, 64, 32, 32, F32, "ref", True, True, 58),    # 5 chunks
     (1, 1280, 2, 64, 16, 32, F32, "ref", True, False, 59),  # 40 chunks: compose walks past its read-ahead
     (2, 96, 2, 32, 32, 32, BF16, "ref", True, True, 64),    # bf16 with a rate per (head, n)
-    (1, 256, 2, 64, 16, 32, F32, "steep", True, True, 65),  # in-chunk decays that underflow fp32
+    # decays that underflow fp32 within a chunk: 65 keeps every chunk in the
+    # factored form (factors up to e^+-71), 67 takes none (exponential per term)
+    (1, 256, 2, 64, 16, 32, F32, "steep", True, True, 65),
+    (1, 256, 2, 64, 16, 32, F32, "cliff", True, True, 67),
+    (2, 128, 2, 32, 32, 32, BF16, "cliff", True, True, 68),
     (2, 64, 3, 32, 16, 32, F16, "cfg", False, True, 66),    # fp16, per-head rate
 ]
 
@@ -502,6 +506,11 @@ GLA_CASES = [
     (1, 320, 2, 32, 16, F32, "signed", True, True, 52),     # T = 16: 20 chunks
     (2, 200, 2, 32, 8, F32, "zeros", True, True, 53),       # T = 8: 25 chunks, zero gates
     (1, 320, 2, 64, 16, BF16, "cfg", True, True, 54),       # bf16 with T = 16
+    # per-chunk fp32-MFMA kernels (fp32 / fp16 inputs, T = 32, Dh 32 / 64)
+    (1, 256, 2, 64, 32, F32, "signed", True, True, 55),     # gates of either sign
+    (2, 192, 3, 32, 32, F16, "zeros", True, True, 56),      # zero gates cut the recurrence
+    (1, 1280, 2, 32, 32, F32, "ref", True, False, 57),      # 40 chunks: the walk past its read-ahead
+    (3, 512, 12, 64, 32, F32, "cfg", False, True, 58),      # BASELINE config 2's shape, fp32
 ]
 
 
