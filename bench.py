@@ -47,6 +47,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "SSD/GLA fwd+bwd tokens/s at B3·L512·H12·Dh64; achieved HBM GB/s % of peak"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0   # dense bf16 MFMA, MI355X
+MFMA_F32_PEAK_TFLOPS = 157.3     # dense fp32 MFMA, MI355X
 
 
 # ------------------------------------------------------------------ HIP graph
@@ -132,7 +133,7 @@ def make_ssd(cfg, device, dtype):
     import torch
     from mlx_recurrence_amd import _lib
     B, L, H, Dh, N, seg = cfg["B"], cfg["L"], cfg["H"], cfg["Dh"], cfg["N"], cfg["seg"]
-    dense = cfg.get("dense", False)   # A_neg [H, N] varying over n (the reference tests' A): VALU engine
+    dense = cfg.get("dense", False)   # A_neg [H, N] varying over n (the reference tests' A)
     dtype = torch.float32 if cfg.get("dtype") == "f32" else dtype
     g = torch.Generator().manual_seed(cfg.get("seed", 1))
     u = _gen((B, L, H, Dh), g)
@@ -564,9 +565,9 @@ WORKLOADS = {
                dict(B=8, L=4096, H=80, Dh=64, N=128, seg=32)),
     # configs 1 and 2 with 32x the batch: the same kernels with the GPU filled
     # (at B = 3 the passes are latency-bound), reported beside the headline
-    # the reference's general input contract on the VALU engine: A_neg [H, N]
-    # varying over n (its tests' draw), fp32 inputs, and its production SSD
-    # shape Dh 128, N 64 (chunked forward, VALU backward)
+    # the reference's general input contract (per-chunk fp32-MFMA kernels):
+    # A_neg [H, N] varying over n (its tests' draw), fp32 inputs; and its
+    # production SSD / GLA shape Dh 128 (N 64)
     "ssd_dense": ("ssd_scan fwd+bwd, dense A_neg [H, N] (BASELINE config 1 shape)", make_ssd,
                   dict(B=3, L=512, H=12, Dh=64, N=16, seg=32, dense=True)),
     "ssd_f32": ("ssd_scan fwd+bwd, fp32 inputs (BASELINE config 1 shape)", make_ssd,
@@ -873,7 +874,7 @@ COUNTER_SETS = {
     "fetch": ["TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum", "TCC_BUBBLE_sum"],
     "write": ["TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum"],
     "mfma": ["SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU",
-             "SQ_INSTS_MFMA", "SQ_BUSY_CU_CYCLES"],
+             "SQ_INSTS_MFMA", "SQ_BUSY_CU_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_F32"],
 }
 CALIBRATIONS = {"copy": ("fetch", "write"), "sector": ("fetch", "write"), "gemm": ("mfma",)}
 CAL_MB = 256          # copy / sector read source size
@@ -1083,6 +1084,7 @@ def pmc_summary(root):
                     k.update(mfma_busy_cycles=busy, gui_active_cycles=gui,
                              mfma_util=busy / (gui / info["xcc"] * info["simd"]) if gui else None,
                              mfma_flops=v["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512,
+                             mfma_flops_f32=v.get("SQ_INSTS_VALU_MFMA_MOPS_F32", 0) * 512,
                              insts_valu=v["SQ_INSTS_VALU"], insts_mfma=v["SQ_INSTS_MFMA"],
                              busy_cu_cycles=v["SQ_BUSY_CU_CYCLES"])
                 rows.append(k)
@@ -1143,9 +1145,10 @@ def profile_markdown(summary, trace_dir, out_md, commands):
               "(inputs, outputs and checkpoints at their API dtypes), all moved by its main kernel; the other "
               "kernels of a pass move workspace data only.  MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / "
               f"(GRBM_GUI_ACTIVE / {info.get('xcc', 8)} XCDs x {info.get('simd', 1024)} SIMDs); MFMA GFLOP = "
-              "SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 per dispatch; MOPS / MFMA inst = that count over SQ_INSTS_MFMA "
+              "SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 per dispatch, or SQ_INSTS_VALU_MFMA_MOPS_F32 x 512 (marked f32) "
+              "for the kernels on the fp32 MFMA; MOPS / MFMA inst = that count over SQ_INSTS_MFMA "
               "(64 for 32x32x16, 32 for 16x16x32, 16 for 16x16x16 bf16: the K = 16 shapes issue at half the "
-              "peak rate, so their busy share exceeds their share of the 2.5 PFLOP/s peak); "
+              "peak rate, so their busy share exceeds their share of the 2.5 PFLOP/s peak; 4 for 16x16x4 fp32); "
               "VALU / MFMA = SQ_INSTS_VALU, SQ_INSTS_MFMA (instructions per dispatch).", "",
               "| workload | pass | kernel | fetch MB | write MB | pass algorithmic MB | MFMA busy | MFMA GFLOP | "
               "MOPS / MFMA inst | VALU insts | MFMA insts |", "|---|---|---|---|---|---|---|---|---|---|---|"]
@@ -1159,11 +1162,13 @@ def profile_markdown(summary, trace_dir, out_md, commands):
         for pname in ("fwd", "bwd"):
             alg = (w[f"{pname}_bytes"] if w else _c4_bytes()[pname]) / 1e6
             for k in entry[pname]:
+                f32 = k.get("mfma_flops_f32", 0) > (k.get("mfma_flops") or 0)
+                fl = k.get("mfma_flops_f32") if f32 else k.get("mfma_flops")
                 lines.append(f"| {wname} | {pname} | `{k['kernel'][:60]}` | {fmt(k['fetch_bytes'] and k['fetch_bytes'] / 1e6, '{:.3f}')} | "
                              f"{fmt(k['write_bytes'] and k['write_bytes'] / 1e6, '{:.3f}')} | {alg:.3f} | "
                              f"{fmt(k.get('mfma_util') and 100 * k['mfma_util'], '{:.1f} %')} | "
-                             f"{fmt(k.get('mfma_flops') and k['mfma_flops'] / 1e9, '{:.2f}')} | "
-                             f"{fmt(k.get('insts_mfma') and k['mfma_flops'] / 512 / k['insts_mfma'], '{:.1f}')} | "
+                             f"{fmt(fl / 1e9 if fl is not None else None, '{:.2f}')}{' f32' if f32 else ''} | "
+                             f"{fmt(k.get('insts_mfma') and fl / 512 / k['insts_mfma'], '{:.1f}')} | "
                              f"{fmt(k.get('insts_valu'), '{:.3g}')} | {fmt(k.get('insts_mfma'), '{:.3g}')} |")
     pathlib.Path(out_md).write_text("\n".join(lines) + "\n")
     print(f"wrote {out_md}")
@@ -1196,7 +1201,9 @@ def traffic_of(name, dom):
 
 def mfma_of(name, dom):
     """MFMA figures of the dominant kernel against MI355X's dense bf16 peak
-    (2.5 PFLOP/s = 1024 SIMDs x 1024 flops per cycle x 2.4 GHz):
+    (2.5 PFLOP/s = 1024 SIMDs x 1024 flops per cycle x 2.4 GHz), or, for the
+    kernels on the fp32 MFMA (more fp32 than bf16 MOPS), its fp32 peak
+    (157.3 TFLOP/s) with SQ_INSTS_VALU_MFMA_MOPS_F32:
       util      busy share of the MFMA units, SQ_VALU_MFMA_BUSY_CYCLES / (the
                 live-measured average launch duration x 2.4 GHz x SIMDs);
       frac      bf16 MFMA flops (SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512) / that
@@ -1209,25 +1216,29 @@ def mfma_of(name, dom):
     flops, and util = frac there.  util > frac where a kernel issues the K = 16
     shapes (16x16x16, 32x32x8 bf16), which take as many busy cycles per
     instruction as the K = 32 shapes for half the flops; mops_per_mfma_inst
-    shows the mix (32 for 16x16x32 bf16, 16 for 16x16x16).  None where the
-    kernel issues no MFMA."""
+    shows the mix (32 for 16x16x32 bf16, 16 for 16x16x16, 4 for 16x16x4 fp32).
+    None where the kernel issues no MFMA."""
     k = _pmc_kernel(name, dom)
-    if k is None or not k.get("mfma_flops"):
+    if k is None or not (k.get("mfma_flops") or k.get("mfma_flops_f32")):
         return None
-    tflops = k["mfma_flops"] / (dom["us"] * 1e-6) / 1e12
+    f32 = k.get("mfma_flops_f32", 0) > k.get("mfma_flops", 0)   # the fp32-MFMA kernels (fp32 / dense-A paths)
+    flops = k["mfma_flops_f32"] if f32 else k["mfma_flops"]
+    peak = MFMA_F32_PEAK_TFLOPS if f32 else MFMA_BF16_PEAK_TFLOPS
+    tflops = flops / (dom["us"] * 1e-6) / 1e12
     try:
         info = json.loads(PMC_FILE.read_text()).get("agent", {})
     except (OSError, ValueError):
         info = {}
     simd, clk = info.get("simd", 1024), info.get("clk_mhz", 2400)
     util = k["mfma_busy_cycles"] / (dom["us"] * 1e-6 * clk * 1e6 * simd) if k.get("mfma_busy_cycles") else None
-    mops_inst = k["mfma_flops"] / 512 / k["insts_mfma"] if k.get("insts_mfma") else None
-    return {"util": util, "achieved": tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": tflops / MFMA_BF16_PEAK_TFLOPS, "util_grbm": k.get("mfma_util"),
-            "flops_per_launch": k["mfma_flops"], "mops_per_mfma_inst": mops_inst,
+    mops_inst = flops / 512 / k["insts_mfma"] if k.get("insts_mfma") else None
+    kind, pk = ("F32", "157.3 TFLOP/s (fp32 MFMA)") if f32 else ("BF16", "2.5 PFLOP/s")
+    return {"util": util, "achieved": tflops, "peak": peak, "unit": "TFLOP/s", "dtype": "f32" if f32 else "bf16",
+            "frac": tflops / peak, "util_grbm": k.get("mfma_util"),
+            "flops_per_launch": flops, "mops_per_mfma_inst": mops_inst,
             "valu_insts": k.get("insts_valu"), "mfma_insts": k.get("insts_mfma"),
             "formula": "util = SQ_VALU_MFMA_BUSY_CYCLES / (live launch duration x 2.4 GHz x 1024 SIMDs); "
-                       "frac = SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 / live duration / 2.5 PFLOP/s; util_grbm = busy "
+                       f"frac = SQ_INSTS_VALU_MFMA_MOPS_{kind} x 512 / live duration / {pk}; util_grbm = busy "
                        "cycles / (GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs)"}
 
 
@@ -1237,7 +1248,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="ssd", choices=sorted(WORKLOADS))
-    ap.add_argument("--also", default="gla,rglru,rotlru,ssd_c4,ssd_dh128,gla_dh128",
+    ap.add_argument("--also", default="gla,rglru,rotlru,ssd_c4,ssd_dh128,gla_dh128,ssd_dense,ssd_f32,gla_f32",
                     help="comma-separated extra workloads reported beside (each with its roofline and CPU leg)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the single-token decode step lines")
@@ -1284,7 +1295,11 @@ def main():
     extras = {}
     for nm in [s for s in args.also.split(",") if s and s != args.workload]:
         r = measure(nm, args.steps, args.warmup, dtype, device, cpu_s / 2)
-        extras[nm] = dict(workload=r["workload"], config=r["cfg"], tokens_per_s=r["tokens_per_s"],
+        ecfg = dict(r["cfg"])
+        if ecfg.get("dense") or ecfg.get("dtype") == "f32":
+            ecfg["arithmetic"] = ("per-chunk kernels on the fp32 MFMA (v_mfma_f32_16x16x4_f32): fp32 products "
+                                  "and sums; inputs of the workload's dtype widened to fp32")
+        extras[nm] = dict(workload=r["workload"], config=ecfg, tokens_per_s=r["tokens_per_s"],
                           ms_per_step=r["ms_per_step"], fwd_us=r["fwd_us"], bwd_us=r["bwd_us"],
                           eager_ms_per_step=r["eager_ms_per_step"],
                           roofline=dict(bound="hbm", achieved=r["achieved_gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
