@@ -33,6 +33,10 @@ CASES = [
     ("rglru_gated", dict(B=8, L=4096, D=2560, seg=32)),
     ("rotlru", dict(B=8, L=4096, D=2560, seg=32)),
     ("rotlru_theta", dict(B=8, L=4096, D=2560, seg=32)),
+    # the per-chunk fp32-MFMA kernels: a rate per (head, n), fp32 SSD, fp32 GLA
+    ("ssd", dict(B=3, L=512, H=12, Dh=64, N=16, seg=32, dense=True)),
+    ("ssd", dict(B=3, L=512, H=12, Dh=64, N=16, seg=32, dtype="f32")),
+    ("gla", dict(B=3, L=512, H=12, Dh=64, seg=32, dtype="f32")),
 ]
 MAKERS = {"ssd": bench.make_ssd, "gla": bench.make_gla, "rglru": bench.make_rglru,
           "rglru_gated": bench.make_rglru_gated, "rotlru": bench.make_rotlru,
