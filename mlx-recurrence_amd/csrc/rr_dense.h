@@ -47,14 +47,14 @@ __device__ __forceinline__ float kept_exp(bool keep, float x) {
 // are in flight at once.
 template <int ROWS, int W, int NT = 256>
 struct Slab {
-  static constexpr int N = ROWS * W / NT;
-  static_assert(ROWS * W % NT == 0, "slab must split evenly over the threads");
+  static constexpr int N = (ROWS * W + NT - 1) / NT;   // elements per thread
+  static constexpr bool kExact = ROWS * W % NT == 0;   // else the last pass is partial
   float v[N];
   template <typename T>
   __device__ __forceinline__ void load(const T* src, int64_t stride, int tid) {
 #pragma unroll
     for (int j = 0; j < N; ++j) {
-      const int i = tid + NT * j;
+      const int i = min(tid + NT * j, ROWS * W - 1);   // (partial pass: a duplicate, in bounds, not stored)
       v[j] = rr::ld(src, (int64_t)(i / W) * stride + i % W);
     }
   }
@@ -63,7 +63,7 @@ struct Slab {
   __device__ __forceinline__ void load_t(const T* src, int64_t stride, int tid) {
 #pragma unroll
     for (int j = 0; j < N; ++j) {
-      const int i = tid + NT * j;
+      const int i = min(tid + NT * j, ROWS * W - 1);
       v[j] = rr::ld(src, (int64_t)(i % W) * stride + i / W);
     }
   }
@@ -76,7 +76,7 @@ struct Slab {
 #pragma unroll
     for (int j = 0; j < N; ++j) {
       const int i = tid + NT * j;
-      dst[i / W][i % W] = v[j];
+      if (kExact || i < ROWS * W) dst[i / W][i % W] = v[j];
     }
   }
 };

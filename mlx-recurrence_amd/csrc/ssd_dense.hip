@@ -121,8 +121,9 @@ __device__ __forceinline__ void step_scalars(float dv, float av, float* del, flo
   const bool fast = fac != nullptr && __builtin_amdgcn_readfirstlane(__float_as_int(fac->fast)) != 0;
   const float cm = fac != nullptr ? fac->cm : 0.f;
 #pragma unroll
-  for (int j = 0; j < Q * NS / NT; ++j) {
+  for (int j = 0; j < (Q * NS + NT - 1) / NT; ++j) {
     const int i = tid + NT * j, t = i / NS, n = i % NS;
+    if (Q * NS % NT != 0 && i >= Q * NS) break;
     const float an = a[n], ct = cd[t];
     if (E != nullptr) E[t][n] = __expf(an * ct);
     if (m31 != nullptr) m31[t][n] = __expf(an * (c31 - ct));
@@ -147,8 +148,9 @@ template <int NS, int PN, int PQ, int NT = 256>
 __device__ __forceinline__ void form_w(float (*W)[PQ], const float (*Cm)[PN], const float (*Bm)[PN], const float* cd,
                                        const float* a, int tid) {
 #pragma unroll
-  for (int j = 0; j < Q * Q / NT; ++j) {
+  for (int j = 0; j < (Q * Q + NT - 1) / NT; ++j) {
     const int i = tid + NT * j, t = i / Q, s = i % Q;
+    if (Q * Q % NT != 0 && i >= Q * Q) break;
     const bool keep = t >= s;
     const float dc = cd[t] - cd[s];
     float w = 0.f;
@@ -289,6 +291,122 @@ __global__ __launch_bounds__(256) void dense_out_kernel(DenseArgsT<InT> p) {
   }
 }
 
+// The masked sums of the backward: ZF[s,n] = sum_{t>=s} F_n[t,s] C_t[n], ZW (the
+// same weighted by cd_t - cd_s), dC2[t,n] = sum_{s<=t} F_n[t,s] delta_s B_s[n],
+// and (WITH_W) W of a factored chunk, from G2, the step scalars and (factored)
+// ECt / BEi or (steep) B, C.  S: a gradient kernel's LDS (same member names).
+template <int NS, int NT, int NW, bool WITH_W, class S>
+__device__ __forceinline__ void masked_sums(S& sm, bool fast, int tid, int w, int lane) {
+  constexpr int NBN = NS / 16, W0 = WITH_W ? 4 : 0;
+  if (fast) {
+    // Ef_s^-1 G2m^T ECt, the same with G2m o (cd_t - cd_s), Ef_t G2m (delta BEi):
+    // masked MFMA products (G2m: G2 for t >= s, 0 else; the k-range of a block
+    // skips its all-zero part).  Blocks: W's four, then ZF, ZW, dC2 (2 NBN each).
+    const float cm = sm.fac.cm;
+    for (int blk = w; blk < W0 + 6 * NBN; blk += NW) {
+      if (blk < W0) {
+        form_w_block<NS, S::PN, S::PQ>(sm.W, sm.ECt, sm.BEi, 16 * (blk >> 1), 16 * (blk & 1), lane);
+        continue;
+      }
+      const int kind = (blk - W0) / (2 * NBN), rem = (blk - W0) % (2 * NBN);
+      const int r0 = 16 * (rem / NBN), n0 = 16 * (rem % NBN);
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      const auto ect = [&](int k, int c) { return sm.ECt[k][n0 + c]; };
+      if (kind == 0) {          // ZF, rows s
+        const auto fa = [&](int r, int k) { return k >= r0 + r ? sm.G2[k][r0 + r] : 0.f; };
+        acc = r0 == 0 ? mm16r<0, Q>(fa, ect, lane, acc) : mm16r<16, Q>(fa, ect, lane, acc);
+      } else if (kind == 1) {   // ZW, rows s
+        const auto fa = [&](int r, int k) {
+          const int s = r0 + r;
+          return k >= s ? sm.G2[k][s] * (sm.cd[k] - sm.cd[s]) : 0.f;
+        };
+        acc = r0 == 0 ? mm16r<0, Q>(fa, ect, lane, acc) : mm16r<16, Q>(fa, ect, lane, acc);
+      } else {                  // dC2, rows t
+        const auto fa = [&](int r, int k) { return k <= r0 + r ? sm.G2[r0 + r][k] : 0.f; };
+        const auto fb = [&](int k, int c) { return sm.del[k] * sm.BEi[k][n0 + c]; };
+        acc = r0 == 0 ? mm16r<0, 16>(fa, fb, lane, acc) : mm16r<0, Q>(fa, fb, lane, acc);
+      }
+      const int n = n0 + (lane & 15);
+      const float an = sm.a[n];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = r0 + 4 * (lane >> 4) + r;
+        const float x = an * (sm.cd[row] - cm);
+        if (kind == 0) sm.ZF[row][n] = acc[r] * __expf(-x);
+        else if (kind == 1) sm.ZW[row][n] = acc[r] * __expf(-x);
+        else sm.dC2[row][n] = acc[r] * __expf(x);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int jj = 0; jj < (Q * NS + NT - 1) / NT; ++jj) {
+      const int i = tid + NT * jj, j = i / NS, n = i % NS;
+      if (Q * NS % NT != 0 && i >= Q * NS) break;
+      const float an = sm.a[n], cj = sm.cd[j];
+      float zf = 0.f, zw = 0.f, dc2 = 0.f;
+#pragma unroll 8
+      for (int k = 0; k < Q; ++k) {
+        // ZF, ZW: s = j, t = k; dC2: t = j, s = k
+        const float dk = sm.cd[k] - cj;
+        const float g = sm.G2[k][j] * kept_exp(k >= j, an * dk) * sm.Cm[k][n];
+        zf += g;
+        zw += g * dk;
+        dc2 += sm.G2[j][k] * kept_exp(k <= j, -an * dk) * sm.del[k] * sm.Bm[k][n];
+      }
+      sm.ZF[j][n] = zf;
+      sm.ZW[j][n] = zw;
+      sm.dC2[j][n] = dc2;
+    }
+  }
+}
+
+// The backward's epilogue: dB = delta Z, dC = E GH + dC2, then D[t,n] by
+// scans over t, this chunk's dA and d(delta) (needs ZF, ZW, dC2, GH, UL, tr).
+template <int NS, int NT, int NW, class S, typename InT>
+__device__ __forceinline__ void grad_epilogue(const DenseArgsT<InT>& p, S& sm, const ChunkPos& cp, int tid, int w,
+                                              int lane) {
+  // dB = delta Z, dC = E GH + dC2
+#pragma unroll
+  for (int jj = 0; jj < (Q * NS + NT - 1) / NT; ++jj) {
+    const int i = tid + NT * jj, t = i / NS, n = i % NS;
+    if (Q * NS % NT != 0 && i >= Q * NS) break;
+    const int64_t gi = ((cp.row0 + t) * p.H + cp.h) * NS + n;
+    rr::st(p.dB, gi, sm.del[t] * (sm.ZF[t][n] + sm.m31[t][n] * sm.UL[t][n]));
+    rr::st(p.dC, gi, sm.E[t][n] * sm.GH[t][n] + sm.dC2[t][n]);
+  }
+  // D[t,n] by scans over t (lanes t of a half-wave, one n per half-wave); dA
+  // of this chunk and the per-(wave, half) partials of d(delta)
+  {
+    const int t = lane & (Q - 1), hf = lane >> 5;
+    float ddp = 0.f;
+    for (int n2 = 2 * w; n2 < NS; n2 += 2 * NW) {
+      const int n = n2 + hf;   // NS even: n < NS
+      const float e = sm.E[t][n], c = sm.Cm[t][n], bd = sm.del[t] * sm.Bm[t][n], zf = sm.ZF[t][n];
+      const float x = e * c * sm.GH[t][n];
+      const float rt = c * sm.dC2[t][n] - bd * zf;
+      const float yv = sm.m31[t][n] * bd * sm.UL[t][n];
+      const float px = rr::prefix32_sum(x), pr = rr::prefix32_sum(rt), py = rr::prefix32_sum(yv);
+      const float tx = __shfl(px, 31 + 32 * hf), trr = __shfl(pr, 31 + 32 * hf);
+      const float D = (tx - px + x) + (trr - pr + rt) + sm.E[Q - 1][n] * sm.tr[n] + (py - yv);
+      const float ct = sm.cd[t], c31 = sm.cd[Q - 1];
+      const float da = rr::prefix32_sum(x * ct + yv * (c31 - ct) + bd * sm.ZW[t][n]);
+      if (t == Q - 1)
+        p.gA_part[((int64_t)cp.h * (p.B * p.nC) + (int64_t)cp.b * p.nC + cp.c) * NS + n] =
+            da + c31 * sm.E[Q - 1][n] * sm.tr[n];
+      ddp += sm.a[n] * D + sm.Bm[t][n] * (zf + sm.m31[t][n] * sm.UL[t][n]);
+    }
+    sm.ddp[w][hf][t] = ddp;
+  }
+  __syncthreads();
+  if (tid < Q) {
+    float s = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) s += sm.ddp[ww][0][tid] + sm.ddp[ww][1][tid];
+    rr::st(p.ddelta, (cp.row0 + tid) * p.H + cp.h, s);
+  }
+}
+
+
 // ------------------------------------------------------------------ backward
 // Eight waves per chunk: the LDS of a chunk allows two workgroups per CU, and
 // the phases below are LDS-latency bound, so more waves per workgroup keep the
@@ -388,67 +506,8 @@ __global__ __launch_bounds__(kGradThreads) void dense_grad_kernel(DenseArgsT<InT
     for (int part = 0; part < NT / NS; ++part) s += sm.trp[part][tid];
     sm.tr[tid] = s;
   }
-  // ---- B2: ZF[s,n] = sum_{t>=s} F_n[t,s] C_t[n], ZW (the same weighted by cd_t - cd_s);
-  //          dC2[t,n] = sum_{s<=t} F_n[t,s] delta_s B_s[n]; W of a factored chunk
-  if (fast) {
-    // Ef_s^-1 G2m^T ECt, the same with G2m o (cd_t - cd_s), Ef_t G2m (delta BEi):
-    // masked MFMA products (G2m: G2 for t >= s, 0 else; the k-range of a block
-    // skips its all-zero part).  Blocks: W's four, then ZF, ZW, dC2 (2 NBN each).
-    const float cm = sm.fac.cm;
-    for (int blk = w; blk < 4 + 6 * NBN; blk += NW) {
-      if (blk < 4) {
-        form_w_block<NS, S::PN, S::PQ>(sm.W, sm.ECt, sm.BEi, 16 * (blk >> 1), 16 * (blk & 1), lane);
-        continue;
-      }
-      const int kind = (blk - 4) / (2 * NBN), rem = (blk - 4) % (2 * NBN);
-      const int r0 = 16 * (rem / NBN), n0 = 16 * (rem % NBN);
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-      const auto ect = [&](int k, int c) { return sm.ECt[k][n0 + c]; };
-      if (kind == 0) {          // ZF, rows s
-        const auto fa = [&](int r, int k) { return k >= r0 + r ? sm.G2[k][r0 + r] : 0.f; };
-        acc = r0 == 0 ? mm16r<0, Q>(fa, ect, lane, acc) : mm16r<16, Q>(fa, ect, lane, acc);
-      } else if (kind == 1) {   // ZW, rows s
-        const auto fa = [&](int r, int k) {
-          const int s = r0 + r;
-          return k >= s ? sm.G2[k][s] * (sm.cd[k] - sm.cd[s]) : 0.f;
-        };
-        acc = r0 == 0 ? mm16r<0, Q>(fa, ect, lane, acc) : mm16r<16, Q>(fa, ect, lane, acc);
-      } else {                  // dC2, rows t
-        const auto fa = [&](int r, int k) { return k <= r0 + r ? sm.G2[r0 + r][k] : 0.f; };
-        const auto fb = [&](int k, int c) { return sm.del[k] * sm.BEi[k][n0 + c]; };
-        acc = r0 == 0 ? mm16r<0, 16>(fa, fb, lane, acc) : mm16r<0, Q>(fa, fb, lane, acc);
-      }
-      const int n = n0 + (lane & 15);
-      const float an = sm.a[n];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = r0 + 4 * (lane >> 4) + r;
-        const float x = an * (sm.cd[row] - cm);
-        if (kind == 0) sm.ZF[row][n] = acc[r] * __expf(-x);
-        else if (kind == 1) sm.ZW[row][n] = acc[r] * __expf(-x);
-        else sm.dC2[row][n] = acc[r] * __expf(x);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int jj = 0; jj < Q * NS / NT; ++jj) {
-      const int i = tid + NT * jj, j = i / NS, n = i % NS;
-      const float an = sm.a[n], cj = sm.cd[j];
-      float zf = 0.f, zw = 0.f, dc2 = 0.f;
-#pragma unroll 8
-      for (int k = 0; k < Q; ++k) {
-        // ZF, ZW: s = j, t = k; dC2: t = j, s = k
-        const float dk = sm.cd[k] - cj;
-        const float g = sm.G2[k][j] * kept_exp(k >= j, an * dk) * sm.Cm[k][n];
-        zf += g;
-        zw += g * dk;
-        dc2 += sm.G2[j][k] * kept_exp(k <= j, -an * dk) * sm.del[k] * sm.Bm[k][n];
-      }
-      sm.ZF[j][n] = zf;
-      sm.ZW[j][n] = zw;
-      sm.dC2[j][n] = dc2;
-    }
-  }
+  // ---- B2: the masked sums over s and t (and W of a factored chunk)
+  masked_sums<NS, NT, NW, true>(sm, fast, tid, w, lane);
   __syncthreads();
   // ---- C: du = diag(delta) (W^T dY + (B o m31) lam^T) (MFMA)
   constexpr int NBD = DH / 16;
@@ -465,44 +524,226 @@ __global__ __launch_bounds__(kGradThreads) void dense_grad_kernel(DenseArgsT<InT
       rr::st(p.du, ((cp.row0 + s) * p.H + cp.h) * DH + d0 + (lane & 15), sm.del[s] * acc[r]);
     }
   }
-  // dB = delta Z, dC = E GH + dC2
-#pragma unroll
-  for (int jj = 0; jj < Q * NS / NT; ++jj) {
-    const int i = tid + NT * jj, t = i / NS, n = i % NS;
-    const int64_t gi = ((cp.row0 + t) * p.H + cp.h) * NS + n;
-    rr::st(p.dB, gi, sm.del[t] * (sm.ZF[t][n] + sm.m31[t][n] * sm.UL[t][n]));
-    rr::st(p.dC, gi, sm.E[t][n] * sm.GH[t][n] + sm.dC2[t][n]);
-  }
-  // D[t,n] by scans over t (lanes t of a half-wave, one n per half-wave); dA
-  // of this chunk and the per-(wave, half) partials of d(delta)
-  {
-    const int t = lane & (Q - 1), hf = lane >> 5;
-    float ddp = 0.f;
-    for (int n2 = 2 * w; n2 < NS; n2 += 2 * NW) {
-      const int n = n2 + hf;   // NS even: n < NS
-      const float e = sm.E[t][n], c = sm.Cm[t][n], bd = sm.del[t] * sm.Bm[t][n], zf = sm.ZF[t][n];
-      const float x = e * c * sm.GH[t][n];
-      const float rt = c * sm.dC2[t][n] - bd * zf;
-      const float yv = sm.m31[t][n] * bd * sm.UL[t][n];
-      const float px = rr::prefix32_sum(x), pr = rr::prefix32_sum(rt), py = rr::prefix32_sum(yv);
-      const float tx = __shfl(px, 31 + 32 * hf), trr = __shfl(pr, 31 + 32 * hf);
-      const float D = (tx - px + x) + (trr - pr + rt) + sm.E[Q - 1][n] * sm.tr[n] + (py - yv);
-      const float ct = sm.cd[t], c31 = sm.cd[Q - 1];
-      const float da = rr::prefix32_sum(x * ct + yv * (c31 - ct) + bd * sm.ZW[t][n]);
-      if (t == Q - 1)
-        p.gA_part[((int64_t)cp.h * (p.B * p.nC) + (int64_t)cp.b * p.nC + cp.c) * NS + n] =
-            da + c31 * sm.E[Q - 1][n] * sm.tr[n];
-      ddp += sm.a[n] * D + sm.Bm[t][n] * (zf + sm.m31[t][n] * sm.UL[t][n]);
-    }
-    sm.ddp[w][hf][t] = ddp;
-  }
+  grad_epilogue<NS, NT, NW>(p, sm, cp, tid, w, lane);
+}
+
+// ------------------------------------------------------------------ wide states
+// Dh 128 (and N 64): the chunk's state does not fit the LDS whole, so the
+// output and gradient kernels stream it in blocks of kDB rows of d, staged
+// through registers one block ahead.  Everything indexed by n (B, C, the
+// decays, W, and the gradient's GH, UL, ZF, ZW, dC2) stays resident; the sums
+// over d (Y's state term per block; the gradient's G2 = dY U^T, GH = dY h_in,
+// UL = U lam and tr) accumulate in MFMA accumulators across the blocks, and du
+// is formed block by block.
+constexpr int kDB = 32;                   // rows of d per streamed block
+constexpr int kStreamOutThreads = 256;
+constexpr int kStreamGradThreads = 1024, kStreamGradWaves = kStreamGradThreads / 64;
+
+template <int NS>
+struct alignas(16) OutStreamSmem {
+  static constexpr int PN = NS + 4, PQ = Q + 4, PB = kDB + 4;
+  float Bm[Q][PN], Cm[Q][PN], E[Q][PN], ECt[Q][PN], BEi[Q][PN];
+  float W[Q][PQ];
+  float U[Q][PB];      // u of the block [s][d]
+  float hin[kDB][PN];  // the entering state's rows of the block
+  float del[Q], cd[Q], a[NS];
+  Factor fac;
+};
+
+// The state entering chunk c, rows db * kDB .. + kDB - 1 (checkpoint c - 1,
+// h0 or zero), into a slab.
+template <int DH, int NS, int NT, typename InT>
+__device__ __forceinline__ void load_hin_rows(Slab<kDB, NS, NT>& hs, const DenseArgsT<InT>& p, const ChunkPos& cp,
+                                              int db, int tid) {
+  if (cp.c > 0) hs.load(p.ckpt + (cp.bh * p.nC + cp.c - 1) * DH * NS + db * kDB * NS, NS, tid);
+  else if (p.h0 != nullptr) hs.load(p.h0 + cp.bh * DH * NS + db * kDB * NS, NS, tid);
+  else hs.zero();
+}
+
+template <typename InT, int DH, int NS>
+__global__ __launch_bounds__(kStreamOutThreads) void dense_out_stream_kernel(DenseArgsT<InT> p) {
+  constexpr int NT = kStreamOutThreads, NDB = DH / kDB;
+  using S = OutStreamSmem<NS>;
+  __shared__ S sm;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const ChunkPos cp = chunk_pos(p);
+  const int64_t xoff = (cp.row0 * p.H + cp.h) * DH, voff = (cp.row0 * p.H + cp.h) * NS;
+  Slab<Q, NS, NT> Bv, Cv;
+  Slab<Q, kDB, NT> U;
+  Slab<kDB, NS, NT> Hs;
+  float dv, av;
+  Bv.load(p.Bm + voff, (int64_t)p.H * NS, tid);
+  Cv.load(p.Cm + voff, (int64_t)p.H * NS, tid);
+  U.load(p.u + xoff, (int64_t)p.H * DH, tid);
+  load_hin_rows<DH, NS, NT>(Hs, p, cp, 0, tid);
+  load_step<NS>(p, cp, tid, dv, av);
+  Bv.store(sm.Bm, tid);
+  Cv.store(sm.Cm, tid);
+  step_scalars<NS, S::PN, NT>(dv, av, sm.del, sm.cd, sm.a, &sm.fac, sm.E, nullptr, sm.ECt, sm.BEi, sm.Cm, sm.Bm, tid);
   __syncthreads();
-  if (tid < Q) {
-    float s = 0.f;
+  if (__builtin_amdgcn_readfirstlane(__float_as_int(sm.fac.fast)) != 0)
+    form_w_block<NS, S::PN, S::PQ>(sm.W, sm.ECt, sm.BEi, 16 * (w >> 1), 16 * (w & 1), lane);
+  else
+    form_w<NS, S::PN, S::PQ, NT>(sm.W, sm.Cm, sm.Bm, sm.cd, sm.a, tid);
+  for (int db = 0; db < NDB; ++db) {
+    U.store(sm.U, tid);
+    Hs.store(sm.hin, tid);
+    __syncthreads();   // (also: W, for the first block)
+    if (db + 1 < NDB) {   // the next block's loads, in flight during this one
+      U.load(p.u + xoff + (db + 1) * kDB, (int64_t)p.H * DH, tid);
+      load_hin_rows<DH, NS, NT>(Hs, p, cp, db + 1, tid);
+    }
+    // Y[t][d] = sum_s W[t][s] delta_s U[s][d] + sum_n C[t][n] E[t][n] hin[d][n]:
+    // wave w, block (t0, d0) = (16 (w >> 1), 16 (w & 1)) of the kDB rows
+    {
+      const int t0 = 16 * (w >> 1), d0 = 16 * (w & 1);
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      acc = mm16<Q>([&](int r, int k) { return sm.W[t0 + r][k] * sm.del[k]; },
+                    [&](int k, int c) { return sm.U[k][d0 + c]; }, lane, acc);
+      acc = mm16<NS>([&](int r, int k) { return sm.Cm[t0 + r][k] * sm.E[t0 + r][k]; },
+                     [&](int k, int c) { return sm.hin[d0 + c][k]; }, lane, acc);
 #pragma unroll
-    for (int ww = 0; ww < NW; ++ww) s += sm.ddp[ww][0][tid] + sm.ddp[ww][1][tid];
-    rr::st(p.ddelta, (cp.row0 + tid) * p.H + cp.h, s);
+      for (int r = 0; r < 4; ++r) {
+        const int t = t0 + 4 * (lane >> 4) + r;
+        p.y[((cp.row0 + t) * p.H + cp.h) * DH + db * kDB + d0 + (lane & 15)] = acc[r];
+      }
+    }
+    __syncthreads();   // the next block's stores overwrite U and hin
   }
+}
+
+template <int NS>
+struct alignas(16) GradStreamSmem {
+  static constexpr int PN = NS + 4, PQ = Q + 4, PB = kDB + 4;
+  float Bm[Q][PN], Cm[Q][PN], E[Q][PN], m31[Q][PN], ECt[Q][PN], BEi[Q][PN];
+  float G2[Q][PQ], W[Q][PQ];
+  float GH[Q][PN], UL[Q][PN], ZF[Q][PN], ZW[Q][PN], dC2[Q][PN];
+  float U[Q][PB], G[Q][PB];         // u, dY of the block [t][d]
+  float hin[kDB][PN], lam[kDB][PN];  // the entering state's and the adjoint's rows of the block
+  float del[Q], cd[Q], a[NS], trp[kStreamGradThreads / NS][NS], tr[NS];
+  float ddp[kStreamGradWaves][2][Q];
+  Factor fac;
+};
+
+template <typename InT, int DH, int NS>
+__global__ __launch_bounds__(kStreamGradThreads) void dense_grad_stream_kernel(DenseArgsT<InT> p) {
+  constexpr int NT = kStreamGradThreads, NW = kStreamGradWaves, NDB = DH / kDB, NBN = NS / 16;
+  constexpr int NACC = 4 + 4 * NBN;   // accumulated blocks: G2 (4), GH (2 NBN), UL (2 NBN)
+  static_assert(NACC <= 2 * NW, "two accumulated blocks per wave at most");
+  using S = GradStreamSmem<NS>;
+  __shared__ S sm;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const ChunkPos cp = chunk_pos(p);
+  const int64_t xoff = (cp.row0 * p.H + cp.h) * DH, voff = (cp.row0 * p.H + cp.h) * NS;
+  const int64_t soff = (cp.bh * p.nC + cp.c) * DH * NS;   // this chunk's adjoint slot
+  Slab<Q, NS, NT> Bv, Cv;
+  Slab<Q, kDB, NT> Us, Gs;
+  Slab<kDB, NS, NT> Hs, Ls;
+  float dv, av;
+  Bv.load(p.Bm + voff, (int64_t)p.H * NS, tid);
+  Cv.load(p.Cm + voff, (int64_t)p.H * NS, tid);
+  Us.load(p.u + xoff, (int64_t)p.H * DH, tid);
+  Gs.load(p.dy + xoff, (int64_t)p.H * DH, tid);
+  load_hin_rows<DH, NS, NT>(Hs, p, cp, 0, tid);
+  Ls.load(p.lamws + soff, NS, tid);
+  load_step<NS>(p, cp, tid, dv, av);
+  Bv.store(sm.Bm, tid);
+  Cv.store(sm.Cm, tid);
+  step_scalars<NS, S::PN, NT>(dv, av, sm.del, sm.cd, sm.a, &sm.fac, sm.E, sm.m31, sm.ECt, sm.BEi, sm.Cm, sm.Bm, tid);
+  __syncthreads();
+  const bool fast = __builtin_amdgcn_readfirstlane(__float_as_int(sm.fac.fast)) != 0;
+  // W first: du, formed block by block, needs it
+  if (fast) {
+    if (w < 4) form_w_block<NS, S::PN, S::PQ>(sm.W, sm.ECt, sm.BEi, 16 * (w >> 1), 16 * (w & 1), lane);
+  } else {
+    form_w<NS, S::PN, S::PQ, NT>(sm.W, sm.Cm, sm.Bm, sm.cd, sm.a, tid);
+  }
+  // accumulated blocks of this wave: b = w and w + NW (b < NACC); du blocks of
+  // a d-block (2 row blocks s x 2 column blocks d): waves NW - 4 .. NW - 1
+  f32x4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  float trs = 0.f;   // this thread's share of tr[n], n = tid % NS (NT is a multiple of NS)
+  for (int db = 0; db < NDB; ++db) {
+    Us.store(sm.U, tid);
+    Gs.store(sm.G, tid);
+    Hs.store(sm.hin, tid);
+    Ls.store(sm.lam, tid);
+    __syncthreads();   // (also: W, for the first block)
+    if (db + 1 < NDB) {
+      Us.load(p.u + xoff + (db + 1) * kDB, (int64_t)p.H * DH, tid);
+      Gs.load(p.dy + xoff + (db + 1) * kDB, (int64_t)p.H * DH, tid);
+      load_hin_rows<DH, NS, NT>(Hs, p, cp, db + 1, tid);
+      Ls.load(p.lamws + soff + (db + 1) * kDB * NS, NS, tid);
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int b = w + NW * m;
+      if (b >= NACC) continue;
+      if (b < 4) {   // G2[t][s] += sum_d dY[t][d] U[s][d]
+        const int t0 = 16 * (b >> 1), s0 = 16 * (b & 1);
+        acc[m] = mm16<kDB>([&](int r, int k) { return sm.G[t0 + r][k]; },
+                           [&](int k, int c) { return sm.U[s0 + c][k]; }, lane, acc[m]);
+      } else {
+        const int kind = (b - 4) / (2 * NBN), rem = (b - 4) % (2 * NBN);
+        const int t0 = 16 * (rem / NBN), n0 = 16 * (rem % NBN);
+        if (kind == 0)   // GH[t][n] += sum_d dY[t][d] h_in[d][n]
+          acc[m] = mm16<kDB>([&](int r, int k) { return sm.G[t0 + r][k]; },
+                             [&](int k, int c) { return sm.hin[k][n0 + c]; }, lane, acc[m]);
+        else             // UL[s][n] += sum_d U[s][d] lam[d][n]
+          acc[m] = mm16<kDB>([&](int r, int k) { return sm.U[t0 + r][k]; },
+                             [&](int k, int c) { return sm.lam[k][n0 + c]; }, lane, acc[m]);
+      }
+    }
+    if (w >= NW - 4) {
+      // du[s][d] = delta_s (sum_t W[t][s] dY[t][d] + sum_n B[s][n] m31[s][n] lam[d][n])
+      const int v = w - (NW - 4), s0 = 16 * (v >> 1), d0 = 16 * (v & 1);
+      f32x4_t du = {0.f, 0.f, 0.f, 0.f};
+      du = mm16<Q>([&](int r, int k) { return sm.W[k][s0 + r]; }, [&](int k, int c) { return sm.G[k][d0 + c]; },
+                   lane, du);
+      du = mm16<NS>([&](int r, int k) { return sm.Bm[s0 + r][k] * sm.m31[s0 + r][k]; },
+                    [&](int k, int c) { return sm.lam[d0 + c][k]; }, lane, du);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int s = s0 + 4 * (lane >> 4) + r;
+        rr::st(p.du, ((cp.row0 + s) * p.H + cp.h) * DH + db * kDB + d0 + (lane & 15), sm.del[s] * du[r]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < (kDB * NS + NT - 1) / NT; ++j) {   // tr partials (elements in column tid % NS)
+      const int i = tid + NT * j;
+      if (kDB * NS % NT == 0 || i < kDB * NS) trs += sm.lam[i / NS][i % NS] * sm.hin[i / NS][i % NS];
+    }
+    __syncthreads();   // the next block's stores overwrite the staging
+  }
+  // the accumulated blocks into LDS; tr
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const int b = w + NW * m;
+    if (b >= NACC) continue;
+    if (b < 4) {
+      const int t0 = 16 * (b >> 1), s0 = 16 * (b & 1);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sm.G2[t0 + 4 * (lane >> 4) + r][s0 + (lane & 15)] = acc[m][r];
+    } else {
+      const int kind = (b - 4) / (2 * NBN), rem = (b - 4) % (2 * NBN);
+      const int t0 = 16 * (rem / NBN), n0 = 16 * (rem % NBN);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (kind == 0) sm.GH[t0 + 4 * (lane >> 4) + r][n0 + (lane & 15)] = acc[m][r];
+        else sm.UL[t0 + 4 * (lane >> 4) + r][n0 + (lane & 15)] = acc[m][r];
+      }
+    }
+  }
+  sm.trp[tid / NS][tid % NS] = trs;
+  __syncthreads();
+  if (tid < NS) {
+    float t = 0.f;
+#pragma unroll
+    for (int part = 0; part < NT / NS; ++part) t += sm.trp[part][tid];
+    sm.tr[tid] = t;
+  }
+  masked_sums<NS, NT, NW, false>(sm, fast, tid, w, lane);
+  __syncthreads();
+  grad_epilogue<NS, NT, NW>(p, sm, cp, tid, w, lane);
 }
 
 template <typename InT, int DH, int NS>
@@ -529,11 +770,22 @@ int launch(const rr::DenseArgs& a, int what, hipStream_t s) {
   p.mapP = a.mapP;
   p.B = a.B; p.L = a.L; p.H = a.H; p.DH = a.DH; p.NS = a.NS; p.nC = a.nC;
   const dim3 grid((unsigned)((int64_t)a.B * a.H * a.nC)), blk(256);
+  constexpr bool kStream = DH > 64 || NS > 32;   // the state streamed in blocks of d (wide states)
   switch (what) {
     case rr::kDenseMapsFwd: hipLaunchKernelGGL((dense_map_kernel<InT, DH, NS, false>), grid, blk, 0, s, p); break;
     case rr::kDenseMapsBwd: hipLaunchKernelGGL((dense_map_kernel<InT, DH, NS, true>), grid, blk, 0, s, p); break;
-    case rr::kDenseOut: hipLaunchKernelGGL((dense_out_kernel<InT, DH, NS>), grid, blk, 0, s, p); break;
-    default: hipLaunchKernelGGL((dense_grad_kernel<InT, DH, NS>), grid, dim3(kGradThreads), 0, s, p); break;
+    case rr::kDenseOut:
+      if constexpr (kStream)
+        hipLaunchKernelGGL((dense_out_stream_kernel<InT, DH, NS>), grid, dim3(kStreamOutThreads), 0, s, p);
+      else
+        hipLaunchKernelGGL((dense_out_kernel<InT, DH, NS>), grid, blk, 0, s, p);
+      break;
+    default:
+      if constexpr (kStream)
+        hipLaunchKernelGGL((dense_grad_stream_kernel<InT, DH, NS>), grid, dim3(kStreamGradThreads), 0, s, p);
+      else
+        hipLaunchKernelGGL((dense_grad_kernel<InT, DH, NS>), grid, dim3(kGradThreads), 0, s, p);
+      break;
   }
   return rr::check_launch(what == rr::kDenseOut ? "ssd dense forward" : what == rr::kDenseGrad ? "ssd dense backward"
                                                                                                : "ssd dense chunk maps");
@@ -546,6 +798,10 @@ int launch_shape(const rr::DenseArgs& a, int what, hipStream_t s) {
     case 32032: return launch<InT, 32, 32>(a, what, s);
     case 64016: return launch<InT, 64, 16>(a, what, s);
     case 64032: return launch<InT, 64, 32>(a, what, s);
+    case 64064: return launch<InT, 64, 64>(a, what, s);
+    case 128016: return launch<InT, 128, 16>(a, what, s);
+    case 128032: return launch<InT, 128, 32>(a, what, s);
+    case 128064: return launch<InT, 128, 64>(a, what, s);
     default: return rr::fail(RR_EUNSUPPORTED, "ssd dense: unsupported (Dh, N)");
   }
 }
@@ -555,7 +811,9 @@ int launch_shape(const rr::DenseArgs& a, int what, hipStream_t s) {
 namespace rr {
 
 bool ssd_dense_supported(int64_t T, int64_t Dh, int64_t N, int64_t B, int64_t H, int64_t nC) {
-  return T == Q && (Dh == 32 || Dh == 64) && (N == 16 || N == 32) && B * H * nC < ((int64_t)1 << 31);
+  return T == Q && B * H * nC < ((int64_t)1 << 31) &&
+         (((Dh == 32 || Dh == 64) && (N == 16 || N == 32)) || (Dh == 64 && N == 64) ||
+          (Dh == 128 && (N == 16 || N == 32 || N == 64)));
 }
 
 int ssd_dense_launch(const DenseArgs& a, int dtype, int what, hipStream_t s) {

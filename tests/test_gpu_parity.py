@@ -383,6 +383,13 @@ SSD_CASES = [
     (1, 256, 2, 64, 16, 32, F32, "cliff", True, True, 67),
     (2, 128, 2, 32, 32, 32, BF16, "cliff", True, True, 68),
     (2, 64, 3, 32, 16, 32, F16, "cfg", False, True, 66),    # fp16, per-head rate
+    # wide states (Dh 128, N 64): the output and gradient kernels stream d in blocks
+    (1, 160, 2, 128, 64, 32, F32, "ref", True, True, 69),
+    (2, 96, 2, 128, 16, 32, BF16, "ref", True, True, 70),
+    (1, 128, 3, 128, 32, 32, F16, "cfg", True, True, 71),
+    (1, 192, 2, 64, 64, 32, F32, "ref", True, False, 72),
+    (1, 128, 2, 128, 64, 32, F32, "cliff", True, True, 73),  # steep chunks: an exponential per term
+    (3, 512, 12, 128, 64, 32, F32, "ref", False, True, 74),  # the reference's production shape, its A_neg [H, N]
 ]
 
 
