@@ -450,6 +450,317 @@ __global__ __launch_bounds__(kGlaGradThreads) void gla_grad_kernel(GlaArgsT<InT>
   }
 }
 
+// ------------------------------------------------------------------ wide states
+// Dh 128: the 128 x 128 state is streamed in blocks of kJB rows of j (the value
+// index), staged through registers one block ahead; q, k and the decays stay
+// resident.  The forward forms Y per block; the backward accumulates the sums
+// over j (G2 = dY V^T, GH = dY h_in, UL = V lam, tr) in MFMA accumulators
+// across the blocks and forms dv (with K lam^T) per block; dq, dk and dg follow
+// the loop as in the resident kernel (E and MG formed from CB, G2 and M).
+constexpr int kJB = 32;
+constexpr int kGlaStreamOutThreads = 256;
+constexpr int kGlaStreamGradThreads = 1024, kGlaStreamGradWaves = kGlaStreamGradThreads / 64;
+
+// Rows j0 .. j0 + kJB - 1 of the state entering chunk c, as [j][i].
+template <int D, int NT, typename InT>
+__device__ __forceinline__ void load_entering_rows(Slab<kJB, D, NT>& hs, const GlaArgsT<InT>& p, const ChunkPos& cp,
+                                                   int j0, int tid) {
+  if (cp.c > 0) hs.load(p.ckpt + (cp.bh * p.nC + cp.c - 1) * D * D + (int64_t)j0 * D, D, tid);
+  else if (p.h0 != nullptr) hs.load_t(p.h0 + cp.bh * D * D + j0, D, tid);   // h0 is [i][j]
+  else hs.zero();
+}
+
+template <int D>
+struct alignas(16) GlaOutStreamSmem {
+  static constexpr int PD = D + 4, PQ = Q + 4, PB = kJB + 4;
+  float Qm[Q][PD], K[Q][PD];
+  float M[Q][PQ], P[Q][PQ];
+  float V[Q][PB];       // v of the block [s][j]
+  float hin[kJB][PD];   // the entering state's rows of the block [j][i]
+  float g[Q], gam[Q], gm1[Q], m31[Q];
+};
+
+template <typename InT, int D>
+__global__ __launch_bounds__(kGlaStreamOutThreads) void gla_out_stream_kernel(GlaArgsT<InT> p) {
+  constexpr int NT = kGlaStreamOutThreads, NJB = D / kJB;
+  using S = GlaOutStreamSmem<D>;
+  __shared__ S sm;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const ChunkPos cp = chunk_pos(p.H, p.L, p.nC);
+  const int64_t off = (cp.row0 * p.H + cp.h) * D, stride = (int64_t)p.H * D;
+  Slab<Q, kJB, NT> Vs;
+  Slab<kJB, D, NT> Hs;
+  {
+    Slab<Q, D, NT> Qs, Ks;
+    Qs.load(p.q + off, stride, tid);
+    Ks.load(p.k + off, stride, tid);
+    Vs.load(p.v + off, stride, tid);
+    load_entering_rows<D, NT>(Hs, p, cp, 0, tid);
+    const float gv = rr::ld(p.g, (cp.row0 + (tid & (Q - 1))) * p.H + cp.h);
+    Qs.store(sm.Qm, tid);
+    Ks.store(sm.K, tid);
+    if (tid < Q) sm.g[tid] = gv;
+  }
+  __syncthreads();
+  gate_products<S::PQ>(sm.g, sm.M, sm.gam, sm.gm1, sm.m31, tid);
+  {
+    // P = M o (Q K^T): wave w, block (w >> 1, w & 1) (the upper one is zero)
+    const int t0 = 16 * (w >> 1), s0 = 16 * (w & 1);
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    if (t0 >= s0)
+      acc = mm16<D>([&](int r, int k) { return sm.Qm[t0 + r][k]; }, [&](int k, int c) { return sm.K[s0 + c][k]; },
+                    lane, acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = t0 + 4 * (lane >> 4) + r, s = s0 + (lane & 15);
+      sm.P[t][s] = sm.M[t][s] * acc[r];
+    }
+  }
+  for (int jb = 0; jb < NJB; ++jb) {
+    Vs.store(sm.V, tid);
+    Hs.store(sm.hin, tid);
+    __syncthreads();   // (also: P, for the first block)
+    if (jb + 1 < NJB) {
+      Vs.load(p.v + off + (jb + 1) * kJB, stride, tid);
+      load_entering_rows<D, NT>(Hs, p, cp, (jb + 1) * kJB, tid);
+    }
+    // Y[t][j] = sum_{s <= t} P[t][s] V[s][j] + gam_t sum_i Q[t][i] hin[j][i]:
+    // wave w, block (t0, j0) = (16 (w >> 1), 16 (w & 1)) of the block's rows
+    {
+      const int t0 = 16 * (w >> 1), j0 = 16 * (w & 1);
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      const auto fp = [&](int r, int k) { return sm.P[t0 + r][k]; };
+      const auto fv = [&](int k, int c) { return sm.V[k][j0 + c]; };
+      acc = t0 == 0 ? mm16r<0, 16>(fp, fv, lane, acc) : mm16r<0, Q>(fp, fv, lane, acc);
+      acc = mm16<D>([&](int r, int k) { return sm.gam[t0 + r] * sm.Qm[t0 + r][k]; },
+                    [&](int k, int c) { return sm.hin[j0 + c][k]; }, lane, acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = t0 + 4 * (lane >> 4) + r;
+        p.y[((cp.row0 + t) * p.H + cp.h) * D + jb * kJB + j0 + (lane & 15)] = acc[r];
+      }
+    }
+    __syncthreads();   // the next block's stores overwrite V and hin
+  }
+}
+
+template <int D>
+struct alignas(16) GlaGradStreamSmem {
+  static constexpr int PD = D + 4, PQ = Q + 4, PB = kJB + 4, NIB = D / 16;
+  float Qm[Q][PD], K[Q][PD];
+  float M[Q][PQ], CB[Q][PQ], G2[Q][PQ];
+  float GH[Q][PD], UL[Q][PD];
+  float V[Q][PB], G[Q][PB];              // v, dY of the block [t][j]
+  float hin[kJB][PD], lam[kJB][PD];      // the entering state's and the adjoint's rows of the block [j][i]
+  float g[Q], gam[Q], gm1[Q], m31[Q];
+  float Xp[NIB][Q], Yp[NIB][Q];          // per column-block row sums of GH o Q and UL o K
+  float HpP[2][Q];
+  float trw[kGlaStreamGradWaves];
+};
+
+template <typename InT, int D>
+__global__ __launch_bounds__(kGlaStreamGradThreads) void gla_grad_stream_kernel(GlaArgsT<InT> p) {
+  constexpr int NT = kGlaStreamGradThreads, NW = kGlaStreamGradWaves, NJB = D / kJB, NIB = D / 16;
+  constexpr int NACC = 4 + 4 * NIB;   // accumulated blocks: G2 (4), GH (2 NIB), UL (2 NIB)
+  constexpr int MPW = (NACC + NW - 1) / NW;
+  using S = GlaGradStreamSmem<D>;
+  __shared__ S sm;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l15 = lane & 15, l4 = lane >> 4;
+  const ChunkPos cp = chunk_pos(p.H, p.L, p.nC);
+  const int64_t off = (cp.row0 * p.H + cp.h) * D, stride = (int64_t)p.H * D;
+  const int64_t soff = (cp.bh * p.nC + cp.c) * D * D;   // this chunk's adjoint slot
+  Slab<Q, kJB, NT> Vs, Gs;
+  Slab<kJB, D, NT> Hs, Ls;
+  {
+    Slab<Q, D, NT> Qs, Ks;
+    Qs.load(p.q + off, stride, tid);
+    Ks.load(p.k + off, stride, tid);
+    Vs.load(p.v + off, stride, tid);
+    Gs.load(p.dy + off, stride, tid);
+    load_entering_rows<D, NT>(Hs, p, cp, 0, tid);
+    Ls.load(p.lamws + soff, D, tid);
+    const float gv = rr::ld(p.g, (cp.row0 + (tid & (Q - 1))) * p.H + cp.h);
+    Qs.store(sm.Qm, tid);
+    Ks.store(sm.K, tid);
+    if (tid < Q) sm.g[tid] = gv;
+  }
+  __syncthreads();
+  gate_products<S::PQ>(sm.g, sm.M, sm.gam, sm.gm1, sm.m31, tid);
+  if (w < 4) {   // CB = Q K^T (lower blocks; the upper one is masked everywhere it is used)
+    const int t0 = 16 * (w >> 1), s0 = 16 * (w & 1);
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    if (t0 >= s0)
+      acc = mm16<D>([&](int r, int k) { return sm.Qm[t0 + r][k]; }, [&](int k, int c) { return sm.K[s0 + c][k]; },
+                    lane, acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm.CB[t0 + 4 * l4 + r][s0 + l15] = acc[r];
+  }
+  // accumulated blocks of this wave: b = w + NW m (b < NACC); dv blocks of a
+  // j-block (2 row blocks s x 2 column blocks j): waves NW - 4 .. NW - 1
+  f32x4_t acc[MPW];
+#pragma unroll
+  for (int m = 0; m < MPW; ++m) acc[m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float trs = 0.f;
+  for (int jb = 0; jb < NJB; ++jb) {
+    Vs.store(sm.V, tid);
+    Gs.store(sm.G, tid);
+    Hs.store(sm.hin, tid);
+    Ls.store(sm.lam, tid);
+    __syncthreads();   // (also: CB, for the first block)
+    if (jb + 1 < NJB) {
+      Vs.load(p.v + off + (jb + 1) * kJB, stride, tid);
+      Gs.load(p.dy + off + (jb + 1) * kJB, stride, tid);
+      load_entering_rows<D, NT>(Hs, p, cp, (jb + 1) * kJB, tid);
+      Ls.load(p.lamws + soff + (int64_t)(jb + 1) * kJB * D, D, tid);
+    }
+#pragma unroll
+    for (int m = 0; m < MPW; ++m) {
+      const int b = w + NW * m;
+      if (b >= NACC) continue;
+      if (b < 4) {   // G2[t][s] += sum_j dY[t][j] V[s][j]
+        const int t0 = 16 * (b >> 1), s0 = 16 * (b & 1);
+        if (t0 >= s0)
+          acc[m] = mm16<kJB>([&](int r, int k) { return sm.G[t0 + r][k]; },
+                             [&](int k, int c) { return sm.V[s0 + c][k]; }, lane, acc[m]);
+      } else {
+        const int kind = (b - 4) / (2 * NIB), rem = (b - 4) % (2 * NIB);
+        const int t0 = 16 * (rem / NIB), i0 = 16 * (rem % NIB);
+        if (kind == 0)   // GH[t][i] += sum_j dY[t][j] h_in[j][i]
+          acc[m] = mm16<kJB>([&](int r, int k) { return sm.G[t0 + r][k]; },
+                             [&](int k, int c) { return sm.hin[k][i0 + c]; }, lane, acc[m]);
+        else             // UL[s][i] += sum_j V[s][j] lam[j][i]
+          acc[m] = mm16<kJB>([&](int r, int k) { return sm.V[t0 + r][k]; },
+                             [&](int k, int c) { return sm.lam[k][i0 + c]; }, lane, acc[m]);
+      }
+    }
+    if (w >= NW - 4) {
+      // dv[s][j] = sum_{t >= s} M[t][s] CB[t][s] dY[t][j] + m31_s sum_i K[s][i] lam[j][i]
+      const int v = w - (NW - 4), s0 = 16 * (v >> 1), j0 = 16 * (v & 1);
+      f32x4_t dv = {0.f, 0.f, 0.f, 0.f};
+      const auto fa = [&](int r, int k) { return sm.M[k][s0 + r] * sm.CB[k][s0 + r]; };
+      const auto fb = [&](int k, int c) { return sm.G[k][j0 + c]; };
+      dv = s0 == 0 ? mm16r<0, Q>(fa, fb, lane, dv) : mm16r<16, Q>(fa, fb, lane, dv);
+      f32x4_t kl = {0.f, 0.f, 0.f, 0.f};
+      kl = mm16<D>([&](int r, int k) { return sm.K[s0 + r][k]; }, [&](int k, int c) { return sm.lam[j0 + c][k]; },
+                   lane, kl);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int s = s0 + 4 * l4 + r;
+        rr::st(p.dv, ((cp.row0 + s) * p.H + cp.h) * D + jb * kJB + j0 + l15, dv[r] + sm.m31[s] * kl[r]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < (kJB * D + NT - 1) / NT; ++j) {   // tr = sum lam o h_in
+      const int i = tid + NT * j;
+      if (kJB * D % NT == 0 || i < kJB * D) trs += sm.lam[i / D][i % D] * sm.hin[i / D][i % D];
+    }
+    __syncthreads();   // the next block's stores overwrite the staging
+  }
+  // the accumulated blocks into LDS, with the X / Y row-sum partials
+#pragma unroll
+  for (int m = 0; m < MPW; ++m) {
+    const int b = w + NW * m;
+    if (b >= NACC) continue;
+    if (b < 4) {
+      const int t0 = 16 * (b >> 1), s0 = 16 * (b & 1);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sm.G2[t0 + 4 * l4 + r][s0 + l15] = acc[m][r];
+    } else {
+      const int kind = (b - 4) / (2 * NIB), rem = (b - 4) % (2 * NIB);
+      const int t0 = 16 * (rem / NIB), ib = rem % NIB, i0 = 16 * ib;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = t0 + 4 * l4 + r;
+        if (kind == 0) {
+          sm.GH[t][i0 + l15] = acc[m][r];
+          const float x = rr::row16_sum(acc[m][r] * sm.Qm[t][i0 + l15]);
+          if (l15 == 0) sm.Xp[ib][t] = x;
+        } else {
+          sm.UL[t][i0 + l15] = acc[m][r];
+          const float y = rr::row16_sum(acc[m][r] * sm.K[t][i0 + l15]);
+          if (l15 == 0) sm.Yp[ib][t] = y;
+        }
+      }
+    }
+  }
+  {
+    const float t = rr::wave_sum(trs);
+    if (lane == 0) sm.trw[w] = t;
+  }
+  __syncthreads();
+  // dq[t][i] = gam_t GH[t][i] + sum_{s <= t} M[t][s] G2[t][s] K[s][i];
+  // dk[s][i] = sum_{t >= s} M[t][s] G2[t][s] Q[t][i] + m31_s UL[s][i];
+  // then the dg column sums of W2 = E Mh (E = CB o G2): blocks 0 .. 4 NIB + 2
+  for (int blk = w; blk < 4 * NIB + 3; blk += NW) {
+    if (blk < 4 * NIB) {
+      const int kind = blk / (2 * NIB), rem = blk % (2 * NIB);
+      const int r0 = 16 * (rem / NIB), i0 = 16 * (rem % NIB);
+      f32x4_t a4 = {0.f, 0.f, 0.f, 0.f};
+      if (kind == 0) {
+        const auto fa = [&](int r, int k) { return sm.M[r0 + r][k] * sm.G2[r0 + r][k]; };
+        const auto fb = [&](int k, int c) { return sm.K[k][i0 + c]; };
+        a4 = r0 == 0 ? mm16r<0, 16>(fa, fb, lane, a4) : mm16r<0, Q>(fa, fb, lane, a4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = r0 + 4 * l4 + r;
+          rr::st(p.dq, ((cp.row0 + t) * p.H + cp.h) * D + i0 + l15, a4[r] + sm.gam[t] * sm.GH[t][i0 + l15]);
+        }
+      } else {
+        const auto fa = [&](int r, int k) { return sm.M[k][r0 + r] * sm.G2[k][r0 + r]; };
+        const auto fb = [&](int k, int c) { return sm.Qm[k][i0 + c]; };
+        a4 = r0 == 0 ? mm16r<0, Q>(fa, fb, lane, a4) : mm16r<16, Q>(fa, fb, lane, a4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int s = r0 + 4 * l4 + r;
+          rr::st(p.dk, ((cp.row0 + s) * p.H + cp.h) * D + i0 + l15, a4[r] + sm.m31[s] * sm.UL[s][i0 + l15]);
+        }
+      }
+    } else {
+      // W2[t'][t] = sum_{s < t} E[t'][s] M[t-1][s]; column sums over t' of
+      // M[t'][t] (W2 + X[t'] gam_{t-1}) for rows tp0 .. tp0 + 15
+      const int v = blk - 4 * NIB, tp0 = v == 0 ? 0 : 16, t0 = v == 2 ? 16 : 0;
+      f32x4_t a4 = {0.f, 0.f, 0.f, 0.f};
+      const auto fa = [&](int r, int k) { return sm.CB[tp0 + r][k] * sm.G2[tp0 + r][k]; };
+      const auto fb = [&](int k, int c) {
+        const int t = t0 + c;
+        return k < t ? sm.M[t - 1][k] : 0.f;
+      };
+      a4 = t0 == 0 ? mm16r<0, 16>(fa, fb, lane, a4) : mm16r<0, Q>(fa, fb, lane, a4);
+      const int t = t0 + l15;
+      float cs = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tp = tp0 + 4 * l4 + r;
+        float x = 0.f;
+#pragma unroll
+        for (int ib = 0; ib < NIB; ++ib) x += sm.Xp[ib][tp];
+        cs += sm.M[tp][t] * (a4[r] + x * sm.gm1[t]);
+      }
+      cs += __shfl_xor(cs, 16);
+      cs += __shfl_xor(cs, 32);
+      if (l4 == 0) sm.HpP[tp0 / 16][t] = cs;
+    }
+  }
+  __syncthreads();
+  // dg_t = the column sums + m31_t (P_t + gam_{t-1} tr), P_t = sum_{s < t} M[t-1][s] Y_s
+  if (tid < Q) {
+    const int t = tid;
+    float tr = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) tr += sm.trw[ww];
+    float pt = 0.f;
+    for (int s = 0; s < t; ++s) {
+      float y = 0.f;
+#pragma unroll
+      for (int ib = 0; ib < NIB; ++ib) y += sm.Yp[ib][s];
+      pt += sm.M[t - 1][s] * y;
+    }
+    const float hp = (t < 16 ? sm.HpP[0][t] : 0.f) + sm.HpP[1][t];
+    rr::st(p.dg, (cp.row0 + t) * p.H + cp.h, hp + sm.m31[t] * (pt + sm.gm1[t] * tr));
+  }
+}
+
 template <typename InT, int D>
 int launch(const rr::GlaDenseArgs& a, int what, hipStream_t s) {
   GlaArgsT<InT> p;
@@ -473,8 +784,18 @@ int launch(const rr::GlaDenseArgs& a, int what, hipStream_t s) {
   switch (what) {
     case rr::kDenseMapsFwd: hipLaunchKernelGGL((gla_map_kernel<InT, D, false>), grid, dim3(256), 0, s, p); break;
     case rr::kDenseMapsBwd: hipLaunchKernelGGL((gla_map_kernel<InT, D, true>), grid, dim3(256), 0, s, p); break;
-    case rr::kDenseOut: hipLaunchKernelGGL((gla_out_kernel<InT, D>), grid, dim3(256), 0, s, p); break;
-    default: hipLaunchKernelGGL((gla_grad_kernel<InT, D>), grid, dim3(kGlaGradThreads), 0, s, p); break;
+    case rr::kDenseOut:
+      if constexpr (D > 64)
+        hipLaunchKernelGGL((gla_out_stream_kernel<InT, D>), grid, dim3(kGlaStreamOutThreads), 0, s, p);
+      else
+        hipLaunchKernelGGL((gla_out_kernel<InT, D>), grid, dim3(256), 0, s, p);
+      break;
+    default:
+      if constexpr (D > 64)
+        hipLaunchKernelGGL((gla_grad_stream_kernel<InT, D>), grid, dim3(kGlaStreamGradThreads), 0, s, p);
+      else
+        hipLaunchKernelGGL((gla_grad_kernel<InT, D>), grid, dim3(kGlaGradThreads), 0, s, p);
+      break;
   }
   return rr::check_launch(what == rr::kDenseOut    ? "gla dense forward"
                           : what == rr::kDenseGrad ? "gla dense backward"
@@ -486,6 +807,7 @@ int launch_shape(const rr::GlaDenseArgs& a, int what, hipStream_t s) {
   switch (a.D) {
     case 32: return launch<InT, 32>(a, what, s);
     case 64: return launch<InT, 64>(a, what, s);
+    case 128: return launch<InT, 128>(a, what, s);
     default: return rr::fail(RR_EUNSUPPORTED, "gla dense: unsupported Dh");
   }
 }
@@ -495,7 +817,7 @@ int launch_shape(const rr::GlaDenseArgs& a, int what, hipStream_t s) {
 namespace rr {
 
 bool gla_dense_supported(int64_t T, int64_t Dh, int64_t B, int64_t H, int64_t nC) {
-  return T == Q && (Dh == 32 || Dh == 64) && B * H * nC < ((int64_t)1 << 31);
+  return T == Q && (Dh == 32 || Dh == 64 || Dh == 128) && B * H * nC < ((int64_t)1 << 31);
 }
 
 int gla_dense_launch(const GlaDenseArgs& a, int dtype, int what, hipStream_t s) {

@@ -518,6 +518,10 @@ GLA_CASES = [
     (2, 192, 3, 32, 32, F16, "zeros", True, True, 56),      # zero gates cut the recurrence
     (1, 1280, 2, 32, 32, F32, "ref", True, False, 57),      # 40 chunks: the walk past its read-ahead
     (3, 512, 12, 64, 32, F32, "cfg", False, True, 58),      # BASELINE config 2's shape, fp32
+    # Dh 128 (a 128 x 128 state): output and gradient kernels stream j in blocks
+    (1, 160, 2, 128, 32, F32, "signed", True, True, 59),
+    (2, 96, 2, 128, 32, F16, "zeros", True, True, 60),
+    (3, 512, 12, 128, 32, F32, "ref", True, True, 61),      # the reference's production shape, fp32
 ]
 
 
