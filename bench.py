@@ -577,6 +577,10 @@ WORKLOADS = {
     "gla_f32": ("gla_scan fwd+bwd, fp32 inputs (BASELINE config 2 shape)", make_gla,
                 dict(B=3, L=512, H=12, Dh=64, seg=32, dtype="f32")),
     "gla_dh128": ("gla_scan fwd+bwd at Dh 128 (B3 L512 H12)", make_gla, dict(B=3, L=512, H=12, Dh=128, seg=32)),
+    "ssd_dense_dh128": ("ssd_scan fwd+bwd, dense A_neg [H, N], at Dh 128, N 64 (B3 L512 H12)", make_ssd,
+                        dict(B=3, L=512, H=12, Dh=128, N=64, seg=32, dense=True)),
+    "gla_f32_dh128": ("gla_scan fwd+bwd, fp32 inputs, at Dh 128 (B3 L512 H12)", make_gla,
+                      dict(B=3, L=512, H=12, Dh=128, seg=32, dtype="f32")),
     "ssd_b96": ("ssd_scan fwd+bwd (BASELINE config 1 shape, B = 96)", make_ssd,
                 dict(B=96, L=512, H=12, Dh=64, N=16, seg=32)),
     "gla_b96": ("gla_scan fwd+bwd (BASELINE config 2 shape, B = 96)", make_gla,
@@ -880,7 +884,8 @@ CALIBRATIONS = {"copy": ("fetch", "write"), "sector": ("fetch", "write"), "gemm"
 CAL_MB = 256          # copy / sector read source size
 CAL_GEMM = 8192       # M = N = K of the calibration GEMM
 PROFILED_WORKLOADS = ["ssd", "gla", "rglru", "rotlru", "ssd_c4", "ssd_dh128", "gla_dh128", "rglru_gated",
-                      "rotlru_theta", "ssd_b96", "gla_b96", "ssd_dense", "ssd_f32", "gla_f32", "gdn"]
+                      "rotlru_theta", "ssd_b96", "gla_b96", "ssd_dense", "ssd_f32", "gla_f32", "ssd_dense_dh128",
+                      "gla_f32_dh128", "gdn"]
 PROFILE_COMMANDS = [
     "rocprofv3 --kernel-trace --stats -d $R/gpurun_out/prof_trace -o trace --output-format csv -- "
     "python3 bench.py --steps 20 --warmup 3 --no-cpu --no-decode --also " + ",".join(PROFILED_WORKLOADS[1:]),
@@ -1248,7 +1253,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="ssd", choices=sorted(WORKLOADS))
-    ap.add_argument("--also", default="gla,rglru,rotlru,ssd_c4,ssd_dh128,gla_dh128,ssd_dense,ssd_f32,gla_f32",
+    ap.add_argument("--also", default="gla,rglru,rotlru,ssd_c4,ssd_dh128,gla_dh128,ssd_dense,ssd_f32,gla_f32,"
+                                      "ssd_dense_dh128,gla_f32_dh128",
                     help="comma-separated extra workloads reported beside (each with its roofline and CPU leg)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the single-token decode step lines")
