@@ -37,6 +37,9 @@ CASES = [
     ("ssd", dict(B=3, L=512, H=12, Dh=64, N=16, seg=32, dense=True)),
     ("ssd", dict(B=3, L=512, H=12, Dh=64, N=16, seg=32, dtype="f32")),
     ("gla", dict(B=3, L=512, H=12, Dh=64, seg=32, dtype="f32")),
+    # the same at the reference's published shape (wide states: d streamed in blocks)
+    ("ssd", dict(B=3, L=512, H=12, Dh=128, N=64, seg=32, dense=True)),
+    ("gla", dict(B=3, L=512, H=12, Dh=128, seg=32, dtype="f32")),
 ]
 MAKERS = {"ssd": bench.make_ssd, "gla": bench.make_gla, "rglru": bench.make_rglru,
           "rglru_gated": bench.make_rglru_gated, "rotlru": bench.make_rotlru,
