@@ -104,7 +104,9 @@ size_t rr_ssd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t Dh, int64
  * this call write or read: the library walks the grids of the pass's kernels
  * with their own workgroup decode and slot arithmetic.  For tests that the
  * kernels stay inside rr_ssd_workspace_bytes.  No reference counterpart.
- * Returns -1 for invalid arguments or a call that runs on the VALU engine. */
+ * Returns -1 for invalid arguments or a call that the chunked bf16 kernels do
+ * not run (the fp32-MFMA and VALU paths carve fixed regions of the size
+ * rr_ssd_workspace_bytes returns). */
 int64_t rr_ssd_workspace_extent(int64_t B, int64_t L, int64_t H, int64_t Dh, int64_t N, int64_t seg,
                                 int64_t A_stride_n, int dtype, int pass);
 

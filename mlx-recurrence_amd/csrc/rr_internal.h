@@ -136,11 +136,13 @@ struct DenseArgs {
 };
 enum DenseKernel { kDenseMapsFwd = 0, kDenseMapsBwd = 1, kDenseOut = 2, kDenseGrad = 3 };
 // True when the chunk kernels cover the call: checkpoint interval T = 32,
-// Dh in {32, 64}, N in {16, 32}, and a 1-D grid of one workgroup per chunk.
+// Dh in {32, 64} with N in {16, 32}, Dh 64 with N 64, or Dh 128 with N in
+// {16, 32, 64} (the wide ones streamed in blocks of d), and a 1-D grid of one
+// workgroup per chunk.
 bool ssd_dense_supported(int64_t T, int64_t Dh, int64_t N, int64_t B, int64_t H, int64_t nC);
 int ssd_dense_launch(const DenseArgs& a, int dtype, int what, hipStream_t s);
 // GLA for fp32 / fp16 inputs (and bf16 where the chunked kernels do not run),
-// T = 32, Dh in {32, 64} (gla_dense.hip): the same three-kernel scheme, the
+// T = 32, Dh in {32, 64, 128} (gla_dense.hip): the same three-kernel scheme, the
 // maps in the layout dense_compose walks (mapP: gam_31 in every column).
 struct GlaDenseArgs {
   const void* q;

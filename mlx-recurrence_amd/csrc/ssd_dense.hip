@@ -34,17 +34,19 @@
 // (Derived from the per-step adjoint and checked in float64 against the oracle
 // before this code; the GPU parity tests check it against the oracle.)
 //
-// Work split: a workgroup of four waves per chunk, in three kernels per pass
-// (chunk maps; the walk over them, one thread per state element; every
-// chunk's outputs or gradients).  Each workgroup issues all of its global
-// loads before it writes any of them to LDS (one memory latency per chunk, not
-// one per staged row).  The inputs and the
-// intermediates live in LDS as fp32, and the contractions run on the fp32 MFMA
-// (fp32 products and sums: fp32 inputs keep fp32 accuracy, where a bf16 hi + lo
-// operand split would leave ~2^-18 per product).  The per-n masked sums W, ZF and dC2
-// run on the VALU, one thread per output element, with the decay of each
-// (t, s, n) formed by its own exponential (exact for any rate and step size:
-// no rescaled factors that could overflow).
+// Work split: one workgroup per chunk, three kernels per pass (chunk maps;
+// the walk over them, one thread per state element; every chunk's outputs or
+// gradients: four waves for the maps and outputs, eight for the gradients,
+// sixteen for the gradients of wide states).  Each workgroup issues all of its
+// global loads before it writes any of them to LDS (one memory latency per
+// chunk, not one per staged row).  The inputs and the intermediates live in
+// LDS as fp32, and the contractions run on the fp32 MFMA (fp32 products and
+// sums: fp32 inputs keep fp32 accuracy, where a bf16 hi + lo operand split
+// would leave ~2^-18 per product).  The per-n masked sums W, ZF, ZW and dC2 are
+// masked MFMA products of the factored decays where the chunk's factors stay
+// in range, and VALU sums with an exponential per (t, s, n) in steep chunks
+// (see Factor below).  Wide states (Dh 128, N 64) stream d in blocks (see the
+// wide-state kernels at the end).
 #include "rr_common.h"
 #include "rr_dense.h"
 #include "rr_internal.h"

@@ -153,9 +153,9 @@ def tile_schedule(scan: int, pass_: int, B: int, L: int, D: int, seg: int, dtype
 
 def ssd_workspace_extent(B: int, L: int, H: int, Dh: int, N: int, seg: int, a_stride_n: int, dtype: int,
                          pass_: int) -> int:
-    """One past the largest workspace byte the chunked SSD kernels of a pass
-    touch (walked over their grids by the library), or -1 where the call runs
-    on the VALU engine."""
+    """One past the largest workspace byte the chunked (bf16) SSD kernels of a
+    pass touch (walked over their grids by the library), or -1 where the call
+    runs on the fp32-MFMA or VALU paths (fixed workspace regions)."""
     return int(load().rr_ssd_workspace_extent(B, L, H, Dh, N, seg, a_stride_n, dtype, pass_))
 
 
