@@ -98,13 +98,18 @@ struct alignas(16) GlaMapSmem {
   float g[Q], w[Q], tot;
 };
 
+// Workgroup size of the map and output kernels: eight waves (the chunk's
+// 16 x 16 output blocks spread over more waves).
+constexpr int kGlaSmallThreads = 512, kGlaSmallWaves = kGlaSmallThreads / 64;
+
 template <typename InT, int D, bool BWD>
-__global__ __launch_bounds__(256) void gla_map_kernel(GlaArgsT<InT> p) {
+__global__ __launch_bounds__(kGlaSmallThreads) void gla_map_kernel(GlaArgsT<InT> p) {
+  constexpr int NT = kGlaSmallThreads, NW = kGlaSmallWaves;
   __shared__ GlaMapSmem<D> sm;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const ChunkPos cp = chunk_pos(p.H, p.L, p.nC);
   const int64_t off = (cp.row0 * p.H + cp.h) * D, stride = (int64_t)p.H * D;
-  Slab<Q, D> X, Y;
+  Slab<Q, D, NT> X, Y;
   if constexpr (BWD) {
     X.load(p.dy + off, stride, tid);
     Y.load(p.q + off, stride, tid);
@@ -130,7 +135,7 @@ __global__ __launch_bounds__(256) void gla_map_kernel(GlaArgsT<InT> p) {
   __syncthreads();
   constexpr int NB = D / 16;
   float* dst = p.mapE + (cp.bh * p.nC + cp.c) * D * D;
-  for (int blk = w; blk < NB * NB; blk += 4) {
+  for (int blk = w; blk < NB * NB; blk += NW) {
     const int j0 = 16 * (blk / NB), i0 = 16 * (blk % NB);
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
     acc = mm16<Q>([&](int r, int k) { return sm.X[k][j0 + r]; },
@@ -152,19 +157,20 @@ struct alignas(16) GlaOutSmem {
 };
 
 template <typename InT, int D>
-__global__ __launch_bounds__(256) void gla_out_kernel(GlaArgsT<InT> p) {
+__global__ __launch_bounds__(kGlaSmallThreads) void gla_out_kernel(GlaArgsT<InT> p) {
+  constexpr int NT = kGlaSmallThreads, NW = kGlaSmallWaves;
   using S = GlaOutSmem<D>;
   __shared__ S sm;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const ChunkPos cp = chunk_pos(p.H, p.L, p.nC);
   const int64_t off = (cp.row0 * p.H + cp.h) * D, stride = (int64_t)p.H * D;
   {
-    Slab<Q, D> Qs, Ks, Vs;
-    Slab<D, D> Hs;
+    Slab<Q, D, NT> Qs, Ks, Vs;
+    Slab<D, D, NT> Hs;
     Qs.load(p.q + off, stride, tid);
     Ks.load(p.k + off, stride, tid);
     Vs.load(p.v + off, stride, tid);
-    load_entering<D, 256>(Hs, p, cp, tid);
+    load_entering<D, NT>(Hs, p, cp, tid);
     const float gv = rr::ld(p.g, (cp.row0 + (tid & (Q - 1))) * p.H + cp.h);
     Qs.store(sm.Qm, tid);
     Ks.store(sm.K, tid);
@@ -174,7 +180,7 @@ __global__ __launch_bounds__(256) void gla_out_kernel(GlaArgsT<InT> p) {
   }
   __syncthreads();
   gate_products<S::PQ>(sm.g, sm.M, sm.gam, sm.gm1, sm.m31, tid);
-  {
+  if (w < 4) {
     // P = M o (Q K^T): wave w, block (w >> 1, w & 1) (the upper one is zero)
     const int t0 = 16 * (w >> 1), s0 = 16 * (w & 1);
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -190,7 +196,7 @@ __global__ __launch_bounds__(256) void gla_out_kernel(GlaArgsT<InT> p) {
   __syncthreads();
   // Y[t][j] = sum_{s <= t} P[t][s] V[s][j] + gam_t sum_i Q[t][i] hin[j][i]
   constexpr int NB = D / 16;
-  for (int blk = w; blk < 2 * NB; blk += 4) {
+  for (int blk = w; blk < 2 * NB; blk += NW) {
     const int t0 = 16 * (blk / NB), j0 = 16 * (blk % NB);
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
     const auto fp = [&](int r, int k) { return sm.P[t0 + r][k]; };
@@ -782,13 +788,17 @@ int launch(const rr::GlaDenseArgs& a, int what, hipStream_t s) {
   p.B = a.B; p.L = a.L; p.H = a.H; p.nC = a.nC;
   const dim3 grid((unsigned)((int64_t)a.B * a.H * a.nC));
   switch (what) {
-    case rr::kDenseMapsFwd: hipLaunchKernelGGL((gla_map_kernel<InT, D, false>), grid, dim3(256), 0, s, p); break;
-    case rr::kDenseMapsBwd: hipLaunchKernelGGL((gla_map_kernel<InT, D, true>), grid, dim3(256), 0, s, p); break;
+    case rr::kDenseMapsFwd:
+      hipLaunchKernelGGL((gla_map_kernel<InT, D, false>), grid, dim3(kGlaSmallThreads), 0, s, p);
+      break;
+    case rr::kDenseMapsBwd:
+      hipLaunchKernelGGL((gla_map_kernel<InT, D, true>), grid, dim3(kGlaSmallThreads), 0, s, p);
+      break;
     case rr::kDenseOut:
       if constexpr (D > 64)
         hipLaunchKernelGGL((gla_out_stream_kernel<InT, D>), grid, dim3(kGlaStreamOutThreads), 0, s, p);
       else
-        hipLaunchKernelGGL((gla_out_kernel<InT, D>), grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL((gla_out_kernel<InT, D>), grid, dim3(kGlaSmallThreads), 0, s, p);
       break;
     default:
       if constexpr (D > 64)

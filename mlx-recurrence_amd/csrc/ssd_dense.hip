@@ -247,16 +247,18 @@ struct alignas(16) OutSmem {
   Factor fac;
 };
 
+constexpr int kOutThreads = 512, kOutWaves = kOutThreads / 64;   // eight waves: the Y blocks spread out
 template <typename InT, int DH, int NS>
-__global__ __launch_bounds__(256) void dense_out_kernel(DenseArgsT<InT> p) {
+__global__ __launch_bounds__(kOutThreads) void dense_out_kernel(DenseArgsT<InT> p) {
+  constexpr int NT = kOutThreads, NW = kOutWaves;
   using S = OutSmem<DH, NS>;
   __shared__ S sm;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const ChunkPos cp = chunk_pos(p);
   const int64_t xoff = (cp.row0 * p.H + cp.h) * DH, voff = (cp.row0 * p.H + cp.h) * NS;
-  Slab<Q, DH> U;
-  Slab<Q, NS> Bv, Cv;
-  Slab<DH, NS> Hs;   // the state entering the chunk: checkpoint c - 1, h0 or zero
+  Slab<Q, DH, NT> U;
+  Slab<Q, NS, NT> Bv, Cv;
+  Slab<DH, NS, NT> Hs;   // the state entering the chunk: checkpoint c - 1, h0 or zero
   float dv, av;
   U.load(p.u + xoff, (int64_t)p.H * DH, tid);
   Bv.load(p.Bm + voff, (int64_t)p.H * NS, tid);
@@ -269,16 +271,17 @@ __global__ __launch_bounds__(256) void dense_out_kernel(DenseArgsT<InT> p) {
   Bv.store(sm.Bm, tid);
   Cv.store(sm.Cm, tid);
   Hs.store(sm.hin, tid);
-  step_scalars<NS, S::PN>(dv, av, sm.del, sm.cd, sm.a, &sm.fac, sm.E, nullptr, sm.ECt, sm.BEi, sm.Cm, sm.Bm, tid);
+  step_scalars<NS, S::PN, NT>(dv, av, sm.del, sm.cd, sm.a, &sm.fac, sm.E, nullptr, sm.ECt, sm.BEi, sm.Cm, sm.Bm, tid);
   __syncthreads();
-  if (__builtin_amdgcn_readfirstlane(__float_as_int(sm.fac.fast)) != 0)
-    form_w_block<NS, S::PN, S::PQ>(sm.W, sm.ECt, sm.BEi, 16 * (w >> 1), 16 * (w & 1), lane);
-  else
-    form_w<NS, S::PN, S::PQ>(sm.W, sm.Cm, sm.Bm, sm.cd, sm.a, tid);
+  if (__builtin_amdgcn_readfirstlane(__float_as_int(sm.fac.fast)) != 0) {
+    if (w < 4) form_w_block<NS, S::PN, S::PQ>(sm.W, sm.ECt, sm.BEi, 16 * (w >> 1), 16 * (w & 1), lane);
+  } else {
+    form_w<NS, S::PN, S::PQ, NT>(sm.W, sm.Cm, sm.Bm, sm.cd, sm.a, tid);
+  }
   __syncthreads();
   // Y [t][d] = sum_s W[t][s] delta_s U[s][d] + sum_n C[t][n] E[t][n] hin[d][n]
   constexpr int NBD = DH / 16;
-  for (int blk = w; blk < 2 * NBD; blk += 4) {
+  for (int blk = w; blk < 2 * NBD; blk += NW) {
     const int t0 = 16 * (blk / NBD), d0 = 16 * (blk % NBD);
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
     acc = mm16<Q>([&](int r, int k) { return sm.W[t0 + r][k] * sm.del[k]; },
@@ -780,7 +783,7 @@ int launch(const rr::DenseArgs& a, int what, hipStream_t s) {
       if constexpr (kStream)
         hipLaunchKernelGGL((dense_out_stream_kernel<InT, DH, NS>), grid, dim3(kStreamOutThreads), 0, s, p);
       else
-        hipLaunchKernelGGL((dense_out_kernel<InT, DH, NS>), grid, blk, 0, s, p);
+        hipLaunchKernelGGL((dense_out_kernel<InT, DH, NS>), grid, dim3(kOutThreads), 0, s, p);
       break;
     default:
       if constexpr (kStream)
