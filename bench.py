@@ -13,7 +13,10 @@ captured in a HIP graph (G consecutive steps per graph, G the largest divisor
 of K up to 20, so the ~15 us host cost of a graph launch is amortised as it
 would be inside a model's graph) and replayed; W warm-up steps, then K timed
 steps bracketed by synchronisation.  The eager torch.autograd path is timed too and
-reported as "eager_ms_per_step".
+reported as "eager_ms_per_step" (torch's default autograd engine, whose backward
+runs on a per-device worker thread) and "eager_calling_thread_ms_per_step" (the
+same step with the engine's worker threads off, the backward on the calling
+thread: torch.autograd.set_multithreading_enabled(False)).
 
 Roofline: the dominant kernel of the step is isolated by capturing 50 copies
 of its pass into a HIP graph, deleting every other node, re-chaining the 50
@@ -780,19 +783,29 @@ def measure(name, steps, warmup, dtype, device, cpu_seconds):
     dom = max(kernels, key=lambda r: r["us"])
     achieved = dom["pass_bytes"] / (dom["us"] * 1e-6) / 1e9  # GB/s
 
-    # eager autograd API: median of 5 timed runs of ne steps each, after warm-up
-    for _ in range(10):
-        w["eager"]()
-    torch.cuda.synchronize()
+    # eager autograd API: median of 5 timed runs of ne steps each, after warm-up;
+    # once with torch's default engine (the backward runs on its per-device
+    # worker thread: two thread hand-offs per step) and once with the engine's
+    # worker threads off (torch.autograd.set_multithreading_enabled(False): the
+    # backward runs on the calling thread), which isolates the hand-offs
     ne = max(10, min(steps, 50))
-    runs = []
-    for _ in range(5):
-        e0 = time.perf_counter()
-        for _ in range(ne):
+
+    def eager_time():
+        for _ in range(10):
             w["eager"]()
         torch.cuda.synchronize()
-        runs.append((time.perf_counter() - e0) * 1e3 / ne)
-    eager_ms = sorted(runs)[len(runs) // 2]
+        runs = []
+        for _ in range(5):
+            e0 = time.perf_counter()
+            for _ in range(ne):
+                w["eager"]()
+            torch.cuda.synchronize()
+            runs.append((time.perf_counter() - e0) * 1e3 / ne)
+        return sorted(runs)[len(runs) // 2]
+
+    eager_ms = eager_time()
+    with torch.autograd.set_multithreading_enabled(False):
+        eager_ct_ms = eager_time()
 
     # transient memory of one eager fwd+bwd: peak allocation beyond the inputs,
     # minus the outputs and gradients the call returns (y, grads)
@@ -810,7 +823,7 @@ def measure(name, steps, warmup, dtype, device, cpu_seconds):
                   "pass_us": pass_us[dom["pass_"]],
                   "pass_frac": dom["pass_bytes"] / (pass_us[dom["pass_"]] * 1e-6) / 1e9 / HBM_PEAK_GBS,
                   "n_kernels_in_pass": dom["n_kernels"]},
-        achieved_gbs=achieved, eager_ms_per_step=eager_ms,
+        achieved_gbs=achieved, eager_ms_per_step=eager_ms, eager_calling_thread_ms_per_step=eager_ct_ms,
         peak_transient_bytes=int(peak_extra), state_history_bytes=int(w["state_hist_bytes"]),
     )
     if cpu_seconds > 0:
@@ -1308,6 +1321,7 @@ def main():
         extras[nm] = dict(workload=r["workload"], config=ecfg, tokens_per_s=r["tokens_per_s"],
                           ms_per_step=r["ms_per_step"], fwd_us=r["fwd_us"], bwd_us=r["bwd_us"],
                           eager_ms_per_step=r["eager_ms_per_step"],
+                          eager_calling_thread_ms_per_step=r["eager_calling_thread_ms_per_step"],
                           roofline=dict(bound="hbm", achieved=r["achieved_gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
                                         traffic=traffic_of(nm, r["dominant"]),
                                         frac=r["achieved_gbs"] / HBM_PEAK_GBS, kernel=r["dominant"]),
@@ -1352,6 +1366,7 @@ def main():
         "bwd_us": r["bwd_us"],
         "kernels": r["kernels"],
         "eager_ms_per_step": r["eager_ms_per_step"],
+        "eager_calling_thread_ms_per_step": r["eager_calling_thread_ms_per_step"],
         "peak_transient_bytes": r["peak_transient_bytes"],
         "state_history_bytes": r["state_history_bytes"],
         "also": extras,
