@@ -111,17 +111,24 @@ template <int DH, int NS, int MODE, bool GLA>
 union ColBwdShared {
   ColBwdSmem<DH, NS, GLA, MODE != kWhole> m;
 };
+// Wide states (past kDirectMaxState) in the direct mode: the adjoint summed by
+// direct_sum_wide; du's row-owned operands of it go through the workspace
+// (the pipelined mode's adjoint slots).
+template <int DH, int NS>
+constexpr bool kWideDirect = DH * NS > rr::chunked::kDirectMaxState;
 template <int DH, int NS, bool GLA>
 union ColBwdShared<DH, NS, kDirect, GLA> {
   ColBwdSmem<DH, NS, GLA, true> m;
-  rr::chunked::DirectSmem<DH, NS, true> d;
+  rr::chunked::DirectLds<DH, NS, true> d;
 };
 
 // Workgroups per CU the LDS allows (the register budget follows); SSD's
-// direct mode (short sequences, few workgroups) keeps the registers of two.
+// direct mode for short sequences (few workgroups) keeps the registers of two.
 template <int DH, int NS, int MODE, bool GLA>
 constexpr int kColBwdWgs = MODE == kPair ? 2   // the carried du operands: the registers of two
-                           : (int)(160 * 1024 / sizeof(ColBwdShared<DH, NS, MODE, GLA>)) >= 3 && (GLA || MODE != kDirect) ? 3
+                           : (int)(160 * 1024 / sizeof(ColBwdShared<DH, NS, MODE, GLA>)) >= 3 &&
+                                     (GLA || MODE != kDirect || kWideDirect<DH, NS>)
+                               ? 3
                            : (int)(160 * 1024 / sizeof(ColBwdShared<DH, NS, MODE, GLA>)) >= 2                          ? 2
                                                                                                                       : 1;
 
@@ -221,7 +228,78 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
         }
     }
   };
-  if constexpr (MODE == kDirect) {
+  if constexpr (MODE == kDirect && kWideDirect<DH, NS>) {
+    // the adjoint leaving the chunk, this wave's column blocks (direct_sum_wide)
+    const bool g0 = cbeg == 0 && p.dh0 != nullptr;   // uniform
+    const float gam_all = rr::chunked::direct_sum_wide<DH, NS, GLA, true>(p, cbeg, b, h, a, smu.d, lam, g0);
+    if (p.dfinal != nullptr) {
+      const float* dfb = p.dfinal + bh * DH * NS;
+#pragma unroll
+      for (int cc = 0; cc < CPW; ++cc) {
+        if (w + 4 * cc < NBN) {
+#pragma unroll
+          for (int db = 0; db < NBD; ++db)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              lam[cc][db][r] +=
+                  rr::chunked::direct_ext<DH, NS, GLA>(gam_all, dfb, 16 * db + 4 * l4 + r, 16 * (w + 4 * cc) + l15);
+        }
+      }
+    }
+    if (g0) {
+      // dh0 = tot_0 lam(0) + G_0, G_0 = (gam o dY_0)^T C_0: chunk 0's step
+      // scalars are range index 0 of the sum; the operands come straight
+      // from memory (A: dY rows 8 (lane / 16) + e of column d; B: C rows of
+      // column n)
+      const float t0 = smu.d.tot[0];
+      const int64_t row0 = (int64_t)b * p.L;
+      float gw[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) gw[e] = smu.d.coef[0][8 * l4 + e];
+      u16x8_t cfr[CPW];
+#pragma unroll
+      for (int cc = 0; cc < CPW; ++cc) {
+        const int nb = min(w + 4 * cc, NBN - 1);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cfr[cc][e] = p.Cm[((row0 + 8 * l4 + e) * p.H + h) * NS + 16 * nb + l15];
+      }
+#pragma unroll
+      for (int db = 0; db < NBD; ++db) {
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = gw[e] * p.dy[((row0 + 8 * l4 + e) * p.H + h) * DH + 16 * db + l15];
+        u16x8_t xh, xl;
+        rr::bf_split8(x, xh, xl);
+#pragma unroll
+        for (int cc = 0; cc < CPW; ++cc) {
+          if (w + 4 * cc < NBN) {
+            f32x4_t g = {0.f, 0.f, 0.f, 0.f};
+            g = mfma16(xh, cfr[cc], g);
+            g = mfma16(xl, cfr[cc], g);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              p.dh0[bh * DH * NS +
+                    rr::chunked::state_off<GLA, DH, NS>(16 * db + 4 * l4 + r, 16 * (w + 4 * cc) + l15)] =
+                  t0 * lam[cc][db][r] + g[r];
+          }
+        }
+      }
+    }
+    // du's operands (rows mydb + 4 k of lam, every column: other waves'
+    // blocks) are read in phase B2 as in the pipelined mode, from the
+    // workspace slot of this chunk, written here
+    float* lsl = p.agg + rr::chunked::adj_slot(bh, p.nC, 1, cbeg) * DH * NS;
+#pragma unroll
+    for (int cc = 0; cc < CPW; ++cc) {
+      if (w + 4 * cc < NBN) {
+#pragma unroll
+        for (int db = 0; db < NBD; ++db)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) lsl[(16 * db + 4 * l4 + r) * NS + 16 * (w + 4 * cc) + l15] = lam[cc][db][r];
+      }
+    }
+    __syncthreads();   // the chunk below reuses the LDS of the sum
+  } else if constexpr (MODE == kDirect) {
     // the adjoint leaving the chunk; chunk 0's workgroup also stores dh0
     const float gam_all = rr::chunked::direct_sum<DH, NS, GLA, true, true>(p, cbeg, b, h, a, smu.d, p.dh0);
     const float* dfb = p.dfinal != nullptr ? p.dfinal + bh * DH * NS : nullptr;
@@ -541,7 +619,7 @@ __global__ __launch_bounds__(256, (kColBwdWgs<DH, NS, MODE, GLA>)) void col_bwd_
         }
       }
     }
-    if constexpr (MODE == kPipe) {
+    if constexpr (MODE == kPipe || (MODE == kDirect && kWideDirect<DH, NS>)) {
 #pragma unroll
       for (int k = 0; k < DPW; ++k) {
         const int d = 16 * min(mydb + 4 * k, NBD - 1) + l15;
@@ -912,10 +990,11 @@ int launch(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
                          p);
     }
   } else if (p.mode == kDirect) {
-    if constexpr (DH * NS <= rr::chunked::kDirectMaxState)
+    // (wide: the states the host picks it for, SSD Dh 128 with N 64 and GLA Dh 128)
+    if constexpr (!kWideDirect<DH, NS> || (DH % 64 == 0 && NS % 64 == 0 && (GLA || (DH == 128 && NS == 64))))
       hipLaunchKernelGGL((col_bwd_kernel<DH, NS, kDirect, GLA>), rr::chunked::chunk_grid(p), dim3(256), 0, s, p);
     else
-      return rr::fail(RR_EUNSUPPORTED, "chunked backward: state too large for the direct mode");
+      return rr::fail(RR_EUNSUPPORTED, "chunked backward: no direct mode for this state");
   } else {
     hipLaunchKernelGGL((col_bwd_kernel<DH, NS, kWhole, GLA>), dim3(1, p.H, (unsigned)B), dim3(256), 0, s, p);
   }

@@ -45,13 +45,17 @@ constexpr int64_t kGlaWholeBwdMaxChunks = 16;
 int gla2_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass) {
   if (B * H >= kGlaWholeMinHeads && (pass == 0 || nC <= kGlaWholeBwdMaxChunks)) return chunked::kWhole;
   if (pass == 0 && res_fwd_supported(B, H, nC, Dh, Dh)) return chunked::kRes;   // short heads, resident
-  if (Dh * Dh > chunked::kDirectMaxState) return chunked::kPipe;
+  if (Dh * Dh > chunked::kDirectMaxState)   // Dh 128: the wide direct mode (direct_sum_wide) while resident
+    return nC <= chunked::kDirectMaxChunks && B * H * nC <= kGlaDirectMaxWorkgroups ? chunked::kDirect
+                                                                                     : chunked::kPipe;
   if (nC <= kGlaDirectMaxChunks) return chunked::kDirect;
   return nC <= chunked::kDirectMaxChunks && B * H * nC <= kGlaDirectMaxWorkgroups ? chunked::kDirect : chunked::kPipe;
 }
 
 size_t gla2_ws_bytes(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass) {
   const int mode = gla2_mode(B, H, nC, Dh, pass);
+  if (mode == chunked::kDirect && Dh * Dh > chunked::kDirectMaxState)   // wide: the backward's adjoints
+    return pass == 1 ? (size_t)align64(B * H * nC * Dh * Dh) * sizeof(float) : 0;
   if (mode == chunked::kDirect || mode == chunked::kWhole || mode == chunked::kRes) return 0;
   int64_t f = align64(B * H * nC);
   if (pass == 1) f += align64(B * H * nC * Dh * Dh);
@@ -61,6 +65,10 @@ size_t gla2_ws_bytes(int64_t B, int64_t H, int64_t nC, int64_t Dh, int pass) {
 void gla2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass) {
   float* f = static_cast<float*>(ws);
   a.ws = a.tot = a.agg = nullptr;
+  if (a.mode == chunked::kDirect && a.DH * a.DH > chunked::kDirectMaxState) {   // wide: the backward's adjoints
+    a.agg = pass == 1 ? f : nullptr;
+    return;
+  }
   if (a.mode == chunked::kDirect || a.mode == chunked::kWhole || a.mode == chunked::kRes) return;
   a.tot = f;
   f += align64(B * a.H * a.nC);

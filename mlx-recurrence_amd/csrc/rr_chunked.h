@@ -1117,6 +1117,225 @@ __device__ __forceinline__ float direct_ext(float gam_all, const float* ext, int
   return gam_all * ext[state_off<GLA, DH, NS>(d, n)];
 }
 
+// ------------------------------------------------------------------ direct mode, wide states
+// The same sums for states past kDirectMaxState (Dh 128 with N 64, GLA's
+// 128 x 128), whose every-block accumulators would not fit one wave's
+// registers and whose partial sums would not fit the LDS: every wave walks
+// every summed chunk and accumulates only the state blocks its kernel owns,
+// in that kernel's register layout, so nothing is reduced across waves:
+//   forward (fwd_kernel): row blocks db = w + 4 i, every column block nb,
+//     transposed (element r at n = 16 nb + 4 (lane / 16) + r, d = 16 db +
+//     lane % 16): acc[i][nb] += ((F m31 w) o B)^T U;
+//   backward (col_bwd_kernel): column blocks nb = w + 4 i, every row block
+//     db, natural (element r at d = 16 db + 4 (lane / 16) + r, n = 16 nb +
+//     lane % 16): acc[i][db] += ((F gam) o dY)^T C.
+// A summed chunk is staged once per workgroup: each thread loads its pieces
+// (the loads of the chunk two ahead are in flight meanwhile), applies the fp32
+// step factors to the fp32-weighted operand (forward B, backward dY) and
+// splits it into bf16 hi + lo; then every wave reads its operands by
+// transposing LDS reads (16x16x32 MFMA, two per block and chunk).  The step
+// scalars of the range (wave w: chunks j0 + w + 4 k) and the chunk factors F_j
+// are formed first, as in direct_sum.  With g0 (backward, chunk 0) chunk 0's
+// step scalars are formed as well (range index 0), for the caller's dh0.
+// (Measured against it at Dh 128, B3 L512 H12: weighting U instead of B,
+// row-owned backward sums redistributed through memory, and double-buffered
+// staging overlapping the products were each no faster; the loop is bound by
+// the VALU work of the weighting and splitting, which the workgroups sharing
+// a CU all do at once.)
+template <int DH, int NS, bool BWD>
+struct alignas(16) WideSmem {
+  using SX = Staged<DH>;   // fwd: U [s][d]; bwd: (F gam o dY) hi, lo [t][d]
+  using SY = Staged<NS>;   // fwd: (F m31 w o B) hi, lo [s][n]; bwd: C [t][n]
+  uint16_t X[BWD ? 2 : 1][SX::SIZE];
+  uint16_t Y[BWD ? 1 : 2][SY::SIZE];
+  float coef[kDirectMaxChunks][Q];   // step factors of the range's chunks: m31 w (fwd), gam (bwd)
+  float tot[kDirectMaxChunks];       // their chunk decays gam_31
+};
+
+template <int DH, int NS, bool GLA, bool BWD, int NI, int NJ>
+__device__ float direct_sum_wide(const ChunkArgs& p, int c, int b, int h, float a, WideSmem<DH, NS, BWD>& s,
+                                 f32x4_t (&acc)[NI][NJ], bool g0) {
+  using S = WideSmem<DH, NS, BWD>;
+  using SX = typename S::SX;
+  using SY = typename S::SY;
+  constexpr int NBD = DH / 16, NBN = NS / 16;
+  static_assert(NJ == (BWD ? NBD : NBN) && NI == (BWD ? (NBN + 3) / 4 : (NBD + 3) / 4), "direct_sum_wide: blocks");
+  static_assert(DH % 64 == 0 && NS % 64 == 0, "direct_sum_wide: whole pieces per thread");
+  // pieces per thread and chunk: fwd U rows (8 bf16), bwd dY rows (4 fp32); B / C rows (8 bf16)
+  constexpr int XV = BWD ? Q * DH / 4 / 256 : Q * DH / 8 / 256, XW = BWD ? DH / 4 : DH / 8;
+  constexpr int YV = Q * NS / 8 / 256;
+  using XT = std::conditional_t<BWD, float4, u16x8_t>;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t rowH = p.H;
+  const int kfirst = BWD ? c + 1 : 0;          // first summed chunk
+  const int j0 = BWD && g0 ? 0 : kfirst;       // range with step scalars: [j0, j1)
+  const int j1 = BWD ? p.nC : c;
+  const int cnt = j1 - j0;
+  const int ns = j1 - kfirst;                  // summed chunks: [kfirst, j1)
+  const int nw = cnt > w ? (cnt - w + 3) / 4 : 0;   // this wave's chunks of the range (uniform per wave)
+  const float neutral = GLA ? 1.f : 0.f;
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // 1. step scalars of the range's chunks into LDS
+  {
+    auto chunk = [&](int k) { return cnt > 0 ? min(j0 + w + 4 * k, j1 - 1) : c; };
+    float xs[kDirectPerWave];
+#pragma unroll
+    for (int k = 0; k < kDirectPerWave; ++k) {
+      const int64_t row0 = (int64_t)b * p.L + (int64_t)chunk(k) * Q;
+      const int tl = k < nw ? lane & (Q - 1) : 0;
+      xs[k] = bf_val(p.delta[(row0 + tl) * rowH + h]);   // lanes >= 32 take the neutral input below
+    }
+#pragma unroll
+    for (int k = 0; k < kDirectPerWave; ++k) {
+      if (k < nw) {
+        const StepScalars sc = step_scalars<GLA>(lane < Q ? xs[k] : neutral, a, lane);
+        const int jj = chunk(k) - j0;
+        if (lane < Q) s.coef[jj][lane] = BWD ? sc.gam : sc.m31 * sc.w;
+        if (lane == 0) s.tot[jj] = sc.tot;
+      }
+    }
+  }
+  __syncthreads();
+
+  // 2. chunk factors by a product scan over the range (lane i: range index
+  //    i), in every wave: fwd F_j = tot_{j+1} ... tot_{j1-1} at lane
+  //    cnt - 1 - i, bwd F_j = tot_{kfirst} ... tot_{j-1} at lane i
+  float e;
+  {
+    const int i = lane & 31;
+    float v;
+    if constexpr (BWD) {
+      const int src = i - 1;
+      const float t = s.tot[min(max(src, 0), kDirectMaxChunks - 1)];   // read in every lane
+      v = src >= 0 && src < cnt && j0 + src >= kfirst ? t : 1.f;
+    } else {
+      const int src = cnt - i;
+      const float t = s.tot[min(max(src, 0), kDirectMaxChunks - 1)];   // read in every lane
+      v = i > 0 && src >= 0 && src < cnt ? t : 1.f;
+    }
+    e = prefix_prod32(v, lane);
+  }
+  const float gam_all = __shfl(e, min(cnt, 31));
+  if (ns <= 0) return gam_all;   // workgroup-uniform
+
+  // 3. the summed chunks, two slots of loads in flight.  Summed chunk k is
+  //    chunk kfirst + k; past the last one (k >= ns) the loads repeat one
+  //    address of the last chunk in every lane and the weighted operand is
+  //    staged as zeros (the products add 0), so every pass of the loop runs
+  //    the same loads, waits and products.
+  XT xr[2][XV];
+  u16x8_t yr[2][YV];
+  auto load = [&](int slot, int k) {
+    const int on = k < ns ? 1 : 0;   // uniform
+    const int64_t row0 = (int64_t)b * p.L + (int64_t)(kfirst + min(k, ns - 1)) * Q;
+#pragma unroll
+    for (int v = 0; v < XV; ++v) {
+      const int i = on * (tid + 256 * v), t = i / XW, x0 = (BWD ? 4 : 8) * (i % XW);
+      if constexpr (BWD)
+        xr[slot][v] = *reinterpret_cast<const float4*>(p.dy + ((row0 + t) * rowH + h) * DH + x0);
+      else
+        xr[slot][v] = *reinterpret_cast<const u16x8_t*>(p.u + ((row0 + t) * rowH + h) * DH + x0);
+    }
+    const uint16_t* ysrc = BWD ? p.Cm : p.Bm;
+#pragma unroll
+    for (int v = 0; v < YV; ++v) {
+      const int i = on * (tid + 256 * v), t = i / (NS / 8), n0 = 8 * (i % (NS / 8));
+      yr[slot][v] = *reinterpret_cast<const u16x8_t*>(ysrc + ((row0 + t) * rowH + h) * NS + n0);
+    }
+  };
+  auto stage = [&](int slot, int k) {
+    const bool live = k < ns;                      // uniform; otherwise the weighted operand is staged as 0
+    const int jj = kfirst + min(k, ns - 1) - j0;   // range index
+    const float F = __shfl(e, BWD ? jj : cnt - 1 - jj);
+#pragma unroll
+    for (int v = 0; v < XV; ++v) {
+      const int i = tid + 256 * v, t = i / XW, x0 = (BWD ? 4 : 8) * (i % XW);
+      if constexpr (BWD) {
+        const float cf = F * s.coef[jj][t];
+        const float4 g = xr[slot][v];
+        const f32x4_t x = {live ? cf * g.x : 0.f, live ? cf * g.y : 0.f, live ? cf * g.z : 0.f,
+                           live ? cf * g.w : 0.f};
+        u16x4_t hi, lo;
+        rr::bf_split4(x, hi, lo);
+        *reinterpret_cast<u16x4_t*>(&s.X[0][SX::off(t, x0)]) = hi;
+        *reinterpret_cast<u16x4_t*>(&s.X[BWD ? 1 : 0][SX::off(t, x0)]) = lo;
+      } else {
+        *reinterpret_cast<u16x8_t*>(&s.X[0][SX::off(t, x0)]) = xr[slot][v];
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < YV; ++v) {
+      const int i = tid + 256 * v, t = i / (NS / 8), n0 = 8 * (i % (NS / 8));
+      if constexpr (BWD) {
+        *reinterpret_cast<u16x8_t*>(&s.Y[0][SY::off(t, n0)]) = yr[slot][v];
+      } else {
+        const float cf = F * s.coef[jj][t];
+        float yw[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) yw[q] = live ? cf * bf_val(yr[slot][v][q]) : 0.f;
+        u16x8_t hi, lo;
+        rr::bf_split8(yw, hi, lo);
+        *reinterpret_cast<u16x8_t*>(&s.Y[0][SY::off(t, n0)]) = hi;
+        *reinterpret_cast<u16x8_t*>(&s.Y[BWD ? 0 : 1][SY::off(t, n0)]) = lo;
+      }
+    }
+  };
+  auto products = [&]() {
+    if constexpr (BWD) {
+      u16x8_t cf[NI];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) cf[i] = frag_tr_st<SY>(s.Y[0], 16 * min(w + 4 * i, NBN - 1), lane);
+#pragma unroll
+      for (int db = 0; db < NBD; ++db) {
+        const u16x8_t xh = frag_tr_st<SX>(s.X[0], 16 * db, lane);
+        const u16x8_t xl = frag_tr_st<SX>(s.X[BWD ? 1 : 0], 16 * db, lane);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          if (w + 4 * i < NBN) {
+            acc[i][db] = mfma16(xh, cf[i], acc[i][db]);
+            acc[i][db] = mfma16(xl, cf[i], acc[i][db]);
+          }
+        }
+      }
+    } else {
+      u16x8_t xf[NI];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) xf[i] = frag_tr_st<SX>(s.X[0], 16 * min(w + 4 * i, NBD - 1), lane);
+#pragma unroll
+      for (int nb = 0; nb < NBN; ++nb) {
+        const u16x8_t yh = frag_tr_st<SY>(s.Y[0], 16 * nb, lane);
+        const u16x8_t yl = frag_tr_st<SY>(s.Y[BWD ? 0 : 1], 16 * nb, lane);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          if (w + 4 * i < NBD) {
+            acc[i][nb] = mfma16(yh, xf[i], acc[i][nb]);
+            acc[i][nb] = mfma16(yl, xf[i], acc[i][nb]);
+          }
+        }
+      }
+    }
+  };
+  load(0, 0);
+  load(1, 1);
+  for (int k = 0; k < ns; k += 2) {
+    stage(0, k);
+    load(0, k + 2);
+    __syncthreads();
+    products();
+    __syncthreads();
+    stage(1, k + 1);   // past the last summed chunk: zeros
+    load(1, k + 3);
+    __syncthreads();
+    products();
+    __syncthreads();
+  }
+  return gam_all;
+}
+
 // ------------------------------------------------------------------ forward
 // TRB (SSD with N <= 32): the end state reads B transposed from LDS and
 // weights it in registers; otherwise (m31 o w o B)^T is staged as BwT.
@@ -1139,10 +1358,14 @@ template <int DH, int NS, bool DIRECT, bool TRB>
 union FwdShared {
   FwdSmem<DH, NS, TRB> f;
 };
+// The direct sums' LDS: the narrow form's (DirectSmem) up to kDirectMaxState,
+// the wide form's (WideSmem) past it.
+template <int DH, int NS, bool BWD>
+using DirectLds = std::conditional_t<(DH * NS <= kDirectMaxState), DirectSmem<DH, NS, BWD>, WideSmem<DH, NS, BWD>>;
 template <int DH, int NS, bool TRB>
 union FwdShared<DH, NS, true, TRB> {
   FwdSmem<DH, NS, TRB> f;
-  DirectSmem<DH, NS, false> d;
+  DirectLds<DH, NS, false> d;
 };
 
 // One chunk per workgroup with the entering state from checkpoint slot c - 1
@@ -1159,11 +1382,14 @@ union FwdShared<DH, NS, true, TRB> {
 // rows with no cross-wave sum and no LDS copy of the state:
 //   Y[t, d] = (W U)[t, d] + gam_t (C h_in^T)[t, d],  W = M o C B^T o w_s
 //   h_end^T = gam_31 h_in^T + (m31 o w o B)^T U
-// GLA's direct mode: three workgroups per CU where the LDS allows it (a chunk
-// per workgroup, so every workgroup of a 16-chunk sequence at batch 3 can be
-// resident); the register budget follows.
+// GLA's direct mode, and the wide direct mode: three workgroups per CU where
+// the LDS allows it (a chunk per workgroup, so every workgroup of a 16-chunk
+// sequence at batch 3 can be resident); the register budget follows.
 template <int DH, int NS, int MODE, bool GLA>
-constexpr int kFwdWgs = GLA && MODE == kDirect && 160 * 1024 / sizeof(FwdShared<DH, NS, true, false>) >= 3 ? 3 : 1;
+constexpr int kFwdWgs = (GLA || DH * NS > kDirectMaxState) && MODE == kDirect &&
+                                160 * 1024 / sizeof(FwdShared<DH, NS, true, !GLA && NS <= 32>) >= 3
+                            ? 3
+                            : 1;
 
 template <int DH, int NS, int MODE, bool GLA>
 __global__ __launch_bounds__(256, (kFwdWgs<DH, NS, MODE, GLA>)) void fwd_kernel(ChunkArgs p) {
@@ -1223,7 +1449,27 @@ __global__ __launch_bounds__(256, (kFwdWgs<DH, NS, MODE, GLA>)) void fwd_kernel(
     // unconditional (in-bounds) load, so no branch waits on it
     xv = bf_val(p.delta[(row0 + (tid & (Q - 1))) * rowH + h]);
   };
-  if constexpr (MODE == kDirect) {
+  if constexpr (MODE == kDirect && DH * NS > kDirectMaxState) {
+    // wide state: every wave sums its own rows of the state (direct_sum_wide),
+    // then the chunk's loads go out
+    const float gam_all = direct_sum_wide<DH, NS, GLA, false>(p, cbeg, b, h, a, smu.d, hst, false);
+    issue(cbeg, tid);
+    if (p.h0 != nullptr) {
+      const float* h0b = p.h0 + bh * DH * NS;
+#pragma unroll
+      for (int i = 0; i < DBW; ++i) {
+        const int db = w + 4 * i;
+        if (db < NBD) {
+#pragma unroll
+          for (int nb = 0; nb < NBN; ++nb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              hst[i][nb][r] += direct_ext<DH, NS, GLA>(gam_all, h0b, 16 * db + l15, 16 * nb + 4 * l4 + r);
+        }
+      }
+    }
+    __syncthreads();   // the chunk below reuses the LDS of the sum
+  } else if constexpr (MODE == kDirect) {
     // the chunk's loads go out when each wave has staged its last summed chunk
     f32x4_t own[DH == 64 ? NBN : 1];
     const float gam_all =
@@ -1467,10 +1713,11 @@ int launch_fwd(const ChunkArgs& p, int64_t B, hipStream_t s) {
     if (int rc = launch_scan<DH, NS, GLA>(p, B, s, false)) return rc;
     hipLaunchKernelGGL((fwd_kernel<DH, NS, kPipe, GLA>), chunk_grid(p), dim3(256), 0, s, p);
   } else if (p.mode == kDirect || p.mode == kSum) {   // R == 1; kSum forward = direct
-    if constexpr (DH * NS <= kDirectMaxState)
+    // (wide: the states the host picks it for, SSD Dh 128 with N 64 and GLA Dh 128)
+    if constexpr (DH * NS <= kDirectMaxState || (DH % 64 == 0 && NS % 64 == 0 && (GLA || (DH == 128 && NS == 64))))
       hipLaunchKernelGGL((fwd_kernel<DH, NS, kDirect, GLA>), chunk_grid(p), dim3(256), 0, s, p);
     else
-      return fail(RR_EUNSUPPORTED, "chunked forward: state too large for the direct mode");
+      return fail(RR_EUNSUPPORTED, "chunked forward: no direct mode for this state");
   } else {   // R == nC
     hipLaunchKernelGGL((fwd_kernel<DH, NS, kWhole, GLA>), dim3(1, p.H, (unsigned)B), dim3(256), 0, s, p);
   }

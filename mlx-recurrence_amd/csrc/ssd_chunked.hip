@@ -850,6 +850,13 @@ bool ssd2_bwd_supported(int64_t Dh, int64_t N) {
 // for the shortest heads.
 constexpr int64_t kDirectMaxChunksWide = 4;
 constexpr int64_t kDirectMaxWorkgroups = 4096;
+// Dh 128 with N 64 (the reference's production shape) in short heads, few of
+// them: the direct mode with block-owned sums (direct_sum_wide) while every
+// chunk's workgroup can be resident at once (three per CU).
+constexpr int64_t kWideDirectMaxWorkgroups = 3 * 256;
+bool wide_direct(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N) {
+  return Dh == 128 && N == 64 && nC <= chunked::kDirectMaxChunks && B * H * nC <= kWideDirectMaxWorkgroups;
+}
 
 int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N, int pass) {
   const int64_t grid = nC * ((B * H + chunked::kXcds - 1) / chunked::kXcds * chunked::kXcds);
@@ -859,6 +866,7 @@ int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N, int pa
   // B96 L512 H12 Dh64 N16 137 / 414 vs 194 / 357 (sum mode); B8 L4096 H80
   // Dh64 N128 2308 / 7457 vs 4025 / 4873 (pipelined)).
   if (B * H >= 512 && pass == 0) return chunked::kWhole;
+  if (wide_direct(B, H, nC, Dh, N)) return chunked::kDirect;
   // Short heads: the forward holds all chunks of a head in one workgroup per
   // 16-column slice of d (no re-reads, no cross-workgroup carry)
   if (pass == 0 && res_fwd_supported(B, H, nC, Dh, N)) return chunked::kRes;
@@ -888,10 +896,15 @@ int chunked_run(int mode, int64_t nC) {
 
 // Workspace layout (floats, each part 256-byte aligned): per-chunk decays
 // [B,H,nC] (pipelined mode), dA partials [B,H,nR,N] (backward), backward
-// chunk aggregates / adjoints [B,H,nC,Dh,N] (pipelined backward).
+// chunk aggregates / adjoints [B,H,nC,Dh,N] (pipelined backward; the wide
+// direct mode's adjoints, which du's operands are read back from).
 namespace {
 int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }
+bool adjoint_slots(int mode, int64_t Dh, int64_t N) {
+  return mode == chunked::kPipe || mode == chunked::kPair ||
+         (mode == chunked::kDirect && Dh * N > chunked::kDirectMaxState);
 }
+}  // namespace
 
 size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int mode, int64_t Dh, int64_t N, int pass) {
   const int64_t R = chunked_run(mode, nC), nR = (nC + R - 1) / R;
@@ -899,7 +912,7 @@ size_t ssd2_ws_bytes(int64_t B, int64_t H, int64_t nC, int mode, int64_t Dh, int
   int64_t f = pipe ? align64(B * H * nC) : 0;
   if (pass == 1) {
     f += align64(B * H * nR * N);
-    if (pipe) f += align64(B * H * nR * Dh * N);   // one adjoint per run
+    if (adjoint_slots(mode, Dh, N)) f += align64(B * H * nR * Dh * N);   // one adjoint per run
   }
   return (size_t)f * sizeof(float);
 }
@@ -912,7 +925,7 @@ void ssd2_carve_ws(ChunkArgs& a, void* ws, int64_t B, int pass) {
   if (pipe) { a.tot = f; f += align64(B * a.H * a.nC); }
   if (pass == 1) {
     a.ws = f; f += align64(B * a.H * nR * a.NS);
-    if (pipe) a.agg = f;
+    if (adjoint_slots(a.mode, a.DH, a.NS)) a.agg = f;
   }
 }
 
@@ -961,10 +974,10 @@ int64_t ssd2_ws_extent(int64_t B, int64_t H, int64_t nC, int mode, int64_t Dh, i
     }
   } else {
     for (int64_t id = 0; id < chunk_grid_size(a.B, a.H, a.nC); ++id) {
-      const ChunkId c = decode_chunk((int)id, a.B, a.H, a.nC, a.NS, mode == kSum, false);
+      const ChunkId c = decode_chunk((int)id, a.B, a.H, a.nC, a.NS, mode == kSum || mode == kDirect, false);
       if (!c.valid) continue;
       const int64_t bh = (int64_t)c.b * H + c.h;
-      if (mode == kPipe) touch(a.agg, adj_slot(bh, a.nC, 1, c.c) * state, state);
+      if (adjoint_slots(mode, Dh, N)) touch(a.agg, adj_slot(bh, a.nC, 1, c.c) * state, state);
       touch(a.ws, dA_slot(bh, nR, c.c) * N, N);
     }
   }

@@ -40,6 +40,10 @@ CASES = [
     # the same at the reference's published shape (wide states: d streamed in blocks)
     ("ssd", dict(B=3, L=512, H=12, Dh=128, N=64, seg=32, dense=True)),
     ("gla", dict(B=3, L=512, H=12, Dh=128, seg=32, dtype="f32")),
+    # the published shape in bf16 with a per-head rate: the wide direct mode
+    # (block-owned sums over the other chunks, the adjoint through the workspace)
+    ("ssd", dict(B=3, L=512, H=12, Dh=128, N=64, seg=32)),
+    ("gla", dict(B=3, L=512, H=12, Dh=128, seg=32)),
 ]
 MAKERS = {"ssd": bench.make_ssd, "gla": bench.make_gla, "rglru": bench.make_rglru,
           "rglru_gated": bench.make_rglru_gated, "rotlru": bench.make_rotlru,

@@ -333,7 +333,7 @@ SSD_CASES = [
     (1, 256, 4, 64, 128, 32, BF16, "cfg", True, True, 12),  # config 4's N = 128, reduced
     (2, 512, 3, 64, 16, 32, BF16, "cfg", True, True, 13),   # chunked kernels, entering-state sums
     (1, 128, 2, 32, 32, 32, BF16, "cfg", True, False, 14),
-    (1, 96, 2, 128, 64, 32, BF16, "cfg", False, True, 15),
+    (1, 96, 2, 128, 64, 32, BF16, "cfg", False, True, 15),  # wide direct mode, 3 chunks
     (2, 64, 2, 64, 16, 32, BF16, "ref", False, False, 16),  # dense A, bf16: VALU engine
     # B*H >= 512: one workgroup walks a whole head (state carried in registers)
     (1, 128, 512, 32, 16, 32, BF16, "cfg", True, True, 17),
@@ -356,7 +356,14 @@ SSD_CASES = [
     (1, 64, 512, 32, 64, 32, BF16, "cfg", True, True, 34),   # whole head
     (2, 96, 256, 64, 128, 32, BF16, "cfg", True, True, 35),  # whole head, config 4's tile
     # Dh = 128 (column-owned backward, two du row blocks per wave)
-    (3, 512, 12, 128, 64, 32, BF16, "cfg", True, True, 40),   # the reference's production shape: pipelined
+    (3, 512, 12, 128, 64, 32, BF16, "cfg", True, True, 40),   # the reference's production shape: wide direct mode
+    # wide direct mode (Dh 128, N 64, short heads): block-owned sums over the
+    # other chunks, dh0 from chunk 0's workgroup; one chunk (nothing summed),
+    # an odd count of summed chunks; 16 chunks at Dh 64 / N 128 (pipelined)
+    (2, 32, 3, 128, 64, 32, BF16, "cfg", True, True, 75),
+    (1, 224, 4, 128, 64, 32, BF16, "cfg", True, False, 76),
+    (2, 512, 5, 64, 128, 32, BF16, "cfg", True, True, 77),
+    (1, 1024, 2, 128, 64, 32, BF16, "cfg", True, True, 78),   # 32 chunks: pipelined
     (1, 160, 3, 128, 128, 32, BF16, "cfg", True, True, 41),   # N = 128, pipelined
     (2, 192, 160, 128, 64, 32, BF16, "cfg", False, True, 42), # B*H >= 320: per-head adjoint scan
     # pipelined with B*H >= 320: the per-head state / adjoint scan kernel
@@ -490,8 +497,12 @@ GLA_CASES = [
     # bf16 with T = 32: chunked MFMA kernels
     (2, 256, 3, 64, 32, BF16, "cfg", True, True, 20),
     (1, 128, 2, 32, 32, BF16, "ref", True, True, 21),
-    (1, 96, 2, 128, 32, BF16, "cfg", True, True, 22),   # Dh = 128: pipelined forward and backward (a 128 x 128 state)
+    (1, 96, 2, 128, 32, BF16, "cfg", True, True, 22),   # Dh = 128 (a 128 x 128 state): wide direct mode
     (1, 256, 3, 128, 32, BF16, "signed", True, True, 39),  # Dh = 128, 8 chunks, gates of either sign
+    (3, 512, 12, 128, 32, BF16, "cfg", True, True, 41),    # the reference's production shape: wide direct, 16 chunks
+    (1, 480, 2, 128, 32, BF16, "zeros", True, True, 42),   # wide direct, 15 chunks, zero gates
+    (2, 32, 3, 128, 32, BF16, "signed", True, True, 43),   # wide direct, one chunk
+    (1, 640, 2, 128, 32, BF16, "cfg", True, True, 44),     # Dh = 128, 20 chunks: pipelined
     (2, 32, 2, 64, 32, BF16, "cfg", True, True, 23),    # one chunk
     (1, 160, 2, 64, 32, BF16, "signed", True, True, 24),
     (1, 128, 2, 32, 32, BF16, "zeros", True, True, 25),

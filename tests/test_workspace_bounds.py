@@ -30,7 +30,10 @@ SHAPES = [
     (2, 1056, 4, 64, 64),      # nC 33, few heads: aggregate + adjoint-pass kernels
     (3, 512, 12, 64, 16),      # sum mode
     (3, 512, 12, 64, 64),      # per-chunk mode, wide state, few heads
-    (2, 128, 3, 128, 64),      # direct mode (nC 4), Dh 128
+    (2, 128, 3, 128, 64),      # wide direct mode (nC 4), Dh 128
+    (3, 512, 12, 128, 64),     # wide direct mode: the reference's published shape
+    (2, 256, 6, 64, 128),      # Dh 64 N 128, short heads: pipelined
+    (4, 512, 16, 128, 64),     # Dh 128, 1024 chunk workgroups: per-chunk mode
     (96, 512, 12, 64, 16),     # SSD c1 shape at B 96: per-chunk with the scan
 ]
 
@@ -67,7 +70,7 @@ def test_pair_mode_bound_detects_the_old_slot_spacing():
 
 
 def test_extent_for_valu_engine_calls_and_bad_arguments():
-    # a dense A_neg [H, N] runs on the VALU engine: no chunked bound
+    # a dense A_neg [H, N] or fp32 inputs run other kernels: no bound from this walk
     assert _lib.ssd_workspace_extent(3, 512, 12, 64, 16, 32, 1, BF16, 1) == -1
     assert _lib.ssd_workspace_extent(3, 512, 12, 64, 16, 32, 0, 0, 1) == -1   # fp32 inputs
     assert _lib.ssd_workspace_extent(0, 512, 12, 64, 16, 32, 0, BF16, 1) == -1
