@@ -364,6 +364,8 @@ SSD_CASES = [
     (1, 224, 4, 128, 64, 32, BF16, "cfg", True, False, 76),
     (2, 512, 5, 64, 128, 32, BF16, "cfg", True, True, 77),
     (1, 1024, 2, 128, 64, 32, BF16, "cfg", True, True, 78),   # 32 chunks: pipelined
+    (4, 512, 12, 128, 64, 32, BF16, "cfg", True, True, 79),   # 768 chunk workgroups: the wide direct mode's largest
+    (5, 512, 12, 128, 64, 32, BF16, "cfg", False, True, 80),  # 960: pipelined
     (1, 160, 3, 128, 128, 32, BF16, "cfg", True, True, 41),   # N = 128, pipelined
     (2, 192, 160, 128, 64, 32, BF16, "cfg", False, True, 42), # B*H >= 320: per-head adjoint scan
     # pipelined with B*H >= 320: the per-head state / adjoint scan kernel
@@ -503,6 +505,7 @@ GLA_CASES = [
     (1, 480, 2, 128, 32, BF16, "zeros", True, True, 42),   # wide direct, 15 chunks, zero gates
     (2, 32, 3, 128, 32, BF16, "signed", True, True, 43),   # wide direct, one chunk
     (1, 640, 2, 128, 32, BF16, "cfg", True, True, 44),     # Dh = 128, 20 chunks: pipelined
+    (4, 512, 12, 128, 32, BF16, "signed", True, True, 45),  # 768 chunk workgroups: the wide direct mode's largest
     (2, 32, 2, 64, 32, BF16, "cfg", True, True, 23),    # one chunk
     (1, 160, 2, 64, 32, BF16, "signed", True, True, 24),
     (1, 128, 2, 32, 32, BF16, "zeros", True, True, 25),
