@@ -174,7 +174,8 @@ __device__ __forceinline__ int state_off(int d, int n) {
 //           (pass_kernel), chunk kernel;
 //   kDirect one workgroup per chunk forming its entering state (forward) or
 //           leaving adjoint (backward) from the raw inputs of the other chunks
-//           (direct_sum; nC <= kDirectMaxChunks): one kernel per pass;
+//           (direct_sum, or direct_sum_wide for states past kDirectMaxState;
+//           nC <= kDirectMaxChunks): one kernel per pass;
 //   kSum    the same sum, for the backward's small-N kernel (its own
 //           instantiation); the forward runs the direct kernel.
 // Both read up to nC - 1 chunks of inputs per workgroup (quadratic in nC), so

@@ -42,9 +42,10 @@ struct ChunkArgs {
 // heads of nC chunks of a Dh x N state: a whole head per workgroup for the
 // forward when the heads alone fill the GPU (and for either pass when a 1-D
 // per-chunk grid would exceed 2^31 workgroups); else one workgroup per chunk,
-// with the entering states formed directly (nC <= 4, Dh * N <= 64 * 64), from
-// the chunk aggregates (nC <= 16, N <= 32) or by the pipelined aggregate and
-// state-pass kernels.
+// with the entering states formed directly (nC <= 4 with Dh * N <= 64 * 64;
+// nC <= 16 with Dh 128, N 64 and at most 768 chunk workgroups), from the chunk
+// aggregates (nC <= 16, N <= 32) or by the pipelined aggregate and state-pass
+// kernels.
 int chunked_mode(int64_t B, int64_t H, int64_t nC, int64_t Dh, int64_t N, int pass);
 int chunked_run(int mode, int64_t nC);   // ChunkArgs::R of a mode
 
