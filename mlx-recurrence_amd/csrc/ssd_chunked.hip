@@ -815,8 +815,11 @@ __global__ __launch_bounds__(T) void ssd2_dA_kernel(const float* __restrict__ pa
 
 int launch_dA(const rr::ChunkArgs& p, int64_t B, hipStream_t s) {
   const int nR = (p.nC + p.R - 1) / p.R;   // runs per head
-  // (a larger workgroup only where there are many partials to sum)
-  if ((int64_t)B * nR * p.NS > 4096)
+  // (a larger workgroup where the smaller one would leave a thread more than
+  // four partials: more than one round of dependent loads, which come from
+  // other XCDs' writes.  Dh 128 / N 64 at B3 L512: 3072 partials per head,
+  // 3.96 µs with 256 threads)
+  if ((int64_t)B * nR * p.NS > 1024)
     hipLaunchKernelGGL(ssd2_dA_kernel<1024>, dim3(p.H), dim3(1024), 0, s, p.ws, p.dA, (int)B, p.H, nR, p.NS, p.dA_sn);
   else
     hipLaunchKernelGGL(ssd2_dA_kernel<256>, dim3(p.H), dim3(256), 0, s, p.ws, p.dA, (int)B, p.H, nR, p.NS, p.dA_sn);
