@@ -1225,9 +1225,9 @@ __device__ float direct_sum_wide(const ChunkArgs& p, int c, int b, int h, float 
 
   // 3. the summed chunks, two slots of loads in flight.  Summed chunk k is
   //    chunk kfirst + k; past the last one (k >= ns) the loads repeat one
-  //    address of the last chunk in every lane and the weighted operand is
-  //    staged as zeros (the products add 0), so every pass of the loop runs
-  //    the same loads, waits and products.
+  //    address of the last chunk in every lane and its factor is 0 (the
+  //    weighted operand is staged as zeros and the products add 0), so every
+  //    pass of the loop runs the same loads, waits and products.
   XT xr[2][XV];
   u16x8_t yr[2][YV];
   auto load = [&](int slot, int k) {
@@ -1249,19 +1249,17 @@ __device__ float direct_sum_wide(const ChunkArgs& p, int c, int b, int h, float 
     }
   };
   auto stage = [&](int slot, int k) {
-    const bool live = k < ns;                      // uniform; otherwise the weighted operand is staged as 0
+    const bool live = k < ns;                      // uniform
     const int jj = kfirst + min(k, ns - 1) - j0;   // range index
     const float F = __shfl(e, BWD ? jj : cnt - 1 - jj);
 #pragma unroll
     for (int v = 0; v < XV; ++v) {
       const int i = tid + 256 * v, t = i / XW, x0 = (BWD ? 4 : 8) * (i % XW);
       if constexpr (BWD) {
-        const float cf = F * s.coef[jj][t];
+        const float cf = live ? F * s.coef[jj][t] : 0.f;
         const float4 g = xr[slot][v];
-        const f32x4_t x = {live ? cf * g.x : 0.f, live ? cf * g.y : 0.f, live ? cf * g.z : 0.f,
-                           live ? cf * g.w : 0.f};
         u16x4_t hi, lo;
-        rr::bf_split4(x, hi, lo);
+        rr::bf_split4(f32x4_t{cf * g.x, cf * g.y, cf * g.z, cf * g.w}, hi, lo);
         *reinterpret_cast<u16x4_t*>(&s.X[0][SX::off(t, x0)]) = hi;
         *reinterpret_cast<u16x4_t*>(&s.X[BWD ? 1 : 0][SX::off(t, x0)]) = lo;
       } else {
@@ -1274,10 +1272,10 @@ __device__ float direct_sum_wide(const ChunkArgs& p, int c, int b, int h, float 
       if constexpr (BWD) {
         *reinterpret_cast<u16x8_t*>(&s.Y[0][SY::off(t, n0)]) = yr[slot][v];
       } else {
-        const float cf = F * s.coef[jj][t];
+        const float cf = live ? F * s.coef[jj][t] : 0.f;
         float yw[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) yw[q] = live ? cf * bf_val(yr[slot][v][q]) : 0.f;
+        for (int q = 0; q < 8; ++q) yw[q] = cf * bf_val(yr[slot][v][q]);
         u16x8_t hi, lo;
         rr::bf_split8(yw, hi, lo);
         *reinterpret_cast<u16x8_t*>(&s.Y[0][SY::off(t, n0)]) = hi;
