@@ -1140,9 +1140,10 @@ __device__ __forceinline__ float direct_ext(float gam_all, const float* ext, int
 // step scalars are formed as well (range index 0), for the caller's dh0.
 // (Measured against it at Dh 128, B3 L512 H12: weighting U instead of B,
 // row-owned backward sums redistributed through memory, and double-buffered
-// staging overlapping the products were each no faster; the loop is bound by
-// the VALU work of the weighting and splitting, which the workgroups sharing
-// a CU all do at once.)
+// staging overlapping the products were each no faster.  Probes that drop
+// one part of the loop each — the products, the barriers, the weighting and
+// splitting, the L2 misses — save at most a third of the sum's time: it is
+// the dependent latency of each summed chunk.)
 template <int DH, int NS, bool BWD>
 struct alignas(16) WideSmem {
   using SX = Staged<DH>;   // fwd: U [s][d]; bwd: (F gam o dY) hi, lo [t][d]
