@@ -75,3 +75,28 @@ def test_extent_for_valu_engine_calls_and_bad_arguments():
     assert _lib.ssd_workspace_extent(3, 512, 12, 64, 16, 32, 0, 0, 1) == -1   # fp32 inputs
     assert _lib.ssd_workspace_extent(0, 512, 12, 64, 16, 32, 0, BF16, 1) == -1
     assert _lib.ssd_workspace_extent(3, 512, 12, 64, 16, 32, 0, BF16, 2) == -1
+
+
+def test_wide_direct_mode_workspace_at_the_published_shape():
+    """The reference's published shape (B3 L512 H12 Dh128 N64, bf16, a rate per
+    head) runs the wide direct mode: one kernel per pass, so the forward needs
+    no workspace, and the backward holds the dA partials [B,H,nC,N] and one
+    adjoint [Dh,N] per chunk (du's operand rows), each part 256-byte aligned.
+    Past 768 chunk workgroups the same state takes the resident forward (no
+    workspace) and the pipelined backward (per-chunk decays as well)."""
+    lib = _lib.load()
+    B, L, H, Dh, N = 3, 512, 12, 128, 64
+    nC = L // 32
+
+    def al(nbytes):
+        return (nbytes + ALIGN - 1) // ALIGN * ALIGN
+
+    assert int(lib.rr_ssd_workspace_bytes(B, L, H, Dh, N, 32, 0, BF16, 0)) == 0
+    assert int(lib.rr_ssd_workspace_bytes(B, L, H, Dh, N, 32, 0, BF16, 1)) == \
+        al(B * H * nC * N * 4) + al(B * H * nC * Dh * N * 4)
+    assert int(lib.rr_gla_workspace_bytes(B, L, H, Dh, 32, BF16, 0)) == 0
+    assert int(lib.rr_gla_workspace_bytes(B, L, H, Dh, 32, BF16, 1)) == al(B * H * nC * Dh * Dh * 4)
+    # 5 x 12 x 16 = 960 chunk workgroups
+    assert int(lib.rr_ssd_workspace_bytes(5, L, H, Dh, N, 32, 0, BF16, 0)) == 0
+    assert int(lib.rr_ssd_workspace_bytes(5, L, H, Dh, N, 32, 0, BF16, 1)) == \
+        al(5 * H * nC * 4) + al(5 * H * nC * N * 4) + al(5 * H * nC * Dh * N * 4)
