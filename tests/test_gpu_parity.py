@@ -443,6 +443,7 @@ SSD_HEAD_VECTOR_CASES = [
     # (B, L, H, Dh, N, seg, dtype, seed): A_neg passed as the [H] vector itself
     (3, 512, 12, 64, 16, 32, BF16, 60),   # BASELINE config 1 (sum-mode chunk kernel + dA reduction)
     (1, 256, 4, 64, 128, 32, BF16, 61),   # column-owned backward
+    (3, 512, 12, 128, 64, 32, BF16, 64),  # the published shape: wide direct mode, 1024-thread dA reduction
     (1, 128, 2, 32, 16, 32, F32, 62),     # fp32: the VALU engine
     (2, 96, 2, 32, 24, 16, F32, 63),      # VALU engine, N = 24, T = 16
 ]
